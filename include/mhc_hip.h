@@ -1,0 +1,106 @@
+/*
+ * mhc_hip.h - C ABI of the MI355X (gfx950) mHC hyper-connection library.
+ *
+ * This is the drop-in boundary that replaces the reference's native module
+ * `mhc_ascend` (src/python/bindings.cpp, pybind11 + ATen + ACL).  Every entry
+ * point takes plain device pointers, sizes and a HIP stream (`hipStream_t`
+ * passed as `void*`; NULL = the null stream), enqueues its kernels on that
+ * stream and returns without synchronising.  Buffers are caller-owned,
+ * contiguous, row-major.  Scratch memory is passed in by the caller
+ * (`workspace` / `workspace_bytes`, size from the matching *_workspace_size
+ * query); the library keeps no hidden device state, so calls are reentrant.
+ *
+ * Element types: `dtype` arguments take MHC_DTYPE_F32 or MHC_DTYPE_BF16 and
+ * describe the storage of the large [B, n, C] / [B, C] tensors; all
+ * arithmetic is fp32.  Small parameters (H, M, weights) are fp32.
+ *
+ * Status: 0 on success; MHC_ERR_* (< 0) for argument errors, with a message
+ * from mhc_last_error(); > 0 is the hipError_t of a failed launch.
+ *
+ * The reference interface each entry replaces is cited as file:line of
+ * ParadoxZW/mHC_Ascend.
+ */
+#ifndef MHC_HIP_H_
+#define MHC_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MHC_DTYPE_F32 0
+#define MHC_DTYPE_BF16 1
+
+#define MHC_SUCCESS 0
+#define MHC_ERR_INVALID (-1)     /* bad pointer, shape or dtype (TORCH_CHECK in the reference) */
+#define MHC_ERR_UNSUPPORTED (-2) /* valid request this build has no kernel for (e.g. n not compiled) */
+#define MHC_ERR_WORKSPACE (-3)   /* workspace smaller than the *_workspace_size query */
+
+/* ABI version: major * 10000 + minor * 100 + patch. */
+int mhc_abi_version(void);
+
+/* Message for the last MHC_ERR_* returned on this thread ("" if none). */
+const char* mhc_last_error(void);
+
+/* ---- kernel timing (HIP events on the launch stream) ----------------------
+ * When enabled, the library records a start/end hipEvent pair around each of
+ * its main kernels on the stream it launches them on.  mhc_timing_query
+ * synchronises the recorded events of `kernel` and returns the summed
+ * duration (ms) and the launch count since the last reset.  No counterpart
+ * in the reference (its benchmark times whole calls with NPU events,
+ * benchmark.py:196-204). */
+int mhc_timing_enable(int enable);
+int mhc_timing_reset(void);
+int mhc_timing_query(const char* kernel, double* total_ms, int64_t* launches);
+
+/* ---- Sinkhorn-Knopp --------------------------------------------------------
+ * out = SK_{num_iters, eps}(inp) on [batch, n, n] fp32, dividing rows then
+ * columns by (sum + eps) each iteration.
+ * Replaces sinkhorn_knopp_fwd (bindings.cpp:155-187). */
+int mhc_sinkhorn_knopp_fwd(const float* inp, float* out, int64_t batch, int32_t n, int32_t num_iters, float eps,
+                           void* stream);
+
+/* grad_inp = exact VJP of SK at inp.  `out` (the forward result) is accepted
+ * for signature parity and may be NULL; the kernel recomputes the forward
+ * history in registers.
+ * Replaces sinkhorn_knopp_bwd (bindings.cpp:189-231). */
+int mhc_sinkhorn_knopp_bwd(const float* grad_out, const float* inp, const float* out, float* grad_inp,
+                           int64_t batch, int32_t n, int32_t num_iters, float eps, void* stream);
+
+/* ---- fused static-H mHC layer ----------------------------------------------
+ * x [batch, n, hidden] (x_dtype), weight [hidden] fp32, h_pre/h_post [n],
+ * h_res [n, n] raw (pre-activation) parameters.
+ *   h_pre = sigmoid(H_pre), h_post = 2 sigmoid(H_post), M = SK(exp(H_res))
+ *   out[b,i,:] = sum_j M[i,j] x[b,j,:] + h_post[i] * RMSNorm(sum_i h_pre[i] x[b,i,:]) * weight
+ * out [batch, n, hidden] fp32; rms [batch] (may be NULL); coef [2n + n*n]
+ * receives (h_pre, h_post, M) for the backward.
+ * Replaces the static branch of MHCLayer.forward (layer.py:142-170), i.e.
+ * stream_aggregate_fwd + rmsnorm_fwd + sinkhorn_knopp_fwd +
+ * stream_distribute_mix_add_fwd (bindings.cpp:307, 237, 155, 380). */
+int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const float* weight, const float* h_pre,
+                         const float* h_post, const float* h_res, float* out, float* rms, float* coef,
+                         int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
+                         float rmsnorm_eps, void* stream);
+
+size_t mhc_layer_static_bwd_workspace_size(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype);
+
+/* Gradients of the static layer for cotangent grad_out [batch, n, hidden]
+ * fp32: grad_x (x_dtype), grad_weight [hidden] fp32, grad_h_pre/grad_h_post
+ * [n], grad_h_res [n, n] (token-summed).  `coef` is the forward's output.
+ * Replaces the backward chain of the static layer:
+ * stream_distribute_mix_add_bwd, rmsnorm_bwd, stream_aggregate_bwd,
+ * sinkhorn_knopp_bwd (bindings.cpp:418, 268, 340, 189) plus the autograd
+ * expand/exp/sigmoid backward of layer.py:144-160 and ops.py:211, 279-281. */
+int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, const float* weight,
+                         const float* h_pre, const float* h_post, const float* h_res, const float* coef,
+                         void* grad_x, float* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
+                         void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
+                         int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MHC_HIP_H_ */

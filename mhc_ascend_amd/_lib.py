@@ -1,0 +1,114 @@
+"""ctypes binding of libmhc_hip.so (the C ABI declared in include/mhc_hip.h).
+
+The library is loaded lazily on first use.  ``import torch`` happens first so
+that the library's ``libamdhip64.so.7`` dependency resolves to the HIP
+runtime torch already loaded (same SONAME) - one runtime per process, and
+torch's HIP streams are valid handles for the library.
+
+There is no fallback: if the library is missing or fails to load, every op
+raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Dict, List, Tuple
+
+import torch  # noqa: F401  (must precede loading the HIP library)
+
+LIB_NAME = "libmhc_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+F32 = 0
+BF16 = 1
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes).  Must match include/mhc_hip.h (checked by
+# tests/test_abi.py against the header text).
+SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
+    "mhc_abi_version": (ctypes.c_int, []),
+    "mhc_last_error": (ctypes.c_char_p, []),
+    "mhc_timing_enable": (ctypes.c_int, [ctypes.c_int]),
+    "mhc_timing_reset": (ctypes.c_int, []),
+    "mhc_timing_query": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
+    "mhc_sinkhorn_knopp_fwd": (ctypes.c_int, [_vp, _vp, _i64, _i32, _i32, _f32, _vp]),
+    "mhc_sinkhorn_knopp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
+    "mhc_layer_static_fwd": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                            _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
+    "mhc_layer_static_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
+    "mhc_layer_static_bwd": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                            _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load and declare the library (idempotent)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"mhc_ascend_amd: HIP library {LIB_PATH} is not built; run "
+                    "`python -m mhc_ascend_amd.csrc.build` (or __graft_entry__.build())")
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke a status-returning entry point; raise RuntimeError on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.mhc_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Raw hipStream_t of the current torch stream on ``t``'s device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise RuntimeError(f"mhc_ascend_amd: unsupported storage dtype {dt} (float32 or bfloat16)")
+
+
+# ---- kernel timing ----------------------------------------------------------
+
+def timing_enable(on: bool = True) -> None:
+    call("mhc_timing_enable", 1 if on else 0)
+
+
+def timing_reset() -> None:
+    call("mhc_timing_reset")
+
+
+def timing_query(kernel: str) -> Tuple[float, int]:
+    ms = ctypes.c_double(0.0)
+    n = _i64(0)
+    call("mhc_timing_query", kernel.encode(), ctypes.byref(ms), ctypes.byref(n))
+    return ms.value, n.value

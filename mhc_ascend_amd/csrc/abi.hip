@@ -1,0 +1,282 @@
+// C-ABI entry points (include/mhc_hip.h): argument validation, workspace
+// carving and kernel sequencing.  Host code only; kernels live in the other
+// translation units.
+#include <math.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "mhc_hip.h"
+#include "mhc_internal.h"
+
+namespace mhc {
+
+// ---------------------------------------------------------------------------
+// Errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_last_error;
+
+static int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+static int hip_status(hipError_t e) {
+    if (e == hipSuccess) return MHC_SUCCESS;
+    g_last_error = std::string("HIP error: ") + hipGetErrorString(e);
+    return (int)e;
+}
+
+#define MHC_REQUIRE(cond, msg) \
+    do {                       \
+        if (!(cond)) return fail(MHC_ERR_INVALID, msg); \
+    } while (0)
+
+static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
+
+static bool supported_layer_n(int n) { return n == 4; }
+
+// ---------------------------------------------------------------------------
+// Device properties
+// ---------------------------------------------------------------------------
+int device_cu_count() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cache[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cache[dev] = cus;
+    }
+    return cache[dev];
+}
+
+// The row kernels are compiled with __launch_bounds__(512) and chunk counts
+// VPT in {1, 2, 4, 8}; at most 128 floats of row state stay live per thread
+// so that a 512-lane workgroup fits in 256 VGPRs without spilling.
+RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live) {
+    RowTiling best{0, 0};
+    if (C <= 0 || C % wc != 0) return best;
+    const int64_t chunks = C / wc;
+    double best_score = 1e30;
+    for (int vpt = 1; vpt <= 8; vpt *= 2) {
+        if (n_arrays_live * vpt * wc > 128) break;  // live row state per thread (floats)
+        int64_t threads = (chunks + vpt - 1) / vpt;
+        threads = ((threads + 63) / 64) * 64;
+        if (threads > 512) continue;
+        const double waste = (double)(threads * vpt - chunks) / (double)(threads * vpt);
+        const double shape = fabs(log2((double)threads / 256.0)) * 0.02;
+        const double score = waste + shape;
+        if (score < best_score) {
+            best_score = score;
+            best.threads = (int)threads;
+            best.vpt = vpt;
+        }
+    }
+    return best;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel timing registry
+// ---------------------------------------------------------------------------
+struct TimingRecord {
+    std::string name;
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+    bool pending = false;
+};
+
+static std::mutex g_timing_mu;
+static bool g_timing_on = false;
+static std::vector<TimingRecord> g_records;
+static std::unordered_map<std::string, std::pair<double, int64_t>> g_totals;
+
+int timing_begin(const char* name, hipStream_t s) {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    if (!g_timing_on) return -1;
+    int idx = -1;
+    for (size_t i = 0; i < g_records.size(); ++i) {
+        if (!g_records[i].pending) { idx = (int)i; break; }
+    }
+    if (idx < 0) {
+        TimingRecord r;
+        if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return -1;
+        g_records.push_back(r);
+        idx = (int)g_records.size() - 1;
+    }
+    TimingRecord& r = g_records[idx];
+    r.name = name;
+    r.pending = true;
+    hipEventRecord(r.start, s);
+    return idx;
+}
+
+void timing_end(int token, hipStream_t s) {
+    if (token < 0) return;
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    hipEventRecord(g_records[token].stop, s);
+}
+
+static void timing_drain_locked() {
+    for (auto& r : g_records) {
+        if (!r.pending) continue;
+        hipEventSynchronize(r.stop);
+        float ms = 0.f;
+        hipEventElapsedTime(&ms, r.start, r.stop);
+        auto& t = g_totals[r.name];
+        t.first += ms;
+        t.second += 1;
+        r.pending = false;
+    }
+}
+
+}  // namespace mhc
+
+using namespace mhc;
+
+extern "C" {
+
+int mhc_abi_version(void) { return 100; }
+
+const char* mhc_last_error(void) { return g_last_error.c_str(); }
+
+int mhc_timing_enable(int enable) {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    g_timing_on = enable != 0;
+    return MHC_SUCCESS;
+}
+
+int mhc_timing_reset(void) {
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    timing_drain_locked();
+    g_totals.clear();
+    return MHC_SUCCESS;
+}
+
+int mhc_timing_query(const char* kernel, double* total_ms, int64_t* launches) {
+    if (!kernel || !total_ms || !launches) return fail(MHC_ERR_INVALID, "mhc_timing_query: null argument");
+    std::lock_guard<std::mutex> lk(g_timing_mu);
+    timing_drain_locked();
+    auto it = g_totals.find(kernel);
+    *total_ms = it == g_totals.end() ? 0.0 : it->second.first;
+    *launches = it == g_totals.end() ? 0 : it->second.second;
+    return MHC_SUCCESS;
+}
+
+// ---- Sinkhorn ---------------------------------------------------------------
+int mhc_sinkhorn_knopp_fwd(const float* inp, float* out, int64_t batch, int32_t n, int32_t num_iters, float eps,
+                           void* stream) {
+    MHC_REQUIRE(batch >= 0, "sinkhorn_knopp_fwd: batch must be >= 0");
+    MHC_REQUIRE(n >= 1, "sinkhorn_knopp_fwd: n must be >= 1");
+    MHC_REQUIRE(num_iters >= 0, "sinkhorn_knopp_fwd: num_iters must be >= 0");
+    if (batch == 0) return MHC_SUCCESS;
+    MHC_REQUIRE(inp && out, "sinkhorn_knopp_fwd: null pointer");
+    if (n > 8) return fail(MHC_ERR_UNSUPPORTED, "sinkhorn_knopp_fwd: n > 8 is not compiled in this build");
+    return hip_status(launch_sinkhorn_fwd(n, inp, out, batch, num_iters, eps, (hipStream_t)stream));
+}
+
+int mhc_sinkhorn_knopp_bwd(const float* grad_out, const float* inp, const float* out, float* grad_inp,
+                           int64_t batch, int32_t n, int32_t num_iters, float eps, void* stream) {
+    (void)out;
+    MHC_REQUIRE(batch >= 0, "sinkhorn_knopp_bwd: batch must be >= 0");
+    MHC_REQUIRE(n >= 1, "sinkhorn_knopp_bwd: n must be >= 1");
+    MHC_REQUIRE(num_iters >= 0, "sinkhorn_knopp_bwd: num_iters must be >= 0");
+    if (batch == 0) return MHC_SUCCESS;
+    MHC_REQUIRE(grad_out && inp && grad_inp, "sinkhorn_knopp_bwd: null pointer");
+    if (n > 8) return fail(MHC_ERR_UNSUPPORTED, "sinkhorn_knopp_bwd: n > 8 is not compiled in this build");
+    return hip_status(launch_sinkhorn_bwd(n, grad_out, inp, grad_inp, batch, num_iters, eps, (hipStream_t)stream));
+}
+
+// ---- static layer -----------------------------------------------------------
+static int check_layer_shape(const char* fn, int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype,
+                             int32_t num_iters) {
+    if (batch < 0) return fail(MHC_ERR_INVALID, std::string(fn) + ": batch must be >= 0");
+    if (n < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": n must be >= 1");
+    if (hidden < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": hidden must be >= 1");
+    if (num_iters < 0) return fail(MHC_ERR_INVALID, std::string(fn) + ": num_iters must be >= 0");
+    if (!valid_dtype(x_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": x_dtype must be F32 or BF16");
+    if (!supported_layer_n(n))
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) + " is not compiled in this build");
+    const int wc = x_dtype == kBF16 ? 8 : 4;
+    if (hidden % wc != 0)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of " + std::to_string(wc) +
+                                             " for this dtype");
+    const RowTiling t = choose_row_tiling(hidden, wc, 2 * n);
+    if (t.vpt <= 0) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
+    return MHC_SUCCESS;
+}
+
+int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const float* weight, const float* h_pre,
+                         const float* h_post, const float* h_res, float* out, float* rms, float* coef,
+                         int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
+                         float rmsnorm_eps, void* stream) {
+    int st = check_layer_shape("layer_static_fwd", batch, n, hidden, x_dtype, num_iters);
+    if (st) return st;
+    MHC_REQUIRE(weight && h_pre && h_post && h_res && coef, "layer_static_fwd: null parameter pointer");
+    MHC_REQUIRE(batch == 0 || (x && out), "layer_static_fwd: null x/out");
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = launch_static_coef(n, h_pre, h_post, h_res, coef, num_iters, sinkhorn_eps, s);
+    if (e != hipSuccess) return hip_status(e);
+    return hip_status(launch_layer_fwd(x_dtype, n, x, weight, coef, 0, out, rms, batch, hidden, rmsnorm_eps, s));
+}
+
+struct StaticBwdWs {
+    int grid;
+    size_t dw_off, scal_off, total;
+};
+
+static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
+    StaticBwdWs w{};
+    w.grid = batch > 0 ? layer_bwd_grid(x_dtype, n, batch, hidden) : 1;
+    w.dw_off = 0;
+    size_t dw = (size_t)w.grid * hidden * sizeof(float);
+    w.scal_off = (dw + 255) & ~(size_t)255;
+    size_t sc = (size_t)batch * (n * n + 2 * n + 2) * sizeof(float);
+    w.total = w.scal_off + ((sc + 255) & ~(size_t)255);
+    return w;
+}
+
+size_t mhc_layer_static_bwd_workspace_size(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
+    if (batch < 0 || n < 1 || hidden < 1) return 0;
+    return static_bwd_ws(batch, n, hidden, x_dtype).total;
+}
+
+int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, const float* weight,
+                         const float* h_pre, const float* h_post, const float* h_res, const float* coef,
+                         void* grad_x, float* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
+                         void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
+                         int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream) {
+    int st = check_layer_shape("layer_static_bwd", batch, n, hidden, x_dtype, num_iters);
+    if (st) return st;
+    MHC_REQUIRE(weight && h_pre && h_post && h_res && coef, "layer_static_bwd: null parameter pointer");
+    MHC_REQUIRE(grad_weight && grad_h_pre && grad_h_post && grad_h_res, "layer_static_bwd: null gradient pointer");
+    MHC_REQUIRE(batch == 0 || (grad_out && x && grad_x), "layer_static_bwd: null grad_out/x/grad_x");
+    hipStream_t s = (hipStream_t)stream;
+    const StaticBwdWs w = static_bwd_ws(batch, n, hidden, x_dtype);
+    if (batch == 0) {
+        // Empty batch: every gradient is zero (fill kernels, not memsets, so
+        // the call stays capturable in a HIP graph).
+        hipError_t e = launch_fill_zero(grad_weight, hidden, s);
+        if (e == hipSuccess) e = launch_fill_zero(grad_h_pre, n, s);
+        if (e == hipSuccess) e = launch_fill_zero(grad_h_post, n, s);
+        if (e == hipSuccess) e = launch_fill_zero(grad_h_res, (int64_t)n * n, s);
+        return hip_status(e);
+    }
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "layer_static_bwd: workspace smaller than mhc_layer_static_bwd_workspace_size()");
+    float* dw_part = (float*)((char*)workspace + w.dw_off);
+    float* scal_part = (float*)((char*)workspace + w.scal_off);
+    hipError_t e = launch_layer_bwd(x_dtype, n, 0, grad_out, x, weight, coef, 0, grad_x, dw_part, scal_part, w.grid,
+                                    batch, hidden, rmsnorm_eps, s);
+    if (e != hipSuccess) return hip_status(e);
+    e = launch_column_sum(dw_part, w.grid, hidden, grad_weight, s);
+    if (e != hipSuccess) return hip_status(e);
+    return hip_status(launch_static_finalize(n, scal_part, (int)batch, h_pre, h_post, h_res, grad_h_pre, grad_h_post,
+                                             grad_h_res, num_iters, sinkhorn_eps, s));
+}
+
+}  // extern "C"

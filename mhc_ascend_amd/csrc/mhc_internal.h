@@ -1,0 +1,57 @@
+// Host-side declarations shared by the kernel translation units and the
+// C-ABI layer (abi.hip).  Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace mhc {
+
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+inline int dtype_size(int dt) { return dt == kBF16 ? 2 : 4; }
+
+// Per-thread work split of one token row of C channels: `threads` lanes each
+// own `vpt` chunks of `wc` channels (chunk q = k * threads + tid).
+struct RowTiling {
+    int threads;
+    int vpt;
+};
+RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live);
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// Optional per-kernel timing on the launch stream (see mhc_timing_* in the
+// public header).  `begin` returns a token passed to `end`.
+int timing_begin(const char* name, hipStream_t s);
+void timing_end(int token, hipStream_t s);
+
+// ---- layer.hip -------------------------------------------------------------
+hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res, float* coef,
+                              int iters, float sk_eps, hipStream_t s);
+hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
+                            int64_t coef_stride, float* out, float* rms_out, int64_t B, int64_t C, float eps,
+                            hipStream_t s);
+// mode 0: static (writes dx, per-block sums of [dM, dh_post_act, dh_pre_act]
+//         into scal_out[grid][n*n+2n]);
+// mode 1: per-token reduction only (no dx; scal_out[B][n*n+2n+2] holds
+//         dM, dh_post_act, dh_pre_act, inv_rms, k2).
+hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
+                            const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
+                            int grid, int64_t B, int64_t C, float eps, hipStream_t s);
+int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
+hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s);
+hipError_t launch_column_sum(const float* part, int rows, int64_t cols, float* out, hipStream_t s);
+hipError_t launch_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
+                                  const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
+                                  float* d_h_res, int iters, float sk_eps, hipStream_t s);
+
+// ---- sinkhorn.hip ----------------------------------------------------------
+hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batch, int iters, float eps,
+                               hipStream_t s);
+hipError_t launch_sinkhorn_bwd(int n, const float* grad_out, const float* inp, float* grad_inp, int64_t batch,
+                               int iters, float eps, hipStream_t s);
+
+}  // namespace mhc

@@ -1,0 +1,139 @@
+"""Tensor-level host side of the C ABI: the functions of the reference's
+native module ``mhc_ascend`` (bindings.cpp:1020-1117) with the same names,
+argument order and return tuples, plus the fused-layer entry points.
+
+Each function checks devices, shapes and dtypes the way the reference's
+TORCH_CHECKs do (RuntimeError), allocates its outputs with torch's caching
+allocator on the input's device, and enqueues the HIP kernels on torch's
+current stream.  Nothing synchronises.  There is no CPU path: CPU tensors
+raise.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from . import _lib
+from ._lib import call, dtype_code, ptr, stream_of
+
+
+def _check_device(fn: str, *tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(f"{fn}: tensors must be on a HIP device (got {t.device}); "
+                               "mhc_ascend_amd has no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{fn}: all tensors must be on the same device ({dev} vs {t.device})")
+    return dev
+
+
+def _f32c(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.float32).contiguous()
+
+
+# =============================================================================
+# Sinkhorn-Knopp (bindings.cpp:155-231)
+# =============================================================================
+
+def sinkhorn_knopp_fwd(inp: torch.Tensor, num_iters: int = 20, eps: float = 1e-8) -> torch.Tensor:
+    """out = SK(inp) on [B, n, n] fp32 (bindings.cpp:155-187)."""
+    _check_device("sinkhorn_knopp_fwd", inp)
+    if inp.dim() != 3:
+        raise RuntimeError("Input must be 3D tensor [B, M, N]")
+    if inp.size(1) != inp.size(2):
+        raise RuntimeError(f"Sinkhorn-Knopp requires square matrices (M == N), got M={inp.size(1)}, N={inp.size(2)}")
+    if inp.dtype != torch.float32:
+        raise RuntimeError("inp must be float32")
+    inp = inp.contiguous()
+    out = torch.empty_like(inp)
+    with torch.cuda.device(inp.device):
+        call("mhc_sinkhorn_knopp_fwd", ptr(inp), ptr(out), inp.size(0), inp.size(1), int(num_iters), float(eps),
+             stream_of(inp))
+    return out
+
+
+def sinkhorn_knopp_bwd(grad_out: torch.Tensor, inp: torch.Tensor, out: torch.Tensor, num_iters: int = 20,
+                       eps: float = 1e-8) -> torch.Tensor:
+    """Exact VJP of SK at inp (bindings.cpp:189-231)."""
+    _check_device("sinkhorn_knopp_bwd", grad_out, inp, out)
+    for name, t in (("grad_out", grad_out), ("inp", inp), ("out", out)):
+        if t.dtype != torch.float32:
+            raise RuntimeError(f"{name} must be float32")
+    if grad_out.shape != inp.shape:
+        raise RuntimeError("grad_out shape must match inp")
+    if out.shape != inp.shape:
+        raise RuntimeError("out shape must match inp")
+    if inp.dim() != 3 or inp.size(1) != inp.size(2):
+        raise RuntimeError(f"Sinkhorn-Knopp requires square matrices (M == N), got shape {tuple(inp.shape)}")
+    grad_out = grad_out.contiguous()
+    inp = inp.contiguous()
+    grad_inp = torch.empty_like(inp)
+    with torch.cuda.device(inp.device):
+        call("mhc_sinkhorn_knopp_bwd", ptr(grad_out), ptr(inp), 0, ptr(grad_inp), inp.size(0), inp.size(1),
+             int(num_iters), float(eps), stream_of(inp))
+    return grad_inp
+
+
+# =============================================================================
+# Fused static-H layer (layer.py:142-170)
+# =============================================================================
+
+def _layer_x(fn: str, x: torch.Tensor) -> torch.Tensor:
+    if x.dim() != 3:
+        raise RuntimeError(f"{fn}: x must be 3D [B, n, C]")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        x = x.float()
+    return x.contiguous()
+
+
+def mhc_layer_static_fwd(x: torch.Tensor, rmsnorm_weight: torch.Tensor, H_pre: torch.Tensor,
+                         H_post: torch.Tensor, H_res: torch.Tensor, num_iters: int = 20,
+                         sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5
+                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fused static-H forward.  Returns (out fp32 [B,n,C], rms [B], coef [2n+n^2])."""
+    _check_device("mhc_layer_static_fwd", x, rmsnorm_weight, H_pre, H_post, H_res)
+    x = _layer_x("mhc_layer_static_fwd", x)
+    B, n, C = x.shape
+    if rmsnorm_weight.numel() != C or H_pre.numel() != n or H_post.numel() != n or H_res.numel() != n * n:
+        raise RuntimeError("mhc_layer_static_fwd: parameter shapes do not match x [B, n, C]")
+    w, hp, hq, hr = _f32c(rmsnorm_weight), _f32c(H_pre), _f32c(H_post), _f32c(H_res)
+    out = torch.empty((B, n, C), dtype=torch.float32, device=x.device)
+    rms = torch.empty((B,), dtype=torch.float32, device=x.device)
+    coef = torch.empty((2 * n + n * n,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        call("mhc_layer_static_fwd", ptr(x), dtype_code(x.dtype), ptr(w), ptr(hp), ptr(hq), ptr(hr), ptr(out),
+             ptr(rms), ptr(coef), B, n, C, int(num_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
+    return out, rms, coef
+
+
+def mhc_layer_static_bwd(grad_out: torch.Tensor, x: torch.Tensor, rmsnorm_weight: torch.Tensor,
+                         H_pre: torch.Tensor, H_post: torch.Tensor, H_res: torch.Tensor, coef: torch.Tensor,
+                         num_iters: int = 20, sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5):
+    """Fused static-H backward.  Returns (grad_x [x dtype], grad_weight fp32 [C],
+    grad_H_pre [n], grad_H_post [n], grad_H_res [n, n])."""
+    _check_device("mhc_layer_static_bwd", grad_out, x, rmsnorm_weight, H_pre, H_post, H_res, coef)
+    x = _layer_x("mhc_layer_static_bwd", x)
+    B, n, C = x.shape
+    if grad_out.shape != x.shape:
+        raise RuntimeError("mhc_layer_static_bwd: grad_out must match x [B, n, C]")
+    g = _f32c(grad_out)
+    w, hp, hq, hr = _f32c(rmsnorm_weight), _f32c(H_pre), _f32c(H_post), _f32c(H_res)
+    dev = x.device
+    grad_x = torch.empty_like(x)
+    gw = torch.empty((C,), dtype=torch.float32, device=dev)
+    ghp = torch.empty((n,), dtype=torch.float32, device=dev)
+    ghq = torch.empty((n,), dtype=torch.float32, device=dev)
+    ghr = torch.empty((n, n), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        ws_bytes = _lib.load().mhc_layer_static_bwd_workspace_size(B, n, C, dtype_code(x.dtype))
+        ws = torch.empty((max(int(ws_bytes), 1),), dtype=torch.uint8, device=dev)
+        call("mhc_layer_static_bwd", ptr(g), ptr(x), dtype_code(x.dtype), ptr(w), ptr(hp), ptr(hq), ptr(hr),
+             ptr(coef), ptr(grad_x), ptr(gw), ptr(ghp), ptr(ghq), ptr(ghr), ptr(ws), int(ws_bytes), B, n, C,
+             int(num_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
+    return grad_x, gw, ghp, ghq, ghr

@@ -1,0 +1,69 @@
+"""C-ABI surface checks that need no GPU: the library loads, exports every
+function include/mhc_hip.h declares with the ctypes signatures the Python
+binding uses, and rejects bad arguments before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from mhc_ascend_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mhc_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:int|size_t|const char\s*\*)\s*(mhc_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_and_binding_declare_the_same_functions():
+    decl = header_functions()
+    assert decl, "no functions parsed from the header"
+    assert decl == set(_lib.SIGNATURES), (decl ^ set(_lib.SIGNATURES))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_pure_host_entry_points():
+    lib = _lib.load()
+    assert lib.mhc_abi_version() >= 100
+    assert lib.mhc_timing_enable(0) == 0
+    assert isinstance(lib.mhc_last_error(), bytes)
+
+
+@pytest.mark.parametrize("n,iters,batch", [(0, 20, 4), (4, -1, 4), (4, 20, -1)])
+def test_sinkhorn_rejects_bad_arguments_on_host(n, iters, batch):
+    lib = _lib.load()
+    rc = lib.mhc_sinkhorn_knopp_fwd(1, 1, batch, n, iters, 1e-8, None)
+    assert rc == -1
+    assert lib.mhc_last_error()
+
+
+def test_layer_rejects_unsupported_and_invalid_on_host():
+    lib = _lib.load()
+    # n not compiled -> UNSUPPORTED; bad dtype -> INVALID; ragged hidden -> UNSUPPORTED
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 3, 64, 20, 1e-8, 1e-5, None) == -2
+    assert lib.mhc_layer_static_fwd(1, 7, 1, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 4, 66, 20, 1e-8, 1e-5, None) == -2
+    assert b"hidden" in lib.mhc_last_error()
+    # workspace too small
+    assert lib.mhc_layer_static_bwd(1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 8, 4, 64, 20, 1e-8, 1e-5,
+                                    None) == -3
+
+
+def test_cpu_tensors_raise_no_fallback():
+    import mhc_ascend_amd as mhc
+    x = torch.rand(2, 4, 4)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        mhc.sinkhorn_knopp(x)
+    layer = mhc.MHCLayer(16, 4, use_dynamic_h=False)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        layer(torch.randn(3, 4, 16))

@@ -1,0 +1,189 @@
+"""GPU parity: batched Sinkhorn-Knopp and the fused static-H layer against
+the CPU oracle (float64) on identical seeded inputs.
+
+Tolerances: fp32 forward rtol 1e-4 / atol 1e-5;
+gradients rtol 1e-3 with an absolute floor of 1e-5 (per-token tensors) or
+1e-4 (token-summed parameter gradients) times max|ref|; values stored in
+bf16 rtol 2e-2.
+"""
+import pytest
+import torch
+
+import mhc_ascend_amd as mhc
+from mhc_ascend_amd import native
+from oracle import csk
+from oracle import reference as R
+from tests.conftest import assert_close, grad_atol
+
+pytestmark = pytest.mark.gpu
+
+FWD = dict(rtol=1e-4, atol=1e-5)
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------------------
+# Sinkhorn-Knopp
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("iters", [0, 1, 20, 40])
+def test_sinkhorn_fwd_bwd_matches_oracle(device, n, iters):
+    B = 333  # not a multiple of the matrices per wave
+    g = _gen(100 * n + iters)
+    a = torch.exp(torch.randn(B, n, n, generator=g))
+    go = torch.randn(B, n, n, generator=g)
+    ad = a.to(device).requires_grad_(True)
+    out = mhc.sinkhorn_knopp(ad, iters, 1e-8)
+    out.backward(go.to(device))
+    ref = torch.from_numpy(csk.sinkhorn_fwd(a.double().numpy(), iters, 1e-8))
+    gref = torch.from_numpy(csk.sinkhorn_bwd(go.double().numpy(), a.double().numpy(), iters, 1e-8))
+    assert_close(out, ref, what=f"SK fwd n={n} T={iters}", **FWD)
+    assert_close(ad.grad, gref, 1e-3, grad_atol(gref, 1e-5), f"SK bwd n={n} T={iters}")
+
+
+def test_sinkhorn_config_c2_shape(device):
+    """Config C2: [65536, 4, 4] ~ U(0,1), 20 iterations, eps 1e-8."""
+    g = _gen(2)
+    a = torch.rand(65536, 4, 4, generator=g)
+    out = native.sinkhorn_knopp_fwd(a.to(device), 20, 1e-8).cpu()
+    idx = torch.randperm(65536, generator=g)[:2048]
+    ref = torch.from_numpy(csk.sinkhorn_fwd(a[idx].double().numpy(), 20, 1e-8))
+    assert_close(out[idx], ref, what="SK C2 subsample", **FWD)
+    assert_close(out.sum(-2), torch.ones(65536, 4), 0, 1e-5, "SK C2 column sums")
+    go = torch.randn(65536, 4, 4, generator=g)
+    gi = native.sinkhorn_knopp_bwd(go.to(device), a.to(device), out.to(device), 20, 1e-8).cpu()
+    gref = torch.from_numpy(csk.sinkhorn_bwd(go[idx].double().numpy(), a[idx].double().numpy(), 20, 1e-8))
+    assert_close(gi[idx], gref, 1e-3, grad_atol(gref, 1e-5), "SK C2 bwd subsample")
+
+
+def test_sinkhorn_rejects_non_square(device):
+    with pytest.raises(RuntimeError, match="square"):
+        native.sinkhorn_knopp_fwd(torch.rand(4, 3, 4, device=device))
+
+
+# ---------------------------------------------------------------------------
+# Fused static-H layer
+# ---------------------------------------------------------------------------
+
+def _run_static(d, device, iters=20, sk_eps=1e-8, rms_eps=1e-5, grad=None):
+    x = d["x"].to(device).requires_grad_(True)
+    ps = [d[k].to(device).requires_grad_(True) for k in ("weight", "H_pre", "H_post", "H_res")]
+    out = mhc.mhc_layer_static(x, *ps, iters, sk_eps, rms_eps)
+    out.backward((d["grad"] if grad is None else grad).to(device))
+    return out, x.grad, [p.grad for p in ps]
+
+
+def _oracle_static(d, iters=20, sk_eps=1e-8, rms_eps=1e-5, grad=None):
+    x = d["x"].double().requires_grad_(True)
+    ps = [d[k].double().requires_grad_(True) for k in ("weight", "H_pre", "H_post", "H_res")]
+    out = R.mhc_layer_static(x, *ps, iters, sk_eps, rms_eps, dtype=torch.float64)
+    out.backward((d["grad"] if grad is None else grad).double())
+    return out.detach(), x.grad, [p.grad for p in ps]
+
+
+def _check_static(d, got, want, x_bf16=False, tag=""):
+    out, gx, gp = got
+    rout, rgx, rgp = want
+    assert out.dtype == torch.float32
+    assert_close(out, rout, what=f"{tag} out", **FWD)
+    if x_bf16:
+        assert gx.dtype == torch.bfloat16
+        assert_close(gx, rgx, 2e-2, grad_atol(rgx, 1e-2), f"{tag} dx (bf16)")
+    else:
+        assert_close(gx, rgx, 1e-3, grad_atol(rgx, 1e-5), f"{tag} dx")
+    names = ["d_weight", "d_H_pre", "d_H_post", "d_H_res"]
+    for nm, a, e in zip(names, gp, rgp):
+        if nm == "d_weight":
+            # the parameter is bf16 (layer.py:65), so autograd stores a bf16 grad
+            assert_close(a, e, 8e-3, grad_atol(e, 1e-3), f"{tag} {nm}")
+        else:
+            assert_close(a, e, 1e-3, grad_atol(e, 1e-4), f"{tag} {nm}")
+
+
+def test_static_layer_config_c1(device):
+    """Config C1 shape [32, 4, 256] fp32 with the module's default init,
+    checked with loss = sum(y) (the reference benchmark's cotangent) and with
+    a random cotangent (which, unlike sum(y), reaches H_res)."""
+    torch.manual_seed(0)
+    layer = mhc.MHCLayer(256, 4, use_dynamic_h=False)
+    x = torch.randn(32, 4, 256, generator=_gen(0))
+    d = {"x": x, "weight": layer.rmsnorm_weight.data, "H_pre": layer.H_pre.data, "H_post": layer.H_post.data,
+         "H_res": layer.H_res.data, "grad": torch.randn(32, 4, 256, generator=_gen(1))}
+    for grad in (torch.ones(32, 4, 256), d["grad"]):
+        _check_static(d, _run_static(d, device, grad=grad), _oracle_static(d, grad=grad), tag="C1")
+
+
+@pytest.mark.parametrize("B,C", [(1, 64), (7, 256), (64, 1024), (33, 4096), (16, 7168)])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_static_layer_matches_oracle(device, B, C, x_dtype):
+    d = R.static_layer_inputs(B, 4, C, seed=B + C, x_dtype=x_dtype)
+    _check_static(d, _run_static(d, device), _oracle_static(d), x_bf16=x_dtype == torch.bfloat16,
+                  tag=f"B={B} C={C} {x_dtype}")
+
+
+def test_static_layer_module_matches_functional(device):
+    torch.manual_seed(3)
+    layer = mhc.MHCLayer(512, 4, use_dynamic_h=False).to(device)
+    with torch.no_grad():
+        layer.H_pre.normal_()
+        layer.H_post.normal_()
+        layer.H_res.normal_()
+    x = torch.randn(24, 4, 512, generator=_gen(3)).to(device)
+    out = layer(x)
+    ref = R.mhc_layer_static(x.cpu().double(), layer.rmsnorm_weight.cpu().double(), layer.H_pre.cpu().double(),
+                             layer.H_post.cpu().double(), layer.H_res.cpu().double(), 20, 1e-8, 1e-5,
+                             dtype=torch.float64)
+    assert_close(out, ref, what="module", **FWD)
+
+
+def test_static_layer_config_c3_full_size(device):
+    """Config C3 [8192, 4, 4096] fp32: per-token outputs on a token
+    subsample against the oracle; token-summed parameter gradients through
+    additivity (full batch == sum of the two halves) and against the oracle
+    on a 256-token slice."""
+    B, n, C = 8192, 4, 4096
+    d = R.static_layer_inputs(B, n, C, seed=33)
+    out, gx, gp = _run_static(d, device)
+    idx = torch.randperm(B, generator=_gen(5))[:48]
+    sub = {k: (v[idx] if k in ("x", "grad") else v) for k, v in d.items()}
+    rout, rgx, _ = _oracle_static(sub)
+    assert_close(out.detach().cpu()[idx], rout, what="C3 out subsample", **FWD)
+    assert_close(gx.cpu()[idx], rgx, 1e-3, grad_atol(rgx, 1e-5), "C3 dx subsample")
+    halves = [{k: (v[s] if k in ("x", "grad") else v) for k, v in d.items()}
+              for s in (slice(0, B // 2), slice(B // 2, B))]
+    g1 = _run_static(halves[0], device)[2]
+    g2 = _run_static(halves[1], device)[2]
+    for nm, full, a, b in zip(["d_weight", "d_H_pre", "d_H_post", "d_H_res"], gp, g1, g2):
+        s = a.float() + b.float()
+        tol = (8e-3, 1e-3) if nm == "d_weight" else (1e-4, 1e-5)
+        assert_close(full.float(), s, tol[0], grad_atol(s, tol[1]), f"C3 additivity {nm}")
+    sl = {k: (v[:256] if k in ("x", "grad") else v) for k, v in d.items()}
+    _check_static(sl, _run_static(sl, device), _oracle_static(sl), tag="C3 slice")
+
+
+def test_static_layer_native_fp32_weight_grad(device):
+    """The fp32 weight gradient before autograd casts it to the bf16 parameter."""
+    d = R.static_layer_inputs(40, 4, 1024, seed=9)
+    dev = {k: v.to(device) for k, v in d.items()}
+    out, rms, coef = native.mhc_layer_static_fwd(dev["x"], dev["weight"], dev["H_pre"], dev["H_post"], dev["H_res"])
+    gx, gw, ghp, ghq, ghr = native.mhc_layer_static_bwd(dev["grad"], dev["x"], dev["weight"], dev["H_pre"],
+                                                        dev["H_post"], dev["H_res"], coef)
+    _, _, rgp = _oracle_static(d)
+    assert gw.dtype == torch.float32
+    assert_close(gw, rgp[0], 1e-3, grad_atol(rgp[0], 1e-5), "fp32 d_weight")
+    # saved rms and coefficients
+    xa = (torch.sigmoid(d["H_pre"].double())[None, :, None] * d["x"].double()).sum(1)
+    assert_close(rms, torch.sqrt((xa * xa).mean(-1) + 1e-5), 1e-5, 0, "rms")
+    m = R.sinkhorn_knopp(torch.exp(d["H_res"].double()), 20, 1e-8)
+    assert_close(coef[8:].view(4, 4), m, 1e-5, 1e-7, "M")
+
+
+def test_static_layer_empty_batch(device):
+    d = R.static_layer_inputs(0, 4, 256, seed=1)
+    out, gx, gp = _run_static(d, device)
+    assert out.shape == (0, 4, 256) and gx.shape == (0, 4, 256)
+    for gparam in gp:
+        assert float(gparam.float().abs().max()) == 0.0
