@@ -41,7 +41,8 @@ def test_sinkhorn_fwd_bwd_matches_oracle(device, n, iters):
     ref = torch.from_numpy(csk.sinkhorn_fwd(a.double().numpy(), iters, 1e-8))
     gref = torch.from_numpy(csk.sinkhorn_bwd(go.double().numpy(), a.double().numpy(), iters, 1e-8))
     assert_close(out, ref, what=f"SK fwd n={n} T={iters}", **FWD)
-    assert_close(ad.grad, gref, 1e-3, grad_atol(gref, 1e-5), f"SK bwd n={n} T={iters}")
+    # n = 1 (and T = 0 columns) has an analytically ~0 gradient: absolute floor 1e-6
+    assert_close(ad.grad, gref, 1e-3, max(grad_atol(gref, 1e-5), 1e-6), f"SK bwd n={n} T={iters}")
 
 
 def test_sinkhorn_config_c2_shape(device):
@@ -77,10 +78,16 @@ def _run_static(d, device, iters=20, sk_eps=1e-8, rms_eps=1e-5, grad=None):
 
 
 def _oracle_static(d, iters=20, sk_eps=1e-8, rms_eps=1e-5, grad=None):
+    """Oracle outputs and gradients; also the gradient w.r.t. the mixing
+    matrix M (the cotangent entering the Sinkhorn adjoint), which sets the
+    scale of fp32 rounding in d_H_res."""
     x = d["x"].double().requires_grad_(True)
     ps = [d[k].double().requires_grad_(True) for k in ("weight", "H_pre", "H_post", "H_res")]
-    out = R.mhc_layer_static(x, *ps, iters, sk_eps, rms_eps, dtype=torch.float64)
+    m = R.sinkhorn_knopp(torch.exp(ps[3]), iters, sk_eps)
+    m.retain_grad()
+    out = R._layer_core(x, ps[0], torch.sigmoid(ps[1]), 2 * torch.sigmoid(ps[2]), m, rms_eps)
     out.backward((d["grad"] if grad is None else grad).double())
+    _oracle_static.dm_scale = float(m.grad.abs().max())
     return out.detach(), x.grad, [p.grad for p in ps]
 
 
@@ -99,6 +106,11 @@ def _check_static(d, got, want, x_bf16=False, tag=""):
         if nm == "d_weight":
             # the parameter is bf16 (layer.py:65), so autograd stores a bf16 grad
             assert_close(a, e, 8e-3, grad_atol(e, 1e-3), f"{tag} {nm}")
+        elif nm == "d_H_res":
+            # fp32 rounding of the Sinkhorn adjoint scales with |dL/dM|; with
+            # loss = sum(y) the exact d_H_res is 0 (column-constant cotangent)
+            floor = max(grad_atol(e, 1e-4), 1e-7 * getattr(_oracle_static, "dm_scale", 0.0))
+            assert_close(a, e, 1e-3, floor, f"{tag} {nm}")
         else:
             assert_close(a, e, 1e-3, grad_atol(e, 1e-4), f"{tag} {nm}")
 
@@ -152,14 +164,23 @@ def test_static_layer_config_c3_full_size(device):
     rout, rgx, _ = _oracle_static(sub)
     assert_close(out.detach().cpu()[idx], rout, what="C3 out subsample", **FWD)
     assert_close(gx.cpu()[idx], rgx, 1e-3, grad_atol(rgx, 1e-5), "C3 dx subsample")
-    halves = [{k: (v[s] if k in ("x", "grad") else v) for k, v in d.items()}
-              for s in (slice(0, B // 2), slice(B // 2, B))]
-    g1 = _run_static(halves[0], device)[2]
-    g2 = _run_static(halves[1], device)[2]
-    for nm, full, a, b in zip(["d_weight", "d_H_pre", "d_H_post", "d_H_res"], gp, g1, g2):
-        s = a.float() + b.float()
-        tol = (8e-3, 1e-3) if nm == "d_weight" else (1e-4, 1e-5)
-        assert_close(full.float(), s, tol[0], grad_atol(s, tol[1]), f"C3 additivity {nm}")
+    # additivity of the fp32 token-summed gradients (native entry points;
+    # the module's bf16 weight grad would add bf16 rounding of each half)
+    dev = {k: v.to(device) for k, v in d.items()}
+
+    def native_grads(sl_):
+        _, _, coef = native.mhc_layer_static_fwd(dev["x"][sl_], dev["weight"], dev["H_pre"], dev["H_post"],
+                                                 dev["H_res"])
+        return native.mhc_layer_static_bwd(dev["grad"][sl_], dev["x"][sl_], dev["weight"], dev["H_pre"],
+                                           dev["H_post"], dev["H_res"], coef)[1:]
+
+    full = native_grads(slice(0, B))
+    h1 = native_grads(slice(0, B // 2))
+    h2 = native_grads(slice(B // 2, B))
+    for nm, f, a, b in zip(["d_weight", "d_H_pre", "d_H_post", "d_H_res"], full, h1, h2):
+        # the Sinkhorn adjoint is linear in dM, so d_H_res is additive too
+        ssum = a + b
+        assert_close(f, ssum, 1e-4, grad_atol(ssum, 1e-4 if nm == "d_H_res" else 1e-5), f"C3 additivity {nm}")
     sl = {k: (v[:256] if k in ("x", "grad") else v) for k, v in d.items()}
     _check_static(sl, _run_static(sl, device), _oracle_static(sl), tag="C3 slice")
 
