@@ -23,6 +23,19 @@ import sys
 import time
 
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E, AMD public spec
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (calibrated FETCH_SIZE + WRITE_SIZE), or None if not measured."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.md")
+    if not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1]), os.path.relpath(path, ROOT)
+    return None, None
 
 
 def _die(msg: str, code: int = 2):
@@ -168,6 +181,7 @@ def main(argv=None) -> int:
     step_gbps = wl.step_bytes() / (ms_per_step / 1e3) / 1e9
     k_avg_ms = k_ms / max(k_n, 1)
     k_gbps = wl.kernel_bytes() / (k_avg_ms / 1e3) / 1e9 if k_n else None
+    traffic, traffic_src = measured_traffic(wl.kernel, wl.name)
 
     cpu = None
     if a.cpu_seconds > 0:
@@ -201,7 +215,8 @@ def main(argv=None) -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": (k_gbps / PEAK_HBM_GBPS) if k_gbps else None,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "avg_launch_ms": k_avg_ms,
             "launches": k_n,
             "algorithmic_bytes": wl.kernel_bytes(),

@@ -70,32 +70,37 @@ int mhc_sinkhorn_knopp_bwd(const float* grad_out, const float* inp, const float*
                            int64_t batch, int32_t n, int32_t num_iters, float eps, void* stream);
 
 /* ---- fused static-H mHC layer ----------------------------------------------
- * x [batch, n, hidden] (x_dtype), weight [hidden] fp32, h_pre/h_post [n],
- * h_res [n, n] raw (pre-activation) parameters.
+ * x [batch, n, hidden] (x_dtype), weight [hidden] (weight_dtype: the
+ * reference keeps it bf16, layer.py:65), h_pre/h_post [n], h_res [n, n] raw
+ * (pre-activation) fp32 parameters.
  *   h_pre = sigmoid(H_pre), h_post = 2 sigmoid(H_post), M = SK(exp(H_res))
  *   out[b,i,:] = sum_j M[i,j] x[b,j,:] + h_post[i] * RMSNorm(sum_i h_pre[i] x[b,i,:]) * weight
- * out [batch, n, hidden] fp32; rms [batch] (may be NULL); coef [2n + n*n]
- * receives (h_pre, h_post, M) for the backward.
+ * out [batch, n, hidden] fp32; rms [batch] fp32 (may be NULL); `saved`
+ * (mhc_layer_static_saved_size bytes) receives h_pre, h_post, M and the fp32
+ * weight for the backward.
  * Replaces the static branch of MHCLayer.forward (layer.py:142-170), i.e.
  * stream_aggregate_fwd + rmsnorm_fwd + sinkhorn_knopp_fwd +
  * stream_distribute_mix_add_fwd (bindings.cpp:307, 237, 155, 380). */
-int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const float* weight, const float* h_pre,
-                         const float* h_post, const float* h_res, float* out, float* rms, float* coef,
-                         int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
-                         float rmsnorm_eps, void* stream);
+size_t mhc_layer_static_saved_size(int32_t n, int32_t hidden);
+
+int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const void* weight, int32_t weight_dtype,
+                         const float* h_pre, const float* h_post, const float* h_res, float* out, float* rms,
+                         float* saved, int64_t batch, int32_t n, int32_t hidden, int32_t num_iters,
+                         float sinkhorn_eps, float rmsnorm_eps, void* stream);
 
 size_t mhc_layer_static_bwd_workspace_size(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype);
 
 /* Gradients of the static layer for cotangent grad_out [batch, n, hidden]
- * fp32: grad_x (x_dtype), grad_weight [hidden] fp32, grad_h_pre/grad_h_post
- * [n], grad_h_res [n, n] (token-summed).  `coef` is the forward's output.
+ * fp32: grad_x (x_dtype), grad_weight [hidden] (weight_dtype), grad_h_pre /
+ * grad_h_post [n] and grad_h_res [n, n] fp32 (token-summed).  `saved` is the
+ * forward's.  Deterministic (fixed-order reductions, no atomics).
  * Replaces the backward chain of the static layer:
  * stream_distribute_mix_add_bwd, rmsnorm_bwd, stream_aggregate_bwd,
  * sinkhorn_knopp_bwd (bindings.cpp:418, 268, 340, 189) plus the autograd
  * expand/exp/sigmoid backward of layer.py:144-160 and ops.py:211, 279-281. */
-int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, const float* weight,
-                         const float* h_pre, const float* h_post, const float* h_res, const float* coef,
-                         void* grad_x, float* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
+int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, int32_t weight_dtype,
+                         const float* h_pre, const float* h_post, const float* h_res, const float* saved,
+                         void* grad_x, void* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
                          void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
                          int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
 

@@ -18,7 +18,9 @@ from typing import Dict, List, Tuple
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_NAME = "libmhc_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# MHC_HIP_LIB selects another build of the same library (same ABI), e.g. for
+# comparing kernel variants; by default the in-tree build is loaded.
+LIB_PATH = os.environ.get("MHC_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 F32 = 0
 BF16 = 1
@@ -39,10 +41,11 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "mhc_timing_query": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
     "mhc_sinkhorn_knopp_fwd": (ctypes.c_int, [_vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "mhc_sinkhorn_knopp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
-    "mhc_layer_static_fwd": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+    "mhc_layer_static_saved_size": (_sz, [_i32, _i32]),
+    "mhc_layer_static_fwd": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                             _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
     "mhc_layer_static_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
-    "mhc_layer_static_bwd": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp,
+    "mhc_layer_static_bwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp,
                                             _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                             _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
 }

@@ -111,22 +111,22 @@ int timing_begin(const char* name, hipStream_t s) {
     TimingRecord& r = g_records[idx];
     r.name = name;
     r.pending = true;
-    hipEventRecord(r.start, s);
+    (void)hipEventRecord(r.start, s);
     return idx;
 }
 
 void timing_end(int token, hipStream_t s) {
     if (token < 0) return;
     std::lock_guard<std::mutex> lk(g_timing_mu);
-    hipEventRecord(g_records[token].stop, s);
+    (void)hipEventRecord(g_records[token].stop, s);
 }
 
 static void timing_drain_locked() {
     for (auto& r : g_records) {
         if (!r.pending) continue;
-        hipEventSynchronize(r.stop);
+        (void)hipEventSynchronize(r.stop);
         float ms = 0.f;
-        hipEventElapsedTime(&ms, r.start, r.stop);
+        (void)hipEventElapsedTime(&ms, r.start, r.stop);
         auto& t = g_totals[r.name];
         t.first += ms;
         t.second += 1;
@@ -210,33 +210,45 @@ static int check_layer_shape(const char* fn, int64_t batch, int32_t n, int32_t h
     return MHC_SUCCESS;
 }
 
-int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const float* weight, const float* h_pre,
-                         const float* h_post, const float* h_res, float* out, float* rms, float* coef,
-                         int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
-                         float rmsnorm_eps, void* stream) {
+size_t mhc_layer_static_saved_size(int32_t n, int32_t hidden) {
+    if (n < 1 || hidden < 1) return 0;
+    return ((size_t)saved_w_offset(n) + (size_t)hidden) * sizeof(float);
+}
+
+int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const void* weight, int32_t weight_dtype,
+                         const float* h_pre, const float* h_post, const float* h_res, float* out, float* rms,
+                         float* saved, int64_t batch, int32_t n, int32_t hidden, int32_t num_iters,
+                         float sinkhorn_eps, float rmsnorm_eps, void* stream) {
     int st = check_layer_shape("layer_static_fwd", batch, n, hidden, x_dtype, num_iters);
     if (st) return st;
-    MHC_REQUIRE(weight && h_pre && h_post && h_res && coef, "layer_static_fwd: null parameter pointer");
+    MHC_REQUIRE(valid_dtype(weight_dtype), "layer_static_fwd: weight_dtype must be F32 or BF16");
+    MHC_REQUIRE(weight && h_pre && h_post && h_res && saved, "layer_static_fwd: null parameter pointer");
     MHC_REQUIRE(batch == 0 || (x && out), "layer_static_fwd: null x/out");
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = launch_static_coef(n, h_pre, h_post, h_res, coef, num_iters, sinkhorn_eps, s);
+    hipError_t e = launch_static_coef(n, h_pre, h_post, h_res, weight, weight_dtype, hidden, saved, num_iters,
+                                      sinkhorn_eps, s);
     if (e != hipSuccess) return hip_status(e);
-    return hip_status(launch_layer_fwd(x_dtype, n, x, weight, coef, 0, out, rms, batch, hidden, rmsnorm_eps, s));
+    const float* w32 = saved + saved_w_offset(n);
+    return hip_status(launch_layer_fwd(x_dtype, n, x, w32, saved, 0, out, rms, batch, hidden, rmsnorm_eps, s));
 }
+
+// Row groups of the two-stage dw column sum.
+static const int kDwSplit = 16;
 
 struct StaticBwdWs {
     int grid;
-    size_t dw_off, scal_off, total;
+    size_t dw_off, scal_off, stage_off, total;
 };
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
     StaticBwdWs w{};
     w.grid = batch > 0 ? layer_bwd_grid(x_dtype, n, batch, hidden) : 1;
     w.dw_off = 0;
-    size_t dw = (size_t)w.grid * hidden * sizeof(float);
-    w.scal_off = (dw + 255) & ~(size_t)255;
-    size_t sc = (size_t)batch * (n * n + 2 * n + 2) * sizeof(float);
-    w.total = w.scal_off + ((sc + 255) & ~(size_t)255);
+    w.scal_off = align256((size_t)w.grid * hidden * sizeof(float));
+    w.stage_off = w.scal_off + align256((size_t)w.grid * (n * n + 2 * n) * sizeof(float));
+    w.total = w.stage_off + align256((size_t)kDwSplit * hidden * sizeof(float));
     return w;
 }
 
@@ -245,38 +257,41 @@ size_t mhc_layer_static_bwd_workspace_size(int64_t batch, int32_t n, int32_t hid
     return static_bwd_ws(batch, n, hidden, x_dtype).total;
 }
 
-int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, const float* weight,
-                         const float* h_pre, const float* h_post, const float* h_res, const float* coef,
-                         void* grad_x, float* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
+int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, int32_t weight_dtype,
+                         const float* h_pre, const float* h_post, const float* h_res, const float* saved,
+                         void* grad_x, void* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
                          void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
                          int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream) {
     int st = check_layer_shape("layer_static_bwd", batch, n, hidden, x_dtype, num_iters);
     if (st) return st;
-    MHC_REQUIRE(weight && h_pre && h_post && h_res && coef, "layer_static_bwd: null parameter pointer");
+    MHC_REQUIRE(valid_dtype(weight_dtype), "layer_static_bwd: weight_dtype must be F32 or BF16");
+    MHC_REQUIRE(h_pre && h_post && h_res && saved, "layer_static_bwd: null parameter pointer");
     MHC_REQUIRE(grad_weight && grad_h_pre && grad_h_post && grad_h_res, "layer_static_bwd: null gradient pointer");
     MHC_REQUIRE(batch == 0 || (grad_out && x && grad_x), "layer_static_bwd: null grad_out/x/grad_x");
     hipStream_t s = (hipStream_t)stream;
     const StaticBwdWs w = static_bwd_ws(batch, n, hidden, x_dtype);
-    if (batch == 0) {
-        // Empty batch: every gradient is zero (fill kernels, not memsets, so
-        // the call stays capturable in a HIP graph).
-        hipError_t e = launch_fill_zero(grad_weight, hidden, s);
-        if (e == hipSuccess) e = launch_fill_zero(grad_h_pre, n, s);
-        if (e == hipSuccess) e = launch_fill_zero(grad_h_post, n, s);
-        if (e == hipSuccess) e = launch_fill_zero(grad_h_res, (int64_t)n * n, s);
-        return hip_status(e);
-    }
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "layer_static_bwd: workspace smaller than mhc_layer_static_bwd_workspace_size()");
     float* dw_part = (float*)((char*)workspace + w.dw_off);
     float* scal_part = (float*)((char*)workspace + w.scal_off);
-    hipError_t e = launch_layer_bwd(x_dtype, n, 0, grad_out, x, weight, coef, 0, grad_x, dw_part, scal_part, w.grid,
-                                    batch, hidden, rmsnorm_eps, s);
-    if (e != hipSuccess) return hip_status(e);
-    e = launch_column_sum(dw_part, w.grid, hidden, grad_weight, s);
-    if (e != hipSuccess) return hip_status(e);
-    return hip_status(launch_static_finalize(n, scal_part, (int)batch, h_pre, h_post, h_res, grad_h_pre, grad_h_post,
-                                             grad_h_res, num_iters, sinkhorn_eps, s));
+    float* stage = (float*)((char*)workspace + w.stage_off);
+    hipError_t e = hipSuccess;
+    int rows = w.grid;
+    if (batch == 0) {
+        // Empty batch: zero partials (fill kernels, not memsets, so the call
+        // stays capturable in a HIP graph); the finalize then writes zeros.
+        rows = 1;
+        e = launch_fill_zero(dw_part, hidden, s);
+        if (e == hipSuccess) e = launch_fill_zero(scal_part, n * n + 2 * n, s);
+    } else {
+        e = launch_layer_bwd(x_dtype, n, 0, grad_out, x, saved + saved_w_offset(n), saved, 0, grad_x, dw_part,
+                             scal_part, w.grid, batch, hidden, rmsnorm_eps, s);
+    }
+    if (e == hipSuccess) e = launch_column_partial(dw_part, rows, hidden, stage, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(n, weight_dtype, stage, kDwSplit, hidden, grad_weight, scal_part, rows, h_pre,
+                                  h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
+    return hip_status(e);
 }
 
 }  // extern "C"

@@ -28,60 +28,109 @@ template <int N> constexpr int coef_size() { return 2 * N + N * N; }
 
 // ---------------------------------------------------------------------------
 // Static coefficients: h_pre = sigmoid(H_pre), h_post = 2 sigmoid(H_post),
-// M = SK(exp(H_res)) (layer.py:144-160), computed once per call.
+// M = SK(exp(H_res)) (layer.py:144-160), computed once per call, plus the
+// RMSNorm weight converted to fp32.  saved = [coef (2n+n^2) | pad | w32 (C)]
+// with w32 at saved_w_offset(n) floats.
 // ---------------------------------------------------------------------------
-template <int N>
-__global__ __launch_bounds__(64) void static_coef_kernel(const float* __restrict__ h_pre,
-                                                         const float* __restrict__ h_post,
-                                                         const float* __restrict__ h_res, float* __restrict__ coef,
-                                                         int iters, float eps) {
+template <int N, typename TW>
+__global__ __launch_bounds__(256) void static_coef_kernel(const float* __restrict__ h_pre,
+                                                          const float* __restrict__ h_post,
+                                                          const float* __restrict__ h_res,
+                                                          const TW* __restrict__ weight, int C,
+                                                          float* __restrict__ saved, int w_off, int iters,
+                                                          float eps) {
+    if (blockIdx.x > 0) {
+        // weight -> fp32, 8 elements per lane, one pass
+        const int c0 = ((blockIdx.x - 1) * blockDim.x + threadIdx.x) * 8;
+        if (c0 + 8 <= C) {
+            float v[8];
+            load_run<TW, 8>(weight + c0, v);
+            store_run<float, 8>(saved + w_off + c0, v);
+        } else {
+            for (int c = c0; c < C; ++c) saved[w_off + c] = VecIO<TW>::scalar(weight + c);
+        }
+        return;
+    }
+    if (threadIdx.x >= kWave) return;
     const int r = threadIdx.x;
     float a[N];
 #pragma unroll
     for (int c = 0; c < N; ++c) a[c] = (r < N) ? expf(h_res[r * N + c]) : 0.f;
-    sk_forward<N>(a, iters, eps);
+    sk_forward<N>(a, iters, eps, r < N);
     if (r < N) {
-        coef[r] = sigmoidf(h_pre[r]);
-        coef[N + r] = 2.f * sigmoidf(h_post[r]);
+        saved[r] = sigmoidf(h_pre[r]);
+        saved[N + r] = 2.f * sigmoidf(h_post[r]);
 #pragma unroll
-        for (int c = 0; c < N; ++c) coef[2 * N + r * N + c] = a[c];
+        for (int c = 0; c < N; ++c) saved[2 * N + r * N + c] = a[c];
     }
 }
 
 // ---------------------------------------------------------------------------
-// Fused forward.  grid = B workgroups, block = tiling.threads.
+// Token-row I/O: this thread's VPT chunks of WC channels of each of the N
+// streams of one token (chunk q = k * blockDim.x + tid, channel q * WC).
+// NTL selects non-temporal loads.  All streaming rows use them: a plain-load
+// forward is faster in isolation but slows the following backward more than
+// it gains (whole fwd+bwd step measured at n=4, C=4096).
+// ---------------------------------------------------------------------------
+template <typename T, int N, int VPT, int WC, bool NTL>
+__device__ __forceinline__ void load_rows(const T* __restrict__ base, int C, float (&v)[N][VPT][WC]) {
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            if (c0 < C) {
+                if constexpr (NTL) {
+                    load_run_nt<T, WC>(base + (int64_t)i * C + c0, v[i][k]);
+                } else {
+                    load_run<T, WC>(base + (int64_t)i * C + c0, v[i][k]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < WC; ++e) v[i][k][e] = 0.f;
+            }
+        }
+    }
+}
+
+template <int VPT, int WC>
+__device__ __forceinline__ void load_weight(const float* __restrict__ w, int C, float (&wv)[VPT][WC]) {
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        if (c0 < C) {
+            load_run<float, WC>(w + c0, wv[k]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < WC; ++e) wv[k][e] = 0.f;
+        }
+    }
+}
+
+// Workgroup size bound: the prefetching variants hold two token rows and
+// run with up to 256 lanes (512 VGPRs available); the others up to 512.
+#define MHC_ROW_BOUNDS(PF) __attribute__((amdgpu_flat_work_group_size(1, (PF) ? 256 : 512)))
+
+// ---------------------------------------------------------------------------
+// Fused forward.  Persistent workgroups stride over tokens; with PF the next
+// token's rows are loaded into a second register buffer while the current
+// token is reduced and written (the barriers only wait for LDS).
 // ---------------------------------------------------------------------------
 template <typename TX, int N, int VPT>
-__global__ __launch_bounds__(512) void layer_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
-                                                         const float* __restrict__ coef, int64_t coef_stride,
-                                                         float* __restrict__ out, float* __restrict__ rms_out, int C,
-                                                         float eps) {
+__device__ __forceinline__ void fwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
+                                          const float (&wv)[VPT][VecIO<TX>::W],
+                                          const float (&xv)[N][VPT][VecIO<TX>::W], float* __restrict__ out,
+                                          float* __restrict__ rms_out, int C, float eps, float* red) {
     constexpr int WC = VecIO<TX>::W;
     constexpr int NC = coef_size<N>();
-    __shared__ float red[8];
-    const int64_t b = blockIdx.x;
     const float* cf = coef + b * coef_stride;
     float cfv[NC];
 #pragma unroll
     for (int k = 0; k < NC; ++k) cfv[k] = cf[k];
-
-    const TX* xb = x + b * (int64_t)N * C;
-    float xv[N][VPT][WC];
     float xa[VPT][WC];
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-        const bool ok = c0 < C;
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            if (ok) {
-                load_run<TX, WC>(xb + (int64_t)i * C + c0, xv[i][k]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < WC; ++e) xv[i][k][e] = 0.f;
-            }
-        }
 #pragma unroll
         for (int e = 0; e < WC; ++e) {
             float s = 0.f;
@@ -95,17 +144,14 @@ __global__ __launch_bounds__(512) void layer_fwd_kernel(const TX* __restrict__ x
     block_sum<1>(v, red);
     const float r = sqrtf(v[0] / (float)C + eps);
     const float inv = 1.f / r;
-
     float* ob = out + b * (int64_t)N * C;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
         if (c0 < C) {
-            float wv[WC];
-            load_run<float, WC>(w + c0, wv);
             float y[WC];
 #pragma unroll
-            for (int e = 0; e < WC; ++e) y[e] = xa[k][e] * inv * wv[e];
+            for (int e = 0; e < WC; ++e) y[e] = xa[k][e] * inv * wv[k][e];
 #pragma unroll
             for (int i = 0; i < N; ++i) {
                 float o[WC];
@@ -116,143 +162,82 @@ __global__ __launch_bounds__(512) void layer_fwd_kernel(const TX* __restrict__ x
                     for (int j = 0; j < N; ++j) s += cfv[2 * N + i * N + j] * xv[j][k][e];
                     o[e] = s;
                 }
-                store_run<float, WC>(ob + (int64_t)i * C + c0, o);
+                store_run_nt<float, WC>(ob + (int64_t)i * C + c0, o);
             }
         }
     }
     if (threadIdx.x == 0 && rms_out) rms_out[b] = r;
 }
 
+template <typename TX, int N, int VPT, bool PF>
+__global__ MHC_ROW_BOUNDS(PF) void layer_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
+                                                    const float* __restrict__ coef, int64_t coef_stride,
+                                                    float* __restrict__ out, float* __restrict__ rms_out, int64_t B,
+                                                    int C, float eps) {
+    constexpr int WC = VecIO<TX>::W;
+    __shared__ float red[8];
+    float wv[VPT][WC];
+    load_weight<VPT, WC>(w, C, wv);
+    const int64_t G = gridDim.x;
+    const int64_t NCs = (int64_t)N * C;
+    int64_t b = blockIdx.x;
+    if constexpr (PF) {
+        float xA[N][VPT][WC], xB[N][VPT][WC];
+        if (b < B) load_rows<TX, N, VPT, WC, true>(x + b * NCs, C, xA);
+        while (b < B) {
+            const int64_t b1 = b + G;
+            if (b1 < B) load_rows<TX, N, VPT, WC, true>(x + b1 * NCs, C, xB);
+            fwd_token<TX, N, VPT>(b, coef, coef_stride, wv, xA, out, rms_out, C, eps, red);
+            if (b1 >= B) break;
+            const int64_t b2 = b1 + G;
+            if (b2 < B) load_rows<TX, N, VPT, WC, true>(x + b2 * NCs, C, xA);
+            fwd_token<TX, N, VPT>(b1, coef, coef_stride, wv, xB, out, rms_out, C, eps, red);
+            b = b2;
+        }
+    } else {
+        for (; b < B; b += G) {
+            float xv[N][VPT][WC];
+            load_rows<TX, N, VPT, WC, true>(x + b * NCs, C, xv);
+            fwd_token<TX, N, VPT>(b, coef, coef_stride, wv, xv, out, rms_out, C, eps, red);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
-// Fused backward.  Persistent: grid <= B workgroups loop over tokens.
-// Every token's row sums go to scal_out[b][NS + 2] = (dM[n*n],
-// dh_post_act[n], dh_pre_act[n], 1/r, k2 = dot/(C r^3)); dw accumulates in
-// registers per workgroup and is written to dw_part[blockIdx.x][C].
-// MODE 0 (static H) also writes dx; MODE 1 (dynamic H) leaves dx to a later
-// kernel that needs the per-token Sinkhorn backward first.
+// Fused backward.  Persistent workgroups stride over tokens (optionally with
+// the two-buffer prefetch of the forward).  Per token the block forms
+// (dM[n*n], dh_post_act[n], dh_pre_act[n], 1/r, k2 = dot/(C r^3)).  MODE 0
+// (static H) writes dx and sums the first n*n+2n of those over its tokens
+// (thread t keeps entry t in one register) into scal_out[blockIdx.x][n*n+2n];
+// MODE 1 (dynamic H) writes them per token to scal_out[b][n*n+2n+2] and
+// leaves dx to a later kernel that needs the per-token Sinkhorn backward
+// first.  dw accumulates in registers and goes to dw_part[blockIdx.x][C].
 // ---------------------------------------------------------------------------
 template <typename TX, int N, int VPT, int MODE>
-__global__ __launch_bounds__(512) void layer_bwd_kernel(const float* __restrict__ g, const TX* __restrict__ x,
-                                                        const float* __restrict__ w, const float* __restrict__ coef,
-                                                        int64_t coef_stride, TX* __restrict__ dx,
-                                                        float* __restrict__ dw_part, float* __restrict__ scal_out,
-                                                        int64_t B, int C, float eps) {
+__device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
+                                          const float (&wv)[VPT][VecIO<TX>::W],
+                                          const float (&xv)[N][VPT][VecIO<TX>::W],
+                                          const float (&gv)[N][VPT][VecIO<TX>::W],
+                                          float (&dwacc)[VPT][VecIO<TX>::W], float& sacc, TX* __restrict__ dx,
+                                          float* __restrict__ scal_out, int C, float eps, float* red) {
     constexpr int WC = VecIO<TX>::W;
     constexpr int NC = coef_size<N>();
-    constexpr int NS = N * N + 2 * N;              // dM, dh_post_act, dh_pre_act
-    constexpr int NR = 2 + N * N + 3 * N;          // ss, dot, dM, t_i, u_j, v_j
-    __shared__ float red[9 * NR];                   // 8 wave partials + totals
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NR = 2 + N * N + 3 * N;  // ss, dot, dM, t_i, u_j, v_j
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int nwaves = blockDim.x / kWave;
     float* tot = red + 8 * NR;
-
-    float wv[VPT][WC];
-    float dwacc[VPT][WC];
+    const float* cf = coef + b * coef_stride;
+    float cfv[NC];
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-        if (c0 < C) {
-            load_run<float, WC>(w + c0, wv[k]);
-        } else {
+    for (int k = 0; k < NC; ++k) cfv[k] = cf[k];
+    {
+        float rv[NR];
 #pragma unroll
-            for (int e = 0; e < WC; ++e) wv[k][e] = 0.f;
-        }
-#pragma unroll
-        for (int e = 0; e < WC; ++e) dwacc[k][e] = 0.f;
-    }
-
-    for (int64_t b = blockIdx.x; b < B; b += gridDim.x) {
-        const float* cf = coef + b * coef_stride;
-        float cfv[NC];
-#pragma unroll
-        for (int k = 0; k < NC; ++k) cfv[k] = cf[k];
-
-        const TX* xb = x + b * (int64_t)N * C;
-        const float* gb = g + b * (int64_t)N * C;
-        float xv[N][VPT][WC];
-        float gv[N][VPT][WC];
+        for (int k = 0; k < NR; ++k) rv[k] = 0.f;
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
-            const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-            const bool ok = c0 < C;
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-                if (ok) {
-                    load_run<TX, WC>(xb + (int64_t)i * C + c0, xv[i][k]);
-                    load_run<float, WC>(gb + (int64_t)i * C + c0, gv[i][k]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < WC; ++e) { xv[i][k][e] = 0.f; gv[i][k][e] = 0.f; }
-                }
-            }
-        }
-
-        {
-            float rv[NR];
-#pragma unroll
-            for (int k = 0; k < NR; ++k) rv[k] = 0.f;
-#pragma unroll
-            for (int k = 0; k < VPT; ++k) {
-#pragma unroll
-                for (int e = 0; e < WC; ++e) {
-                    float xa = 0.f, gy = 0.f;
-#pragma unroll
-                    for (int i = 0; i < N; ++i) {
-                        xa += cfv[i] * xv[i][k][e];
-                        gy += cfv[N + i] * gv[i][k][e];
-                    }
-                    const float wgy = wv[k][e] * gy;
-                    const float wxa = wv[k][e] * xa;
-                    rv[0] += xa * xa;
-                    rv[1] += wgy * xa;
-#pragma unroll
-                    for (int i = 0; i < N; ++i) {
-#pragma unroll
-                        for (int j = 0; j < N; ++j) rv[2 + i * N + j] += gv[i][k][e] * xv[j][k][e];
-                        rv[2 + N * N + i] += gv[i][k][e] * wxa;
-                        rv[2 + N * N + N + i] += wgy * xv[i][k][e];
-                        rv[2 + N * N + 2 * N + i] += xa * xv[i][k][e];
-                    }
-                }
-            }
-            wave_sum<NR>(rv);
-            if (lane == 0) {
-#pragma unroll
-                for (int k = 0; k < NR; ++k) red[wave * NR + k] = rv[k];
-            }
-        }
-        __syncthreads();
-        if (threadIdx.x < NR) {
-            float s = 0.f;
-            for (int q = 0; q < nwaves; ++q) s += red[q * NR + threadIdx.x];
-            tot[threadIdx.x] = s;
-        }
-        __syncthreads();
-        const float r = sqrtf(tot[0] / (float)C + eps);
-        const float inv = 1.f / r;
-        const float k2 = tot[1] * inv * inv * inv / (float)C;
-
-        if (threadIdx.x < NS + 2) {
-            const int t = threadIdx.x;
-            float v;
-            if (t < N * N) {
-                v = tot[2 + t];
-            } else if (t < N * N + N) {
-                v = tot[2 + t] * inv;                                   // dh_post_act = (sum G_i xa w) / r
-            } else if (t < NS) {
-                const int j = t - N * N - N;
-                v = inv * tot[2 + N * N + N + j] - k2 * tot[2 + N * N + 2 * N + j];  // dh_pre_act
-            } else {
-                v = (t == NS) ? inv : k2;
-            }
-            scal_out[b * (NS + 2) + t] = v;
-        }
-
-#pragma unroll
-        for (int k = 0; k < VPT; ++k) {
-            const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-            float gxa[WC];
 #pragma unroll
             for (int e = 0; e < WC; ++e) {
                 float xa = 0.f, gy = 0.f;
@@ -261,24 +246,140 @@ __global__ __launch_bounds__(512) void layer_bwd_kernel(const float* __restrict_
                     xa += cfv[i] * xv[i][k][e];
                     gy += cfv[N + i] * gv[i][k][e];
                 }
-                gxa[e] = wv[k][e] * gy * inv - xa * k2;
-                dwacc[k][e] += gy * xa * inv;
-            }
-            if (MODE == 0 && c0 < C) {
-                TX* db = dx + b * (int64_t)N * C;
+                const float wgy = wv[k][e] * gy;
+                const float wxa = wv[k][e] * xa;
+                rv[0] += xa * xa;
+                rv[1] += wgy * xa;
 #pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    float d[WC];
+                for (int i = 0; i < N; ++i) {
 #pragma unroll
-                    for (int e = 0; e < WC; ++e) {
-                        float s = cfv[j] * gxa[e];
-#pragma unroll
-                        for (int i = 0; i < N; ++i) s += cfv[2 * N + i * N + j] * gv[i][k][e];
-                        d[e] = s;
-                    }
-                    store_run<TX, WC>(db + (int64_t)j * C + c0, d);
+                    for (int j = 0; j < N; ++j) rv[2 + i * N + j] += gv[i][k][e] * xv[j][k][e];
+                    rv[2 + N * N + i] += gv[i][k][e] * wxa;
+                    rv[2 + N * N + N + i] += wgy * xv[i][k][e];
+                    rv[2 + N * N + 2 * N + i] += xa * xv[i][k][e];
                 }
             }
+        }
+        wave_sum_last<NR>(rv);
+        if (lane == kWave - 1) {
+#pragma unroll
+            for (int k = 0; k < NR; ++k) red[wave * NR + k] = rv[k];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < NR) {
+        float s = 0.f;
+        for (int q = 0; q < nwaves; ++q) s += red[q * NR + threadIdx.x];
+        tot[threadIdx.x] = s;
+    }
+    __syncthreads();
+    const float r = sqrtf(tot[0] / (float)C + eps);
+    const float inv = 1.f / r;
+    const float k2 = tot[1] * inv * inv * inv / (float)C;
+
+    if (threadIdx.x < NS + 2) {
+        const int t = threadIdx.x;
+        float v;
+        if (t < N * N) {
+            v = tot[2 + t];
+        } else if (t < N * N + N) {
+            v = tot[2 + t] * inv;  // dh_post_act = (sum G_i xa w) / r
+        } else if (t < NS) {
+            const int j = t - N * N - N;
+            v = inv * tot[2 + N * N + N + j] - k2 * tot[2 + N * N + 2 * N + j];  // dh_pre_act
+        } else {
+            v = (t == NS) ? inv : k2;
+        }
+        if (MODE == 0) {
+            sacc += v;
+        } else {
+            scal_out[b * (NS + 2) + t] = v;
+        }
+    }
+
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        float gxa[WC];
+#pragma unroll
+        for (int e = 0; e < WC; ++e) {
+            float xa = 0.f, gy = 0.f;
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                xa += cfv[i] * xv[i][k][e];
+                gy += cfv[N + i] * gv[i][k][e];
+            }
+            gxa[e] = wv[k][e] * gy * inv - xa * k2;
+            dwacc[k][e] += gy * xa * inv;
+        }
+        if (MODE == 0 && c0 < C) {
+            TX* db = dx + b * (int64_t)N * C;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float d[WC];
+#pragma unroll
+                for (int e = 0; e < WC; ++e) {
+                    float s = cfv[j] * gxa[e];
+#pragma unroll
+                    for (int i = 0; i < N; ++i) s += cfv[2 * N + i * N + j] * gv[i][k][e];
+                    d[e] = s;
+                }
+                store_run_nt<TX, WC>(db + (int64_t)j * C + c0, d);
+            }
+        }
+    }
+}
+
+template <typename TX, int N, int VPT, int MODE, bool PF>
+__global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g, const TX* __restrict__ x,
+                                                    const float* __restrict__ w, const float* __restrict__ coef,
+                                                    int64_t coef_stride, TX* __restrict__ dx,
+                                                    float* __restrict__ dw_part, float* __restrict__ scal_out,
+                                                    int64_t B, int C, float eps) {
+    constexpr int WC = VecIO<TX>::W;
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NR = 2 + N * N + 3 * N;
+    __shared__ float red[9 * NR];  // 8 wave partials + totals
+    float wv[VPT][WC];
+    load_weight<VPT, WC>(w, C, wv);
+    float dwacc[VPT][WC];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+#pragma unroll
+        for (int e = 0; e < WC; ++e) dwacc[k][e] = 0.f;
+    }
+    float sacc = 0.f;
+    const int64_t G = gridDim.x;
+    const int64_t NCs = (int64_t)N * C;
+    int64_t b = blockIdx.x;
+    if constexpr (PF) {
+        float xA[N][VPT][WC], gA[N][VPT][WC], xB[N][VPT][WC], gB[N][VPT][WC];
+        if (b < B) {
+            load_rows<TX, N, VPT, WC, true>(x + b * NCs, C, xA);
+            load_rows<float, N, VPT, WC, true>(g + b * NCs, C, gA);
+        }
+        while (b < B) {
+            const int64_t b1 = b + G;
+            if (b1 < B) {
+                load_rows<TX, N, VPT, WC, true>(x + b1 * NCs, C, xB);
+                load_rows<float, N, VPT, WC, true>(g + b1 * NCs, C, gB);
+            }
+            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xA, gA, dwacc, sacc, dx, scal_out, C, eps, red);
+            if (b1 >= B) break;
+            const int64_t b2 = b1 + G;
+            if (b2 < B) {
+                load_rows<TX, N, VPT, WC, true>(x + b2 * NCs, C, xA);
+                load_rows<float, N, VPT, WC, true>(g + b2 * NCs, C, gA);
+            }
+            bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xB, gB, dwacc, sacc, dx, scal_out, C, eps, red);
+            b = b2;
+        }
+    } else {
+        for (; b < B; b += G) {
+            float xv[N][VPT][WC], gv[N][VPT][WC];
+            load_rows<TX, N, VPT, WC, true>(x + b * NCs, C, xv);
+            load_rows<float, N, VPT, WC, true>(g + b * NCs, C, gv);
+            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, C, eps, red);
         }
     }
 
@@ -288,77 +389,118 @@ __global__ __launch_bounds__(512) void layer_bwd_kernel(const float* __restrict_
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
         if (c0 < C) store_run<float, WC>(dwp + c0, dwacc[k]);
     }
+    if (MODE == 0 && threadIdx.x < NS) scal_out[(int64_t)blockIdx.x * NS + threadIdx.x] = sacc;
 }
 
 // ---------------------------------------------------------------------------
-// out[c] = sum_r part[r][c]   (fixed order -> deterministic)
-// grid = ceil(cols / 64), block = 256: wave w sums rows w, w+4, ...
+// Deterministic column sums of per-workgroup partials part[rows][cols]:
+// stage 1 (grid = col tiles of 256 x rsplit row groups) writes
+// stage[rsplit][cols]; the finalize kernel sums the rsplit rows.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ part, int rows, int64_t cols,
-                                                         float* __restrict__ out) {
-    __shared__ float red[4][64];
+__global__ __launch_bounds__(256) void column_partial_kernel(const float* __restrict__ part, int rows,
+                                                             int64_t cols, float* __restrict__ stage) {
+    __shared__ float4 red[4][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t c = (int64_t)blockIdx.x * 64 + lane;
-    float s = 0.f;
+    const int64_t c = (int64_t)blockIdx.x * 256 + lane * 4;
+    const int r0 = (int)((int64_t)rows * blockIdx.y / gridDim.y);
+    const int r1 = (int)((int64_t)rows * (blockIdx.y + 1) / gridDim.y);
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (c < cols) {
-        for (int r = wave; r < rows; r += 4) s += part[(int64_t)r * cols + c];
+        int r = r0 + wave;
+        // 8 independent loads in flight per step; fixed summation order
+        for (; r + 28 < r1; r += 32) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(part + (int64_t)(r + 4 * u) * cols + c);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { s.x += v[u].x; s.y += v[u].y; s.z += v[u].z; s.w += v[u].w; }
+        }
+        for (; r < r1; r += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(part + (int64_t)r * cols + c);
+            s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+        }
     }
     red[wave][lane] = s;
     __syncthreads();
-    if (wave == 0 && c < cols) out[c] = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+    if (wave == 0 && c < cols) {
+        float4 t = red[0][lane];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) {
+            t.x += red[q][lane].x; t.y += red[q][lane].y; t.z += red[q][lane].z; t.w += red[q][lane].w;
+        }
+        *reinterpret_cast<float4*>(stage + (int64_t)blockIdx.y * cols + c) = t;
+    }
 }
 
-// ---------------------------------------------------------------------------
-// Static parameter gradients: sum the per-token [dM, dh_post_act, dh_pre_act],
-// apply the activation derivatives (ops.py:211, 279-281) and one Sinkhorn
-// backward on the token-summed dM (SK is shared, so its VJP is linear in dM):
+// Blocks [0, ceil(cols/256)) finish the dw sum (rsplit staged rows) and
+// store it in the weight's dtype.  With N > 0 the last block also forms the
+// static parameter gradients from the per-workgroup sums of
+// [dM, dh_post_act, dh_pre_act]: the activation derivatives (ops.py:211,
+// 279-281) and ONE Sinkhorn backward on the token-summed dM (M is shared, so
+// its VJP is linear in dM):
 //     dH_pre = dh_pre_act h_pre (1 - h_pre)
 //     dH_post = dh_post_act h_post (1 - h_post / 2)
 //     dH_res = SK^T(dM) * exp(H_res)
-// ---------------------------------------------------------------------------
-template <int N>
-__global__ __launch_bounds__(256) void static_finalize_kernel(const float* __restrict__ part, int rows,
-                                                              const float* __restrict__ h_pre,
-                                                              const float* __restrict__ h_post,
-                                                              const float* __restrict__ h_res, float* d_h_pre,
-                                                              float* d_h_post, float* d_h_res, int iters,
-                                                              float eps) {
-    constexpr int NS = N * N + 2 * N;
-    __shared__ float red[4 * NS];
-    float v[NS];
+constexpr int kColSplit = 16;  // max row groups of the two-stage column sum
+
+template <int N, typename TW>
+__global__ __launch_bounds__(256) void layer_finalize_kernel(
+    const float* __restrict__ stage, int rsplit, int64_t cols, TW* __restrict__ dw,
+    const float* __restrict__ scal_part, int rows, const float* __restrict__ h_pre,
+    const float* __restrict__ h_post, const float* __restrict__ h_res, float* __restrict__ d_h_pre,
+    float* __restrict__ d_h_post, float* __restrict__ d_h_res, int iters, float eps) {
+    const int col_blocks = (int)((cols + 255) / 256);
+    if ((int)blockIdx.x < col_blocks) {
+        const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        if (c < cols) {
+            float v[kColSplit];
 #pragma unroll
-    for (int k = 0; k < NS; ++k) v[k] = 0.f;
-    for (int r = threadIdx.x; r < rows; r += blockDim.x) {
-#pragma unroll
-        for (int k = 0; k < NS; ++k) v[k] += part[(int64_t)r * (NS + 2) + k];
-    }
-    block_sum<NS>(v, red);
-    if (threadIdx.x < 64) {
-        const int r = threadIdx.x;
-        float e[N], gm[N];
-#pragma unroll
-        for (int c = 0; c < N; ++c) {
-            e[c] = (r < N) ? expf(h_res[r * N + c]) : 0.f;
+            for (int r = 0; r < kColSplit; ++r) v[r] = (r < rsplit) ? stage[(int64_t)r * cols + c] : 0.f;
             float s = 0.f;
 #pragma unroll
-            for (int q = 0; q < N; ++q) s = (r == q) ? v[q * N + c] : s;
-            gm[c] = (r < N) ? s : 0.f;
+            for (int r = 0; r < kColSplit; ++r) s += v[r];
+            VecIO<TW>::put(dw + c, s);
         }
-        sk_backward<N>(gm, e, iters, eps);
-        if (r < N) {
+        return;
+    }
+    if constexpr (N > 0) {
+        constexpr int NS = N * N + 2 * N;
+        __shared__ float red[4 * NS];
+        float v[NS];
 #pragma unroll
-            for (int c = 0; c < N; ++c) d_h_res[r * N + c] = gm[c] * e[c];
-            float hp = 0.f, hq = 0.f, tp = 0.f, tq = 0.f;
+        for (int k = 0; k < NS; ++k) v[k] = 0.f;
+        for (int r = threadIdx.x; r < rows; r += blockDim.x) {
 #pragma unroll
-            for (int q = 0; q < N; ++q) {
-                hp = (r == q) ? v[N * N + N + q] : hp;
-                hq = (r == q) ? v[N * N + q] : hq;
+            for (int k = 0; k < NS; ++k) v[k] += scal_part[(int64_t)r * NS + k];
+        }
+        block_sum<NS>(v, red);
+        if (threadIdx.x < kWave) {
+            const int r = threadIdx.x;
+            float e[N], gm[N];
+#pragma unroll
+            for (int c = 0; c < N; ++c) {
+                e[c] = (r < N) ? expf(h_res[r * N + c]) : 0.f;
+                float s = 0.f;
+#pragma unroll
+                for (int q = 0; q < N; ++q) s = (r == q) ? v[q * N + c] : s;
+                gm[c] = (r < N) ? s : 0.f;
             }
-            tp = sigmoidf(h_pre[r]);
-            tq = 2.f * sigmoidf(h_post[r]);
-            d_h_pre[r] = hp * tp * (1.f - tp);
-            d_h_post[r] = hq * tq * (1.f - tq * 0.5f);
+            sk_backward<N>(gm, e, iters, eps, r < N);
+            if (r < N) {
+#pragma unroll
+                for (int c = 0; c < N; ++c) d_h_res[r * N + c] = gm[c] * e[c];
+                float hp = 0.f, hq = 0.f;
+#pragma unroll
+                for (int q = 0; q < N; ++q) {
+                    hp = (r == q) ? v[N * N + N + q] : hp;
+                    hq = (r == q) ? v[N * N + q] : hq;
+                }
+                const float tp = sigmoidf(h_pre[r]);
+                const float tq = 2.f * sigmoidf(h_post[r]);
+                d_h_pre[r] = hp * tp * (1.f - tp);
+                d_h_post[r] = hq * tq * (1.f - tq * 0.5f);
+            }
         }
     }
 }
@@ -398,12 +540,93 @@ constexpr bool row_fits(int n_arrays, int vpt) {
     return n_arrays * vpt * VecIO<TX>::W <= 128;
 }
 
-hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res, float* coef,
-                              int iters, float sk_eps, hipStream_t s) {
-    MHC_DISPATCH_N(n, hipLaunchKernelGGL((static_coef_kernel<N_>), dim3(1), dim3(64), 0, s, h_pre, h_post, h_res,
-                                         coef, iters, sk_eps));
+int saved_w_offset(int n) { return ((2 * n + n * n + 63) / 64) * 64; }
+
+hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res,
+                              const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
+                              hipStream_t s) {
+    const int off = saved_w_offset(n);
+    const unsigned blocks = 1 + (unsigned)((C + 2047) / 2048);
+    if (w_dtype == kBF16) {
+        MHC_DISPATCH_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, bf16_t>), dim3(blocks), dim3(256), 0, s,
+                                             h_pre, h_post, h_res, (const bf16_t*)weight, (int)C, saved, off, iters,
+                                             sk_eps));
+    } else {
+        MHC_DISPATCH_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, float>), dim3(blocks), dim3(256), 0, s,
+                                             h_pre, h_post, h_res, (const float*)weight, (int)C, saved, off, iters,
+                                             sk_eps));
+    }
     return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// Persistent row kernels: pick the instantiation, size the grid from its
+// occupancy (resident workgroups per CU x CUs, capped by the token count).
+// ---------------------------------------------------------------------------
+#define MHC_PICK_VPT(v, ...)                                     \
+    switch (v) {                                                 \
+        case 1: { constexpr int V_ = 1; __VA_ARGS__; break; }    \
+        case 2: { constexpr int V_ = 2; __VA_ARGS__; break; }    \
+        case 4: { constexpr int V_ = 4; __VA_ARGS__; break; }    \
+        case 8: { constexpr int V_ = 8; __VA_ARGS__; break; }    \
+        default: break;                                          \
+    }
+
+template <typename TX, int N, int V, bool PF>
+static const void* fwd_fn() {
+    if constexpr (row_fits<TX>(N, V)) return reinterpret_cast<const void*>(&layer_fwd_kernel<TX, N, V, PF>);
+    return nullptr;
+}
+
+template <typename TX, int N, int V, int MODE, bool PF>
+static const void* bwd_fn() {
+    if constexpr (row_fits<TX>(2 * N, V)) return reinterpret_cast<const void*>(&layer_bwd_kernel<TX, N, V, MODE, PF>);
+    return nullptr;
+}
+
+static const void* pick_fwd(int x_dtype, int n, int vpt, bool pf) {
+    const void* fn = nullptr;
+    if (n != 4) return nullptr;
+    constexpr int N_ = 4;
+    if (x_dtype == kBF16) {
+        MHC_PICK_VPT(vpt, fn = pf ? fwd_fn<bf16_t, N_, V_, true>() : fwd_fn<bf16_t, N_, V_, false>());
+    } else {
+        MHC_PICK_VPT(vpt, fn = pf ? fwd_fn<float, N_, V_, true>() : fwd_fn<float, N_, V_, false>());
+    }
+    return fn;
+}
+
+static const void* pick_bwd(int x_dtype, int n, int vpt, int mode, bool pf) {
+    const void* fn = nullptr;
+    if (n != 4) return nullptr;
+    constexpr int N_ = 4;
+#define MHC_BWD_FN(TX_) \
+    MHC_PICK_VPT(vpt, fn = mode == 0 ? (pf ? bwd_fn<TX_, N_, V_, 0, true>() : bwd_fn<TX_, N_, V_, 0, false>()) \
+                                     : (pf ? bwd_fn<TX_, N_, V_, 1, true>() : bwd_fn<TX_, N_, V_, 1, false>()))
+    if (x_dtype == kBF16) {
+        MHC_BWD_FN(bf16_t);
+    } else {
+        MHC_BWD_FN(float);
+    }
+#undef MHC_BWD_FN
+    return fn;
+}
+
+static int persistent_grid(const void* fn, int threads, int64_t B) {
+    int per_cu = 0;
+    if (fn == nullptr || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess ||
+        per_cu < 1) {
+        (void)hipGetLastError();
+        per_cu = 1;
+    }
+    int64_t g = (int64_t)device_cu_count() * per_cu;
+    if (g > B) g = B;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+// Workgroups of <= 256 lanes run the two-buffer prefetch variant.
+static bool use_prefetch(const RowTiling& t) { return t.threads <= 256; }
 
 hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
                             int64_t coef_stride, float* out, float* rms_out, int64_t B, int64_t C, float eps,
@@ -412,29 +635,23 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
     const int wc = x_dtype == kBF16 ? 8 : 4;
     const RowTiling t = choose_row_tiling(C, wc, n);
     if (t.vpt <= 0) return hipErrorInvalidValue;
+    const void* fn = pick_fwd(x_dtype, n, t.vpt, use_prefetch(t));
+    if (!fn) return hipErrorInvalidValue;
+    const int grid = persistent_grid(fn, t.threads, B);
+    int Ci = (int)C;
+    void* args[] = {(void*)&x, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&out, (void*)&rms_out,
+                    (void*)&B, (void*)&Ci, (void*)&eps};
     const int tok = timing_begin("layer_fwd", s);
-#define MHC_FWD_LAUNCH(TX_)                                                                                     \
-    MHC_DISPATCH_N(n, MHC_DISPATCH_VPT(t.vpt, if constexpr (row_fits<TX_>(N_, V_)) {                              \
-        hipLaunchKernelGGL((layer_fwd_kernel<TX_, N_, V_>), dim3(B), dim3(t.threads), 0, s, (const TX_*)x, w, coef, \
-                           coef_stride, out, rms_out, (int)C, eps);                                                \
-    } else { return hipErrorInvalidValue; }))
-    if (x_dtype == kBF16) { MHC_FWD_LAUNCH(bf16_t); } else { MHC_FWD_LAUNCH(float); }
-#undef MHC_FWD_LAUNCH
+    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
-    return hipGetLastError();
+    return e != hipSuccess ? e : hipGetLastError();
 }
 
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
     const int wc = x_dtype == kBF16 ? 8 : 4;
     const RowTiling t = choose_row_tiling(C, wc, 2 * n);
-    const int waves = (t.threads + 63) / 64;
-    // Aim for ~8 resident waves per CU; the row state makes occupancy
-    // register-bound, so more workgroups only add dw partials.
-    int per_cu = waves >= 8 ? 1 : 8 / waves;
-    int64_t g = (int64_t)device_cu_count() * per_cu;
-    if (g > B) g = B;
-    if (g < 1) g = 1;
-    return (int)g;
+    if (t.vpt <= 0) return 1;
+    return persistent_grid(pick_bwd(x_dtype, n, t.vpt, 0, use_prefetch(t)), t.threads, B);
 }
 
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
@@ -443,33 +660,45 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
     const int wc = x_dtype == kBF16 ? 8 : 4;
     const RowTiling t = choose_row_tiling(C, wc, 2 * n);
     if (t.vpt <= 0) return hipErrorInvalidValue;
+    const void* fn = pick_bwd(x_dtype, n, t.vpt, mode, use_prefetch(t));
+    if (!fn) return hipErrorInvalidValue;
+    int Ci = (int)C;
+    void* args[] = {(void*)&g, (void*)&x, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&dx,
+                    (void*)&dw_part, (void*)&scal_out, (void*)&B, (void*)&Ci, (void*)&eps};
     const int tok = timing_begin(mode == 0 ? "layer_bwd" : "layer_bwd_reduce", s);
-#define MHC_BWD_LAUNCH(TX_, MODE_)                                                                               \
-    MHC_DISPATCH_N(n, MHC_DISPATCH_VPT(t.vpt, if constexpr (row_fits<TX_>(2 * N_, V_)) {                          \
-        hipLaunchKernelGGL((layer_bwd_kernel<TX_, N_, V_, MODE_>), dim3(grid), dim3(t.threads), 0, s, g,          \
-                           (const TX_*)x, w, coef, coef_stride, (TX_*)dx, dw_part, scal_out, B, (int)C, eps);      \
-    } else { return hipErrorInvalidValue; }))
-    if (x_dtype == kBF16) {
-        if (mode == 0) { MHC_BWD_LAUNCH(bf16_t, 0); } else { MHC_BWD_LAUNCH(bf16_t, 1); }
-    } else {
-        if (mode == 0) { MHC_BWD_LAUNCH(float, 0); } else { MHC_BWD_LAUNCH(float, 1); }
-    }
-#undef MHC_BWD_LAUNCH
+    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
-    return hipGetLastError();
+    return e != hipSuccess ? e : hipGetLastError();
 }
 
-hipError_t launch_column_sum(const float* part, int rows, int64_t cols, float* out, hipStream_t s) {
+hipError_t launch_column_partial(const float* part, int rows, int64_t cols, float* stage, int rsplit,
+                                 hipStream_t s) {
     if (cols == 0) return hipSuccess;
-    hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)((cols + 63) / 64)), dim3(256), 0, s, part, rows, cols, out);
+    hipLaunchKernelGGL(column_partial_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
+                       rows, cols, stage);
     return hipGetLastError();
 }
 
-hipError_t launch_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
-                                  const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                  float* d_h_res, int iters, float sk_eps, hipStream_t s) {
-    MHC_DISPATCH_N(n, hipLaunchKernelGGL((static_finalize_kernel<N_>), dim3(1), dim3(256), 0, s, scal_part, rows,
-                                         h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps));
+hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsplit, int64_t cols, void* dw,
+                                 const float* scal_part, int rows, const float* h_pre, const float* h_post,
+                                 const float* h_res, float* d_h_pre, float* d_h_post, float* d_h_res, int iters,
+                                 float sk_eps, hipStream_t s) {
+    const unsigned col_blocks = (unsigned)((cols + 255) / 256);
+    const unsigned blocks = col_blocks + (n > 0 ? 1 : 0);
+    if (blocks == 0) return hipSuccess;
+#define MHC_FIN_LAUNCH(N_, TW_)                                                                                  \
+    hipLaunchKernelGGL((layer_finalize_kernel<N_, TW_>), dim3(blocks), dim3(256), 0, s, stage, rsplit, cols,      \
+                       (TW_*)dw, scal_part, rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps)
+    if (n == 0) {
+        if (w_dtype == kBF16) { MHC_FIN_LAUNCH(0, bf16_t); } else { MHC_FIN_LAUNCH(0, float); }
+    } else {
+        if (w_dtype == kBF16) {
+            MHC_DISPATCH_N(n, MHC_FIN_LAUNCH(N_, bf16_t));
+        } else {
+            MHC_DISPATCH_N(n, MHC_FIN_LAUNCH(N_, float));
+        }
+    }
+#undef MHC_FIN_LAUNCH
     return hipGetLastError();
 }
 

@@ -69,6 +69,63 @@ template <> struct VecIO<bf16_t> {
     __device__ __forceinline__ static void put(bf16_t* p, float v) { *p = f32_to_bf16(v); }
 };
 
+// Non-temporal 16-byte accesses (the `nt` bit: streaming data that will not
+// be re-read soon).
+__device__ __forceinline__ uint4 ld16_nt(const void* p) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    return make_uint4(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1),
+                      __builtin_nontemporal_load(q + 2), __builtin_nontemporal_load(q + 3));
+}
+__device__ __forceinline__ void st16_nt(void* p, uint4 v) {
+    uint32_t* q = reinterpret_cast<uint32_t*>(p);
+    __builtin_nontemporal_store(v.x, q);
+    __builtin_nontemporal_store(v.y, q + 1);
+    __builtin_nontemporal_store(v.z, q + 2);
+    __builtin_nontemporal_store(v.w, q + 3);
+}
+
+// Streaming (non-temporal) runs of WN elements, WN a multiple of 16 bytes.
+template <typename T, int WN>
+__device__ __forceinline__ void load_run_nt(const T* p, float (&v)[WN]) {
+    constexpr int PER = 16 / sizeof(T);
+    static_assert(WN % PER == 0, "non-temporal runs are whole 16-byte pieces");
+#pragma unroll
+    for (int s = 0; s < WN / PER; ++s) {
+        const uint4 q = ld16_nt(p + s * PER);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[s * PER + e] = __uint_as_float(w[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[s * PER + 2 * e] = __uint_as_float(w[e] << 16);
+                v[s * PER + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+            }
+        }
+    }
+}
+
+template <typename T, int WN>
+__device__ __forceinline__ void store_run_nt(T* p, const float (&v)[WN]) {
+    constexpr int PER = 16 / sizeof(T);
+    static_assert(WN % PER == 0, "non-temporal runs are whole 16-byte pieces");
+#pragma unroll
+    for (int s = 0; s < WN / PER; ++s) {
+        uint32_t w[4];
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(v[s * PER + e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = static_cast<uint32_t>(f32_to_bf16(v[s * PER + 2 * e])) |
+                       (static_cast<uint32_t>(f32_to_bf16(v[s * PER + 2 * e + 1])) << 16);
+        }
+        st16_nt(p + s * PER, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+}
+
 // Load/store W_OUT-wide runs of element type T from/to a float array by
 // splitting into 16-byte pieces (W_OUT must be a multiple of VecIO<T>::W,
 // or VecIO<T>::W a multiple of W_OUT with a scalar fallback).
@@ -116,15 +173,58 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[WN]) {
 }
 
 // ---------------------------------------------------------------------------
-// Reductions
+// Reductions.  Cross-lane steps inside 16-lane rows use DPP (quad_perm,
+// row_half_mirror, row_mirror); rows are combined with row_bcast15/31 (all
+// GFX9-family DPP controls, available on gfx950).
 // ---------------------------------------------------------------------------
+namespace dpp {
+constexpr int kQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141; // lane i <- lane 7-i within 8
+constexpr int kRowMirror = 0x140;     // lane i <- lane 15-i within 16
+constexpr int kRowBcast15 = 0x142;    // lane 15 of row r -> row r+1
+constexpr int kRowBcast31 = 0x143;    // lane 31 -> rows 2, 3
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+}  // namespace dpp
+
+// Sum over the aligned group of G lanes containing this lane (G a power of
+// two dividing 64); every lane of the group receives the group total.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (G >= 2) v += dpp::mov<dpp::kQuadXor1>(v);
+    if constexpr (G >= 4) v += dpp::mov<dpp::kQuadXor2>(v);
+    if constexpr (G >= 8) v += dpp::mov<dpp::kRowHalfMirror>(v);
+    if constexpr (G >= 16) v += dpp::mov<dpp::kRowMirror>(v);
+    if constexpr (G >= 32) v += __shfl_xor(v, 16, kWave);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+// Wave total of NV values; valid in lane 63 only.
+template <int NV>
+__device__ __forceinline__ void wave_sum_last(float (&v)[NV]) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        float x = v[i];
+        x += dpp::mov<dpp::kQuadXor1>(x);
+        x += dpp::mov<dpp::kQuadXor2>(x);
+        x += dpp::mov<dpp::kRowHalfMirror>(x);
+        x += dpp::mov<dpp::kRowMirror>(x);
+        x += dpp::mov<dpp::kRowBcast15, 0xA>(x);
+        x += dpp::mov<dpp::kRowBcast31, 0xC>(x);
+        v[i] = x;
+    }
+}
+
+// Wave total of NV values in every lane.
 template <int NV>
 __device__ __forceinline__ void wave_sum(float (&v)[NV]) {
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] += __shfl_xor(v[i], off, kWave);
-    }
+    for (int i = 0; i < NV; ++i) v[i] = group_sum<kWave>(v[i]);
 }
 
 // Sum NV values over the whole block; every thread receives the totals.
@@ -132,11 +232,11 @@ __device__ __forceinline__ void wave_sum(float (&v)[NV]) {
 // back-to-back calls may reuse the same `lds`.
 template <int NV>
 __device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
-    wave_sum<NV>(v);
+    wave_sum_last<NV>(v);
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int nwaves = blockDim.x / kWave;
-    if (lane == 0) {
+    if (lane == kWave - 1) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) lds[wave * NV + i] = v[i];
     }
@@ -150,50 +250,49 @@ __device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
     __syncthreads();
 }
 
-// Sum over the aligned group of G lanes containing this lane (G a power of
-// two dividing 64).
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 constexpr int pow2ceil(int n) { return n <= 1 ? 1 : 2 * pow2ceil((n + 1) / 2); }
 
+// 1/d from the hardware reciprocal (v_rcp_f32, ~1 ulp) refined by one
+// Newton-Raphson step r' = r + r (1 - d r).  Unlike IEEE division it does not
+// serialise on VCC, so independent reciprocals overlap.
+__device__ __forceinline__ float rcp_nr(float d) {
+    const float r = __builtin_amdgcn_rcpf(d);
+    const float e = fmaf(-d, r, 1.0f);
+    return fmaf(r, e, r);
+}
+
 // ---------------------------------------------------------------------------
 // Sinkhorn-Knopp on an N x N matrix held one row per lane in a group of
-// G = pow2ceil(N) lanes (lanes r >= N hold zero rows and stay zero).
+// G = pow2ceil(N) lanes.  Lanes with active == false (padding rows r >= N)
+// hold zero rows, stay zero and contribute nothing to column sums.
 // Forward (ops_pytorch_backward.py:9-33): T times, A = X/(rowsum+eps),
-// Y = A/(colsum+eps).  All divisions are IEEE.
+// Y = A/(colsum+eps); each row / column scale is one Newton-refined
+// reciprocal applied by multiplication.
 // ---------------------------------------------------------------------------
 template <int N>
-__device__ __forceinline__ void sk_row_step(float (&a)[N], float eps, float& rs) {
+__device__ __forceinline__ void sk_row_step(float (&a)[N], float eps, bool active, float& rinv) {
     float s = 0.f;
 #pragma unroll
     for (int c = 0; c < N; ++c) s += a[c];
-    rs = s + eps;
+    rinv = active ? rcp_nr(s + eps) : 0.f;
 #pragma unroll
-    for (int c = 0; c < N; ++c) a[c] = a[c] / rs;
+    for (int c = 0; c < N; ++c) a[c] *= rinv;
 }
 
 template <int N>
 __device__ __forceinline__ void sk_col_step(float (&a)[N], float eps) {
     constexpr int G = pow2ceil(N);
 #pragma unroll
-    for (int c = 0; c < N; ++c) {
-        const float cs = group_sum<G>(a[c]) + eps;
-        a[c] = a[c] / cs;
-    }
+    for (int c = 0; c < N; ++c) a[c] *= rcp_nr(group_sum<G>(a[c]) + eps);
 }
 
 template <int N>
-__device__ __forceinline__ void sk_forward(float (&a)[N], int iters, float eps) {
+__device__ __forceinline__ void sk_forward(float (&a)[N], int iters, float eps, bool active) {
     for (int t = 0; t < iters; ++t) {
-        float rs;
-        sk_row_step<N>(a, eps, rs);
+        float rinv;
+        sk_row_step<N>(a, eps, active, rinv);
         sk_col_step<N>(a, eps);
     }
 }
@@ -202,43 +301,44 @@ __device__ __forceinline__ void sk_forward(float (&a)[N], int iters, float eps) 
 template <int N> struct SkHist { static constexpr int TMAX = (N <= 4) ? 32 : (N <= 8 ? 12 : 0); };
 
 // Exact adjoint of sk_forward (lane holds row r of grad_out in `g`, row r of
-// the forward input in `x0`; on return `g` holds row r of grad_inp).
+// the forward input in `x0`; on return `g` holds row r of grad_inp).  With
+// A the post-row-step matrix of an iteration, cs its column sums + eps and
+// rinv = 1/(rowsum + eps) of the row step:
 //   column step: dA[r][c] = (dY[r][c] - sum_r' dY[r'][c] Y[r'][c]) / cs[c]
-//   row step:    dX[r][c] = (dA[r][c] - sum_c' dA[r][c'] A[r][c']) / rs[r]
-// For iters <= TMAX the post-row-step rows A_t and row sums rs_t of every
-// iteration stay in registers; otherwise each iteration's state is
-// recomputed from x0 (O(iters^2) work, no history).
+//   row step:    dX[r][c] = (dA[r][c] - sum_c' dA[r][c'] A[r][c']) * rinv[r]
+// For iters <= TMAX the rows A_t and rinv_t of every iteration stay in
+// registers; otherwise each iteration's state is recomputed from x0
+// (O(iters^2) work, no history).
 template <int N>
-__device__ __forceinline__ void sk_adjoint_step(float (&g)[N], const float (&A)[N], float rs, float eps) {
+__device__ __forceinline__ void sk_adjoint_step(float (&g)[N], const float (&A)[N], float rinv, float eps) {
     constexpr int G = pow2ceil(N);
     float dA[N];
 #pragma unroll
     for (int c = 0; c < N; ++c) {
-        const float cs = group_sum<G>(A[c]) + eps;
-        const float y = A[c] / cs;
-        const float dot = group_sum<G>(g[c] * y);
-        dA[c] = (g[c] - dot) / cs;
+        const float cinv = rcp_nr(group_sum<G>(A[c]) + eps);
+        const float dot = group_sum<G>(g[c] * (A[c] * cinv));
+        dA[c] = (g[c] - dot) * cinv;
     }
     float rdot = 0.f;
 #pragma unroll
     for (int c = 0; c < N; ++c) rdot += dA[c] * A[c];
 #pragma unroll
-    for (int c = 0; c < N; ++c) g[c] = (dA[c] - rdot) / rs;
+    for (int c = 0; c < N; ++c) g[c] = (dA[c] - rdot) * rinv;
 }
 
 template <int N>
-__device__ __forceinline__ void sk_backward(float (&g)[N], const float (&x0)[N], int iters, float eps) {
+__device__ __forceinline__ void sk_backward(float (&g)[N], const float (&x0)[N], int iters, float eps, bool active) {
     constexpr int TMAX = SkHist<N>::TMAX;
     if (TMAX > 0 && iters <= TMAX) {
         float hA[TMAX > 0 ? TMAX : 1][N];
-        float hrs[TMAX > 0 ? TMAX : 1];
+        float hr[TMAX > 0 ? TMAX : 1];
         float a[N];
 #pragma unroll
         for (int c = 0; c < N; ++c) a[c] = x0[c];
 #pragma unroll
         for (int t = 0; t < TMAX; ++t) {
             if (t < iters) {
-                sk_row_step<N>(a, eps, hrs[t]);
+                sk_row_step<N>(a, eps, active, hr[t]);
 #pragma unroll
                 for (int c = 0; c < N; ++c) hA[t][c] = a[c];
                 sk_col_step<N>(a, eps);
@@ -246,19 +346,19 @@ __device__ __forceinline__ void sk_backward(float (&g)[N], const float (&x0)[N],
         }
 #pragma unroll
         for (int t = TMAX - 1; t >= 0; --t) {
-            if (t < iters) sk_adjoint_step<N>(g, hA[t], hrs[t], eps);
+            if (t < iters) sk_adjoint_step<N>(g, hA[t], hr[t], eps);
         }
     } else {
         for (int t = iters - 1; t >= 0; --t) {
             float a[N];
 #pragma unroll
             for (int c = 0; c < N; ++c) a[c] = x0[c];
-            float rs = 0.f;
+            float rinv = 0.f;
             for (int s = 0; s <= t; ++s) {
-                sk_row_step<N>(a, eps, rs);
+                sk_row_step<N>(a, eps, active, rinv);
                 if (s < t) sk_col_step<N>(a, eps);
             }
-            sk_adjoint_step<N>(g, a, rs, eps);
+            sk_adjoint_step<N>(g, a, rinv, eps);
         }
     }
 }

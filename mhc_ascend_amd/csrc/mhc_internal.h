@@ -29,13 +29,16 @@ int timing_begin(const char* name, hipStream_t s);
 void timing_end(int token, hipStream_t s);
 
 // ---- layer.hip -------------------------------------------------------------
-hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res, float* coef,
-                              int iters, float sk_eps, hipStream_t s);
+// saved = [coef (2n + n^2) | pad | fp32 weight (C)], weight at saved_w_offset(n) floats
+int saved_w_offset(int n);
+hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res,
+                              const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
+                              hipStream_t s);
 hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
                             int64_t coef_stride, float* out, float* rms_out, int64_t B, int64_t C, float eps,
                             hipStream_t s);
-// mode 0: static (writes dx, per-block sums of [dM, dh_post_act, dh_pre_act]
-//         into scal_out[grid][n*n+2n]);
+// mode 0: static (writes dx, per-workgroup sums of [dM, dh_post_act,
+//         dh_pre_act] into scal_out[grid][n*n+2n]);
 // mode 1: per-token reduction only (no dx; scal_out[B][n*n+2n+2] holds
 //         dM, dh_post_act, dh_pre_act, inv_rms, k2).
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
@@ -43,10 +46,15 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
                             int grid, int64_t B, int64_t C, float eps, hipStream_t s);
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s);
-hipError_t launch_column_sum(const float* part, int rows, int64_t cols, float* out, hipStream_t s);
-hipError_t launch_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
-                                  const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                  float* d_h_res, int iters, float sk_eps, hipStream_t s);
+// Two-stage deterministic column sum of part[rows][cols]: stage[rsplit][cols].
+hipError_t launch_column_partial(const float* part, int rows, int64_t cols, float* stage, int rsplit,
+                                 hipStream_t s);
+// dw = sum of the rsplit staged rows (stored as w_dtype); with n > 0 also the
+// static parameter gradients from scal_part[rows][n*n+2n].
+hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsplit, int64_t cols, void* dw,
+                                 const float* scal_part, int rows, const float* h_pre, const float* h_post,
+                                 const float* h_res, float* d_h_pre, float* d_h_post, float* d_h_res, int iters,
+                                 float sk_eps, hipStream_t s);
 
 // ---- sinkhorn.hip ----------------------------------------------------------
 hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batch, int iters, float eps,

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void sinkhorn_fwd_kernel(const float* __restri
 #pragma unroll
         for (int c = 0; c < N; ++c) a[c] = 0.f;
     }
-    sk_forward<N>(a, iters, eps);
+    sk_forward<N>(a, iters, eps, ok);
     if (ok) store_row<N>(out + m * N * N + r * N, a);
 }
 
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const float* __restri
 #pragma unroll
         for (int c = 0; c < N; ++c) { x0[c] = 0.f; g[c] = 0.f; }
     }
-    sk_backward<N>(g, x0, iters, eps);
+    sk_backward<N>(g, x0, iters, eps, ok);
     if (ok) store_row<N>(grad_inp + m * N * N + r * N, g);
 }
 

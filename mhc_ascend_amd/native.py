@@ -92,48 +92,60 @@ def _layer_x(fn: str, x: torch.Tensor) -> torch.Tensor:
     return x.contiguous()
 
 
+def _weight(w: torch.Tensor) -> torch.Tensor:
+    if w.dtype not in (torch.float32, torch.bfloat16):
+        w = w.float()
+    return w.contiguous()
+
+
 def mhc_layer_static_fwd(x: torch.Tensor, rmsnorm_weight: torch.Tensor, H_pre: torch.Tensor,
                          H_post: torch.Tensor, H_res: torch.Tensor, num_iters: int = 20,
                          sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5
                          ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Fused static-H forward.  Returns (out fp32 [B,n,C], rms [B], coef [2n+n^2])."""
+    """Fused static-H forward.  Returns (out fp32 [B,n,C], rms [B], saved)
+    where ``saved`` holds (h_pre, h_post, M, fp32 weight) for the backward;
+    ``saved[:2n+n*n]`` are the activated coefficients."""
     _check_device("mhc_layer_static_fwd", x, rmsnorm_weight, H_pre, H_post, H_res)
     x = _layer_x("mhc_layer_static_fwd", x)
     B, n, C = x.shape
     if rmsnorm_weight.numel() != C or H_pre.numel() != n or H_post.numel() != n or H_res.numel() != n * n:
         raise RuntimeError("mhc_layer_static_fwd: parameter shapes do not match x [B, n, C]")
-    w, hp, hq, hr = _f32c(rmsnorm_weight), _f32c(H_pre), _f32c(H_post), _f32c(H_res)
+    w = _weight(rmsnorm_weight)
+    hp, hq, hr = _f32c(H_pre), _f32c(H_post), _f32c(H_res)
     out = torch.empty((B, n, C), dtype=torch.float32, device=x.device)
     rms = torch.empty((B,), dtype=torch.float32, device=x.device)
-    coef = torch.empty((2 * n + n * n,), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    saved = torch.empty((lib.mhc_layer_static_saved_size(n, C) // 4,), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
-        call("mhc_layer_static_fwd", ptr(x), dtype_code(x.dtype), ptr(w), ptr(hp), ptr(hq), ptr(hr), ptr(out),
-             ptr(rms), ptr(coef), B, n, C, int(num_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
-    return out, rms, coef
+        call("mhc_layer_static_fwd", ptr(x), dtype_code(x.dtype), ptr(w), dtype_code(w.dtype), ptr(hp), ptr(hq),
+             ptr(hr), ptr(out), ptr(rms), ptr(saved), B, n, C, int(num_iters), float(sinkhorn_eps),
+             float(rmsnorm_eps), stream_of(x))
+    return out, rms, saved
 
 
 def mhc_layer_static_bwd(grad_out: torch.Tensor, x: torch.Tensor, rmsnorm_weight: torch.Tensor,
-                         H_pre: torch.Tensor, H_post: torch.Tensor, H_res: torch.Tensor, coef: torch.Tensor,
+                         H_pre: torch.Tensor, H_post: torch.Tensor, H_res: torch.Tensor, saved: torch.Tensor,
                          num_iters: int = 20, sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5):
-    """Fused static-H backward.  Returns (grad_x [x dtype], grad_weight fp32 [C],
-    grad_H_pre [n], grad_H_post [n], grad_H_res [n, n])."""
-    _check_device("mhc_layer_static_bwd", grad_out, x, rmsnorm_weight, H_pre, H_post, H_res, coef)
+    """Fused static-H backward.  Returns (grad_x [x dtype], grad_weight
+    [C, weight dtype], grad_H_pre [n], grad_H_post [n], grad_H_res [n, n])."""
+    _check_device("mhc_layer_static_bwd", grad_out, x, rmsnorm_weight, H_pre, H_post, H_res, saved)
     x = _layer_x("mhc_layer_static_bwd", x)
     B, n, C = x.shape
     if grad_out.shape != x.shape:
         raise RuntimeError("mhc_layer_static_bwd: grad_out must match x [B, n, C]")
     g = _f32c(grad_out)
-    w, hp, hq, hr = _f32c(rmsnorm_weight), _f32c(H_pre), _f32c(H_post), _f32c(H_res)
+    wdt = rmsnorm_weight.dtype if rmsnorm_weight.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    hp, hq, hr = _f32c(H_pre), _f32c(H_post), _f32c(H_res)
     dev = x.device
     grad_x = torch.empty_like(x)
-    gw = torch.empty((C,), dtype=torch.float32, device=dev)
+    gw = torch.empty((C,), dtype=wdt, device=dev)
     ghp = torch.empty((n,), dtype=torch.float32, device=dev)
     ghq = torch.empty((n,), dtype=torch.float32, device=dev)
     ghr = torch.empty((n, n), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         ws_bytes = _lib.load().mhc_layer_static_bwd_workspace_size(B, n, C, dtype_code(x.dtype))
         ws = torch.empty((max(int(ws_bytes), 1),), dtype=torch.uint8, device=dev)
-        call("mhc_layer_static_bwd", ptr(g), ptr(x), dtype_code(x.dtype), ptr(w), ptr(hp), ptr(hq), ptr(hr),
-             ptr(coef), ptr(grad_x), ptr(gw), ptr(ghp), ptr(ghq), ptr(ghr), ptr(ws), int(ws_bytes), B, n, C,
-             int(num_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
+        call("mhc_layer_static_bwd", ptr(g), ptr(x), dtype_code(x.dtype), dtype_code(wdt), ptr(hp), ptr(hq),
+             ptr(hr), ptr(saved), ptr(grad_x), ptr(gw), ptr(ghp), ptr(ghq), ptr(ghr), ptr(ws), int(ws_bytes), B, n,
+             C, int(num_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
     return grad_x, gw, ghp, ghq, ghr

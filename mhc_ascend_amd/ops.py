@@ -58,16 +58,16 @@ class MHCLayerStaticFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, rmsnorm_weight, H_pre, H_post, H_res, num_iters: int, sinkhorn_eps: float,
                 rmsnorm_eps: float):
-        out, _rms, coef = native.mhc_layer_static_fwd(x, rmsnorm_weight, H_pre, H_post, H_res, num_iters,
-                                                      sinkhorn_eps, rmsnorm_eps)
-        ctx.save_for_backward(x, rmsnorm_weight, H_pre, H_post, H_res, coef)
+        out, _rms, saved = native.mhc_layer_static_fwd(x, rmsnorm_weight, H_pre, H_post, H_res, num_iters,
+                                                       sinkhorn_eps, rmsnorm_eps)
+        ctx.save_for_backward(x, rmsnorm_weight, H_pre, H_post, H_res, saved)
         ctx.cfg = (num_iters, sinkhorn_eps, rmsnorm_eps)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        x, w, hp, hq, hr, coef = ctx.saved_tensors
-        gx, gw, ghp, ghq, ghr = native.mhc_layer_static_bwd(grad_out, x, w, hp, hq, hr, coef, *ctx.cfg)
+        x, w, hp, hq, hr, saved = ctx.saved_tensors
+        gx, gw, ghp, ghq, ghr = native.mhc_layer_static_bwd(grad_out, x, w, hp, hq, hr, saved, *ctx.cfg)
         return gx.to(x.dtype), gw, ghp.view_as(hp), ghq.view_as(hq), ghr.view_as(hr), None, None, None
 
 

@@ -50,13 +50,15 @@ def test_sinkhorn_rejects_bad_arguments_on_host(n, iters, batch):
 def test_layer_rejects_unsupported_and_invalid_on_host():
     lib = _lib.load()
     # n not compiled -> UNSUPPORTED; bad dtype -> INVALID; ragged hidden -> UNSUPPORTED
-    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 3, 64, 20, 1e-8, 1e-5, None) == -2
-    assert lib.mhc_layer_static_fwd(1, 7, 1, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
-    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 4, 66, 20, 1e-8, 1e-5, None) == -2
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 3, 64, 20, 1e-8, 1e-5, None) == -2
+    assert lib.mhc_layer_static_fwd(1, 7, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 5, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 66, 20, 1e-8, 1e-5, None) == -2
     assert b"hidden" in lib.mhc_last_error()
     # workspace too small
     assert lib.mhc_layer_static_bwd(1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 8, 4, 64, 20, 1e-8, 1e-5,
                                     None) == -3
+    assert lib.mhc_layer_static_saved_size(4, 256) == (64 + 256) * 4
 
 
 def test_cpu_tensors_raise_no_fallback():

@@ -41,8 +41,25 @@ def test_sinkhorn_fwd_bwd_matches_oracle(device, n, iters):
     ref = torch.from_numpy(csk.sinkhorn_fwd(a.double().numpy(), iters, 1e-8))
     gref = torch.from_numpy(csk.sinkhorn_bwd(go.double().numpy(), a.double().numpy(), iters, 1e-8))
     assert_close(out, ref, what=f"SK fwd n={n} T={iters}", **FWD)
-    # n = 1 (and T = 0 columns) has an analytically ~0 gradient: absolute floor 1e-6
+    # n = 1 has an analytically ~0 gradient: absolute floor 1e-6
     assert_close(ad.grad, gref, 1e-3, max(grad_atol(gref, 1e-5), 1e-6), f"SK bwd n={n} T={iters}")
+
+
+@pytest.mark.parametrize("n", [3, 5, 6, 7])
+def test_sinkhorn_padded_groups_with_zero_eps(device, n):
+    """n that is not a power of two leaves padding lanes in each lane group;
+    with eps = 0 they must not divide by zero into the real rows' sums."""
+    g = _gen(7 + n)
+    a = torch.exp(torch.randn(100, n, n, generator=g))
+    go = torch.randn(100, n, n, generator=g)
+    ad = a.to(device).requires_grad_(True)
+    out = mhc.sinkhorn_knopp(ad, 20, 0.0)
+    out.backward(go.to(device))
+    ref = torch.from_numpy(csk.sinkhorn_fwd(a.double().numpy(), 20, 0.0))
+    gref = torch.from_numpy(csk.sinkhorn_bwd(go.double().numpy(), a.double().numpy(), 20, 0.0))
+    assert bool(torch.isfinite(out).all()) and bool(torch.isfinite(ad.grad).all())
+    assert_close(out, ref, what=f"SK fwd eps=0 n={n}", **FWD)
+    assert_close(ad.grad, gref, 1e-3, max(grad_atol(gref, 1e-5), 1e-6), f"SK bwd eps=0 n={n}")
 
 
 def test_sinkhorn_config_c2_shape(device):
@@ -169,10 +186,10 @@ def test_static_layer_config_c3_full_size(device):
     dev = {k: v.to(device) for k, v in d.items()}
 
     def native_grads(sl_):
-        _, _, coef = native.mhc_layer_static_fwd(dev["x"][sl_], dev["weight"], dev["H_pre"], dev["H_post"],
-                                                 dev["H_res"])
-        return native.mhc_layer_static_bwd(dev["grad"][sl_], dev["x"][sl_], dev["weight"], dev["H_pre"],
-                                           dev["H_post"], dev["H_res"], coef)[1:]
+        w32 = dev["weight"].float()
+        _, _, saved = native.mhc_layer_static_fwd(dev["x"][sl_], w32, dev["H_pre"], dev["H_post"], dev["H_res"])
+        return native.mhc_layer_static_bwd(dev["grad"][sl_], dev["x"][sl_], w32, dev["H_pre"],
+                                           dev["H_post"], dev["H_res"], saved)[1:]
 
     full = native_grads(slice(0, B))
     h1 = native_grads(slice(0, B // 2))
@@ -189,9 +206,10 @@ def test_static_layer_native_fp32_weight_grad(device):
     """The fp32 weight gradient before autograd casts it to the bf16 parameter."""
     d = R.static_layer_inputs(40, 4, 1024, seed=9)
     dev = {k: v.to(device) for k, v in d.items()}
-    out, rms, coef = native.mhc_layer_static_fwd(dev["x"], dev["weight"], dev["H_pre"], dev["H_post"], dev["H_res"])
-    gx, gw, ghp, ghq, ghr = native.mhc_layer_static_bwd(dev["grad"], dev["x"], dev["weight"], dev["H_pre"],
-                                                        dev["H_post"], dev["H_res"], coef)
+    w32 = dev["weight"].float()
+    out, rms, saved = native.mhc_layer_static_fwd(dev["x"], w32, dev["H_pre"], dev["H_post"], dev["H_res"])
+    gx, gw, ghp, ghq, ghr = native.mhc_layer_static_bwd(dev["grad"], dev["x"], w32, dev["H_pre"],
+                                                        dev["H_post"], dev["H_res"], saved)
     _, _, rgp = _oracle_static(d)
     assert gw.dtype == torch.float32
     assert_close(gw, rgp[0], 1e-3, grad_atol(rgp[0], 1e-5), "fp32 d_weight")
@@ -199,7 +217,8 @@ def test_static_layer_native_fp32_weight_grad(device):
     xa = (torch.sigmoid(d["H_pre"].double())[None, :, None] * d["x"].double()).sum(1)
     assert_close(rms, torch.sqrt((xa * xa).mean(-1) + 1e-5), 1e-5, 0, "rms")
     m = R.sinkhorn_knopp(torch.exp(d["H_res"].double()), 20, 1e-8)
-    assert_close(coef[8:].view(4, 4), m, 1e-5, 1e-7, "M")
+    assert_close(saved[8:24].view(4, 4), m, 1e-5, 1e-7, "M")
+    assert_close(saved[64:64 + 1024], d["weight"].double(), 0, 0, "fp32 weight copy")
 
 
 def test_static_layer_empty_batch(device):
