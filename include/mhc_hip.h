@@ -69,6 +69,67 @@ int mhc_sinkhorn_knopp_fwd(const float* inp, float* out, int64_t batch, int32_t 
 int mhc_sinkhorn_knopp_bwd(const float* grad_out, const float* inp, const float* out, float* grad_inp,
                            int64_t batch, int32_t n, int32_t num_iters, float eps, void* stream);
 
+/* ---- RMSNorm ---------------------------------------------------------------
+ * out = inp / rms * weight, rms = sqrt(mean(inp^2) + eps) per row of `hidden`.
+ * inp/out [batch, hidden] (dtype), weight [hidden] fp32, rms [batch] fp32.
+ * Replaces rmsnorm_fwd (bindings.cpp:237-266); the reference forces bf16
+ * storage, here out has the input's dtype. */
+int mhc_rmsnorm_fwd(const void* inp, int32_t dtype, const float* weight, void* out, float* rms, int64_t batch,
+                    int32_t hidden, float eps, void* stream);
+
+size_t mhc_rmsnorm_bwd_workspace_size(int64_t batch, int32_t hidden, int32_t dtype);
+
+/* grad_inp = w g / rms - inp (sum g w inp) / (hidden rms^3) (dtype);
+ * grad_weight = sum_rows g inp / rms (fp32 [hidden], deterministic).
+ * grad_out has the input's dtype.  Replaces rmsnorm_bwd (bindings.cpp:268-301). */
+int mhc_rmsnorm_bwd(const void* grad_out, const void* inp, int32_t dtype, const float* weight, const float* rms,
+                    void* grad_inp, float* grad_weight, void* workspace, size_t workspace_bytes, int64_t batch,
+                    int32_t hidden, void* stream);
+
+/* rms[b] = sqrt(mean_k inp[b, k]^2 + eps) for inp [batch, k] (dtype).
+ * Replaces compute_rms_fwd (bindings.cpp:543-566). */
+int mhc_compute_rms_fwd(const void* inp, int32_t dtype, float* rms, int64_t batch, int64_t k, float eps,
+                        void* stream);
+
+/* ---- stream aggregate --------------------------------------------------------
+ * h = sigmoid(h_pre_raw[b]), out[b, :] = sum_i h_i inp[b, i, :].
+ * inp [batch, n, hidden] and out [batch, hidden] (dtype); h_pre_raw fp32
+ * with batch stride 0 (shared) or n; h_pre_act [batch, n] receives h.
+ * Replaces stream_aggregate_fwd (bindings.cpp:307-338). */
+int mhc_stream_aggregate_fwd(const void* inp, int32_t dtype, const float* h_pre_raw, int64_t h_batch_stride,
+                             void* out, float* h_pre_act, int64_t batch, int32_t n, int32_t hidden, void* stream);
+
+/* grad_inp[b, i, :] = grad_out[b, :] h_i (dtype); grad_h_pre_act[b, i] =
+ * sum_c grad_out x_i (before the sigmoid derivative, as the reference
+ * returns it); grad_h_pre_raw = grad_h_pre_act h (1 - h).  Either fp32
+ * output may be NULL.  Replaces stream_aggregate_bwd (bindings.cpp:340-374)
+ * and the sigmoid derivative of ops.py:211. */
+int mhc_stream_aggregate_bwd(const void* grad_out, const void* inp, int32_t dtype, const float* h_pre_act,
+                             int64_t h_batch_stride, void* grad_inp, float* grad_h_pre_act, float* grad_h_pre_raw,
+                             int64_t batch, int32_t n, int32_t hidden, void* stream);
+
+/* ---- stream distribute-mix-add ------------------------------------------------
+ * h = 2 sigmoid(h_post_raw[b]), out[b, i, :] = h_i y[b, :] + sum_j M[b, i, j] x[b, j, :].
+ * y_norm [batch, hidden] and x_inp [batch, n, hidden] (dtype); out fp32;
+ * h_post_raw / M fp32 with batch stride 0 or n / n*n; h_post_act [batch, n].
+ * Replaces stream_distribute_mix_add_fwd (bindings.cpp:380-416). */
+int mhc_stream_distribute_mix_add_fwd(const void* y_norm, const float* h_post_raw, int64_t h_batch_stride,
+                                      const float* M, int64_t m_batch_stride, const void* x_inp, int32_t dtype,
+                                      float* out, float* h_post_act, int64_t batch, int32_t n, int32_t hidden,
+                                      void* stream);
+
+/* For grad_out [batch, n, hidden] fp32: grad_x[b, j] = sum_i M_ij g_i and
+ * grad_y = sum_i h_i g_i (dtype); grad_M[b, i, j] = sum_c g_i x_j,
+ * grad_h_post_act[b, i] = sum_c g_i y, grad_h_post_raw = grad_h_post_act
+ * h (1 - h/2) (fp32; the last two may be NULL).
+ * Replaces stream_distribute_mix_add_bwd (bindings.cpp:418-460) and the
+ * derivative of ops.py:279-281. */
+int mhc_stream_distribute_mix_add_bwd(const float* grad_out, const void* x_inp, const void* y_norm, int32_t dtype,
+                                      const float* M, int64_t m_batch_stride, const float* h_post_act,
+                                      int64_t h_batch_stride, void* grad_x, void* grad_y, float* grad_M,
+                                      float* grad_h_post_act, float* grad_h_post_raw, int64_t batch, int32_t n,
+                                      int32_t hidden, void* stream);
+
 /* ---- fused static-H mHC layer ----------------------------------------------
  * x [batch, n, hidden] (x_dtype), weight [hidden] (weight_dtype: the
  * reference keeps it bf16, layer.py:65), h_pre/h_post [n], h_res [n, n] raw

@@ -12,6 +12,11 @@ __version__ = "0.1.0"
 from .layer import MHCLayer, create_mhc_layer, MHCResidualWrapper, replace_residual_with_mhc  # noqa: E402
 from .ops import (  # noqa: E402
     sinkhorn_knopp,
+    rmsnorm,
+    stream_aggregate,
+    stream_distribute_mix_add,
+    stream_distribute,
+    compute_rms,
     mhc_layer_static,
 )
 
@@ -21,5 +26,10 @@ __all__ = [
     "create_mhc_layer",
     "replace_residual_with_mhc",
     "sinkhorn_knopp",
+    "rmsnorm",
+    "stream_aggregate",
+    "stream_distribute_mix_add",
+    "stream_distribute",
+    "compute_rms",
     "mhc_layer_static",
 ]

@@ -41,6 +41,16 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "mhc_timing_query": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
     "mhc_sinkhorn_knopp_fwd": (ctypes.c_int, [_vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "mhc_sinkhorn_knopp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
+    "mhc_rmsnorm_fwd": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i64, _i32, _f32, _vp]),
+    "mhc_rmsnorm_bwd_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "mhc_rmsnorm_bwd": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _vp]),
+    "mhc_compute_rms_fwd": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i64, _f32, _vp]),
+    "mhc_stream_aggregate_fwd": (ctypes.c_int, [_vp, _i32, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _vp]),
+    "mhc_stream_aggregate_bwd": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
+    "mhc_stream_distribute_mix_add_fwd": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _vp,
+                                                         _i64, _i32, _i32, _vp]),
+    "mhc_stream_distribute_mix_add_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i64, _vp, _i64, _vp, _vp,
+                                                         _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
     "mhc_layer_static_saved_size": (_sz, [_i32, _i32]),
     "mhc_layer_static_fwd": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                             _i64, _i32, _i32, _i32, _f32, _f32, _vp]),

@@ -294,4 +294,147 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
     return hip_status(e);
 }
 
+// ---- standalone operators ---------------------------------------------------
+static int check_rows(const char* fn, int64_t batch, int64_t hidden, int32_t dtype, int n_arrays) {
+    if (batch < 0) return fail(MHC_ERR_INVALID, std::string(fn) + ": batch must be >= 0");
+    if (hidden < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": hidden must be >= 1");
+    if (!valid_dtype(dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": dtype must be F32 or BF16");
+    const int wc = dtype == kBF16 ? 8 : 4;
+    if (hidden % wc != 0)
+        return fail(MHC_ERR_UNSUPPORTED,
+                    std::string(fn) + ": hidden must be a multiple of " + std::to_string(wc) + " for this dtype");
+    if (choose_row_tiling(hidden, wc, n_arrays).vpt <= 0)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
+    return MHC_SUCCESS;
+}
+
+static int check_stream_n(const char* fn, int32_t n) {
+    if (n < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": n must be >= 1");
+    if (!supported_layer_n(n))
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) + " is not compiled in this build");
+    return MHC_SUCCESS;
+}
+
+int mhc_rmsnorm_fwd(const void* inp, int32_t dtype, const float* weight, void* out, float* rms, int64_t batch,
+                    int32_t hidden, float eps, void* stream) {
+    int st = check_rows("rmsnorm_fwd", batch, hidden, dtype, 1);
+    if (st) return st;
+    MHC_REQUIRE(batch == 0 || (inp && weight && out && rms), "rmsnorm_fwd: null pointer");
+    return hip_status(launch_rmsnorm_fwd(dtype, inp, weight, out, rms, batch, hidden, eps, (hipStream_t)stream));
+}
+
+struct RowsBwdWs {
+    int grid;
+    size_t part_off, stage_off, total;
+};
+
+static RowsBwdWs rmsnorm_bwd_ws(int64_t batch, int32_t hidden, int32_t dtype) {
+    RowsBwdWs w{};
+    w.grid = batch > 0 ? rmsnorm_bwd_grid(dtype, batch, hidden) : 1;
+    w.part_off = 0;
+    w.stage_off = align256((size_t)w.grid * hidden * sizeof(float));
+    w.total = w.stage_off + align256((size_t)kDwSplit * hidden * sizeof(float));
+    return w;
+}
+
+size_t mhc_rmsnorm_bwd_workspace_size(int64_t batch, int32_t hidden, int32_t dtype) {
+    if (batch < 0 || hidden < 1) return 0;
+    return rmsnorm_bwd_ws(batch, hidden, dtype).total;
+}
+
+int mhc_rmsnorm_bwd(const void* grad_out, const void* inp, int32_t dtype, const float* weight, const float* rms,
+                    void* grad_inp, float* grad_weight, void* workspace, size_t workspace_bytes, int64_t batch,
+                    int32_t hidden, void* stream) {
+    int st = check_rows("rmsnorm_bwd", batch, hidden, dtype, 2);
+    if (st) return st;
+    MHC_REQUIRE(weight && grad_weight, "rmsnorm_bwd: null weight/grad_weight");
+    MHC_REQUIRE(batch == 0 || (grad_out && inp && rms && grad_inp), "rmsnorm_bwd: null pointer");
+    const RowsBwdWs w = rmsnorm_bwd_ws(batch, hidden, dtype);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "rmsnorm_bwd: workspace smaller than mhc_rmsnorm_bwd_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    float* part = (float*)((char*)workspace + w.part_off);
+    float* stage = (float*)((char*)workspace + w.stage_off);
+    int rows = w.grid;
+    hipError_t e;
+    if (batch == 0) {
+        rows = 1;
+        e = launch_fill_zero(part, hidden, s);
+    } else {
+        e = launch_rmsnorm_bwd(dtype, grad_out, inp, weight, rms, grad_inp, part, w.grid, batch, hidden, s);
+    }
+    if (e == hipSuccess) e = launch_column_partial(part, rows, hidden, stage, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(0, kF32, stage, kDwSplit, hidden, grad_weight, nullptr, 0, nullptr, nullptr, nullptr,
+                                  nullptr, nullptr, nullptr, 0, 0.f, s);
+    return hip_status(e);
+}
+
+int mhc_compute_rms_fwd(const void* inp, int32_t dtype, float* rms, int64_t batch, int64_t k, float eps,
+                        void* stream) {
+    int st = check_rows("compute_rms_fwd", batch, k, dtype, 1);
+    if (st) return st;
+    MHC_REQUIRE(batch == 0 || (inp && rms), "compute_rms_fwd: null pointer");
+    return hip_status(launch_compute_rms(dtype, inp, rms, batch, k, eps, (hipStream_t)stream));
+}
+
+int mhc_stream_aggregate_fwd(const void* inp, int32_t dtype, const float* h_pre_raw, int64_t h_batch_stride,
+                             void* out, float* h_pre_act, int64_t batch, int32_t n, int32_t hidden, void* stream) {
+    int st = check_stream_n("stream_aggregate_fwd", n);
+    if (!st) st = check_rows("stream_aggregate_fwd", batch, hidden, dtype, n + 1);
+    if (st) return st;
+    MHC_REQUIRE(h_batch_stride == 0 || h_batch_stride == n, "stream_aggregate_fwd: h_batch_stride must be 0 or n");
+    MHC_REQUIRE(batch == 0 || (inp && h_pre_raw && out && h_pre_act), "stream_aggregate_fwd: null pointer");
+    return hip_status(launch_aggregate_fwd(dtype, n, inp, h_pre_raw, h_batch_stride, out, h_pre_act, batch, hidden,
+                                           (hipStream_t)stream));
+}
+
+int mhc_stream_aggregate_bwd(const void* grad_out, const void* inp, int32_t dtype, const float* h_pre_act,
+                             int64_t h_batch_stride, void* grad_inp, float* grad_h_pre_act, float* grad_h_pre_raw,
+                             int64_t batch, int32_t n, int32_t hidden, void* stream) {
+    int st = check_stream_n("stream_aggregate_bwd", n);
+    if (!st) st = check_rows("stream_aggregate_bwd", batch, hidden, dtype, n + 1);
+    if (st) return st;
+    MHC_REQUIRE(h_batch_stride == 0 || h_batch_stride == n, "stream_aggregate_bwd: h_batch_stride must be 0 or n");
+    MHC_REQUIRE(batch == 0 || (grad_out && inp && h_pre_act && grad_inp), "stream_aggregate_bwd: null pointer");
+    return hip_status(launch_aggregate_bwd(dtype, n, grad_out, inp, h_pre_act, h_batch_stride, grad_inp,
+                                           grad_h_pre_act, grad_h_pre_raw, batch, hidden, (hipStream_t)stream));
+}
+
+int mhc_stream_distribute_mix_add_fwd(const void* y_norm, const float* h_post_raw, int64_t h_batch_stride,
+                                      const float* M, int64_t m_batch_stride, const void* x_inp, int32_t dtype,
+                                      float* out, float* h_post_act, int64_t batch, int32_t n, int32_t hidden,
+                                      void* stream) {
+    int st = check_stream_n("stream_distribute_mix_add_fwd", n);
+    if (!st) st = check_rows("stream_distribute_mix_add_fwd", batch, hidden, dtype, n + 1);
+    if (st) return st;
+    MHC_REQUIRE(h_batch_stride == 0 || h_batch_stride == n,
+                "stream_distribute_mix_add_fwd: h_batch_stride must be 0 or n");
+    MHC_REQUIRE(m_batch_stride == 0 || m_batch_stride == (int64_t)n * n,
+                "stream_distribute_mix_add_fwd: m_batch_stride must be 0 or n*n");
+    MHC_REQUIRE(batch == 0 || (y_norm && h_post_raw && M && x_inp && out && h_post_act),
+                "stream_distribute_mix_add_fwd: null pointer");
+    return hip_status(launch_distribute_fwd(dtype, n, y_norm, h_post_raw, h_batch_stride, M, m_batch_stride, x_inp,
+                                            out, h_post_act, batch, hidden, (hipStream_t)stream));
+}
+
+int mhc_stream_distribute_mix_add_bwd(const float* grad_out, const void* x_inp, const void* y_norm, int32_t dtype,
+                                      const float* M, int64_t m_batch_stride, const float* h_post_act,
+                                      int64_t h_batch_stride, void* grad_x, void* grad_y, float* grad_M,
+                                      float* grad_h_post_act, float* grad_h_post_raw, int64_t batch, int32_t n,
+                                      int32_t hidden, void* stream) {
+    int st = check_stream_n("stream_distribute_mix_add_bwd", n);
+    if (!st) st = check_rows("stream_distribute_mix_add_bwd", batch, hidden, dtype, 2 * n + 1);
+    if (st) return st;
+    MHC_REQUIRE(h_batch_stride == 0 || h_batch_stride == n,
+                "stream_distribute_mix_add_bwd: h_batch_stride must be 0 or n");
+    MHC_REQUIRE(m_batch_stride == 0 || m_batch_stride == (int64_t)n * n,
+                "stream_distribute_mix_add_bwd: m_batch_stride must be 0 or n*n");
+    MHC_REQUIRE(batch == 0 || (grad_out && x_inp && y_norm && M && h_post_act && grad_x && grad_y && grad_M),
+                "stream_distribute_mix_add_bwd: null pointer");
+    return hip_status(launch_distribute_bwd(dtype, n, grad_out, x_inp, y_norm, M, m_batch_stride, h_post_act,
+                                            h_batch_stride, grad_x, grad_y, grad_M, grad_h_post_act, grad_h_post_raw,
+                                            batch, hidden, (hipStream_t)stream));
+}
+
 }  // extern "C"

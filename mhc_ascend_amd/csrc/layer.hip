@@ -21,6 +21,7 @@
 // partials are reduced deterministically afterwards.
 #include "mhc_device.h"
 #include "mhc_internal.h"
+#include "mhc_rows.h"
 
 namespace mhc {
 
@@ -64,52 +65,6 @@ __global__ __launch_bounds__(256) void static_coef_kernel(const float* __restric
         for (int c = 0; c < N; ++c) saved[2 * N + r * N + c] = a[c];
     }
 }
-
-// ---------------------------------------------------------------------------
-// Token-row I/O: this thread's VPT chunks of WC channels of each of the N
-// streams of one token (chunk q = k * blockDim.x + tid, channel q * WC).
-// NTL selects non-temporal loads.  All streaming rows use them: a plain-load
-// forward is faster in isolation but slows the following backward more than
-// it gains (whole fwd+bwd step measured at n=4, C=4096).
-// ---------------------------------------------------------------------------
-template <typename T, int N, int VPT, int WC, bool NTL>
-__device__ __forceinline__ void load_rows(const T* __restrict__ base, int C, float (&v)[N][VPT][WC]) {
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-#pragma unroll
-        for (int i = 0; i < N; ++i) {
-            if (c0 < C) {
-                if constexpr (NTL) {
-                    load_run_nt<T, WC>(base + (int64_t)i * C + c0, v[i][k]);
-                } else {
-                    load_run<T, WC>(base + (int64_t)i * C + c0, v[i][k]);
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < WC; ++e) v[i][k][e] = 0.f;
-            }
-        }
-    }
-}
-
-template <int VPT, int WC>
-__device__ __forceinline__ void load_weight(const float* __restrict__ w, int C, float (&wv)[VPT][WC]) {
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-        if (c0 < C) {
-            load_run<float, WC>(w + c0, wv[k]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < WC; ++e) wv[k][e] = 0.f;
-        }
-    }
-}
-
-// Workgroup size bound: the prefetching variants hold two token rows and
-// run with up to 256 lanes (512 VGPRs available); the others up to 512.
-#define MHC_ROW_BOUNDS(PF) __attribute__((amdgpu_flat_work_group_size(1, (PF) ? 256 : 512)))
 
 // ---------------------------------------------------------------------------
 // Fused forward.  Persistent workgroups stride over tokens; with PF the next
@@ -533,12 +488,6 @@ hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s) {
         case 8: { constexpr int V_ = 8; __VA_ARGS__; break; }    \
         default: return hipErrorInvalidValue;                    \
     }
-
-// Row state budget shared with choose_row_tiling(): n_arrays * VPT * W <= 128.
-template <typename TX>
-constexpr bool row_fits(int n_arrays, int vpt) {
-    return n_arrays * vpt * VecIO<TX>::W <= 128;
-}
 
 int saved_w_offset(int n) { return ((2 * n + n * n + 63) / 64) * 64; }
 

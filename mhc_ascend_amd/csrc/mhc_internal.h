@@ -56,6 +56,24 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
                                  const float* h_res, float* d_h_pre, float* d_h_post, float* d_h_res, int iters,
                                  float sk_eps, hipStream_t s);
 
+// ---- ops.hip ---------------------------------------------------------------
+hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, float* rms, int64_t B, int64_t C,
+                              float eps, hipStream_t s);
+int rmsnorm_bwd_grid(int dt, int64_t B, int64_t C);
+hipError_t launch_rmsnorm_bwd(int dt, const void* g, const void* x, const float* w, const float* rms, void* gx,
+                              float* dw_part, int grid, int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_compute_rms(int dt, const void* x, float* rms, int64_t B, int64_t K, float eps, hipStream_t s);
+hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out, float* h_act,
+                                int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
+                                void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_distribute_fwd(int dt, int n, const void* y, const float* H, int64_t hs, const float* M,
+                                 int64_t ms, const void* x, float* out, float* h_act, int64_t B, int64_t C,
+                                 hipStream_t s);
+hipError_t launch_distribute_bwd(int dt, int n, const float* g, const void* x, const void* y, const float* M,
+                                 int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
+                                 float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
+
 // ---- sinkhorn.hip ----------------------------------------------------------
 hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batch, int iters, float eps,
                                hipStream_t s);

@@ -81,6 +81,178 @@ def sinkhorn_knopp_bwd(grad_out: torch.Tensor, inp: torch.Tensor, out: torch.Ten
 
 
 # =============================================================================
+# RMSNorm (bindings.cpp:237-301) and compute_rms (bindings.cpp:543-566)
+# =============================================================================
+
+def _storage(t: torch.Tensor) -> torch.Tensor:
+    """Large-tensor storage: fp32 or bf16, contiguous (others become fp32)."""
+    if t.dtype not in (torch.float32, torch.bfloat16):
+        t = t.float()
+    return t.contiguous()
+
+
+def _coef_view(fn: str, t: torch.Tensor, B: int, per: int):
+    """A per-token coefficient tensor [B, *] as (fp32 tensor, batch stride):
+    a tensor broadcast over the batch (stride 0, e.g. expand()) is passed
+    once with stride 0; anything else is made contiguous."""
+    if t.dtype != torch.float32:
+        t = t.float()
+    if t.dim() >= 2 and t.size(0) == B and t.stride(0) == 0:
+        one = t[0].contiguous()
+        if one.numel() != per:
+            raise RuntimeError(f"{fn}: coefficient shape {tuple(t.shape)} does not match n")
+        return one, 0
+    t = t.contiguous()
+    if t.numel() != B * per:
+        raise RuntimeError(f"{fn}: coefficient shape {tuple(t.shape)} does not match [B={B}, {per}]")
+    return t, per
+
+
+def rmsnorm_fwd(inp: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(out, rms) for inp [B, C] (bindings.cpp:237-266).  out keeps inp's dtype."""
+    _check_device("rmsnorm_fwd", inp, weight)
+    if inp.dim() != 2:
+        raise RuntimeError("Input must be 2D tensor [B, C]")
+    x = _storage(inp)
+    B, C = x.shape
+    if weight.numel() != C:
+        raise RuntimeError("weight must have C elements")
+    w = _f32c(weight)
+    out = torch.empty_like(x)
+    rms = torch.empty((B,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        call("mhc_rmsnorm_fwd", ptr(x), dtype_code(x.dtype), ptr(w), ptr(out), ptr(rms), B, C, float(eps),
+             stream_of(x))
+    return out, rms
+
+
+def rmsnorm_bwd(grad_out: torch.Tensor, inp: torch.Tensor, weight: torch.Tensor,
+                rms: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(grad_inp [inp dtype], grad_weight fp32 [C]) (bindings.cpp:268-301)."""
+    _check_device("rmsnorm_bwd", grad_out, inp, weight, rms)
+    x = _storage(inp)
+    B, C = x.shape
+    g = grad_out.to(x.dtype).contiguous()
+    if g.shape != x.shape:
+        raise RuntimeError("grad_out shape must match inp")
+    w, r = _f32c(weight), _f32c(rms)
+    gx = torch.empty_like(x)
+    gw = torch.empty((C,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        ws_bytes = _lib.load().mhc_rmsnorm_bwd_workspace_size(B, C, dtype_code(x.dtype))
+        ws = torch.empty((max(int(ws_bytes), 1),), dtype=torch.uint8, device=x.device)
+        call("mhc_rmsnorm_bwd", ptr(g), ptr(x), dtype_code(x.dtype), ptr(w), ptr(r), ptr(gx), ptr(gw), ptr(ws),
+             int(ws_bytes), B, C, stream_of(x))
+    return gx, gw
+
+
+def compute_rms_fwd(inp: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
+    """rms [B] of inp [B, K] (bindings.cpp:543-566)."""
+    _check_device("compute_rms_fwd", inp)
+    if inp.dim() != 2:
+        raise RuntimeError("Input must be 2D tensor [B, K]")
+    x = _storage(inp)
+    B, K = x.shape
+    rms = torch.empty((B,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        call("mhc_compute_rms_fwd", ptr(x), dtype_code(x.dtype), ptr(rms), B, K, float(eps), stream_of(x))
+    return rms
+
+
+# =============================================================================
+# Stream aggregate (bindings.cpp:307-374) and distribute-mix-add (380-460)
+# =============================================================================
+
+def stream_aggregate_fwd(inp: torch.Tensor, H_pre_raw: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(out [B, C] in inp's dtype, H_pre_activated [B, n]) (bindings.cpp:307-338)."""
+    _check_device("stream_aggregate_fwd", inp, H_pre_raw)
+    if inp.dim() != 3:
+        raise RuntimeError("Input must be 3D tensor [B, n, C]")
+    x = _storage(inp)
+    B, n, C = x.shape
+    h, hs = _coef_view("stream_aggregate_fwd", H_pre_raw, B, n)
+    out = torch.empty((B, C), dtype=x.dtype, device=x.device)
+    h_act = torch.empty((B, n), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        call("mhc_stream_aggregate_fwd", ptr(x), dtype_code(x.dtype), ptr(h), hs, ptr(out), ptr(h_act), B, n, C,
+             stream_of(x))
+    return out, h_act
+
+
+def _aggregate_bwd(grad_out, inp, H_pre_activated, want_raw: bool):
+    _check_device("stream_aggregate_bwd", grad_out, inp, H_pre_activated)
+    x = _storage(inp)
+    B, n, C = x.shape
+    g = grad_out.to(x.dtype).contiguous()
+    if g.shape != (B, C):
+        raise RuntimeError("grad_out must be [B, C]")
+    h, hs = _coef_view("stream_aggregate_bwd", H_pre_activated, B, n)
+    gx = torch.empty_like(x)
+    gh = torch.empty((B, n), dtype=torch.float32, device=x.device)
+    graw = torch.empty((B, n), dtype=torch.float32, device=x.device) if want_raw else None
+    with torch.cuda.device(x.device):
+        call("mhc_stream_aggregate_bwd", ptr(g), ptr(x), dtype_code(x.dtype), ptr(h), hs, ptr(gx), ptr(gh),
+             ptr(graw), B, n, C, stream_of(x))
+    return gx, gh, graw
+
+
+def stream_aggregate_bwd(grad_out: torch.Tensor, inp: torch.Tensor,
+                         H_pre_activated: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(grad_inp, grad_H_pre_activated) before the sigmoid derivative (bindings.cpp:340-374)."""
+    gx, gh, _ = _aggregate_bwd(grad_out, inp, H_pre_activated, False)
+    return gx, gh
+
+
+def stream_distribute_mix_add_fwd(y_norm: torch.Tensor, H_post_raw: torch.Tensor, M: torch.Tensor,
+                                  x_inp: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(out fp32 [B, n, C], H_post_activated [B, n]) (bindings.cpp:380-416)."""
+    _check_device("stream_distribute_mix_add_fwd", y_norm, H_post_raw, M, x_inp)
+    if x_inp.dim() != 3:
+        raise RuntimeError("x_inp must be 3D tensor [B, n, C]")
+    x = _storage(x_inp)
+    B, n, C = x.shape
+    y = y_norm.to(x.dtype).contiguous()
+    if y.shape != (B, C):
+        raise RuntimeError("y_norm must be [B, C]")
+    h, hs = _coef_view("stream_distribute_mix_add_fwd", H_post_raw, B, n)
+    m, ms = _coef_view("stream_distribute_mix_add_fwd", M, B, n * n)
+    out = torch.empty((B, n, C), dtype=torch.float32, device=x.device)
+    h_act = torch.empty((B, n), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        call("mhc_stream_distribute_mix_add_fwd", ptr(y), ptr(h), hs, ptr(m), ms, ptr(x), dtype_code(x.dtype),
+             ptr(out), ptr(h_act), B, n, C, stream_of(x))
+    return out, h_act
+
+
+def _distribute_bwd(grad_out, x_inp, y_norm, M, H_post_activated, want_raw: bool):
+    _check_device("stream_distribute_mix_add_bwd", grad_out, x_inp, y_norm, M, H_post_activated)
+    x = _storage(x_inp)
+    B, n, C = x.shape
+    y = y_norm.to(x.dtype).contiguous()
+    g = _f32c(grad_out)
+    if g.shape != x.shape:
+        raise RuntimeError("grad_out shape must match x_inp")
+    m, ms = _coef_view("stream_distribute_mix_add_bwd", M, B, n * n)
+    h, hs = _coef_view("stream_distribute_mix_add_bwd", H_post_activated, B, n)
+    gx = torch.empty_like(x)
+    gy = torch.empty((B, C), dtype=x.dtype, device=x.device)
+    gM = torch.empty((B, n, n), dtype=torch.float32, device=x.device)
+    gh = torch.empty((B, n), dtype=torch.float32, device=x.device)
+    graw = torch.empty((B, n), dtype=torch.float32, device=x.device) if want_raw else None
+    with torch.cuda.device(x.device):
+        call("mhc_stream_distribute_mix_add_bwd", ptr(g), ptr(x), ptr(y), dtype_code(x.dtype), ptr(m), ms, ptr(h),
+             hs, ptr(gx), ptr(gy), ptr(gM), ptr(gh), ptr(graw), B, n, C, stream_of(x))
+    return gx, gy, gM, gh, graw
+
+
+def stream_distribute_mix_add_bwd(grad_out: torch.Tensor, x_inp: torch.Tensor, y_norm: torch.Tensor,
+                                  M: torch.Tensor, H_post_activated: torch.Tensor):
+    """(grad_x, grad_y, grad_M, grad_H_post_activated) (bindings.cpp:418-460)."""
+    gx, gy, gM, gh, _ = _distribute_bwd(grad_out, x_inp, y_norm, M, H_post_activated, False)
+    return gx, gy, gM, gh
+
+
+# =============================================================================
 # Fused static-H layer (layer.py:142-170)
 # =============================================================================
 

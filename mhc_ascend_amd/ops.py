@@ -48,6 +48,91 @@ def sinkhorn_knopp(inp: torch.Tensor, num_iters: int = 20, eps: float = 1e-8) ->
 
 
 # =============================================================================
+# RMSNorm (ops.py:126-175)
+# =============================================================================
+
+class RMSNormFunction(torch.autograd.Function):
+    """Root Mean Square normalisation of [B, C] rows."""
+
+    @staticmethod
+    def forward(ctx, inp: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+        out, rms = native.rmsnorm_fwd(inp, weight, eps)
+        ctx.save_for_backward(inp, weight, rms)
+        ctx.eps = eps
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out: torch.Tensor):
+        inp, weight, rms = ctx.saved_tensors
+        grad_inp, grad_weight = native.rmsnorm_bwd(grad_out, inp, weight, rms)
+        return grad_inp.to(inp.dtype), grad_weight, None
+
+
+def rmsnorm(inp: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """RMSNorm of inp [B, C]; the output keeps inp's dtype (fp32 or bf16)."""
+    return RMSNormFunction.apply(inp, weight, eps)
+
+
+# =============================================================================
+# Stream aggregate (ops.py:182-227)
+# =============================================================================
+
+class StreamAggregateFunction(torch.autograd.Function):
+    """out = sum_i sigmoid(H_pre_raw[:, i]) * inp[:, i]."""
+
+    @staticmethod
+    def forward(ctx, inp: torch.Tensor, H_pre_raw: torch.Tensor) -> torch.Tensor:
+        out, h_act = native.stream_aggregate_fwd(inp, H_pre_raw)
+        ctx.save_for_backward(inp, h_act)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out: torch.Tensor):
+        inp, h_act = ctx.saved_tensors
+        gx, _, graw = native._aggregate_bwd(grad_out, inp, h_act, True)
+        return gx.to(inp.dtype), graw
+
+
+def stream_aggregate(inp: torch.Tensor, H_pre_raw: torch.Tensor) -> torch.Tensor:
+    """Aggregate [B, n, C] streams with sigmoid weights H_pre_raw [B, n]."""
+    return StreamAggregateFunction.apply(inp, H_pre_raw)
+
+
+# =============================================================================
+# Stream distribute-mix-add (ops.py:234-304)
+# =============================================================================
+
+class StreamDistributeMixAddFunction(torch.autograd.Function):
+    """out[:, i] = 2 sigmoid(H_post_raw[:, i]) * y_norm + sum_j M[:, i, j] x[:, j]."""
+
+    @staticmethod
+    def forward(ctx, y_norm, H_post_raw, M, x_inp):
+        out, h_act = native.stream_distribute_mix_add_fwd(y_norm, H_post_raw, M, x_inp)
+        ctx.save_for_backward(x_inp, y_norm, M, h_act)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x_inp, y_norm, M, h_act = ctx.saved_tensors
+        gx, gy, gM, _, graw = native._distribute_bwd(grad_out, x_inp, y_norm, M, h_act, True)
+        return gy.to(y_norm.dtype), graw, gM, gx.to(x_inp.dtype)
+
+
+def stream_distribute_mix_add(y_norm: torch.Tensor, H_post_raw: torch.Tensor, M: torch.Tensor,
+                              x_inp: torch.Tensor) -> torch.Tensor:
+    """Distribute y_norm [B, C] to n streams, mix x_inp [B, n, C] with M and add (fp32 out)."""
+    return StreamDistributeMixAddFunction.apply(y_norm, H_post_raw, M, x_inp)
+
+
+stream_distribute = stream_distribute_mix_add
+
+
+def compute_rms(x_flat: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
+    """Per-row RMS of x_flat [B, K] (ops.py:357-369); no autograd, as in the reference."""
+    return native.compute_rms_fwd(x_flat, eps)
+
+
+# =============================================================================
 # Fused static-H layer (layer.py:142-170 as one HBM pass per direction)
 # =============================================================================
 
