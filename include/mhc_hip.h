@@ -165,6 +165,58 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
                          void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
                          int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
 
+/* ---- dynamic-H projection ----------------------------------------------------
+ * out[b, o] = sum_k inp[b, k] weight[o, k]: inp [batch, k] (dtype), weight
+ * [out_dim, k] fp32, out [batch, out_dim] fp32; out_dim <= 32, k % 32 == 0.
+ * bf16 MFMA on a hi/lo bf16 split of the operands (about fp32 accuracy).
+ * Replaces fused_rmsnorm_matmul_fwd (bindings.cpp:480-528), which rounds
+ * inputs and result to bf16. */
+size_t mhc_fused_rmsnorm_matmul_fwd_workspace_size(int64_t batch, int64_t k);
+int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* weight, float* out, void* workspace,
+                                 size_t workspace_bytes, int64_t batch, int64_t k, int32_t out_dim, void* stream);
+
+/* grad_x = grad_out . phi ([batch, k] fp32), grad_phi = grad_out^T . x_flat
+ * ([out_dim, k] fp32, deterministic).  Replaces fused_rmsnorm_matmul_bwd
+ * (bindings.cpp:530-541). */
+size_t mhc_fused_rmsnorm_matmul_bwd_workspace_size(int64_t batch, int64_t k, int32_t out_dim);
+int mhc_fused_rmsnorm_matmul_bwd(const float* grad_out, const float* x_flat, const float* phi, float* grad_x,
+                                 float* grad_phi, void* workspace, size_t workspace_bytes, int64_t batch, int64_t k,
+                                 int32_t out_dim, void* stream);
+
+/* ---- fused dynamic-H mHC layer --------------------------------------------------
+ * Per token: x_flat = x[b] (n*hidden), r_h = sqrt(mean(x_flat^2) + rmsnorm_eps),
+ * P = x_flat . [phi_pre; phi_post; phi_res]^T, t_k = alpha_k P_k / r_h + b_k,
+ * h_pre = sigmoid(t_pre), h_post = 2 sigmoid(t_post), M = SK(exp(t_res)),
+ * then the static formulas with per-token h and M.
+ * phi_pre / phi_post [n, n*hidden], phi_res [n*n, n*hidden], b_pre / b_post
+ * [n], b_res [n, n] fp32; alpha_* are single fp32 values in DEVICE memory
+ * (no host synchronisation).  out [batch, n, hidden] fp32; `saved`
+ * (mhc_layer_dynamic_saved_size bytes) receives what the backward needs.
+ * Replaces mhc_layer_fwd_dynamic (bindings.cpp:880-952) and the inference
+ * path of ops.py:376-419. */
+size_t mhc_layer_dynamic_saved_size(int64_t batch, int32_t n, int32_t hidden);
+size_t mhc_layer_dynamic_fwd_workspace_size(int64_t batch, int32_t n, int32_t hidden);
+int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, int32_t weight_dtype,
+                          const float* phi_pre, const float* phi_post, const float* phi_res, const float* alpha_pre,
+                          const float* alpha_post, const float* alpha_res, const float* b_pre, const float* b_post,
+                          const float* b_res, float* out, float* saved, void* workspace, size_t workspace_bytes,
+                          int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
+                          float rmsnorm_eps, void* stream);
+
+/* Gradients for grad_out [batch, n, hidden] fp32: grad_x (x_dtype),
+ * grad_weight [hidden] (weight_dtype), grad_phi [2n+n^2, n*hidden] (rows
+ * pre, post, res), grad_alpha [3] (pre, post, res), grad_b [2n+n^2]
+ * (pre, post, res row-major), all fp32 and deterministic.
+ * Replaces mhc_layer_bwd_dynamic (bindings.cpp:600-874). */
+size_t mhc_layer_dynamic_bwd_workspace_size(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype);
+int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype, int32_t weight_dtype,
+                          const float* phi_pre, const float* phi_post, const float* phi_res, const float* alpha_pre,
+                          const float* alpha_post, const float* alpha_res, const float* b_pre, const float* b_post,
+                          const float* b_res, const float* saved, void* grad_x, void* grad_weight, float* grad_phi,
+                          float* grad_alpha, float* grad_b, void* workspace, size_t workspace_bytes, int64_t batch,
+                          int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,10 @@ from .ops import (  # noqa: E402
     stream_distribute_mix_add,
     stream_distribute,
     compute_rms,
+    fused_rmsnorm_matmul,
     mhc_layer_static,
+    mhc_layer_fused_dynamic_training,
+    mhc_layer_fused_dynamic_inference,
 )
 
 __all__ = [
@@ -31,5 +34,8 @@ __all__ = [
     "stream_distribute_mix_add",
     "stream_distribute",
     "compute_rms",
+    "fused_rmsnorm_matmul",
     "mhc_layer_static",
+    "mhc_layer_fused_dynamic_training",
+    "mhc_layer_fused_dynamic_inference",
 ]

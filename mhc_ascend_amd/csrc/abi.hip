@@ -437,4 +437,268 @@ int mhc_stream_distribute_mix_add_bwd(const float* grad_out, const void* x_inp, 
                                             batch, hidden, (hipStream_t)stream));
 }
 
+// ---- dynamic-H projection operators ------------------------------------------
+static size_t align_floats(size_t n) { return (n + 63) & ~(size_t)63; }
+
+struct ProjFwdWs {
+    int ks;
+    size_t phib_off, p_off, ss_off, total;
+};
+
+static ProjFwdWs proj_fwd_ws(int64_t batch, int64_t k) {
+    ProjFwdWs w{};
+    w.ks = batch > 0 ? proj_ksplit(batch, k) : 1;
+    w.phib_off = 0;
+    w.p_off = align256((size_t)3 * 32 * k * 2);  // three bf16 planes of Phi
+    w.ss_off = w.p_off + align256((size_t)w.ks * batch * 32 * sizeof(float));
+    w.total = w.ss_off + align256((size_t)w.ks * batch * sizeof(float));
+    return w;
+}
+
+static int check_proj(const char* fn, int64_t batch, int64_t k, int32_t out_dim) {
+    if (batch < 0 || k < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": batch must be >= 0 and k >= 1");
+    if (out_dim < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": out_dim must be >= 1");
+    if (out_dim > 32) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": out_dim > 32 is not supported");
+    if (k % 32 != 0) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": k must be a multiple of 32");
+    return MHC_SUCCESS;
+}
+
+size_t mhc_fused_rmsnorm_matmul_fwd_workspace_size(int64_t batch, int64_t k) {
+    if (batch < 0 || k < 1) return 0;
+    return proj_fwd_ws(batch, k).total;
+}
+
+int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* weight, float* out, void* workspace,
+                                 size_t workspace_bytes, int64_t batch, int64_t k, int32_t out_dim, void* stream) {
+    int st = check_proj("fused_rmsnorm_matmul_fwd", batch, k, out_dim);
+    if (st) return st;
+    MHC_REQUIRE(valid_dtype(dtype), "fused_rmsnorm_matmul_fwd: dtype must be F32 or BF16");
+    MHC_REQUIRE(weight && (batch == 0 || (inp && out)), "fused_rmsnorm_matmul_fwd: null pointer");
+    if (batch == 0) return MHC_SUCCESS;
+    const ProjFwdWs w = proj_fwd_ws(batch, k);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "fused_rmsnorm_matmul_fwd: workspace too small");
+    hipStream_t s = (hipStream_t)stream;
+    bf16_raw_t* phib = (bf16_raw_t*)((char*)workspace + w.phib_off);
+    float* pp = (float*)((char*)workspace + w.p_off);
+    float* ss = (float*)((char*)workspace + w.ss_off);
+    hipError_t e = launch_phi_split(weight, weight, weight, out_dim, out_dim, k, phib, s);
+    if (e == hipSuccess) e = launch_proj_mfma(dtype, inp, phib, pp, ss, batch, k, w.ks, s);
+    if (e == hipSuccess) e = launch_proj_reduce(pp, w.ks, batch, out_dim, out, s);
+    return hip_status(e);
+}
+
+struct ProjBwdWs {
+    int tiles;
+    size_t part_off, stage_off, total;
+};
+
+static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
+    ProjBwdWs w{};
+    w.tiles = batch > 0 ? dyn_dx_tiles(batch, k) : 1;
+    w.part_off = 0;
+    w.stage_off = align256((size_t)w.tiles * out_dim * k * sizeof(float));
+    w.total = w.stage_off + align256((size_t)kDwSplit * out_dim * k * sizeof(float));
+    return w;
+}
+
+size_t mhc_fused_rmsnorm_matmul_bwd_workspace_size(int64_t batch, int64_t k, int32_t out_dim) {
+    if (batch < 0 || k < 1 || out_dim < 1) return 0;
+    return proj_bwd_ws(batch, k, out_dim).total;
+}
+
+int mhc_fused_rmsnorm_matmul_bwd(const float* grad_out, const float* x_flat, const float* phi, float* grad_x,
+                                 float* grad_phi, void* workspace, size_t workspace_bytes, int64_t batch, int64_t k,
+                                 int32_t out_dim, void* stream) {
+    int st = check_proj("fused_rmsnorm_matmul_bwd", batch, k, out_dim);
+    if (st) return st;
+    MHC_REQUIRE(phi && grad_phi && (batch == 0 || (grad_out && x_flat && grad_x)),
+                "fused_rmsnorm_matmul_bwd: null pointer");
+    const ProjBwdWs w = proj_bwd_ws(batch, k, out_dim);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "fused_rmsnorm_matmul_bwd: workspace too small");
+    hipStream_t s = (hipStream_t)stream;
+    float* part = (float*)((char*)workspace + w.part_off);
+    float* stage = (float*)((char*)workspace + w.stage_off);
+    const int64_t cols = (int64_t)out_dim * k;
+    int rows = w.tiles;
+    hipError_t e;
+    if (batch == 0) {
+        rows = 1;
+        e = launch_fill_zero(part, cols, s);
+    } else {
+        e = launch_proj_bwd(grad_out, out_dim, x_flat, phi, grad_x, part, w.tiles, batch, k, s);
+    }
+    if (e == hipSuccess) e = launch_column_partial(part, rows, cols, stage, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(0, kF32, stage, kDwSplit, cols, grad_phi, nullptr, 0, nullptr, nullptr, nullptr,
+                                  nullptr, nullptr, nullptr, 0, 0.f, s);
+    return hip_status(e);
+}
+
+// ---- fused dynamic-H layer ----------------------------------------------------
+// saved (floats): [w32 (C) | coef (B x np) | P (B x np) | r_h (B)], each 64-aligned
+struct DynSaved {
+    size_t w_off, coef_off, p_off, rh_off, total;
+};
+
+static DynSaved dyn_saved(int64_t batch, int32_t n, int32_t hidden) {
+    const size_t np = 2 * n + n * n;
+    DynSaved d{};
+    d.w_off = 0;
+    d.coef_off = align_floats(hidden);
+    d.p_off = d.coef_off + align_floats(batch * np);
+    d.rh_off = d.p_off + align_floats(batch * np);
+    d.total = d.rh_off + align_floats(batch);
+    return d;
+}
+
+size_t mhc_layer_dynamic_saved_size(int64_t batch, int32_t n, int32_t hidden) {
+    if (batch < 0 || n < 1 || hidden < 1) return 0;
+    return dyn_saved(batch, n, hidden).total * sizeof(float);
+}
+
+size_t mhc_layer_dynamic_fwd_workspace_size(int64_t batch, int32_t n, int32_t hidden) {
+    if (batch < 0 || n < 1 || hidden < 1) return 0;
+    return proj_fwd_ws(batch, (int64_t)n * hidden).total;
+}
+
+static int check_dyn(const char* fn, int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype, int32_t w_dtype,
+                     int32_t num_iters) {
+    int st = check_layer_shape(fn, batch, n, hidden, x_dtype, num_iters);
+    if (st) return st;
+    if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
+    if (((int64_t)n * hidden) % 32 != 0)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
+    return MHC_SUCCESS;
+}
+
+int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, int32_t weight_dtype,
+                          const float* phi_pre, const float* phi_post, const float* phi_res, const float* alpha_pre,
+                          const float* alpha_post, const float* alpha_res, const float* b_pre, const float* b_post,
+                          const float* b_res, float* out, float* saved, void* workspace, size_t workspace_bytes,
+                          int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
+                          float rmsnorm_eps, void* stream) {
+    int st = check_dyn("layer_dynamic_fwd", batch, n, hidden, x_dtype, weight_dtype, num_iters);
+    if (st) return st;
+    MHC_REQUIRE(weight && phi_pre && phi_post && phi_res && alpha_pre && alpha_post && alpha_res && b_pre &&
+                    b_post && b_res && saved,
+                "layer_dynamic_fwd: null parameter pointer");
+    MHC_REQUIRE(batch == 0 || (x && out), "layer_dynamic_fwd: null x/out");
+    hipStream_t s = (hipStream_t)stream;
+    const DynSaved d = dyn_saved(batch, n, hidden);
+    float* w32 = saved + d.w_off;
+    hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
+    if (e != hipSuccess || batch == 0) return hip_status(e);
+    const int64_t K = (int64_t)n * hidden;
+    const ProjFwdWs w = proj_fwd_ws(batch, K);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "layer_dynamic_fwd: workspace smaller than mhc_layer_dynamic_fwd_workspace_size()");
+    bf16_raw_t* phib = (bf16_raw_t*)((char*)workspace + w.phib_off);
+    float* pp = (float*)((char*)workspace + w.p_off);
+    float* ss = (float*)((char*)workspace + w.ss_off);
+    const int np = 2 * n + n * n;
+    e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+    if (e == hipSuccess) e = launch_proj_mfma(x_dtype, x, phib, pp, ss, batch, K, w.ks, s);
+    if (e == hipSuccess)
+        e = launch_dyn_coef_fwd(n, pp, ss, w.ks, batch, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
+                                saved + d.coef_off, saved + d.p_off, saved + d.rh_off, num_iters, sinkhorn_eps,
+                                rmsnorm_eps, s);
+    if (e == hipSuccess)
+        e = launch_layer_fwd(x_dtype, n, x, w32, saved + d.coef_off, np, out, nullptr, batch, hidden, rmsnorm_eps, s);
+    return hip_status(e);
+}
+
+struct DynBwdWs {
+    int grid, cblocks, tiles;
+    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, total;
+};
+
+static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
+    DynBwdWs w{};
+    const int64_t np = 2 * n + n * n;
+    const int64_t K = (int64_t)n * hidden;
+    w.grid = batch > 0 ? layer_bwd_grid(x_dtype, n, batch, hidden) : 1;
+    w.cblocks = batch > 0 ? dyn_coef_bwd_blocks(n, batch) : 1;
+    w.tiles = batch > 0 ? dyn_dx_tiles(batch, hidden) : 1;
+    size_t o = 0;
+    w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
+    w.scal_off = o; o += align256((size_t)batch * (n * n + 2 * n + 2) * 4);
+    w.dp_off = o; o += align256((size_t)batch * 32 * 4);
+    w.s_off = o; o += align256((size_t)batch * 4);
+    w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
+    w.phip_off = o; o += align256((size_t)w.tiles * np * K * 4);
+    w.stw_off = o; o += align256((size_t)kDwSplit * hidden * 4);
+    w.stp_off = o; o += align256((size_t)kDwSplit * np * K * 4);
+    w.total = o;
+    return w;
+}
+
+size_t mhc_layer_dynamic_bwd_workspace_size(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
+    if (batch < 0 || n < 1 || hidden < 1) return 0;
+    return dyn_bwd_ws(batch, n, hidden, x_dtype).total;
+}
+
+int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype, int32_t weight_dtype,
+                          const float* phi_pre, const float* phi_post, const float* phi_res, const float* alpha_pre,
+                          const float* alpha_post, const float* alpha_res, const float* b_pre, const float* b_post,
+                          const float* b_res, const float* saved, void* grad_x, void* grad_weight, float* grad_phi,
+                          float* grad_alpha, float* grad_b, void* workspace, size_t workspace_bytes, int64_t batch,
+                          int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
+                          void* stream) {
+    (void)b_pre;
+    (void)b_post;
+    int st = check_dyn("layer_dynamic_bwd", batch, n, hidden, x_dtype, weight_dtype, num_iters);
+    if (st) return st;
+    MHC_REQUIRE(phi_pre && phi_post && phi_res && alpha_pre && alpha_post && alpha_res && b_res && saved,
+                "layer_dynamic_bwd: null parameter pointer");
+    MHC_REQUIRE(grad_weight && grad_phi && grad_alpha && grad_b, "layer_dynamic_bwd: null gradient pointer");
+    MHC_REQUIRE(batch == 0 || (grad_out && x && grad_x), "layer_dynamic_bwd: null grad_out/x/grad_x");
+    const DynBwdWs w = dyn_bwd_ws(batch, n, hidden, x_dtype);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "layer_dynamic_bwd: workspace smaller than mhc_layer_dynamic_bwd_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    float* dw_part = (float*)(ws + w.dw_off);
+    float* scal = (float*)(ws + w.scal_off);
+    float* dp = (float*)(ws + w.dp_off);
+    float* stok = (float*)(ws + w.s_off);
+    float* cpart = (float*)(ws + w.cpart_off);
+    float* phip = (float*)(ws + w.phip_off);
+    float* stw = (float*)(ws + w.stw_off);
+    float* stp = (float*)(ws + w.stp_off);
+    const DynSaved d = dyn_saved(batch, n, hidden);
+    const int np = 2 * n + n * n;
+    const int64_t K = (int64_t)n * hidden;
+    const float* w32 = saved + d.w_off;
+    hipError_t e = hipSuccess;
+    int rows_w = w.grid, rows_p = w.tiles, rows_c = w.cblocks;
+    if (batch == 0) {
+        rows_w = rows_p = rows_c = 1;
+        e = launch_fill_zero(dw_part, hidden, s);
+        if (e == hipSuccess) e = launch_fill_zero(phip, (int64_t)np * K, s);
+        if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
+    } else {
+        e = launch_layer_bwd(x_dtype, n, 1, grad_out, x, w32, saved + d.coef_off, np, nullptr, dw_part, scal, w.grid,
+                             batch, hidden, rmsnorm_eps, s);
+        if (e == hipSuccess)
+            e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
+                                    alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
+                                    s);
+        if (e == hipSuccess)
+            e = launch_dyn_dx(x_dtype, n, grad_out, x, w32, saved + d.coef_off, scal, dp, stok, phi_pre, phi_post,
+                              phi_res, grad_x, phip, w.tiles, batch, hidden, s);
+    }
+    if (e == hipSuccess) e = launch_column_partial(dw_part, rows_w, hidden, stw, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(0, weight_dtype, stw, kDwSplit, hidden, grad_weight, nullptr, 0, nullptr, nullptr,
+                                  nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+    if (e == hipSuccess) e = launch_column_partial(phip, rows_p, (int64_t)np * K, stp, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(0, kF32, stp, kDwSplit, (int64_t)np * K, grad_phi, nullptr, 0, nullptr, nullptr,
+                                  nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+    if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
+    return hip_status(e);
+}
+
 }  // extern "C"

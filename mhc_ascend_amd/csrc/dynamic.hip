@@ -1,0 +1,671 @@
+// Dynamic-H mHC layer: per-token H projected from the flattened token row
+// (bindings.cpp:880-952 forward, 600-874 backward), and the projection
+// operators fused_rmsnorm_matmul / compute_rms (bindings.cpp:480-566).
+//
+//   x_flat = x[b].reshape(n*C);  r_h = sqrt(mean(x_flat^2) + rms_eps)
+//   P = x_flat . Phi^T,  Phi = [phi_pre; phi_post; phi_res]  ([2n+n^2, nC])
+//   t_k = alpha_k P_k / r_h + b_k;  h_pre = sigmoid(t_pre),
+//   h_post = 2 sigmoid(t_post),  M = SK(exp(t_res as n x n))
+//   then the fused aggregate -> RMSNorm -> distribute pass of layer.hip.
+//
+// Kernels here:
+//   phi_split_kernel    Phi (fp32) -> bf16 hi / mid / lo planes [3][32][K]
+//                       (hi + mid + lo carries all 24 mantissa bits)
+//   proj_mfma_kernel    P partials (split-K) and sum(x^2) partials; bf16
+//                       MFMA 16x16x32 on the planes gives fp32 accuracy
+//   dyn_coef_fwd_kernel per token: sum partials, t, sigmoid, Sinkhorn
+//   dyn_coef_bwd_kernel per token: Sinkhorn adjoint, dP, d r_h, db/dalpha
+//   dyn_dx_kernel       dx = stream terms + dP.Phi + s x_flat; dPhi partials
+#include "mhc_device.h"
+#include "mhc_internal.h"
+#include "mhc_rows.h"
+
+namespace mhc {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kNPad = 32;  // projection outputs padded to two 16-wide MFMA tiles
+
+__device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+    // A rows = lane % 16, B cols = lane % 16, k = 8 * (lane / 16) + 0..7;
+    // D[4 * (lane / 16) + i][lane % 16] in element i.
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Row o of the concatenated projection (pre rows, then post, then res).
+__device__ __forceinline__ const float* phi_row(const float* pre, const float* post, const float* res, int n, int o,
+                                                int64_t K) {
+    if (o < n) return pre + (int64_t)o * K;
+    if (o < 2 * n) return post + (int64_t)(o - n) * K;
+    return res + (int64_t)(o - 2 * n) * K;
+}
+
+// ---------------------------------------------------------------------------
+// fp32 -> three bf16 terms: v = hi + mid + lo exactly up to the last bit
+// for normal values (3 x 8 significant bits = the fp32 mantissa).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void split3(float v, float& h, float& m, float& l) {
+    h = bf16_to_f32(f32_to_bf16(v));
+    const float r = v - h;
+    m = bf16_to_f32(f32_to_bf16(r));
+    l = r - m;
+}
+
+// Phi -> bf16 planes phib[p][o][k], p = hi / mid / lo; rows np..31 are zero.
+// grid-stride over 32 * K / 8.
+__global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict__ pre, const float* __restrict__ post,
+                                                        const float* __restrict__ res, int n, int np, int64_t K,
+                                                        bf16_t* __restrict__ phib) {
+    const int64_t per_row = K / 8;
+    const int64_t total = (int64_t)kNPad * per_row;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int o = (int)(i / per_row);
+        const int64_t k = (i % per_row) * 8;
+        float v[8];
+        if (o < np) {
+            load_run<float, 8>(phi_row(pre, post, res, n, o, K) + k, v);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = 0.f;
+        }
+        uint32_t w[3][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float h0, m0, l0, h1, m1, l1;
+            split3(v[2 * e], h0, m0, l0);
+            split3(v[2 * e + 1], h1, m1, l1);
+            w[0][e] = pack_bf16(h0, h1);
+            w[1][e] = pack_bf16(m0, m1);
+            w[2][e] = pack_bf16(l0, l1);
+        }
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+            *reinterpret_cast<uint4*>(phib + ((int64_t)p * kNPad + o) * K + k) =
+                make_uint4(w[p][0], w[p][1], w[p][2], w[p][3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K projection on MFMA.  Workgroup = 64 tokens (4 M-tiles of 16) x
+// one K range; its 4 waves take interleaved 32-wide k steps and are summed
+// through LDS.  bf16 x is exact in bf16: P = x.(hi + mid + lo) (3 MFMAs per
+// tile); fp32 x is split the same way and the six products down to 2^-16
+// relative weight are kept (xh.(hi+mid+lo) + xm.(hi+mid) + xl.hi), leaving
+// terms of order 2^-24.  Also sum x^2.  p_part[ks][B][32], ss_part[ks][B].
+// ---------------------------------------------------------------------------
+template <typename TX>
+__global__ __launch_bounds__(256) void proj_mfma_kernel(const TX* __restrict__ x, const bf16_t* __restrict__ phib,
+                                                        float* __restrict__ p_part, float* __restrict__ ss_part,
+                                                        int64_t B, int64_t K, int64_t kchunk) {
+    __shared__ float red[3][36][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row = lane & 15;
+    const int kg = lane >> 4;
+    const int64_t tok0 = (int64_t)blockIdx.x * 64;
+    const int64_t kb = (int64_t)blockIdx.y * kchunk;
+    const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
+
+    f32x4_t acc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    float ss[4] = {0.f, 0.f, 0.f, 0.f};
+    const TX* xr[4];
+    bool vr[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const int64_t tok = tok0 + mt * 16 + row;
+        vr[mt] = tok < B;
+        xr[mt] = x + (vr[mt] ? tok : 0) * K;
+    }
+    const bf16_t* pb[3][2];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) pb[p][nt] = phib + ((int64_t)p * kNPad + nt * 16 + row) * K;
+    }
+
+    for (int64_t k0 = kb + wave * 32; k0 < ke; k0 += 128) {
+        const int64_t kk = k0 + kg * 8;
+        u32x4_t bv[3][2];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) bv[p][nt] = *reinterpret_cast<const u32x4_t*>(pb[p][nt] + kk);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            if constexpr (sizeof(TX) == 2) {
+                u32x4_t a = u32x4_t{0u, 0u, 0u, 0u};
+                if (vr[mt]) {
+                    const uint4 q = ld16_nt(xr[mt] + kk);
+                    a = u32x4_t{q.x, q.y, q.z, q.w};
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float lo = __uint_as_float(a[e] << 16), hi = __uint_as_float(a[e] & 0xffff0000u);
+                    ss[mt] += lo * lo + hi * hi;
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+                    for (int p = 0; p < 3; ++p) acc[mt][nt] = mfma16x16x32(a, bv[p][nt], acc[mt][nt]);
+                }
+            } else {
+                float v[8];
+                if (vr[mt]) {
+                    load_run_nt<float, 8>(reinterpret_cast<const float*>(xr[mt]) + kk, v);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+                }
+                u32x4_t ah, am, al;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ss[mt] += v[2 * e] * v[2 * e] + v[2 * e + 1] * v[2 * e + 1];
+                    float h0, m0, l0, h1, m1, l1;
+                    split3(v[2 * e], h0, m0, l0);
+                    split3(v[2 * e + 1], h1, m1, l1);
+                    ah[e] = pack_bf16(h0, h1);
+                    am[e] = pack_bf16(m0, m1);
+                    al[e] = pack_bf16(l0, l1);
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    acc[mt][nt] = mfma16x16x32(ah, bv[0][nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(ah, bv[1][nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(am, bv[0][nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(ah, bv[2][nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(am, bv[1][nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(al, bv[0][nt], acc[mt][nt]);
+                }
+            }
+        }
+    }
+
+    // waves 1..3 hand their partials to wave 0 through LDS
+    if (wave > 0) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave - 1][(mt * 2 + nt) * 4 + i][lane] = acc[mt][nt][i];
+            }
+            red[wave - 1][32 + mt][lane] = ss[mt];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mt][nt][i] += red[q][(mt * 2 + nt) * 4 + i][lane];
+            }
+            ss[mt] += red[q][32 + mt][lane];
+        }
+    }
+    float* pp = p_part + (int64_t)blockIdx.y * B * kNPad;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t tok = tok0 + mt * 16 + kg * 4 + i;
+            if (tok < B) {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) pp[tok * kNPad + nt * 16 + row] = acc[mt][nt][i];
+            }
+        }
+        // lanes row, row+16, row+32, row+48 hold parts of token row's sum
+        float s2 = ss[mt];
+        s2 += __shfl_xor(s2, 16, kWave);
+        s2 += __shfl_xor(s2, 32, kWave);
+        const int64_t tok = tok0 + mt * 16 + row;
+        if (kg == 0 && tok < B) ss_part[(int64_t)blockIdx.y * B + tok] = s2;
+    }
+}
+
+// P[b][o] = sum_ks p_part[ks][b][o] for o < np (standalone projection).
+__global__ __launch_bounds__(256) void proj_reduce_kernel(const float* __restrict__ p_part, int ks, int64_t B,
+                                                          int np, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B * np) return;
+    const int64_t b = i / np;
+    const int o = (int)(i % np);
+    float s = 0.f;
+    for (int q = 0; q < ks; ++q) s += p_part[((int64_t)q * B + b) * kNPad + o];
+    out[i] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Per-token coefficients (bindings.cpp:909-929).  One token per group of
+// G = pow2ceil(n) lanes; lane r owns t_pre[r], t_post[r] and row r of t_res.
+// coef[b] = (h_pre, h_post, M row-major); p_out[b] = P (np values); rh[b].
+// ---------------------------------------------------------------------------
+template <int N>
+__global__ __launch_bounds__(256) void dyn_coef_fwd_kernel(
+    const float* __restrict__ p_part, const float* __restrict__ ss_part, int ks, int64_t B, int64_t K,
+    const float* __restrict__ a_pre, const float* __restrict__ a_post, const float* __restrict__ a_res,
+    const float* __restrict__ b_pre, const float* __restrict__ b_post, const float* __restrict__ b_res,
+    float* __restrict__ coef, float* __restrict__ p_out, float* __restrict__ rh, int iters, float sk_eps,
+    float rms_eps) {
+    constexpr int G = pow2ceil(N);
+    constexpr int NP = 2 * N + N * N;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t tok = gid / G;
+    const int r = (int)(gid % G);
+    const bool tv = tok < B;
+    const bool active = tv && r < N;
+    float pp = 0.f, pq = 0.f, pr[N], ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < N; ++c) pr[c] = 0.f;
+    if (tv) {
+        for (int q = 0; q < ks; ++q) {
+            const float* pb = p_part + ((int64_t)q * B + tok) * kNPad;
+            ss += ss_part[(int64_t)q * B + tok];
+            if (r < N) {
+                pp += pb[r];
+                pq += pb[N + r];
+#pragma unroll
+                for (int c = 0; c < N; ++c) pr[c] += pb[2 * N + r * N + c];
+            }
+        }
+    }
+    const float r_h = sqrtf(ss / (float)K + rms_eps);
+    const float inv = 1.f / r_h;
+    const int rr = r < N ? r : 0;
+    const float hp = sigmoidf(pp * a_pre[0] * inv + b_pre[rr]);
+    const float hq = 2.f * sigmoidf(pq * a_post[0] * inv + b_post[rr]);
+    float e[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) e[c] = active ? expf(pr[c] * a_res[0] * inv + b_res[rr * N + c]) : 0.f;
+    sk_forward<N>(e, iters, sk_eps, active);
+    if (active) {
+        float* cf = coef + tok * NP;
+        cf[r] = hp;
+        cf[N + r] = hq;
+#pragma unroll
+        for (int c = 0; c < N; ++c) cf[2 * N + r * N + c] = e[c];
+        float* po = p_out + tok * NP;
+        po[r] = pp;
+        po[N + r] = pq;
+#pragma unroll
+        for (int c = 0; c < N; ++c) po[2 * N + r * N + c] = pr[c];
+    }
+    if (tv && r == 0) rh[tok] = r_h;
+}
+
+// ---------------------------------------------------------------------------
+// Per-token coefficient backward (bindings.cpp:777-848):
+//   dt_pre = dh_pre_act h_pre (1 - h_pre);  dt_post = dh_post_act h_post (1 - h_post/2)
+//   dt_res = SK^T(dM) * exp(t_res)
+//   dP_k = alpha_k dt_k / r_h;  d r_h = -sum_k alpha_k dt_k P_k / r_h^2
+//   s = d r_h / (K r_h)  (coefficient of x_flat in dx)
+// dp_out[b][32] (zero padded), s_out[b]; per-workgroup partial sums of
+// db (np values) and dalpha (3) in part[blk][np + 3].
+// ---------------------------------------------------------------------------
+template <int N>
+__global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
+    const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
+    const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
+    const float* __restrict__ a_post, const float* __restrict__ a_res, const float* __restrict__ b_res,
+    float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int iters, float sk_eps) {
+    constexpr int G = pow2ceil(N);
+    constexpr int NP = 2 * N + N * N;
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NV = NP + 3;
+    __shared__ float red[4 * NV];
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t tok = gid / G;
+    const int r = (int)(gid % G);
+    const bool tv = tok < B;
+    const bool active = tv && r < N;
+    const int rr = r < N ? r : 0;
+    const int64_t tk = tv ? tok : 0;
+    const float* sc = scal + tk * (NS + 2);
+    const float* cf = coef + tk * NP;
+    const float* pv = p + tk * NP;
+    const float ap = a_pre[0], aq = a_post[0], ar = a_res[0];
+    const float r_h = rh[tk];
+    const float inv = 1.f / r_h;
+
+    float gm[N], e[N], pr[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+        gm[c] = active ? sc[rr * N + c] : 0.f;
+        pr[c] = pv[2 * N + rr * N + c];
+        e[c] = active ? expf(pr[c] * ar * inv + b_res[rr * N + c]) : 0.f;
+    }
+    sk_backward<N>(gm, e, iters, sk_eps, active);
+    const float hp = cf[rr], hq = cf[N + rr];
+    const float dt_pre = active ? sc[N * N + N + rr] * hp * (1.f - hp) : 0.f;
+    const float dt_post = active ? sc[N * N + rr] * hq * (1.f - 0.5f * hq) : 0.f;
+    float dt_res[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) dt_res[c] = active ? gm[c] * e[c] : 0.f;
+    const float pp = pv[rr], pq = pv[N + rr];
+    float lp = 0.f;
+#pragma unroll
+    for (int c = 0; c < N; ++c) lp += dt_res[c] * pr[c];
+    const float l_pre = dt_pre * pp, l_post = dt_post * pq;
+    const float tot = group_sum<G>(ap * l_pre + aq * l_post + ar * lp);
+    if (active) {
+        float* dp = dp_out + tok * kNPad;
+        dp[r] = ap * dt_pre * inv;
+        dp[N + r] = aq * dt_post * inv;
+#pragma unroll
+        for (int c = 0; c < N; ++c) dp[2 * N + r * N + c] = ar * dt_res[c] * inv;
+        if (r == 0) {
+            for (int o = NP; o < kNPad; ++o) dp[o] = 0.f;
+            s_out[tok] = -tot * inv * inv * inv / (float)K;
+        }
+    }
+    // per-workgroup partial sums of db and dalpha
+    float v[NV];
+#pragma unroll
+    for (int q = 0; q < N; ++q) {
+        v[q] = (r == q) ? dt_pre : 0.f;
+        v[N + q] = (r == q) ? dt_post : 0.f;
+#pragma unroll
+        for (int c = 0; c < N; ++c) v[2 * N + q * N + c] = (r == q) ? dt_res[c] : 0.f;
+    }
+    v[NP] = l_pre * inv;
+    v[NP + 1] = l_post * inv;
+    v[NP + 2] = lp * inv;
+    block_sum<NV>(v, red);
+    if (threadIdx.x < NV) {
+        float t = 0.f;
+#pragma unroll
+        for (int q = 0; q < NV; ++q) t = (q == (int)threadIdx.x) ? v[q] : t;
+        part[(int64_t)blockIdx.x * NV + threadIdx.x] = t;
+    }
+}
+
+// out[c] = sum_r part[r][c] for a few columns (db, dalpha); one workgroup.
+__global__ __launch_bounds__(256) void small_column_sum_kernel(const float* __restrict__ part, int rows, int cols,
+                                                               float* __restrict__ out_db, float* __restrict__ out_da,
+                                                               int np) {
+    __shared__ float red[256];
+    for (int c = 0; c < cols; ++c) {
+        float s = 0.f;
+        for (int q = threadIdx.x; q < rows; q += blockDim.x) s += part[(int64_t)q * cols + c];
+        red[threadIdx.x] = s;
+        __syncthreads();
+        for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) {
+            if (c < np) out_db[c] = red[0];
+            else out_da[c - np] = red[0];
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dx and dPhi partials.  Workgroup = 64 channels x a tile of tokens; lane =
+// one channel c for all N streams; the 4 waves take every 4th token of the
+// tile.  Phi[o][j*C + c] (NP x N values) stays in registers.
+//   MODE 0 (layer): dx_j = sum_i M_ij g_i + h_pre_j gxa + s x_j + sum_o dP_o Phi_o[j*C+c],
+//                   gxa = w gy inv - xa k2, from the per-token scalars of the
+//                   layer backward reduction;
+//   MODE 1 (projection only, N = 1, C = K): dx = sum_o dP_o Phi_o[c].
+//   dPhi_part[tile][o][j*C + c] = sum_{t in tile} dP_o[t] x_j[t][c].
+// ---------------------------------------------------------------------------
+template <typename TX, int N, int NP, int MODE>
+__global__ __launch_bounds__(256) void dyn_dx_kernel(
+    const float* __restrict__ g, const TX* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ coef, const float* __restrict__ scal, const float* __restrict__ dp, int dp_stride,
+    const float* __restrict__ s, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
+    const float* __restrict__ phi_res, int np_rt, TX* __restrict__ dx, float* __restrict__ dphi_part, int64_t B,
+    int C, int64_t tile) {
+    constexpr int NC = 2 * N + N * N;
+    constexpr int NS = N * N + 2 * N;
+    __shared__ float red[3][N * 6][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = blockIdx.x * 64 + lane;
+    const bool cv = c < C;
+    const int cc = cv ? c : 0;
+    const int64_t K = (int64_t)N * C;
+    const int npr = MODE == 0 ? NP : np_rt;
+
+    float ph[NP][N];
+#pragma unroll
+    for (int o = 0; o < NP; ++o) {
+        const bool ov = o < npr;
+        const float* row = ov ? phi_row(phi_pre, phi_post, phi_res, MODE == 0 ? N : np_rt, o, K) : phi_pre;
+#pragma unroll
+        for (int j = 0; j < N; ++j) ph[o][j] = (ov && cv) ? row[(int64_t)j * C + cc] : 0.f;
+    }
+    float acc[NP][N];
+#pragma unroll
+    for (int o = 0; o < NP; ++o) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) acc[o][j] = 0.f;
+    }
+    const float wv = (MODE == 0 && cv) ? w[cc] : 0.f;
+    const int64_t t0 = (int64_t)blockIdx.y * tile;
+    const int64_t t1 = (t0 + tile < B) ? t0 + tile : B;
+
+    for (int64_t t = t0 + wave; t < t1; t += 4) {
+        float dpv[NP];
+#pragma unroll
+        for (int o = 0; o < NP; ++o) dpv[o] = (o < npr) ? dp[t * dp_stride + o] : 0.f;
+        float xi[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) xi[j] = cv ? VecIO<TX>::scalar(x + (t * N + j) * (int64_t)C + cc) : 0.f;
+        float d[N];
+        if constexpr (MODE == 0) {
+            const float* cf = coef + t * NC;
+            const float* sc = scal + t * (NS + 2);
+            const float inv = sc[NS], k2 = sc[NS + 1], sv = s[t];
+            float gi[N];
+#pragma unroll
+            for (int i = 0; i < N; ++i) gi[i] = cv ? __builtin_nontemporal_load(g + (t * N + i) * (int64_t)C + cc) : 0.f;
+            float xa = 0.f, gy = 0.f;
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                xa += cf[i] * xi[i];
+                gy += cf[N + i] * gi[i];
+            }
+            const float gxa = wv * gy * inv - xa * k2;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                float v = cf[j] * gxa + sv * xi[j];
+#pragma unroll
+                for (int i = 0; i < N; ++i) v += cf[2 * N + i * N + j] * gi[i];
+                d[j] = v;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < N; ++j) d[j] = 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+#pragma unroll
+            for (int o = 0; o < NP; ++o) {
+                d[j] += dpv[o] * ph[o][j];
+                acc[o][j] += dpv[o] * xi[j];
+            }
+        }
+        if (cv) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) VecIO<TX>::put(dx + (t * N + j) * (int64_t)C + cc, d[j]);
+        }
+    }
+
+    // sum the 4 waves' dPhi partials (6 projection rows per round) and store
+    float* out = dphi_part + (int64_t)blockIdx.y * npr * K;
+#pragma unroll
+    for (int o0 = 0; o0 < NP; o0 += 6) {
+        if (wave > 0) {
+#pragma unroll
+            for (int q = 0; q < 6; ++q) {
+                if (o0 + q < NP) {
+#pragma unroll
+                    for (int j = 0; j < N; ++j) red[wave - 1][q * N + j][lane] = acc[o0 + q][j];
+                }
+            }
+        }
+        __syncthreads();
+        if (wave == 0 && cv) {
+#pragma unroll
+            for (int q = 0; q < 6; ++q) {
+                const int o = o0 + q;
+                if (o < npr) {
+#pragma unroll
+                    for (int j = 0; j < N; ++j) {
+                        const float v = acc[o][j] + red[0][q * N + j][lane] + red[1][q * N + j][lane] +
+                                        red[2][q * N + j][lane];
+                        out[(int64_t)o * K + (int64_t)j * C + c] = v;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
+                            bf16_t* phib, hipStream_t s) {
+    const int64_t total = (int64_t)kNPad * (K / 8);
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(phi_split_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pre, post, res, n, np, K, phib);
+    return hipGetLastError();
+}
+
+int proj_ksplit(int64_t B, int64_t K) {
+    const int64_t mblocks = (B + 63) / 64;
+    int64_t ks = (2 * (int64_t)device_cu_count() + mblocks - 1) / mblocks;
+    const int64_t kmax = K / 256;
+    if (ks > kmax) ks = kmax;
+    if (ks < 1) ks = 1;
+    return (int)ks;
+}
+
+hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_t* phib, float* p_part, float* ss_part, int64_t B,
+                            int64_t K, int ks, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    int64_t kchunk = (K + ks - 1) / ks;
+    kchunk = ((kchunk + 127) / 128) * 128;
+    const dim3 grid((unsigned)((B + 63) / 64), (unsigned)ks);
+    const int tok = timing_begin("proj", s);
+    if (x_dtype == kBF16) {
+        hipLaunchKernelGGL(proj_mfma_kernel<bf16_t>, grid, dim3(256), 0, s, (const bf16_t*)x, phib, p_part, ss_part, B,
+                           K, kchunk);
+    } else {
+        hipLaunchKernelGGL(proj_mfma_kernel<float>, grid, dim3(256), 0, s, (const float*)x, phib, p_part, ss_part, B, K,
+                           kchunk);
+    }
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s) {
+    const int64_t total = B * np;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(proj_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, p_part, ks, B, np,
+                       out);
+    return hipGetLastError();
+}
+
+#define MHC_DYN_N(n, ...)                                        \
+    switch (n) {                                                 \
+        case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }    \
+        default: return hipErrorInvalidValue;                    \
+    }
+
+hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part, int ks, int64_t B, int64_t K,
+                               const float* a_pre, const float* a_post, const float* a_res, const float* b_pre,
+                               const float* b_post, const float* b_res, float* coef, float* p_out, float* rh,
+                               int iters, float sk_eps, float rms_eps, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    const int64_t threads = B * pow2ceil(n);
+    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    MHC_DYN_N(n, hipLaunchKernelGGL((dyn_coef_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, p_part, ss_part, ks, B,
+                                    K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, iters, sk_eps,
+                                    rms_eps));
+    return hipGetLastError();
+}
+
+int dyn_coef_bwd_blocks(int n, int64_t B) { return (int)((B * pow2ceil(n) + 255) / 256); }
+
+hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
+                               int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
+                               const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
+                               hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)dyn_coef_bwd_blocks(n, B);
+    MHC_DYN_N(n, hipLaunchKernelGGL((dyn_coef_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                                    a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps));
+    return hipGetLastError();
+}
+
+hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
+                                   hipStream_t s) {
+    hipLaunchKernelGGL(small_column_sum_kernel, dim3(1), dim3(256), 0, s, part, rows, cols, out_db, out_da, np);
+    return hipGetLastError();
+}
+
+int dyn_dx_tiles(int64_t B, int64_t C) {
+    const int64_t bx = (C + 63) / 64;
+    int64_t tiles = (4 * (int64_t)device_cu_count() + bx - 1) / bx;
+    if (tiles > (B + 3) / 4) tiles = (B + 3) / 4;
+    if (tiles < 1) tiles = 1;
+    return (int)tiles;
+}
+
+hipError_t launch_dyn_dx(int x_dtype, int n, const float* g, const void* x, const float* w, const float* coef,
+                         const float* scal, const float* dp, const float* s_tok, const float* phi_pre,
+                         const float* phi_post, const float* phi_res, void* dx, float* dphi_part, int tiles,
+                         int64_t B, int64_t C, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    const int64_t tile = (B + tiles - 1) / tiles;
+    const dim3 grid((unsigned)((C + 63) / 64), (unsigned)tiles);
+    const int tok = timing_begin("dyn_dx", s);
+    if (x_dtype == kBF16) {
+        MHC_DYN_N(n, hipLaunchKernelGGL((dyn_dx_kernel<bf16_t, N_, 2 * N_ + N_ * N_, 0>), grid, dim3(256), 0, s, g,
+                                        (const bf16_t*)x, w, coef, scal, dp, kNPad, s_tok, phi_pre, phi_post, phi_res,
+                                        0, (bf16_t*)dx, dphi_part, B, (int)C, tile));
+    } else {
+        MHC_DYN_N(n, hipLaunchKernelGGL((dyn_dx_kernel<float, N_, 2 * N_ + N_ * N_, 0>), grid, dim3(256), 0, s, g,
+                                        (const float*)x, w, coef, scal, dp, kNPad, s_tok, phi_pre, phi_post, phi_res,
+                                        0, (float*)dx, dphi_part, B, (int)C, tile));
+    }
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+// Projection-only backward: dx[b][k] = sum_o dP[b][o] Phi[o][k] (fp32 out),
+// dPhi partials as above; dP [B][np] with row stride np; Phi [np][K].
+hipError_t launch_proj_bwd(const float* dP, int np, const float* x, const float* phi, float* dx, float* dphi_part,
+                           int tiles, int64_t B, int64_t K, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    const int64_t tile = (B + tiles - 1) / tiles;
+    const dim3 grid((unsigned)((K + 63) / 64), (unsigned)tiles);
+    hipLaunchKernelGGL((dyn_dx_kernel<float, 1, kNPad, 1>), grid, dim3(256), 0, s, nullptr, x, nullptr, nullptr,
+                       nullptr, dP, np, nullptr, phi, phi, phi, np, dx, dphi_part, B, (int)K, tile);
+    return hipGetLastError();
+}
+
+}  // namespace mhc

@@ -460,6 +460,12 @@ __global__ __launch_bounds__(256) void layer_finalize_kernel(
     }
 }
 
+template <typename TW>
+__global__ __launch_bounds__(256) void weight_f32_kernel(const TW* __restrict__ w, int64_t C, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < C) out[i] = VecIO<TW>::scalar(w + i);
+}
+
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.f;
@@ -468,6 +474,17 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, i
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
+hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, hipStream_t s) {
+    if (C <= 0) return hipSuccess;
+    const unsigned blocks = (unsigned)((C + 255) / 256);
+    if (w_dtype == kBF16) {
+        hipLaunchKernelGGL(weight_f32_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)w, C, out);
+    } else {
+        hipLaunchKernelGGL(weight_f32_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)w, C, out);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);

@@ -74,6 +74,34 @@ hipError_t launch_distribute_bwd(int dt, int n, const float* g, const void* x, c
                                  int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
                                  float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
 
+// ---- dynamic.hip -----------------------------------------------------------
+typedef uint16_t bf16_raw_t;
+hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
+                            bf16_raw_t* phib, hipStream_t s);
+int proj_ksplit(int64_t B, int64_t K);
+hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_raw_t* phib, float* p_part, float* ss_part,
+                            int64_t B, int64_t K, int ks, hipStream_t s);
+hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s);
+hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part, int ks, int64_t B, int64_t K,
+                               const float* a_pre, const float* a_post, const float* a_res, const float* b_pre,
+                               const float* b_post, const float* b_res, float* coef, float* p_out, float* rh,
+                               int iters, float sk_eps, float rms_eps, hipStream_t s);
+int dyn_coef_bwd_blocks(int n, int64_t B);
+hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
+                               int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
+                               const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
+                               hipStream_t s);
+hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
+                                   hipStream_t s);
+int dyn_dx_tiles(int64_t B, int64_t C);
+hipError_t launch_dyn_dx(int x_dtype, int n, const float* g, const void* x, const float* w, const float* coef,
+                         const float* scal, const float* dp, const float* s_tok, const float* phi_pre,
+                         const float* phi_post, const float* phi_res, void* dx, float* dphi_part, int tiles,
+                         int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_proj_bwd(const float* dP, int np, const float* x, const float* phi, float* dx, float* dphi_part,
+                           int tiles, int64_t B, int64_t K, hipStream_t s);
+hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, hipStream_t s);
+
 // ---- sinkhorn.hip ----------------------------------------------------------
 hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batch, int iters, float eps,
                                hipStream_t s);

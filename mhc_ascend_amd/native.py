@@ -321,3 +321,146 @@ def mhc_layer_static_bwd(grad_out: torch.Tensor, x: torch.Tensor, rmsnorm_weight
              ptr(hr), ptr(saved), ptr(grad_x), ptr(gw), ptr(ghp), ptr(ghq), ptr(ghr), ptr(ws), int(ws_bytes), B, n,
              C, int(num_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
     return grad_x, gw, ghp, ghq, ghr
+
+
+# =============================================================================
+# Dynamic-H projection (bindings.cpp:480-541) and fused dynamic layer
+# (bindings.cpp:600-952)
+# =============================================================================
+
+def _ws(dev, nbytes: int) -> torch.Tensor:
+    return torch.empty((max(int(nbytes), 1),), dtype=torch.uint8, device=dev)
+
+
+def fused_rmsnorm_matmul_fwd(inp: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """P = inp @ weight^T, fp32 [B, out_dim] (bindings.cpp:480-528); inp [B, K]
+    fp32 or bf16, weight [out_dim, K].  Split-bf16 MFMA keeps ~fp32 accuracy
+    (the reference rounds inputs and P to bf16)."""
+    _check_device("fused_rmsnorm_matmul_fwd", inp, weight)
+    if inp.dim() != 2 or weight.dim() != 2 or weight.size(1) != inp.size(1):
+        raise RuntimeError("fused_rmsnorm_matmul_fwd: expected inp [B, K] and weight [out_dim, K]")
+    x = _storage(inp)
+    phi = _f32c(weight)
+    B, K = x.shape
+    out = torch.empty((B, phi.size(0)), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        wsb = _lib.load().mhc_fused_rmsnorm_matmul_fwd_workspace_size(B, K)
+        ws = _ws(x.device, wsb)
+        call("mhc_fused_rmsnorm_matmul_fwd", ptr(x), dtype_code(x.dtype), ptr(phi), ptr(out), ptr(ws), int(wsb), B,
+             K, phi.size(0), stream_of(x))
+    return out
+
+
+def fused_rmsnorm_matmul_bwd(grad_out: torch.Tensor, x_flat: torch.Tensor,
+                             phi_concat: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(grad_x = grad_out @ phi, grad_phi = grad_out^T @ x_flat), fp32 (bindings.cpp:530-541)."""
+    _check_device("fused_rmsnorm_matmul_bwd", grad_out, x_flat, phi_concat)
+    g, x, phi = _f32c(grad_out), _f32c(x_flat), _f32c(phi_concat)
+    B, K = x.shape
+    out_dim = phi.size(0)
+    gx = torch.empty((B, K), dtype=torch.float32, device=x.device)
+    gphi = torch.empty((out_dim, K), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        wsb = _lib.load().mhc_fused_rmsnorm_matmul_bwd_workspace_size(B, K, out_dim)
+        ws = _ws(x.device, wsb)
+        call("mhc_fused_rmsnorm_matmul_bwd", ptr(g), ptr(x), ptr(phi), ptr(gx), ptr(gphi), ptr(ws), int(wsb), B, K,
+             out_dim, stream_of(x))
+    return gx, gphi
+
+
+def _scalar_param(a, dev) -> torch.Tensor:
+    """alpha as a 1-element fp32 device tensor (device pointer, no host sync)."""
+    if torch.is_tensor(a):
+        return a.detach().to(device=dev, dtype=torch.float32).reshape(1).contiguous()
+    return torch.full((1,), float(a), dtype=torch.float32, device=dev)
+
+
+def _phi_parts(phi_pre, phi_post, phi_res, n, nC):
+    parts = [_f32c(phi_pre), _f32c(phi_post), _f32c(phi_res)]
+    for t, rows in zip(parts, (n, n, n * n)):
+        if t.numel() != rows * nC:
+            raise RuntimeError(f"dynamic layer: projection of {tuple(t.shape)} does not match [{rows}, {nC}]")
+    return parts
+
+
+def mhc_layer_dynamic_fwd(x_expanded: torch.Tensor, rmsnorm_weight: torch.Tensor, phi_pre: torch.Tensor,
+                          phi_post: torch.Tensor, phi_res: torch.Tensor, alpha_pre, alpha_post, alpha_res,
+                          b_pre: torch.Tensor, b_post: torch.Tensor, b_res: torch.Tensor, sinkhorn_iters: int = 20,
+                          sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Fused dynamic-H forward: (out fp32 [B, n, C], saved) where saved holds
+    the fp32 weight, per-token (h_pre, h_post, M), P and r_h for the
+    backward.  Unlike mhc_layer_fwd_dynamic of the reference (bindings.cpp:
+    880-952, 9 tensors) no [B, C] / [B, nC] intermediates are materialised."""
+    _check_device("mhc_layer_dynamic_fwd", x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, b_pre, b_post,
+                  b_res)
+    x = _layer_x("mhc_layer_dynamic_fwd", x_expanded)
+    B, n, C = x.shape
+    dev = x.device
+    w = _weight(rmsnorm_weight)
+    if w.numel() != C:
+        raise RuntimeError("mhc_layer_dynamic_fwd: rmsnorm_weight must have C elements")
+    pp, pq, pr = _phi_parts(phi_pre, phi_post, phi_res, n, n * C)
+    a = [_scalar_param(v, dev) for v in (alpha_pre, alpha_post, alpha_res)]
+    bp, bq, br = _f32c(b_pre), _f32c(b_post), _f32c(b_res)
+    out = torch.empty((B, n, C), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    saved = torch.empty((lib.mhc_layer_dynamic_saved_size(B, n, C) // 4,), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        wsb = lib.mhc_layer_dynamic_fwd_workspace_size(B, n, C)
+        ws = _ws(dev, wsb)
+        call("mhc_layer_dynamic_fwd", ptr(x), dtype_code(x.dtype), ptr(w), dtype_code(w.dtype), ptr(pp), ptr(pq),
+             ptr(pr), ptr(a[0]), ptr(a[1]), ptr(a[2]), ptr(bp), ptr(bq), ptr(br), ptr(out), ptr(saved), ptr(ws),
+             int(wsb), B, n, C, int(sinkhorn_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
+    return out, saved
+
+
+def mhc_layer_dynamic_bwd(grad_output: torch.Tensor, x_expanded: torch.Tensor, rmsnorm_weight: torch.Tensor,
+                          saved: torch.Tensor, phi_pre: torch.Tensor, phi_post: torch.Tensor, phi_res: torch.Tensor,
+                          alpha_pre, alpha_post, alpha_res, b_pre: torch.Tensor, b_post: torch.Tensor,
+                          b_res: torch.Tensor, sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
+                          rmsnorm_eps: float = 1e-5):
+    """Fused dynamic-H backward.  Returns the reference's 11 gradients
+    (bindings.cpp:600-611): grad_x, grad_rmsnorm_weight, d_phi_pre,
+    d_phi_post, d_phi_res, d_alpha_pre, d_alpha_post, d_alpha_res, d_b_pre,
+    d_b_post, d_b_res."""
+    _check_device("mhc_layer_dynamic_bwd", grad_output, x_expanded, rmsnorm_weight, saved, phi_pre, phi_post,
+                  phi_res, b_pre, b_post, b_res)
+    x = _layer_x("mhc_layer_dynamic_bwd", x_expanded)
+    B, n, C = x.shape
+    dev = x.device
+    if grad_output.shape != x.shape:
+        raise RuntimeError("mhc_layer_dynamic_bwd: grad_output must match x [B, n, C]")
+    g = _f32c(grad_output)
+    wdt = rmsnorm_weight.dtype if rmsnorm_weight.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    pp, pq, pr = _phi_parts(phi_pre, phi_post, phi_res, n, n * C)
+    a = [_scalar_param(v, dev) for v in (alpha_pre, alpha_post, alpha_res)]
+    bp, bq, br = _f32c(b_pre), _f32c(b_post), _f32c(b_res)
+    np_ = 2 * n + n * n
+    grad_x = torch.empty_like(x)
+    gw = torch.empty((C,), dtype=wdt, device=dev)
+    gphi = torch.empty((np_, n * C), dtype=torch.float32, device=dev)
+    galpha = torch.empty((3,), dtype=torch.float32, device=dev)
+    gb = torch.empty((np_,), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        wsb = _lib.load().mhc_layer_dynamic_bwd_workspace_size(B, n, C, dtype_code(x.dtype))
+        ws = _ws(dev, wsb)
+        call("mhc_layer_dynamic_bwd", ptr(g), ptr(x), dtype_code(x.dtype), dtype_code(wdt), ptr(pp), ptr(pq),
+             ptr(pr), ptr(a[0]), ptr(a[1]), ptr(a[2]), ptr(bp), ptr(bq), ptr(br), ptr(saved), ptr(grad_x), ptr(gw),
+             ptr(gphi), ptr(galpha), ptr(gb), ptr(ws), int(wsb), B, n, C, int(sinkhorn_iters),
+             float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
+    return (grad_x, gw, gphi[:n], gphi[n:2 * n], gphi[2 * n:], galpha[0], galpha[1], galpha[2], gb[:n],
+            gb[n:2 * n], gb[2 * n:].view(n, n))
+
+
+def _split_phi_concat(phi_concat: torch.Tensor, n: int):
+    return phi_concat[:n], phi_concat[n:2 * n], phi_concat[2 * n:2 * n + n * n]
+
+
+def mhc_layer_fwd_dynamic(x_expanded, rmsnorm_weight, phi_concat, alpha_pre, alpha_post, alpha_res, b_pre, b_post,
+                          b_res, sinkhorn_iters=20, sinkhorn_eps=1e-8, rmsnorm_eps=1e-5):
+    """Reference-order entry (bindings.cpp:880-952): phi_concat = [pre; post;
+    res] [2n+n^2, nC]; alphas may be floats or tensors.  Returns (out, saved)."""
+    n = x_expanded.size(1)
+    pp, pq, pr = _split_phi_concat(_f32c(phi_concat), n)
+    return mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, pp, pq, pr, alpha_pre, alpha_post, alpha_res, b_pre,
+                                 b_post, b_res, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)

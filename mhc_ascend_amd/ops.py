@@ -162,3 +162,85 @@ def mhc_layer_static(x: torch.Tensor, rmsnorm_weight: torch.Tensor, H_pre: torch
     """Static-H mHC layer on x [B, n, C] -> fp32 [B, n, C]."""
     return MHCLayerStaticFunction.apply(x, rmsnorm_weight, H_pre, H_post, H_res, sinkhorn_iters, sinkhorn_eps,
                                         rmsnorm_eps)
+
+
+# =============================================================================
+# Dynamic-H projection (ops.py:311-369)
+# =============================================================================
+
+class FusedProjectionFunction(torch.autograd.Function):
+    """P = x_flat @ phi_concat^T (fp32), with its backward."""
+
+    @staticmethod
+    def forward(ctx, x_flat: torch.Tensor, phi_concat: torch.Tensor) -> torch.Tensor:
+        out = native.fused_rmsnorm_matmul_fwd(x_flat, phi_concat)
+        ctx.save_for_backward(x_flat, phi_concat)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out: torch.Tensor):
+        x_flat, phi_concat = ctx.saved_tensors
+        gx, gphi = native.fused_rmsnorm_matmul_bwd(grad_out, x_flat, phi_concat)
+        return gx.to(x_flat.dtype), gphi.to(phi_concat.dtype)
+
+
+def fused_rmsnorm_matmul(x_flat: torch.Tensor, phi_concat: torch.Tensor) -> torch.Tensor:
+    """Project x_flat [B, K] with phi_concat [out_dim, K] -> fp32 [B, out_dim]."""
+    return FusedProjectionFunction.apply(x_flat, phi_concat)
+
+
+# =============================================================================
+# Dynamic-H layer (ops.py:376-667)
+# =============================================================================
+
+def mhc_layer_fused_dynamic_inference(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
+                                      alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters: int = 20,
+                                      sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5) -> torch.Tensor:
+    """Dynamic-H forward without autograd state (ops.py:376-419)."""
+    out, _ = native.mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
+                                          alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
+                                          rmsnorm_eps)
+    return out
+
+
+class MHCLayerDynamicFunction(torch.autograd.Function):
+    """Fused dynamic-H layer: projection -> per-token H -> aggregate ->
+    RMSNorm -> distribute-mix-add, and its backward (ops.py:426-603)."""
+
+    @staticmethod
+    def forward(ctx, x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post, alpha_res, b_pre,
+                b_post, b_res, sinkhorn_iters: int, sinkhorn_eps: float, rmsnorm_eps: float):
+        out, saved = native.mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
+                                                  alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters,
+                                                  sinkhorn_eps, rmsnorm_eps)
+        ctx.save_for_backward(x_expanded, rmsnorm_weight, saved, phi_pre, phi_post, phi_res, alpha_pre, alpha_post,
+                              alpha_res, b_pre, b_post, b_res)
+        ctx.cfg = (sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (x, w, saved, phi_pre, phi_post, phi_res, a_pre, a_post, a_res, b_pre, b_post, b_res) = ctx.saved_tensors
+        grads = native.mhc_layer_dynamic_bwd(grad_output, x, w, saved, phi_pre, phi_post, phi_res, a_pre, a_post,
+                                             a_res, b_pre, b_post, b_res, *ctx.cfg)
+        gx, gw, gpp, gpq, gpr, gap, gaq, gar, gbp, gbq, gbr = grads
+        return (gx.to(x.dtype), gw, gpp.view_as(phi_pre), gpq.view_as(phi_post), gpr.view_as(phi_res),
+                gap.view_as(a_pre), gaq.view_as(a_post), gar.view_as(a_res), gbp.view_as(b_pre),
+                gbq.view_as(b_post), gbr.view_as(b_res), None, None, None)
+
+
+def mhc_layer_fused_dynamic_training(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post,
+                                     alpha_res, b_pre, b_post, b_res, sinkhorn_iters: int = 20,
+                                     sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5) -> torch.Tensor:
+    """Dynamic-H layer with autograd (ops.py:606-667).  Float alphas become
+    device tensors; alpha tensors stay on the device (no .item() syncs)."""
+    dev = phi_pre.device
+    if not torch.is_tensor(alpha_pre):
+        alpha_pre = torch.tensor(alpha_pre, device=dev, dtype=torch.float32)
+    if not torch.is_tensor(alpha_post):
+        alpha_post = torch.tensor(alpha_post, device=dev, dtype=torch.float32)
+    if not torch.is_tensor(alpha_res):
+        alpha_res = torch.tensor(alpha_res, device=dev, dtype=torch.float32)
+    return MHCLayerDynamicFunction.apply(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
+                                         alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
+                                         rmsnorm_eps)

@@ -1,0 +1,162 @@
+"""GPU parity of the dynamic-H path: the projection operators
+(fused_rmsnorm_matmul fwd/bwd) and the fused dynamic layer (config C4)
+against the float64 CPU oracle on identical seeded inputs.
+
+Tolerances: fp32 outputs rtol 1e-4 / atol 1e-5; gradients rtol 1e-3 with an
+absolute floor relative to max|ref| (1e-5 per-token, 1e-4 token-summed);
+bf16-stored gradients rtol 2e-2."""
+import pytest
+import torch
+
+import mhc_ascend_amd as mhc
+from mhc_ascend_amd import native
+from oracle import reference as R
+from tests.conftest import assert_close, grad_atol
+
+pytestmark = pytest.mark.gpu
+
+FWD = dict(rtol=1e-4, atol=1e-5)
+PARAMS = ["weight", "phi_pre", "phi_post", "phi_res", "alpha_pre", "alpha_post", "alpha_res", "b_pre", "b_post",
+          "b_res"]
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,K,out_dim", [(1, 32, 1), (70, 1024, 24), (300, 4096, 32), (65, 16384, 24)])
+def test_projection(device, dtype, B, K, out_dim):
+    g = _gen(B + K + out_dim)
+    x = torch.randn(B, K, generator=g).to(dtype)
+    phi = 0.02 * torch.randn(out_dim, K, generator=g)
+    go = torch.randn(B, out_dim, generator=g)
+    xd = x.float().to(device).requires_grad_(True) if dtype == torch.float32 else x.to(device)
+    pd = phi.to(device).requires_grad_(True)
+    out = mhc.fused_rmsnorm_matmul(xd, pd)
+    ref = R.projection(x.double(), phi.double())
+    # split-bf16 operands: ~2^-16 relative per product
+    assert_close(out, ref, 1e-4, grad_atol(ref, 1e-5), f"P B={B} K={K} o={out_dim}")
+    gx, gphi = native.fused_rmsnorm_matmul_bwd(go.to(device), x.float().to(device), pd.detach())
+    assert_close(gx, go.double() @ phi.double(), 1e-4, grad_atol(go.double() @ phi.double(), 1e-5), "dx")
+    gref = go.double().t() @ x.double()
+    assert_close(gphi, gref, 1e-4, grad_atol(gref, 1e-5), "dphi")
+
+
+def _run_dyn(d, device, iters=20, sk_eps=1e-8, rms_eps=1e-5, training=True):
+    x = d["x"].to(device).requires_grad_(True)
+    ps = [d[k].to(device).requires_grad_(True) for k in PARAMS]
+    if training:
+        out = mhc.mhc_layer_fused_dynamic_training(x, *ps, iters, sk_eps, rms_eps)
+        out.backward(d["grad"].to(device))
+        return out, x.grad, [p.grad for p in ps]
+    with torch.no_grad():
+        return mhc.mhc_layer_fused_dynamic_inference(x, *ps, iters, sk_eps, rms_eps), None, None
+
+
+def _oracle_dyn(d, iters=20, sk_eps=1e-8, rms_eps=1e-5):
+    x = d["x"].double().requires_grad_(True)
+    ps = [d[k].double().requires_grad_(True) for k in PARAMS]
+    out = R.mhc_layer_dynamic(x, *ps, iters, sk_eps, rms_eps, dtype=torch.float64)
+    out.backward(d["grad"].double())
+    return out.detach(), x.grad, [p.grad for p in ps]
+
+
+def _check_dyn(got, want, x_dtype, tag):
+    out, gx, gp = got
+    rout, rgx, rgp = want
+    assert out.dtype == torch.float32
+    assert_close(out, rout, what=f"{tag} out", **FWD)
+    if gx is None:
+        return
+    if x_dtype == torch.bfloat16:
+        assert gx.dtype == torch.bfloat16
+        assert_close(gx, rgx, 2e-2, grad_atol(rgx, 1e-2), f"{tag} dx (bf16)")
+    else:
+        assert_close(gx, rgx, 1e-3, grad_atol(rgx, 1e-5), f"{tag} dx")
+    for nm, a, e in zip(PARAMS, gp, rgp):
+        if nm == "weight":
+            assert_close(a, e, 8e-3, grad_atol(e, 1e-3), f"{tag} d_weight (bf16 param)")
+        else:
+            assert_close(a, e, 1e-3, grad_atol(e, 1e-4), f"{tag} d_{nm}")
+
+
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,C", [(1, 64), (7, 256), (64, 1024), (33, 4096)])
+def test_dynamic_layer_matches_oracle(device, x_dtype, B, C):
+    d = R.dynamic_layer_inputs(B, 4, C, seed=B + C, x_dtype=x_dtype, b_std=0.5)
+    _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"B={B} C={C} {x_dtype}")
+
+
+@pytest.mark.parametrize("alpha,phi_std", [(0.5, 0.05), (2.0, 0.02)])
+def test_dynamic_layer_strong_dynamic_h(device, alpha, phi_std):
+    """Large alpha makes t (and so h, M) vary strongly per token."""
+    d = R.dynamic_layer_inputs(40, 4, 512, seed=int(alpha * 10), x_dtype=torch.float32, alpha=alpha,
+                               phi_std=phi_std, b_std=1.0)
+    _check_dyn(_run_dyn(d, device), _oracle_dyn(d), torch.float32, f"alpha={alpha}")
+
+
+def test_dynamic_inference_equals_training_forward(device):
+    d = R.dynamic_layer_inputs(16, 4, 256, seed=2, b_std=0.5)
+    out_t = _run_dyn(d, device)[0].detach()
+    out_i = _run_dyn(d, device, training=False)[0]
+    assert torch.equal(out_t, out_i)
+
+
+def test_dynamic_module_train_and_eval(device):
+    torch.manual_seed(4)
+    layer = mhc.MHCLayer(256, 4, use_dynamic_h=True).to(device)
+    with torch.no_grad():
+        layer.b_pre.normal_()
+        layer.b_res.normal_()
+        layer.alpha_res.fill_(0.3)
+    x = torch.randn(24, 4, 256, generator=_gen(4)).to(device)
+    g = torch.randn(24, 4, 256, generator=_gen(5)).to(device)
+    layer.train()
+    xt = x.clone().requires_grad_(True)
+    out = layer(xt)
+    out.backward(g)
+    d = {"x": x.cpu(), "grad": g.cpu()}
+    for k in PARAMS:
+        d[k] = getattr(layer, "rmsnorm_weight" if k == "weight" else k).detach().cpu()
+    rout, rgx, rgp = _oracle_dyn(d)
+    assert_close(out, rout, what="module out", **FWD)
+    assert_close(xt.grad, rgx, 1e-3, grad_atol(rgx, 1e-5), "module dx")
+    assert_close(layer.phi_res.grad, rgp[3], 1e-3, grad_atol(rgp[3], 1e-4), "module d_phi_res")
+    assert_close(layer.alpha_res.grad, rgp[6], 1e-3, grad_atol(rgp[6], 1e-4), "module d_alpha_res")
+    layer.eval()
+    with torch.no_grad():
+        assert_close(layer(x), rout, what="module eval", **FWD)
+
+
+def test_dynamic_layer_config_c4_full_size(device):
+    """Config C4: x bf16 [8192, 4, 4096], phi ~ N(0, 0.02), alpha 0.01, b 0.
+    Per-token outputs on a token subsample vs the oracle; token-summed
+    parameter gradients by additivity over two halves (fp32 native grads)
+    and against the oracle on a 128-token slice."""
+    B, n, C = 8192, 4, 4096
+    d = R.dynamic_layer_inputs(B, n, C, seed=44)
+    dev = {k: v.to(device) for k, v in d.items()}
+    pvals = [dev[k] for k in PARAMS]
+
+    def grads(sl):
+        w32 = dev["weight"].float()
+        out, saved = native.mhc_layer_dynamic_fwd(dev["x"][sl], w32, *pvals[1:])
+        g = native.mhc_layer_dynamic_bwd(dev["grad"][sl], dev["x"][sl], w32, saved, *pvals[1:])
+        return out, g
+
+    out, g_full = grads(slice(0, B))
+    idx = torch.randperm(B, generator=_gen(6))[:32]
+    sub = {k: (v[idx] if k in ("x", "grad") else v) for k, v in d.items()}
+    rout, rgx, _ = _oracle_dyn(sub)
+    assert_close(out.cpu()[idx], rout, what="C4 out subsample", **FWD)
+    assert_close(g_full[0].cpu()[idx], rgx, 2e-2, grad_atol(rgx, 1e-2), "C4 dx subsample (bf16)")
+    _, g1 = grads(slice(0, B // 2))
+    _, g2 = grads(slice(B // 2, B))
+    names = ["d_weight", "d_phi_pre", "d_phi_post", "d_phi_res", "d_alpha_pre", "d_alpha_post", "d_alpha_res",
+             "d_b_pre", "d_b_post", "d_b_res"]
+    for k, nm in enumerate(names):
+        s = g1[k + 1] + g2[k + 1]
+        assert_close(g_full[k + 1], s, 1e-4, grad_atol(s, 1e-5), f"C4 additivity {nm}")
+    sl = {k: (v[:128] if k in ("x", "grad") else v) for k, v in d.items()}
+    _check_dyn(_run_dyn(sl, device), _oracle_dyn(sl), torch.bfloat16, "C4 slice")
