@@ -103,7 +103,7 @@ int mhc_stream_aggregate_fwd(const void* inp, int32_t dtype, const float* h_pre_
  * sum_c grad_out x_i (before the sigmoid derivative, as the reference
  * returns it); grad_h_pre_raw = grad_h_pre_act h (1 - h).  Either fp32
  * output may be NULL.  Replaces stream_aggregate_bwd (bindings.cpp:340-374)
- * and the sigmoid derivative of ops.py:211. */
+ * and the sigmoid derivative of ops.py:172. */
 int mhc_stream_aggregate_bwd(const void* grad_out, const void* inp, int32_t dtype, const float* h_pre_act,
                              int64_t h_batch_stride, void* grad_inp, float* grad_h_pre_act, float* grad_h_pre_raw,
                              int64_t batch, int32_t n, int32_t hidden, void* stream);
@@ -123,7 +123,7 @@ int mhc_stream_distribute_mix_add_fwd(const void* y_norm, const float* h_post_ra
  * grad_h_post_act[b, i] = sum_c g_i y, grad_h_post_raw = grad_h_post_act
  * h (1 - h/2) (fp32; the last two may be NULL).
  * Replaces stream_distribute_mix_add_bwd (bindings.cpp:418-460) and the
- * derivative of ops.py:279-281. */
+ * derivative of ops.py:240-242. */
 int mhc_stream_distribute_mix_add_bwd(const float* grad_out, const void* x_inp, const void* y_norm, int32_t dtype,
                                       const float* M, int64_t m_batch_stride, const float* h_post_act,
                                       int64_t h_batch_stride, void* grad_x, void* grad_y, float* grad_M,
@@ -158,7 +158,7 @@ size_t mhc_layer_static_bwd_workspace_size(int64_t batch, int32_t n, int32_t hid
  * Replaces the backward chain of the static layer:
  * stream_distribute_mix_add_bwd, rmsnorm_bwd, stream_aggregate_bwd,
  * sinkhorn_knopp_bwd (bindings.cpp:418, 268, 340, 189) plus the autograd
- * expand/exp/sigmoid backward of layer.py:144-160 and ops.py:211, 279-281. */
+ * expand/exp/sigmoid backward of layer.py:144-160 and ops.py:172, 240-242. */
 int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, int32_t weight_dtype,
                          const float* h_pre, const float* h_post, const float* h_res, const float* saved,
                          void* grad_x, void* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
@@ -193,7 +193,7 @@ int mhc_fused_rmsnorm_matmul_bwd(const float* grad_out, const float* x_flat, con
  * (no host synchronisation).  out [batch, n, hidden] fp32; `saved`
  * (mhc_layer_dynamic_saved_size bytes) receives what the backward needs.
  * Replaces mhc_layer_fwd_dynamic (bindings.cpp:880-952) and the inference
- * path of ops.py:376-419. */
+ * path of ops.py:337-380. */
 size_t mhc_layer_dynamic_saved_size(int64_t batch, int32_t n, int32_t hidden);
 size_t mhc_layer_dynamic_fwd_workspace_size(int64_t batch, int32_t n, int32_t hidden);
 int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, int32_t weight_dtype,

@@ -201,10 +201,9 @@ static int check_layer_shape(const char* fn, int64_t batch, int32_t n, int32_t h
     if (!valid_dtype(x_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": x_dtype must be F32 or BF16");
     if (!supported_layer_n(n))
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) + " is not compiled in this build");
-    const int wc = x_dtype == kBF16 ? 8 : 4;
+    const int wc = 4;  // channels per lane chunk of the fused layer kernels (both dtypes)
     if (hidden % wc != 0)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of " + std::to_string(wc) +
-                                             " for this dtype");
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of " + std::to_string(wc));
     const RowTiling t = choose_row_tiling(hidden, wc, 2 * n);
     if (t.vpt <= 0) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
     return MHC_SUCCESS;
@@ -495,7 +494,7 @@ struct ProjBwdWs {
 
 static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
     ProjBwdWs w{};
-    w.tiles = batch > 0 ? dyn_dx_tiles(batch, k) : 1;
+    w.tiles = batch > 0 ? proj_bwd_tiles(batch, k) : 1;
     w.part_off = 0;
     w.stage_off = align256((size_t)w.tiles * out_dim * k * sizeof(float));
     w.total = w.stage_off + align256((size_t)kDwSplit * out_dim * k * sizeof(float));
@@ -527,7 +526,8 @@ int mhc_fused_rmsnorm_matmul_bwd(const float* grad_out, const float* x_flat, con
         rows = 1;
         e = launch_fill_zero(part, cols, s);
     } else {
-        e = launch_proj_bwd(grad_out, out_dim, x_flat, phi, grad_x, part, w.tiles, batch, k, s);
+        e = launch_proj_bwd(kF32, x_flat, grad_out, out_dim, nullptr, phi, phi, phi, out_dim, out_dim, grad_x,
+                            false, part, w.tiles, batch, k, s);
     }
     if (e == hipSuccess) e = launch_column_partial(part, rows, cols, stage, kDwSplit, s);
     if (e == hipSuccess)
@@ -620,7 +620,7 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     const int64_t K = (int64_t)n * hidden;
     w.grid = batch > 0 ? layer_bwd_grid(x_dtype, n, batch, hidden) : 1;
     w.cblocks = batch > 0 ? dyn_coef_bwd_blocks(n, batch) : 1;
-    w.tiles = batch > 0 ? dyn_dx_tiles(batch, hidden) : 1;
+    w.tiles = batch > 0 ? proj_bwd_tiles(batch, (int64_t)n * hidden) : 1;
     size_t o = 0;
     w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
     w.scal_off = o; o += align256((size_t)batch * (n * n + 2 * n + 2) * 4);
@@ -679,15 +679,15 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         if (e == hipSuccess) e = launch_fill_zero(phip, (int64_t)np * K, s);
         if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
     } else {
-        e = launch_layer_bwd(x_dtype, n, 1, grad_out, x, w32, saved + d.coef_off, np, nullptr, dw_part, scal, w.grid,
+        e = launch_layer_bwd(x_dtype, n, 1, grad_out, x, w32, saved + d.coef_off, np, grad_x, dw_part, scal, w.grid,
                              batch, hidden, rmsnorm_eps, s);
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
                                     s);
         if (e == hipSuccess)
-            e = launch_dyn_dx(x_dtype, n, grad_out, x, w32, saved + d.coef_off, scal, dp, stok, phi_pre, phi_post,
-                              phi_res, grad_x, phip, w.tiles, batch, hidden, s);
+            e = launch_proj_bwd(x_dtype, x, dp, 32, stok, phi_pre, phi_post, phi_res, n, np, grad_x, true, phip,
+                                w.tiles, batch, K, s);
     }
     if (e == hipSuccess) e = launch_column_partial(dw_part, rows_w, hidden, stw, kDwSplit, s);
     if (e == hipSuccess)

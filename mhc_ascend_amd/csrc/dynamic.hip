@@ -15,7 +15,7 @@
 //                       MFMA 16x16x32 on the planes gives fp32 accuracy
 //   dyn_coef_fwd_kernel per token: sum partials, t, sigmoid, Sinkhorn
 //   dyn_coef_bwd_kernel per token: Sinkhorn adjoint, dP, d r_h, db/dalpha
-//   dyn_dx_kernel       dx = stream terms + dP.Phi + s x_flat; dPhi partials
+//   proj_bwd_mfma_kernel dx += dP.Phi + s x_flat (fp32 MFMA); dPhi partials
 #include "mhc_device.h"
 #include "mhc_internal.h"
 #include "mhc_rows.h"
@@ -418,127 +418,205 @@ __global__ __launch_bounds__(256) void small_column_sum_kernel(const float* __re
 }
 
 // ---------------------------------------------------------------------------
-// dx and dPhi partials.  Workgroup = 64 channels x a tile of tokens; lane =
-// one channel c for all N streams; the 4 waves take every 4th token of the
-// tile.  Phi[o][j*C + c] (NP x N values) stays in registers.
-//   MODE 0 (layer): dx_j = sum_i M_ij g_i + h_pre_j gxa + s x_j + sum_o dP_o Phi_o[j*C+c],
-//                   gxa = w gy inv - xa k2, from the per-token scalars of the
-//                   layer backward reduction;
-//   MODE 1 (projection only, N = 1, C = K): dx = sum_o dP_o Phi_o[c].
-//   dPhi_part[tile][o][j*C + c] = sum_{t in tile} dP_o[t] x_j[t][c].
+// Projection backward on the fp32 matrix cores (v_mfma_f32_32x32x2_f32), over
+// the flattened rows x[b][k] (k = j*C + c for the layer):
+//   dx[b][k] = dx_in[b][k] + s[b] x[b][k] + sum_o dP[b][o] Phi[o][k]
+//   dPhi_part[tile][o][k] = sum_{b in tile} dP[b][o] x[b][k]
+// In the layer backward dx_in is the stream part already written by the row
+// kernel (bindings.cpp:834-848 adds the same two terms to grad_x_flat).
+// Workgroup = 4 waves x 32 columns each, looping over a tile of tokens in
+// blocks of 32.  Per block a wave runs two MFMA chains:
+//   dx_proj (32 tokens x 32 columns) reducing over o (NOH per lane half);
+//   dPhi    (32 o x 32 columns) reducing over the block's 32 tokens.
+// MFMA 32x32x2 f32 operand layout: A: lane l holds A[l % 32][l / 32];
+// B: lane l holds B[l / 32][l % 32]; D: register r of lane l holds
+// D[dtok(r, l / 32)][l % 32].  The dPhi chain takes its B operand (x) from
+// the same registers the dx epilogue reads, by pairing reduction index h of
+// instruction r with token dtok(r, h).
 // ---------------------------------------------------------------------------
-template <typename TX, int N, int NP, int MODE>
-__global__ __launch_bounds__(256) void dyn_dx_kernel(
-    const float* __restrict__ g, const TX* __restrict__ x, const float* __restrict__ w,
-    const float* __restrict__ coef, const float* __restrict__ scal, const float* __restrict__ dp, int dp_stride,
-    const float* __restrict__ s, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
-    const float* __restrict__ phi_res, int np_rt, TX* __restrict__ dx, float* __restrict__ dphi_part, int64_t B,
-    int C, int64_t tile) {
-    constexpr int NC = 2 * N + N * N;
-    constexpr int NS = N * N + 2 * N;
-    __shared__ float red[3][N * 6][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int c = blockIdx.x * 64 + lane;
-    const bool cv = c < C;
-    const int cc = cv ? c : 0;
-    const int64_t K = (int64_t)N * C;
-    const int npr = MODE == 0 ? NP : np_rt;
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-    float ph[NP][N];
-#pragma unroll
-    for (int o = 0; o < NP; ++o) {
-        const bool ov = o < npr;
-        const float* row = ov ? phi_row(phi_pre, phi_post, phi_res, MODE == 0 ? N : np_rt, o, K) : phi_pre;
-#pragma unroll
-        for (int j = 0; j < N; ++j) ph[o][j] = (ov && cv) ? row[(int64_t)j * C + cc] : 0.f;
-    }
-    float acc[NP][N];
-#pragma unroll
-    for (int o = 0; o < NP; ++o) {
-#pragma unroll
-        for (int j = 0; j < N; ++j) acc[o][j] = 0.f;
-    }
-    const float wv = (MODE == 0 && cv) ? w[cc] : 0.f;
-    const int64_t t0 = (int64_t)blockIdx.y * tile;
-    const int64_t t1 = (t0 + tile < B) ? t0 + tile : B;
+__device__ __forceinline__ f32x16_t mfma32x32x2(float a, float b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
 
-    for (int64_t t = t0 + wave; t < t1; t += 4) {
-        float dpv[NP];
-#pragma unroll
-        for (int o = 0; o < NP; ++o) dpv[o] = (o < npr) ? dp[t * dp_stride + o] : 0.f;
-        float xi[N];
-#pragma unroll
-        for (int j = 0; j < N; ++j) xi[j] = cv ? VecIO<TX>::scalar(x + (t * N + j) * (int64_t)C + cc) : 0.f;
-        float d[N];
-        if constexpr (MODE == 0) {
-            const float* cf = coef + t * NC;
-            const float* sc = scal + t * (NS + 2);
-            const float inv = sc[NS], k2 = sc[NS + 1], sv = s[t];
-            float gi[N];
-#pragma unroll
-            for (int i = 0; i < N; ++i) gi[i] = cv ? __builtin_nontemporal_load(g + (t * N + i) * (int64_t)C + cc) : 0.f;
-            float xa = 0.f, gy = 0.f;
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-                xa += cf[i] * xi[i];
-                gy += cf[N + i] * gi[i];
-            }
-            const float gxa = wv * gy * inv - xa * k2;
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float v = cf[j] * gxa + sv * xi[j];
-#pragma unroll
-                for (int i = 0; i < N; ++i) v += cf[2 * N + i * N + j] * gi[i];
-                d[j] = v;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < N; ++j) d[j] = 0.f;
-        }
-#pragma unroll
-        for (int j = 0; j < N; ++j) {
-#pragma unroll
-            for (int o = 0; o < NP; ++o) {
-                d[j] += dpv[o] * ph[o][j];
-                acc[o][j] += dpv[o] * xi[j];
-            }
-        }
-        if (cv) {
-#pragma unroll
-            for (int j = 0; j < N; ++j) VecIO<TX>::put(dx + (t * N + j) * (int64_t)C + cc, d[j]);
-        }
-    }
+// Row of a 32-row MFMA tile held in D register r by lane half h.
+__device__ __forceinline__ int dtok(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
 
-    // sum the 4 waves' dPhi partials (6 projection rows per round) and store
-    float* out = dphi_part + (int64_t)blockIdx.y * npr * K;
+// Raw element load (no conversion) and its conversion to fp32, kept apart so
+// that every load of a block is issued before the first conversion waits.
+template <typename T> struct RawElem;
+template <> struct RawElem<float> {
+    typedef uint32_t type;
+    __device__ __forceinline__ static type load(const float* p) { return __float_as_uint(*p); }
+    __device__ __forceinline__ static float f32(type v) { return __uint_as_float(v); }
+};
+template <> struct RawElem<bf16_t> {
+    typedef uint32_t type;
+    __device__ __forceinline__ static type load(const bf16_t* p) { return *p; }
+    __device__ __forceinline__ static float f32(type v) { return __uint_as_float(v << 16); }
+};
+
+// Workgroup = 4 waves over 128 columns (32 each) and a tile of tokens, in
+// stages of 32 tokens.  Each stage's x (and dx_in) tile, dP rows and s values
+// are fetched with coalesced 16-byte loads into registers while the previous
+// stage is computed out of LDS, then written to the other LDS buffer
+// (two-stage pipeline, one barrier per stage).  Rows past the tile end and
+// columns past K are stored as zeros and never written back.
+// ACC: add the existing dx (the stream part of the layer backward); HAS_S:
+// add s[b] x.
+template <typename TX, int NOH, bool ACC, bool HAS_S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void proj_bwd_mfma_kernel(
+    const TX* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
+    const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
+    int n_pre, int np, TX* __restrict__ dx, float* __restrict__ dphi_part, int64_t B, int64_t K, int64_t tile) {
+    constexpr int TB = 32;                      // tokens per stage
+    constexpr int CB = 128;                     // columns per workgroup
+    constexpr int EPV = 16 / sizeof(TX);        // elements per 16-byte vector
+    constexpr int VPR = CB / EPV;               // vectors per tile row
+    constexpr int RPP = 256 / VPR;              // tile rows per load pass
+    constexpr int PASSES = TB / RPP;
+    constexpr int PITCH = CB * sizeof(TX) + 16;  // bytes per LDS tile row (16-byte pad: no bank aliasing
+                                                 // between the two lane halves, rows 4 apart)
+    constexpr int NARR = ACC ? 2 : 1;
+    __shared__ __align__(16) char tiles_lds[2][NARR][TB * PITCH];
+    __shared__ float dp_lds[2][TB][33];  // rows padded: the dx_proj operand reads a column
+    __shared__ float s_lds[2][TB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const int64_t kb0 = (int64_t)blockIdx.x * CB;
+    const int64_t kc = kb0 + wave * 32 + col;
+    const bool wave_on = kb0 + wave * 32 < K;  // K % 32 == 0: whole waves are in or out
+
+    // loader role: pass p covers tile row lrow + p * RPP, 16-byte vector lvec
+    const int lrow = tid / VPR;
+    const int lvec = tid % VPR;
+    const int64_t lcol = kb0 + (int64_t)lvec * EPV;
+    const bool lcol_ok = lcol < K;
+    const int dtk = tid >> 3;        // dP loader: token tid / 8, o = 4 (tid % 8) + q
+    const int dpo = (tid & 7) * 4;
+
+    float bphi[NOH];
 #pragma unroll
-    for (int o0 = 0; o0 < NP; o0 += 6) {
-        if (wave > 0) {
+    for (int m = 0; m < NOH; ++m) {
+        const int o = NOH * h + m;
+        bphi[m] = (wave_on && o < np) ? phi_row(phi_pre, phi_post, phi_res, n_pre, o, K)[kc] : 0.f;
+    }
+    f32x16_t accP;
 #pragma unroll
-            for (int q = 0; q < 6; ++q) {
-                if (o0 + q < NP) {
+    for (int r = 0; r < 16; ++r) accP[r] = 0.f;
+
+    const int64_t t_begin = (int64_t)blockIdx.y * tile;
+    const int64_t t_end = (t_begin + tile < B) ? t_begin + tile : B;
+
+    // Two register sets of fetched stages: stage i+2 is being fetched while
+    // stage i is computed and stage i+1 (fetched one stage earlier) is moved
+    // into LDS, so every load has a whole stage of compute to arrive in.
+    struct Fetched {
+        uint4 x[PASSES], d[PASSES];
+        float dp[4], s;
+    };
+    Fetched f0, f1;
+    auto fetch = [&](Fetched& f, int64_t t0) __attribute__((always_inline)) {  // issue the global loads of stage t0 (t0 < t_end)
 #pragma unroll
-                    for (int j = 0; j < N; ++j) red[wave - 1][q * N + j][lane] = acc[o0 + q][j];
-                }
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t t = t0 + lrow + p * RPP;
+            const int64_t off = (t < t_end ? t : t0) * K + (lcol_ok ? lcol : 0);
+            f.x[p] = ld16_nt(x + off);
+            if constexpr (ACC) f.d[p] = ld16_nt(dx + off);
+        }
+        const int64_t td = t0 + dtk;
+        const int64_t tdc = td < t_end ? td : t0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) f.dp[q] = dP[tdc * dp_stride + (dpo + q < np ? dpo + q : 0)];
+        f.s = 0.f;
+        if constexpr (HAS_S) {
+            if (tid < TB) f.s = s_tok[(t0 + tid < t_end) ? t0 + tid : t0];
+        }
+    };
+    auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {  // fetched stage -> LDS buffer, masked
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int row = lrow + p * RPP;
+            const uint32_t m = (lcol_ok && t0 + row < t_end) ? 0xffffffffu : 0u;  // zero masked rows
+            const uint4 vx = f.x[p];
+            *reinterpret_cast<uint4*>(&tiles_lds[buf][0][row * PITCH + lvec * 16]) =
+                make_uint4(vx.x & m, vx.y & m, vx.z & m, vx.w & m);
+            if constexpr (ACC) {
+                const uint4 vd = f.d[p];
+                *reinterpret_cast<uint4*>(&tiles_lds[buf][1][row * PITCH + lvec * 16]) =
+                    make_uint4(vd.x & m, vd.y & m, vd.z & m, vd.w & m);
             }
         }
+        const bool tok_ok = t0 + dtk < t_end;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dp_lds[buf][dtk][dpo + q] = (tok_ok && dpo + q < np) ? f.dp[q] : 0.f;
+        if constexpr (HAS_S) {
+            if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? f.s : 0.f;
+        }
+    };
+    auto compute = [&](int64_t t0, int cur) __attribute__((always_inline)) {
+        if (!wave_on) return;
+        const TX* xt = reinterpret_cast<const TX*>(tiles_lds[cur][0]);
+        const TX* dt = reinterpret_cast<const TX*>(tiles_lds[cur][ACC ? 1 : 0]);
+        constexpr int EPR = PITCH / sizeof(TX);  // elements per LDS row
+        const int c = wave * 32 + col;
+        float a1[NOH];
+#pragma unroll
+        for (int m = 0; m < NOH; ++m) a1[m] = dp_lds[cur][col][NOH * h + m];
+        f32x16_t acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+        for (int m = 0; m < NOH; ++m) acc = mfma32x32x2(a1[m], bphi[m], acc);
+        float xv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = dtok(r, h);
+            xv[r] = VecIO<TX>::scalar(xt + t * EPR + c);
+            accP = mfma32x32x2(dp_lds[cur][t][col], xv[r], accP);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = dtok(r, h);
+            float v = acc[r];
+            if constexpr (ACC) v += VecIO<TX>::scalar(dt + t * EPR + c);
+            if constexpr (HAS_S) v += s_lds[cur][t] * xv[r];
+            if (t0 + t < t_end) VecIO<TX>::put(dx + (t0 + t) * K + kc, v);
+        }
+    };
+
+    if (t_begin < t_end) {
+        fetch(f0, t_begin);
+        commit(f0, t_begin, 0);
+        if (t_begin + TB < t_end) fetch(f1, t_begin + TB);
+    }
+    __syncthreads();
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += 2 * TB) {
+        // even stage t0 in LDS buffer 0; f1 holds stage t0 + TB
+        const int64_t t1 = t0 + TB, t2 = t0 + 2 * TB, t3 = t0 + 3 * TB;
+        if (t2 < t_end) fetch(f0, t2);
+        compute(t0, 0);
+        if (t1 < t_end) commit(f1, t1, 1);
         __syncthreads();
-        if (wave == 0 && cv) {
-#pragma unroll
-            for (int q = 0; q < 6; ++q) {
-                const int o = o0 + q;
-                if (o < npr) {
-#pragma unroll
-                    for (int j = 0; j < N; ++j) {
-                        const float v = acc[o][j] + red[0][q * N + j][lane] + red[1][q * N + j][lane] +
-                                        red[2][q * N + j][lane];
-                        out[(int64_t)o * K + (int64_t)j * C + c] = v;
-                    }
-                }
-            }
-        }
+        if (t1 >= t_end) break;
+        // odd stage t1 in LDS buffer 1; f0 holds stage t2
+        if (t3 < t_end) fetch(f1, t3);
+        compute(t1, 1);
+        if (t2 < t_end) commit(f0, t2, 0);
         __syncthreads();
+    }
+    if (!wave_on) return;
+    // dPhi partial: register r holds o = dtok(r, h) at column kc
+    float* out = dphi_part + (int64_t)blockIdx.y * np * K;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int o = dtok(r, h);
+        if (o < np) out[(int64_t)o * K + kc] = accP[r];
     }
 }
 
@@ -627,44 +705,42 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
     return hipGetLastError();
 }
 
-int dyn_dx_tiles(int64_t B, int64_t C) {
-    const int64_t bx = (C + 63) / 64;
-    int64_t tiles = (4 * (int64_t)device_cu_count() + bx - 1) / bx;
-    if (tiles > (B + 3) / 4) tiles = (B + 3) / 4;
+int proj_bwd_tiles(int64_t B, int64_t K) {
+    const int64_t gx = (K + 127) / 128;
+    int64_t tiles = (4 * (int64_t)device_cu_count() + gx - 1) / gx;
+    const int64_t blocks = (B + 31) / 32;
+    if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;
     return (int)tiles;
 }
 
-hipError_t launch_dyn_dx(int x_dtype, int n, const float* g, const void* x, const float* w, const float* coef,
-                         const float* scal, const float* dp, const float* s_tok, const float* phi_pre,
-                         const float* phi_post, const float* phi_res, void* dx, float* dphi_part, int tiles,
-                         int64_t B, int64_t C, hipStream_t s) {
+hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
+                           const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
+                           void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
+                           hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const int64_t tile = (B + tiles - 1) / tiles;
-    const dim3 grid((unsigned)((C + 63) / 64), (unsigned)tiles);
-    const int tok = timing_begin("dyn_dx", s);
+    if (np < 1 || np > 32 || K % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
+    // token tile: a multiple of the 32-token block
+    int64_t tile = (B + tiles - 1) / tiles;
+    tile = ((tile + 31) / 32) * 32;
+    const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
+    const int tok = timing_begin("proj_bwd", s);
+#define MHC_PROJ_BWD(TX_, NOH_, ACC_, S_)                                                                       \
+    hipLaunchKernelGGL((proj_bwd_mfma_kernel<TX_, NOH_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP,    \
+                       dp_stride, s_tok, phi_pre, phi_post, phi_res, n_pre, np, (TX_*)dx, dphi_part, B, K, tile)
+    // the layer backward accumulates with the r_h term; the standalone operator does neither
+    const bool layer = accumulate && s_tok != nullptr;
+    if (!layer && (accumulate || s_tok != nullptr)) return hipErrorInvalidValue;
     if (x_dtype == kBF16) {
-        MHC_DYN_N(n, hipLaunchKernelGGL((dyn_dx_kernel<bf16_t, N_, 2 * N_ + N_ * N_, 0>), grid, dim3(256), 0, s, g,
-                                        (const bf16_t*)x, w, coef, scal, dp, kNPad, s_tok, phi_pre, phi_post, phi_res,
-                                        0, (bf16_t*)dx, dphi_part, B, (int)C, tile));
+        if (!layer) return hipErrorInvalidValue;
+        if (np <= 24) { MHC_PROJ_BWD(bf16_t, 12, true, true); } else { MHC_PROJ_BWD(bf16_t, 16, true, true); }
+    } else if (layer) {
+        if (np <= 24) { MHC_PROJ_BWD(float, 12, true, true); } else { MHC_PROJ_BWD(float, 16, true, true); }
     } else {
-        MHC_DYN_N(n, hipLaunchKernelGGL((dyn_dx_kernel<float, N_, 2 * N_ + N_ * N_, 0>), grid, dim3(256), 0, s, g,
-                                        (const float*)x, w, coef, scal, dp, kNPad, s_tok, phi_pre, phi_post, phi_res,
-                                        0, (float*)dx, dphi_part, B, (int)C, tile));
+        if (np <= 24) { MHC_PROJ_BWD(float, 12, false, false); } else { MHC_PROJ_BWD(float, 16, false, false); }
     }
+#undef MHC_PROJ_BWD
     timing_end(tok, s);
-    return hipGetLastError();
-}
-
-// Projection-only backward: dx[b][k] = sum_o dP[b][o] Phi[o][k] (fp32 out),
-// dPhi partials as above; dP [B][np] with row stride np; Phi [np][K].
-hipError_t launch_proj_bwd(const float* dP, int np, const float* x, const float* phi, float* dx, float* dphi_part,
-                           int tiles, int64_t B, int64_t K, hipStream_t s) {
-    if (B == 0) return hipSuccess;
-    const int64_t tile = (B + tiles - 1) / tiles;
-    const dim3 grid((unsigned)((K + 63) / 64), (unsigned)tiles);
-    hipLaunchKernelGGL((dyn_dx_kernel<float, 1, kNPad, 1>), grid, dim3(256), 0, s, nullptr, x, nullptr, nullptr,
-                       nullptr, dP, np, nullptr, phi, phi, phi, np, dx, dphi_part, B, (int)K, tile);
     return hipGetLastError();
 }
 

@@ -73,10 +73,10 @@ __global__ __launch_bounds__(256) void static_coef_kernel(const float* __restric
 // ---------------------------------------------------------------------------
 template <typename TX, int N, int VPT>
 __device__ __forceinline__ void fwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
-                                          const float (&wv)[VPT][VecIO<TX>::W],
-                                          const float (&xv)[N][VPT][VecIO<TX>::W], float* __restrict__ out,
+                                          const float (&wv)[VPT][kLayerWC],
+                                          const float (&xv)[N][VPT][kLayerWC], float* __restrict__ out,
                                           float* __restrict__ rms_out, int C, float eps, float* red) {
-    constexpr int WC = VecIO<TX>::W;
+    constexpr int WC = kLayerWC;
     constexpr int NC = coef_size<N>();
     const float* cf = coef + b * coef_stride;
     float cfv[NC];
@@ -129,7 +129,7 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_fwd_kernel(const TX* __restrict__ x, co
                                                     const float* __restrict__ coef, int64_t coef_stride,
                                                     float* __restrict__ out, float* __restrict__ rms_out, int64_t B,
                                                     int C, float eps) {
-    constexpr int WC = VecIO<TX>::W;
+    constexpr int WC = kLayerWC;
     __shared__ float red[8];
     float wv[VPT][WC];
     load_weight<VPT, WC>(w, C, wv);
@@ -137,16 +137,20 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_fwd_kernel(const TX* __restrict__ x, co
     const int64_t NCs = (int64_t)N * C;
     int64_t b = blockIdx.x;
     if constexpr (PF) {
-        float xA[N][VPT][WC], xB[N][VPT][WC];
-        if (b < B) load_rows<TX, N, VPT, WC, true>(x + b * NCs, C, xA);
+        // token rows stay raw (unconverted words) until their token is processed
+        RawRows<TX, N, VPT, WC> xA, xB;
+        float xv[N][VPT][WC];
+        if (b < B) load_rows_raw<TX, N, VPT, WC, true>(x + b * NCs, C, xA);
         while (b < B) {
             const int64_t b1 = b + G;
-            if (b1 < B) load_rows<TX, N, VPT, WC, true>(x + b1 * NCs, C, xB);
-            fwd_token<TX, N, VPT>(b, coef, coef_stride, wv, xA, out, rms_out, C, eps, red);
+            if (b1 < B) load_rows_raw<TX, N, VPT, WC, true>(x + b1 * NCs, C, xB);
+            unpack_rows<TX, N, VPT, WC>(xA, C, xv);
+            fwd_token<TX, N, VPT>(b, coef, coef_stride, wv, xv, out, rms_out, C, eps, red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
-            if (b2 < B) load_rows<TX, N, VPT, WC, true>(x + b2 * NCs, C, xA);
-            fwd_token<TX, N, VPT>(b1, coef, coef_stride, wv, xB, out, rms_out, C, eps, red);
+            if (b2 < B) load_rows_raw<TX, N, VPT, WC, true>(x + b2 * NCs, C, xA);
+            unpack_rows<TX, N, VPT, WC>(xB, C, xv);
+            fwd_token<TX, N, VPT>(b1, coef, coef_stride, wv, xv, out, rms_out, C, eps, red);
             b = b2;
         }
     } else {
@@ -164,18 +168,20 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_fwd_kernel(const TX* __restrict__ x, co
 // (dM[n*n], dh_post_act[n], dh_pre_act[n], 1/r, k2 = dot/(C r^3)).  MODE 0
 // (static H) writes dx and sums the first n*n+2n of those over its tokens
 // (thread t keeps entry t in one register) into scal_out[blockIdx.x][n*n+2n];
-// MODE 1 (dynamic H) writes them per token to scal_out[b][n*n+2n+2] and
-// leaves dx to a later kernel that needs the per-token Sinkhorn backward
-// first.  dw accumulates in registers and goes to dw_part[blockIdx.x][C].
+// MODE 1 (dynamic H) writes them per token to scal_out[b][n*n+2n+2]; its dx
+// holds the stream terms only (sum_i M_ij G_i + h_pre_j gxa), and a later
+// kernel adds the terms that need the per-token Sinkhorn backward first (the
+// projection and r_h terms).  dw accumulates in registers and goes to
+// dw_part[blockIdx.x][C].
 // ---------------------------------------------------------------------------
 template <typename TX, int N, int VPT, int MODE>
 __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
-                                          const float (&wv)[VPT][VecIO<TX>::W],
-                                          const float (&xv)[N][VPT][VecIO<TX>::W],
-                                          const float (&gv)[N][VPT][VecIO<TX>::W],
-                                          float (&dwacc)[VPT][VecIO<TX>::W], float& sacc, TX* __restrict__ dx,
+                                          const float (&wv)[VPT][kLayerWC],
+                                          const float (&xv)[N][VPT][kLayerWC],
+                                          const float (&gv)[N][VPT][kLayerWC],
+                                          float (&dwacc)[VPT][kLayerWC], float& sacc, TX* __restrict__ dx,
                                           float* __restrict__ scal_out, int C, float eps, float* red) {
-    constexpr int WC = VecIO<TX>::W;
+    constexpr int WC = kLayerWC;
     constexpr int NC = coef_size<N>();
     constexpr int NS = N * N + 2 * N;
     constexpr int NR = 2 + N * N + 3 * N;  // ss, dot, dM, t_i, u_j, v_j
@@ -267,7 +273,7 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
             gxa[e] = wv[k][e] * gy * inv - xa * k2;
             dwacc[k][e] += gy * xa * inv;
         }
-        if (MODE == 0 && c0 < C) {
+        if (c0 < C) {
             TX* db = dx + b * (int64_t)N * C;
 #pragma unroll
             for (int j = 0; j < N; ++j) {
@@ -291,7 +297,7 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
                                                     int64_t coef_stride, TX* __restrict__ dx,
                                                     float* __restrict__ dw_part, float* __restrict__ scal_out,
                                                     int64_t B, int C, float eps) {
-    constexpr int WC = VecIO<TX>::W;
+    constexpr int WC = kLayerWC;
     constexpr int NS = N * N + 2 * N;
     constexpr int NR = 2 + N * N + 3 * N;
     __shared__ float red[9 * NR];  // 8 wave partials + totals
@@ -308,32 +314,43 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
     const int64_t NCs = (int64_t)N * C;
     int64_t b = blockIdx.x;
     if constexpr (PF) {
-        float xA[N][VPT][WC], gA[N][VPT][WC], xB[N][VPT][WC], gB[N][VPT][WC];
+        // token rows stay raw (unconverted words) until their token is processed
+        RawRows<TX, N, VPT, WC> xA, xB;
+        RawRows<float, N, VPT, WC> gA, gB;
+        float xv[N][VPT][WC], gv[N][VPT][WC];
         if (b < B) {
-            load_rows<TX, N, VPT, WC, true>(x + b * NCs, C, xA);
-            load_rows<float, N, VPT, WC, true>(g + b * NCs, C, gA);
+            load_rows_raw<TX, N, VPT, WC, true>(x + b * NCs, C, xA);
+            load_rows_raw<float, N, VPT, WC, true>(g + b * NCs, C, gA);
         }
         while (b < B) {
             const int64_t b1 = b + G;
             if (b1 < B) {
-                load_rows<TX, N, VPT, WC, true>(x + b1 * NCs, C, xB);
-                load_rows<float, N, VPT, WC, true>(g + b1 * NCs, C, gB);
+                load_rows_raw<TX, N, VPT, WC, true>(x + b1 * NCs, C, xB);
+                load_rows_raw<float, N, VPT, WC, true>(g + b1 * NCs, C, gB);
             }
-            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xA, gA, dwacc, sacc, dx, scal_out, C, eps, red);
+            unpack_rows<TX, N, VPT, WC>(xA, C, xv);
+            unpack_rows<float, N, VPT, WC>(gA, C, gv);
+            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, C, eps, red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
             if (b2 < B) {
-                load_rows<TX, N, VPT, WC, true>(x + b2 * NCs, C, xA);
-                load_rows<float, N, VPT, WC, true>(g + b2 * NCs, C, gA);
+                load_rows_raw<TX, N, VPT, WC, true>(x + b2 * NCs, C, xA);
+                load_rows_raw<float, N, VPT, WC, true>(g + b2 * NCs, C, gA);
             }
-            bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xB, gB, dwacc, sacc, dx, scal_out, C, eps, red);
+            unpack_rows<TX, N, VPT, WC>(xB, C, xv);
+            unpack_rows<float, N, VPT, WC>(gB, C, gv);
+            bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, C, eps, red);
             b = b2;
         }
     } else {
         for (; b < B; b += G) {
+            RawRows<TX, N, VPT, WC> xr;
+            RawRows<float, N, VPT, WC> gr;
             float xv[N][VPT][WC], gv[N][VPT][WC];
-            load_rows<TX, N, VPT, WC, true>(x + b * NCs, C, xv);
-            load_rows<float, N, VPT, WC, true>(g + b * NCs, C, gv);
+            load_rows_raw<TX, N, VPT, WC, true>(x + b * NCs, C, xr);
+            load_rows_raw<float, N, VPT, WC, true>(g + b * NCs, C, gr);
+            unpack_rows<TX, N, VPT, WC>(xr, C, xv);
+            unpack_rows<float, N, VPT, WC>(gr, C, gv);
             bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, C, eps, red);
         }
     }
@@ -391,8 +408,8 @@ __global__ __launch_bounds__(256) void column_partial_kernel(const float* __rest
 // Blocks [0, ceil(cols/256)) finish the dw sum (rsplit staged rows) and
 // store it in the weight's dtype.  With N > 0 the last block also forms the
 // static parameter gradients from the per-workgroup sums of
-// [dM, dh_post_act, dh_pre_act]: the activation derivatives (ops.py:211,
-// 279-281) and ONE Sinkhorn backward on the token-summed dM (M is shared, so
+// [dM, dh_post_act, dh_pre_act]: the activation derivatives (ops.py:172,
+// 240-242) and ONE Sinkhorn backward on the token-summed dM (M is shared, so
 // its VJP is linear in dM):
 //     dH_pre = dh_pre_act h_pre (1 - h_pre)
 //     dH_post = dh_post_act h_post (1 - h_post / 2)
@@ -540,13 +557,13 @@ hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, co
 
 template <typename TX, int N, int V, bool PF>
 static const void* fwd_fn() {
-    if constexpr (row_fits<TX>(N, V)) return reinterpret_cast<const void*>(&layer_fwd_kernel<TX, N, V, PF>);
+    if constexpr (layer_row_fits(N, V)) return reinterpret_cast<const void*>(&layer_fwd_kernel<TX, N, V, PF>);
     return nullptr;
 }
 
 template <typename TX, int N, int V, int MODE, bool PF>
 static const void* bwd_fn() {
-    if constexpr (row_fits<TX>(2 * N, V)) return reinterpret_cast<const void*>(&layer_bwd_kernel<TX, N, V, MODE, PF>);
+    if constexpr (layer_row_fits(2 * N, V)) return reinterpret_cast<const void*>(&layer_bwd_kernel<TX, N, V, MODE, PF>);
     return nullptr;
 }
 
@@ -598,7 +615,7 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
                             int64_t coef_stride, float* out, float* rms_out, int64_t B, int64_t C, float eps,
                             hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const int wc = x_dtype == kBF16 ? 8 : 4;
+    const int wc = kLayerWC;
     const RowTiling t = choose_row_tiling(C, wc, n);
     if (t.vpt <= 0) return hipErrorInvalidValue;
     const void* fn = pick_fwd(x_dtype, n, t.vpt, use_prefetch(t));
@@ -614,7 +631,7 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
 }
 
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
-    const int wc = x_dtype == kBF16 ? 8 : 4;
+    const int wc = kLayerWC;
     const RowTiling t = choose_row_tiling(C, wc, 2 * n);
     if (t.vpt <= 0) return 1;
     return persistent_grid(pick_bwd(x_dtype, n, t.vpt, 0, use_prefetch(t)), t.threads, B);
@@ -623,7 +640,7 @@ int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, hipStream_t s) {
-    const int wc = x_dtype == kBF16 ? 8 : 4;
+    const int wc = kLayerWC;
     const RowTiling t = choose_row_tiling(C, wc, 2 * n);
     if (t.vpt <= 0) return hipErrorInvalidValue;
     const void* fn = pick_bwd(x_dtype, n, t.vpt, mode, use_prefetch(t));

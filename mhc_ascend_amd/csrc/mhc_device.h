@@ -84,11 +84,28 @@ __device__ __forceinline__ void st16_nt(void* p, uint4 v) {
     __builtin_nontemporal_store(v.w, q + 3);
 }
 
-// Streaming (non-temporal) runs of WN elements, WN a multiple of 16 bytes.
+__device__ __forceinline__ uint2 ld8_nt(const void* p) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    return make_uint2(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1));
+}
+__device__ __forceinline__ void st8_nt(void* p, uint2 v) {
+    uint32_t* q = reinterpret_cast<uint32_t*>(p);
+    __builtin_nontemporal_store(v.x, q);
+    __builtin_nontemporal_store(v.y, q + 1);
+}
+
+// Streaming (non-temporal) runs of WN elements: whole 16-byte pieces, or one
+// 8-byte piece (four bf16).
 template <typename T, int WN>
 __device__ __forceinline__ void load_run_nt(const T* p, float (&v)[WN]) {
     constexpr int PER = 16 / sizeof(T);
-    static_assert(WN % PER == 0, "non-temporal runs are whole 16-byte pieces");
+    if constexpr (sizeof(T) == 2 && WN == 4) {
+        const uint2 q = ld8_nt(p);
+        v[0] = __uint_as_float(q.x << 16); v[1] = __uint_as_float(q.x & 0xffff0000u);
+        v[2] = __uint_as_float(q.y << 16); v[3] = __uint_as_float(q.y & 0xffff0000u);
+        return;
+    }
+    static_assert(WN % PER == 0 || (sizeof(T) == 2 && WN == 4), "non-temporal runs are 16-byte pieces");
 #pragma unroll
     for (int s = 0; s < WN / PER; ++s) {
         const uint4 q = ld16_nt(p + s * PER);
@@ -109,7 +126,12 @@ __device__ __forceinline__ void load_run_nt(const T* p, float (&v)[WN]) {
 template <typename T, int WN>
 __device__ __forceinline__ void store_run_nt(T* p, const float (&v)[WN]) {
     constexpr int PER = 16 / sizeof(T);
-    static_assert(WN % PER == 0, "non-temporal runs are whole 16-byte pieces");
+    if constexpr (sizeof(T) == 2 && WN == 4) {
+        st8_nt(p, make_uint2(static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16),
+                             static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16)));
+        return;
+    }
+    static_assert(WN % PER == 0 || (sizeof(T) == 2 && WN == 4), "non-temporal runs are 16-byte pieces");
 #pragma unroll
     for (int s = 0; s < WN / PER; ++s) {
         uint32_t w[4];

@@ -39,8 +39,8 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
                             hipStream_t s);
 // mode 0: static (writes dx, per-workgroup sums of [dM, dh_post_act,
 //         dh_pre_act] into scal_out[grid][n*n+2n]);
-// mode 1: per-token reduction only (no dx; scal_out[B][n*n+2n+2] holds
-//         dM, dh_post_act, dh_pre_act, inv_rms, k2).
+// mode 1: dx = stream terms only, and per token scal_out[B][n*n+2n+2] =
+//         dM, dh_post_act, dh_pre_act, inv_rms, k2.
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, hipStream_t s);
@@ -93,13 +93,16 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                                hipStream_t s);
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s);
-int dyn_dx_tiles(int64_t B, int64_t C);
-hipError_t launch_dyn_dx(int x_dtype, int n, const float* g, const void* x, const float* w, const float* coef,
-                         const float* scal, const float* dp, const float* s_tok, const float* phi_pre,
-                         const float* phi_post, const float* phi_res, void* dx, float* dphi_part, int tiles,
-                         int64_t B, int64_t C, hipStream_t s);
-hipError_t launch_proj_bwd(const float* dP, int np, const float* x, const float* phi, float* dx, float* dphi_part,
-                           int tiles, int64_t B, int64_t K, hipStream_t s);
+// Projection backward on fp32 MFMA over the flattened [B, K] rows:
+//   dx[b][k] = (accumulate ? dx[b][k] : 0) + (s ? s[b] x[b][k] : 0) + sum_o dP[b][o] Phi[o][k]
+//   dphi_part[tile][o][k] = sum_{b in tile} dP[b][o] x[b][k]
+// Phi row o is phi_row(pre, post, res, n_pre, o): rows < n_pre from `pre`,
+// the next n_pre from `post`, the rest from `res`.  np <= 32, K % 32 == 0.
+int proj_bwd_tiles(int64_t B, int64_t K);
+hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
+                           const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
+                           void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
+                           hipStream_t s);
 hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, hipStream_t s);
 
 // ---- sinkhorn.hip ----------------------------------------------------------

@@ -15,25 +15,82 @@ namespace mhc {
 // forward is faster in isolation but slows the following backward more than
 // it gains (whole fwd+bwd step measured at n=4, C=4096).
 // ---------------------------------------------------------------------------
+//
+// Loads are split in two steps.  load_rows_raw issues the 16-byte loads into
+// raw 32-bit words and converts nothing; unpack_rows turns the words into
+// fp32.  Keeping the conversion out of the load (and out of its bounds-check
+// branch) lets every load of a row - and of the next token's row in the
+// prefetching kernels - be in flight together: a bf16 unpack next to its load
+// makes the compiler wait for that one load before issuing the next.
+// ---------------------------------------------------------------------------
+template <typename T, int WC>
+struct RawChunk {
+    static_assert((WC * sizeof(T)) % 16 == 0 || WC * sizeof(T) == 8, "row chunks are 8 bytes or 16-byte pieces");
+    static constexpr int kWords = WC * (int)sizeof(T) / 4;
+};
+
+template <typename T, int N, int VPT, int WC>
+using RawRows = uint32_t[N][VPT][RawChunk<T, WC>::kWords];
+
 template <typename T, int N, int VPT, int WC, bool NTL>
-__device__ __forceinline__ void load_rows(const T* __restrict__ base, int C, float (&v)[N][VPT][WC]) {
+__device__ __forceinline__ void load_rows_raw(const T* __restrict__ base, int C, RawRows<T, N, VPT, WC>& r) {
+    constexpr int W = RawChunk<T, WC>::kWords;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        // Chunks past the row end load channel 0 instead (always in bounds)
+        // and are zeroed by unpack_rows: no branch around the load.
+        int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        c0 = c0 < C ? c0 : 0;
 #pragma unroll
         for (int i = 0; i < N; ++i) {
-            if (c0 < C) {
-                if constexpr (NTL) {
-                    load_run_nt<T, WC>(base + (int64_t)i * C + c0, v[i][k]);
-                } else {
-                    load_run<T, WC>(base + (int64_t)i * C + c0, v[i][k]);
-                }
+            const char* p = reinterpret_cast<const char*>(base + (int64_t)i * C + c0);
+            if constexpr (W == 2) {
+                const uint2 q = NTL ? ld8_nt(p) : *reinterpret_cast<const uint2*>(p);
+                r[i][k][0] = q.x;
+                r[i][k][1] = q.y;
             } else {
 #pragma unroll
-                for (int e = 0; e < WC; ++e) v[i][k][e] = 0.f;
+                for (int s = 0; s < W / 4; ++s) {
+                    const uint4 q = NTL ? ld16_nt(p + 16 * s) : *reinterpret_cast<const uint4*>(p + 16 * s);
+                    r[i][k][4 * s] = q.x;
+                    r[i][k][4 * s + 1] = q.y;
+                    r[i][k][4 * s + 2] = q.z;
+                    r[i][k][4 * s + 3] = q.w;
+                }
             }
         }
     }
+}
+
+template <typename T, int N, int VPT, int WC>
+__device__ __forceinline__ void unpack_rows(const RawRows<T, N, VPT, WC>& r, int C, float (&v)[N][VPT][WC]) {
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const bool ok = (k * blockDim.x + threadIdx.x) * WC < C;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+#pragma unroll
+            for (int e = 0; e < WC; ++e) {
+                float f;
+                if constexpr (sizeof(T) == 4) {
+                    f = __uint_as_float(r[i][k][e]);
+                } else {
+                    const uint32_t w = r[i][k][e >> 1];
+                    f = __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+                }
+                v[i][k][e] = ok ? f : 0.f;
+            }
+        }
+    }
+}
+
+// Both steps at once, for rows used right away.  Call sites that load several
+// arrays issue all load_rows_raw first and unpack afterwards.
+template <typename T, int N, int VPT, int WC, bool NTL>
+__device__ __forceinline__ void load_rows(const T* __restrict__ base, int C, float (&v)[N][VPT][WC]) {
+    RawRows<T, N, VPT, WC> r;
+    load_rows_raw<T, N, VPT, WC, NTL>(base, C, r);
+    unpack_rows<T, N, VPT, WC>(r, C, v);
 }
 
 template <int VPT, int WC>
@@ -75,5 +132,15 @@ template <typename TX>
 constexpr bool row_fits(int n_arrays, int vpt) {
     return n_arrays * vpt * VecIO<TX>::W <= 128;
 }
+
+// Channels per lane chunk in the fused layer kernels, for both storage
+// dtypes.  They mix fp32 arrays (cotangent, output) with the x storage type;
+// four channels make every fp32 access a contiguous 16-byte piece per lane
+// and every bf16 access an 8-byte one, so each wave instruction covers one
+// contiguous span.  (Eight bf16 channels per lane would split each fp32
+// access into two 16-byte pieces at a 32-byte lane stride.)
+constexpr int kLayerWC = 4;
+
+constexpr bool layer_row_fits(int n_arrays, int vpt) { return n_arrays * vpt * kLayerWC <= 128; }
 
 }  // namespace mhc

@@ -64,9 +64,12 @@ __global__ MHC_ROW_BOUNDS(false) void rmsnorm_bwd_kernel(const T* __restrict__ g
         for (int e = 0; e < WC; ++e) dwacc[k][e] = 0.f;
     }
     for (int64_t b = blockIdx.x; b < B; b += gridDim.x) {
+        RawRows<T, 1, VPT, WC> xr, gr;
         float xv[1][VPT][WC], gv[1][VPT][WC];
-        load_rows<T, 1, VPT, WC, true>(x + b * C, C, xv);
-        load_rows<T, 1, VPT, WC, true>(g + b * C, C, gv);
+        load_rows_raw<T, 1, VPT, WC, true>(x + b * C, C, xr);
+        load_rows_raw<T, 1, VPT, WC, true>(g + b * C, C, gr);
+        unpack_rows<T, 1, VPT, WC>(xr, C, xv);
+        unpack_rows<T, 1, VPT, WC>(gr, C, gv);
         const float inv = 1.f / rms[b];
         float dot = 0.f;
 #pragma unroll
@@ -154,9 +157,13 @@ __global__ MHC_ROW_BOUNDS(false) void aggregate_bwd_kernel(const T* __restrict__
     float h[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) h[i] = h_act[b * h_stride + i];
+    RawRows<T, 1, VPT, WC> gr;
+    RawRows<T, N, VPT, WC> xr;
     float gv[1][VPT][WC], xv[N][VPT][WC];
-    load_rows<T, 1, VPT, WC, true>(g + b * C, C, gv);
-    load_rows<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xv);
+    load_rows_raw<T, 1, VPT, WC, true>(g + b * C, C, gr);
+    load_rows_raw<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xr);
+    unpack_rows<T, 1, VPT, WC>(gr, C, gv);
+    unpack_rows<T, N, VPT, WC>(xr, C, xv);
     float s[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) s[i] = 0.f;
@@ -212,9 +219,13 @@ __global__ MHC_ROW_BOUNDS(false) void distribute_fwd_kernel(const T* __restrict_
     for (int i = 0; i < N; ++i) h[i] = 2.f * sigmoidf(H[b * h_stride + i]);
 #pragma unroll
     for (int k = 0; k < N * N; ++k) m[k] = M[b * m_stride + k];
+    RawRows<T, 1, VPT, WC> yr;
+    RawRows<T, N, VPT, WC> xr;
     float yv[1][VPT][WC], xv[N][VPT][WC];
-    load_rows<T, 1, VPT, WC, true>(y + b * C, C, yv);
-    load_rows<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xv);
+    load_rows_raw<T, 1, VPT, WC, true>(y + b * C, C, yr);
+    load_rows_raw<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xr);
+    unpack_rows<T, 1, VPT, WC>(yr, C, yv);
+    unpack_rows<T, N, VPT, WC>(xr, C, xv);
     float* ob = out + b * (int64_t)N * C;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
@@ -253,10 +264,16 @@ __global__ MHC_ROW_BOUNDS(false) void distribute_bwd_kernel(
     for (int i = 0; i < N; ++i) h[i] = h_act[b * h_stride + i];
 #pragma unroll
     for (int k = 0; k < N * N; ++k) m[k] = M[b * m_stride + k];
+    RawRows<float, N, VPT, WC> gr;
+    RawRows<T, N, VPT, WC> xr;
+    RawRows<T, 1, VPT, WC> yr;
     float gv[N][VPT][WC], xv[N][VPT][WC], yv[1][VPT][WC];
-    load_rows<float, N, VPT, WC, true>(g + b * (int64_t)N * C, C, gv);
-    load_rows<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xv);
-    load_rows<T, 1, VPT, WC, true>(y + b * C, C, yv);
+    load_rows_raw<float, N, VPT, WC, true>(g + b * (int64_t)N * C, C, gr);
+    load_rows_raw<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xr);
+    load_rows_raw<T, 1, VPT, WC, true>(y + b * C, C, yr);
+    unpack_rows<float, N, VPT, WC>(gr, C, gv);
+    unpack_rows<T, N, VPT, WC>(xr, C, xv);
+    unpack_rows<T, 1, VPT, WC>(yr, C, yv);
     float s[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) s[k] = 0.f;

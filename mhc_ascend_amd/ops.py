@@ -4,12 +4,12 @@ Public functional ops keep the reference's names, arguments and defaults.
 Documented differences from the Ascend implementation (all toward the
 PyTorch reference math, which is the contract):
   * arithmetic is fp32 end to end; the Ascend path rounds several
-    intermediates to bf16 (ops.py:144-147, 257, 282);
+    intermediates to bf16 (ops.py:105-107, 218, 243, 280-281);
   * standalone ops return the dtype of their input instead of bf16;
   * the Sinkhorn backward is the exact gradient (the Ascend kernel's row
     step is approximate, sinkhorn_knopp.cpp:1773-1795);
   * alpha parameters stay on the device (no ``.item()`` host syncs,
-    ops.py:459-461, 572-574).
+    ops.py:362-364, 420-422, 533-535).
 """
 from __future__ import annotations
 
@@ -21,7 +21,7 @@ from . import native
 
 
 # =============================================================================
-# Sinkhorn-Knopp (ops.py:71-119)
+# Sinkhorn-Knopp (ops.py:32-80)
 # =============================================================================
 
 class SinkhornKnoppFunction(torch.autograd.Function):
@@ -48,7 +48,7 @@ def sinkhorn_knopp(inp: torch.Tensor, num_iters: int = 20, eps: float = 1e-8) ->
 
 
 # =============================================================================
-# RMSNorm (ops.py:126-175)
+# RMSNorm (ops.py:87-136)
 # =============================================================================
 
 class RMSNormFunction(torch.autograd.Function):
@@ -74,7 +74,7 @@ def rmsnorm(inp: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch
 
 
 # =============================================================================
-# Stream aggregate (ops.py:182-227)
+# Stream aggregate (ops.py:143-188)
 # =============================================================================
 
 class StreamAggregateFunction(torch.autograd.Function):
@@ -99,7 +99,7 @@ def stream_aggregate(inp: torch.Tensor, H_pre_raw: torch.Tensor) -> torch.Tensor
 
 
 # =============================================================================
-# Stream distribute-mix-add (ops.py:234-304)
+# Stream distribute-mix-add (ops.py:195-265)
 # =============================================================================
 
 class StreamDistributeMixAddFunction(torch.autograd.Function):
@@ -128,7 +128,7 @@ stream_distribute = stream_distribute_mix_add
 
 
 def compute_rms(x_flat: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
-    """Per-row RMS of x_flat [B, K] (ops.py:357-369); no autograd, as in the reference."""
+    """Per-row RMS of x_flat [B, K] (ops.py:318-330); no autograd, as in the reference."""
     return native.compute_rms_fwd(x_flat, eps)
 
 
@@ -165,7 +165,7 @@ def mhc_layer_static(x: torch.Tensor, rmsnorm_weight: torch.Tensor, H_pre: torch
 
 
 # =============================================================================
-# Dynamic-H projection (ops.py:311-369)
+# Dynamic-H projection (ops.py:272-315)
 # =============================================================================
 
 class FusedProjectionFunction(torch.autograd.Function):
@@ -190,13 +190,13 @@ def fused_rmsnorm_matmul(x_flat: torch.Tensor, phi_concat: torch.Tensor) -> torc
 
 
 # =============================================================================
-# Dynamic-H layer (ops.py:376-667)
+# Dynamic-H layer (ops.py:337-628)
 # =============================================================================
 
 def mhc_layer_fused_dynamic_inference(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
                                       alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters: int = 20,
                                       sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5) -> torch.Tensor:
-    """Dynamic-H forward without autograd state (ops.py:376-419)."""
+    """Dynamic-H forward without autograd state (ops.py:337-380)."""
     out, _ = native.mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
                                           alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
                                           rmsnorm_eps)
@@ -205,7 +205,7 @@ def mhc_layer_fused_dynamic_inference(x_expanded, rmsnorm_weight, phi_pre, phi_p
 
 class MHCLayerDynamicFunction(torch.autograd.Function):
     """Fused dynamic-H layer: projection -> per-token H -> aggregate ->
-    RMSNorm -> distribute-mix-add, and its backward (ops.py:426-603)."""
+    RMSNorm -> distribute-mix-add, and its backward (ops.py:387-564)."""
 
     @staticmethod
     def forward(ctx, x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post, alpha_res, b_pre,
@@ -232,7 +232,7 @@ class MHCLayerDynamicFunction(torch.autograd.Function):
 def mhc_layer_fused_dynamic_training(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post,
                                      alpha_res, b_pre, b_post, b_res, sinkhorn_iters: int = 20,
                                      sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5) -> torch.Tensor:
-    """Dynamic-H layer with autograd (ops.py:606-667).  Float alphas become
+    """Dynamic-H layer with autograd (ops.py:567-628).  Float alphas become
     device tensors; alpha tensors stay on the device (no .item() syncs)."""
     dev = phi_pre.device
     if not torch.is_tensor(alpha_pre):

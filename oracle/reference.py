@@ -136,7 +136,7 @@ def stream_distribute_mix_add(y_norm: torch.Tensor, h_post_raw: torch.Tensor, m:
 
 def projection(x_flat: torch.Tensor, phi: torch.Tensor) -> torch.Tensor:
     """Dynamic-H projection ``P = x_flat @ phi^T`` (bindings.cpp:480-528,
-    ops.py:311-354).  phi is [out_dim, K] (layer.py:69-71 layout)."""
+    ops.py:272-315).  phi is [out_dim, K] (layer.py:69-71 layout)."""
     return x_flat @ phi.to(x_flat.dtype).t()
 
 
@@ -192,7 +192,7 @@ def dynamic_h_coefficients(x: torch.Tensor, phi_pre: torch.Tensor, phi_post: tor
 
     x_flat = x.reshape(B, n*C); r_h = sqrt(mean(x_flat^2) + rmsnorm_eps)
     (the main path uses rmsnorm_eps, bindings.cpp:909); P = x_flat @ phi^T
-    with phi = [phi_pre; phi_post; phi_res] (ops.py:455-457);
+    with phi = [phi_pre; phi_post; phi_res] (ops.py:416-418);
     t_k = alpha_k * P_k / r_h + b_k; t_res reshaped row-major to n x n;
     h_pre = sigmoid, h_post = 2*sigmoid, M = SK(exp(t_res)).
     """
@@ -221,7 +221,7 @@ def mhc_layer_dynamic(x: torch.Tensor, weight: torch.Tensor, phi_pre: torch.Tens
                       b_pre: torch.Tensor, b_post: torch.Tensor, b_res: torch.Tensor,
                       num_iters: int = 20, sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5,
                       dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    """Dynamic-H mHC layer (bindings.cpp:880-952; ops.py:426-667; layer.py:104-141).
+    """Dynamic-H mHC layer (bindings.cpp:880-952; ops.py:387-628; layer.py:104-141).
 
     The reference rounds x_flat, phi and P to bf16 around its projection
     (bindings.cpp:906, 913, 526-527); the contract is the exact math, so
