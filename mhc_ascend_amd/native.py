@@ -464,3 +464,14 @@ def mhc_layer_fwd_dynamic(x_expanded, rmsnorm_weight, phi_concat, alpha_pre, alp
     pp, pq, pr = _split_phi_concat(_f32c(phi_concat), n)
     return mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, pp, pq, pr, alpha_pre, alpha_post, alpha_res, b_pre,
                                  b_post, b_res, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
+
+
+def mhc_layer_bwd_dynamic(grad_output, x_expanded, rmsnorm_weight, saved, phi_pre, phi_post, phi_res, alpha_pre,
+                          alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters=20, sinkhorn_eps=1e-8,
+                          rmsnorm_eps=1e-5):
+    """Reference-named backward (bindings.cpp:600-874).  Takes the `saved`
+    buffer of mhc_layer_fwd_dynamic in place of the reference's ten saved
+    tensors; returns its 11 gradients in the same order."""
+    return mhc_layer_dynamic_bwd(grad_output, x_expanded, rmsnorm_weight, saved, phi_pre, phi_post, phi_res,
+                                 alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
+                                 rmsnorm_eps)
