@@ -268,10 +268,11 @@ class WrapperWorkload:
         return 20 * self.F + 3 * self.phi_bytes()
 
     def kernel_bytes(self):
-        return {}
+        F = self.F
+        return {"wrap_proj": 4 * F, "wrap_fwd": 8 * F, "wrap_bwd_reduce": 12 * F, "wrap_proj_bwd": 12 * F}
 
     def flops(self):
-        return {"proj": 2 * self.tokens * self.n * self.C * (2 * self.n + self.n * self.n)}
+        return {"wrap_proj": 2 * self.tokens * self.n * self.C * (2 * self.n + self.n * self.n)}
 
     def config(self):
         return {"workload": "C5 MHCResidualWrapper dynamic-H fwd+bwd", "tokens": self.tokens, "batch": self.Bo,
@@ -301,8 +302,8 @@ class WrapperWorkload:
 
 
 WORKLOADS = {"static": StaticWorkload, "dynamic": DynamicWorkload, "wrapper": WrapperWorkload}
-KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "wrap_proj", "wrap_fwd", "wrap_bwd_reduce",
-           "wrap_dx")
+KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "wrap_proj", "wrap_fwd", "wrap_bwd",
+           "wrap_bwd_reduce", "wrap_proj_bwd")
 
 
 # ---------------------------------------------------------------------------

@@ -217,6 +217,54 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
                           int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
                           void* stream);
 
+/* ---- fused MHCResidualWrapper ---------------------------------------------------
+ * The wrapper of layer.py:225-329 on residual / branch [tokens, hidden]
+ * (dtype): streams X_0 = residual, X_1 = branch and, for i >= 2,
+ * X_i = residual * 0.1^(i-1) rounded to dtype (MHC_WRAPPER_DECAY,
+ * layer.py:306-308) or 0 (MHC_WRAPPER_ZERO); the mHC layer on X; the mean
+ * over the n streams (layer.py:316) -> out [tokens, hidden] fp32.  X is never
+ * materialised.  Parameters and `saved` are those of the layer entries
+ * above.  Backward: grad_out [tokens, hidden] fp32 -> grad_residual,
+ * grad_branch (dtype) and the layer's parameter gradients.
+ * Replaces MHCResidualWrapper.forward (layer.py:269-322) over
+ * mhc_layer_fwd_dynamic / mhc_layer_bwd_dynamic (bindings.cpp:880-952,
+ * 600-874) or the static layer chain. */
+#define MHC_WRAPPER_DECAY 0
+#define MHC_WRAPPER_ZERO 1
+
+size_t mhc_wrapper_dynamic_saved_size(int64_t tokens, int32_t n, int32_t hidden);
+size_t mhc_wrapper_dynamic_fwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden);
+int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dtype, int32_t residual_mode,
+                            const void* weight, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
+                            const float* phi_res, const float* alpha_pre, const float* alpha_post,
+                            const float* alpha_res, const float* b_pre, const float* b_post, const float* b_res,
+                            float* out, float* saved, void* workspace, size_t workspace_bytes, int64_t tokens,
+                            int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
+                            void* stream);
+size_t mhc_wrapper_dynamic_bwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
+                                              int32_t residual_mode);
+int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const void* branch, int32_t dtype,
+                            int32_t residual_mode, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
+                            const float* phi_res, const float* alpha_pre, const float* alpha_post,
+                            const float* alpha_res, const float* b_res, const float* saved, void* grad_residual,
+                            void* grad_branch, void* grad_weight, float* grad_phi, float* grad_alpha, float* grad_b,
+                            void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
+                            int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
+
+/* Static H: saved is mhc_layer_static_saved_size(n, hidden) bytes. */
+int mhc_wrapper_static_fwd(const void* residual, const void* branch, int32_t dtype, int32_t residual_mode,
+                           const void* weight, int32_t weight_dtype, const float* h_pre, const float* h_post,
+                           const float* h_res, float* out, float* saved, int64_t tokens, int32_t n, int32_t hidden,
+                           int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
+size_t mhc_wrapper_static_bwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
+                                             int32_t residual_mode);
+int mhc_wrapper_static_bwd(const float* grad_out, const void* residual, const void* branch, int32_t dtype,
+                           int32_t residual_mode, int32_t weight_dtype, const float* h_pre, const float* h_post,
+                           const float* h_res, const float* saved, void* grad_residual, void* grad_branch,
+                           void* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
+                           void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
+                           int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,8 @@ LIB_PATH = os.environ.get("MHC_HIP_LIB") or os.path.join(os.path.dirname(os.path
 
 F32 = 0
 BF16 = 1
+WRAPPER_DECAY = 0
+WRAPPER_ZERO = 1
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -63,6 +65,20 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "mhc_layer_dynamic_bwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32,
                                              _f32, _vp]),
+    "mhc_wrapper_dynamic_saved_size": (_sz, [_i64, _i32, _i32]),
+    "mhc_wrapper_dynamic_fwd_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "mhc_wrapper_dynamic_fwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                               _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32, _f32,
+                                               _vp]),
+    "mhc_wrapper_dynamic_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "mhc_wrapper_dynamic_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                               _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32,
+                                               _f32, _f32, _vp]),
+    "mhc_wrapper_static_fwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i32,
+                                              _i32, _i32, _f32, _f32, _vp]),
+    "mhc_wrapper_static_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "mhc_wrapper_static_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                              _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
     "mhc_layer_static_saved_size": (_sz, [_i32, _i32]),
     "mhc_layer_static_fwd": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
                                             _i64, _i32, _i32, _i32, _f32, _f32, _vp]),

@@ -701,4 +701,244 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     return hip_status(e);
 }
 
+// ---- fused MHCResidualWrapper ------------------------------------------------
+static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidden, int32_t dtype, int32_t w_dtype,
+                         int32_t mode, int32_t num_iters, bool dynamic) {
+    int st = check_layer_shape(fn, tokens, n, hidden, dtype, num_iters);
+    if (st) return st;
+    if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
+    if (mode != MHC_WRAPPER_DECAY && mode != MHC_WRAPPER_ZERO)
+        return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");
+    if (dynamic && hidden % 32 != 0)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of 32");
+    if (choose_row_tiling(hidden, 4, 6).vpt <= 0)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
+    return MHC_SUCCESS;
+}
+
+size_t mhc_wrapper_dynamic_saved_size(int64_t tokens, int32_t n, int32_t hidden) {
+    return mhc_layer_dynamic_saved_size(tokens, n, hidden);
+}
+
+struct WrapFwdWs {
+    int ks;
+    size_t phib_off, p_off, ss_off, total;
+};
+
+static WrapFwdWs wrap_fwd_ws(int64_t tokens, int32_t n, int32_t hidden) {
+    WrapFwdWs w{};
+    const int64_t K = (int64_t)n * hidden;
+    w.ks = tokens > 0 ? wrap_proj_csplit(tokens, hidden) : 1;
+    w.phib_off = 0;
+    w.p_off = align256((size_t)3 * 32 * K * 2);
+    w.ss_off = w.p_off + align256((size_t)w.ks * tokens * 32 * sizeof(float));
+    w.total = w.ss_off + align256((size_t)w.ks * tokens * sizeof(float));
+    return w;
+}
+
+size_t mhc_wrapper_dynamic_fwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden) {
+    if (tokens < 0 || n < 1 || hidden < 1) return 0;
+    return wrap_fwd_ws(tokens, n, hidden).total;
+}
+
+int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dtype, int32_t residual_mode,
+                            const void* weight, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
+                            const float* phi_res, const float* alpha_pre, const float* alpha_post,
+                            const float* alpha_res, const float* b_pre, const float* b_post, const float* b_res,
+                            float* out, float* saved, void* workspace, size_t workspace_bytes, int64_t tokens,
+                            int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
+                            void* stream) {
+    int st = check_wrapper("wrapper_dynamic_fwd", tokens, n, hidden, dtype, weight_dtype, residual_mode, num_iters,
+                           true);
+    if (st) return st;
+    MHC_REQUIRE(weight && phi_pre && phi_post && phi_res && alpha_pre && alpha_post && alpha_res && b_pre &&
+                    b_post && b_res && saved,
+                "wrapper_dynamic_fwd: null parameter pointer");
+    MHC_REQUIRE(tokens == 0 || (residual && branch && out), "wrapper_dynamic_fwd: null residual/branch/out");
+    hipStream_t s = (hipStream_t)stream;
+    const DynSaved d = dyn_saved(tokens, n, hidden);
+    float* w32 = saved + d.w_off;
+    hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
+    if (e != hipSuccess || tokens == 0) return hip_status(e);
+    const WrapFwdWs w = wrap_fwd_ws(tokens, n, hidden);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "wrapper_dynamic_fwd: workspace smaller than mhc_wrapper_dynamic_fwd_workspace_size()");
+    const bool decay = residual_mode == MHC_WRAPPER_DECAY;
+    const int64_t K = (int64_t)n * hidden;
+    const int np = 2 * n + n * n;
+    bf16_raw_t* phib = (bf16_raw_t*)((char*)workspace + w.phib_off);
+    float* pp = (float*)((char*)workspace + w.p_off);
+    float* ss = (float*)((char*)workspace + w.ss_off);
+    e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+    if (e == hipSuccess) e = launch_wrap_proj(dtype, n, decay, residual, branch, phib, pp, ss, tokens, hidden, w.ks, s);
+    if (e == hipSuccess)
+        e = launch_dyn_coef_fwd(n, pp, ss, w.ks, tokens, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
+                                saved + d.coef_off, saved + d.p_off, saved + d.rh_off, num_iters, sinkhorn_eps,
+                                rmsnorm_eps, s);
+    if (e == hipSuccess)
+        e = launch_wrap_fwd(dtype, n, decay, residual, branch, w32, saved + d.coef_off, np, out, tokens, hidden,
+                            rmsnorm_eps, s);
+    return hip_status(e);
+}
+
+struct WrapBwdWs {
+    int grid, cblocks, tiles;
+    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, total;
+};
+
+static WrapBwdWs wrap_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype, bool dynamic, bool decay) {
+    WrapBwdWs w{};
+    const int64_t np = 2 * n + n * n;
+    const int64_t K = (int64_t)n * hidden;
+    w.grid = tokens > 0 ? wrap_bwd_grid(dtype, n, decay, tokens, hidden) : 1;
+    size_t o = 0;
+    w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
+    w.stw_off = o; o += align256((size_t)kDwSplit * hidden * 4);
+    if (!dynamic) {
+        w.scal_off = o; o += align256((size_t)w.grid * (n * n + 2 * n) * 4);
+        w.total = o;
+        return w;
+    }
+    w.cblocks = tokens > 0 ? dyn_coef_bwd_blocks(n, tokens) : 1;
+    w.tiles = tokens > 0 ? wrap_proj_bwd_tiles(tokens, hidden) : 1;
+    w.scal_off = o; o += align256((size_t)tokens * (n * n + 2 * n + 2) * 4);
+    w.dp_off = o; o += align256((size_t)tokens * 32 * 4);
+    w.s_off = o; o += align256((size_t)tokens * 4);
+    w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
+    w.phip_off = o; o += align256((size_t)w.tiles * np * K * 4);
+    w.stp_off = o; o += align256((size_t)kDwSplit * np * K * 4);
+    w.total = o;
+    return w;
+}
+
+size_t mhc_wrapper_dynamic_bwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
+                                              int32_t residual_mode) {
+    if (tokens < 0 || n < 1 || hidden < 1) return 0;
+    return wrap_bwd_ws(tokens, n, hidden, dtype, true, residual_mode == MHC_WRAPPER_DECAY).total;
+}
+
+int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const void* branch, int32_t dtype,
+                            int32_t residual_mode, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
+                            const float* phi_res, const float* alpha_pre, const float* alpha_post,
+                            const float* alpha_res, const float* b_res, const float* saved, void* grad_residual,
+                            void* grad_branch, void* grad_weight, float* grad_phi, float* grad_alpha, float* grad_b,
+                            void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
+                            int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream) {
+    int st = check_wrapper("wrapper_dynamic_bwd", tokens, n, hidden, dtype, weight_dtype, residual_mode, num_iters,
+                           true);
+    if (st) return st;
+    MHC_REQUIRE(phi_pre && phi_post && phi_res && alpha_pre && alpha_post && alpha_res && b_res && saved,
+                "wrapper_dynamic_bwd: null parameter pointer");
+    MHC_REQUIRE(grad_weight && grad_phi && grad_alpha && grad_b, "wrapper_dynamic_bwd: null gradient pointer");
+    MHC_REQUIRE(tokens == 0 || (grad_out && residual && branch && grad_residual && grad_branch),
+                "wrapper_dynamic_bwd: null grad_out/residual/branch/grad pointer");
+    const bool decay = residual_mode == MHC_WRAPPER_DECAY;
+    const WrapBwdWs w = wrap_bwd_ws(tokens, n, hidden, dtype, true, decay);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "wrapper_dynamic_bwd: workspace smaller than mhc_wrapper_dynamic_bwd_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    float* dw_part = (float*)(ws + w.dw_off);
+    float* scal = (float*)(ws + w.scal_off);
+    float* dp = (float*)(ws + w.dp_off);
+    float* stok = (float*)(ws + w.s_off);
+    float* cpart = (float*)(ws + w.cpart_off);
+    float* phip = (float*)(ws + w.phip_off);
+    float* stw = (float*)(ws + w.stw_off);
+    float* stp = (float*)(ws + w.stp_off);
+    const DynSaved d = dyn_saved(tokens, n, hidden);
+    const int np = 2 * n + n * n;
+    const int64_t K = (int64_t)n * hidden;
+    const float* w32 = saved + d.w_off;
+    hipError_t e = hipSuccess;
+    int rows_w = w.grid, rows_p = w.tiles, rows_c = w.cblocks;
+    if (tokens == 0) {
+        rows_w = rows_p = rows_c = 1;
+        e = launch_fill_zero(dw_part, hidden, s);
+        if (e == hipSuccess) e = launch_fill_zero(phip, (int64_t)np * K, s);
+        if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
+    } else {
+        e = launch_wrap_bwd(dtype, n, 1, decay, grad_out, residual, branch, w32, saved + d.coef_off, np,
+                            grad_residual, grad_branch, dw_part, scal, w.grid, tokens, hidden, rmsnorm_eps, s);
+        if (e == hipSuccess)
+            e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
+                                    alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
+                                    s);
+        if (e == hipSuccess)
+            e = launch_wrap_proj_bwd(dtype, n, decay, residual, branch, dp, stok, phi_pre, phi_post, phi_res,
+                                     grad_residual, grad_branch, phip, w.tiles, tokens, hidden, s);
+    }
+    if (e == hipSuccess) e = launch_column_partial(dw_part, rows_w, hidden, stw, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(0, weight_dtype, stw, kDwSplit, hidden, grad_weight, nullptr, 0, nullptr, nullptr,
+                                  nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+    if (e == hipSuccess) e = launch_column_partial(phip, rows_p, (int64_t)np * K, stp, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(0, kF32, stp, kDwSplit, (int64_t)np * K, grad_phi, nullptr, 0, nullptr, nullptr,
+                                  nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+    if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
+    return hip_status(e);
+}
+
+int mhc_wrapper_static_fwd(const void* residual, const void* branch, int32_t dtype, int32_t residual_mode,
+                           const void* weight, int32_t weight_dtype, const float* h_pre, const float* h_post,
+                           const float* h_res, float* out, float* saved, int64_t tokens, int32_t n, int32_t hidden,
+                           int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream) {
+    int st = check_wrapper("wrapper_static_fwd", tokens, n, hidden, dtype, weight_dtype, residual_mode, num_iters,
+                           false);
+    if (st) return st;
+    MHC_REQUIRE(weight && h_pre && h_post && h_res && saved, "wrapper_static_fwd: null parameter pointer");
+    MHC_REQUIRE(tokens == 0 || (residual && branch && out), "wrapper_static_fwd: null residual/branch/out");
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = launch_static_coef(n, h_pre, h_post, h_res, weight, weight_dtype, hidden, saved, num_iters,
+                                      sinkhorn_eps, s);
+    if (e != hipSuccess) return hip_status(e);
+    return hip_status(launch_wrap_fwd(dtype, n, residual_mode == MHC_WRAPPER_DECAY, residual, branch,
+                                      saved + saved_w_offset(n), saved, 0, out, tokens, hidden, rmsnorm_eps, s));
+}
+
+size_t mhc_wrapper_static_bwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
+                                             int32_t residual_mode) {
+    if (tokens < 0 || n < 1 || hidden < 1) return 0;
+    return wrap_bwd_ws(tokens, n, hidden, dtype, false, residual_mode == MHC_WRAPPER_DECAY).total;
+}
+
+int mhc_wrapper_static_bwd(const float* grad_out, const void* residual, const void* branch, int32_t dtype,
+                           int32_t residual_mode, int32_t weight_dtype, const float* h_pre, const float* h_post,
+                           const float* h_res, const float* saved, void* grad_residual, void* grad_branch,
+                           void* grad_weight, float* grad_h_pre, float* grad_h_post, float* grad_h_res,
+                           void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
+                           int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream) {
+    int st = check_wrapper("wrapper_static_bwd", tokens, n, hidden, dtype, weight_dtype, residual_mode, num_iters,
+                           false);
+    if (st) return st;
+    MHC_REQUIRE(h_pre && h_post && h_res && saved, "wrapper_static_bwd: null parameter pointer");
+    MHC_REQUIRE(grad_weight && grad_h_pre && grad_h_post && grad_h_res, "wrapper_static_bwd: null gradient pointer");
+    MHC_REQUIRE(tokens == 0 || (grad_out && residual && branch && grad_residual && grad_branch),
+                "wrapper_static_bwd: null grad_out/residual/branch/grad pointer");
+    const bool decay = residual_mode == MHC_WRAPPER_DECAY;
+    const WrapBwdWs w = wrap_bwd_ws(tokens, n, hidden, dtype, false, decay);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "wrapper_static_bwd: workspace smaller than mhc_wrapper_static_bwd_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    float* dw_part = (float*)((char*)workspace + w.dw_off);
+    float* scal_part = (float*)((char*)workspace + w.scal_off);
+    float* stage = (float*)((char*)workspace + w.stw_off);
+    hipError_t e = hipSuccess;
+    int rows = w.grid;
+    if (tokens == 0) {
+        rows = 1;
+        e = launch_fill_zero(dw_part, hidden, s);
+        if (e == hipSuccess) e = launch_fill_zero(scal_part, n * n + 2 * n, s);
+    } else {
+        e = launch_wrap_bwd(dtype, n, 0, decay, grad_out, residual, branch, saved + saved_w_offset(n), saved, 0,
+                            grad_residual, grad_branch, dw_part, scal_part, w.grid, tokens, hidden, rmsnorm_eps, s);
+    }
+    if (e == hipSuccess) e = launch_column_partial(dw_part, rows, hidden, stage, kDwSplit, s);
+    if (e == hipSuccess)
+        e = launch_layer_finalize(n, weight_dtype, stage, kDwSplit, hidden, grad_weight, scal_part, rows, h_pre,
+                                  h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
+    return hip_status(e);
+}
+
 }  // extern "C"

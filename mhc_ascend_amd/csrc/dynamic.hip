@@ -39,13 +39,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
-// Row o of the concatenated projection (pre rows, then post, then res).
-__device__ __forceinline__ const float* phi_row(const float* pre, const float* post, const float* res, int n, int o,
-                                                int64_t K) {
-    if (o < n) return pre + (int64_t)o * K;
-    if (o < 2 * n) return post + (int64_t)(o - n) * K;
-    return res + (int64_t)(o - 2 * n) * K;
-}
 
 // ---------------------------------------------------------------------------
 // fp32 -> three bf16 terms: v = hi + mid + lo exactly up to the last bit

@@ -274,6 +274,15 @@ __device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Row o of the concatenated dynamic-H projection [pre; post; res] (ops.py:416-418):
+// rows < n from `pre`, the next n from `post`, the rest from `res`; K = n * C.
+__device__ __forceinline__ const float* phi_row(const float* pre, const float* post, const float* res, int n, int o,
+                                                int64_t K) {
+    if (o < n) return pre + (int64_t)o * K;
+    if (o < 2 * n) return post + (int64_t)(o - n) * K;
+    return res + (int64_t)(o - 2 * n) * K;
+}
+
 constexpr int pow2ceil(int n) { return n <= 1 ? 1 : 2 * pow2ceil((n + 1) / 2); }
 
 // 1/d from the hardware reciprocal (v_rcp_f32, ~1 ulp) refined by one

@@ -105,6 +105,27 @@ hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_s
                            hipStream_t s);
 hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, hipStream_t s);
 
+// ---- wrapper.hip -----------------------------------------------------------
+// Fused MHCResidualWrapper (n = 4): streams synthesised from (residual,
+// branch); decay = 'decay' mode (else 'zero').
+hipError_t launch_wrap_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
+                           const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
+                           hipStream_t s);
+int wrap_bwd_grid(int dt, int n, bool decay, int64_t B, int64_t C);
+// mode 0: static (per-workgroup sums of [dM, dh_post_act, dh_pre_act] in
+// scal_out[grid][n*n+2n]); mode 1: dynamic (per-token scal_out[B][n*n+2n+2]).
+hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, const void* res, const void* br,
+                           const float* w, const float* coef, int64_t coef_stride, void* dres, void* dbr,
+                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s);
+int wrap_proj_csplit(int64_t B, int64_t C);
+hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const void* br, const bf16_raw_t* phib,
+                            float* p_part, float* ss_part, int64_t B, int64_t C, int ks, hipStream_t s);
+int wrap_proj_bwd_tiles(int64_t B, int64_t C);
+hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
+                                const float* s_tok, const float* phi_pre, const float* phi_post, const float* phi_res,
+                                void* dres, void* dbr, float* dphi_part, int tiles, int64_t B, int64_t C,
+                                hipStream_t s);
+
 // ---- sinkhorn.hip ----------------------------------------------------------
 hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batch, int iters, float eps,
                                hipStream_t s);

@@ -1,0 +1,965 @@
+// MHCResidualWrapper fused on gfx950 (layer.py:269-322).
+//
+// The wrapper turns (residual r, branch b) [tokens, C] into n layer streams
+//     X_0 = r,  X_1 = b,  X_i = r * 0.1^(i-1) rounded to the storage dtype
+//     ('decay', layer.py:306-308) or X_i = 0 ('zero'),
+// runs the mHC layer on X [tokens, n, C] and returns the mean over streams.
+// Here X never exists in memory: every kernel rebuilds the stream values of
+// the channels it holds from r and b, in registers.  The stream mean folds
+// into the layer's output:
+//     mean_i out_i = sum_j cm_j X_j + hs * y,   cm_j = (1/n) sum_i M_ij,
+//                                               hs = (1/n) sum_i h_post_i.
+// Backward, with G the cotangent of the mean (every stream receives G / n):
+//     gy = hs G,  gxa = w gy / r_rms - xa k2,  dX_j = cm_j G + h_pre_j gxa
+//     d r = dX_0 + sum_{i>=2} 0.1^(i-1) dX_i,  d b = dX_1
+// plus, for dynamic H, the projection and r_h terms (s X_j + dP . Phi_j).
+//
+// Kernels:
+//   wrap_fwd_kernel       row pass: xa, RMSNorm, the stream mean (fp32 out)
+//   wrap_bwd_kernel       row pass: all row sums of a token, the stream parts
+//                         of d r / d b; MODE 0 static (per-workgroup sums),
+//                         MODE 1 dynamic (per-token scalars)
+//   wrap_proj_kernel      P = X_flat . Phi^T split-K on bf16 MFMA, reading r
+//                         and b once per channel for all n streams
+//   wrap_proj_bwd_kernel  d r, d b += s X + dP . Phi (fp32 MFMA, Phi folded
+//                         over the residual-derived streams) and dPhi
+#include "mhc_device.h"
+#include "mhc_internal.h"
+#include "mhc_rows.h"
+
+namespace mhc {
+
+// 0.1^e in double, as Python's 0.1 ** e for the small e used here
+// (layer.py:308 multiplies by that double; the product is formed in fp32).
+constexpr double pow01(int e) { return e <= 0 ? 1.0 : 0.1 * pow01(e - 1); }
+
+template <int I>
+constexpr float decay_mult() { return (float)pow01(I - 1); }
+
+// Round to the storage dtype (the synthesised stream is a tensor of it).
+template <typename TX>
+__device__ __forceinline__ float round_store(float v) {
+    if constexpr (sizeof(TX) == 2) {
+        return bf16_to_f32(f32_to_bf16(v));
+    } else {
+        return v;
+    }
+}
+
+// Stream I of the synthesised row at one element.
+template <typename TX, int I, bool DECAY>
+__device__ __forceinline__ float wrap_stream(float r, float b) {
+    if constexpr (I == 0) {
+        return r;
+    } else if constexpr (I == 1) {
+        return b;
+    } else if constexpr (DECAY) {
+        constexpr float m = decay_mult<I>();
+        return round_store<TX>(r * m);
+    } else {
+        return 0.f;
+    }
+}
+
+template <typename TX, int N, bool DECAY>
+__device__ __forceinline__ void wrap_streams(float r, float b, float (&x)[N]) {
+    x[0] = r;
+    if constexpr (N > 1) x[1] = b;
+    if constexpr (N > 2) x[2] = wrap_stream<TX, 2, DECAY>(r, b);
+    if constexpr (N > 3) x[3] = wrap_stream<TX, 3, DECAY>(r, b);
+    static_assert(N <= 4, "wrapper kernels are instantiated for n <= 4");
+}
+
+// d r contribution weight of stream j (0 for the branch and for zero streams)
+template <int J, bool DECAY>
+__device__ __forceinline__ float res_weight() {
+    constexpr float w = J == 0 ? 1.f : (J == 1 ? 0.f : (DECAY ? decay_mult<J>() : 0.f));
+    return w;
+}
+
+template <int N> constexpr int wcoef_size() { return 2 * N + N * N; }
+
+// ---------------------------------------------------------------------------
+// Forward row pass.
+// ---------------------------------------------------------------------------
+template <typename TX, int N, int VPT, bool DECAY>
+__device__ __forceinline__ void wrap_fwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
+                                               const float (&wv)[VPT][kLayerWC], const float (&rv)[1][VPT][kLayerWC],
+                                               const float (&bv)[1][VPT][kLayerWC], float* __restrict__ out, int C,
+                                               float eps, float* red) {
+    constexpr int WC = kLayerWC;
+    const float* cf = coef + b * coef_stride;
+    float hp[N], cm[N], hs = 0.f;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        hp[j] = cf[j];
+        hs += cf[N + j];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) s += cf[2 * N + i * N + j];
+        cm[j] = s * (1.f / N);
+    }
+    hs *= 1.f / N;
+    float xa[VPT][WC];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+#pragma unroll
+        for (int e = 0; e < WC; ++e) {
+            float x[N];
+            wrap_streams<TX, N, DECAY>(rv[0][k][e], bv[0][k][e], x);
+            float s = 0.f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) s += hp[j] * x[j];
+            xa[k][e] = s;
+            ss += s * s;
+        }
+    }
+    float v[1] = {ss};
+    block_sum<1>(v, red);
+    const float inv = 1.f / sqrtf(v[0] / (float)C + eps);
+    float* ob = out + b * (int64_t)C;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        if (c0 < C) {
+            float o[WC];
+#pragma unroll
+            for (int e = 0; e < WC; ++e) {
+                float x[N];
+                wrap_streams<TX, N, DECAY>(rv[0][k][e], bv[0][k][e], x);
+                float s = hs * (xa[k][e] * inv * wv[k][e]);
+#pragma unroll
+                for (int j = 0; j < N; ++j) s += cm[j] * x[j];
+                o[e] = s;
+            }
+            store_run_nt<float, WC>(ob + c0, o);
+        }
+    }
+}
+
+template <typename TX, int N, int VPT, bool PF, bool DECAY>
+__global__ MHC_ROW_BOUNDS(PF) void wrap_fwd_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
+                                                   const float* __restrict__ w, const float* __restrict__ coef,
+                                                   int64_t coef_stride, float* __restrict__ out, int64_t B, int C,
+                                                   float eps) {
+    constexpr int WC = kLayerWC;
+    __shared__ float red[8];
+    float wv[VPT][WC];
+    load_weight<VPT, WC>(w, C, wv);
+    const int64_t G = gridDim.x;
+    int64_t b = blockIdx.x;
+    RawRows<TX, 1, VPT, WC> rA, bA, rB, bB;
+    float rv[1][VPT][WC], bv[1][VPT][WC];
+    if constexpr (PF) {
+        if (b < B) {
+            load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
+            load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
+        }
+        while (b < B) {
+            const int64_t b1 = b + G;
+            if (b1 < B) {
+                load_rows_raw<TX, 1, VPT, WC, true>(res + b1 * C, C, rB);
+                load_rows_raw<TX, 1, VPT, WC, true>(br + b1 * C, C, bB);
+            }
+            unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
+            unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
+            wrap_fwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, rv, bv, out, C, eps, red);
+            if (b1 >= B) break;
+            const int64_t b2 = b1 + G;
+            if (b2 < B) {
+                load_rows_raw<TX, 1, VPT, WC, true>(res + b2 * C, C, rA);
+                load_rows_raw<TX, 1, VPT, WC, true>(br + b2 * C, C, bA);
+            }
+            unpack_rows<TX, 1, VPT, WC>(rB, C, rv);
+            unpack_rows<TX, 1, VPT, WC>(bB, C, bv);
+            wrap_fwd_token<TX, N, VPT, DECAY>(b1, coef, coef_stride, wv, rv, bv, out, C, eps, red);
+            b = b2;
+        }
+    } else {
+        for (; b < B; b += G) {
+            load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
+            load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
+            unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
+            unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
+            wrap_fwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, rv, bv, out, C, eps, red);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward row pass.  Per token the block forms, in one reduction,
+//   ss = sum xa^2, gwx = sum G w xa, u_j = sum G X_j, v_j = sum G w X_j,
+//   z_j = sum xa X_j
+// and from them the scalars of the layer backward in its layout
+// (dM[n*n], dh_post_act[n], dh_pre_act[n], 1/r, k2):
+//   dM_ij = u_j / n,  dh_post_act_i = gwx / (n r),
+//   dh_pre_act_j = hs v_j / r - k2 z_j,  k2 = hs gwx / (C r^3).
+// MODE 0 sums the first n*n+2n per workgroup (static H, shared M); MODE 1
+// writes them per token (dynamic H).  d r / d b get the stream terms.
+// ---------------------------------------------------------------------------
+template <typename TX, int N, int VPT, int MODE, bool DECAY>
+__device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
+                                               const float (&wv)[VPT][kLayerWC], const float (&gv)[1][VPT][kLayerWC],
+                                               const float (&rv)[1][VPT][kLayerWC],
+                                               const float (&bv)[1][VPT][kLayerWC], float (&dwacc)[VPT][kLayerWC],
+                                               float& sacc, TX* __restrict__ dres, TX* __restrict__ dbr,
+                                               float* __restrict__ scal_out, int C, float eps, float* red) {
+    constexpr int WC = kLayerWC;
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NR = 2 + 3 * N;  // ss, gwx, u_j, v_j, z_j
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nwaves = blockDim.x / kWave;
+    float* tot = red + 8 * NR;
+    const float* cf = coef + b * coef_stride;
+    float hp[N], cm[N], hs = 0.f;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        hp[j] = cf[j];
+        hs += cf[N + j];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) s += cf[2 * N + i * N + j];
+        cm[j] = s * (1.f / N);
+    }
+    hs *= 1.f / N;
+    {
+        float rsum[NR];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) rsum[q] = 0.f;
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+#pragma unroll
+            for (int e = 0; e < WC; ++e) {
+                float x[N];
+                wrap_streams<TX, N, DECAY>(rv[0][k][e], bv[0][k][e], x);
+                float xa = 0.f;
+#pragma unroll
+                for (int j = 0; j < N; ++j) xa += hp[j] * x[j];
+                const float g = gv[0][k][e];
+                const float wg = wv[k][e] * g;
+                rsum[0] += xa * xa;
+                rsum[1] += wg * xa;
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    rsum[2 + j] += g * x[j];
+                    rsum[2 + N + j] += wg * x[j];
+                    rsum[2 + 2 * N + j] += xa * x[j];
+                }
+            }
+        }
+        wave_sum_last<NR>(rsum);
+        if (lane == kWave - 1) {
+#pragma unroll
+            for (int q = 0; q < NR; ++q) red[wave * NR + q] = rsum[q];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < NR) {
+        float s = 0.f;
+        for (int q = 0; q < nwaves; ++q) s += red[q * NR + threadIdx.x];
+        tot[threadIdx.x] = s;
+    }
+    __syncthreads();
+    const float inv = 1.f / sqrtf(tot[0] / (float)C + eps);
+    const float gwx = tot[1];
+    const float k2 = hs * gwx * inv * inv * inv / (float)C;
+
+    if (threadIdx.x < NS + 2) {
+        const int t = threadIdx.x;
+        float v;
+        if (t < N * N) {
+            v = tot[2 + t % N] * (1.f / N);  // dM_ij = u_j / n
+        } else if (t < N * N + N) {
+            v = gwx * inv * (1.f / N);  // dh_post_act_i
+        } else if (t < NS) {
+            const int j = t - N * N - N;
+            v = hs * inv * tot[2 + N + j] - k2 * tot[2 + 2 * N + j];  // dh_pre_act_j
+        } else {
+            v = (t == NS) ? inv : k2;
+        }
+        if (MODE == 0) {
+            sacc += v;
+        } else {
+            scal_out[b * (NS + 2) + t] = v;
+        }
+    }
+
+    TX* drb = dres + b * (int64_t)C;
+    TX* dbb = dbr + b * (int64_t)C;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        float dr[WC], db[WC];
+#pragma unroll
+        for (int e = 0; e < WC; ++e) {
+            float x[N];
+            wrap_streams<TX, N, DECAY>(rv[0][k][e], bv[0][k][e], x);
+            float xa = 0.f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) xa += hp[j] * x[j];
+            const float g = gv[0][k][e];
+            const float gy = hs * g;
+            const float gxa = wv[k][e] * gy * inv - xa * k2;
+            dwacc[k][e] += gy * xa * inv;
+            float a = 0.f;
+            if constexpr (N > 0) a += cm[0] * g + hp[0] * gxa;
+            if constexpr (N > 2) a += res_weight<2, DECAY>() * (cm[2] * g + hp[2] * gxa);
+            if constexpr (N > 3) a += res_weight<3, DECAY>() * (cm[3] * g + hp[3] * gxa);
+            dr[e] = a;
+            db[e] = (N > 1) ? cm[N > 1 ? 1 : 0] * g + hp[N > 1 ? 1 : 0] * gxa : 0.f;
+        }
+        if (c0 < C) {
+            store_run_nt<TX, WC>(drb + c0, dr);
+            store_run_nt<TX, WC>(dbb + c0, db);
+        }
+    }
+}
+
+template <typename TX, int N, int VPT, int MODE, bool PF, bool DECAY>
+__global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, const TX* __restrict__ res,
+                                                   const TX* __restrict__ br, const float* __restrict__ w,
+                                                   const float* __restrict__ coef, int64_t coef_stride,
+                                                   TX* __restrict__ dres, TX* __restrict__ dbr,
+                                                   float* __restrict__ dw_part, float* __restrict__ scal_out,
+                                                   int64_t B, int C, float eps) {
+    constexpr int WC = kLayerWC;
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NR = 2 + 3 * N;
+    __shared__ float red[9 * NR];
+    float wv[VPT][WC];
+    load_weight<VPT, WC>(w, C, wv);
+    float dwacc[VPT][WC];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+#pragma unroll
+        for (int e = 0; e < WC; ++e) dwacc[k][e] = 0.f;
+    }
+    float sacc = 0.f;
+    const int64_t G = gridDim.x;
+    int64_t b = blockIdx.x;
+    RawRows<float, 1, VPT, WC> gA, gB;
+    RawRows<TX, 1, VPT, WC> rA, bA, rB, bB;
+    float gv[1][VPT][WC], rv[1][VPT][WC], bv[1][VPT][WC];
+    if constexpr (PF) {
+        if (b < B) {
+            load_rows_raw<float, 1, VPT, WC, true>(g + b * C, C, gA);
+            load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
+            load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
+        }
+        while (b < B) {
+            const int64_t b1 = b + G;
+            if (b1 < B) {
+                load_rows_raw<float, 1, VPT, WC, true>(g + b1 * C, C, gB);
+                load_rows_raw<TX, 1, VPT, WC, true>(res + b1 * C, C, rB);
+                load_rows_raw<TX, 1, VPT, WC, true>(br + b1 * C, C, bB);
+            }
+            unpack_rows<float, 1, VPT, WC>(gA, C, gv);
+            unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
+            unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
+            wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
+                                                    scal_out, C, eps, red);
+            if (b1 >= B) break;
+            const int64_t b2 = b1 + G;
+            if (b2 < B) {
+                load_rows_raw<float, 1, VPT, WC, true>(g + b2 * C, C, gA);
+                load_rows_raw<TX, 1, VPT, WC, true>(res + b2 * C, C, rA);
+                load_rows_raw<TX, 1, VPT, WC, true>(br + b2 * C, C, bA);
+            }
+            unpack_rows<float, 1, VPT, WC>(gB, C, gv);
+            unpack_rows<TX, 1, VPT, WC>(rB, C, rv);
+            unpack_rows<TX, 1, VPT, WC>(bB, C, bv);
+            wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b1, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
+                                                    scal_out, C, eps, red);
+            b = b2;
+        }
+    } else {
+        for (; b < B; b += G) {
+            load_rows_raw<float, 1, VPT, WC, true>(g + b * C, C, gA);
+            load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
+            load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
+            unpack_rows<float, 1, VPT, WC>(gA, C, gv);
+            unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
+            unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
+            wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
+                                                    scal_out, C, eps, red);
+        }
+    }
+    float* dwp = dw_part + (int64_t)blockIdx.x * C;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        if (c0 < C) store_run<float, WC>(dwp + c0, dwacc[k]);
+    }
+    if (MODE == 0 && threadIdx.x < NS) scal_out[(int64_t)blockIdx.x * NS + threadIdx.x] = sacc;
+}
+
+// ---------------------------------------------------------------------------
+// Projection of the synthesised row: P[b][o] = sum_j sum_c X_j[b][c]
+// Phi[o][j*C + c], and sum_j sum_c X_j^2, on bf16 MFMA 16x16x32.  Workgroup =
+// 64 tokens (4 M-tiles of 16) x one channel range; its 4 waves take
+// interleaved 32-channel steps.  Each step loads the r and b pieces once and
+// runs the MFMAs of all n streams against the Phi planes at k = j*C + c.
+// bf16 storage: every stream is exact in bf16, so P = X.(hi + mid + lo) (three
+// MFMAs per stream and N-tile).  fp32 storage: X is split into hi/mid/lo too
+// and the six products down to 2^-16 relative weight are kept, as in
+// proj_mfma_kernel.  p_part[ks][B][32], ss_part[ks][B].
+// ---------------------------------------------------------------------------
+typedef __bf16 wbf16x8_t __attribute__((ext_vector_type(8)));
+typedef float wf32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int wu32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ wf32x4_t wmfma16x16x32(wu32x4_t a, wu32x4_t b, wf32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(wbf16x8_t, a), __builtin_bit_cast(wbf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t wpack(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+__device__ __forceinline__ void wsplit3(float v, float& h, float& m, float& l) {
+    h = bf16_to_f32(f32_to_bf16(v));
+    const float r = v - h;
+    m = bf16_to_f32(f32_to_bf16(r));
+    l = r - m;
+}
+
+template <typename TX, int N, bool DECAY>
+__global__ __launch_bounds__(256) void wrap_proj_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
+                                                        const bf16_t* __restrict__ phib, float* __restrict__ p_part,
+                                                        float* __restrict__ ss_part, int64_t B, int C,
+                                                        int64_t cchunk) {
+    constexpr int KP = 32;                       // padded projection rows
+    constexpr int W = 8 * (int)sizeof(TX) / 4;   // 32-bit words of 8 elements
+    constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
+    __shared__ float red[3][36][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row = lane & 15;
+    const int kg = lane >> 4;
+    const int64_t K = (int64_t)N * C;
+    const int64_t tok0 = (int64_t)blockIdx.x * 64;
+    const int64_t cb = (int64_t)blockIdx.y * cchunk;
+    const int64_t ce = (cb + cchunk < C) ? cb + cchunk : C;
+
+    wf32x4_t acc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    float ss[4] = {0.f, 0.f, 0.f, 0.f};
+    int64_t rowoff[4];
+    uint32_t vmask[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const int64_t tok = tok0 + mt * 16 + row;
+        vmask[mt] = tok < B ? 0xffffffffu : 0u;
+        rowoff[mt] = (tok < B ? tok : 0) * C;
+    }
+
+    for (int64_t c0 = cb + wave * 32; c0 < ce; c0 += 128) {
+        const int64_t cc = c0 + kg * 8;
+        // raw r and b words at channels cc..cc+7 of each M-tile row (rows past
+        // the batch read row 0 and are masked to zero)
+        uint32_t rw[4][W], bw[4][W];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int s4 = 0; s4 < W / 4; ++s4) {
+                const uint4 qr = ld16_nt(reinterpret_cast<const char*>(res + rowoff[mt] + cc) + 16 * s4);
+                const uint4 qb = ld16_nt(reinterpret_cast<const char*>(br + rowoff[mt] + cc) + 16 * s4);
+                rw[mt][4 * s4] = qr.x & vmask[mt]; rw[mt][4 * s4 + 1] = qr.y & vmask[mt];
+                rw[mt][4 * s4 + 2] = qr.z & vmask[mt]; rw[mt][4 * s4 + 3] = qr.w & vmask[mt];
+                bw[mt][4 * s4] = qb.x & vmask[mt]; bw[mt][4 * s4 + 1] = qb.y & vmask[mt];
+                bw[mt][4 * s4 + 2] = qb.z & vmask[mt]; bw[mt][4 * s4 + 3] = qb.w & vmask[mt];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NSTR; ++j) {
+            wu32x4_t bvp[3][2];
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    bvp[p][nt] = *reinterpret_cast<const wu32x4_t*>(phib + ((int64_t)p * KP + nt * 16 + row) * K +
+                                                                     (int64_t)j * C + cc);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                float xv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float r, b;
+                    if constexpr (sizeof(TX) == 2) {
+                        r = __uint_as_float((e & 1) ? (rw[mt][e >> 1] & 0xffff0000u) : (rw[mt][e >> 1] << 16));
+                        b = __uint_as_float((e & 1) ? (bw[mt][e >> 1] & 0xffff0000u) : (bw[mt][e >> 1] << 16));
+                    } else {
+                        r = __uint_as_float(rw[mt][e]);
+                        b = __uint_as_float(bw[mt][e]);
+                    }
+                    float x[N];
+                    wrap_streams<TX, N, DECAY>(r, b, x);
+                    xv[e] = x[j];
+                    ss[mt] += x[j] * x[j];
+                }
+                if constexpr (sizeof(TX) == 2) {
+                    wu32x4_t a;
+                    if (j == 0) {
+                        a = wu32x4_t{rw[mt][0], rw[mt][1], rw[mt][2], rw[mt][3]};
+                    } else if (j == 1) {
+                        a = wu32x4_t{bw[mt][0], bw[mt][1], bw[mt][2], bw[mt][3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) a[e] = wpack(xv[2 * e], xv[2 * e + 1]);
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+                        for (int p = 0; p < 3; ++p) acc[mt][nt] = wmfma16x16x32(a, bvp[p][nt], acc[mt][nt]);
+                    }
+                } else {
+                    wu32x4_t ah, am, al;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float h0, m0, l0, h1, m1, l1;
+                        wsplit3(xv[2 * e], h0, m0, l0);
+                        wsplit3(xv[2 * e + 1], h1, m1, l1);
+                        ah[e] = wpack(h0, h1);
+                        am[e] = wpack(m0, m1);
+                        al[e] = wpack(l0, l1);
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < 2; ++nt) {
+                        acc[mt][nt] = wmfma16x16x32(ah, bvp[0][nt], acc[mt][nt]);
+                        acc[mt][nt] = wmfma16x16x32(ah, bvp[1][nt], acc[mt][nt]);
+                        acc[mt][nt] = wmfma16x16x32(am, bvp[0][nt], acc[mt][nt]);
+                        acc[mt][nt] = wmfma16x16x32(ah, bvp[2][nt], acc[mt][nt]);
+                        acc[mt][nt] = wmfma16x16x32(am, bvp[1][nt], acc[mt][nt]);
+                        acc[mt][nt] = wmfma16x16x32(al, bvp[0][nt], acc[mt][nt]);
+                    }
+                }
+            }
+        }
+    }
+
+    // waves 1..3 hand their partials to wave 0 through LDS
+    if (wave > 0) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave - 1][(mt * 2 + nt) * 4 + i][lane] = acc[mt][nt][i];
+            }
+            red[wave - 1][32 + mt][lane] = ss[mt];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mt][nt][i] += red[q][(mt * 2 + nt) * 4 + i][lane];
+            }
+            ss[mt] += red[q][32 + mt][lane];
+        }
+    }
+    float* pp = p_part + (int64_t)blockIdx.y * B * KP;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t tok = tok0 + mt * 16 + kg * 4 + i;
+            if (tok < B) {
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) pp[tok * KP + nt * 16 + row] = acc[mt][nt][i];
+            }
+        }
+        float s2 = ss[mt];
+        s2 += __shfl_xor(s2, 16, kWave);
+        s2 += __shfl_xor(s2, 32, kWave);
+        const int64_t tok = tok0 + mt * 16 + row;
+        if (kg == 0 && tok < B) ss_part[(int64_t)blockIdx.y * B + tok] = s2;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Projection backward of the wrapper (fp32 MFMA 32x32x2), over channels c:
+//   d r[b][c] += s[b] sum_j w_j X_j + sum_o dP[b][o] Phi_r[o][c]
+//   d b[b][c] += s[b] X_1        + sum_o dP[b][o] Phi[o][C + c]
+//   dPhi_part[tile][o][j*C + c] = sum_{b in tile} dP[b][o] X_j[b][c]
+// with w_j the d r weight of stream j (1, 0, 0.1, 0.01, ...) and Phi_r =
+// sum_j w_j Phi_j: the residual-derived streams share one dx_proj chain.
+// Same staging as proj_bwd_mfma_kernel: workgroup = 4 waves x 32 channels,
+// stages of 32 tokens, two register sets of fetched stages, LDS tiles.
+// ---------------------------------------------------------------------------
+typedef float wf32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ wf32x16_t wmfma32x32x2(float a, float b, wf32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int wdtok(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+template <typename TX, int N, bool DECAY>
+__global__ __launch_bounds__(256) void wrap_proj_bwd_kernel(
+    const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ dP,
+    const float* __restrict__ s_tok, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
+    const float* __restrict__ phi_res, TX* __restrict__ dres, TX* __restrict__ dbr, float* __restrict__ dphi_part,
+    int64_t B, int C, int64_t tile) {
+    constexpr int NP = 2 * N + N * N;
+    constexpr int NOH = (NP + 1) / 2;          // projection rows per lane half
+    static_assert(NP <= 32, "projection rows must fit one 32-row tile");
+    constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
+    constexpr int TB = 32;
+    constexpr int CB = 128;
+    constexpr int EPV = 16 / sizeof(TX);
+    constexpr int VPR = CB / EPV;
+    constexpr int RPP = 256 / VPR;
+    constexpr int PASSES = TB / RPP;
+    constexpr int PITCH = CB * sizeof(TX) + 16;
+    constexpr int EPR = PITCH / sizeof(TX);
+    __shared__ __align__(16) char tiles_lds[2][4][TB * PITCH];  // r, b, d r (in), d b (in)
+    __shared__ float dp_lds[2][TB][33];
+    __shared__ float s_lds[2][TB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const int64_t K = (int64_t)N * C;
+    const int64_t cb0 = (int64_t)blockIdx.x * CB;
+    const int64_t cc = cb0 + wave * 32 + col;
+    const bool wave_on = cb0 + wave * 32 < C;  // C % 32 == 0
+
+    const int lrow = tid / VPR;
+    const int lvec = tid % VPR;
+    const int64_t lcol = cb0 + (int64_t)lvec * EPV;
+    const bool lcol_ok = lcol < C;
+    const int dtk = tid >> 3;
+    const int dpo = (tid & 7) * 4;
+
+    // dx_proj B operands: residual-folded Phi and the branch stream's Phi
+    float bphi_r[NOH], bphi_b[NOH];
+#pragma unroll
+    for (int m = 0; m < NOH; ++m) {
+        const int o = NOH * h + m;
+        float vr = 0.f, vb = 0.f;
+        if (wave_on && o < NP) {
+            const float* rowp = phi_row(phi_pre, phi_post, phi_res, N, o, K);
+            vr = rowp[cc];
+            if constexpr (N > 1) vb = rowp[C + cc];
+            if constexpr (N > 2) vr += res_weight<2, DECAY>() * rowp[2 * (int64_t)C + cc];
+            if constexpr (N > 3) vr += res_weight<3, DECAY>() * rowp[3 * (int64_t)C + cc];
+        }
+        bphi_r[m] = vr;
+        bphi_b[m] = vb;
+    }
+    wf32x16_t accP[NSTR];
+#pragma unroll
+    for (int j = 0; j < NSTR; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) accP[j][r] = 0.f;
+    }
+
+    const int64_t t_begin = (int64_t)blockIdx.y * tile;
+    const int64_t t_end = (t_begin + tile < B) ? t_begin + tile : B;
+
+    // One register set of fetched data: stage i+1 is fetched at the start of
+    // stage i's compute and written to the other LDS buffer after it.
+    uint4 fv[4][PASSES];
+    float fdp[4], fs = 0.f;
+    const TX* srcs[4] = {res, br, dres, dbr};
+    auto fetch = [&](int64_t t0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t t = t0 + lrow + p * RPP;
+            const int64_t off = (t < t_end ? t : t0) * (int64_t)C + (lcol_ok ? lcol : 0);
+#pragma unroll
+            for (int a = 0; a < 4; ++a) fv[a][p] = ld16_nt(srcs[a] + off);
+        }
+        const int64_t td = t0 + dtk;
+        const int64_t tdc = td < t_end ? td : t0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) fdp[q] = dP[tdc * 32 + dpo + q];
+        fs = (tid < TB) ? s_tok[(t0 + tid < t_end) ? t0 + tid : t0] : 0.f;
+    };
+    auto commit = [&](int64_t t0, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int row = lrow + p * RPP;
+            const uint32_t m = (lcol_ok && t0 + row < t_end) ? 0xffffffffu : 0u;
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const uint4 v = fv[a][p];
+                *reinterpret_cast<uint4*>(&tiles_lds[buf][a][row * PITCH + lvec * 16]) =
+                    make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+            }
+        }
+        const bool tok_ok = t0 + dtk < t_end;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dp_lds[buf][dtk][dpo + q] = (tok_ok && dpo + q < NP) ? fdp[q] : 0.f;
+        if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? fs : 0.f;
+    };
+    auto compute = [&](int64_t t0, int cur) __attribute__((always_inline)) {
+        if (!wave_on) return;
+        const TX* rt = reinterpret_cast<const TX*>(tiles_lds[cur][0]);
+        const TX* bt = reinterpret_cast<const TX*>(tiles_lds[cur][1]);
+        const TX* drt = reinterpret_cast<const TX*>(tiles_lds[cur][2]);
+        const TX* dbt = reinterpret_cast<const TX*>(tiles_lds[cur][3]);
+        const int c = wave * 32 + col;
+        // dPhi: reduction over the block's tokens, one chain per stream
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = wdtok(r, h);
+            const float a2 = dp_lds[cur][t][col];
+            float x[N];
+            wrap_streams<TX, N, DECAY>(VecIO<TX>::scalar(rt + t * EPR + c), VecIO<TX>::scalar(bt + t * EPR + c), x);
+#pragma unroll
+            for (int j = 0; j < NSTR; ++j) accP[j] = wmfma32x32x2(a2, x[j], accP[j]);
+        }
+        // dx_proj for the residual-folded and the branch stream
+        wf32x16_t accr, accb;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            accr[r] = 0.f;
+            accb[r] = 0.f;
+        }
+#pragma unroll
+        for (int m = 0; m < NOH; ++m) {
+            const float a1 = dp_lds[cur][col][NOH * h + m];
+            accr = wmfma32x32x2(a1, bphi_r[m], accr);
+            if constexpr (N > 1) accb = wmfma32x32x2(a1, bphi_b[m], accb);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int t = wdtok(r, h);
+            const float s = s_lds[cur][t];
+            float x[N];
+            wrap_streams<TX, N, DECAY>(VecIO<TX>::scalar(rt + t * EPR + c), VecIO<TX>::scalar(bt + t * EPR + c), x);
+            float sx_r = x[0];
+            if constexpr (N > 2) sx_r += res_weight<2, DECAY>() * x[2];
+            if constexpr (N > 3) sx_r += res_weight<3, DECAY>() * x[3];
+            const float vr = VecIO<TX>::scalar(drt + t * EPR + c) + s * sx_r + accr[r];
+            const float vb = VecIO<TX>::scalar(dbt + t * EPR + c) + (N > 1 ? s * x[N > 1 ? 1 : 0] + accb[r] : 0.f);
+            if (t0 + t < t_end) {
+                VecIO<TX>::put(dres + (t0 + t) * (int64_t)C + cc, vr);
+                VecIO<TX>::put(dbr + (t0 + t) * (int64_t)C + cc, vb);
+            }
+        }
+    };
+
+    if (t_begin < t_end) {
+        fetch(t_begin);
+        commit(t_begin, 0);
+    }
+    __syncthreads();
+    int cur = 0;
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += TB) {
+        const bool has_next = t0 + TB < t_end;
+        if (has_next) fetch(t0 + TB);
+        compute(t0, cur);
+        if (has_next) commit(t0 + TB, cur ^ 1);
+        __syncthreads();
+        cur ^= 1;
+    }
+    if (!wave_on) return;
+    float* out = dphi_part + (int64_t)blockIdx.y * NP * K;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int o = wdtok(r, h);
+            if (o < NP) out[(int64_t)o * K + (int64_t)j * C + cc] = (j < NSTR) ? accP[j < NSTR ? j : 0][r] : 0.f;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+#define MHC_WRAP_PICK_VPT(v, ...)                                \
+    switch (v) {                                                 \
+        case 1: { constexpr int V_ = 1; __VA_ARGS__; break; }    \
+        case 2: { constexpr int V_ = 2; __VA_ARGS__; break; }    \
+        case 4: { constexpr int V_ = 4; __VA_ARGS__; break; }    \
+        case 8: { constexpr int V_ = 8; __VA_ARGS__; break; }    \
+        default: break;                                          \
+    }
+
+// live row arrays per thread: forward r, b (+ prefetch); backward g, r, b
+static constexpr int kWrapFwdArrays = 2;
+static constexpr int kWrapBwdArrays = 3;
+
+template <typename TX, int V, bool PF, bool DECAY>
+static const void* wrap_fwd_fn() {
+    if constexpr (layer_row_fits(kWrapFwdArrays * 2, V)) return reinterpret_cast<const void*>(&wrap_fwd_kernel<TX, 4, V, PF, DECAY>);
+    return nullptr;
+}
+
+template <typename TX, int V, int MODE, bool PF, bool DECAY>
+static const void* wrap_bwd_fn() {
+    if constexpr (layer_row_fits(kWrapBwdArrays * 2, V))
+        return reinterpret_cast<const void*>(&wrap_bwd_kernel<TX, 4, V, MODE, PF, DECAY>);
+    return nullptr;
+}
+
+static int wrap_grid(const void* fn, int threads, int64_t B) {
+    int per_cu = 0;
+    if (fn == nullptr || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess ||
+        per_cu < 1) {
+        (void)hipGetLastError();
+        per_cu = 1;
+    }
+    int64_t g = (int64_t)device_cu_count() * per_cu;
+    if (g > B) g = B;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+static const void* pick_wrap_fwd(int dt, int vpt, bool pf, bool decay) {
+    const void* fn = nullptr;
+#define MHC_WF(TX_) \
+    MHC_WRAP_PICK_VPT(vpt, fn = pf ? (decay ? wrap_fwd_fn<TX_, V_, true, true>() : wrap_fwd_fn<TX_, V_, true, false>()) \
+                                  : (decay ? wrap_fwd_fn<TX_, V_, false, true>() : wrap_fwd_fn<TX_, V_, false, false>()))
+    if (dt == kBF16) {
+        MHC_WF(bf16_t);
+    } else {
+        MHC_WF(float);
+    }
+#undef MHC_WF
+    return fn;
+}
+
+static const void* pick_wrap_bwd(int dt, int vpt, int mode, bool pf, bool decay) {
+    const void* fn = nullptr;
+#define MHC_WB(TX_, M_)                                                                                         \
+    MHC_WRAP_PICK_VPT(vpt, fn = pf ? (decay ? wrap_bwd_fn<TX_, V_, M_, true, true>()                            \
+                                            : wrap_bwd_fn<TX_, V_, M_, true, false>())                          \
+                                   : (decay ? wrap_bwd_fn<TX_, V_, M_, false, true>()                           \
+                                            : wrap_bwd_fn<TX_, V_, M_, false, false>()))
+    if (dt == kBF16) {
+        if (mode == 0) { MHC_WB(bf16_t, 0); } else { MHC_WB(bf16_t, 1); }
+    } else {
+        if (mode == 0) { MHC_WB(float, 0); } else { MHC_WB(float, 1); }
+    }
+#undef MHC_WB
+    return fn;
+}
+
+static bool wrap_prefetch(const RowTiling& t) { return t.threads <= 256; }
+
+hipError_t launch_wrap_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
+                           const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
+                           hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (n != 4) return hipErrorInvalidValue;
+    const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapFwdArrays * 2);
+    if (t.vpt <= 0) return hipErrorInvalidValue;
+    const void* fn = pick_wrap_fwd(dt, t.vpt, wrap_prefetch(t), decay);
+    if (!fn) return hipErrorInvalidValue;
+    const int grid = wrap_grid(fn, t.threads, B);
+    int Ci = (int)C;
+    void* args[] = {(void*)&res, (void*)&br, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&out, (void*)&B,
+                    (void*)&Ci, (void*)&eps};
+    const int tok = timing_begin("wrap_fwd", s);
+    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
+    timing_end(tok, s);
+    return e != hipSuccess ? e : hipGetLastError();
+}
+
+int wrap_bwd_grid(int dt, int n, bool decay, int64_t B, int64_t C) {
+    (void)n;
+    const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapBwdArrays * 2);
+    if (t.vpt <= 0) return 1;
+    return wrap_grid(pick_wrap_bwd(dt, t.vpt, 0, wrap_prefetch(t), decay), t.threads, B);
+}
+
+hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, const void* res, const void* br,
+                           const float* w, const float* coef, int64_t coef_stride, void* dres, void* dbr,
+                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s) {
+    if (n != 4) return hipErrorInvalidValue;
+    const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapBwdArrays * 2);
+    if (t.vpt <= 0) return hipErrorInvalidValue;
+    const void* fn = pick_wrap_bwd(dt, t.vpt, mode, wrap_prefetch(t), decay);
+    if (!fn) return hipErrorInvalidValue;
+    int Ci = (int)C;
+    void* args[] = {(void*)&g, (void*)&res, (void*)&br, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&dres,
+                    (void*)&dbr, (void*)&dw_part, (void*)&scal_out, (void*)&B, (void*)&Ci, (void*)&eps};
+    const int tok = timing_begin(mode == 0 ? "wrap_bwd" : "wrap_bwd_reduce", s);
+    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
+    timing_end(tok, s);
+    return e != hipSuccess ? e : hipGetLastError();
+}
+
+int wrap_proj_csplit(int64_t B, int64_t C) {
+    const int64_t mblocks = (B + 63) / 64;
+    int64_t ks = (2 * (int64_t)device_cu_count() + mblocks - 1) / mblocks;
+    const int64_t kmax = C / 256;
+    if (ks > kmax) ks = kmax;
+    if (ks < 1) ks = 1;
+    return (int)ks;
+}
+
+hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const void* br, const bf16_raw_t* phib,
+                            float* p_part, float* ss_part, int64_t B, int64_t C, int ks, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (n != 4 || C % 32 != 0) return hipErrorInvalidValue;
+    int64_t cchunk = (C + ks - 1) / ks;
+    cchunk = ((cchunk + 127) / 128) * 128;
+    const dim3 grid((unsigned)((B + 63) / 64), (unsigned)ks);
+    const int tok = timing_begin("wrap_proj", s);
+#define MHC_WP(TX_, D_)                                                                                          \
+    hipLaunchKernelGGL((wrap_proj_kernel<TX_, 4, D_>), grid, dim3(256), 0, s, (const TX_*)res, (const TX_*)br,   \
+                       phib, p_part, ss_part, B, (int)C, cchunk)
+    if (dt == kBF16) {
+        if (decay) { MHC_WP(bf16_t, true); } else { MHC_WP(bf16_t, false); }
+    } else {
+        if (decay) { MHC_WP(float, true); } else { MHC_WP(float, false); }
+    }
+#undef MHC_WP
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+int wrap_proj_bwd_tiles(int64_t B, int64_t C) {
+    const int64_t gx = (C + 127) / 128;
+    int64_t tiles = (2 * (int64_t)device_cu_count() + gx - 1) / gx;
+    const int64_t blocks = (B + 31) / 32;
+    if (tiles > blocks) tiles = blocks;
+    if (tiles < 1) tiles = 1;
+    return (int)tiles;
+}
+
+hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
+                                const float* s_tok, const float* phi_pre, const float* phi_post, const float* phi_res,
+                                void* dres, void* dbr, float* dphi_part, int tiles, int64_t B, int64_t C,
+                                hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (n != 4 || C % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
+    int64_t tile = (B + tiles - 1) / tiles;
+    tile = ((tile + 31) / 32) * 32;
+    const dim3 grid((unsigned)((C + 127) / 128), (unsigned)tiles);
+    const int tok = timing_begin("wrap_proj_bwd", s);
+#define MHC_WPB(TX_, D_)                                                                                          \
+    hipLaunchKernelGGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(256), 0, s, (const TX_*)res, (const TX_*)br, \
+                       dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, dphi_part, B, (int)C, tile)
+    if (dt == kBF16) {
+        if (decay) { MHC_WPB(bf16_t, true); } else { MHC_WPB(bf16_t, false); }
+    } else {
+        if (decay) { MHC_WPB(float, true); } else { MHC_WPB(float, false); }
+    }
+#undef MHC_WPB
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+}  // namespace mhc

@@ -109,6 +109,10 @@ class MHCResidualWrapper(nn.Module):
     averaged over streams; [B, T, C] inputs come back as [B, T, C] when
     T > 1 and as [B*T, C] otherwise (layer.py:319-320).  ``use_post_norm``
     is accepted and ignored, as in the reference (layer.py:261).
+
+    All of it runs as one fused pass per direction (ops.mhc_residual_wrapper):
+    the [B*T, n, C] stream tensor of layer.py:299-310 and the layer's
+    [B*T, n, C] output are never materialised.
     """
 
     def __init__(self, hidden_dim: int, expansion_rate: int = 4, residual_mode: str = 'decay',
@@ -131,15 +135,7 @@ class MHCResidualWrapper(nn.Module):
             T = 1
         if self.residual_mode not in ("zero", "decay"):
             raise ValueError(f"Unknown residual_mode: {self.residual_mode}")
-        n = self.expansion_rate
-        streams = [residual, branch_output]
-        for i in range(2, n):
-            if self.residual_mode == "decay":
-                streams.append(residual * (0.1 ** (i - 1)))
-            else:
-                streams.append(torch.zeros_like(residual))
-        mhc_input = torch.stack(streams[:n], dim=1)
-        output = self.mhc(mhc_input).mean(dim=1)
+        output = ops.mhc_residual_wrapper(residual, branch_output, self.mhc, self.residual_mode)
         if T > 1:
             output = output.reshape(B, T, C)
         return output

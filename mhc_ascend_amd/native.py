@@ -475,3 +475,138 @@ def mhc_layer_bwd_dynamic(grad_output, x_expanded, rmsnorm_weight, saved, phi_pr
     return mhc_layer_dynamic_bwd(grad_output, x_expanded, rmsnorm_weight, saved, phi_pre, phi_post, phi_res,
                                  alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
                                  rmsnorm_eps)
+
+
+# =============================================================================
+# Fused MHCResidualWrapper (layer.py:269-322): the n streams are synthesised
+# from (residual, branch) inside the kernels; outputs are the stream mean.
+# =============================================================================
+
+def _wrapper_inputs(fn: str, residual: torch.Tensor, branch: torch.Tensor, residual_mode: str, n: int):
+    _check_device(fn, residual, branch)
+    if residual.shape != branch.shape or residual.dim() != 2:
+        raise RuntimeError(f"{fn}: residual and branch must both be [tokens, hidden] of one shape")
+    if residual_mode not in ("decay", "zero"):
+        raise ValueError(f"Unknown residual_mode: {residual_mode}")
+    if n < 2:
+        # the reference writes stream 1 (layer.py:301), which needs n >= 2
+        raise RuntimeError(f"{fn}: expansion_rate must be >= 2 (stream 1 holds the branch)")
+    r = _storage(residual)
+    b = branch.to(r.dtype).contiguous()
+    mode = _lib.WRAPPER_DECAY if residual_mode == "decay" else _lib.WRAPPER_ZERO
+    return r, b, mode
+
+
+def wrapper_dynamic_fwd(residual: torch.Tensor, branch: torch.Tensor, residual_mode: str, n: int,
+                        rmsnorm_weight: torch.Tensor, phi_pre, phi_post, phi_res, alpha_pre, alpha_post, alpha_res,
+                        b_pre, b_post, b_res, sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
+                        rmsnorm_eps: float = 1e-5) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(mean of the dynamic-H layer's n output streams, fp32 [tokens, C]; saved)."""
+    r, b, mode = _wrapper_inputs("wrapper_dynamic_fwd", residual, branch, residual_mode, n)
+    _check_device("wrapper_dynamic_fwd", r, rmsnorm_weight, phi_pre, phi_post, phi_res, b_pre, b_post, b_res)
+    T, C = r.shape
+    dev = r.device
+    w = _weight(rmsnorm_weight)
+    if w.numel() != C:
+        raise RuntimeError("wrapper_dynamic_fwd: rmsnorm_weight must have C elements")
+    pp, pq, pr = _phi_parts(phi_pre, phi_post, phi_res, n, n * C)
+    a = [_scalar_param(v, dev) for v in (alpha_pre, alpha_post, alpha_res)]
+    bp, bq, br = _f32c(b_pre), _f32c(b_post), _f32c(b_res)
+    out = torch.empty((T, C), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    saved = torch.empty((lib.mhc_wrapper_dynamic_saved_size(T, n, C) // 4,), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        wsb = lib.mhc_wrapper_dynamic_fwd_workspace_size(T, n, C)
+        ws = _ws(dev, wsb)
+        call("mhc_wrapper_dynamic_fwd", ptr(r), ptr(b), dtype_code(r.dtype), mode, ptr(w), dtype_code(w.dtype),
+             ptr(pp), ptr(pq), ptr(pr), ptr(a[0]), ptr(a[1]), ptr(a[2]), ptr(bp), ptr(bq), ptr(br), ptr(out),
+             ptr(saved), ptr(ws), int(wsb), T, n, C, int(sinkhorn_iters), float(sinkhorn_eps), float(rmsnorm_eps),
+             stream_of(r))
+    return out, saved
+
+
+def wrapper_dynamic_bwd(grad_out: torch.Tensor, residual: torch.Tensor, branch: torch.Tensor, residual_mode: str,
+                        n: int, rmsnorm_weight: torch.Tensor, saved: torch.Tensor, phi_pre, phi_post, phi_res,
+                        alpha_pre, alpha_post, alpha_res, b_res, sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
+                        rmsnorm_eps: float = 1e-5):
+    """(grad_residual, grad_branch, grad_rmsnorm_weight, d_phi_pre, d_phi_post,
+    d_phi_res, d_alpha_pre, d_alpha_post, d_alpha_res, d_b_pre, d_b_post, d_b_res)."""
+    r, b, mode = _wrapper_inputs("wrapper_dynamic_bwd", residual, branch, residual_mode, n)
+    _check_device("wrapper_dynamic_bwd", grad_out, r, rmsnorm_weight, saved, phi_pre, phi_post, phi_res, b_res)
+    T, C = r.shape
+    dev = r.device
+    if grad_out.shape != r.shape:
+        raise RuntimeError("wrapper_dynamic_bwd: grad_out must be [tokens, hidden]")
+    g = _f32c(grad_out)
+    wdt = rmsnorm_weight.dtype if rmsnorm_weight.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    pp, pq, pr = _phi_parts(phi_pre, phi_post, phi_res, n, n * C)
+    a = [_scalar_param(v, dev) for v in (alpha_pre, alpha_post, alpha_res)]
+    br = _f32c(b_res)
+    np_ = 2 * n + n * n
+    gr = torch.empty_like(r)
+    gb = torch.empty_like(b)
+    gw = torch.empty((C,), dtype=wdt, device=dev)
+    gphi = torch.empty((np_, n * C), dtype=torch.float32, device=dev)
+    galpha = torch.empty((3,), dtype=torch.float32, device=dev)
+    gbias = torch.empty((np_,), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        wsb = _lib.load().mhc_wrapper_dynamic_bwd_workspace_size(T, n, C, dtype_code(r.dtype), mode)
+        ws = _ws(dev, wsb)
+        call("mhc_wrapper_dynamic_bwd", ptr(g), ptr(r), ptr(b), dtype_code(r.dtype), mode, dtype_code(wdt), ptr(pp),
+             ptr(pq), ptr(pr), ptr(a[0]), ptr(a[1]), ptr(a[2]), ptr(br), ptr(saved), ptr(gr), ptr(gb), ptr(gw),
+             ptr(gphi), ptr(galpha), ptr(gbias), ptr(ws), int(wsb), T, n, C, int(sinkhorn_iters),
+             float(sinkhorn_eps), float(rmsnorm_eps), stream_of(r))
+    return (gr, gb, gw, gphi[:n], gphi[n:2 * n], gphi[2 * n:], galpha[0], galpha[1], galpha[2], gbias[:n],
+            gbias[n:2 * n], gbias[2 * n:].view(n, n))
+
+
+def wrapper_static_fwd(residual: torch.Tensor, branch: torch.Tensor, residual_mode: str, n: int,
+                       rmsnorm_weight: torch.Tensor, H_pre: torch.Tensor, H_post: torch.Tensor, H_res: torch.Tensor,
+                       sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
+                       rmsnorm_eps: float = 1e-5) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(mean of the static-H layer's n output streams, fp32 [tokens, C]; saved)."""
+    r, b, mode = _wrapper_inputs("wrapper_static_fwd", residual, branch, residual_mode, n)
+    _check_device("wrapper_static_fwd", r, rmsnorm_weight, H_pre, H_post, H_res)
+    T, C = r.shape
+    dev = r.device
+    w = _weight(rmsnorm_weight)
+    if w.numel() != C or H_pre.numel() != n or H_post.numel() != n or H_res.numel() != n * n:
+        raise RuntimeError("wrapper_static_fwd: parameter shapes do not match n and C")
+    hp, hq, hr = _f32c(H_pre), _f32c(H_post), _f32c(H_res)
+    out = torch.empty((T, C), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    saved = torch.empty((lib.mhc_layer_static_saved_size(n, C) // 4,), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        call("mhc_wrapper_static_fwd", ptr(r), ptr(b), dtype_code(r.dtype), mode, ptr(w), dtype_code(w.dtype), ptr(hp),
+             ptr(hq), ptr(hr), ptr(out), ptr(saved), T, n, C, int(sinkhorn_iters), float(sinkhorn_eps),
+             float(rmsnorm_eps), stream_of(r))
+    return out, saved
+
+
+def wrapper_static_bwd(grad_out: torch.Tensor, residual: torch.Tensor, branch: torch.Tensor, residual_mode: str,
+                       n: int, rmsnorm_weight: torch.Tensor, H_pre: torch.Tensor, H_post: torch.Tensor,
+                       H_res: torch.Tensor, saved: torch.Tensor, sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
+                       rmsnorm_eps: float = 1e-5):
+    """(grad_residual, grad_branch, grad_rmsnorm_weight, grad_H_pre, grad_H_post, grad_H_res)."""
+    r, b, mode = _wrapper_inputs("wrapper_static_bwd", residual, branch, residual_mode, n)
+    _check_device("wrapper_static_bwd", grad_out, r, rmsnorm_weight, H_pre, H_post, H_res, saved)
+    T, C = r.shape
+    dev = r.device
+    if grad_out.shape != r.shape:
+        raise RuntimeError("wrapper_static_bwd: grad_out must be [tokens, hidden]")
+    g = _f32c(grad_out)
+    wdt = rmsnorm_weight.dtype if rmsnorm_weight.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    hp, hq, hr = _f32c(H_pre), _f32c(H_post), _f32c(H_res)
+    gr = torch.empty_like(r)
+    gb = torch.empty_like(b)
+    gw = torch.empty((C,), dtype=wdt, device=dev)
+    ghp = torch.empty((n,), dtype=torch.float32, device=dev)
+    ghq = torch.empty((n,), dtype=torch.float32, device=dev)
+    ghr = torch.empty((n, n), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        wsb = _lib.load().mhc_wrapper_static_bwd_workspace_size(T, n, C, dtype_code(r.dtype), mode)
+        ws = _ws(dev, wsb)
+        call("mhc_wrapper_static_bwd", ptr(g), ptr(r), ptr(b), dtype_code(r.dtype), mode, dtype_code(wdt), ptr(hp),
+             ptr(hq), ptr(hr), ptr(saved), ptr(gr), ptr(gb), ptr(gw), ptr(ghp), ptr(ghq), ptr(ghr), ptr(ws), int(wsb),
+             T, n, C, int(sinkhorn_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(r))
+    return gr, gb, gw, ghp, ghq, ghr

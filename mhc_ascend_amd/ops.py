@@ -244,3 +244,70 @@ def mhc_layer_fused_dynamic_training(x_expanded, rmsnorm_weight, phi_pre, phi_po
     return MHCLayerDynamicFunction.apply(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
                                          alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
                                          rmsnorm_eps)
+
+
+# =============================================================================
+# Fused MHCResidualWrapper (layer.py:269-322)
+# =============================================================================
+
+class MHCWrapperDynamicFunction(torch.autograd.Function):
+    """Stream synthesis -> dynamic-H layer -> stream mean, fused: the
+    [tokens, n, C] stream tensor and the layer output are never materialised."""
+
+    @staticmethod
+    def forward(ctx, residual, branch, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post, alpha_res,
+                b_pre, b_post, b_res, residual_mode: str, n: int, sinkhorn_iters: int, sinkhorn_eps: float,
+                rmsnorm_eps: float):
+        out, saved = native.wrapper_dynamic_fwd(residual, branch, residual_mode, n, rmsnorm_weight, phi_pre, phi_post,
+                                                phi_res, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
+                                                sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
+        ctx.save_for_backward(residual, branch, rmsnorm_weight, saved, phi_pre, phi_post, phi_res, alpha_pre,
+                              alpha_post, alpha_res, b_pre, b_post, b_res)
+        ctx.cfg = (residual_mode, n, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        r, b, w, saved, pp, pq, pr, ap, aq, ar, bp, bq, br = ctx.saved_tensors
+        mode, n, iters, sk_eps, rms_eps = ctx.cfg
+        gr, gb, gw, gpp, gpq, gpr, gap, gaq, gar, gbp, gbq, gbr = native.wrapper_dynamic_bwd(
+            grad_out, r, b, mode, n, w, saved, pp, pq, pr, ap, aq, ar, br, iters, sk_eps, rms_eps)
+        return (gr.to(r.dtype), gb.to(b.dtype), gw, gpp.view_as(pp), gpq.view_as(pq), gpr.view_as(pr),
+                gap.view_as(ap), gaq.view_as(aq), gar.view_as(ar), gbp.view_as(bp), gbq.view_as(bq),
+                gbr.view_as(br), None, None, None, None, None)
+
+
+class MHCWrapperStaticFunction(torch.autograd.Function):
+    """Stream synthesis -> static-H layer -> stream mean, fused."""
+
+    @staticmethod
+    def forward(ctx, residual, branch, rmsnorm_weight, H_pre, H_post, H_res, residual_mode: str, n: int,
+                sinkhorn_iters: int, sinkhorn_eps: float, rmsnorm_eps: float):
+        out, saved = native.wrapper_static_fwd(residual, branch, residual_mode, n, rmsnorm_weight, H_pre, H_post,
+                                               H_res, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
+        ctx.save_for_backward(residual, branch, rmsnorm_weight, H_pre, H_post, H_res, saved)
+        ctx.cfg = (residual_mode, n, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        r, b, w, hp, hq, hr, saved = ctx.saved_tensors
+        mode, n, iters, sk_eps, rms_eps = ctx.cfg
+        gr, gb, gw, ghp, ghq, ghr = native.wrapper_static_bwd(grad_out, r, b, mode, n, w, hp, hq, hr, saved, iters,
+                                                              sk_eps, rms_eps)
+        return (gr.to(r.dtype), gb.to(b.dtype), gw, ghp.view_as(hp), ghq.view_as(hq), ghr.view_as(hr), None, None,
+                None, None, None)
+
+
+def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, layer, residual_mode: str = "decay"):
+    """Fused MHCResidualWrapper on residual / branch_output [tokens, C] for the
+    parameters of ``layer`` (an MHCLayer); returns fp32 [tokens, C]."""
+    n = layer.expansion_rate
+    args = (layer.num_sinkhorn_iters, layer.sinkhorn_eps, layer.rmsnorm_eps)
+    if layer.use_dynamic_h:
+        return MHCWrapperDynamicFunction.apply(residual, branch_output, layer.rmsnorm_weight, layer.phi_pre,
+                                               layer.phi_post, layer.phi_res, layer.alpha_pre, layer.alpha_post,
+                                               layer.alpha_res, layer.b_pre, layer.b_post, layer.b_res,
+                                               residual_mode, n, *args)
+    return MHCWrapperStaticFunction.apply(residual, branch_output, layer.rmsnorm_weight, layer.H_pre, layer.H_post,
+                                          layer.H_res, residual_mode, n, *args)

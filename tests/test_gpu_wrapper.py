@@ -1,0 +1,161 @@
+"""GPU parity of the fused MHCResidualWrapper (layer.py:225-329) against the
+float64 CPU oracle: stream synthesis ('decay' with the storage-dtype rounding
+of residual*0.1**(i-1), and 'zero'), the layer (dynamic and static H), the
+stream mean and the [B, T, C] reshape; forward and every gradient.
+
+Tolerances: fp32 outputs rtol 1e-4; gradients rtol 1e-3 (fp32 storage) or
+2e-2 (bf16 storage) with absolute floors relative to max|ref|.  Config C5 runs
+at its width C=7168 on a reduced token count (the full-size oracle needs
+~200 GB)."""
+import pytest
+import torch
+
+import mhc_ascend_amd as mhc
+from oracle import reference as R
+from tests.conftest import assert_close, grad_atol
+
+pytestmark = pytest.mark.gpu
+
+DYN = ["phi_pre", "phi_post", "phi_res", "alpha_pre", "alpha_post", "alpha_res", "b_pre", "b_post", "b_res"]
+STA = ["H_pre", "H_post", "H_res"]
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _make(C, dynamic, seed, alpha=0.3, phi_std=0.05):
+    torch.manual_seed(seed)
+    wrap = mhc.MHCResidualWrapper(C, 4, use_dynamic_h=dynamic)
+    layer = wrap.mhc
+    g = _gen(seed + 1)
+    with torch.no_grad():
+        layer.rmsnorm_weight.copy_((1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16))
+        if dynamic:
+            for k in ("phi_pre", "phi_post", "phi_res"):
+                getattr(layer, k).copy_(phi_std * torch.randn(getattr(layer, k).shape, generator=g))
+            for k in ("alpha_pre", "alpha_post", "alpha_res"):
+                getattr(layer, k).fill_(alpha)
+            for k in ("b_pre", "b_post", "b_res"):
+                getattr(layer, k).copy_(0.3 * torch.randn(getattr(layer, k).shape, generator=g))
+        else:
+            for k in STA:
+                getattr(layer, k).copy_(torch.randn(getattr(layer, k).shape, generator=g))
+    return wrap
+
+
+def _oracle(wrap, res, br, grad, mode):
+    """float64 oracle: streams synthesised in the storage dtype, layer in f64."""
+    layer = wrap.mhc
+    names = DYN if layer.use_dynamic_h else STA
+    w = layer.rmsnorm_weight.detach().cpu().double().requires_grad_(True)
+    ps = [getattr(layer, k).detach().cpu().double().requires_grad_(True) for k in names]
+    r = res.detach().cpu().clone().requires_grad_(True)
+    b = br.detach().cpu().clone().requires_grad_(True)
+    if layer.use_dynamic_h:
+        fn = lambda X: R.mhc_layer_dynamic(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
+    else:
+        fn = lambda X: R.mhc_layer_static(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
+    out = R.mhc_residual_wrapper(r, b, fn, 4, mode)
+    out.backward(grad.double())
+    return out.detach(), r.grad, b.grad, w.grad, [p.grad for p in ps]
+
+
+def _run(wrap, res, br, grad, device):
+    wrap = wrap.to(device)
+    r = res.to(device).requires_grad_(True)
+    b = br.to(device).requires_grad_(True)
+    out = wrap(r, b)
+    out.backward(grad.to(device))
+    layer = wrap.mhc
+    names = DYN if layer.use_dynamic_h else STA
+    return out.detach(), r.grad, b.grad, layer.rmsnorm_weight.grad, [getattr(layer, k).grad for k in names]
+
+
+def _check(got, want, dtype, names, tag):
+    out, gr, gb, gw, gp = got
+    rout, rgr, rgb, rgw, rgp = want
+    assert out.dtype == torch.float32 and tuple(out.shape) == tuple(rout.shape), (out.dtype, out.shape, rout.shape)
+    assert_close(out, rout, 1e-4, grad_atol(rout, 1e-5), f"{tag} out")
+    bf = dtype == torch.bfloat16
+    assert gr.dtype == dtype and gb.dtype == dtype
+    rt, fr = (2e-2, 1e-2) if bf else (1e-3, 1e-5)
+    # the bf16 oracle's leaf grads are rounded to bf16 by autograd too
+    assert_close(gr.float(), rgr.double(), rt, grad_atol(rgr.double(), fr), f"{tag} d residual")
+    assert_close(gb.float(), rgb.double(), rt, grad_atol(rgb.double(), fr), f"{tag} d branch")
+    assert_close(gw.float(), rgw, 8e-3, grad_atol(rgw, 1e-3), f"{tag} d_weight (bf16 param)")
+    # Through the stream mean every stream gets the same cotangent G / n, so
+    # dM is constant along i and the Sinkhorn adjoint's last column step
+    # cancels it: the H_res-side gradients are 0 up to eps-terms (~1e-20
+    # relative) and fp32 rounding.  Their absolute floor therefore comes from
+    # the non-vanishing members of the same family.
+    fam = {}
+    for nm, e in zip(names, rgp):
+        key = nm.split("_")[0]
+        fam[key] = max(fam.get(key, 0.0), float(e.abs().max()))
+    for nm, a, e in zip(names, gp, rgp):
+        floor = max(grad_atol(e, 1e-4), 1e-5 * fam[nm.split("_")[0]])
+        assert_close(a, e, 1e-3, floor, f"{tag} d_{nm}")
+        if nm.endswith("res"):
+            assert float(a.abs().max()) <= 1e-5 * fam[nm.split("_")[0]], f"{tag} d_{nm} should vanish"
+
+
+@pytest.mark.parametrize("dynamic", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["decay", "zero"])
+@pytest.mark.parametrize("shape", [(3, 5, 256), (37, 1024)])
+def test_wrapper_matches_oracle(device, dynamic, dtype, mode, shape):
+    C = shape[-1]
+    seed = len(shape) * 100 + C + (7 if dynamic else 0) + (3 if mode == "zero" else 0)
+    wrap = _make(C, dynamic, seed)
+    wrap.residual_mode = mode
+    g = _gen(seed + 2)
+    res = torch.randn(*shape, generator=g).to(dtype)
+    br = torch.randn(*shape, generator=g).to(dtype)
+    grad = torch.randn(*shape, generator=g)
+    want = _oracle(wrap, res, br, grad, mode)
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, dtype, DYN if dynamic else STA, f"dyn={dynamic} {dtype} {mode} {shape}")
+
+
+@pytest.mark.parametrize("dynamic", [True, False])
+def test_wrapper_config_c5_width(device, dynamic):
+    """Config C5 at its width: residual/branch bf16 [B=16, T=4, 7168], phi
+    ~ N(0, 0.02), alpha 0.01, b 0 (the layer defaults of layer.py:69-79)."""
+    C = 7168
+    torch.manual_seed(5)
+    wrap = mhc.MHCResidualWrapper(C, 4, use_dynamic_h=dynamic)
+    g = _gen(55)
+    res = torch.randn(16, 4, C, generator=g).to(torch.bfloat16)
+    br = torch.randn(16, 4, C, generator=g).to(torch.bfloat16)
+    grad = torch.randn(16, 4, C, generator=g)
+    want = _oracle(wrap, res, br, grad, "decay")
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, torch.bfloat16, DYN if dynamic else STA, f"C5 width dyn={dynamic}")
+
+
+def test_wrapper_single_token_rows_stay_flat(device):
+    """[B, 1, C] comes back as [B, C] (layer.py:319-320)."""
+    wrap = _make(128, True, 9).to(device)
+    res = torch.randn(6, 1, 128, generator=_gen(10)).to(device)
+    br = torch.randn(6, 1, 128, generator=_gen(11)).to(device)
+    assert tuple(wrap(res, br).shape) == (6, 128)
+
+
+def test_wrapper_rejects_unknown_mode(device):
+    wrap = _make(64, True, 12).to(device)
+    wrap.residual_mode = "bogus"
+    x = torch.randn(4, 64, device=device)
+    with pytest.raises(ValueError, match="Unknown residual_mode"):
+        wrap(x, x)
+
+
+def test_wrapper_eval_no_grad_matches_training_forward(device):
+    wrap = _make(256, True, 13).to(device)
+    res = torch.randn(20, 256, generator=_gen(14)).to(device)
+    br = torch.randn(20, 256, generator=_gen(15)).to(device)
+    out_t = wrap(res, br).detach()
+    wrap.eval()
+    with torch.no_grad():
+        out_e = wrap(res, br)
+    assert torch.equal(out_t, out_e)
