@@ -15,7 +15,7 @@
 //                       MFMA 16x16x32 on the planes gives fp32 accuracy
 //   dyn_coef_fwd_kernel per token: sum partials, t, sigmoid, Sinkhorn
 //   dyn_coef_bwd_kernel per token: Sinkhorn adjoint, dP, d r_h, db/dalpha
-//   proj_bwd_mfma_kernel dx += dP.Phi + s x_flat (fp32 MFMA); dPhi partials
+//   proj_bwd_mfma_kernel dx += dP.Phi + s x_flat, dPhi partials (bf16 MFMA, split operands)
 #include "mhc_device.h"
 #include "mhc_internal.h"
 #include "mhc_rows.h"
@@ -35,9 +35,7 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c)
                                                    c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-}
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) { return pack_bf16x2(lo, hi); }
 
 
 // ---------------------------------------------------------------------------
@@ -411,55 +409,71 @@ __global__ __launch_bounds__(256) void small_column_sum_kernel(const float* __re
 }
 
 // ---------------------------------------------------------------------------
-// Projection backward on the fp32 matrix cores (v_mfma_f32_32x32x2_f32), over
-// the flattened rows x[b][k] (k = j*C + c for the layer):
+// Projection backward on the bf16 matrix cores, over the flattened rows
+// x[b][k] (k = j*C + c for the layer):
 //   dx[b][k] = dx_in[b][k] + s[b] x[b][k] + sum_o dP[b][o] Phi[o][k]
 //   dPhi_part[tile][o][k] = sum_{b in tile} dP[b][o] x[b][k]
 // In the layer backward dx_in is the stream part already written by the row
 // kernel (bindings.cpp:834-848 adds the same two terms to grad_x_flat).
-// Workgroup = 4 waves x 32 columns each, looping over a tile of tokens in
-// blocks of 32.  Per block a wave runs two MFMA chains:
-//   dx_proj (32 tokens x 32 columns) reducing over o (NOH per lane half);
-//   dPhi    (32 o x 32 columns) reducing over the block's 32 tokens.
-// MFMA 32x32x2 f32 operand layout: A: lane l holds A[l % 32][l / 32];
-// B: lane l holds B[l / 32][l % 32]; D: register r of lane l holds
-// D[dtok(r, l / 32)][l % 32].  The dPhi chain takes its B operand (x) from
-// the same registers the dx epilogue reads, by pairing reduction index h of
-// instruction r with token dtok(r, h).
+//
+// fp32 operands are split into bf16 hi + lo (v = hi + lo to 2^-16 relative);
+// products keep hi.hi + hi.lo + lo.hi, so both products carry ~2^-16
+// relative error per term (bf16 x is exact and needs no lo part).
+// MFMA 16x16x32 bf16 layout: A row = lane % 16, B column = lane % 16, the
+// lane's 8 reduction indices are 8 (lane / 16) .. + 7; D register i of lane l
+// is D[4 (l / 16) + i][l % 16].
+//   dx_proj^T (16 columns x 16 tokens): A = Phi^T, B = dP^T, reducing over o
+//     (padded to 32: one step); lane l then holds token l % 16 at four
+//     consecutive columns, so its epilogue is 8-byte LDS accesses;
+//   dPhi (16 o x 16 columns): A = dP^T, B = x over the stage's 32 tokens.
+// Each stage's dP is split into hi/lo bf16 once, when it is written to LDS,
+// in token-major and o-major copies, so both operands are single 16-byte
+// reads.  Workgroup = 4 waves x 32 columns; stages of 32 tokens; x and dx_in
+// tiles arrive with coalesced 16-byte loads (two stages in flight), results
+// return to the dx tile in LDS and leave with coalesced 16-byte stores.
 // ---------------------------------------------------------------------------
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ f32x16_t mfma32x32x2(float a, float b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ void split_pack8(const float (&v)[8], u32x4_t& hi, u32x4_t& lo) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float h0 = bf16_to_f32(f32_to_bf16(v[2 * e]));
+        const float h1 = bf16_to_f32(f32_to_bf16(v[2 * e + 1]));
+        hi[e] = pack_bf16(h0, h1);
+        lo[e] = pack_bf16(v[2 * e] - h0, v[2 * e + 1] - h1);
+    }
 }
 
-// Row of a 32-row MFMA tile held in D register r by lane half h.
-__device__ __forceinline__ int dtok(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+// Four consecutive elements at an 8-byte aligned LDS address (8-byte accesses only).
+template <typename TX>
+__device__ __forceinline__ void lds_get4(const char* p, float (&v)[4]) {
+    const uint2* q = reinterpret_cast<const uint2*>(p);
+    if constexpr (sizeof(TX) == 2) {
+        const uint2 w = q[0];
+        v[0] = __uint_as_float(w.x << 16); v[1] = __uint_as_float(w.x & 0xffff0000u);
+        v[2] = __uint_as_float(w.y << 16); v[3] = __uint_as_float(w.y & 0xffff0000u);
+    } else {
+        const uint2 a = q[0], b = q[1];
+        v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+        v[2] = __uint_as_float(b.x); v[3] = __uint_as_float(b.y);
+    }
+}
+template <typename TX>
+__device__ __forceinline__ void lds_put4(char* p, const float (&v)[4]) {
+    uint2* q = reinterpret_cast<uint2*>(p);
+    if constexpr (sizeof(TX) == 2) {
+        q[0] = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+    } else {
+        q[0] = make_uint2(__float_as_uint(v[0]), __float_as_uint(v[1]));
+        q[1] = make_uint2(__float_as_uint(v[2]), __float_as_uint(v[3]));
+    }
+}
 
-// Raw element load (no conversion) and its conversion to fp32, kept apart so
-// that every load of a block is issued before the first conversion waits.
-template <typename T> struct RawElem;
-template <> struct RawElem<float> {
-    typedef uint32_t type;
-    __device__ __forceinline__ static type load(const float* p) { return __float_as_uint(*p); }
-    __device__ __forceinline__ static float f32(type v) { return __uint_as_float(v); }
-};
-template <> struct RawElem<bf16_t> {
-    typedef uint32_t type;
-    __device__ __forceinline__ static type load(const bf16_t* p) { return *p; }
-    __device__ __forceinline__ static float f32(type v) { return __uint_as_float(v << 16); }
-};
+// LDS row pitch of a 128-column stage tile (8-byte aligned rows; 8 extra
+// bytes spread the token rows read by the four lane groups over the banks).
+template <typename TX> constexpr int pb_pitch() { return 128 * (int)sizeof(TX) + 8; }
+constexpr int kDpPitch = 40;  // bf16 per row of the split dP copies (32 + 8 pad)
 
-// Workgroup = 4 waves over 128 columns (32 each) and a tile of tokens, in
-// stages of 32 tokens.  Each stage's x (and dx_in) tile, dP rows and s values
-// are fetched with coalesced 16-byte loads into registers while the previous
-// stage is computed out of LDS, then written to the other LDS buffer
-// (two-stage pipeline, one barrier per stage).  Rows past the tile end and
-// columns past K are stored as zeros and never written back.
-// ACC: add the existing dx (the stream part of the layer backward); HAS_S:
-// add s[b] x.
-template <typename TX, int NOH, bool ACC, bool HAS_S>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void proj_bwd_mfma_kernel(
+template <typename TX, bool ACC, bool HAS_S>
+__global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     const TX* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
     const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
     int n_pre, int np, TX* __restrict__ dx, float* __restrict__ dphi_part, int64_t B, int64_t K, int64_t tile) {
@@ -469,52 +483,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     constexpr int VPR = CB / EPV;               // vectors per tile row
     constexpr int RPP = 256 / VPR;              // tile rows per load pass
     constexpr int PASSES = TB / RPP;
-    constexpr int PITCH = CB * sizeof(TX) + 16;  // bytes per LDS tile row (16-byte pad: no bank aliasing
-                                                 // between the two lane halves, rows 4 apart)
-    constexpr int NARR = ACC ? 2 : 1;
-    __shared__ __align__(16) char tiles_lds[2][NARR][TB * PITCH];
-    __shared__ float dp_lds[2][TB][33];  // rows padded: the dx_proj operand reads a column
+    constexpr int PITCH = pb_pitch<TX>();
+    __shared__ __align__(16) char tiles_lds[2][2][TB * PITCH];       // [buf][x | dx]
+    __shared__ __align__(16) bf16_t dps_lds[2][4][32 * kDpPitch];    // [buf][hi_row, lo_row, hi_col, lo_col]
     __shared__ float s_lds[2][TB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int h = lane >> 5;
-    const int col = lane & 31;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
     const int64_t kb0 = (int64_t)blockIdx.x * CB;
-    const int64_t kc = kb0 + wave * 32 + col;
-    const bool wave_on = kb0 + wave * 32 < K;  // K % 32 == 0: whole waves are in or out
+    const int wc0 = wave * 32;
+    const bool wave_on = kb0 + wc0 < K;  // K % 32 == 0: whole waves are in or out
 
-    // loader role: pass p covers tile row lrow + p * RPP, 16-byte vector lvec
     const int lrow = tid / VPR;
     const int lvec = tid % VPR;
     const int64_t lcol = kb0 + (int64_t)lvec * EPV;
     const bool lcol_ok = lcol < K;
-    const int dtk = tid >> 3;        // dP loader: token tid / 8, o = 4 (tid % 8) + q
+    const int dtk = tid >> 3;
     const int dpo = (tid & 7) * 4;
 
-    float bphi[NOH];
+    // dx_proj A operands (Phi^T): Phi[8 lg + e][column 16 ct + lr]
+    u32x4_t phh[2], phl[2];
 #pragma unroll
-    for (int m = 0; m < NOH; ++m) {
-        const int o = NOH * h + m;
-        bphi[m] = (wave_on && o < np) ? phi_row(phi_pre, phi_post, phi_res, n_pre, o, K)[kc] : 0.f;
+    for (int ct = 0; ct < 2; ++ct) {
+        const int64_t k = kb0 + wc0 + 16 * ct + lr;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int o = 8 * lg + e;
+            v[e] = (wave_on && o < np) ? phi_row(phi_pre, phi_post, phi_res, n_pre, o, K)[k] : 0.f;
+        }
+        split_pack8(v, phh[ct], phl[ct]);
     }
-    f32x16_t accP;
+    f32x4_t accP[2][2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) accP[r] = 0.f;
+    for (int ot = 0; ot < 2; ++ot) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) accP[ot][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
     const int64_t t_begin = (int64_t)blockIdx.y * tile;
     const int64_t t_end = (t_begin + tile < B) ? t_begin + tile : B;
 
-    // Two register sets of fetched stages: stage i+2 is being fetched while
-    // stage i is computed and stage i+1 (fetched one stage earlier) is moved
-    // into LDS, so every load has a whole stage of compute to arrive in.
+    // Two register sets of fetched stages: stage i+2 is fetched while stage i
+    // computes and stage i+1 (fetched one stage earlier) moves into LDS.
     struct Fetched {
         uint4 x[PASSES], d[PASSES];
         float dp[4], s;
     };
     Fetched f0, f1;
-    auto fetch = [&](Fetched& f, int64_t t0) __attribute__((always_inline)) {  // issue the global loads of stage t0 (t0 < t_end)
+    auto fetch = [&](Fetched& f, int64_t t0) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int64_t t = t0 + lrow + p * RPP;
@@ -531,55 +551,119 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             if (tid < TB) f.s = s_tok[(t0 + tid < t_end) ? t0 + tid : t0];
         }
     };
-    auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {  // fetched stage -> LDS buffer, masked
+    auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
             const uint32_t m = (lcol_ok && t0 + row < t_end) ? 0xffffffffu : 0u;  // zero masked rows
             const uint4 vx = f.x[p];
-            *reinterpret_cast<uint4*>(&tiles_lds[buf][0][row * PITCH + lvec * 16]) =
-                make_uint4(vx.x & m, vx.y & m, vx.z & m, vx.w & m);
+            uint2* px = reinterpret_cast<uint2*>(&tiles_lds[buf][0][row * PITCH + lvec * 16]);
+            px[0] = make_uint2(vx.x & m, vx.y & m);
+            px[1] = make_uint2(vx.z & m, vx.w & m);
             if constexpr (ACC) {
                 const uint4 vd = f.d[p];
-                *reinterpret_cast<uint4*>(&tiles_lds[buf][1][row * PITCH + lvec * 16]) =
-                    make_uint4(vd.x & m, vd.y & m, vd.z & m, vd.w & m);
+                uint2* pd = reinterpret_cast<uint2*>(&tiles_lds[buf][1][row * PITCH + lvec * 16]);
+                pd[0] = make_uint2(vd.x & m, vd.y & m);
+                pd[1] = make_uint2(vd.z & m, vd.w & m);
             }
         }
+        // dP of token dtk, o = dpo .. dpo + 3: split once into hi / lo bf16,
+        // token-major (one 8-byte write each) and o-major copies
         const bool tok_ok = t0 + dtk < t_end;
+        float hi[4], lo[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dp_lds[buf][dtk][dpo + q] = (tok_ok && dpo + q < np) ? f.dp[q] : 0.f;
+        for (int q = 0; q < 4; ++q) {
+            const float v = (tok_ok && dpo + q < np) ? f.dp[q] : 0.f;
+            hi[q] = bf16_to_f32(f32_to_bf16(v));
+            lo[q] = v - hi[q];
+        }
+        *reinterpret_cast<uint2*>(&dps_lds[buf][0][dtk * kDpPitch + dpo]) =
+            make_uint2(pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
+        *reinterpret_cast<uint2*>(&dps_lds[buf][1][dtk * kDpPitch + dpo]) =
+            make_uint2(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            dps_lds[buf][2][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(hi[q]);
+            dps_lds[buf][3][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(lo[q]);
+        }
         if constexpr (HAS_S) {
             if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? f.s : 0.f;
         }
     };
-    auto compute = [&](int64_t t0, int cur) __attribute__((always_inline)) {
+    auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> u32x4_t {
+        const uint4 q = *reinterpret_cast<const uint4*>(p);
+        return u32x4_t{q.x, q.y, q.z, q.w};
+    };
+    auto compute = [&](int cur) __attribute__((always_inline)) {
         if (!wave_on) return;
-        const TX* xt = reinterpret_cast<const TX*>(tiles_lds[cur][0]);
-        const TX* dt = reinterpret_cast<const TX*>(tiles_lds[cur][ACC ? 1 : 0]);
-        constexpr int EPR = PITCH / sizeof(TX);  // elements per LDS row
-        const int c = wave * 32 + col;
-        float a1[NOH];
+        const char* xt = tiles_lds[cur][0];
+        char* dt = tiles_lds[cur][1];
+        // dPhi: A = dP^T (o = 16 ot + lr, tokens 8 lg .. + 7), B = x (same tokens, column 16 ct + lr)
+        u32x4_t xh[2], xl[2];
 #pragma unroll
-        for (int m = 0; m < NOH; ++m) a1[m] = dp_lds[cur][col][NOH * h + m];
-        f32x16_t acc;
+        for (int ct = 0; ct < 2; ++ct) {
+            const int c = wc0 + 16 * ct + lr;
+            float v[8];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+            for (int e = 0; e < 8; ++e) v[e] = VecIO<TX>::scalar(reinterpret_cast<const TX*>(xt + (8 * lg + e) * PITCH) + c);
+            if constexpr (sizeof(TX) == 2) {
 #pragma unroll
-        for (int m = 0; m < NOH; ++m) acc = mfma32x32x2(a1[m], bphi[m], acc);
-        float xv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = dtok(r, h);
-            xv[r] = VecIO<TX>::scalar(xt + t * EPR + c);
-            accP = mfma32x32x2(dp_lds[cur][t][col], xv[r], accP);
+                for (int e = 0; e < 4; ++e) xh[ct][e] = pack_bf16(v[2 * e], v[2 * e + 1]);  // exact
+            } else {
+                split_pack8(v, xh[ct], xl[ct]);
+            }
         }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = dtok(r, h);
-            float v = acc[r];
-            if constexpr (ACC) v += VecIO<TX>::scalar(dt + t * EPR + c);
-            if constexpr (HAS_S) v += s_lds[cur][t] * xv[r];
-            if (t0 + t < t_end) VecIO<TX>::put(dx + (t0 + t) * K + kc, v);
+        for (int ot = 0; ot < 2; ++ot) {
+            const u32x4_t ah = read16(&dps_lds[cur][2][(16 * ot + lr) * kDpPitch + 8 * lg]);
+            const u32x4_t al = read16(&dps_lds[cur][3][(16 * ot + lr) * kDpPitch + 8 * lg]);
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                accP[ot][ct] = mfma16x16x32(ah, xh[ct], accP[ot][ct]);
+                accP[ot][ct] = mfma16x16x32(al, xh[ct], accP[ot][ct]);
+                if constexpr (sizeof(TX) == 4) accP[ot][ct] = mfma16x16x32(ah, xl[ct], accP[ot][ct]);
+            }
+        }
+        // dx_proj^T: D[column 16 ct + 4 lg + i][token 16 tt + lr]
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = 16 * tt + lr;
+            const u32x4_t bh = read16(&dps_lds[cur][0][t * kDpPitch + 8 * lg]);
+            const u32x4_t bl = read16(&dps_lds[cur][1][t * kDpPitch + 8 * lg]);
+            const float st = HAS_S ? s_lds[cur][t] : 0.f;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                d = mfma16x16x32(phh[ct], bh, d);
+                d = mfma16x16x32(phl[ct], bh, d);
+                d = mfma16x16x32(phh[ct], bl, d);
+                // epilogue: four consecutive columns of token t, in place in the dx tile
+                const int c0 = wc0 + 16 * ct + 4 * lg;
+                const int boff = t * PITCH + c0 * (int)sizeof(TX);  // 8-byte aligned
+                float xv[4], dv[4];
+                lds_get4<TX>(xt + boff, xv);
+                if constexpr (ACC) {
+                    lds_get4<TX>(dt + boff, dv);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dv[i] = 0.f;
+                }
+                float o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i] = d[i] + dv[i] + st * xv[i];
+                lds_put4<TX>(dt + boff, o);
+            }
+        }
+    };
+    auto store = [&](int64_t t0, int cur) __attribute__((always_inline)) {  // dx tile -> HBM, 16-byte pieces
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int row = lrow + p * RPP;
+            if (lcol_ok && t0 + row < t_end) {
+                const uint2* ps = reinterpret_cast<const uint2*>(&tiles_lds[cur][1][row * PITCH + lvec * 16]);
+                const uint2 u0 = ps[0], u1 = ps[1];
+                st16_nt(dx + (t0 + row) * K + lcol, make_uint4(u0.x, u0.y, u1.x, u1.y));
+            }
         }
     };
 
@@ -593,23 +677,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         // even stage t0 in LDS buffer 0; f1 holds stage t0 + TB
         const int64_t t1 = t0 + TB, t2 = t0 + 2 * TB, t3 = t0 + 3 * TB;
         if (t2 < t_end) fetch(f0, t2);
-        compute(t0, 0);
+        compute(0);
+        __syncthreads();  // the dx tile is complete
+        store(t0, 0);
         if (t1 < t_end) commit(f1, t1, 1);
         __syncthreads();
         if (t1 >= t_end) break;
         // odd stage t1 in LDS buffer 1; f0 holds stage t2
         if (t3 < t_end) fetch(f1, t3);
-        compute(t1, 1);
+        compute(1);
+        __syncthreads();
+        store(t1, 1);
         if (t2 < t_end) commit(f0, t2, 0);
         __syncthreads();
     }
     if (!wave_on) return;
-    // dPhi partial: register r holds o = dtok(r, h) at column kc
+    // dPhi partial: accP[ot][ct] register i holds o = 16 ot + 4 lg + i at column 16 ct + lr
     float* out = dphi_part + (int64_t)blockIdx.y * np * K;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int o = dtok(r, h);
-        if (o < np) out[(int64_t)o * K + kc] = accP[r];
+    for (int ot = 0; ot < 2; ++ot) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int o = 16 * ot + 4 * lg + i;
+                if (o < np) out[(int64_t)o * K + kb0 + wc0 + 16 * ct + lr] = accP[ot][ct][i];
+            }
+        }
     }
 }
 
@@ -718,19 +812,19 @@ hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_s
     tile = ((tile + 31) / 32) * 32;
     const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
     const int tok = timing_begin("proj_bwd", s);
-#define MHC_PROJ_BWD(TX_, NOH_, ACC_, S_)                                                                       \
-    hipLaunchKernelGGL((proj_bwd_mfma_kernel<TX_, NOH_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP,    \
-                       dp_stride, s_tok, phi_pre, phi_post, phi_res, n_pre, np, (TX_*)dx, dphi_part, B, K, tile)
+#define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \
+    hipLaunchKernelGGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP, dp_stride,  \
+                       s_tok, phi_pre, phi_post, phi_res, n_pre, np, (TX_*)dx, dphi_part, B, K, tile)
     // the layer backward accumulates with the r_h term; the standalone operator does neither
     const bool layer = accumulate && s_tok != nullptr;
     if (!layer && (accumulate || s_tok != nullptr)) return hipErrorInvalidValue;
     if (x_dtype == kBF16) {
         if (!layer) return hipErrorInvalidValue;
-        if (np <= 24) { MHC_PROJ_BWD(bf16_t, 12, true, true); } else { MHC_PROJ_BWD(bf16_t, 16, true, true); }
+        MHC_PROJ_BWD(bf16_t, true, true);
     } else if (layer) {
-        if (np <= 24) { MHC_PROJ_BWD(float, 12, true, true); } else { MHC_PROJ_BWD(float, 16, true, true); }
+        MHC_PROJ_BWD(float, true, true);
     } else {
-        if (np <= 24) { MHC_PROJ_BWD(float, 12, false, false); } else { MHC_PROJ_BWD(float, 16, false, false); }
+        MHC_PROJ_BWD(float, false, false);
     }
 #undef MHC_PROJ_BWD
     timing_end(tok, s);

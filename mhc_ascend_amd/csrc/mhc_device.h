@@ -21,12 +21,18 @@ __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
     return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16; NaN stays a quiet NaN.
-__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<bf16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<bf16_t>(u >> 16);
+// fp32 -> bf16, round to nearest even, NaN stays a quiet NaN: gfx950's
+// v_cvt_pk_bf16_f32 (bit-identical to the rounding-bias formulation
+// u + 0x7fff + ((u >> 16) & 1) for every non-NaN input; checked on the GPU
+// over 4M inputs including ties, denormals, overflow and infinities).
+typedef __bf16 hw_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float hw_f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+// Two fp32 -> two bf16 in one word (lo in bits 0-15): one instruction.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(hw_f32x2_t{lo, hi}, hw_bf16x2_t));
 }
 
 // ---------------------------------------------------------------------------
@@ -61,8 +67,7 @@ template <> struct VecIO<bf16_t> {
     __device__ __forceinline__ static void store(bf16_t* p, const float (&v)[8]) {
         uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            w[i] = static_cast<uint32_t>(f32_to_bf16(v[2 * i])) | (static_cast<uint32_t>(f32_to_bf16(v[2 * i + 1])) << 16);
+        for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
         *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
     }
     __device__ __forceinline__ static float scalar(const bf16_t* p) { return bf16_to_f32(*p); }
@@ -127,8 +132,7 @@ template <typename T, int WN>
 __device__ __forceinline__ void store_run_nt(T* p, const float (&v)[WN]) {
     constexpr int PER = 16 / sizeof(T);
     if constexpr (sizeof(T) == 2 && WN == 4) {
-        st8_nt(p, make_uint2(static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16),
-                             static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16)));
+        st8_nt(p, make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])));
         return;
     }
     static_assert(WN % PER == 0 || (sizeof(T) == 2 && WN == 4), "non-temporal runs are 16-byte pieces");
@@ -140,9 +144,7 @@ __device__ __forceinline__ void store_run_nt(T* p, const float (&v)[WN]) {
             for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(v[s * PER + e]);
         } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                w[e] = static_cast<uint32_t>(f32_to_bf16(v[s * PER + 2 * e])) |
-                       (static_cast<uint32_t>(f32_to_bf16(v[s * PER + 2 * e + 1])) << 16);
+            for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(v[s * PER + 2 * e], v[s * PER + 2 * e + 1]);
         }
         st16_nt(p + s * PER, make_uint4(w[0], w[1], w[2], w[3]));
     }
@@ -184,10 +186,7 @@ __device__ __forceinline__ void store_run(T* p, const float (&v)[WN]) {
             VecIO<T>::store(p + s * W, t);
         }
     } else if constexpr (WN == 4 && W == 8) {
-        uint2 q;
-        q.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
-        q.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
-        *reinterpret_cast<uint2*>(p) = q;
+        *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     } else {
 #pragma unroll
         for (int e = 0; e < WN; ++e) VecIO<T>::put(p + e, v[e]);

@@ -415,9 +415,7 @@ __device__ __forceinline__ wf32x4_t wmfma16x16x32(wu32x4_t a, wu32x4_t b, wf32x4
                                                    c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t wpack(float lo, float hi) {
-    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-}
+__device__ __forceinline__ uint32_t wpack(float lo, float hi) { return pack_bf16x2(lo, hi); }
 
 __device__ __forceinline__ void wsplit3(float v, float& h, float& m, float& l) {
     h = bf16_to_f32(f32_to_bf16(v));
