@@ -589,194 +589,313 @@ __global__ __launch_bounds__(256) void wrap_proj_kernel(const TX* __restrict__ r
 }
 
 // ---------------------------------------------------------------------------
-// Projection backward of the wrapper (fp32 MFMA 32x32x2), over channels c:
+// Projection backward of the wrapper, over channels c (bf16 MFMA 16x16x32
+// with hi/lo split fp32 operands, as proj_bwd_mfma_kernel):
 //   d r[b][c] += s[b] sum_j w_j X_j + sum_o dP[b][o] Phi_r[o][c]
 //   d b[b][c] += s[b] X_1        + sum_o dP[b][o] Phi[o][C + c]
 //   dPhi_part[tile][o][j*C + c] = sum_{b in tile} dP[b][o] X_j[b][c]
 // with w_j the d r weight of stream j (1, 0, 0.1, 0.01, ...) and Phi_r =
 // sum_j w_j Phi_j: the residual-derived streams share one dx_proj chain.
-// Same staging as proj_bwd_mfma_kernel: workgroup = 4 waves x 32 channels,
-// stages of 32 tokens, two register sets of fetched stages, LDS tiles.
+// Workgroup = 8 waves x 16 columns; stages of 32 tokens with r, b and the
+// stream parts of d r / d b staged in LDS (two stages in flight in
+// registers); results return in place to the d r / d b tiles and leave with
+// coalesced 16-byte stores.
 // ---------------------------------------------------------------------------
-typedef float wf32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ wf32x16_t wmfma32x32x2(float a, float b, wf32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+template <typename TX> constexpr int wpb_pitch() { return 128 * (int)sizeof(TX) + 8; }
+constexpr int kWDpPitch = 40;
+
+__device__ __forceinline__ void wsplit_pack8(const float (&v)[8], wu32x4_t& hi, wu32x4_t& lo) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float h0 = bf16_to_f32(f32_to_bf16(v[2 * e]));
+        const float h1 = bf16_to_f32(f32_to_bf16(v[2 * e + 1]));
+        hi[e] = wpack(h0, h1);
+        lo[e] = wpack(v[2 * e] - h0, v[2 * e + 1] - h1);
+    }
 }
 
-__device__ __forceinline__ int wdtok(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+template <typename TX>
+__device__ __forceinline__ void wlds_get4(const char* p, float (&v)[4]) {
+    const uint2* q = reinterpret_cast<const uint2*>(p);
+    if constexpr (sizeof(TX) == 2) {
+        const uint2 w = q[0];
+        v[0] = __uint_as_float(w.x << 16); v[1] = __uint_as_float(w.x & 0xffff0000u);
+        v[2] = __uint_as_float(w.y << 16); v[3] = __uint_as_float(w.y & 0xffff0000u);
+    } else {
+        const uint2 a = q[0], b = q[1];
+        v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+        v[2] = __uint_as_float(b.x); v[3] = __uint_as_float(b.y);
+    }
+}
+template <typename TX>
+__device__ __forceinline__ void wlds_put4(char* p, const float (&v)[4]) {
+    uint2* q = reinterpret_cast<uint2*>(p);
+    if constexpr (sizeof(TX) == 2) {
+        q[0] = make_uint2(wpack(v[0], v[1]), wpack(v[2], v[3]));
+    } else {
+        q[0] = make_uint2(__float_as_uint(v[0]), __float_as_uint(v[1]));
+        q[1] = make_uint2(__float_as_uint(v[2]), __float_as_uint(v[3]));
+    }
+}
 
 template <typename TX, int N, bool DECAY>
-__global__ __launch_bounds__(256) void wrap_proj_bwd_kernel(
+__global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
     const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ dP,
     const float* __restrict__ s_tok, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
     const float* __restrict__ phi_res, TX* __restrict__ dres, TX* __restrict__ dbr, float* __restrict__ dphi_part,
     int64_t B, int C, int64_t tile) {
     constexpr int NP = 2 * N + N * N;
-    constexpr int NOH = (NP + 1) / 2;          // projection rows per lane half
     static_assert(NP <= 32, "projection rows must fit one 32-row tile");
     constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
     constexpr int TB = 32;
     constexpr int CB = 128;
+    constexpr int NT = 512;
     constexpr int EPV = 16 / sizeof(TX);
     constexpr int VPR = CB / EPV;
-    constexpr int RPP = 256 / VPR;
+    constexpr int RPP = NT / VPR;
     constexpr int PASSES = TB / RPP;
-    constexpr int PITCH = CB * sizeof(TX) + 16;
-    constexpr int EPR = PITCH / sizeof(TX);
-    __shared__ __align__(16) char tiles_lds[2][4][TB * PITCH];  // r, b, d r (in), d b (in)
-    __shared__ float dp_lds[2][TB][33];
+    constexpr int PITCH = wpb_pitch<TX>();
+    __shared__ __align__(16) char tiles_lds[2][4][TB * PITCH];   // [buf][r | b | d r | d b]
+    __shared__ __align__(16) bf16_t dps_lds[2][4][32 * kWDpPitch];
     __shared__ float s_lds[2][TB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int h = lane >> 5;
-    const int col = lane & 31;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
     const int64_t K = (int64_t)N * C;
     const int64_t cb0 = (int64_t)blockIdx.x * CB;
-    const int64_t cc = cb0 + wave * 32 + col;
-    const bool wave_on = cb0 + wave * 32 < C;  // C % 32 == 0
+    const int wc0 = wave * 16;
+    const bool wave_on = cb0 + wc0 < C;  // C % 16 == 0
 
     const int lrow = tid / VPR;
     const int lvec = tid % VPR;
     const int64_t lcol = cb0 + (int64_t)lvec * EPV;
     const bool lcol_ok = lcol < C;
-    const int dtk = tid >> 3;
+    const bool dp_loader = tid < 256;
+    const int dtk = (tid & 255) >> 3;
     const int dpo = (tid & 7) * 4;
 
-    // dx_proj B operands: residual-folded Phi and the branch stream's Phi
-    float bphi_r[NOH], bphi_b[NOH];
+    // dx_proj A operands: Phi_r^T and Phi_1^T at column wc0 + lr, o = 8 lg + e
+    wu32x4_t prh, prl, pbh, pbl;
+    {
+        const int64_t c = cb0 + wc0 + lr;
+        float vr[8], vb[8];
 #pragma unroll
-    for (int m = 0; m < NOH; ++m) {
-        const int o = NOH * h + m;
-        float vr = 0.f, vb = 0.f;
-        if (wave_on && o < NP) {
-            const float* rowp = phi_row(phi_pre, phi_post, phi_res, N, o, K);
-            vr = rowp[cc];
-            if constexpr (N > 1) vb = rowp[C + cc];
-            if constexpr (N > 2) vr += res_weight<2, DECAY>() * rowp[2 * (int64_t)C + cc];
-            if constexpr (N > 3) vr += res_weight<3, DECAY>() * rowp[3 * (int64_t)C + cc];
+        for (int e = 0; e < 8; ++e) {
+            const int o = 8 * lg + e;
+            float r = 0.f, b = 0.f;
+            if (wave_on && o < NP) {
+                const float* rowp = phi_row(phi_pre, phi_post, phi_res, N, o, K);
+                r = rowp[c];
+                if constexpr (N > 1) b = rowp[C + c];
+                if constexpr (N > 2) r += res_weight<2, DECAY>() * rowp[2 * (int64_t)C + c];
+                if constexpr (N > 3) r += res_weight<3, DECAY>() * rowp[3 * (int64_t)C + c];
+            }
+            vr[e] = r;
+            vb[e] = b;
         }
-        bphi_r[m] = vr;
-        bphi_b[m] = vb;
+        wsplit_pack8(vr, prh, prl);
+        wsplit_pack8(vb, pbh, pbl);
     }
-    wf32x16_t accP[NSTR];
+    wf32x4_t accP[NSTR][2];
 #pragma unroll
     for (int j = 0; j < NSTR; ++j) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) accP[j][r] = 0.f;
+        accP[j][0] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
+        accP[j][1] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 
     const int64_t t_begin = (int64_t)blockIdx.y * tile;
     const int64_t t_end = (t_begin + tile < B) ? t_begin + tile : B;
 
-    // One register set of fetched data: stage i+1 is fetched at the start of
-    // stage i's compute and written to the other LDS buffer after it.
-    uint4 fv[4][PASSES];
-    float fdp[4], fs = 0.f;
+    struct Fetched {
+        uint4 v[4][PASSES];
+        float dp[4], s;
+    };
+    Fetched f0, f1;
     const TX* srcs[4] = {res, br, dres, dbr};
-    auto fetch = [&](int64_t t0) __attribute__((always_inline)) {
+    auto fetch = [&](Fetched& f, int64_t t0) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int64_t t = t0 + lrow + p * RPP;
             const int64_t off = (t < t_end ? t : t0) * (int64_t)C + (lcol_ok ? lcol : 0);
 #pragma unroll
-            for (int a = 0; a < 4; ++a) fv[a][p] = ld16_nt(srcs[a] + off);
+            for (int a = 0; a < 4; ++a) f.v[a][p] = ld16_nt(srcs[a] + off);
         }
         const int64_t td = t0 + dtk;
         const int64_t tdc = td < t_end ? td : t0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) fdp[q] = dP[tdc * 32 + dpo + q];
-        fs = (tid < TB) ? s_tok[(t0 + tid < t_end) ? t0 + tid : t0] : 0.f;
+        for (int q = 0; q < 4; ++q) f.dp[q] = dp_loader ? dP[tdc * 32 + dpo + q] : 0.f;
+        f.s = (tid < TB) ? s_tok[(t0 + tid < t_end) ? t0 + tid : t0] : 0.f;
     };
-    auto commit = [&](int64_t t0, int buf) __attribute__((always_inline)) {
+    auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
             const uint32_t m = (lcol_ok && t0 + row < t_end) ? 0xffffffffu : 0u;
 #pragma unroll
             for (int a = 0; a < 4; ++a) {
-                const uint4 v = fv[a][p];
-                *reinterpret_cast<uint4*>(&tiles_lds[buf][a][row * PITCH + lvec * 16]) =
-                    make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+                const uint4 v = f.v[a][p];
+                uint2* pw = reinterpret_cast<uint2*>(&tiles_lds[buf][a][row * PITCH + lvec * 16]);
+                pw[0] = make_uint2(v.x & m, v.y & m);
+                pw[1] = make_uint2(v.z & m, v.w & m);
             }
         }
-        const bool tok_ok = t0 + dtk < t_end;
+        if (dp_loader) {
+            const bool tok_ok = t0 + dtk < t_end;
+            float hi[4], lo[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dp_lds[buf][dtk][dpo + q] = (tok_ok && dpo + q < NP) ? fdp[q] : 0.f;
-        if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? fs : 0.f;
+            for (int q = 0; q < 4; ++q) {
+                const float v = (tok_ok && dpo + q < NP) ? f.dp[q] : 0.f;
+                hi[q] = bf16_to_f32(f32_to_bf16(v));
+                lo[q] = v - hi[q];
+            }
+            *reinterpret_cast<uint2*>(&dps_lds[buf][0][dtk * kWDpPitch + dpo]) =
+                make_uint2(wpack(hi[0], hi[1]), wpack(hi[2], hi[3]));
+            *reinterpret_cast<uint2*>(&dps_lds[buf][1][dtk * kWDpPitch + dpo]) =
+                make_uint2(wpack(lo[0], lo[1]), wpack(lo[2], lo[3]));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                dps_lds[buf][2][(dpo + q) * kWDpPitch + dtk] = f32_to_bf16(hi[q]);
+                dps_lds[buf][3][(dpo + q) * kWDpPitch + dtk] = f32_to_bf16(lo[q]);
+            }
+        }
+        if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? f.s : 0.f;
     };
-    auto compute = [&](int64_t t0, int cur) __attribute__((always_inline)) {
+    auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> wu32x4_t {
+        const uint4 q = *reinterpret_cast<const uint4*>(p);
+        return wu32x4_t{q.x, q.y, q.z, q.w};
+    };
+    auto compute = [&](int cur) __attribute__((always_inline)) {
         if (!wave_on) return;
-        const TX* rt = reinterpret_cast<const TX*>(tiles_lds[cur][0]);
-        const TX* bt = reinterpret_cast<const TX*>(tiles_lds[cur][1]);
-        const TX* drt = reinterpret_cast<const TX*>(tiles_lds[cur][2]);
-        const TX* dbt = reinterpret_cast<const TX*>(tiles_lds[cur][3]);
-        const int c = wave * 32 + col;
-        // dPhi: reduction over the block's tokens, one chain per stream
+        const char* rt = tiles_lds[cur][0];
+        const char* bt = tiles_lds[cur][1];
+        char* drt = tiles_lds[cur][2];
+        char* dbt = tiles_lds[cur][3];
+        // dPhi: B operands x_j over tokens 8 lg .. + 7 at column wc0 + lr
+        wu32x4_t xh[NSTR], xl[NSTR];
+        {
+            const int c = wc0 + lr;
+            float xs[NSTR][8];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = wdtok(r, h);
-            const float a2 = dp_lds[cur][t][col];
-            float x[N];
-            wrap_streams<TX, N, DECAY>(VecIO<TX>::scalar(rt + t * EPR + c), VecIO<TX>::scalar(bt + t * EPR + c), x);
+            for (int e = 0; e < 8; ++e) {
+                const int t = 8 * lg + e;
+                const float r = VecIO<TX>::scalar(reinterpret_cast<const TX*>(rt + t * PITCH) + c);
+                const float b = VecIO<TX>::scalar(reinterpret_cast<const TX*>(bt + t * PITCH) + c);
+                float x[N];
+                wrap_streams<TX, N, DECAY>(r, b, x);
 #pragma unroll
-            for (int j = 0; j < NSTR; ++j) accP[j] = wmfma32x32x2(a2, x[j], accP[j]);
+                for (int j = 0; j < NSTR; ++j) xs[j][e] = x[j];
+            }
+#pragma unroll
+            for (int j = 0; j < NSTR; ++j) {
+                if constexpr (sizeof(TX) == 2) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) xh[j][e] = wpack(xs[j][2 * e], xs[j][2 * e + 1]);  // exact
+                } else {
+                    wsplit_pack8(xs[j], xh[j], xl[j]);
+                }
+            }
         }
-        // dx_proj for the residual-folded and the branch stream
-        wf32x16_t accr, accb;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            accr[r] = 0.f;
-            accb[r] = 0.f;
+        for (int ot = 0; ot < 2; ++ot) {
+            const wu32x4_t ah = read16(&dps_lds[cur][2][(16 * ot + lr) * kWDpPitch + 8 * lg]);
+            const wu32x4_t al = read16(&dps_lds[cur][3][(16 * ot + lr) * kWDpPitch + 8 * lg]);
+#pragma unroll
+            for (int j = 0; j < NSTR; ++j) {
+                accP[j][ot] = wmfma16x16x32(ah, xh[j], accP[j][ot]);
+                accP[j][ot] = wmfma16x16x32(al, xh[j], accP[j][ot]);
+                if constexpr (sizeof(TX) == 4) accP[j][ot] = wmfma16x16x32(ah, xl[j], accP[j][ot]);
+            }
         }
+        // dx_proj^T for d r and d b: D[column wc0 + 4 lg + i][token 16 tt + lr]
 #pragma unroll
-        for (int m = 0; m < NOH; ++m) {
-            const float a1 = dp_lds[cur][col][NOH * h + m];
-            accr = wmfma32x32x2(a1, bphi_r[m], accr);
-            if constexpr (N > 1) accb = wmfma32x32x2(a1, bphi_b[m], accb);
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = 16 * tt + lr;
+            const wu32x4_t bh = read16(&dps_lds[cur][0][t * kWDpPitch + 8 * lg]);
+            const wu32x4_t bl = read16(&dps_lds[cur][1][t * kWDpPitch + 8 * lg]);
+            wf32x4_t dr = wf32x4_t{0.f, 0.f, 0.f, 0.f}, db = dr;
+            dr = wmfma16x16x32(prh, bh, dr);
+            dr = wmfma16x16x32(prl, bh, dr);
+            dr = wmfma16x16x32(prh, bl, dr);
+            db = wmfma16x16x32(pbh, bh, db);
+            db = wmfma16x16x32(pbl, bh, db);
+            db = wmfma16x16x32(pbh, bl, db);
+            const float st = s_lds[cur][t];
+            const int boff = t * PITCH + (wc0 + 4 * lg) * (int)sizeof(TX);  // 8-byte aligned
+            float rv[4], bv[4], drv[4], dbv[4];
+            wlds_get4<TX>(rt + boff, rv);
+            wlds_get4<TX>(bt + boff, bv);
+            wlds_get4<TX>(drt + boff, drv);
+            wlds_get4<TX>(dbt + boff, dbv);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float x[N];
+                wrap_streams<TX, N, DECAY>(rv[i], bv[i], x);
+                float sx_r = x[0];
+                if constexpr (N > 2) sx_r += res_weight<2, DECAY>() * x[2];
+                if constexpr (N > 3) sx_r += res_weight<3, DECAY>() * x[3];
+                drv[i] += st * sx_r + dr[i];
+                dbv[i] += (N > 1 ? st * x[N > 1 ? 1 : 0] : 0.f) + db[i];
+            }
+            wlds_put4<TX>(drt + boff, drv);
+            wlds_put4<TX>(dbt + boff, dbv);
         }
+    };
+    auto store = [&](int64_t t0, int cur) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = wdtok(r, h);
-            const float s = s_lds[cur][t];
-            float x[N];
-            wrap_streams<TX, N, DECAY>(VecIO<TX>::scalar(rt + t * EPR + c), VecIO<TX>::scalar(bt + t * EPR + c), x);
-            float sx_r = x[0];
-            if constexpr (N > 2) sx_r += res_weight<2, DECAY>() * x[2];
-            if constexpr (N > 3) sx_r += res_weight<3, DECAY>() * x[3];
-            const float vr = VecIO<TX>::scalar(drt + t * EPR + c) + s * sx_r + accr[r];
-            const float vb = VecIO<TX>::scalar(dbt + t * EPR + c) + (N > 1 ? s * x[N > 1 ? 1 : 0] + accb[r] : 0.f);
-            if (t0 + t < t_end) {
-                VecIO<TX>::put(dres + (t0 + t) * (int64_t)C + cc, vr);
-                VecIO<TX>::put(dbr + (t0 + t) * (int64_t)C + cc, vb);
+        for (int p = 0; p < PASSES; ++p) {
+            const int row = lrow + p * RPP;
+            if (lcol_ok && t0 + row < t_end) {
+#pragma unroll
+                for (int a = 2; a < 4; ++a) {
+                    const uint2* ps = reinterpret_cast<const uint2*>(&tiles_lds[cur][a][row * PITCH + lvec * 16]);
+                    const uint2 u0 = ps[0], u1 = ps[1];
+                    TX* dst = (a == 2 ? dres : dbr) + (t0 + row) * (int64_t)C + lcol;
+                    st16_nt(dst, make_uint4(u0.x, u0.y, u1.x, u1.y));
+                }
             }
         }
     };
 
     if (t_begin < t_end) {
-        fetch(t_begin);
-        commit(t_begin, 0);
+        fetch(f0, t_begin);
+        commit(f0, t_begin, 0);
+        if (t_begin + TB < t_end) fetch(f1, t_begin + TB);
     }
     __syncthreads();
-    int cur = 0;
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += TB) {
-        const bool has_next = t0 + TB < t_end;
-        if (has_next) fetch(t0 + TB);
-        compute(t0, cur);
-        if (has_next) commit(t0 + TB, cur ^ 1);
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += 2 * TB) {
+        const int64_t t1 = t0 + TB, t2 = t0 + 2 * TB, t3 = t0 + 3 * TB;
+        if (t2 < t_end) fetch(f0, t2);
+        compute(0);
         __syncthreads();
-        cur ^= 1;
+        store(t0, 0);
+        if (t1 < t_end) commit(f1, t1, 1);
+        __syncthreads();
+        if (t1 >= t_end) break;
+        if (t3 < t_end) fetch(f1, t3);
+        compute(1);
+        __syncthreads();
+        store(t1, 1);
+        if (t2 < t_end) commit(f0, t2, 0);
+        __syncthreads();
     }
     if (!wave_on) return;
+    // dPhi partial: accP[j][ot] register i holds o = 16 ot + 4 lg + i at channel wc0 + lr of stream j
     float* out = dphi_part + (int64_t)blockIdx.y * NP * K;
 #pragma unroll
     for (int j = 0; j < N; ++j) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int o = wdtok(r, h);
-            if (o < NP) out[(int64_t)o * K + (int64_t)j * C + cc] = (j < NSTR) ? accP[j < NSTR ? j : 0][r] : 0.f;
+        for (int ot = 0; ot < 2; ++ot) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int o = 16 * ot + 4 * lg + i;
+                if (o < NP)
+                    out[(int64_t)o * K + (int64_t)j * C + cb0 + wc0 + lr] = (j < NSTR) ? accP[j < NSTR ? j : 0][ot][i] : 0.f;
+            }
         }
     }
 }
@@ -948,7 +1067,7 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, cons
     const dim3 grid((unsigned)((C + 127) / 128), (unsigned)tiles);
     const int tok = timing_begin("wrap_proj_bwd", s);
 #define MHC_WPB(TX_, D_)                                                                                          \
-    hipLaunchKernelGGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(256), 0, s, (const TX_*)res, (const TX_*)br, \
+    hipLaunchKernelGGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(512), 0, s, (const TX_*)res, (const TX_*)br, \
                        dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, dphi_part, B, (int)C, tile)
     if (dt == kBF16) {
         if (decay) { MHC_WPB(bf16_t, true); } else { MHC_WPB(bf16_t, false); }
