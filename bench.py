@@ -186,8 +186,11 @@ class DynamicWorkload:
 
     def kernel_bytes(self):
         E = self.E
-        return {"proj": 2 * E + self.phi_bytes() * 3 // 2, "layer_fwd": 6 * E, "layer_bwd_reduce": 6 * E,
-                "dyn_dx": 8 * E + self.phi_bytes()}
+        # proj: x bf16 + Phi as three bf16 planes; layer_fwd: x + fp32 out;
+        # layer_bwd_reduce: g fp32 + x, writes the stream part of dx (bf16);
+        # proj_bwd: x + dx read, dx written, Phi read
+        return {"proj": 2 * E + self.phi_bytes() * 3 // 2, "layer_fwd": 6 * E, "layer_bwd_reduce": 8 * E,
+                "proj_bwd": 6 * E + self.phi_bytes()}
 
     def flops(self):
         # projection x_flat [B, nC] . Phi^T [nC, 2n+n^2]
