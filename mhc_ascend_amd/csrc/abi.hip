@@ -459,6 +459,7 @@ static int check_proj(const char* fn, int64_t batch, int64_t k, int32_t out_dim)
     if (out_dim < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": out_dim must be >= 1");
     if (out_dim > 32) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": out_dim > 32 is not supported");
     if (k % 32 != 0) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": k must be a multiple of 32");
+    if (k > (int64_t(1) << 22)) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": k > 4194304 is not supported");
     return MHC_SUCCESS;
 }
 

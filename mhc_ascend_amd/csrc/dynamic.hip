@@ -49,16 +49,22 @@ __device__ __forceinline__ void split3(float v, float& h, float& m, float& l) {
     l = r - m;
 }
 
-// Phi -> bf16 planes phib[p][o][k], p = hi / mid / lo; rows np..31 are zero.
-// grid-stride over 32 * K / 8.
+// Phi -> bf16 planes in MFMA B-fragment order, p = hi / mid / lo:
+//   phif[((p * 2 + nt) * (K / 32) + ks) * 64 + lane]  (16 bytes = 8 bf16)
+//     = Phi_p[nt * 16 + lane % 16][32 ks + 8 (lane / 16) .. + 7]
+// so one wave's B operand of a 32-wide k step is 1 KB contiguous.  Rows
+// np..31 are zero.  Grid-stride over 2 * (K / 32) * 64 fragments.
 __global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict__ pre, const float* __restrict__ post,
                                                         const float* __restrict__ res, int n, int np, int64_t K,
-                                                        bf16_t* __restrict__ phib) {
-    const int64_t per_row = K / 8;
-    const int64_t total = (int64_t)kNPad * per_row;
+                                                        uint4* __restrict__ phif) {
+    const int64_t ksteps = K / 32;
+    const int64_t total = 2 * ksteps * 64;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int o = (int)(i / per_row);
-        const int64_t k = (i % per_row) * 8;
+        const int lane = (int)(i & 63);
+        const int64_t ks = (i >> 6) % ksteps;
+        const int nt = (int)((i >> 6) / ksteps);
+        const int o = nt * 16 + (lane & 15);
+        const int64_t k = ks * 32 + 8 * (lane >> 4);
         float v[8];
         if (o < np) {
             load_run<float, 8>(phi_row(pre, post, res, n, o, K) + k, v);
@@ -78,70 +84,111 @@ __global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict_
         }
 #pragma unroll
         for (int p = 0; p < 3; ++p)
-            *reinterpret_cast<uint4*>(phib + ((int64_t)p * kNPad + o) * K + k) =
-                make_uint4(w[p][0], w[p][1], w[p][2], w[p][3]);
+            phif[((int64_t)(p * 2 + nt) * ksteps + ks) * 64 + lane] = make_uint4(w[p][0], w[p][1], w[p][2], w[p][3]);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Split-K projection on MFMA.  Workgroup = 64 tokens (4 M-tiles of 16) x
-// one K range; its 4 waves take interleaved 32-wide k steps and are summed
-// through LDS.  bf16 x is exact in bf16: P = x.(hi + mid + lo) (3 MFMAs per
-// tile); fp32 x is split the same way and the six products down to 2^-16
-// relative weight are kept (xh.(hi+mid+lo) + xm.(hi+mid) + xl.hi), leaving
-// terms of order 2^-24.  Also sum x^2.  p_part[ks][B][32], ss_part[ks][B].
+// Split-K projection on MFMA.  Workgroup = TB = 16*MT tokens x one K range,
+// walked in stages of 128 k.  A stage of x is loaded with whole-row 16-byte
+// pieces (16 lanes per 256-byte row for bf16), so every request is a full
+// cache line, and staged in LDS; wave w then takes the 32-wide k step w of
+// the stage for all TB tokens (MT A fragments read from LDS) against its B
+// fragments of the Phi planes (1 KB contiguous loads).  bf16 x is exact in
+// bf16: P = x.(hi + mid + lo) (3 MFMAs per tile); fp32 x is split the same
+// way and the six products down to 2^-16 relative weight are kept
+// (xh.(hi+mid+lo) + xm.(hi+mid) + xl.hi), leaving terms of order 2^-24.
+// Also sum x^2.  p_part[ks][B][32], ss_part[ks][B].
+// Pipeline: x of stage s+2 and Phi of stage s+2 are in flight while stage s
+// is on the matrix cores; one barrier per stage.
 // ---------------------------------------------------------------------------
-template <typename TX>
-__global__ __launch_bounds__(256) void proj_mfma_kernel(const TX* __restrict__ x, const bf16_t* __restrict__ phib,
-                                                        float* __restrict__ p_part, float* __restrict__ ss_part,
-                                                        int64_t B, int64_t K, int64_t kchunk) {
-    __shared__ float red[3][36][64];
+template <typename TX> constexpr int proj_mt() { return sizeof(TX) == 2 ? 8 : 4; }
+constexpr int kProjKS = 128;  // k per stage
+
+template <typename TX, int MT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void proj_mfma_kernel(
+    const TX* __restrict__ x, const uint4* __restrict__ phif, float* __restrict__ p_part,
+    float* __restrict__ ss_part, int64_t B, int64_t K, int64_t kchunk) {
+    constexpr int TB = 16 * MT;
+    constexpr int KS = kProjKS;
+    constexpr int EPV = 16 / (int)sizeof(TX);  // elements per 16-byte piece
+    constexpr int VPR = KS / EPV;              // pieces per row of a stage
+    constexpr int RPP = 256 / VPR;             // rows per load pass
+    constexpr int PASSES = TB / RPP;
+    constexpr int PITCH = KS * (int)sizeof(TX) + 16;
+    constexpr int XW = sizeof(TX) / 2;         // A pieces per lane per k step
+    static_assert(PASSES * RPP == TB, "stage rows");
+    static_assert(3 * 9 * MT * 64 * 4 <= 2 * TB * PITCH, "epilogue reuses the stage buffers");
+    __shared__ __align__(16) char xs[2][TB * PITCH];
+
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = (int)wave_uniform(threadIdx.x >> 6);
     const int row = lane & 15;
     const int kg = lane >> 4;
-    const int64_t tok0 = (int64_t)blockIdx.x * 64;
+    const int64_t tok0 = (int64_t)blockIdx.x * TB;
     const int64_t kb = (int64_t)blockIdx.y * kchunk;
     const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
+    const int64_t nst = ke > kb ? (ke - kb + KS - 1) / KS : 0;
+    const int64_t ksteps = K / 32;
 
-    f32x4_t acc[4][2];
+    f32x4_t acc[MT][2];
+    float ss[MT];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        ss[mt] = 0.f;
     }
-    float ss[4] = {0.f, 0.f, 0.f, 0.f};
-    const TX* xr[4];
-    bool vr[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const int64_t tok = tok0 + mt * 16 + row;
-        vr[mt] = tok < B;
-        xr[mt] = x + (vr[mt] ? tok : 0) * K;
-    }
-    const bf16_t* pb[3][2];
-#pragma unroll
-    for (int p = 0; p < 3; ++p) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) pb[p][nt] = phib + ((int64_t)p * kNPad + nt * 16 + row) * K;
-    }
+    // rows of this block past the batch read zeros (resource range)
+    const int64_t rows = (B - tok0 < TB) ? B - tok0 : TB;
+    const buf_rsrc_t xrs = make_buf_rsrc(x + tok0 * K, (uint32_t)(rows * K * (int64_t)sizeof(TX)));
+    const buf_rsrc_t prs = make_buf_rsrc(phif, (uint32_t)(6 * ksteps * 64 * 16));
+    const int lrow = threadIdx.x / VPR;
+    const int lvec = threadIdx.x % VPR;
+    const uint32_t xoff = (uint32_t)(((int64_t)lrow * K + lvec * EPV) * (int64_t)sizeof(TX));
+    const uint32_t xpass = (uint32_t)((int64_t)RPP * K * (int64_t)sizeof(TX));
 
-    for (int64_t k0 = kb + wave * 32; k0 < ke; k0 += 128) {
-        const int64_t kk = k0 + kg * 8;
-        u32x4_t bv[3][2];
+    uint4 F0[PASSES], F1[PASSES], G0[6], G1[6];
+    // The whole x offset is per lane: the range check covers the lane offset
+    // only, so a column past K in the block's last row reads zeros instead
+    // of memory past the tensor.  Columns past ke are zeroed at commit.
+    // Token blocks start at different stages of their K range, so the
+    // workgroups reading one K range at a time spread over its columns (and
+    // the memory channels) instead of all reading the same 256 bytes of
+    // their rows when the row pitch is a multiple of the channel period.
+    const int64_t rot = nst > 0 ? (int64_t)blockIdx.x % nst : 0;
+    auto srot = [&](int64_t st) __attribute__((always_inline)) {
+        const int64_t r = st + rot;
+        return r < nst ? r : r - nst;
+    };
+    auto fetch_x = [&](uint4 (&f)[PASSES], int64_t st) __attribute__((always_inline)) {
+        const uint32_t col = (uint32_t)((kb + srot(st) * KS) * (int64_t)sizeof(TX));
 #pragma unroll
-        for (int p = 0; p < 3; ++p) {
+        for (int p = 0; p < PASSES; ++p) f[p] = buf_ld16<true, true>(xrs, xoff + p * xpass + col, 0u);
+    };
+    auto fetch_phi = [&](uint4 (&g)[6], int64_t st) __attribute__((always_inline)) {
+        // this wave's k step of stage st, clamped to the last one (a step
+        // past ke meets x = 0, so any finite fragment contributes nothing)
+        int64_t kstep = (kb + srot(st) * KS) / 32 + wave;
+        kstep = kstep < ksteps ? kstep : ksteps - 1;
+        const uint32_t so = (uint32_t)(kstep * 64 * 16);
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) bv[p][nt] = *reinterpret_cast<const u32x4_t*>(pb[p][nt] + kk);
-        }
+        for (int q = 0; q < 6; ++q) g[q] = buf_ld16<false, true>(prs, (uint32_t)((q * ksteps * 64 + lane) * 16), so);
+    };
+    auto commit = [&](const uint4 (&f)[PASSES], int64_t st, int buf) __attribute__((always_inline)) {
+        const uint32_t m = (kb + srot(st) * KS + lvec * EPV < ke) ? 0xffffffffu : 0u;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int p = 0; p < PASSES; ++p)
+            *reinterpret_cast<uint4*>(&xs[buf][(lrow + p * RPP) * PITCH + lvec * 16]) =
+                make_uint4(f[p].x & m, f[p].y & m, f[p].z & m, f[p].w & m);
+    };
+    auto bop = [](const uint4& q) __attribute__((always_inline)) { return u32x4_t{q.x, q.y, q.z, q.w}; };
+    auto compute = [&](int buf, const uint4 (&g)[6]) __attribute__((always_inline)) {
+        const char* base = &xs[buf][row * PITCH + (wave * 32 + kg * 8) * (int)sizeof(TX)];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
             if constexpr (sizeof(TX) == 2) {
-                u32x4_t a = u32x4_t{0u, 0u, 0u, 0u};
-                if (vr[mt]) {
-                    const uint4 q = ld16_nt(xr[mt] + kk);
-                    a = u32x4_t{q.x, q.y, q.z, q.w};
-                }
+                const u32x4_t a = bop(*reinterpret_cast<const uint4*>(base + mt * 16 * PITCH));
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float lo = __uint_as_float(a[e] << 16), hi = __uint_as_float(a[e] & 0xffff0000u);
@@ -150,15 +197,17 @@ __global__ __launch_bounds__(256) void proj_mfma_kernel(const TX* __restrict__ x
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
-                    for (int p = 0; p < 3; ++p) acc[mt][nt] = mfma16x16x32(a, bv[p][nt], acc[mt][nt]);
+                    for (int p = 0; p < 3; ++p) acc[mt][nt] = mfma16x16x32(a, bop(g[p * 2 + nt]), acc[mt][nt]);
                 }
             } else {
                 float v[8];
-                if (vr[mt]) {
-                    load_run_nt<float, 8>(reinterpret_cast<const float*>(xr[mt]) + kk, v);
-                } else {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+                for (int q = 0; q < XW; ++q) {
+                    const uint4 w = *reinterpret_cast<const uint4*>(base + mt * 16 * PITCH + 16 * q);
+                    v[4 * q] = __uint_as_float(w.x);
+                    v[4 * q + 1] = __uint_as_float(w.y);
+                    v[4 * q + 2] = __uint_as_float(w.z);
+                    v[4 * q + 3] = __uint_as_float(w.w);
                 }
                 u32x4_t ah, am, al;
 #pragma unroll
@@ -173,46 +222,77 @@ __global__ __launch_bounds__(256) void proj_mfma_kernel(const TX* __restrict__ x
                 }
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
-                    acc[mt][nt] = mfma16x16x32(ah, bv[0][nt], acc[mt][nt]);
-                    acc[mt][nt] = mfma16x16x32(ah, bv[1][nt], acc[mt][nt]);
-                    acc[mt][nt] = mfma16x16x32(am, bv[0][nt], acc[mt][nt]);
-                    acc[mt][nt] = mfma16x16x32(ah, bv[2][nt], acc[mt][nt]);
-                    acc[mt][nt] = mfma16x16x32(am, bv[1][nt], acc[mt][nt]);
-                    acc[mt][nt] = mfma16x16x32(al, bv[0][nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(ah, bop(g[0 * 2 + nt]), acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(ah, bop(g[1 * 2 + nt]), acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(am, bop(g[0 * 2 + nt]), acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(ah, bop(g[2 * 2 + nt]), acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(am, bop(g[1 * 2 + nt]), acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(al, bop(g[0 * 2 + nt]), acc[mt][nt]);
                 }
             }
         }
+    };
+
+    // Stages run in pairs with no exit between them (an exit there lets the
+    // compiler sink a prefetch to its use); a prefetch past the last stage
+    // re-reads stage 0.  buf 0 holds even stages, buf 1 odd ones.
+    if (nst > 0) {
+        auto clampst = [&](int64_t st) __attribute__((always_inline)) { return st < nst ? st : (int64_t)0; };
+        fetch_x(F0, 0);
+        fetch_phi(G0, 0);
+        commit(F0, 0, 0);
+        fetch_x(F1, clampst(1));
+        fetch_phi(G1, clampst(1));
+        __syncthreads();
+        int64_t i = 0;
+        for (; i + 2 <= nst; i += 2) {
+            fetch_x(F0, clampst(i + 2));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(0, G0);
+            fetch_phi(G0, clampst(i + 2));
+            commit(F1, i + 1, 1);
+            __syncthreads();
+            fetch_x(F1, clampst(i + 3));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(1, G1);
+            fetch_phi(G1, clampst(i + 3));
+            commit(F0, i + 2, 0);
+            __syncthreads();
+        }
+        if (i < nst) compute(0, G0);
     }
+    __syncthreads();  // the stage buffers become the cross-wave reduction area
+    float (*red)[9 * MT][64] = reinterpret_cast<float (*)[9 * MT][64]>(&xs[0][0]);
 
     // waves 1..3 hand their partials to wave 0 through LDS
     if (wave > 0) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) red[wave - 1][(mt * 2 + nt) * 4 + i][lane] = acc[mt][nt][i];
             }
-            red[wave - 1][32 + mt][lane] = ss[mt];
+            red[wave - 1][8 * MT + mt][lane] = ss[mt];
         }
     }
     __syncthreads();
     if (wave != 0) return;
-#pragma unroll
+#pragma unroll 1
     for (int q = 0; q < 3; ++q) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[mt][nt][i] += red[q][(mt * 2 + nt) * 4 + i][lane];
             }
-            ss[mt] += red[q][32 + mt][lane];
+            ss[mt] += red[q][8 * MT + mt][lane];
         }
     }
     float* pp = p_part + (int64_t)blockIdx.y * B * kNPad;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t tok = tok0 + mt * 16 + kg * 4 + i;
@@ -712,17 +792,18 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
 // ---------------------------------------------------------------------------
 hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
                             bf16_t* phib, hipStream_t s) {
-    const int64_t total = (int64_t)kNPad * (K / 8);
+    const int64_t total = 2 * (K / 32) * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(phi_split_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pre, post, res, n, np, K, phib);
+    hipLaunchKernelGGL(phi_split_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pre, post, res, n, np, K,
+                       reinterpret_cast<uint4*>(phib));
     return hipGetLastError();
 }
 
 int proj_ksplit(int64_t B, int64_t K) {
-    const int64_t mblocks = (B + 63) / 64;
+    const int64_t mblocks = (B + 127) / 128;
     int64_t ks = (2 * (int64_t)device_cu_count() + mblocks - 1) / mblocks;
-    const int64_t kmax = K / 256;
+    const int64_t kmax = (K + 2 * kProjKS - 1) / (2 * kProjKS);
     if (ks > kmax) ks = kmax;
     if (ks < 1) ks = 1;
     return (int)ks;
@@ -731,16 +812,22 @@ int proj_ksplit(int64_t B, int64_t K) {
 hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_t* phib, float* p_part, float* ss_part, int64_t B,
                             int64_t K, int ks, hipStream_t s) {
     if (B == 0) return hipSuccess;
+    // 32-bit buffer offsets: a 128-row block of fp32 x and the Phi planes
+    if (K % 32 != 0 || K > (int64_t(1) << 22)) return hipErrorInvalidValue;
     int64_t kchunk = (K + ks - 1) / ks;
-    kchunk = ((kchunk + 127) / 128) * 128;
-    const dim3 grid((unsigned)((B + 63) / 64), (unsigned)ks);
+    kchunk = ((kchunk + kProjKS - 1) / kProjKS) * kProjKS;
+    const uint4* phif = reinterpret_cast<const uint4*>(phib);
     const int tok = timing_begin("proj", s);
     if (x_dtype == kBF16) {
-        hipLaunchKernelGGL(proj_mfma_kernel<bf16_t>, grid, dim3(256), 0, s, (const bf16_t*)x, phib, p_part, ss_part, B,
-                           K, kchunk);
+        constexpr int MT = proj_mt<bf16_t>();
+        const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
+        hipLaunchKernelGGL((proj_mfma_kernel<bf16_t, MT>), grid, dim3(256), 0, s, (const bf16_t*)x, phif, p_part,
+                           ss_part, B, K, kchunk);
     } else {
-        hipLaunchKernelGGL(proj_mfma_kernel<float>, grid, dim3(256), 0, s, (const float*)x, phib, p_part, ss_part, B, K,
-                           kchunk);
+        constexpr int MT = proj_mt<float>();
+        const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
+        hipLaunchKernelGGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, p_part,
+                           ss_part, B, K, kchunk);
     }
     timing_end(tok, s);
     return hipGetLastError();

@@ -89,6 +89,31 @@ __device__ __forceinline__ void st16_nt(void* p, uint4 v) {
     __builtin_nontemporal_store(v.w, q + 3);
 }
 
+// Raw buffer loads: a scalar resource over [base, base + bytes) plus a 32-bit
+// per-lane offset and a wave-uniform scalar offset, so a load needs no 64-bit
+// address arithmetic in vector registers.  A load whose per-lane offset is at
+// or past `bytes` returns zeros (the hardware range check), which masks rows
+// past the end of a block without a branch.  Word 3 = 0x00020000 is the raw
+// (untyped, 32-bit data format) descriptor of the gfx9 family.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc_t;
+
+__device__ __forceinline__ buf_rsrc_t make_buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// cache-policy operand: 2 = nt (streaming), 0 = default.  PIN sets the
+// compiler-only volatile bit (bit 31): the load stays where it is written, so
+// a prefetch is not sunk towards its use (the hardware still runs it
+// asynchronously; the wait comes only at the first use).
+template <bool NT, bool PIN = false>
+__device__ __forceinline__ uint4 buf_ld16(buf_rsrc_t r, uint32_t voff, uint32_t soff) {
+    constexpr int aux = (NT ? 2 : 0) | (PIN ? (int)0x80000000u : 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, aux);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ uint32_t wave_uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
 __device__ __forceinline__ uint2 ld8_nt(const void* p) {
     const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
     return make_uint2(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1));

@@ -482,8 +482,8 @@ __global__ __launch_bounds__(256) void wrap_proj_kernel(const TX* __restrict__ r
             for (int p = 0; p < 3; ++p) {
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt)
-                    bvp[p][nt] = *reinterpret_cast<const wu32x4_t*>(phib + ((int64_t)p * KP + nt * 16 + row) * K +
-                                                                     (int64_t)j * C + cc);
+                    bvp[p][nt] = *reinterpret_cast<const wu32x4_t*>(
+                        phib + (((int64_t)(p * 2 + nt) * (K / 32) + ((int64_t)j * C + c0) / 32) * 64 + lane) * 8);
             }
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt) {

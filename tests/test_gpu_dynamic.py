@@ -25,7 +25,8 @@ def _gen(seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,K,out_dim", [(1, 32, 1), (70, 1024, 24), (300, 4096, 32), (65, 16384, 24)])
+@pytest.mark.parametrize("B,K,out_dim", [(1, 32, 1), (3, 96, 8), (70, 1024, 24), (129, 4160, 24), (300, 4096, 32),
+                                         (65, 16384, 24)])
 def test_projection(device, dtype, B, K, out_dim):
     g = _gen(B + K + out_dim)
     x = torch.randn(B, K, generator=g).to(dtype)
