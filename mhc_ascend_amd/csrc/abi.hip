@@ -231,8 +231,6 @@ int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const void* weight, int
     return hip_status(launch_layer_fwd(x_dtype, n, x, w32, saved, 0, out, rms, batch, hidden, rmsnorm_eps, s));
 }
 
-// Row groups of the two-stage dw column sum.
-static const int kDwSplit = 16;
 
 struct StaticBwdWs {
     int grid;
@@ -247,7 +245,7 @@ static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32
     w.dw_off = 0;
     w.scal_off = align256((size_t)w.grid * hidden * sizeof(float));
     w.stage_off = w.scal_off + align256((size_t)w.grid * (n * n + 2 * n) * sizeof(float));
-    w.total = w.stage_off + align256((size_t)kDwSplit * hidden * sizeof(float));
+    w.total = w.stage_off + align256(column_sums_stage_floats(hidden) * sizeof(float));
     return w;
 }
 
@@ -286,9 +284,8 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
         e = launch_layer_bwd(x_dtype, n, 0, grad_out, x, saved + saved_w_offset(n), saved, 0, grad_x, dw_part,
                              scal_part, w.grid, batch, hidden, rmsnorm_eps, s);
     }
-    if (e == hipSuccess) e = launch_column_partial(dw_part, rows, hidden, stage, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(n, weight_dtype, stage, kDwSplit, hidden, grad_weight, scal_part, rows, h_pre,
+        e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stage, grad_weight, scal_part, rows, h_pre,
                                   h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
     return hip_status(e);
 }
@@ -332,7 +329,7 @@ static RowsBwdWs rmsnorm_bwd_ws(int64_t batch, int32_t hidden, int32_t dtype) {
     w.grid = batch > 0 ? rmsnorm_bwd_grid(dtype, batch, hidden) : 1;
     w.part_off = 0;
     w.stage_off = align256((size_t)w.grid * hidden * sizeof(float));
-    w.total = w.stage_off + align256((size_t)kDwSplit * hidden * sizeof(float));
+    w.total = w.stage_off + align256(column_sums_stage_floats(hidden) * sizeof(float));
     return w;
 }
 
@@ -362,9 +359,8 @@ int mhc_rmsnorm_bwd(const void* grad_out, const void* inp, int32_t dtype, const 
     } else {
         e = launch_rmsnorm_bwd(dtype, grad_out, inp, weight, rms, grad_inp, part, w.grid, batch, hidden, s);
     }
-    if (e == hipSuccess) e = launch_column_partial(part, rows, hidden, stage, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(0, kF32, stage, kDwSplit, hidden, grad_weight, nullptr, 0, nullptr, nullptr, nullptr,
+        e = launch_column_finalize(0, kF32, part, rows, hidden, stage, grad_weight, nullptr, 0, nullptr, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, 0, 0.f, s);
     return hip_status(e);
 }
@@ -498,7 +494,7 @@ static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
     w.tiles = batch > 0 ? proj_bwd_tiles(batch, k) : 1;
     w.part_off = 0;
     w.stage_off = align256((size_t)w.tiles * out_dim * k * sizeof(float));
-    w.total = w.stage_off + align256((size_t)kDwSplit * out_dim * k * sizeof(float));
+    w.total = w.stage_off + align256(column_sums_stage_floats((int64_t)out_dim * k) * sizeof(float));
     return w;
 }
 
@@ -530,9 +526,8 @@ int mhc_fused_rmsnorm_matmul_bwd(const float* grad_out, const float* x_flat, con
         e = launch_proj_bwd(kF32, x_flat, grad_out, out_dim, nullptr, phi, phi, phi, out_dim, out_dim, grad_x,
                             false, part, w.tiles, batch, k, s);
     }
-    if (e == hipSuccess) e = launch_column_partial(part, rows, cols, stage, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(0, kF32, stage, kDwSplit, cols, grad_phi, nullptr, 0, nullptr, nullptr, nullptr,
+        e = launch_column_finalize(0, kF32, part, rows, cols, stage, grad_phi, nullptr, 0, nullptr, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, 0, 0.f, s);
     return hip_status(e);
 }
@@ -629,8 +624,8 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     w.s_off = o; o += align256((size_t)batch * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     w.phip_off = o; o += align256((size_t)w.tiles * np * K * 4);
-    w.stw_off = o; o += align256((size_t)kDwSplit * hidden * 4);
-    w.stp_off = o; o += align256((size_t)kDwSplit * np * K * 4);
+    w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
+    w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)np * K) * 4);
     w.total = o;
     return w;
 }
@@ -690,13 +685,11 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
             e = launch_proj_bwd(x_dtype, x, dp, 32, stok, phi_pre, phi_post, phi_res, n, np, grad_x, true, phip,
                                 w.tiles, batch, K, s);
     }
-    if (e == hipSuccess) e = launch_column_partial(dw_part, rows_w, hidden, stw, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(0, weight_dtype, stw, kDwSplit, hidden, grad_weight, nullptr, 0, nullptr, nullptr,
+        e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
-    if (e == hipSuccess) e = launch_column_partial(phip, rows_p, (int64_t)np * K, stp, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(0, kF32, stp, kDwSplit, (int64_t)np * K, grad_phi, nullptr, 0, nullptr, nullptr,
+        e = launch_column_finalize(0, kF32, phip, rows_p, (int64_t)np * K, stp, grad_phi, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
     if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
     return hip_status(e);
@@ -794,7 +787,7 @@ static WrapBwdWs wrap_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, int32_t 
     w.grid = tokens > 0 ? wrap_bwd_grid(dtype, n, decay, tokens, hidden) : 1;
     size_t o = 0;
     w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
-    w.stw_off = o; o += align256((size_t)kDwSplit * hidden * 4);
+    w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
     if (!dynamic) {
         w.scal_off = o; o += align256((size_t)w.grid * (n * n + 2 * n) * 4);
         w.total = o;
@@ -807,7 +800,7 @@ static WrapBwdWs wrap_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, int32_t 
     w.s_off = o; o += align256((size_t)tokens * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     w.phip_off = o; o += align256((size_t)w.tiles * np * K * 4);
-    w.stp_off = o; o += align256((size_t)kDwSplit * np * K * 4);
+    w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)np * K) * 4);
     w.total = o;
     return w;
 }
@@ -869,13 +862,11 @@ int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const v
             e = launch_wrap_proj_bwd(dtype, n, decay, residual, branch, dp, stok, phi_pre, phi_post, phi_res,
                                      grad_residual, grad_branch, phip, w.tiles, tokens, hidden, s);
     }
-    if (e == hipSuccess) e = launch_column_partial(dw_part, rows_w, hidden, stw, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(0, weight_dtype, stw, kDwSplit, hidden, grad_weight, nullptr, 0, nullptr, nullptr,
+        e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
-    if (e == hipSuccess) e = launch_column_partial(phip, rows_p, (int64_t)np * K, stp, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(0, kF32, stp, kDwSplit, (int64_t)np * K, grad_phi, nullptr, 0, nullptr, nullptr,
+        e = launch_column_finalize(0, kF32, phip, rows_p, (int64_t)np * K, stp, grad_phi, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
     if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
     return hip_status(e);
@@ -935,9 +926,8 @@ int mhc_wrapper_static_bwd(const float* grad_out, const void* residual, const vo
         e = launch_wrap_bwd(dtype, n, 0, decay, grad_out, residual, branch, saved + saved_w_offset(n), saved, 0,
                             grad_residual, grad_branch, dw_part, scal_part, w.grid, tokens, hidden, rmsnorm_eps, s);
     }
-    if (e == hipSuccess) e = launch_column_partial(dw_part, rows, hidden, stage, kDwSplit, s);
     if (e == hipSuccess)
-        e = launch_layer_finalize(n, weight_dtype, stage, kDwSplit, hidden, grad_weight, scal_part, rows, h_pre,
+        e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stage, grad_weight, scal_part, rows, h_pre,
                                   h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
     return hip_status(e);
 }

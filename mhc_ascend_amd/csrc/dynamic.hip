@@ -466,23 +466,39 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
     }
 }
 
-// out[c] = sum_r part[r][c] for a few columns (db, dalpha); one workgroup.
-__global__ __launch_bounds__(256) void small_column_sum_kernel(const float* __restrict__ part, int rows, int cols,
-                                                               float* __restrict__ out_db, float* __restrict__ out_da,
-                                                               int np) {
-    __shared__ float red[256];
-    for (int c = 0; c < cols; ++c) {
+// out[c] = sum_r part[r][c] for a few columns (db, dalpha); one workgroup of
+// 32 columns x 32 row phases, each phase summing every 32nd row in order and
+// the phases added in order (deterministic).
+__global__ __launch_bounds__(1024) void small_column_sum_kernel(const float* __restrict__ part, int rows, int cols,
+                                                                float* __restrict__ out_db, float* __restrict__ out_da,
+                                                                int np) {
+    __shared__ float red[32][33];
+    const int cl = threadIdx.x & 31;
+    const int ph = threadIdx.x >> 5;
+    for (int c0 = 0; c0 < cols; c0 += 32) {
+        const int col = c0 + cl;
         float s = 0.f;
-        for (int q = threadIdx.x; q < rows; q += blockDim.x) s += part[(int64_t)q * cols + c];
-        red[threadIdx.x] = s;
-        __syncthreads();
-        for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-            if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-            __syncthreads();
+        if (col < cols) {
+            int q = ph;
+            for (; q + 96 < rows; q += 128) {
+                const float a0 = part[(int64_t)q * cols + col];
+                const float a1 = part[(int64_t)(q + 32) * cols + col];
+                const float a2 = part[(int64_t)(q + 64) * cols + col];
+                const float a3 = part[(int64_t)(q + 96) * cols + col];
+                s += a0;
+                s += a1;
+                s += a2;
+                s += a3;
+            }
+            for (; q < rows; q += 32) s += part[(int64_t)q * cols + col];
         }
-        if (threadIdx.x == 0) {
-            if (c < np) out_db[c] = red[0];
-            else out_da[c - np] = red[0];
+        red[ph][cl] = s;
+        __syncthreads();
+        if (ph == 0 && col < cols) {
+            float t = 0.f;
+            for (int k = 0; k < 32; ++k) t += red[k][cl];
+            if (col < np) out_db[col] = t;
+            else out_da[col - np] = t;
         }
         __syncthreads();
     }
@@ -875,7 +891,7 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
 
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s) {
-    hipLaunchKernelGGL(small_column_sum_kernel, dim3(1), dim3(256), 0, s, part, rows, cols, out_db, out_da, np);
+    hipLaunchKernelGGL(small_column_sum_kernel, dim3(1), dim3(1024), 0, s, part, rows, cols, out_db, out_da, np);
     return hipGetLastError();
 }
 

@@ -52,17 +52,27 @@ __global__ __launch_bounds__(256) void static_coef_kernel(const float* __restric
         }
         return;
     }
-    if (threadIdx.x >= kWave) return;
     const int r = threadIdx.x;
-    float a[N];
-#pragma unroll
-    for (int c = 0; c < N; ++c) a[c] = (r < N) ? expf(h_res[r * N + c]) : 0.f;
-    sk_forward<N>(a, iters, eps, r < N);
     if (r < N) {
         saved[r] = sigmoidf(h_pre[r]);
         saved[N + r] = 2.f * sigmoidf(h_post[r]);
+    }
+    if (r >= kWave) return;
+    if constexpr (N == 4) {
+        // the shared M = SK(exp(H_res)): one element per lane of lanes 0..15
+        // (the finalize's adjoint recomputes it with the same code)
+        float a = r < 16 ? expf(h_res[r]) : 0.f;
+        sk16_forward(a, iters, eps);
+        if (r < 16) saved[2 * N + r] = a;
+    } else {
+        float a[N];
 #pragma unroll
-        for (int c = 0; c < N; ++c) saved[2 * N + r * N + c] = a[c];
+        for (int c = 0; c < N; ++c) a[c] = (r < N) ? expf(h_res[r * N + c]) : 0.f;
+        sk_forward<N>(a, iters, eps, r < N);
+        if (r < N) {
+#pragma unroll
+            for (int c = 0; c < N; ++c) saved[2 * N + r * N + c] = a[c];
+        }
     }
 }
 
@@ -405,40 +415,60 @@ __global__ __launch_bounds__(256) void column_partial_kernel(const float* __rest
     }
 }
 
-// Blocks [0, ceil(cols/256)) finish the dw sum (rsplit staged rows) and
-// store it in the weight's dtype.  With N > 0 the last block also forms the
-// static parameter gradients from the per-workgroup sums of
+// Blocks [0, ceil(cols/64)) finish the column sums of stage[rsplit][cols]
+// (per-workgroup partials, or their first-pass sums when there are many)
+// and store them in the weight's dtype: 64 columns per block, blockDim/64
+// row phases (up to 16, from the row count), fixed summation order.  With N > 0 the last block also forms the static
+// parameter gradients from the per-workgroup sums of
 // [dM, dh_post_act, dh_pre_act]: the activation derivatives (ops.py:172,
 // 240-242) and ONE Sinkhorn backward on the token-summed dM (M is shared, so
 // its VJP is linear in dM):
 //     dH_pre = dh_pre_act h_pre (1 - h_pre)
 //     dH_post = dh_post_act h_post (1 - h_post / 2)
 //     dH_res = SK^T(dM) * exp(H_res)
-constexpr int kColSplit = 16;  // max row groups of the two-stage column sum
+// For n = 4 the Sinkhorn recompute and adjoint run one element per lane of a
+// 16-lane row, as the forward's coefficient kernel computes M.
+constexpr int kColSplit = 16;   // row groups of the first pass when rows are many
+constexpr int kDirectRows = 512;  // partial rows the finalize sums directly
 
 template <int N, typename TW>
-__global__ __launch_bounds__(256) void layer_finalize_kernel(
+__global__ __launch_bounds__(1024) void layer_finalize_kernel(
     const float* __restrict__ stage, int rsplit, int64_t cols, TW* __restrict__ dw,
     const float* __restrict__ scal_part, int rows, const float* __restrict__ h_pre,
     const float* __restrict__ h_post, const float* __restrict__ h_res, float* __restrict__ d_h_pre,
     float* __restrict__ d_h_post, float* __restrict__ d_h_res, int iters, float eps) {
-    const int col_blocks = (int)((cols + 255) / 256);
+    const int col_blocks = (int)((cols + 63) / 64);
     if ((int)blockIdx.x < col_blocks) {
-        const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+        __shared__ float cred[16][64];
+        const int lane = threadIdx.x & 63;
+        const int ph = threadIdx.x >> 6;
+        const int nph = blockDim.x >> 6;
+        const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+        float s = 0.f;
         if (c < cols) {
-            float v[kColSplit];
+            // 8 loads in flight per step, fixed summation order
+            int r = ph;
+            for (; r + 7 * nph < rsplit; r += 8 * nph) {
+                float a[8];
 #pragma unroll
-            for (int r = 0; r < kColSplit; ++r) v[r] = (r < rsplit) ? stage[(int64_t)r * cols + c] : 0.f;
-            float s = 0.f;
+                for (int u = 0; u < 8; ++u) a[u] = stage[(int64_t)(r + u * nph) * cols + c];
 #pragma unroll
-            for (int r = 0; r < kColSplit; ++r) s += v[r];
-            VecIO<TW>::put(dw + c, s);
+                for (int u = 0; u < 8; ++u) s += a[u];
+            }
+            for (; r < rsplit; r += nph) s += stage[(int64_t)r * cols + c];
+        }
+        cred[ph][lane] = s;
+        __syncthreads();
+        if (ph == 0 && c < cols) {
+            float t = 0.f;
+            for (int k = 0; k < nph; ++k) t += cred[k][lane];
+            VecIO<TW>::put(dw + c, t);
         }
         return;
     }
     if constexpr (N > 0) {
         constexpr int NS = N * N + 2 * N;
-        __shared__ float red[4 * NS];
+        __shared__ float red[16 * NS];
         float v[NS];
 #pragma unroll
         for (int k = 0; k < NS; ++k) v[k] = 0.f;
@@ -447,7 +477,18 @@ __global__ __launch_bounds__(256) void layer_finalize_kernel(
             for (int k = 0; k < NS; ++k) v[k] += scal_part[(int64_t)r * NS + k];
         }
         block_sum<NS>(v, red);
-        if (threadIdx.x < kWave) {
+        if constexpr (N == 4) {
+            if (threadIdx.x < kWave) {
+                // one element per lane of lanes 0..15, as the forward computed M
+                const int l = threadIdx.x;
+                const float e = l < 16 ? expf(h_res[l]) : 0.f;
+                float g = 0.f;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) g = (l == q) ? v[q] : g;
+                sk16_backward(g, e, iters, eps);
+                if (l < 16) d_h_res[l] = g * e;
+            }
+        } else if (threadIdx.x < kWave) {
             const int r = threadIdx.x;
             float e[N], gm[N];
 #pragma unroll
@@ -462,17 +503,20 @@ __global__ __launch_bounds__(256) void layer_finalize_kernel(
             if (r < N) {
 #pragma unroll
                 for (int c = 0; c < N; ++c) d_h_res[r * N + c] = gm[c] * e[c];
-                float hp = 0.f, hq = 0.f;
-#pragma unroll
-                for (int q = 0; q < N; ++q) {
-                    hp = (r == q) ? v[N * N + N + q] : hp;
-                    hq = (r == q) ? v[N * N + q] : hq;
-                }
-                const float tp = sigmoidf(h_pre[r]);
-                const float tq = 2.f * sigmoidf(h_post[r]);
-                d_h_pre[r] = hp * tp * (1.f - tp);
-                d_h_post[r] = hq * tq * (1.f - tq * 0.5f);
             }
+        }
+        if (threadIdx.x < N) {
+            const int r = threadIdx.x;
+            float hp = 0.f, hq = 0.f;
+#pragma unroll
+            for (int q = 0; q < N; ++q) {
+                hp = (r == q) ? v[N * N + N + q] : hp;
+                hq = (r == q) ? v[N * N + q] : hq;
+            }
+            const float tp = sigmoidf(h_pre[r]);
+            const float tq = 2.f * sigmoidf(h_post[r]);
+            d_h_pre[r] = hp * tp * (1.f - tp);
+            d_h_post[r] = hq * tq * (1.f - tq * 0.5f);
         }
     }
 }
@@ -666,11 +710,18 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
                                  const float* scal_part, int rows, const float* h_pre, const float* h_post,
                                  const float* h_res, float* d_h_pre, float* d_h_post, float* d_h_res, int iters,
                                  float sk_eps, hipStream_t s) {
-    const unsigned col_blocks = (unsigned)((cols + 255) / 256);
+    const unsigned col_blocks = (unsigned)((cols + 63) / 64);
     const unsigned blocks = col_blocks + (n > 0 ? 1 : 0);
     if (blocks == 0) return hipSuccess;
+    // row phases per column block (64 lanes each): up to 16 for many partial
+    // rows; with the static scalar block (n > 0) exactly 4, since its
+    // reductions cost more with more waves and it is the longer block
+    int phases = 1;
+    while (phases < 16 && phases < rsplit) phases *= 2;
+    if (n > 0) phases = 4;
+    const unsigned threads = 64u * (unsigned)phases;
 #define MHC_FIN_LAUNCH(N_, TW_)                                                                                  \
-    hipLaunchKernelGGL((layer_finalize_kernel<N_, TW_>), dim3(blocks), dim3(256), 0, s, stage, rsplit, cols,      \
+    hipLaunchKernelGGL((layer_finalize_kernel<N_, TW_>), dim3(blocks), dim3(threads), 0, s, stage, rsplit, cols,  \
                        (TW_*)dw, scal_part, rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps)
     if (n == 0) {
         if (w_dtype == kBF16) { MHC_FIN_LAUNCH(0, bf16_t); } else { MHC_FIN_LAUNCH(0, float); }
@@ -683,6 +734,21 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
     }
 #undef MHC_FIN_LAUNCH
     return hipGetLastError();
+}
+
+size_t column_sums_stage_floats(int64_t cols) { return (size_t)kColSplit * (size_t)cols; }
+
+hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int rows, int64_t cols, float* stage,
+                                  void* dw, const float* scal_part, int scal_rows, const float* h_pre,
+                                  const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
+                                  float* d_h_res, int iters, float sk_eps, hipStream_t s) {
+    if (rows <= kDirectRows)
+        return launch_layer_finalize(n, w_dtype, part, rows, cols, dw, scal_part, scal_rows, h_pre, h_post, h_res,
+                                     d_h_pre, d_h_post, d_h_res, iters, sk_eps, s);
+    hipError_t e = launch_column_partial(part, rows, cols, stage, kColSplit, s);
+    if (e != hipSuccess) return e;
+    return launch_layer_finalize(n, w_dtype, stage, kColSplit, cols, dw, scal_part, scal_rows, h_pre, h_post, h_res,
+                                 d_h_pre, d_h_post, d_h_res, iters, sk_eps, s);
 }
 
 }  // namespace mhc

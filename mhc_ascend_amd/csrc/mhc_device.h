@@ -230,6 +230,8 @@ constexpr int kRowHalfMirror = 0x141; // lane i <- lane 7-i within 8
 constexpr int kRowMirror = 0x140;     // lane i <- lane 15-i within 16
 constexpr int kRowBcast15 = 0x142;    // lane 15 of row r -> row r+1
 constexpr int kRowBcast31 = 0x143;    // lane 31 -> rows 2, 3
+constexpr int kRowRor4 = 0x124;       // lane i <- lane (i - 4) mod 16 within 16
+constexpr int kRowRor8 = 0x128;       // lane i <- lane (i - 8) mod 16 within 16
 
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ float mov(float v) {
@@ -287,11 +289,17 @@ __device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
         for (int i = 0; i < NV; ++i) lds[wave * NV + i] = v[i];
     }
     __syncthreads();
+    // A wave's NV totals are read together (independent loads), so the second
+    // level costs one LDS round trip per wave rather than one per value and
+    // wave; the summation order (waves in order from 0) is unchanged.
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        float s = 0.f;
-        for (int w = 0; w < nwaves; ++w) s += lds[w * NV + i];
-        v[i] = s;
+    for (int i = 0; i < NV; ++i) v[i] = 0.f;
+    for (int w = 0; w < nwaves; ++w) {
+        float t[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) t[i] = lds[w * NV + i];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] += t[i];
     }
     __syncthreads();
 }
@@ -414,6 +422,70 @@ __device__ __forceinline__ void sk_backward(float (&g)[N], const float (&x0)[N],
                 if (s < t) sk_col_step<N>(a, eps);
             }
             sk_adjoint_step<N>(g, a, rinv, eps);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Sinkhorn-Knopp on a 4 x 4 matrix held one element per lane in a 16-lane DPP
+// row (lane 4 r + c of the row holds element (r, c)): a row sum is a quad
+// reduction, a column sum two rotations within the row, so an iteration is a
+// few full-rate instructions (for one shared matrix such as the static H_res,
+// where the latency of the chain is the cost).  The adjoint follows the same
+// formulas as sk_adjoint_step, with the per-iteration post-row-step element
+// and row scale kept in registers for iters <= kSk16Hist.
+// ---------------------------------------------------------------------------
+constexpr int kSk16Hist = 32;
+
+__device__ __forceinline__ float sk16_row_sum(float v) { return group_sum<4>(v); }
+__device__ __forceinline__ float sk16_col_sum(float v) {
+    v += dpp::mov<dpp::kRowRor4>(v);
+    v += dpp::mov<dpp::kRowRor8>(v);
+    return v;
+}
+
+__device__ __forceinline__ void sk16_forward(float& a, int iters, float eps) {
+    for (int t = 0; t < iters; ++t) {
+        a *= rcp_nr(sk16_row_sum(a) + eps);
+        a *= rcp_nr(sk16_col_sum(a) + eps);
+    }
+}
+
+__device__ __forceinline__ void sk16_adjoint_step(float& g, float A, float ri, float eps) {
+    const float ci = rcp_nr(sk16_col_sum(A) + eps);
+    const float dot = sk16_col_sum(g * (A * ci));
+    const float dA = (g - dot) * ci;
+    const float rd = sk16_row_sum(dA * A);
+    g = (dA - rd) * ri;
+}
+
+// g: element of dL/dM in, dL/dX out; x0: element of the forward input X.
+__device__ __forceinline__ void sk16_backward(float& g, float x0, int iters, float eps) {
+    if (iters <= kSk16Hist) {
+        float hA[kSk16Hist], hr[kSk16Hist];
+        float a = x0;
+#pragma unroll
+        for (int t = 0; t < kSk16Hist; ++t) {
+            if (t < iters) {
+                hr[t] = rcp_nr(sk16_row_sum(a) + eps);
+                a *= hr[t];
+                hA[t] = a;
+                a *= rcp_nr(sk16_col_sum(a) + eps);
+            }
+        }
+#pragma unroll
+        for (int t = kSk16Hist - 1; t >= 0; --t) {
+            if (t < iters) sk16_adjoint_step(g, hA[t], hr[t], eps);
+        }
+    } else {
+        for (int t = iters - 1; t >= 0; --t) {
+            float a = x0, ri = 0.f;
+            for (int s = 0; s <= t; ++s) {
+                ri = rcp_nr(sk16_row_sum(a) + eps);
+                a *= ri;
+                if (s < t) a *= rcp_nr(sk16_col_sum(a) + eps);
+            }
+            sk16_adjoint_step(g, a, ri, eps);
         }
     }
 }

@@ -55,6 +55,14 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
                                  const float* scal_part, int rows, const float* h_pre, const float* h_post,
                                  const float* h_res, float* d_h_pre, float* d_h_post, float* d_h_res, int iters,
                                  float sk_eps, hipStream_t s);
+// Column sums of part[rows][cols] into dw (w_dtype), plus the static scalar
+// gradients when n > 0: one launch when rows is small (the finalize reads the
+// partials directly), else a first pass into stage[column_sums_stage_floats].
+size_t column_sums_stage_floats(int64_t cols);
+hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int rows, int64_t cols, float* stage,
+                                  void* dw, const float* scal_part, int scal_rows, const float* h_pre,
+                                  const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
+                                  float* d_h_res, int iters, float sk_eps, hipStream_t s);
 
 // ---- ops.hip ---------------------------------------------------------------
 hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, float* rms, int64_t B, int64_t C,
