@@ -491,7 +491,7 @@ struct ProjBwdWs {
 
 static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
     ProjBwdWs w{};
-    w.tiles = batch > 0 ? proj_bwd_tiles(batch, k) : 1;
+    w.tiles = batch > 0 ? proj_bwd_tiles(kF32, batch, k) : 1;
     w.part_off = 0;
     w.stage_off = align256((size_t)w.tiles * out_dim * k * sizeof(float));
     w.total = w.stage_off + align256(column_sums_stage_floats((int64_t)out_dim * k) * sizeof(float));
@@ -616,7 +616,7 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     const int64_t K = (int64_t)n * hidden;
     w.grid = batch > 0 ? layer_bwd_grid(x_dtype, n, batch, hidden) : 1;
     w.cblocks = batch > 0 ? dyn_coef_bwd_blocks(n, batch) : 1;
-    w.tiles = batch > 0 ? proj_bwd_tiles(batch, (int64_t)n * hidden) : 1;
+    w.tiles = batch > 0 ? proj_bwd_tiles(x_dtype, batch, (int64_t)n * hidden) : 1;
     size_t o = 0;
     w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
     w.scal_off = o; o += align256((size_t)batch * (n * n + 2 * n + 2) * 4);
@@ -794,7 +794,7 @@ static WrapBwdWs wrap_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, int32_t 
         return w;
     }
     w.cblocks = tokens > 0 ? dyn_coef_bwd_blocks(n, tokens) : 1;
-    w.tiles = tokens > 0 ? wrap_proj_bwd_tiles(tokens, hidden) : 1;
+    w.tiles = tokens > 0 ? wrap_proj_bwd_tiles(dtype, tokens, hidden) : 1;
     w.scal_off = o; o += align256((size_t)tokens * (n * n + 2 * n + 2) * 4);
     w.dp_off = o; o += align256((size_t)tokens * 32 * 4);
     w.s_off = o; o += align256((size_t)tokens * 4);

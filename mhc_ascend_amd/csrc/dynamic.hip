@@ -895,9 +895,19 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
     return hipGetLastError();
 }
 
-int proj_bwd_tiles(int64_t B, int64_t K) {
+// Token tiles of the projection backward: column blocks x tiles fill two
+// rounds of resident workgroups (rounded down, so a last partial round is
+// nearly full rather than leaving most CUs idle while it runs), at least one.
+int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
     const int64_t gx = (K + 127) / 128;
-    int64_t tiles = (4 * (int64_t)device_cu_count() + gx - 1) / gx;
+    const void* fn = x_dtype == kBF16 ? reinterpret_cast<const void*>(&proj_bwd_mfma_kernel<bf16_t, true, true>)
+                                      : reinterpret_cast<const void*>(&proj_bwd_mfma_kernel<float, true, true>);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu < 1) {
+        (void)hipGetLastError();
+        per_cu = 1;
+    }
+    int64_t tiles = 2 * (int64_t)device_cu_count() * per_cu / gx;
     const int64_t blocks = (B + 31) / 32;
     if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;

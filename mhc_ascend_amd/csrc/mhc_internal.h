@@ -101,12 +101,12 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                                hipStream_t s);
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s);
-// Projection backward on fp32 MFMA over the flattened [B, K] rows:
+// Projection backward (bf16 MFMA, split operands) over the flattened [B, K] rows:
 //   dx[b][k] = (accumulate ? dx[b][k] : 0) + (s ? s[b] x[b][k] : 0) + sum_o dP[b][o] Phi[o][k]
 //   dphi_part[tile][o][k] = sum_{b in tile} dP[b][o] x[b][k]
 // Phi row o is phi_row(pre, post, res, n_pre, o): rows < n_pre from `pre`,
 // the next n_pre from `post`, the rest from `res`.  np <= 32, K % 32 == 0.
-int proj_bwd_tiles(int64_t B, int64_t K);
+int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K);
 hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
                            const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                            void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
@@ -128,7 +128,7 @@ hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, 
 int wrap_proj_csplit(int64_t B, int64_t C);
 hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const void* br, const bf16_raw_t* phib,
                             float* p_part, float* ss_part, int64_t B, int64_t C, int ks, hipStream_t s);
-int wrap_proj_bwd_tiles(int64_t B, int64_t C);
+int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C);
 hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
                                 const float* s_tok, const float* phi_pre, const float* phi_post, const float* phi_res,
                                 void* dres, void* dbr, float* dphi_part, int tiles, int64_t B, int64_t C,

@@ -1047,9 +1047,19 @@ hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const vo
     return hipGetLastError();
 }
 
-int wrap_proj_bwd_tiles(int64_t B, int64_t C) {
+// Token tiles: column blocks x tiles fill two rounds of resident workgroups
+// (rounded down, so a last partial round is nearly full rather than leaving
+// most CUs idle while it runs), at least one.
+int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
     const int64_t gx = (C + 127) / 128;
-    int64_t tiles = (2 * (int64_t)device_cu_count() + gx - 1) / gx;
+    const void* fn = dt == kBF16 ? reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<bf16_t, 4, true>)
+                                 : reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<float, 4, true>);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 512, 0) != hipSuccess || per_cu < 1) {
+        (void)hipGetLastError();
+        per_cu = 1;
+    }
+    int64_t tiles = 2 * (int64_t)device_cu_count() * per_cu / gx;
     const int64_t blocks = (B + 31) / 32;
     if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;
