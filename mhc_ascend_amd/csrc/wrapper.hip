@@ -23,6 +23,8 @@
 //                         and b once per channel for all n streams
 //   wrap_proj_bwd_kernel  d r, d b += s X + dP . Phi (fp32 MFMA, Phi folded
 //                         over the residual-derived streams) and dPhi
+#include <type_traits>
+
 #include "mhc_device.h"
 #include "mhc_internal.h"
 #include "mhc_rows.h"
@@ -398,13 +400,21 @@ __global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, 
 // ---------------------------------------------------------------------------
 // Projection of the synthesised row: P[b][o] = sum_j sum_c X_j[b][c]
 // Phi[o][j*C + c], and sum_j sum_c X_j^2, on bf16 MFMA 16x16x32.  Workgroup =
-// 64 tokens (4 M-tiles of 16) x one channel range; its 4 waves take
-// interleaved 32-channel steps.  Each step loads the r and b pieces once and
-// runs the MFMAs of all n streams against the Phi planes at k = j*C + c.
-// bf16 storage: every stream is exact in bf16, so P = X.(hi + mid + lo) (three
-// MFMAs per stream and N-tile).  fp32 storage: X is split into hi/mid/lo too
-// and the six products down to 2^-16 relative weight are kept, as in
-// proj_mfma_kernel.  p_part[ks][B][32], ss_part[ks][B].
+// TB = 16*MT tokens x one channel range, walked in stages of 128 channels:
+// the residual and branch pieces of a stage are loaded as whole 256-byte row
+// slices and staged in LDS; wave w takes the 32-channel step w of the stage,
+// forms the stream operands of its rows in registers and runs them against
+// the Phi fragments at k = j*C + c (1 KB contiguous loads in the fragment
+// order of phi_split_kernel).  bf16 storage: every stream is exact in bf16,
+// so P = X.(hi + mid + lo) (three MFMAs per stream and N-tile).  fp32
+// storage: X is split into hi/mid/lo too and the six products down to 2^-16
+// relative weight are kept, as in proj_mfma_kernel.  p_part[ks][B][32],
+// ss_part[ks][B].
+// Pipeline per stage s: the r/b pieces of s+1 load while s computes; the Phi
+// fragments of streams {0,1} and {2,3} reload right after their MFMAs, so
+// each half's next fragments load behind the other half's work.  Token
+// blocks start at different stages (concurrent blocks read different
+// columns).
 // ---------------------------------------------------------------------------
 typedef __bf16 wbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float wf32x4_t __attribute__((ext_vector_type(4)));
@@ -424,154 +434,247 @@ __device__ __forceinline__ void wsplit3(float v, float& h, float& m, float& l) {
     l = r - m;
 }
 
+__device__ __forceinline__ wu32x4_t wop(const uint4& q) { return wu32x4_t{q.x, q.y, q.z, q.w}; }
+
+template <typename TX> constexpr int wproj_mt() { return sizeof(TX) == 2 ? 4 : 2; }
+
+// Stream J's MFMA products for one M-tile: r/b hold the tile row's 8
+// channels (raw 16-byte pieces and their values), g the stream's 6 Phi
+// fragments (plane p, N-tile nt at index 2p + nt).
+template <typename TX, int J, bool DECAY>
+__device__ __forceinline__ void wproj_stream(const uint4 (&rw)[sizeof(TX) / 2], const uint4 (&bw)[sizeof(TX) / 2],
+                                             const float (&r)[8], const float (&b)[8], const uint4* g,
+                                             wf32x4_t (&acc)[2], float& ss) {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        x[e] = wrap_stream<TX, J, DECAY>(r[e], b[e]);
+        ss += x[e] * x[e];
+    }
+    if constexpr (sizeof(TX) == 2) {
+        wu32x4_t a;
+        if constexpr (J == 0) {
+            a = wop(rw[0]);
+        } else if constexpr (J == 1) {
+            a = wop(bw[0]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] = wpack(x[2 * e], x[2 * e + 1]);  // exact: x is a bf16 value
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+            for (int p = 0; p < 3; ++p) acc[nt] = wmfma16x16x32(a, wop(g[2 * p + nt]), acc[nt]);
+        }
+    } else {
+        wu32x4_t ah, am, al;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float h0, m0, l0, h1, m1, l1;
+            wsplit3(x[2 * e], h0, m0, l0);
+            wsplit3(x[2 * e + 1], h1, m1, l1);
+            ah[e] = wpack(h0, h1);
+            am[e] = wpack(m0, m1);
+            al[e] = wpack(l0, l1);
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            acc[nt] = wmfma16x16x32(ah, wop(g[0 + nt]), acc[nt]);
+            acc[nt] = wmfma16x16x32(ah, wop(g[2 + nt]), acc[nt]);
+            acc[nt] = wmfma16x16x32(am, wop(g[0 + nt]), acc[nt]);
+            acc[nt] = wmfma16x16x32(ah, wop(g[4 + nt]), acc[nt]);
+            acc[nt] = wmfma16x16x32(am, wop(g[2 + nt]), acc[nt]);
+            acc[nt] = wmfma16x16x32(al, wop(g[0 + nt]), acc[nt]);
+        }
+    }
+}
+
 template <typename TX, int N, bool DECAY>
-__global__ __launch_bounds__(256) void wrap_proj_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
-                                                        const bf16_t* __restrict__ phib, float* __restrict__ p_part,
-                                                        float* __restrict__ ss_part, int64_t B, int C,
-                                                        int64_t cchunk) {
-    constexpr int KP = 32;                       // padded projection rows
-    constexpr int W = 8 * (int)sizeof(TX) / 4;   // 32-bit words of 8 elements
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void wrap_proj_kernel(
+    const TX* __restrict__ res, const TX* __restrict__ br, const uint4* __restrict__ phif,
+    float* __restrict__ p_part, float* __restrict__ ss_part, int64_t B, int C, int64_t cchunk) {
+    constexpr int MT = wproj_mt<TX>();
+    constexpr int TB = 16 * MT;
+    constexpr int KP = 32;  // padded projection rows
+    constexpr int KS = 128;
+    constexpr int EPV = 16 / (int)sizeof(TX);
+    constexpr int VPR = KS / EPV;
+    constexpr int RPP = 256 / VPR;
+    constexpr int PASSES = TB / RPP;
+    constexpr int PITCH = KS * (int)sizeof(TX) + 16;
+    constexpr int XW = sizeof(TX) / 2;
     constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
-    __shared__ float red[3][36][64];
+    constexpr int NHA = NSTR < 2 ? NSTR : 2;           // streams of the first Phi half
+    constexpr int NHB = NSTR - NHA;
+    static_assert(N == 4, "wrapper projection is instantiated for n = 4");
+    static_assert(PASSES * RPP == TB, "stage rows");
+    static_assert(3 * 9 * MT * 64 * 4 <= 2 * 2 * TB * PITCH, "epilogue reuses the stage buffers");
+    __shared__ __align__(16) char xs[2][2][TB * PITCH];  // [buf][r | b]
+
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = (int)wave_uniform(threadIdx.x >> 6);
     const int row = lane & 15;
     const int kg = lane >> 4;
     const int64_t K = (int64_t)N * C;
-    const int64_t tok0 = (int64_t)blockIdx.x * 64;
+    const int64_t ksteps = K / 32;
+    const int64_t tok0 = (int64_t)blockIdx.x * TB;
     const int64_t cb = (int64_t)blockIdx.y * cchunk;
     const int64_t ce = (cb + cchunk < C) ? cb + cchunk : C;
+    const int64_t nst = ce > cb ? (ce - cb + KS - 1) / KS : 0;
 
-    wf32x4_t acc[4][2];
+    wf32x4_t acc[MT][2];
+    float ss[MT];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) {
+        acc[mt][0] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
+        acc[mt][1] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
+        ss[mt] = 0.f;
     }
-    float ss[4] = {0.f, 0.f, 0.f, 0.f};
-    int64_t rowoff[4];
-    uint32_t vmask[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const int64_t tok = tok0 + mt * 16 + row;
-        vmask[mt] = tok < B ? 0xffffffffu : 0u;
-        rowoff[mt] = (tok < B ? tok : 0) * C;
-    }
+    // rows of this block past the batch read zeros (resource range); the
+    // whole offset is per lane, so a column past C in the last row does too
+    const int64_t rows = (B - tok0 < TB) ? B - tok0 : TB;
+    const uint32_t xbytes = (uint32_t)(rows * C * (int64_t)sizeof(TX));
+    const buf_rsrc_t rrs = make_buf_rsrc(res + tok0 * C, xbytes);
+    const buf_rsrc_t brs = make_buf_rsrc(br + tok0 * C, xbytes);
+    const buf_rsrc_t prs = make_buf_rsrc(phif, (uint32_t)(6 * ksteps * 64 * 16));
+    const int lrow = threadIdx.x / VPR;
+    const int lvec = threadIdx.x % VPR;
+    const uint32_t xoff = (uint32_t)(((int64_t)lrow * C + lvec * EPV) * (int64_t)sizeof(TX));
+    const uint32_t xpass = (uint32_t)((int64_t)RPP * C * (int64_t)sizeof(TX));
+    const int64_t rot = nst > 0 ? (int64_t)blockIdx.x % nst : 0;
+    auto srot = [&](int64_t st) __attribute__((always_inline)) {
+        const int64_t r = st + rot;
+        return r < nst ? r : r - nst;
+    };
+    auto clampst = [&](int64_t st) __attribute__((always_inline)) { return st < nst ? st : (int64_t)0; };
 
-    for (int64_t c0 = cb + wave * 32; c0 < ce; c0 += 128) {
-        const int64_t cc = c0 + kg * 8;
-        // raw r and b words at channels cc..cc+7 of each M-tile row (rows past
-        // the batch read row 0 and are masked to zero)
-        uint32_t rw[4][W], bw[4][W];
+    uint4 F[2][PASSES];
+    uint4 GA[6 * (NHA > 0 ? NHA : 1)];
+    uint4 GB[6 * (NHB > 0 ? NHB : 1)];
+    auto fetch_x = [&](int64_t st) __attribute__((always_inline)) {
+        const uint32_t col = (uint32_t)((cb + srot(st) * KS) * (int64_t)sizeof(TX));
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-            for (int s4 = 0; s4 < W / 4; ++s4) {
-                const uint4 qr = ld16_nt(reinterpret_cast<const char*>(res + rowoff[mt] + cc) + 16 * s4);
-                const uint4 qb = ld16_nt(reinterpret_cast<const char*>(br + rowoff[mt] + cc) + 16 * s4);
-                rw[mt][4 * s4] = qr.x & vmask[mt]; rw[mt][4 * s4 + 1] = qr.y & vmask[mt];
-                rw[mt][4 * s4 + 2] = qr.z & vmask[mt]; rw[mt][4 * s4 + 3] = qr.w & vmask[mt];
-                bw[mt][4 * s4] = qb.x & vmask[mt]; bw[mt][4 * s4 + 1] = qb.y & vmask[mt];
-                bw[mt][4 * s4 + 2] = qb.z & vmask[mt]; bw[mt][4 * s4 + 3] = qb.w & vmask[mt];
-            }
+        for (int p = 0; p < PASSES; ++p) {
+            F[0][p] = buf_ld16<true, true>(rrs, xoff + p * xpass + col, 0u);
+            F[1][p] = buf_ld16<true, true>(brs, xoff + p * xpass + col, 0u);
         }
+    };
+    // Phi fragments of streams j0 .. j0+nj-1 at this wave's 32 channels of
+    // stage st (clamped to the last k step: past ce the operands are zero)
+    auto fetch_phi = [&](uint4* g, int j0, int nj, int64_t st) __attribute__((always_inline)) {
+        const int64_t c0 = cb + srot(st) * KS + wave * 32;
 #pragma unroll
-        for (int j = 0; j < NSTR; ++j) {
-            wu32x4_t bvp[3][2];
+        for (int jj = 0; jj < nj; ++jj) {
+            int64_t kstep = ((int64_t)(j0 + jj) * C + c0) / 32;
+            kstep = kstep < ksteps ? kstep : ksteps - 1;
+            const uint32_t so = (uint32_t)(kstep * 64 * 16);
 #pragma unroll
-            for (int p = 0; p < 3; ++p) {
+            for (int q = 0; q < 6; ++q)
+                g[6 * jj + q] = buf_ld16<false, true>(prs, (uint32_t)((q * ksteps * 64 + lane) * 16), so);
+        }
+    };
+    auto commit = [&](int64_t st, int buf) __attribute__((always_inline)) {
+        const uint32_t m = (cb + srot(st) * KS + lvec * EPV < ce) ? 0xffffffffu : 0u;
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                    bvp[p][nt] = *reinterpret_cast<const wu32x4_t*>(
-                        phib + (((int64_t)(p * 2 + nt) * (K / 32) + ((int64_t)j * C + c0) / 32) * 64 + lane) * 8);
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p)
+                *reinterpret_cast<uint4*>(&xs[buf][a][(lrow + p * RPP) * PITCH + lvec * 16]) =
+                    make_uint4(F[a][p].x & m, F[a][p].y & m, F[a][p].z & m, F[a][p].w & m);
+        }
+    };
+    // MFMAs of streams J0 (and J0 + 1 when two) against fragments g
+    auto compute_half = [&](int buf, const uint4* g, auto j0c, auto njc) __attribute__((always_inline)) {
+        constexpr int J0 = decltype(j0c)::value;
+        constexpr int NJ = decltype(njc)::value;
+        const int off = row * PITCH + (wave * 32 + kg * 8) * (int)sizeof(TX);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            uint4 rw[XW], bw[XW];
+#pragma unroll
+            for (int q = 0; q < XW; ++q) {
+                rw[q] = *reinterpret_cast<const uint4*>(&xs[buf][0][off + mt * 16 * PITCH + 16 * q]);
+                bw[q] = *reinterpret_cast<const uint4*>(&xs[buf][1][off + mt * 16 * PITCH + 16 * q]);
             }
+            float r[8], b[8];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                float xv[8];
+            for (int q = 0; q < XW; ++q) {
+                const uint32_t rr[4] = {rw[q].x, rw[q].y, rw[q].z, rw[q].w};
+                const uint32_t bb[4] = {bw[q].x, bw[q].y, bw[q].z, bw[q].w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    float r, b;
+                for (int e = 0; e < 4; ++e) {
                     if constexpr (sizeof(TX) == 2) {
-                        r = __uint_as_float((e & 1) ? (rw[mt][e >> 1] & 0xffff0000u) : (rw[mt][e >> 1] << 16));
-                        b = __uint_as_float((e & 1) ? (bw[mt][e >> 1] & 0xffff0000u) : (bw[mt][e >> 1] << 16));
+                        r[2 * e] = __uint_as_float(rr[e] << 16);
+                        r[2 * e + 1] = __uint_as_float(rr[e] & 0xffff0000u);
+                        b[2 * e] = __uint_as_float(bb[e] << 16);
+                        b[2 * e + 1] = __uint_as_float(bb[e] & 0xffff0000u);
                     } else {
-                        r = __uint_as_float(rw[mt][e]);
-                        b = __uint_as_float(bw[mt][e]);
-                    }
-                    float x[N];
-                    wrap_streams<TX, N, DECAY>(r, b, x);
-                    xv[e] = x[j];
-                    ss[mt] += x[j] * x[j];
-                }
-                if constexpr (sizeof(TX) == 2) {
-                    wu32x4_t a;
-                    if (j == 0) {
-                        a = wu32x4_t{rw[mt][0], rw[mt][1], rw[mt][2], rw[mt][3]};
-                    } else if (j == 1) {
-                        a = wu32x4_t{bw[mt][0], bw[mt][1], bw[mt][2], bw[mt][3]};
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) a[e] = wpack(xv[2 * e], xv[2 * e + 1]);
-                    }
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) {
-#pragma unroll
-                        for (int p = 0; p < 3; ++p) acc[mt][nt] = wmfma16x16x32(a, bvp[p][nt], acc[mt][nt]);
-                    }
-                } else {
-                    wu32x4_t ah, am, al;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float h0, m0, l0, h1, m1, l1;
-                        wsplit3(xv[2 * e], h0, m0, l0);
-                        wsplit3(xv[2 * e + 1], h1, m1, l1);
-                        ah[e] = wpack(h0, h1);
-                        am[e] = wpack(m0, m1);
-                        al[e] = wpack(l0, l1);
-                    }
-#pragma unroll
-                    for (int nt = 0; nt < 2; ++nt) {
-                        acc[mt][nt] = wmfma16x16x32(ah, bvp[0][nt], acc[mt][nt]);
-                        acc[mt][nt] = wmfma16x16x32(ah, bvp[1][nt], acc[mt][nt]);
-                        acc[mt][nt] = wmfma16x16x32(am, bvp[0][nt], acc[mt][nt]);
-                        acc[mt][nt] = wmfma16x16x32(ah, bvp[2][nt], acc[mt][nt]);
-                        acc[mt][nt] = wmfma16x16x32(am, bvp[1][nt], acc[mt][nt]);
-                        acc[mt][nt] = wmfma16x16x32(al, bvp[0][nt], acc[mt][nt]);
+                        r[4 * q + e] = __uint_as_float(rr[e]);
+                        b[4 * q + e] = __uint_as_float(bb[e]);
                     }
                 }
             }
+            if constexpr (NJ > 0) wproj_stream<TX, J0, DECAY>(rw, bw, r, b, g, acc[mt], ss[mt]);
+            if constexpr (NJ > 1) wproj_stream<TX, J0 + 1, DECAY>(rw, bw, r, b, g + 6, acc[mt], ss[mt]);
+        }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I2 = std::integral_constant<int, 2>;
+    using IHA = std::integral_constant<int, NHA>;
+    using IHB = std::integral_constant<int, NHB>;
+
+    if (nst > 0) {
+        fetch_x(0);
+        fetch_phi(GA, 0, NHA, 0);
+        if constexpr (NHB > 0) fetch_phi(GB, 2, NHB, 0);
+        commit(0, 0);
+        __syncthreads();
+        for (int64_t st = 0; st < nst; ++st) {
+            const int buf = (int)(st & 1);
+            fetch_x(clampst(st + 1));
+            __builtin_amdgcn_sched_barrier(0);
+            compute_half(buf, GA, I0{}, IHA{});
+            fetch_phi(GA, 0, NHA, clampst(st + 1));
+            if constexpr (NHB > 0) {
+                compute_half(buf, GB, I2{}, IHB{});
+                fetch_phi(GB, 2, NHB, clampst(st + 1));
+            }
+            commit(clampst(st + 1), buf ^ 1);
+            __syncthreads();
         }
     }
+    __syncthreads();  // the stage buffers become the cross-wave reduction area
+    float (*red)[9 * MT][64] = reinterpret_cast<float (*)[9 * MT][64]>(&xs[0][0][0]);
 
     // waves 1..3 hand their partials to wave 0 through LDS
     if (wave > 0) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) red[wave - 1][(mt * 2 + nt) * 4 + i][lane] = acc[mt][nt][i];
             }
-            red[wave - 1][32 + mt][lane] = ss[mt];
+            red[wave - 1][8 * MT + mt][lane] = ss[mt];
         }
     }
     __syncthreads();
     if (wave != 0) return;
-#pragma unroll
+#pragma unroll 1
     for (int q = 0; q < 3; ++q) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[mt][nt][i] += red[q][(mt * 2 + nt) * 4 + i][lane];
             }
-            ss[mt] += red[q][32 + mt][lane];
+            ss[mt] += red[q][8 * MT + mt][lane];
         }
     }
     float* pp = p_part + (int64_t)blockIdx.y * B * KP;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t tok = tok0 + mt * 16 + kg * 4 + i;
@@ -1030,13 +1133,15 @@ hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const vo
                             float* p_part, float* ss_part, int64_t B, int64_t C, int ks, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (n != 4 || C % 32 != 0) return hipErrorInvalidValue;
+    if (C > (int64_t(1) << 20)) return hipErrorInvalidValue;  // 32-bit buffer offsets
     int64_t cchunk = (C + ks - 1) / ks;
     cchunk = ((cchunk + 127) / 128) * 128;
-    const dim3 grid((unsigned)((B + 63) / 64), (unsigned)ks);
+    const uint4* phif = reinterpret_cast<const uint4*>(phib);
     const int tok = timing_begin("wrap_proj", s);
 #define MHC_WP(TX_, D_)                                                                                          \
-    hipLaunchKernelGGL((wrap_proj_kernel<TX_, 4, D_>), grid, dim3(256), 0, s, (const TX_*)res, (const TX_*)br,   \
-                       phib, p_part, ss_part, B, (int)C, cchunk)
+    hipLaunchKernelGGL((wrap_proj_kernel<TX_, 4, D_>),                                                           \
+                       dim3((unsigned)((B + 16 * wproj_mt<TX_>() - 1) / (16 * wproj_mt<TX_>())), (unsigned)ks),   \
+                       dim3(256), 0, s, (const TX_*)res, (const TX_*)br, phif, p_part, ss_part, B, (int)C, cchunk)
     if (dt == kBF16) {
         if (decay) { MHC_WP(bf16_t, true); } else { MHC_WP(bf16_t, false); }
     } else {
