@@ -125,8 +125,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     const int wave = (int)wave_uniform(threadIdx.x >> 6);
     const int row = lane & 15;
     const int kg = lane >> 4;
-    const int64_t tok0 = (int64_t)blockIdx.x * TB;
-    const int64_t kb = (int64_t)blockIdx.y * kchunk;
+    // block -> (token block, K split) from the linear id with the K split
+    // fastest: workgroups go round-robin over the 8 XCDs by linear id, so
+    // with ks a multiple of 8 each XCD serves only its own K splits (and
+    // holds only their part of Phi in its L2)
+    const int64_t lin = (int64_t)blockIdx.x + (int64_t)blockIdx.y * gridDim.x;
+    const int64_t ksplit = lin % gridDim.y;
+    const int64_t tblk = lin / gridDim.y;
+    const int64_t tok0 = tblk * TB;
+    const int64_t kb = ksplit * kchunk;
     const int64_t ke = (kb + kchunk < K) ? kb + kchunk : K;
     const int64_t nst = ke > kb ? (ke - kb + KS - 1) / KS : 0;
     const int64_t ksteps = K / 32;
@@ -152,11 +159,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     // The whole x offset is per lane: the range check covers the lane offset
     // only, so a column past K in the block's last row reads zeros instead
     // of memory past the tensor.  Columns past ke are zeroed at commit.
-    // Token blocks start at different stages of their K range, so the
-    // workgroups reading one K range at a time spread over its columns (and
-    // the memory channels) instead of all reading the same 256 bytes of
-    // their rows when the row pitch is a multiple of the channel period.
-    const int64_t rot = nst > 0 ? (int64_t)blockIdx.x % nst : 0;
+    // Blocks start at different stages of their K range, so the workgroups
+    // reading one K range at a time spread over its columns (and the memory
+    // channels) instead of all reading the same 256 bytes of their rows when
+    // the row pitch is a multiple of the channel period.  With ks a multiple
+    // of 8 the start goes by token block (an XCD's Phi is its K splits'
+    // part); otherwise by XCD, so the blocks of one XCD move through a small
+    // window of Phi that stays in its L2.
+    const int64_t rot = nst <= 0 ? 0 : (gridDim.y % 8 == 0 ? tblk % nst : ((lin % 8) * nst) / 8);
     auto srot = [&](int64_t st) __attribute__((always_inline)) {
         const int64_t r = st + rot;
         return r < nst ? r : r - nst;
@@ -290,7 +300,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             ss[mt] += red[q][8 * MT + mt][lane];
         }
     }
-    float* pp = p_part + (int64_t)blockIdx.y * B * kNPad;
+    float* pp = p_part + ksplit * B * kNPad;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -306,7 +316,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         s2 += __shfl_xor(s2, 16, kWave);
         s2 += __shfl_xor(s2, 32, kWave);
         const int64_t tok = tok0 + mt * 16 + row;
-        if (kg == 0 && tok < B) ss_part[(int64_t)blockIdx.y * B + tok] = s2;
+        if (kg == 0 && tok < B) ss_part[ksplit * B + tok] = s2;
     }
 }
 

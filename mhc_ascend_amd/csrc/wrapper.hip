@@ -412,9 +412,9 @@ __global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, 
 // ss_part[ks][B].
 // Pipeline per stage s: the r/b pieces of s+1 load while s computes; the Phi
 // fragments of streams {0,1} and {2,3} reload right after their MFMAs, so
-// each half's next fragments load behind the other half's work.  Token
-// blocks start at different stages (concurrent blocks read different
-// columns).
+// each half's next fragments load behind the other half's work.  Blocks
+// start at different stages by XCD: concurrent XCDs read different columns,
+// and the blocks of one XCD share a small window of Phi in its L2.
 // ---------------------------------------------------------------------------
 typedef __bf16 wbf16x8_t __attribute__((ext_vector_type(8)));
 typedef float wf32x4_t __attribute__((ext_vector_type(4)));
@@ -541,7 +541,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
     const int lvec = threadIdx.x % VPR;
     const uint32_t xoff = (uint32_t)(((int64_t)lrow * C + lvec * EPV) * (int64_t)sizeof(TX));
     const uint32_t xpass = (uint32_t)((int64_t)RPP * C * (int64_t)sizeof(TX));
-    const int64_t rot = nst > 0 ? (int64_t)blockIdx.x % nst : 0;
+    // start stage by XCD (workgroups go round-robin over the 8 XCDs)
+    const int64_t xcd = ((int64_t)blockIdx.x + (int64_t)blockIdx.y * gridDim.x) % 8;
+    const int64_t rot = nst > 0 ? (xcd * nst) / 8 : 0;
     auto srot = [&](int64_t st) __attribute__((always_inline)) {
         const int64_t r = st + rot;
         return r < nst ? r : r - nst;
