@@ -1,6 +1,6 @@
 """Benchmark of the mHC layer forward+backward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload static|dynamic|wrapper]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload static|dynamic|wrapper|ops]
 
 Prints ONE JSON line: tokens/s of the whole fwd+bwd step, the achieved HBM
 GB/s from algorithmic bytes, the roofline of the dominant kernel (HIP-event
@@ -12,6 +12,8 @@ Workloads (the metric is quoted at n=4, C=4096):
   static  - C3: MHCLayer static-H, x fp32 [8192, 4, 4096]          (default)
   dynamic - C4: MHCLayer dynamic-H, x bf16 [8192, 4, 4096], phi [16384, 24]
   wrapper - C5: MHCResidualWrapper, residual/branch bf16 [65536, 4, 7168]
+  ops     - C2: standalone sinkhorn_knopp / rmsnorm / stream_aggregate fwd+bwd
+            (value = the step's achieved HBM GB/s)
 Inputs are synthetic (seeded N(0,1)) and already resident in HBM; each step
 uses the next of several rotating input sets (together well above the
 256 MB MALL) so no step reads the previous step's data from cache.
@@ -304,9 +306,104 @@ class WrapperWorkload:
                            f"on {tok} of {self.tokens} tokens, n={self.n}, C={self.C}; median of {runs} runs")
 
 
-WORKLOADS = {"static": StaticWorkload, "dynamic": DynamicWorkload, "wrapper": WrapperWorkload}
+class OpsWorkload:
+    """C2: the standalone operators, fp32, forward + backward through autograd:
+    sinkhorn_knopp [65536, 4, 4] ~U(0,1) (20 iterations, eps 1e-8), rmsnorm
+    [16384, 4096] with weight ~N(1, 0.1) (eps 1e-5), stream_aggregate
+    [16384, 4, 4096] with H_pre ~N(0,1) [16384, 4].  The reported value is the
+    step's achieved HBM GB/s over the algorithmic bytes of all six kernels."""
+
+    name = "ops"
+    S, R, n, C = 65536, 16384, 4, 4096
+    dtype = "f32"
+    sets = 2
+    metric = "mHC standalone ops (sinkhorn, rmsnorm, stream_aggregate) fwd+bwd achieved HBM GB/s (C2)"
+    unit = "GB/s"
+
+    def __init__(self, torch, mhc, device):
+        self.torch, self.mhc = torch, mhc
+        S, R, n, C = self.S, self.R, self.n, self.C
+        g = torch.Generator(device=device).manual_seed(0)
+        rnd = lambda *shape: torch.randn(*shape, device=device, generator=g)
+        self.sk = [torch.rand(S, n, n, device=device, generator=g).requires_grad_(True) for _ in range(self.sets)]
+        self.gsk = [rnd(S, n, n) for _ in range(self.sets)]
+        self.rx = [rnd(R, C).requires_grad_(True) for _ in range(self.sets)]
+        self.rw = (1.0 + 0.1 * rnd(C)).requires_grad_(True)
+        self.gr = [rnd(R, C) for _ in range(self.sets)]
+        self.ax = [rnd(R, n, C).requires_grad_(True) for _ in range(self.sets)]
+        self.ah = [rnd(R, n).requires_grad_(True) for _ in range(self.sets)]
+        self.ga = [rnd(R, C) for _ in range(self.sets)]
+        self.i = 0
+
+    def step(self):
+        k = self.i % self.sets
+        self.i += 1
+        ag = self.torch.autograd.grad
+        m = self.mhc
+        o1 = m.sinkhorn_knopp(self.sk[k], 20, 1e-8)
+        r1 = ag(o1, [self.sk[k]], self.gsk[k])
+        o2 = m.rmsnorm(self.rx[k], self.rw, 1e-5)
+        r2 = ag(o2, [self.rx[k], self.rw], self.gr[k])
+        o3 = m.stream_aggregate(self.ax[k], self.ah[k])
+        r3 = ag(o3, [self.ax[k], self.ah[k]], self.ga[k])
+        return r1, r2, r3
+
+    @property
+    def tokens(self):
+        return self.R
+
+    def kernel_bytes(self):
+        S, R, n, C = self.S, self.R, self.n, self.C
+        sk = S * n * n * 4
+        row = R * C * 4
+        return {
+            "sinkhorn_fwd": 2 * sk,                               # read inp, write out
+            "sinkhorn_bwd": 3 * sk,                               # read grad, inp; write grad_inp
+            "rmsnorm_fwd": 2 * row + C * 4 + R * 4,               # read x, w; write y, rms
+            "rmsnorm_bwd": 3 * row + C * 4 + R * 4 + C * 4,       # read g, x, w, rms; write dx, dw
+            "aggregate_fwd": n * row + row + R * n * 4 * 2,       # read x, H; write out, H_act
+            "aggregate_bwd": row + 2 * n * row + R * n * 4 * 2,   # read g, x, H_act; write dx, dH
+        }
+
+    def step_bytes(self):
+        return sum(self.kernel_bytes().values())
+
+    def flops(self):
+        return {}
+
+    def config(self):
+        return {"workload": "C2 standalone ops fwd+bwd", "sinkhorn": [self.S, self.n, self.n], "sinkhorn_iters": 20,
+                "rmsnorm": [self.R, self.C], "stream_aggregate": [self.R, self.n, self.C], "x_dtype": "f32"}
+
+    def cpu_baseline(self, torch, R, seconds):
+        """The oracle's three ops fwd+bwd (autograd) on a row sample; returns
+        the achieved GB/s of the same algorithmic bytes, scaled to the sample."""
+        rows, mats = 256, 1024
+        g = torch.Generator().manual_seed(1)
+        sk = torch.rand(mats, self.n, self.n, generator=g).requires_grad_(True)
+        x = torch.randn(rows, self.C, generator=g).requires_grad_(True)
+        w = (1.0 + 0.1 * torch.randn(self.C, generator=g)).requires_grad_(True)
+        ax = torch.randn(rows, self.n, self.C, generator=g).requires_grad_(True)
+        ah = torch.randn(rows, self.n, generator=g).requires_grad_(True)
+
+        def run():
+            R.sinkhorn_knopp(sk, 20, 1e-8).sum().backward()
+            R.rmsnorm(x, w, 1e-5)[0].sum().backward()
+            R.stream_aggregate(ax, ah)[0].sum().backward()
+
+        med, runs = _timed_cpu(run, seconds)
+        kb = self.kernel_bytes()
+        sample_bytes = (kb["sinkhorn_fwd"] + kb["sinkhorn_bwd"]) * mats / self.S + \
+            (kb["rmsnorm_fwd"] + kb["rmsnorm_bwd"] + kb["aggregate_fwd"] + kb["aggregate_bwd"]) * rows / self.R
+        return sample_bytes / med / 1e9, (f"oracle.reference sinkhorn_knopp ({mats} matrices), rmsnorm and "
+                                          f"stream_aggregate ({rows} rows) fp32 fwd+bwd (autograd); GB/s of the "
+                                          f"same algorithmic bytes scaled to the sample; median of {runs} runs")
+
+
+WORKLOADS = {"static": StaticWorkload, "dynamic": DynamicWorkload, "wrapper": WrapperWorkload, "ops": OpsWorkload}
 KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "wrap_proj", "wrap_fwd", "wrap_bwd",
-           "wrap_bwd_reduce", "wrap_proj_bwd")
+           "wrap_bwd_reduce", "wrap_proj_bwd", "sinkhorn_fwd", "sinkhorn_bwd", "rmsnorm_fwd", "rmsnorm_bwd",
+           "aggregate_fwd", "aggregate_bwd")
 
 
 # ---------------------------------------------------------------------------
@@ -401,12 +498,14 @@ def main(argv=None) -> int:
         torch.set_num_threads(cores)
         print(f"[bench] CPU baseline on {cores} cores for ~{a.cpu_seconds:.0f} s", file=sys.stderr, flush=True)
         v, sample = wl.cpu_baseline(torch, R, a.cpu_seconds)
-        cpu = {"value": v, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port", "sample": sample}
+        cpu = {"value": v, "unit": getattr(wl, "unit", "tokens/s"), "cores": torch.get_num_threads(), "kind": "port",
+               "sample": sample}
 
+    ops = getattr(wl, "unit", "tokens/s") == "GB/s"
     rec = {
-        "metric": METRIC,
-        "value": tokens_per_s,
-        "unit": "tokens/s",
+        "metric": getattr(wl, "metric", METRIC),
+        "value": step_gbps if ops else tokens_per_s,
+        "unit": getattr(wl, "unit", "tokens/s"),
         "n_gpus": 1,
         "steps": steps,
         "warmup": a.warmup,
