@@ -476,6 +476,142 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// n = 4: one token per 16-lane DPP row.  Lane l holds element (l/4, l%4) of
+// t_res and, for l < 8, t_pre[l] (l < 4) or t_post[l-4] (the coefficient
+// order), so the Sinkhorn iterations are a few DPP steps per lane
+// (sk16_forward / sk16_backward) and the per-token loads and stores are
+// contiguous.  Lanes of tokens past the batch compute on token 0 and store
+// nothing.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dyn_coef16_fwd_kernel(
+    const float* __restrict__ p_part, const float* __restrict__ ss_part, int ks, int64_t B, int64_t K,
+    const float* __restrict__ a_pre, const float* __restrict__ a_post, const float* __restrict__ a_res,
+    const float* __restrict__ b_pre, const float* __restrict__ b_post, const float* __restrict__ b_res,
+    float* __restrict__ coef, float* __restrict__ p_out, float* __restrict__ rh, int iters, float sk_eps,
+    float rms_eps) {
+    constexpr int N = 4;
+    constexpr int NP = 2 * N + N * N;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t tok = gid >> 4;
+    const int l = (int)(gid & 15);
+    const bool tv = tok < B;
+    const int64_t tk = tv ? tok : 0;
+    float pres = 0.f, ppq = 0.f, ss = 0.f;
+    for (int q = 0; q < ks; ++q) {
+        const float* pb = p_part + ((int64_t)q * B + tk) * kNPad;
+        ss += ss_part[(int64_t)q * B + tk];
+        pres += pb[2 * N + l];
+        ppq += pb[l & 7];
+    }
+    const float r_h = sqrtf(ss / (float)K + rms_eps);
+    const float inv = 1.f / r_h;
+    const float h = (l < N) ? sigmoidf(ppq * a_pre[0] * inv + b_pre[l & 3])
+                            : 2.f * sigmoidf(ppq * a_post[0] * inv + b_post[(l - N) & 3]);
+    float e = expf(pres * a_res[0] * inv + b_res[l]);
+    sk16_forward(e, iters, sk_eps);
+    if (tv) {
+        float* cf = coef + tok * NP;
+        float* po = p_out + tok * NP;
+        cf[2 * N + l] = e;
+        po[2 * N + l] = pres;
+        if (l < 2 * N) {
+            cf[l] = h;
+            po[l] = ppq;
+        }
+        if (l == 0) rh[tok] = r_h;
+    }
+}
+
+int dyn_coef16_bwd_blocks(int64_t B) {
+    int64_t g = (B + 15) / 16;
+    if (g > 1024) g = 1024;
+    return (int)(g < 1 ? 1 : g);
+}
+
+// Backward of dyn_coef16_fwd_kernel (the formulas of dyn_coef_bwd_kernel).
+// Workgroups stride over groups of 16 tokens; each lane sums its db / dalpha
+// terms over its tokens in order, then the block reduces them into
+// part[blk][27] = (db_pre[4], db_post[4], db_res[16], dalpha_pre, dalpha_post,
+// dalpha_res).
+__global__ __launch_bounds__(256) void dyn_coef16_bwd_kernel(
+    const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
+    const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
+    const float* __restrict__ a_post, const float* __restrict__ a_res, const float* __restrict__ b_res,
+    float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int iters, float sk_eps) {
+    constexpr int N = 4;
+    constexpr int NP = 2 * N + N * N;
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NV = NP + 3;
+    __shared__ float red[4][NV];
+    const int l = threadIdx.x & 15;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const float ap = a_pre[0], aq = a_post[0], ar = a_res[0];
+    const float apq = (l < N) ? ap : aq;
+    float acc_pp = 0.f, acc_res = 0.f, acc_a = 0.f, acc_b = 0.f, acc_c = 0.f;
+    const int64_t groups = (B + 15) / 16;
+    for (int64_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {  // uniform trip count per block
+        const int64_t tok = grp * 16 + (threadIdx.x >> 4);
+        const bool tv = tok < B;
+        const int64_t tk = tv ? tok : 0;
+        const float* sc = scal + tk * (NS + 2);
+        const float* cf = coef + tk * NP;
+        const float* pv = p + tk * NP;
+        const float inv = 1.f / rh[tk];
+        const float pr = pv[2 * N + l];
+        const float e = expf(pr * ar * inv + b_res[l]);
+        float g = sc[l];  // dM element
+        sk16_backward(g, e, iters, sk_eps);
+        const float dt_res = g * e;
+        const float hv = cf[l & 7];
+        // dh_post_act[q] at sc[N*N + q], dh_pre_act[q] at sc[N*N + N + q]
+        const float dh = (l < N) ? sc[N * N + N + (l & 3)] : sc[N * N + ((l - N) & 3)];
+        const float dt_pp = (l < N) ? dh * hv * (1.f - hv) : dh * hv * (1.f - 0.5f * hv);
+        const float lpp = (l < 2 * N) ? dt_pp * pv[l & 7] : 0.f;  // l_pre or l_post
+        const float lres = dt_res * pr;
+        const float tot = group_sum<16>(apq * lpp + ar * lres);
+        if (tv) {
+            float* dp = dp_out + tok * kNPad;
+            dp[2 * N + l] = ar * dt_res * inv;
+            if (l < 2 * N) dp[l] = apq * dt_pp * inv;
+            else dp[2 * N + N * N + (l - 2 * N)] = 0.f;  // padding entries 24..31
+            if (l == 0) s_out[tok] = -tot * inv * inv * inv / (float)K;
+            if (l < 2 * N) acc_pp += dt_pp;
+            acc_res += dt_res;
+            if (l < N) acc_a += lpp * inv;
+            else if (l < 2 * N) acc_b += lpp * inv;
+            acc_c += lres * inv;
+        }
+    }
+    // lanes of one slot: l, l+16, l+32, l+48 of every wave, then the waves
+    acc_a = group_sum<16>(acc_a);
+    acc_b = group_sum<16>(acc_b);
+    acc_c = group_sum<16>(acc_c);
+    float v[5] = {acc_pp, acc_res, acc_a, acc_b, acc_c};
+#pragma unroll
+    for (int k = 0; k < 5; ++k) {
+        v[k] += __shfl_xor(v[k], 16, kWave);
+        v[k] += __shfl_xor(v[k], 32, kWave);
+    }
+    if (lane < 16) {
+        if (l < 2 * N) red[wave][l] = v[0];
+        red[wave][2 * N + l] = v[1];
+        if (l == 0) {
+            red[wave][NP] = v[2];
+            red[wave][NP + 1] = v[3];
+            red[wave][NP + 2] = v[4];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < NV) {
+        const int nw = blockDim.x >> 6;
+        float t = 0.f;
+        for (int w = 0; w < nw; ++w) t += red[w][threadIdx.x];
+        part[(int64_t)blockIdx.x * NV + threadIdx.x] = t;
+    }
+}
+
 // out[c] = sum_r part[r][c] for a few columns (db, dalpha); one workgroup of
 // 32 columns x 32 row phases, each phase summing every 32nd row in order and
 // the phases added in order (deterministic).
@@ -878,6 +1014,12 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
                                const float* b_post, const float* b_res, float* coef, float* p_out, float* rh,
                                int iters, float sk_eps, float rms_eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
+    if (n == 4) {
+        hipLaunchKernelGGL(dyn_coef16_fwd_kernel, dim3((unsigned)((B * 16 + 255) / 256)), dim3(256), 0, s, p_part,
+                           ss_part, ks, B, K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, iters,
+                           sk_eps, rms_eps);
+        return hipGetLastError();
+    }
     const int64_t threads = B * pow2ceil(n);
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     MHC_DYN_N(n, hipLaunchKernelGGL((dyn_coef_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, p_part, ss_part, ks, B,
@@ -886,7 +1028,10 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
     return hipGetLastError();
 }
 
-int dyn_coef_bwd_blocks(int n, int64_t B) { return (int)((B * pow2ceil(n) + 255) / 256); }
+int dyn_coef_bwd_blocks(int n, int64_t B) {
+    if (n == 4) return dyn_coef16_bwd_blocks(B);
+    return (int)((B * pow2ceil(n) + 255) / 256);
+}
 
 hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
@@ -894,6 +1039,11 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                                hipStream_t s) {
     if (B == 0) return hipSuccess;
     const unsigned blocks = (unsigned)dyn_coef_bwd_blocks(n, B);
+    if (n == 4) {
+        hipLaunchKernelGGL(dyn_coef16_bwd_kernel, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K, a_pre, a_post,
+                           a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        return hipGetLastError();
+    }
     MHC_DYN_N(n, hipLaunchKernelGGL((dyn_coef_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
                                     a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps));
     return hipGetLastError();

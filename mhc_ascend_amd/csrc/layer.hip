@@ -415,10 +415,11 @@ __global__ __launch_bounds__(256) void column_partial_kernel(const float* __rest
     }
 }
 
-// Blocks [0, ceil(cols/64)) finish the column sums of stage[rsplit][cols]
+// The first blocks finish the column sums of stage[rsplit][cols]
 // (per-workgroup partials, or their first-pass sums when there are many)
-// and store them in the weight's dtype: 64 columns per block, blockDim/64
-// row phases (up to 16, from the row count), fixed summation order.  With N > 0 the last block also forms the static
+// and store them in the weight's dtype: 256 lanes per block as `phases` row
+// phases (1, 2 or 4, from the row count) x 256/phases columns, fixed
+// summation order.  With N > 0 the last block also forms the static
 // parameter gradients from the per-workgroup sums of
 // [dM, dh_post_act, dh_pre_act]: the activation derivatives (ops.py:172,
 // 240-242) and ONE Sinkhorn backward on the token-summed dM (M is shared, so
@@ -432,43 +433,48 @@ constexpr int kColSplit = 16;   // row groups of the first pass when rows are ma
 constexpr int kDirectRows = 512;  // partial rows the finalize sums directly
 
 template <int N, typename TW>
-__global__ __launch_bounds__(1024) void layer_finalize_kernel(
+__global__ __launch_bounds__(256) void layer_finalize_kernel(
     const float* __restrict__ stage, int rsplit, int64_t cols, TW* __restrict__ dw,
     const float* __restrict__ scal_part, int rows, const float* __restrict__ h_pre,
     const float* __restrict__ h_post, const float* __restrict__ h_res, float* __restrict__ d_h_pre,
-    float* __restrict__ d_h_post, float* __restrict__ d_h_res, int iters, float eps) {
-    const int col_blocks = (int)((cols + 63) / 64);
+    float* __restrict__ d_h_post, float* __restrict__ d_h_res, int iters, float eps, int phases) {
+    // column blocks: 256 lanes = `phases` row phases x (256 / phases) columns
+    const int cpb = 256 / phases;
+    const int col_blocks = (int)((cols + cpb - 1) / cpb);
     if ((int)blockIdx.x < col_blocks) {
-        __shared__ float cred[16][64];
-        const int lane = threadIdx.x & 63;
-        const int ph = threadIdx.x >> 6;
-        const int nph = blockDim.x >> 6;
-        const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+        __shared__ float cred[256];
+        const int cl = threadIdx.x % cpb;
+        const int ph = threadIdx.x / cpb;
+        const int64_t c = (int64_t)blockIdx.x * cpb + cl;
         float s = 0.f;
         if (c < cols) {
             // 8 loads in flight per step, fixed summation order
             int r = ph;
-            for (; r + 7 * nph < rsplit; r += 8 * nph) {
+            for (; r + 7 * phases < rsplit; r += 8 * phases) {
                 float a[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) a[u] = stage[(int64_t)(r + u * nph) * cols + c];
+                for (int u = 0; u < 8; ++u) a[u] = stage[(int64_t)(r + u * phases) * cols + c];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) s += a[u];
             }
-            for (; r < rsplit; r += nph) s += stage[(int64_t)r * cols + c];
+            for (; r < rsplit; r += phases) s += stage[(int64_t)r * cols + c];
         }
-        cred[ph][lane] = s;
+        if (phases == 1) {
+            if (c < cols) VecIO<TW>::put(dw + c, s);
+            return;
+        }
+        cred[threadIdx.x] = s;
         __syncthreads();
         if (ph == 0 && c < cols) {
             float t = 0.f;
-            for (int k = 0; k < nph; ++k) t += cred[k][lane];
+            for (int k = 0; k < phases; ++k) t += cred[k * cpb + cl];
             VecIO<TW>::put(dw + c, t);
         }
         return;
     }
     if constexpr (N > 0) {
         constexpr int NS = N * N + 2 * N;
-        __shared__ float red[16 * NS];
+        __shared__ float red[4 * NS];
         float v[NS];
 #pragma unroll
         for (int k = 0; k < NS; ++k) v[k] = 0.f;
@@ -710,19 +716,19 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
                                  const float* scal_part, int rows, const float* h_pre, const float* h_post,
                                  const float* h_res, float* d_h_pre, float* d_h_post, float* d_h_res, int iters,
                                  float sk_eps, hipStream_t s) {
-    const unsigned col_blocks = (unsigned)((cols + 63) / 64);
+    // row phases per 256-lane column block: one for a few partial rows (each
+    // lane sums its column), more for many rows; the static scalar block
+    // (n > 0) runs with the same 256 lanes
+    const int phases = rsplit <= 16 ? 1 : (rsplit <= 64 ? 2 : 4);
+    const int64_t cpb = 256 / phases;
+    const unsigned col_blocks = (unsigned)((cols + cpb - 1) / cpb);
     const unsigned blocks = col_blocks + (n > 0 ? 1 : 0);
     if (blocks == 0) return hipSuccess;
-    // row phases per column block (64 lanes each): up to 16 for many partial
-    // rows; with the static scalar block (n > 0) exactly 4, since its
-    // reductions cost more with more waves and it is the longer block
-    int phases = 1;
-    while (phases < 16 && phases < rsplit) phases *= 2;
-    if (n > 0) phases = 4;
-    const unsigned threads = 64u * (unsigned)phases;
+    const unsigned threads = 256;
 #define MHC_FIN_LAUNCH(N_, TW_)                                                                                  \
     hipLaunchKernelGGL((layer_finalize_kernel<N_, TW_>), dim3(blocks), dim3(threads), 0, s, stage, rsplit, cols,  \
-                       (TW_*)dw, scal_part, rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps)
+                       (TW_*)dw, scal_part, rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, \
+                       phases)
     if (n == 0) {
         if (w_dtype == kBF16) { MHC_FIN_LAUNCH(0, bf16_t); } else { MHC_FIN_LAUNCH(0, float); }
     } else {

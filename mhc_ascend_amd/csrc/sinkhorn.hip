@@ -6,7 +6,8 @@
 // column sums are lane-group butterflies.  The backward keeps the forward
 // history (post-row-step rows and row sums) in registers and applies the
 // exact adjoint (the reference's row step is approximate,
-// sinkhorn_knopp.cpp:1773-1795).
+// sinkhorn_knopp.cpp:1773-1795).  Small n = 4 batches run one element per
+// lane of a 16-lane DPP row instead (sk16_* in mhc_device.h).
 #include "mhc_device.h"
 #include "mhc_internal.h"
 
@@ -74,6 +75,33 @@ __global__ __launch_bounds__(256) void sinkhorn_bwd_kernel(const float* __restri
     if (ok) store_row<N>(grad_inp + m * N * N + r * N, g);
 }
 
+// n = 4: one matrix per 16-lane DPP row, one element per lane (lane 4 r + c);
+// the loads and stores are one contiguous float per lane.  The chain per
+// matrix is about 4x shorter than with one row per lane but issues more
+// instructions in total, so it is used for batches that leave the chip
+// latency-bound; large batches (throughput-bound) keep one row per lane.
+constexpr int64_t kSk16MaxBatch = 16384;
+__global__ __launch_bounds__(256) void sinkhorn16_fwd_kernel(const float* __restrict__ inp, float* __restrict__ out,
+                                                             int64_t batch, int iters, float eps) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool ok = gid < batch * 16;
+    float a = ok ? inp[gid] : 0.f;
+    sk16_forward(a, iters, eps);
+    if (ok) out[gid] = a;
+}
+
+__global__ __launch_bounds__(256) void sinkhorn16_bwd_kernel(const float* __restrict__ grad_out,
+                                                             const float* __restrict__ inp,
+                                                             float* __restrict__ grad_inp, int64_t batch, int iters,
+                                                             float eps) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const bool ok = gid < batch * 16;
+    float g = ok ? grad_out[gid] : 0.f;
+    const float x0 = ok ? inp[gid] : 0.f;
+    sk16_backward(g, x0, iters, eps);
+    if (ok) grad_inp[gid] = g;
+}
+
 #define MHC_SK_DISPATCH(n, ...)                                   \
     switch (n) {                                                  \
         case 1: { constexpr int N_ = 1; __VA_ARGS__; break; }     \
@@ -94,8 +122,13 @@ hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batc
     const int64_t threads = batch * G;
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     const int tok = timing_begin("sinkhorn_fwd", s);
-    MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, inp, out, batch,
-                                          iters, eps));
+    if (n == 4 && batch < kSk16MaxBatch) {
+        hipLaunchKernelGGL(sinkhorn16_fwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s, inp, out,
+                           batch, iters, eps);
+    } else {
+        MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, inp, out,
+                                              batch, iters, eps));
+    }
     timing_end(tok, s);
     return hipGetLastError();
 }
@@ -107,8 +140,13 @@ hipError_t launch_sinkhorn_bwd(int n, const float* grad_out, const float* inp, f
     const int64_t threads = batch * G;
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     const int tok = timing_begin("sinkhorn_bwd", s);
-    MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, grad_out, inp,
-                                          grad_inp, batch, iters, eps));
+    if (n == 4 && batch < kSk16MaxBatch) {
+        hipLaunchKernelGGL(sinkhorn16_bwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s,
+                           grad_out, inp, grad_inp, batch, iters, eps);
+    } else {
+        MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, grad_out,
+                                              inp, grad_inp, batch, iters, eps));
+    }
     timing_end(tok, s);
     return hipGetLastError();
 }
