@@ -74,19 +74,18 @@ template <> struct VecIO<bf16_t> {
     __device__ __forceinline__ static void put(bf16_t* p, float v) { *p = f32_to_bf16(v); }
 };
 
-// Non-temporal 16-byte accesses (the `nt` bit: streaming data that will not
-// be re-read soon).
+// Non-temporal 16- and 8-byte accesses (the `nt` bit: streaming data that
+// will not be re-read soon).  Each is one vector access: per-component
+// non-temporal stores get merged into a wide store without the bit.
+typedef unsigned int nt_u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int nt_u32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint4 ld16_nt(const void* p) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    return make_uint4(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1),
-                      __builtin_nontemporal_load(q + 2), __builtin_nontemporal_load(q + 3));
+    const nt_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
 }
 __device__ __forceinline__ void st16_nt(void* p, uint4 v) {
-    uint32_t* q = reinterpret_cast<uint32_t*>(p);
-    __builtin_nontemporal_store(v.x, q);
-    __builtin_nontemporal_store(v.y, q + 1);
-    __builtin_nontemporal_store(v.z, q + 2);
-    __builtin_nontemporal_store(v.w, q + 3);
+    __builtin_nontemporal_store(nt_u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<nt_u32x4_t*>(p));
 }
 
 // Raw buffer loads: a scalar resource over [base, base + bytes) plus a 32-bit
@@ -115,13 +114,11 @@ __device__ __forceinline__ uint4 buf_ld16(buf_rsrc_t r, uint32_t voff, uint32_t 
 __device__ __forceinline__ uint32_t wave_uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ uint2 ld8_nt(const void* p) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    return make_uint2(__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1));
+    const nt_u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x2_t*>(p));
+    return make_uint2(v[0], v[1]);
 }
 __device__ __forceinline__ void st8_nt(void* p, uint2 v) {
-    uint32_t* q = reinterpret_cast<uint32_t*>(p);
-    __builtin_nontemporal_store(v.x, q);
-    __builtin_nontemporal_store(v.y, q + 1);
+    __builtin_nontemporal_store(nt_u32x2_t{v.x, v.y}, reinterpret_cast<nt_u32x2_t*>(p));
 }
 
 // Streaming (non-temporal) runs of WN elements: whole 16-byte pieces, or one
