@@ -57,8 +57,10 @@ int device_cu_count() {
 
 // The row kernels are compiled with __launch_bounds__(512) and chunk counts
 // VPT in {1, 2, 4, 8}; at most 128 floats of row state stay live per thread
-// so that a 512-lane workgroup fits in 256 VGPRs without spilling.
-RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live) {
+// so that a 512-lane workgroup fits in 256 VGPRs without spilling.  The
+// score prefers exact coverage of the row, then workgroups near
+// pref_threads lanes.
+RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live, int pref_threads) {
     RowTiling best{0, 0};
     if (C <= 0 || C % wc != 0) return best;
     const int64_t chunks = C / wc;
@@ -69,7 +71,7 @@ RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live) {
         threads = ((threads + 63) / 64) * 64;
         if (threads > 512) continue;
         const double waste = (double)(threads * vpt - chunks) / (double)(threads * vpt);
-        const double shape = fabs(log2((double)threads / 256.0)) * 0.02;
+        const double shape = fabs(log2((double)threads / (double)pref_threads)) * 0.02;
         const double score = waste + shape;
         if (score < best_score) {
             best_score = score;

@@ -18,7 +18,7 @@ struct RowTiling {
     int threads;
     int vpt;
 };
-RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live);
+RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live, int pref_threads = 256);
 
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
