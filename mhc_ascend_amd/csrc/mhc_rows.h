@@ -110,8 +110,6 @@ __device__ __forceinline__ void load_weight(const float* __restrict__ w, int C, 
 // Workgroup size bound: the prefetching variants hold two token rows and
 // run with up to 256 lanes (512 VGPRs available); the others up to 512.
 #define MHC_ROW_BOUNDS(PF) __attribute__((amdgpu_flat_work_group_size(1, (PF) ? 256 : 512)))
-// The fused forward runs its prefetch variant with up to 512 lanes too.
-#define MHC_FWD_BOUNDS __attribute__((amdgpu_flat_work_group_size(1, 512)))
 
 // Store one stream row chunk set (VPT chunks of WC channels).
 template <typename T, int VPT, int WC, bool NT>

@@ -140,53 +140,27 @@ __device__ __forceinline__ void wrap_fwd_token(int64_t b, const float* __restric
     }
 }
 
-template <typename TX, int N, int VPT, bool PF, bool DECAY>
-__global__ MHC_ROW_BOUNDS(PF) void wrap_fwd_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
-                                                   const float* __restrict__ w, const float* __restrict__ coef,
-                                                   int64_t coef_stride, float* __restrict__ out, int64_t B, int C,
-                                                   float eps) {
+// One token per workgroup (grid = tokens): the row loads of the next
+// workgroups on the CU overlap this one's reduction, which measured faster
+// than persistent workgroups with a register prefetch for this pass.
+template <typename TX, int N, int VPT, bool DECAY>
+__global__ MHC_ROW_BOUNDS(false) void wrap_fwd_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
+                                                      const float* __restrict__ w, const float* __restrict__ coef,
+                                                      int64_t coef_stride, float* __restrict__ out, int64_t B, int C,
+                                                      float eps) {
     constexpr int WC = kLayerWC;
     __shared__ float red[8];
+    const int64_t b = blockIdx.x;
+    if (b >= B) return;
+    RawRows<TX, 1, VPT, WC> rA, bA;
+    load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
+    load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
     float wv[VPT][WC];
     load_weight<VPT, WC>(w, C, wv);
-    const int64_t G = gridDim.x;
-    int64_t b = blockIdx.x;
-    RawRows<TX, 1, VPT, WC> rA, bA, rB, bB;
     float rv[1][VPT][WC], bv[1][VPT][WC];
-    if constexpr (PF) {
-        if (b < B) {
-            load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
-            load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
-        }
-        while (b < B) {
-            const int64_t b1 = b + G;
-            if (b1 < B) {
-                load_rows_raw<TX, 1, VPT, WC, true>(res + b1 * C, C, rB);
-                load_rows_raw<TX, 1, VPT, WC, true>(br + b1 * C, C, bB);
-            }
-            unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
-            unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
-            wrap_fwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, rv, bv, out, C, eps, red);
-            if (b1 >= B) break;
-            const int64_t b2 = b1 + G;
-            if (b2 < B) {
-                load_rows_raw<TX, 1, VPT, WC, true>(res + b2 * C, C, rA);
-                load_rows_raw<TX, 1, VPT, WC, true>(br + b2 * C, C, bA);
-            }
-            unpack_rows<TX, 1, VPT, WC>(rB, C, rv);
-            unpack_rows<TX, 1, VPT, WC>(bB, C, bv);
-            wrap_fwd_token<TX, N, VPT, DECAY>(b1, coef, coef_stride, wv, rv, bv, out, C, eps, red);
-            b = b2;
-        }
-    } else {
-        for (; b < B; b += G) {
-            load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
-            load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
-            unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
-            unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
-            wrap_fwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, rv, bv, out, C, eps, red);
-        }
-    }
+    unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
+    unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
+    wrap_fwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, rv, bv, out, C, eps, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -1017,13 +991,13 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
         default: break;                                          \
     }
 
-// live row arrays per thread: forward r, b (+ prefetch); backward g, r, b
+// live row arrays per thread: forward r, b (raw words and values); backward g, r, b
 static constexpr int kWrapFwdArrays = 2;
 static constexpr int kWrapBwdArrays = 3;
 
-template <typename TX, int V, bool PF, bool DECAY>
+template <typename TX, int V, bool DECAY>
 static const void* wrap_fwd_fn() {
-    if constexpr (layer_row_fits(kWrapFwdArrays * 2, V)) return reinterpret_cast<const void*>(&wrap_fwd_kernel<TX, 4, V, PF, DECAY>);
+    if constexpr (layer_row_fits(kWrapFwdArrays * 2, V)) return reinterpret_cast<const void*>(&wrap_fwd_kernel<TX, 4, V, DECAY>);
     return nullptr;
 }
 
@@ -1047,11 +1021,10 @@ static int wrap_grid(const void* fn, int threads, int64_t B) {
     return (int)g;
 }
 
-static const void* pick_wrap_fwd(int dt, int vpt, bool pf, bool decay) {
+static const void* pick_wrap_fwd(int dt, int vpt, bool decay) {
     const void* fn = nullptr;
 #define MHC_WF(TX_) \
-    MHC_WRAP_PICK_VPT(vpt, fn = pf ? (decay ? wrap_fwd_fn<TX_, V_, true, true>() : wrap_fwd_fn<TX_, V_, true, false>()) \
-                                  : (decay ? wrap_fwd_fn<TX_, V_, false, true>() : wrap_fwd_fn<TX_, V_, false, false>()))
+    MHC_WRAP_PICK_VPT(vpt, fn = decay ? wrap_fwd_fn<TX_, V_, true>() : wrap_fwd_fn<TX_, V_, false>())
     if (dt == kBF16) {
         MHC_WF(bf16_t);
     } else {
@@ -1084,11 +1057,12 @@ hipError_t launch_wrap_fwd(int dt, int n, bool decay, const void* res, const voi
                            hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (n != 4) return hipErrorInvalidValue;
-    const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapFwdArrays * 2);
+    const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapFwdArrays * 2, 512);
     if (t.vpt <= 0) return hipErrorInvalidValue;
-    const void* fn = pick_wrap_fwd(dt, t.vpt, wrap_prefetch(t), decay);
+    const void* fn = pick_wrap_fwd(dt, t.vpt, decay);
     if (!fn) return hipErrorInvalidValue;
-    const int grid = wrap_grid(fn, t.threads, B);
+    if (B > 0x7fffffff) return hipErrorInvalidValue;  // grid x limit
+    const unsigned grid = (unsigned)B;  // one token per workgroup
     int Ci = (int)C;
     void* args[] = {(void*)&res, (void*)&br, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&out, (void*)&B,
                     (void*)&Ci, (void*)&eps};
