@@ -37,7 +37,12 @@ static int hip_status(hipError_t e) {
 
 static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
 
-static bool supported_layer_n(int n) { return n == 4; }
+// The fused layer kernels are compiled for n in {2, 4, 8}; dynamic H needs
+// 2n + n^2 <= 32 projection outputs (n <= 4); the fused wrapper is n = 4.
+static bool supported_layer_n(int n) { return n == 2 || n == 4 || n == 8; }
+static bool supported_dynamic_n(int n) { return n == 2 || n == 4; }
+// the standalone aggregate / distribute operators
+static bool supported_ops_n(int n) { return n == 1 || n == 2 || n == 4 || n == 8; }
 
 // ---------------------------------------------------------------------------
 // Device properties
@@ -56,8 +61,8 @@ int device_cu_count() {
 }
 
 // The row kernels are compiled with __launch_bounds__(512) and chunk counts
-// VPT in {1, 2, 4, 8}; at most 128 floats of row state stay live per thread
-// so that a 512-lane workgroup fits in 256 VGPRs without spilling.  The
+// VPT in {1, 2, 4, 8}; at most kRowStateBudget floats of row state stay live
+// per thread so that a 512-lane workgroup fits in 256 VGPRs without spilling.  The
 // score prefers exact coverage of the row, then workgroups near
 // pref_threads lanes.
 RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live, int pref_threads) {
@@ -66,7 +71,7 @@ RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live, int pref_threa
     const int64_t chunks = C / wc;
     double best_score = 1e30;
     for (int vpt = 1; vpt <= 8; vpt *= 2) {
-        if (n_arrays_live * vpt * wc > 128) break;  // live row state per thread (floats)
+        if (n_arrays_live * vpt * wc > kRowStateBudget) break;  // live row state per thread (floats)
         int64_t threads = (chunks + vpt - 1) / vpt;
         threads = ((threads + 63) / 64) * 64;
         if (threads > 512) continue;
@@ -308,7 +313,7 @@ static int check_rows(const char* fn, int64_t batch, int64_t hidden, int32_t dty
 
 static int check_stream_n(const char* fn, int32_t n) {
     if (n < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": n must be >= 1");
-    if (!supported_layer_n(n))
+    if (!supported_ops_n(n))
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) + " is not compiled in this build");
     return MHC_SUCCESS;
 }
@@ -566,6 +571,9 @@ static int check_dyn(const char* fn, int64_t batch, int32_t n, int32_t hidden, i
     int st = check_layer_shape(fn, batch, n, hidden, x_dtype, num_iters);
     if (st) return st;
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
+    if (!supported_dynamic_n(n))
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": dynamic H is compiled for n in {2, 4}, not n=" +
+                                             std::to_string(n));
     if (((int64_t)n * hidden) % 32 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
     return MHC_SUCCESS;
@@ -702,6 +710,7 @@ static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidd
                          int32_t mode, int32_t num_iters, bool dynamic) {
     int st = check_layer_shape(fn, tokens, n, hidden, dtype, num_iters);
     if (st) return st;
+    if (n != 4) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper is compiled for n = 4");
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (mode != MHC_WRAPPER_DECAY && mode != MHC_WRAPPER_ZERO)
         return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");

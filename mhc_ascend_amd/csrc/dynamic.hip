@@ -1005,6 +1005,7 @@ hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, fl
 
 #define MHC_DYN_N(n, ...)                                        \
     switch (n) {                                                 \
+        case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }    \
         case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }    \
         default: return hipErrorInvalidValue;                    \
     }

@@ -541,7 +541,9 @@ hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s) {
 
 #define MHC_DISPATCH_N(n, ...)                                   \
     switch (n) {                                                 \
+        case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }    \
         case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }    \
+        case 8: { constexpr int N_ = 8; __VA_ARGS__; break; }    \
         default: return hipErrorInvalidValue;                    \
     }
 
@@ -600,29 +602,40 @@ static const void* bwd_fn() {
 
 static const void* pick_fwd(int x_dtype, int n, int vpt) {
     const void* fn = nullptr;
-    if (n != 4) return nullptr;
-    constexpr int N_ = 4;
-    if (x_dtype == kBF16) {
-        MHC_PICK_VPT(vpt, fn = fwd_fn<bf16_t, N_, V_>());
-    } else {
-        MHC_PICK_VPT(vpt, fn = fwd_fn<float, N_, V_>());
+#define MHC_FWD_N(N_)                                                            \
+    if (x_dtype == kBF16) {                                                      \
+        MHC_PICK_VPT(vpt, fn = fwd_fn<bf16_t, N_, V_>());                        \
+    } else {                                                                     \
+        MHC_PICK_VPT(vpt, fn = fwd_fn<float, N_, V_>());                         \
     }
+    switch (n) {
+        case 2: { MHC_FWD_N(2); break; }
+        case 4: { MHC_FWD_N(4); break; }
+        case 8: { MHC_FWD_N(8); break; }
+        default: break;
+    }
+#undef MHC_FWD_N
     return fn;
 }
 
+// MODE 1 (dynamic H) exists for the n whose 2n + n^2 projection outputs fit
+// one 32-wide projection tile (n <= 4).
 static const void* pick_bwd(int x_dtype, int n, int vpt, int mode, bool pf) {
     const void* fn = nullptr;
-    if (n != 4) return nullptr;
-    constexpr int N_ = 4;
-#define MHC_BWD_FN(TX_) \
-    MHC_PICK_VPT(vpt, fn = mode == 0 ? (pf ? bwd_fn<TX_, N_, V_, 0, true>() : bwd_fn<TX_, N_, V_, 0, false>()) \
+#define MHC_BWD_FN(TX_, N_)                                                                                     \
+    MHC_PICK_VPT(vpt, fn = mode == 0 ? (pf ? bwd_fn<TX_, N_, V_, 0, true>() : bwd_fn<TX_, N_, V_, 0, false>())   \
                                      : (pf ? bwd_fn<TX_, N_, V_, 1, true>() : bwd_fn<TX_, N_, V_, 1, false>()))
-    if (x_dtype == kBF16) {
-        MHC_BWD_FN(bf16_t);
-    } else {
-        MHC_BWD_FN(float);
+#define MHC_BWD_FN0(TX_, N_) \
+    MHC_PICK_VPT(vpt, fn = mode == 0 ? (pf ? bwd_fn<TX_, N_, V_, 0, true>() : bwd_fn<TX_, N_, V_, 0, false>()) : nullptr)
+    const bool bf = x_dtype == kBF16;
+    switch (n) {
+        case 2: { if (bf) { MHC_BWD_FN(bf16_t, 2); } else { MHC_BWD_FN(float, 2); } break; }
+        case 4: { if (bf) { MHC_BWD_FN(bf16_t, 4); } else { MHC_BWD_FN(float, 4); } break; }
+        case 8: { if (bf) { MHC_BWD_FN0(bf16_t, 8); } else { MHC_BWD_FN0(float, 8); } break; }
+        default: break;
     }
 #undef MHC_BWD_FN
+#undef MHC_BWD_FN0
     return fn;
 }
 
@@ -661,9 +674,13 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
     return e != hipSuccess ? e : hipGetLastError();
 }
 
+// The backward hands one of its 2 + n^2 + 3n row sums to each thread.
+static RowTiling bwd_tiling(int64_t C, int n) {
+    return with_min_threads(choose_row_tiling(C, kLayerWC, 2 * n), 2 + n * n + 3 * n);
+}
+
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
-    const int wc = kLayerWC;
-    const RowTiling t = choose_row_tiling(C, wc, 2 * n);
+    const RowTiling t = bwd_tiling(C, n);
     if (t.vpt <= 0) return 1;
     return persistent_grid(pick_bwd(x_dtype, n, t.vpt, 0, use_prefetch(t)), t.threads, B);
 }
@@ -671,8 +688,7 @@ int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, hipStream_t s) {
-    const int wc = kLayerWC;
-    const RowTiling t = choose_row_tiling(C, wc, 2 * n);
+    const RowTiling t = bwd_tiling(C, n);
     if (t.vpt <= 0) return hipErrorInvalidValue;
     const void* fn = pick_bwd(x_dtype, n, t.vpt, mode, use_prefetch(t));
     if (!fn) return hipErrorInvalidValue;

@@ -18,7 +18,15 @@ struct RowTiling {
     int threads;
     int vpt;
 };
+// Live row state per thread (floats) the row kernels are sized for.
+constexpr int kRowStateBudget = 136;
 RowTiling choose_row_tiling(int64_t C, int wc, int n_arrays_live, int pref_threads = 256);
+// A tiling with at least `need` lanes (kernels whose block reductions hand
+// one value per thread; lanes past the row are masked out).
+inline RowTiling with_min_threads(RowTiling t, int need) {
+    if (t.vpt > 0 && t.threads < need) t.threads = ((need + 63) / 64) * 64;
+    return t;
+}
 
 // Number of compute units of the current device (cached per device).
 int device_cu_count();

@@ -5,6 +5,7 @@
 #pragma once
 
 #include "mhc_device.h"
+#include "mhc_internal.h"
 
 namespace mhc {
 
@@ -127,10 +128,12 @@ __device__ __forceinline__ void store_row1(T* __restrict__ base, int C, const fl
     }
 }
 
-// Row state budget shared with choose_row_tiling(): n_arrays * VPT * W <= 128.
+// Row state budget shared with choose_row_tiling(): n_arrays * VPT * W <= 136
+// floats per thread (128 plus the one row of the distribute backward's
+// y at n = 8 in bf16: 2n + 1 = 17 rows of 8 channels).
 template <typename TX>
 constexpr bool row_fits(int n_arrays, int vpt) {
-    return n_arrays * vpt * VecIO<TX>::W <= 128;
+    return n_arrays * vpt * VecIO<TX>::W <= kRowStateBudget;
 }
 
 // Channels per lane chunk in the fused layer kernels, for both storage
@@ -141,6 +144,6 @@ constexpr bool row_fits(int n_arrays, int vpt) {
 // access into two 16-byte pieces at a 32-byte lane stride.)
 constexpr int kLayerWC = 4;
 
-constexpr bool layer_row_fits(int n_arrays, int vpt) { return n_arrays * vpt * kLayerWC <= 128; }
+constexpr bool layer_row_fits(int n_arrays, int vpt) { return n_arrays * vpt * kLayerWC <= kRowStateBudget; }
 
 }  // namespace mhc

@@ -403,7 +403,10 @@ hipError_t launch_compute_rms(int dt, const void* x, float* rms, int64_t B, int6
 
 #define MHC_OPS_N(n, ...)                                        \
     switch (n) {                                                 \
+        case 1: { constexpr int N_ = 1; __VA_ARGS__; break; }    \
+        case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }    \
         case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }    \
+        case 8: { constexpr int N_ = 8; __VA_ARGS__; break; }    \
         default: return hipErrorInvalidValue;                    \
     }
 
@@ -454,7 +457,8 @@ hipError_t launch_distribute_bwd(int dt, int n, const float* g, const void* x, c
                                  int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
                                  float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2 * n + 1);
+    // the block hands one of the n*n + n row sums to each thread
+    const RowTiling t = with_min_threads(choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2 * n + 1), n * n + n);
     if (t.vpt <= 0) return hipErrorInvalidValue;
     const int tok = timing_begin("distribute_bwd", s);
     MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, 2 * N_ + 1, T_,

@@ -303,6 +303,22 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
     """Fused MHCResidualWrapper on residual / branch_output [tokens, C] for the
     parameters of ``layer`` (an MHCLayer); returns fp32 [tokens, C]."""
     n = layer.expansion_rate
+    if n != 4:
+        # The fused wrapper kernels are compiled for n = 4.  Other n build the
+        # n streams with device tensor ops, as layer.py:299-310 does, and run
+        # the fused layer on them (layer.py:313-316).
+        if n < 2:
+            raise RuntimeError("mhc_residual_wrapper: expansion_rate must be >= 2 (stream 1 holds the branch)")
+        if residual_mode not in ("zero", "decay"):
+            raise ValueError(f"Unknown residual_mode: {residual_mode}")
+        C = residual.shape[-1]
+        X = torch.zeros(residual.shape[0], n, C, device=residual.device, dtype=residual.dtype)
+        X[:, 0] = residual
+        X[:, 1] = branch_output
+        if residual_mode == "decay":
+            for i in range(2, n):
+                X[:, i] = residual * (0.1 ** (i - 1))
+        return layer(X).mean(dim=1)
     args = (layer.num_sinkhorn_iters, layer.sinkhorn_eps, layer.rmsnorm_eps)
     if layer.use_dynamic_h:
         return MHCWrapperDynamicFunction.apply(residual, branch_output, layer.rmsnorm_weight, layer.phi_pre,

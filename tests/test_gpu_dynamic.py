@@ -89,6 +89,21 @@ def test_dynamic_layer_matches_oracle(device, x_dtype, B, C):
     _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"B={B} C={C} {x_dtype}")
 
 
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,C", [(5, 64), (40, 1280)])
+def test_dynamic_layer_n2_matches_oracle(device, x_dtype, B, C):
+    """Expansion rate 2 (8 projection outputs; one row per lane-pair Sinkhorn)."""
+    d = R.dynamic_layer_inputs(B, 2, C, seed=2 * B + C, x_dtype=x_dtype, alpha=0.3, phi_std=0.05, b_std=0.5)
+    _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n=2 B={B} C={C} {x_dtype}")
+
+
+def test_dynamic_layer_n8_is_unsupported(device):
+    """2n + n^2 = 80 projection outputs exceed the one-tile projection."""
+    layer = mhc.MHCLayer(64, 8, use_dynamic_h=True).to(device)
+    with pytest.raises(RuntimeError, match="dynamic H is compiled for n in"):
+        layer(torch.randn(3, 8, 64, device=device))
+
+
 @pytest.mark.parametrize("alpha,phi_std", [(0.5, 0.05), (2.0, 0.02)])
 def test_dynamic_layer_strong_dynamic_h(device, alpha, phi_std):
     """Large alpha makes t (and so h, M) vary strongly per token."""

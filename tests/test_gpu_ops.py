@@ -107,6 +107,43 @@ def test_stream_aggregate(device, dtype, shared, B, C):
                  "aggregate dH")
 
 
+@pytest.mark.parametrize("n", [1, 2, 8])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_stream_ops_general_n(device, n, dtype):
+    """stream_aggregate and stream_distribute_mix_add at n = 1, 2, 8 (the
+    distribute backward's n*n + n row sums need >= 72 lanes at n = 8)."""
+    B, C = 9, 64 if n == 8 else 256
+    g = _gen(100 + n)
+    x = torch.randn(B, n, C, generator=g).to(dtype)
+    H = torch.randn(B, n, generator=g)
+    go = torch.randn(B, C, generator=g).to(dtype)
+    xd, Hd = _leaf(x, device), _leaf(H, device)
+    out = mhc.stream_aggregate(xd, Hd)
+    out.backward(go.to(device))
+    xr, Hr = _ref_leaf(x), _ref_leaf(H)
+    ref, _ = R.stream_aggregate(xr, Hr)
+    ref.backward(go.double())
+    _check_out(out, ref.detach(), dtype, f"n={n} aggregate out")
+    _check_grad(xd.grad, xr.grad, dtype, f"n={n} aggregate dx")
+
+    y = torch.randn(B, C, generator=g).to(dtype)
+    Hq = torch.randn(B, n, generator=g)
+    M = torch.rand(B, n, n, generator=g)
+    gd = torch.randn(B, n, C, generator=g)
+    xd, yd, Hd, Md = (_leaf(t, device) for t in (x, y, Hq, M))
+    out = mhc.stream_distribute(yd, Hd, Md, xd)
+    out.backward(gd.to(device))
+    xr, yr, Hr, Mr = (_ref_leaf(t) for t in (x, y, Hq, M))
+    ref, _ = R.stream_distribute_mix_add(yr, Hr, Mr, xr)
+    ref.backward(gd.double())
+    assert out.dtype == torch.float32
+    assert_close(out, ref.detach(), what=f"n={n} distribute out", **FWD)
+    _check_grad(xd.grad, xr.grad, dtype, f"n={n} distribute dx")
+    _check_grad(yd.grad, yr.grad, dtype, f"n={n} distribute dy")
+    assert_close(Md.grad, Mr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Mr.grad, 1e-4),
+                 f"n={n} distribute dM")
+
+
 def test_stream_aggregate_config_c2(device):
     """Config C2: x [16384, 4, 4096] ~ N(0,1), H_pre [16384, 4] ~ N(0,1)."""
     g = _gen(12)

@@ -153,6 +153,38 @@ def test_static_layer_matches_oracle(device, B, C, x_dtype):
                   tag=f"B={B} C={C} {x_dtype}")
 
 
+@pytest.mark.parametrize("n,B,C", [(2, 5, 64), (2, 37, 1280), (8, 3, 64), (8, 128, 1280), (8, 9, 4096)])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_static_layer_general_n(device, n, B, C, x_dtype):
+    """Expansion rates 2 and 8 (the paper's (128, 1280, 8) among them); C=64
+    with n=8 is a 16-chunk row whose block reduction of 90 row sums needs
+    more lanes than the row has chunks."""
+    d = R.static_layer_inputs(B, n, C, seed=n * 1000 + B + C, x_dtype=x_dtype)
+    _check_static(d, _run_static(d, device), _oracle_static(d), x_bf16=x_dtype == torch.bfloat16,
+                  tag=f"n={n} B={B} C={C} {x_dtype}")
+
+
+def test_static_layer_module_general_n(device):
+    """MHCLayer(expansion_rate=8) forward/backward through the module."""
+    torch.manual_seed(8)
+    layer = mhc.MHCLayer(1280, 8, use_dynamic_h=False).to(device)
+    with torch.no_grad():
+        layer.H_pre.normal_()
+        layer.H_post.normal_()
+        layer.H_res.normal_()
+    x = torch.randn(6, 8, 1280, generator=_gen(8))
+    g = torch.randn(6, 8, 1280, generator=_gen(9))
+    xd = x.to(device).requires_grad_(True)
+    out = layer(xd)
+    out.backward(g.to(device))
+    d = {"x": x, "grad": g, "weight": layer.rmsnorm_weight.detach().cpu(), "H_pre": layer.H_pre.detach().cpu(),
+         "H_post": layer.H_post.detach().cpu(), "H_res": layer.H_res.detach().cpu()}
+    rout, rgx, rgp = _oracle_static(d)
+    assert_close(out, rout, what="n=8 module out", **FWD)
+    assert_close(xd.grad, rgx, 1e-3, grad_atol(rgx, 1e-5), "n=8 module dx")
+    assert_close(layer.H_res.grad, rgp[3], 1e-3, grad_atol(rgp[3], 1e-4), "n=8 module d_H_res")
+
+
 def test_static_layer_module_matches_functional(device):
     torch.manual_seed(3)
     layer = mhc.MHCLayer(512, 4, use_dynamic_h=False).to(device)

@@ -134,6 +134,47 @@ def test_wrapper_config_c5_width(device, dynamic):
     _check(got, want, torch.bfloat16, DYN if dynamic else STA, f"C5 width dyn={dynamic}")
 
 
+@pytest.mark.parametrize("n,dynamic", [(2, False), (8, False), (2, True)])
+@pytest.mark.parametrize("mode", ["decay", "zero"])
+def test_wrapper_general_n(device, n, dynamic, mode):
+    """Expansion rates other than 4: the streams are built with device tensor
+    ops and run through the fused layer (the wrapper kernels are n = 4)."""
+    C = 256
+    torch.manual_seed(n)
+    wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=dynamic)
+    wrap.residual_mode = mode
+    layer = wrap.mhc
+    g = _gen(70 + n)
+    with torch.no_grad():
+        layer.rmsnorm_weight.copy_((1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16))
+        if dynamic:
+            for k in ("phi_pre", "phi_post", "phi_res"):
+                getattr(layer, k).copy_(0.05 * torch.randn(getattr(layer, k).shape, generator=g))
+            for k in ("alpha_pre", "alpha_post", "alpha_res"):
+                getattr(layer, k).fill_(0.3)
+        else:
+            for k in STA:
+                getattr(layer, k).copy_(torch.randn(getattr(layer, k).shape, generator=g))
+    res = torch.randn(3, 5, C, generator=g)
+    br = torch.randn(3, 5, C, generator=g)
+    grad = torch.randn(3, 5, C, generator=g)
+    layer_names = DYN if dynamic else STA
+    w = layer.rmsnorm_weight.detach().cpu().double().requires_grad_(True)
+    ps = [getattr(layer, k).detach().cpu().double().requires_grad_(True) for k in layer_names]
+    r = res.clone().requires_grad_(True)
+    b = br.clone().requires_grad_(True)
+    if dynamic:
+        fn = lambda X: R.mhc_layer_dynamic(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
+    else:
+        fn = lambda X: R.mhc_layer_static(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
+    want_out = R.mhc_residual_wrapper(r, b, fn, n, mode)
+    want_out.backward(grad.double())
+    got = _run(wrap, res, br, grad, device)
+    assert_close(got[0], want_out.detach(), 1e-4, grad_atol(want_out.detach(), 1e-5), f"n={n} out")
+    assert_close(got[1], r.grad.double(), 1e-3, grad_atol(r.grad.double(), 1e-5), f"n={n} d residual")
+    assert_close(got[2], b.grad.double(), 1e-3, grad_atol(b.grad.double(), 1e-5), f"n={n} d branch")
+
+
 def test_wrapper_single_token_rows_stay_flat(device):
     """[B, 1, C] comes back as [B, C] (layer.py:319-320)."""
     wrap = _make(128, True, 9).to(device)
