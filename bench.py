@@ -1,6 +1,6 @@
 """Benchmark of the mHC layer forward+backward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload static|dynamic|wrapper|ops]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload static|dynamic|infer|wrapper|ops]
 
 Prints ONE JSON line: tokens/s of the whole fwd+bwd step, the achieved HBM
 GB/s from algorithmic bytes, the roofline of the dominant kernel (HIP-event
@@ -11,6 +11,8 @@ a bounded token sample).
 Workloads (the metric is quoted at n=4, C=4096):
   static  - C3: MHCLayer static-H, x fp32 [8192, 4, 4096]          (default)
   dynamic - C4: MHCLayer dynamic-H, x bf16 [8192, 4, 4096], phi [16384, 24]
+  infer   - C4 shape forward only (eval, no_grad, parameters packed once);
+            --out-dtype f32 (the reference's output) or bf16
   wrapper - C5: MHCResidualWrapper, residual/branch bf16 [65536, 4, 7168]
   ops     - C2: standalone sinkhorn_knopp / rmsnorm / stream_aggregate fwd+bwd
             (value = the step's achieved HBM GB/s)
@@ -219,6 +221,66 @@ class DynamicWorkload:
                               f"{self.B} tokens, n={self.n}, C={self.C}; median of {runs} runs")
 
 
+class InferWorkload(DynamicWorkload):
+    """C4 shape, forward only: the dynamic-H MHCLayer in eval mode under
+    no_grad (the inference path of ops.py:337-380), its weight and
+    projections packed once (MHCLayer.prepare_inference), output fp32 as the
+    reference or bf16 (--out-dtype)."""
+
+    name = "infer"
+    metric = "mHC dynamic-H layer forward-only (inference) tokens/sec (C4 shape, n=4, C=4096)"
+    out_dtype = "f32"
+
+    def __init__(self, torch, mhc, device):
+        super().__init__(torch, mhc, device)
+        self.xs = [x.detach() for x in self.xs]
+        self.gs = []
+        self.layer.eval()
+        self.odt = torch.bfloat16 if self.out_dtype == "bf16" else torch.float32
+        self.mhc = mhc
+        self.layer.prepare_inference()
+
+    def step(self):
+        x = self.xs[self.i % self.sets]
+        self.i += 1
+        L = self.layer
+        with self.torch.no_grad():
+            return self.mhc.mhc_layer_fused_dynamic_inference(
+                x, L.rmsnorm_weight, L.phi_pre, L.phi_post, L.phi_res, L.alpha_pre, L.alpha_post, L.alpha_res,
+                L.b_pre, L.b_post, L.b_res, L.num_sinkhorn_iters, L.sinkhorn_eps, L.rmsnorm_eps,
+                out_dtype=self.odt, packed=L._packed())
+
+    def out_bytes(self):
+        return (2 if self.out_dtype == "bf16" else 4) * self.E
+
+    def step_bytes(self):
+        # read x bf16 (2E), write out (4E fp32 / 2E bf16), Phi planes read once
+        return 2 * self.E + self.out_bytes() + self.phi_bytes() * 3 // 2
+
+    def kernel_bytes(self):
+        return {"proj": 2 * self.E + self.phi_bytes() * 3 // 2, "layer_fwd": 2 * self.E + self.out_bytes()}
+
+    def config(self):
+        return {"workload": "C4 MHCLayer dynamic-H forward-only (eval, no_grad)", "tokens": self.B, "n": self.n,
+                "C": self.C, "x_dtype": "bf16", "out_dtype": self.out_dtype,
+                "phi": [self.n * self.C, 2 * self.n + self.n * self.n], "sinkhorn_iters": 20}
+
+    def cpu_baseline(self, torch, R, seconds):
+        sample = 256
+        d = R.dynamic_layer_inputs(sample, self.n, self.C, seed=1)
+        names = ("weight", "phi_pre", "phi_post", "phi_res", "alpha_pre", "alpha_post", "alpha_res", "b_pre",
+                 "b_post", "b_res")
+        ps = [d[k].float() for k in names]
+
+        def run():
+            with torch.no_grad():
+                R.mhc_layer_dynamic(d["x"], *ps, 20, 1e-8, 1e-5, dtype=torch.float32)
+
+        med, runs = _timed_cpu(run, seconds)
+        return sample / med, (f"oracle.reference.mhc_layer_dynamic fp32 forward (no_grad) on {sample} of "
+                              f"{self.B} tokens, n={self.n}, C={self.C}; median of {runs} runs")
+
+
 class WrapperWorkload:
     """C5: MHCResidualWrapper (dynamic H, 'decay') fwd+bwd at DeepSeek-V3
     width: residual, branch bf16 [65536, 4, 7168] (262,144 tokens)."""
@@ -400,7 +462,8 @@ class OpsWorkload:
                                           f"same algorithmic bytes scaled to the sample; median of {runs} runs")
 
 
-WORKLOADS = {"static": StaticWorkload, "dynamic": DynamicWorkload, "wrapper": WrapperWorkload, "ops": OpsWorkload}
+WORKLOADS = {"static": StaticWorkload, "dynamic": DynamicWorkload, "infer": InferWorkload,
+             "wrapper": WrapperWorkload, "ops": OpsWorkload}
 KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "wrap_proj", "wrap_fwd", "wrap_bwd",
            "wrap_bwd_reduce", "wrap_proj_bwd", "sinkhorn_fwd", "sinkhorn_bwd", "rmsnorm_fwd", "rmsnorm_bwd",
            "aggregate_fwd", "aggregate_bwd")
@@ -414,6 +477,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 50; 10 for wrapper)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="static")
+    ap.add_argument("--out-dtype", choices=("f32", "bf16"), default="f32",
+                    help="infer workload: output dtype (f32 as the reference, or bf16)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bounded CPU-baseline sample time (0 disables)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -435,6 +500,7 @@ def main(argv=None) -> int:
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    InferWorkload.out_dtype = a.out_dtype
     wl = WORKLOADS[a.workload](torch, mhc, device)
 
     print(f"[bench] workload={wl.name} warmup={a.warmup} steps={steps}", file=sys.stderr, flush=True)

@@ -203,6 +203,32 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
                           int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
                           float rmsnorm_eps, void* stream);
 
+/* ---- forward-only dynamic-H layer (inference) ----------------------------------
+ * The forward of mhc_layer_dynamic_fwd without the backward's saved state, in
+ * two steps.  mhc_layer_dynamic_pack writes what depends on the parameters
+ * alone - the fp32 RMSNorm weight and [phi_pre; phi_post; phi_res] as three
+ * bf16 planes in the projection kernel's operand order - into `packed`
+ * (device memory of mhc_layer_dynamic_packed_size bytes, 256-byte aligned).
+ * Pack once per parameter update.  mhc_layer_dynamic_infer then runs the
+ * projection, the per-token H and the fused row pass, and writes
+ * out [batch, n, hidden] in out_dtype: MHC_DTYPE_F32 as the reference, or
+ * MHC_DTYPE_BF16 (rounded to nearest even) to halve the output traffic.
+ * `packed` must come from mhc_layer_dynamic_pack with the same n and hidden;
+ * alpha_* and b_* are as in mhc_layer_dynamic_fwd.  Results equal
+ * mhc_layer_dynamic_fwd's `out` bit for bit at out_dtype F32.
+ * Replaces the inference path of ops.py:337-380 (mhc_layer_fwd_dynamic,
+ * bindings.cpp:880-952, with its saved outputs dropped). */
+size_t mhc_layer_dynamic_packed_size(int32_t n, int32_t hidden);
+int mhc_layer_dynamic_pack(const void* weight, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
+                           const float* phi_res, void* packed, size_t packed_bytes, int32_t n, int32_t hidden,
+                           void* stream);
+size_t mhc_layer_dynamic_infer_workspace_size(int64_t batch, int32_t n, int32_t hidden);
+int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, const float* alpha_pre,
+                            const float* alpha_post, const float* alpha_res, const float* b_pre, const float* b_post,
+                            const float* b_res, void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                            int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
+                            float rmsnorm_eps, void* stream);
+
 /* Gradients for grad_out [batch, n, hidden] fp32: grad_x (x_dtype),
  * grad_weight [hidden] (weight_dtype), grad_phi [2n+n^2, n*hidden] (rows
  * pre, post, res), grad_alpha [3] (pre, post, res), grad_b [2n+n^2]

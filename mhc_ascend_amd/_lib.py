@@ -61,6 +61,11 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "mhc_layer_dynamic_fwd_workspace_size": (_sz, [_i64, _i32, _i32]),
     "mhc_layer_dynamic_fwd": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
+    "mhc_layer_dynamic_packed_size": (_sz, [_i32, _i32]),
+    "mhc_layer_dynamic_pack": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp, _sz, _i32, _i32, _vp]),
+    "mhc_layer_dynamic_infer_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "mhc_layer_dynamic_infer": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _sz,
+                                               _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
     "mhc_layer_dynamic_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "mhc_layer_dynamic_bwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32,

@@ -235,7 +235,7 @@ int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const void* weight, int
                                       sinkhorn_eps, s);
     if (e != hipSuccess) return hip_status(e);
     const float* w32 = saved + saved_w_offset(n);
-    return hip_status(launch_layer_fwd(x_dtype, n, x, w32, saved, 0, out, rms, batch, hidden, rmsnorm_eps, s));
+    return hip_status(launch_layer_fwd(x_dtype, n, x, w32, saved, 0, out, kF32, rms, batch, hidden, rmsnorm_eps, s));
 }
 
 
@@ -611,7 +611,76 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
                                 saved + d.coef_off, saved + d.p_off, saved + d.rh_off, num_iters, sinkhorn_eps,
                                 rmsnorm_eps, s);
     if (e == hipSuccess)
-        e = launch_layer_fwd(x_dtype, n, x, w32, saved + d.coef_off, np, out, nullptr, batch, hidden, rmsnorm_eps, s);
+        e = launch_layer_fwd(x_dtype, n, x, w32, saved + d.coef_off, np, out, kF32, nullptr, batch, hidden, rmsnorm_eps, s);
+    return hip_status(e);
+}
+
+// ---- forward-only dynamic-H layer ---------------------------------------------
+// packed: [w32 (C floats) | Phi as three bf16 planes in fragment order], the
+// planes 256-byte aligned.  workspace: [coef (B x np) | projection partials].
+static size_t packed_phib_off(int32_t hidden) { return align256((size_t)hidden * sizeof(float)); }
+
+size_t mhc_layer_dynamic_packed_size(int32_t n, int32_t hidden) {
+    if (n < 1 || hidden < 1) return 0;
+    return packed_phib_off(hidden) + align256((size_t)3 * 32 * ((int64_t)n * hidden) * 2);
+}
+
+int mhc_layer_dynamic_pack(const void* weight, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
+                           const float* phi_res, void* packed, size_t packed_bytes, int32_t n, int32_t hidden,
+                           void* stream) {
+    int st = check_dyn("layer_dynamic_pack", 0, n, hidden, kF32, weight_dtype, 0);
+    if (st) return st;
+    MHC_REQUIRE(weight && phi_pre && phi_post && phi_res && packed, "layer_dynamic_pack: null pointer");
+    if (packed_bytes < mhc_layer_dynamic_packed_size(n, hidden))
+        return fail(MHC_ERR_WORKSPACE, "layer_dynamic_pack: buffer smaller than mhc_layer_dynamic_packed_size()");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t K = (int64_t)n * hidden;
+    hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, (float*)packed, s);
+    if (e == hipSuccess)
+        e = launch_phi_split(phi_pre, phi_post, phi_res, n, 2 * n + n * n, K,
+                             (bf16_raw_t*)((char*)packed + packed_phib_off(hidden)), s);
+    return hip_status(e);
+}
+
+static size_t infer_proj_off(int64_t batch, int32_t n) { return align256((size_t)batch * (2 * n + n * n) * 4); }
+
+size_t mhc_layer_dynamic_infer_workspace_size(int64_t batch, int32_t n, int32_t hidden) {
+    if (batch < 0 || n < 1 || hidden < 1) return 0;
+    const ProjFwdWs w = proj_fwd_ws(batch, (int64_t)n * hidden);
+    return infer_proj_off(batch, n) + (w.total - w.p_off);
+}
+
+int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, const float* alpha_pre,
+                            const float* alpha_post, const float* alpha_res, const float* b_pre, const float* b_post,
+                            const float* b_res, void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                            int64_t batch, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps,
+                            float rmsnorm_eps, void* stream) {
+    int st = check_dyn("layer_dynamic_infer", batch, n, hidden, x_dtype, kF32, num_iters);
+    if (st) return st;
+    if (!valid_dtype(out_dtype)) return fail(MHC_ERR_INVALID, "layer_dynamic_infer: out_dtype must be F32 or BF16");
+    MHC_REQUIRE(packed && alpha_pre && alpha_post && alpha_res && b_pre && b_post && b_res,
+                "layer_dynamic_infer: null parameter pointer");
+    if (batch == 0) return MHC_SUCCESS;
+    MHC_REQUIRE(x && out, "layer_dynamic_infer: null x/out");
+    if (!workspace || workspace_bytes < mhc_layer_dynamic_infer_workspace_size(batch, n, hidden))
+        return fail(MHC_ERR_WORKSPACE,
+                    "layer_dynamic_infer: workspace smaller than mhc_layer_dynamic_infer_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t K = (int64_t)n * hidden;
+    const int np = 2 * n + n * n;
+    const ProjFwdWs w = proj_fwd_ws(batch, K);
+    const float* w32 = (const float*)packed;
+    const bf16_raw_t* phib = (const bf16_raw_t*)((const char*)packed + packed_phib_off(hidden));
+    float* coef = (float*)workspace;
+    char* pw = (char*)workspace + infer_proj_off(batch, n);
+    float* pp = (float*)pw;
+    float* ss = (float*)(pw + (w.ss_off - w.p_off));
+    hipError_t e = launch_proj_mfma(x_dtype, x, phib, pp, ss, batch, K, w.ks, s);
+    if (e == hipSuccess)
+        e = launch_dyn_coef_fwd(n, pp, ss, w.ks, batch, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
+                                coef, nullptr, nullptr, num_iters, sinkhorn_eps, rmsnorm_eps, s);
+    if (e == hipSuccess)
+        e = launch_layer_fwd(x_dtype, n, x, w32, coef, np, out, out_dtype, nullptr, batch, hidden, rmsnorm_eps, s);
     return hip_status(e);
 }
 

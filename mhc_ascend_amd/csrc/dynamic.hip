@@ -335,7 +335,8 @@ __global__ __launch_bounds__(256) void proj_reduce_kernel(const float* __restric
 // ---------------------------------------------------------------------------
 // Per-token coefficients (bindings.cpp:909-929).  One token per group of
 // G = pow2ceil(n) lanes; lane r owns t_pre[r], t_post[r] and row r of t_res.
-// coef[b] = (h_pre, h_post, M row-major); p_out[b] = P (np values); rh[b].
+// coef[b] = (h_pre, h_post, M row-major); p_out[b] = P (np values); rh[b]
+// (p_out and rh may be null: the forward-only entry keeps neither).
 // ---------------------------------------------------------------------------
 template <int N>
 __global__ __launch_bounds__(256) void dyn_coef_fwd_kernel(
@@ -381,13 +382,15 @@ __global__ __launch_bounds__(256) void dyn_coef_fwd_kernel(
         cf[N + r] = hq;
 #pragma unroll
         for (int c = 0; c < N; ++c) cf[2 * N + r * N + c] = e[c];
-        float* po = p_out + tok * NP;
-        po[r] = pp;
-        po[N + r] = pq;
+        if (p_out) {
+            float* po = p_out + tok * NP;
+            po[r] = pp;
+            po[N + r] = pq;
 #pragma unroll
-        for (int c = 0; c < N; ++c) po[2 * N + r * N + c] = pr[c];
+            for (int c = 0; c < N; ++c) po[2 * N + r * N + c] = pr[c];
+        }
     }
-    if (tv && r == 0) rh[tok] = r_h;
+    if (tv && r == 0 && rh) rh[tok] = r_h;
 }
 
 // ---------------------------------------------------------------------------
@@ -512,14 +515,14 @@ __global__ __launch_bounds__(256) void dyn_coef16_fwd_kernel(
     sk16_forward(e, iters, sk_eps);
     if (tv) {
         float* cf = coef + tok * NP;
-        float* po = p_out + tok * NP;
         cf[2 * N + l] = e;
-        po[2 * N + l] = pres;
-        if (l < 2 * N) {
-            cf[l] = h;
-            po[l] = ppq;
+        if (l < 2 * N) cf[l] = h;
+        if (p_out) {
+            float* po = p_out + tok * NP;
+            po[2 * N + l] = pres;
+            if (l < 2 * N) po[l] = ppq;
         }
-        if (l == 0) rh[tok] = r_h;
+        if (l == 0 && rh) rh[tok] = r_h;
     }
 }
 

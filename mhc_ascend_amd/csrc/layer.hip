@@ -82,10 +82,10 @@ __global__ __launch_bounds__(256) void static_coef_kernel(const float* __restric
 // measured faster than persistent workgroups with a register prefetch for
 // this pass (C4 bf16 147 -> 136 us; fp32 equal).
 // ---------------------------------------------------------------------------
-template <typename TX, int N, int VPT>
+template <typename TX, typename TO, int N, int VPT>
 __device__ __forceinline__ void fwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
                                           const float (&wv)[VPT][kLayerWC],
-                                          const float (&xv)[N][VPT][kLayerWC], float* __restrict__ out,
+                                          const float (&xv)[N][VPT][kLayerWC], TO* __restrict__ out,
                                           float* __restrict__ rms_out, int C, float eps, float* red) {
     constexpr int WC = kLayerWC;
     constexpr int NC = coef_size<N>();
@@ -110,7 +110,7 @@ __device__ __forceinline__ void fwd_token(int64_t b, const float* __restrict__ c
     block_sum<1>(v, red);
     const float r = sqrtf(v[0] / (float)C + eps);
     const float inv = 1.f / r;
-    float* ob = out + b * (int64_t)N * C;
+    TO* ob = out + b * (int64_t)N * C;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
@@ -128,17 +128,17 @@ __device__ __forceinline__ void fwd_token(int64_t b, const float* __restrict__ c
                     for (int j = 0; j < N; ++j) s += cfv[2 * N + i * N + j] * xv[j][k][e];
                     o[e] = s;
                 }
-                store_run_nt<float, WC>(ob + (int64_t)i * C + c0, o);
+                store_run_nt<TO, WC>(ob + (int64_t)i * C + c0, o);
             }
         }
     }
     if (threadIdx.x == 0 && rms_out) rms_out[b] = r;
 }
 
-template <typename TX, int N, int VPT>
+template <typename TX, typename TO, int N, int VPT>
 __global__ MHC_ROW_BOUNDS(false) void layer_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
                                                        const float* __restrict__ coef, int64_t coef_stride,
-                                                       float* __restrict__ out, float* __restrict__ rms_out, int64_t B,
+                                                       TO* __restrict__ out, float* __restrict__ rms_out, int64_t B,
                                                        int C, float eps) {
     constexpr int WC = kLayerWC;
     __shared__ float red[8];
@@ -150,7 +150,7 @@ __global__ MHC_ROW_BOUNDS(false) void layer_fwd_kernel(const TX* __restrict__ x,
     load_weight<VPT, WC>(w, C, wv);
     float xv[N][VPT][WC];
     unpack_rows<TX, N, VPT, WC>(xr, C, xv);
-    fwd_token<TX, N, VPT>(b, coef, coef_stride, wv, xv, out, rms_out, C, eps, red);
+    fwd_token<TX, TO, N, VPT>(b, coef, coef_stride, wv, xv, out, rms_out, C, eps, red);
 }
 
 // ---------------------------------------------------------------------------
@@ -588,9 +588,9 @@ hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, co
         default: break;                                          \
     }
 
-template <typename TX, int N, int V>
+template <typename TX, typename TO, int N, int V>
 static const void* fwd_fn() {
-    if constexpr (layer_row_fits(N, V)) return reinterpret_cast<const void*>(&layer_fwd_kernel<TX, N, V>);
+    if constexpr (layer_row_fits(N, V)) return reinterpret_cast<const void*>(&layer_fwd_kernel<TX, TO, N, V>);
     return nullptr;
 }
 
@@ -600,13 +600,19 @@ static const void* bwd_fn() {
     return nullptr;
 }
 
-static const void* pick_fwd(int x_dtype, int n, int vpt) {
+static const void* pick_fwd(int x_dtype, int out_dtype, int n, int vpt) {
     const void* fn = nullptr;
+#define MHC_FWD_TO(TX_, N_)                                                      \
+    if (out_dtype == kBF16) {                                                    \
+        MHC_PICK_VPT(vpt, fn = fwd_fn<TX_, bf16_t, N_, V_>());                   \
+    } else {                                                                     \
+        MHC_PICK_VPT(vpt, fn = fwd_fn<TX_, float, N_, V_>());                    \
+    }
 #define MHC_FWD_N(N_)                                                            \
     if (x_dtype == kBF16) {                                                      \
-        MHC_PICK_VPT(vpt, fn = fwd_fn<bf16_t, N_, V_>());                        \
+        MHC_FWD_TO(bf16_t, N_)                                                   \
     } else {                                                                     \
-        MHC_PICK_VPT(vpt, fn = fwd_fn<float, N_, V_>());                         \
+        MHC_FWD_TO(float, N_)                                                    \
     }
     switch (n) {
         case 2: { MHC_FWD_N(2); break; }
@@ -615,6 +621,7 @@ static const void* pick_fwd(int x_dtype, int n, int vpt) {
         default: break;
     }
 #undef MHC_FWD_N
+#undef MHC_FWD_TO
     return fn;
 }
 
@@ -656,12 +663,12 @@ static int persistent_grid(const void* fn, int threads, int64_t B) {
 static bool use_prefetch(const RowTiling& t) { return t.threads <= 256; }
 
 hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
-                            int64_t coef_stride, float* out, float* rms_out, int64_t B, int64_t C, float eps,
-                            hipStream_t s) {
+                            int64_t coef_stride, void* out, int out_dtype, float* rms_out, int64_t B, int64_t C,
+                            float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
     const RowTiling t = choose_row_tiling(C, kLayerWC, n, 512);
     if (t.vpt <= 0) return hipErrorInvalidValue;
-    const void* fn = pick_fwd(x_dtype, n, t.vpt);
+    const void* fn = pick_fwd(x_dtype, out_dtype, n, t.vpt);
     if (!fn) return hipErrorInvalidValue;
     if (B > 0x7fffffff) return hipErrorInvalidValue;  // grid x limit
     const unsigned grid = (unsigned)B;  // one token per workgroup

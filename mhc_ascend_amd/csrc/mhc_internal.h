@@ -42,9 +42,10 @@ int saved_w_offset(int n);
 hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res,
                               const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
                               hipStream_t s);
+// out is [B, n, C] in out_dtype (fp32, or bf16 for the inference entry).
 hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
-                            int64_t coef_stride, float* out, float* rms_out, int64_t B, int64_t C, float eps,
-                            hipStream_t s);
+                            int64_t coef_stride, void* out, int out_dtype, float* rms_out, int64_t B, int64_t C,
+                            float eps, hipStream_t s);
 // mode 0: static (writes dx, per-workgroup sums of [dM, dh_post_act,
 //         dh_pre_act] into scal_out[grid][n*n+2n]);
 // mode 1: dx = stream terms only, and per token scal_out[B][n*n+2n+2] =

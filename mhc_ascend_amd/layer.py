@@ -57,6 +57,7 @@ class MHCLayer(nn.Module):
             self.H_pre = nn.Parameter(torch.zeros(n, dtype=torch.float32))
             self.H_post = nn.Parameter(torch.zeros(n, dtype=torch.float32))
             self.H_res = nn.Parameter((alpha_init * torch.randn(n, n)).float())
+        self._inference_pack = None  # (parameter versions, packed tensor)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B, n, C = x.shape
@@ -69,13 +70,43 @@ class MHCLayer(nn.Module):
                 return ops.mhc_layer_fused_dynamic_inference(
                     x, self.rmsnorm_weight, self.phi_pre, self.phi_post, self.phi_res,
                     self.alpha_pre, self.alpha_post, self.alpha_res, self.b_pre, self.b_post, self.b_res,
-                    self.num_sinkhorn_iters, self.sinkhorn_eps, self.rmsnorm_eps)
+                    self.num_sinkhorn_iters, self.sinkhorn_eps, self.rmsnorm_eps, packed=self._packed())
             return ops.mhc_layer_fused_dynamic_training(
                 x, self.rmsnorm_weight, self.phi_pre, self.phi_post, self.phi_res,
                 self.alpha_pre, self.alpha_post, self.alpha_res, self.b_pre, self.b_post, self.b_res,
                 self.num_sinkhorn_iters, self.sinkhorn_eps, self.rmsnorm_eps)
         return ops.mhc_layer_static(x, self.rmsnorm_weight, self.H_pre, self.H_post, self.H_res,
                                     self.num_sinkhorn_iters, self.sinkhorn_eps, self.rmsnorm_eps)
+
+    # ---- forward-only dynamic H ------------------------------------------
+    def _pack_key(self):
+        return tuple((p.data_ptr(), p._version)
+                     for p in (self.rmsnorm_weight, self.phi_pre, self.phi_post, self.phi_res))
+
+    def prepare_inference(self) -> None:
+        """Pack the weight and projections once for eval-mode, no-grad
+        forwards (dynamic H only), instead of on every call.  The snapshot is
+        dropped when a parameter is updated in place (optimizer steps,
+        load_state_dict), moved, or the layer is put back into training mode;
+        writes through ``.data`` bypass that check, so call this again after
+        them."""
+        if not self.use_dynamic_h:
+            return
+        with torch.no_grad():
+            packed = ops.native.mhc_layer_dynamic_pack(self.rmsnorm_weight, self.phi_pre, self.phi_post,
+                                                       self.phi_res)
+        self._inference_pack = (self._pack_key(), packed)
+
+    def _packed(self):
+        if self._inference_pack is not None and self._inference_pack[0] == self._pack_key():
+            return self._inference_pack[1]
+        self._inference_pack = None
+        return None
+
+    def train(self, mode: bool = True):
+        if mode:
+            self._inference_pack = None
+        return super().train(mode)
 
     def extra_repr(self) -> str:
         return (

@@ -414,6 +414,56 @@ def mhc_layer_dynamic_fwd(x_expanded: torch.Tensor, rmsnorm_weight: torch.Tensor
     return out, saved
 
 
+def mhc_layer_dynamic_pack(rmsnorm_weight: torch.Tensor, phi_pre: torch.Tensor, phi_post: torch.Tensor,
+                           phi_res: torch.Tensor) -> torch.Tensor:
+    """The parameter-only part of the dynamic forward (fp32 weight, projection
+    planes) packed for mhc_layer_dynamic_infer: repack after every parameter
+    update.  Returns an opaque uint8 device tensor."""
+    _check_device("mhc_layer_dynamic_pack", rmsnorm_weight, phi_pre, phi_post, phi_res)
+    w = _weight(rmsnorm_weight)
+    C = w.numel()
+    n = phi_pre.size(0) if phi_pre.dim() > 0 else 0
+    pp, pq, pr = _phi_parts(phi_pre, phi_post, phi_res, n, n * C)
+    dev = w.device
+    lib = _lib.load()
+    nbytes = int(lib.mhc_layer_dynamic_packed_size(n, C))
+    packed = _ws(dev, nbytes)
+    with torch.cuda.device(dev):
+        call("mhc_layer_dynamic_pack", ptr(w), dtype_code(w.dtype), ptr(pp), ptr(pq), ptr(pr), ptr(packed), nbytes,
+             n, C, stream_of(w))
+    return packed
+
+
+def mhc_layer_dynamic_infer(x_expanded: torch.Tensor, packed: torch.Tensor, alpha_pre, alpha_post, alpha_res,
+                            b_pre: torch.Tensor, b_post: torch.Tensor, b_res: torch.Tensor, sinkhorn_iters: int = 20,
+                            sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5,
+                            out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Forward-only dynamic-H layer on parameters packed by
+    mhc_layer_dynamic_pack: out [B, n, C] in out_dtype (fp32 or bf16).  No
+    state for a backward is written (ops.py:337-380)."""
+    _check_device("mhc_layer_dynamic_infer", x_expanded, packed, b_pre, b_post, b_res)
+    x = _layer_x("mhc_layer_dynamic_infer", x_expanded)
+    B, n, C = x.shape
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError("mhc_layer_dynamic_infer: out_dtype must be torch.float32 or torch.bfloat16")
+    lib = _lib.load()
+    if packed.dtype != torch.uint8 or packed.numel() < lib.mhc_layer_dynamic_packed_size(n, C):
+        raise RuntimeError("mhc_layer_dynamic_infer: packed parameters do not match x [B, n, C]")
+    dev = x.device
+    a = [_scalar_param(v, dev) for v in (alpha_pre, alpha_post, alpha_res)]
+    bp, bq, br = _f32c(b_pre), _f32c(b_post), _f32c(b_res)
+    if bp.numel() != n or bq.numel() != n or br.numel() != n * n:
+        raise RuntimeError("mhc_layer_dynamic_infer: b_pre/b_post must have n and b_res n*n elements")
+    out = torch.empty((B, n, C), dtype=out_dtype, device=dev)
+    with torch.cuda.device(dev):
+        wsb = lib.mhc_layer_dynamic_infer_workspace_size(B, n, C)
+        ws = _ws(dev, wsb)
+        call("mhc_layer_dynamic_infer", ptr(x), dtype_code(x.dtype), ptr(packed), ptr(a[0]), ptr(a[1]), ptr(a[2]),
+             ptr(bp), ptr(bq), ptr(br), ptr(out), dtype_code(out_dtype), ptr(ws), int(wsb), B, n, C,
+             int(sinkhorn_iters), float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
+    return out
+
+
 def mhc_layer_dynamic_bwd(grad_output: torch.Tensor, x_expanded: torch.Tensor, rmsnorm_weight: torch.Tensor,
                           saved: torch.Tensor, phi_pre: torch.Tensor, phi_post: torch.Tensor, phi_res: torch.Tensor,
                           alpha_pre, alpha_post, alpha_res, b_pre: torch.Tensor, b_post: torch.Tensor,

@@ -195,12 +195,18 @@ def fused_rmsnorm_matmul(x_flat: torch.Tensor, phi_concat: torch.Tensor) -> torc
 
 def mhc_layer_fused_dynamic_inference(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
                                       alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters: int = 20,
-                                      sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5) -> torch.Tensor:
-    """Dynamic-H forward without autograd state (ops.py:337-380)."""
-    out, _ = native.mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
-                                          alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
-                                          rmsnorm_eps)
-    return out
+                                      sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5,
+                                      out_dtype: torch.dtype = torch.float32, packed=None) -> torch.Tensor:
+    """Dynamic-H forward without autograd state (ops.py:337-380).
+
+    Extensions (keyword-only in practice, defaults give the reference's
+    result): ``out_dtype=torch.bfloat16`` writes the output in bf16;
+    ``packed`` (from native.mhc_layer_dynamic_pack on the same weight and
+    projections) skips the per-call packing of the parameters."""
+    if packed is None:
+        packed = native.mhc_layer_dynamic_pack(rmsnorm_weight, phi_pre, phi_post, phi_res)
+    return native.mhc_layer_dynamic_infer(x_expanded, packed, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
+                                          sinkhorn_iters, sinkhorn_eps, rmsnorm_eps, out_dtype)
 
 
 class MHCLayerDynamicFunction(torch.autograd.Function):

@@ -119,6 +119,69 @@ def test_dynamic_inference_equals_training_forward(device):
     assert torch.equal(out_t, out_i)
 
 
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,B,C", [(4, 1, 64), (4, 37, 1280), (2, 9, 256), (4, 300, 4096)])
+def test_dynamic_inference_packed_and_bf16_out(device, x_dtype, n, B, C):
+    """The forward-only entry on packed parameters: its fp32 output is the
+    training forward's bit for bit, its bf16 output is that result rounded to
+    nearest even, and the oracle bounds both."""
+    d = R.dynamic_layer_inputs(B, n, C, seed=3 * B + C + n, x_dtype=x_dtype, alpha=0.3, phi_std=0.05, b_std=0.5)
+    x = d["x"].to(device)
+    ps = [d[k].to(device) for k in PARAMS]
+    with torch.no_grad():
+        fwd_out, _ = native.mhc_layer_dynamic_fwd(x, *ps, 20, 1e-8, 1e-5)
+        packed = native.mhc_layer_dynamic_pack(*ps[:4])
+        o32 = native.mhc_layer_dynamic_infer(x, packed, *ps[4:], 20, 1e-8, 1e-5)
+        o16 = native.mhc_layer_dynamic_infer(x, packed, *ps[4:], 20, 1e-8, 1e-5, out_dtype=torch.bfloat16)
+        o16_api = mhc.mhc_layer_fused_dynamic_inference(x, *ps, 20, 1e-8, 1e-5, out_dtype=torch.bfloat16)
+    assert o32.dtype == torch.float32 and o16.dtype == torch.bfloat16
+    assert torch.equal(o32, fwd_out)
+    assert torch.equal(o16, fwd_out.to(torch.bfloat16))
+    assert torch.equal(o16_api, o16)
+    rout = R.mhc_layer_dynamic(d["x"].double(), *[d[k].double() for k in PARAMS], 20, 1e-8, 1e-5,
+                               dtype=torch.float64)
+    assert_close(o32, rout, what=f"infer n={n} B={B} C={C}", **FWD)
+    assert_close(o16, rout, 2 ** -8, 1e-5, f"infer bf16 out n={n} B={B} C={C}")
+
+
+def test_dynamic_module_inference_pack_snapshot(device):
+    """prepare_inference() packs once; an in-place parameter update drops the
+    snapshot, and the eval forward then equals the training forward on the
+    new parameters."""
+    torch.manual_seed(6)
+    layer = mhc.MHCLayer(512, 4).to(device).eval()
+    x = torch.randn(20, 4, 512, generator=_gen(6)).to(device)
+    with torch.no_grad():
+        base = layer(x)
+        layer.prepare_inference()
+        assert layer._packed() is not None
+        assert torch.equal(layer(x), base)
+        layer.phi_res.add_(0.05 * torch.randn(layer.phi_res.shape, generator=_gen(7)).to(device))
+        assert layer._packed() is None
+        after = layer(x)
+    assert not torch.equal(after, base)
+    layer.train()
+    assert torch.equal(after, layer(x).detach())
+    layer.eval()
+    layer.prepare_inference()
+    layer.train()
+    assert layer._inference_pack is None
+
+
+def test_dynamic_inference_rejects_bad_arguments(device):
+    layer = mhc.MHCLayer(64, 4).to(device)
+    scal = [layer.alpha_pre, layer.alpha_post, layer.alpha_res, layer.b_pre, layer.b_post, layer.b_res]
+    with torch.no_grad():
+        packed = native.mhc_layer_dynamic_pack(layer.rmsnorm_weight, layer.phi_pre, layer.phi_post, layer.phi_res)
+        with pytest.raises(RuntimeError, match="packed parameters do not match"):
+            native.mhc_layer_dynamic_infer(torch.randn(3, 4, 128, device=device), packed, *scal)
+        with pytest.raises(RuntimeError, match="out_dtype"):
+            native.mhc_layer_dynamic_infer(torch.randn(3, 4, 64, device=device), packed, *scal,
+                                           out_dtype=torch.float16)
+        empty = native.mhc_layer_dynamic_infer(torch.randn(0, 4, 64, device=device), packed, *scal)
+    assert tuple(empty.shape) == (0, 4, 64)
+
+
 def test_dynamic_module_train_and_eval(device):
     torch.manual_seed(4)
     layer = mhc.MHCLayer(256, 4, use_dynamic_h=True).to(device)
