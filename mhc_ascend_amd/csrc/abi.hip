@@ -182,7 +182,7 @@ int mhc_sinkhorn_knopp_fwd(const float* inp, float* out, int64_t batch, int32_t 
     MHC_REQUIRE(num_iters >= 0, "sinkhorn_knopp_fwd: num_iters must be >= 0");
     if (batch == 0) return MHC_SUCCESS;
     MHC_REQUIRE(inp && out, "sinkhorn_knopp_fwd: null pointer");
-    if (n > 8) return fail(MHC_ERR_UNSUPPORTED, "sinkhorn_knopp_fwd: n > 8 is not compiled in this build");
+    if (n > 64) return fail(MHC_ERR_UNSUPPORTED, "sinkhorn_knopp_fwd: n > 64 is not supported (one matrix row per lane of a wave)");
     return hip_status(launch_sinkhorn_fwd(n, inp, out, batch, num_iters, eps, (hipStream_t)stream));
 }
 
@@ -194,7 +194,7 @@ int mhc_sinkhorn_knopp_bwd(const float* grad_out, const float* inp, const float*
     MHC_REQUIRE(num_iters >= 0, "sinkhorn_knopp_bwd: num_iters must be >= 0");
     if (batch == 0) return MHC_SUCCESS;
     MHC_REQUIRE(grad_out && inp && grad_inp, "sinkhorn_knopp_bwd: null pointer");
-    if (n > 8) return fail(MHC_ERR_UNSUPPORTED, "sinkhorn_knopp_bwd: n > 8 is not compiled in this build");
+    if (n > 64) return fail(MHC_ERR_UNSUPPORTED, "sinkhorn_knopp_bwd: n > 64 is not supported (one matrix row per lane of a wave)");
     return hip_status(launch_sinkhorn_bwd(n, grad_out, inp, grad_inp, batch, num_iters, eps, (hipStream_t)stream));
 }
 

@@ -424,6 +424,67 @@ __device__ __forceinline__ void sk_backward(float (&g)[N], const float (&x0)[N],
 }
 
 // ---------------------------------------------------------------------------
+// Sinkhorn-Knopp on an n x n matrix with n <= NM (NM = 16, 32 or 64) held one
+// row per lane in a group of NM lanes, for n above the exact instantiations.
+// Columns c >= n are padding: they hold zero, take no part in the column
+// steps (with eps = 0 their scale would be 1/0) and their adjoint is zero.
+// Same formulas as sk_forward / sk_adjoint_step; the backward recomputes each
+// iteration's state from x0 (no history: a row is NM registers).
+// ---------------------------------------------------------------------------
+template <int NM>
+__device__ __forceinline__ void skw_col_step(float (&a)[NM], int n, float eps) {
+#pragma unroll
+    for (int c = 0; c < NM; ++c) {
+        if (c < n) a[c] *= rcp_nr(group_sum<NM>(a[c]) + eps);
+    }
+}
+
+template <int NM>
+__device__ __forceinline__ void skw_forward(float (&a)[NM], int n, int iters, float eps, bool active) {
+    for (int t = 0; t < iters; ++t) {
+        float rinv;
+        sk_row_step<NM>(a, eps, active, rinv);
+        skw_col_step<NM>(a, n, eps);
+    }
+}
+
+template <int NM>
+__device__ __forceinline__ void skw_adjoint_step(float (&g)[NM], const float (&A)[NM], int n, float rinv,
+                                                 float eps) {
+    float dA[NM];
+#pragma unroll
+    for (int c = 0; c < NM; ++c) {
+        dA[c] = 0.f;
+        if (c < n) {
+            const float cinv = rcp_nr(group_sum<NM>(A[c]) + eps);
+            const float dot = group_sum<NM>(g[c] * (A[c] * cinv));
+            dA[c] = (g[c] - dot) * cinv;
+        }
+    }
+    float rdot = 0.f;
+#pragma unroll
+    for (int c = 0; c < NM; ++c) rdot += dA[c] * A[c];
+#pragma unroll
+    for (int c = 0; c < NM; ++c) g[c] = c < n ? (dA[c] - rdot) * rinv : 0.f;
+}
+
+template <int NM>
+__device__ __forceinline__ void skw_backward(float (&g)[NM], const float (&x0)[NM], int n, int iters, float eps,
+                                             bool active) {
+    for (int t = iters - 1; t >= 0; --t) {
+        float a[NM];
+#pragma unroll
+        for (int c = 0; c < NM; ++c) a[c] = x0[c];
+        float rinv = 0.f;
+        for (int s = 0; s <= t; ++s) {
+            sk_row_step<NM>(a, eps, active, rinv);
+            if (s < t) skw_col_step<NM>(a, n, eps);
+        }
+        skw_adjoint_step<NM>(g, a, n, rinv, eps);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Sinkhorn-Knopp on a 4 x 4 matrix held one element per lane in a 16-lane DPP
 // row (lane 4 r + c of the row holds element (r, c)): a row sum is a quad
 // reduction, a column sum two rotations within the row, so an iteration is a

@@ -7,7 +7,9 @@
 // history (post-row-step rows and row sums) in registers and applies the
 // exact adjoint (the reference's row step is approximate,
 // sinkhorn_knopp.cpp:1773-1795).  Small n = 4 batches run one element per
-// lane of a 16-lane DPP row instead (sk16_* in mhc_device.h).
+// lane of a 16-lane DPP row instead (sk16_* in mhc_device.h); 8 < n <= 64
+// runs the masked wide kernels (skw_*), whose backward recomputes the
+// forward state per iteration instead of keeping a history.
 #include "mhc_device.h"
 #include "mhc_internal.h"
 
@@ -102,6 +104,66 @@ __global__ __launch_bounds__(256) void sinkhorn16_bwd_kernel(const float* __rest
     if (ok) grad_inp[gid] = g;
 }
 
+// 8 < n <= 64: one matrix per group of NM = pow2ceil(n) lanes (16, 32 or
+// 64), one row per lane, n taken at run time with the padded columns masked.
+template <int NM>
+__global__ __launch_bounds__(256) void sinkhorn_wide_fwd_kernel(const float* __restrict__ inp,
+                                                                float* __restrict__ out, int n, int64_t batch,
+                                                                int iters, float eps) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t m = gid / NM;
+    const int r = (int)(gid % NM);
+    const bool ok = (m < batch) && (r < n);
+    const float* row = inp + (m * n + r) * n;
+    float a[NM];
+#pragma unroll
+    for (int c = 0; c < NM; ++c) a[c] = (ok && c < n) ? row[c] : 0.f;
+    skw_forward<NM>(a, n, iters, eps, ok);
+    if (ok) {
+        float* o = out + (m * n + r) * n;
+#pragma unroll
+        for (int c = 0; c < NM; ++c) {
+            if (c < n) o[c] = a[c];
+        }
+    }
+}
+
+template <int NM>
+__global__ __launch_bounds__(256) void sinkhorn_wide_bwd_kernel(const float* __restrict__ grad_out,
+                                                                const float* __restrict__ inp,
+                                                                float* __restrict__ grad_inp, int n, int64_t batch,
+                                                                int iters, float eps) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t m = gid / NM;
+    const int r = (int)(gid % NM);
+    const bool ok = (m < batch) && (r < n);
+    const int64_t off = (m * n + r) * n;
+    float x0[NM], g[NM];
+#pragma unroll
+    for (int c = 0; c < NM; ++c) {
+        x0[c] = (ok && c < n) ? inp[off + c] : 0.f;
+        g[c] = (ok && c < n) ? grad_out[off + c] : 0.f;
+    }
+    skw_backward<NM>(g, x0, n, iters, eps, ok);
+    if (ok) {
+#pragma unroll
+        for (int c = 0; c < NM; ++c) {
+            if (c < n) grad_inp[off + c] = g[c];
+        }
+    }
+}
+
+#define MHC_SK_WIDE(n, ...)                                                   \
+    if (n <= 16) {                                                            \
+        constexpr int NM_ = 16; __VA_ARGS__;                                  \
+    } else if (n <= 32) {                                                     \
+        constexpr int NM_ = 32; __VA_ARGS__;                                  \
+    } else if (n <= 64) {                                                     \
+        constexpr int NM_ = 64; __VA_ARGS__;                                  \
+    } else {                                                                  \
+        return hipErrorInvalidValue;                                          \
+    }
+
 #define MHC_SK_DISPATCH(n, ...)                                   \
     switch (n) {                                                  \
         case 1: { constexpr int N_ = 1; __VA_ARGS__; break; }     \
@@ -125,6 +187,9 @@ hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batc
     if (n == 4 && batch < kSk16MaxBatch) {
         hipLaunchKernelGGL(sinkhorn16_fwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s, inp, out,
                            batch, iters, eps);
+    } else if (n > 8) {
+        MHC_SK_WIDE(n, hipLaunchKernelGGL((sinkhorn_wide_fwd_kernel<NM_>), dim3(blocks), dim3(256), 0, s, inp, out, n,
+                                          batch, iters, eps));
     } else {
         MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, inp, out,
                                               batch, iters, eps));
@@ -143,6 +208,9 @@ hipError_t launch_sinkhorn_bwd(int n, const float* grad_out, const float* inp, f
     if (n == 4 && batch < kSk16MaxBatch) {
         hipLaunchKernelGGL(sinkhorn16_bwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s,
                            grad_out, inp, grad_inp, batch, iters, eps);
+    } else if (n > 8) {
+        MHC_SK_WIDE(n, hipLaunchKernelGGL((sinkhorn_wide_bwd_kernel<NM_>), dim3(blocks), dim3(256), 0, s, grad_out,
+                                          inp, grad_inp, n, batch, iters, eps));
     } else {
         MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, grad_out,
                                               inp, grad_inp, batch, iters, eps));

@@ -47,6 +47,14 @@ def test_sinkhorn_rejects_bad_arguments_on_host(n, iters, batch):
     assert lib.mhc_last_error()
 
 
+def test_sinkhorn_rejects_n_above_a_wave_on_host():
+    """Rows of one matrix live in the lanes of one wave: n <= 64."""
+    lib = _lib.load()
+    assert lib.mhc_sinkhorn_knopp_fwd(1, 1, 4, 65, 20, 1e-8, None) == -2
+    assert b"n > 64" in lib.mhc_last_error()
+    assert lib.mhc_sinkhorn_knopp_bwd(1, 1, 1, 1, 4, 65, 20, 1e-8, None) == -2
+
+
 def test_layer_rejects_unsupported_and_invalid_on_host():
     lib = _lib.load()
     # n not compiled -> UNSUPPORTED; bad dtype -> INVALID; ragged hidden -> UNSUPPORTED

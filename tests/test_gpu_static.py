@@ -28,7 +28,7 @@ def _gen(seed):
 # Sinkhorn-Knopp
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8, 9, 16, 24, 32, 64])
 @pytest.mark.parametrize("iters", [0, 1, 20, 40])
 def test_sinkhorn_fwd_bwd_matches_oracle(device, n, iters):
     B = 333  # not a multiple of the matrices per wave
@@ -45,10 +45,11 @@ def test_sinkhorn_fwd_bwd_matches_oracle(device, n, iters):
     assert_close(ad.grad, gref, 1e-3, max(grad_atol(gref, 1e-5), 1e-6), f"SK bwd n={n} T={iters}")
 
 
-@pytest.mark.parametrize("n", [3, 5, 6, 7])
+@pytest.mark.parametrize("n", [3, 5, 6, 7, 12, 20, 40])
 def test_sinkhorn_padded_groups_with_zero_eps(device, n):
-    """n that is not a power of two leaves padding lanes in each lane group;
-    with eps = 0 they must not divide by zero into the real rows' sums."""
+    """n that is not a power of two leaves padding lanes in each lane group
+    (and, above 8, padding columns in each row); with eps = 0 they must not
+    divide by zero into the real rows' sums."""
     g = _gen(7 + n)
     a = torch.exp(torch.randn(100, n, n, generator=g))
     go = torch.randn(100, n, n, generator=g)
