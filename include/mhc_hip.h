@@ -167,11 +167,12 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
 
 /* ---- dynamic-H projection ----------------------------------------------------
  * out[b, o] = sum_k inp[b, k] weight[o, k]: inp [batch, k] (dtype), weight
- * [out_dim, k] fp32, out [batch, out_dim] fp32; out_dim <= 32, k % 32 == 0.
+ * [out_dim, k] fp32, out [batch, out_dim] fp32; out_dim <= 8192 (tiles of
+ * 32 rows, one pass over inp each), k % 32 == 0.
  * bf16 MFMA on a hi/lo bf16 split of the operands (about fp32 accuracy).
  * Replaces fused_rmsnorm_matmul_fwd (bindings.cpp:480-528), which rounds
  * inputs and result to bf16. */
-size_t mhc_fused_rmsnorm_matmul_fwd_workspace_size(int64_t batch, int64_t k);
+size_t mhc_fused_rmsnorm_matmul_fwd_workspace_size(int64_t batch, int64_t k, int32_t out_dim);
 int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* weight, float* out, void* workspace,
                                  size_t workspace_bytes, int64_t batch, int64_t k, int32_t out_dim, void* stream);
 

@@ -40,7 +40,7 @@ static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
 // The fused layer kernels are compiled for n in {2, 4, 8}; dynamic H needs
 // 2n + n^2 <= 32 projection outputs (n <= 4); the fused wrapper is n = 4.
 static bool supported_layer_n(int n) { return n == 2 || n == 4 || n == 8; }
-static bool supported_dynamic_n(int n) { return n == 2 || n == 4; }
+static bool supported_dynamic_n(int n) { return n == 2 || n == 4 || n == 8; }
 // the standalone aggregate / distribute operators
 static bool supported_ops_n(int n) { return n == 1 || n == 2 || n == 4 || n == 8; }
 
@@ -147,7 +147,7 @@ using namespace mhc;
 
 extern "C" {
 
-int mhc_abi_version(void) { return 100; }
+int mhc_abi_version(void) { return 101; }
 
 const char* mhc_last_error(void) { return g_last_error.c_str(); }
 
@@ -447,12 +447,16 @@ struct ProjFwdWs {
     size_t phib_off, p_off, ss_off, total;
 };
 
-static ProjFwdWs proj_fwd_ws(int64_t batch, int64_t k) {
+// [Phi planes (three bf16 planes per 32-row output tile) | P partials
+//  [tile][ks][B][32] | sum x^2 partials [ks][B]]
+static size_t phi_planes_bytes(int64_t k, int np) { return align256((size_t)proj_tiles(np) * 3 * 32 * k * 2); }
+
+static ProjFwdWs proj_fwd_ws(int64_t batch, int64_t k, int np) {
     ProjFwdWs w{};
     w.ks = batch > 0 ? proj_ksplit(batch, k) : 1;
     w.phib_off = 0;
-    w.p_off = align256((size_t)3 * 32 * k * 2);  // three bf16 planes of Phi
-    w.ss_off = w.p_off + align256((size_t)w.ks * batch * 32 * sizeof(float));
+    w.p_off = phi_planes_bytes(k, np);
+    w.ss_off = w.p_off + align256((size_t)proj_tiles(np) * w.ks * batch * kProjTile * sizeof(float));
     w.total = w.ss_off + align256((size_t)w.ks * batch * sizeof(float));
     return w;
 }
@@ -460,15 +464,17 @@ static ProjFwdWs proj_fwd_ws(int64_t batch, int64_t k) {
 static int check_proj(const char* fn, int64_t batch, int64_t k, int32_t out_dim) {
     if (batch < 0 || k < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": batch must be >= 0 and k >= 1");
     if (out_dim < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": out_dim must be >= 1");
-    if (out_dim > 32) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": out_dim > 32 is not supported");
+    if (out_dim > kMaxProjRows)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": out_dim > " + std::to_string(kMaxProjRows) +
+                                             " is not supported");
     if (k % 32 != 0) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": k must be a multiple of 32");
     if (k > (int64_t(1) << 22)) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": k > 4194304 is not supported");
     return MHC_SUCCESS;
 }
 
-size_t mhc_fused_rmsnorm_matmul_fwd_workspace_size(int64_t batch, int64_t k) {
-    if (batch < 0 || k < 1) return 0;
-    return proj_fwd_ws(batch, k).total;
+size_t mhc_fused_rmsnorm_matmul_fwd_workspace_size(int64_t batch, int64_t k, int32_t out_dim) {
+    if (batch < 0 || k < 1 || out_dim < 1) return 0;
+    return proj_fwd_ws(batch, k, out_dim).total;
 }
 
 int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* weight, float* out, void* workspace,
@@ -478,7 +484,7 @@ int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* we
     MHC_REQUIRE(valid_dtype(dtype), "fused_rmsnorm_matmul_fwd: dtype must be F32 or BF16");
     MHC_REQUIRE(weight && (batch == 0 || (inp && out)), "fused_rmsnorm_matmul_fwd: null pointer");
     if (batch == 0) return MHC_SUCCESS;
-    const ProjFwdWs w = proj_fwd_ws(batch, k);
+    const ProjFwdWs w = proj_fwd_ws(batch, k, out_dim);
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "fused_rmsnorm_matmul_fwd: workspace too small");
     hipStream_t s = (hipStream_t)stream;
@@ -486,7 +492,7 @@ int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* we
     float* pp = (float*)((char*)workspace + w.p_off);
     float* ss = (float*)((char*)workspace + w.ss_off);
     hipError_t e = launch_phi_split(weight, weight, weight, out_dim, out_dim, k, phib, s);
-    if (e == hipSuccess) e = launch_proj_mfma(dtype, inp, phib, pp, ss, batch, k, w.ks, s);
+    if (e == hipSuccess) e = launch_proj_mfma(dtype, inp, phib, out_dim, pp, ss, batch, k, w.ks, s);
     if (e == hipSuccess) e = launch_proj_reduce(pp, w.ks, batch, out_dim, out, s);
     return hip_status(e);
 }
@@ -496,13 +502,43 @@ struct ProjBwdWs {
     size_t part_off, stage_off, total;
 };
 
+// dPhi partials and column-sum stage for one 32-row output tile at a time
+// (the output tiles are reduced one after another through the same buffers).
+static int tile_rows(int np) { return np < kProjTile ? np : kProjTile; }
+
 static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
     ProjBwdWs w{};
     w.tiles = batch > 0 ? proj_bwd_tiles(kF32, batch, k) : 1;
     w.part_off = 0;
-    w.stage_off = align256((size_t)w.tiles * out_dim * k * sizeof(float));
-    w.total = w.stage_off + align256(column_sums_stage_floats((int64_t)out_dim * k) * sizeof(float));
+    w.stage_off = align256((size_t)w.tiles * tile_rows(out_dim) * k * sizeof(float));
+    w.total = w.stage_off + align256(column_sums_stage_floats((int64_t)tile_rows(out_dim) * k) * sizeof(float));
     return w;
+}
+
+// The projection backward over all output tiles of Phi (rows o0 = 32 t ..):
+// dx gets every tile's term (the first tile also s x, or starts from zero
+// when !accumulate), and each tile's dPhi partials are column-summed into
+// grad_phi rows o0 .. before the next tile reuses the partial buffer.
+static hipError_t proj_bwd_all(int x_dtype, const void* x, const float* dp, int dp_stride_, const float* s_tok,
+                               const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
+                               void* dx, bool accumulate, float* part, int tiles, float* stage, float* grad_phi,
+                               int64_t batch, int64_t K, hipStream_t s) {
+    hipError_t e = hipSuccess;
+    for (int o0 = 0; o0 < np && e == hipSuccess; o0 += kProjTile) {
+        const int rows_t = np - o0 < kProjTile ? np - o0 : kProjTile;
+        int rows = tiles;
+        if (batch == 0) {
+            rows = 1;
+            e = launch_fill_zero(part, (int64_t)rows_t * K, s);
+        } else {
+            e = launch_proj_bwd(x_dtype, x, dp + o0, dp_stride_, o0 == 0 ? s_tok : nullptr, phi_pre, phi_post,
+                                phi_res, n_pre, o0, rows_t, dx, accumulate || o0 > 0, part, tiles, batch, K, s);
+        }
+        if (e == hipSuccess)
+            e = launch_column_finalize(0, kF32, part, rows, (int64_t)rows_t * K, stage, grad_phi + (int64_t)o0 * K,
+                                      nullptr, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+    }
+    return e;
 }
 
 size_t mhc_fused_rmsnorm_matmul_bwd_workspace_size(int64_t batch, int64_t k, int32_t out_dim) {
@@ -523,20 +559,8 @@ int mhc_fused_rmsnorm_matmul_bwd(const float* grad_out, const float* x_flat, con
     hipStream_t s = (hipStream_t)stream;
     float* part = (float*)((char*)workspace + w.part_off);
     float* stage = (float*)((char*)workspace + w.stage_off);
-    const int64_t cols = (int64_t)out_dim * k;
-    int rows = w.tiles;
-    hipError_t e;
-    if (batch == 0) {
-        rows = 1;
-        e = launch_fill_zero(part, cols, s);
-    } else {
-        e = launch_proj_bwd(kF32, x_flat, grad_out, out_dim, nullptr, phi, phi, phi, out_dim, out_dim, grad_x,
-                            false, part, w.tiles, batch, k, s);
-    }
-    if (e == hipSuccess)
-        e = launch_column_finalize(0, kF32, part, rows, cols, stage, grad_phi, nullptr, 0, nullptr, nullptr, nullptr,
-                                  nullptr, nullptr, nullptr, 0, 0.f, s);
-    return hip_status(e);
+    return hip_status(proj_bwd_all(kF32, x_flat, grad_out, out_dim, nullptr, phi, phi, phi, out_dim, out_dim, grad_x,
+                                   false, part, w.tiles, stage, grad_phi, batch, k, s));
 }
 
 // ---- fused dynamic-H layer ----------------------------------------------------
@@ -563,7 +587,7 @@ size_t mhc_layer_dynamic_saved_size(int64_t batch, int32_t n, int32_t hidden) {
 
 size_t mhc_layer_dynamic_fwd_workspace_size(int64_t batch, int32_t n, int32_t hidden) {
     if (batch < 0 || n < 1 || hidden < 1) return 0;
-    return proj_fwd_ws(batch, (int64_t)n * hidden).total;
+    return proj_fwd_ws(batch, (int64_t)n * hidden, 2 * n + n * n).total;
 }
 
 static int check_dyn(const char* fn, int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype, int32_t w_dtype,
@@ -572,7 +596,7 @@ static int check_dyn(const char* fn, int64_t batch, int32_t n, int32_t hidden, i
     if (st) return st;
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (!supported_dynamic_n(n))
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": dynamic H is compiled for n in {2, 4}, not n=" +
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": dynamic H is compiled for n in {2, 4, 8}, not n=" +
                                              std::to_string(n));
     if (((int64_t)n * hidden) % 32 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
@@ -597,7 +621,7 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
     hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
     if (e != hipSuccess || batch == 0) return hip_status(e);
     const int64_t K = (int64_t)n * hidden;
-    const ProjFwdWs w = proj_fwd_ws(batch, K);
+    const ProjFwdWs w = proj_fwd_ws(batch, K, 2 * n + n * n);
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "layer_dynamic_fwd: workspace smaller than mhc_layer_dynamic_fwd_workspace_size()");
     bf16_raw_t* phib = (bf16_raw_t*)((char*)workspace + w.phib_off);
@@ -605,7 +629,7 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
     float* ss = (float*)((char*)workspace + w.ss_off);
     const int np = 2 * n + n * n;
     e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
-    if (e == hipSuccess) e = launch_proj_mfma(x_dtype, x, phib, pp, ss, batch, K, w.ks, s);
+    if (e == hipSuccess) e = launch_proj_mfma(x_dtype, x, phib, np, pp, ss, batch, K, w.ks, s);
     if (e == hipSuccess)
         e = launch_dyn_coef_fwd(n, pp, ss, w.ks, batch, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
                                 saved + d.coef_off, saved + d.p_off, saved + d.rh_off, num_iters, sinkhorn_eps,
@@ -622,7 +646,7 @@ static size_t packed_phib_off(int32_t hidden) { return align256((size_t)hidden *
 
 size_t mhc_layer_dynamic_packed_size(int32_t n, int32_t hidden) {
     if (n < 1 || hidden < 1) return 0;
-    return packed_phib_off(hidden) + align256((size_t)3 * 32 * ((int64_t)n * hidden) * 2);
+    return packed_phib_off(hidden) + phi_planes_bytes((int64_t)n * hidden, 2 * n + n * n);
 }
 
 int mhc_layer_dynamic_pack(const void* weight, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
@@ -646,7 +670,7 @@ static size_t infer_proj_off(int64_t batch, int32_t n) { return align256((size_t
 
 size_t mhc_layer_dynamic_infer_workspace_size(int64_t batch, int32_t n, int32_t hidden) {
     if (batch < 0 || n < 1 || hidden < 1) return 0;
-    const ProjFwdWs w = proj_fwd_ws(batch, (int64_t)n * hidden);
+    const ProjFwdWs w = proj_fwd_ws(batch, (int64_t)n * hidden, 2 * n + n * n);
     return infer_proj_off(batch, n) + (w.total - w.p_off);
 }
 
@@ -668,14 +692,14 @@ int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, 
     hipStream_t s = (hipStream_t)stream;
     const int64_t K = (int64_t)n * hidden;
     const int np = 2 * n + n * n;
-    const ProjFwdWs w = proj_fwd_ws(batch, K);
+    const ProjFwdWs w = proj_fwd_ws(batch, K, np);
     const float* w32 = (const float*)packed;
     const bf16_raw_t* phib = (const bf16_raw_t*)((const char*)packed + packed_phib_off(hidden));
     float* coef = (float*)workspace;
     char* pw = (char*)workspace + infer_proj_off(batch, n);
     float* pp = (float*)pw;
     float* ss = (float*)(pw + (w.ss_off - w.p_off));
-    hipError_t e = launch_proj_mfma(x_dtype, x, phib, pp, ss, batch, K, w.ks, s);
+    hipError_t e = launch_proj_mfma(x_dtype, x, phib, np, pp, ss, batch, K, w.ks, s);
     if (e == hipSuccess)
         e = launch_dyn_coef_fwd(n, pp, ss, w.ks, batch, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
                                 coef, nullptr, nullptr, num_iters, sinkhorn_eps, rmsnorm_eps, s);
@@ -699,12 +723,12 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     size_t o = 0;
     w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
     w.scal_off = o; o += align256((size_t)batch * (n * n + 2 * n + 2) * 4);
-    w.dp_off = o; o += align256((size_t)batch * 32 * 4);
+    w.dp_off = o; o += align256((size_t)batch * dp_stride((int)np) * 4);
     w.s_off = o; o += align256((size_t)batch * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
-    w.phip_off = o; o += align256((size_t)w.tiles * np * K * 4);
+    w.phip_off = o; o += align256((size_t)w.tiles * tile_rows((int)np) * K * 4);
     w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
-    w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)np * K) * 4);
+    w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)tile_rows((int)np) * K) * 4);
     w.total = o;
     return w;
 }
@@ -749,9 +773,8 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     hipError_t e = hipSuccess;
     int rows_w = w.grid, rows_p = w.tiles, rows_c = w.cblocks;
     if (batch == 0) {
-        rows_w = rows_p = rows_c = 1;
+        rows_w = rows_c = 1;
         e = launch_fill_zero(dw_part, hidden, s);
-        if (e == hipSuccess) e = launch_fill_zero(phip, (int64_t)np * K, s);
         if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
     } else {
         e = launch_layer_bwd(x_dtype, n, 1, grad_out, x, w32, saved + d.coef_off, np, grad_x, dw_part, scal, w.grid,
@@ -760,15 +783,12 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
                                     s);
-        if (e == hipSuccess)
-            e = launch_proj_bwd(x_dtype, x, dp, 32, stok, phi_pre, phi_post, phi_res, n, np, grad_x, true, phip,
-                                w.tiles, batch, K, s);
     }
     if (e == hipSuccess)
-        e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,
-                                  nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+        e = proj_bwd_all(x_dtype, x, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, np, grad_x, true, phip,
+                         rows_p, stp, grad_phi, batch, K, s);
     if (e == hipSuccess)
-        e = launch_column_finalize(0, kF32, phip, rows_p, (int64_t)np * K, stp, grad_phi, nullptr, 0, nullptr, nullptr,
+        e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
     if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
     return hip_status(e);

@@ -52,18 +52,23 @@ __device__ __forceinline__ void split3(float v, float& h, float& m, float& l) {
 // Phi -> bf16 planes in MFMA B-fragment order, p = hi / mid / lo:
 //   phif[((p * 2 + nt) * (K / 32) + ks) * 64 + lane]  (16 bytes = 8 bf16)
 //     = Phi_p[nt * 16 + lane % 16][32 ks + 8 (lane / 16) .. + 7]
-// so one wave's B operand of a 32-wide k step is 1 KB contiguous.  Rows
-// np..31 are zero.  Grid-stride over 2 * (K / 32) * 64 fragments.
+// so one wave's B operand of a 32-wide k step is 1 KB contiguous.  More
+// than 32 rows are split into output tiles of 32 rows, tile t at
+// phif + t * 6 * (K / 32) * 64 holding rows 32 t .. 32 t + 31; rows past np
+// are zero.  Grid-stride over tiles * 2 * (K / 32) * 64 fragments.
 __global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict__ pre, const float* __restrict__ post,
                                                         const float* __restrict__ res, int n, int np, int64_t K,
                                                         uint4* __restrict__ phif) {
     const int64_t ksteps = K / 32;
-    const int64_t total = 2 * ksteps * 64;
+    const int64_t per_tile = 2 * ksteps * 64;
+    const int64_t total = (int64_t)((np + 31) / 32) * per_tile;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int lane = (int)(i & 63);
-        const int64_t ks = (i >> 6) % ksteps;
-        const int nt = (int)((i >> 6) / ksteps);
-        const int o = nt * 16 + (lane & 15);
+        const int64_t t = i / per_tile;
+        const int64_t it = i - t * per_tile;
+        const int lane = (int)(it & 63);
+        const int64_t ks = (it >> 6) % ksteps;
+        const int nt = (int)((it >> 6) / ksteps);
+        const int o = (int)t * 32 + nt * 16 + (lane & 15);
         const int64_t k = ks * 32 + 8 * (lane >> 4);
         float v[8];
         if (o < np) {
@@ -84,7 +89,8 @@ __global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict_
         }
 #pragma unroll
         for (int p = 0; p < 3; ++p)
-            phif[((int64_t)(p * 2 + nt) * ksteps + ks) * 64 + lane] = make_uint4(w[p][0], w[p][1], w[p][2], w[p][3]);
+            phif[t * 3 * per_tile + ((int64_t)(p * 2 + nt) * ksteps + ks) * 64 + lane] =
+                make_uint4(w[p][0], w[p][1], w[p][2], w[p][3]);
     }
 }
 
@@ -98,7 +104,8 @@ __global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict_
 // bf16: P = x.(hi + mid + lo) (3 MFMAs per tile); fp32 x is split the same
 // way and the six products down to 2^-16 relative weight are kept
 // (xh.(hi+mid+lo) + xm.(hi+mid) + xl.hi), leaving terms of order 2^-24.
-// Also sum x^2.  p_part[ks][B][32], ss_part[ks][B].
+// Also sum x^2.  p_part[ks][B][32], ss_part[ks][B] (null: not stored; one
+// launch per 32-row output tile of Phi, all but the first without it).
 // Pipeline: x of stage s+2 and Phi of stage s+2 are in flight while stage s
 // is on the matrix cores; one barrier per stage.
 // ---------------------------------------------------------------------------
@@ -316,11 +323,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         s2 += __shfl_xor(s2, 16, kWave);
         s2 += __shfl_xor(s2, 32, kWave);
         const int64_t tok = tok0 + mt * 16 + row;
-        if (kg == 0 && tok < B) ss_part[ksplit * B + tok] = s2;
+        if (kg == 0 && tok < B && ss_part) ss_part[ksplit * B + tok] = s2;
     }
 }
 
-// P[b][o] = sum_ks p_part[ks][b][o] for o < np (standalone projection).
+// Split-K partial q of projection output o of token b.  The partials of
+// the output tiles are stored tile-major: p_part[o / 32][q][b][o % 32].
+__device__ __forceinline__ float p_part_at(const float* __restrict__ p_part, int ks, int64_t B, int q, int64_t b,
+                                           int o) {
+    return p_part[(((int64_t)(o >> 5) * ks + q) * B + b) * kNPad + (o & 31)];
+}
+
+// P[b][o] = sum_ks p_part[.][ks][b][.] for o < np (standalone projection).
 __global__ __launch_bounds__(256) void proj_reduce_kernel(const float* __restrict__ p_part, int ks, int64_t B,
                                                           int np, float* __restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -328,7 +342,7 @@ __global__ __launch_bounds__(256) void proj_reduce_kernel(const float* __restric
     const int64_t b = i / np;
     const int o = (int)(i % np);
     float s = 0.f;
-    for (int q = 0; q < ks; ++q) s += p_part[((int64_t)q * B + b) * kNPad + o];
+    for (int q = 0; q < ks; ++q) s += p_part_at(p_part, ks, B, q, b, o);
     out[i] = s;
 }
 
@@ -357,13 +371,12 @@ __global__ __launch_bounds__(256) void dyn_coef_fwd_kernel(
     for (int c = 0; c < N; ++c) pr[c] = 0.f;
     if (tv) {
         for (int q = 0; q < ks; ++q) {
-            const float* pb = p_part + ((int64_t)q * B + tok) * kNPad;
             ss += ss_part[(int64_t)q * B + tok];
             if (r < N) {
-                pp += pb[r];
-                pq += pb[N + r];
+                pp += p_part_at(p_part, ks, B, q, tok, r);
+                pq += p_part_at(p_part, ks, B, q, tok, N + r);
 #pragma unroll
-                for (int c = 0; c < N; ++c) pr[c] += pb[2 * N + r * N + c];
+                for (int c = 0; c < N; ++c) pr[c] += p_part_at(p_part, ks, B, q, tok, 2 * N + r * N + c);
             }
         }
     }
@@ -399,8 +412,9 @@ __global__ __launch_bounds__(256) void dyn_coef_fwd_kernel(
 //   dt_res = SK^T(dM) * exp(t_res)
 //   dP_k = alpha_k dt_k / r_h;  d r_h = -sum_k alpha_k dt_k P_k / r_h^2
 //   s = d r_h / (K r_h)  (coefficient of x_flat in dx)
-// dp_out[b][32] (zero padded), s_out[b]; per-workgroup partial sums of
-// db (np values) and dalpha (3) in part[blk][np + 3].
+// dp_out[b][dp_stride(np)] (np rounded up to 32, zero padded), s_out[b];
+// per-workgroup partial sums of db (np values) and dalpha (3) in
+// part[blk][np + 3].
 // ---------------------------------------------------------------------------
 template <int N>
 __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
@@ -448,13 +462,14 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
     const float l_pre = dt_pre * pp, l_post = dt_post * pq;
     const float tot = group_sum<G>(ap * l_pre + aq * l_post + ar * lp);
     if (active) {
-        float* dp = dp_out + tok * kNPad;
+        constexpr int NPT = dp_stride(NP);
+        float* dp = dp_out + tok * NPT;
         dp[r] = ap * dt_pre * inv;
         dp[N + r] = aq * dt_post * inv;
 #pragma unroll
         for (int c = 0; c < N; ++c) dp[2 * N + r * N + c] = ar * dt_res[c] * inv;
         if (r == 0) {
-            for (int o = NP; o < kNPad; ++o) dp[o] = 0.f;
+            for (int o = NP; o < NPT; ++o) dp[o] = 0.f;
             s_out[tok] = -tot * inv * inv * inv / (float)K;
         }
     }
@@ -660,6 +675,9 @@ __global__ __launch_bounds__(1024) void small_column_sum_kernel(const float* __r
 //   dPhi_part[tile][o][k] = sum_{b in tile} dP[b][o] x[b][k]
 // In the layer backward dx_in is the stream part already written by the row
 // kernel (bindings.cpp:834-848 adds the same two terms to grad_x_flat).
+// One launch covers the 32-row output tile o0 .. o0 + np - 1 of Phi (np <=
+// 32, dP pointing at its column o0); projections with more rows run one
+// launch per tile, the later ones accumulating without the s term.
 //
 // fp32 operands are split into bf16 hi + lo (v = hi + lo to 2^-16 relative);
 // products keep hi.hi + hi.lo + lo.hi, so both products carry ~2^-16
@@ -721,7 +739,8 @@ template <typename TX, bool ACC, bool HAS_S>
 __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     const TX* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
     const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
-    int n_pre, int np, TX* __restrict__ dx, float* __restrict__ dphi_part, int64_t B, int64_t K, int64_t tile) {
+    int n_pre, int o0, int np, TX* __restrict__ dx, float* __restrict__ dphi_part, int64_t B, int64_t K,
+    int64_t tile) {
     constexpr int TB = 32;                      // tokens per stage
     constexpr int CB = 128;                     // columns per workgroup
     constexpr int EPV = 16 / sizeof(TX);        // elements per 16-byte vector
@@ -758,7 +777,7 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int o = 8 * lg + e;
-            v[e] = (wave_on && o < np) ? phi_row(phi_pre, phi_post, phi_res, n_pre, o, K)[k] : 0.f;
+            v[e] = (wave_on && o < np) ? phi_row(phi_pre, phi_post, phi_res, n_pre, o0 + o, K)[k] : 0.f;
         }
         split_pack8(v, phh[ct], phl[ct]);
     }
@@ -957,7 +976,7 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
 // ---------------------------------------------------------------------------
 hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
                             bf16_t* phib, hipStream_t s) {
-    const int64_t total = 2 * (K / 32) * 64;
+    const int64_t total = (int64_t)proj_tiles(np) * 2 * (K / 32) * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     hipLaunchKernelGGL(phi_split_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pre, post, res, n, np, K,
@@ -974,28 +993,35 @@ int proj_ksplit(int64_t B, int64_t K) {
     return (int)ks;
 }
 
-hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_t* phib, float* p_part, float* ss_part, int64_t B,
-                            int64_t K, int ks, hipStream_t s) {
+hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_t* phib, int np, float* p_part, float* ss_part,
+                            int64_t B, int64_t K, int ks, hipStream_t s) {
     if (B == 0) return hipSuccess;
     // 32-bit buffer offsets: a 128-row block of fp32 x and the Phi planes
-    if (K % 32 != 0 || K > (int64_t(1) << 22)) return hipErrorInvalidValue;
+    if (K % 32 != 0 || K > (int64_t(1) << 22) || np < 1) return hipErrorInvalidValue;
     int64_t kchunk = (K + ks - 1) / ks;
     kchunk = ((kchunk + kProjKS - 1) / kProjKS) * kProjKS;
-    const uint4* phif = reinterpret_cast<const uint4*>(phib);
-    const int tok = timing_begin("proj", s);
-    if (x_dtype == kBF16) {
-        constexpr int MT = proj_mt<bf16_t>();
-        const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
-        hipLaunchKernelGGL((proj_mfma_kernel<bf16_t, MT>), grid, dim3(256), 0, s, (const bf16_t*)x, phif, p_part,
-                           ss_part, B, K, kchunk);
-    } else {
-        constexpr int MT = proj_mt<float>();
-        const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
-        hipLaunchKernelGGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, p_part,
-                           ss_part, B, K, kchunk);
+    // one launch per 32-row output tile; the first also stores sum x^2
+    for (int t = 0; t < proj_tiles(np); ++t) {
+        const uint4* phif = reinterpret_cast<const uint4*>(phib) + (int64_t)t * 6 * (K / 32) * 64;
+        float* pp = p_part + (int64_t)t * ks * B * kNPad;
+        float* ssp = t == 0 ? ss_part : nullptr;
+        const int tok = timing_begin("proj", s);
+        if (x_dtype == kBF16) {
+            constexpr int MT = proj_mt<bf16_t>();
+            const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
+            hipLaunchKernelGGL((proj_mfma_kernel<bf16_t, MT>), grid, dim3(256), 0, s, (const bf16_t*)x, phif, pp, ssp,
+                               B, K, kchunk);
+        } else {
+            constexpr int MT = proj_mt<float>();
+            const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
+            hipLaunchKernelGGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, pp, ssp,
+                               B, K, kchunk);
+        }
+        timing_end(tok, s);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
-    timing_end(tok, s);
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s) {
@@ -1010,6 +1036,7 @@ hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, fl
     switch (n) {                                                 \
         case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }    \
         case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }    \
+        case 8: { constexpr int N_ = 8; __VA_ARGS__; break; }    \
         default: return hipErrorInvalidValue;                    \
     }
 
@@ -1079,27 +1106,35 @@ int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
 }
 
 hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
-                           const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
-                           void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
+                           const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int o0,
+                           int np, void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
                            hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (np < 1 || np > 32 || K % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
+    if (np < 1 || np > kProjTile || o0 < 0 || K % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
     // token tile: a multiple of the 32-token block
     int64_t tile = (B + tiles - 1) / tiles;
     tile = ((tile + 31) / 32) * 32;
     const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
-    const int tok = timing_begin("proj_bwd", s);
 #define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \
     hipLaunchKernelGGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP, dp_stride,  \
-                       s_tok, phi_pre, phi_post, phi_res, n_pre, np, (TX_*)dx, dphi_part, B, K, tile)
-    // the layer backward accumulates with the r_h term; the standalone operator does neither
-    const bool layer = accumulate && s_tok != nullptr;
-    if (!layer && (accumulate || s_tok != nullptr)) return hipErrorInvalidValue;
+                       s_tok, phi_pre, phi_post, phi_res, n_pre, o0, np, (TX_*)dx, dphi_part, B, K, tile)
+    // The layer backward accumulates (with the r_h term on the first output
+    // tile only); the standalone operator starts from zero on its first tile.
+    // An s term without accumulation, or a bf16 dx from zero, is not built.
+    const bool has_s = s_tok != nullptr;
+    if (has_s && !accumulate) return hipErrorInvalidValue;
+    if (x_dtype == kBF16 && !accumulate) return hipErrorInvalidValue;
+    const int tok = timing_begin("proj_bwd", s);
     if (x_dtype == kBF16) {
-        if (!layer) return hipErrorInvalidValue;
-        MHC_PROJ_BWD(bf16_t, true, true);
-    } else if (layer) {
+        if (has_s) {
+            MHC_PROJ_BWD(bf16_t, true, true);
+        } else {
+            MHC_PROJ_BWD(bf16_t, true, false);
+        }
+    } else if (has_s) {
         MHC_PROJ_BWD(float, true, true);
+    } else if (accumulate) {
+        MHC_PROJ_BWD(float, true, false);
     } else {
         MHC_PROJ_BWD(float, false, false);
     }

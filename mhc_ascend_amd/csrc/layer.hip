@@ -625,24 +625,19 @@ static const void* pick_fwd(int x_dtype, int out_dtype, int n, int vpt) {
     return fn;
 }
 
-// MODE 1 (dynamic H) exists for the n whose 2n + n^2 projection outputs fit
-// one 32-wide projection tile (n <= 4).
 static const void* pick_bwd(int x_dtype, int n, int vpt, int mode, bool pf) {
     const void* fn = nullptr;
 #define MHC_BWD_FN(TX_, N_)                                                                                     \
     MHC_PICK_VPT(vpt, fn = mode == 0 ? (pf ? bwd_fn<TX_, N_, V_, 0, true>() : bwd_fn<TX_, N_, V_, 0, false>())   \
                                      : (pf ? bwd_fn<TX_, N_, V_, 1, true>() : bwd_fn<TX_, N_, V_, 1, false>()))
-#define MHC_BWD_FN0(TX_, N_) \
-    MHC_PICK_VPT(vpt, fn = mode == 0 ? (pf ? bwd_fn<TX_, N_, V_, 0, true>() : bwd_fn<TX_, N_, V_, 0, false>()) : nullptr)
     const bool bf = x_dtype == kBF16;
     switch (n) {
         case 2: { if (bf) { MHC_BWD_FN(bf16_t, 2); } else { MHC_BWD_FN(float, 2); } break; }
         case 4: { if (bf) { MHC_BWD_FN(bf16_t, 4); } else { MHC_BWD_FN(float, 4); } break; }
-        case 8: { if (bf) { MHC_BWD_FN0(bf16_t, 8); } else { MHC_BWD_FN0(float, 8); } break; }
+        case 8: { if (bf) { MHC_BWD_FN(bf16_t, 8); } else { MHC_BWD_FN(float, 8); } break; }
         default: break;
     }
 #undef MHC_BWD_FN
-#undef MHC_BWD_FN0
     return fn;
 }
 

@@ -93,11 +93,22 @@ hipError_t launch_distribute_bwd(int dt, int n, const float* g, const void* x, c
 
 // ---- dynamic.hip -----------------------------------------------------------
 typedef uint16_t bf16_raw_t;
+// Projection outputs come in tiles of 32 rows (two 16-wide MFMA tiles).
+constexpr int kProjTile = 32;
+constexpr int proj_tiles(int np) { return (np + kProjTile - 1) / kProjTile; }
+// Row stride of the per-token projection cotangent dP [B][dp_stride(np)].
+constexpr int dp_stride(int np) { return proj_tiles(np) * kProjTile; }
+// Largest number of projection rows (output tiles run one after another).
+constexpr int kMaxProjRows = 8192;
+// Phi [np rows, K] -> proj_tiles(np) output tiles of three bf16 planes
+// (3 * 32 * K bf16 each) in the projection kernel's operand order.
 hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
                             bf16_raw_t* phib, hipStream_t s);
 int proj_ksplit(int64_t B, int64_t K);
-hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_raw_t* phib, float* p_part, float* ss_part,
-                            int64_t B, int64_t K, int ks, hipStream_t s);
+// P partials of all proj_tiles(np) output tiles, tile-major:
+// p_part[tile][ks][B][32], plus ss_part[ks][B] = partial sums of x^2.
+hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_raw_t* phib, int np, float* p_part,
+                            float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s);
 hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s);
 hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part, int ks, int64_t B, int64_t K,
                                const float* a_pre, const float* a_post, const float* a_res, const float* b_pre,
@@ -110,15 +121,17 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                                hipStream_t s);
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s);
-// Projection backward (bf16 MFMA, split operands) over the flattened [B, K] rows:
-//   dx[b][k] = (accumulate ? dx[b][k] : 0) + (s ? s[b] x[b][k] : 0) + sum_o dP[b][o] Phi[o][k]
+// Projection backward (bf16 MFMA, split operands) over the flattened [B, K]
+// rows, for the output rows o0 .. o0 + np - 1 (np <= 32; dP points at
+// column o0 of its rows):
+//   dx[b][k] = (accumulate ? dx[b][k] : 0) + (s ? s[b] x[b][k] : 0) + sum_o dP[b][o] Phi[o0 + o][k]
 //   dphi_part[tile][o][k] = sum_{b in tile} dP[b][o] x[b][k]
 // Phi row o is phi_row(pre, post, res, n_pre, o): rows < n_pre from `pre`,
-// the next n_pre from `post`, the rest from `res`.  np <= 32, K % 32 == 0.
+// the next n_pre from `post`, the rest from `res`.  K % 32 == 0.
 int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K);
 hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
-                           const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
-                           void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
+                           const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int o0,
+                           int np, void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
                            hipStream_t s);
 hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, hipStream_t s);
 

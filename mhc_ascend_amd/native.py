@@ -344,7 +344,7 @@ def fused_rmsnorm_matmul_fwd(inp: torch.Tensor, weight: torch.Tensor) -> torch.T
     B, K = x.shape
     out = torch.empty((B, phi.size(0)), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
-        wsb = _lib.load().mhc_fused_rmsnorm_matmul_fwd_workspace_size(B, K)
+        wsb = _lib.load().mhc_fused_rmsnorm_matmul_fwd_workspace_size(B, K, phi.size(0))
         ws = _ws(x.device, wsb)
         call("mhc_fused_rmsnorm_matmul_fwd", ptr(x), dtype_code(x.dtype), ptr(phi), ptr(out), ptr(ws), int(wsb), B,
              K, phi.size(0), stream_of(x))

@@ -70,18 +70,23 @@ def test_layer_rejects_unsupported_and_invalid_on_host():
 
 
 def test_expansion_rate_support_on_host():
-    """Layers compile n in {2, 4, 8}; dynamic H n in {2, 4} (2n + n^2 <= 32
-    projection outputs); the fused wrapper n = 4 (other n go through the
-    layer).  All rejected before any device work."""
+    """Layers compile n in {2, 4, 8}, dynamic H included (2n + n^2 = 80
+    projection rows at n = 8 run as three 32-row output tiles); the fused
+    wrapper n = 4 (other n go through the layer).  All rejected before any
+    device work."""
     lib = _lib.load()
     # static layer: n = 2, 8 pass the host checks; with a null x they fail on that
     for n in (2, 8):
         assert lib.mhc_layer_static_fwd(None, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, n, 64, 20, 1e-8, 1e-5, None) == -1
         assert b"null x" in lib.mhc_last_error()
     assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 6, 64, 20, 1e-8, 1e-5, None) == -2
-    rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1 << 30, 8, 8, 64, 20, 1e-8,
+    rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1 << 30, 8, 6, 64, 20, 1e-8,
                                    1e-5, None)
-    assert rc == -2 and b"dynamic H is compiled for n in" in lib.mhc_last_error()
+    assert rc == -2 and b"n=6 is not compiled" in lib.mhc_last_error()
+    # dynamic n = 8 passes the shape checks; a null out then fails before any launch
+    rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, 1, 1, 1 << 30, 8, 8, 64, 20, 1e-8,
+                                   1e-5, None)
+    assert rc == -1 and b"null x/out" in lib.mhc_last_error()
     rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 2, 256, 20, 1e-8, 1e-5, None)
     assert rc == -2 and b"fused wrapper is compiled for n = 4" in lib.mhc_last_error()
 

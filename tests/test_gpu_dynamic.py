@@ -26,7 +26,7 @@ def _gen(seed):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,K,out_dim", [(1, 32, 1), (3, 96, 8), (70, 1024, 24), (129, 4160, 24), (300, 4096, 32),
-                                         (65, 16384, 24)])
+                                         (65, 16384, 24), (9, 320, 33), (70, 1024, 80), (40, 2048, 100)])
 def test_projection(device, dtype, B, K, out_dim):
     g = _gen(B + K + out_dim)
     x = torch.randn(B, K, generator=g).to(dtype)
@@ -97,11 +97,19 @@ def test_dynamic_layer_n2_matches_oracle(device, x_dtype, B, C):
     _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n=2 B={B} C={C} {x_dtype}")
 
 
-def test_dynamic_layer_n8_is_unsupported(device):
-    """2n + n^2 = 80 projection outputs exceed the one-tile projection."""
-    layer = mhc.MHCLayer(64, 8, use_dynamic_h=True).to(device)
-    with pytest.raises(RuntimeError, match="dynamic H is compiled for n in"):
-        layer(torch.randn(3, 8, 64, device=device))
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,C", [(3, 64), (37, 320), (128, 1280)])
+def test_dynamic_layer_n8_matches_oracle(device, x_dtype, B, C):
+    """Expansion rate 8: 2n + n^2 = 80 projection rows in three 32-row
+    output tiles; (128, 1280) is a paper configuration (benchmark.py:306)."""
+    d = R.dynamic_layer_inputs(B, 8, C, seed=8 * B + C, x_dtype=x_dtype, alpha=0.3, phi_std=0.05, b_std=0.5)
+    _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n=8 B={B} C={C} {x_dtype}")
+
+
+def test_dynamic_layer_unsupported_n_raises(device):
+    layer = mhc.MHCLayer(64, 3, use_dynamic_h=True).to(device)
+    with pytest.raises(RuntimeError, match="n=3 is not compiled"):
+        layer(torch.randn(3, 3, 64, device=device))
 
 
 @pytest.mark.parametrize("alpha,phi_std", [(0.5, 0.05), (2.0, 0.02)])
