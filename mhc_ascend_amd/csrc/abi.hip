@@ -39,7 +39,7 @@ static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
 
 // The fused layer kernels are compiled for n in {2, 4, 8}; dynamic H needs
 // 2n + n^2 <= 32 projection outputs (n <= 4); the fused wrapper is n = 4.
-static bool supported_layer_n(int n) { return n == 2 || n == 4 || n == 8; }
+static bool supported_layer_n(int n) { return n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
 static bool supported_dynamic_n(int n) { return n == 2 || n == 4 || n == 8; }
 // the standalone aggregate / distribute operators
 static bool supported_ops_n(int n) { return n == 1 || n == 2 || n == 4 || n == 8; }
@@ -208,11 +208,10 @@ static int check_layer_shape(const char* fn, int64_t batch, int32_t n, int32_t h
     if (!valid_dtype(x_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": x_dtype must be F32 or BF16");
     if (!supported_layer_n(n))
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) + " is not compiled in this build");
-    const int wc = 4;  // channels per lane chunk of the fused layer kernels (both dtypes)
-    if (hidden % wc != 0)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of " + std::to_string(wc));
-    const RowTiling t = choose_row_tiling(hidden, wc, 2 * n);
-    if (t.vpt <= 0) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
+    // register rows (n <= 8, 4-channel chunks that fit) or the channel-loop kernels
+    if ((layer_fwd_is_wide(n, hidden) || layer_bwd_is_wide(n, hidden)) && !wide_supported(n, hidden))
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden=" + std::to_string(hidden) +
+                                             " is too large for the row kernels at n=" + std::to_string(n));
     return MHC_SUCCESS;
 }
 
@@ -800,6 +799,8 @@ static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidd
     int st = check_layer_shape(fn, tokens, n, hidden, dtype, num_iters);
     if (st) return st;
     if (n != 4) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper is compiled for n = 4");
+    if (hidden % 4 != 0)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper needs hidden % 4 == 0");
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (mode != MHC_WRAPPER_DECAY && mode != MHC_WRAPPER_ZERO)
         return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");

@@ -24,7 +24,7 @@ BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_NAME = "libmhc_hip.so"
 LIB_PATH = os.path.join(PKG, LIB_NAME)
 
-SOURCES = ["abi.hip", "dynamic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wrapper.hip"]
+SOURCES = ["abi.hip", "dynamic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wide.hip", "wrapper.hip"]
 
 ARCH = os.environ.get("MHC_OFFLOAD_ARCH", "gfx950")
 

@@ -396,6 +396,19 @@ __global__ __launch_bounds__(256) void column_partial_kernel(const float* __rest
     }
 }
 
+// Same sums with one column per lane, for column counts that are not a
+// multiple of 4 (rows are then not 16-byte aligned).
+__global__ __launch_bounds__(256) void column_partial1_kernel(const float* __restrict__ part, int rows,
+                                                              int64_t cols, float* __restrict__ stage) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    const int r0 = (int)((int64_t)rows * blockIdx.y / gridDim.y);
+    const int r1 = (int)((int64_t)rows * (blockIdx.y + 1) / gridDim.y);
+    float s = 0.f;
+    for (int r = r0; r < r1; ++r) s += part[(int64_t)r * cols + c];
+    stage[(int64_t)blockIdx.y * cols + c] = s;
+}
+
 // The first blocks finish the column sums of stage[rsplit][cols]
 // (per-workgroup partials, or their first-pass sums when there are many)
 // and store them in the weight's dtype: 256 lanes per block as `phases` row
@@ -558,22 +571,33 @@ hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s) {
 
 int saved_w_offset(int n) { return ((2 * n + n * n + 63) / 64) * 64; }
 
+#define MHC_COEF_N(n, ...)                                       \
+    switch (n) {                                                 \
+        case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }    \
+        case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }    \
+        case 8: { constexpr int N_ = 8; __VA_ARGS__; break; }    \
+        case 16: { constexpr int N_ = 16; __VA_ARGS__; break; }  \
+        case 32: { constexpr int N_ = 32; __VA_ARGS__; break; }  \
+        default: return hipErrorInvalidValue;                    \
+    }
+
 hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res,
                               const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
                               hipStream_t s) {
     const int off = saved_w_offset(n);
     const unsigned blocks = 1 + (unsigned)((C + 2047) / 2048);
     if (w_dtype == kBF16) {
-        MHC_DISPATCH_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, bf16_t>), dim3(blocks), dim3(256), 0, s,
-                                             h_pre, h_post, h_res, (const bf16_t*)weight, (int)C, saved, off, iters,
-                                             sk_eps));
+        MHC_COEF_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, bf16_t>), dim3(blocks), dim3(256), 0, s,
+                                         h_pre, h_post, h_res, (const bf16_t*)weight, (int)C, saved, off, iters,
+                                         sk_eps));
     } else {
-        MHC_DISPATCH_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, float>), dim3(blocks), dim3(256), 0, s,
-                                             h_pre, h_post, h_res, (const float*)weight, (int)C, saved, off, iters,
-                                             sk_eps));
+        MHC_COEF_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, float>), dim3(blocks), dim3(256), 0, s,
+                                         h_pre, h_post, h_res, (const float*)weight, (int)C, saved, off, iters,
+                                         sk_eps));
     }
     return hipGetLastError();
 }
+#undef MHC_COEF_N
 
 // ---------------------------------------------------------------------------
 // Persistent row kernels: pick the instantiation, size the grid from its
@@ -657,12 +681,23 @@ static int persistent_grid(const void* fn, int threads, int64_t B) {
 // Backward workgroups of <= 256 lanes run the two-buffer prefetch variant.
 static bool use_prefetch(const RowTiling& t) { return t.threads <= 256; }
 
+// The register-row kernels take n <= 8 and a multiple of the 4-channel
+// chunk that fits their row state; everything else runs the channel-loop
+// kernels of wide.hip.
+static RowTiling fwd_tiling(int64_t C, int n) {
+    if (n > 8) return RowTiling{0, 0};
+    return choose_row_tiling(C, kLayerWC, n, 512);
+}
+
+bool layer_fwd_is_wide(int n, int64_t C) { return fwd_tiling(C, n).vpt <= 0; }
+
 hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
                             int64_t coef_stride, void* out, int out_dtype, float* rms_out, int64_t B, int64_t C,
                             float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = choose_row_tiling(C, kLayerWC, n, 512);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
+    const RowTiling t = fwd_tiling(C, n);
+    if (t.vpt <= 0)
+        return launch_wide_fwd(x_dtype, out_dtype, n, x, w, coef, coef_stride, out, rms_out, B, C, eps, s);
     const void* fn = pick_fwd(x_dtype, out_dtype, n, t.vpt);
     if (!fn) return hipErrorInvalidValue;
     if (B > 0x7fffffff) return hipErrorInvalidValue;  // grid x limit
@@ -678,12 +713,15 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
 
 // The backward hands one of its 2 + n^2 + 3n row sums to each thread.
 static RowTiling bwd_tiling(int64_t C, int n) {
+    if (n > 8) return RowTiling{0, 0};
     return with_min_threads(choose_row_tiling(C, kLayerWC, 2 * n), 2 + n * n + 3 * n);
 }
 
+bool layer_bwd_is_wide(int n, int64_t C) { return bwd_tiling(C, n).vpt <= 0; }
+
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
     const RowTiling t = bwd_tiling(C, n);
-    if (t.vpt <= 0) return 1;
+    if (t.vpt <= 0) return wide_bwd_grid(x_dtype, n, B, C);
     return persistent_grid(pick_bwd(x_dtype, n, t.vpt, 0, use_prefetch(t)), t.threads, B);
 }
 
@@ -691,7 +729,9 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, hipStream_t s) {
     const RowTiling t = bwd_tiling(C, n);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
+    if (t.vpt <= 0)
+        return launch_wide_bwd(x_dtype, n, mode, g, x, w, coef, coef_stride, dx, dw_part, scal_out, grid, B, C, eps,
+                               s);
     const void* fn = pick_bwd(x_dtype, n, t.vpt, mode, use_prefetch(t));
     if (!fn) return hipErrorInvalidValue;
     int Ci = (int)C;
@@ -706,8 +746,13 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
 hipError_t launch_column_partial(const float* part, int rows, int64_t cols, float* stage, int rsplit,
                                  hipStream_t s) {
     if (cols == 0) return hipSuccess;
-    hipLaunchKernelGGL(column_partial_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
-                       rows, cols, stage);
+    if (cols % 4 != 0) {
+        hipLaunchKernelGGL(column_partial1_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
+                           rows, cols, stage);
+    } else {
+        hipLaunchKernelGGL(column_partial_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
+                           rows, cols, stage);
+    }
     return hipGetLastError();
 }
 
@@ -747,6 +792,14 @@ hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int row
                                   void* dw, const float* scal_part, int scal_rows, const float* h_pre,
                                   const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
                                   float* d_h_res, int iters, float sk_eps, hipStream_t s) {
+    if (n > 8) {
+        // the static scalar gradients of wide n have their own kernel
+        hipError_t e = launch_column_finalize(0, w_dtype, part, rows, cols, stage, dw, nullptr, 0, nullptr, nullptr,
+                                              nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+        if (e != hipSuccess) return e;
+        return launch_wide_static_finalize(n, scal_part, scal_rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res,
+                                           iters, sk_eps, s);
+    }
     if (rows <= kDirectRows)
         return launch_layer_finalize(n, w_dtype, part, rows, cols, dw, scal_part, scal_rows, h_pre, h_post, h_res,
                                      d_h_pre, d_h_post, d_h_res, iters, sk_eps, s);

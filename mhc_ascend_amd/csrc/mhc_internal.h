@@ -54,6 +54,10 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, hipStream_t s);
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
+// Whether the layer forward / backward of (n, C) runs the channel-loop
+// kernels of wide.hip rather than the register rows.
+bool layer_fwd_is_wide(int n, int64_t C);
+bool layer_bwd_is_wide(int n, int64_t C);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s);
 // Two-stage deterministic column sum of part[rows][cols]: stage[rsplit][cols].
 hipError_t launch_column_partial(const float* part, int rows, int64_t cols, float* stage, int rsplit,
@@ -72,6 +76,26 @@ hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int row
                                   void* dw, const float* scal_part, int scal_rows, const float* h_pre,
                                   const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
                                   float* d_h_res, int iters, float sk_eps, hipStream_t s);
+
+// ---- wide.hip --------------------------------------------------------------
+// Channel-loop layer kernels (any C up to kWideMaxC; n in {2, 4, 8, 16, 32}):
+// used for n > 8 and where the register rows do not fit C.  The backward's
+// dw partial of a workgroup sits in LDS (C floats).
+constexpr int kWideMaxC = 12288;
+bool wide_supported(int n, int64_t C);
+hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
+                           int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
+                           hipStream_t s);
+int wide_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
+// Same outputs as launch_layer_bwd (mode 0 / 1); for n >= 16 the dM entries
+// come from a second kernel on the same stream.
+hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
+                           const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out, int grid,
+                           int64_t B, int64_t C, float eps, hipStream_t s);
+// Static H gradients for n >= 16 from scal_part[rows][n^2 + 2n].
+hipError_t launch_wide_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
+                                       const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
+                                       float* d_h_res, int iters, float sk_eps, hipStream_t s);
 
 // ---- ops.hip ---------------------------------------------------------------
 hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, float* rms, int64_t B, int64_t C,

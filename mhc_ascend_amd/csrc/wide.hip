@@ -1,0 +1,467 @@
+// Channel-loop ("wide") row kernels of the mHC layer: one lane per channel,
+// and each token row is walked twice - once for its row sums, once (reading
+// it again, from cache) for the outputs - instead of being held in
+// registers.  They serve what the register-resident kernels of layer.hip
+// cannot hold: expansion rates above 8 (the paper's n = 32 configurations,
+// benchmark.py:307-309) and, at any n, hidden sizes that are not a multiple
+// of the 4-channel chunk (the reference pads those rows, stream_ops.cpp:66-68)
+// or too wide for the register rows.  Loads and stores are element-wise, so
+// no alignment is assumed.
+//
+// Math (layer.py:142-170, ops_pytorch_backward.py:9-150), per token b with
+// coefficients cf = (h_pre[n], h_post[n], M[n][n]):
+//   xa = sum_j h_pre_j x_j,  r = sqrt(mean_c xa^2 + eps),  y = xa / r * w
+//   out_i = h_post_i y + sum_j M_ij x_j
+// Backward for cotangent g: gy = sum_i h_post_i g_i, k2 = sum(w gy xa)/(C r^3),
+//   gxa = w gy / r - xa k2,  dx_j = h_pre_j gxa + sum_i M_ij g_i,
+//   dw += gy xa / r,  dh_post_i = sum(g_i xa w) / r,
+//   dh_pre_j = sum(w gy x_j) / r - k2 sum(xa x_j),  dM_ij = sum g_i x_j.
+// dM (n^2 row sums) is formed in the row pass for n <= 8 and by the Gram
+// kernel below for larger n.
+#include "mhc_device.h"
+#include "mhc_internal.h"
+
+namespace mhc {
+
+constexpr int kWideThreads = 256;
+
+template <typename T>
+__device__ __forceinline__ float ld_elem_nt(const T* p) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_nontemporal_load(p);
+    } else {
+        return bf16_to_f32(__builtin_nontemporal_load(p));
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void st_elem_nt(T* p, float v) {
+    if constexpr (sizeof(T) == 4) {
+        __builtin_nontemporal_store(v, p);
+    } else {
+        __builtin_nontemporal_store(f32_to_bf16(v), p);
+    }
+}
+
+// Block totals of NV per-thread values into tot[NV] (LDS; every thread may
+// read them after the call).  red holds NV * (blockDim.x / 64) floats.
+template <int NV>
+__device__ __forceinline__ void wide_block_total(float (&v)[NV], float* red, float* tot) {
+    wave_sum_last<NV>(v);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int nwaves = blockDim.x / kWave;
+    if (lane == kWave - 1) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) red[wave * NV + k] = v[k];
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < NV; k += blockDim.x) {
+        float s = 0.f;
+        for (int q = 0; q < nwaves; ++q) s += red[q * NV + k];
+        tot[k] = s;
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Forward: one token per workgroup (grid = tokens); out in TO (fp32, or bf16
+// for the forward-only entry); rms_out[b] = r when not null.
+// ---------------------------------------------------------------------------
+template <typename TX, typename TO, int N>
+__global__ __launch_bounds__(kWideThreads) void wide_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
+                                                                const float* __restrict__ coef, int64_t coef_stride,
+                                                                TO* __restrict__ out, float* __restrict__ rms_out,
+                                                                int64_t B, int C, float eps) {
+    __shared__ float red[kWideThreads / kWave];
+    __shared__ float tot[1];
+    const int64_t b = blockIdx.x;
+    if (b >= B) return;
+    const float* cf = coef + b * coef_stride;
+    const TX* xb = x + b * (int64_t)N * C;
+    float ss[1] = {0.f};
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float xa = 0.f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) xa += cf[j] * VecIO<TX>::scalar(xb + (int64_t)j * C + c);
+        ss[0] += xa * xa;
+    }
+    wide_block_total<1>(ss, red, tot);
+    const float r = sqrtf(tot[0] / (float)C + eps);
+    const float inv = 1.f / r;
+    TO* ob = out + b * (int64_t)N * C;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float xv[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) xv[j] = ld_elem_nt(xb + (int64_t)j * C + c);
+        float xa = 0.f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) xa += cf[j] * xv[j];
+        const float y = xa * inv * w[c];
+        for (int i = 0; i < N; ++i) {
+            float s = cf[N + i] * y;
+#pragma unroll
+            for (int j = 0; j < N; ++j) s += cf[2 * N + i * N + j] * xv[j];
+            st_elem_nt(ob + (int64_t)i * C + c, s);
+        }
+    }
+    if (threadIdx.x == 0 && rms_out) rms_out[b] = r;
+}
+
+// ---------------------------------------------------------------------------
+// Backward.  Persistent workgroups stride over tokens; the workgroup's dw
+// partial lives in LDS (dynamic shared memory, C floats, each entry owned by
+// the lane that owns the channel) and goes to dw_part[blockIdx.x][C] at the
+// end.  Per-token scalars as in layer.hip (layout [dM | dh_post | dh_pre |
+// 1/r | k2]): MODE 0 sums them per workgroup into scal_out[blockIdx.x][NS],
+// MODE 1 writes them per token into scal_out[b][NS + 2].  With DM false the
+// dM entries are left to stream_gram_kernel.
+// ---------------------------------------------------------------------------
+template <typename TX, int N, int MODE, bool DM>
+__global__ __launch_bounds__(kWideThreads) void wide_bwd_kernel(const float* __restrict__ g, const TX* __restrict__ x,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ coef, int64_t coef_stride,
+                                                                TX* __restrict__ dx, float* __restrict__ dw_part,
+                                                                float* __restrict__ scal_out, int64_t B, int C,
+                                                                float eps) {
+    extern __shared__ float dws[];
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NR = 2 + 3 * N + (DM ? N * N : 0);  // ss, dot, t_i, u_j, v_j (, dM)
+    // scalar entries this kernel writes: E0 .. NS + 1, one per lane
+    constexpr int E0 = DM ? 0 : N * N;
+    constexpr int NE = NS + 2 - E0;
+    static_assert(NE <= kWideThreads, "one scalar entry per lane");
+    __shared__ float red[(kWideThreads / kWave) * NR];
+    __shared__ float tot[NR];
+    const int tid = threadIdx.x;
+    for (int c = tid; c < C; c += blockDim.x) dws[c] = 0.f;
+    float sacc = 0.f;
+    const int64_t NCs = (int64_t)N * C;
+    for (int64_t b = blockIdx.x; b < B; b += gridDim.x) {
+        const float* cf = coef + b * coef_stride;
+        const TX* xb = x + b * NCs;
+        const float* gb = g + b * NCs;
+        float rv[NR];
+#pragma unroll
+        for (int k = 0; k < NR; ++k) rv[k] = 0.f;
+        for (int c = tid; c < C; c += blockDim.x) {
+            float xv[N], gv[N];
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                xv[j] = VecIO<TX>::scalar(xb + (int64_t)j * C + c);
+                gv[j] = gb[(int64_t)j * C + c];
+            }
+            float xa = 0.f, gy = 0.f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                xa += cf[j] * xv[j];
+                gy += cf[N + j] * gv[j];
+            }
+            const float wc = w[c];
+            const float wgy = wc * gy, wxa = wc * xa;
+            rv[0] += xa * xa;
+            rv[1] += wgy * xa;
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                rv[2 + i] += gv[i] * wxa;
+                rv[2 + N + i] += wgy * xv[i];
+                rv[2 + 2 * N + i] += xa * xv[i];
+            }
+            if constexpr (DM) {
+#pragma unroll
+                for (int i = 0; i < N; ++i) {
+#pragma unroll
+                    for (int j = 0; j < N; ++j) rv[2 + 3 * N + i * N + j] += gv[i] * xv[j];
+                }
+            }
+        }
+        wide_block_total<NR>(rv, red, tot);
+        const float r = sqrtf(tot[0] / (float)C + eps);
+        const float inv = 1.f / r;
+        const float k2 = tot[1] * inv * inv * inv / (float)C;
+        if (tid < NE) {
+            const int t = E0 + tid;
+            float v;
+            if (t < N * N) {
+                v = tot[2 + 3 * N + t];
+            } else if (t < N * N + N) {
+                v = tot[2 + t - N * N] * inv;  // dh_post_act
+            } else if (t < NS) {
+                const int j = t - N * N - N;
+                v = inv * tot[2 + N + j] - k2 * tot[2 + 2 * N + j];  // dh_pre_act
+            } else {
+                v = t == NS ? inv : k2;
+            }
+            if (MODE == 0) {
+                sacc += v;
+            } else {
+                scal_out[b * (NS + 2) + t] = v;
+            }
+        }
+        TX* db = dx + b * NCs;
+        for (int c = tid; c < C; c += blockDim.x) {
+            float xv[N], gv[N];
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                xv[j] = ld_elem_nt(xb + (int64_t)j * C + c);
+                gv[j] = ld_elem_nt(gb + (int64_t)j * C + c);
+            }
+            float xa = 0.f, gy = 0.f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                xa += cf[j] * xv[j];
+                gy += cf[N + j] * gv[j];
+            }
+            const float gxa = w[c] * gy * inv - xa * k2;
+            dws[c] += gy * xa * inv;
+            for (int j = 0; j < N; ++j) {
+                float s = cf[j] * gxa;
+#pragma unroll
+                for (int i = 0; i < N; ++i) s += cf[2 * N + i * N + j] * gv[i];
+                st_elem_nt(db + (int64_t)j * C + c, s);
+            }
+        }
+    }
+    float* dwp = dw_part + (int64_t)blockIdx.x * C;
+    for (int c = tid; c < C; c += blockDim.x) dwp[c] = dws[c];
+    if (MODE == 0 && tid < NE && E0 + tid < NS) scal_out[(int64_t)blockIdx.x * NS + E0 + tid] = sacc;
+}
+
+// ---------------------------------------------------------------------------
+// dM_ij = sum_c g_i x_j of one token (n >= 16): 64-channel tiles of g and x
+// staged in LDS, each of the (n/2)^2 lanes forming a 2 x 2 block of dM.
+// MODE 0 sums over the workgroup's tokens (same persistent grid as
+// wide_bwd_kernel) into scal_out[blockIdx.x][0 .. n^2); MODE 1 writes each
+// token's dM to scal_out[b][0 .. n^2).  Fixed summation order.
+// ---------------------------------------------------------------------------
+template <int N> constexpr int gram_threads() { return (N / 2) * (N / 2); }
+
+template <typename TX, int N, int MODE>
+__global__ __launch_bounds__(gram_threads<N>()) void stream_gram_kernel(const float* __restrict__ g,
+                                                                        const TX* __restrict__ x,
+                                                                        float* __restrict__ scal_out, int64_t B,
+                                                                        int C) {
+    constexpr int CT = 64;
+    constexpr int T = gram_threads<N>();
+    constexpr int NS = N * N + 2 * N;
+    __shared__ float gs[N][CT + 1];
+    __shared__ float xs[N][CT + 1];
+    const int tid = threadIdx.x;
+    const int i0 = 2 * (tid / (N / 2));
+    const int j0 = 2 * (tid % (N / 2));
+    float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    const int64_t NCs = (int64_t)N * C;
+    for (int64_t b = blockIdx.x; b < B; b += gridDim.x) {
+        if (MODE == 1) {
+            acc[0][0] = acc[0][1] = acc[1][0] = acc[1][1] = 0.f;
+        }
+        const float* gb = g + b * NCs;
+        const TX* xb = x + b * NCs;
+        for (int c0 = 0; c0 < C; c0 += CT) {
+            for (int e = tid; e < N * CT; e += T) {
+                const int row = e / CT;
+                const int cc = e - row * CT;
+                const int c = c0 + cc;
+                const bool ok = c < C;
+                gs[row][cc] = ok ? gb[(int64_t)row * C + c] : 0.f;
+                xs[row][cc] = ok ? VecIO<TX>::scalar(xb + (int64_t)row * C + c) : 0.f;
+            }
+            __syncthreads();
+#pragma unroll 8
+            for (int cc = 0; cc < CT; ++cc) {
+                const float g0 = gs[i0][cc], g1 = gs[i0 + 1][cc];
+                const float x0 = xs[j0][cc], x1 = xs[j0 + 1][cc];
+                acc[0][0] += g0 * x0;
+                acc[0][1] += g0 * x1;
+                acc[1][0] += g1 * x0;
+                acc[1][1] += g1 * x1;
+            }
+            __syncthreads();
+        }
+        if (MODE == 1) {
+            float* o = scal_out + b * (NS + 2);
+            o[i0 * N + j0] = acc[0][0];
+            o[i0 * N + j0 + 1] = acc[0][1];
+            o[(i0 + 1) * N + j0] = acc[1][0];
+            o[(i0 + 1) * N + j0 + 1] = acc[1][1];
+        }
+    }
+    if (MODE == 0) {
+        float* o = scal_out + (int64_t)blockIdx.x * NS;
+        o[i0 * N + j0] = acc[0][0];
+        o[i0 * N + j0 + 1] = acc[0][1];
+        o[(i0 + 1) * N + j0] = acc[1][0];
+        o[(i0 + 1) * N + j0 + 1] = acc[1][1];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Static parameter gradients for n >= 16 from the per-workgroup sums
+// scal_part[rows][n^2 + 2n]: column totals in LDS, then (as layer.hip's
+// finalize) dH_pre = dh_pre_act h_pre (1 - h_pre), dH_post = dh_post_act
+// h_post (1 - h_post / 2) and dH_res = SK^T(dM) * exp(H_res), the Sinkhorn
+// adjoint one row per lane of the first wave.
+// ---------------------------------------------------------------------------
+template <int N>
+__global__ __launch_bounds__(256) void wide_static_finalize_kernel(
+    const float* __restrict__ scal_part, int rows, const float* __restrict__ h_pre, const float* __restrict__ h_post,
+    const float* __restrict__ h_res, float* __restrict__ d_h_pre, float* __restrict__ d_h_post,
+    float* __restrict__ d_h_res, int iters, float eps) {
+    constexpr int NS = N * N + 2 * N;
+    __shared__ float tot[NS];
+    for (int k = threadIdx.x; k < NS; k += blockDim.x) {
+        float s = 0.f;
+        for (int r = 0; r < rows; ++r) s += scal_part[(int64_t)r * NS + k];
+        tot[k] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        const int r = threadIdx.x;
+        const bool act = r < N;
+        float e[N], gm[N];
+#pragma unroll
+        for (int c = 0; c < N; ++c) {
+            e[c] = act ? expf(h_res[r * N + c]) : 0.f;
+            gm[c] = act ? tot[r * N + c] : 0.f;
+        }
+        sk_backward<N>(gm, e, iters, eps, act);
+        if (act) {
+#pragma unroll
+            for (int c = 0; c < N; ++c) d_h_res[r * N + c] = gm[c] * e[c];
+        }
+    }
+    if (threadIdx.x < N) {
+        const int r = threadIdx.x;
+        const float tp = sigmoidf(h_pre[r]);
+        const float tq = 2.f * sigmoidf(h_post[r]);
+        d_h_pre[r] = tot[N * N + N + r] * tp * (1.f - tp);
+        d_h_post[r] = tot[N * N + r] * tq * (1.f - tq * 0.5f);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+#define MHC_WIDE_N(n, ...)                                        \
+    switch (n) {                                                  \
+        case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }     \
+        case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }     \
+        case 8: { constexpr int N_ = 8; __VA_ARGS__; break; }     \
+        case 16: { constexpr int N_ = 16; __VA_ARGS__; break; }   \
+        case 32: { constexpr int N_ = 32; __VA_ARGS__; break; }   \
+        default: return hipErrorInvalidValue;                     \
+    }
+
+bool wide_supported(int n, int64_t C) {
+    return (n == 2 || n == 4 || n == 8 || n == 16 || n == 32) && C >= 1 && C <= kWideMaxC;
+}
+
+hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
+                           int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
+                           hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!wide_supported(n, C) || B > 0x7fffffff) return hipErrorInvalidValue;
+    const int Ci = (int)C;
+    const dim3 grid((unsigned)B), block(kWideThreads);
+    const int tok = timing_begin("layer_fwd", s);
+#define MHC_WIDE_FWD(TX_, TO_)                                                                                   \
+    MHC_WIDE_N(n, hipLaunchKernelGGL((wide_fwd_kernel<TX_, TO_, N_>), grid, block, 0, s, (const TX_*)x, w, coef, \
+                                     coef_stride, (TO_*)out, rms_out, B, Ci, eps))
+    if (x_dtype == kBF16) {
+        if (out_dtype == kBF16) { MHC_WIDE_FWD(bf16_t, bf16_t); } else { MHC_WIDE_FWD(bf16_t, float); }
+    } else {
+        if (out_dtype == kBF16) { MHC_WIDE_FWD(float, bf16_t); } else { MHC_WIDE_FWD(float, float); }
+    }
+#undef MHC_WIDE_FWD
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+template <typename TX, int N, int MODE>
+static const void* wide_bwd_fn() {
+    return reinterpret_cast<const void*>(&wide_bwd_kernel<TX, N, MODE, (N <= 8)>);
+}
+
+int wide_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
+    if (!wide_supported(n, C) || B <= 0) return 1;
+    const void* fn = nullptr;
+    auto pick = [&]() -> hipError_t {
+        if (x_dtype == kBF16) {
+            MHC_WIDE_N(n, fn = wide_bwd_fn<bf16_t, N_, 0>());
+        } else {
+            MHC_WIDE_N(n, fn = wide_bwd_fn<float, N_, 0>());
+        }
+        return hipSuccess;
+    };
+    if (pick() != hipSuccess || !fn) return 1;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWideThreads, (size_t)C * sizeof(float)) !=
+            hipSuccess ||
+        per_cu < 1) {
+        (void)hipGetLastError();
+        per_cu = 1;
+    }
+    int64_t grid = (int64_t)device_cu_count() * per_cu;
+    if (grid > B) grid = B;
+    return (int)(grid < 1 ? 1 : grid);
+}
+
+hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
+                           const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out, int grid,
+                           int64_t B, int64_t C, float eps, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!wide_supported(n, C) || grid < 1 || (mode != 0 && mode != 1)) return hipErrorInvalidValue;
+    const int Ci = (int)C;
+    const size_t lds = (size_t)C * sizeof(float);
+    const int tok = timing_begin(mode == 0 ? "layer_bwd" : "layer_bwd_reduce", s);
+#define MHC_WIDE_BWD(TX_, M_)                                                                                      \
+    MHC_WIDE_N(n, hipLaunchKernelGGL((wide_bwd_kernel<TX_, N_, M_, (N_ <= 8)>), dim3(grid), dim3(kWideThreads), lds, \
+                                     s, g, (const TX_*)x, w, coef, coef_stride, (TX_*)dx, dw_part, scal_out, B, Ci,  \
+                                     eps))
+    if (x_dtype == kBF16) {
+        if (mode == 0) { MHC_WIDE_BWD(bf16_t, 0); } else { MHC_WIDE_BWD(bf16_t, 1); }
+    } else {
+        if (mode == 0) { MHC_WIDE_BWD(float, 0); } else { MHC_WIDE_BWD(float, 1); }
+    }
+#undef MHC_WIDE_BWD
+    hipError_t e = hipGetLastError();
+    timing_end(tok, s);
+    if (e != hipSuccess || n <= 8) return e;
+    // dM for n >= 16: same grid in MODE 0 (its rows of scal_out), one
+    // workgroup per token in MODE 1
+    const dim3 ggrid(mode == 0 ? (unsigned)grid : (unsigned)(B < 65536 ? B : 65536));
+#define MHC_GRAM(TX_, M_)                                                                                         \
+    if (n == 16) {                                                                                                \
+        hipLaunchKernelGGL((stream_gram_kernel<TX_, 16, M_>), ggrid, dim3(gram_threads<16>()), 0, s, g,            \
+                           (const TX_*)x, scal_out, B, Ci);                                                       \
+    } else {                                                                                                      \
+        hipLaunchKernelGGL((stream_gram_kernel<TX_, 32, M_>), ggrid, dim3(gram_threads<32>()), 0, s, g,            \
+                           (const TX_*)x, scal_out, B, Ci);                                                       \
+    }
+    const int tg = timing_begin("stream_gram", s);
+    if (x_dtype == kBF16) {
+        if (mode == 0) { MHC_GRAM(bf16_t, 0); } else { MHC_GRAM(bf16_t, 1); }
+    } else {
+        if (mode == 0) { MHC_GRAM(float, 0); } else { MHC_GRAM(float, 1); }
+    }
+#undef MHC_GRAM
+    timing_end(tg, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_wide_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
+                                       const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
+                                       float* d_h_res, int iters, float sk_eps, hipStream_t s) {
+    if (n == 16) {
+        hipLaunchKernelGGL((wide_static_finalize_kernel<16>), dim3(1), dim3(256), 0, s, scal_part, rows, h_pre, h_post,
+                           h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps);
+    } else if (n == 32) {
+        hipLaunchKernelGGL((wide_static_finalize_kernel<32>), dim3(1), dim3(256), 0, s, scal_part, rows, h_pre, h_post,
+                           h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mhc

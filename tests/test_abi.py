@@ -57,12 +57,15 @@ def test_sinkhorn_rejects_n_above_a_wave_on_host():
 
 def test_layer_rejects_unsupported_and_invalid_on_host():
     lib = _lib.load()
-    # n not compiled -> UNSUPPORTED; bad dtype -> INVALID; ragged hidden -> UNSUPPORTED
+    # n not compiled -> UNSUPPORTED; bad dtype -> INVALID; hidden past the
+    # channel-loop kernels' LDS row (12288 channels at n = 32) -> UNSUPPORTED
     assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 3, 64, 20, 1e-8, 1e-5, None) == -2
     assert lib.mhc_layer_static_fwd(1, 7, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
     assert lib.mhc_layer_static_fwd(1, 0, 1, 5, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
-    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 66, 20, 1e-8, 1e-5, None) == -2
-    assert b"hidden" in lib.mhc_last_error()
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 32, 12289, 20, 1e-8, 1e-5, None) == -2
+    assert b"too large for the row kernels" in lib.mhc_last_error()
+    # a ragged hidden size passes the host checks (channel-loop kernels)
+    assert lib.mhc_layer_static_fwd(None, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 66, 20, 1e-8, 1e-5, None) == -1
     # workspace too small
     assert lib.mhc_layer_static_bwd(1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 8, 4, 64, 20, 1e-8, 1e-5,
                                     None) == -3
@@ -70,13 +73,13 @@ def test_layer_rejects_unsupported_and_invalid_on_host():
 
 
 def test_expansion_rate_support_on_host():
-    """Layers compile n in {2, 4, 8}, dynamic H included (2n + n^2 = 80
-    projection rows at n = 8 run as three 32-row output tiles); the fused
-    wrapper n = 4 (other n go through the layer).  All rejected before any
-    device work."""
+    """Static layers compile n in {2, 4, 8, 16, 32}; dynamic H n in {2, 4, 8}
+    (2n + n^2 = 80 projection rows at n = 8 run as three 32-row output
+    tiles); the fused wrapper n = 4 (other n go through the layer).  All
+    rejected before any device work."""
     lib = _lib.load()
-    # static layer: n = 2, 8 pass the host checks; with a null x they fail on that
-    for n in (2, 8):
+    # static layer: these n pass the host checks; with a null x they fail on that
+    for n in (2, 8, 16, 32):
         assert lib.mhc_layer_static_fwd(None, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, n, 64, 20, 1e-8, 1e-5, None) == -1
         assert b"null x" in lib.mhc_last_error()
     assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 6, 64, 20, 1e-8, 1e-5, None) == -2

@@ -106,6 +106,14 @@ def test_dynamic_layer_n8_matches_oracle(device, x_dtype, B, C):
     _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n=8 B={B} C={C} {x_dtype}")
 
 
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_dynamic_layer_n8_wide_hidden(device, x_dtype):
+    """n = 8, C = 10240: the register forward holds the rows, the backward's
+    do not fit and run the channel-loop kernel (dM in its row sums)."""
+    d = R.dynamic_layer_inputs(4, 8, 10240, seed=81, x_dtype=x_dtype, alpha=0.3, phi_std=0.02, b_std=0.5)
+    _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n=8 C=10240 {x_dtype}")
+
+
 def test_dynamic_layer_unsupported_n_raises(device):
     layer = mhc.MHCLayer(64, 3, use_dynamic_h=True).to(device)
     with pytest.raises(RuntimeError, match="n=3 is not compiled"):

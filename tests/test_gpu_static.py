@@ -165,6 +165,50 @@ def test_static_layer_general_n(device, n, B, C, x_dtype):
                   tag=f"n={n} B={B} C={C} {x_dtype}")
 
 
+@pytest.mark.parametrize("n,B,C", [(16, 5, 64), (16, 19, 999), (32, 3, 100), (32, 32, 1280)])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_static_layer_wide_n(device, n, B, C, x_dtype):
+    """Expansion rates 16 and 32 on the channel-loop kernels, dM from the
+    per-token Gram kernel; (B, C, n) = (32, 1280, 32) is a paper
+    configuration (benchmark.py:307)."""
+    d = R.static_layer_inputs(B, n, C, seed=n * 1000 + B + C, x_dtype=x_dtype)
+    _check_static(d, _run_static(d, device), _oracle_static(d), x_bf16=x_dtype == torch.bfloat16,
+                  tag=f"n={n} B={B} C={C} {x_dtype}")
+
+
+@pytest.mark.parametrize("n,C", [(2, 1), (2, 7), (4, 250), (4, 1001), (8, 13), (8, 10240)])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+def test_static_layer_ragged_hidden(device, n, C, x_dtype):
+    """Hidden sizes that are not a multiple of the 4-channel chunk (the
+    reference pads such rows, stream_ops.cpp:66-68) run the channel-loop
+    kernels; (8, 10240) fits the register forward but not its backward."""
+    d = R.static_layer_inputs(6, n, C, seed=7 * n + C, x_dtype=x_dtype)
+    _check_static(d, _run_static(d, device), _oracle_static(d), x_bf16=x_dtype == torch.bfloat16,
+                  tag=f"n={n} C={C} {x_dtype}")
+
+
+def test_static_layer_module_n32(device):
+    """MHCLayer(expansion_rate=32) through the module, non-trivial H."""
+    torch.manual_seed(32)
+    layer = mhc.MHCLayer(320, 32, use_dynamic_h=False).to(device)
+    with torch.no_grad():
+        layer.H_pre.normal_()
+        layer.H_post.normal_()
+        layer.H_res.normal_()
+    x = torch.randn(9, 32, 320, generator=_gen(32))
+    g = torch.randn(9, 32, 320, generator=_gen(33))
+    xd = x.to(device).requires_grad_(True)
+    out = layer(xd)
+    out.backward(g.to(device))
+    d = {"x": x, "grad": g, "weight": layer.rmsnorm_weight.detach().cpu(), "H_pre": layer.H_pre.detach().cpu(),
+         "H_post": layer.H_post.detach().cpu(), "H_res": layer.H_res.detach().cpu()}
+    rout, rgx, rgp = _oracle_static(d)
+    assert_close(out, rout, what="n=32 module out", **FWD)
+    assert_close(xd.grad, rgx, 1e-3, grad_atol(rgx, 1e-5), "n=32 module dx")
+    assert_close(layer.H_pre.grad, rgp[1], 1e-3, grad_atol(rgp[1], 1e-4), "n=32 module d_H_pre")
+    assert_close(layer.H_res.grad, rgp[3], 1e-3, grad_atol(rgp[3], 1e-4), "n=32 module d_H_res")
+
+
 def test_static_layer_module_general_n(device):
     """MHCLayer(expansion_rate=8) forward/backward through the module."""
     torch.manual_seed(8)
