@@ -40,7 +40,7 @@ static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
 // The fused layer kernels are compiled for n in {2, 4, 8}; dynamic H needs
 // 2n + n^2 <= 32 projection outputs (n <= 4); the fused wrapper is n = 4.
 static bool supported_layer_n(int n) { return n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
-static bool supported_dynamic_n(int n) { return n == 2 || n == 4 || n == 8; }
+static bool supported_dynamic_n(int n) { return n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
 // the standalone aggregate / distribute operators
 static bool supported_ops_n(int n) { return n == 1 || n == 2 || n == 4 || n == 8; }
 
@@ -595,7 +595,7 @@ static int check_dyn(const char* fn, int64_t batch, int32_t n, int32_t hidden, i
     if (st) return st;
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (!supported_dynamic_n(n))
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": dynamic H is compiled for n in {2, 4, 8}, not n=" +
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": dynamic H is compiled for n in {2, 4, 8, 16, 32}, not n=" +
                                              std::to_string(n));
     if (((int64_t)n * hidden) % 32 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
@@ -707,18 +707,26 @@ int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, 
     return hip_status(e);
 }
 
+// With bf16 x and more than one 32-row projection tile (n >= 8), dx is
+// accumulated in fp32 (x upcast once, exactly) and rounded to bf16 once at
+// the end, as the reference's fp32 autograd does; one tile adds its terms
+// to the bf16 stream part directly.
+static bool dyn_bwd_f32_acc(int32_t n, int32_t x_dtype) { return x_dtype == kBF16 && 2 * n + n * n > kProjTile; }
+
 struct DynBwdWs {
     int grid, cblocks, tiles;
-    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, total;
+    int wdt;  // element type the row and projection kernels run on
+    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, total;
 };
 
 static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
     DynBwdWs w{};
     const int64_t np = 2 * n + n * n;
     const int64_t K = (int64_t)n * hidden;
-    w.grid = batch > 0 ? layer_bwd_grid(x_dtype, n, batch, hidden) : 1;
+    w.wdt = dyn_bwd_f32_acc(n, x_dtype) ? kF32 : x_dtype;
+    w.grid = batch > 0 ? layer_bwd_grid(w.wdt, n, batch, hidden) : 1;
     w.cblocks = batch > 0 ? dyn_coef_bwd_blocks(n, batch) : 1;
-    w.tiles = batch > 0 ? proj_bwd_tiles(x_dtype, batch, (int64_t)n * hidden) : 1;
+    w.tiles = batch > 0 ? proj_bwd_tiles(w.wdt, batch, (int64_t)n * hidden) : 1;
     size_t o = 0;
     w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
     w.scal_off = o; o += align256((size_t)batch * (n * n + 2 * n + 2) * 4);
@@ -728,6 +736,9 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     w.phip_off = o; o += align256((size_t)w.tiles * tile_rows((int)np) * K * 4);
     w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
     w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)tile_rows((int)np) * K) * 4);
+    const size_t acc = w.wdt != x_dtype ? (size_t)batch * K * 4 : 0;
+    w.xw_off = o; o += align256(acc);
+    w.dxw_off = o; o += align256(acc);
     w.total = o;
     return w;
 }
@@ -765,6 +776,11 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     float* phip = (float*)(ws + w.phip_off);
     float* stw = (float*)(ws + w.stw_off);
     float* stp = (float*)(ws + w.stp_off);
+    float* xw = (float*)(ws + w.xw_off);
+    float* dxw = (float*)(ws + w.dxw_off);
+    // the tensors the row and projection kernels work on
+    const void* xk = w.wdt != x_dtype ? (const void*)xw : x;
+    void* dxk = w.wdt != x_dtype ? (void*)dxw : grad_x;
     const DynSaved d = dyn_saved(batch, n, hidden);
     const int np = 2 * n + n * n;
     const int64_t K = (int64_t)n * hidden;
@@ -776,16 +792,19 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         e = launch_fill_zero(dw_part, hidden, s);
         if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
     } else {
-        e = launch_layer_bwd(x_dtype, n, 1, grad_out, x, w32, saved + d.coef_off, np, grad_x, dw_part, scal, w.grid,
-                             batch, hidden, rmsnorm_eps, s);
+        if (w.wdt != x_dtype) e = launch_weight_f32(x, x_dtype, batch * K, xw, s);
+        if (e == hipSuccess)
+            e = launch_layer_bwd(w.wdt, n, 1, grad_out, xk, w32, saved + d.coef_off, np, dxk, dw_part, scal, w.grid,
+                                 batch, hidden, rmsnorm_eps, s);
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
                                     s);
     }
     if (e == hipSuccess)
-        e = proj_bwd_all(x_dtype, x, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, np, grad_x, true, phip,
+        e = proj_bwd_all(w.wdt, xk, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, np, dxk, true, phip,
                          rows_p, stp, grad_phi, batch, K, s);
+    if (e == hipSuccess && w.wdt != x_dtype) e = launch_cast_bf16(dxw, batch * K, grad_x, s);
     if (e == hipSuccess)
         e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);

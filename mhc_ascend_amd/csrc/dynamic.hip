@@ -495,6 +495,73 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// The same for n >= 16, one token per group of n lanes: the db / dalpha
+// terms (np + 3 values, too many to block-sum in registers) are written per
+// token to part[b][np + 3] and column-summed over the tokens afterwards.
+// The Sinkhorn adjoint recomputes each iteration (no register history).
+// ---------------------------------------------------------------------------
+template <int N>
+__global__ __launch_bounds__(256) void dyn_coef_bwd_wide_kernel(
+    const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
+    const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
+    const float* __restrict__ a_post, const float* __restrict__ a_res, const float* __restrict__ b_res,
+    float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int iters, float sk_eps) {
+    constexpr int NP = 2 * N + N * N;
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NV = NP + 3;
+    constexpr int NPT = dp_stride(NP);
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t tok = gid / N;
+    const int r = (int)(gid % N);
+    const bool tv = tok < B;
+    const int64_t tk = tv ? tok : 0;
+    const float* sc = scal + tk * (NS + 2);
+    const float* cf = coef + tk * NP;
+    const float* pv = p + tk * NP;
+    const float ap = a_pre[0], aq = a_post[0], ar = a_res[0];
+    const float inv = 1.f / rh[tk];
+
+    float gm[N], e[N], pr[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+        gm[c] = tv ? sc[r * N + c] : 0.f;
+        pr[c] = pv[2 * N + r * N + c];
+        e[c] = tv ? expf(pr[c] * ar * inv + b_res[r * N + c]) : 0.f;
+    }
+    sk_backward<N>(gm, e, iters, sk_eps, tv);
+    const float hp = cf[r], hq = cf[N + r];
+    const float dt_pre = tv ? sc[N * N + N + r] * hp * (1.f - hp) : 0.f;
+    const float dt_post = tv ? sc[N * N + r] * hq * (1.f - 0.5f * hq) : 0.f;
+    float lp = 0.f;
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+        gm[c] = tv ? gm[c] * e[c] : 0.f;  // dt_res row r
+        lp += gm[c] * pr[c];
+    }
+    const float l_pre = dt_pre * pv[r], l_post = dt_post * pv[N + r];
+    const float tot = group_sum<N>(ap * l_pre + aq * l_post + ar * lp);
+    const float s_pre = group_sum<N>(l_pre), s_post = group_sum<N>(l_post), s_res = group_sum<N>(lp);
+    if (!tv) return;
+    float* dp = dp_out + tok * NPT;
+    dp[r] = ap * dt_pre * inv;
+    dp[N + r] = aq * dt_post * inv;
+#pragma unroll
+    for (int c = 0; c < N; ++c) dp[2 * N + r * N + c] = ar * gm[c] * inv;
+    float* pt = part + tok * NV;
+    pt[r] = dt_pre;
+    pt[N + r] = dt_post;
+#pragma unroll
+    for (int c = 0; c < N; ++c) pt[2 * N + r * N + c] = gm[c];
+    if (r == 0) {
+        for (int o = NP; o < NPT; ++o) dp[o] = 0.f;
+        s_out[tok] = -tot * inv * inv * inv / (float)K;
+        pt[NP] = s_pre * inv;
+        pt[NP + 1] = s_post * inv;
+        pt[NP + 2] = s_res * inv;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // n = 4: one token per 16-lane DPP row.  Lane l holds element (l/4, l%4) of
 // t_res and, for l < 8, t_pre[l] (l < 4) or t_post[l-4] (the coefficient
 // order), so the Sinkhorn iterations are a few DPP steps per lane
@@ -1037,6 +1104,8 @@ hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, fl
         case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }    \
         case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }    \
         case 8: { constexpr int N_ = 8; __VA_ARGS__; break; }    \
+        case 16: { constexpr int N_ = 16; __VA_ARGS__; break; }  \
+        case 32: { constexpr int N_ = 32; __VA_ARGS__; break; }  \
         default: return hipErrorInvalidValue;                    \
     }
 
@@ -1059,8 +1128,11 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
     return hipGetLastError();
 }
 
+// Rows of the db / dalpha partials: one per workgroup, or one per token for
+// n >= 16.
 int dyn_coef_bwd_blocks(int n, int64_t B) {
     if (n == 4) return dyn_coef16_bwd_blocks(B);
+    if (n >= 16) return (int)(B < 1 ? 1 : B);
     return (int)((B * pow2ceil(n) + 255) / 256);
 }
 
@@ -1075,8 +1147,26 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                            a_res, b_res, dp_out, s_out, part, iters, sk_eps);
         return hipGetLastError();
     }
-    MHC_DYN_N(n, hipLaunchKernelGGL((dyn_coef_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
-                                    a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps));
+    if (n >= 16) {
+        const unsigned wblocks = (unsigned)((B * n + 255) / 256);
+        if (n == 16) {
+            hipLaunchKernelGGL((dyn_coef_bwd_wide_kernel<16>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        } else if (n == 32) {
+            hipLaunchKernelGGL((dyn_coef_bwd_wide_kernel<32>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        } else {
+            return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
+    switch (n) {
+        case 2: hipLaunchKernelGGL((dyn_coef_bwd_kernel<2>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                                   a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps); break;
+        case 8: hipLaunchKernelGGL((dyn_coef_bwd_kernel<8>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                                   a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -527,6 +527,12 @@ __global__ __launch_bounds__(256) void weight_f32_kernel(const TW* __restrict__ 
     if (i < C) out[i] = VecIO<TW>::scalar(w + i);
 }
 
+__global__ __launch_bounds__(256) void cast_bf16_kernel(const float* __restrict__ in, int64_t n,
+                                                        bf16_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f32_to_bf16(in[i]);
+}
+
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.f;
@@ -543,6 +549,12 @@ hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, 
     } else {
         hipLaunchKernelGGL(weight_f32_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)w, C, out);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_cast_bf16(const float* in, int64_t n, void* out, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(cast_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, n, (bf16_t*)out);
     return hipGetLastError();
 }
 

@@ -59,6 +59,8 @@ int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
 bool layer_fwd_is_wide(int n, int64_t C);
 bool layer_bwd_is_wide(int n, int64_t C);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s);
+// out[i] = bf16(in[i]) (round to nearest even) for n elements.
+hipError_t launch_cast_bf16(const float* in, int64_t n, void* out, hipStream_t s);
 // Two-stage deterministic column sum of part[rows][cols]: stage[rsplit][cols].
 hipError_t launch_column_partial(const float* part, int rows, int64_t cols, float* stage, int rsplit,
                                  hipStream_t s);

@@ -73,10 +73,10 @@ def test_layer_rejects_unsupported_and_invalid_on_host():
 
 
 def test_expansion_rate_support_on_host():
-    """Static layers compile n in {2, 4, 8, 16, 32}; dynamic H n in {2, 4, 8}
-    (2n + n^2 = 80 projection rows at n = 8 run as three 32-row output
-    tiles); the fused wrapper n = 4 (other n go through the layer).  All
-    rejected before any device work."""
+    """Layers compile n in {2, 4, 8, 16, 32}, dynamic H included (its
+    2n + n^2 projection rows run as 32-row output tiles); the fused wrapper
+    n = 4 (other n go through the layer).  All rejected before any device
+    work."""
     lib = _lib.load()
     # static layer: these n pass the host checks; with a null x they fail on that
     for n in (2, 8, 16, 32):

@@ -114,6 +114,17 @@ def test_dynamic_layer_n8_wide_hidden(device, x_dtype):
     _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n=8 C=10240 {x_dtype}")
 
 
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,B,C", [(16, 5, 64), (32, 3, 96), (32, 32, 1280)])
+def test_dynamic_layer_wide_n(device, x_dtype, n, B, C):
+    """Expansion rates 16 and 32: 2n + n^2 projection rows (1088 at n = 32)
+    in 32-row output tiles, per-token Sinkhorn on n-lane groups, dM from the
+    per-token Gram kernel; (32, 1280, 32) is a paper configuration
+    (benchmark.py:307)."""
+    d = R.dynamic_layer_inputs(B, n, C, seed=n * 100 + B + C, x_dtype=x_dtype, alpha=0.1, phi_std=0.02, b_std=0.5)
+    _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n={n} B={B} C={C} {x_dtype}")
+
+
 def test_dynamic_layer_unsupported_n_raises(device):
     layer = mhc.MHCLayer(64, 3, use_dynamic_h=True).to(device)
     with pytest.raises(RuntimeError, match="n=3 is not compiled"):
@@ -136,7 +147,8 @@ def test_dynamic_inference_equals_training_forward(device):
 
 
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n,B,C", [(4, 1, 64), (4, 37, 1280), (2, 9, 256), (4, 300, 4096)])
+@pytest.mark.parametrize("n,B,C", [(4, 1, 64), (4, 37, 1280), (2, 9, 256), (4, 300, 4096), (8, 5, 320),
+                                   (32, 4, 1280)])
 def test_dynamic_inference_packed_and_bf16_out(device, x_dtype, n, B, C):
     """The forward-only entry on packed parameters: its fp32 output is the
     training forward's bit for bit, its bf16 output is that result rounded to
