@@ -42,7 +42,7 @@ static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
 static bool supported_layer_n(int n) { return n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
 static bool supported_dynamic_n(int n) { return n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
 // the standalone aggregate / distribute operators
-static bool supported_ops_n(int n) { return n == 1 || n == 2 || n == 4 || n == 8; }
+static bool supported_ops_n(int n) { return n == 1 || n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
 
 // ---------------------------------------------------------------------------
 // Device properties
@@ -297,16 +297,18 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
 }
 
 // ---- standalone operators ---------------------------------------------------
-static int check_rows(const char* fn, int64_t batch, int64_t hidden, int32_t dtype, int n_arrays) {
+// Rows the register kernels cannot take run the channel-loop kernels, which
+// take any width; the RMSNorm backward's keeps its dw row in LDS (dw_row).
+static int check_rows(const char* fn, int64_t batch, int64_t hidden, int32_t dtype, int n_arrays,
+                      bool dw_row = false) {
     if (batch < 0) return fail(MHC_ERR_INVALID, std::string(fn) + ": batch must be >= 0");
     if (hidden < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": hidden must be >= 1");
     if (!valid_dtype(dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": dtype must be F32 or BF16");
-    const int wc = dtype == kBF16 ? 8 : 4;
-    if (hidden % wc != 0)
-        return fail(MHC_ERR_UNSUPPORTED,
-                    std::string(fn) + ": hidden must be a multiple of " + std::to_string(wc) + " for this dtype");
-    if (choose_row_tiling(hidden, wc, n_arrays).vpt <= 0)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
+    if (hidden > 0x7fffffff) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be < 2^31");
+    const bool regs = choose_row_tiling(hidden, dtype == kBF16 ? 8 : 4, n_arrays).vpt > 0;
+    if (!regs && dw_row && hidden > kWideMaxC)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden=" + std::to_string(hidden) +
+                                             " is too large for the row kernels");
     return MHC_SUCCESS;
 }
 
@@ -347,7 +349,7 @@ size_t mhc_rmsnorm_bwd_workspace_size(int64_t batch, int32_t hidden, int32_t dty
 int mhc_rmsnorm_bwd(const void* grad_out, const void* inp, int32_t dtype, const float* weight, const float* rms,
                     void* grad_inp, float* grad_weight, void* workspace, size_t workspace_bytes, int64_t batch,
                     int32_t hidden, void* stream) {
-    int st = check_rows("rmsnorm_bwd", batch, hidden, dtype, 2);
+    int st = check_rows("rmsnorm_bwd", batch, hidden, dtype, 2, true);
     if (st) return st;
     MHC_REQUIRE(weight && grad_weight, "rmsnorm_bwd: null weight/grad_weight");
     MHC_REQUIRE(batch == 0 || (grad_out && inp && rms && grad_inp), "rmsnorm_bwd: null pointer");

@@ -94,6 +94,26 @@ int wide_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
 hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                            const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out, int grid,
                            int64_t B, int64_t C, float eps, hipStream_t s);
+// Standalone operators on rows of any width, n in {1, 2, 4, 8, 16, 32}
+// (same outputs as the launch_* of ops.hip; the RMSNorm backward's dw
+// partial rows [grid][C] come from wide_rmsnorm_bwd_grid, C <= kWideMaxC).
+hipError_t launch_wide_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, float* rms, int64_t B, int64_t C,
+                                   float eps, hipStream_t s);
+int wide_rmsnorm_bwd_grid(int dt, int64_t B, int64_t C);
+hipError_t launch_wide_rmsnorm_bwd(int dt, const void* g, const void* x, const float* w, const float* rms, void* gx,
+                                   float* dw_part, int grid, int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_wide_compute_rms(int dt, const void* x, float* rms, int64_t B, int64_t K, float eps,
+                                   hipStream_t s);
+hipError_t launch_wide_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out,
+                                     float* h_act, int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_wide_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
+                                     void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_wide_distribute_fwd(int dt, int n, const void* y, const float* H, int64_t hs, const float* M,
+                                      int64_t ms, const void* x, float* out, float* h_act, int64_t B, int64_t C,
+                                      hipStream_t s);
+hipError_t launch_wide_distribute_bwd(int dt, int n, const float* g, const void* x, const void* y, const float* M,
+                                      int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
+                                      float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
 // Static H gradients for n >= 16 from scal_part[rows][n^2 + 2n].
 hipError_t launch_wide_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
                                        const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,

@@ -1,4 +1,6 @@
 // Standalone stream / norm operators of the mHC API, one HBM pass each.
+// Rows that are not a multiple of the 16-byte vector, too wide for the
+// register rows, or n > 8 run the channel-loop variants of wide.hip.
 //
 // They replace the Ascend kernels bound at bindings.cpp:237-374 and
 // 380-460 (rmsnorm.cpp, stream_ops.cpp) and compute_rms.cpp (bound at
@@ -363,8 +365,13 @@ hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, fl
                               float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
     const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 1);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
     const int tok = timing_begin("rmsnorm_fwd", s);
+    if (t.vpt <= 0) {
+        // rows that are not a multiple of the vector (or too wide): channel loop
+        const hipError_t e = launch_wide_rmsnorm_fwd(dt, x, w, y, rms, B, C, eps, s);
+        timing_end(tok, s);
+        return e;
+    }
     MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 1, T_, hipLaunchKernelGGL((rmsnorm_fwd_kernel<T_, V_>), dim3(B), dim3(t.threads),
                                                                0, s, (const T_*)x, w, (T_*)y, rms, (int)C, eps)));
     timing_end(tok, s);
@@ -373,7 +380,7 @@ hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, fl
 
 int rmsnorm_bwd_grid(int dt, int64_t B, int64_t C) {
     const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2);
-    if (t.vpt <= 0) return 1;
+    if (t.vpt <= 0) return wide_rmsnorm_bwd_grid(dt, B, C);
     int64_t g = (int64_t)device_cu_count() * ((t.threads <= 256) ? 4 : 2);
     if (g > B) g = B;
     return g < 1 ? 1 : (int)g;
@@ -382,8 +389,12 @@ int rmsnorm_bwd_grid(int dt, int64_t B, int64_t C) {
 hipError_t launch_rmsnorm_bwd(int dt, const void* g, const void* x, const float* w, const float* rms, void* gx,
                               float* dw_part, int grid, int64_t B, int64_t C, hipStream_t s) {
     const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
     const int tok = timing_begin("rmsnorm_bwd", s);
+    if (t.vpt <= 0) {
+        const hipError_t e = launch_wide_rmsnorm_bwd(dt, g, x, w, rms, gx, dw_part, grid, B, C, s);
+        timing_end(tok, s);
+        return e;
+    }
     MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 2, T_, hipLaunchKernelGGL((rmsnorm_bwd_kernel<T_, V_>), dim3(grid),
                                                                dim3(t.threads), 0, s, (const T_*)g, (const T_*)x, w,
                                                                rms, (T_*)gx, dw_part, B, (int)C)));
@@ -394,7 +405,7 @@ hipError_t launch_rmsnorm_bwd(int dt, const void* g, const void* x, const float*
 hipError_t launch_compute_rms(int dt, const void* x, float* rms, int64_t B, int64_t K, float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
     const RowTiling t = choose_row_tiling(K, dt == kBF16 ? 8 : 4, 1);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
+    if (t.vpt <= 0) return launch_wide_compute_rms(dt, x, rms, B, K, eps, s);
     MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 1, T_, hipLaunchKernelGGL((compute_rms_kernel<T_, V_>), dim3(B),
                                                                dim3(t.threads), 0, s, (const T_*)x, rms, (int)K,
                                                                eps)));
@@ -413,9 +424,13 @@ hipError_t launch_compute_rms(int dt, const void* x, float* rms, int64_t B, int6
 hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out, float* h_act,
                                 int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
+    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
     const int tok = timing_begin("aggregate_fwd", s);
+    if (t.vpt <= 0) {
+        const hipError_t e = launch_wide_aggregate_fwd(dt, n, x, H, hs, out, h_act, B, C, s);
+        timing_end(tok, s);
+        return e;
+    }
     MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, hipLaunchKernelGGL((aggregate_fwd_kernel<T_, N_, V_>),
                                                                                  dim3(B), dim3(t.threads), 0, s,
                                                                                  (const T_*)x, H, hs, (T_*)out, h_act,
@@ -427,9 +442,13 @@ hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, in
 hipError_t launch_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
                                 void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
+    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
     const int tok = timing_begin("aggregate_bwd", s);
+    if (t.vpt <= 0) {
+        const hipError_t e = launch_wide_aggregate_bwd(dt, n, g, x, h_act, hs, gx, gh_act, gh_raw, B, C, s);
+        timing_end(tok, s);
+        return e;
+    }
     MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, hipLaunchKernelGGL((aggregate_bwd_kernel<T_, N_, V_>),
                                                                                  dim3(B), dim3(t.threads), 0, s,
                                                                                  (const T_*)g, (const T_*)x, h_act, hs,
@@ -442,9 +461,13 @@ hipError_t launch_distribute_fwd(int dt, int n, const void* y, const float* H, i
                                  int64_t ms, const void* x, float* out, float* h_act, int64_t B, int64_t C,
                                  hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
+    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
     const int tok = timing_begin("distribute_fwd", s);
+    if (t.vpt <= 0) {
+        const hipError_t e = launch_wide_distribute_fwd(dt, n, y, H, hs, M, ms, x, out, h_act, B, C, s);
+        timing_end(tok, s);
+        return e;
+    }
     MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, hipLaunchKernelGGL((distribute_fwd_kernel<T_, N_, V_>),
                                                                                  dim3(B), dim3(t.threads), 0, s,
                                                                                  (const T_*)y, H, hs, M, ms,
@@ -458,9 +481,15 @@ hipError_t launch_distribute_bwd(int dt, int n, const float* g, const void* x, c
                                  float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
     // the block hands one of the n*n + n row sums to each thread
-    const RowTiling t = with_min_threads(choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2 * n + 1), n * n + n);
-    if (t.vpt <= 0) return hipErrorInvalidValue;
+    const RowTiling t =
+        n > 8 ? RowTiling{0, 0} : with_min_threads(choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2 * n + 1), n * n + n);
     const int tok = timing_begin("distribute_bwd", s);
+    if (t.vpt <= 0) {
+        const hipError_t e =
+            launch_wide_distribute_bwd(dt, n, g, x, y, M, ms, h_act, hs, gx, gy, gM, gh_act, gh_raw, B, C, s);
+        timing_end(tok, s);
+        return e;
+    }
     MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, 2 * N_ + 1, T_,
                                            hipLaunchKernelGGL((distribute_bwd_kernel<T_, N_, V_>), dim3(B),
                                                               dim3(t.threads), 0, s, g, (const T_*)x, (const T_*)y, M,

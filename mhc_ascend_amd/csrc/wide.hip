@@ -232,7 +232,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_bwd_kernel(const float* __r
 // staged in LDS, each of the (n/2)^2 lanes forming a 2 x 2 block of dM.
 // MODE 0 sums over the workgroup's tokens (same persistent grid as
 // wide_bwd_kernel) into scal_out[blockIdx.x][0 .. n^2); MODE 1 writes each
-// token's dM to scal_out[b][0 .. n^2).  Fixed summation order.
+// token's dM to scal_out[b * ostride + 0 .. n^2).  Fixed summation order.
 // ---------------------------------------------------------------------------
 template <int N> constexpr int gram_threads() { return (N / 2) * (N / 2); }
 
@@ -240,7 +240,7 @@ template <typename TX, int N, int MODE>
 __global__ __launch_bounds__(gram_threads<N>()) void stream_gram_kernel(const float* __restrict__ g,
                                                                         const TX* __restrict__ x,
                                                                         float* __restrict__ scal_out, int64_t B,
-                                                                        int C) {
+                                                                        int C, int64_t ostride) {
     constexpr int CT = 64;
     constexpr int T = gram_threads<N>();
     constexpr int NS = N * N + 2 * N;
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(gram_threads<N>()) void stream_gram_kernel(const fl
             __syncthreads();
         }
         if (MODE == 1) {
-            float* o = scal_out + b * (NS + 2);
+            float* o = scal_out + b * ostride;
             o[i0 * N + j0] = acc[0][0];
             o[i0 * N + j0 + 1] = acc[0][1];
             o[(i0 + 1) * N + j0] = acc[1][0];
@@ -336,6 +336,223 @@ __global__ __launch_bounds__(256) void wide_static_finalize_kernel(
         const float tq = 2.f * sigmoidf(h_post[r]);
         d_h_pre[r] = tot[N * N + N + r] * tp * (1.f - tp);
         d_h_post[r] = tot[N * N + r] * tq * (1.f - tq * 0.5f);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Standalone operators on rows of any width and n in {1, 2, 4, 8, 16, 32}
+// (the formulas of ops.hip; bindings.cpp:237-374, 380-460, 543-566).  One
+// token row per workgroup (the RMSNorm backward: persistent, dw in LDS).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kWideThreads) void wide_rmsnorm_fwd_kernel(const T* __restrict__ x,
+                                                                        const float* __restrict__ w,
+                                                                        T* __restrict__ y, float* __restrict__ rms,
+                                                                        int C, float eps) {
+    __shared__ float red[kWideThreads / kWave];
+    __shared__ float tot[1];
+    const int64_t b = blockIdx.x;
+    const T* xb = x + b * C;
+    float ss[1] = {0.f};
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        const float v = VecIO<T>::scalar(xb + c);
+        ss[0] += v * v;
+    }
+    wide_block_total<1>(ss, red, tot);
+    const float r = sqrtf(tot[0] / (float)C + eps);
+    const float inv = 1.f / r;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) st_elem_nt(y + b * C + c, ld_elem_nt(xb + c) * inv * w[c]);
+    if (threadIdx.x == 0) rms[b] = r;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kWideThreads) void wide_rmsnorm_bwd_kernel(const T* __restrict__ g,
+                                                                        const T* __restrict__ x,
+                                                                        const float* __restrict__ w,
+                                                                        const float* __restrict__ rms,
+                                                                        T* __restrict__ gx,
+                                                                        float* __restrict__ dw_part, int64_t B,
+                                                                        int C) {
+    extern __shared__ float dws[];
+    __shared__ float red[kWideThreads / kWave];
+    __shared__ float tot[1];
+    for (int c = threadIdx.x; c < C; c += blockDim.x) dws[c] = 0.f;
+    for (int64_t b = blockIdx.x; b < B; b += gridDim.x) {
+        const T* xb = x + b * C;
+        const T* gb = g + b * C;
+        const float inv = 1.f / rms[b];
+        float dot[1] = {0.f};
+        for (int c = threadIdx.x; c < C; c += blockDim.x)
+            dot[0] += VecIO<T>::scalar(gb + c) * w[c] * VecIO<T>::scalar(xb + c);
+        wide_block_total<1>(dot, red, tot);
+        const float k2 = tot[0] * inv * inv * inv / (float)C;
+        for (int c = threadIdx.x; c < C; c += blockDim.x) {
+            const float gv = ld_elem_nt(gb + c), xv = ld_elem_nt(xb + c);
+            st_elem_nt(gx + b * C + c, w[c] * gv * inv - xv * k2);
+            dws[c] += gv * xv * inv;
+        }
+    }
+    for (int c = threadIdx.x; c < C; c += blockDim.x) dw_part[(int64_t)blockIdx.x * C + c] = dws[c];
+}
+
+template <typename T>
+__global__ __launch_bounds__(kWideThreads) void wide_compute_rms_kernel(const T* __restrict__ x,
+                                                                        float* __restrict__ rms, int64_t K,
+                                                                        float eps) {
+    __shared__ float red[kWideThreads / kWave];
+    __shared__ float tot[1];
+    const int64_t b = blockIdx.x;
+    float ss[1] = {0.f};
+    for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
+        const float v = ld_elem_nt(x + b * K + k);
+        ss[0] += v * v;
+    }
+    wide_block_total<1>(ss, red, tot);
+    if (threadIdx.x == 0) rms[b] = sqrtf(tot[0] / (float)K + eps);
+}
+
+template <typename T, int N>
+__global__ __launch_bounds__(kWideThreads) void wide_aggregate_fwd_kernel(const T* __restrict__ x,
+                                                                          const float* __restrict__ H,
+                                                                          int64_t h_stride, T* __restrict__ out,
+                                                                          float* __restrict__ h_act, int C) {
+    const int64_t b = blockIdx.x;
+    float h[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) h[i] = sigmoidf(H[b * h_stride + i]);
+    const T* xb = x + b * (int64_t)N * C;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) s += h[i] * ld_elem_nt(xb + (int64_t)i * C + c);
+        st_elem_nt(out + b * C + c, s);
+    }
+    if (threadIdx.x < N) {
+        float hi = 0.f;
+#pragma unroll
+        for (int q = 0; q < N; ++q) hi = (q == (int)threadIdx.x) ? h[q] : hi;
+        h_act[b * N + threadIdx.x] = hi;
+    }
+}
+
+template <typename T, int N>
+__global__ __launch_bounds__(kWideThreads) void wide_aggregate_bwd_kernel(
+    const T* __restrict__ g, const T* __restrict__ x, const float* __restrict__ h_act, int64_t h_stride,
+    T* __restrict__ gx, float* __restrict__ gh_act, float* __restrict__ gh_raw, int C) {
+    __shared__ float red[(kWideThreads / kWave) * N];
+    __shared__ float tot[N];
+    const int64_t b = blockIdx.x;
+    float h[N], sv[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        h[i] = h_act[b * h_stride + i];
+        sv[i] = 0.f;
+    }
+    const T* xb = x + b * (int64_t)N * C;
+    T* gb = gx + b * (int64_t)N * C;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        const float gv = ld_elem_nt(g + b * C + c);
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            sv[i] += gv * ld_elem_nt(xb + (int64_t)i * C + c);
+            st_elem_nt(gb + (int64_t)i * C + c, gv * h[i]);
+        }
+    }
+    wide_block_total<N>(sv, red, tot);
+    if (threadIdx.x < N) {
+        const int i = threadIdx.x;
+        const float hi = h_act[b * h_stride + i];
+        if (gh_act) gh_act[b * N + i] = tot[i];
+        if (gh_raw) gh_raw[b * N + i] = tot[i] * hi * (1.f - hi);
+    }
+}
+
+template <typename T, int N>
+__global__ __launch_bounds__(kWideThreads) void wide_distribute_fwd_kernel(
+    const T* __restrict__ y, const float* __restrict__ H, int64_t h_stride, const float* __restrict__ M,
+    int64_t m_stride, const T* __restrict__ x, float* __restrict__ out, float* __restrict__ h_act, int C) {
+    const int64_t b = blockIdx.x;
+    float h[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) h[i] = 2.f * sigmoidf(H[b * h_stride + i]);
+    const float* mb = M + b * m_stride;
+    const T* xb = x + b * (int64_t)N * C;
+    float* ob = out + b * (int64_t)N * C;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float xv[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) xv[j] = ld_elem_nt(xb + (int64_t)j * C + c);
+        const float yv = ld_elem_nt(y + b * C + c);
+        for (int i = 0; i < N; ++i) {
+            float s = h[i] * yv;
+#pragma unroll
+            for (int j = 0; j < N; ++j) s += mb[i * N + j] * xv[j];
+            st_elem_nt(ob + (int64_t)i * C + c, s);
+        }
+    }
+    if (threadIdx.x < N) {
+        float hi = 0.f;
+#pragma unroll
+        for (int q = 0; q < N; ++q) hi = (q == (int)threadIdx.x) ? h[q] : hi;
+        h_act[b * N + threadIdx.x] = hi;
+    }
+}
+
+// dM in the row sums for n <= 8 (DM); for n >= 16 stream_gram_kernel writes it.
+template <typename T, int N, bool DM>
+__global__ __launch_bounds__(kWideThreads) void wide_distribute_bwd_kernel(
+    const float* __restrict__ g, const T* __restrict__ x, const T* __restrict__ y, const float* __restrict__ M,
+    int64_t m_stride, const float* __restrict__ h_act, int64_t h_stride, T* __restrict__ gx, T* __restrict__ gy,
+    float* __restrict__ gM, float* __restrict__ gh_act, float* __restrict__ gh_raw, int C) {
+    constexpr int NR = N + (DM ? N * N : 0);  // dh_act_i (, dM_ij)
+    __shared__ float red[(kWideThreads / kWave) * NR];
+    __shared__ float tot[NR];
+    const int64_t b = blockIdx.x;
+    float h[N], sv[NR];
+#pragma unroll
+    for (int i = 0; i < N; ++i) h[i] = h_act[b * h_stride + i];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) sv[k] = 0.f;
+    const float* mb = M + b * m_stride;
+    const float* gb = g + b * (int64_t)N * C;
+    const T* xb = x + b * (int64_t)N * C;
+    T* dxb = gx + b * (int64_t)N * C;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        float gv[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) gv[i] = ld_elem_nt(gb + (int64_t)i * C + c);
+        const float yv = ld_elem_nt(y + b * C + c);
+        float dy = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            sv[i] += gv[i] * yv;
+            dy += h[i] * gv[i];
+        }
+        st_elem_nt(gy + b * C + c, dy);
+        if constexpr (DM) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                const float xj = ld_elem_nt(xb + (int64_t)j * C + c);
+#pragma unroll
+                for (int i = 0; i < N; ++i) sv[N + i * N + j] += gv[i] * xj;
+            }
+        }
+        for (int j = 0; j < N; ++j) {
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < N; ++i) t += mb[i * N + j] * gv[i];
+            st_elem_nt(dxb + (int64_t)j * C + c, t);
+        }
+    }
+    wide_block_total<NR>(sv, red, tot);
+    for (int t = threadIdx.x; t < NR; t += blockDim.x) {
+        if (t < N) {
+            const float hi = h_act[b * h_stride + t];
+            if (gh_act) gh_act[b * N + t] = tot[t];
+            if (gh_raw) gh_raw[b * N + t] = tot[t] * hi * (1.f - 0.5f * hi);
+        } else {
+            gM[b * N * N + (t - N)] = tot[t];
+        }
     }
 }
 
@@ -433,10 +650,10 @@ hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const v
 #define MHC_GRAM(TX_, M_)                                                                                         \
     if (n == 16) {                                                                                                \
         hipLaunchKernelGGL((stream_gram_kernel<TX_, 16, M_>), ggrid, dim3(gram_threads<16>()), 0, s, g,            \
-                           (const TX_*)x, scal_out, B, Ci);                                                       \
+                           (const TX_*)x, scal_out, B, Ci, (int64_t)(16 * 16 + 2 * 16 + 2));                      \
     } else {                                                                                                      \
         hipLaunchKernelGGL((stream_gram_kernel<TX_, 32, M_>), ggrid, dim3(gram_threads<32>()), 0, s, g,            \
-                           (const TX_*)x, scal_out, B, Ci);                                                       \
+                           (const TX_*)x, scal_out, B, Ci, (int64_t)(32 * 32 + 2 * 32 + 2));                      \
     }
     const int tg = timing_begin("stream_gram", s);
     if (x_dtype == kBF16) {
@@ -446,6 +663,124 @@ hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const v
     }
 #undef MHC_GRAM
     timing_end(tg, s);
+    return hipGetLastError();
+}
+
+#define MHC_WIDE_OPS_N(n, ...)                                    \
+    switch (n) {                                                  \
+        case 1: { constexpr int N_ = 1; __VA_ARGS__; break; }     \
+        case 2: { constexpr int N_ = 2; __VA_ARGS__; break; }     \
+        case 4: { constexpr int N_ = 4; __VA_ARGS__; break; }     \
+        case 8: { constexpr int N_ = 8; __VA_ARGS__; break; }     \
+        case 16: { constexpr int N_ = 16; __VA_ARGS__; break; }   \
+        case 32: { constexpr int N_ = 32; __VA_ARGS__; break; }   \
+        default: return hipErrorInvalidValue;                     \
+    }
+#define MHC_WIDE_T(dt, ...)                                       \
+    if (dt == kBF16) {                                            \
+        using T_ = bf16_t;                                        \
+        __VA_ARGS__;                                              \
+    } else {                                                      \
+        using T_ = float;                                         \
+        __VA_ARGS__;                                              \
+    }
+
+static bool grid_ok(int64_t B) { return B > 0 && B <= 0x7fffffff; }
+
+hipError_t launch_wide_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, float* rms, int64_t B, int64_t C,
+                                   float eps, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
+    MHC_WIDE_T(dt, hipLaunchKernelGGL((wide_rmsnorm_fwd_kernel<T_>), dim3((unsigned)B), dim3(kWideThreads), 0, s,
+                                      (const T_*)x, w, (T_*)y, rms, (int)C, eps));
+    return hipGetLastError();
+}
+
+int wide_rmsnorm_bwd_grid(int dt, int64_t B, int64_t C) {
+    if (B <= 0 || C < 1 || C > kWideMaxC) return 1;
+    const void* fn = dt == kBF16 ? reinterpret_cast<const void*>(&wide_rmsnorm_bwd_kernel<bf16_t>)
+                                 : reinterpret_cast<const void*>(&wide_rmsnorm_bwd_kernel<float>);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWideThreads, (size_t)C * sizeof(float)) !=
+            hipSuccess ||
+        per_cu < 1) {
+        (void)hipGetLastError();
+        per_cu = 1;
+    }
+    int64_t grid = (int64_t)device_cu_count() * per_cu;
+    if (grid > B) grid = B;
+    return (int)(grid < 1 ? 1 : grid);
+}
+
+hipError_t launch_wide_rmsnorm_bwd(int dt, const void* g, const void* x, const float* w, const float* rms, void* gx,
+                                   float* dw_part, int grid, int64_t B, int64_t C, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (grid < 1 || C < 1 || C > kWideMaxC) return hipErrorInvalidValue;
+    MHC_WIDE_T(dt, hipLaunchKernelGGL((wide_rmsnorm_bwd_kernel<T_>), dim3(grid), dim3(kWideThreads),
+                                      (size_t)C * sizeof(float), s, (const T_*)g, (const T_*)x, w, rms, (T_*)gx,
+                                      dw_part, B, (int)C));
+    return hipGetLastError();
+}
+
+hipError_t launch_wide_compute_rms(int dt, const void* x, float* rms, int64_t B, int64_t K, float eps,
+                                   hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!grid_ok(B) || K < 1) return hipErrorInvalidValue;
+    MHC_WIDE_T(dt, hipLaunchKernelGGL((wide_compute_rms_kernel<T_>), dim3((unsigned)B), dim3(kWideThreads), 0, s,
+                                      (const T_*)x, rms, K, eps));
+    return hipGetLastError();
+}
+
+hipError_t launch_wide_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out,
+                                     float* h_act, int64_t B, int64_t C, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_aggregate_fwd_kernel<T_, N_>), dim3((unsigned)B),
+                                                        dim3(kWideThreads), 0, s, (const T_*)x, H, hs, (T_*)out,
+                                                        h_act, (int)C)));
+    return hipGetLastError();
+}
+
+hipError_t launch_wide_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
+                                     void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_aggregate_bwd_kernel<T_, N_>), dim3((unsigned)B),
+                                                        dim3(kWideThreads), 0, s, (const T_*)g, (const T_*)x, h_act,
+                                                        hs, (T_*)gx, gh_act, gh_raw, (int)C)));
+    return hipGetLastError();
+}
+
+hipError_t launch_wide_distribute_fwd(int dt, int n, const void* y, const float* H, int64_t hs, const float* M,
+                                      int64_t ms, const void* x, float* out, float* h_act, int64_t B, int64_t C,
+                                      hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_distribute_fwd_kernel<T_, N_>), dim3((unsigned)B),
+                                                        dim3(kWideThreads), 0, s, (const T_*)y, H, hs, M, ms,
+                                                        (const T_*)x, out, h_act, (int)C)));
+    return hipGetLastError();
+}
+
+hipError_t launch_wide_distribute_bwd(int dt, int n, const float* g, const void* x, const void* y, const float* M,
+                                      int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
+                                      float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_distribute_bwd_kernel<T_, N_, (N_ <= 8)>),
+                                                        dim3((unsigned)B), dim3(kWideThreads), 0, s, g,
+                                                        (const T_*)x, (const T_*)y, M, ms, h_act, hs, (T_*)gx,
+                                                        (T_*)gy, gM, gh_act, gh_raw, (int)C)));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || n <= 8) return e;
+    const dim3 ggrid((unsigned)(B < 65536 ? B : 65536));
+    MHC_WIDE_T(dt, if (n == 16) {
+        hipLaunchKernelGGL((stream_gram_kernel<T_, 16, 1>), ggrid, dim3(gram_threads<16>()), 0, s, g, (const T_*)x,
+                           gM, B, (int)C, (int64_t)(16 * 16));
+    } else {
+        hipLaunchKernelGGL((stream_gram_kernel<T_, 32, 1>), ggrid, dim3(gram_threads<32>()), 0, s, g, (const T_*)x,
+                           gM, B, (int)C, (int64_t)(32 * 32));
+    });
     return hipGetLastError();
 }
 

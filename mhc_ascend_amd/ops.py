@@ -309,15 +309,17 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
     """Fused MHCResidualWrapper on residual / branch_output [tokens, C] for the
     parameters of ``layer`` (an MHCLayer); returns fp32 [tokens, C]."""
     n = layer.expansion_rate
-    if n != 4:
-        # The fused wrapper kernels are compiled for n = 4.  Other n build the
-        # n streams with device tensor ops, as layer.py:299-310 does, and run
-        # the fused layer on them (layer.py:313-316).
+    C = residual.shape[-1]
+    # The fused wrapper kernels take n = 4 and 4-channel rows (32-channel
+    # with dynamic H) up to 16384 channels.  Other shapes build the n streams
+    # with device tensor ops, as layer.py:299-310 does, and run the layer on
+    # them (layer.py:313-316).
+    fused = n == 4 and C % 4 == 0 and C <= 16384 and (not layer.use_dynamic_h or C % 32 == 0)
+    if not fused:
         if n < 2:
             raise RuntimeError("mhc_residual_wrapper: expansion_rate must be >= 2 (stream 1 holds the branch)")
         if residual_mode not in ("zero", "decay"):
             raise ValueError(f"Unknown residual_mode: {residual_mode}")
-        C = residual.shape[-1]
         X = torch.zeros(residual.shape[0], n, C, device=residual.device, dtype=residual.dtype)
         X[:, 0] = residual
         X[:, 1] = branch_output

@@ -44,8 +44,10 @@ def _check_grad(got, ref, dtype, what, frac=1e-5):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,C", [(1, 64), (37, 256), (130, 4096), (9, 7168)])
+@pytest.mark.parametrize("B,C", [(1, 64), (37, 256), (130, 4096), (9, 7168), (5, 1001), (3, 13), (4, 4100)])
 def test_rmsnorm(device, dtype, B, C):
+    """Includes rows that are not a multiple of the 16-byte vector (1001, 13;
+    4100 for bf16), which run the channel-loop kernels."""
     g = _gen(B + C)
     x = torch.randn(B, C, generator=g).to(dtype)
     w = 1 + 0.1 * torch.randn(C, generator=g)
@@ -78,11 +80,12 @@ def test_rmsnorm_config_c2(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_compute_rms(device, dtype):
+@pytest.mark.parametrize("K", [4 * 1024, 4 * 1001 + 3])
+def test_compute_rms(device, dtype, K):
     g = _gen(3)
-    x = torch.randn(50, 4 * 1024, generator=g).to(dtype)
+    x = torch.randn(50, K, generator=g).to(dtype)
     got = mhc.compute_rms(x.to(device), 1e-8)
-    assert_close(got, R.compute_rms(x.double(), 1e-8), 1e-5, 0, "compute_rms")
+    assert_close(got, R.compute_rms(x.double(), 1e-8), 1e-5, 0, f"compute_rms K={K}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -107,12 +110,15 @@ def test_stream_aggregate(device, dtype, shared, B, C):
                  "aggregate dH")
 
 
-@pytest.mark.parametrize("n", [1, 2, 8])
+@pytest.mark.parametrize("n,C", [(1, 256), (2, 256), (8, 64), (16, 256), (32, 320), (1, 3), (4, 77), (8, 1001),
+                                 (32, 50)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_stream_ops_general_n(device, n, dtype):
-    """stream_aggregate and stream_distribute_mix_add at n = 1, 2, 8 (the
-    distribute backward's n*n + n row sums need >= 72 lanes at n = 8)."""
-    B, C = 9, 64 if n == 8 else 256
+def test_stream_ops_general_n(device, n, C, dtype):
+    """stream_aggregate and stream_distribute_mix_add at n = 1 .. 32 and
+    rows that are not a multiple of the vector (the distribute backward's
+    n*n + n row sums need >= 72 lanes at n = 8; dM comes from the per-token
+    Gram kernel at n >= 16)."""
+    B = 9
     g = _gen(100 + n)
     x = torch.randn(B, n, C, generator=g).to(dtype)
     H = torch.randn(B, n, generator=g)
@@ -125,6 +131,8 @@ def test_stream_ops_general_n(device, n, dtype):
     ref.backward(go.double())
     _check_out(out, ref.detach(), dtype, f"n={n} aggregate out")
     _check_grad(xd.grad, xr.grad, dtype, f"n={n} aggregate dx")
+    assert_close(Hd.grad, Hr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Hr.grad, 1e-4),
+                 f"n={n} aggregate dH")
 
     y = torch.randn(B, C, generator=g).to(dtype)
     Hq = torch.randn(B, n, generator=g)
@@ -142,6 +150,8 @@ def test_stream_ops_general_n(device, n, dtype):
     _check_grad(yd.grad, yr.grad, dtype, f"n={n} distribute dy")
     assert_close(Md.grad, Mr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Mr.grad, 1e-4),
                  f"n={n} distribute dM")
+    assert_close(Hd.grad, Hr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Hr.grad, 1e-4),
+                 f"n={n} distribute dH")
 
 
 def test_stream_aggregate_config_c2(device):

@@ -134,12 +134,13 @@ def test_wrapper_config_c5_width(device, dynamic):
     _check(got, want, torch.bfloat16, DYN if dynamic else STA, f"C5 width dyn={dynamic}")
 
 
-@pytest.mark.parametrize("n,dynamic", [(2, False), (8, False), (2, True)])
+@pytest.mark.parametrize("n,dynamic,C", [(2, False, 256), (8, False, 256), (2, True, 256), (8, True, 128),
+                                         (32, False, 64), (32, True, 64), (4, False, 250)])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
-def test_wrapper_general_n(device, n, dynamic, mode):
-    """Expansion rates other than 4: the streams are built with device tensor
-    ops and run through the fused layer (the wrapper kernels are n = 4)."""
-    C = 256
+def test_wrapper_general_n(device, n, dynamic, C, mode):
+    """Shapes the fused wrapper kernels do not take (n != 4, or rows that
+    are not a multiple of 4): the streams are built with device tensor ops
+    and run through the layer."""
     torch.manual_seed(n)
     wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=dynamic)
     wrap.residual_mode = mode
