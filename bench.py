@@ -1,6 +1,7 @@
 """Benchmark of the mHC layer forward+backward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload static|dynamic|infer|wrapper|ops]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload static|dynamic|infer|infer_bf16|wrapper|ops] [--paper-configs]
 
 Prints ONE JSON line: tokens/s of the whole fwd+bwd step, the achieved HBM
 GB/s from algorithmic bytes, the roofline of the dominant kernel (HIP-event
@@ -11,11 +12,13 @@ a bounded token sample).
 Workloads (the metric is quoted at n=4, C=4096):
   static  - C3: MHCLayer static-H, x fp32 [8192, 4, 4096]          (default)
   dynamic - C4: MHCLayer dynamic-H, x bf16 [8192, 4, 4096], phi [16384, 24]
-  infer   - C4 shape forward only (eval, no_grad, parameters packed once);
-            --out-dtype f32 (the reference's output) or bf16
+  infer   - C4 shape forward only (eval, no_grad, parameters packed once),
+            fp32 output as the reference; infer_bf16 the same with bf16 output
   wrapper - C5: MHCResidualWrapper, residual/branch bf16 [65536, 4, 7168]
   ops     - C2: standalone sinkhorn_knopp / rmsnorm / stream_aggregate fwd+bwd
             (value = the step's achieved HBM GB/s)
+--paper-configs runs the reference's 9-configuration sweep (benchmark.py:
+299-311) instead, static and dynamic H, and prints per-configuration ms.
 Inputs are synthetic (seeded N(0,1)) and already resident in HBM; each step
 uses the next of several rotating input sets (together well above the
 256 MB MALL) so no step reads the previous step's data from cache.
@@ -225,7 +228,7 @@ class InferWorkload(DynamicWorkload):
     """C4 shape, forward only: the dynamic-H MHCLayer in eval mode under
     no_grad (the inference path of ops.py:337-380), its weight and
     projections packed once (MHCLayer.prepare_inference), output fp32 as the
-    reference or bf16 (--out-dtype)."""
+    reference (workload infer) or bf16 (workload infer_bf16)."""
 
     name = "infer"
     metric = "mHC dynamic-H layer forward-only (inference) tokens/sec (C4 shape, n=4, C=4096)"
@@ -279,6 +282,14 @@ class InferWorkload(DynamicWorkload):
         med, runs = _timed_cpu(run, seconds)
         return sample / med, (f"oracle.reference.mhc_layer_dynamic fp32 forward (no_grad) on {sample} of "
                               f"{self.B} tokens, n={self.n}, C={self.C}; median of {runs} runs")
+
+
+class InferBF16Workload(InferWorkload):
+    """The forward-only C4 workload with its output written in bf16."""
+
+    name = "infer_bf16"
+    metric = "mHC dynamic-H layer forward-only (inference, bf16 output) tokens/sec (C4 shape, n=4, C=4096)"
+    out_dtype = "bf16"
 
 
 class WrapperWorkload:
@@ -463,13 +474,67 @@ class OpsWorkload:
 
 
 WORKLOADS = {"static": StaticWorkload, "dynamic": DynamicWorkload, "infer": InferWorkload,
-             "wrapper": WrapperWorkload, "ops": OpsWorkload}
+             "infer_bf16": InferBF16Workload, "wrapper": WrapperWorkload, "ops": OpsWorkload}
 KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "wrap_proj", "wrap_fwd", "wrap_bwd",
            "wrap_bwd_reduce", "wrap_proj_bwd", "sinkhorn_fwd", "sinkhorn_bwd", "rmsnorm_fwd", "rmsnorm_bwd",
            "aggregate_fwd", "aggregate_bwd")
 
 
 # ---------------------------------------------------------------------------
+# The reference's configuration sweep (benchmark.py:299-311, protocol of
+# benchmark.py:175-269): per (B, C, n), static and dynamic H, the forward in
+# eval mode under no_grad and forward + backward of out.sum() in train mode,
+# fp32 x drawn fresh per run, caches flushed before each run, events around
+# the call, 10% trimmed mean.
+# ---------------------------------------------------------------------------
+PAPER_CONFIGS = [(320, 1280, 4), (512, 1920, 4), (1280, 2560, 4), (2560, 1280, 4), (128, 1280, 8), (256, 1280, 8),
+                 (32, 1280, 32), (64, 1280, 32), (128, 1280, 32)]
+
+
+def paper_sweep(torch, mhc, device, warmup=10, runs=100):
+    flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=device)
+
+    def timed(fn, B, n, C, train):
+        times = []
+        for it in range(warmup + runs):
+            x = torch.randn(B, n, C, device=device, requires_grad=train)
+            flush.zero_()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            fn(x)
+            t1.record()
+            torch.cuda.synchronize()
+            if it >= warmup:
+                times.append(t0.elapsed_time(t1))
+        times.sort()
+        trim = runs // 10
+        times = times[trim:len(times) - trim] if trim else times
+        return sum(times) / len(times)
+
+    rows = []
+    for dynamic in (False, True):
+        for B, C, n in PAPER_CONFIGS:
+            torch.manual_seed(0)
+            layer = mhc.MHCLayer(C, n, use_dynamic_h=dynamic).to(device)
+
+            def fwd(x):
+                with torch.no_grad():
+                    layer(x)
+
+            def fwd_bwd(x):
+                layer(x).sum().backward()
+
+            layer.eval()
+            f_ms = timed(fwd, B, n, C, False)
+            layer.train()
+            fb_ms = timed(fwd_bwd, B, n, C, True)
+            rows.append({"dynamic_h": dynamic, "B": B, "C": C, "n": n, "fwd_ms": f_ms, "fwd_bwd_ms": fb_ms})
+            print(f"[bench] paper {'dynamic' if dynamic else 'static '} B={B:5d} C={C:5d} n={n:3d} "
+                  f"fwd {f_ms:8.4f} ms  fwd+bwd {fb_ms:8.4f} ms", file=sys.stderr, flush=True)
+            del layer
+    return rows
+
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -477,10 +542,11 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 50; 10 for wrapper)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="static")
-    ap.add_argument("--out-dtype", choices=("f32", "bf16"), default="f32",
-                    help="infer workload: output dtype (f32 as the reference, or bf16)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bounded CPU-baseline sample time (0 disables)")
+    ap.add_argument("--paper-configs", action="store_true",
+                    help="instead of a workload: the reference's 9-configuration sweep (benchmark.py:299-311), "
+                         "static and dynamic H, forward and forward+backward ms per configuration")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 1 GiB device copy (known bytes) for PMC counter calibration")
     a = ap.parse_args(argv)
@@ -500,7 +566,20 @@ def main(argv=None) -> int:
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    InferWorkload.out_dtype = a.out_dtype
+    if a.paper_configs:
+        rows = paper_sweep(torch, mhc, device)
+        geo = 1.0
+        for r in rows:
+            geo *= r["fwd_bwd_ms"]
+        geo **= 1.0 / len(rows)
+        print(json.dumps({"metric": "mHC layer ms per paper configuration (benchmark.py:301-311 protocol)",
+                          "value": geo, "unit": "ms (geometric mean of fwd+bwd over the 18 rows)", "n_gpus": 1,
+                          "higher_is_better": False, "vs_baseline": None, "dtype": "f32",
+                          "data": "synthetic N(0,1) fp32 x, fresh per run; 512 MB cache flush before each run",
+                          "config": {"workload": "paper configuration sweep", "warmup": 10, "runs": 100,
+                                     "trimmed": "10% each end"},
+                          "rows": rows}), flush=True)
+        return 0
     wl = WORKLOADS[a.workload](torch, mhc, device)
 
     print(f"[bench] workload={wl.name} warmup={a.warmup} steps={steps}", file=sys.stderr, flush=True)
