@@ -240,7 +240,7 @@ int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const void* weight, int
 
 struct StaticBwdWs {
     int grid;
-    size_t dw_off, scal_off, stage_off, total;
+    size_t dw_off, scal_off, stage_off, hist_off, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -251,7 +251,8 @@ static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32
     w.dw_off = 0;
     w.scal_off = align256((size_t)w.grid * hidden * sizeof(float));
     w.stage_off = w.scal_off + align256((size_t)w.grid * (n * n + 2 * n) * sizeof(float));
-    w.total = w.stage_off + align256(column_sums_stage_floats(hidden) * sizeof(float));
+    w.hist_off = w.stage_off + align256(column_sums_stage_floats(hidden) * sizeof(float));
+    w.total = w.hist_off + (n >= 16 ? kStaticSkHistBytes : 0);  // Sinkhorn adjoint history (wide n)
     return w;
 }
 
@@ -292,7 +293,8 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
     }
     if (e == hipSuccess)
         e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stage, grad_weight, scal_part, rows, h_pre,
-                                  h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
+                                  h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s,
+                                  n >= 16 ? (float*)((char*)workspace + w.hist_off) : nullptr);
     return hip_status(e);
 }
 
@@ -454,7 +456,7 @@ static size_t phi_planes_bytes(int64_t k, int np) { return align256((size_t)proj
 
 static ProjFwdWs proj_fwd_ws(int64_t batch, int64_t k, int np) {
     ProjFwdWs w{};
-    w.ks = batch > 0 ? proj_ksplit(batch, k) : 1;
+    w.ks = batch > 0 ? proj_ksplit(batch, k, np) : 1;
     w.phib_off = 0;
     w.p_off = phi_planes_bytes(k, np);
     w.ss_off = w.p_off + align256((size_t)proj_tiles(np) * w.ks * batch * kProjTile * sizeof(float));
@@ -718,7 +720,7 @@ static bool dyn_bwd_f32_acc(int32_t n, int32_t x_dtype) { return x_dtype == kBF1
 struct DynBwdWs {
     int grid, cblocks, tiles;
     int wdt;  // element type the row and projection kernels run on
-    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, total;
+    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, hist_off, total;
 };
 
 static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
@@ -741,6 +743,7 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     const size_t acc = w.wdt != x_dtype ? (size_t)batch * K * 4 : 0;
     w.xw_off = o; o += align256(acc);
     w.dxw_off = o; o += align256(acc);
+    w.hist_off = o; o += n >= 16 && batch > 0 ? kSkHistBytes : 0;  // Sinkhorn adjoint history
     w.total = o;
     return w;
 }
@@ -768,6 +771,9 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     const DynBwdWs w = dyn_bwd_ws(batch, n, hidden, x_dtype);
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "layer_dynamic_bwd: workspace smaller than mhc_layer_dynamic_bwd_workspace_size()");
+    if (n >= 16 && batch > 0 && dyn_coef_bwd_hist_slots(n, batch, num_iters) < 1)
+        return fail(MHC_ERR_UNSUPPORTED, "layer_dynamic_bwd: num_iters too large for the Sinkhorn history at n=" +
+                                             std::to_string(n));
     hipStream_t s = (hipStream_t)stream;
     char* ws = (char*)workspace;
     float* dw_part = (float*)(ws + w.dw_off);
@@ -801,7 +807,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
-                                    s);
+                                    n >= 16 ? (float*)(ws + w.hist_off) : nullptr, s);
     }
     if (e == hipSuccess)
         e = proj_bwd_all(w.wdt, xk, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, np, dxk, true, phip,
@@ -979,7 +985,7 @@ int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const v
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
-                                    s);
+                                    nullptr, s);
         if (e == hipSuccess)
             e = launch_wrap_proj_bwd(dtype, n, decay, residual, branch, dp, stok, phi_pre, phi_post, phi_res,
                                      grad_residual, grad_branch, phip, w.tiles, tokens, hidden, s);

@@ -104,8 +104,8 @@ __global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict_
 // bf16: P = x.(hi + mid + lo) (3 MFMAs per tile); fp32 x is split the same
 // way and the six products down to 2^-16 relative weight are kept
 // (xh.(hi+mid+lo) + xm.(hi+mid) + xl.hi), leaving terms of order 2^-24.
-// Also sum x^2.  p_part[ks][B][32], ss_part[ks][B] (null: not stored; one
-// launch per 32-row output tile of Phi, all but the first without it).
+// Also sum x^2.  blockIdx.z is the 32-row output tile of Phi: partials
+// p_part[tile][ks][B][32]; tile 0 also stores ss_part[ks][B].
 // Pipeline: x of stage s+2 and Phi of stage s+2 are in flight while stage s
 // is on the matrix cores; one barrier per stage.
 // ---------------------------------------------------------------------------
@@ -156,7 +156,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     // rows of this block past the batch read zeros (resource range)
     const int64_t rows = (B - tok0 < TB) ? B - tok0 : TB;
     const buf_rsrc_t xrs = make_buf_rsrc(x + tok0 * K, (uint32_t)(rows * K * (int64_t)sizeof(TX)));
-    const buf_rsrc_t prs = make_buf_rsrc(phif, (uint32_t)(6 * ksteps * 64 * 16));
+    const int64_t otile = blockIdx.z;
+    const buf_rsrc_t prs = make_buf_rsrc(phif + otile * 6 * ksteps * 64, (uint32_t)(6 * ksteps * 64 * 16));
     const int lrow = threadIdx.x / VPR;
     const int lvec = threadIdx.x % VPR;
     const uint32_t xoff = (uint32_t)(((int64_t)lrow * K + lvec * EPV) * (int64_t)sizeof(TX));
@@ -307,7 +308,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
             ss[mt] += red[q][8 * MT + mt][lane];
         }
     }
-    float* pp = p_part + ksplit * B * kNPad;
+    float* pp = p_part + (otile * gridDim.y + ksplit) * B * kNPad;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -323,7 +324,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         s2 += __shfl_xor(s2, 16, kWave);
         s2 += __shfl_xor(s2, 32, kWave);
         const int64_t tok = tok0 + mt * 16 + row;
-        if (kg == 0 && tok < B && ss_part) ss_part[ksplit * B + tok] = s2;
+        if (kg == 0 && tok < B && otile == 0) ss_part[ksplit * B + tok] = s2;
     }
 }
 
@@ -498,66 +499,75 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
 // The same for n >= 16, one token per group of n lanes: the db / dalpha
 // terms (np + 3 values, too many to block-sum in registers) are written per
 // token to part[b][np + 3] and column-summed over the tokens afterwards.
-// The Sinkhorn adjoint recomputes each iteration (no register history).
+// The Sinkhorn adjoint keeps its per-iteration state in hist (one slot of
+// iters * (n + 1) * n floats per lane group); the groups stride over the
+// tokens with a trip count that is the same for every lane of the grid.
 // ---------------------------------------------------------------------------
 template <int N>
 __global__ __launch_bounds__(256) void dyn_coef_bwd_wide_kernel(
     const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
     const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
     const float* __restrict__ a_post, const float* __restrict__ a_res, const float* __restrict__ b_res,
-    float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int iters, float sk_eps) {
+    float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int iters, float sk_eps,
+    float* __restrict__ hist) {
     constexpr int NP = 2 * N + N * N;
     constexpr int NS = N * N + 2 * N;
     constexpr int NV = NP + 3;
     constexpr int NPT = dp_stride(NP);
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t tok = gid / N;
+    const int64_t slot = gid / N;
+    const int64_t slots = (int64_t)gridDim.x * blockDim.x / N;
     const int r = (int)(gid % N);
-    const bool tv = tok < B;
-    const int64_t tk = tv ? tok : 0;
-    const float* sc = scal + tk * (NS + 2);
-    const float* cf = coef + tk * NP;
-    const float* pv = p + tk * NP;
+    float* hs = hist + slot * (int64_t)iters * (N + 1) * N;
     const float ap = a_pre[0], aq = a_post[0], ar = a_res[0];
-    const float inv = 1.f / rh[tk];
+    for (int64_t base = 0; base < B; base += slots) {
+        const int64_t tok = base + slot;
+        const bool tv = tok < B;
+        const int64_t tk = tv ? tok : 0;
+        const float* sc = scal + tk * (NS + 2);
+        const float* cf = coef + tk * NP;
+        const float* pv = p + tk * NP;
+        const float inv = 1.f / rh[tk];
 
-    float gm[N], e[N], pr[N];
+        float gm[N], e[N], pr[N];
 #pragma unroll
-    for (int c = 0; c < N; ++c) {
-        gm[c] = tv ? sc[r * N + c] : 0.f;
-        pr[c] = pv[2 * N + r * N + c];
-        e[c] = tv ? expf(pr[c] * ar * inv + b_res[r * N + c]) : 0.f;
-    }
-    sk_backward<N>(gm, e, iters, sk_eps, tv);
-    const float hp = cf[r], hq = cf[N + r];
-    const float dt_pre = tv ? sc[N * N + N + r] * hp * (1.f - hp) : 0.f;
-    const float dt_post = tv ? sc[N * N + r] * hq * (1.f - 0.5f * hq) : 0.f;
-    float lp = 0.f;
+        for (int c = 0; c < N; ++c) {
+            gm[c] = tv ? sc[r * N + c] : 0.f;
+            pr[c] = pv[2 * N + r * N + c];
+            e[c] = tv ? expf(pr[c] * ar * inv + b_res[r * N + c]) : 0.f;
+        }
+        sk_backward_mem<N>(gm, e, iters, sk_eps, tv, hs, r);
+        const float hp = cf[r], hq = cf[N + r];
+        const float dt_pre = tv ? sc[N * N + N + r] * hp * (1.f - hp) : 0.f;
+        const float dt_post = tv ? sc[N * N + r] * hq * (1.f - 0.5f * hq) : 0.f;
+        float lp = 0.f;
 #pragma unroll
-    for (int c = 0; c < N; ++c) {
-        gm[c] = tv ? gm[c] * e[c] : 0.f;  // dt_res row r
-        lp += gm[c] * pr[c];
-    }
-    const float l_pre = dt_pre * pv[r], l_post = dt_post * pv[N + r];
-    const float tot = group_sum<N>(ap * l_pre + aq * l_post + ar * lp);
-    const float s_pre = group_sum<N>(l_pre), s_post = group_sum<N>(l_post), s_res = group_sum<N>(lp);
-    if (!tv) return;
-    float* dp = dp_out + tok * NPT;
-    dp[r] = ap * dt_pre * inv;
-    dp[N + r] = aq * dt_post * inv;
+        for (int c = 0; c < N; ++c) {
+            gm[c] = tv ? gm[c] * e[c] : 0.f;  // dt_res row r
+            lp += gm[c] * pr[c];
+        }
+        const float l_pre = dt_pre * pv[r], l_post = dt_post * pv[N + r];
+        const float tot = group_sum<N>(ap * l_pre + aq * l_post + ar * lp);
+        const float s_pre = group_sum<N>(l_pre), s_post = group_sum<N>(l_post), s_res = group_sum<N>(lp);
+        if (tv) {
+            float* dp = dp_out + tok * NPT;
+            dp[r] = ap * dt_pre * inv;
+            dp[N + r] = aq * dt_post * inv;
 #pragma unroll
-    for (int c = 0; c < N; ++c) dp[2 * N + r * N + c] = ar * gm[c] * inv;
-    float* pt = part + tok * NV;
-    pt[r] = dt_pre;
-    pt[N + r] = dt_post;
+            for (int c = 0; c < N; ++c) dp[2 * N + r * N + c] = ar * gm[c] * inv;
+            float* pt = part + tok * NV;
+            pt[r] = dt_pre;
+            pt[N + r] = dt_post;
 #pragma unroll
-    for (int c = 0; c < N; ++c) pt[2 * N + r * N + c] = gm[c];
-    if (r == 0) {
-        for (int o = NP; o < NPT; ++o) dp[o] = 0.f;
-        s_out[tok] = -tot * inv * inv * inv / (float)K;
-        pt[NP] = s_pre * inv;
-        pt[NP + 1] = s_post * inv;
-        pt[NP + 2] = s_res * inv;
+            for (int c = 0; c < N; ++c) pt[2 * N + r * N + c] = gm[c];
+            if (r == 0) {
+                for (int o = NP; o < NPT; ++o) dp[o] = 0.f;
+                s_out[tok] = -tot * inv * inv * inv / (float)K;
+                pt[NP] = s_pre * inv;
+                pt[NP + 1] = s_post * inv;
+                pt[NP + 2] = s_res * inv;
+            }
+        }
     }
 }
 
@@ -697,16 +707,16 @@ __global__ __launch_bounds__(256) void dyn_coef16_bwd_kernel(
     }
 }
 
-// out[c] = sum_r part[r][c] for a few columns (db, dalpha); one workgroup of
-// 32 columns x 32 row phases, each phase summing every 32nd row in order and
-// the phases added in order (deterministic).
+// out[c] = sum_r part[r][c] for a few columns (db, dalpha); one workgroup
+// per 32 columns, as 32 columns x 32 row phases, each phase summing every
+// 32nd row in order and the phases added in order (deterministic).
 __global__ __launch_bounds__(1024) void small_column_sum_kernel(const float* __restrict__ part, int rows, int cols,
                                                                 float* __restrict__ out_db, float* __restrict__ out_da,
                                                                 int np) {
     __shared__ float red[32][33];
     const int cl = threadIdx.x & 31;
     const int ph = threadIdx.x >> 5;
-    for (int c0 = 0; c0 < cols; c0 += 32) {
+    for (int c0 = blockIdx.x * 32; c0 < cols; c0 += gridDim.x * 32) {
         const int col = c0 + cl;
         float s = 0.f;
         if (col < cols) {
@@ -1051,9 +1061,11 @@ hipError_t launch_phi_split(const float* pre, const float* post, const float* re
     return hipGetLastError();
 }
 
-int proj_ksplit(int64_t B, int64_t K) {
-    const int64_t mblocks = (B + 127) / 128;
-    int64_t ks = (2 * (int64_t)device_cu_count() + mblocks - 1) / mblocks;
+// K splits so that token blocks x splits x output tiles fill about two
+// workgroups per CU, at least 256 columns per split.
+int proj_ksplit(int64_t B, int64_t K, int np) {
+    const int64_t blocks = ((B + 127) / 128) * proj_tiles(np);
+    int64_t ks = (2 * (int64_t)device_cu_count() + blocks - 1) / blocks;
     const int64_t kmax = (K + 2 * kProjKS - 1) / (2 * kProjKS);
     if (ks > kmax) ks = kmax;
     if (ks < 1) ks = 1;
@@ -1067,28 +1079,23 @@ hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_t* phib, int 
     if (K % 32 != 0 || K > (int64_t(1) << 22) || np < 1) return hipErrorInvalidValue;
     int64_t kchunk = (K + ks - 1) / ks;
     kchunk = ((kchunk + kProjKS - 1) / kProjKS) * kProjKS;
-    // one launch per 32-row output tile; the first also stores sum x^2
-    for (int t = 0; t < proj_tiles(np); ++t) {
-        const uint4* phif = reinterpret_cast<const uint4*>(phib) + (int64_t)t * 6 * (K / 32) * 64;
-        float* pp = p_part + (int64_t)t * ks * B * kNPad;
-        float* ssp = t == 0 ? ss_part : nullptr;
-        const int tok = timing_begin("proj", s);
-        if (x_dtype == kBF16) {
-            constexpr int MT = proj_mt<bf16_t>();
-            const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
-            hipLaunchKernelGGL((proj_mfma_kernel<bf16_t, MT>), grid, dim3(256), 0, s, (const bf16_t*)x, phif, pp, ssp,
-                               B, K, kchunk);
-        } else {
-            constexpr int MT = proj_mt<float>();
-            const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks);
-            hipLaunchKernelGGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, pp, ssp,
-                               B, K, kchunk);
-        }
-        timing_end(tok, s);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+    // grid z = the 32-row output tiles of Phi (tile 0 also stores sum x^2)
+    const unsigned tiles = (unsigned)proj_tiles(np);
+    const uint4* phif = reinterpret_cast<const uint4*>(phib);
+    const int tok = timing_begin("proj", s);
+    if (x_dtype == kBF16) {
+        constexpr int MT = proj_mt<bf16_t>();
+        const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks, tiles);
+        hipLaunchKernelGGL((proj_mfma_kernel<bf16_t, MT>), grid, dim3(256), 0, s, (const bf16_t*)x, phif, p_part,
+                           ss_part, B, K, kchunk);
+    } else {
+        constexpr int MT = proj_mt<float>();
+        const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks, tiles);
+        hipLaunchKernelGGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, p_part,
+                           ss_part, B, K, kchunk);
     }
-    return hipSuccess;
+    timing_end(tok, s);
+    return hipGetLastError();
 }
 
 hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s) {
@@ -1136,10 +1143,24 @@ int dyn_coef_bwd_blocks(int n, int64_t B) {
     return (int)((B * pow2ceil(n) + 255) / 256);
 }
 
+// Lane groups (token slots) of the n >= 16 coefficient backward: a whole
+// number of 256-lane workgroups, at most one slot per token, as many as fit
+// kSkHistBytes of history; 0 if not even one workgroup's slots fit.
+int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters) {
+    if (n < 16) return 0;
+    const int per_wg = 256 / n;
+    const int64_t slot_bytes = (int64_t)(iters > 0 ? iters : 1) * (n + 1) * n * (int64_t)sizeof(float);
+    const int64_t fit_wgs = (int64_t)kSkHistBytes / slot_bytes / per_wg;
+    int64_t wgs = (B + per_wg - 1) / per_wg;
+    if (wgs > fit_wgs) wgs = fit_wgs;
+    if (wgs < 1) return fit_wgs < 1 ? 0 : per_wg;
+    return (int)(wgs * per_wg);
+}
+
 hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
-                               hipStream_t s) {
+                               float* hist, hipStream_t s) {
     if (B == 0) return hipSuccess;
     const unsigned blocks = (unsigned)dyn_coef_bwd_blocks(n, B);
     if (n == 4) {
@@ -1148,13 +1169,15 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
         return hipGetLastError();
     }
     if (n >= 16) {
-        const unsigned wblocks = (unsigned)((B * n + 255) / 256);
+        const int slots = dyn_coef_bwd_hist_slots(n, B, iters);
+        if (!hist || slots < 1) return hipErrorInvalidValue;
+        const unsigned wblocks = (unsigned)slots * n / 256;
         if (n == 16) {
             hipLaunchKernelGGL((dyn_coef_bwd_wide_kernel<16>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
-                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps, hist);
         } else if (n == 32) {
             hipLaunchKernelGGL((dyn_coef_bwd_wide_kernel<32>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
-                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps, hist);
         } else {
             return hipErrorInvalidValue;
         }
@@ -1172,7 +1195,8 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
 
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s) {
-    hipLaunchKernelGGL(small_column_sum_kernel, dim3(1), dim3(1024), 0, s, part, rows, cols, out_db, out_da, np);
+    hipLaunchKernelGGL(small_column_sum_kernel, dim3((unsigned)((cols + 31) / 32)), dim3(1024), 0, s, part, rows, cols,
+                       out_db, out_da, np);
     return hipGetLastError();
 }
 

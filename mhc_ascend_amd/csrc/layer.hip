@@ -803,14 +803,14 @@ size_t column_sums_stage_floats(int64_t cols) { return (size_t)kColSplit * (size
 hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int rows, int64_t cols, float* stage,
                                   void* dw, const float* scal_part, int scal_rows, const float* h_pre,
                                   const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                  float* d_h_res, int iters, float sk_eps, hipStream_t s) {
+                                  float* d_h_res, int iters, float sk_eps, hipStream_t s, float* sk_hist) {
     if (n > 8) {
         // the static scalar gradients of wide n have their own kernel
         hipError_t e = launch_column_finalize(0, w_dtype, part, rows, cols, stage, dw, nullptr, 0, nullptr, nullptr,
                                               nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
         if (e != hipSuccess) return e;
         return launch_wide_static_finalize(n, scal_part, scal_rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res,
-                                           iters, sk_eps, s);
+                                           iters, sk_eps, sk_hist, sk_hist ? kStaticSkHistBytes : 0, s);
     }
     if (rows <= kDirectRows)
         return launch_layer_finalize(n, w_dtype, part, rows, cols, dw, scal_part, scal_rows, h_pre, h_post, h_res,

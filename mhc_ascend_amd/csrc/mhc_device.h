@@ -423,6 +423,37 @@ __device__ __forceinline__ void sk_backward(float (&g)[N], const float (&x0)[N],
     }
 }
 
+// The same adjoint with the per-iteration state kept in memory instead of
+// registers or recomputed: O(iters) steps for N too large for a register
+// history.  Lane r of the matrix's group of G = pow2ceil(N) lanes stores
+// column c of iteration t at hist[(t * (N + 1) + c) * G + r] and the row
+// scale at c = N (iters * (N + 1) * G floats per matrix).  Each lane reads
+// back only what it wrote, so program order is the only ordering needed.
+template <int N>
+__device__ __forceinline__ void sk_backward_mem(float (&g)[N], const float (&x0)[N], int iters, float eps,
+                                                bool active, float* __restrict__ hist, int r) {
+    constexpr int G = pow2ceil(N);
+    float a[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) a[c] = x0[c];
+    for (int t = 0; t < iters; ++t) {
+        float rinv;
+        sk_row_step<N>(a, eps, active, rinv);
+        float* h = hist + (int64_t)t * (N + 1) * G + r;
+#pragma unroll
+        for (int c = 0; c < N; ++c) h[c * G] = a[c];
+        h[N * G] = rinv;
+        sk_col_step<N>(a, eps);
+    }
+    for (int t = iters - 1; t >= 0; --t) {
+        const float* h = hist + (int64_t)t * (N + 1) * G + r;
+        float A[N];
+#pragma unroll
+        for (int c = 0; c < N; ++c) A[c] = h[c * G];
+        sk_adjoint_step<N>(g, A, h[N * G], eps);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Sinkhorn-Knopp on an n x n matrix with n <= NM (NM = 16, 32 or 64) held one
 // row per lane in a group of NM lanes, for n above the exact instantiations.

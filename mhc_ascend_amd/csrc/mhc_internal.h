@@ -74,10 +74,11 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
 // gradients when n > 0: one launch when rows is small (the finalize reads the
 // partials directly), else a first pass into stage[column_sums_stage_floats].
 size_t column_sums_stage_floats(int64_t cols);
+// sk_hist (kStaticSkHistBytes, n >= 16 only): the static Sinkhorn adjoint's history.
 hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int rows, int64_t cols, float* stage,
                                   void* dw, const float* scal_part, int scal_rows, const float* h_pre,
                                   const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                  float* d_h_res, int iters, float sk_eps, hipStream_t s);
+                                  float* d_h_res, int iters, float sk_eps, hipStream_t s, float* sk_hist = nullptr);
 
 // ---- wide.hip --------------------------------------------------------------
 // Channel-loop layer kernels (any C up to kWideMaxC; n in {2, 4, 8, 16, 32}):
@@ -114,10 +115,14 @@ hipError_t launch_wide_distribute_fwd(int dt, int n, const void* y, const float*
 hipError_t launch_wide_distribute_bwd(int dt, int n, const float* g, const void* x, const void* y, const float* M,
                                       int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
                                       float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
-// Static H gradients for n >= 16 from scal_part[rows][n^2 + 2n].
+// Static H gradients for n >= 16 from scal_part[rows][n^2 + 2n]; the
+// Sinkhorn adjoint keeps its history in hist when iters * (n + 1) * n
+// floats fit hist_bytes, else recomputes it.
+constexpr size_t kStaticSkHistBytes = size_t(4) << 20;
 hipError_t launch_wide_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
                                        const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                       float* d_h_res, int iters, float sk_eps, hipStream_t s);
+                                       float* d_h_res, int iters, float sk_eps, float* hist, size_t hist_bytes,
+                                       hipStream_t s);
 
 // ---- ops.hip ---------------------------------------------------------------
 hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, float* rms, int64_t B, int64_t C,
@@ -150,7 +155,7 @@ constexpr int kMaxProjRows = 8192;
 // (3 * 32 * K bf16 each) in the projection kernel's operand order.
 hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
                             bf16_raw_t* phib, hipStream_t s);
-int proj_ksplit(int64_t B, int64_t K);
+int proj_ksplit(int64_t B, int64_t K, int np);
 // P partials of all proj_tiles(np) output tiles, tile-major:
 // p_part[tile][ks][B][32], plus ss_part[ks][B] = partial sums of x^2.
 hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_raw_t* phib, int np, float* p_part,
@@ -161,10 +166,15 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
                                const float* b_post, const float* b_res, float* coef, float* p_out, float* rh,
                                int iters, float sk_eps, float rms_eps, hipStream_t s);
 int dyn_coef_bwd_blocks(int n, int64_t B);
+// n >= 16: the Sinkhorn adjoint's per-iteration history lives in a region
+// of kSkHistBytes (hist; null for n < 16), split into token slots of
+// iters * (n + 1) * n floats; 0 slots = iters too large for the region.
+constexpr size_t kSkHistBytes = size_t(64) << 20;
+int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters);
 hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
-                               hipStream_t s);
+                               float* hist, hipStream_t s);
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s);
 // Projection backward (bf16 MFMA, split operands) over the flattened [B, K]

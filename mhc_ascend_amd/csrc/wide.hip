@@ -300,13 +300,14 @@ __global__ __launch_bounds__(gram_threads<N>()) void stream_gram_kernel(const fl
 // scal_part[rows][n^2 + 2n]: column totals in LDS, then (as layer.hip's
 // finalize) dH_pre = dh_pre_act h_pre (1 - h_pre), dH_post = dh_post_act
 // h_post (1 - h_post / 2) and dH_res = SK^T(dM) * exp(H_res), the Sinkhorn
-// adjoint one row per lane of the first wave.
+// adjoint one row per lane of the first n lanes, its per-iteration state in
+// hist (iters * (n + 1) * n floats) or, without hist, recomputed.
 // ---------------------------------------------------------------------------
 template <int N>
 __global__ __launch_bounds__(256) void wide_static_finalize_kernel(
     const float* __restrict__ scal_part, int rows, const float* __restrict__ h_pre, const float* __restrict__ h_post,
     const float* __restrict__ h_res, float* __restrict__ d_h_pre, float* __restrict__ d_h_post,
-    float* __restrict__ d_h_res, int iters, float eps) {
+    float* __restrict__ d_h_res, int iters, float eps, float* __restrict__ hist) {
     constexpr int NS = N * N + 2 * N;
     __shared__ float tot[NS];
     for (int k = threadIdx.x; k < NS; k += blockDim.x) {
@@ -315,20 +316,21 @@ __global__ __launch_bounds__(256) void wide_static_finalize_kernel(
         tot[k] = s;
     }
     __syncthreads();
-    if (threadIdx.x < kWave) {
+    if (threadIdx.x < N) {
         const int r = threadIdx.x;
-        const bool act = r < N;
         float e[N], gm[N];
 #pragma unroll
         for (int c = 0; c < N; ++c) {
-            e[c] = act ? expf(h_res[r * N + c]) : 0.f;
-            gm[c] = act ? tot[r * N + c] : 0.f;
+            e[c] = expf(h_res[r * N + c]);
+            gm[c] = tot[r * N + c];
         }
-        sk_backward<N>(gm, e, iters, eps, act);
-        if (act) {
+        if (hist) {
+            sk_backward_mem<N>(gm, e, iters, eps, true, hist, r);
+        } else {
+            sk_backward<N>(gm, e, iters, eps, true);
+        }
 #pragma unroll
-            for (int c = 0; c < N; ++c) d_h_res[r * N + c] = gm[c] * e[c];
-        }
+        for (int c = 0; c < N; ++c) d_h_res[r * N + c] = gm[c] * e[c];
     }
     if (threadIdx.x < N) {
         const int r = threadIdx.x;
@@ -786,13 +788,16 @@ hipError_t launch_wide_distribute_bwd(int dt, int n, const float* g, const void*
 
 hipError_t launch_wide_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
                                        const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                       float* d_h_res, int iters, float sk_eps, hipStream_t s) {
+                                       float* d_h_res, int iters, float sk_eps, float* hist, size_t hist_bytes,
+                                       hipStream_t s) {
+    // the history when it fits, else the recomputing adjoint
+    if ((size_t)(iters > 0 ? iters : 0) * (n + 1) * n * sizeof(float) > hist_bytes) hist = nullptr;
     if (n == 16) {
         hipLaunchKernelGGL((wide_static_finalize_kernel<16>), dim3(1), dim3(256), 0, s, scal_part, rows, h_pre, h_post,
-                           h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps);
+                           h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, hist);
     } else if (n == 32) {
         hipLaunchKernelGGL((wide_static_finalize_kernel<32>), dim3(1), dim3(256), 0, s, scal_part, rows, h_pre, h_post,
-                           h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps);
+                           h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, hist);
     } else {
         return hipErrorInvalidValue;
     }
