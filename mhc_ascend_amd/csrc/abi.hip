@@ -521,11 +521,16 @@ static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
 // The projection backward over all output tiles of Phi (rows o0 = 32 t ..):
 // dx gets every tile's term (the first tile also s x, or starts from zero
 // when !accumulate), and each tile's dPhi partials are column-summed into
-// grad_phi rows o0 .. before the next tile reuses the partial buffer.
+// grad_phi rows o0 .. before the next tile reuses the partial buffer.  Many
+// tiles with fp32 x and a moderate batch take the two-kernel path instead
+// (dx over all tiles in one pass, dPhi written directly).
 static hipError_t proj_bwd_all(int x_dtype, const void* x, const float* dp, int dp_stride_, const float* s_tok,
                                const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                                void* dx, bool accumulate, float* part, int tiles, float* stage, float* grad_phi,
                                int64_t batch, int64_t K, hipStream_t s) {
+    if (batch > 0 && proj_bwd_wide_path(x_dtype, np, batch))
+        return launch_proj_bwd_wide((const float*)x, dp, dp_stride_, s_tok, phi_pre, phi_post, phi_res, n_pre, np,
+                                    (float*)dx, accumulate, grad_phi, batch, K, s);
     hipError_t e = hipSuccess;
     for (int o0 = 0; o0 < np && e == hipSuccess; o0 += kProjTile) {
         const int rows_t = np - o0 < kProjTile ? np - o0 : kProjTile;

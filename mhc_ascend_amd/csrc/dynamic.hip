@@ -1200,6 +1200,247 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Projection backward over many 32-row output tiles (2n + n^2 > 32 rows:
+// n >= 8), fp32 x and dx (bf16 x is upcast before it gets here), for
+// batches up to kProjWideMaxB tokens.  The per-tile kernel above would read
+// x and dx once per tile (34 times at n = 32); instead:
+//   proj_bwd_dx_kernel:   one workgroup per 128 columns x 32 tokens loops
+//     over the output tiles, dx_proj^T (columns x tokens) accumulating in
+//     MFMA registers: A = Phi^T (the next tile's values loaded while the
+//     current one computes; the token blocks of one column block run on one
+//     XCD and share Phi through its L2), B = dP^T read straight
+//     from dP; then one epilogue dx = dx_proj + (ACC ? dx : 0) + s x.
+//   proj_bwd_dphi_kernel: one workgroup per 64 output rows x 128 columns
+//     walks all tokens in 32-token stages, dPhi = dP^T x in MFMA registers,
+//     and stores its rows of dPhi directly (no partials, no column sums).
+//     The row blocks of one column block get ids on one XCD, so they share
+//     those x columns through its L2.
+// Operands are split hi / lo (hi.hi + lo.hi + hi.lo, as above).
+// ---------------------------------------------------------------------------
+constexpr int kProjWideMaxB = 1024;
+constexpr int kDxStages = 1;  // 32-token stages per dx workgroup
+
+// 8 consecutive fp32 (32-byte aligned) as two 16-byte loads
+__device__ __forceinline__ void ld8f(const float* p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <bool ACC, bool HAS_S>
+__global__ __launch_bounds__(256) void proj_bwd_dx_kernel(
+    const float* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
+    const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
+    int n_pre, int np, float* __restrict__ dx, int64_t B, int64_t K) {
+    constexpr int CB = 128;
+    constexpr int TS = kDxStages;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    // Workgroups go round-robin over the 8 XCDs by linear id; the token
+    // blocks of one column block are given ids on the same XCD, one after
+    // another, so they share that column block's Phi in the XCD's L2.
+    const int64_t tblocks = (B + 32 * TS - 1) / (32 * TS);
+    const int64_t lin = blockIdx.x;
+    const int64_t idx = lin / 8;
+    const int64_t cb = (idx / tblocks) * 8 + lin % 8;
+    const int64_t kb0 = cb * CB + wave * 32;  // this wave's 32 columns
+    if (kb0 >= K) return;  // padding ids, and K % 32 == 0: whole waves are in or out
+    const int64_t tb0 = (idx % tblocks) * (32 * TS);
+    f32x4_t d[TS][2][2];
+#pragma unroll
+    for (int st = 0; st < TS; ++st) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) d[st][tt][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    // dP columns are read 8 at a time: a stride that is a multiple of 8
+    // allows the aligned 16-byte loads (the layer's dP rows are)
+    const bool dp_vec = (dp_stride % 8) == 0;
+    // A = Phi^T: Phi[o0 + 8 lg + e][column 16 ct + lr]; the next tile's
+    // values are loaded while the current tile is on the matrix cores
+    float pv[2][8];
+    auto load_phi = [&](int o0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int o = o0 + 8 * lg + e;
+                pv[ct][e] = o < np ? phi_row(phi_pre, phi_post, phi_res, n_pre, o, K)[kb0 + 16 * ct + lr] : 0.f;
+            }
+        }
+    };
+    load_phi(0);
+    for (int o0 = 0; o0 < np; o0 += 32) {
+        u32x4_t phh[2], phl[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) split_pack8(pv[ct], phh[ct], phl[ct]);
+        if (o0 + 32 < np) load_phi(o0 + 32);
+#pragma unroll
+        for (int st = 0; st < TS; ++st) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                // B = dP^T: dP[token 16 tt + lr][o0 + 8 lg .. + 7]
+                const int64_t t = tb0 + 32 * st + 16 * tt + lr;
+                float v[8];
+                const int ob = o0 + 8 * lg;
+                if (t < B && dp_vec && ob + 8 <= np) {
+                    ld8f(dP + t * dp_stride + ob, v);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = (t < B && ob + e < np) ? dP[t * dp_stride + ob + e] : 0.f;
+                }
+                u32x4_t bh, bl;
+                split_pack8(v, bh, bl);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    d[st][tt][ct] = mfma16x16x32(phh[ct], bh, d[st][tt][ct]);
+                    d[st][tt][ct] = mfma16x16x32(phl[ct], bh, d[st][tt][ct]);
+                    d[st][tt][ct] = mfma16x16x32(phh[ct], bl, d[st][tt][ct]);
+                }
+            }
+        }
+    }
+    // D[column 16 ct + 4 lg + i][token 16 tt + lr]: four consecutive columns of one token
+#pragma unroll
+    for (int st = 0; st < TS; ++st) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int64_t t = tb0 + 32 * st + 16 * tt + lr;
+            if (t >= B) continue;
+            const float sv = HAS_S ? s_tok[t] : 0.f;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const int64_t off = t * K + kb0 + 16 * ct + 4 * lg;
+                float4 o = make_float4(d[st][tt][ct][0], d[st][tt][ct][1], d[st][tt][ct][2], d[st][tt][ct][3]);
+                if constexpr (ACC) {
+                    const float4 a = *reinterpret_cast<const float4*>(dx + off);
+                    o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
+                }
+                if constexpr (HAS_S) {
+                    const float4 xv = *reinterpret_cast<const float4*>(x + off);
+                    o.x += sv * xv.x; o.y += sv * xv.y; o.z += sv * xv.z; o.w += sv * xv.w;
+                }
+                *reinterpret_cast<float4*>(dx + off) = o;
+            }
+        }
+    }
+}
+
+constexpr int kDphiRows = 64;  // output rows (two 32-row tiles) per dPhi workgroup
+
+__global__ __launch_bounds__(256) void proj_bwd_dphi_kernel(const float* __restrict__ x, const float* __restrict__ dP,
+                                                            int dp_stride, int np, float* __restrict__ dphi,
+                                                            int64_t B, int64_t K) {
+    constexpr int CB = 128;
+    constexpr int OT = kDphiRows / 16;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    // the row blocks of one column block on one XCD (as in proj_bwd_dx_kernel)
+    const int64_t rblocks = (np + kDphiRows - 1) / kDphiRows;
+    const int64_t lin = blockIdx.x;
+    const int64_t idx = lin / 8;
+    const int o0 = (int)(idx % rblocks) * kDphiRows;
+    const int64_t kb0 = ((idx / rblocks) * 8 + lin % 8) * CB + wave * 32;
+    if (kb0 >= K) return;
+    f32x4_t acc[OT][2];
+#pragma unroll
+    for (int ot = 0; ot < OT; ++ot) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) acc[ot][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int64_t t0 = 0; t0 < B; t0 += 32) {
+        // A = dP^T: rows o = o0 + 16 ot + lr, tokens t0 + 8 lg + e
+        u32x4_t ah[OT], al[OT];
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) {
+            const int o = o0 + 16 * ot + lr;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t t = t0 + 8 * lg + e;
+                v[e] = (t < B && o < np) ? dP[t * dp_stride + o] : 0.f;
+            }
+            split_pack8(v, ah[ot], al[ot]);
+        }
+        // B = x: tokens t0 + 8 lg + e, column 16 ct + lr
+        u32x4_t xh[2], xl[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t t = t0 + 8 * lg + e;
+                v[e] = t < B ? x[t * K + kb0 + 16 * ct + lr] : 0.f;
+            }
+            split_pack8(v, xh[ct], xl[ct]);
+        }
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) {
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                acc[ot][ct] = mfma16x16x32(ah[ot], xh[ct], acc[ot][ct]);
+                acc[ot][ct] = mfma16x16x32(al[ot], xh[ct], acc[ot][ct]);
+                acc[ot][ct] = mfma16x16x32(ah[ot], xl[ct], acc[ot][ct]);
+            }
+        }
+    }
+    // D[o 16 ot + 4 lg + i][column 16 ct + lr]
+#pragma unroll
+    for (int ot = 0; ot < OT; ++ot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int o = o0 + 16 * ot + 4 * lg + i;
+            if (o >= np) continue;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) dphi[(int64_t)o * K + kb0 + 16 * ct + lr] = acc[ot][ct][i];
+        }
+    }
+}
+
+bool proj_bwd_wide_path(int x_dtype, int np, int64_t B) {
+    return x_dtype == kF32 && np > kProjTile && B >= 1 && B <= kProjWideMaxB;
+}
+
+hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, const float* s_tok,
+                                const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
+                                float* dx, bool accumulate, float* dphi, int64_t B, int64_t K, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (np <= kProjTile || B > kProjWideMaxB || K % 32 != 0) return hipErrorInvalidValue;
+    if (s_tok && !accumulate) return hipErrorInvalidValue;
+    const unsigned cblocks = (unsigned)((K + 127) / 128);
+    // 1-D grid: 8 XCD lanes x ceil(column blocks / 8) x token blocks
+    const unsigned tblocks = (unsigned)((B + 32 * kDxStages - 1) / (32 * kDxStages));
+    const dim3 gdx(8u * ((cblocks + 7) / 8) * tblocks);
+    const int tok = timing_begin("proj_bwd", s);
+    if (s_tok) {
+        hipLaunchKernelGGL((proj_bwd_dx_kernel<true, true>), gdx, dim3(256), 0, s, x, dP, dp_stride, s_tok, phi_pre,
+                           phi_post, phi_res, n_pre, np, dx, B, K);
+    } else if (accumulate) {
+        hipLaunchKernelGGL((proj_bwd_dx_kernel<true, false>), gdx, dim3(256), 0, s, x, dP, dp_stride, s_tok, phi_pre,
+                           phi_post, phi_res, n_pre, np, dx, B, K);
+    } else {
+        hipLaunchKernelGGL((proj_bwd_dx_kernel<false, false>), gdx, dim3(256), 0, s, x, dP, dp_stride, s_tok, phi_pre,
+                           phi_post, phi_res, n_pre, np, dx, B, K);
+    }
+    hipError_t e = hipGetLastError();
+    timing_end(tok, s);
+    if (e != hipSuccess) return e;
+    const int tg = timing_begin("proj_bwd_dphi", s);
+    const unsigned rblocks = (unsigned)((np + kDphiRows - 1) / kDphiRows);
+    hipLaunchKernelGGL(proj_bwd_dphi_kernel, dim3(8u * ((cblocks + 7) / 8) * rblocks), dim3(256), 0, s, x, dP,
+                       dp_stride, np, dphi, B, K);
+    timing_end(tg, s);
+    return hipGetLastError();
+}
+
 // Token tiles of the projection backward: column blocks x tiles fill two
 // rounds of resident workgroups (rounded down, so a last partial round is
 // nearly full rather than leaving most CUs idle while it runs), at least one.

@@ -26,7 +26,8 @@ def _gen(seed):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,K,out_dim", [(1, 32, 1), (3, 96, 8), (70, 1024, 24), (129, 4160, 24), (300, 4096, 32),
-                                         (65, 16384, 24), (9, 320, 33), (70, 1024, 80), (40, 2048, 100)])
+                                         (65, 16384, 24), (9, 320, 33), (70, 1024, 80), (40, 2048, 100),
+                                         (1500, 96, 40)])
 def test_projection(device, dtype, B, K, out_dim):
     g = _gen(B + K + out_dim)
     x = torch.randn(B, K, generator=g).to(dtype)
@@ -98,10 +99,12 @@ def test_dynamic_layer_n2_matches_oracle(device, x_dtype, B, C):
 
 
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,C", [(3, 64), (37, 320), (128, 1280)])
+@pytest.mark.parametrize("B,C", [(3, 64), (37, 320), (128, 1280), (1100, 64)])
 def test_dynamic_layer_n8_matches_oracle(device, x_dtype, B, C):
     """Expansion rate 8: 2n + n^2 = 80 projection rows in three 32-row
-    output tiles; (128, 1280) is a paper configuration (benchmark.py:306)."""
+    output tiles; (128, 1280) is a paper configuration (benchmark.py:306).
+    Up to 1024 tokens the projection backward runs over all tiles at once;
+    B = 1100 takes the per-tile path."""
     d = R.dynamic_layer_inputs(B, 8, C, seed=8 * B + C, x_dtype=x_dtype, alpha=0.3, phi_std=0.05, b_std=0.5)
     _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n=8 B={B} C={C} {x_dtype}")
 
