@@ -724,12 +724,12 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
 }
 
 // The backward hands one of its 2 + n^2 + 3n row sums to each thread.  With
-// bf16 x (8-byte x and dx accesses per lane) wide workgroups with one token
-// in registers were measured faster than 256 lanes with the two-token
-// prefetch (C4 MODE 1: 225 -> 208 us); fp32 rows keep the prefetch.
+// bf16 x (8-byte x and dx accesses per lane) 512-lane workgroups with one
+// token in registers were measured faster than 256 lanes with the two-token
+// prefetch (C4 MODE 1: 216 -> 208 us); fp32 rows keep the prefetch.
 static RowTiling bwd_tiling(int64_t C, int n, int x_dtype = kF32) {
     if (n > 8) return RowTiling{0, 0};
-    return with_min_threads(choose_row_tiling(C, kLayerWC, 2 * n, x_dtype == kBF16 ? 1024 : 256), 2 + n * n + 3 * n);
+    return with_min_threads(choose_row_tiling(C, kLayerWC, 2 * n, x_dtype == kBF16 ? 512 : 256), 2 + n * n + 3 * n);
 }
 
 bool layer_bwd_is_wide(int n, int64_t C) { return bwd_tiling(C, n).vpt <= 0; }
