@@ -10,6 +10,7 @@ raises ``RuntimeError``.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -126,9 +127,23 @@ def call(name: str, *args) -> None:
         raise RuntimeError(f"{name} failed (status {rc}): {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_same_device = contextlib.nullcontext()
+
+
 def stream_of(t: torch.Tensor) -> int:
     """Raw hipStream_t of the current torch stream on ``t``'s device."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index if t.device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def on_device(dev: torch.device):
+    """Make ``dev`` the current device for a library call (the library sizes
+    grids for the current device); a no-op context when it already is."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return _same_device
+    return torch.cuda.device(dev)
 
 
 def ptr(t) -> int:

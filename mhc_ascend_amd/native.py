@@ -52,7 +52,7 @@ def sinkhorn_knopp_fwd(inp: torch.Tensor, num_iters: int = 20, eps: float = 1e-8
         raise RuntimeError("inp must be float32")
     inp = inp.contiguous()
     out = torch.empty_like(inp)
-    with torch.cuda.device(inp.device):
+    with _lib.on_device(inp.device):
         call("mhc_sinkhorn_knopp_fwd", ptr(inp), ptr(out), inp.size(0), inp.size(1), int(num_iters), float(eps),
              stream_of(inp))
     return out
@@ -74,7 +74,7 @@ def sinkhorn_knopp_bwd(grad_out: torch.Tensor, inp: torch.Tensor, out: torch.Ten
     grad_out = grad_out.contiguous()
     inp = inp.contiguous()
     grad_inp = torch.empty_like(inp)
-    with torch.cuda.device(inp.device):
+    with _lib.on_device(inp.device):
         call("mhc_sinkhorn_knopp_bwd", ptr(grad_out), ptr(inp), 0, ptr(grad_inp), inp.size(0), inp.size(1),
              int(num_iters), float(eps), stream_of(inp))
     return grad_inp
@@ -120,7 +120,7 @@ def rmsnorm_fwd(inp: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> T
     w = _f32c(weight)
     out = torch.empty_like(x)
     rms = torch.empty((B,), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         call("mhc_rmsnorm_fwd", ptr(x), dtype_code(x.dtype), ptr(w), ptr(out), ptr(rms), B, C, float(eps),
              stream_of(x))
     return out, rms
@@ -138,7 +138,7 @@ def rmsnorm_bwd(grad_out: torch.Tensor, inp: torch.Tensor, weight: torch.Tensor,
     w, r = _f32c(weight), _f32c(rms)
     gx = torch.empty_like(x)
     gw = torch.empty((C,), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         ws_bytes = _lib.load().mhc_rmsnorm_bwd_workspace_size(B, C, dtype_code(x.dtype))
         ws = torch.empty((max(int(ws_bytes), 1),), dtype=torch.uint8, device=x.device)
         call("mhc_rmsnorm_bwd", ptr(g), ptr(x), dtype_code(x.dtype), ptr(w), ptr(r), ptr(gx), ptr(gw), ptr(ws),
@@ -154,7 +154,7 @@ def compute_rms_fwd(inp: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
     x = _storage(inp)
     B, K = x.shape
     rms = torch.empty((B,), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         call("mhc_compute_rms_fwd", ptr(x), dtype_code(x.dtype), ptr(rms), B, K, float(eps), stream_of(x))
     return rms
 
@@ -173,7 +173,7 @@ def stream_aggregate_fwd(inp: torch.Tensor, H_pre_raw: torch.Tensor) -> Tuple[to
     h, hs = _coef_view("stream_aggregate_fwd", H_pre_raw, B, n)
     out = torch.empty((B, C), dtype=x.dtype, device=x.device)
     h_act = torch.empty((B, n), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         call("mhc_stream_aggregate_fwd", ptr(x), dtype_code(x.dtype), ptr(h), hs, ptr(out), ptr(h_act), B, n, C,
              stream_of(x))
     return out, h_act
@@ -190,7 +190,7 @@ def _aggregate_bwd(grad_out, inp, H_pre_activated, want_raw: bool):
     gx = torch.empty_like(x)
     gh = torch.empty((B, n), dtype=torch.float32, device=x.device)
     graw = torch.empty((B, n), dtype=torch.float32, device=x.device) if want_raw else None
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         call("mhc_stream_aggregate_bwd", ptr(g), ptr(x), dtype_code(x.dtype), ptr(h), hs, ptr(gx), ptr(gh),
              ptr(graw), B, n, C, stream_of(x))
     return gx, gh, graw
@@ -218,7 +218,7 @@ def stream_distribute_mix_add_fwd(y_norm: torch.Tensor, H_post_raw: torch.Tensor
     m, ms = _coef_view("stream_distribute_mix_add_fwd", M, B, n * n)
     out = torch.empty((B, n, C), dtype=torch.float32, device=x.device)
     h_act = torch.empty((B, n), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         call("mhc_stream_distribute_mix_add_fwd", ptr(y), ptr(h), hs, ptr(m), ms, ptr(x), dtype_code(x.dtype),
              ptr(out), ptr(h_act), B, n, C, stream_of(x))
     return out, h_act
@@ -239,7 +239,7 @@ def _distribute_bwd(grad_out, x_inp, y_norm, M, H_post_activated, want_raw: bool
     gM = torch.empty((B, n, n), dtype=torch.float32, device=x.device)
     gh = torch.empty((B, n), dtype=torch.float32, device=x.device)
     graw = torch.empty((B, n), dtype=torch.float32, device=x.device) if want_raw else None
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         call("mhc_stream_distribute_mix_add_bwd", ptr(g), ptr(x), ptr(y), dtype_code(x.dtype), ptr(m), ms, ptr(h),
              hs, ptr(gx), ptr(gy), ptr(gM), ptr(gh), ptr(graw), B, n, C, stream_of(x))
     return gx, gy, gM, gh, graw
@@ -288,7 +288,7 @@ def mhc_layer_static_fwd(x: torch.Tensor, rmsnorm_weight: torch.Tensor, H_pre: t
     rms = torch.empty((B,), dtype=torch.float32, device=x.device)
     lib = _lib.load()
     saved = torch.empty((lib.mhc_layer_static_saved_size(n, C) // 4,), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         call("mhc_layer_static_fwd", ptr(x), dtype_code(x.dtype), ptr(w), dtype_code(w.dtype), ptr(hp), ptr(hq),
              ptr(hr), ptr(out), ptr(rms), ptr(saved), B, n, C, int(num_iters), float(sinkhorn_eps),
              float(rmsnorm_eps), stream_of(x))
@@ -314,7 +314,7 @@ def mhc_layer_static_bwd(grad_out: torch.Tensor, x: torch.Tensor, rmsnorm_weight
     ghp = torch.empty((n,), dtype=torch.float32, device=dev)
     ghq = torch.empty((n,), dtype=torch.float32, device=dev)
     ghr = torch.empty((n, n), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         ws_bytes = _lib.load().mhc_layer_static_bwd_workspace_size(B, n, C, dtype_code(x.dtype))
         ws = torch.empty((max(int(ws_bytes), 1),), dtype=torch.uint8, device=dev)
         call("mhc_layer_static_bwd", ptr(g), ptr(x), dtype_code(x.dtype), dtype_code(wdt), ptr(hp), ptr(hq),
@@ -343,7 +343,7 @@ def fused_rmsnorm_matmul_fwd(inp: torch.Tensor, weight: torch.Tensor) -> torch.T
     phi = _f32c(weight)
     B, K = x.shape
     out = torch.empty((B, phi.size(0)), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         wsb = _lib.load().mhc_fused_rmsnorm_matmul_fwd_workspace_size(B, K, phi.size(0))
         ws = _ws(x.device, wsb)
         call("mhc_fused_rmsnorm_matmul_fwd", ptr(x), dtype_code(x.dtype), ptr(phi), ptr(out), ptr(ws), int(wsb), B,
@@ -360,7 +360,7 @@ def fused_rmsnorm_matmul_bwd(grad_out: torch.Tensor, x_flat: torch.Tensor,
     out_dim = phi.size(0)
     gx = torch.empty((B, K), dtype=torch.float32, device=x.device)
     gphi = torch.empty((out_dim, K), dtype=torch.float32, device=x.device)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         wsb = _lib.load().mhc_fused_rmsnorm_matmul_bwd_workspace_size(B, K, out_dim)
         ws = _ws(x.device, wsb)
         call("mhc_fused_rmsnorm_matmul_bwd", ptr(g), ptr(x), ptr(phi), ptr(gx), ptr(gphi), ptr(ws), int(wsb), B, K,
@@ -405,7 +405,7 @@ def mhc_layer_dynamic_fwd(x_expanded: torch.Tensor, rmsnorm_weight: torch.Tensor
     out = torch.empty((B, n, C), dtype=torch.float32, device=dev)
     lib = _lib.load()
     saved = torch.empty((lib.mhc_layer_dynamic_saved_size(B, n, C) // 4,), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         wsb = lib.mhc_layer_dynamic_fwd_workspace_size(B, n, C)
         ws = _ws(dev, wsb)
         call("mhc_layer_dynamic_fwd", ptr(x), dtype_code(x.dtype), ptr(w), dtype_code(w.dtype), ptr(pp), ptr(pq),
@@ -428,7 +428,7 @@ def mhc_layer_dynamic_pack(rmsnorm_weight: torch.Tensor, phi_pre: torch.Tensor, 
     lib = _lib.load()
     nbytes = int(lib.mhc_layer_dynamic_packed_size(n, C))
     packed = _ws(dev, nbytes)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         call("mhc_layer_dynamic_pack", ptr(w), dtype_code(w.dtype), ptr(pp), ptr(pq), ptr(pr), ptr(packed), nbytes,
              n, C, stream_of(w))
     return packed
@@ -455,7 +455,7 @@ def mhc_layer_dynamic_infer(x_expanded: torch.Tensor, packed: torch.Tensor, alph
     if bp.numel() != n or bq.numel() != n or br.numel() != n * n:
         raise RuntimeError("mhc_layer_dynamic_infer: b_pre/b_post must have n and b_res n*n elements")
     out = torch.empty((B, n, C), dtype=out_dtype, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         wsb = lib.mhc_layer_dynamic_infer_workspace_size(B, n, C)
         ws = _ws(dev, wsb)
         call("mhc_layer_dynamic_infer", ptr(x), dtype_code(x.dtype), ptr(packed), ptr(a[0]), ptr(a[1]), ptr(a[2]),
@@ -491,7 +491,7 @@ def mhc_layer_dynamic_bwd(grad_output: torch.Tensor, x_expanded: torch.Tensor, r
     gphi = torch.empty((np_, n * C), dtype=torch.float32, device=dev)
     galpha = torch.empty((3,), dtype=torch.float32, device=dev)
     gb = torch.empty((np_,), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         wsb = _lib.load().mhc_layer_dynamic_bwd_workspace_size(B, n, C, dtype_code(x.dtype))
         ws = _ws(dev, wsb)
         call("mhc_layer_dynamic_bwd", ptr(g), ptr(x), dtype_code(x.dtype), dtype_code(wdt), ptr(pp), ptr(pq),
@@ -565,7 +565,7 @@ def wrapper_dynamic_fwd(residual: torch.Tensor, branch: torch.Tensor, residual_m
     out = torch.empty((T, C), dtype=torch.float32, device=dev)
     lib = _lib.load()
     saved = torch.empty((lib.mhc_wrapper_dynamic_saved_size(T, n, C) // 4,), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         wsb = lib.mhc_wrapper_dynamic_fwd_workspace_size(T, n, C)
         ws = _ws(dev, wsb)
         call("mhc_wrapper_dynamic_fwd", ptr(r), ptr(b), dtype_code(r.dtype), mode, ptr(w), dtype_code(w.dtype),
@@ -599,7 +599,7 @@ def wrapper_dynamic_bwd(grad_out: torch.Tensor, residual: torch.Tensor, branch: 
     gphi = torch.empty((np_, n * C), dtype=torch.float32, device=dev)
     galpha = torch.empty((3,), dtype=torch.float32, device=dev)
     gbias = torch.empty((np_,), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         wsb = _lib.load().mhc_wrapper_dynamic_bwd_workspace_size(T, n, C, dtype_code(r.dtype), mode)
         ws = _ws(dev, wsb)
         call("mhc_wrapper_dynamic_bwd", ptr(g), ptr(r), ptr(b), dtype_code(r.dtype), mode, dtype_code(wdt), ptr(pp),
@@ -626,7 +626,7 @@ def wrapper_static_fwd(residual: torch.Tensor, branch: torch.Tensor, residual_mo
     out = torch.empty((T, C), dtype=torch.float32, device=dev)
     lib = _lib.load()
     saved = torch.empty((lib.mhc_layer_static_saved_size(n, C) // 4,), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         call("mhc_wrapper_static_fwd", ptr(r), ptr(b), dtype_code(r.dtype), mode, ptr(w), dtype_code(w.dtype), ptr(hp),
              ptr(hq), ptr(hr), ptr(out), ptr(saved), T, n, C, int(sinkhorn_iters), float(sinkhorn_eps),
              float(rmsnorm_eps), stream_of(r))
@@ -653,7 +653,7 @@ def wrapper_static_bwd(grad_out: torch.Tensor, residual: torch.Tensor, branch: t
     ghp = torch.empty((n,), dtype=torch.float32, device=dev)
     ghq = torch.empty((n,), dtype=torch.float32, device=dev)
     ghr = torch.empty((n, n), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         wsb = _lib.load().mhc_wrapper_static_bwd_workspace_size(T, n, C, dtype_code(r.dtype), mode)
         ws = _ws(dev, wsb)
         call("mhc_wrapper_static_bwd", ptr(g), ptr(r), ptr(b), dtype_code(r.dtype), mode, dtype_code(wdt), ptr(hp),

@@ -233,3 +233,27 @@ def test_reference_static_composition_from_ops(device, B, C):
     for nm, a, e in zip(["dw", "dH_pre", "dH_post", "dH_res"], [w.grad, hp.grad, hq.grad, hr.grad],
                         [p.grad for p in pr]):
         assert_close(a, e, 1e-3, grad_atol(e, 1e-4), f"composition {nm}")
+
+
+def test_calls_run_on_the_callers_stream(device):
+    """The library enqueues on torch's current stream (bindings.cpp:59 uses
+    the current NPU stream): under a side stream the raw handle it receives
+    is that stream's, and results match the default-stream ones."""
+    from mhc_ascend_amd import _lib
+    g = _gen(90)
+    x = torch.randn(33, 4, 512, generator=g).to(device)
+    torch.manual_seed(90)
+    layer = mhc.MHCLayer(512, 4, use_dynamic_h=True).to(device)
+    with torch.no_grad():
+        want = layer(x)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert _lib.stream_of(x) == side.cuda_stream
+        with torch.no_grad():
+            got = layer(x)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert _lib.stream_of(x) == torch.cuda.current_stream().cuda_stream
