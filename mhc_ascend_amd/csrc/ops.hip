@@ -364,7 +364,7 @@ __global__ MHC_ROW_BOUNDS(false) void distribute_bwd_kernel(
 hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, float* rms, int64_t B, int64_t C,
                               float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 1);
+    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 1, 512);
     const int tok = timing_begin("rmsnorm_fwd", s);
     if (t.vpt <= 0) {
         // rows that are not a multiple of the vector (or too wide): channel loop
@@ -379,7 +379,7 @@ hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, fl
 }
 
 int rmsnorm_bwd_grid(int dt, int64_t B, int64_t C) {
-    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2);
+    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2, 512);
     if (t.vpt <= 0) return wide_rmsnorm_bwd_grid(dt, B, C);
     int64_t g = (int64_t)device_cu_count() * ((t.threads <= 256) ? 4 : 2);
     if (g > B) g = B;
@@ -388,7 +388,7 @@ int rmsnorm_bwd_grid(int dt, int64_t B, int64_t C) {
 
 hipError_t launch_rmsnorm_bwd(int dt, const void* g, const void* x, const float* w, const float* rms, void* gx,
                               float* dw_part, int grid, int64_t B, int64_t C, hipStream_t s) {
-    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2);
+    const RowTiling t = choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2, 512);
     const int tok = timing_begin("rmsnorm_bwd", s);
     if (t.vpt <= 0) {
         const hipError_t e = launch_wide_rmsnorm_bwd(dt, g, x, w, rms, gx, dw_part, grid, B, C, s);
@@ -424,7 +424,7 @@ hipError_t launch_compute_rms(int dt, const void* x, float* rms, int64_t B, int6
 hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out, float* h_act,
                                 int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
+    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1, 512);
     const int tok = timing_begin("aggregate_fwd", s);
     if (t.vpt <= 0) {
         const hipError_t e = launch_wide_aggregate_fwd(dt, n, x, H, hs, out, h_act, B, C, s);
@@ -442,7 +442,7 @@ hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, in
 hipError_t launch_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
                                 void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
+    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1, 512);
     const int tok = timing_begin("aggregate_bwd", s);
     if (t.vpt <= 0) {
         const hipError_t e = launch_wide_aggregate_bwd(dt, n, g, x, h_act, hs, gx, gh_act, gh_raw, B, C, s);
@@ -461,7 +461,7 @@ hipError_t launch_distribute_fwd(int dt, int n, const void* y, const float* H, i
                                  int64_t ms, const void* x, float* out, float* h_act, int64_t B, int64_t C,
                                  hipStream_t s) {
     if (B == 0) return hipSuccess;
-    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1);
+    const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1, 512);
     const int tok = timing_begin("distribute_fwd", s);
     if (t.vpt <= 0) {
         const hipError_t e = launch_wide_distribute_fwd(dt, n, y, H, hs, M, ms, x, out, h_act, B, C, s);
