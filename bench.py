@@ -485,7 +485,8 @@ KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "wr
 # benchmark.py:175-269): per (B, C, n), static and dynamic H, the forward in
 # eval mode under no_grad and forward + backward of out.sum() in train mode,
 # fp32 x drawn fresh per run, caches flushed before each run, events around
-# the call, 10% trimmed mean.
+# the call, 10% trimmed mean.  A third column replays the same forward +
+# backward library calls from a HIP graph (no host overhead).
 # ---------------------------------------------------------------------------
 PAPER_CONFIGS = [(320, 1280, 4), (512, 1920, 4), (1280, 2560, 4), (2560, 1280, 4), (128, 1280, 8), (256, 1280, 8),
                  (32, 1280, 32), (64, 1280, 32), (128, 1280, 32)]
@@ -512,6 +513,53 @@ def paper_sweep(torch, mhc, device, warmup=10, runs=100):
         times = times[trim:len(times) - trim] if trim else times
         return sum(times) / len(times)
 
+    from mhc_ascend_amd import native
+
+    def graph_ms(layer, B, n, C, dynamic):
+        """The same fwd + bwd through the library entries, captured once in a
+        HIP graph and replayed: the kernels' time without host overhead."""
+        x = torch.randn(B, n, C, device=device)
+        g = torch.ones(B, n, C, device=device)
+        L = layer
+        if dynamic:
+            ps = [L.rmsnorm_weight, L.phi_pre, L.phi_post, L.phi_res, L.alpha_pre, L.alpha_post, L.alpha_res,
+                  L.b_pre, L.b_post, L.b_res]
+            ps = [p.detach() for p in ps]
+
+            def step():
+                out, saved = native.mhc_layer_dynamic_fwd(x, *ps, 20, 1e-8, 1e-5)
+                native.mhc_layer_dynamic_bwd(g, x, ps[0], saved, *ps[1:], 20, 1e-8, 1e-5)
+        else:
+            ps = [p.detach() for p in (L.rmsnorm_weight, L.H_pre, L.H_post, L.H_res)]
+
+            def step():
+                out, rms, saved = native.mhc_layer_static_fwd(x, *ps, 20, 1e-8, 1e-5)
+                native.mhc_layer_static_bwd(g, x, *ps, saved, 20, 1e-8, 1e-5)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        times = []
+        for it in range(warmup + runs):
+            flush.zero_()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record()
+            graph.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            if it >= warmup:
+                times.append(t0.elapsed_time(t1))
+        times.sort()
+        trim = runs // 10
+        times = times[trim:len(times) - trim] if trim else times
+        return sum(times) / len(times)
+
     rows = []
     for dynamic in (False, True):
         for B, C, n in PAPER_CONFIGS:
@@ -529,9 +577,12 @@ def paper_sweep(torch, mhc, device, warmup=10, runs=100):
             f_ms = timed(fwd, B, n, C, False)
             layer.train()
             fb_ms = timed(fwd_bwd, B, n, C, True)
-            rows.append({"dynamic_h": dynamic, "B": B, "C": C, "n": n, "fwd_ms": f_ms, "fwd_bwd_ms": fb_ms})
+            gr_ms = graph_ms(layer, B, n, C, dynamic)
+            rows.append({"dynamic_h": dynamic, "B": B, "C": C, "n": n, "fwd_ms": f_ms, "fwd_bwd_ms": fb_ms,
+                         "graph_fwd_bwd_ms": gr_ms})
             print(f"[bench] paper {'dynamic' if dynamic else 'static '} B={B:5d} C={C:5d} n={n:3d} "
-                  f"fwd {f_ms:8.4f} ms  fwd+bwd {fb_ms:8.4f} ms", file=sys.stderr, flush=True)
+                  f"fwd {f_ms:8.4f} ms  fwd+bwd {fb_ms:8.4f} ms  graph fwd+bwd {gr_ms:8.4f} ms",
+                  file=sys.stderr, flush=True)
             del layer
     return rows
 
