@@ -321,8 +321,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         }
         // lanes row, row+16, row+32, row+48 hold parts of token row's sum
         float s2 = ss[mt];
-        s2 += __shfl_xor(s2, 16, kWave);
-        s2 += __shfl_xor(s2, 32, kWave);
+        s2 = xor32_add(xor16_add(s2));
         const int64_t tok = tok0 + mt * 16 + row;
         if (kg == 0 && tok < B && otile == 0) ss_part[ksplit * B + tok] = s2;
     }
@@ -686,8 +685,7 @@ __global__ __launch_bounds__(256) void dyn_coef16_bwd_kernel(
     float v[5] = {acc_pp, acc_res, acc_a, acc_b, acc_c};
 #pragma unroll
     for (int k = 0; k < 5; ++k) {
-        v[k] += __shfl_xor(v[k], 16, kWave);
-        v[k] += __shfl_xor(v[k], 32, kWave);
+        v[k] = xor32_add(xor16_add(v[k]));
     }
     if (lane < 16) {
         if (l < 2 * N) red[wave][l] = v[0];

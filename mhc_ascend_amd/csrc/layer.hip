@@ -57,6 +57,19 @@ __global__ __launch_bounds__(256) void static_coef_kernel(const float* __restric
         saved[r] = sigmoidf(h_pre[r]);
         saved[N + r] = 2.f * sigmoidf(h_post[r]);
     }
+    if constexpr (N == skb::kN) {
+        // the whole workgroup on the one 32 x 32 matrix (the finalize's
+        // adjoint recomputes it with the same code)
+        __shared__ float part[skb::kPartFloats];
+        const int i = skb::row(), c0 = skb::col0();
+        float a[skb::kV];
+#pragma unroll
+        for (int k = 0; k < skb::kV; ++k) a[k] = expf(h_res[i * N + c0 + k]);
+        skb::forward(a, iters, eps, part);
+#pragma unroll
+        for (int k = 0; k < skb::kV; ++k) saved[2 * N + i * N + c0 + k] = a[k];
+        return;
+    }
     if (r >= kWave) return;
     if constexpr (N == 4) {
         // the shared M = SK(exp(H_res)): one element per lane of lanes 0..15

@@ -236,6 +236,22 @@ __device__ __forceinline__ float mov(float v) {
 }
 }  // namespace dpp
 
+// v + v[lane ^ 16] and v + v[lane ^ 32] with the gfx950 lane-swap VALU ops
+// instead of an LDS permute.  v_permlane16_swap(v, v) returns
+// {rows (0, 0, 2, 2), rows (1, 1, 3, 3)} of v (a row is 16 lanes),
+// v_permlane32_swap(v, v) returns {halves (0, 0), halves (1, 1)}, so the sum
+// of the pair is the partner sum in every lane; the two operands are added
+// in the same order in both lanes of a pair (IEEE addition commutes, so this
+// is bit-identical to v + shuffle).  The whole pair must be active.
+__device__ __forceinline__ float xor16_add(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float xor32_add(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
 // Sum over the aligned group of G lanes containing this lane (G a power of
 // two dividing 64); every lane of the group receives the group total.
 template <int G>
@@ -244,8 +260,8 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (G >= 4) v += dpp::mov<dpp::kQuadXor2>(v);
     if constexpr (G >= 8) v += dpp::mov<dpp::kRowHalfMirror>(v);
     if constexpr (G >= 16) v += dpp::mov<dpp::kRowMirror>(v);
-    if constexpr (G >= 32) v += __shfl_xor(v, 16, kWave);
-    if constexpr (G >= 64) v += __shfl_xor(v, 32, kWave);
+    if constexpr (G >= 32) v = xor16_add(v);
+    if constexpr (G >= 64) v = xor32_add(v);
     return v;
 }
 
@@ -445,12 +461,28 @@ __device__ __forceinline__ void sk_backward_mem(float (&g)[N], const float (&x0)
         h[N * G] = rinv;
         sk_col_step<N>(a, eps);
     }
-    for (int t = iters - 1; t >= 0; --t) {
-        const float* h = hist + (int64_t)t * (N + 1) * G + r;
-        float A[N];
+    // iteration t - 1's state is loaded while iteration t's adjoint runs
+    float A[N], ri = 0.f;
+    if (iters > 0) {
+        const float* h = hist + (int64_t)(iters - 1) * (N + 1) * G + r;
 #pragma unroll
         for (int c = 0; c < N; ++c) A[c] = h[c * G];
-        sk_adjoint_step<N>(g, A, h[N * G], eps);
+        ri = h[N * G];
+    }
+    for (int t = iters - 1; t >= 0; --t) {
+        float An[N], rn = 0.f;
+#pragma unroll
+        for (int c = 0; c < N; ++c) An[c] = 0.f;
+        if (t > 0) {
+            const float* h = hist + (int64_t)(t - 1) * (N + 1) * G + r;
+#pragma unroll
+            for (int c = 0; c < N; ++c) An[c] = h[c * G];
+            rn = h[N * G];
+        }
+        sk_adjoint_step<N>(g, A, ri, eps);
+#pragma unroll
+        for (int c = 0; c < N; ++c) A[c] = An[c];
+        ri = rn;
     }
 }
 
@@ -578,5 +610,135 @@ __device__ __forceinline__ void sk16_backward(float& g, float x0, int iters, flo
         }
     }
 }
+
+
+// ---------------------------------------------------------------------------
+// Sinkhorn-Knopp on one 32 x 32 matrix spread over a 256-lane workgroup, for
+// a matrix whose chain of iterations is the latency of a launch (the static
+// H_res, or one token's matrix per workgroup).  Lane t holds row t / 8,
+// columns 4 (t % 8) .. 4 (t % 8) + 3.  A row is 8 consecutive lanes (DPP
+// sum); a column is lanes t, t ^ 8, t ^ 16, ... of each wave (row_ror:8 and
+// the lane-swap ops), then the four waves' partials through LDS, added in
+// wave order.  Every step is an xor butterfly, so all lanes of a row or
+// column hold the same bits of its sum.  One barrier per iteration; the LDS
+// partials alternate between two buffers, so a wave's next write never meets
+// a slower wave's reads of the previous step.  Same formulas as sk_forward /
+// sk_adjoint_step (ops_pytorch_backward.py:9-33, 36-72).
+// ---------------------------------------------------------------------------
+namespace skb {
+constexpr int kThreads = 256;
+constexpr int kN = 32;
+constexpr int kV = 4;                 // columns per lane
+constexpr int kLPR = kN / kV;         // lanes per row (8)
+constexpr int kNW = kThreads / kWave; // waves (4)
+constexpr int kTMax = 32;             // iterations the adjoint keeps in registers
+constexpr int kPartFloats = 2 * kNW * kN;  // LDS column partials, double-buffered
+constexpr int kHistFloats = kTMax * kN;    // LDS column scales of the adjoint
+
+__device__ __forceinline__ int row() { return threadIdx.x / kLPR; }
+__device__ __forceinline__ int col0() { return (threadIdx.x % kLPR) * kV; }
+
+// In-wave sum over the 8 lanes holding the same columns.
+__device__ __forceinline__ float col_wave_sum(float v) {
+    v += dpp::mov<dpp::kRowRor8>(v);
+    v = xor16_add(v);
+    return xor32_add(v);
+}
+
+// Column totals of the lane's kV columns; `buf` is kNW * kN floats of LDS.
+__device__ __forceinline__ void col_total(float (&v)[kV], float* buf) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    float p[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) p[k] = col_wave_sum(v[k]);
+    if (lane < kLPR) *reinterpret_cast<float4*>(buf + wave * kN + lane * kV) = make_float4(p[0], p[1], p[2], p[3]);
+    __syncthreads();
+    float4 q[kNW];
+#pragma unroll
+    for (int w = 0; w < kNW; ++w) q[w] = *reinterpret_cast<const float4*>(buf + w * kN + col0());
+    float t[kV] = {q[0].x, q[0].y, q[0].z, q[0].w};
+#pragma unroll
+    for (int w = 1; w < kNW; ++w) {
+        t[0] += q[w].x;
+        t[1] += q[w].y;
+        t[2] += q[w].z;
+        t[3] += q[w].w;
+    }
+#pragma unroll
+    for (int k = 0; k < kV; ++k) v[k] = t[k];
+}
+
+__device__ __forceinline__ void row_scale(float (&a)[kV], float eps, float& rinv) {
+    float s = ((a[0] + a[1]) + a[2]) + a[3];
+    s = group_sum<kLPR>(s);
+    rinv = rcp_nr(s + eps);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] *= rinv;
+}
+
+__device__ __forceinline__ void col_scale(float (&a)[kV], float eps, float* buf, float (&cinv)[kV]) {
+    float s[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) s[k] = a[k];
+    col_total(s, buf);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        cinv[k] = rcp_nr(s[k] + eps);
+        a[k] *= cinv[k];
+    }
+}
+
+// a: the lane's four elements of X in, of SK(X) out.  part: kPartFloats of LDS.
+__device__ __forceinline__ void forward(float (&a)[kV], int iters, float eps, float* part) {
+    for (int t = 0; t < iters; ++t) {
+        float ri, ci[kV];
+        row_scale(a, eps, ri);
+        col_scale(a, eps, part + (t & 1) * kNW * kN, ci);
+    }
+}
+
+// g: the lane's elements of dL/dM in, dL/dX out; x0: elements of X.
+// Requires iters <= kTMax.  part: kPartFloats, hc: kHistFloats of LDS.
+__device__ __forceinline__ void backward(float (&g)[kV], const float (&x0)[kV], int iters, float eps, float* part,
+                                         float* hc) {
+    float hA[kTMax][kV], hr[kTMax];
+    float a[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] = x0[k];
+    const bool writer = threadIdx.x < kLPR;  // row 0 stores the column scales
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+        if (t < iters) {
+            row_scale(a, eps, hr[t]);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) hA[t][k] = a[k];
+            float ci[kV];
+            col_scale(a, eps, part + (t & 1) * kNW * kN, ci);
+            if (writer) *reinterpret_cast<float4*>(hc + t * kN + col0()) = make_float4(ci[0], ci[1], ci[2], ci[3]);
+        }
+    }
+    __syncthreads();
+    // adjoint steps continue the buffer alternation: step t uses (t + 1) & 1
+#pragma unroll
+    for (int t = kTMax - 1; t >= 0; --t) {
+        if (t < iters) {
+            const float4 cv = *reinterpret_cast<const float4*>(hc + t * kN + col0());
+            const float ci[kV] = {cv.x, cv.y, cv.z, cv.w};
+            float d[kV];
+#pragma unroll
+            for (int k = 0; k < kV; ++k) d[k] = g[k] * (hA[t][k] * ci[k]);
+            col_total(d, part + ((t + 1) & 1) * kNW * kN);
+            float dA[kV];
+#pragma unroll
+            for (int k = 0; k < kV; ++k) dA[k] = (g[k] - d[k]) * ci[k];
+            float rd = ((dA[0] * hA[t][0] + dA[1] * hA[t][1]) + dA[2] * hA[t][2]) + dA[3] * hA[t][3];
+            rd = group_sum<kLPR>(rd);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) g[k] = (dA[k] - rd) * hr[t];
+        }
+    }
+}
+}  // namespace skb
 
 }  // namespace mhc

@@ -300,23 +300,70 @@ __global__ __launch_bounds__(gram_threads<N>()) void stream_gram_kernel(const fl
 // scal_part[rows][n^2 + 2n]: column totals in LDS, then (as layer.hip's
 // finalize) dH_pre = dh_pre_act h_pre (1 - h_pre), dH_post = dh_post_act
 // h_post (1 - h_post / 2) and dH_res = SK^T(dM) * exp(H_res), the Sinkhorn
-// adjoint one row per lane of the first n lanes, its per-iteration state in
-// hist (iters * (n + 1) * n floats) or, without hist, recomputed.
+// adjoint on the whole workgroup for n = 32 (iters <= skb::kTMax, state in
+// registers), otherwise one row per lane of the first n lanes with its
+// per-iteration state in hist (iters * (n + 1) * n floats) or, without hist,
+// recomputed.
 // ---------------------------------------------------------------------------
+constexpr int kStaticFinalizeThreads = skb::kThreads;
+
 template <int N>
-__global__ __launch_bounds__(256) void wide_static_finalize_kernel(
+__global__ __launch_bounds__(kStaticFinalizeThreads) void wide_static_finalize_kernel(
     const float* __restrict__ scal_part, int rows, const float* __restrict__ h_pre, const float* __restrict__ h_post,
     const float* __restrict__ h_res, float* __restrict__ d_h_pre, float* __restrict__ d_h_post,
     float* __restrict__ d_h_res, int iters, float eps, float* __restrict__ hist) {
     constexpr int NS = N * N + 2 * N;
+    constexpr int KPT = (NS + kStaticFinalizeThreads - 1) / kStaticFinalizeThreads;
+    constexpr int RB = 4;  // rows loaded per round trip
     __shared__ float tot[NS];
-    for (int k = threadIdx.x; k < NS; k += blockDim.x) {
-        float s = 0.f;
-        for (int r = 0; r < rows; ++r) s += scal_part[(int64_t)r * NS + k];
-        tot[k] = s;
+    {
+        // column sums of the partial rows, in row order; each lane's columns
+        // and RB rows are loaded together
+        float acc[KPT];
+#pragma unroll
+        for (int q = 0; q < KPT; ++q) acc[q] = 0.f;
+        for (int r0 = 0; r0 < rows; r0 += RB) {
+            float v[RB][KPT];
+#pragma unroll
+            for (int j = 0; j < RB; ++j) {
+#pragma unroll
+                for (int q = 0; q < KPT; ++q) {
+                    const int k = threadIdx.x + q * kStaticFinalizeThreads;
+                    v[j][q] = (r0 + j < rows && k < NS) ? scal_part[(int64_t)(r0 + j) * NS + k] : 0.f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < RB; ++j) {
+#pragma unroll
+                for (int q = 0; q < KPT; ++q) {
+                    if (r0 + j < rows) acc[q] += v[j][q];
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < KPT; ++q) {
+            const int k = threadIdx.x + q * kStaticFinalizeThreads;
+            if (k < NS) tot[k] = acc[q];
+        }
     }
     __syncthreads();
-    if (threadIdx.x < N) {
+    if constexpr (N == skb::kN) {
+        if (iters <= skb::kTMax) {
+            __shared__ float part[skb::kPartFloats];
+            __shared__ float hc[skb::kHistFloats];
+            const int i = skb::row(), c0 = skb::col0();
+            float e[skb::kV], gm[skb::kV];
+#pragma unroll
+            for (int k = 0; k < skb::kV; ++k) {
+                e[k] = expf(h_res[i * N + c0 + k]);
+                gm[k] = tot[i * N + c0 + k];
+            }
+            skb::backward(gm, e, iters, eps, part, hc);
+#pragma unroll
+            for (int k = 0; k < skb::kV; ++k) d_h_res[i * N + c0 + k] = gm[k] * e[k];
+        }
+    }
+    if (threadIdx.x < N && (N != skb::kN || iters > skb::kTMax)) {
         const int r = threadIdx.x;
         float e[N], gm[N];
 #pragma unroll
@@ -793,10 +840,10 @@ hipError_t launch_wide_static_finalize(int n, const float* scal_part, int rows, 
     // the history when it fits, else the recomputing adjoint
     if ((size_t)(iters > 0 ? iters : 0) * (n + 1) * n * sizeof(float) > hist_bytes) hist = nullptr;
     if (n == 16) {
-        hipLaunchKernelGGL((wide_static_finalize_kernel<16>), dim3(1), dim3(256), 0, s, scal_part, rows, h_pre, h_post,
+        hipLaunchKernelGGL((wide_static_finalize_kernel<16>), dim3(1), dim3(kStaticFinalizeThreads), 0, s, scal_part, rows, h_pre, h_post,
                            h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, hist);
     } else if (n == 32) {
-        hipLaunchKernelGGL((wide_static_finalize_kernel<32>), dim3(1), dim3(256), 0, s, scal_part, rows, h_pre, h_post,
+        hipLaunchKernelGGL((wide_static_finalize_kernel<32>), dim3(1), dim3(kStaticFinalizeThreads), 0, s, scal_part, rows, h_pre, h_post,
                            h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, hist);
     } else {
         return hipErrorInvalidValue;

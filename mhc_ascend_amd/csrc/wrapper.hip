@@ -660,8 +660,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
             }
         }
         float s2 = ss[mt];
-        s2 += __shfl_xor(s2, 16, kWave);
-        s2 += __shfl_xor(s2, 32, kWave);
+        s2 = xor32_add(xor16_add(s2));
         const int64_t tok = tok0 + mt * 16 + row;
         if (kg == 0 && tok < B) ss_part[(int64_t)blockIdx.y * B + tok] = s2;
     }

@@ -176,6 +176,15 @@ def test_static_layer_wide_n(device, n, B, C, x_dtype):
                   tag=f"n={n} B={B} C={C} {x_dtype}")
 
 
+@pytest.mark.parametrize("iters", [0, 1, 7, 32, 33, 45])
+def test_static_layer_n32_iteration_counts(device, iters):
+    """n = 32: the Sinkhorn forward and adjoint on the whole workgroup keep
+    up to 32 iterations of state in registers; 33 and more take the
+    one-row-per-lane adjoint with its history in the workspace."""
+    d = R.static_layer_inputs(5, 32, 64, seed=3200 + iters)
+    _check_static(d, _run_static(d, device, iters=iters), _oracle_static(d, iters=iters), tag=f"n=32 T={iters}")
+
+
 @pytest.mark.parametrize("n,C", [(2, 1), (2, 7), (4, 250), (4, 1001), (8, 13), (8, 10240)])
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
 def test_static_layer_ragged_hidden(device, n, C, x_dtype):
