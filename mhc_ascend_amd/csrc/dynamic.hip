@@ -571,6 +571,143 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_wide_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// n = 32: one token per 256-lane workgroup, the token's 32 x 32 matrix spread
+// over the workgroup (skb: lane t holds row i = t / 8, columns c0 .. c0 + 3
+// with c0 = 4 (t % 8)), so its Sinkhorn chain takes a barrier and a few
+// instructions per iteration instead of 32 columns' reductions on one lane.
+// Same formulas and outputs as dyn_coef_fwd_kernel / dyn_coef_bwd_wide_kernel;
+// the backward keeps the iteration state in registers (iters <= skb::kTMax).
+// P row o of token b sits in tile o / 32, so a lane's four t_res columns are
+// one 16-byte run of a partial row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(skb::kThreads) void dyn_coef32_fwd_kernel(
+    const float* __restrict__ p_part, const float* __restrict__ ss_part, int ks, int64_t B, int64_t K,
+    const float* __restrict__ a_pre, const float* __restrict__ a_post, const float* __restrict__ a_res,
+    const float* __restrict__ b_pre, const float* __restrict__ b_post, const float* __restrict__ b_res,
+    float* __restrict__ coef, float* __restrict__ p_out, float* __restrict__ rh, int iters, float sk_eps,
+    float rms_eps) {
+    constexpr int N = skb::kN;
+    constexpr int NP = 2 * N + N * N;
+    constexpr int V = skb::kV;
+    __shared__ float part[skb::kPartFloats];
+    const int64_t tok = blockIdx.x;
+    const int i = skb::row(), c0 = skb::col0();
+    float pp = 0.f, pq = 0.f, pr[V] = {0.f, 0.f, 0.f, 0.f}, ss = 0.f;
+    for (int q = 0; q < ks; ++q) {
+        ss += ss_part[(int64_t)q * B + tok];
+        pp += p_part_at(p_part, ks, B, q, tok, i);
+        pq += p_part_at(p_part, ks, B, q, tok, N + i);
+        const float4 v = *reinterpret_cast<const float4*>(
+            p_part + (((int64_t)(2 + i) * ks + q) * B + tok) * kNPad + c0);
+        pr[0] += v.x;
+        pr[1] += v.y;
+        pr[2] += v.z;
+        pr[3] += v.w;
+    }
+    const float r_h = sqrtf(ss / (float)K + rms_eps);
+    const float inv = 1.f / r_h;
+    float e[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) e[k] = expf(pr[k] * a_res[0] * inv + b_res[i * N + c0 + k]);
+    skb::forward(e, iters, sk_eps, part);
+    float* cf = coef + tok * NP;
+#pragma unroll
+    for (int k = 0; k < V; ++k) cf[2 * N + i * N + c0 + k] = e[k];
+    if (c0 == 0) {
+        cf[i] = sigmoidf(pp * a_pre[0] * inv + b_pre[i]);
+        cf[N + i] = 2.f * sigmoidf(pq * a_post[0] * inv + b_post[i]);
+    }
+    if (p_out) {
+        float* po = p_out + tok * NP;
+#pragma unroll
+        for (int k = 0; k < V; ++k) po[2 * N + i * N + c0 + k] = pr[k];
+        if (c0 == 0) {
+            po[i] = pp;
+            po[N + i] = pq;
+        }
+    }
+    if (threadIdx.x == 0 && rh) rh[tok] = r_h;
+}
+
+__global__ __launch_bounds__(skb::kThreads) void dyn_coef32_bwd_kernel(
+    const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
+    const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
+    const float* __restrict__ a_post, const float* __restrict__ a_res, const float* __restrict__ b_res,
+    float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int iters, float sk_eps) {
+    constexpr int N = skb::kN;
+    constexpr int NP = 2 * N + N * N;
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NV = NP + 3;
+    constexpr int NPT = dp_stride(NP);
+    constexpr int V = skb::kV;
+    __shared__ float pbuf[skb::kPartFloats];
+    __shared__ float hc[skb::kHistFloats];
+    __shared__ float red[skb::kNW][4];
+    const int64_t tok = blockIdx.x;
+    const int i = skb::row(), c0 = skb::col0();
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const float ap = a_pre[0], aq = a_post[0], ar = a_res[0];
+    const float* sc = scal + tok * (NS + 2);
+    const float* cf = coef + tok * NP;
+    const float* pv = p + tok * NP;
+    const float inv = 1.f / rh[tok];
+    float gm[V], e[V], pr[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        gm[k] = sc[i * N + c0 + k];
+        pr[k] = pv[2 * N + i * N + c0 + k];
+        e[k] = expf(pr[k] * ar * inv + b_res[i * N + c0 + k]);
+    }
+    skb::backward(gm, e, iters, sk_eps, pbuf, hc);
+    const float hp = cf[i], hq = cf[N + i];
+    const float dt_pre = sc[N * N + N + i] * hp * (1.f - hp);
+    const float dt_post = sc[N * N + i] * hq * (1.f - 0.5f * hq);
+    float lp = 0.f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        gm[k] *= e[k];  // dt_res
+        lp += gm[k] * pr[k];
+    }
+    lp = group_sum<skb::kLPR>(lp);
+    const float l_pre = dt_pre * pv[i], l_post = dt_post * pv[N + i];
+    // sums over the 32 rows: one lane per row, the wave, then the 4 waves
+    const bool lead = c0 == 0;
+    float v[4] = {ap * l_pre + aq * l_post + ar * lp, l_pre, l_post, lp};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = group_sum<kWave>(lead ? v[k] : 0.f);
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) red[wave][k] = v[k];
+    }
+    float* dp = dp_out + tok * NPT;
+#pragma unroll
+    for (int k = 0; k < V; ++k) dp[2 * N + i * N + c0 + k] = ar * gm[k] * inv;
+    float* pt = part + tok * NV;
+#pragma unroll
+    for (int k = 0; k < V; ++k) pt[2 * N + i * N + c0 + k] = gm[k];
+    if (lead) {
+        dp[i] = ap * dt_pre * inv;
+        dp[N + i] = aq * dt_post * inv;
+        pt[i] = dt_pre;
+        pt[N + i] = dt_post;
+    }
+    for (int o = NP + (int)threadIdx.x; o < NPT; o += skb::kThreads) dp[o] = 0.f;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t[4] = {red[0][0], red[0][1], red[0][2], red[0][3]};
+#pragma unroll
+        for (int w = 1; w < skb::kNW; ++w) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) t[k] += red[w][k];
+        }
+        s_out[tok] = -t[0] * inv * inv * inv / (float)K;
+        pt[NP] = t[1] * inv;
+        pt[NP + 1] = t[2] * inv;
+        pt[NP + 2] = t[3] * inv;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // n = 4: one token per 16-lane DPP row.  Lane l holds element (l/4, l%4) of
 // t_res and, for l < 8, t_pre[l] (l < 4) or t_post[l-4] (the coefficient
 // order), so the Sinkhorn iterations are a few DPP steps per lane
@@ -1125,6 +1262,11 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
                            sk_eps, rms_eps);
         return hipGetLastError();
     }
+    if (n == skb::kN) {
+        hipLaunchKernelGGL(dyn_coef32_fwd_kernel, dim3((unsigned)B), dim3(skb::kThreads), 0, s, p_part, ss_part, ks, B,
+                           K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, iters, sk_eps, rms_eps);
+        return hipGetLastError();
+    }
     const int64_t threads = B * pow2ceil(n);
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     MHC_DYN_N(n, hipLaunchKernelGGL((dyn_coef_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, p_part, ss_part, ks, B,
@@ -1164,6 +1306,11 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
     if (n == 4) {
         hipLaunchKernelGGL(dyn_coef16_bwd_kernel, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K, a_pre, a_post,
                            a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        return hipGetLastError();
+    }
+    if (n == skb::kN && iters <= skb::kTMax) {
+        hipLaunchKernelGGL(dyn_coef32_bwd_kernel, dim3((unsigned)B), dim3(skb::kThreads), 0, s, scal, coef, p, rh, B, K,
+                           a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
         return hipGetLastError();
     }
     if (n >= 16) {

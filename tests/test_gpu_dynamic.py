@@ -128,6 +128,16 @@ def test_dynamic_layer_wide_n(device, x_dtype, n, B, C):
     _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n={n} B={B} C={C} {x_dtype}")
 
 
+@pytest.mark.parametrize("iters", [0, 1, 32, 33])
+def test_dynamic_layer_n32_iteration_counts(device, iters):
+    """n = 32 runs one token per workgroup with the Sinkhorn adjoint's state
+    in registers for up to 32 iterations; 33 takes the lane-group adjoint
+    with its history in the workspace."""
+    d = R.dynamic_layer_inputs(6, 32, 64, seed=3300 + iters, x_dtype=torch.float32, alpha=0.1, phi_std=0.02,
+                               b_std=0.5)
+    _check_dyn(_run_dyn(d, device, iters=iters), _oracle_dyn(d, iters=iters), torch.float32, f"n=32 T={iters}")
+
+
 def test_dynamic_layer_unsupported_n_raises(device):
     layer = mhc.MHCLayer(64, 3, use_dynamic_h=True).to(device)
     with pytest.raises(RuntimeError, match="n=3 is not compiled"):
