@@ -240,7 +240,7 @@ int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const void* weight, int
 
 struct StaticBwdWs {
     int grid;
-    size_t dw_off, scal_off, stage_off, hist_off, total;
+    size_t dw_off, scal_off, stage_off, hist_off, rows_off, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -252,7 +252,8 @@ static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32
     w.scal_off = align256((size_t)w.grid * hidden * sizeof(float));
     w.stage_off = w.scal_off + align256((size_t)w.grid * (n * n + 2 * n) * sizeof(float));
     w.hist_off = w.stage_off + align256(column_sums_stage_floats(hidden) * sizeof(float));
-    w.total = w.hist_off + (n >= 16 ? kStaticSkHistBytes : 0);  // Sinkhorn adjoint history (wide n)
+    w.rows_off = w.hist_off + (n >= 16 ? kStaticSkHistBytes : 0);  // Sinkhorn adjoint history (wide n)
+    w.total = w.rows_off + align256(batch > 0 ? layer_bwd_scratch_bytes(x_dtype, n, batch, hidden) : 0);
     return w;
 }
 
@@ -289,7 +290,8 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
         if (e == hipSuccess) e = launch_fill_zero(scal_part, n * n + 2 * n, s);
     } else {
         e = launch_layer_bwd(x_dtype, n, 0, grad_out, x, saved + saved_w_offset(n), saved, 0, grad_x, dw_part,
-                             scal_part, w.grid, batch, hidden, rmsnorm_eps, s);
+                             scal_part, w.grid, batch, hidden, rmsnorm_eps, (float*)((char*)workspace + w.rows_off),
+                             s);
     }
     if (e == hipSuccess)
         e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stage, grad_weight, scal_part, rows, h_pre,
@@ -725,7 +727,8 @@ static bool dyn_bwd_f32_acc(int32_t n, int32_t x_dtype) { return x_dtype == kBF1
 struct DynBwdWs {
     int grid, cblocks, tiles;
     int wdt;  // element type the row and projection kernels run on
-    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, hist_off, total;
+    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, hist_off, rows_off,
+        total;
 };
 
 static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
@@ -749,6 +752,7 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     w.xw_off = o; o += align256(acc);
     w.dxw_off = o; o += align256(acc);
     w.hist_off = o; o += n >= 16 && batch > 0 ? kSkHistBytes : 0;  // Sinkhorn adjoint history
+    w.rows_off = o; o += align256(batch > 0 ? layer_bwd_scratch_bytes(w.wdt, n, batch, hidden) : 0);
     w.total = o;
     return w;
 }
@@ -808,7 +812,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         if (w.wdt != x_dtype) e = launch_weight_f32(x, x_dtype, batch * K, xw, s);
         if (e == hipSuccess)
             e = launch_layer_bwd(w.wdt, n, 1, grad_out, xk, w32, saved + d.coef_off, np, dxk, dw_part, scal, w.grid,
-                                 batch, hidden, rmsnorm_eps, s);
+                                 batch, hidden, rmsnorm_eps, (float*)(ws + w.rows_off), s);
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,

@@ -753,13 +753,17 @@ int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
     return persistent_grid(pick_bwd(x_dtype, n, t.vpt, 0, use_prefetch(t)), t.threads, B);
 }
 
+size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C) {
+    return bwd_tiling(C, n, x_dtype).vpt <= 0 ? wide_bwd_scratch_bytes(n, B, C) : 0;
+}
+
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
-                            int grid, int64_t B, int64_t C, float eps, hipStream_t s) {
+                            int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s) {
     const RowTiling t = bwd_tiling(C, n, x_dtype);
     if (t.vpt <= 0)
         return launch_wide_bwd(x_dtype, n, mode, g, x, w, coef, coef_stride, dx, dw_part, scal_out, grid, B, C, eps,
-                               s);
+                               scratch, s);
     const void* fn = pick_bwd(x_dtype, n, t.vpt, mode, use_prefetch(t));
     if (!fn) return hipErrorInvalidValue;
     int Ci = (int)C;

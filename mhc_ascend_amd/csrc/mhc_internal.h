@@ -50,10 +50,13 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
 //         dh_pre_act] into scal_out[grid][n*n+2n]);
 // mode 1: dx = stream terms only, and per token scal_out[B][n*n+2n+2] =
 //         dM, dh_post_act, dh_pre_act, inv_rms, k2.
+// scratch: layer_bwd_scratch_bytes (the channel-chunked wide backward's
+// partial row sums; 0 bytes and unused otherwise).
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
-                            int grid, int64_t B, int64_t C, float eps, hipStream_t s);
+                            int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s);
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
+size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C);
 // Whether the layer forward / backward of (n, C) runs the channel-loop
 // kernels of wide.hip rather than the register rows.
 bool layer_fwd_is_wide(int n, int64_t C);
@@ -89,12 +92,17 @@ bool wide_supported(int n, int64_t C);
 hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
                            int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
                            hipStream_t s);
+// Partial rows of the backward (mode 0 scalar rows and dw rows): the
+// persistent grid, or one per token when a token's channels are split over
+// several workgroups (few tokens); then the launch needs scratch of
+// wide_bwd_scratch_bytes (0 otherwise).
 int wide_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
+size_t wide_bwd_scratch_bytes(int n, int64_t B, int64_t C);
 // Same outputs as launch_layer_bwd (mode 0 / 1); for n >= 16 the dM entries
 // come from a second kernel on the same stream.
 hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                            const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out, int grid,
-                           int64_t B, int64_t C, float eps, hipStream_t s);
+                           int64_t B, int64_t C, float eps, float* scratch, hipStream_t s);
 // Standalone operators on rows of any width, n in {1, 2, 4, 8, 16, 32}
 // (same outputs as the launch_* of ops.hip; the RMSNorm backward's dw
 // partial rows [grid][C] come from wide_rmsnorm_bwd_grid, C <= kWideMaxC).

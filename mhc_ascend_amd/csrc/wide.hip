@@ -65,57 +65,172 @@ __device__ __forceinline__ void wide_block_total(float (&v)[NV], float* red, flo
 }
 
 // ---------------------------------------------------------------------------
-// Forward: one token per workgroup (grid = tokens); out in TO (fp32, or bf16
-// for the forward-only entry); rms_out[b] = r when not null.
+// Forward: one workgroup per (token b, channel chunk s).  Its row sum of
+// xa^2 runs over the whole token, so no workgroup waits for another and no
+// scratch is needed; the outputs are its chunk's.  With S > 1 chunks the
+// token's S workgroups are placed on one XCD (workgroups go round-robin over
+// the 8 XCDs by linear id: id = 8 (S t + s) + xcd for token b = 8 t + xcd),
+// so all but the first read the row from that XCD's L2.  Two channels per
+// lane and step keep 2 N loads in flight.  out in TO (fp32, or bf16 for the
+// forward-only entry); rms_out[b] = r when not null (chunk 0).
 // ---------------------------------------------------------------------------
 template <typename TX, typename TO, int N>
 __global__ __launch_bounds__(kWideThreads) void wide_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
                                                                 const float* __restrict__ coef, int64_t coef_stride,
                                                                 TO* __restrict__ out, float* __restrict__ rms_out,
-                                                                int64_t B, int C, float eps) {
+                                                                int64_t B, int C, float eps, int S, int chunk) {
+    constexpr int NC = 2 * N + N * N;
     __shared__ float red[kWideThreads / kWave];
     __shared__ float tot[1];
-    const int64_t b = blockIdx.x;
+    __shared__ float cfs[NC];
+    int64_t b = blockIdx.x;
+    int sc = 0;
+    if (S > 1) {
+        const int64_t k = blockIdx.x / 8;
+        b = (k / S) * 8 + blockIdx.x % 8;
+        sc = (int)(k % S);
+    }
     if (b >= B) return;
     const float* cf = coef + b * coef_stride;
+    // the coefficients go to LDS for the output pass (read there, all lanes
+    // one address, instead of one dependent scalar load round per output row)
+    for (int k = threadIdx.x; k < NC; k += blockDim.x) cfs[k] = cf[k];
     const TX* xb = x + b * (int64_t)N * C;
     float ss[1] = {0.f};
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
-        float xa = 0.f;
+    {
+        const int step = 2 * (int)blockDim.x;
+        int c = threadIdx.x;
+        for (; c + (int)blockDim.x < C; c += step) {
+            float xa0 = 0.f, xa1 = 0.f;
 #pragma unroll
-        for (int j = 0; j < N; ++j) xa += cf[j] * VecIO<TX>::scalar(xb + (int64_t)j * C + c);
-        ss[0] += xa * xa;
+            for (int j = 0; j < N; ++j) {
+                xa0 += cf[j] * VecIO<TX>::scalar(xb + (int64_t)j * C + c);
+                xa1 += cf[j] * VecIO<TX>::scalar(xb + (int64_t)j * C + c + blockDim.x);
+            }
+            ss[0] += xa0 * xa0;
+            ss[0] += xa1 * xa1;
+        }
+        if (c < C) {
+            float xa = 0.f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) xa += cf[j] * VecIO<TX>::scalar(xb + (int64_t)j * C + c);
+            ss[0] += xa * xa;
+        }
     }
     wide_block_total<1>(ss, red, tot);
     const float r = sqrtf(tot[0] / (float)C + eps);
     const float inv = 1.f / r;
     TO* ob = out + b * (int64_t)N * C;
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const int c_end = (sc + 1) * chunk < C ? (sc + 1) * chunk : C;
+    for (int c = sc * chunk + threadIdx.x; c < c_end; c += blockDim.x) {
         float xv[N];
 #pragma unroll
         for (int j = 0; j < N; ++j) xv[j] = ld_elem_nt(xb + (int64_t)j * C + c);
         float xa = 0.f;
 #pragma unroll
-        for (int j = 0; j < N; ++j) xa += cf[j] * xv[j];
+        for (int j = 0; j < N; ++j) xa += cfs[j] * xv[j];
         const float y = xa * inv * w[c];
+#pragma unroll 4
         for (int i = 0; i < N; ++i) {
-            float s = cf[N + i] * y;
+            float s = cfs[N + i] * y;
 #pragma unroll
-            for (int j = 0; j < N; ++j) s += cf[2 * N + i * N + j] * xv[j];
+            for (int j = 0; j < N; ++j) s += cfs[2 * N + i * N + j] * xv[j];
             st_elem_nt(ob + (int64_t)i * C + c, s);
         }
     }
-    if (threadIdx.x == 0 && rms_out) rms_out[b] = r;
+    if (threadIdx.x == 0 && sc == 0 && rms_out) rms_out[b] = r;
+}
+
+// ---------------------------------------------------------------------------
+// Backward pieces shared by the persistent and the chunked kernels.
+// Row sums per channel (NR of them): ss, dot, t_i, u_j, v_j (, dM_ij).
+// Per-token scalar entries (layout [dM | dh_post | dh_pre | 1/r | k2]) from
+// the row totals; dx of one channel (returns its dw term gy xa / r).
+// ---------------------------------------------------------------------------
+template <int N, bool DM> constexpr int wide_nr() { return 2 + 3 * N + (DM ? N * N : 0); }
+
+template <typename TX, int N, bool DM>
+__device__ __forceinline__ void wide_bwd_accum(const float* __restrict__ cf, const TX* __restrict__ xb,
+                                               const float* __restrict__ gb, const float* __restrict__ w, int c,
+                                               int C, float (&rv)[wide_nr<N, DM>()]) {
+    float xv[N], gv[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        xv[j] = VecIO<TX>::scalar(xb + (int64_t)j * C + c);
+        gv[j] = gb[(int64_t)j * C + c];
+    }
+    float xa = 0.f, gy = 0.f;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        xa += cf[j] * xv[j];
+        gy += cf[N + j] * gv[j];
+    }
+    const float wc = w[c];
+    const float wgy = wc * gy, wxa = wc * xa;
+    rv[0] += xa * xa;
+    rv[1] += wgy * xa;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        rv[2 + i] += gv[i] * wxa;
+        rv[2 + N + i] += wgy * xv[i];
+        rv[2 + 2 * N + i] += xa * xv[i];
+    }
+    if constexpr (DM) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+#pragma unroll
+            for (int j = 0; j < N; ++j) rv[2 + 3 * N + i * N + j] += gv[i] * xv[j];
+        }
+    }
+}
+
+template <int N>
+__device__ __forceinline__ float wide_bwd_scalar(const float* tot, int t, float inv, float k2) {
+    constexpr int NS = N * N + 2 * N;
+    if (t < N * N) return tot[2 + 3 * N + t];
+    if (t < N * N + N) return tot[2 + t - N * N] * inv;  // dh_post_act
+    if (t < NS) {
+        const int j = t - N * N - N;
+        return inv * tot[2 + N + j] - k2 * tot[2 + 2 * N + j];  // dh_pre_act
+    }
+    return t == NS ? inv : k2;
+}
+
+template <typename TX, int N>
+__device__ __forceinline__ float wide_bwd_dx(const float* __restrict__ cf, const TX* __restrict__ xb,
+                                             const float* __restrict__ gb, const float* __restrict__ w,
+                                             TX* __restrict__ db, int c, int C, float inv, float k2) {
+    float xv[N], gv[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        xv[j] = ld_elem_nt(xb + (int64_t)j * C + c);
+        gv[j] = ld_elem_nt(gb + (int64_t)j * C + c);
+    }
+    float xa = 0.f, gy = 0.f;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        xa += cf[j] * xv[j];
+        gy += cf[N + j] * gv[j];
+    }
+    const float gxa = w[c] * gy * inv - xa * k2;
+#pragma unroll 4
+    for (int j = 0; j < N; ++j) {
+        float s = cf[j] * gxa;
+#pragma unroll
+        for (int i = 0; i < N; ++i) s += cf[2 * N + i * N + j] * gv[i];
+        st_elem_nt(db + (int64_t)j * C + c, s);
+    }
+    return gy * xa * inv;
 }
 
 // ---------------------------------------------------------------------------
 // Backward.  Persistent workgroups stride over tokens; the workgroup's dw
 // partial lives in LDS (dynamic shared memory, C floats, each entry owned by
 // the lane that owns the channel) and goes to dw_part[blockIdx.x][C] at the
-// end.  Per-token scalars as in layer.hip (layout [dM | dh_post | dh_pre |
-// 1/r | k2]): MODE 0 sums them per workgroup into scal_out[blockIdx.x][NS],
-// MODE 1 writes them per token into scal_out[b][NS + 2].  With DM false the
-// dM entries are left to stream_gram_kernel.
+// end.  Per-token scalars: MODE 0 sums them per workgroup into
+// scal_out[blockIdx.x][NS], MODE 1 writes them per token into
+// scal_out[b][NS + 2].  With DM false the dM entries are left to
+// stream_gram_kernel.
 // ---------------------------------------------------------------------------
 template <typename TX, int N, int MODE, bool DM>
 __global__ __launch_bounds__(kWideThreads) void wide_bwd_kernel(const float* __restrict__ g, const TX* __restrict__ x,
@@ -126,7 +241,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_bwd_kernel(const float* __r
                                                                 float eps) {
     extern __shared__ float dws[];
     constexpr int NS = N * N + 2 * N;
-    constexpr int NR = 2 + 3 * N + (DM ? N * N : 0);  // ss, dot, t_i, u_j, v_j (, dM)
+    constexpr int NR = wide_nr<N, DM>();
     // scalar entries this kernel writes: E0 .. NS + 1, one per lane
     constexpr int E0 = DM ? 0 : N * N;
     constexpr int NE = NS + 2 - E0;
@@ -137,61 +252,23 @@ __global__ __launch_bounds__(kWideThreads) void wide_bwd_kernel(const float* __r
     for (int c = tid; c < C; c += blockDim.x) dws[c] = 0.f;
     float sacc = 0.f;
     const int64_t NCs = (int64_t)N * C;
+    __shared__ float cfs[2 * N + N * N];
     for (int64_t b = blockIdx.x; b < B; b += gridDim.x) {
         const float* cf = coef + b * coef_stride;
         const TX* xb = x + b * NCs;
         const float* gb = g + b * NCs;
+        for (int k = tid; k < 2 * N + N * N; k += blockDim.x) cfs[k] = cf[k];
         float rv[NR];
 #pragma unroll
         for (int k = 0; k < NR; ++k) rv[k] = 0.f;
-        for (int c = tid; c < C; c += blockDim.x) {
-            float xv[N], gv[N];
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                xv[j] = VecIO<TX>::scalar(xb + (int64_t)j * C + c);
-                gv[j] = gb[(int64_t)j * C + c];
-            }
-            float xa = 0.f, gy = 0.f;
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                xa += cf[j] * xv[j];
-                gy += cf[N + j] * gv[j];
-            }
-            const float wc = w[c];
-            const float wgy = wc * gy, wxa = wc * xa;
-            rv[0] += xa * xa;
-            rv[1] += wgy * xa;
-#pragma unroll
-            for (int i = 0; i < N; ++i) {
-                rv[2 + i] += gv[i] * wxa;
-                rv[2 + N + i] += wgy * xv[i];
-                rv[2 + 2 * N + i] += xa * xv[i];
-            }
-            if constexpr (DM) {
-#pragma unroll
-                for (int i = 0; i < N; ++i) {
-#pragma unroll
-                    for (int j = 0; j < N; ++j) rv[2 + 3 * N + i * N + j] += gv[i] * xv[j];
-                }
-            }
-        }
+        for (int c = tid; c < C; c += blockDim.x) wide_bwd_accum<TX, N, DM>(cf, xb, gb, w, c, C, rv);
         wide_block_total<NR>(rv, red, tot);
         const float r = sqrtf(tot[0] / (float)C + eps);
         const float inv = 1.f / r;
         const float k2 = tot[1] * inv * inv * inv / (float)C;
         if (tid < NE) {
             const int t = E0 + tid;
-            float v;
-            if (t < N * N) {
-                v = tot[2 + 3 * N + t];
-            } else if (t < N * N + N) {
-                v = tot[2 + t - N * N] * inv;  // dh_post_act
-            } else if (t < NS) {
-                const int j = t - N * N - N;
-                v = inv * tot[2 + N + j] - k2 * tot[2 + 2 * N + j];  // dh_pre_act
-            } else {
-                v = t == NS ? inv : k2;
-            }
+            const float v = wide_bwd_scalar<N>(tot, t, inv, k2);
             if (MODE == 0) {
                 sacc += v;
             } else {
@@ -199,28 +276,8 @@ __global__ __launch_bounds__(kWideThreads) void wide_bwd_kernel(const float* __r
             }
         }
         TX* db = dx + b * NCs;
-        for (int c = tid; c < C; c += blockDim.x) {
-            float xv[N], gv[N];
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                xv[j] = ld_elem_nt(xb + (int64_t)j * C + c);
-                gv[j] = ld_elem_nt(gb + (int64_t)j * C + c);
-            }
-            float xa = 0.f, gy = 0.f;
-#pragma unroll
-            for (int j = 0; j < N; ++j) {
-                xa += cf[j] * xv[j];
-                gy += cf[N + j] * gv[j];
-            }
-            const float gxa = w[c] * gy * inv - xa * k2;
-            dws[c] += gy * xa * inv;
-            for (int j = 0; j < N; ++j) {
-                float s = cf[j] * gxa;
-#pragma unroll
-                for (int i = 0; i < N; ++i) s += cf[2 * N + i * N + j] * gv[i];
-                st_elem_nt(db + (int64_t)j * C + c, s);
-            }
-        }
+        for (int c = tid; c < C; c += blockDim.x) dws[c] += wide_bwd_dx<TX, N>(cfs, xb, gb, w, db, c, C, inv, k2);
+        __syncthreads();  // cfs is restaged for the next token
     }
     float* dwp = dw_part + (int64_t)blockIdx.x * C;
     for (int c = tid; c < C; c += blockDim.x) dwp[c] = dws[c];
@@ -228,70 +285,241 @@ __global__ __launch_bounds__(kWideThreads) void wide_bwd_kernel(const float* __r
 }
 
 // ---------------------------------------------------------------------------
-// dM_ij = sum_c g_i x_j of one token (n >= 16): 64-channel tiles of g and x
-// staged in LDS, each of the (n/2)^2 lanes forming a 2 x 2 block of dM.
-// MODE 0 sums over the workgroup's tokens (same persistent grid as
-// wide_bwd_kernel) into scal_out[blockIdx.x][0 .. n^2); MODE 1 writes each
-// token's dM to scal_out[b * ostride + 0 .. n^2).  Fixed summation order.
+// Backward over channel chunks, for fewer tokens than fill the chip:
+// workgroup (b, s) of grid B x S takes token b's channel chunk s.  The first
+// kernel stores the chunk's row sums in part[b][s][NR]; the second adds a
+// token's S partials in chunk order, forms the per-token scalars (chunk 0
+// stores them: MODE 1 per token as wide_bwd_kernel, MODE 0 as row b of
+// scal_out[B][NS]) and the chunk's dx and dw terms (row b of dw_part[B][C]).
+// Same outputs as wide_bwd_kernel with one token per workgroup.
 // ---------------------------------------------------------------------------
-template <int N> constexpr int gram_threads() { return (N / 2) * (N / 2); }
-
-template <typename TX, int N, int MODE>
-__global__ __launch_bounds__(gram_threads<N>()) void stream_gram_kernel(const float* __restrict__ g,
-                                                                        const TX* __restrict__ x,
-                                                                        float* __restrict__ scal_out, int64_t B,
-                                                                        int C, int64_t ostride) {
-    constexpr int CT = 64;
-    constexpr int T = gram_threads<N>();
-    constexpr int NS = N * N + 2 * N;
-    __shared__ float gs[N][CT + 1];
-    __shared__ float xs[N][CT + 1];
-    const int tid = threadIdx.x;
-    const int i0 = 2 * (tid / (N / 2));
-    const int j0 = 2 * (tid % (N / 2));
-    float acc[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+template <typename TX, int N, bool DM>
+__global__ __launch_bounds__(kWideThreads) void wide_bwd_sums_kernel(const float* __restrict__ g,
+                                                                     const TX* __restrict__ x,
+                                                                     const float* __restrict__ w,
+                                                                     const float* __restrict__ coef,
+                                                                     int64_t coef_stride, float* __restrict__ part,
+                                                                     int64_t B, int C, int S, int chunk) {
+    constexpr int NR = wide_nr<N, DM>();
+    __shared__ float red[(kWideThreads / kWave) * NR];
+    __shared__ float tot[NR];
+    const int64_t b = blockIdx.x / S;
+    const int sc = (int)(blockIdx.x % S);
+    if (b >= B) return;
     const int64_t NCs = (int64_t)N * C;
+    const float* cf = coef + b * coef_stride;
+    const TX* xb = x + b * NCs;
+    const float* gb = g + b * NCs;
+    float rv[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) rv[k] = 0.f;
+    const int c_end = (sc + 1) * chunk < C ? (sc + 1) * chunk : C;
+    for (int c = sc * chunk + (int)threadIdx.x; c < c_end; c += blockDim.x)
+        wide_bwd_accum<TX, N, DM>(cf, xb, gb, w, c, C, rv);
+    wide_block_total<NR>(rv, red, tot);
+    for (int k = threadIdx.x; k < NR; k += blockDim.x) part[((int64_t)blockIdx.x) * NR + k] = tot[k];
+}
+
+template <typename TX, int N, int MODE, bool DM>
+__global__ __launch_bounds__(kWideThreads) void wide_bwd_out_kernel(
+    const float* __restrict__ g, const TX* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ coef, int64_t coef_stride, TX* __restrict__ dx, float* __restrict__ dw_part,
+    float* __restrict__ scal_out, const float* __restrict__ part, int64_t B, int C, float eps, int S, int chunk) {
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NR = wide_nr<N, DM>();
+    constexpr int E0 = DM ? 0 : N * N;
+    constexpr int NE = NS + 2 - E0;
+    static_assert(NE <= kWideThreads && NR <= kWideThreads, "one entry per lane");
+    __shared__ float tot[NR];
+    __shared__ float cfs[2 * N + N * N];
+    const int64_t b = blockIdx.x / S;
+    const int sc = (int)(blockIdx.x % S);
+    if (b >= B) return;
+    const int tid = threadIdx.x;
+    for (int k = tid; k < 2 * N + N * N; k += blockDim.x) cfs[k] = coef[b * coef_stride + k];
+    if (tid < NR) {
+        const float* pb = part + b * S * NR + tid;
+        float v = 0.f;
+        for (int q = 0; q < S; ++q) v += pb[(int64_t)q * NR];
+        tot[tid] = v;
+    }
+    __syncthreads();
+    const float r = sqrtf(tot[0] / (float)C + eps);
+    const float inv = 1.f / r;
+    const float k2 = tot[1] * inv * inv * inv / (float)C;
+    if (sc == 0 && tid < NE) {
+        const int t = E0 + tid;
+        const float v = wide_bwd_scalar<N>(tot, t, inv, k2);
+        if (MODE == 1) {
+            scal_out[b * (NS + 2) + t] = v;
+        } else if (t < NS) {
+            scal_out[b * NS + t] = v;
+        }
+    }
+    const int64_t NCs = (int64_t)N * C;
+    const TX* xb = x + b * NCs;
+    const float* gb = g + b * NCs;
+    TX* db = dx + b * NCs;
+    float* dwp = dw_part + b * C;
+    const int c_end = (sc + 1) * chunk < C ? (sc + 1) * chunk : C;
+    for (int c = sc * chunk + tid; c < c_end; c += blockDim.x)
+        dwp[c] = wide_bwd_dx<TX, N>(cfs, xb, gb, w, db, c, C, inv, k2);
+}
+
+// ---------------------------------------------------------------------------
+// dM_ij = sum_c g_i x_j of each token (n = 16, 32) on the fp32 matrix cores:
+// v_mfma_f32_32x32x2_f32 (n = 32) or v_mfma_f32_16x16x4_f32 (n = 16) with
+// A = g (row i = stream i), B = x^T and k = channel.  Lane l holds stream
+// i = l % n in k slot h = l / n (KQ = 64 / n slots).  A step of a wave loads
+// 16 consecutive channels of g_i and x_i at c0 + 16 h (16 KQ channels per
+// step) and issues 16 MFMAs, product q taking channel c0 + 16 h + q in slot
+// h; steps go round-robin to the 4 waves, the next one in flight while the
+// current one is on the matrix cores.  The waves' partial matrices are
+// added through LDS in wave order.  MODE 0 sums the workgroup's tokens
+// (strided over the grid, as wide_bwd_kernel's) into
+// scal_out[blockIdx.x][0 .. n^2); MODE 1 stores each token's dM at
+// scal_out[b * ostride + 0 .. n^2).  VEC: 16-byte loads (C % 8 == 0 and
+// aligned rows), else element loads.
+// ---------------------------------------------------------------------------
+typedef float gram_f32x16_t __attribute__((ext_vector_type(16)));
+typedef float gram_f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int N> struct GramMfma;
+template <> struct GramMfma<32> {
+    using acc_t = gram_f32x16_t;
+    static constexpr int R = 16;  // accumulator registers per lane
+    __device__ __forceinline__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+    // element (row, col) of D held in register r of lane l
+    __device__ __forceinline__ static int row(int l, int r) { return 8 * (r / 4) + 4 * (l / 32) + (r % 4); }
+    __device__ __forceinline__ static int col(int l) { return l % 32; }
+};
+template <> struct GramMfma<16> {
+    using acc_t = gram_f32x4_t;
+    static constexpr int R = 4;
+    __device__ __forceinline__ static acc_t step(float a, float b, acc_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+    __device__ __forceinline__ static int row(int l, int r) { return 4 * (l / 16) + r; }
+    __device__ __forceinline__ static int col(int l) { return l % 16; }
+};
+
+// 16 consecutive channels c .. c + 15 of one row as floats; channels past C
+// read zero.  VEC: C % 8 == 0 and 16-byte aligned rows, so each 16-byte
+// piece is wholly inside or outside the row.
+template <typename T, bool VEC>
+__device__ __forceinline__ void gram_load16(const T* __restrict__ row, int c, int C, float (&v)[16]) {
+    if constexpr (VEC) {
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (c + 4 * u < C) q = *reinterpret_cast<const float4*>(row + c + 4 * u);
+                v[4 * u] = q.x;
+                v[4 * u + 1] = q.y;
+                v[4 * u + 2] = q.z;
+                v[4 * u + 3] = q.w;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                uint4 q = make_uint4(0u, 0u, 0u, 0u);
+                if (c + 8 * u < C) q = *reinterpret_cast<const uint4*>(row + c + 8 * u);
+                const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[8 * u + 2 * e] = __uint_as_float(wv[e] << 16);
+                    v[8 * u + 2 * e + 1] = __uint_as_float(wv[e] & 0xffff0000u);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) v[q] = (c + q < C) ? VecIO<T>::scalar(row + c + q) : 0.f;
+    }
+}
+
+template <typename TX, int N, int MODE, bool VEC>
+__global__ __launch_bounds__(kWideThreads) void stream_gram_kernel(const float* __restrict__ g,
+                                                                  const TX* __restrict__ x,
+                                                                  float* __restrict__ scal_out, int64_t B, int C,
+                                                                  int64_t ostride) {
+    using M = GramMfma<N>;
+    using acc_t = typename M::acc_t;
+    constexpr int KQ = kWave / N;       // k slots per MFMA
+    constexpr int SC = 16 * KQ;         // channels per wave step
+    constexpr int NW = kWideThreads / kWave;
+    constexpr int NS = N * N + 2 * N;
+    __shared__ float red[NW - 1][M::R][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int i = lane % N, h = lane / N;
+    const int nsteps = (C + SC - 1) / SC;
+    const int64_t NCs = (int64_t)N * C;
+    acc_t acc = {};
     for (int64_t b = blockIdx.x; b < B; b += gridDim.x) {
-        if (MODE == 1) {
-            acc[0][0] = acc[0][1] = acc[1][0] = acc[1][1] = 0.f;
+        if (MODE == 1) acc = acc_t{};
+        const float* gr = g + b * NCs + (int64_t)i * C;
+        const TX* xr = x + b * NCs + (int64_t)i * C;
+        float ga[16], xa[16];
+        int st = wave;
+        if (st < nsteps) {
+            gram_load16<float, VEC>(gr, st * SC + 16 * h, C, ga);
+            gram_load16<TX, VEC>(xr, st * SC + 16 * h, C, xa);
         }
-        const float* gb = g + b * NCs;
-        const TX* xb = x + b * NCs;
-        for (int c0 = 0; c0 < C; c0 += CT) {
-            for (int e = tid; e < N * CT; e += T) {
-                const int row = e / CT;
-                const int cc = e - row * CT;
-                const int c = c0 + cc;
-                const bool ok = c < C;
-                gs[row][cc] = ok ? gb[(int64_t)row * C + c] : 0.f;
-                xs[row][cc] = ok ? VecIO<TX>::scalar(xb + (int64_t)row * C + c) : 0.f;
+        for (; st < nsteps; st += NW) {
+            float gn[16], xn[16];
+            const int nx = st + NW;
+            if (nx < nsteps) {
+                gram_load16<float, VEC>(gr, nx * SC + 16 * h, C, gn);
+                gram_load16<TX, VEC>(xr, nx * SC + 16 * h, C, xn);
+            }
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc = M::step(ga[q], xa[q], acc);
+            if (nx < nsteps) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    ga[q] = gn[q];
+                    xa[q] = xn[q];
+                }
+            }
+        }
+        if (MODE == 1) {
+            if (wave > 0) {
+#pragma unroll
+                for (int r = 0; r < M::R; ++r) red[wave - 1][r][lane] = acc[r];
             }
             __syncthreads();
-#pragma unroll 8
-            for (int cc = 0; cc < CT; ++cc) {
-                const float g0 = gs[i0][cc], g1 = gs[i0 + 1][cc];
-                const float x0 = xs[j0][cc], x1 = xs[j0 + 1][cc];
-                acc[0][0] += g0 * x0;
-                acc[0][1] += g0 * x1;
-                acc[1][0] += g1 * x0;
-                acc[1][1] += g1 * x1;
+            if (wave == 0) {
+                float* o = scal_out + b * ostride;
+#pragma unroll
+                for (int r = 0; r < M::R; ++r) {
+                    float v = acc[r];
+#pragma unroll
+                    for (int q = 0; q < NW - 1; ++q) v += red[q][r][lane];
+                    o[M::row(lane, r) * N + M::col(lane)] = v;
+                }
             }
             __syncthreads();
-        }
-        if (MODE == 1) {
-            float* o = scal_out + b * ostride;
-            o[i0 * N + j0] = acc[0][0];
-            o[i0 * N + j0 + 1] = acc[0][1];
-            o[(i0 + 1) * N + j0] = acc[1][0];
-            o[(i0 + 1) * N + j0 + 1] = acc[1][1];
         }
     }
     if (MODE == 0) {
-        float* o = scal_out + (int64_t)blockIdx.x * NS;
-        o[i0 * N + j0] = acc[0][0];
-        o[i0 * N + j0 + 1] = acc[0][1];
-        o[(i0 + 1) * N + j0] = acc[1][0];
-        o[(i0 + 1) * N + j0 + 1] = acc[1][1];
+        if (wave > 0) {
+#pragma unroll
+            for (int r = 0; r < M::R; ++r) red[wave - 1][r][lane] = acc[r];
+        }
+        __syncthreads();
+        if (wave == 0) {
+            float* o = scal_out + (int64_t)blockIdx.x * NS;
+#pragma unroll
+            for (int r = 0; r < M::R; ++r) {
+                float v = acc[r];
+#pragma unroll
+                for (int q = 0; q < NW - 1; ++q) v += red[q][r][lane];
+                o[M::row(lane, r) * N + M::col(lane)] = v;
+            }
+        }
     }
 }
 
@@ -622,17 +850,29 @@ bool wide_supported(int n, int64_t C) {
     return (n == 2 || n == 4 || n == 8 || n == 16 || n == 32) && C >= 1 && C <= kWideMaxC;
 }
 
+// Channel chunks per token: one chunk of kWideThreads channels per
+// workgroup (one channel per lane) when there are fewer tokens than two
+// workgroups per CU, else whole rows.
+static int wide_fwd_chunks(int64_t B, int64_t C) {
+    if (B >= 2 * (int64_t)device_cu_count()) return 1;
+    const int64_t S = (C + kWideThreads - 1) / kWideThreads;
+    return (int)(S < 1 ? 1 : S);
+}
+
 hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
                            int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
                            hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!wide_supported(n, C) || B > 0x7fffffff) return hipErrorInvalidValue;
     const int Ci = (int)C;
-    const dim3 grid((unsigned)B), block(kWideThreads);
+    const int S = wide_fwd_chunks(B, C);
+    const int chunk = (int)((C + S - 1) / S);
+    // with chunks, the token count is rounded up to whole XCD rounds
+    const dim3 grid((unsigned)(S > 1 ? ((B + 7) / 8) * 8 * S : B)), block(kWideThreads);
     const int tok = timing_begin("layer_fwd", s);
 #define MHC_WIDE_FWD(TX_, TO_)                                                                                   \
     MHC_WIDE_N(n, hipLaunchKernelGGL((wide_fwd_kernel<TX_, TO_, N_>), grid, block, 0, s, (const TX_*)x, w, coef, \
-                                     coef_stride, (TO_*)out, rms_out, B, Ci, eps))
+                                     coef_stride, (TO_*)out, rms_out, B, Ci, eps, S, chunk))
     if (x_dtype == kBF16) {
         if (out_dtype == kBF16) { MHC_WIDE_FWD(bf16_t, bf16_t); } else { MHC_WIDE_FWD(bf16_t, float); }
     } else {
@@ -648,8 +888,21 @@ static const void* wide_bwd_fn() {
     return reinterpret_cast<const void*>(&wide_bwd_kernel<TX, N, MODE, (N <= 8)>);
 }
 
+// Channel chunks of the backward: as the forward's, used only when a token
+// splits into at least two chunks (then the partial rows are one per token).
+static int wide_bwd_chunks(int64_t B, int64_t C) { return wide_fwd_chunks(B, C); }
+
+size_t wide_bwd_scratch_bytes(int n, int64_t B, int64_t C) {
+    if (!wide_supported(n, C) || B <= 0) return 0;
+    const int S = wide_bwd_chunks(B, C);
+    if (S < 2) return 0;
+    const int nr = 2 + 3 * n + (n <= 8 ? n * n : 0);
+    return (size_t)B * S * nr * sizeof(float);
+}
+
 int wide_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
     if (!wide_supported(n, C) || B <= 0) return 1;
+    if (wide_bwd_chunks(B, C) >= 2) return (int)B;
     const void* fn = nullptr;
     auto pick = [&]() -> hipError_t {
         if (x_dtype == kBF16) {
@@ -674,35 +927,68 @@ int wide_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
 
 hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                            const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out, int grid,
-                           int64_t B, int64_t C, float eps, hipStream_t s) {
+                           int64_t B, int64_t C, float eps, float* scratch, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!wide_supported(n, C) || grid < 1 || (mode != 0 && mode != 1)) return hipErrorInvalidValue;
     const int Ci = (int)C;
-    const size_t lds = (size_t)C * sizeof(float);
+    const int S = wide_bwd_chunks(B, C);
     const int tok = timing_begin(mode == 0 ? "layer_bwd" : "layer_bwd_reduce", s);
+    if (S >= 2) {
+        // chunked: the partial rows are one per token
+        if (!scratch || grid != B) return hipErrorInvalidValue;
+        const int chunk = (int)((C + S - 1) / S);
+        const dim3 cgrid((unsigned)(B * S));
+#define MHC_WIDE_BWD2(TX_, M_)                                                                                     \
+    MHC_WIDE_N(n, {                                                                                                 \
+        hipLaunchKernelGGL((wide_bwd_sums_kernel<TX_, N_, (N_ <= 8)>), cgrid, dim3(kWideThreads), 0, s, g,          \
+                           (const TX_*)x, w, coef, coef_stride, scratch, B, Ci, S, chunk);                          \
+        hipLaunchKernelGGL((wide_bwd_out_kernel<TX_, N_, M_, (N_ <= 8)>), cgrid, dim3(kWideThreads), 0, s, g,       \
+                           (const TX_*)x, w, coef, coef_stride, (TX_*)dx, dw_part, scal_out, scratch, B, Ci, eps,  \
+                           S, chunk);                                                                               \
+    })
+        if (x_dtype == kBF16) {
+            if (mode == 0) { MHC_WIDE_BWD2(bf16_t, 0); } else { MHC_WIDE_BWD2(bf16_t, 1); }
+        } else {
+            if (mode == 0) { MHC_WIDE_BWD2(float, 0); } else { MHC_WIDE_BWD2(float, 1); }
+        }
+#undef MHC_WIDE_BWD2
+    } else {
+        const size_t lds = (size_t)C * sizeof(float);
 #define MHC_WIDE_BWD(TX_, M_)                                                                                      \
     MHC_WIDE_N(n, hipLaunchKernelGGL((wide_bwd_kernel<TX_, N_, M_, (N_ <= 8)>), dim3(grid), dim3(kWideThreads), lds, \
                                      s, g, (const TX_*)x, w, coef, coef_stride, (TX_*)dx, dw_part, scal_out, B, Ci,  \
                                      eps))
-    if (x_dtype == kBF16) {
-        if (mode == 0) { MHC_WIDE_BWD(bf16_t, 0); } else { MHC_WIDE_BWD(bf16_t, 1); }
-    } else {
-        if (mode == 0) { MHC_WIDE_BWD(float, 0); } else { MHC_WIDE_BWD(float, 1); }
-    }
+        if (x_dtype == kBF16) {
+            if (mode == 0) { MHC_WIDE_BWD(bf16_t, 0); } else { MHC_WIDE_BWD(bf16_t, 1); }
+        } else {
+            if (mode == 0) { MHC_WIDE_BWD(float, 0); } else { MHC_WIDE_BWD(float, 1); }
+        }
 #undef MHC_WIDE_BWD
+    }
     hipError_t e = hipGetLastError();
     timing_end(tok, s);
     if (e != hipSuccess || n <= 8) return e;
     // dM for n >= 16: same grid in MODE 0 (its rows of scal_out), one
     // workgroup per token in MODE 1
     const dim3 ggrid(mode == 0 ? (unsigned)grid : (unsigned)(B < 65536 ? B : 65536));
+    const bool vec = C % 8 == 0 && ((uintptr_t)g % 16) == 0 && ((uintptr_t)x % 16) == 0;
 #define MHC_GRAM(TX_, M_)                                                                                         \
     if (n == 16) {                                                                                                \
-        hipLaunchKernelGGL((stream_gram_kernel<TX_, 16, M_>), ggrid, dim3(gram_threads<16>()), 0, s, g,            \
-                           (const TX_*)x, scal_out, B, Ci, (int64_t)(16 * 16 + 2 * 16 + 2));                      \
+        if (vec) {                                                                                                \
+            hipLaunchKernelGGL((stream_gram_kernel<TX_, 16, M_, true>), ggrid, dim3(kWideThreads), 0, s, g,       \
+                               (const TX_*)x, scal_out, B, Ci, (int64_t)(16 * 16 + 2 * 16 + 2));                 \
+        } else {                                                                                                  \
+            hipLaunchKernelGGL((stream_gram_kernel<TX_, 16, M_, false>), ggrid, dim3(kWideThreads), 0, s, g,      \
+                               (const TX_*)x, scal_out, B, Ci, (int64_t)(16 * 16 + 2 * 16 + 2));                 \
+        }                                                                                                         \
     } else {                                                                                                      \
-        hipLaunchKernelGGL((stream_gram_kernel<TX_, 32, M_>), ggrid, dim3(gram_threads<32>()), 0, s, g,            \
-                           (const TX_*)x, scal_out, B, Ci, (int64_t)(32 * 32 + 2 * 32 + 2));                      \
+        if (vec) {                                                                                                \
+            hipLaunchKernelGGL((stream_gram_kernel<TX_, 32, M_, true>), ggrid, dim3(kWideThreads), 0, s, g,       \
+                               (const TX_*)x, scal_out, B, Ci, (int64_t)(32 * 32 + 2 * 32 + 2));                 \
+        } else {                                                                                                  \
+            hipLaunchKernelGGL((stream_gram_kernel<TX_, 32, M_, false>), ggrid, dim3(kWideThreads), 0, s, g,      \
+                               (const TX_*)x, scal_out, B, Ci, (int64_t)(32 * 32 + 2 * 32 + 2));                 \
+        }                                                                                                         \
     }
     const int tg = timing_begin("stream_gram", s);
     if (x_dtype == kBF16) {
@@ -823,12 +1109,23 @@ hipError_t launch_wide_distribute_bwd(int dt, int n, const float* g, const void*
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || n <= 8) return e;
     const dim3 ggrid((unsigned)(B < 65536 ? B : 65536));
+    const bool vec = C % 8 == 0 && ((uintptr_t)g % 16) == 0 && ((uintptr_t)x % 16) == 0;
     MHC_WIDE_T(dt, if (n == 16) {
-        hipLaunchKernelGGL((stream_gram_kernel<T_, 16, 1>), ggrid, dim3(gram_threads<16>()), 0, s, g, (const T_*)x,
-                           gM, B, (int)C, (int64_t)(16 * 16));
+        if (vec) {
+            hipLaunchKernelGGL((stream_gram_kernel<T_, 16, 1, true>), ggrid, dim3(kWideThreads), 0, s, g,
+                               (const T_*)x, gM, B, (int)C, (int64_t)(16 * 16));
+        } else {
+            hipLaunchKernelGGL((stream_gram_kernel<T_, 16, 1, false>), ggrid, dim3(kWideThreads), 0, s, g,
+                               (const T_*)x, gM, B, (int)C, (int64_t)(16 * 16));
+        }
     } else {
-        hipLaunchKernelGGL((stream_gram_kernel<T_, 32, 1>), ggrid, dim3(gram_threads<32>()), 0, s, g, (const T_*)x,
-                           gM, B, (int)C, (int64_t)(32 * 32));
+        if (vec) {
+            hipLaunchKernelGGL((stream_gram_kernel<T_, 32, 1, true>), ggrid, dim3(kWideThreads), 0, s, g,
+                               (const T_*)x, gM, B, (int)C, (int64_t)(32 * 32));
+        } else {
+            hipLaunchKernelGGL((stream_gram_kernel<T_, 32, 1, false>), ggrid, dim3(kWideThreads), 0, s, g,
+                               (const T_*)x, gM, B, (int)C, (int64_t)(32 * 32));
+        }
     });
     return hipGetLastError();
 }
