@@ -449,18 +449,22 @@ static size_t align_floats(size_t n) { return (n + 63) & ~(size_t)63; }
 
 struct ProjFwdWs {
     int ks;
-    size_t phib_off, p_off, ss_off, total;
+    bool stream;  // more than one output tile: the streaming projection
+    size_t phib_off, xpl_off, p_off, ss_off, total;
 };
 
-// [Phi planes (three bf16 planes per 32-row output tile) | P partials
-//  [tile][ks][B][32] | sum x^2 partials [ks][B]]
+// [Phi planes (one 32-row output tile: three bf16 planes) or, with more
+//  tiles, fp32 x split into three bf16 planes | P partials [tile][ks][B][32]
+//  | sum x^2 partials [ks][B]]
 static size_t phi_planes_bytes(int64_t k, int np) { return align256((size_t)proj_tiles(np) * 3 * 32 * k * 2); }
 
 static ProjFwdWs proj_fwd_ws(int64_t batch, int64_t k, int np) {
     ProjFwdWs w{};
     w.ks = batch > 0 ? proj_ksplit(batch, k, np) : 1;
+    w.stream = proj_stream_path(np);
     w.phib_off = 0;
-    w.p_off = phi_planes_bytes(k, np);
+    w.xpl_off = w.stream ? 0 : phi_planes_bytes(k, np);
+    w.p_off = w.xpl_off + (w.stream ? align256(proj_xplanes_bytes(batch, k)) : 0);
     w.ss_off = w.p_off + align256((size_t)proj_tiles(np) * w.ks * batch * kProjTile * sizeof(float));
     w.total = w.ss_off + align256((size_t)w.ks * batch * sizeof(float));
     return w;
@@ -496,8 +500,14 @@ int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* we
     bf16_raw_t* phib = (bf16_raw_t*)((char*)workspace + w.phib_off);
     float* pp = (float*)((char*)workspace + w.p_off);
     float* ss = (float*)((char*)workspace + w.ss_off);
-    hipError_t e = launch_phi_split(weight, weight, weight, out_dim, out_dim, k, phib, s);
-    if (e == hipSuccess) e = launch_proj_mfma(dtype, inp, phib, out_dim, pp, ss, batch, k, w.ks, s);
+    hipError_t e = hipSuccess;
+    if (w.stream) {
+        e = launch_proj_stream(dtype, inp, (bf16_raw_t*)((char*)workspace + w.xpl_off), weight, weight, weight,
+                               out_dim, nullptr, out_dim, pp, ss, batch, k, w.ks, s);
+    } else {
+        e = launch_phi_split(weight, weight, weight, out_dim, out_dim, k, phib, s);
+        if (e == hipSuccess) e = launch_proj_mfma(dtype, inp, phib, out_dim, pp, ss, batch, k, w.ks, s);
+    }
     if (e == hipSuccess) e = launch_proj_reduce(pp, w.ks, batch, out_dim, out, s);
     return hip_status(e);
 }
@@ -638,8 +648,13 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
     float* pp = (float*)((char*)workspace + w.p_off);
     float* ss = (float*)((char*)workspace + w.ss_off);
     const int np = 2 * n + n * n;
-    e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
-    if (e == hipSuccess) e = launch_proj_mfma(x_dtype, x, phib, np, pp, ss, batch, K, w.ks, s);
+    if (w.stream) {
+        e = launch_proj_stream(x_dtype, x, (bf16_raw_t*)((char*)workspace + w.xpl_off), phi_pre, phi_post, phi_res,
+                               n, nullptr, np, pp, ss, batch, K, w.ks, s);
+    } else {
+        e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+        if (e == hipSuccess) e = launch_proj_mfma(x_dtype, x, phib, np, pp, ss, batch, K, w.ks, s);
+    }
     if (e == hipSuccess)
         e = launch_dyn_coef_fwd(n, pp, ss, w.ks, batch, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
                                 saved + d.coef_off, saved + d.p_off, saved + d.rh_off, num_iters, sinkhorn_eps,
@@ -681,7 +696,7 @@ static size_t infer_proj_off(int64_t batch, int32_t n) { return align256((size_t
 size_t mhc_layer_dynamic_infer_workspace_size(int64_t batch, int32_t n, int32_t hidden) {
     if (batch < 0 || n < 1 || hidden < 1) return 0;
     const ProjFwdWs w = proj_fwd_ws(batch, (int64_t)n * hidden, 2 * n + n * n);
-    return infer_proj_off(batch, n) + (w.total - w.p_off);
+    return infer_proj_off(batch, n) + (w.total - w.xpl_off);
 }
 
 int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, const float* alpha_pre,
@@ -706,10 +721,17 @@ int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, 
     const float* w32 = (const float*)packed;
     const bf16_raw_t* phib = (const bf16_raw_t*)((const char*)packed + packed_phib_off(hidden));
     float* coef = (float*)workspace;
+    // [coef | x planes (streaming path) | P partials | sum x^2 partials]
     char* pw = (char*)workspace + infer_proj_off(batch, n);
-    float* pp = (float*)pw;
-    float* ss = (float*)(pw + (w.ss_off - w.p_off));
-    hipError_t e = launch_proj_mfma(x_dtype, x, phib, np, pp, ss, batch, K, w.ks, s);
+    float* pp = (float*)(pw + (w.p_off - w.xpl_off));
+    float* ss = (float*)(pw + (w.ss_off - w.xpl_off));
+    hipError_t e = hipSuccess;
+    if (w.stream) {
+        e = launch_proj_stream(x_dtype, x, (bf16_raw_t*)pw, nullptr, nullptr, nullptr, n, phib, np, pp, ss, batch, K,
+                               w.ks, s);
+    } else {
+        e = launch_proj_mfma(x_dtype, x, phib, np, pp, ss, batch, K, w.ks, s);
+    }
     if (e == hipSuccess)
         e = launch_dyn_coef_fwd(n, pp, ss, w.ks, batch, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
                                 coef, nullptr, nullptr, num_iters, sinkhorn_eps, rmsnorm_eps, s);

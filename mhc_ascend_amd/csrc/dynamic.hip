@@ -327,6 +327,299 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
 }
 
+// ---------------------------------------------------------------------------
+// Projection over more than one 32-row output tile (2n + n^2 > 32: n >= 8),
+// reading Phi once.  Workgroup = 128 output rows (one 32-row output tile
+// per wave, two 16-row MFMA tiles that share each x fragment read from LDS)
+// x TB = 16 MT tokens x one K range; Phi is the large operand here
+// (178 MB at n = 32, C = 1280), so each element of it is loaded by one lane
+// of one workgroup per token block and never staged.  x arrives as XPL
+// bf16 planes ([XPL][B][K]: fp32 x split hi / mid / lo by
+// proj_xsplit_kernel, or bf16 x itself) and goes through LDS, 64 k per
+// stage, double-buffered, one barrier per stage.  A wave's Phi fragments
+// (its 32 rows x 32 k: 2 x 8 consecutive fp32 per lane) are loaded two
+// stages ahead and split into hi / mid / lo in registers (PHI_PLANES: read the
+// fragment-order planes of phi_split_kernel instead, as packed for the
+// forward-only entry).  Products as proj_mfma_kernel: bf16 x:
+// x.(hi + mid + lo); fp32 x: xh.(hi + mid + lo) + xm.(hi + mid) + xl.hi.
+// Partials p_part[tile][ks][B][32], the layout proj_mfma_kernel writes;
+// with bf16 x the workgroups of output block 0 also store ss_part[ks][B]
+// (fp32 x: proj_xsplit_kernel stores it).  Workgroups that stage the same x
+// (same token block and K range) get ids on one XCD.
+// ---------------------------------------------------------------------------
+constexpr int kStreamOB = 128;                    // output rows per workgroup (32 per wave)
+constexpr int kStreamKS = 64;                     // k per LDS stage
+constexpr int kStreamPitch = kStreamKS * 2 + 16;  // bytes per staged row of one plane
+
+// fp32 x -> xp[3][B][K] bf16 (split3 per element) and ss_part[q][b] = sum
+// of x^2 over K range q of the projection: workgroup (b, q), fixed order.
+__global__ __launch_bounds__(256) void proj_xsplit_kernel(const float* __restrict__ x, uint4* __restrict__ xp,
+                                                          float* __restrict__ ss_part, int64_t B, int64_t K,
+                                                          int64_t kchunk, int ks) {
+    __shared__ float red[256 / kWave];
+    const int64_t b = blockIdx.x / ks;
+    const int q = (int)(blockIdx.x % ks);
+    const int64_t kb = q * kchunk;
+    const int64_t ke = kb + kchunk < K ? kb + kchunk : K;
+    const int64_t plane = B * K / 8;  // 16-byte pieces per plane
+    float ss[1] = {0.f};
+    for (int64_t k = kb + 8 * (int64_t)threadIdx.x; k < ke; k += 8 * (int64_t)blockDim.x) {
+        const float4 a = *reinterpret_cast<const float4*>(x + b * K + k);
+        const float4 c = *reinterpret_cast<const float4*>(x + b * K + k + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+        uint32_t w[3][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float h0, m0, l0, h1, m1, l1;
+            split3(v[2 * e], h0, m0, l0);
+            split3(v[2 * e + 1], h1, m1, l1);
+            w[0][e] = pack_bf16(h0, h1);
+            w[1][e] = pack_bf16(m0, m1);
+            w[2][e] = pack_bf16(l0, l1);
+            ss[0] += v[2 * e] * v[2 * e] + v[2 * e + 1] * v[2 * e + 1];
+        }
+        const int64_t pc = (b * K + k) / 8;
+#pragma unroll
+        for (int p2 = 0; p2 < 3; ++p2) xp[p2 * plane + pc] = make_uint4(w[p2][0], w[p2][1], w[p2][2], w[p2][3]);
+    }
+    block_sum<1>(ss, red);
+    if (threadIdx.x == 0) ss_part[(int64_t)q * B + b] = ss[0];
+}
+
+template <int XPL, int MT, bool PHI_PLANES>
+__global__ __launch_bounds__(256) void proj_stream_kernel(
+    const bf16_t* __restrict__ xpl, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
+    const float* __restrict__ phi_res, int n_pre, const uint4* __restrict__ phif, int np, float* __restrict__ p_part,
+    float* __restrict__ ss_part, int64_t B, int64_t K, int64_t kchunk, int ks, int oblocks, int64_t groups) {
+    constexpr int TB = 16 * MT;
+    constexpr int KS = kStreamKS;
+    constexpr int PITCH = kStreamPitch;
+    constexpr int PIECES = XPL * TB * (KS * 2 / 16);  // 16-byte pieces per stage
+    constexpr int PPT = (PIECES + 255) / 256;         // per thread
+    __shared__ __align__(16) char xs[2][XPL * TB * PITCH];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row = lane & 15;
+    const int kg = lane >> 4;
+    // id = 8 (gq * oblocks + oi) + gx for group g = 8 gq + gx (token block
+    // x K range): one group's output blocks share an XCD
+    const int64_t lin = blockIdx.x;
+    const int64_t rest = lin / 8;
+    const int oi = (int)(rest % oblocks);
+    const int64_t grp = (rest / oblocks) * 8 + lin % 8;
+    if (grp >= groups) return;
+    const int64_t tblk = grp / ks;
+    const int ksplit = (int)(grp % ks);
+    const int64_t tok0 = tblk * TB;
+    const int ow = oi * kStreamOB + 32 * wave;  // the wave's output tile: rows ow .. ow + 31
+    const bool wave_on = ow < np;
+    const int64_t kb = ksplit * kchunk;
+    const int64_t ke = kb + kchunk < K ? kb + kchunk : K;
+    const int nst = ke > kb ? (int)((ke - kb + KS - 1) / KS) : 0;
+    const int64_t ksteps = K / 32;
+    const int64_t plane = B * K;  // elements per x plane
+
+    f32x4_t acc[MT][2];
+    float ss[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        acc[mt][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        acc[mt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        ss[mt] = 0.f;
+    }
+    const bool do_ss = XPL == 1 && oi == 0 && wave == 0;
+
+    // x stage st: piece i = tid + 256 u of this thread = (plane, token row,
+    // 16-byte column), the plane fixed per u (TB * 8 is a multiple of 256).
+    // Buffer loads: rows past the batch read zero through the per-plane
+    // range, columns past the K range are zeroed at commit, no branches.
+    static_assert((TB * 8) % 256 == 0, "whole planes per piece round");
+    const int64_t rows = B - tok0 < TB ? B - tok0 : TB;
+    buf_rsrc_t xr[XPL];
+#pragma unroll
+    for (int p2 = 0; p2 < XPL; ++p2)
+        xr[p2] = make_buf_rsrc(xpl + p2 * plane + tok0 * K, (uint32_t)(rows * K * 2));
+    auto fetch_x = [&](uint4 (&f)[PPT], int st) __attribute__((always_inline)) {
+        const int64_t k0 = kb + (int64_t)st * KS;
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            const int r = (i / 8) % TB;
+            const int c = i % 8;
+            f[u] = buf_ld16<false, true>(xr[(256 * u) / (TB * 8)], (uint32_t)(((int64_t)r * K + k0 + 8 * c) * 2), 0u);
+        }
+    };
+    auto commit = [&](const uint4 (&f)[PPT], int st, int buf) __attribute__((always_inline)) {
+        const int64_t k0 = kb + (int64_t)st * KS;
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            const int pl = (256 * u) / (TB * 8);
+            const int r = (i / 8) % TB;
+            const int c = i % 8;
+            const uint32_t m = k0 + 8 * c < ke ? 0xffffffffu : 0u;
+            *reinterpret_cast<uint4*>(&xs[buf][(pl * TB + r) * PITCH + 16 * c]) =
+                make_uint4(f[u].x & m, f[u].y & m, f[u].z & m, f[u].w & m);
+        }
+    };
+    // Phi fragments of stage st (its two k steps) for the wave's two 16-row
+    // MFMA tiles nt: rows ow + 16 nt + row, k = 32 kstep + 8 kg .. + 7;
+    // loaded two stages ahead, a step past the last one clamped (x is zero
+    // there)
+    struct PhiStage {
+        float f[2][2][8];
+        uint4 q[2][2][3];
+    };
+    auto fetch_phi = [&](PhiStage& ps, int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            int64_t kstep = (kb + (int64_t)st * KS) / 32 + kk;
+            kstep = kstep < ksteps ? kstep : ksteps - 1;
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                if constexpr (PHI_PLANES) {
+                    const int tile = ow / 32;
+#pragma unroll
+                    for (int p2 = 0; p2 < 3; ++p2)
+                        ps.q[kk][nt][p2] =
+                            wave_on ? phif[((int64_t)(tile * 6 + p2 * 2 + nt) * ksteps + kstep) * 64 + lane]
+                                    : make_uint4(0u, 0u, 0u, 0u);
+                } else {
+                    // rows past np read the last row (no branch) and are zeroed
+                    const int o = ow + 16 * nt + row;
+                    const bool ov = o < np;
+                    const float* pr =
+                        phi_row(phi_pre, phi_post, phi_res, n_pre, ov ? o : np - 1, K) + kstep * 32 + 8 * kg;
+                    const float4 a = *reinterpret_cast<const float4*>(pr);
+                    const float4 c = *reinterpret_cast<const float4*>(pr + 4);
+                    const float v[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ps.f[kk][nt][e] = ov ? v[e] : 0.f;
+                }
+            }
+        }
+    };
+    auto phi_planes = [&](const PhiStage& ps, int kk, int nt, u32x4_t& h, u32x4_t& m, u32x4_t& l)
+        __attribute__((always_inline)) {
+        if constexpr (PHI_PLANES) {
+            h = u32x4_t{ps.q[kk][nt][0].x, ps.q[kk][nt][0].y, ps.q[kk][nt][0].z, ps.q[kk][nt][0].w};
+            m = u32x4_t{ps.q[kk][nt][1].x, ps.q[kk][nt][1].y, ps.q[kk][nt][1].z, ps.q[kk][nt][1].w};
+            l = u32x4_t{ps.q[kk][nt][2].x, ps.q[kk][nt][2].y, ps.q[kk][nt][2].z, ps.q[kk][nt][2].w};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float h0, m0, l0, h1, m1, l1;
+                split3(ps.f[kk][nt][2 * e], h0, m0, l0);
+                split3(ps.f[kk][nt][2 * e + 1], h1, m1, l1);
+                h[e] = pack_bf16(h0, h1);
+                m[e] = pack_bf16(m0, m1);
+                l[e] = pack_bf16(l0, l1);
+            }
+        }
+    };
+    auto compute = [&](int buf, int kk, const u32x4_t (&ph)[2], const u32x4_t (&pm)[2], const u32x4_t (&pl)[2])
+        __attribute__((always_inline)) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const char* base = &xs[buf][(16 * mt + row) * PITCH + (32 * kk + 8 * kg) * 2];
+            const uint4 q0 = *reinterpret_cast<const uint4*>(base);
+            const u32x4_t a0 = u32x4_t{q0.x, q0.y, q0.z, q0.w};
+            if constexpr (XPL == 1) {
+                if (do_ss) {
+                    const uint32_t wv[4] = {q0.x, q0.y, q0.z, q0.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float lo = __uint_as_float(wv[e] << 16), hi = __uint_as_float(wv[e] & 0xffff0000u);
+                        ss[mt] += lo * lo + hi * hi;
+                    }
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    acc[mt][nt] = mfma16x16x32(a0, ph[nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(a0, pm[nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(a0, pl[nt], acc[mt][nt]);
+                }
+            } else {
+                const uint4 q1 = *reinterpret_cast<const uint4*>(base + TB * PITCH);
+                const uint4 q2 = *reinterpret_cast<const uint4*>(base + 2 * TB * PITCH);
+                const u32x4_t a1 = u32x4_t{q1.x, q1.y, q1.z, q1.w};
+                const u32x4_t a2 = u32x4_t{q2.x, q2.y, q2.z, q2.w};
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt) {
+                    acc[mt][nt] = mfma16x16x32(a0, ph[nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(a0, pm[nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(a1, ph[nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(a0, pl[nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(a1, pm[nt], acc[mt][nt]);
+                    acc[mt][nt] = mfma16x16x32(a2, ph[nt], acc[mt][nt]);
+                }
+            }
+        }
+    };
+
+    if (nst > 0) {
+        // Phi of stage s lives in ring slot s % 3 (no register copies, so
+        // nothing waits for a load before its stage); x is staged one ahead
+        uint4 f[PPT];
+        PhiStage p0, p1, p2;
+        fetch_x(f, 0);
+        fetch_phi(p0, 0);
+        fetch_phi(p1, 1);
+        commit(f, 0, 0);
+        __syncthreads();
+        // x of the next stage is issued before Phi two ahead: the loads
+        // complete in issue order, so the commit's wait leaves Phi in flight
+        auto step = [&](int st, const PhiStage& cur, PhiStage& ahead) __attribute__((always_inline)) {
+            const int buf = st & 1;
+            if (st + 1 < nst) fetch_x(f, st + 1);
+            fetch_phi(ahead, st + 2);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                u32x4_t ph[2], pm[2], pl[2];
+                phi_planes(cur, kk, 0, ph[0], pm[0], pl[0]);
+                phi_planes(cur, kk, 1, ph[1], pm[1], pl[1]);
+                if (wave_on || do_ss) compute(buf, kk, ph, pm, pl);
+            }
+            if (st + 1 < nst) commit(f, st + 1, buf ^ 1);
+            __syncthreads();
+        };
+        int st = 0;
+        for (; st + 3 <= nst; st += 3) {
+            step(st, p0, p2);
+            step(st + 1, p1, p0);
+            step(st + 2, p2, p1);
+        }
+        if (st < nst) step(st, p0, p2);
+        if (st + 1 < nst) step(st + 1, p1, p0);
+    }
+    if (wave_on) {
+        // D[token 16 mt + 4 kg + i][output ow + 16 nt + row]
+        const int tile = ow / 32;
+        float* pp = p_part + ((int64_t)tile * ks + ksplit) * B * kNPad + row;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t t = tok0 + 16 * mt + 4 * kg + i;
+                if (t < B) {
+                    pp[t * kNPad] = acc[mt][0][i];
+                    pp[t * kNPad + 16] = acc[mt][1][i];
+                }
+            }
+        }
+    }
+    if (do_ss) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            // lanes row, row + 16, row + 32, row + 48 hold parts of token row's sum
+            const float s2 = xor32_add(xor16_add(ss[mt]));
+            const int64_t t = tok0 + 16 * mt + row;
+            if (kg == 0 && t < B) ss_part[(int64_t)ksplit * B + t] = s2;
+        }
+    }
+}
+
 // Split-K partial q of projection output o of token b.  The partials of
 // the output tiles are stored tile-major: p_part[o / 32][q][b][o % 32].
 __device__ __forceinline__ float p_part_at(const float* __restrict__ p_part, int ks, int64_t B, int q, int64_t b,
@@ -1196,9 +1489,44 @@ hipError_t launch_phi_split(const float* pre, const float* post, const float* re
     return hipGetLastError();
 }
 
+// Tokens per workgroup of the streaming projection (16 MT, MT = 2, 4, 8).
+static int proj_stream_mt(int64_t B) { return B > 32 ? 4 : 2; }
+
+template <int XPL, int PHI>
+static const void* proj_stream_fn(int mt) {
+    switch (mt) {
+        case 2: return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 2, PHI != 0>);
+        case 4: return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 4, PHI != 0>);
+        default: return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 8, PHI != 0>);
+    }
+}
+
+bool proj_stream_path(int np) { return np > kProjTile; }
+
+// K splits of the streaming projection: token blocks x output blocks x
+// splits fill two rounds of resident workgroups (occupancy of the fp32-x
+// kernel, whose LDS stage is the larger), at least two stages per split.
+static int proj_stream_ksplit(int64_t B, int64_t K, int np) {
+    const int mt = proj_stream_mt(B);
+    const int64_t groups0 = ((B + 16 * mt - 1) / (16 * mt)) * ((np + kStreamOB - 1) / kStreamOB);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, proj_stream_fn<3, 0>(mt), 256, 0) != hipSuccess ||
+        per_cu < 1) {
+        (void)hipGetLastError();
+        per_cu = 1;
+    }
+    // rounded down: a last partial round would leave most CUs idle while it runs
+    int64_t ks = 2 * (int64_t)device_cu_count() * per_cu / groups0;
+    const int64_t kmax = (K + 2 * kStreamKS - 1) / (2 * kStreamKS);
+    if (ks > kmax) ks = kmax;
+    if (ks < 1) ks = 1;
+    return (int)ks;
+}
+
 // K splits so that token blocks x splits x output tiles fill about two
 // workgroups per CU, at least 256 columns per split.
 int proj_ksplit(int64_t B, int64_t K, int np) {
+    if (proj_stream_path(np)) return proj_stream_ksplit(B, K, np);
     const int64_t blocks = ((B + 127) / 128) * proj_tiles(np);
     int64_t ks = (2 * (int64_t)device_cu_count() + blocks - 1) / blocks;
     const int64_t kmax = (K + 2 * kProjKS - 1) / (2 * kProjKS);
@@ -1229,6 +1557,51 @@ hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_t* phib, int 
         hipLaunchKernelGGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, p_part,
                            ss_part, B, K, kchunk);
     }
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, const float* phi_pre,
+                              const float* phi_post, const float* phi_res, int n_pre, const bf16_raw_t* phib, int np,
+                              float* p_part, float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (K % 32 != 0 || np <= kProjTile || ks < 1 || (x_dtype == kF32 && !xplanes)) return hipErrorInvalidValue;
+    int64_t kchunk = (K + ks - 1) / ks;
+    kchunk = ((kchunk + kStreamKS - 1) / kStreamKS) * kStreamKS;
+    const int mt = proj_stream_mt(B);
+    const int64_t tb = (B + 16 * mt - 1) / (16 * mt);
+    const int ob = (np + kStreamOB - 1) / kStreamOB;
+    const int64_t groups = tb * ks;
+    const dim3 grid((unsigned)(((groups + 7) / 8) * 8 * ob));
+    const int tok = timing_begin("proj", s);
+    const bf16_t* xp = reinterpret_cast<const bf16_t*>(x);
+    if (x_dtype == kF32) {
+        hipLaunchKernelGGL(proj_xsplit_kernel, dim3((unsigned)(B * ks)), dim3(256), 0, s, (const float*)x,
+                           reinterpret_cast<uint4*>(xplanes), ss_part, B, K, kchunk, ks);
+        xp = reinterpret_cast<const bf16_t*>(xplanes);
+    }
+    const uint4* phif = reinterpret_cast<const uint4*>(phib);
+#define MHC_STREAM(XPL_, MT_)                                                                                   \
+    if (phib) {                                                                                                 \
+        hipLaunchKernelGGL((proj_stream_kernel<XPL_, MT_, true>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,   \
+                           phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups);             \
+    } else {                                                                                                    \
+        hipLaunchKernelGGL((proj_stream_kernel<XPL_, MT_, false>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,  \
+                           phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups);             \
+    }
+#define MHC_STREAM_MT(XPL_)                               \
+    switch (mt) {                                         \
+        case 2: { MHC_STREAM(XPL_, 2); break; }           \
+        case 4: { MHC_STREAM(XPL_, 4); break; }           \
+        default: { MHC_STREAM(XPL_, 8); break; }          \
+    }
+    if (x_dtype == kF32) {
+        MHC_STREAM_MT(3);
+    } else {
+        MHC_STREAM_MT(1);
+    }
+#undef MHC_STREAM_MT
+#undef MHC_STREAM
     timing_end(tok, s);
     return hipGetLastError();
 }

@@ -168,6 +168,16 @@ int proj_ksplit(int64_t B, int64_t K, int np);
 // p_part[tile][ks][B][32], plus ss_part[ks][B] = partial sums of x^2.
 hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_raw_t* phib, int np, float* p_part,
                             float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s);
+// More than one output tile (np > 32): the streaming projection reads Phi
+// once (fp32 rows from pre / post / res as phi_row, or, when phib is not
+// null, the planes of launch_phi_split); fp32 x is first split into
+// xplanes (proj_xplanes_bytes) with ss_part.  Same p_part / ss_part layout
+// as launch_proj_mfma, ks from proj_ksplit.
+bool proj_stream_path(int np);
+constexpr size_t proj_xplanes_bytes(int64_t B, int64_t K) { return (size_t)(3 * B * K * 2); }
+hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, const float* phi_pre,
+                              const float* phi_post, const float* phi_res, int n_pre, const bf16_raw_t* phib, int np,
+                              float* p_part, float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s);
 hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s);
 hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part, int ks, int64_t B, int64_t K,
                                const float* a_pre, const float* a_post, const float* a_res, const float* b_pre,
