@@ -525,7 +525,11 @@ static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
     ProjBwdWs w{};
     w.tiles = batch > 0 ? proj_bwd_tiles(kF32, batch, k) : 1;
     w.part_off = 0;
-    w.stage_off = align256((size_t)w.tiles * tile_rows(out_dim) * k * sizeof(float));
+    // the partials region also serves the all-tiles path as its dP planes
+    size_t part = (size_t)w.tiles * tile_rows(out_dim) * k * sizeof(float);
+    if (batch > 0 && proj_bwd_wide_path(kF32, out_dim, batch) && part < proj_bwd_wide_scratch_bytes(out_dim, batch))
+        part = proj_bwd_wide_scratch_bytes(out_dim, batch);
+    w.stage_off = align256(part);
     w.total = w.stage_off + align256(column_sums_stage_floats((int64_t)tile_rows(out_dim) * k) * sizeof(float));
     return w;
 }
@@ -542,7 +546,7 @@ static hipError_t proj_bwd_all(int x_dtype, const void* x, const float* dp, int 
                                int64_t batch, int64_t K, hipStream_t s) {
     if (batch > 0 && proj_bwd_wide_path(x_dtype, np, batch))
         return launch_proj_bwd_wide((const float*)x, dp, dp_stride_, s_tok, phi_pre, phi_post, phi_res, n_pre, np,
-                                    (float*)dx, accumulate, grad_phi, batch, K, s);
+                                    (float*)dx, accumulate, grad_phi, part, batch, K, s);
     hipError_t e = hipSuccess;
     for (int o0 = 0; o0 < np && e == hipSuccess; o0 += kProjTile) {
         const int rows_t = np - o0 < kProjTile ? np - o0 : kProjTile;
@@ -767,7 +771,11 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     w.dp_off = o; o += align256((size_t)batch * dp_stride((int)np) * 4);
     w.s_off = o; o += align256((size_t)batch * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
-    w.phip_off = o; o += align256((size_t)w.tiles * tile_rows((int)np) * K * 4);
+    // projection partials (per-tile path) or dP planes (all-tiles path)
+    size_t phip = (size_t)w.tiles * tile_rows((int)np) * K * 4;
+    if (batch > 0 && proj_bwd_wide_path(w.wdt, (int)np, batch) && phip < proj_bwd_wide_scratch_bytes((int)np, batch))
+        phip = proj_bwd_wide_scratch_bytes((int)np, batch);
+    w.phip_off = o; o += align256(phip);
     w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
     w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)tile_rows((int)np) * K) * 4);
     const size_t acc = w.wdt != x_dtype ? (size_t)batch * K * 4 : 0;

@@ -1723,12 +1723,11 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
 // n >= 8), fp32 x and dx (bf16 x is upcast before it gets here), for
 // batches up to kProjWideMaxB tokens.  The per-tile kernel above would read
 // x and dx once per tile (34 times at n = 32); instead:
-//   proj_bwd_dx_kernel:   one workgroup per 128 columns x 32 tokens loops
-//     over the output tiles, dx_proj^T (columns x tokens) accumulating in
-//     MFMA registers: A = Phi^T (the next tile's values loaded while the
-//     current one computes; the token blocks of one column block run on one
-//     XCD and share Phi through its L2), B = dP^T read straight
-//     from dP; then one epilogue dx = dx_proj + (ACC ? dx : 0) + s x.
+//   dp_split_kernel + proj_bwd_dx2_kernel: dP split into hi / lo planes
+//     once; one workgroup per 128 columns x up to 128 tokens loops over the
+//     output tiles, dx_proj^T accumulating in MFMA registers (A = Phi^T,
+//     split in registers, B = the dP planes through LDS); then one epilogue
+//     dx = dx_proj + (ACC ? dx : 0) + s x.
 //   proj_bwd_dphi_kernel: one workgroup per 64 output rows x 128 columns
 //     walks all tokens in 32-token stages, dPhi = dP^T x in MFMA registers,
 //     and stores its rows of dPhi directly (no partials, no column sums).
@@ -1737,115 +1736,171 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
 // Operands are split hi / lo (hi.hi + lo.hi + hi.lo, as above).
 // ---------------------------------------------------------------------------
 constexpr int kProjWideMaxB = 1024;
-constexpr int kDxStages = 1;  // 32-token stages per dx workgroup
 
-// 8 consecutive fp32 (32-byte aligned) as two 16-byte loads
-__device__ __forceinline__ void ld8f(const float* p, float (&v)[8]) {
-    const float4 a = *reinterpret_cast<const float4*>(p);
-    const float4 b = *reinterpret_cast<const float4*>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+// dP [B][stride] (np valid columns) -> bf16 planes hi / lo [B][np32]
+// (np32 = np rounded up to 32, zero past np): 8 consecutive outputs of a
+// token are one 16-byte piece, the B-operand fragment of proj_bwd_dx2_kernel.
+__global__ __launch_bounds__(256) void dp_split_kernel(const float* __restrict__ dP, int stride, int np, int np32,
+                                                       int64_t B, uint4* __restrict__ dph, uint4* __restrict__ dpl) {
+    const int64_t per_row = np32 / 8;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= B * per_row) return;
+    const int64_t t = i / per_row;
+    const int o0 = (int)(i % per_row) * 8;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = o0 + e < np ? dP[t * stride + o0 + e] : 0.f;
+    u32x4_t h, l;
+    split_pack8(v, h, l);
+    dph[i] = make_uint4(h[0], h[1], h[2], h[3]);
+    dpl[i] = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
+// dx over all output tiles, one workgroup per 128 columns x up to 128
+// tokens (token blocks of one column block on one XCD, sharing that column
+// block's Phi in its L2): wave w owns columns 32 w .. 32 w + 31 (two
+// 16-column MFMA tiles ct) for all the workgroup's tokens, so every Phi
+// element is loaded and split hi / lo once per token block.  The 32-output
+// tile's dP planes (hi, lo: 16 KB for 128 tokens) go through LDS, shared by
+// the four waves, double-buffered; the Phi fragments (A = Phi^T: 8 outputs
+// of one column per lane, two tiles) are loaded two output tiles ahead.
+// Products hi.hi + lo.hi + hi.lo (as proj_bwd_mfma_kernel); then
+// dx = dx_proj + (ACC ? dx : 0) + (HAS_S ? s x : 0).
+constexpr int kDx2Tok = 128;                 // tokens per workgroup
+constexpr int kDx2Pitch = 64 + 16;           // bytes per token row of one dP plane tile in LDS
+
 template <bool ACC, bool HAS_S>
-__global__ __launch_bounds__(256) void proj_bwd_dx_kernel(
-    const float* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
-    const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
-    int n_pre, int np, float* __restrict__ dx, int64_t B, int64_t K) {
+__global__ __launch_bounds__(256) void proj_bwd_dx2_kernel(
+    const float* __restrict__ x, const uint4* __restrict__ dph, const uint4* __restrict__ dpl, int np32,
+    const float* __restrict__ s_tok, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
+    const float* __restrict__ phi_res, int n_pre, int np, float* __restrict__ dx, int64_t B, int64_t K) {
     constexpr int CB = 128;
-    constexpr int TS = kDxStages;
+    constexpr int TT = kDx2Tok / 16;
+    constexpr int PITCH = kDx2Pitch;
+    __shared__ __align__(16) char dps[2][2][kDx2Tok * PITCH];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    // Workgroups go round-robin over the 8 XCDs by linear id; the token
-    // blocks of one column block are given ids on the same XCD, one after
-    // another, so they share that column block's Phi in the XCD's L2.
-    const int64_t tblocks = (B + 32 * TS - 1) / (32 * TS);
+    const int64_t tblocks = (B + kDx2Tok - 1) / kDx2Tok;
+    const int64_t cblocks = (K + CB - 1) / CB;
     const int64_t lin = blockIdx.x;
     const int64_t idx = lin / 8;
     const int64_t cb = (idx / tblocks) * 8 + lin % 8;
-    const int64_t kb0 = cb * CB + wave * 32;  // this wave's 32 columns
-    if (kb0 >= K) return;  // padding ids, and K % 32 == 0: whole waves are in or out
-    const int64_t tb0 = (idx % tblocks) * (32 * TS);
-    f32x4_t d[TS][2][2];
+    if (cb >= cblocks) return;  // padding ids: the whole workgroup
+    const int64_t tok0 = (idx % tblocks) * kDx2Tok;
+    const int64_t kb0 = cb * CB + wave * 32;
+    const bool wave_on = kb0 < K;  // K % 32 == 0: whole waves are in or out
+    const int tiles = np32 / 32;
+    const int64_t prow = np32 / 8;  // 16-byte pieces per token row of a plane
+
+    f32x4_t d[TT][2];
 #pragma unroll
-    for (int st = 0; st < TS; ++st) {
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) d[st][tt][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        }
+    for (int tt = 0; tt < TT; ++tt) {
+        d[tt][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        d[tt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-    // dP columns are read 8 at a time: a stride that is a multiple of 8
-    // allows the aligned 16-byte loads (the layer's dP rows are)
-    const bool dp_vec = (dp_stride % 8) == 0;
-    // A = Phi^T: Phi[o0 + 8 lg + e][column 16 ct + lr]; the next tile's
-    // values are loaded while the current tile is on the matrix cores
-    float pv[2][8];
-    auto load_phi = [&](int o0) __attribute__((always_inline)) {
+    // dP planes of output tile ot: piece i = tid + 256 u = (plane, token, 16-byte column)
+    auto fetch_dp = [&](uint4 (&f)[4], int ot) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int o = o0 + 8 * lg + e;
-                pv[ct][e] = o < np ? phi_row(phi_pre, phi_post, phi_res, n_pre, o, K)[kb0 + 16 * ct + lr] : 0.f;
-            }
+        for (int u = 0; u < 4; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            const int pl = i / (kDx2Tok * 4);
+            const int r = (i / 4) % kDx2Tok;
+            const int c = i % 4;
+            const int64_t t = tok0 + r;
+            const uint4* src = pl == 0 ? dph : dpl;
+            f[u] = (t < B && ot < tiles) ? src[t * prow + ot * 4 + c] : make_uint4(0u, 0u, 0u, 0u);
         }
     };
-    load_phi(0);
-    for (int o0 = 0; o0 < np; o0 += 32) {
-        u32x4_t phh[2], phl[2];
+    auto commit = [&](const uint4 (&f)[4], int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) split_pack8(pv[ct], phh[ct], phl[ct]);
-        if (o0 + 32 < np) load_phi(o0 + 32);
+        for (int u = 0; u < 4; ++u) {
+            const int i = threadIdx.x + 256 * u;
+            const int pl = i / (kDx2Tok * 4);
+            const int r = (i / 4) % kDx2Tok;
+            const int c = i % 4;
+            *reinterpret_cast<uint4*>(&dps[buf][pl][r * PITCH + 16 * c]) = f[u];
+        }
+    };
+    // A = Phi^T fragments of output tile ot: Phi[32 ot + 8 lg + e][kb0 + 16 ct + lr]
+    struct PhiTile {
+        float v[2][8];
+    };
+    auto fetch_phi = [&](PhiTile& pt, int ot) __attribute__((always_inline)) {
+        const int64_t col = wave_on ? kb0 + lr : 0;
 #pragma unroll
-        for (int st = 0; st < TS; ++st) {
+        for (int e = 0; e < 8; ++e) {
+            const int o = 32 * ot + 8 * lg + e;
+            const bool ov = o < np;
+            const float* pr = phi_row(phi_pre, phi_post, phi_res, n_pre, ov ? o : np - 1, K) + col;
+            const float a = pr[0], b = pr[16];
+            pt.v[0][e] = ov ? a : 0.f;
+            pt.v[1][e] = ov ? b : 0.f;
+        }
+    };
+    auto tile_step = [&](int ot, const PhiTile& cur, PhiTile& ahead, uint4 (&f)[4]) __attribute__((always_inline)) {
+        const int buf = ot & 1;
+        if (ot + 1 < tiles) fetch_dp(f, ot + 1);
+        fetch_phi(ahead, ot + 2 < tiles ? ot + 2 : tiles - 1);
+        if (wave_on) {
+            u32x4_t ah[2], al[2];
+            split_pack8(cur.v[0], ah[0], al[0]);
+            split_pack8(cur.v[1], ah[1], al[1]);
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                // B = dP^T: dP[token 16 tt + lr][o0 + 8 lg .. + 7]
-                const int64_t t = tb0 + 32 * st + 16 * tt + lr;
-                float v[8];
-                const int ob = o0 + 8 * lg;
-                if (t < B && dp_vec && ob + 8 <= np) {
-                    ld8f(dP + t * dp_stride + ob, v);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = (t < B && ob + e < np) ? dP[t * dp_stride + ob + e] : 0.f;
-                }
-                u32x4_t bh, bl;
-                split_pack8(v, bh, bl);
+            for (int tt = 0; tt < TT; ++tt) {
+                const uint4 qh = *reinterpret_cast<const uint4*>(&dps[buf][0][(16 * tt + lr) * PITCH + 16 * lg]);
+                const uint4 ql = *reinterpret_cast<const uint4*>(&dps[buf][1][(16 * tt + lr) * PITCH + 16 * lg]);
+                const u32x4_t bh = u32x4_t{qh.x, qh.y, qh.z, qh.w};
+                const u32x4_t bl = u32x4_t{ql.x, ql.y, ql.z, ql.w};
 #pragma unroll
                 for (int ct = 0; ct < 2; ++ct) {
-                    d[st][tt][ct] = mfma16x16x32(phh[ct], bh, d[st][tt][ct]);
-                    d[st][tt][ct] = mfma16x16x32(phl[ct], bh, d[st][tt][ct]);
-                    d[st][tt][ct] = mfma16x16x32(phh[ct], bl, d[st][tt][ct]);
+                    d[tt][ct] = mfma16x16x32(ah[ct], bh, d[tt][ct]);
+                    d[tt][ct] = mfma16x16x32(al[ct], bh, d[tt][ct]);
+                    d[tt][ct] = mfma16x16x32(ah[ct], bl, d[tt][ct]);
                 }
             }
         }
+        if (ot + 1 < tiles) commit(f, buf ^ 1);
+        __syncthreads();
+    };
+    {
+        uint4 f[4];
+        PhiTile p0, p1, p2;
+        fetch_dp(f, 0);
+        fetch_phi(p0, 0);
+        fetch_phi(p1, tiles > 1 ? 1 : 0);
+        commit(f, 0);
+        __syncthreads();
+        int ot = 0;
+        for (; ot + 3 <= tiles; ot += 3) {
+            tile_step(ot, p0, p2, f);
+            tile_step(ot + 1, p1, p0, f);
+            tile_step(ot + 2, p2, p1, f);
+        }
+        if (ot < tiles) tile_step(ot, p0, p2, f);
+        if (ot + 1 < tiles) tile_step(ot + 1, p1, p0, f);
     }
+    if (!wave_on) return;
     // D[column 16 ct + 4 lg + i][token 16 tt + lr]: four consecutive columns of one token
 #pragma unroll
-    for (int st = 0; st < TS; ++st) {
+    for (int tt = 0; tt < TT; ++tt) {
+        const int64_t t = tok0 + 16 * tt + lr;
+        if (t >= B) continue;
+        const float sv = HAS_S ? s_tok[t] : 0.f;
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int64_t t = tb0 + 32 * st + 16 * tt + lr;
-            if (t >= B) continue;
-            const float sv = HAS_S ? s_tok[t] : 0.f;
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const int64_t off = t * K + kb0 + 16 * ct + 4 * lg;
-                float4 o = make_float4(d[st][tt][ct][0], d[st][tt][ct][1], d[st][tt][ct][2], d[st][tt][ct][3]);
-                if constexpr (ACC) {
-                    const float4 a = *reinterpret_cast<const float4*>(dx + off);
-                    o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
-                }
-                if constexpr (HAS_S) {
-                    const float4 xv = *reinterpret_cast<const float4*>(x + off);
-                    o.x += sv * xv.x; o.y += sv * xv.y; o.z += sv * xv.z; o.w += sv * xv.w;
-                }
-                *reinterpret_cast<float4*>(dx + off) = o;
+        for (int ct = 0; ct < 2; ++ct) {
+            const int64_t off = t * K + kb0 + 16 * ct + 4 * lg;
+            float4 o = make_float4(d[tt][ct][0], d[tt][ct][1], d[tt][ct][2], d[tt][ct][3]);
+            if constexpr (ACC) {
+                const float4 a = *reinterpret_cast<const float4*>(dx + off);
+                o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
             }
+            if constexpr (HAS_S) {
+                const float4 xv = *reinterpret_cast<const float4*>(x + off);
+                o.x += sv * xv.x; o.y += sv * xv.y; o.z += sv * xv.z; o.w += sv * xv.w;
+            }
+            *reinterpret_cast<float4*>(dx + off) = o;
         }
     }
 }
@@ -1861,7 +1916,7 @@ __global__ __launch_bounds__(256) void proj_bwd_dphi_kernel(const float* __restr
     const int wave = threadIdx.x >> 6;
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    // the row blocks of one column block on one XCD (as in proj_bwd_dx_kernel)
+    // the row blocks of one column block on one XCD (as in proj_bwd_dx2_kernel)
     const int64_t rblocks = (np + kDphiRows - 1) / kDphiRows;
     const int64_t lin = blockIdx.x;
     const int64_t idx = lin / 8;
@@ -1927,26 +1982,39 @@ bool proj_bwd_wide_path(int x_dtype, int np, int64_t B) {
     return x_dtype == kF32 && np > kProjTile && B >= 1 && B <= kProjWideMaxB;
 }
 
+size_t proj_bwd_wide_scratch_bytes(int np, int64_t B) {
+    const size_t plane = (((size_t)B * proj_tiles(np) * kProjTile * 2) + 255) & ~(size_t)255;
+    return 2 * plane;
+}
+
 hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, const float* s_tok,
                                 const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
-                                float* dx, bool accumulate, float* dphi, int64_t B, int64_t K, hipStream_t s) {
+                                float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
+                                hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (np <= kProjTile || B > kProjWideMaxB || K % 32 != 0) return hipErrorInvalidValue;
+    if (np <= kProjTile || B > kProjWideMaxB || K % 32 != 0 || !scratch) return hipErrorInvalidValue;
     if (s_tok && !accumulate) return hipErrorInvalidValue;
     const unsigned cblocks = (unsigned)((K + 127) / 128);
+    const int np32 = proj_tiles(np) * kProjTile;
+    // dP -> hi / lo bf16 planes in scratch
+    uint4* dph = reinterpret_cast<uint4*>(scratch);
+    uint4* dpl = reinterpret_cast<uint4*>((char*)scratch + proj_bwd_wide_scratch_bytes(np, B) / 2);
+    const int64_t pieces = B * (np32 / 8);
+    hipLaunchKernelGGL(dp_split_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, dP, dp_stride, np,
+                       np32, B, dph, dpl);
     // 1-D grid: 8 XCD lanes x ceil(column blocks / 8) x token blocks
-    const unsigned tblocks = (unsigned)((B + 32 * kDxStages - 1) / (32 * kDxStages));
+    const unsigned tblocks = (unsigned)((B + kDx2Tok - 1) / kDx2Tok);
     const dim3 gdx(8u * ((cblocks + 7) / 8) * tblocks);
     const int tok = timing_begin("proj_bwd", s);
     if (s_tok) {
-        hipLaunchKernelGGL((proj_bwd_dx_kernel<true, true>), gdx, dim3(256), 0, s, x, dP, dp_stride, s_tok, phi_pre,
+        hipLaunchKernelGGL((proj_bwd_dx2_kernel<true, true>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok, phi_pre,
                            phi_post, phi_res, n_pre, np, dx, B, K);
     } else if (accumulate) {
-        hipLaunchKernelGGL((proj_bwd_dx_kernel<true, false>), gdx, dim3(256), 0, s, x, dP, dp_stride, s_tok, phi_pre,
+        hipLaunchKernelGGL((proj_bwd_dx2_kernel<true, false>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok, phi_pre,
                            phi_post, phi_res, n_pre, np, dx, B, K);
     } else {
-        hipLaunchKernelGGL((proj_bwd_dx_kernel<false, false>), gdx, dim3(256), 0, s, x, dP, dp_stride, s_tok, phi_pre,
-                           phi_post, phi_res, n_pre, np, dx, B, K);
+        hipLaunchKernelGGL((proj_bwd_dx2_kernel<false, false>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok,
+                           phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
     }
     hipError_t e = hipGetLastError();
     timing_end(tok, s);
