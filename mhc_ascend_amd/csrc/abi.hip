@@ -527,8 +527,8 @@ static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
     w.part_off = 0;
     // the partials region also serves the all-tiles path as its dP planes
     size_t part = (size_t)w.tiles * tile_rows(out_dim) * k * sizeof(float);
-    if (batch > 0 && proj_bwd_wide_path(kF32, out_dim, batch) && part < proj_bwd_wide_scratch_bytes(out_dim, batch))
-        part = proj_bwd_wide_scratch_bytes(out_dim, batch);
+    if (batch > 0 && proj_bwd_wide_path(kF32, out_dim, batch) && part < proj_bwd_wide_scratch_bytes(out_dim, batch, k))
+        part = proj_bwd_wide_scratch_bytes(out_dim, batch, k);
     w.stage_off = align256(part);
     w.total = w.stage_off + align256(column_sums_stage_floats((int64_t)tile_rows(out_dim) * k) * sizeof(float));
     return w;
@@ -773,8 +773,9 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     // projection partials (per-tile path) or dP planes (all-tiles path)
     size_t phip = (size_t)w.tiles * tile_rows((int)np) * K * 4;
-    if (batch > 0 && proj_bwd_wide_path(w.wdt, (int)np, batch) && phip < proj_bwd_wide_scratch_bytes((int)np, batch))
-        phip = proj_bwd_wide_scratch_bytes((int)np, batch);
+    if (batch > 0 && proj_bwd_wide_path(w.wdt, (int)np, batch) &&
+        phip < proj_bwd_wide_scratch_bytes((int)np, batch, K))
+        phip = proj_bwd_wide_scratch_bytes((int)np, batch, K);
     w.phip_off = o; o += align256(phip);
     w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
     w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)tile_rows((int)np) * K) * 4);

@@ -1728,11 +1728,12 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
 //     output tiles, dx_proj^T accumulating in MFMA registers (A = Phi^T,
 //     split in registers, B = the dP planes through LDS); then one epilogue
 //     dx = dx_proj + (ACC ? dx : 0) + s x.
-//   proj_bwd_dphi_kernel: one workgroup per 64 output rows x 128 columns
-//     walks all tokens in 32-token stages, dPhi = dP^T x in MFMA registers,
-//     and stores its rows of dPhi directly (no partials, no column sums).
-//     The row blocks of one column block get ids on one XCD, so they share
-//     those x columns through its L2.
+//   dp_tsplit_kernel + x_tsplit_kernel + proj_bwd_dphi_kernel: dP and x
+//     split once into transposed hi / lo planes (tokens contiguous); one
+//     workgroup per 128 output rows x 128 columns walks all tokens,
+//     dPhi = dP^T x in MFMA registers, and stores its rows of dPhi directly
+//     (no partials, no column sums).  The row blocks of one column block get
+//     ids on one XCD, so they share those x columns through its L2.
 // Operands are split hi / lo (hi.hi + lo.hi + hi.lo, as above).
 // ---------------------------------------------------------------------------
 constexpr int kProjWideMaxB = 1024;
@@ -1905,66 +1906,158 @@ __global__ __launch_bounds__(256) void proj_bwd_dx2_kernel(
     }
 }
 
-constexpr int kDphiRows = 64;  // output rows (two 32-row tiles) per dPhi workgroup
+// Transposed hi / lo planes for dPhi = dP^T x, whose reduction runs over
+// tokens: an MFMA fragment wants 8 consecutive tokens of one output row /
+// one column, which are strided in the token-major dP and x.  Both are
+// split once into [row][Bp] bf16 planes (Bp = tokens rounded up to 32,
+// zero past the batch), so the fragments are 16-byte loads and the dPhi
+// kernel does no splitting.
+//   dpT[o][t] from dP[t][o] (rows up to `rows`, zero past np): one lane
+//   per (o, 8 tokens).
+__global__ __launch_bounds__(256) void dp_tsplit_kernel(const float* __restrict__ dP, int stride, int np, int rows,
+                                                        int64_t B, int64_t Bp, uint4* __restrict__ th,
+                                                        uint4* __restrict__ tl) {
+    const int64_t groups = Bp / 8;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)rows * groups) return;
+    const int o = (int)(i / groups);
+    const int64_t t0 = (i % groups) * 8;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (o < np && t0 + e < B) ? dP[(t0 + e) * stride + o] : 0.f;
+    u32x4_t h, l;
+    split_pack8(v, h, l);
+    th[i] = make_uint4(h[0], h[1], h[2], h[3]);
+    tl[i] = make_uint4(l[0], l[1], l[2], l[3]);
+}
 
-__global__ __launch_bounds__(256) void proj_bwd_dphi_kernel(const float* __restrict__ x, const float* __restrict__ dP,
-                                                            int dp_stride, int np, float* __restrict__ dphi,
-                                                            int64_t B, int64_t K) {
+//   xT[k][t] from x[t][k]: a 32-token x 64-column tile through LDS (loads
+//   along k, stores along t).
+constexpr int kXtCols = 64;
+__global__ __launch_bounds__(256) void x_tsplit_kernel(const float* __restrict__ x, int64_t B, int64_t K, int64_t Bp,
+                                                       uint4* __restrict__ th, uint4* __restrict__ tl) {
+    __shared__ float tile[32][kXtCols + 1];
+    const int64_t cb = blockIdx.x;   // column block
+    const int64_t tb = blockIdx.y;   // 32-token block
+    const int64_t k0 = cb * kXtCols, t0 = tb * 32;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int i = threadIdx.x + 256 * u;
+        const int r = i / kXtCols, c = i % kXtCols;
+        const int64_t t = t0 + r, k = k0 + c;
+        tile[r][c] = (t < B && k < K) ? x[t * K + k] : 0.f;
+    }
+    __syncthreads();
+    const int c = threadIdx.x % kXtCols;
+    const int g = threadIdx.x / kXtCols;  // 8-token group 0..3
+    const int64_t k = k0 + c;
+    if (k >= K) return;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = tile[8 * g + e][c];
+    u32x4_t h, l;
+    split_pack8(v, h, l);
+    const int64_t idx = (k * Bp + t0 + 8 * g) / 8;
+    th[idx] = make_uint4(h[0], h[1], h[2], h[3]);
+    tl[idx] = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+// dPhi rows: one workgroup per 128 output rows x 128 columns walks all
+// tokens, dPhi = hi.hi + lo.hi + hi.lo in MFMA registers, its rows stored
+// directly (non-temporal).  A = dP^T (the workgroup's 128 rows, shared by
+// its four waves)
+// goes through LDS 128 tokens at a time; B = x^T fragments of the wave's
+// own 32 columns come straight from the transposed planes, the next 32
+// tokens' in flight while the current ones are on the matrix cores.  The
+// row blocks of one column block get ids on one XCD, sharing those x
+// columns through its L2.
+constexpr int kDphiRows = 128;                // output rows (four 32-row tiles) per dPhi workgroup
+constexpr int kDphiTok = 128;                 // tokens per LDS chunk of dP^T
+constexpr int kDphiPitch = kDphiTok * 2 + 16;  // bytes per row of one plane in LDS
+
+__global__ __launch_bounds__(256) void proj_bwd_dphi_kernel(const uint4* __restrict__ dth, const uint4* __restrict__ dtl,
+                                                            const uint4* __restrict__ xth, const uint4* __restrict__ xtl,
+                                                            int np, float* __restrict__ dphi, int64_t Bp, int64_t K) {
     constexpr int CB = 128;
     constexpr int OT = kDphiRows / 16;
+    constexpr int PITCH = kDphiPitch;
+    __shared__ __align__(16) char as[2][kDphiRows * PITCH];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int lr = lane & 15;
     const int lg = lane >> 4;
-    // the row blocks of one column block on one XCD (as in proj_bwd_dx2_kernel)
     const int64_t rblocks = (np + kDphiRows - 1) / kDphiRows;
+    const int64_t cblocks = (K + CB - 1) / CB;
     const int64_t lin = blockIdx.x;
     const int64_t idx = lin / 8;
     const int o0 = (int)(idx % rblocks) * kDphiRows;
-    const int64_t kb0 = ((idx / rblocks) * 8 + lin % 8) * CB + wave * 32;
-    if (kb0 >= K) return;
+    const int64_t cb = (idx / rblocks) * 8 + lin % 8;
+    if (cb >= cblocks) return;  // padding ids: the whole workgroup
+    const int64_t kb0 = cb * CB + wave * 32;
+    const bool wave_on = kb0 < K;  // K % 32 == 0: whole waves are in or out
+    const int64_t rowp = Bp / 8;   // 16-byte pieces per plane row
     f32x4_t acc[OT][2];
 #pragma unroll
     for (int ot = 0; ot < OT; ++ot) {
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) acc[ot][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-    for (int64_t t0 = 0; t0 < B; t0 += 32) {
-        // A = dP^T: rows o = o0 + 16 ot + lr, tokens t0 + 8 lg + e
-        u32x4_t ah[OT], al[OT];
-#pragma unroll
-        for (int ot = 0; ot < OT; ++ot) {
-            const int o = o0 + 16 * ot + lr;
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int64_t t = t0 + 8 * lg + e;
-                v[e] = (t < B && o < np) ? dP[t * dp_stride + o] : 0.f;
-            }
-            split_pack8(v, ah[ot], al[ot]);
-        }
-        // B = x: tokens t0 + 8 lg + e, column 16 ct + lr
-        u32x4_t xh[2], xl[2];
+    auto u4 = [](const uint4& q) __attribute__((always_inline)) { return u32x4_t{q.x, q.y, q.z, q.w}; };
+    // B = x^T: column kb0 + 16 ct + lr, tokens t0 + 8 lg .. + 7
+    struct BFrag {
+        uint4 h[2], l[2];
+    };
+    auto load_b = [&](BFrag& f, int64_t t0) __attribute__((always_inline)) {
+        const int64_t tp = (t0 + 8 * lg) / 8;
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int64_t t = t0 + 8 * lg + e;
-                v[e] = t < B ? x[t * K + kb0 + 16 * ct + lr] : 0.f;
-            }
-            split_pack8(v, xh[ct], xl[ct]);
+            const int64_t r = (wave_on ? kb0 + 16 * ct + lr : 0) * rowp + tp;
+            f.h[ct] = xth[r];
+            f.l[ct] = xtl[r];
         }
-#pragma unroll
-        for (int ot = 0; ot < OT; ++ot) {
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                acc[ot][ct] = mfma16x16x32(ah[ot], xh[ct], acc[ot][ct]);
-                acc[ot][ct] = mfma16x16x32(al[ot], xh[ct], acc[ot][ct]);
-                acc[ot][ct] = mfma16x16x32(ah[ot], xl[ct], acc[ot][ct]);
-            }
+    };
+    for (int64_t c0 = 0; c0 < Bp; c0 += kDphiTok) {
+        const int tc = Bp - c0 < kDphiTok ? (int)(Bp - c0) : kDphiTok;  // a multiple of 32
+        // dP^T rows o0 .. o0 + 63, tokens c0 .. c0 + tc - 1, both planes:
+        // piece i = (plane, row, 16-byte column)
+        const int pieces = 2 * kDphiRows * (tc / 8);
+        for (int i = threadIdx.x; i < pieces; i += 256) {
+            const int pl = i / (kDphiRows * (tc / 8));
+            const int r = (i / (tc / 8)) % kDphiRows;
+            const int c = i % (tc / 8);
+            const uint4* src = pl == 0 ? dth : dtl;
+            *reinterpret_cast<uint4*>(&as[pl][r * PITCH + 16 * c]) = src[(int64_t)(o0 + r) * rowp + c0 / 8 + c];
         }
+        __syncthreads();
+        if (wave_on) {
+            BFrag fa, fb;
+            int t = 0;
+            load_b(fa, c0);
+            auto mma = [&](const BFrag& f, int tt) __attribute__((always_inline)) {
+#pragma unroll
+                for (int ot = 0; ot < OT; ++ot) {
+                    const int off = (16 * ot + lr) * PITCH + (tt + 8 * lg) * 2;
+                    const u32x4_t ah = u4(*reinterpret_cast<const uint4*>(&as[0][off]));
+                    const u32x4_t al = u4(*reinterpret_cast<const uint4*>(&as[1][off]));
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) {
+                        acc[ot][ct] = mfma16x16x32(ah, u4(f.h[ct]), acc[ot][ct]);
+                        acc[ot][ct] = mfma16x16x32(al, u4(f.h[ct]), acc[ot][ct]);
+                        acc[ot][ct] = mfma16x16x32(ah, u4(f.l[ct]), acc[ot][ct]);
+                    }
+                }
+            };
+            for (; t + 64 <= tc; t += 64) {
+                load_b(fb, c0 + t + 32);
+                mma(fa, t);
+                if (t + 64 < tc) load_b(fa, c0 + t + 64);
+                mma(fb, t + 32);
+            }
+            if (t < tc) mma(fa, t);
+        }
+        __syncthreads();  // the chunk is restaged
     }
+    if (!wave_on) return;
     // D[o 16 ot + 4 lg + i][column 16 ct + lr]
 #pragma unroll
     for (int ot = 0; ot < OT; ++ot) {
@@ -1973,7 +2066,7 @@ __global__ __launch_bounds__(256) void proj_bwd_dphi_kernel(const float* __restr
             const int o = o0 + 16 * ot + 4 * lg + i;
             if (o >= np) continue;
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) dphi[(int64_t)o * K + kb0 + 16 * ct + lr] = acc[ot][ct][i];
+            for (int ct = 0; ct < 2; ++ct) __builtin_nontemporal_store(acc[ot][ct][i], dphi + (int64_t)o * K + kb0 + 16 * ct + lr);
         }
     }
 }
@@ -1982,10 +2075,26 @@ bool proj_bwd_wide_path(int x_dtype, int np, int64_t B) {
     return x_dtype == kF32 && np > kProjTile && B >= 1 && B <= kProjWideMaxB;
 }
 
-size_t proj_bwd_wide_scratch_bytes(int np, int64_t B) {
-    const size_t plane = (((size_t)B * proj_tiles(np) * kProjTile * 2) + 255) & ~(size_t)255;
-    return 2 * plane;
+// scratch of the all-tiles path: [dP hi | dP lo] ([B][np32] bf16),
+// [dP^T hi | lo] ([np64][Bp], np64 = np rounded up to the dPhi row block),
+// [x^T hi | lo] ([K][Bp]); each plane 256-byte aligned.
+struct WideScratch {
+    size_t dp_plane, dpt_plane, xt_plane, total;
+};
+static WideScratch wide_scratch(int np, int64_t B, int64_t K) {
+    auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const int64_t np32 = (int64_t)proj_tiles(np) * kProjTile;
+    const int64_t np64 = (np + kDphiRows - 1) / kDphiRows * kDphiRows;  // dPhi row blocks
+    const int64_t Bp = (B + 31) / 32 * 32;
+    WideScratch w{};
+    w.dp_plane = al((size_t)B * np32 * 2);
+    w.dpt_plane = al((size_t)np64 * Bp * 2);
+    w.xt_plane = al((size_t)K * Bp * 2);
+    w.total = 2 * (w.dp_plane + w.dpt_plane + w.xt_plane);
+    return w;
 }
+
+size_t proj_bwd_wide_scratch_bytes(int np, int64_t B, int64_t K) { return wide_scratch(np, B, K).total; }
 
 hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, const float* s_tok,
                                 const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
@@ -1996,9 +2105,16 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
     if (s_tok && !accumulate) return hipErrorInvalidValue;
     const unsigned cblocks = (unsigned)((K + 127) / 128);
     const int np32 = proj_tiles(np) * kProjTile;
+    const int64_t Bp = (B + 31) / 32 * 32;
+    const WideScratch ws = wide_scratch(np, B, K);
+    char* sc = reinterpret_cast<char*>(scratch);
     // dP -> hi / lo bf16 planes in scratch
-    uint4* dph = reinterpret_cast<uint4*>(scratch);
-    uint4* dpl = reinterpret_cast<uint4*>((char*)scratch + proj_bwd_wide_scratch_bytes(np, B) / 2);
+    uint4* dph = reinterpret_cast<uint4*>(sc);
+    uint4* dpl = reinterpret_cast<uint4*>(sc + ws.dp_plane);
+    uint4* dth = reinterpret_cast<uint4*>(sc + 2 * ws.dp_plane);
+    uint4* dtl = reinterpret_cast<uint4*>(sc + 2 * ws.dp_plane + ws.dpt_plane);
+    uint4* xth = reinterpret_cast<uint4*>(sc + 2 * (ws.dp_plane + ws.dpt_plane));
+    uint4* xtl = reinterpret_cast<uint4*>(sc + 2 * (ws.dp_plane + ws.dpt_plane) + ws.xt_plane);
     const int64_t pieces = B * (np32 / 8);
     hipLaunchKernelGGL(dp_split_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, dP, dp_stride, np,
                        np32, B, dph, dpl);
@@ -2020,9 +2136,15 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
     timing_end(tok, s);
     if (e != hipSuccess) return e;
     const int tg = timing_begin("proj_bwd_dphi", s);
+    const int np64 = (np + kDphiRows - 1) / kDphiRows * kDphiRows;
+    const int64_t tgroups = (int64_t)np64 * (Bp / 8);
+    hipLaunchKernelGGL(dp_tsplit_kernel, dim3((unsigned)((tgroups + 255) / 256)), dim3(256), 0, s, dP, dp_stride, np,
+                       np64, B, Bp, dth, dtl);
+    hipLaunchKernelGGL(x_tsplit_kernel, dim3((unsigned)((K + kXtCols - 1) / kXtCols), (unsigned)(Bp / 32)), dim3(256),
+                       0, s, x, B, K, Bp, xth, xtl);
     const unsigned rblocks = (unsigned)((np + kDphiRows - 1) / kDphiRows);
-    hipLaunchKernelGGL(proj_bwd_dphi_kernel, dim3(8u * ((cblocks + 7) / 8) * rblocks), dim3(256), 0, s, x, dP,
-                       dp_stride, np, dphi, B, K);
+    hipLaunchKernelGGL(proj_bwd_dphi_kernel, dim3(8u * ((cblocks + 7) / 8) * rblocks), dim3(256), 0, s, dth, dtl, xth,
+                       xtl, np, dphi, Bp, K);
     timing_end(tg, s);
     return hipGetLastError();
 }

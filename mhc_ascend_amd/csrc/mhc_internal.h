@@ -204,10 +204,10 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
 // the next n_pre from `post`, the rest from `res`.  K % 32 == 0.
 int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K);
 // More than one output tile, fp32 x, up to 1024 tokens: dx over all tiles in
-// one pass and dPhi written directly (no partials).  scratch holds dP as
-// two bf16 planes (proj_bwd_wide_scratch_bytes).
+// one pass and dPhi written directly (no partials).  scratch holds dP, dP^T
+// and x^T as bf16 hi / lo planes (proj_bwd_wide_scratch_bytes).
 bool proj_bwd_wide_path(int x_dtype, int np, int64_t B);
-size_t proj_bwd_wide_scratch_bytes(int np, int64_t B);
+size_t proj_bwd_wide_scratch_bytes(int np, int64_t B, int64_t K);
 hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, const float* s_tok,
                                 const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                                 float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
