@@ -328,7 +328,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 }
 
 // ---------------------------------------------------------------------------
-// Projection over more than one 32-row output tile (2n + n^2 > 32: n >= 8),
+// Projection over more than 128 output rows (2n + n^2 > 128: n >= 16),
 // reading Phi once.  Workgroup = 128 output rows (one 32-row output tile
 // per wave, two 16-row MFMA tiles that share each x fragment read from LDS)
 // x TB = 16 MT tokens x one K range; Phi is the large operand here
@@ -1501,7 +1501,10 @@ static const void* proj_stream_fn(int mt) {
     }
 }
 
-bool proj_stream_path(int np) { return np > kProjTile; }
+// The streaming projection pays off where Phi outweighs x (np > 128, n >= 16:
+// 288 rows at n = 16, 1088 at n = 32); below that the per-tile kernel, whose
+// x re-reads are few, is faster.
+bool proj_stream_path(int np) { return np > kStreamOB; }
 
 // K splits of the streaming projection: token blocks x output blocks x
 // splits fill two rounds of resident workgroups (occupancy of the fp32-x
@@ -1515,8 +1518,10 @@ static int proj_stream_ksplit(int64_t B, int64_t K, int np) {
         (void)hipGetLastError();
         per_cu = 1;
     }
-    // rounded down: a last partial round would leave most CUs idle while it runs
+    // rounded down: a last partial round would leave most CUs idle while it
+    // runs; at most 32 splits (the coefficient kernel adds them per token)
     int64_t ks = 2 * (int64_t)device_cu_count() * per_cu / groups0;
+    if (ks > 32) ks = 32;
     const int64_t kmax = (K + 2 * kStreamKS - 1) / (2 * kStreamKS);
     if (ks > kmax) ks = kmax;
     if (ks < 1) ks = 1;
@@ -1722,7 +1727,8 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
 // Projection backward over many 32-row output tiles (2n + n^2 > 32 rows:
 // n >= 8), fp32 x and dx (bf16 x is upcast before it gets here), for
 // batches up to kProjWideMaxB tokens.  The per-tile kernel above would read
-// x and dx once per tile (34 times at n = 32); instead:
+// x and dx once per tile (34 times at n = 32); instead, up to 128 rows the
+// two small-np kernels below, and above that:
 //   dp_split_kernel + proj_bwd_dx2_kernel: dP split into hi / lo planes
 //     once; one workgroup per 128 columns x up to 128 tokens loops over the
 //     output tiles, dx_proj^T accumulating in MFMA registers (A = Phi^T,
@@ -1737,6 +1743,200 @@ hipError_t launch_small_column_sum(const float* part, int rows, int cols, float*
 // Operands are split hi / lo (hi.hi + lo.hi + hi.lo, as above).
 // ---------------------------------------------------------------------------
 constexpr int kProjWideMaxB = 1024;
+
+// ---------------------------------------------------------------------------
+// Up to 128 output rows (n = 8: 80), where the all-tiles kernels below would
+// have few workgroups: dx from one workgroup per 128 columns x 32 tokens
+// looping over the output tiles (A = Phi^T, the next tile's values loaded
+// while the current one computes, split hi / lo in registers; B = dP^T read
+// straight from dP and split), and dPhi from one workgroup per 64 output
+// rows x 128 columns walking all tokens in 32-token stages (dP^T and x
+// split in registers).  The token blocks (row blocks) of one column block
+// run on one XCD and share Phi (those x columns) through its L2.
+// ---------------------------------------------------------------------------
+// 8 consecutive fp32 (32-byte aligned) as two 16-byte loads
+__device__ __forceinline__ void ld8f(const float* p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <bool ACC, bool HAS_S>
+__global__ __launch_bounds__(256) void proj_bwd_dx_small_kernel(
+    const float* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
+    const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
+    int n_pre, int np, float* __restrict__ dx, int64_t B, int64_t K) {
+    constexpr int CB = 128;
+    constexpr int TS = 1;  // 32-token stages per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    // Workgroups go round-robin over the 8 XCDs by linear id; the token
+    // blocks of one column block are given ids on the same XCD, one after
+    // another, so they share that column block's Phi in the XCD's L2.
+    const int64_t tblocks = (B + 32 * TS - 1) / (32 * TS);
+    const int64_t lin = blockIdx.x;
+    const int64_t idx = lin / 8;
+    const int64_t cb = (idx / tblocks) * 8 + lin % 8;
+    const int64_t kb0 = cb * CB + wave * 32;  // this wave's 32 columns
+    if (kb0 >= K) return;  // padding ids, and K % 32 == 0: whole waves are in or out
+    const int64_t tb0 = (idx % tblocks) * (32 * TS);
+    f32x4_t d[TS][2][2];
+#pragma unroll
+    for (int st = 0; st < TS; ++st) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) d[st][tt][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    // dP columns are read 8 at a time: a stride that is a multiple of 8
+    // allows the aligned 16-byte loads (the layer's dP rows are)
+    const bool dp_vec = (dp_stride % 8) == 0;
+    // A = Phi^T: Phi[o0 + 8 lg + e][column 16 ct + lr]; the next tile's
+    // values are loaded while the current tile is on the matrix cores
+    float pv[2][8];
+    auto load_phi = [&](int o0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int o = o0 + 8 * lg + e;
+                pv[ct][e] = o < np ? phi_row(phi_pre, phi_post, phi_res, n_pre, o, K)[kb0 + 16 * ct + lr] : 0.f;
+            }
+        }
+    };
+    load_phi(0);
+    for (int o0 = 0; o0 < np; o0 += 32) {
+        u32x4_t phh[2], phl[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) split_pack8(pv[ct], phh[ct], phl[ct]);
+        if (o0 + 32 < np) load_phi(o0 + 32);
+#pragma unroll
+        for (int st = 0; st < TS; ++st) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                // B = dP^T: dP[token 16 tt + lr][o0 + 8 lg .. + 7]
+                const int64_t t = tb0 + 32 * st + 16 * tt + lr;
+                float v[8];
+                const int ob = o0 + 8 * lg;
+                if (t < B && dp_vec && ob + 8 <= np) {
+                    ld8f(dP + t * dp_stride + ob, v);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = (t < B && ob + e < np) ? dP[t * dp_stride + ob + e] : 0.f;
+                }
+                u32x4_t bh, bl;
+                split_pack8(v, bh, bl);
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    d[st][tt][ct] = mfma16x16x32(phh[ct], bh, d[st][tt][ct]);
+                    d[st][tt][ct] = mfma16x16x32(phl[ct], bh, d[st][tt][ct]);
+                    d[st][tt][ct] = mfma16x16x32(phh[ct], bl, d[st][tt][ct]);
+                }
+            }
+        }
+    }
+    // D[column 16 ct + 4 lg + i][token 16 tt + lr]: four consecutive columns of one token
+#pragma unroll
+    for (int st = 0; st < TS; ++st) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int64_t t = tb0 + 32 * st + 16 * tt + lr;
+            if (t >= B) continue;
+            const float sv = HAS_S ? s_tok[t] : 0.f;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const int64_t off = t * K + kb0 + 16 * ct + 4 * lg;
+                float4 o = make_float4(d[st][tt][ct][0], d[st][tt][ct][1], d[st][tt][ct][2], d[st][tt][ct][3]);
+                if constexpr (ACC) {
+                    const float4 a = *reinterpret_cast<const float4*>(dx + off);
+                    o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
+                }
+                if constexpr (HAS_S) {
+                    const float4 xv = *reinterpret_cast<const float4*>(x + off);
+                    o.x += sv * xv.x; o.y += sv * xv.y; o.z += sv * xv.z; o.w += sv * xv.w;
+                }
+                *reinterpret_cast<float4*>(dx + off) = o;
+            }
+        }
+    }
+}
+
+constexpr int kDphiSmallRows = 64;  // output rows (two 32-row tiles) per workgroup
+
+__global__ __launch_bounds__(256) void proj_bwd_dphi_small_kernel(const float* __restrict__ x, const float* __restrict__ dP,
+                                                            int dp_stride, int np, float* __restrict__ dphi,
+                                                            int64_t B, int64_t K) {
+    constexpr int CB = 128;
+    constexpr int OT = kDphiSmallRows / 16;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    // the row blocks of one column block on one XCD (as in proj_bwd_dx_small_kernel)
+    const int64_t rblocks = (np + kDphiSmallRows - 1) / kDphiSmallRows;
+    const int64_t lin = blockIdx.x;
+    const int64_t idx = lin / 8;
+    const int o0 = (int)(idx % rblocks) * kDphiSmallRows;
+    const int64_t kb0 = ((idx / rblocks) * 8 + lin % 8) * CB + wave * 32;
+    if (kb0 >= K) return;
+    f32x4_t acc[OT][2];
+#pragma unroll
+    for (int ot = 0; ot < OT; ++ot) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) acc[ot][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int64_t t0 = 0; t0 < B; t0 += 32) {
+        // A = dP^T: rows o = o0 + 16 ot + lr, tokens t0 + 8 lg + e
+        u32x4_t ah[OT], al[OT];
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) {
+            const int o = o0 + 16 * ot + lr;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t t = t0 + 8 * lg + e;
+                v[e] = (t < B && o < np) ? dP[t * dp_stride + o] : 0.f;
+            }
+            split_pack8(v, ah[ot], al[ot]);
+        }
+        // B = x: tokens t0 + 8 lg + e, column 16 ct + lr
+        u32x4_t xh[2], xl[2];
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int64_t t = t0 + 8 * lg + e;
+                v[e] = t < B ? x[t * K + kb0 + 16 * ct + lr] : 0.f;
+            }
+            split_pack8(v, xh[ct], xl[ct]);
+        }
+#pragma unroll
+        for (int ot = 0; ot < OT; ++ot) {
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                acc[ot][ct] = mfma16x16x32(ah[ot], xh[ct], acc[ot][ct]);
+                acc[ot][ct] = mfma16x16x32(al[ot], xh[ct], acc[ot][ct]);
+                acc[ot][ct] = mfma16x16x32(ah[ot], xl[ct], acc[ot][ct]);
+            }
+        }
+    }
+    // D[o 16 ot + 4 lg + i][column 16 ct + lr]
+#pragma unroll
+    for (int ot = 0; ot < OT; ++ot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int o = o0 + 16 * ot + 4 * lg + i;
+            if (o >= np) continue;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) dphi[(int64_t)o * K + kb0 + 16 * ct + lr] = acc[ot][ct][i];
+        }
+    }
+}
 
 // dP [B][stride] (np valid columns) -> bf16 planes hi / lo [B][np32]
 // (np32 = np rounded up to 32, zero past np): 8 consecutive outputs of a
@@ -2087,6 +2287,7 @@ static WideScratch wide_scratch(int np, int64_t B, int64_t K) {
     const int64_t np64 = (np + kDphiRows - 1) / kDphiRows * kDphiRows;  // dPhi row blocks
     const int64_t Bp = (B + 31) / 32 * 32;
     WideScratch w{};
+    if (np <= kStreamOB) return w;  // the small-np kernels split in registers
     w.dp_plane = al((size_t)B * np32 * 2);
     w.dpt_plane = al((size_t)np64 * Bp * 2);
     w.xt_plane = al((size_t)K * Bp * 2);
@@ -2101,9 +2302,35 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
                                 float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
                                 hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (np <= kProjTile || B > kProjWideMaxB || K % 32 != 0 || !scratch) return hipErrorInvalidValue;
+    if (np <= kProjTile || B > kProjWideMaxB || K % 32 != 0) return hipErrorInvalidValue;
     if (s_tok && !accumulate) return hipErrorInvalidValue;
     const unsigned cblocks = (unsigned)((K + 127) / 128);
+    if (np <= kStreamOB) {
+        // 1-D grid: 8 XCD lanes x ceil(column blocks / 8) x 32-token blocks
+        const unsigned tb32 = (unsigned)((B + 31) / 32);
+        const dim3 gs(8u * ((cblocks + 7) / 8) * tb32);
+        const int tk = timing_begin("proj_bwd", s);
+        if (s_tok) {
+            hipLaunchKernelGGL((proj_bwd_dx_small_kernel<true, true>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
+                               phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
+        } else if (accumulate) {
+            hipLaunchKernelGGL((proj_bwd_dx_small_kernel<true, false>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
+                               phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
+        } else {
+            hipLaunchKernelGGL((proj_bwd_dx_small_kernel<false, false>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
+                               phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
+        }
+        hipError_t e = hipGetLastError();
+        timing_end(tk, s);
+        if (e != hipSuccess) return e;
+        const int tg = timing_begin("proj_bwd_dphi", s);
+        const unsigned rb = (unsigned)((np + kDphiSmallRows - 1) / kDphiSmallRows);
+        hipLaunchKernelGGL(proj_bwd_dphi_small_kernel, dim3(8u * ((cblocks + 7) / 8) * rb), dim3(256), 0, s, x, dP,
+                           dp_stride, np, dphi, B, K);
+        timing_end(tg, s);
+        return hipGetLastError();
+    }
+    if (!scratch) return hipErrorInvalidValue;
     const int np32 = proj_tiles(np) * kProjTile;
     const int64_t Bp = (B + 31) / 32 * 32;
     const WideScratch ws = wide_scratch(np, B, K);

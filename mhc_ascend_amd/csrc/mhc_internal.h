@@ -168,7 +168,7 @@ int proj_ksplit(int64_t B, int64_t K, int np);
 // p_part[tile][ks][B][32], plus ss_part[ks][B] = partial sums of x^2.
 hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_raw_t* phib, int np, float* p_part,
                             float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s);
-// More than one output tile (np > 32): the streaming projection reads Phi
+// More than 128 rows (proj_stream_path): the streaming projection reads Phi
 // once (fp32 rows from pre / post / res as phi_row, or, when phib is not
 // null, the planes of launch_phi_split); fp32 x is first split into
 // xplanes (proj_xplanes_bytes) with ss_part.  Same p_part / ss_part layout

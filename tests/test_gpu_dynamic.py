@@ -27,8 +27,11 @@ def _gen(seed):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,K,out_dim", [(1, 32, 1), (3, 96, 8), (70, 1024, 24), (129, 4160, 24), (300, 4096, 32),
                                          (65, 16384, 24), (9, 320, 33), (70, 1024, 80), (40, 2048, 100),
-                                         (1500, 96, 40)])
+                                         (1500, 96, 40), (37, 1024, 129), (130, 2048, 300), (200, 640, 1088)])
 def test_projection(device, dtype, B, K, out_dim):
+    """Projection forward / backward against float64; more than 128 output
+    rows run the streaming kernel (Phi once, fp32 x as bf16 planes), up to
+    1024 tokens the backward's all-tiles path."""
     g = _gen(B + K + out_dim)
     x = torch.randn(B, K, generator=g).to(dtype)
     phi = 0.02 * torch.randn(out_dim, K, generator=g)
