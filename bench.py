@@ -492,7 +492,7 @@ PAPER_CONFIGS = [(320, 1280, 4), (512, 1920, 4), (1280, 2560, 4), (2560, 1280, 4
                  (32, 1280, 32), (64, 1280, 32), (128, 1280, 32)]
 
 
-def paper_sweep(torch, mhc, device, warmup=10, runs=100):
+def paper_sweep(torch, mhc, device, warmup=10, runs=100, only=None):
     flush = torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=device)
 
     def timed(fn, B, n, C, train):
@@ -563,6 +563,8 @@ def paper_sweep(torch, mhc, device, warmup=10, runs=100):
     rows = []
     for dynamic in (False, True):
         for B, C, n in PAPER_CONFIGS:
+            if only and (B, C, n) not in only:
+                continue
             torch.manual_seed(0)
             layer = mhc.MHCLayer(C, n, use_dynamic_h=dynamic).to(device)
 
@@ -598,6 +600,8 @@ def main(argv=None) -> int:
     ap.add_argument("--paper-configs", action="store_true",
                     help="instead of a workload: the reference's 9-configuration sweep (benchmark.py:299-311), "
                          "static and dynamic H, forward and forward+backward ms per configuration")
+    ap.add_argument("--paper-filter", action="append", default=[], metavar="B,C,n",
+                    help="with --paper-configs: run only these configurations (repeatable)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 1 GiB device copy (known bytes) for PMC counter calibration")
     a = ap.parse_args(argv)
@@ -618,7 +622,15 @@ def main(argv=None) -> int:
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     if a.paper_configs:
-        rows = paper_sweep(torch, mhc, device)
+        only = None
+        if a.paper_filter:
+            only = set()
+            for f in a.paper_filter:
+                cfg = tuple(int(v) for v in f.split(","))
+                if cfg not in PAPER_CONFIGS:
+                    _die(f"bench.py: --paper-filter {f} is not one of the configurations {PAPER_CONFIGS}")
+                only.add(cfg)
+        rows = paper_sweep(torch, mhc, device, only=only)
         geo = 1.0
         for r in rows:
             geo *= r["fwd_bwd_ms"]

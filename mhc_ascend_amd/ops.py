@@ -19,6 +19,10 @@ import torch
 
 from . import native
 
+# Projection rows above which the library's dynamic forward streams the fp32
+# projections (2n + n^2 > 128: n >= 16) instead of split planes.
+_STREAM_PROJ_ROWS = 128
+
 
 # =============================================================================
 # Sinkhorn-Knopp (ops.py:32-80)
@@ -204,6 +208,13 @@ def mhc_layer_fused_dynamic_inference(x_expanded, rmsnorm_weight, phi_pre, phi_p
     ``packed`` (from native.mhc_layer_dynamic_pack on the same weight and
     projections) skips the per-call packing of the parameters."""
     if packed is None:
+        if out_dtype == torch.float32 and 2 * phi_pre.shape[0] + phi_res.shape[0] > _STREAM_PROJ_ROWS:
+            # More than 128 projection rows: the forward reads the fp32
+            # projections directly (no packing pass), and its fp32 output is
+            # the packed entry's bit for bit.
+            return native.mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
+                                                alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters,
+                                                sinkhorn_eps, rmsnorm_eps)[0]
         packed = native.mhc_layer_dynamic_pack(rmsnorm_weight, phi_pre, phi_post, phi_res)
     return native.mhc_layer_dynamic_infer(x_expanded, packed, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
                                           sinkhorn_iters, sinkhorn_eps, rmsnorm_eps, out_dtype)
