@@ -24,6 +24,7 @@
 namespace mhc {
 
 constexpr int kWideThreads = 256;
+constexpr int kWideFwdThreads = 1024;  // the forward: one token per workgroup, 1-2 channels per lane
 
 template <typename T>
 __device__ __forceinline__ float ld_elem_nt(const T* p) {
@@ -65,31 +66,25 @@ __device__ __forceinline__ void wide_block_total(float (&v)[NV], float* red, flo
 }
 
 // ---------------------------------------------------------------------------
-// Forward: one workgroup per (token b, channel chunk s).  Its row sum of
-// xa^2 runs over the whole token, so no workgroup waits for another and no
-// scratch is needed; the outputs are its chunk's.  With S > 1 chunks the
-// token's S workgroups are placed on one XCD (workgroups go round-robin over
-// the 8 XCDs by linear id: id = 8 (S t + s) + xcd for token b = 8 t + xcd),
-// so all but the first read the row from that XCD's L2.  Two channels per
-// lane and step keep 2 N loads in flight.  out in TO (fp32, or bf16 for the
-// forward-only entry); rms_out[b] = r when not null (chunk 0).
+// Forward: one token per workgroup of 1024 lanes (one or two channels per
+// lane at the paper widths), so the row sum of xa^2 is one round of 2 N
+// loads per lane in flight and the output pass re-reads the row from cache.
+// (Splitting a token's channels over 256-lane workgroups, each redoing the
+// row sum, measured slower at 32-128 tokens: the n = 32, C = 1280 eval
+// forward took 0.076 against 0.058 ms at 32 tokens.)  out in TO (fp32, or
+// bf16 for the
+// forward-only entry); rms_out[b] = r when not null.
 // ---------------------------------------------------------------------------
 template <typename TX, typename TO, int N>
-__global__ __launch_bounds__(kWideThreads) void wide_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
-                                                                const float* __restrict__ coef, int64_t coef_stride,
-                                                                TO* __restrict__ out, float* __restrict__ rms_out,
-                                                                int64_t B, int C, float eps, int S, int chunk) {
+__global__ __launch_bounds__(kWideFwdThreads) void wide_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
+                                                                   const float* __restrict__ coef, int64_t coef_stride,
+                                                                   TO* __restrict__ out, float* __restrict__ rms_out,
+                                                                   int64_t B, int C, float eps) {
     constexpr int NC = 2 * N + N * N;
-    __shared__ float red[kWideThreads / kWave];
+    __shared__ float red[kWideFwdThreads / kWave];
     __shared__ float tot[1];
     __shared__ float cfs[NC];
-    int64_t b = blockIdx.x;
-    int sc = 0;
-    if (S > 1) {
-        const int64_t k = blockIdx.x / 8;
-        b = (k / S) * 8 + blockIdx.x % 8;
-        sc = (int)(k % S);
-    }
+    const int64_t b = blockIdx.x;
     if (b >= B) return;
     const float* cf = coef + b * coef_stride;
     // the coefficients go to LDS for the output pass (read there, all lanes
@@ -121,8 +116,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_fwd_kernel(const TX* __rest
     const float r = sqrtf(tot[0] / (float)C + eps);
     const float inv = 1.f / r;
     TO* ob = out + b * (int64_t)N * C;
-    const int c_end = (sc + 1) * chunk < C ? (sc + 1) * chunk : C;
-    for (int c = sc * chunk + threadIdx.x; c < c_end; c += blockDim.x) {
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
         float xv[N];
 #pragma unroll
         for (int j = 0; j < N; ++j) xv[j] = ld_elem_nt(xb + (int64_t)j * C + c);
@@ -138,7 +132,7 @@ __global__ __launch_bounds__(kWideThreads) void wide_fwd_kernel(const TX* __rest
             st_elem_nt(ob + (int64_t)i * C + c, s);
         }
     }
-    if (threadIdx.x == 0 && sc == 0 && rms_out) rms_out[b] = r;
+    if (threadIdx.x == 0 && rms_out) rms_out[b] = r;
 }
 
 // ---------------------------------------------------------------------------
@@ -850,29 +844,17 @@ bool wide_supported(int n, int64_t C) {
     return (n == 2 || n == 4 || n == 8 || n == 16 || n == 32) && C >= 1 && C <= kWideMaxC;
 }
 
-// Channel chunks per token: one chunk of kWideThreads channels per
-// workgroup (one channel per lane) when there are fewer tokens than two
-// workgroups per CU, else whole rows.
-static int wide_fwd_chunks(int64_t B, int64_t C) {
-    if (B >= 2 * (int64_t)device_cu_count()) return 1;
-    const int64_t S = (C + kWideThreads - 1) / kWideThreads;
-    return (int)(S < 1 ? 1 : S);
-}
-
 hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
                            int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
                            hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!wide_supported(n, C) || B > 0x7fffffff) return hipErrorInvalidValue;
     const int Ci = (int)C;
-    const int S = wide_fwd_chunks(B, C);
-    const int chunk = (int)((C + S - 1) / S);
-    // with chunks, the token count is rounded up to whole XCD rounds
-    const dim3 grid((unsigned)(S > 1 ? ((B + 7) / 8) * 8 * S : B)), block(kWideThreads);
+    const dim3 grid((unsigned)B), block(kWideFwdThreads);
     const int tok = timing_begin("layer_fwd", s);
 #define MHC_WIDE_FWD(TX_, TO_)                                                                                   \
     MHC_WIDE_N(n, hipLaunchKernelGGL((wide_fwd_kernel<TX_, TO_, N_>), grid, block, 0, s, (const TX_*)x, w, coef, \
-                                     coef_stride, (TO_*)out, rms_out, B, Ci, eps, S, chunk))
+                                     coef_stride, (TO_*)out, rms_out, B, Ci, eps))
     if (x_dtype == kBF16) {
         if (out_dtype == kBF16) { MHC_WIDE_FWD(bf16_t, bf16_t); } else { MHC_WIDE_FWD(bf16_t, float); }
     } else {
@@ -888,9 +870,15 @@ static const void* wide_bwd_fn() {
     return reinterpret_cast<const void*>(&wide_bwd_kernel<TX, N, MODE, (N <= 8)>);
 }
 
-// Channel chunks of the backward: as the forward's, used only when a token
-// splits into at least two chunks (then the partial rows are one per token).
-static int wide_bwd_chunks(int64_t B, int64_t C) { return wide_fwd_chunks(B, C); }
+// Channel chunks of the backward: one chunk of kWideThreads channels per
+// workgroup (one channel per lane) when there are fewer tokens than two
+// workgroups per CU, used only when a token splits into at least two chunks
+// (then the partial rows are one per token).
+static int wide_bwd_chunks(int64_t B, int64_t C) {
+    if (B >= 2 * (int64_t)device_cu_count()) return 1;
+    const int64_t S = (C + kWideThreads - 1) / kWideThreads;
+    return (int)(S < 1 ? 1 : S);
+}
 
 size_t wide_bwd_scratch_bytes(int n, int64_t B, int64_t C) {
     if (!wide_supported(n, C) || B <= 0) return 0;
