@@ -886,6 +886,9 @@ __global__ __launch_bounds__(skb::kThreads) void dyn_coef32_fwd_kernel(
     const int64_t tok = blockIdx.x;
     const int i = skb::row(), c0 = skb::col0();
     float pp = 0.f, pq = 0.f, pr[V] = {0.f, 0.f, 0.f, 0.f}, ss = 0.f;
+    // unrolled so that the loads of several splits are in flight together
+    // (the sums stay in split order)
+#pragma unroll 8
     for (int q = 0; q < ks; ++q) {
         ss += ss_part[(int64_t)q * B + tok];
         pp += p_part_at(p_part, ks, B, q, tok, i);
@@ -1519,9 +1522,11 @@ static int proj_stream_ksplit(int64_t B, int64_t K, int np) {
         per_cu = 1;
     }
     // rounded down: a last partial round would leave most CUs idle while it
-    // runs; at most 32 splits (the coefficient kernel adds them per token)
+    // runs; splits x tokens at most 4096 (the partials the coefficient
+    // kernel adds per token: 32 splits at 128 tokens, 128 at 32)
     int64_t ks = 2 * (int64_t)device_cu_count() * per_cu / groups0;
-    if (ks > 32) ks = 32;
+    const int64_t kcap = B > 0 ? (4096 + B - 1) / B : 1;
+    if (ks > kcap) ks = kcap;
     const int64_t kmax = (K + 2 * kStreamKS - 1) / (2 * kStreamKS);
     if (ks > kmax) ks = kmax;
     if (ks < 1) ks = 1;
