@@ -1492,16 +1492,16 @@ hipError_t launch_phi_split(const float* pre, const float* post, const float* re
     return hipGetLastError();
 }
 
-// Tokens per workgroup of the streaming projection (16 MT, MT = 2, 4, 8).
+// Tokens per workgroup of the streaming projection (16 MT): 64 above 32
+// tokens (two workgroups per CU fit; 128-token workgroups read Phi once per
+// 128 tokens but fit one per CU, and measured slower in the one-tile-per-
+// wave form: 165 against 129 us at n = 32, 128 tokens), else 32.
 static int proj_stream_mt(int64_t B) { return B > 32 ? 4 : 2; }
 
 template <int XPL, int PHI>
 static const void* proj_stream_fn(int mt) {
-    switch (mt) {
-        case 2: return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 2, PHI != 0>);
-        case 4: return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 4, PHI != 0>);
-        default: return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 8, PHI != 0>);
-    }
+    if (mt == 2) return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 2, PHI != 0>);
+    return reinterpret_cast<const void*>(&proj_stream_kernel<XPL, 4, PHI != 0>);
 }
 
 // The streaming projection pays off where Phi outweighs x (np > 128, n >= 16:
@@ -1600,10 +1600,10 @@ hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, c
                            phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups);             \
     }
 #define MHC_STREAM_MT(XPL_)                               \
-    switch (mt) {                                         \
-        case 2: { MHC_STREAM(XPL_, 2); break; }           \
-        case 4: { MHC_STREAM(XPL_, 4); break; }           \
-        default: { MHC_STREAM(XPL_, 8); break; }          \
+    if (mt == 2) {                                        \
+        MHC_STREAM(XPL_, 2);                              \
+    } else {                                              \
+        MHC_STREAM(XPL_, 4);                              \
     }
     if (x_dtype == kF32) {
         MHC_STREAM_MT(3);

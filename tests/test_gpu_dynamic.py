@@ -212,6 +212,27 @@ def test_dynamic_module_inference_pack_snapshot(device):
     assert layer._inference_pack is None
 
 
+def test_dynamic_module_eval_n32_unpacked_and_packed(device):
+    """n = 32 (1088 projection rows): the unpacked eval forward runs the
+    streaming training forward, the packed one the forward-only entry on
+    the split planes; both equal the training forward bit for bit."""
+    torch.manual_seed(32)
+    layer = mhc.MHCLayer(128, 32).to(device)
+    with torch.no_grad():
+        for k in ("phi_pre", "phi_post", "phi_res"):
+            getattr(layer, k).normal_(0.0, 0.05)
+        layer.alpha_res.fill_(0.2)
+    x = torch.randn(40, 32, 128, generator=_gen(33)).to(device)
+    train_out = layer(x).detach()
+    layer.eval()
+    with torch.no_grad():
+        unpacked = layer(x)
+        layer.prepare_inference()
+        packed = layer(x)
+    assert torch.equal(unpacked, train_out)
+    assert torch.equal(packed, train_out)
+
+
 def test_dynamic_inference_rejects_bad_arguments(device):
     layer = mhc.MHCLayer(64, 4).to(device)
     scal = [layer.alpha_pre, layer.alpha_post, layer.alpha_res, layer.b_pre, layer.b_post, layer.b_res]
