@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
+import importlib.util
 import os
 import threading
 from typing import Dict, List, Tuple
@@ -116,6 +117,35 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+AUTOGRAD_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_mhc_autograd.so")
+_autograd = None
+_autograd_done = False
+_autograd_lock = threading.Lock()
+
+
+def autograd():
+    """The C++ autograd nodes of the fused layers (``_mhc_autograd.so``, a
+    torch extension built beside the library), bound to this library's
+    entry points; None when it is not built or ``MHC_CPP_AUTOGRAD=0``, in
+    which case the layers run their Python autograd functions over the same
+    entry points (identical results, more host time per call)."""
+    global _autograd, _autograd_done
+    if _autograd_done:
+        return _autograd
+    lib = load()
+    with _autograd_lock:
+        if not _autograd_done:
+            if os.environ.get("MHC_CPP_AUTOGRAD", "1") != "0" and os.path.exists(AUTOGRAD_PATH):
+                spec = importlib.util.spec_from_file_location("mhc_ascend_amd._mhc_autograd", AUTOGRAD_PATH)
+                mod = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(mod)
+                mod.bind({name: ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
+                          for name in mod.entry_names()})
+                _autograd = mod
+            _autograd_done = True
+    return _autograd
 
 
 def call(name: str, *args) -> None:

@@ -3,9 +3,12 @@
     python -m mhc_ascend_amd.csrc.build [--jobs N] [--verbose]
 
 Each .hip translation unit is compiled to an object in parallel, then all
-are linked into ``mhc_ascend_amd/libmhc_hip.so``.  Every call rebuilds from
-scratch (the build is the "does it compile" check); outputs go to the
-package directory and ``mhc_ascend_amd/csrc/_build``.
+are linked into ``mhc_ascend_amd/libmhc_hip.so``.  Alongside, g++ builds
+``mhc_ascend_amd/_mhc_autograd.so``, the C++ autograd nodes of the fused
+layers (autograd.cpp, a torch extension that calls the library through the
+addresses of its C-ABI entry points).  Every call rebuilds from scratch (the
+build is the "does it compile" check); outputs go to the package directory
+and ``mhc_ascend_amd/csrc/_build``.
 """
 from __future__ import annotations
 
@@ -23,6 +26,8 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_NAME = "libmhc_hip.so"
 LIB_PATH = os.path.join(PKG, LIB_NAME)
+AUTOGRAD_NAME = "_mhc_autograd"
+AUTOGRAD_PATH = os.path.join(PKG, AUTOGRAD_NAME + ".so")
 
 SOURCES = ["abi.hip", "dynamic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wide.hip", "wrapper.hip"]
 
@@ -60,6 +65,22 @@ def _run(cmd, verbose):
         print(out, flush=True)
 
 
+def _autograd_cmd(out: str):
+    """g++ line for the torch extension (the include and library paths of
+    torch.utils.cpp_extension; HIP headers for ATen's HIP stream API)."""
+    import sysconfig
+
+    import torch.utils.cpp_extension as ce
+
+    incs = ce.include_paths("cuda") + [sysconfig.get_paths()["include"], INCLUDE]
+    libdir = ce.library_paths()[0]
+    return (["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
+             "-DTORCH_API_INCLUDE_EXTENSION_H", f"-DTORCH_EXTENSION_NAME={AUTOGRAD_NAME}"]
+            + [f"-I{i}" for i in incs]
+            + [os.path.join(CSRC, "autograd.cpp"), "-o", out, f"-L{libdir}", "-lc10", "-ltorch", "-ltorch_cpu",
+               "-ltorch_python", "-lc10_hip", "-ltorch_hip"])
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> str:
     hipcc = _hipcc()
     os.makedirs(BUILD_DIR, exist_ok=True)
@@ -69,9 +90,12 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         cmds.append([hipcc, *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    ag_tmp = AUTOGRAD_PATH + ".tmp"
+    cmds.append(_autograd_cmd(ag_tmp))
     jobs = jobs or min(len(cmds), os.cpu_count() or 4, 16)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
+    os.replace(ag_tmp, AUTOGRAD_PATH)
     tmp = LIB_PATH + ".tmp"
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB_PATH)

@@ -17,7 +17,7 @@ from typing import Tuple
 
 import torch
 
-from . import native
+from . import _lib, native
 
 # Projection rows above which the library's dynamic forward streams the fp32
 # projections (2n + n^2 > 128: n >= 16) instead of split planes.
@@ -164,6 +164,10 @@ def mhc_layer_static(x: torch.Tensor, rmsnorm_weight: torch.Tensor, H_pre: torch
                      H_res: torch.Tensor, sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
                      rmsnorm_eps: float = 1e-5) -> torch.Tensor:
     """Static-H mHC layer on x [B, n, C] -> fp32 [B, n, C]."""
+    ag = _lib.autograd()
+    if ag is not None:
+        return ag.static_layer(x, rmsnorm_weight, H_pre, H_post, H_res, int(sinkhorn_iters), float(sinkhorn_eps),
+                               float(rmsnorm_eps))
     return MHCLayerStaticFunction.apply(x, rmsnorm_weight, H_pre, H_post, H_res, sinkhorn_iters, sinkhorn_eps,
                                         rmsnorm_eps)
 
@@ -258,6 +262,11 @@ def mhc_layer_fused_dynamic_training(x_expanded, rmsnorm_weight, phi_pre, phi_po
         alpha_post = torch.tensor(alpha_post, device=dev, dtype=torch.float32)
     if not torch.is_tensor(alpha_res):
         alpha_res = torch.tensor(alpha_res, device=dev, dtype=torch.float32)
+    ag = _lib.autograd()
+    if ag is not None:
+        return ag.dynamic_layer(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post,
+                                alpha_res, b_pre, b_post, b_res, int(sinkhorn_iters), float(sinkhorn_eps),
+                                float(rmsnorm_eps))
     return MHCLayerDynamicFunction.apply(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
                                          alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
                                          rmsnorm_eps)

@@ -102,3 +102,15 @@ def test_cpu_tensors_raise_no_fallback():
     layer = mhc.MHCLayer(16, 4, use_dynamic_h=False)
     with pytest.raises(RuntimeError, match="HIP device"):
         layer(torch.randn(3, 4, 16))
+
+
+def test_autograd_extension_binds_every_entry():
+    """_mhc_autograd.so (built with the library) imports on the CPU and binds
+    only entry points the header declares and the ctypes table types."""
+    from mhc_ascend_amd import _lib
+
+    ag = _lib.autograd()
+    assert ag is not None, f"{_lib.AUTOGRAD_PATH} is not built"
+    names = ag.entry_names()
+    assert names and all(n in _lib.SIGNATURES for n in names)
+    assert callable(ag.static_layer) and callable(ag.dynamic_layer)
