@@ -1256,9 +1256,15 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     constexpr int RPP = 256 / VPR;              // tile rows per load pass
     constexpr int PASSES = TB / RPP;
     constexpr int PITCH = pb_pitch<TX>();
-    __shared__ __align__(16) char tiles_lds[2][2][TB * PITCH];       // [buf][x | dx]
-    __shared__ __align__(16) bf16_t dps_lds[2][4][32 * kDpPitch];    // [buf][hi_row, lo_row, hi_col, lo_col]
-    __shared__ float s_lds[2][TB];
+    // Only the dx tile is double-buffered: a stage's store reads it while
+    // the next stage is committed.  x, the dP copies and s of the next
+    // stage are committed after the barrier that ends the compute reading
+    // them, so one copy each suffices (35.6 KB of LDS for bf16 x: three
+    // workgroups per CU instead of two).
+    __shared__ __align__(16) char x_lds[TB * PITCH];
+    __shared__ __align__(16) char dx_lds[2][TB * PITCH];
+    __shared__ __align__(16) bf16_t dps_lds[4][32 * kDpPitch];  // hi_row, lo_row, hi_col, lo_col
+    __shared__ float s_lds[TB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1329,12 +1335,12 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
             const int row = lrow + p * RPP;
             const uint32_t m = (lcol_ok && t0 + row < t_end) ? 0xffffffffu : 0u;  // zero masked rows
             const uint4 vx = f.x[p];
-            uint2* px = reinterpret_cast<uint2*>(&tiles_lds[buf][0][row * PITCH + lvec * 16]);
+            uint2* px = reinterpret_cast<uint2*>(&x_lds[row * PITCH + lvec * 16]);
             px[0] = make_uint2(vx.x & m, vx.y & m);
             px[1] = make_uint2(vx.z & m, vx.w & m);
             if constexpr (ACC) {
                 const uint4 vd = f.d[p];
-                uint2* pd = reinterpret_cast<uint2*>(&tiles_lds[buf][1][row * PITCH + lvec * 16]);
+                uint2* pd = reinterpret_cast<uint2*>(&dx_lds[buf][row * PITCH + lvec * 16]);
                 pd[0] = make_uint2(vd.x & m, vd.y & m);
                 pd[1] = make_uint2(vd.z & m, vd.w & m);
             }
@@ -1349,17 +1355,17 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
             hi[q] = bf16_to_f32(f32_to_bf16(v));
             lo[q] = v - hi[q];
         }
-        *reinterpret_cast<uint2*>(&dps_lds[buf][0][dtk * kDpPitch + dpo]) =
+        *reinterpret_cast<uint2*>(&dps_lds[0][dtk * kDpPitch + dpo]) =
             make_uint2(pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
-        *reinterpret_cast<uint2*>(&dps_lds[buf][1][dtk * kDpPitch + dpo]) =
+        *reinterpret_cast<uint2*>(&dps_lds[1][dtk * kDpPitch + dpo]) =
             make_uint2(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]));
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            dps_lds[buf][2][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(hi[q]);
-            dps_lds[buf][3][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(lo[q]);
+            dps_lds[2][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(hi[q]);
+            dps_lds[3][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(lo[q]);
         }
         if constexpr (HAS_S) {
-            if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? f.s : 0.f;
+            if (tid < TB) s_lds[tid] = (t0 + tid < t_end) ? f.s : 0.f;
         }
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> u32x4_t {
@@ -1368,8 +1374,8 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     };
     auto compute = [&](int cur) __attribute__((always_inline)) {
         if (!wave_on) return;
-        const char* xt = tiles_lds[cur][0];
-        char* dt = tiles_lds[cur][1];
+        const char* xt = x_lds;
+        char* dt = dx_lds[cur];
         // dPhi: A = dP^T (o = 16 ot + lr, tokens 8 lg .. + 7), B = x (same tokens, column 16 ct + lr)
         u32x4_t xh[2], xl[2];
 #pragma unroll
@@ -1387,8 +1393,8 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
         }
 #pragma unroll
         for (int ot = 0; ot < 2; ++ot) {
-            const u32x4_t ah = read16(&dps_lds[cur][2][(16 * ot + lr) * kDpPitch + 8 * lg]);
-            const u32x4_t al = read16(&dps_lds[cur][3][(16 * ot + lr) * kDpPitch + 8 * lg]);
+            const u32x4_t ah = read16(&dps_lds[2][(16 * ot + lr) * kDpPitch + 8 * lg]);
+            const u32x4_t al = read16(&dps_lds[3][(16 * ot + lr) * kDpPitch + 8 * lg]);
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
                 accP[ot][ct] = mfma16x16x32(ah, xh[ct], accP[ot][ct]);
@@ -1400,9 +1406,9 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 16 * tt + lr;
-            const u32x4_t bh = read16(&dps_lds[cur][0][t * kDpPitch + 8 * lg]);
-            const u32x4_t bl = read16(&dps_lds[cur][1][t * kDpPitch + 8 * lg]);
-            const float st = HAS_S ? s_lds[cur][t] : 0.f;
+            const u32x4_t bh = read16(&dps_lds[0][t * kDpPitch + 8 * lg]);
+            const u32x4_t bl = read16(&dps_lds[1][t * kDpPitch + 8 * lg]);
+            const float st = HAS_S ? s_lds[t] : 0.f;
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
                 f32x4_t d = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -1432,7 +1438,7 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
             if (lcol_ok && t0 + row < t_end) {
-                const uint2* ps = reinterpret_cast<const uint2*>(&tiles_lds[cur][1][row * PITCH + lvec * 16]);
+                const uint2* ps = reinterpret_cast<const uint2*>(&dx_lds[cur][row * PITCH + lvec * 16]);
                 const uint2 u0 = ps[0], u1 = ps[1];
                 st16_nt(dx + (t0 + row) * K + lcol, make_uint4(u0.x, u0.y, u1.x, u1.y));
             }
