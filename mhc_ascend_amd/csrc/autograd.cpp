@@ -8,6 +8,9 @@
 // forward and the autograd engine's hand-off to a Python backward out of
 // every step.
 //
+// The fused MHCResidualWrapper (layer.py:269-322) has nodes of the same kind
+// (mhc_ascend_amd.ops.MHCWrapperStaticFunction / MHCWrapperDynamicFunction).
+//
 // The entry points are not linked: bind() receives their addresses from the
 // ctypes handle of the already loaded library, so both paths share one copy
 // of it (one error state, one set of per-device caches) whichever build of
@@ -39,7 +42,15 @@ using torch::autograd::tensor_list;
     X(mhc_layer_dynamic_fwd_workspace_size)   \
     X(mhc_layer_dynamic_fwd)                  \
     X(mhc_layer_dynamic_bwd_workspace_size)   \
-    X(mhc_layer_dynamic_bwd)
+    X(mhc_layer_dynamic_bwd)                  \
+    X(mhc_wrapper_dynamic_saved_size)         \
+    X(mhc_wrapper_dynamic_fwd_workspace_size) \
+    X(mhc_wrapper_dynamic_fwd)                \
+    X(mhc_wrapper_dynamic_bwd_workspace_size) \
+    X(mhc_wrapper_dynamic_bwd)                \
+    X(mhc_wrapper_static_fwd)                 \
+    X(mhc_wrapper_static_bwd_workspace_size)  \
+    X(mhc_wrapper_static_bwd)
 
 struct Entries {
 #define MHC_DECLARE(name) decltype(&::name) name = nullptr;
@@ -287,6 +298,186 @@ struct DynamicLayer : public torch::autograd::Function<DynamicLayer> {
     }
 };
 
+// ---- fused MHCResidualWrapper (layer.py:269-322) ----------------------------
+std::vector<int64_t> flat_shapes(std::initializer_list<const Tensor*> ts) {
+    std::vector<int64_t> v;  // rank, then sizes, of each tensor in order
+    for (const Tensor* t : ts) {
+        v.push_back(t->dim());
+        for (int64_t d : t->sizes()) v.push_back(d);
+    }
+    return v;
+}
+
+std::vector<std::vector<int64_t>> unflat_shapes(const std::vector<int64_t>& flat) {
+    std::vector<std::vector<int64_t>> out;
+    for (size_t i = 0; i < flat.size();) {
+        const int64_t r = flat[i++];
+        out.emplace_back(flat.begin() + i, flat.begin() + i + r);
+        i += r;
+    }
+    return out;
+}
+
+// residual / branch [tokens, hidden] as the kernels read them: residual in
+// fp32 or bf16 (others become fp32), branch in the residual's dtype.
+std::pair<Tensor, Tensor> wrapper_inputs(const char* fn, const Tensor& residual, const Tensor& branch) {
+    check_device(fn, {&residual, &branch});
+    TORCH_CHECK(residual.sizes() == branch.sizes() && residual.dim() == 2, fn,
+                ": residual and branch must both be [tokens, hidden] of one shape");
+    Tensor r = (storage_dtype(residual.scalar_type()) ? residual : residual.to(at::kFloat)).contiguous();
+    return {r, branch.to(r.scalar_type()).contiguous()};
+}
+
+int32_t wrapper_mode(const std::string& mode, int64_t n, const char* fn) {
+    TORCH_CHECK_VALUE(mode == "decay" || mode == "zero", "Unknown residual_mode: ", mode);
+    // the reference writes stream 1 (layer.py:301), which needs n >= 2
+    TORCH_CHECK(n >= 2, fn, ": expansion_rate must be >= 2 (stream 1 holds the branch)");
+    return mode == "decay" ? MHC_WRAPPER_DECAY : MHC_WRAPPER_ZERO;
+}
+
+struct StaticWrapper : public torch::autograd::Function<StaticWrapper> {
+    static Tensor forward(AutogradContext* ctx, const Tensor& res_in, const Tensor& br_in, const Tensor& w_in,
+                          const Tensor& hp_in, const Tensor& hq_in, const Tensor& hr_in, int64_t mode, int64_t n,
+                          int64_t iters, double sk_eps, double rms_eps) {
+        const char* fn = "wrapper_static_fwd";
+        auto [r, b] = wrapper_inputs(fn, res_in, br_in);
+        check_device(fn, {&r, &w_in, &hp_in, &hq_in, &hr_in});
+        const at::DeviceGuard guard(r.device());
+        const int64_t T = r.size(0), C = r.size(1);
+        const Tensor w = weight(w_in);
+        TORCH_CHECK(w.numel() == C && hp_in.numel() == n && hq_in.numel() == n && hr_in.numel() == n * n,
+                    "wrapper_static_fwd: parameter shapes do not match n and C");
+        const Tensor hp = f32c(hp_in), hq = f32c(hq_in), hr = f32c(hr_in);
+        const auto f32 = r.options().dtype(at::kFloat);
+        Tensor out = at::empty({T, C}, f32);
+        Tensor saved = at::empty({(int64_t)(lib.mhc_layer_static_saved_size((int32_t)n, (int32_t)C) / 4)}, f32);
+        check(lib.mhc_wrapper_static_fwd(r.data_ptr(), b.data_ptr(), dtype_code(r.scalar_type()), (int32_t)mode,
+                                         w.data_ptr(), dtype_code(w.scalar_type()), fp(hp), fp(hq), fp(hr), fp(out),
+                                         fp(saved), T, (int32_t)n, (int32_t)C, (int32_t)iters, (float)sk_eps,
+                                         (float)rms_eps, stream()),
+              "mhc_wrapper_static_fwd");
+        ctx->save_for_backward({r, b, w, hp, hq, hr, saved});
+        ctx->saved_data["dtypes"] = std::vector<int64_t>{(int64_t)res_in.scalar_type(), (int64_t)br_in.scalar_type()};
+        ctx->saved_data["shapes"] = flat_shapes({&hp_in, &hq_in, &hr_in});
+        ctx->saved_data["cfg"] = std::vector<double>{(double)mode, (double)n, (double)iters, sk_eps, rms_eps};
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        const char* fn = "wrapper_static_bwd";
+        const auto sv = ctx->get_saved_variables();
+        const Tensor &r = sv[0], &b = sv[1], &w = sv[2], &saved = sv[6];
+        check_device(fn, {&grads[0], &r});
+        const at::DeviceGuard guard(r.device());
+        const auto cfg = ctx->saved_data["cfg"].toDoubleVector();
+        const int64_t T = r.size(0), C = r.size(1), n = (int64_t)cfg[1];
+        const int32_t mode = (int32_t)cfg[0];
+        TORCH_CHECK(grads[0].sizes() == r.sizes(), "wrapper_static_bwd: grad_out must be [tokens, hidden]");
+        const Tensor g = f32c(grads[0]);
+        const auto f32 = r.options().dtype(at::kFloat);
+        Tensor gr = at::empty_like(r), gb = at::empty_like(b);
+        Tensor gw = at::empty({C}, w.options());
+        Tensor ghp = at::empty({n}, f32), ghq = at::empty({n}, f32), ghr = at::empty({n, n}, f32);
+        const int dt = dtype_code(r.scalar_type());
+        const size_t wsb = lib.mhc_wrapper_static_bwd_workspace_size(T, (int32_t)n, (int32_t)C, dt, mode);
+        Tensor ws = workspace(wsb, r);
+        check(lib.mhc_wrapper_static_bwd(fp(g), r.data_ptr(), b.data_ptr(), dt, mode, dtype_code(w.scalar_type()),
+                                         fp(sv[3]), fp(sv[4]), fp(sv[5]), fp(saved), gr.data_ptr(), gb.data_ptr(),
+                                         gw.data_ptr(), fp(ghp), fp(ghq), fp(ghr), ws.data_ptr(), wsb, T, (int32_t)n,
+                                         (int32_t)C, (int32_t)cfg[2], (float)cfg[3], (float)cfg[4], stream()),
+              "mhc_wrapper_static_bwd");
+        const auto dts = ctx->saved_data["dtypes"].toIntVector();
+        const auto shp = unflat_shapes(ctx->saved_data["shapes"].toIntVector());
+        return {gr.to((at::ScalarType)dts[0]), gb.to((at::ScalarType)dts[1]), gw, ghp.view(shp[0]), ghq.view(shp[1]),
+                ghr.view(shp[2]), Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+struct DynamicWrapper : public torch::autograd::Function<DynamicWrapper> {
+    static Tensor forward(AutogradContext* ctx, const Tensor& res_in, const Tensor& br_in, const Tensor& w_in,
+                          const Tensor& pp_in, const Tensor& pq_in, const Tensor& pr_in, const Tensor& ap_in,
+                          const Tensor& aq_in, const Tensor& ar_in, const Tensor& bp_in, const Tensor& bq_in,
+                          const Tensor& bres_in, int64_t mode, int64_t n, int64_t iters, double sk_eps,
+                          double rms_eps) {
+        const char* fn = "wrapper_dynamic_fwd";
+        auto [r, b] = wrapper_inputs(fn, res_in, br_in);
+        check_device(fn, {&r, &w_in, &pp_in, &pq_in, &pr_in, &bp_in, &bq_in, &bres_in});
+        const at::DeviceGuard guard(r.device());
+        const int64_t T = r.size(0), C = r.size(1);
+        const Tensor w = weight(w_in);
+        TORCH_CHECK(w.numel() == C, "wrapper_dynamic_fwd: rmsnorm_weight must have C elements");
+        const auto ph = phi_parts(pp_in, pq_in, pr_in, n, n * C);
+        const Tensor ap = scalar_param(ap_in, r.device()), aq = scalar_param(aq_in, r.device()),
+                     ar = scalar_param(ar_in, r.device());
+        const Tensor bp = f32c(bp_in), bq = f32c(bq_in), bres = f32c(bres_in);
+        const auto f32 = r.options().dtype(at::kFloat);
+        Tensor out = at::empty({T, C}, f32);
+        Tensor saved =
+            at::empty({(int64_t)(lib.mhc_wrapper_dynamic_saved_size(T, (int32_t)n, (int32_t)C) / 4)}, f32);
+        const size_t wsb = lib.mhc_wrapper_dynamic_fwd_workspace_size(T, (int32_t)n, (int32_t)C);
+        Tensor ws = workspace(wsb, r);
+        check(lib.mhc_wrapper_dynamic_fwd(r.data_ptr(), b.data_ptr(), dtype_code(r.scalar_type()), (int32_t)mode,
+                                          w.data_ptr(), dtype_code(w.scalar_type()), fp(ph[0]), fp(ph[1]), fp(ph[2]),
+                                          fp(ap), fp(aq), fp(ar), fp(bp), fp(bq), fp(bres), fp(out), fp(saved),
+                                          ws.data_ptr(), wsb, T, (int32_t)n, (int32_t)C, (int32_t)iters,
+                                          (float)sk_eps, (float)rms_eps, stream()),
+              "mhc_wrapper_dynamic_fwd");
+        ctx->save_for_backward({r, b, w, saved, ph[0], ph[1], ph[2], ap, aq, ar, bres});
+        ctx->saved_data["dtypes"] = std::vector<int64_t>{(int64_t)res_in.scalar_type(), (int64_t)br_in.scalar_type()};
+        ctx->saved_data["shapes"] =
+            flat_shapes({&pp_in, &pq_in, &pr_in, &ap_in, &aq_in, &ar_in, &bp_in, &bq_in, &bres_in});
+        ctx->saved_data["cfg"] = std::vector<double>{(double)mode, (double)n, (double)iters, sk_eps, rms_eps};
+        return out;
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        const char* fn = "wrapper_dynamic_bwd";
+        const auto sv = ctx->get_saved_variables();
+        const Tensor &r = sv[0], &b = sv[1], &w = sv[2], &saved = sv[3];
+        check_device(fn, {&grads[0], &r});
+        const at::DeviceGuard guard(r.device());
+        const auto cfg = ctx->saved_data["cfg"].toDoubleVector();
+        const int64_t T = r.size(0), C = r.size(1), n = (int64_t)cfg[1], np = 2 * n + n * n;
+        const int32_t mode = (int32_t)cfg[0];
+        TORCH_CHECK(grads[0].sizes() == r.sizes(), "wrapper_dynamic_bwd: grad_out must be [tokens, hidden]");
+        const Tensor g = f32c(grads[0]);
+        const auto f32 = r.options().dtype(at::kFloat);
+        Tensor gr = at::empty_like(r), gb = at::empty_like(b);
+        Tensor gw = at::empty({C}, w.options());
+        Tensor gphi = at::empty({np, n * C}, f32);
+        Tensor galpha = at::empty({3}, f32);
+        Tensor gbias = at::empty({np}, f32);
+        const int dt = dtype_code(r.scalar_type());
+        const size_t wsb = lib.mhc_wrapper_dynamic_bwd_workspace_size(T, (int32_t)n, (int32_t)C, dt, mode);
+        Tensor ws = workspace(wsb, r);
+        check(lib.mhc_wrapper_dynamic_bwd(fp(g), r.data_ptr(), b.data_ptr(), dt, mode, dtype_code(w.scalar_type()),
+                                          fp(sv[4]), fp(sv[5]), fp(sv[6]), fp(sv[7]), fp(sv[8]), fp(sv[9]),
+                                          fp(sv[10]), fp(saved), gr.data_ptr(), gb.data_ptr(), gw.data_ptr(),
+                                          fp(gphi), fp(galpha), fp(gbias), ws.data_ptr(), wsb, T, (int32_t)n,
+                                          (int32_t)C, (int32_t)cfg[2], (float)cfg[3], (float)cfg[4], stream()),
+              "mhc_wrapper_dynamic_bwd");
+        const auto dts = ctx->saved_data["dtypes"].toIntVector();
+        const auto shp = unflat_shapes(ctx->saved_data["shapes"].toIntVector());
+        return {gr.to((at::ScalarType)dts[0]),
+                gb.to((at::ScalarType)dts[1]),
+                gw,
+                gphi.narrow(0, 0, n).view(shp[0]),
+                gphi.narrow(0, n, n).view(shp[1]),
+                gphi.narrow(0, 2 * n, n * n).view(shp[2]),
+                galpha.narrow(0, 0, 1).view(shp[3]),
+                galpha.narrow(0, 1, 1).view(shp[4]),
+                galpha.narrow(0, 2, 1).view(shp[5]),
+                gbias.narrow(0, 0, n).view(shp[6]),
+                gbias.narrow(0, n, n).view(shp[7]),
+                gbias.narrow(0, 2 * n, n * n).view(shp[8]),
+                Tensor(),
+                Tensor(),
+                Tensor(),
+                Tensor(),
+                Tensor()};
+    }
+};
+
 Tensor static_layer(const Tensor& x, const Tensor& w, const Tensor& hp, const Tensor& hq, const Tensor& hr,
                     int64_t iters, double sk_eps, double rms_eps) {
     require_bound();
@@ -298,6 +489,24 @@ Tensor dynamic_layer(const Tensor& x, const Tensor& w, const Tensor& pp, const T
                      const Tensor& br, int64_t iters, double sk_eps, double rms_eps) {
     require_bound();
     return DynamicLayer::apply(x, w, pp, pq, pr, ap, aq, ar, bp, bq, br, iters, sk_eps, rms_eps);
+}
+
+Tensor static_wrapper(const Tensor& residual, const Tensor& branch, const Tensor& w, const Tensor& hp,
+                      const Tensor& hq, const Tensor& hr, const std::string& mode, int64_t n, int64_t iters,
+                      double sk_eps, double rms_eps) {
+    require_bound();
+    const int32_t m = wrapper_mode(mode, n, "wrapper_static_fwd");
+    return StaticWrapper::apply(residual, branch, w, hp, hq, hr, (int64_t)m, n, iters, sk_eps, rms_eps);
+}
+
+Tensor dynamic_wrapper(const Tensor& residual, const Tensor& branch, const Tensor& w, const Tensor& pp,
+                       const Tensor& pq, const Tensor& pr, const Tensor& ap, const Tensor& aq, const Tensor& ar,
+                       const Tensor& bp, const Tensor& bq, const Tensor& bres, const std::string& mode, int64_t n,
+                       int64_t iters, double sk_eps, double rms_eps) {
+    require_bound();
+    const int32_t m = wrapper_mode(mode, n, "wrapper_dynamic_fwd");
+    return DynamicWrapper::apply(residual, branch, w, pp, pq, pr, ap, aq, ar, bp, bq, bres, (int64_t)m, n, iters,
+                                 sk_eps, rms_eps);
 }
 
 }  // namespace
@@ -312,4 +521,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("dynamic_layer", &dynamic_layer,
           "dynamic-H layer with autograd: (x, weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post, "
           "alpha_res, b_pre, b_post, b_res, num_iters, sinkhorn_eps, rmsnorm_eps) -> fp32 [B, n, C]");
+    m.def("static_wrapper", &static_wrapper,
+          "fused static-H MHCResidualWrapper with autograd: (residual, branch, weight, H_pre, H_post, H_res, "
+          "residual_mode, n, num_iters, sinkhorn_eps, rmsnorm_eps) -> fp32 [tokens, C]");
+    m.def("dynamic_wrapper", &dynamic_wrapper,
+          "fused dynamic-H MHCResidualWrapper with autograd: (residual, branch, weight, phi_pre, phi_post, phi_res, "
+          "alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res, residual_mode, n, num_iters, sinkhorn_eps, "
+          "rmsnorm_eps) -> fp32 [tokens, C]");
 }

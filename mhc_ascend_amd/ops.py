@@ -348,6 +348,15 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
                 X[:, i] = residual * (0.1 ** (i - 1))
         return layer(X).mean(dim=1)
     args = (layer.num_sinkhorn_iters, layer.sinkhorn_eps, layer.rmsnorm_eps)
+    ag = _lib.autograd()
+    if ag is not None:
+        if layer.use_dynamic_h:
+            return ag.dynamic_wrapper(residual, branch_output, layer.rmsnorm_weight, layer.phi_pre, layer.phi_post,
+                                      layer.phi_res, layer.alpha_pre, layer.alpha_post, layer.alpha_res, layer.b_pre,
+                                      layer.b_post, layer.b_res, residual_mode, n, int(args[0]), float(args[1]),
+                                      float(args[2]))
+        return ag.static_wrapper(residual, branch_output, layer.rmsnorm_weight, layer.H_pre, layer.H_post,
+                                 layer.H_res, residual_mode, n, int(args[0]), float(args[1]), float(args[2]))
     if layer.use_dynamic_h:
         return MHCWrapperDynamicFunction.apply(residual, branch_output, layer.rmsnorm_weight, layer.phi_pre,
                                                layer.phi_post, layer.phi_res, layer.alpha_pre, layer.alpha_post,

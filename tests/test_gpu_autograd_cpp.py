@@ -1,5 +1,6 @@
-"""GPU: the C++ autograd nodes of the fused layers (_mhc_autograd.so, the
-path mhc_layer_static / mhc_layer_fused_dynamic_training / MHCLayer take)
+"""GPU: the C++ autograd nodes of the fused layers and of the fused
+MHCResidualWrapper (_mhc_autograd.so, the path mhc_layer_static /
+mhc_layer_fused_dynamic_training / MHCLayer / mhc_residual_wrapper take)
 against the Python autograd functions over the same C-ABI entry points
 (the structure of the reference's ops.py:387-564 autograd function).
 
@@ -152,3 +153,52 @@ def test_cpp_nodes_raise_like_python(device):
                          torch.zeros(4, 256, device=device), torch.zeros(16, 256, device=device),
                          *[torch.tensor(1.0, device=device)] * 3, torch.zeros(4, device=device),
                          torch.zeros(4, device=device), torch.zeros(4, 4, device=device), 20, 1e-8, 1e-5)
+
+
+@pytest.mark.parametrize("dynamic", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["decay", "zero"])
+def test_wrapper_cpp_equals_python(device, dynamic, dtype, mode):
+    """The fused wrapper's C++ node against MHCWrapper*Function: output and
+    the gradients of residual, branch and every layer parameter equal."""
+    torch.manual_seed(5)
+    T, C = 77, 256
+    layer = mhc.MHCLayer(C, expansion_rate=4, use_dynamic_h=dynamic).to(device)
+    r0 = torch.randn(T, C, device=device).to(dtype)
+    b0 = torch.randn(T, C, device=device).to(dtype)
+    grad = torch.randn(T, C, device=device)
+    cfg = (layer.num_sinkhorn_iters, layer.sinkhorn_eps, layer.rmsnorm_eps)
+
+    def grads_of(fn):
+        layer.zero_grad()
+        r = r0.clone().requires_grad_(True)
+        b = b0.clone().requires_grad_(True)
+        out = fn(r, b)
+        out.backward(grad)
+        return out.detach(), r.grad, b.grad, {k: p.grad.clone() for k, p in layer.named_parameters()}
+
+    _ag()
+    got = grads_of(lambda r, b: ops.mhc_residual_wrapper(r, b, layer, mode))
+    if dynamic:
+        want = grads_of(lambda r, b: ops.MHCWrapperDynamicFunction.apply(
+            r, b, layer.rmsnorm_weight, layer.phi_pre, layer.phi_post, layer.phi_res, layer.alpha_pre,
+            layer.alpha_post, layer.alpha_res, layer.b_pre, layer.b_post, layer.b_res, mode, 4, *cfg))
+    else:
+        want = grads_of(lambda r, b: ops.MHCWrapperStaticFunction.apply(
+            r, b, layer.rmsnorm_weight, layer.H_pre, layer.H_post, layer.H_res, mode, 4, *cfg))
+    _same(got[0], want[0], "out")
+    _same(got[1], want[1], "grad residual")
+    _same(got[2], want[2], "grad branch")
+    for k in want[3]:
+        _same(got[3][k], want[3][k], f"grad {k}")
+
+
+def test_wrapper_cpp_raises_like_python(device):
+    ag = _ag()
+    layer = mhc.MHCLayer(64, expansion_rate=4, use_dynamic_h=False).to(device)
+    r = torch.randn(5, 64, device=device)
+    args = (layer.rmsnorm_weight, layer.H_pre, layer.H_post, layer.H_res)
+    with pytest.raises(ValueError, match="Unknown residual_mode"):
+        ag.static_wrapper(r, r, *args, "other", 4, 20, 1e-8, 1e-5)
+    with pytest.raises(RuntimeError, match="one shape"):
+        ag.static_wrapper(r, r[:4], *args, "decay", 4, 20, 1e-8, 1e-5)
