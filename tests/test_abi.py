@@ -114,3 +114,21 @@ def test_autograd_extension_binds_every_entry():
     names = ag.entry_names()
     assert names and all(n in _lib.SIGNATURES for n in names)
     assert callable(ag.static_layer) and callable(ag.dynamic_layer)
+
+
+def test_autograd_extension_switch(monkeypatch):
+    """MHC_CPP_AUTOGRAD=0 selects the Python autograd functions (the layers
+    then call the same entry points from Python); the default binds the
+    C++ nodes."""
+    from mhc_ascend_amd import _lib
+
+    saved = (_lib._autograd, _lib._autograd_done)
+    try:
+        monkeypatch.setenv("MHC_CPP_AUTOGRAD", "0")
+        _lib._autograd, _lib._autograd_done = None, False
+        assert _lib.autograd() is None
+        monkeypatch.delenv("MHC_CPP_AUTOGRAD")
+        _lib._autograd, _lib._autograd_done = None, False
+        assert _lib.autograd() is not None
+    finally:
+        _lib._autograd, _lib._autograd_done = saved
