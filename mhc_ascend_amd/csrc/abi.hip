@@ -663,11 +663,12 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
         e = launch_dyn_coef_fwd(n, pp, ss, w.ks, batch, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
                                 saved + d.coef_off, saved + d.p_off, saved + d.rh_off, num_iters, sinkhorn_eps,
                                 rmsnorm_eps, s);
-    // the channel-loop forward keeps each token's r in the sum x^2 partials
-    // (free once the coefficients are formed) to split its output pass
+    // the channel-loop forward uses the sum x^2 partials (ks * batch floats,
+    // free once the coefficients are formed) as scratch for its row sums
     float* rs = layer_fwd_is_wide(n, hidden) ? ss : nullptr;
     if (e == hipSuccess)
-        e = launch_layer_fwd(x_dtype, n, x, w32, saved + d.coef_off, np, out, kF32, rs, batch, hidden, rmsnorm_eps, s);
+        e = launch_layer_fwd(x_dtype, n, x, w32, saved + d.coef_off, np, out, kF32, rs, batch, hidden, rmsnorm_eps, s,
+                             rs ? (int64_t)w.ks * batch : 0);
     return hip_status(e);
 }
 
@@ -744,7 +745,8 @@ int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, 
                                 coef, nullptr, nullptr, num_iters, sinkhorn_eps, rmsnorm_eps, s);
     float* rs = layer_fwd_is_wide(n, hidden) ? ss : nullptr;  // as in mhc_layer_dynamic_fwd
     if (e == hipSuccess)
-        e = launch_layer_fwd(x_dtype, n, x, w32, coef, np, out, out_dtype, rs, batch, hidden, rmsnorm_eps, s);
+        e = launch_layer_fwd(x_dtype, n, x, w32, coef, np, out, out_dtype, rs, batch, hidden, rmsnorm_eps, s,
+                             rs ? (int64_t)w.ks * batch : 0);
     return hip_status(e);
 }
 

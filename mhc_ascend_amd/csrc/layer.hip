@@ -718,11 +718,11 @@ bool layer_fwd_is_wide(int n, int64_t C) { return fwd_tiling(C, n).vpt <= 0; }
 
 hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
                             int64_t coef_stride, void* out, int out_dtype, float* rms_out, int64_t B, int64_t C,
-                            float eps, hipStream_t s) {
+                            float eps, hipStream_t s, int64_t rms_scratch) {
     if (B == 0) return hipSuccess;
     const RowTiling t = fwd_tiling(C, n);
     if (t.vpt <= 0)
-        return launch_wide_fwd(x_dtype, out_dtype, n, x, w, coef, coef_stride, out, rms_out, B, C, eps, s);
+        return launch_wide_fwd(x_dtype, out_dtype, n, x, w, coef, coef_stride, out, rms_out, B, C, eps, s, rms_scratch);
     const void* fn = pick_fwd(x_dtype, out_dtype, n, t.vpt);
     if (!fn) return hipErrorInvalidValue;
     if (B > 0x7fffffff) return hipErrorInvalidValue;  // grid x limit

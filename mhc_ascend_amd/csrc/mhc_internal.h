@@ -43,9 +43,11 @@ hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, co
                               const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
                               hipStream_t s);
 // out is [B, n, C] in out_dtype (fp32, or bf16 for the inference entry).
+// rms_scratch > 0: rms_out is scratch of that many floats (>= B) whose
+// contents the caller does not need; 0: rms_out (when not null) receives r.
 hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, const float* coef,
                             int64_t coef_stride, void* out, int out_dtype, float* rms_out, int64_t B, int64_t C,
-                            float eps, hipStream_t s);
+                            float eps, hipStream_t s, int64_t rms_scratch = 0);
 // mode 0: static (writes dx, per-workgroup sums of [dM, dh_post_act,
 //         dh_pre_act] into scal_out[grid][n*n+2n]);
 // mode 1: dx = stream terms only, and per token scal_out[B][n*n+2n+2] =
@@ -91,7 +93,7 @@ constexpr int kWideMaxC = 12288;
 bool wide_supported(int n, int64_t C);
 hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
                            int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
-                           hipStream_t s);
+                           hipStream_t s, int64_t rms_scratch = 0);
 // Partial rows of the backward (mode 0 scalar rows and dw rows): the
 // persistent grid, or one per token when a token's channels are split over
 // several workgroups (few tokens); then the launch needs scratch of

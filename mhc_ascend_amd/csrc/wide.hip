@@ -179,12 +179,39 @@ __global__ __launch_bounds__(kWideFwdThreads) void wide_fwd_rms_kernel(const TX*
 
 constexpr int kWideFwdChunk = 256;
 
+// Row-sum partials of one 256-channel chunk (for callers whose r is only an
+// intermediate): part[b * gridDim.x + chunk] = the chunk's sum of xa^2, in
+// fixed-order wave and block sums.
+template <typename TX, int N>
+__global__ __launch_bounds__(kWideFwdChunk) void wide_fwd_part_kernel(const TX* __restrict__ x,
+                                                                      const float* __restrict__ coef,
+                                                                      int64_t coef_stride, float* __restrict__ part,
+                                                                      int64_t B, int C) {
+    __shared__ float red[kWideFwdChunk / kWave];
+    __shared__ float tot[1];
+    const int64_t b = blockIdx.y;
+    if (b >= B) return;
+    const float* cf = coef + b * coef_stride;
+    const TX* xb = x + b * (int64_t)N * C;
+    const int c = (int)blockIdx.x * kWideFwdChunk + (int)threadIdx.x;
+    float ss[1] = {0.f};
+    if (c < C) {
+        float xa = 0.f;
+#pragma unroll
+        for (int j = 0; j < N; ++j) xa += cf[j] * VecIO<TX>::scalar(xb + (int64_t)j * C + c);
+        ss[0] = xa * xa;
+    }
+    wide_block_total<1>(ss, red, tot);
+    if (threadIdx.x == 0) part[b * (int64_t)gridDim.x + blockIdx.x] = tot[0];
+}
+
 template <typename TX, typename TO, int N>
 __global__ __launch_bounds__(kWideFwdChunk) void wide_fwd_out_kernel(const TX* __restrict__ x,
                                                                      const float* __restrict__ w,
                                                                      const float* __restrict__ coef,
                                                                      int64_t coef_stride, TO* __restrict__ out,
-                                                                     const float* __restrict__ rms, int64_t B, int C) {
+                                                                     const float* __restrict__ rms, int S, int64_t B,
+                                                                     int C, float eps) {
     constexpr int NC = 2 * N + N * N;
     __shared__ float cfs[NC];
     const int64_t b = blockIdx.y;
@@ -192,7 +219,16 @@ __global__ __launch_bounds__(kWideFwdChunk) void wide_fwd_out_kernel(const TX* _
     const float* cf = coef + b * coef_stride;
     for (int k = threadIdx.x; k < NC; k += blockDim.x) cfs[k] = cf[k];
     __syncthreads();
-    const float inv = 1.f / rms[b];
+    // r of the token: rms[b], or (S > 0) from its S chunk partials rms[b S ..]
+    float r;
+    if (S > 0) {
+        float t = 0.f;
+        for (int q = 0; q < S; ++q) t += rms[b * S + q];
+        r = sqrtf(t / (float)C + eps);
+    } else {
+        r = rms[b];
+    }
+    const float inv = 1.f / r;
     const int c = (int)blockIdx.x * kWideFwdChunk + (int)threadIdx.x;
     if (c < C) wide_fwd_channel<TX, TO, N>(x + b * (int64_t)N * C, cfs, inv, w, out + b * (int64_t)N * C, c, C);
 }
@@ -908,7 +944,7 @@ bool wide_supported(int n, int64_t C) {
 
 hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
                            int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
-                           hipStream_t s) {
+                           hipStream_t s, int64_t rms_scratch) {
     if (B == 0) return hipSuccess;
     if (!wide_supported(n, C) || B > 0x7fffffff) return hipErrorInvalidValue;
     const int Ci = (int)C;
@@ -917,14 +953,23 @@ hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, con
     // (rms_out) and the tokens alone would leave CUs idle
     const int64_t chunks = (C + kWideFwdChunk - 1) / kWideFwdChunk;
     const bool split = rms_out != nullptr && chunks >= 2 && B < 2 * (int64_t)device_cu_count();
+    // rms_out as scratch of rms_scratch floats (r not needed by the caller):
+    // the row sums too run over token x chunk workgroups, into B * chunks partials
+    const bool parts = split && rms_scratch >= B * chunks;
+    const int S = parts ? (int)chunks : 0;
     const dim3 ogrid((unsigned)chunks, (unsigned)B), oblock(kWideFwdChunk);
     const int tok = timing_begin("layer_fwd", s);
 #define MHC_WIDE_FWD(TX_, TO_)                                                                                      \
     MHC_WIDE_N(n, if (split) {                                                                                      \
-        hipLaunchKernelGGL((wide_fwd_rms_kernel<TX_, N_>), grid, block, 0, s, (const TX_*)x, coef, coef_stride,    \
-                           rms_out, B, Ci, eps);                                                                    \
+        if (parts) {                                                                                                \
+            hipLaunchKernelGGL((wide_fwd_part_kernel<TX_, N_>), ogrid, oblock, 0, s, (const TX_*)x, coef,          \
+                               coef_stride, rms_out, B, Ci);                                                        \
+        } else {                                                                                                    \
+            hipLaunchKernelGGL((wide_fwd_rms_kernel<TX_, N_>), grid, block, 0, s, (const TX_*)x, coef, coef_stride,\
+                               rms_out, B, Ci, eps);                                                                \
+        }                                                                                                           \
         hipLaunchKernelGGL((wide_fwd_out_kernel<TX_, TO_, N_>), ogrid, oblock, 0, s, (const TX_*)x, w, coef,       \
-                           coef_stride, (TO_*)out, (const float*)rms_out, B, Ci);                                  \
+                           coef_stride, (TO_*)out, (const float*)rms_out, S, B, Ci, eps);                          \
     } else {                                                                                                        \
         hipLaunchKernelGGL((wide_fwd_kernel<TX_, TO_, N_>), grid, block, 0, s, (const TX_*)x, w, coef, coef_stride, \
                            (TO_*)out, rms_out, B, Ci, eps);                                                         \
