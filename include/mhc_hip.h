@@ -244,6 +244,51 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
                           int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
                           void* stream);
 
+/* ---- reference-shaped dynamic-H pair ---------------------------------------------
+ * The reference's native pair with its own call shape, for a caller that
+ * keeps the reference's ops.py (ops.py:425-448, 518-542): the forward
+ * returns nine tensors and the backward takes them back with 23 arguments.
+ * Both run the fused entries above; the extra tensors cost one more pass
+ * over x in the forward and a recomputed projection P in the backward (as
+ * the reference's backward recomputes it, bindings.cpp:764-766).
+ *
+ * mhc_layer_fwd_dynamic - replaces mhc_layer_fwd_dynamic (bindings.cpp:
+ * 880-952).  phi_concat [2n+n^2, n*hidden] fp32 = [phi_pre; phi_post;
+ * phi_res] (ops.py:416-418); the alphas are host floats.  Outputs (in the
+ * reference's order): output [batch, n, hidden] fp32, rms [batch] fp32 (RMS
+ * of x_agg), x_agg [batch, hidden] bf16, h_pre_act / h_post_act [batch, n]
+ * fp32, M [batch, n, n] fp32, y_norm [batch, hidden] bf16, x_flat
+ * [batch, n*hidden] bf16, rms_h [batch] fp32.  All arithmetic is fp32; only
+ * the three tensors the reference stores in bf16 are rounded on output. */
+size_t mhc_layer_fwd_dynamic_workspace_size(int64_t batch, int32_t n, int32_t hidden);
+int mhc_layer_fwd_dynamic(const void* x, int32_t x_dtype, const void* weight, int32_t weight_dtype,
+                          const float* phi_concat, float alpha_pre, float alpha_post, float alpha_res,
+                          const float* b_pre, const float* b_post, const float* b_res, float* output, float* rms,
+                          void* x_agg_bf16, float* h_pre_act, float* h_post_act, float* M, void* y_norm_bf16,
+                          void* x_flat_bf16, float* rms_h, void* workspace, size_t workspace_bytes, int64_t batch,
+                          int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
+                          void* stream);
+
+/* mhc_layer_bwd_dynamic - replaces mhc_layer_bwd_dynamic (bindings.cpp:
+ * 600-874), arguments in its order.  h_pre_act, h_post_act, M and rms_h are
+ * used as given; P is recomputed from x; rms, x_agg_bf16, y_norm_bf16 and
+ * x_flat_bf16 are not read (the row pass recomputes them in fp32 from x;
+ * they may be NULL).  Gradients: grad_x (x_dtype), grad_weight [hidden]
+ * fp32 (as the reference's), grad_phi_pre [n, n*hidden], grad_phi_post
+ * [n, n*hidden], grad_phi_res [n*n, n*hidden], one fp32 value each for the
+ * alphas, grad_b_pre / grad_b_post [n], grad_b_res [n, n]; deterministic. */
+size_t mhc_layer_bwd_dynamic_workspace_size(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype);
+int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dtype, const void* weight,
+                          int32_t weight_dtype, const float* rms, const void* x_agg_bf16, const float* h_pre_act,
+                          const float* h_post_act, const float* M, const void* y_norm_bf16, const void* x_flat_bf16,
+                          const float* rms_h, const float* phi_pre, const float* phi_post, const float* phi_res,
+                          float alpha_pre, float alpha_post, float alpha_res, const float* b_pre, const float* b_post,
+                          const float* b_res, void* grad_x, float* grad_weight, float* grad_phi_pre,
+                          float* grad_phi_post, float* grad_phi_res, float* grad_alpha_pre, float* grad_alpha_post,
+                          float* grad_alpha_res, float* grad_b_pre, float* grad_b_post, float* grad_b_res,
+                          void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
+                          int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
+
 /* ---- fused MHCResidualWrapper ---------------------------------------------------
  * The wrapper of layer.py:225-329 on residual / branch [tokens, hidden]
  * (dtype): streams X_0 = residual, X_1 = branch and, for i >= 2,

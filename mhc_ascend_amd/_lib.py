@@ -72,6 +72,15 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "mhc_layer_dynamic_bwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32,
                                              _f32, _vp]),
+    "mhc_layer_fwd_dynamic_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "mhc_layer_fwd_dynamic": (ctypes.c_int, [_vp, _i32, _vp, _i32, _vp, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp,
+                                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32,
+                                             _f32, _f32, _vp]),
+    "mhc_layer_bwd_dynamic_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
+    "mhc_layer_bwd_dynamic": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             _vp, _vp, _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32,
+                                             _f32, _vp]),
     "mhc_wrapper_dynamic_saved_size": (_sz, [_i64, _i32, _i32]),
     "mhc_wrapper_dynamic_fwd_workspace_size": (_sz, [_i64, _i32, _i32]),
     "mhc_wrapper_dynamic_fwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -543,7 +543,8 @@ static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
 static hipError_t proj_bwd_all(int x_dtype, const void* x, const float* dp, int dp_stride_, const float* s_tok,
                                const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                                void* dx, bool accumulate, float* part, int tiles, float* stage, float* grad_phi,
-                               int64_t batch, int64_t K, hipStream_t s) {
+                               int64_t batch, int64_t K, hipStream_t s, const float* dx_step = nullptr,
+                               int groups = 0) {
     if (batch > 0 && proj_bwd_wide_path(x_dtype, np, batch))
         return launch_proj_bwd_wide((const float*)x, dp, dp_stride_, s_tok, phi_pre, phi_post, phi_res, n_pre, np,
                                     (float*)dx, accumulate, grad_phi, part, batch, K, s);
@@ -556,7 +557,8 @@ static hipError_t proj_bwd_all(int x_dtype, const void* x, const float* dp, int 
             e = launch_fill_zero(part, (int64_t)rows_t * K, s);
         } else {
             e = launch_proj_bwd(x_dtype, x, dp + o0, dp_stride_, o0 == 0 ? s_tok : nullptr, phi_pre, phi_post,
-                                phi_res, n_pre, o0, rows_t, dx, accumulate || o0 > 0, part, tiles, batch, K, s);
+                                phi_res, n_pre, o0, rows_t, dx, accumulate || o0 > 0, part, tiles, batch, K, s,
+                                dx_step, groups);
         }
         if (e == hipSuccess)
             e = launch_column_finalize(0, kF32, part, rows, (int64_t)rows_t * K, stage, grad_phi + (int64_t)o0 * K,
@@ -750,24 +752,31 @@ int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, 
     return hip_status(e);
 }
 
-// With bf16 x and more than one 32-row projection tile (n >= 8), dx is
-// accumulated in fp32 (x upcast once, exactly) and rounded to bf16 once at
-// the end, as the reference's fp32 autograd does; one tile adds its terms
-// to the bf16 stream part directly.
-static bool dyn_bwd_f32_acc(int32_t n, int32_t x_dtype) { return x_dtype == kBF16 && 2 * n + n * n > kProjTile; }
+// dx of bf16 x is rounded to bf16 once, from the fp32 sum of the row pass's
+// stream part and the projection's terms, as the reference's fp32 autograd
+// does.  With one 32-row projection tile (n <= 4) on the register-row
+// kernels and hidden % 128 == 0 the stream part travels as int16 fixed point
+// (one scale per half wave of the row kernel and token, in the workspace)
+// and the projection kernel rounds the sum.  Otherwise (n >= 8, rows the channel-loop kernels take,
+// other hidden sizes) x is upcast once (exactly) and dx accumulates in fp32
+// across the kernels.
+static bool dyn_bwd_f32_acc(int32_t n, int32_t hidden, int32_t x_dtype) {
+    return x_dtype == kBF16 && (2 * n + n * n > kProjTile || layer_bwd_is_wide(n, hidden) || hidden % 128 != 0);
+}
 
 struct DynBwdWs {
     int grid, cblocks, tiles;
-    int wdt;  // element type the row and projection kernels run on
-    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, hist_off, rows_off,
-        total;
+    int wdt;     // element type the row and projection kernels run on
+    int groups;  // fixed-point groups per token of the bf16 stream part
+    size_t dw_off, scal_off, dp_off, s_off, step_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, hist_off,
+        rows_off, total;
 };
 
 static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
     DynBwdWs w{};
     const int64_t np = 2 * n + n * n;
     const int64_t K = (int64_t)n * hidden;
-    w.wdt = dyn_bwd_f32_acc(n, x_dtype) ? kF32 : x_dtype;
+    w.wdt = dyn_bwd_f32_acc(n, hidden, x_dtype) ? kF32 : x_dtype;
     w.grid = batch > 0 ? layer_bwd_grid(w.wdt, n, batch, hidden) : 1;
     w.cblocks = batch > 0 ? dyn_coef_bwd_blocks(n, batch) : 1;
     w.tiles = batch > 0 ? proj_bwd_tiles(w.wdt, batch, (int64_t)n * hidden) : 1;
@@ -776,6 +785,9 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     w.scal_off = o; o += align256((size_t)batch * (n * n + 2 * n + 2) * 4);
     w.dp_off = o; o += align256((size_t)batch * dp_stride((int)np) * 4);
     w.s_off = o; o += align256((size_t)batch * 4);
+    // fixed-point steps of the bf16 stream part
+    w.groups = w.wdt == kBF16 ? layer_bwd_fixed_groups(w.wdt, n, hidden) : 0;
+    w.step_off = o; o += align256((size_t)batch * w.groups * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     // projection partials (per-tile path) or dP planes (all-tiles path)
     size_t phip = (size_t)w.tiles * tile_rows((int)np) * K * 4;
@@ -832,6 +844,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     float* stp = (float*)(ws + w.stp_off);
     float* xw = (float*)(ws + w.xw_off);
     float* dxw = (float*)(ws + w.dxw_off);
+    float* step = w.wdt == kBF16 ? (float*)(ws + w.step_off) : nullptr;
     // the tensors the row and projection kernels work on
     const void* xk = w.wdt != x_dtype ? (const void*)xw : x;
     void* dxk = w.wdt != x_dtype ? (void*)dxw : grad_x;
@@ -849,7 +862,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         if (w.wdt != x_dtype) e = launch_weight_f32(x, x_dtype, batch * K, xw, s);
         if (e == hipSuccess)
             e = launch_layer_bwd(w.wdt, n, 1, grad_out, xk, w32, saved + d.coef_off, np, dxk, dw_part, scal, w.grid,
-                                 batch, hidden, rmsnorm_eps, (float*)(ws + w.rows_off), s);
+                                 batch, hidden, rmsnorm_eps, (float*)(ws + w.rows_off), s, step);
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
@@ -857,12 +870,182 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     }
     if (e == hipSuccess)
         e = proj_bwd_all(w.wdt, xk, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, np, dxk, true, phip,
-                         rows_p, stp, grad_phi, batch, K, s);
+                         rows_p, stp, grad_phi, batch, K, s, step, w.groups);
     if (e == hipSuccess && w.wdt != x_dtype) e = launch_cast_bf16(dxw, batch * K, grad_x, s);
     if (e == hipSuccess)
         e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
     if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
+    return hip_status(e);
+}
+
+// ---- reference-shaped dynamic-H entries ----------------------------------------
+// The calls of the reference's native module as its ops.py makes them (the
+// nine-tensor forward, the 23-argument backward), over the fused entries.
+//
+// forward workspace: [alphas (3 floats) | fused saved state | fused forward workspace]
+struct RefFwdWs {
+    size_t alpha_off, saved_off, fwd_off, total;
+};
+
+static RefFwdWs ref_fwd_ws(int64_t batch, int32_t n, int32_t hidden) {
+    RefFwdWs w{};
+    w.alpha_off = 0;
+    w.saved_off = 256;
+    w.fwd_off = w.saved_off + align256(dyn_saved(batch, n, hidden).total * sizeof(float));
+    w.total = w.fwd_off + align256(mhc_layer_dynamic_fwd_workspace_size(batch, n, hidden));
+    return w;
+}
+
+size_t mhc_layer_fwd_dynamic_workspace_size(int64_t batch, int32_t n, int32_t hidden) {
+    if (batch < 0 || n < 1 || hidden < 1) return 0;
+    return ref_fwd_ws(batch, n, hidden).total;
+}
+
+int mhc_layer_fwd_dynamic(const void* x, int32_t x_dtype, const void* weight, int32_t weight_dtype,
+                          const float* phi_concat, float alpha_pre, float alpha_post, float alpha_res,
+                          const float* b_pre, const float* b_post, const float* b_res, float* output, float* rms,
+                          void* x_agg_bf16, float* h_pre_act, float* h_post_act, float* M, void* y_norm_bf16,
+                          void* x_flat_bf16, float* rms_h, void* workspace, size_t workspace_bytes, int64_t batch,
+                          int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps,
+                          void* stream) {
+    int st = check_dyn("layer_fwd_dynamic", batch, n, hidden, x_dtype, weight_dtype, num_iters);
+    if (st) return st;
+    MHC_REQUIRE(weight && phi_concat && b_pre && b_post && b_res, "layer_fwd_dynamic: null parameter pointer");
+    MHC_REQUIRE(batch == 0 || (x && output && rms && x_agg_bf16 && h_pre_act && h_post_act && M && y_norm_bf16 &&
+                               x_flat_bf16 && rms_h),
+                "layer_fwd_dynamic: null x or output pointer");
+    const RefFwdWs w = ref_fwd_ws(batch, n, hidden);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "layer_fwd_dynamic: workspace smaller than mhc_layer_fwd_dynamic_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    float* alphas = (float*)(ws + w.alpha_off);
+    float* saved = (float*)(ws + w.saved_off);
+    const int64_t K = (int64_t)n * hidden;
+    hipError_t e = launch_set_scalars(alphas, alpha_pre, alpha_post, alpha_res, s);
+    if (e != hipSuccess) return hip_status(e);
+    st = mhc_layer_dynamic_fwd(x, x_dtype, weight, weight_dtype, phi_concat, phi_concat + n * K,
+                               phi_concat + 2 * n * K, alphas, alphas + 1, alphas + 2, b_pre, b_post, b_res, output,
+                               saved, ws + w.fwd_off, w.total - w.fwd_off, batch, n, hidden, num_iters, sinkhorn_eps,
+                               rmsnorm_eps, stream);
+    if (st) return st;
+    const DynSaved d = dyn_saved(batch, n, hidden);
+    return hip_status(launch_dyn_intermediates(x_dtype, x, saved + d.w_off, saved + d.coef_off, saved + d.rh_off, n,
+                                               batch, hidden, rmsnorm_eps, rms, x_agg_bf16, y_norm_bf16, x_flat_bf16,
+                                               h_pre_act, h_post_act, M, rms_h, s));
+}
+
+// backward workspace: [alphas | grad_alpha (3) + grad_b (np) | fused saved
+// state | projection (P recompute), then the fused backward's workspace |
+// grad_phi rows when the caller's three blocks are not consecutive]
+struct RefBwdWs {
+    size_t alpha_off, small_off, saved_off, work_off, gphi_off, total;
+};
+
+static RefBwdWs ref_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
+    const int np = 2 * n + n * n;
+    const int64_t K = (int64_t)n * hidden;
+    RefBwdWs w{};
+    w.alpha_off = 0;
+    w.small_off = 256;
+    w.saved_off = w.small_off + align256((size_t)(3 + np) * sizeof(float));
+    w.work_off = w.saved_off + align256(dyn_saved(batch, n, hidden).total * sizeof(float));
+    size_t work = dyn_bwd_ws(batch, n, hidden, x_dtype).total;
+    const size_t proj = proj_fwd_ws(batch, K, np).total;
+    if (proj > work) work = proj;
+    w.gphi_off = w.work_off + align256(work);
+    w.total = w.gphi_off + align256((size_t)np * K * sizeof(float));
+    return w;
+}
+
+size_t mhc_layer_bwd_dynamic_workspace_size(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
+    if (batch < 0 || n < 1 || hidden < 1) return 0;
+    return ref_bwd_ws(batch, n, hidden, x_dtype).total;
+}
+
+int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dtype, const void* weight,
+                          int32_t weight_dtype, const float* rms, const void* x_agg_bf16, const float* h_pre_act,
+                          const float* h_post_act, const float* M, const void* y_norm_bf16, const void* x_flat_bf16,
+                          const float* rms_h, const float* phi_pre, const float* phi_post, const float* phi_res,
+                          float alpha_pre, float alpha_post, float alpha_res, const float* b_pre, const float* b_post,
+                          const float* b_res, void* grad_x, float* grad_weight, float* grad_phi_pre,
+                          float* grad_phi_post, float* grad_phi_res, float* grad_alpha_pre, float* grad_alpha_post,
+                          float* grad_alpha_res, float* grad_b_pre, float* grad_b_post, float* grad_b_res,
+                          void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
+                          int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream) {
+    // rms, x_agg, y_norm and x_flat are recomputed in fp32 from x inside the
+    // fused row pass; they are accepted for the reference's call shape.
+    (void)rms;
+    (void)x_agg_bf16;
+    (void)y_norm_bf16;
+    (void)x_flat_bf16;
+    int st = check_dyn("layer_bwd_dynamic", batch, n, hidden, x_dtype, weight_dtype, num_iters);
+    if (st) return st;
+    MHC_REQUIRE(weight && phi_pre && phi_post && phi_res && b_res, "layer_bwd_dynamic: null parameter pointer");
+    MHC_REQUIRE(grad_weight && grad_phi_pre && grad_phi_post && grad_phi_res && grad_alpha_pre && grad_alpha_post &&
+                    grad_alpha_res && grad_b_pre && grad_b_post && grad_b_res,
+                "layer_bwd_dynamic: null gradient pointer");
+    MHC_REQUIRE(batch == 0 || (grad_output && x && grad_x && h_pre_act && h_post_act && M && rms_h),
+                "layer_bwd_dynamic: null grad_output / x / saved tensor / grad_x");
+    const RefBwdWs w = ref_bwd_ws(batch, n, hidden, x_dtype);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE,
+                    "layer_bwd_dynamic: workspace smaller than mhc_layer_bwd_dynamic_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    const int np = 2 * n + n * n;
+    const int64_t K = (int64_t)n * hidden;
+    float* alphas = (float*)(ws + w.alpha_off);
+    float* galpha = (float*)(ws + w.small_off);
+    float* gb = galpha + 3;
+    float* saved = (float*)(ws + w.saved_off);
+    char* work = ws + w.work_off;
+    const DynSaved d = dyn_saved(batch, n, hidden);
+    hipError_t e = launch_set_scalars(alphas, alpha_pre, alpha_post, alpha_res, s);
+    if (e == hipSuccess) e = launch_weight_f32(weight, weight_dtype, hidden, saved + d.w_off, s);
+    if (e == hipSuccess && batch > 0) {
+        // P = x_flat . Phi^T again (bindings.cpp:764-766), into the saved state
+        const ProjFwdWs p = proj_fwd_ws(batch, K, np);
+        float* pp = (float*)(work + p.p_off);
+        float* ss = (float*)(work + p.ss_off);
+        if (p.stream) {
+            e = launch_proj_stream(x_dtype, x, (bf16_raw_t*)(work + p.xpl_off), phi_pre, phi_post, phi_res, n,
+                                   nullptr, np, pp, ss, batch, K, p.ks, s);
+        } else {
+            e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, (bf16_raw_t*)(work + p.phib_off), s);
+            if (e == hipSuccess)
+                e = launch_proj_mfma(x_dtype, x, (const bf16_raw_t*)(work + p.phib_off), np, pp, ss, batch, K, p.ks,
+                                     s);
+        }
+        if (e == hipSuccess) e = launch_proj_reduce(pp, p.ks, batch, np, saved + d.p_off, s);
+        if (e == hipSuccess)
+            e = launch_dyn_saved_assemble(h_pre_act, h_post_act, M, rms_h, n, batch, saved + d.coef_off,
+                                          saved + d.rh_off, s);
+    }
+    if (e != hipSuccess) return hip_status(e);
+    const bool consecutive = grad_phi_post == grad_phi_pre + (int64_t)n * K &&
+                             grad_phi_res == grad_phi_post + (int64_t)n * K;
+    float* gphi = consecutive ? grad_phi_pre : (float*)(ws + w.gphi_off);
+    st = mhc_layer_dynamic_bwd(grad_output, x, x_dtype, kF32, phi_pre, phi_post, phi_res, alphas, alphas + 1,
+                               alphas + 2, b_pre, b_post, b_res, saved, grad_x, grad_weight, gphi, galpha, gb, work,
+                               w.gphi_off - w.work_off, batch, n, hidden, num_iters, sinkhorn_eps, rmsnorm_eps,
+                               stream);
+    if (st) return st;
+    auto d2d = [&](void* dst, const void* src, size_t bytes) {
+        if (e == hipSuccess) e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s);
+    };
+    if (!consecutive) {
+        d2d(grad_phi_pre, gphi, (size_t)n * K * sizeof(float));
+        d2d(grad_phi_post, gphi + (int64_t)n * K, (size_t)n * K * sizeof(float));
+        d2d(grad_phi_res, gphi + (int64_t)2 * n * K, (size_t)n * n * K * sizeof(float));
+    }
+    d2d(grad_alpha_pre, galpha, sizeof(float));
+    d2d(grad_alpha_post, galpha + 1, sizeof(float));
+    d2d(grad_alpha_res, galpha + 2, sizeof(float));
+    d2d(grad_b_pre, gb, (size_t)n * sizeof(float));
+    d2d(grad_b_post, gb + n, (size_t)n * sizeof(float));
+    d2d(grad_b_res, gb + 2 * n, (size_t)n * n * sizeof(float));
     return hip_status(e);
 }
 
@@ -879,6 +1062,9 @@ static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidd
         return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");
     if (dynamic && hidden % 32 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of 32");
+    // bf16 storage: the backward's stream parts travel in 128-channel groups
+    if (dynamic && dtype == kBF16 && hidden % 128 != 0)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": bf16 hidden must be a multiple of 128");
     if (choose_row_tiling(hidden, 4, 6).vpt <= 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
     return MHC_SUCCESS;
@@ -950,8 +1136,8 @@ int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dt
 }
 
 struct WrapBwdWs {
-    int grid, cblocks, tiles;
-    size_t dw_off, scal_off, dp_off, s_off, cpart_off, phip_off, stw_off, stp_off, total;
+    int grid, cblocks, tiles, groups;
+    size_t dw_off, scal_off, dp_off, s_off, step_off, cpart_off, phip_off, stw_off, stp_off, total;
 };
 
 static WrapBwdWs wrap_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype, bool dynamic, bool decay) {
@@ -972,6 +1158,9 @@ static WrapBwdWs wrap_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, int32_t 
     w.scal_off = o; o += align256((size_t)tokens * (n * n + 2 * n + 2) * 4);
     w.dp_off = o; o += align256((size_t)tokens * 32 * 4);
     w.s_off = o; o += align256((size_t)tokens * 4);
+    // fixed-point steps of d r, d b (bf16 storage)
+    w.groups = dtype == kBF16 ? wrap_bwd_fixed_groups(hidden) : 0;
+    w.step_off = o; o += align256((size_t)tokens * w.groups * 2 * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     w.phip_off = o; o += align256((size_t)w.tiles * np * K * 4);
     w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)np * K) * 4);
@@ -1014,6 +1203,7 @@ int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const v
     float* phip = (float*)(ws + w.phip_off);
     float* stw = (float*)(ws + w.stw_off);
     float* stp = (float*)(ws + w.stp_off);
+    float* step = dtype == kBF16 ? (float*)(ws + w.step_off) : nullptr;
     const DynSaved d = dyn_saved(tokens, n, hidden);
     const int np = 2 * n + n * n;
     const int64_t K = (int64_t)n * hidden;
@@ -1027,14 +1217,14 @@ int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const v
         if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
     } else {
         e = launch_wrap_bwd(dtype, n, 1, decay, grad_out, residual, branch, w32, saved + d.coef_off, np,
-                            grad_residual, grad_branch, dw_part, scal, w.grid, tokens, hidden, rmsnorm_eps, s);
+                            grad_residual, grad_branch, dw_part, scal, w.grid, tokens, hidden, rmsnorm_eps, s, step);
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
                                     nullptr, s);
         if (e == hipSuccess)
             e = launch_wrap_proj_bwd(dtype, n, decay, residual, branch, dp, stok, phi_pre, phi_post, phi_res,
-                                     grad_residual, grad_branch, phip, w.tiles, tokens, hidden, s);
+                                     grad_residual, grad_branch, phip, w.tiles, tokens, hidden, s, step, w.groups);
     }
     if (e == hipSuccess)
         e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,

@@ -29,7 +29,7 @@ LIB_PATH = os.path.join(PKG, LIB_NAME)
 AUTOGRAD_NAME = "_mhc_autograd"
 AUTOGRAD_PATH = os.path.join(PKG, AUTOGRAD_NAME + ".so")
 
-SOURCES = ["abi.hip", "dynamic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wide.hip", "wrapper.hip"]
+SOURCES = ["abi.hip", "compat.hip", "dynamic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wide.hip", "wrapper.hip"]
 
 ARCH = os.environ.get("MHC_OFFLOAD_ARCH", "gfx950")
 

@@ -1247,8 +1247,14 @@ template <typename TX, bool ACC, bool HAS_S>
 __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     const TX* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
     const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
-    int n_pre, int o0, int np, TX* __restrict__ dx, float* __restrict__ dphi_part, int64_t B, int64_t K,
-    int64_t tile) {
+    int n_pre, int o0, int np, TX* __restrict__ dx, const float* __restrict__ dx_step, int groups, int C,
+    float* __restrict__ dphi_part, int64_t B, int64_t K, int64_t tile) {
+    // With bf16 x the incoming dx (ACC) is the row pass's int16 fixed-point
+    // stream part (fixed_scale) with steps dx_step[b][groups]: this block's
+    // 128 columns (channels c .. c + 127 of one stream) are group
+    // (c / 128) % groups of every token.  The sum is rounded once to bf16 on
+    // the way out.
+    constexpr bool QIN = ACC && sizeof(TX) == 2;
     constexpr int TB = 32;                      // tokens per stage
     constexpr int CB = 128;                     // columns per workgroup
     constexpr int EPV = 16 / sizeof(TX);        // elements per 16-byte vector
@@ -1265,6 +1271,7 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     __shared__ __align__(16) char dx_lds[2][TB * PITCH];
     __shared__ __align__(16) bf16_t dps_lds[4][32 * kDpPitch];  // hi_row, lo_row, hi_col, lo_col
     __shared__ float s_lds[TB];
+    __shared__ float q_lds[QIN ? TB : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1309,7 +1316,7 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     // computes and stage i+1 (fetched one stage earlier) moves into LDS.
     struct Fetched {
         uint4 x[PASSES], d[PASSES];
-        float dp[4], s;
+        float dp[4], s, q;
     };
     Fetched f0, f1;
     auto fetch = [&](Fetched& f, int64_t t0) __attribute__((always_inline)) {
@@ -1327,6 +1334,11 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
         f.s = 0.f;
         if constexpr (HAS_S) {
             if (tid < TB) f.s = s_tok[(t0 + tid < t_end) ? t0 + tid : t0];
+        }
+        f.q = 0.f;
+        if constexpr (QIN) {
+            const int grp = (int)((kb0 % C) / kFixedGroup) % groups;
+            if (tid < TB) f.q = dx_step[((t0 + tid < t_end) ? t0 + tid : t0) * groups + grp];
         }
     };
     auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {
@@ -1366,6 +1378,9 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
         }
         if constexpr (HAS_S) {
             if (tid < TB) s_lds[tid] = (t0 + tid < t_end) ? f.s : 0.f;
+        }
+        if constexpr (QIN) {
+            if (tid < TB) q_lds[tid] = (t0 + tid < t_end) ? f.q : 0.f;
         }
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> u32x4_t {
@@ -1420,7 +1435,9 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
                 const int boff = t * PITCH + c0 * (int)sizeof(TX);  // 8-byte aligned
                 float xv[4], dv[4];
                 lds_get4<TX>(xt + boff, xv);
-                if constexpr (ACC) {
+                if constexpr (QIN) {
+                    fixed_unpack4(*reinterpret_cast<const uint2*>(dt + boff), q_lds[t], dv);
+                } else if constexpr (ACC) {
                     lds_get4<TX>(dt + boff, dv);
                 } else {
 #pragma unroll
@@ -2409,16 +2426,21 @@ int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
 hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
                            const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int o0,
                            int np, void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
-                           hipStream_t s) {
+                           hipStream_t s, const float* dx_step, int groups) {
     if (B == 0) return hipSuccess;
     if (np < 1 || np > kProjTile || o0 < 0 || K % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
+    // bf16 x: one output tile, on the fixed-point stream part of the row pass
+    const int C = np > 0 ? (int)(K / (n_pre > 0 ? n_pre : 1)) : 0;
+    if (x_dtype == kBF16 && (o0 != 0 || dx_step == nullptr || groups < 1 || C % kFixedGroup != 0))
+        return hipErrorInvalidValue;
     // token tile: a multiple of the 32-token block
     int64_t tile = (B + tiles - 1) / tiles;
     tile = ((tile + 31) / 32) * 32;
     const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
 #define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \
     hipLaunchKernelGGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP, dp_stride,  \
-                       s_tok, phi_pre, phi_post, phi_res, n_pre, o0, np, (TX_*)dx, dphi_part, B, K, tile)
+                       s_tok, phi_pre, phi_post, phi_res, n_pre, o0, np, (TX_*)dx, dx_step, groups, C, dphi_part, B, K, \
+                       tile)
     // The layer backward accumulates (with the r_h term on the first output
     // tile only); the standalone operator starts from zero on its first tile.
     // An s term without accumulation, or a bf16 dx from zero, is not built.

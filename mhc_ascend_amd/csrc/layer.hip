@@ -184,7 +184,8 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
                                           const float (&xv)[N][VPT][kLayerWC],
                                           const float (&gv)[N][VPT][kLayerWC],
                                           float (&dwacc)[VPT][kLayerWC], float& sacc, TX* __restrict__ dx,
-                                          float* __restrict__ scal_out, int C, float eps, float* red) {
+                                          float* __restrict__ scal_out, float* __restrict__ dx_step, int C,
+                                          float eps, float* red) {
     constexpr int WC = kLayerWC;
     constexpr int NC = coef_size<N>();
     constexpr int NS = N * N + 2 * N;
@@ -262,34 +263,76 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
         }
     }
 
+    if constexpr (MODE == 1 && sizeof(TX) == 2) {
+        // The dynamic backward's stream part with bf16 x: the projection
+        // kernel adds its terms and rounds once, so this part travels as int16
+        // fixed point (fixed_scale), one scale per half wave of this token:
+        // dx_step[b][threadIdx.x / 32].
+        float a[N][VPT][WC];
+        float m = 0.f;
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-        float gxa[WC];
+        for (int k = 0; k < VPT; ++k) {
 #pragma unroll
-        for (int e = 0; e < WC; ++e) {
-            float xa = 0.f, gy = 0.f;
+            for (int e = 0; e < WC; ++e) {
+                float xa = 0.f, gy = 0.f;
 #pragma unroll
-            for (int i = 0; i < N; ++i) {
-                xa += cfv[i] * xv[i][k][e];
-                gy += cfv[N + i] * gv[i][k][e];
-            }
-            gxa[e] = wv[k][e] * gy * inv - xa * k2;
-            dwacc[k][e] += gy * xa * inv;
-        }
-        if (c0 < C) {
-            TX* db = dx + b * (int64_t)N * C;
+                for (int i = 0; i < N; ++i) {
+                    xa += cfv[i] * xv[i][k][e];
+                    gy += cfv[N + i] * gv[i][k][e];
+                }
+                const float gxa = wv[k][e] * gy * inv - xa * k2;
+                dwacc[k][e] += gy * xa * inv;
 #pragma unroll
-            for (int j = 0; j < N; ++j) {
-                float d[WC];
-#pragma unroll
-                for (int e = 0; e < WC; ++e) {
-                    float s = cfv[j] * gxa[e];
+                for (int j = 0; j < N; ++j) {
+                    float s = cfv[j] * gxa;
 #pragma unroll
                     for (int i = 0; i < N; ++i) s += cfv[2 * N + i * N + j] * gv[i][k][e];
-                    d[e] = s;
+                    a[j][k][e] = s;
+                    m = fmaxf(m, fabsf(s));
                 }
-                store_run_nt<TX, WC>(db + (int64_t)j * C + c0, d);
+            }
+        }
+        const FixedScale fs = fixed_scale(half_wave_max_nonneg(m));
+        char* db = reinterpret_cast<char*>(dx + b * (int64_t)N * C);
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+            if (c0 < C) {
+#pragma unroll
+                for (int j = 0; j < N; ++j) st8_nt(db + ((int64_t)j * C + c0) * 2, fixed_pack4(a[j][k], fs.inv));
+            }
+        }
+        if ((threadIdx.x & 31) == 0) dx_step[b * (blockDim.x / 32) + threadIdx.x / 32] = fs.step;
+    } else {
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+            float gxa[WC];
+#pragma unroll
+            for (int e = 0; e < WC; ++e) {
+                float xa = 0.f, gy = 0.f;
+#pragma unroll
+                for (int i = 0; i < N; ++i) {
+                    xa += cfv[i] * xv[i][k][e];
+                    gy += cfv[N + i] * gv[i][k][e];
+                }
+                gxa[e] = wv[k][e] * gy * inv - xa * k2;
+                dwacc[k][e] += gy * xa * inv;
+            }
+            if (c0 < C) {
+                TX* db = dx + b * (int64_t)N * C;
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    float d[WC];
+#pragma unroll
+                    for (int e = 0; e < WC; ++e) {
+                        float s = cfv[j] * gxa[e];
+#pragma unroll
+                        for (int i = 0; i < N; ++i) s += cfv[2 * N + i * N + j] * gv[i][k][e];
+                        d[e] = s;
+                    }
+                    store_run_nt<TX, WC>(db + (int64_t)j * C + c0, d);
+                }
             }
         }
     }
@@ -300,7 +343,7 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
                                                     const float* __restrict__ w, const float* __restrict__ coef,
                                                     int64_t coef_stride, TX* __restrict__ dx,
                                                     float* __restrict__ dw_part, float* __restrict__ scal_out,
-                                                    int64_t B, int C, float eps) {
+                                                    float* __restrict__ dx_step, int64_t B, int C, float eps) {
     constexpr int WC = kLayerWC;
     constexpr int NS = N * N + 2 * N;
     constexpr int NR = 2 + N * N + 3 * N;
@@ -334,7 +377,8 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
             }
             unpack_rows<TX, N, VPT, WC>(xA, C, xv);
             unpack_rows<float, N, VPT, WC>(gA, C, gv);
-            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, C, eps, red);
+            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,
+                                       red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
             if (b2 < B) {
@@ -343,7 +387,8 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
             }
             unpack_rows<TX, N, VPT, WC>(xB, C, xv);
             unpack_rows<float, N, VPT, WC>(gB, C, gv);
-            bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, C, eps, red);
+            bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,
+                                       red);
             b = b2;
         }
     } else {
@@ -355,7 +400,8 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
             load_rows_raw<float, N, VPT, WC, true>(g + b * NCs, C, gr);
             unpack_rows<TX, N, VPT, WC>(xr, C, xv);
             unpack_rows<float, N, VPT, WC>(gr, C, gv);
-            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, C, eps, red);
+            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,
+                                       red);
         }
     }
 
@@ -747,6 +793,11 @@ static RowTiling bwd_tiling(int64_t C, int n, int x_dtype = kF32) {
 
 bool layer_bwd_is_wide(int n, int64_t C) { return bwd_tiling(C, n).vpt <= 0; }
 
+int layer_bwd_fixed_groups(int x_dtype, int n, int64_t C) {
+    const RowTiling t = bwd_tiling(C, n, x_dtype);
+    return t.vpt > 0 ? t.threads / 32 : 0;
+}
+
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
     const RowTiling t = bwd_tiling(C, n, x_dtype);
     if (t.vpt <= 0) return wide_bwd_grid(x_dtype, n, B, C);
@@ -759,16 +810,22 @@ size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C) {
 
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
-                            int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s) {
+                            int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s,
+                            float* dx_step) {
     const RowTiling t = bwd_tiling(C, n, x_dtype);
-    if (t.vpt <= 0)
+    if (t.vpt <= 0) {
+        // the channel-loop kernels write a bf16 stream part; the dynamic
+        // entries send bf16 x there through fp32 accumulation instead
+        if (mode == 1 && x_dtype == kBF16) return hipErrorInvalidValue;
         return launch_wide_bwd(x_dtype, n, mode, g, x, w, coef, coef_stride, dx, dw_part, scal_out, grid, B, C, eps,
                                scratch, s);
+    }
+    if (mode == 1 && x_dtype == kBF16 && (dx_step == nullptr || C % kFixedGroup != 0)) return hipErrorInvalidValue;
     const void* fn = pick_bwd(x_dtype, n, t.vpt, mode, use_prefetch(t));
     if (!fn) return hipErrorInvalidValue;
     int Ci = (int)C;
     void* args[] = {(void*)&g, (void*)&x, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&dx,
-                    (void*)&dw_part, (void*)&scal_out, (void*)&B, (void*)&Ci, (void*)&eps};
+                    (void*)&dw_part, (void*)&scal_out, (void*)&dx_step, (void*)&B, (void*)&Ci, (void*)&eps};
     const int tok = timing_begin(mode == 0 ? "layer_bwd" : "layer_bwd_reduce", s);
     hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);

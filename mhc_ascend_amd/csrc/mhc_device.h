@@ -317,6 +317,64 @@ __device__ __forceinline__ void block_sum(float (&v)[NV], float* lds) {
     __syncthreads();
 }
 
+// Maximum of a non-negative value over the aligned 32 lanes (half wave)
+// containing this lane; every lane of the half receives it.  Row maxima by
+// DPP, then rows (0, 1) and (2, 3) through v_permlane16_swap.  The whole
+// wave must be active.
+__device__ __forceinline__ float half_wave_max_nonneg(float x) {
+    x = fmaxf(x, dpp::mov<dpp::kQuadXor1>(x));
+    x = fmaxf(x, dpp::mov<dpp::kQuadXor2>(x));
+    x = fmaxf(x, dpp::mov<dpp::kRowHalfMirror>(x));
+    x = fmaxf(x, dpp::mov<dpp::kRowMirror>(x));
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// ---------------------------------------------------------------------------
+// Fixed-point transport of an fp32 row part between two kernels.
+//
+// Where a gradient is formed in two kernels (a row pass writes one part, a
+// later kernel adds the rest and rounds the sum once to bf16), the first part
+// travels through HBM in the 2 bytes per element the bf16 result occupies, as
+// int16 fractions of a per-group scale m (the group's largest |value|):
+// q = rne(32767 v / m) by v_cvt_pknorm_i16_f32 (clamped to [-1, 1], two
+// elements per instruction), v = q * (m / 32767) on the way back.  The error
+// is at most m / 65534 per element, far below the bf16 rounding of the final
+// sum (2^-8 relative), which stays the only rounding of the gradient.  A
+// group is one half wave's elements of a token row: every lane's 4-channel
+// chunks (all streams, all chunks k) of lanes 32h .. 32h + 31, whose
+// channels are the 128-channel ranges c / 128 = k * H + h (H = row-kernel
+// lanes / 32), so the row kernel finds m with one half-wave reduction and a
+// 128-column block of the row maps to one group.  A non-finite value makes
+// its group non-finite on the way back, as fp32 would.
+// ---------------------------------------------------------------------------
+constexpr int kFixedGroup = 128;  // channels of one half wave's 4-channel chunks
+
+typedef short fixed_s16x2_t __attribute__((ext_vector_type(2)));
+
+struct FixedScale {
+    float inv;   // 1 / m (0 for an all-zero group)
+    float step;  // m / 32767
+};
+
+__device__ __forceinline__ FixedScale fixed_scale(float m) {
+    return FixedScale{m > 0.f ? 1.f / m : 0.f, m * (1.f / 32767.f)};
+}
+
+// Four values -> four int16 in 8 bytes (element 0 in the low half of .x).
+__device__ __forceinline__ uint2 fixed_pack4(const float (&v)[4], float inv) {
+    const fixed_s16x2_t a = __builtin_amdgcn_cvt_pknorm_i16(v[0] * inv, v[1] * inv);
+    const fixed_s16x2_t b = __builtin_amdgcn_cvt_pknorm_i16(v[2] * inv, v[3] * inv);
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+
+__device__ __forceinline__ void fixed_unpack4(uint2 w, float step, float (&v)[4]) {
+    v[0] = (float)(int)(int16_t)(w.x & 0xffffu) * step;
+    v[1] = (float)((int)w.x >> 16) * step;
+    v[2] = (float)(int)(int16_t)(w.y & 0xffffu) * step;
+    v[3] = (float)((int)w.y >> 16) * step;
+}
+
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // Row o of the concatenated dynamic-H projection [pre; post; res] (ops.py:416-418):

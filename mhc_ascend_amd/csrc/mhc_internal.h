@@ -51,13 +51,20 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
 // mode 0: static (writes dx, per-workgroup sums of [dM, dh_post_act,
 //         dh_pre_act] into scal_out[grid][n*n+2n]);
 // mode 1: dx = stream terms only, and per token scal_out[B][n*n+2n+2] =
-//         dM, dh_post_act, dh_pre_act, inv_rms, k2.
+//         dM, dh_post_act, dh_pre_act, inv_rms, k2.  With bf16 x the stream
+//         terms are int16 fixed point (fixed_scale in mhc_device.h) with the
+//         steps dx_step[B][layer_bwd_fixed_groups] (register rows and
+//         C % 128 == 0 only: other bf16 x rows are an error here).
 // scratch: layer_bwd_scratch_bytes (the channel-chunked wide backward's
 // partial row sums; 0 bytes and unused otherwise).
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
-                            int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s);
+                            int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s,
+                            float* dx_step = nullptr);
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
+// Fixed-point groups per token row of the mode-1 stream part (one per half
+// wave of the register-row kernel; 0 when the channel-loop kernels run).
+int layer_bwd_fixed_groups(int x_dtype, int n, int64_t C);
 size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C);
 // Whether the layer forward / backward of (n, C) runs the channel-loop
 // kernels of wide.hip rather than the register rows.
@@ -214,10 +221,13 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
                                 const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                                 float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
                                 hipStream_t s);
+// With bf16 x (one output tile, accumulate) the incoming dx is the layer
+// backward's int16 fixed-point stream part with steps dx_step[B][groups]
+// (groups = layer_bwd_fixed_groups).
 hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
                            const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int o0,
                            int np, void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
-                           hipStream_t s);
+                           hipStream_t s, const float* dx_step = nullptr, int groups = 0);
 hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, hipStream_t s);
 
 // ---- wrapper.hip -----------------------------------------------------------
@@ -228,18 +238,40 @@ hipError_t launch_wrap_fwd(int dt, int n, bool decay, const void* res, const voi
                            hipStream_t s);
 int wrap_bwd_grid(int dt, int n, bool decay, int64_t B, int64_t C);
 // mode 0: static (per-workgroup sums of [dM, dh_post_act, dh_pre_act] in
-// scal_out[grid][n*n+2n]); mode 1: dynamic (per-token scal_out[B][n*n+2n+2]).
+// scal_out[grid][n*n+2n]); mode 1: dynamic (per-token scal_out[B][n*n+2n+2]);
+// its d r / d b stream parts with bf16 storage are int16 fixed point
+// (fixed_scale in mhc_device.h) with steps d_step[B][wrap_bwd_fixed_groups][2].
+int wrap_bwd_fixed_groups(int64_t C);
 hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, const void* res, const void* br,
                            const float* w, const float* coef, int64_t coef_stride, void* dres, void* dbr,
-                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s);
+                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s,
+                           float* d_step = nullptr);
 int wrap_proj_csplit(int64_t B, int64_t C);
 hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const void* br, const bf16_raw_t* phib,
                             float* p_part, float* ss_part, int64_t B, int64_t C, int ks, hipStream_t s);
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C);
+// bf16 storage: dres / dbr come in as the fixed-point stream parts of
+// launch_wrap_bwd (mode 1) with their steps d_step[B][groups][2].
 hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
                                 const float* s_tok, const float* phi_pre, const float* phi_post, const float* phi_res,
                                 void* dres, void* dbr, float* dphi_part, int tiles, int64_t B, int64_t C,
-                                hipStream_t s);
+                                hipStream_t s, const float* d_step = nullptr, int groups = 0);
+
+// ---- compat.hip ------------------------------------------------------------
+// The reference-shaped dynamic-H entries (mhc_layer_fwd_dynamic /
+// mhc_layer_bwd_dynamic).  dst[0..2] = (a, b, c).
+hipError_t launch_set_scalars(float* dst, float a, float b, float c, hipStream_t s);
+// From x, the fp32 weight and the fused forward's per-token coefficients and
+// r_h: rms [B], x_agg / y_norm [B, C] bf16, x_flat [B, n*C] bf16, h_pre /
+// h_post [B, n], M [B, n, n], rms_h [B].
+hipError_t launch_dyn_intermediates(int x_dtype, const void* x, const float* w32, const float* coef, const float* rh,
+                                    int n, int64_t B, int64_t C, float eps, float* rms, void* x_agg, void* y_norm,
+                                    void* x_flat, float* h_pre, float* h_post, float* M, float* rms_h,
+                                    hipStream_t s);
+// The inverse for the coefficients: coef [B, 2n+n^2] = (h_pre, h_post, M),
+// rh [B] = rms_h.
+hipError_t launch_dyn_saved_assemble(const float* h_pre, const float* h_post, const float* M, const float* rms_h,
+                                     int n, int64_t B, float* coef, float* rh, hipStream_t s);
 
 // ---- sinkhorn.hip ----------------------------------------------------------
 hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batch, int iters, float eps,

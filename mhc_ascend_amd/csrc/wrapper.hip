@@ -180,7 +180,8 @@ __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restric
                                                const float (&rv)[1][VPT][kLayerWC],
                                                const float (&bv)[1][VPT][kLayerWC], float (&dwacc)[VPT][kLayerWC],
                                                float& sacc, TX* __restrict__ dres, TX* __restrict__ dbr,
-                                               float* __restrict__ scal_out, int C, float eps, float* red) {
+                                               float* __restrict__ scal_out, float* __restrict__ d_step, int C,
+                                               float eps, float* red) {
     constexpr int WC = kLayerWC;
     constexpr int NS = N * N + 2 * N;
     constexpr int NR = 2 + 3 * N;  // ss, gwx, u_j, v_j, z_j
@@ -264,10 +265,16 @@ __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restric
 
     TX* drb = dres + b * (int64_t)C;
     TX* dbb = dbr + b * (int64_t)C;
+    // The dynamic backward's stream parts with bf16 storage travel as int16
+    // fixed point (fixed_scale), one scale per half wave and token for each:
+    // d_step[b][threadIdx.x / 32][d r, d b].  The projection kernel adds its
+    // terms and rounds once to bf16.
+    constexpr bool QOUT = MODE == 1 && sizeof(TX) == 2;
+    float dr[VPT][WC], db[VPT][WC];
+    float mr = 0.f, mb = 0.f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-        float dr[WC], db[WC];
 #pragma unroll
         for (int e = 0; e < WC; ++e) {
             float x[N];
@@ -283,23 +290,43 @@ __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restric
             if constexpr (N > 0) a += cm[0] * g + hp[0] * gxa;
             if constexpr (N > 2) a += res_weight<2, DECAY>() * (cm[2] * g + hp[2] * gxa);
             if constexpr (N > 3) a += res_weight<3, DECAY>() * (cm[3] * g + hp[3] * gxa);
-            dr[e] = a;
-            db[e] = (N > 1) ? cm[N > 1 ? 1 : 0] * g + hp[N > 1 ? 1 : 0] * gxa : 0.f;
+            dr[k][e] = a;
+            db[k][e] = (N > 1) ? cm[N > 1 ? 1 : 0] * g + hp[N > 1 ? 1 : 0] * gxa : 0.f;
+            if constexpr (QOUT) {
+                mr = fmaxf(mr, fabsf(dr[k][e]));
+                mb = fmaxf(mb, fabsf(db[k][e]));
+            }
         }
-        if (c0 < C) {
-            store_run_nt<TX, WC>(drb + c0, dr);
-            store_run_nt<TX, WC>(dbb + c0, db);
+        if constexpr (!QOUT) {
+            if (c0 < C) {
+                store_run_nt<TX, WC>(drb + c0, dr[k]);
+                store_run_nt<TX, WC>(dbb + c0, db[k]);
+            }
         }
+    }
+    if constexpr (QOUT) {
+        const FixedScale fr = fixed_scale(half_wave_max_nonneg(mr));
+        const FixedScale fb = fixed_scale(half_wave_max_nonneg(mb));
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+            const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+            if (c0 < C) {
+                st8_nt(drb + c0, fixed_pack4(dr[k], fr.inv));
+                st8_nt(dbb + c0, fixed_pack4(db[k], fb.inv));
+            }
+        }
+        const int lane32 = threadIdx.x & 31;
+        if (lane32 < 2) d_step[(b * (blockDim.x / 32) + threadIdx.x / 32) * 2 + lane32] = lane32 ? fb.step : fr.step;
     }
 }
 
 template <typename TX, int N, int VPT, int MODE, bool PF, bool DECAY>
-__global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, const TX* __restrict__ res,
-                                                   const TX* __restrict__ br, const float* __restrict__ w,
-                                                   const float* __restrict__ coef, int64_t coef_stride,
-                                                   TX* __restrict__ dres, TX* __restrict__ dbr,
-                                                   float* __restrict__ dw_part, float* __restrict__ scal_out,
-                                                   int64_t B, int C, float eps) {
+__device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const TX* __restrict__ res,
+                                              const TX* __restrict__ br, const float* __restrict__ w,
+                                              const float* __restrict__ coef, int64_t coef_stride,
+                                              TX* __restrict__ dres, TX* __restrict__ dbr,
+                                              float* __restrict__ dw_part, float* __restrict__ scal_out,
+                                              float* __restrict__ d_step, int64_t B, int C, float eps) {
     constexpr int WC = kLayerWC;
     constexpr int NS = N * N + 2 * N;
     constexpr int NR = 2 + 3 * N;
@@ -335,7 +362,7 @@ __global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, 
             unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
             wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
-                                                    scal_out, C, eps, red);
+                                                    scal_out, d_step, C, eps, red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
             if (b2 < B) {
@@ -347,7 +374,7 @@ __global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, 
             unpack_rows<TX, 1, VPT, WC>(rB, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bB, C, bv);
             wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b1, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
-                                                    scal_out, C, eps, red);
+                                                    scal_out, d_step, C, eps, red);
             b = b2;
         }
     } else {
@@ -359,7 +386,7 @@ __global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, 
             unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
             wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
-                                                    scal_out, C, eps, red);
+                                                    scal_out, d_step, C, eps, red);
         }
     }
     float* dwp = dw_part + (int64_t)blockIdx.x * C;
@@ -369,6 +396,30 @@ __global__ MHC_ROW_BOUNDS(PF) void wrap_bwd_kernel(const float* __restrict__ g, 
         if (c0 < C) store_run<float, WC>(dwp + c0, dwacc[k]);
     }
     if (MODE == 0 && threadIdx.x < NS) scal_out[(int64_t)blockIdx.x * NS + threadIdx.x] = sacc;
+}
+
+// Workgroups of more than 256 lanes hold one token at a time; they are held
+// to 128 VGPRs (4 waves per SIMD: two 448-lane workgroups per CU at C5, where
+// the fixed-point stream part of the dynamic backward otherwise takes 133).
+template <typename TX, int N, int VPT, int MODE, bool DECAY>
+__global__ MHC_ROW_BOUNDS(false) __attribute__((amdgpu_waves_per_eu(4))) void wrap_bwd_kernel(
+    const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
+    const float* __restrict__ coef, int64_t coef_stride, TX* __restrict__ dres, TX* __restrict__ dbr,
+    float* __restrict__ dw_part, float* __restrict__ scal_out, float* __restrict__ d_step, int64_t B, int C,
+    float eps) {
+    wrap_bwd_rows<TX, N, VPT, MODE, false, DECAY>(g, res, br, w, coef, coef_stride, dres, dbr, dw_part, scal_out,
+                                                  d_step, B, C, eps);
+}
+
+// Up to 256 lanes: two tokens in flight (register prefetch).
+template <typename TX, int N, int VPT, int MODE, bool DECAY>
+__global__ MHC_ROW_BOUNDS(true) void wrap_bwd_pf_kernel(
+    const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
+    const float* __restrict__ coef, int64_t coef_stride, TX* __restrict__ dres, TX* __restrict__ dbr,
+    float* __restrict__ dw_part, float* __restrict__ scal_out, float* __restrict__ d_step, int64_t B, int C,
+    float eps) {
+    wrap_bwd_rows<TX, N, VPT, MODE, true, DECAY>(g, res, br, w, coef, coef_stride, dres, dbr, dw_part, scal_out,
+                                                 d_step, B, C, eps);
 }
 
 // ---------------------------------------------------------------------------
@@ -722,8 +773,13 @@ template <typename TX, int N, bool DECAY>
 __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
     const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ dP,
     const float* __restrict__ s_tok, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
-    const float* __restrict__ phi_res, TX* __restrict__ dres, TX* __restrict__ dbr, float* __restrict__ dphi_part,
-    int64_t B, int C, int64_t tile) {
+    const float* __restrict__ phi_res, TX* __restrict__ dres, TX* __restrict__ dbr, const float* __restrict__ d_step,
+    int groups, float* __restrict__ dphi_part, int64_t B, int C, int64_t tile) {
+    // bf16 storage: the incoming d r / d b are the row pass's int16 fixed-point
+    // stream parts (fixed_scale) with steps d_step[b][groups][2]: this block's
+    // 128 channels are group blockIdx.x % groups of every token.  The sums are
+    // rounded once to bf16 on the way out.
+    constexpr bool QIN = sizeof(TX) == 2;
     constexpr int NP = 2 * N + N * N;
     static_assert(NP <= 32, "projection rows must fit one 32-row tile");
     constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
@@ -738,6 +794,7 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
     __shared__ __align__(16) char tiles_lds[2][4][TB * PITCH];   // [buf][r | b | d r | d b]
     __shared__ __align__(16) bf16_t dps_lds[2][4][32 * kWDpPitch];
     __shared__ float s_lds[2][TB];
+    __shared__ float q_lds[2][QIN ? 2 * TB : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -791,7 +848,7 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
 
     struct Fetched {
         uint4 v[4][PASSES];
-        float dp[4], s;
+        float dp[4], s, q;
     };
     Fetched f0, f1;
     const TX* srcs[4] = {res, br, dres, dbr};
@@ -808,6 +865,16 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) f.dp[q] = dp_loader ? dP[tdc * 32 + dpo + q] : 0.f;
         f.s = (tid < TB) ? s_tok[(t0 + tid < t_end) ? t0 + tid : t0] : 0.f;
+        f.q = 0.f;
+        if constexpr (QIN) {
+            // lanes TB .. 3 TB - 1: the steps of (token t0 + (tid - TB) / 2,
+            // part (tid - TB) % 2) for this block's 128 channels
+            const int qi = tid - TB;
+            if (qi >= 0 && qi < 2 * TB) {
+                const int64_t tq = t0 + qi / 2;
+                f.q = d_step[((tq < t_end ? tq : t0) * groups + (int)blockIdx.x % groups) * 2 + (qi & 1)];
+            }
+        }
     };
     auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -842,6 +909,10 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
             }
         }
         if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? f.s : 0.f;
+        if constexpr (QIN) {
+            const int qi = tid - TB;
+            if (qi >= 0 && qi < 2 * TB) q_lds[buf][qi] = (t0 + qi / 2 < t_end) ? f.q : 0.f;
+        }
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> wu32x4_t {
         const uint4 q = *reinterpret_cast<const uint4*>(p);
@@ -907,8 +978,13 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
             float rv[4], bv[4], drv[4], dbv[4];
             wlds_get4<TX>(rt + boff, rv);
             wlds_get4<TX>(bt + boff, bv);
-            wlds_get4<TX>(drt + boff, drv);
-            wlds_get4<TX>(dbt + boff, dbv);
+            if constexpr (QIN) {
+                fixed_unpack4(*reinterpret_cast<const uint2*>(drt + boff), q_lds[cur][2 * t], drv);
+                fixed_unpack4(*reinterpret_cast<const uint2*>(dbt + boff), q_lds[cur][2 * t + 1], dbv);
+            } else {
+                wlds_get4<TX>(drt + boff, drv);
+                wlds_get4<TX>(dbt + boff, dbv);
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float x[N];
@@ -1003,7 +1079,8 @@ static const void* wrap_fwd_fn() {
 template <typename TX, int V, int MODE, bool PF, bool DECAY>
 static const void* wrap_bwd_fn() {
     if constexpr (layer_row_fits(kWrapBwdArrays * 2, V))
-        return reinterpret_cast<const void*>(&wrap_bwd_kernel<TX, 4, V, MODE, PF, DECAY>);
+        return PF ? reinterpret_cast<const void*>(&wrap_bwd_pf_kernel<TX, 4, V, MODE, DECAY>)
+                  : reinterpret_cast<const void*>(&wrap_bwd_kernel<TX, 4, V, MODE, DECAY>);
     return nullptr;
 }
 
@@ -1078,17 +1155,25 @@ int wrap_bwd_grid(int dt, int n, bool decay, int64_t B, int64_t C) {
     return wrap_grid(pick_wrap_bwd(dt, t.vpt, 0, wrap_prefetch(t), decay), t.threads, B);
 }
 
+int wrap_bwd_fixed_groups(int64_t C) {
+    const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapBwdArrays * 2);
+    return t.vpt > 0 ? t.threads / 32 : 0;
+}
+
 hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, const void* res, const void* br,
                            const float* w, const float* coef, int64_t coef_stride, void* dres, void* dbr,
-                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s) {
+                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s,
+                           float* d_step) {
     if (n != 4) return hipErrorInvalidValue;
     const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapBwdArrays * 2);
     if (t.vpt <= 0) return hipErrorInvalidValue;
     const void* fn = pick_wrap_bwd(dt, t.vpt, mode, wrap_prefetch(t), decay);
     if (!fn) return hipErrorInvalidValue;
     int Ci = (int)C;
+    if (mode == 1 && dt == kBF16 && d_step == nullptr) return hipErrorInvalidValue;
     void* args[] = {(void*)&g, (void*)&res, (void*)&br, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&dres,
-                    (void*)&dbr, (void*)&dw_part, (void*)&scal_out, (void*)&B, (void*)&Ci, (void*)&eps};
+                    (void*)&dbr, (void*)&dw_part, (void*)&scal_out, (void*)&d_step, (void*)&B, (void*)&Ci,
+                    (void*)&eps};
     const int tok = timing_begin(mode == 0 ? "wrap_bwd" : "wrap_bwd_reduce", s);
     hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
@@ -1149,16 +1234,18 @@ int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
 hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
                                 const float* s_tok, const float* phi_pre, const float* phi_post, const float* phi_res,
                                 void* dres, void* dbr, float* dphi_part, int tiles, int64_t B, int64_t C,
-                                hipStream_t s) {
+                                hipStream_t s, const float* d_step, int groups) {
     if (B == 0) return hipSuccess;
     if (n != 4 || C % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
+    if (dt == kBF16 && (d_step == nullptr || groups < 1 || C % kFixedGroup != 0)) return hipErrorInvalidValue;
     int64_t tile = (B + tiles - 1) / tiles;
     tile = ((tile + 31) / 32) * 32;
     const dim3 grid((unsigned)((C + 127) / 128), (unsigned)tiles);
     const int tok = timing_begin("wrap_proj_bwd", s);
 #define MHC_WPB(TX_, D_)                                                                                          \
     hipLaunchKernelGGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(512), 0, s, (const TX_*)res, (const TX_*)br, \
-                       dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, dphi_part, B, (int)C, tile)
+                       dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, d_step, groups, dphi_part, B,  \
+                       (int)C, tile)
     if (dt == kBF16) {
         if (decay) { MHC_WPB(bf16_t, true); } else { MHC_WPB(bf16_t, false); }
     } else {

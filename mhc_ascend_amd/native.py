@@ -502,29 +502,114 @@ def mhc_layer_dynamic_bwd(grad_output: torch.Tensor, x_expanded: torch.Tensor, r
             gb[n:2 * n], gb[2 * n:].view(n, n))
 
 
-def _split_phi_concat(phi_concat: torch.Tensor, n: int):
-    return phi_concat[:n], phi_concat[n:2 * n], phi_concat[2 * n:2 * n + n * n]
+def _host_float(v) -> float:
+    """A scalar argument the reference's binding takes as a C float."""
+    return float(v.item()) if torch.is_tensor(v) else float(v)
 
 
-def mhc_layer_fwd_dynamic(x_expanded, rmsnorm_weight, phi_concat, alpha_pre, alpha_post, alpha_res, b_pre, b_post,
-                          b_res, sinkhorn_iters=20, sinkhorn_eps=1e-8, rmsnorm_eps=1e-5):
-    """Reference-order entry (bindings.cpp:880-952): phi_concat = [pre; post;
-    res] [2n+n^2, nC]; alphas may be floats or tensors.  Returns (out, saved)."""
-    n = x_expanded.size(1)
-    pp, pq, pr = _split_phi_concat(_f32c(phi_concat), n)
-    return mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, pp, pq, pr, alpha_pre, alpha_post, alpha_res, b_pre,
-                                 b_post, b_res, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
+def mhc_layer_fwd_dynamic(x_expanded: torch.Tensor, rmsnorm_weight: torch.Tensor, phi_concat: torch.Tensor,
+                          alpha_pre, alpha_post, alpha_res, b_pre: torch.Tensor, b_post: torch.Tensor,
+                          b_res: torch.Tensor, sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
+                          rmsnorm_eps: float = 1e-5):
+    """The reference's dynamic-H forward with its own call shape
+    (bindings.cpp:880-952, unpacked at ops.py:425-448): phi_concat =
+    [phi_pre; phi_post; phi_res] [2n+n^2, nC], alphas as Python floats (or
+    one-element tensors).  Returns its nine tensors in order: output fp32
+    [B, n, C], rms [B] (RMS of x_agg), x_agg_bf16 [B, C], H_pre_activated
+    [B, n], H_post_activated [B, n], M [B, n, n], y_norm_bf16 [B, C],
+    x_flat_bf16 [B, nC], rms_h [B].  Arithmetic is fp32 throughout; the
+    three bf16 tensors are rounded on output only."""
+    _check_device("mhc_layer_fwd_dynamic", x_expanded, rmsnorm_weight, phi_concat, b_pre, b_post, b_res)
+    x = _layer_x("mhc_layer_fwd_dynamic", x_expanded)
+    if phi_concat.dim() != 2:
+        raise RuntimeError("phi_concat must be [out_dim, n*C]")
+    B, n, C = x.shape
+    np_ = 2 * n + n * n
+    if tuple(phi_concat.shape) != (np_, n * C):
+        raise RuntimeError(f"mhc_layer_fwd_dynamic: phi_concat must be [{np_}, {n * C}], got "
+                           f"{tuple(phi_concat.shape)}")
+    w = _weight(rmsnorm_weight)
+    if w.numel() != C:
+        raise RuntimeError("mhc_layer_fwd_dynamic: rmsnorm_weight must have C elements")
+    phi = _f32c(phi_concat)
+    bp, bq, br = _f32c(b_pre), _f32c(b_post), _f32c(b_res)
+    if bp.numel() != n or bq.numel() != n or br.numel() != n * n:
+        raise RuntimeError("mhc_layer_fwd_dynamic: b_pre/b_post must have n and b_res n*n elements")
+    dev = x.device
+    f32 = dict(dtype=torch.float32, device=dev)
+    b16 = dict(dtype=torch.bfloat16, device=dev)
+    output = torch.empty((B, n, C), **f32)
+    rms = torch.empty((B,), **f32)
+    x_agg = torch.empty((B, C), **b16)
+    h_pre = torch.empty((B, n), **f32)
+    h_post = torch.empty((B, n), **f32)
+    M = torch.empty((B, n, n), **f32)
+    y_norm = torch.empty((B, C), **b16)
+    x_flat = torch.empty((B, n * C), **b16)
+    rms_h = torch.empty((B,), **f32)
+    with _lib.on_device(dev):
+        wsb = _lib.load().mhc_layer_fwd_dynamic_workspace_size(B, n, C)
+        ws = _ws(dev, wsb)
+        call("mhc_layer_fwd_dynamic", ptr(x), dtype_code(x.dtype), ptr(w), dtype_code(w.dtype), ptr(phi),
+             _host_float(alpha_pre), _host_float(alpha_post), _host_float(alpha_res), ptr(bp), ptr(bq), ptr(br),
+             ptr(output), ptr(rms), ptr(x_agg), ptr(h_pre), ptr(h_post), ptr(M), ptr(y_norm), ptr(x_flat),
+             ptr(rms_h), ptr(ws), int(wsb), B, n, C, int(sinkhorn_iters), float(sinkhorn_eps), float(rmsnorm_eps),
+             stream_of(x))
+    return output, rms, x_agg, h_pre, h_post, M, y_norm, x_flat, rms_h
 
 
-def mhc_layer_bwd_dynamic(grad_output, x_expanded, rmsnorm_weight, saved, phi_pre, phi_post, phi_res, alpha_pre,
+def mhc_layer_bwd_dynamic(grad_output, x_expanded, rmsnorm_weight, rms, x_agg_bf16, H_pre_activated,
+                          H_post_activated, M, y_norm_bf16, x_flat_bf16, rms_h, phi_pre, phi_post, phi_res, alpha_pre,
                           alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters=20, sinkhorn_eps=1e-8,
                           rmsnorm_eps=1e-5):
-    """Reference-named backward (bindings.cpp:600-874).  Takes the `saved`
-    buffer of mhc_layer_fwd_dynamic in place of the reference's ten saved
-    tensors; returns its 11 gradients in the same order."""
-    return mhc_layer_dynamic_bwd(grad_output, x_expanded, rmsnorm_weight, saved, phi_pre, phi_post, phi_res,
-                                 alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
-                                 rmsnorm_eps)
+    """The reference's dynamic-H backward with its 23-argument call shape
+    (bindings.cpp:600-874, called at ops.py:518-542; alphas as floats).
+    H_pre_activated, H_post_activated, M and rms_h are used as given and P
+    is recomputed from x (as the reference does); rms, x_agg_bf16,
+    y_norm_bf16 and x_flat_bf16 are recomputed in fp32 from x inside the
+    fused row pass and not read.  Returns the 11 gradients in the
+    reference's order and dtypes: grad_x, grad_rmsnorm_weight (fp32),
+    d_phi_pre, d_phi_post, d_phi_res (shaped like the phi arguments),
+    d_alpha_pre, d_alpha_post, d_alpha_res ([1] each), d_b_pre, d_b_post,
+    d_b_res."""
+    _check_device("mhc_layer_bwd_dynamic", grad_output, x_expanded, rmsnorm_weight, H_pre_activated,
+                  H_post_activated, M, rms_h, phi_pre, phi_post, phi_res, b_pre, b_post, b_res)
+    if grad_output.dim() != 3:
+        raise RuntimeError("grad_output must be 3D tensor [B, n, C]")
+    x = _layer_x("mhc_layer_bwd_dynamic", x_expanded)
+    B, n, C = x.shape
+    if grad_output.shape != x.shape:
+        raise RuntimeError("mhc_layer_bwd_dynamic: grad_output must match x [B, n, C]")
+    dev = x.device
+    g = _f32c(grad_output)
+    w = _weight(rmsnorm_weight)
+    if w.numel() != C:
+        raise RuntimeError("mhc_layer_bwd_dynamic: rmsnorm_weight must have C elements")
+    hp, hq, m, rh = _f32c(H_pre_activated), _f32c(H_post_activated), _f32c(M), _f32c(rms_h)
+    if hp.numel() != B * n or hq.numel() != B * n or m.numel() != B * n * n or rh.numel() != B:
+        raise RuntimeError("mhc_layer_bwd_dynamic: saved H_pre/H_post [B, n], M [B, n, n], rms_h [B] do not match x")
+    pp, pq, pr = _phi_parts(phi_pre, phi_post, phi_res, n, n * C)
+    bp, bq, br = _f32c(b_pre), _f32c(b_post), _f32c(b_res)
+    np_ = 2 * n + n * n
+    f32 = dict(dtype=torch.float32, device=dev)
+    grad_x = torch.empty_like(x)
+    gw = torch.empty((C,), **f32)
+    gphi = torch.empty((np_, n * C), **f32)
+    small = torch.empty((3 + np_,), **f32)
+    ga = small[:3]
+    gb = small[3:]
+    with _lib.on_device(dev):
+        wsb = _lib.load().mhc_layer_bwd_dynamic_workspace_size(B, n, C, dtype_code(x.dtype))
+        ws = _ws(dev, wsb)
+        call("mhc_layer_bwd_dynamic", ptr(g), ptr(x), dtype_code(x.dtype), ptr(w), dtype_code(w.dtype), None, None,
+             ptr(hp), ptr(hq), ptr(m), None, None, ptr(rh), ptr(pp), ptr(pq), ptr(pr), _host_float(alpha_pre),
+             _host_float(alpha_post), _host_float(alpha_res), ptr(bp), ptr(bq), ptr(br), ptr(grad_x), ptr(gw),
+             ptr(gphi), ptr(gphi[n:]), ptr(gphi[2 * n:]), ptr(ga), ptr(ga[1:]), ptr(ga[2:]), ptr(gb), ptr(gb[n:]),
+             ptr(gb[2 * n:]), ptr(ws), int(wsb), B, n, C, int(sinkhorn_iters), float(sinkhorn_eps),
+             float(rmsnorm_eps), stream_of(x))
+    return (grad_x, gw, gphi[:n].view_as(phi_pre), gphi[n:2 * n].view_as(phi_post),
+            gphi[2 * n:].view(phi_res.shape), ga[0:1], ga[1:2], ga[2:3], gb[:n].view_as(b_pre),
+            gb[n:2 * n].view_as(b_post), gb[2 * n:].view(b_res.shape))
 
 
 # =============================================================================

@@ -258,12 +258,19 @@ def build_wrapper_streams(residual: torch.Tensor, branch: torch.Tensor, n: int,
 
 
 def mhc_residual_wrapper(residual: torch.Tensor, branch: torch.Tensor, layer_fn, n: int,
-                         mode: str = "decay") -> torch.Tensor:
+                         mode: str = "decay", storage_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """MHCResidualWrapper.forward (layer.py:269-322): synthesise n streams,
     run the layer, average over streams, reshape to [B, T, C] only if T > 1.
 
     ``layer_fn`` maps X [BT, n, C] -> [BT, n, C]; the synthesis is done with
     differentiable ops so autograd reaches residual and branch.
+
+    ``storage_dtype`` (e.g. bf16) with exact leaves (float64 tensors holding
+    storage_dtype values): the 'decay' streams take the value the
+    reference's tensor op gives in that dtype, storage_dtype(float32(r) *
+    float32(0.1**(i-1))) (layer.py:307-308), while the gradient flows
+    through the product with the same float32 constant, as autograd of that
+    op does; the leaves' gradients are then not rounded to storage_dtype.
     """
     shape = residual.shape
     C = shape[-1]
@@ -275,7 +282,15 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch: torch.Tensor, layer_fn,
     br = branch.reshape(B * T, C)
     streams = [res, br]
     for i in range(2, n):
-        streams.append(res * (0.1 ** (i - 1)) if mode == "decay" else torch.zeros_like(res))
+        if mode != "decay":
+            streams.append(torch.zeros_like(res))
+        elif storage_dtype is None:
+            streams.append(res * (0.1 ** (i - 1)))
+        else:
+            c = torch.tensor(0.1 ** (i - 1), dtype=torch.float32)
+            s = res * c.item()
+            value = (res.detach().float() * c).to(storage_dtype).to(res.dtype)
+            streams.append(s + (value - s).detach())
     X = torch.stack(streams[:n], dim=1)
     out = layer_fn(X).mean(dim=1)
     if T > 1:

@@ -37,6 +37,17 @@ def assert_close(actual, expected, rtol, atol, what=""):
             f"max abs err {err.max().item():.3g}, max |ref| {e.abs().max().item():.3g}")
 
 
+BF16_RTOL = 2.0 ** -8  # unit roundoff of bf16 (8 significant bits): one rounding to nearest
+
+
+def assert_close_bf16(actual, expected, what="", floor=1e-3):
+    """A bf16-stored result against a float64 reference: one rounding to
+    nearest (relative 2^-8) plus an absolute floor of `floor` * max|ref| for
+    the fp32 arithmetic before the rounding and for elements near zero."""
+    assert actual.dtype == torch.bfloat16, f"{what}: expected bf16 storage, got {actual.dtype}"
+    assert_close(actual, expected, BF16_RTOL, grad_atol(expected, floor), what)
+
+
 def grad_atol(ref: torch.Tensor, frac: float = 1e-4) -> float:
     """Absolute floor for gradient comparisons: frac * max|ref| (gradients
     summed over many tokens can have entries near zero after cancellation)."""

@@ -9,7 +9,7 @@ import torch
 import mhc_ascend_amd as mhc
 from mhc_ascend_amd import native
 from oracle import reference as R
-from tests.conftest import assert_close, grad_atol
+from tests.conftest import assert_close, assert_close_bf16, grad_atol
 
 pytestmark = pytest.mark.gpu
 
@@ -30,15 +30,14 @@ def _ref_leaf(t):
 
 def _check_out(out, ref, dtype, what):
     if dtype == torch.bfloat16:
-        assert out.dtype == torch.bfloat16
-        assert_close(out, ref, 2e-2, grad_atol(ref, 1e-2), what)
+        assert_close_bf16(out, ref, what)
     else:
         assert_close(out, ref, what=what, **FWD)
 
 
 def _check_grad(got, ref, dtype, what, frac=1e-5):
     if dtype == torch.bfloat16:
-        assert_close(got, ref, 2e-2, grad_atol(ref, 1e-2), what)
+        assert_close_bf16(got, ref, what)
     else:
         assert_close(got, ref, 1e-3, grad_atol(ref, frac), what)
 
@@ -61,7 +60,7 @@ def test_rmsnorm(device, dtype, B, C):
     _check_out(out, ref.detach(), dtype, f"rmsnorm B={B} C={C}")
     _check_grad(xd.grad, xr.grad, dtype, "rmsnorm dx")
     assert wd.grad.dtype == torch.float32
-    assert_close(wd.grad, wr.grad, 1e-3, grad_atol(wr.grad, 1e-4 if dtype == torch.float32 else 1e-2),
+    assert_close(wd.grad, wr.grad, 1e-3, grad_atol(wr.grad, 1e-4),
                  "rmsnorm dw")
     _, rms_got = native.rmsnorm_fwd(x.to(device), w.to(device), 1e-5)
     assert_close(rms_got, rms.detach(), 1e-5, 0, "rms")
@@ -106,7 +105,7 @@ def test_stream_aggregate(device, dtype, shared, B, C):
     ref.backward(go.double())
     _check_out(out, ref.detach(), dtype, "aggregate out")
     _check_grad(xd.grad, xr.grad, dtype, "aggregate dx")
-    assert_close(Hd.grad, Hr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Hr.grad, 1e-4),
+    assert_close(Hd.grad, Hr.grad, 1e-3, grad_atol(Hr.grad, 1e-4),
                  "aggregate dH")
 
 
@@ -131,7 +130,7 @@ def test_stream_ops_general_n(device, n, C, dtype):
     ref.backward(go.double())
     _check_out(out, ref.detach(), dtype, f"n={n} aggregate out")
     _check_grad(xd.grad, xr.grad, dtype, f"n={n} aggregate dx")
-    assert_close(Hd.grad, Hr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Hr.grad, 1e-4),
+    assert_close(Hd.grad, Hr.grad, 1e-3, grad_atol(Hr.grad, 1e-4),
                  f"n={n} aggregate dH")
 
     y = torch.randn(B, C, generator=g).to(dtype)
@@ -148,9 +147,9 @@ def test_stream_ops_general_n(device, n, C, dtype):
     assert_close(out, ref.detach(), what=f"n={n} distribute out", **FWD)
     _check_grad(xd.grad, xr.grad, dtype, f"n={n} distribute dx")
     _check_grad(yd.grad, yr.grad, dtype, f"n={n} distribute dy")
-    assert_close(Md.grad, Mr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Mr.grad, 1e-4),
+    assert_close(Md.grad, Mr.grad, 1e-3, grad_atol(Mr.grad, 1e-4),
                  f"n={n} distribute dM")
-    assert_close(Hd.grad, Hr.grad, 1e-3 if dtype == torch.float32 else 2e-2, grad_atol(Hr.grad, 1e-4),
+    assert_close(Hd.grad, Hr.grad, 1e-3, grad_atol(Hr.grad, 1e-4),
                  f"n={n} distribute dH")
 
 

@@ -4,7 +4,9 @@ of residual*0.1**(i-1), and 'zero'), the layer (dynamic and static H), the
 stream mean and the [B, T, C] reshape; forward and every gradient.
 
 Tolerances: fp32 outputs rtol 1e-4; gradients rtol 1e-3 (fp32 storage) or
-2e-2 (bf16 storage) with absolute floors relative to max|ref|.  Config C5 runs
+one bf16 rounding (2^-8 relative, plus 1e-3 max|ref|) for bf16 storage,
+against an oracle whose leaves are exact (float64) so that its gradients are
+not rounded; absolute floors relative to max|ref|.  Config C5 runs
 at its width C=7168 on a reduced token count (the full-size oracle needs
 ~200 GB)."""
 import pytest
@@ -12,7 +14,7 @@ import torch
 
 import mhc_ascend_amd as mhc
 from oracle import reference as R
-from tests.conftest import assert_close, grad_atol
+from tests.conftest import assert_close, assert_close_bf16, grad_atol
 
 pytestmark = pytest.mark.gpu
 
@@ -50,13 +52,15 @@ def _oracle(wrap, res, br, grad, mode):
     names = DYN if layer.use_dynamic_h else STA
     w = layer.rmsnorm_weight.detach().cpu().double().requires_grad_(True)
     ps = [getattr(layer, k).detach().cpu().double().requires_grad_(True) for k in names]
-    r = res.detach().cpu().clone().requires_grad_(True)
-    b = br.detach().cpu().clone().requires_grad_(True)
+    # exact leaves holding the storage values; the decay streams rounded to
+    # the storage dtype in value only, so the leaf gradients stay unrounded
+    r = res.detach().cpu().double().requires_grad_(True)
+    b = br.detach().cpu().double().requires_grad_(True)
     if layer.use_dynamic_h:
         fn = lambda X: R.mhc_layer_dynamic(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
     else:
         fn = lambda X: R.mhc_layer_static(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
-    out = R.mhc_residual_wrapper(r, b, fn, 4, mode)
+    out = R.mhc_residual_wrapper(r, b, fn, 4, mode, storage_dtype=res.dtype)
     out.backward(grad.double())
     return out.detach(), r.grad, b.grad, w.grad, [p.grad for p in ps]
 
@@ -77,13 +81,14 @@ def _check(got, want, dtype, names, tag):
     rout, rgr, rgb, rgw, rgp = want
     assert out.dtype == torch.float32 and tuple(out.shape) == tuple(rout.shape), (out.dtype, out.shape, rout.shape)
     assert_close(out, rout, 1e-4, grad_atol(rout, 1e-5), f"{tag} out")
-    bf = dtype == torch.bfloat16
     assert gr.dtype == dtype and gb.dtype == dtype
-    rt, fr = (2e-2, 1e-2) if bf else (1e-3, 1e-5)
-    # the bf16 oracle's leaf grads are rounded to bf16 by autograd too
-    assert_close(gr.float(), rgr.double(), rt, grad_atol(rgr.double(), fr), f"{tag} d residual")
-    assert_close(gb.float(), rgb.double(), rt, grad_atol(rgb.double(), fr), f"{tag} d branch")
-    assert_close(gw.float(), rgw, 8e-3, grad_atol(rgw, 1e-3), f"{tag} d_weight (bf16 param)")
+    if dtype == torch.bfloat16:
+        assert_close_bf16(gr, rgr, f"{tag} d residual")
+        assert_close_bf16(gb, rgb, f"{tag} d branch")
+    else:
+        assert_close(gr, rgr, 1e-3, grad_atol(rgr, 1e-5), f"{tag} d residual")
+        assert_close(gb, rgb, 1e-3, grad_atol(rgb, 1e-5), f"{tag} d branch")
+    assert_close_bf16(gw, rgw, f"{tag} d_weight (bf16 param)")
     # Through the stream mean every stream gets the same cotangent G / n, so
     # dM is constant along i and the Sinkhorn adjoint's last column step
     # cancels it: the H_res-side gradients are 0 up to eps-terms (~1e-20
