@@ -230,6 +230,9 @@ int mhc_layer_static_fwd(const void* x, int32_t x_dtype, const void* weight, int
     MHC_REQUIRE(weight && h_pre && h_post && h_res && saved, "layer_static_fwd: null parameter pointer");
     MHC_REQUIRE(batch == 0 || (x && out), "layer_static_fwd: null x/out");
     hipStream_t s = (hipStream_t)stream;
+    if (layer_static_fwd_fused(n, hidden))
+        return hip_status(launch_layer_static_fwd(x_dtype, n, x, weight, weight_dtype, h_pre, h_post, h_res, saved,
+                                                  num_iters, sinkhorn_eps, out, rms, batch, hidden, rmsnorm_eps, s));
     hipError_t e = launch_static_coef(n, h_pre, h_post, h_res, weight, weight_dtype, hidden, saved, num_iters,
                                       sinkhorn_eps, s);
     if (e != hipSuccess) return hip_status(e);

@@ -167,6 +167,76 @@ __global__ MHC_ROW_BOUNDS(false) void layer_fwd_kernel(const TX* __restrict__ x,
 }
 
 // ---------------------------------------------------------------------------
+// Static forward in ONE launch: every workgroup forms the shared coefficients
+// h_pre = sigmoid(H_pre), h_post = 2 sigmoid(H_post), M = SK(exp(H_res)) in
+// its first wave (the same code as static_coef_kernel, so every workgroup
+// gets identical values) while its row loads are in flight, and reads the
+// RMSNorm weight in its own dtype.  Workgroup 0 also writes the backward's
+// saved state ([coef | pad | w32]).  One launch instead of two (n <= 8).
+// ---------------------------------------------------------------------------
+// Lanes of the first wave; each value goes to cf (LDS) and, when `save` is
+// not null, to the saved state.
+template <int N>
+__device__ __forceinline__ void static_coefs_wave(const float* __restrict__ h_pre, const float* __restrict__ h_post,
+                                                  const float* __restrict__ h_res, int iters, float eps,
+                                                  float* __restrict__ cf, float* __restrict__ save) {
+    const int r = threadIdx.x;
+    auto put = [&](int i, float v) {
+        cf[i] = v;
+        if (save) save[i] = v;
+    };
+    if (r < N) {
+        put(r, sigmoidf(h_pre[r]));
+        put(N + r, 2.f * sigmoidf(h_post[r]));
+    }
+    if constexpr (N == 4) {
+        float a = r < 16 ? expf(h_res[r]) : 0.f;
+        sk16_forward(a, iters, eps);
+        if (r < 16) put(2 * N + r, a);
+    } else {
+        float a[N];
+#pragma unroll
+        for (int c = 0; c < N; ++c) a[c] = (r < N) ? expf(h_res[r * N + c]) : 0.f;
+        sk_forward<N>(a, iters, eps, r < N);
+        if (r < N) {
+#pragma unroll
+            for (int c = 0; c < N; ++c) put(2 * N + r * N + c, a[c]);
+        }
+    }
+}
+
+template <typename TX, typename TW, int N, int VPT>
+__global__ MHC_ROW_BOUNDS(false) void layer_static_fwd_kernel(const TX* __restrict__ x, const TW* __restrict__ weight,
+                                                              const float* __restrict__ h_pre,
+                                                              const float* __restrict__ h_post,
+                                                              const float* __restrict__ h_res,
+                                                              float* __restrict__ saved, int w_off, int iters,
+                                                              float sk_eps, float* __restrict__ out,
+                                                              float* __restrict__ rms_out, int64_t B, int C,
+                                                              float eps) {
+    constexpr int WC = kLayerWC;
+    constexpr int NC = coef_size<N>();
+    __shared__ float red[8];
+    __shared__ float cf[NC];
+    const int64_t b = blockIdx.x;
+    RawRows<TX, N, VPT, WC> xr;
+    load_rows_raw<TX, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xr);
+    if (threadIdx.x < kWave) static_coefs_wave<N>(h_pre, h_post, h_res, iters, sk_eps, cf, b == 0 ? saved : nullptr);
+    float wv[VPT][WC];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+#pragma unroll
+        for (int e = 0; e < WC; ++e) wv[k][e] = c0 < C ? VecIO<TW>::scalar(weight + c0 + e) : 0.f;
+        if (b == 0 && c0 < C) store_run<float, WC>(saved + w_off + c0, wv[k]);
+    }
+    __syncthreads();
+    float xv[N][VPT][WC];
+    unpack_rows<TX, N, VPT, WC>(xr, C, xv);
+    fwd_token<TX, float, N, VPT>(b, cf, 0, wv, xv, out, rms_out, C, eps, red);
+}
+
+// ---------------------------------------------------------------------------
 // Fused backward.  Persistent workgroups stride over tokens (optionally with
 // the two-buffer prefetch of the forward).  Per token the block forms
 // (dM[n*n], dh_post_act[n], dh_pre_act[n], 1/r, k2 = dot/(C r^3)).  MODE 0
@@ -778,6 +848,59 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
                     (void*)&B, (void*)&Ci, (void*)&eps};
     const int tok = timing_begin("layer_fwd", s);
     hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
+    timing_end(tok, s);
+    return e != hipSuccess ? e : hipGetLastError();
+}
+
+template <typename TX, typename TW, int N, int V>
+static const void* static_fwd_fn() {
+    if constexpr (layer_row_fits(N, V))
+        return reinterpret_cast<const void*>(&layer_static_fwd_kernel<TX, TW, N, V>);
+    return nullptr;
+}
+
+bool layer_static_fwd_fused(int n, int64_t C) { return n <= 8 && fwd_tiling(C, n).vpt > 0; }
+
+hipError_t launch_layer_static_fwd(int x_dtype, int n, const void* x, const void* weight, int w_dtype,
+                                   const float* h_pre, const float* h_post, const float* h_res, float* saved,
+                                   int iters, float sk_eps, float* out, float* rms_out, int64_t B, int64_t C,
+                                   float eps, hipStream_t s) {
+    const RowTiling t = fwd_tiling(C, n);
+    if (t.vpt <= 0 || n > 8) return hipErrorInvalidValue;
+    if (B == 0) {
+        // no tokens: the saved state alone (the backward still needs it)
+        return launch_static_coef(n, h_pre, h_post, h_res, weight, w_dtype, C, saved, iters, sk_eps, s);
+    }
+    if (B > 0x7fffffff) return hipErrorInvalidValue;  // grid x limit
+    const void* fn = nullptr;
+#define MHC_SF_TW(TX_, N_)                                                                \
+    if (w_dtype == kBF16) {                                                               \
+        MHC_PICK_VPT(t.vpt, fn = static_fwd_fn<TX_, bf16_t, N_, V_>());                   \
+    } else {                                                                              \
+        MHC_PICK_VPT(t.vpt, fn = static_fwd_fn<TX_, float, N_, V_>());                    \
+    }
+#define MHC_SF_N(N_)                                                                      \
+    if (x_dtype == kBF16) {                                                               \
+        MHC_SF_TW(bf16_t, N_)                                                             \
+    } else {                                                                              \
+        MHC_SF_TW(float, N_)                                                              \
+    }
+    switch (n) {
+        case 2: { MHC_SF_N(2); break; }
+        case 4: { MHC_SF_N(4); break; }
+        case 8: { MHC_SF_N(8); break; }
+        default: break;
+    }
+#undef MHC_SF_N
+#undef MHC_SF_TW
+    if (!fn) return hipErrorInvalidValue;
+    int Ci = (int)C;
+    int w_off = saved_w_offset(n);
+    void* args[] = {(void*)&x, (void*)&weight, (void*)&h_pre, (void*)&h_post, (void*)&h_res, (void*)&saved,
+                    (void*)&w_off, (void*)&iters, (void*)&sk_eps, (void*)&out, (void*)&rms_out, (void*)&B,
+                    (void*)&Ci, (void*)&eps};
+    const int tok = timing_begin("layer_fwd", s);
+    hipError_t e = hipLaunchKernel(fn, dim3((unsigned)B), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
     return e != hipSuccess ? e : hipGetLastError();
 }

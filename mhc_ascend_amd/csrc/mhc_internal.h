@@ -42,6 +42,13 @@ int saved_w_offset(int n);
 hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res,
                               const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
                               hipStream_t s);
+// The static forward in one launch (coefficients formed in every
+// workgroup, saved state written by workgroup 0): n <= 8 on register rows.
+bool layer_static_fwd_fused(int n, int64_t C);
+hipError_t launch_layer_static_fwd(int x_dtype, int n, const void* x, const void* weight, int w_dtype,
+                                   const float* h_pre, const float* h_post, const float* h_res, float* saved,
+                                   int iters, float sk_eps, float* out, float* rms_out, int64_t B, int64_t C,
+                                   float eps, hipStream_t s);
 // out is [B, n, C] in out_dtype (fp32, or bf16 for the inference entry).
 // rms_scratch > 0: rms_out is scratch of that many floats (>= B) whose
 // contents the caller does not need; 0: rms_out (when not null) receives r.
