@@ -165,6 +165,22 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
                          void* workspace, size_t workspace_bytes, int64_t batch, int32_t n, int32_t hidden,
                          int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, void* stream);
 
+/* ---- allocation-free static backward ------------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops): the same
+ * gradients as mhc_layer_static_bwd, bit for bit, with its workspace in a
+ * library-owned device array of mhc_noalloc_scratch_bytes() (16 MiB, one per
+ * device, held until the process ends) instead of a caller buffer.  The
+ * caller still passes every input and output.  Shapes whose workspace would
+ * exceed the array return MHC_ERR_UNSUPPORTED.  Calls that overlap on one
+ * device share the array and race: serialise them (one stream, or events). */
+size_t mhc_noalloc_scratch_bytes(void);
+int mhc_layer_static_bwd_noalloc(const float* grad_out, const void* x, int32_t x_dtype, int32_t weight_dtype,
+                                 const float* h_pre, const float* h_post, const float* h_res, const float* saved,
+                                 void* grad_x, void* grad_weight, float* grad_h_pre, float* grad_h_post,
+                                 float* grad_h_res, int64_t batch, int32_t n, int32_t hidden, int32_t num_iters,
+                                 float sinkhorn_eps, float rmsnorm_eps, void* stream);
+
 /* ---- dynamic-H projection ----------------------------------------------------
  * out[b, o] = sum_k inp[b, k] weight[o, k]: inp [batch, k] (dtype), weight
  * [out_dim, k] fp32, out [batch, out_dim] fp32; out_dim <= 8192 (tiles of

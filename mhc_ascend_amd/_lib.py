@@ -55,6 +55,9 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
                                                          _i64, _i32, _i32, _vp]),
     "mhc_stream_distribute_mix_add_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _i64, _vp, _i64, _vp, _vp,
                                                          _vp, _vp, _vp, _i64, _i32, _i32, _vp]),
+    "mhc_noalloc_scratch_bytes": (_sz, []),
+    "mhc_layer_static_bwd_noalloc": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                    _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
     "mhc_fused_rmsnorm_matmul_fwd_workspace_size": (_sz, [_i64, _i64, _i32]),
     "mhc_fused_rmsnorm_matmul_fwd": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _sz, _i64, _i64, _i32, _vp]),
     "mhc_fused_rmsnorm_matmul_bwd_workspace_size": (_sz, [_i64, _i64, _i32]),

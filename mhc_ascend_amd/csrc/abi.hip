@@ -303,6 +303,61 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
     return hip_status(e);
 }
 
+// ---- allocation-free static backward ---------------------------------------
+// mhc_layer_static_bwd with its workspace in a file-scope device array
+// instead of a caller buffer, for callers that cannot allocate (HIP graph
+// capture, serving loops).  Each device holds its own copy of the array for
+// the life of the process; its address on a device comes from
+// hipGetSymbolAddress on that device's first call (the name itself is only a
+// host-side handle).  Nothing in it needs clearing: every kernel writes its
+// partials before anything reads them.  Calls that overlap on one device
+// share the array and race.
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64] = {};
+
+static int scratch_on_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    if (dev < 0 || dev >= 64) return fail(MHC_ERR_UNSUPPORTED, "scratch: device index out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (!p) return fail(MHC_ERR_INVALID, "scratch: hipGetSymbolAddress returned no address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MHC_SUCCESS;
+}
+
+size_t mhc_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int mhc_layer_static_bwd_noalloc(const float* grad_out, const void* x, int32_t x_dtype, int32_t weight_dtype,
+                                 const float* h_pre, const float* h_post, const float* h_res, const float* saved,
+                                 void* grad_x, void* grad_weight, float* grad_h_pre, float* grad_h_post,
+                                 float* grad_h_res, int64_t batch, int32_t n, int32_t hidden, int32_t num_iters,
+                                 float sinkhorn_eps, float rmsnorm_eps, void* stream) {
+    int st = check_layer_shape("layer_static_bwd_noalloc", batch, n, hidden, x_dtype, num_iters);
+    if (st) return st;
+    const size_t need = static_bwd_ws(batch, n, hidden, x_dtype).total;
+    if (need > kNoAllocScratchBytes)
+        return fail(MHC_ERR_UNSUPPORTED, "layer_static_bwd_noalloc: this shape needs " + std::to_string(need) +
+                                             " bytes of scratch, more than the library's " +
+                                             std::to_string(kNoAllocScratchBytes) +
+                                             "; use mhc_layer_static_bwd with a workspace");
+    void* ws = nullptr;
+    st = scratch_on_current_device(&ws);
+    if (st) return st;
+    return mhc_layer_static_bwd(grad_out, x, x_dtype, weight_dtype, h_pre, h_post, h_res, saved, grad_x, grad_weight,
+                                grad_h_pre, grad_h_post, grad_h_res, ws, kNoAllocScratchBytes, batch, n, hidden,
+                                num_iters, sinkhorn_eps, rmsnorm_eps, stream);
+}
+
 // ---- standalone operators ---------------------------------------------------
 // Rows the register kernels cannot take run the channel-loop kernels, which
 // take any width; the RMSNorm backward's keeps its dw row in LDS (dw_row).

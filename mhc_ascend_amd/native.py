@@ -323,6 +323,33 @@ def mhc_layer_static_bwd(grad_out: torch.Tensor, x: torch.Tensor, rmsnorm_weight
     return grad_x, gw, ghp, ghq, ghr
 
 
+def mhc_layer_static_bwd_noalloc(grad_out: torch.Tensor, x: torch.Tensor, rmsnorm_weight: torch.Tensor,
+                                 H_pre: torch.Tensor, H_post: torch.Tensor, H_res: torch.Tensor, saved: torch.Tensor,
+                                 num_iters: int = 20, sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5):
+    """mhc_layer_static_bwd through the allocation-free entry: the library
+    uses its own per-device scratch array instead of a workspace (only the
+    outputs are allocated here).  Same results, bit for bit."""
+    _check_device("mhc_layer_static_bwd_noalloc", grad_out, x, rmsnorm_weight, H_pre, H_post, H_res, saved)
+    x = _layer_x("mhc_layer_static_bwd_noalloc", x)
+    B, n, C = x.shape
+    if grad_out.shape != x.shape:
+        raise RuntimeError("mhc_layer_static_bwd_noalloc: grad_out must match x [B, n, C]")
+    g = _f32c(grad_out)
+    wdt = rmsnorm_weight.dtype if rmsnorm_weight.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    hp, hq, hr = _f32c(H_pre), _f32c(H_post), _f32c(H_res)
+    dev = x.device
+    grad_x = torch.empty_like(x)
+    gw = torch.empty((C,), dtype=wdt, device=dev)
+    ghp = torch.empty((n,), dtype=torch.float32, device=dev)
+    ghq = torch.empty((n,), dtype=torch.float32, device=dev)
+    ghr = torch.empty((n, n), dtype=torch.float32, device=dev)
+    with _lib.on_device(dev):
+        call("mhc_layer_static_bwd_noalloc", ptr(g), ptr(x), dtype_code(x.dtype), dtype_code(wdt), ptr(hp), ptr(hq),
+             ptr(hr), ptr(saved), ptr(grad_x), ptr(gw), ptr(ghp), ptr(ghq), ptr(ghr), B, n, C, int(num_iters),
+             float(sinkhorn_eps), float(rmsnorm_eps), stream_of(x))
+    return grad_x, gw, ghp, ghq, ghr
+
+
 # =============================================================================
 # Dynamic-H projection (bindings.cpp:480-541) and fused dynamic layer
 # (bindings.cpp:600-952)
