@@ -8,7 +8,8 @@
  * stream and returns without synchronising.  Buffers are caller-owned,
  * contiguous, row-major.  Scratch memory is passed in by the caller
  * (`workspace` / `workspace_bytes`, size from the matching *_workspace_size
- * query); the library keeps no hidden device state, so calls are reentrant.
+ * query); the library keeps no hidden device state, so calls are reentrant
+ * (the one exception is the allocation-free entry's scratch array, below).
  *
  * Element types: `dtype` arguments take MHC_DTYPE_F32 or MHC_DTYPE_BF16 and
  * describe the storage of the large [B, n, C] / [B, C] tensors; all
@@ -43,17 +44,6 @@ int mhc_abi_version(void);
 
 /* Message for the last MHC_ERR_* returned on this thread ("" if none). */
 const char* mhc_last_error(void);
-
-/* ---- kernel timing (HIP events on the launch stream) ----------------------
- * When enabled, the library records a start/end hipEvent pair around each of
- * its main kernels on the stream it launches them on.  mhc_timing_query
- * synchronises the recorded events of `kernel` and returns the summed
- * duration (ms) and the launch count since the last reset.  No counterpart
- * in the reference (its benchmark times whole calls with NPU events,
- * benchmark.py:196-204). */
-int mhc_timing_enable(int enable);
-int mhc_timing_reset(void);
-int mhc_timing_query(const char* kernel, double* total_ms, int64_t* launches);
 
 /* ---- Sinkhorn-Knopp --------------------------------------------------------
  * out = SK_{num_iters, eps}(inp) on [batch, n, n] fp32, dividing rows then

@@ -5,8 +5,12 @@ that the library's ``libamdhip64.so.7`` dependency resolves to the HIP
 runtime torch already loaded (same SONAME) - one runtime per process, and
 torch's HIP streams are valid handles for the library.
 
-There is no fallback: if the library is missing or fails to load, every op
-raises ``RuntimeError``.
+There is no fallback: if the library or the C++ autograd extension is
+missing or fails to load, every op raises ``RuntimeError``.
+
+``timed_build()`` is a benchmark facility: inside it every call goes to
+``libmhc_hip_timed.so``, the same sources built with per-kernel HIP-event
+timing (include/mhc_hip_timing.h); the product library has no timing state.
 """
 from __future__ import annotations
 
@@ -19,10 +23,10 @@ from typing import Dict, List, Tuple
 
 import torch  # noqa: F401  (must precede loading the HIP library)
 
+_PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libmhc_hip.so"
-# MHC_HIP_LIB selects another build of the same library (same ABI), e.g. for
-# comparing kernel variants; by default the in-tree build is loaded.
-LIB_PATH = os.environ.get("MHC_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+LIB_PATH = os.path.join(_PKG, LIB_NAME)
+TIMED_LIB_PATH = os.path.join(_PKG, "libmhc_hip_timed.so")
 
 F32 = 0
 BF16 = 1
@@ -40,9 +44,6 @@ _sz = ctypes.c_size_t
 SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "mhc_abi_version": (ctypes.c_int, []),
     "mhc_last_error": (ctypes.c_char_p, []),
-    "mhc_timing_enable": (ctypes.c_int, [ctypes.c_int]),
-    "mhc_timing_reset": (ctypes.c_int, []),
-    "mhc_timing_query": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
     "mhc_sinkhorn_knopp_fwd": (ctypes.c_int, [_vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "mhc_sinkhorn_knopp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "mhc_rmsnorm_fwd": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _i64, _i32, _f32, _vp]),
@@ -107,57 +108,95 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
                                             _i64, _i32, _i32, _i32, _f32, _f32, _vp]),
 }
 
+# The benchmark build's extra entries (include/mhc_hip_timing.h).
+TIMING_SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
+    "mhc_timing_enable": (ctypes.c_int, [ctypes.c_int]),
+    "mhc_timing_reset": (ctypes.c_int, []),
+    "mhc_timing_query": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
+}
+
 _lib = None
+_product = None
 _lock = threading.Lock()
 
 
+def _open(path: str, signatures) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"mhc_ascend_amd: HIP library {path} is not built; run "
+            "`python -m mhc_ascend_amd.csrc.build` (or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in signatures.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
 def load() -> ctypes.CDLL:
-    """Load and declare the library (idempotent)."""
-    global _lib
+    """The library every call goes to (idempotent)."""
+    global _lib, _product
     if _lib is not None:
         return _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(LIB_PATH):
-                raise RuntimeError(
-                    f"mhc_ascend_amd: HIP library {LIB_PATH} is not built; run "
-                    "`python -m mhc_ascend_amd.csrc.build` (or __graft_entry__.build())")
-            lib = ctypes.CDLL(LIB_PATH)
-            for name, (res, args) in SIGNATURES.items():
-                fn = getattr(lib, name)
-                fn.restype = res
-                fn.argtypes = args
-            _lib = lib
+            _product = _open(LIB_PATH, SIGNATURES)
+            _lib = _product
     return _lib
 
 
-AUTOGRAD_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_mhc_autograd.so")
+AUTOGRAD_PATH = os.path.join(_PKG, "_mhc_autograd.so")
 _autograd = None
-_autograd_done = False
 _autograd_lock = threading.Lock()
 
 
+def _bind(mod, lib) -> None:
+    mod.bind({name: ctypes.cast(getattr(lib, name), ctypes.c_void_p).value for name in mod.entry_names()})
+
+
 def autograd():
-    """The C++ autograd nodes of the fused layers (``_mhc_autograd.so``, a
-    torch extension built beside the library), bound to this library's
-    entry points; None when it is not built or ``MHC_CPP_AUTOGRAD=0``, in
-    which case the layers run their Python autograd functions over the same
-    entry points (identical results, more host time per call)."""
-    global _autograd, _autograd_done
-    if _autograd_done:
+    """The C++ autograd nodes of the fused layers and the fused wrapper
+    (``_mhc_autograd.so``, a torch extension built beside the library),
+    bound to the loaded library's entry points.  Raises when it is not
+    built: the fused layers have no other orchestration."""
+    global _autograd
+    if _autograd is not None:
         return _autograd
     lib = load()
     with _autograd_lock:
-        if not _autograd_done:
-            if os.environ.get("MHC_CPP_AUTOGRAD", "1") != "0" and os.path.exists(AUTOGRAD_PATH):
-                spec = importlib.util.spec_from_file_location("mhc_ascend_amd._mhc_autograd", AUTOGRAD_PATH)
-                mod = importlib.util.module_from_spec(spec)
-                spec.loader.exec_module(mod)
-                mod.bind({name: ctypes.cast(getattr(lib, name), ctypes.c_void_p).value
-                          for name in mod.entry_names()})
-                _autograd = mod
-            _autograd_done = True
+        if _autograd is None:
+            if not os.path.exists(AUTOGRAD_PATH):
+                raise RuntimeError(
+                    f"mhc_ascend_amd: the C++ autograd extension {AUTOGRAD_PATH} is not built; run "
+                    "`python -m mhc_ascend_amd.csrc.build` (or __graft_entry__.build())")
+            spec = importlib.util.spec_from_file_location("mhc_ascend_amd._mhc_autograd", AUTOGRAD_PATH)
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            _bind(mod, lib)
+            _autograd = mod
     return _autograd
+
+
+@contextlib.contextmanager
+def timed_build():
+    """Benchmark facility: route every call (ctypes and the C++ autograd
+    nodes) to libmhc_hip_timed.so for the duration of the block, and yield
+    it; its mhc_timing_* entries then time each kernel on its stream.  The
+    two builds run the same kernels on the same buffers (identical
+    sources), so state such as `saved` buffers carries across."""
+    global _lib
+    product = load()
+    ag = autograd()
+    timed = _open(TIMED_LIB_PATH, {**SIGNATURES, **TIMING_SIGNATURES})
+    with _lock:
+        _lib = timed
+        _bind(ag, timed)
+    try:
+        yield timed
+    finally:
+        with _lock:
+            _lib = product
+            _bind(ag, product)
 
 
 def call(name: str, *args) -> None:
@@ -200,7 +239,7 @@ def dtype_code(dt: torch.dtype) -> int:
     raise RuntimeError(f"mhc_ascend_amd: unsupported storage dtype {dt} (float32 or bfloat16)")
 
 
-# ---- kernel timing ----------------------------------------------------------
+# ---- kernel timing (inside timed_build() only) -----------------------------
 
 def timing_enable(on: bool = True) -> None:
     call("mhc_timing_enable", 1 if on else 0)

@@ -8,8 +8,9 @@
 // forward and the autograd engine's hand-off to a Python backward out of
 // every step.
 //
-// The fused MHCResidualWrapper (layer.py:269-322) has nodes of the same kind
-// (mhc_ascend_amd.ops.MHCWrapperStaticFunction / MHCWrapperDynamicFunction).
+// The fused MHCResidualWrapper (layer.py:269-322) has nodes of the same kind.
+// These nodes are the package's only orchestration of the fused entries;
+// tests/pyref_autograd.py restates them in Python for a bit-for-bit check.
 //
 // The entry points are not linked: bind() receives their addresses from the
 // ctypes handle of the already loaded library, so both paths share one copy

@@ -3,7 +3,9 @@
     python -m mhc_ascend_amd.csrc.build [--jobs N] [--verbose]
 
 Each .hip translation unit is compiled to an object in parallel, then all
-are linked into ``mhc_ascend_amd/libmhc_hip.so``.  Alongside, g++ builds
+are linked into ``mhc_ascend_amd/libmhc_hip.so``; the same sources with
+MHC_KERNEL_TIMING make ``libmhc_hip_timed.so``, the benchmark's build with
+per-kernel HIP-event timing (include/mhc_hip_timing.h).  Alongside, g++ builds
 ``mhc_ascend_amd/_mhc_autograd.so``, the C++ autograd nodes of the fused
 layers (autograd.cpp, a torch extension that calls the library through the
 addresses of its C-ABI entry points).  Every call rebuilds from scratch (the
@@ -26,6 +28,7 @@ INCLUDE = os.path.join(REPO, "include")
 BUILD_DIR = os.path.join(CSRC, "_build")
 LIB_NAME = "libmhc_hip.so"
 LIB_PATH = os.path.join(PKG, LIB_NAME)
+TIMED_LIB_PATH = os.path.join(PKG, "libmhc_hip_timed.so")
 AUTOGRAD_NAME = "_mhc_autograd"
 AUTOGRAD_PATH = os.path.join(PKG, AUTOGRAD_NAME + ".so")
 
@@ -82,23 +85,29 @@ def _autograd_cmd(out: str):
 
 
 def build(jobs: int | None = None, verbose: bool = False) -> str:
+    """Build the product library, its benchmark twin with per-kernel timing
+    (the same sources with MHC_KERNEL_TIMING, libmhc_hip_timed.so; only
+    bench.py's per-kernel pass loads it) and the autograd extension."""
     hipcc = _hipcc()
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    objs = []
+    variants = ((LIB_PATH, BUILD_DIR, []), (TIMED_LIB_PATH, os.path.join(BUILD_DIR, "timed"), ["-DMHC_KERNEL_TIMING"]))
+    objs = {lib: [] for lib, _, _ in variants}
     cmds = []
-    for src in SOURCES:
-        obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-        objs.append(obj)
-        cmds.append([hipcc, *COMMON_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+    for lib, bdir, defs in variants:
+        os.makedirs(bdir, exist_ok=True)
+        for src in SOURCES:
+            obj = os.path.join(bdir, os.path.splitext(src)[0] + ".o")
+            objs[lib].append(obj)
+            cmds.append([hipcc, *COMMON_FLAGS, *defs, "-c", os.path.join(CSRC, src), "-o", obj])
     ag_tmp = AUTOGRAD_PATH + ".tmp"
     cmds.append(_autograd_cmd(ag_tmp))
     jobs = jobs or min(len(cmds), os.cpu_count() or 4, 16)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     os.replace(ag_tmp, AUTOGRAD_PATH)
-    tmp = LIB_PATH + ".tmp"
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
-    os.replace(tmp, LIB_PATH)
+    for lib, _, _ in variants:
+        tmp = lib + ".tmp"
+        _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs[lib]], verbose)
+        os.replace(tmp, lib)
     return LIB_PATH
 
 

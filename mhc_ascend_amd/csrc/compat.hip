@@ -114,7 +114,7 @@ __global__ __launch_bounds__(256) void dyn_saved_assemble_kernel(
 }  // namespace
 
 hipError_t launch_set_scalars(float* dst, float a, float b, float c, hipStream_t s) {
-    hipLaunchKernelGGL(set_scalars_kernel, dim3(1), dim3(64), 0, s, dst, a, b, c);
+    MHC_LAUNCH_GGL(set_scalars_kernel, dim3(1), dim3(64), 0, s, dst, a, b, c);
     return hipGetLastError();
 }
 
@@ -126,10 +126,10 @@ hipError_t launch_dyn_intermediates(int x_dtype, const void* x, const float* w32
     if (n > 32) return hipErrorInvalidValue;
     const dim3 grid((unsigned)B), block(kInterThreads);
     if (x_dtype == kBF16)
-        hipLaunchKernelGGL(dyn_intermediates_kernel<bf16_t>, grid, block, 0, s, (const bf16_t*)x, w32, coef, rh, n, C,
+        MHC_LAUNCH_GGL(dyn_intermediates_kernel<bf16_t>, grid, block, 0, s, (const bf16_t*)x, w32, coef, rh, n, C,
                            eps, rms, (bf16_t*)x_agg, (bf16_t*)y_norm, (bf16_t*)x_flat, h_pre, h_post, M, rms_h);
     else
-        hipLaunchKernelGGL(dyn_intermediates_kernel<float>, grid, block, 0, s, (const float*)x, w32, coef, rh, n, C,
+        MHC_LAUNCH_GGL(dyn_intermediates_kernel<float>, grid, block, 0, s, (const float*)x, w32, coef, rh, n, C,
                            eps, rms, (bf16_t*)x_agg, (bf16_t*)y_norm, (bf16_t*)x_flat, h_pre, h_post, M, rms_h);
     return hipGetLastError();
 }
@@ -139,7 +139,7 @@ hipError_t launch_dyn_saved_assemble(const float* h_pre, const float* h_post, co
     if (B == 0) return hipSuccess;
     const int64_t total = B * (2 * n + n * n + 1);
     const unsigned blocks = (unsigned)((total + 255) / 256);
-    hipLaunchKernelGGL(dyn_saved_assemble_kernel, dim3(blocks), dim3(256), 0, s, h_pre, h_post, M, rms_h, n, B,
+    MHC_LAUNCH_GGL(dyn_saved_assemble_kernel, dim3(blocks), dim3(256), 0, s, h_pre, h_post, M, rms_h, n, B,
                        coef, rh);
     return hipGetLastError();
 }

@@ -1510,7 +1510,7 @@ hipError_t launch_phi_split(const float* pre, const float* post, const float* re
     const int64_t total = (int64_t)proj_tiles(np) * 2 * (K / 32) * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(phi_split_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pre, post, res, n, np, K,
+    MHC_LAUNCH_GGL(phi_split_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pre, post, res, n, np, K,
                        reinterpret_cast<uint4*>(phib));
     return hipGetLastError();
 }
@@ -1582,12 +1582,12 @@ hipError_t launch_proj_mfma(int x_dtype, const void* x, const bf16_t* phib, int 
     if (x_dtype == kBF16) {
         constexpr int MT = proj_mt<bf16_t>();
         const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks, tiles);
-        hipLaunchKernelGGL((proj_mfma_kernel<bf16_t, MT>), grid, dim3(256), 0, s, (const bf16_t*)x, phif, p_part,
+        MHC_LAUNCH_GGL((proj_mfma_kernel<bf16_t, MT>), grid, dim3(256), 0, s, (const bf16_t*)x, phif, p_part,
                            ss_part, B, K, kchunk);
     } else {
         constexpr int MT = proj_mt<float>();
         const dim3 grid((unsigned)((B + 16 * MT - 1) / (16 * MT)), (unsigned)ks, tiles);
-        hipLaunchKernelGGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, p_part,
+        MHC_LAUNCH_GGL((proj_mfma_kernel<float, MT>), grid, dim3(256), 0, s, (const float*)x, phif, p_part,
                            ss_part, B, K, kchunk);
     }
     timing_end(tok, s);
@@ -1609,17 +1609,17 @@ hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, c
     const int tok = timing_begin("proj", s);
     const bf16_t* xp = reinterpret_cast<const bf16_t*>(x);
     if (x_dtype == kF32) {
-        hipLaunchKernelGGL(proj_xsplit_kernel, dim3((unsigned)(B * ks)), dim3(256), 0, s, (const float*)x,
+        MHC_LAUNCH_GGL(proj_xsplit_kernel, dim3((unsigned)(B * ks)), dim3(256), 0, s, (const float*)x,
                            reinterpret_cast<uint4*>(xplanes), ss_part, B, K, kchunk, ks);
         xp = reinterpret_cast<const bf16_t*>(xplanes);
     }
     const uint4* phif = reinterpret_cast<const uint4*>(phib);
 #define MHC_STREAM(XPL_, MT_)                                                                                   \
     if (phib) {                                                                                                 \
-        hipLaunchKernelGGL((proj_stream_kernel<XPL_, MT_, true>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,   \
+        MHC_LAUNCH_GGL((proj_stream_kernel<XPL_, MT_, true>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,   \
                            phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups);             \
     } else {                                                                                                    \
-        hipLaunchKernelGGL((proj_stream_kernel<XPL_, MT_, false>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,  \
+        MHC_LAUNCH_GGL((proj_stream_kernel<XPL_, MT_, false>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,  \
                            phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups);             \
     }
 #define MHC_STREAM_MT(XPL_)                               \
@@ -1642,7 +1642,7 @@ hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, c
 hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s) {
     const int64_t total = B * np;
     if (total == 0) return hipSuccess;
-    hipLaunchKernelGGL(proj_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, p_part, ks, B, np,
+    MHC_LAUNCH_GGL(proj_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, p_part, ks, B, np,
                        out);
     return hipGetLastError();
 }
@@ -1663,19 +1663,19 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
                                int iters, float sk_eps, float rms_eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (n == 4) {
-        hipLaunchKernelGGL(dyn_coef16_fwd_kernel, dim3((unsigned)((B * 16 + 255) / 256)), dim3(256), 0, s, p_part,
+        MHC_LAUNCH_GGL(dyn_coef16_fwd_kernel, dim3((unsigned)((B * 16 + 255) / 256)), dim3(256), 0, s, p_part,
                            ss_part, ks, B, K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, iters,
                            sk_eps, rms_eps);
         return hipGetLastError();
     }
     if (n == skb::kN) {
-        hipLaunchKernelGGL(dyn_coef32_fwd_kernel, dim3((unsigned)B), dim3(skb::kThreads), 0, s, p_part, ss_part, ks, B,
+        MHC_LAUNCH_GGL(dyn_coef32_fwd_kernel, dim3((unsigned)B), dim3(skb::kThreads), 0, s, p_part, ss_part, ks, B,
                            K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, iters, sk_eps, rms_eps);
         return hipGetLastError();
     }
     const int64_t threads = B * pow2ceil(n);
     const unsigned blocks = (unsigned)((threads + 255) / 256);
-    MHC_DYN_N(n, hipLaunchKernelGGL((dyn_coef_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, p_part, ss_part, ks, B,
+    MHC_DYN_N(n, MHC_LAUNCH_GGL((dyn_coef_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, p_part, ss_part, ks, B,
                                     K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, iters, sk_eps,
                                     rms_eps));
     return hipGetLastError();
@@ -1710,12 +1710,12 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
     if (B == 0) return hipSuccess;
     const unsigned blocks = (unsigned)dyn_coef_bwd_blocks(n, B);
     if (n == 4) {
-        hipLaunchKernelGGL(dyn_coef16_bwd_kernel, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K, a_pre, a_post,
+        MHC_LAUNCH_GGL(dyn_coef16_bwd_kernel, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K, a_pre, a_post,
                            a_res, b_res, dp_out, s_out, part, iters, sk_eps);
         return hipGetLastError();
     }
     if (n == skb::kN && iters <= skb::kTMax) {
-        hipLaunchKernelGGL(dyn_coef32_bwd_kernel, dim3((unsigned)B), dim3(skb::kThreads), 0, s, scal, coef, p, rh, B, K,
+        MHC_LAUNCH_GGL(dyn_coef32_bwd_kernel, dim3((unsigned)B), dim3(skb::kThreads), 0, s, scal, coef, p, rh, B, K,
                            a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
         return hipGetLastError();
     }
@@ -1724,10 +1724,10 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
         if (!hist || slots < 1) return hipErrorInvalidValue;
         const unsigned wblocks = (unsigned)slots * n / 256;
         if (n == 16) {
-            hipLaunchKernelGGL((dyn_coef_bwd_wide_kernel<16>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+            MHC_LAUNCH_GGL((dyn_coef_bwd_wide_kernel<16>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
                                a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps, hist);
         } else if (n == 32) {
-            hipLaunchKernelGGL((dyn_coef_bwd_wide_kernel<32>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+            MHC_LAUNCH_GGL((dyn_coef_bwd_wide_kernel<32>), dim3(wblocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
                                a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps, hist);
         } else {
             return hipErrorInvalidValue;
@@ -1735,9 +1735,9 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
         return hipGetLastError();
     }
     switch (n) {
-        case 2: hipLaunchKernelGGL((dyn_coef_bwd_kernel<2>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+        case 2: MHC_LAUNCH_GGL((dyn_coef_bwd_kernel<2>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
                                    a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps); break;
-        case 8: hipLaunchKernelGGL((dyn_coef_bwd_kernel<8>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+        case 8: MHC_LAUNCH_GGL((dyn_coef_bwd_kernel<8>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
                                    a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps); break;
         default: return hipErrorInvalidValue;
     }
@@ -1746,7 +1746,7 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
 
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s) {
-    hipLaunchKernelGGL(small_column_sum_kernel, dim3((unsigned)((cols + 31) / 32)), dim3(1024), 0, s, part, rows, cols,
+    MHC_LAUNCH_GGL(small_column_sum_kernel, dim3((unsigned)((cols + 31) / 32)), dim3(1024), 0, s, part, rows, cols,
                        out_db, out_da, np);
     return hipGetLastError();
 }
@@ -2339,13 +2339,13 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
         const dim3 gs(8u * ((cblocks + 7) / 8) * tb32);
         const int tk = timing_begin("proj_bwd", s);
         if (s_tok) {
-            hipLaunchKernelGGL((proj_bwd_dx_small_kernel<true, true>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
+            MHC_LAUNCH_GGL((proj_bwd_dx_small_kernel<true, true>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
                                phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
         } else if (accumulate) {
-            hipLaunchKernelGGL((proj_bwd_dx_small_kernel<true, false>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
+            MHC_LAUNCH_GGL((proj_bwd_dx_small_kernel<true, false>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
                                phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
         } else {
-            hipLaunchKernelGGL((proj_bwd_dx_small_kernel<false, false>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
+            MHC_LAUNCH_GGL((proj_bwd_dx_small_kernel<false, false>), gs, dim3(256), 0, s, x, dP, dp_stride, s_tok,
                                phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
         }
         hipError_t e = hipGetLastError();
@@ -2353,7 +2353,7 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
         if (e != hipSuccess) return e;
         const int tg = timing_begin("proj_bwd_dphi", s);
         const unsigned rb = (unsigned)((np + kDphiSmallRows - 1) / kDphiSmallRows);
-        hipLaunchKernelGGL(proj_bwd_dphi_small_kernel, dim3(8u * ((cblocks + 7) / 8) * rb), dim3(256), 0, s, x, dP,
+        MHC_LAUNCH_GGL(proj_bwd_dphi_small_kernel, dim3(8u * ((cblocks + 7) / 8) * rb), dim3(256), 0, s, x, dP,
                            dp_stride, np, dphi, B, K);
         timing_end(tg, s);
         return hipGetLastError();
@@ -2371,20 +2371,20 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
     uint4* xth = reinterpret_cast<uint4*>(sc + 2 * (ws.dp_plane + ws.dpt_plane));
     uint4* xtl = reinterpret_cast<uint4*>(sc + 2 * (ws.dp_plane + ws.dpt_plane) + ws.xt_plane);
     const int64_t pieces = B * (np32 / 8);
-    hipLaunchKernelGGL(dp_split_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, dP, dp_stride, np,
+    MHC_LAUNCH_GGL(dp_split_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s, dP, dp_stride, np,
                        np32, B, dph, dpl);
     // 1-D grid: 8 XCD lanes x ceil(column blocks / 8) x token blocks
     const unsigned tblocks = (unsigned)((B + kDx2Tok - 1) / kDx2Tok);
     const dim3 gdx(8u * ((cblocks + 7) / 8) * tblocks);
     const int tok = timing_begin("proj_bwd", s);
     if (s_tok) {
-        hipLaunchKernelGGL((proj_bwd_dx2_kernel<true, true>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok, phi_pre,
+        MHC_LAUNCH_GGL((proj_bwd_dx2_kernel<true, true>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok, phi_pre,
                            phi_post, phi_res, n_pre, np, dx, B, K);
     } else if (accumulate) {
-        hipLaunchKernelGGL((proj_bwd_dx2_kernel<true, false>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok, phi_pre,
+        MHC_LAUNCH_GGL((proj_bwd_dx2_kernel<true, false>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok, phi_pre,
                            phi_post, phi_res, n_pre, np, dx, B, K);
     } else {
-        hipLaunchKernelGGL((proj_bwd_dx2_kernel<false, false>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok,
+        MHC_LAUNCH_GGL((proj_bwd_dx2_kernel<false, false>), gdx, dim3(256), 0, s, x, dph, dpl, np32, s_tok,
                            phi_pre, phi_post, phi_res, n_pre, np, dx, B, K);
     }
     hipError_t e = hipGetLastError();
@@ -2393,12 +2393,12 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
     const int tg = timing_begin("proj_bwd_dphi", s);
     const int np64 = (np + kDphiRows - 1) / kDphiRows * kDphiRows;
     const int64_t tgroups = (int64_t)np64 * (Bp / 8);
-    hipLaunchKernelGGL(dp_tsplit_kernel, dim3((unsigned)((tgroups + 255) / 256)), dim3(256), 0, s, dP, dp_stride, np,
+    MHC_LAUNCH_GGL(dp_tsplit_kernel, dim3((unsigned)((tgroups + 255) / 256)), dim3(256), 0, s, dP, dp_stride, np,
                        np64, B, Bp, dth, dtl);
-    hipLaunchKernelGGL(x_tsplit_kernel, dim3((unsigned)((K + kXtCols - 1) / kXtCols), (unsigned)(Bp / 32)), dim3(256),
+    MHC_LAUNCH_GGL(x_tsplit_kernel, dim3((unsigned)((K + kXtCols - 1) / kXtCols), (unsigned)(Bp / 32)), dim3(256),
                        0, s, x, B, K, Bp, xth, xtl);
     const unsigned rblocks = (unsigned)((np + kDphiRows - 1) / kDphiRows);
-    hipLaunchKernelGGL(proj_bwd_dphi_kernel, dim3(8u * ((cblocks + 7) / 8) * rblocks), dim3(256), 0, s, dth, dtl, xth,
+    MHC_LAUNCH_GGL(proj_bwd_dphi_kernel, dim3(8u * ((cblocks + 7) / 8) * rblocks), dim3(256), 0, s, dth, dtl, xth,
                        xtl, np, dphi, Bp, K);
     timing_end(tg, s);
     return hipGetLastError();
@@ -2438,7 +2438,7 @@ hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_s
     tile = ((tile + 31) / 32) * 32;
     const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
 #define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \
-    hipLaunchKernelGGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP, dp_stride,  \
+    MHC_LAUNCH_GGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP, dp_stride,  \
                        s_tok, phi_pre, phi_post, phi_res, n_pre, o0, np, (TX_*)dx, dx_step, groups, C, dphi_part, B, K, \
                        tile)
     // The layer backward accumulates (with the r_h term on the first output

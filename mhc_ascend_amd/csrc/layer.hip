@@ -674,22 +674,22 @@ hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, 
     if (C <= 0) return hipSuccess;
     const unsigned blocks = (unsigned)((C + 255) / 256);
     if (w_dtype == kBF16) {
-        hipLaunchKernelGGL(weight_f32_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)w, C, out);
+        MHC_LAUNCH_GGL(weight_f32_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, (const bf16_t*)w, C, out);
     } else {
-        hipLaunchKernelGGL(weight_f32_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)w, C, out);
+        MHC_LAUNCH_GGL(weight_f32_kernel<float>, dim3(blocks), dim3(256), 0, s, (const float*)w, C, out);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_cast_bf16(const float* in, int64_t n, void* out, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(cast_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, n, (bf16_t*)out);
+    MHC_LAUNCH_GGL(cast_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, n, (bf16_t*)out);
     return hipGetLastError();
 }
 
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+    MHC_LAUNCH_GGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
     return hipGetLastError();
 }
 
@@ -728,11 +728,11 @@ hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, co
     const int off = saved_w_offset(n);
     const unsigned blocks = 1 + (unsigned)((C + 2047) / 2048);
     if (w_dtype == kBF16) {
-        MHC_COEF_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, bf16_t>), dim3(blocks), dim3(256), 0, s,
+        MHC_COEF_N(n, MHC_LAUNCH_GGL((static_coef_kernel<N_, bf16_t>), dim3(blocks), dim3(256), 0, s,
                                          h_pre, h_post, h_res, (const bf16_t*)weight, (int)C, saved, off, iters,
                                          sk_eps));
     } else {
-        MHC_COEF_N(n, hipLaunchKernelGGL((static_coef_kernel<N_, float>), dim3(blocks), dim3(256), 0, s,
+        MHC_COEF_N(n, MHC_LAUNCH_GGL((static_coef_kernel<N_, float>), dim3(blocks), dim3(256), 0, s,
                                          h_pre, h_post, h_res, (const float*)weight, (int)C, saved, off, iters,
                                          sk_eps));
     }
@@ -847,7 +847,7 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
     void* args[] = {(void*)&x, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&out, (void*)&rms_out,
                     (void*)&B, (void*)&Ci, (void*)&eps};
     const int tok = timing_begin("layer_fwd", s);
-    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
+    hipError_t e = mhc_launch_kernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
     return e != hipSuccess ? e : hipGetLastError();
 }
@@ -900,7 +900,7 @@ hipError_t launch_layer_static_fwd(int x_dtype, int n, const void* x, const void
                     (void*)&w_off, (void*)&iters, (void*)&sk_eps, (void*)&out, (void*)&rms_out, (void*)&B,
                     (void*)&Ci, (void*)&eps};
     const int tok = timing_begin("layer_fwd", s);
-    hipError_t e = hipLaunchKernel(fn, dim3((unsigned)B), dim3(t.threads), args, 0, s);
+    hipError_t e = mhc_launch_kernel(fn, dim3((unsigned)B), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
     return e != hipSuccess ? e : hipGetLastError();
 }
@@ -950,7 +950,7 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
     void* args[] = {(void*)&g, (void*)&x, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&dx,
                     (void*)&dw_part, (void*)&scal_out, (void*)&dx_step, (void*)&B, (void*)&Ci, (void*)&eps};
     const int tok = timing_begin(mode == 0 ? "layer_bwd" : "layer_bwd_reduce", s);
-    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
+    hipError_t e = mhc_launch_kernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
     return e != hipSuccess ? e : hipGetLastError();
 }
@@ -959,10 +959,10 @@ hipError_t launch_column_partial(const float* part, int rows, int64_t cols, floa
                                  hipStream_t s) {
     if (cols == 0) return hipSuccess;
     if (cols % 4 != 0) {
-        hipLaunchKernelGGL(column_partial1_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
+        MHC_LAUNCH_GGL(column_partial1_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
                            rows, cols, stage);
     } else {
-        hipLaunchKernelGGL(column_partial_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
+        MHC_LAUNCH_GGL(column_partial_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
                            rows, cols, stage);
     }
     return hipGetLastError();
@@ -982,7 +982,7 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
     if (blocks == 0) return hipSuccess;
     const unsigned threads = 256;
 #define MHC_FIN_LAUNCH(N_, TW_)                                                                                  \
-    hipLaunchKernelGGL((layer_finalize_kernel<N_, TW_>), dim3(blocks), dim3(threads), 0, s, stage, rsplit, cols,  \
+    MHC_LAUNCH_GGL((layer_finalize_kernel<N_, TW_>), dim3(blocks), dim3(threads), 0, s, stage, rsplit, cols,  \
                        (TW_*)dw, scal_part, rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, \
                        phases)
     if (n == 0) {

@@ -3,6 +3,9 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#ifdef MHC_KERNEL_TIMING
+#include <hip/hip_ext.h>
+#endif
 #include <stdint.h>
 #include <stddef.h>
 
@@ -31,10 +34,45 @@ inline RowTiling with_min_threads(RowTiling t, int need) {
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
-// Optional per-kernel timing on the launch stream (see mhc_timing_* in the
-// public header).  `begin` returns a token passed to `end`.
+// Per-kernel timing, compiled in only for the benchmark's build of the
+// library (MHC_KERNEL_TIMING, libmhc_hip_timed.so; include/mhc_hip_timing.h).
+// timing_begin(name) opens a scope (returning a token for timing_end) in
+// which every launch goes through hipExtLaunchKernel with the scope's
+// events: the first launch's dispatch records the start, each launch's end
+// the stop, so the scope measures its kernels' own begin-to-end time (event
+// markers between launches would also count the queue around them).  All
+// launches go through MHC_LAUNCH_GGL / mhc_launch_kernel, which are plain
+// hipLaunchKernelGGL / hipLaunchKernel in the product build, where the
+// scope functions are empty and the library has no timing state.
+#ifdef MHC_KERNEL_TIMING
 int timing_begin(const char* name, hipStream_t s);
 void timing_end(int token, hipStream_t s);
+struct TimingScope {
+    hipEvent_t start;
+    hipEvent_t stop;
+    bool first;
+};
+TimingScope* timing_scope();  // the calling thread's open scope, or null
+hipError_t mhc_launch_kernel(const void* fn, dim3 grid, dim3 block, void** args, size_t shm, hipStream_t s);
+#define MHC_LAUNCH_GGL(kernel, grid, block, shm, stream, ...)                                                \
+    do {                                                                                                     \
+        ::mhc::TimingScope* mhc_ts_ = ::mhc::timing_scope();                                                 \
+        if (mhc_ts_) {                                                                                       \
+            hipExtLaunchKernelGGL(kernel, grid, block, shm, stream, mhc_ts_->first ? mhc_ts_->start : nullptr, \
+                                  mhc_ts_->stop, 0, __VA_ARGS__);                                            \
+            mhc_ts_->first = false;                                                                          \
+        } else {                                                                                             \
+            hipLaunchKernelGGL(kernel, grid, block, shm, stream, __VA_ARGS__);                               \
+        }                                                                                                    \
+    } while (0)
+#else
+inline int timing_begin(const char*, hipStream_t) { return -1; }
+inline void timing_end(int, hipStream_t) {}
+inline hipError_t mhc_launch_kernel(const void* fn, dim3 grid, dim3 block, void** args, size_t shm, hipStream_t s) {
+    return hipLaunchKernel(fn, grid, block, args, shm, s);
+}
+#define MHC_LAUNCH_GGL hipLaunchKernelGGL
+#endif
 
 // ---- layer.hip -------------------------------------------------------------
 // saved = [coef (2n + n^2) | pad | fp32 weight (C)], weight at saved_w_offset(n) floats

@@ -372,7 +372,7 @@ hipError_t launch_rmsnorm_fwd(int dt, const void* x, const float* w, void* y, fl
         timing_end(tok, s);
         return e;
     }
-    MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 1, T_, hipLaunchKernelGGL((rmsnorm_fwd_kernel<T_, V_>), dim3(B), dim3(t.threads),
+    MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 1, T_, MHC_LAUNCH_GGL((rmsnorm_fwd_kernel<T_, V_>), dim3(B), dim3(t.threads),
                                                                0, s, (const T_*)x, w, (T_*)y, rms, (int)C, eps)));
     timing_end(tok, s);
     return hipGetLastError();
@@ -395,7 +395,7 @@ hipError_t launch_rmsnorm_bwd(int dt, const void* g, const void* x, const float*
         timing_end(tok, s);
         return e;
     }
-    MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 2, T_, hipLaunchKernelGGL((rmsnorm_bwd_kernel<T_, V_>), dim3(grid),
+    MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 2, T_, MHC_LAUNCH_GGL((rmsnorm_bwd_kernel<T_, V_>), dim3(grid),
                                                                dim3(t.threads), 0, s, (const T_*)g, (const T_*)x, w,
                                                                rms, (T_*)gx, dw_part, B, (int)C)));
     timing_end(tok, s);
@@ -406,7 +406,7 @@ hipError_t launch_compute_rms(int dt, const void* x, float* rms, int64_t B, int6
     if (B == 0) return hipSuccess;
     const RowTiling t = choose_row_tiling(K, dt == kBF16 ? 8 : 4, 1);
     if (t.vpt <= 0) return launch_wide_compute_rms(dt, x, rms, B, K, eps, s);
-    MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 1, T_, hipLaunchKernelGGL((compute_rms_kernel<T_, V_>), dim3(B),
+    MHC_OPS_T(dt, MHC_OPS_VPT(t.vpt, 1, T_, MHC_LAUNCH_GGL((compute_rms_kernel<T_, V_>), dim3(B),
                                                                dim3(t.threads), 0, s, (const T_*)x, rms, (int)K,
                                                                eps)));
     return hipGetLastError();
@@ -431,7 +431,7 @@ hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, in
         timing_end(tok, s);
         return e;
     }
-    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, hipLaunchKernelGGL((aggregate_fwd_kernel<T_, N_, V_>),
+    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, MHC_LAUNCH_GGL((aggregate_fwd_kernel<T_, N_, V_>),
                                                                                  dim3(B), dim3(t.threads), 0, s,
                                                                                  (const T_*)x, H, hs, (T_*)out, h_act,
                                                                                  (int)C))));
@@ -449,7 +449,7 @@ hipError_t launch_aggregate_bwd(int dt, int n, const void* g, const void* x, con
         timing_end(tok, s);
         return e;
     }
-    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, hipLaunchKernelGGL((aggregate_bwd_kernel<T_, N_, V_>),
+    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, MHC_LAUNCH_GGL((aggregate_bwd_kernel<T_, N_, V_>),
                                                                                  dim3(B), dim3(t.threads), 0, s,
                                                                                  (const T_*)g, (const T_*)x, h_act, hs,
                                                                                  (T_*)gx, gh_act, gh_raw, (int)C))));
@@ -468,7 +468,7 @@ hipError_t launch_distribute_fwd(int dt, int n, const void* y, const float* H, i
         timing_end(tok, s);
         return e;
     }
-    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, hipLaunchKernelGGL((distribute_fwd_kernel<T_, N_, V_>),
+    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, MHC_LAUNCH_GGL((distribute_fwd_kernel<T_, N_, V_>),
                                                                                  dim3(B), dim3(t.threads), 0, s,
                                                                                  (const T_*)y, H, hs, M, ms,
                                                                                  (const T_*)x, out, h_act, (int)C))));
@@ -491,7 +491,7 @@ hipError_t launch_distribute_bwd(int dt, int n, const float* g, const void* x, c
         return e;
     }
     MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, 2 * N_ + 1, T_,
-                                           hipLaunchKernelGGL((distribute_bwd_kernel<T_, N_, V_>), dim3(B),
+                                           MHC_LAUNCH_GGL((distribute_bwd_kernel<T_, N_, V_>), dim3(B),
                                                               dim3(t.threads), 0, s, g, (const T_*)x, (const T_*)y, M,
                                                               ms, h_act, hs, (T_*)gx, (T_*)gy, gM, gh_act, gh_raw,
                                                               (int)C))));

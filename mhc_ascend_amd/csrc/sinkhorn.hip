@@ -185,13 +185,13 @@ hipError_t launch_sinkhorn_fwd(int n, const float* inp, float* out, int64_t batc
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     const int tok = timing_begin("sinkhorn_fwd", s);
     if (n == 4 && batch < kSk16MaxBatch) {
-        hipLaunchKernelGGL(sinkhorn16_fwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s, inp, out,
+        MHC_LAUNCH_GGL(sinkhorn16_fwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s, inp, out,
                            batch, iters, eps);
     } else if (n > 8) {
-        MHC_SK_WIDE(n, hipLaunchKernelGGL((sinkhorn_wide_fwd_kernel<NM_>), dim3(blocks), dim3(256), 0, s, inp, out, n,
+        MHC_SK_WIDE(n, MHC_LAUNCH_GGL((sinkhorn_wide_fwd_kernel<NM_>), dim3(blocks), dim3(256), 0, s, inp, out, n,
                                           batch, iters, eps));
     } else {
-        MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, inp, out,
+        MHC_SK_DISPATCH(n, MHC_LAUNCH_GGL((sinkhorn_fwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, inp, out,
                                               batch, iters, eps));
     }
     timing_end(tok, s);
@@ -206,13 +206,13 @@ hipError_t launch_sinkhorn_bwd(int n, const float* grad_out, const float* inp, f
     const unsigned blocks = (unsigned)((threads + 255) / 256);
     const int tok = timing_begin("sinkhorn_bwd", s);
     if (n == 4 && batch < kSk16MaxBatch) {
-        hipLaunchKernelGGL(sinkhorn16_bwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s,
+        MHC_LAUNCH_GGL(sinkhorn16_bwd_kernel, dim3((unsigned)((batch * 16 + 255) / 256)), dim3(256), 0, s,
                            grad_out, inp, grad_inp, batch, iters, eps);
     } else if (n > 8) {
-        MHC_SK_WIDE(n, hipLaunchKernelGGL((sinkhorn_wide_bwd_kernel<NM_>), dim3(blocks), dim3(256), 0, s, grad_out,
+        MHC_SK_WIDE(n, MHC_LAUNCH_GGL((sinkhorn_wide_bwd_kernel<NM_>), dim3(blocks), dim3(256), 0, s, grad_out,
                                           inp, grad_inp, n, batch, iters, eps));
     } else {
-        MHC_SK_DISPATCH(n, hipLaunchKernelGGL((sinkhorn_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, grad_out,
+        MHC_SK_DISPATCH(n, MHC_LAUNCH_GGL((sinkhorn_bwd_kernel<N_>), dim3(blocks), dim3(256), 0, s, grad_out,
                                               inp, grad_inp, batch, iters, eps));
     }
     timing_end(tok, s);

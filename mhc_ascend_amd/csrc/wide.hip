@@ -962,16 +962,16 @@ hipError_t launch_wide_fwd(int x_dtype, int out_dtype, int n, const void* x, con
 #define MHC_WIDE_FWD(TX_, TO_)                                                                                      \
     MHC_WIDE_N(n, if (split) {                                                                                      \
         if (parts) {                                                                                                \
-            hipLaunchKernelGGL((wide_fwd_part_kernel<TX_, N_>), ogrid, oblock, 0, s, (const TX_*)x, coef,          \
+            MHC_LAUNCH_GGL((wide_fwd_part_kernel<TX_, N_>), ogrid, oblock, 0, s, (const TX_*)x, coef,          \
                                coef_stride, rms_out, B, Ci);                                                        \
         } else {                                                                                                    \
-            hipLaunchKernelGGL((wide_fwd_rms_kernel<TX_, N_>), grid, block, 0, s, (const TX_*)x, coef, coef_stride,\
+            MHC_LAUNCH_GGL((wide_fwd_rms_kernel<TX_, N_>), grid, block, 0, s, (const TX_*)x, coef, coef_stride,\
                                rms_out, B, Ci, eps);                                                                \
         }                                                                                                           \
-        hipLaunchKernelGGL((wide_fwd_out_kernel<TX_, TO_, N_>), ogrid, oblock, 0, s, (const TX_*)x, w, coef,       \
+        MHC_LAUNCH_GGL((wide_fwd_out_kernel<TX_, TO_, N_>), ogrid, oblock, 0, s, (const TX_*)x, w, coef,       \
                            coef_stride, (TO_*)out, (const float*)rms_out, S, B, Ci, eps);                          \
     } else {                                                                                                        \
-        hipLaunchKernelGGL((wide_fwd_kernel<TX_, TO_, N_>), grid, block, 0, s, (const TX_*)x, w, coef, coef_stride, \
+        MHC_LAUNCH_GGL((wide_fwd_kernel<TX_, TO_, N_>), grid, block, 0, s, (const TX_*)x, w, coef, coef_stride, \
                            (TO_*)out, rms_out, B, Ci, eps);                                                         \
     })
     if (x_dtype == kBF16) {
@@ -1047,9 +1047,9 @@ hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const v
         const dim3 cgrid((unsigned)(B * S));
 #define MHC_WIDE_BWD2(TX_, M_)                                                                                     \
     MHC_WIDE_N(n, {                                                                                                 \
-        hipLaunchKernelGGL((wide_bwd_sums_kernel<TX_, N_, (N_ <= 8)>), cgrid, dim3(kWideThreads), 0, s, g,          \
+        MHC_LAUNCH_GGL((wide_bwd_sums_kernel<TX_, N_, (N_ <= 8)>), cgrid, dim3(kWideThreads), 0, s, g,          \
                            (const TX_*)x, w, coef, coef_stride, scratch, B, Ci, S, chunk);                          \
-        hipLaunchKernelGGL((wide_bwd_out_kernel<TX_, N_, M_, (N_ <= 8)>), cgrid, dim3(kWideThreads), 0, s, g,       \
+        MHC_LAUNCH_GGL((wide_bwd_out_kernel<TX_, N_, M_, (N_ <= 8)>), cgrid, dim3(kWideThreads), 0, s, g,       \
                            (const TX_*)x, w, coef, coef_stride, (TX_*)dx, dw_part, scal_out, scratch, B, Ci, eps,  \
                            S, chunk);                                                                               \
     })
@@ -1062,7 +1062,7 @@ hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const v
     } else {
         const size_t lds = (size_t)C * sizeof(float);
 #define MHC_WIDE_BWD(TX_, M_)                                                                                      \
-    MHC_WIDE_N(n, hipLaunchKernelGGL((wide_bwd_kernel<TX_, N_, M_, (N_ <= 8)>), dim3(grid), dim3(kWideThreads), lds, \
+    MHC_WIDE_N(n, MHC_LAUNCH_GGL((wide_bwd_kernel<TX_, N_, M_, (N_ <= 8)>), dim3(grid), dim3(kWideThreads), lds, \
                                      s, g, (const TX_*)x, w, coef, coef_stride, (TX_*)dx, dw_part, scal_out, B, Ci,  \
                                      eps))
         if (x_dtype == kBF16) {
@@ -1082,18 +1082,18 @@ hipError_t launch_wide_bwd(int x_dtype, int n, int mode, const float* g, const v
 #define MHC_GRAM(TX_, M_)                                                                                         \
     if (n == 16) {                                                                                                \
         if (vec) {                                                                                                \
-            hipLaunchKernelGGL((stream_gram_kernel<TX_, 16, M_, true>), ggrid, dim3(kWideThreads), 0, s, g,       \
+            MHC_LAUNCH_GGL((stream_gram_kernel<TX_, 16, M_, true>), ggrid, dim3(kWideThreads), 0, s, g,       \
                                (const TX_*)x, scal_out, B, Ci, (int64_t)(16 * 16 + 2 * 16 + 2));                 \
         } else {                                                                                                  \
-            hipLaunchKernelGGL((stream_gram_kernel<TX_, 16, M_, false>), ggrid, dim3(kWideThreads), 0, s, g,      \
+            MHC_LAUNCH_GGL((stream_gram_kernel<TX_, 16, M_, false>), ggrid, dim3(kWideThreads), 0, s, g,      \
                                (const TX_*)x, scal_out, B, Ci, (int64_t)(16 * 16 + 2 * 16 + 2));                 \
         }                                                                                                         \
     } else {                                                                                                      \
         if (vec) {                                                                                                \
-            hipLaunchKernelGGL((stream_gram_kernel<TX_, 32, M_, true>), ggrid, dim3(kWideThreads), 0, s, g,       \
+            MHC_LAUNCH_GGL((stream_gram_kernel<TX_, 32, M_, true>), ggrid, dim3(kWideThreads), 0, s, g,       \
                                (const TX_*)x, scal_out, B, Ci, (int64_t)(32 * 32 + 2 * 32 + 2));                 \
         } else {                                                                                                  \
-            hipLaunchKernelGGL((stream_gram_kernel<TX_, 32, M_, false>), ggrid, dim3(kWideThreads), 0, s, g,      \
+            MHC_LAUNCH_GGL((stream_gram_kernel<TX_, 32, M_, false>), ggrid, dim3(kWideThreads), 0, s, g,      \
                                (const TX_*)x, scal_out, B, Ci, (int64_t)(32 * 32 + 2 * 32 + 2));                 \
         }                                                                                                         \
     }
@@ -1133,7 +1133,7 @@ hipError_t launch_wide_rmsnorm_fwd(int dt, const void* x, const float* w, void* 
                                    float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
-    MHC_WIDE_T(dt, hipLaunchKernelGGL((wide_rmsnorm_fwd_kernel<T_>), dim3((unsigned)B), dim3(kWideThreads), 0, s,
+    MHC_WIDE_T(dt, MHC_LAUNCH_GGL((wide_rmsnorm_fwd_kernel<T_>), dim3((unsigned)B), dim3(kWideThreads), 0, s,
                                       (const T_*)x, w, (T_*)y, rms, (int)C, eps));
     return hipGetLastError();
 }
@@ -1158,7 +1158,7 @@ hipError_t launch_wide_rmsnorm_bwd(int dt, const void* g, const void* x, const f
                                    float* dw_part, int grid, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (grid < 1 || C < 1 || C > kWideMaxC) return hipErrorInvalidValue;
-    MHC_WIDE_T(dt, hipLaunchKernelGGL((wide_rmsnorm_bwd_kernel<T_>), dim3(grid), dim3(kWideThreads),
+    MHC_WIDE_T(dt, MHC_LAUNCH_GGL((wide_rmsnorm_bwd_kernel<T_>), dim3(grid), dim3(kWideThreads),
                                       (size_t)C * sizeof(float), s, (const T_*)g, (const T_*)x, w, rms, (T_*)gx,
                                       dw_part, B, (int)C));
     return hipGetLastError();
@@ -1168,7 +1168,7 @@ hipError_t launch_wide_compute_rms(int dt, const void* x, float* rms, int64_t B,
                                    hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!grid_ok(B) || K < 1) return hipErrorInvalidValue;
-    MHC_WIDE_T(dt, hipLaunchKernelGGL((wide_compute_rms_kernel<T_>), dim3((unsigned)B), dim3(kWideThreads), 0, s,
+    MHC_WIDE_T(dt, MHC_LAUNCH_GGL((wide_compute_rms_kernel<T_>), dim3((unsigned)B), dim3(kWideThreads), 0, s,
                                       (const T_*)x, rms, K, eps));
     return hipGetLastError();
 }
@@ -1177,7 +1177,7 @@ hipError_t launch_wide_aggregate_fwd(int dt, int n, const void* x, const float* 
                                      float* h_act, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
-    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_aggregate_fwd_kernel<T_, N_>), dim3((unsigned)B),
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, MHC_LAUNCH_GGL((wide_aggregate_fwd_kernel<T_, N_>), dim3((unsigned)B),
                                                         dim3(kWideThreads), 0, s, (const T_*)x, H, hs, (T_*)out,
                                                         h_act, (int)C)));
     return hipGetLastError();
@@ -1187,7 +1187,7 @@ hipError_t launch_wide_aggregate_bwd(int dt, int n, const void* g, const void* x
                                      void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
-    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_aggregate_bwd_kernel<T_, N_>), dim3((unsigned)B),
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, MHC_LAUNCH_GGL((wide_aggregate_bwd_kernel<T_, N_>), dim3((unsigned)B),
                                                         dim3(kWideThreads), 0, s, (const T_*)g, (const T_*)x, h_act,
                                                         hs, (T_*)gx, gh_act, gh_raw, (int)C)));
     return hipGetLastError();
@@ -1198,7 +1198,7 @@ hipError_t launch_wide_distribute_fwd(int dt, int n, const void* y, const float*
                                       hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
-    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_distribute_fwd_kernel<T_, N_>), dim3((unsigned)B),
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, MHC_LAUNCH_GGL((wide_distribute_fwd_kernel<T_, N_>), dim3((unsigned)B),
                                                         dim3(kWideThreads), 0, s, (const T_*)y, H, hs, M, ms,
                                                         (const T_*)x, out, h_act, (int)C)));
     return hipGetLastError();
@@ -1209,7 +1209,7 @@ hipError_t launch_wide_distribute_bwd(int dt, int n, const float* g, const void*
                                       float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (!grid_ok(B) || C < 1 || C > 0x7fffffff) return hipErrorInvalidValue;
-    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, hipLaunchKernelGGL((wide_distribute_bwd_kernel<T_, N_, (N_ <= 8)>),
+    MHC_WIDE_T(dt, MHC_WIDE_OPS_N(n, MHC_LAUNCH_GGL((wide_distribute_bwd_kernel<T_, N_, (N_ <= 8)>),
                                                         dim3((unsigned)B), dim3(kWideThreads), 0, s, g,
                                                         (const T_*)x, (const T_*)y, M, ms, h_act, hs, (T_*)gx,
                                                         (T_*)gy, gM, gh_act, gh_raw, (int)C)));
@@ -1219,18 +1219,18 @@ hipError_t launch_wide_distribute_bwd(int dt, int n, const float* g, const void*
     const bool vec = C % 8 == 0 && ((uintptr_t)g % 16) == 0 && ((uintptr_t)x % 16) == 0;
     MHC_WIDE_T(dt, if (n == 16) {
         if (vec) {
-            hipLaunchKernelGGL((stream_gram_kernel<T_, 16, 1, true>), ggrid, dim3(kWideThreads), 0, s, g,
+            MHC_LAUNCH_GGL((stream_gram_kernel<T_, 16, 1, true>), ggrid, dim3(kWideThreads), 0, s, g,
                                (const T_*)x, gM, B, (int)C, (int64_t)(16 * 16));
         } else {
-            hipLaunchKernelGGL((stream_gram_kernel<T_, 16, 1, false>), ggrid, dim3(kWideThreads), 0, s, g,
+            MHC_LAUNCH_GGL((stream_gram_kernel<T_, 16, 1, false>), ggrid, dim3(kWideThreads), 0, s, g,
                                (const T_*)x, gM, B, (int)C, (int64_t)(16 * 16));
         }
     } else {
         if (vec) {
-            hipLaunchKernelGGL((stream_gram_kernel<T_, 32, 1, true>), ggrid, dim3(kWideThreads), 0, s, g,
+            MHC_LAUNCH_GGL((stream_gram_kernel<T_, 32, 1, true>), ggrid, dim3(kWideThreads), 0, s, g,
                                (const T_*)x, gM, B, (int)C, (int64_t)(32 * 32));
         } else {
-            hipLaunchKernelGGL((stream_gram_kernel<T_, 32, 1, false>), ggrid, dim3(kWideThreads), 0, s, g,
+            MHC_LAUNCH_GGL((stream_gram_kernel<T_, 32, 1, false>), ggrid, dim3(kWideThreads), 0, s, g,
                                (const T_*)x, gM, B, (int)C, (int64_t)(32 * 32));
         }
     });
@@ -1244,10 +1244,10 @@ hipError_t launch_wide_static_finalize(int n, const float* scal_part, int rows, 
     // the history when it fits, else the recomputing adjoint
     if ((size_t)(iters > 0 ? iters : 0) * (n + 1) * n * sizeof(float) > hist_bytes) hist = nullptr;
     if (n == 16) {
-        hipLaunchKernelGGL((wide_static_finalize_kernel<16>), dim3(1), dim3(kStaticFinalizeThreads), 0, s, scal_part, rows, h_pre, h_post,
+        MHC_LAUNCH_GGL((wide_static_finalize_kernel<16>), dim3(1), dim3(kStaticFinalizeThreads), 0, s, scal_part, rows, h_pre, h_post,
                            h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, hist);
     } else if (n == 32) {
-        hipLaunchKernelGGL((wide_static_finalize_kernel<32>), dim3(1), dim3(kStaticFinalizeThreads), 0, s, scal_part, rows, h_pre, h_post,
+        MHC_LAUNCH_GGL((wide_static_finalize_kernel<32>), dim3(1), dim3(kStaticFinalizeThreads), 0, s, scal_part, rows, h_pre, h_post,
                            h_res, d_h_pre, d_h_post, d_h_res, iters, sk_eps, hist);
     } else {
         return hipErrorInvalidValue;

@@ -1143,7 +1143,7 @@ hipError_t launch_wrap_fwd(int dt, int n, bool decay, const void* res, const voi
     void* args[] = {(void*)&res, (void*)&br, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&out, (void*)&B,
                     (void*)&Ci, (void*)&eps};
     const int tok = timing_begin("wrap_fwd", s);
-    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
+    hipError_t e = mhc_launch_kernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
     return e != hipSuccess ? e : hipGetLastError();
 }
@@ -1175,7 +1175,7 @@ hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, 
                     (void*)&dbr, (void*)&dw_part, (void*)&scal_out, (void*)&d_step, (void*)&B, (void*)&Ci,
                     (void*)&eps};
     const int tok = timing_begin(mode == 0 ? "wrap_bwd" : "wrap_bwd_reduce", s);
-    hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
+    hipError_t e = mhc_launch_kernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
     return e != hipSuccess ? e : hipGetLastError();
 }
@@ -1199,7 +1199,7 @@ hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const vo
     const uint4* phif = reinterpret_cast<const uint4*>(phib);
     const int tok = timing_begin("wrap_proj", s);
 #define MHC_WP(TX_, D_)                                                                                          \
-    hipLaunchKernelGGL((wrap_proj_kernel<TX_, 4, D_>),                                                           \
+    MHC_LAUNCH_GGL((wrap_proj_kernel<TX_, 4, D_>),                                                           \
                        dim3((unsigned)((B + 16 * wproj_mt<TX_>() - 1) / (16 * wproj_mt<TX_>())), (unsigned)ks),   \
                        dim3(256), 0, s, (const TX_*)res, (const TX_*)br, phif, p_part, ss_part, B, (int)C, cchunk)
     if (dt == kBF16) {
@@ -1243,7 +1243,7 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, cons
     const dim3 grid((unsigned)((C + 127) / 128), (unsigned)tiles);
     const int tok = timing_begin("wrap_proj_bwd", s);
 #define MHC_WPB(TX_, D_)                                                                                          \
-    hipLaunchKernelGGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(512), 0, s, (const TX_*)res, (const TX_*)br, \
+    MHC_LAUNCH_GGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(512), 0, s, (const TX_*)res, (const TX_*)br, \
                        dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, d_step, groups, dphi_part, B,  \
                        (int)C, tile)
     if (dt == kBF16) {

@@ -140,36 +140,13 @@ def compute_rms(x_flat: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
 # Fused static-H layer (layer.py:142-170 as one HBM pass per direction)
 # =============================================================================
 
-class MHCLayerStaticFunction(torch.autograd.Function):
-    """Static-H mHC layer: aggregate -> RMSNorm -> distribute-mix-add with
-    shared H (one Sinkhorn per call instead of one per token)."""
-
-    @staticmethod
-    def forward(ctx, x, rmsnorm_weight, H_pre, H_post, H_res, num_iters: int, sinkhorn_eps: float,
-                rmsnorm_eps: float):
-        out, _rms, saved = native.mhc_layer_static_fwd(x, rmsnorm_weight, H_pre, H_post, H_res, num_iters,
-                                                       sinkhorn_eps, rmsnorm_eps)
-        ctx.save_for_backward(x, rmsnorm_weight, H_pre, H_post, H_res, saved)
-        ctx.cfg = (num_iters, sinkhorn_eps, rmsnorm_eps)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        x, w, hp, hq, hr, saved = ctx.saved_tensors
-        gx, gw, ghp, ghq, ghr = native.mhc_layer_static_bwd(grad_out, x, w, hp, hq, hr, saved, *ctx.cfg)
-        return gx.to(x.dtype), gw, ghp.view_as(hp), ghq.view_as(hq), ghr.view_as(hr), None, None, None
-
-
 def mhc_layer_static(x: torch.Tensor, rmsnorm_weight: torch.Tensor, H_pre: torch.Tensor, H_post: torch.Tensor,
                      H_res: torch.Tensor, sinkhorn_iters: int = 20, sinkhorn_eps: float = 1e-8,
                      rmsnorm_eps: float = 1e-5) -> torch.Tensor:
-    """Static-H mHC layer on x [B, n, C] -> fp32 [B, n, C]."""
-    ag = _lib.autograd()
-    if ag is not None:
-        return ag.static_layer(x, rmsnorm_weight, H_pre, H_post, H_res, int(sinkhorn_iters), float(sinkhorn_eps),
-                               float(rmsnorm_eps))
-    return MHCLayerStaticFunction.apply(x, rmsnorm_weight, H_pre, H_post, H_res, sinkhorn_iters, sinkhorn_eps,
-                                        rmsnorm_eps)
+    """Static-H mHC layer on x [B, n, C] -> fp32 [B, n, C]: one fused pass per
+    direction (layer.py:142-170), autograd node in C++ (_mhc_autograd.so)."""
+    return _lib.autograd().static_layer(x, rmsnorm_weight, H_pre, H_post, H_res, int(sinkhorn_iters),
+                                        float(sinkhorn_eps), float(rmsnorm_eps))
 
 
 # =============================================================================
@@ -224,32 +201,6 @@ def mhc_layer_fused_dynamic_inference(x_expanded, rmsnorm_weight, phi_pre, phi_p
                                           sinkhorn_iters, sinkhorn_eps, rmsnorm_eps, out_dtype)
 
 
-class MHCLayerDynamicFunction(torch.autograd.Function):
-    """Fused dynamic-H layer: projection -> per-token H -> aggregate ->
-    RMSNorm -> distribute-mix-add, and its backward (ops.py:387-564)."""
-
-    @staticmethod
-    def forward(ctx, x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post, alpha_res, b_pre,
-                b_post, b_res, sinkhorn_iters: int, sinkhorn_eps: float, rmsnorm_eps: float):
-        out, saved = native.mhc_layer_dynamic_fwd(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
-                                                  alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters,
-                                                  sinkhorn_eps, rmsnorm_eps)
-        ctx.save_for_backward(x_expanded, rmsnorm_weight, saved, phi_pre, phi_post, phi_res, alpha_pre, alpha_post,
-                              alpha_res, b_pre, b_post, b_res)
-        ctx.cfg = (sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_output):
-        (x, w, saved, phi_pre, phi_post, phi_res, a_pre, a_post, a_res, b_pre, b_post, b_res) = ctx.saved_tensors
-        grads = native.mhc_layer_dynamic_bwd(grad_output, x, w, saved, phi_pre, phi_post, phi_res, a_pre, a_post,
-                                             a_res, b_pre, b_post, b_res, *ctx.cfg)
-        gx, gw, gpp, gpq, gpr, gap, gaq, gar, gbp, gbq, gbr = grads
-        return (gx.to(x.dtype), gw, gpp.view_as(phi_pre), gpq.view_as(phi_post), gpr.view_as(phi_res),
-                gap.view_as(a_pre), gaq.view_as(a_post), gar.view_as(a_res), gbp.view_as(b_pre),
-                gbq.view_as(b_post), gbr.view_as(b_res), None, None, None)
-
-
 def mhc_layer_fused_dynamic_training(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post,
                                      alpha_res, b_pre, b_post, b_res, sinkhorn_iters: int = 20,
                                      sinkhorn_eps: float = 1e-8, rmsnorm_eps: float = 1e-5) -> torch.Tensor:
@@ -262,68 +213,14 @@ def mhc_layer_fused_dynamic_training(x_expanded, rmsnorm_weight, phi_pre, phi_po
         alpha_post = torch.tensor(alpha_post, device=dev, dtype=torch.float32)
     if not torch.is_tensor(alpha_res):
         alpha_res = torch.tensor(alpha_res, device=dev, dtype=torch.float32)
-    ag = _lib.autograd()
-    if ag is not None:
-        return ag.dynamic_layer(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post,
-                                alpha_res, b_pre, b_post, b_res, int(sinkhorn_iters), float(sinkhorn_eps),
-                                float(rmsnorm_eps))
-    return MHCLayerDynamicFunction.apply(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
-                                         alpha_post, alpha_res, b_pre, b_post, b_res, sinkhorn_iters, sinkhorn_eps,
-                                         rmsnorm_eps)
+    return _lib.autograd().dynamic_layer(x_expanded, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre,
+                                         alpha_post, alpha_res, b_pre, b_post, b_res, int(sinkhorn_iters),
+                                         float(sinkhorn_eps), float(rmsnorm_eps))
 
 
 # =============================================================================
 # Fused MHCResidualWrapper (layer.py:269-322)
 # =============================================================================
-
-class MHCWrapperDynamicFunction(torch.autograd.Function):
-    """Stream synthesis -> dynamic-H layer -> stream mean, fused: the
-    [tokens, n, C] stream tensor and the layer output are never materialised."""
-
-    @staticmethod
-    def forward(ctx, residual, branch, rmsnorm_weight, phi_pre, phi_post, phi_res, alpha_pre, alpha_post, alpha_res,
-                b_pre, b_post, b_res, residual_mode: str, n: int, sinkhorn_iters: int, sinkhorn_eps: float,
-                rmsnorm_eps: float):
-        out, saved = native.wrapper_dynamic_fwd(residual, branch, residual_mode, n, rmsnorm_weight, phi_pre, phi_post,
-                                                phi_res, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
-                                                sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
-        ctx.save_for_backward(residual, branch, rmsnorm_weight, saved, phi_pre, phi_post, phi_res, alpha_pre,
-                              alpha_post, alpha_res, b_pre, b_post, b_res)
-        ctx.cfg = (residual_mode, n, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        r, b, w, saved, pp, pq, pr, ap, aq, ar, bp, bq, br = ctx.saved_tensors
-        mode, n, iters, sk_eps, rms_eps = ctx.cfg
-        gr, gb, gw, gpp, gpq, gpr, gap, gaq, gar, gbp, gbq, gbr = native.wrapper_dynamic_bwd(
-            grad_out, r, b, mode, n, w, saved, pp, pq, pr, ap, aq, ar, br, iters, sk_eps, rms_eps)
-        return (gr.to(r.dtype), gb.to(b.dtype), gw, gpp.view_as(pp), gpq.view_as(pq), gpr.view_as(pr),
-                gap.view_as(ap), gaq.view_as(aq), gar.view_as(ar), gbp.view_as(bp), gbq.view_as(bq),
-                gbr.view_as(br), None, None, None, None, None)
-
-
-class MHCWrapperStaticFunction(torch.autograd.Function):
-    """Stream synthesis -> static-H layer -> stream mean, fused."""
-
-    @staticmethod
-    def forward(ctx, residual, branch, rmsnorm_weight, H_pre, H_post, H_res, residual_mode: str, n: int,
-                sinkhorn_iters: int, sinkhorn_eps: float, rmsnorm_eps: float):
-        out, saved = native.wrapper_static_fwd(residual, branch, residual_mode, n, rmsnorm_weight, H_pre, H_post,
-                                               H_res, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
-        ctx.save_for_backward(residual, branch, rmsnorm_weight, H_pre, H_post, H_res, saved)
-        ctx.cfg = (residual_mode, n, sinkhorn_iters, sinkhorn_eps, rmsnorm_eps)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        r, b, w, hp, hq, hr, saved = ctx.saved_tensors
-        mode, n, iters, sk_eps, rms_eps = ctx.cfg
-        gr, gb, gw, ghp, ghq, ghr = native.wrapper_static_bwd(grad_out, r, b, mode, n, w, hp, hq, hr, saved, iters,
-                                                              sk_eps, rms_eps)
-        return (gr.to(r.dtype), gb.to(b.dtype), gw, ghp.view_as(hp), ghq.view_as(hq), ghr.view_as(hr), None, None,
-                None, None, None)
-
 
 def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, layer, residual_mode: str = "decay"):
     """Fused MHCResidualWrapper on residual / branch_output [tokens, C] for the
@@ -348,20 +245,11 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
             for i in range(2, n):
                 X[:, i] = residual * (0.1 ** (i - 1))
         return layer(X).mean(dim=1)
-    args = (layer.num_sinkhorn_iters, layer.sinkhorn_eps, layer.rmsnorm_eps)
+    iters, sk_eps, rms_eps = int(layer.num_sinkhorn_iters), float(layer.sinkhorn_eps), float(layer.rmsnorm_eps)
     ag = _lib.autograd()
-    if ag is not None:
-        if layer.use_dynamic_h:
-            return ag.dynamic_wrapper(residual, branch_output, layer.rmsnorm_weight, layer.phi_pre, layer.phi_post,
-                                      layer.phi_res, layer.alpha_pre, layer.alpha_post, layer.alpha_res, layer.b_pre,
-                                      layer.b_post, layer.b_res, residual_mode, n, int(args[0]), float(args[1]),
-                                      float(args[2]))
-        return ag.static_wrapper(residual, branch_output, layer.rmsnorm_weight, layer.H_pre, layer.H_post,
-                                 layer.H_res, residual_mode, n, int(args[0]), float(args[1]), float(args[2]))
     if layer.use_dynamic_h:
-        return MHCWrapperDynamicFunction.apply(residual, branch_output, layer.rmsnorm_weight, layer.phi_pre,
-                                               layer.phi_post, layer.phi_res, layer.alpha_pre, layer.alpha_post,
-                                               layer.alpha_res, layer.b_pre, layer.b_post, layer.b_res,
-                                               residual_mode, n, *args)
-    return MHCWrapperStaticFunction.apply(residual, branch_output, layer.rmsnorm_weight, layer.H_pre, layer.H_post,
-                                          layer.H_res, residual_mode, n, *args)
+        return ag.dynamic_wrapper(residual, branch_output, layer.rmsnorm_weight, layer.phi_pre, layer.phi_post,
+                                  layer.phi_res, layer.alpha_pre, layer.alpha_post, layer.alpha_res, layer.b_pre,
+                                  layer.b_post, layer.b_res, residual_mode, n, iters, sk_eps, rms_eps)
+    return ag.static_wrapper(residual, branch_output, layer.rmsnorm_weight, layer.H_pre, layer.H_post, layer.H_res,
+                             residual_mode, n, iters, sk_eps, rms_eps)

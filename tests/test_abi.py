@@ -35,8 +35,21 @@ def test_library_exports_every_declared_symbol():
 def test_pure_host_entry_points():
     lib = _lib.load()
     assert lib.mhc_abi_version() >= 100
-    assert lib.mhc_timing_enable(0) == 0
     assert isinstance(lib.mhc_last_error(), bytes)
+
+
+def test_product_build_has_no_timing_state_and_the_bench_build_does():
+    """Per-kernel timing exists only in the benchmark's build of the same
+    sources (include/mhc_hip_timing.h); the product library exports none of
+    it.  The timed build exports every product entry as well."""
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "mhc_hip_timing.h")).read(), flags=re.S)
+    timing = set(re.findall(r"^\s*int\s+(mhc_timing_\w+)\s*\(", text, flags=re.M))
+    assert timing == set(_lib.TIMING_SIGNATURES)
+    product = ctypes.CDLL(_lib.LIB_PATH)
+    assert not [n for n in timing if hasattr(product, n)]
+    timed = ctypes.CDLL(_lib.TIMED_LIB_PATH)
+    missing = [n for n in header_functions() | timing if not hasattr(timed, n)]
+    assert not missing, missing
 
 
 @pytest.mark.parametrize("n,iters,batch", [(0, 20, 4), (4, -1, 4), (4, 20, -1)])
@@ -116,19 +129,20 @@ def test_autograd_extension_binds_every_entry():
     assert callable(ag.static_layer) and callable(ag.dynamic_layer)
 
 
-def test_autograd_extension_switch(monkeypatch):
-    """MHC_CPP_AUTOGRAD=0 selects the Python autograd functions (the layers
-    then call the same entry points from Python); the default binds the
-    C++ nodes."""
+def test_autograd_extension_is_required(monkeypatch):
+    """The C++ autograd nodes are the only orchestration of the fused layers:
+    bound to the loaded library by default, and a clear error (no silent
+    fallback) when the extension is missing."""
     from mhc_ascend_amd import _lib
 
-    saved = (_lib._autograd, _lib._autograd_done)
+    saved = _lib._autograd
     try:
-        monkeypatch.setenv("MHC_CPP_AUTOGRAD", "0")
-        _lib._autograd, _lib._autograd_done = None, False
-        assert _lib.autograd() is None
-        monkeypatch.delenv("MHC_CPP_AUTOGRAD")
-        _lib._autograd, _lib._autograd_done = None, False
-        assert _lib.autograd() is not None
+        _lib._autograd = None
+        ag = _lib.autograd()
+        assert ag is not None and hasattr(ag, "static_layer")
+        _lib._autograd = None
+        monkeypatch.setattr(_lib, "AUTOGRAD_PATH", _lib.AUTOGRAD_PATH + ".missing")
+        with pytest.raises(RuntimeError, match="autograd extension"):
+            _lib.autograd()
     finally:
-        _lib._autograd, _lib._autograd_done = saved
+        _lib._autograd = saved

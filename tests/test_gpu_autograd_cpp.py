@@ -14,6 +14,7 @@ import torch
 
 import mhc_ascend_amd as mhc
 from mhc_ascend_amd import _lib, ops
+from tests import pyref_autograd as pyref
 
 pytestmark = pytest.mark.gpu
 
@@ -64,7 +65,7 @@ def test_static_layer_cpp_equals_python(device, x_dtype, n, B, C, noncontig):
     a = [x0.detach().clone().requires_grad_(True)] + _leaves(params, device)
     out_c, gc = _run(lambda *t: ag.static_layer(*t, *cfg), a, grad)
     b = [x0.detach().clone().requires_grad_(True)] + _leaves(params, device)
-    out_p, gp = _run(lambda *t: ops.MHCLayerStaticFunction.apply(*t, *cfg), b, grad)
+    out_p, gp = _run(lambda *t: pyref.MHCLayerStaticFunction.apply(*t, *cfg), b, grad)
     _same(out_c, out_p, "out")
     for i, (u, v) in enumerate(zip(gc, gp)):
         _same(u, v, f"grad {i}")
@@ -99,7 +100,7 @@ def test_dynamic_layer_cpp_equals_python(device, x_dtype, n, B, C, float_alpha):
     out_c.backward(grad)
     b = inputs()
     al = [torch.tensor(v, device=device, dtype=torch.float32) if not torch.is_tensor(v) else v for v in b[5:8]]
-    out_p = ops.MHCLayerDynamicFunction.apply(*b[:5], *al, *b[8:], *cfg)
+    out_p = pyref.MHCLayerDynamicFunction.apply(*b[:5], *al, *b[8:], *cfg)
     out_p.backward(grad)
     _same(out_c.detach(), out_p.detach(), "out")
     for i, (u, v) in enumerate(zip(a, b)):
@@ -126,11 +127,11 @@ def test_layer_module_runs_cpp_nodes(device, dynamic):
     x.grad = None
     cfg = (layer.num_sinkhorn_iters, layer.sinkhorn_eps, layer.rmsnorm_eps)
     if dynamic:
-        ref = ops.MHCLayerDynamicFunction.apply(x, layer.rmsnorm_weight, layer.phi_pre, layer.phi_post,
+        ref = pyref.MHCLayerDynamicFunction.apply(x, layer.rmsnorm_weight, layer.phi_pre, layer.phi_post,
                                                 layer.phi_res, layer.alpha_pre, layer.alpha_post, layer.alpha_res,
                                                 layer.b_pre, layer.b_post, layer.b_res, *cfg)
     else:
-        ref = ops.MHCLayerStaticFunction.apply(x, layer.rmsnorm_weight, layer.H_pre, layer.H_post, layer.H_res,
+        ref = pyref.MHCLayerStaticFunction.apply(x, layer.rmsnorm_weight, layer.H_pre, layer.H_post, layer.H_res,
                                                *cfg)
     _same(out.detach(), ref.detach(), "out")
     ref.sum().backward()
@@ -180,11 +181,11 @@ def test_wrapper_cpp_equals_python(device, dynamic, dtype, mode):
     _ag()
     got = grads_of(lambda r, b: ops.mhc_residual_wrapper(r, b, layer, mode))
     if dynamic:
-        want = grads_of(lambda r, b: ops.MHCWrapperDynamicFunction.apply(
+        want = grads_of(lambda r, b: pyref.MHCWrapperDynamicFunction.apply(
             r, b, layer.rmsnorm_weight, layer.phi_pre, layer.phi_post, layer.phi_res, layer.alpha_pre,
             layer.alpha_post, layer.alpha_res, layer.b_pre, layer.b_post, layer.b_res, mode, 4, *cfg))
     else:
-        want = grads_of(lambda r, b: ops.MHCWrapperStaticFunction.apply(
+        want = grads_of(lambda r, b: pyref.MHCWrapperStaticFunction.apply(
             r, b, layer.rmsnorm_weight, layer.H_pre, layer.H_post, layer.H_res, mode, 4, *cfg))
     _same(got[0], want[0], "out")
     _same(got[1], want[1], "grad residual")
