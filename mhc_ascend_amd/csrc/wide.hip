@@ -68,12 +68,15 @@ __device__ __forceinline__ void wide_block_total(float (&v)[NV], float* red, flo
 // ---------------------------------------------------------------------------
 // Forward: one token per workgroup of 1024 lanes (one or two channels per
 // lane at the paper widths), so the row sum of xa^2 is one round of 2 N
-// loads per lane in flight and the output pass re-reads the row from cache.
-// (Splitting a token's channels over 256-lane workgroups, each redoing the
-// row sum, measured slower at 32-128 tokens: the n = 32, C = 1280 eval
-// forward took 0.076 against 0.058 ms at 32 tokens.)  out in TO (fp32, or
-// bf16 for the
-// forward-only entry); rms_out[b] = r when not null.
+// loads per lane in flight and the output pass re-reads the row from cache
+// (wide_fwd_kernel).  With fewer tokens than two workgroups per CU the
+// output pass instead runs over token x 256-channel chunks
+// (wide_fwd_out_kernel), after the row sums: one token per workgroup into the
+// caller's rms (wide_fwd_rms_kernel), or, when the caller lends scratch of
+// at least tokens x chunks floats, token x chunk partials
+// (wide_fwd_part_kernel) that each output workgroup sums in a fixed order.
+// out in TO (fp32, or bf16 for the forward-only entry); rms_out[b] = r when
+// rms_out is the caller's output.
 // ---------------------------------------------------------------------------
 // Row sum of xa^2 over the token's C channels and r = sqrt(mean + eps),
 // block-wide (all threads get r).  cf: the token's coefficients (global).
