@@ -303,3 +303,35 @@ def test_dynamic_layer_config_c4_full_size(device):
         assert_close(g_full[k + 1], s, 1e-4, grad_atol(s, 1e-5), f"C4 additivity {nm}")
     sl = {k: (v[:128] if k in ("x", "grad") else v) for k, v in d.items()}
     _check_dyn(_run_dyn(sl, device), _oracle_dyn(sl), torch.bfloat16, "C4 slice")
+
+
+@pytest.mark.parametrize("B,C", [(1000, 1024), (257, 4096), (3001, 2048)])
+def test_dynamic_layer_backward_many_tokens(device, B, C):
+    """bf16 x at n = 4 with many tokens per persistent workgroup and a token
+    count that fills no launch evenly: every token's dx (B <= 1000) or a
+    strided third of them against the oracle, the parameter gradients against
+    the oracle (B <= 1000) or by additivity over two parts split inside a
+    workgroup's token range."""
+    n = 4
+    d = R.dynamic_layer_inputs(B, n, C, seed=B + C, alpha=0.3, phi_std=0.05, b_std=0.5)
+    if B <= 1000:
+        _check_dyn(_run_dyn(d, device), _oracle_dyn(d), torch.bfloat16, f"many tokens B={B} C={C}")
+        return
+    dev = {k: v.to(device) for k, v in d.items()}
+    pvals = [dev[k] for k in PARAMS]
+
+    def grads(sl):
+        w32 = dev["weight"].float()
+        out, saved = native.mhc_layer_dynamic_fwd(dev["x"][sl], w32, *pvals[1:])
+        return native.mhc_layer_dynamic_bwd(dev["grad"][sl], dev["x"][sl], w32, saved, *pvals[1:])
+
+    g_full = grads(slice(0, B))
+    idx = torch.arange(0, B, 3)
+    sub = {k: (v[idx] if k in ("x", "grad") else v) for k, v in d.items()}
+    _, rgx, _ = _oracle_dyn(sub)
+    assert_close_bf16(g_full[0].cpu()[idx], rgx, f"many tokens B={B} C={C} dx (every third token)")
+    h = 1200  # not a multiple of the block size
+    g1, g2 = grads(slice(0, h)), grads(slice(h, B))
+    for k in range(1, len(g_full)):
+        s = g1[k] + g2[k]
+        assert_close(g_full[k], s, 1e-4, grad_atol(s, 1e-5), f"many tokens B={B} additivity {k}")
