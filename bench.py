@@ -354,7 +354,9 @@ class WrapperWorkload:
 
     def kernel_bytes(self):
         F = self.F
-        return {"wrap_proj": 4 * F, "wrap_fwd": 8 * F, "wrap_bwd_reduce": 12 * F, "wrap_proj_bwd": 12 * F}
+        # wrap_bwd_reduce reads g fp32 and r, b; wrap_proj_bwd reads them again
+        # and writes d r, d b
+        return {"wrap_proj": 4 * F, "wrap_fwd": 8 * F, "wrap_bwd_reduce": 8 * F, "wrap_proj_bwd": 12 * F}
 
     def flops(self):
         f = 2 * self.tokens * self.n * self.C * (2 * self.n + self.n * self.n)

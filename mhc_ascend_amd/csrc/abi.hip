@@ -1161,9 +1161,6 @@ static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidd
         return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");
     if (dynamic && hidden % 32 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of 32");
-    // bf16 storage: the backward's stream parts travel in 128-channel groups
-    if (dynamic && dtype == kBF16 && hidden % 128 != 0)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": bf16 hidden must be a multiple of 128");
     if (choose_row_tiling(hidden, 4, 6).vpt <= 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
     return MHC_SUCCESS;
@@ -1235,31 +1232,34 @@ int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dt
 }
 
 struct WrapBwdWs {
-    int grid, cblocks, tiles, groups;
-    size_t dw_off, scal_off, dp_off, s_off, step_off, cpart_off, phip_off, stw_off, stp_off, total;
+    int grid, cblocks, tiles;
+    size_t dw_off, scal_off, dp_off, s_off, ep_off, cpart_off, phip_off, stw_off, stp_off, total;
 };
 
+// static: [dw partials (grid rows) | stage | per-workgroup scalars];
+// dynamic: [dw partials (tiles rows) | stage | per-token scalars | dP | s |
+// stream-part factors | coefficient partials | dPhi partials | stage]
 static WrapBwdWs wrap_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype, bool dynamic, bool decay) {
     WrapBwdWs w{};
     const int64_t np = 2 * n + n * n;
     const int64_t K = (int64_t)n * hidden;
-    w.grid = tokens > 0 ? wrap_bwd_grid(dtype, n, decay, tokens, hidden) : 1;
     size_t o = 0;
-    w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
-    w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
     if (!dynamic) {
+        w.grid = tokens > 0 ? wrap_bwd_grid(dtype, n, decay, tokens, hidden) : 1;
+        w.dw_off = o; o += align256((size_t)w.grid * hidden * 4);
+        w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
         w.scal_off = o; o += align256((size_t)w.grid * (n * n + 2 * n) * 4);
         w.total = o;
         return w;
     }
     w.cblocks = tokens > 0 ? dyn_coef_bwd_blocks(n, tokens) : 1;
     w.tiles = tokens > 0 ? wrap_proj_bwd_tiles(dtype, tokens, hidden) : 1;
+    w.dw_off = o; o += align256((size_t)w.tiles * hidden * 4);
+    w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
     w.scal_off = o; o += align256((size_t)tokens * (n * n + 2 * n + 2) * 4);
     w.dp_off = o; o += align256((size_t)tokens * 32 * 4);
     w.s_off = o; o += align256((size_t)tokens * 4);
-    // fixed-point steps of d r, d b (bf16 storage)
-    w.groups = dtype == kBF16 ? wrap_bwd_fixed_groups(hidden) : 0;
-    w.step_off = o; o += align256((size_t)tokens * w.groups * 2 * 4);
+    w.ep_off = o; o += align256((size_t)tokens * kWrapEp * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     w.phip_off = o; o += align256((size_t)w.tiles * np * K * 4);
     w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)np * K) * 4);
@@ -1302,32 +1302,33 @@ int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const v
     float* phip = (float*)(ws + w.phip_off);
     float* stw = (float*)(ws + w.stw_off);
     float* stp = (float*)(ws + w.stp_off);
-    float* step = dtype == kBF16 ? (float*)(ws + w.step_off) : nullptr;
+    float* ep = (float*)(ws + w.ep_off);
     const DynSaved d = dyn_saved(tokens, n, hidden);
     const int np = 2 * n + n * n;
     const int64_t K = (int64_t)n * hidden;
     const float* w32 = saved + d.w_off;
     hipError_t e = hipSuccess;
-    int rows_w = w.grid, rows_p = w.tiles, rows_c = w.cblocks;
+    int rows_p = w.tiles, rows_c = w.cblocks;
     if (tokens == 0) {
-        rows_w = rows_p = rows_c = 1;
+        rows_p = rows_c = 1;
         e = launch_fill_zero(dw_part, hidden, s);
         if (e == hipSuccess) e = launch_fill_zero(phip, (int64_t)np * K, s);
         if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
     } else {
-        e = launch_wrap_bwd(dtype, n, 1, decay, grad_out, residual, branch, w32, saved + d.coef_off, np,
-                            grad_residual, grad_branch, dw_part, scal, w.grid, tokens, hidden, rmsnorm_eps, s, step);
+        e = launch_wrap_bwd_red(dtype, n, decay, grad_out, residual, branch, w32, saved + d.coef_off, np, scal, ep,
+                                tokens, hidden, rmsnorm_eps, s);
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
                                     nullptr, s);
         if (e == hipSuccess)
-            e = launch_wrap_proj_bwd(dtype, n, decay, residual, branch, dp, stok, phi_pre, phi_post, phi_res,
-                                     grad_residual, grad_branch, phip, w.tiles, tokens, hidden, s, step, w.groups);
+            e = launch_wrap_proj_bwd(dtype, n, decay, grad_out, residual, branch, w32, ep, dp, stok, phi_pre,
+                                     phi_post, phi_res, grad_residual, grad_branch, dw_part, phip, w.tiles, tokens,
+                                     hidden, s);
     }
     if (e == hipSuccess)
-        e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,
-                                  nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+        e = launch_column_finalize(0, weight_dtype, dw_part, rows_p, hidden, stw, grad_weight, nullptr, 0, nullptr,
+                                   nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
     if (e == hipSuccess)
         e = launch_column_finalize(0, kF32, phip, rows_p, (int64_t)np * K, stp, grad_phi, nullptr, 0, nullptr, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
@@ -1386,7 +1387,7 @@ int mhc_wrapper_static_bwd(const float* grad_out, const void* residual, const vo
         e = launch_fill_zero(dw_part, hidden, s);
         if (e == hipSuccess) e = launch_fill_zero(scal_part, n * n + 2 * n, s);
     } else {
-        e = launch_wrap_bwd(dtype, n, 0, decay, grad_out, residual, branch, saved + saved_w_offset(n), saved, 0,
+        e = launch_wrap_bwd(dtype, n, decay, grad_out, residual, branch, saved + saved_w_offset(n), saved, 0,
                             grad_residual, grad_branch, dw_part, scal_part, w.grid, tokens, hidden, rmsnorm_eps, s);
     }
     if (e == hipSuccess)

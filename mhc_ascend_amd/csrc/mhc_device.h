@@ -111,6 +111,27 @@ __device__ __forceinline__ uint4 buf_ld16(buf_rsrc_t r, uint32_t voff, uint32_t 
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+template <bool PIN = false>
+__device__ __forceinline__ uint32_t buf_ld4(buf_rsrc_t r, uint32_t voff, uint32_t soff) {
+    constexpr int aux = PIN ? (int)0x80000000u : 0;
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, aux);
+}
+
+// Raw buffer store: a lane whose offset is at or past the resource's size
+// stores nothing (the same range check), so partial tiles need no branch
+// around the store.  NT sets the streaming cache policy.
+template <bool NT>
+__device__ __forceinline__ void buf_st16(buf_rsrc_t r, uint32_t voff, uint32_t soff, uint4 v) {
+    constexpr int aux = NT ? 2 : 0;
+    typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4v_t{v.x, v.y, v.z, v.w}, r, (int)voff, (int)soff, aux);
+}
+
+// A per-lane buffer offset that fails the range check of any resource under
+// 2 GiB, also after adding a stage offset that keeps real offsets under
+// 2 GiB (the sum stays below 2^32: no wrap into range).
+constexpr uint32_t kBufOff = 0x80000000u;
+
 __device__ __forceinline__ uint32_t wave_uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ uint2 ld8_nt(const void* p) {

@@ -278,29 +278,36 @@ hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, 
 // ---- wrapper.hip -----------------------------------------------------------
 // Fused MHCResidualWrapper (n = 4): streams synthesised from (residual,
 // branch); decay = 'decay' mode (else 'zero').
+// Floats per token of the dynamic backward's stream-part factors
+// (cm_0..3, h_pre_0..3, hs, 1/r, k2, one spare slot).
+constexpr int kWrapEp = 12;
 hipError_t launch_wrap_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
                            const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
                            hipStream_t s);
 int wrap_bwd_grid(int dt, int n, bool decay, int64_t B, int64_t C);
-// mode 0: static (per-workgroup sums of [dM, dh_post_act, dh_pre_act] in
-// scal_out[grid][n*n+2n]); mode 1: dynamic (per-token scal_out[B][n*n+2n+2]);
-// its d r / d b stream parts with bf16 storage are int16 fixed point
-// (fixed_scale in mhc_device.h) with steps d_step[B][wrap_bwd_fixed_groups][2].
-int wrap_bwd_fixed_groups(int64_t C);
-hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, const void* res, const void* br,
+// Static-H backward: per-workgroup sums of [dM, dh_post_act, dh_pre_act] in
+// scal_out[grid][n*n+2n], d r / d b and the dw partials dw_part[grid][C].
+hipError_t launch_wrap_bwd(int dt, int n, bool decay, const float* g, const void* res, const void* br,
                            const float* w, const float* coef, int64_t coef_stride, void* dres, void* dbr,
-                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s,
-                           float* d_step = nullptr);
+                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps,
+                           hipStream_t s);
+// Dynamic-H backward, pass 1 (reads G, r, b only): per-token scalars
+// scal_out[B][n*n+2n+2] and stream-part factors ep_out[B][kWrapEp].
+hipError_t launch_wrap_bwd_red(int dt, int n, bool decay, const float* g, const void* res, const void* br,
+                               const float* w, const float* coef, int64_t coef_stride, float* scal_out,
+                               float* ep_out, int64_t B, int64_t C, float eps, hipStream_t s);
 int wrap_proj_csplit(int64_t B, int64_t C);
 hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const void* br, const bf16_raw_t* phib,
                             float* p_part, float* ss_part, int64_t B, int64_t C, int ks, hipStream_t s);
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C);
-// bf16 storage: dres / dbr come in as the fixed-point stream parts of
-// launch_wrap_bwd (mode 1) with their steps d_step[B][groups][2].
-hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
-                                const float* s_tok, const float* phi_pre, const float* phi_post, const float* phi_res,
-                                void* dres, void* dbr, float* dphi_part, int tiles, int64_t B, int64_t C,
-                                hipStream_t s, const float* d_step = nullptr, int groups = 0);
+// Dynamic-H backward, pass 2: d r / d b (written, rounded once), dw_part
+// [tiles][C] and dphi_part [tiles][np][n*C] from G, r, b, the factors of
+// launch_wrap_bwd_red, dP and s.
+hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const void* res, const void* br,
+                                const float* w, const float* ep, const float* dP, const float* s_tok,
+                                const float* phi_pre, const float* phi_post, const float* phi_res, void* dres,
+                                void* dbr, float* dw_part, float* dphi_part, int tiles, int64_t B, int64_t C,
+                                hipStream_t s);
 
 // ---- compat.hip ------------------------------------------------------------
 // The reference-shaped dynamic-H entries (mhc_layer_fwd_dynamic /

@@ -16,13 +16,15 @@
 //
 // Kernels:
 //   wrap_fwd_kernel       row pass: xa, RMSNorm, the stream mean (fp32 out)
-//   wrap_bwd_kernel       row pass: all row sums of a token, the stream parts
-//                         of d r / d b; MODE 0 static (per-workgroup sums),
-//                         MODE 1 dynamic (per-token scalars)
+//   wrap_bwd_kernel       static-H row pass: all row sums of a token
+//                         (per-workgroup sums) and d r / d b
+//   wrap_bwd_red_kernel   dynamic-H backward pass 1: the row sums of each
+//                         token (one wave per token), reading only
 //   wrap_proj_kernel      P = X_flat . Phi^T split-K on bf16 MFMA, reading r
 //                         and b once per channel for all n streams
-//   wrap_proj_bwd_kernel  d r, d b += s X + dP . Phi (fp32 MFMA, Phi folded
-//                         over the residual-derived streams) and dPhi
+//   wrap_proj_bwd_kernel  dynamic-H backward pass 2: d r, d b = stream parts
+//                         + s X + dP . Phi (Phi folded over the
+//                         residual-derived streams), dw and dPhi partials
 #include <type_traits>
 
 #include "mhc_device.h"
@@ -171,16 +173,15 @@ __global__ MHC_ROW_BOUNDS(false) void wrap_fwd_kernel(const TX* __restrict__ res
 // (dM[n*n], dh_post_act[n], dh_pre_act[n], 1/r, k2):
 //   dM_ij = u_j / n,  dh_post_act_i = gwx / (n r),
 //   dh_pre_act_j = hs v_j / r - k2 z_j,  k2 = hs gwx / (C r^3).
-// MODE 0 sums the first n*n+2n per workgroup (static H, shared M); MODE 1
-// writes them per token (dynamic H).  d r / d b get the stream terms.
+// The first n*n+2n are summed per workgroup (static H, shared M); d r / d b
+// get the stream terms, which are the whole gradient with static H.
 // ---------------------------------------------------------------------------
-template <typename TX, int N, int VPT, int MODE, bool DECAY>
+template <typename TX, int N, int VPT, bool DECAY>
 __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restrict__ coef, int64_t coef_stride,
                                                const float (&wv)[VPT][kLayerWC], const float (&gv)[1][VPT][kLayerWC],
                                                const float (&rv)[1][VPT][kLayerWC],
                                                const float (&bv)[1][VPT][kLayerWC], float (&dwacc)[VPT][kLayerWC],
-                                               float& sacc, TX* __restrict__ dres, TX* __restrict__ dbr,
-                                               float* __restrict__ scal_out, float* __restrict__ d_step, int C,
+                                               float& sacc, TX* __restrict__ dres, TX* __restrict__ dbr, int C,
                                                float eps, float* red) {
     constexpr int WC = kLayerWC;
     constexpr int NS = N * N + 2 * N;
@@ -243,38 +244,26 @@ __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restric
     const float gwx = tot[1];
     const float k2 = hs * gwx * inv * inv * inv / (float)C;
 
-    if (threadIdx.x < NS + 2) {
+    if (threadIdx.x < NS) {
         const int t = threadIdx.x;
         float v;
         if (t < N * N) {
             v = tot[2 + t % N] * (1.f / N);  // dM_ij = u_j / n
         } else if (t < N * N + N) {
             v = gwx * inv * (1.f / N);  // dh_post_act_i
-        } else if (t < NS) {
+        } else {
             const int j = t - N * N - N;
             v = hs * inv * tot[2 + N + j] - k2 * tot[2 + 2 * N + j];  // dh_pre_act_j
-        } else {
-            v = (t == NS) ? inv : k2;
         }
-        if (MODE == 0) {
-            sacc += v;
-        } else {
-            scal_out[b * (NS + 2) + t] = v;
-        }
+        sacc += v;
     }
 
     TX* drb = dres + b * (int64_t)C;
     TX* dbb = dbr + b * (int64_t)C;
-    // The dynamic backward's stream parts with bf16 storage travel as int16
-    // fixed point (fixed_scale), one scale per half wave and token for each:
-    // d_step[b][threadIdx.x / 32][d r, d b].  The projection kernel adds its
-    // terms and rounds once to bf16.
-    constexpr bool QOUT = MODE == 1 && sizeof(TX) == 2;
-    float dr[VPT][WC], db[VPT][WC];
-    float mr = 0.f, mb = 0.f;
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        float dr[WC], db[WC];
 #pragma unroll
         for (int e = 0; e < WC; ++e) {
             float x[N];
@@ -290,43 +279,23 @@ __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restric
             if constexpr (N > 0) a += cm[0] * g + hp[0] * gxa;
             if constexpr (N > 2) a += res_weight<2, DECAY>() * (cm[2] * g + hp[2] * gxa);
             if constexpr (N > 3) a += res_weight<3, DECAY>() * (cm[3] * g + hp[3] * gxa);
-            dr[k][e] = a;
-            db[k][e] = (N > 1) ? cm[N > 1 ? 1 : 0] * g + hp[N > 1 ? 1 : 0] * gxa : 0.f;
-            if constexpr (QOUT) {
-                mr = fmaxf(mr, fabsf(dr[k][e]));
-                mb = fmaxf(mb, fabsf(db[k][e]));
-            }
+            dr[e] = a;
+            db[e] = (N > 1) ? cm[N > 1 ? 1 : 0] * g + hp[N > 1 ? 1 : 0] * gxa : 0.f;
         }
-        if constexpr (!QOUT) {
-            if (c0 < C) {
-                store_run_nt<TX, WC>(drb + c0, dr[k]);
-                store_run_nt<TX, WC>(dbb + c0, db[k]);
-            }
+        if (c0 < C) {
+            store_run_nt<TX, WC>(drb + c0, dr);
+            store_run_nt<TX, WC>(dbb + c0, db);
         }
-    }
-    if constexpr (QOUT) {
-        const FixedScale fr = fixed_scale(half_wave_max_nonneg(mr));
-        const FixedScale fb = fixed_scale(half_wave_max_nonneg(mb));
-#pragma unroll
-        for (int k = 0; k < VPT; ++k) {
-            const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-            if (c0 < C) {
-                st8_nt(drb + c0, fixed_pack4(dr[k], fr.inv));
-                st8_nt(dbb + c0, fixed_pack4(db[k], fb.inv));
-            }
-        }
-        const int lane32 = threadIdx.x & 31;
-        if (lane32 < 2) d_step[(b * (blockDim.x / 32) + threadIdx.x / 32) * 2 + lane32] = lane32 ? fb.step : fr.step;
     }
 }
 
-template <typename TX, int N, int VPT, int MODE, bool PF, bool DECAY>
+template <typename TX, int N, int VPT, bool PF, bool DECAY>
 __device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const TX* __restrict__ res,
                                               const TX* __restrict__ br, const float* __restrict__ w,
                                               const float* __restrict__ coef, int64_t coef_stride,
                                               TX* __restrict__ dres, TX* __restrict__ dbr,
-                                              float* __restrict__ dw_part, float* __restrict__ scal_out,
-                                              float* __restrict__ d_step, int64_t B, int C, float eps) {
+                                              float* __restrict__ dw_part, float* __restrict__ scal_out, int64_t B,
+                                              int C, float eps) {
     constexpr int WC = kLayerWC;
     constexpr int NS = N * N + 2 * N;
     constexpr int NR = 2 + 3 * N;
@@ -361,8 +330,8 @@ __device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const
             unpack_rows<float, 1, VPT, WC>(gA, C, gv);
             unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
-            wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
-                                                    scal_out, d_step, C, eps, red);
+            wrap_bwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr, C, eps,
+                                              red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
             if (b2 < B) {
@@ -373,8 +342,8 @@ __device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const
             unpack_rows<float, 1, VPT, WC>(gB, C, gv);
             unpack_rows<TX, 1, VPT, WC>(rB, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bB, C, bv);
-            wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b1, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
-                                                    scal_out, d_step, C, eps, red);
+            wrap_bwd_token<TX, N, VPT, DECAY>(b1, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr, C, eps,
+                                              red);
             b = b2;
         }
     } else {
@@ -385,8 +354,8 @@ __device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const
             unpack_rows<float, 1, VPT, WC>(gA, C, gv);
             unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
-            wrap_bwd_token<TX, N, VPT, MODE, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr,
-                                                    scal_out, d_step, C, eps, red);
+            wrap_bwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, gv, rv, bv, dwacc, sacc, dres, dbr, C, eps,
+                                              red);
         }
     }
     float* dwp = dw_part + (int64_t)blockIdx.x * C;
@@ -395,31 +364,186 @@ __device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
         if (c0 < C) store_run<float, WC>(dwp + c0, dwacc[k]);
     }
-    if (MODE == 0 && threadIdx.x < NS) scal_out[(int64_t)blockIdx.x * NS + threadIdx.x] = sacc;
+    if (threadIdx.x < NS) scal_out[(int64_t)blockIdx.x * NS + threadIdx.x] = sacc;
 }
 
-// Workgroups of more than 256 lanes hold one token at a time; they are held
-// to 128 VGPRs (4 waves per SIMD: two 448-lane workgroups per CU at C5, where
-// the fixed-point stream part of the dynamic backward otherwise takes 133).
-template <typename TX, int N, int VPT, int MODE, bool DECAY>
+// Workgroups of more than 256 lanes hold one token at a time.
+template <typename TX, int N, int VPT, bool DECAY>
 __global__ MHC_ROW_BOUNDS(false) __attribute__((amdgpu_waves_per_eu(4))) void wrap_bwd_kernel(
     const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
     const float* __restrict__ coef, int64_t coef_stride, TX* __restrict__ dres, TX* __restrict__ dbr,
-    float* __restrict__ dw_part, float* __restrict__ scal_out, float* __restrict__ d_step, int64_t B, int C,
-    float eps) {
-    wrap_bwd_rows<TX, N, VPT, MODE, false, DECAY>(g, res, br, w, coef, coef_stride, dres, dbr, dw_part, scal_out,
-                                                  d_step, B, C, eps);
+    float* __restrict__ dw_part, float* __restrict__ scal_out, int64_t B, int C, float eps) {
+    wrap_bwd_rows<TX, N, VPT, false, DECAY>(g, res, br, w, coef, coef_stride, dres, dbr, dw_part, scal_out, B, C, eps);
 }
 
 // Up to 256 lanes: two tokens in flight (register prefetch).
-template <typename TX, int N, int VPT, int MODE, bool DECAY>
+template <typename TX, int N, int VPT, bool DECAY>
 __global__ MHC_ROW_BOUNDS(true) void wrap_bwd_pf_kernel(
     const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
     const float* __restrict__ coef, int64_t coef_stride, TX* __restrict__ dres, TX* __restrict__ dbr,
-    float* __restrict__ dw_part, float* __restrict__ scal_out, float* __restrict__ d_step, int64_t B, int C,
-    float eps) {
-    wrap_bwd_rows<TX, N, VPT, MODE, true, DECAY>(g, res, br, w, coef, coef_stride, dres, dbr, dw_part, scal_out,
-                                                 d_step, B, C, eps);
+    float* __restrict__ dw_part, float* __restrict__ scal_out, int64_t B, int C, float eps) {
+    wrap_bwd_rows<TX, N, VPT, true, DECAY>(g, res, br, w, coef, coef_stride, dres, dbr, dw_part, scal_out, B, C, eps);
+}
+
+// ---------------------------------------------------------------------------
+// Dynamic-H backward, pass 1: the row sums of each token and nothing else.
+// One wave per token streams G, r and b in 4-channel chunks (lane l takes
+// chunks l, l + 64, ...; kRedChunks of them in flight per lane), forms the
+// sums of wrap_bwd_token
+//   ss = sum xa^2, gwx = sum G w xa, u_j = sum G X_j, v_j = sum G w X_j,
+//   z_j = sum xa X_j,
+// adds them over the wave (fixed order) and writes the per-token scalars in
+// the layout of the coefficient backward (dM[n*n], dh_post_act[n],
+// dh_pre_act[n], 1/r, k2) to scal_out[b][n*n+2n+2], and the per-token
+// factors of the stream parts to ep_out[b][kWrapEp]: with w_j the d r weight
+// of stream j, cm_j = (1/n) sum_i M_ij and hs = (1/n) sum_i h_post_i,
+//   (A_r, B_r, A_b, B_b) = (sum_j w_j cm_j, sum_j w_j h_pre_j, cm_1, h_pre_1),
+//   then h_pre_0..3, hs/r, k2, 0, 0,
+// so that d r = A_r G + B_r gxa + ... and d b = A_b G + B_b gxa + ... with
+// gxa = (hs/r) w G - k2 xa.  The stream parts of d r / d b and dw are formed
+// by the projection backward, which reads G once more: that read costs less
+// than writing the stream parts here and reading
+// them back there, and this pass then only reads.
+// ---------------------------------------------------------------------------
+constexpr int kRedChunks = 4;
+
+template <typename TX, int N, bool DECAY>
+__global__ __launch_bounds__(256) void wrap_bwd_red_kernel(const float* __restrict__ g, const TX* __restrict__ res,
+                                                           const TX* __restrict__ br, const float* __restrict__ w,
+                                                           const float* __restrict__ coef, int64_t coef_stride,
+                                                           float* __restrict__ scal_out, float* __restrict__ ep_out,
+                                                           int64_t B, int C, float eps) {
+    constexpr int NS = N * N + 2 * N;
+    constexpr int NR = 2 + 3 * N;
+    constexpr int U = kRedChunks;
+    constexpr int XW = (int)sizeof(TX);  // 32-bit words of one 4-channel chunk of r or b
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t b = (int64_t)blockIdx.x * (blockDim.x / kWave) + (int64_t)wave_uniform(threadIdx.x / kWave);
+    if (b >= B) return;
+    const float* cf = coef + b * coef_stride;
+    float hp[N], cm[N], hs = 0.f;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        hp[j] = cf[j];
+        hs += cf[N + j];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) s += cf[2 * N + i * N + j];
+        cm[j] = s * (1.f / N);
+    }
+    hs *= 1.f / N;
+    float rs[NR];
+#pragma unroll
+    for (int q = 0; q < NR; ++q) rs[q] = 0.f;
+    const float* gb = g + b * (int64_t)C;
+    const TX* rb = res + b * (int64_t)C;
+    const TX* bb = br + b * (int64_t)C;
+    const int nq = C / 4;
+    for (int q0 = 0; q0 < nq; q0 += U * kWave) {
+        // all loads of the U chunks first (chunks past the row read chunk 0)
+        uint4 graw[U], wraw[U];
+        uint32_t rraw[U][XW], braw[U][XW];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = q0 + u * kWave + lane;
+            const int c0 = (q < nq ? q : 0) * 4;
+            graw[u] = ld16_nt(gb + c0);
+            wraw[u] = *reinterpret_cast<const uint4*>(w + c0);
+            if constexpr (XW == 2) {
+                const uint2 a = ld8_nt(rb + c0), c = ld8_nt(bb + c0);
+                rraw[u][0] = a.x; rraw[u][1] = a.y;
+                braw[u][0] = c.x; braw[u][1] = c.y;
+            } else {
+                const uint4 a = ld16_nt(rb + c0), c = ld16_nt(bb + c0);
+                rraw[u][0] = a.x; rraw[u][1] = a.y; rraw[u][2] = a.z; rraw[u][3] = a.w;
+                braw[u][0] = c.x; braw[u][1] = c.y; braw[u][2] = c.z; braw[u][3] = c.w;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (q0 + u * kWave + lane >= nq) continue;
+            const float gv[4] = {__uint_as_float(graw[u].x), __uint_as_float(graw[u].y), __uint_as_float(graw[u].z),
+                                 __uint_as_float(graw[u].w)};
+            const float wv[4] = {__uint_as_float(wraw[u].x), __uint_as_float(wraw[u].y), __uint_as_float(wraw[u].z),
+                                 __uint_as_float(wraw[u].w)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float r, bv;
+                if constexpr (XW == 2) {
+                    const uint32_t wr = rraw[u][e >> 1], wb = braw[u][e >> 1];
+                    r = __uint_as_float((e & 1) ? (wr & 0xffff0000u) : (wr << 16));
+                    bv = __uint_as_float((e & 1) ? (wb & 0xffff0000u) : (wb << 16));
+                } else {
+                    r = __uint_as_float(rraw[u][e]);
+                    bv = __uint_as_float(braw[u][e]);
+                }
+                float x[N];
+                wrap_streams<TX, N, DECAY>(r, bv, x);
+                float xa = 0.f;
+#pragma unroll
+                for (int j = 0; j < N; ++j) xa += hp[j] * x[j];
+                const float gg = gv[e];
+                const float wg = wv[e] * gg;
+                rs[0] += xa * xa;
+                rs[1] += wg * xa;
+#pragma unroll
+                for (int j = 0; j < N; ++j) {
+                    rs[2 + j] += gg * x[j];
+                    rs[2 + N + j] += wg * x[j];
+                    rs[2 + 2 * N + j] += xa * x[j];
+                }
+            }
+        }
+    }
+    wave_sum<NR>(rs);
+    const float inv = 1.f / sqrtf(rs[0] / (float)C + eps);
+    const float gwx = rs[1];
+    const float k2 = hs * gwx * inv * inv * inv / (float)C;
+    float v[NS + 2];
+#pragma unroll
+    for (int t = 0; t < NS + 2; ++t) {
+        if (t < N * N) {
+            v[t] = rs[2 + t % N] * (1.f / N);  // dM_ij = u_j / n
+        } else if (t < N * N + N) {
+            v[t] = gwx * inv * (1.f / N);  // dh_post_act_i
+        } else if (t < NS) {
+            const int j = t - N * N - N;
+            v[t] = hs * inv * rs[2 + N + j] - k2 * rs[2 + 2 * N + j];  // dh_pre_act_j
+        } else {
+            v[t] = (t == NS) ? inv : k2;
+        }
+    }
+    float* so = scal_out + b * (NS + 2);
+#pragma unroll
+    for (int t = 0; t < NS + 2; ++t) {
+        if (lane == t) so[t] = v[t];
+    }
+    float ep[kWrapEp];
+#pragma unroll
+    for (int t = 0; t < kWrapEp; ++t) ep[t] = 0.f;
+    ep[0] = cm[0];
+    ep[1] = hp[0];
+    if constexpr (N > 2) {
+        ep[0] += res_weight<2, DECAY>() * cm[2];
+        ep[1] += res_weight<2, DECAY>() * hp[2];
+    }
+    if constexpr (N > 3) {
+        ep[0] += res_weight<3, DECAY>() * cm[3];
+        ep[1] += res_weight<3, DECAY>() * hp[3];
+    }
+    if constexpr (N > 1) {
+        ep[2] = cm[1];
+        ep[3] = hp[1];
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) ep[4 + j] = hp[j];
+    ep[8] = hs * inv;
+    ep[9] = k2;
+    float* eo = ep_out + b * kWrapEp;
+#pragma unroll
+    for (int t = 0; t < kWrapEp; ++t) {
+        if (lane == t) eo[t] = ep[t];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -718,21 +842,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
 }
 
 // ---------------------------------------------------------------------------
-// Projection backward of the wrapper, over channels c (bf16 MFMA 16x16x32
-// with hi/lo split fp32 operands, as proj_bwd_mfma_kernel):
-//   d r[b][c] += s[b] sum_j w_j X_j + sum_o dP[b][o] Phi_r[o][c]
-//   d b[b][c] += s[b] X_1        + sum_o dP[b][o] Phi[o][C + c]
+// Projection backward of the wrapper, dynamic H, pass 2, over channels c
+// (bf16 MFMA 16x16x32 with hi/lo split fp32 operands, as
+// proj_bwd_mfma_kernel):
+//   d r[b][c] = sum_j w_j dX_j + s[b] sum_j w_j X_j + sum_o dP[b][o] Phi_r[o][c]
+//   d b[b][c] = dX_1           + s[b] X_1           + sum_o dP[b][o] Phi[o][C + c]
+//   dX_j = cm_j G + h_pre_j gxa,  gxa = w gy / r - xa k2,  gy = hs G
 //   dPhi_part[tile][o][j*C + c] = sum_{b in tile} dP[b][o] X_j[b][c]
-// with w_j the d r weight of stream j (1, 0, 0.1, 0.01, ...) and Phi_r =
-// sum_j w_j Phi_j: the residual-derived streams share one dx_proj chain.
-// Workgroup = 8 waves x 16 columns; stages of 32 tokens with r, b and the
-// stream parts of d r / d b staged in LDS (two stages in flight in
-// registers); results return in place to the d r / d b tiles and leave with
-// coalesced 16-byte stores.
+//   dw_part[tile][c] = sum_{b in tile} gy xa / r
+// with w_j the d r weight of stream j (1, 0, 0.1, 0.01, ...), Phi_r =
+// sum_j w_j Phi_j (the residual-derived streams share one dx_proj chain) and
+// the per-token factors of wrap_bwd_red_kernel (sum_j w_j dX_j = A_r G +
+// B_r gxa, dX_1 = A_b G + B_b gxa).
+// Every term is summed in fp32 and d r / d b are rounded once to the storage
+// dtype.  Workgroup = 4 waves x 16 columns; stages of 32 tokens with r, b
+// and G staged in LDS (two stages in flight in registers); results go
+// through one LDS tile per output and leave with coalesced 16-byte stores.
 // ---------------------------------------------------------------------------
 typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
 
-template <typename TX> constexpr int wpb_pitch() { return 128 * (int)sizeof(TX) + 8; }
+// Workgroup of the projection backward: 4 waves x 16 channels.  Two such
+// workgroups share a CU (register-bound at two waves per SIMD) and run their
+// stages out of step, so one's loads proceed while the other computes; one
+// 512-lane workgroup per CU moved its waves through the stages in lockstep
+// and left the memory pipe idle during the compute phase (5.05 against
+// about 3.75 ms for the same traffic without compute at C5).
+constexpr int kWpbThreads = 256;
+constexpr int kWpbCols = kWpbThreads / 64 * 16;
+
+template <typename TX> constexpr int wpb_pitch() { return kWpbCols * (int)sizeof(TX) + 8; }
 constexpr int kWDpPitch = 40;
 
 __device__ __forceinline__ void wsplit_pack8(const float (&v)[8], wu32x4_t& hi, wu32x4_t& lo) {
@@ -770,31 +908,37 @@ __device__ __forceinline__ void wlds_put4(char* p, const float (&v)[4]) {
 }
 
 template <typename TX, int N, bool DECAY>
-__global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
-    const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ dP,
-    const float* __restrict__ s_tok, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
-    const float* __restrict__ phi_res, TX* __restrict__ dres, TX* __restrict__ dbr, const float* __restrict__ d_step,
-    int groups, float* __restrict__ dphi_part, int64_t B, int C, int64_t tile) {
-    // bf16 storage: the incoming d r / d b are the row pass's int16 fixed-point
-    // stream parts (fixed_scale) with steps d_step[b][groups][2]: this block's
-    // 128 channels are group blockIdx.x % groups of every token.  The sums are
-    // rounded once to bf16 on the way out.
-    constexpr bool QIN = sizeof(TX) == 2;
+__global__ __launch_bounds__(kWpbThreads) void wrap_proj_bwd_kernel(
+    const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
+    const float* __restrict__ ep, const float* __restrict__ dP, const float* __restrict__ s_tok,
+    const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
+    TX* __restrict__ dres, TX* __restrict__ dbr, float* __restrict__ dw_part, float* __restrict__ dphi_part,
+    int64_t B, int C, int64_t tile) {
     constexpr int NP = 2 * N + N * N;
     static_assert(NP <= 32, "projection rows must fit one 32-row tile");
+    static_assert(N <= 4 && kWrapEp == 12, "factor record: 4 + 4 h_pre + hs/r, k2, spare, s");
     constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
     constexpr int TB = 32;
-    constexpr int CB = 128;
-    constexpr int NT = 512;
+    constexpr int NT = kWpbThreads;
+    constexpr int CB = kWpbCols;
     constexpr int EPV = 16 / sizeof(TX);
-    constexpr int VPR = CB / EPV;
+    constexpr int VPR = CB / EPV;      // 16-byte vectors per r / b tile row
     constexpr int RPP = NT / VPR;
     constexpr int PASSES = TB / RPP;
+    constexpr int GVPR = CB / 4;       // 16-byte vectors per G tile row
+    constexpr int GRPP = NT / GVPR;
+    constexpr int GPASSES = TB / GRPP;
     constexpr int PITCH = wpb_pitch<TX>();
-    __shared__ __align__(16) char tiles_lds[2][4][TB * PITCH];   // [buf][r | b | d r | d b]
-    __shared__ __align__(16) bf16_t dps_lds[2][4][32 * kWDpPitch];
-    __shared__ float s_lds[2][TB];
-    __shared__ float q_lds[2][QIN ? 2 * TB : 1];
+    constexpr int GPITCH = CB * 4 + 16;
+    static_assert(PASSES * RPP == TB && GPASSES * GRPP == TB, "stage rows");
+    // One copy of each stage tile: a stage is committed after the barrier that
+    // ends the compute of the previous one.  out_lds holds the results of the
+    // stage being stored while the next stage is committed.
+    __shared__ __align__(16) char rb_lds[2][TB * PITCH];  // [r | b]
+    __shared__ __align__(16) char g_lds[TB * GPITCH];
+    __shared__ __align__(16) char out_lds[2][TB * PITCH];  // [d r | d b]
+    __shared__ __align__(16) bf16_t dps_lds[4][32 * kWDpPitch];
+    __shared__ __align__(16) float ep_lds[TB][kWrapEp];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -810,12 +954,22 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
     const int lvec = tid % VPR;
     const int64_t lcol = cb0 + (int64_t)lvec * EPV;
     const bool lcol_ok = lcol < C;
+    const int grow = tid / GVPR;
+    const int gvec = tid % GVPR;
+    const int64_t gcol = cb0 + (int64_t)gvec * 4;
+    const bool gcol_ok = gcol < C;
     const bool dp_loader = tid < 256;
     const int dtk = (tid & 255) >> 3;
     const int dpo = (tid & 7) * 4;
+    // factor loaders: lane tid < 3 TB takes piece tid % 3 of token tid / 3;
+    // piece 2 also carries s into the last slot
+    const bool ep_loader = tid < 3 * TB;
+    const int etk = tid / 3;
+    const int epc = tid % 3;
 
     // dx_proj A operands: Phi_r^T and Phi_1^T at column wc0 + lr, o = 8 lg + e
     wu32x4_t prh, prl, pbh, pbl;
+    float wv[4];
     {
         const int64_t c = cb0 + wc0 + lr;
         float vr[8], vb[8];
@@ -835,6 +989,8 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
         }
         wsplit_pack8(vr, prh, prl);
         wsplit_pack8(vb, pbh, pbl);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[i] = wave_on ? w[cb0 + wc0 + 4 * lg + i] : 0.f;
     }
     wf32x4_t accP[NSTR][2];
 #pragma unroll
@@ -842,88 +998,102 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
         accP[j][0] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
         accP[j][1] = wf32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    float dwacc[4] = {0.f, 0.f, 0.f, 0.f};
 
     const int64_t t_begin = (int64_t)blockIdx.y * tile;
     const int64_t t_end = (t_begin + tile < B) ? t_begin + tile : B;
+    const int64_t nrows = t_end > t_begin ? t_end - t_begin : 0;
+
+    // Every global access goes through a buffer resource over this block's
+    // rows [t_begin, t_end) (under 2 GiB each: wrap_proj_bwd_tiles): rows
+    // past t_end and lanes with nothing to load read zeros, and such stores
+    // are dropped, so no access sits behind a branch and the compiler's
+    // wait counts stay exact across the prefetch.  Offsets are bytes.
+    const uint32_t xrow = (uint32_t)C * (uint32_t)sizeof(TX);
+    const buf_rsrc_t rs_r = make_buf_rsrc(res + t_begin * C, (uint32_t)(nrows * xrow));
+    const buf_rsrc_t rs_b = make_buf_rsrc(br + t_begin * C, (uint32_t)(nrows * xrow));
+    const buf_rsrc_t rs_g = make_buf_rsrc(g + t_begin * C, (uint32_t)(nrows * C * 4));
+    const buf_rsrc_t rs_dr = make_buf_rsrc(dres + t_begin * C, (uint32_t)(nrows * xrow));
+    const buf_rsrc_t rs_db = make_buf_rsrc(dbr + t_begin * C, (uint32_t)(nrows * xrow));
+    const buf_rsrc_t rs_p = make_buf_rsrc(dP + t_begin * 32, (uint32_t)(nrows * 128));
+    const buf_rsrc_t rs_e = make_buf_rsrc(ep + t_begin * kWrapEp, (uint32_t)(nrows * kWrapEp * 4));
+    const buf_rsrc_t rs_s = make_buf_rsrc(s_tok + t_begin, (uint32_t)(nrows * 4));
+    // stage-relative lane offsets (kBufOff: nothing to access)
+    const uint32_t xo = lcol_ok ? (uint32_t)lrow * xrow + (uint32_t)(lcol * (int64_t)sizeof(TX)) : kBufOff;
+    const uint32_t go = gcol_ok ? ((uint32_t)grow * (uint32_t)C + (uint32_t)gcol) * 4u : kBufOff;
+    const uint32_t po = dp_loader ? (uint32_t)(dtk * 32 + dpo) * 4u : kBufOff;
+    const uint32_t eo = ep_loader ? (uint32_t)(etk * kWrapEp + 4 * epc) * 4u : kBufOff;
+    const uint32_t so = (ep_loader && epc == 2) ? (uint32_t)etk * 4u : kBufOff;
 
     struct Fetched {
-        uint4 v[4][PASSES];
-        float dp[4], s, q;
+        uint4 v[2][PASSES];
+        uint4 gq[GPASSES];
+        uint4 e, dp;
+        uint32_t s;
     };
     Fetched f0, f1;
-    const TX* srcs[4] = {res, br, dres, dbr};
-    auto fetch = [&](Fetched& f, int64_t t0) __attribute__((always_inline)) {
+    // the stage of rows rel .. rel + TB - 1 (relative to t_begin)
+    auto fetch = [&](Fetched& f, uint32_t rel) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
-            const int64_t t = t0 + lrow + p * RPP;
-            const int64_t off = (t < t_end ? t : t0) * (int64_t)C + (lcol_ok ? lcol : 0);
-#pragma unroll
-            for (int a = 0; a < 4; ++a) f.v[a][p] = ld16_nt(srcs[a] + off);
+            const uint32_t off = xo + (rel + p * RPP) * xrow;
+            f.v[0][p] = buf_ld16<true>(rs_r, off, 0u);
+            f.v[1][p] = buf_ld16<true>(rs_b, off, 0u);
         }
-        const int64_t td = t0 + dtk;
-        const int64_t tdc = td < t_end ? td : t0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) f.dp[q] = dp_loader ? dP[tdc * 32 + dpo + q] : 0.f;
-        f.s = (tid < TB) ? s_tok[(t0 + tid < t_end) ? t0 + tid : t0] : 0.f;
-        f.q = 0.f;
-        if constexpr (QIN) {
-            // lanes TB .. 3 TB - 1: the steps of (token t0 + (tid - TB) / 2,
-            // part (tid - TB) % 2) for this block's 128 channels
-            const int qi = tid - TB;
-            if (qi >= 0 && qi < 2 * TB) {
-                const int64_t tq = t0 + qi / 2;
-                f.q = d_step[((tq < t_end ? tq : t0) * groups + (int)blockIdx.x % groups) * 2 + (qi & 1)];
-            }
-        }
+        for (int p = 0; p < GPASSES; ++p)
+            f.gq[p] = buf_ld16<true>(rs_g, go + (rel + p * GRPP) * (uint32_t)C * 4u, 0u);
+        f.dp = buf_ld16<false>(rs_p, po + rel * 128u, 0u);
+        f.e = buf_ld16<false>(rs_e, eo + rel * (uint32_t)(kWrapEp * 4), 0u);
+        f.s = buf_ld4(rs_s, so + rel * 4u, 0u);
     };
-    auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {
+    auto commit = [&](const Fetched& f) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
-            const uint32_t m = (lcol_ok && t0 + row < t_end) ? 0xffffffffu : 0u;
 #pragma unroll
-            for (int a = 0; a < 4; ++a) {
+            for (int a = 0; a < 2; ++a) {
                 const uint4 v = f.v[a][p];
-                uint2* pw = reinterpret_cast<uint2*>(&tiles_lds[buf][a][row * PITCH + lvec * 16]);
-                pw[0] = make_uint2(v.x & m, v.y & m);
-                pw[1] = make_uint2(v.z & m, v.w & m);
+                uint2* pw = reinterpret_cast<uint2*>(&rb_lds[a][row * PITCH + lvec * 16]);
+                pw[0] = make_uint2(v.x, v.y);
+                pw[1] = make_uint2(v.z, v.w);
             }
         }
+#pragma unroll
+        for (int p = 0; p < GPASSES; ++p)
+            *reinterpret_cast<uint4*>(&g_lds[(grow + p * GRPP) * GPITCH + gvec * 16]) = f.gq[p];
         if (dp_loader) {
-            const bool tok_ok = t0 + dtk < t_end;
+            const uint32_t dw4[4] = {f.dp.x, f.dp.y, f.dp.z, f.dp.w};
             float hi[4], lo[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const float v = (tok_ok && dpo + q < NP) ? f.dp[q] : 0.f;
+                const float v = dpo + q < NP ? __uint_as_float(dw4[q]) : 0.f;
                 hi[q] = bf16_to_f32(f32_to_bf16(v));
                 lo[q] = v - hi[q];
             }
-            *reinterpret_cast<uint2*>(&dps_lds[buf][0][dtk * kWDpPitch + dpo]) =
+            *reinterpret_cast<uint2*>(&dps_lds[0][dtk * kWDpPitch + dpo]) =
                 make_uint2(wpack(hi[0], hi[1]), wpack(hi[2], hi[3]));
-            *reinterpret_cast<uint2*>(&dps_lds[buf][1][dtk * kWDpPitch + dpo]) =
+            *reinterpret_cast<uint2*>(&dps_lds[1][dtk * kWDpPitch + dpo]) =
                 make_uint2(wpack(lo[0], lo[1]), wpack(lo[2], lo[3]));
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                dps_lds[buf][2][(dpo + q) * kWDpPitch + dtk] = f32_to_bf16(hi[q]);
-                dps_lds[buf][3][(dpo + q) * kWDpPitch + dtk] = f32_to_bf16(lo[q]);
+                dps_lds[2][(dpo + q) * kWDpPitch + dtk] = f32_to_bf16(hi[q]);
+                dps_lds[3][(dpo + q) * kWDpPitch + dtk] = f32_to_bf16(lo[q]);
             }
         }
-        if (tid < TB) s_lds[buf][tid] = (t0 + tid < t_end) ? f.s : 0.f;
-        if constexpr (QIN) {
-            const int qi = tid - TB;
-            if (qi >= 0 && qi < 2 * TB) q_lds[buf][qi] = (t0 + qi / 2 < t_end) ? f.q : 0.f;
-        }
+        if (ep_loader)
+            *reinterpret_cast<uint4*>(&ep_lds[etk][4 * epc]) =
+                make_uint4(f.e.x, f.e.y, f.e.z, epc == 2 ? f.s : f.e.w);
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> wu32x4_t {
         const uint4 q = *reinterpret_cast<const uint4*>(p);
         return wu32x4_t{q.x, q.y, q.z, q.w};
     };
-    auto compute = [&](int cur) __attribute__((always_inline)) {
+    auto compute = [&]() __attribute__((always_inline)) {
         if (!wave_on) return;
-        const char* rt = tiles_lds[cur][0];
-        const char* bt = tiles_lds[cur][1];
-        char* drt = tiles_lds[cur][2];
-        char* dbt = tiles_lds[cur][3];
+        const char* rt = rb_lds[0];
+        const char* bt = rb_lds[1];
+        const char* gt = g_lds;
         // dPhi: B operands x_j over tokens 8 lg .. + 7 at column wc0 + lr
         wu32x4_t xh[NSTR], xl[NSTR];
         {
@@ -951,8 +1121,8 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
         }
 #pragma unroll
         for (int ot = 0; ot < 2; ++ot) {
-            const wu32x4_t ah = read16(&dps_lds[cur][2][(16 * ot + lr) * kWDpPitch + 8 * lg]);
-            const wu32x4_t al = read16(&dps_lds[cur][3][(16 * ot + lr) * kWDpPitch + 8 * lg]);
+            const wu32x4_t ah = read16(&dps_lds[2][(16 * ot + lr) * kWDpPitch + 8 * lg]);
+            const wu32x4_t al = read16(&dps_lds[3][(16 * ot + lr) * kWDpPitch + 8 * lg]);
 #pragma unroll
             for (int j = 0; j < NSTR; ++j) {
                 accP[j][ot] = wmfma16x16x32(ah, xh[j], accP[j][ot]);
@@ -960,84 +1130,97 @@ __global__ __launch_bounds__(512) void wrap_proj_bwd_kernel(
                 if constexpr (sizeof(TX) == 4) accP[j][ot] = wmfma16x16x32(ah, xl[j], accP[j][ot]);
             }
         }
-        // dx_proj^T for d r and d b: D[column wc0 + 4 lg + i][token 16 tt + lr]
+        // dx_proj^T for d r and d b: D[column wc0 + 4 lg + i][token 16 tt + lr],
+        // then the stream parts and s X of the same four channels
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 16 * tt + lr;
-            const wu32x4_t bh = read16(&dps_lds[cur][0][t * kWDpPitch + 8 * lg]);
-            const wu32x4_t bl = read16(&dps_lds[cur][1][t * kWDpPitch + 8 * lg]);
-            wf32x4_t dr = wf32x4_t{0.f, 0.f, 0.f, 0.f}, db = dr;
-            dr = wmfma16x16x32(prh, bh, dr);
-            dr = wmfma16x16x32(prl, bh, dr);
-            dr = wmfma16x16x32(prh, bl, dr);
-            db = wmfma16x16x32(pbh, bh, db);
-            db = wmfma16x16x32(pbl, bh, db);
-            db = wmfma16x16x32(pbh, bl, db);
-            const float st = s_lds[cur][t];
-            const int boff = t * PITCH + (wc0 + 4 * lg) * (int)sizeof(TX);  // 8-byte aligned
-            float rv[4], bv[4], drv[4], dbv[4];
+            const wu32x4_t bh = read16(&dps_lds[0][t * kWDpPitch + 8 * lg]);
+            const wu32x4_t bl = read16(&dps_lds[1][t * kWDpPitch + 8 * lg]);
+            wf32x4_t pr = wf32x4_t{0.f, 0.f, 0.f, 0.f}, pb = pr;
+            pr = wmfma16x16x32(prh, bh, pr);
+            pr = wmfma16x16x32(prl, bh, pr);
+            pr = wmfma16x16x32(prh, bl, pr);
+            pb = wmfma16x16x32(pbh, bh, pb);
+            pb = wmfma16x16x32(pbl, bh, pb);
+            pb = wmfma16x16x32(pbh, bl, pb);
+            const float4 e0 = *reinterpret_cast<const float4*>(&ep_lds[t][0]);
+            const float4 e1 = *reinterpret_cast<const float4*>(&ep_lds[t][4]);
+            const float4 e2 = *reinterpret_cast<const float4*>(&ep_lds[t][8]);
+            const float a_r = e0.x, b_r = e0.y, a_b = e0.z, b_b = e0.w;
+            const float hp[4] = {e1.x, e1.y, e1.z, e1.w};
+            const float hsi = e2.x, k2 = e2.y, st = e2.w;
+            const int col = wc0 + 4 * lg;
+            const int boff = t * PITCH + col * (int)sizeof(TX);  // 8-byte aligned
+            float rv[4], bv[4];
             wlds_get4<TX>(rt + boff, rv);
             wlds_get4<TX>(bt + boff, bv);
-            if constexpr (QIN) {
-                fixed_unpack4(*reinterpret_cast<const uint2*>(drt + boff), q_lds[cur][2 * t], drv);
-                fixed_unpack4(*reinterpret_cast<const uint2*>(dbt + boff), q_lds[cur][2 * t + 1], dbv);
-            } else {
-                wlds_get4<TX>(drt + boff, drv);
-                wlds_get4<TX>(dbt + boff, dbv);
-            }
+            const float4 gq = *reinterpret_cast<const float4*>(gt + t * GPITCH + col * 4);
+            const float gv[4] = {gq.x, gq.y, gq.z, gq.w};
+            float drv[4], dbv[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float x[N];
                 wrap_streams<TX, N, DECAY>(rv[i], bv[i], x);
-                float sx_r = x[0];
-                if constexpr (N > 2) sx_r += res_weight<2, DECAY>() * x[2];
-                if constexpr (N > 3) sx_r += res_weight<3, DECAY>() * x[3];
-                drv[i] += st * sx_r + dr[i];
-                dbv[i] += (N > 1 ? st * x[N > 1 ? 1 : 0] : 0.f) + db[i];
+                float xa = 0.f;
+#pragma unroll
+                for (int j = 0; j < N; ++j) xa += hp[j] * x[j];
+                float sx = x[0];
+                if constexpr (N > 2) sx += res_weight<2, DECAY>() * x[2];
+                if constexpr (N > 3) sx += res_weight<3, DECAY>() * x[3];
+                const float gg = gv[i];
+                const float gxa = hsi * (wv[i] * gg) - k2 * xa;
+                dwacc[i] += hsi * (gg * xa);
+                drv[i] = a_r * gg + b_r * gxa + st * sx + pr[i];
+                dbv[i] = (N > 1) ? a_b * gg + b_b * gxa + st * x[N > 1 ? 1 : 0] + pb[i] : pb[i];
             }
-            wlds_put4<TX>(drt + boff, drv);
-            wlds_put4<TX>(dbt + boff, dbv);
+            wlds_put4<TX>(out_lds[0] + boff, drv);
+            wlds_put4<TX>(out_lds[1] + boff, dbv);
         }
     };
-    auto store = [&](int64_t t0, int cur) __attribute__((always_inline)) {
+    auto store = [&](uint32_t rel) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
-            if (lcol_ok && t0 + row < t_end) {
-#pragma unroll
-                for (int a = 2; a < 4; ++a) {
-                    const uint2* ps = reinterpret_cast<const uint2*>(&tiles_lds[cur][a][row * PITCH + lvec * 16]);
-                    const uint2 u0 = ps[0], u1 = ps[1];
-                    TX* dst = (a == 2 ? dres : dbr) + (t0 + row) * (int64_t)C + lcol;
-                    st16_nt(dst, make_uint4(u0.x, u0.y, u1.x, u1.y));
-                }
-            }
+            const uint32_t off = xo + (rel + p * RPP) * xrow;
+            const uint2* pr = reinterpret_cast<const uint2*>(&out_lds[0][row * PITCH + lvec * 16]);
+            const uint2* pb = reinterpret_cast<const uint2*>(&out_lds[1][row * PITCH + lvec * 16]);
+            const uint2 r0 = pr[0], r1 = pr[1], b0 = pb[0], b1 = pb[1];
+            buf_st16<true>(rs_dr, off, 0u, make_uint4(r0.x, r0.y, r1.x, r1.y));
+            buf_st16<true>(rs_db, off, 0u, make_uint4(b0.x, b0.y, b1.x, b1.y));
         }
     };
 
-    if (t_begin < t_end) {
-        fetch(f0, t_begin);
-        commit(f0, t_begin, 0);
-        if (t_begin + TB < t_end) fetch(f1, t_begin + TB);
-    }
+    // Two register sets: stage i+2 is fetched while stage i computes
+    // (fetches and commits past the last row read zeros).
+    auto step = [&](uint32_t r, Fetched& fc, Fetched& fp) __attribute__((always_inline)) {
+        // stage r is in LDS, fc holds stage r + TB, fp is free
+        fetch(fp, r + 2 * TB);
+        compute();
+        __syncthreads();
+        store(r);
+        commit(fc);
+        __syncthreads();
+    };
+    const uint32_t nr = (uint32_t)nrows;
+    fetch(f0, 0u);
+    commit(f0);
+    fetch(f1, TB);
     __syncthreads();
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += 2 * TB) {
-        const int64_t t1 = t0 + TB, t2 = t0 + 2 * TB, t3 = t0 + 3 * TB;
-        if (t2 < t_end) fetch(f0, t2);
-        compute(0);
-        __syncthreads();
-        store(t0, 0);
-        if (t1 < t_end) commit(f1, t1, 1);
-        __syncthreads();
-        if (t1 >= t_end) break;
-        if (t3 < t_end) fetch(f1, t3);
-        compute(1);
-        __syncthreads();
-        store(t1, 1);
-        if (t2 < t_end) commit(f0, t2, 0);
-        __syncthreads();
+    for (uint32_t r0 = 0; r0 < nr; r0 += 2 * TB) {
+        step(r0, f1, f0);
+        if (r0 + TB >= nr) break;
+        step(r0 + TB, f0, f1);
     }
     if (!wave_on) return;
+    // dw partial: dwacc[i] sums this lane's tokens at channel wc0 + 4 lg + i;
+    // the 16 lanes lr of a row hold the block's other tokens
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dwacc[i] = group_sum<16>(dwacc[i]);
+    if (lr == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dw_part[(int64_t)blockIdx.y * C + cb0 + wc0 + 4 * lg + i] = dwacc[i];
+    }
     // dPhi partial: accP[j][ot] register i holds o = 16 ot + 4 lg + i at channel wc0 + lr of stream j
     float* out = dphi_part + (int64_t)blockIdx.y * NP * K;
 #pragma unroll
@@ -1076,11 +1259,11 @@ static const void* wrap_fwd_fn() {
     return nullptr;
 }
 
-template <typename TX, int V, int MODE, bool PF, bool DECAY>
+template <typename TX, int V, bool PF, bool DECAY>
 static const void* wrap_bwd_fn() {
     if constexpr (layer_row_fits(kWrapBwdArrays * 2, V))
-        return PF ? reinterpret_cast<const void*>(&wrap_bwd_pf_kernel<TX, 4, V, MODE, DECAY>)
-                  : reinterpret_cast<const void*>(&wrap_bwd_kernel<TX, 4, V, MODE, DECAY>);
+        return PF ? reinterpret_cast<const void*>(&wrap_bwd_pf_kernel<TX, 4, V, DECAY>)
+                  : reinterpret_cast<const void*>(&wrap_bwd_kernel<TX, 4, V, DECAY>);
     return nullptr;
 }
 
@@ -1110,17 +1293,17 @@ static const void* pick_wrap_fwd(int dt, int vpt, bool decay) {
     return fn;
 }
 
-static const void* pick_wrap_bwd(int dt, int vpt, int mode, bool pf, bool decay) {
+static const void* pick_wrap_bwd(int dt, int vpt, bool pf, bool decay) {
     const void* fn = nullptr;
-#define MHC_WB(TX_, M_)                                                                                         \
-    MHC_WRAP_PICK_VPT(vpt, fn = pf ? (decay ? wrap_bwd_fn<TX_, V_, M_, true, true>()                            \
-                                            : wrap_bwd_fn<TX_, V_, M_, true, false>())                          \
-                                   : (decay ? wrap_bwd_fn<TX_, V_, M_, false, true>()                           \
-                                            : wrap_bwd_fn<TX_, V_, M_, false, false>()))
+#define MHC_WB(TX_)                                                                                    \
+    MHC_WRAP_PICK_VPT(vpt, fn = pf ? (decay ? wrap_bwd_fn<TX_, V_, true, true>()                       \
+                                            : wrap_bwd_fn<TX_, V_, true, false>())                     \
+                                   : (decay ? wrap_bwd_fn<TX_, V_, false, true>()                      \
+                                            : wrap_bwd_fn<TX_, V_, false, false>()))
     if (dt == kBF16) {
-        if (mode == 0) { MHC_WB(bf16_t, 0); } else { MHC_WB(bf16_t, 1); }
+        MHC_WB(bf16_t);
     } else {
-        if (mode == 0) { MHC_WB(float, 0); } else { MHC_WB(float, 1); }
+        MHC_WB(float);
     }
 #undef MHC_WB
     return fn;
@@ -1152,29 +1335,22 @@ int wrap_bwd_grid(int dt, int n, bool decay, int64_t B, int64_t C) {
     (void)n;
     const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapBwdArrays * 2);
     if (t.vpt <= 0) return 1;
-    return wrap_grid(pick_wrap_bwd(dt, t.vpt, 0, wrap_prefetch(t), decay), t.threads, B);
+    return wrap_grid(pick_wrap_bwd(dt, t.vpt, wrap_prefetch(t), decay), t.threads, B);
 }
 
-int wrap_bwd_fixed_groups(int64_t C) {
-    const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapBwdArrays * 2);
-    return t.vpt > 0 ? t.threads / 32 : 0;
-}
-
-hipError_t launch_wrap_bwd(int dt, int n, int mode, bool decay, const float* g, const void* res, const void* br,
+hipError_t launch_wrap_bwd(int dt, int n, bool decay, const float* g, const void* res, const void* br,
                            const float* w, const float* coef, int64_t coef_stride, void* dres, void* dbr,
-                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps, hipStream_t s,
-                           float* d_step) {
+                           float* dw_part, float* scal_out, int grid, int64_t B, int64_t C, float eps,
+                           hipStream_t s) {
     if (n != 4) return hipErrorInvalidValue;
     const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapBwdArrays * 2);
     if (t.vpt <= 0) return hipErrorInvalidValue;
-    const void* fn = pick_wrap_bwd(dt, t.vpt, mode, wrap_prefetch(t), decay);
+    const void* fn = pick_wrap_bwd(dt, t.vpt, wrap_prefetch(t), decay);
     if (!fn) return hipErrorInvalidValue;
     int Ci = (int)C;
-    if (mode == 1 && dt == kBF16 && d_step == nullptr) return hipErrorInvalidValue;
     void* args[] = {(void*)&g, (void*)&res, (void*)&br, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&dres,
-                    (void*)&dbr, (void*)&dw_part, (void*)&scal_out, (void*)&d_step, (void*)&B, (void*)&Ci,
-                    (void*)&eps};
-    const int tok = timing_begin(mode == 0 ? "wrap_bwd" : "wrap_bwd_reduce", s);
+                    (void*)&dbr, (void*)&dw_part, (void*)&scal_out, (void*)&B, (void*)&Ci, (void*)&eps};
+    const int tok = timing_begin("wrap_bwd", s);
     hipError_t e = mhc_launch_kernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);
     return e != hipSuccess ? e : hipGetLastError();
@@ -1214,13 +1390,17 @@ hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const vo
 
 // Token tiles: column blocks x tiles fill two rounds of resident workgroups
 // (rounded down, so a last partial round is nearly full rather than leaving
-// most CUs idle while it runs), at least one.
+// most CUs idle while it runs), at least one, and enough that a tile's rows
+// of G, plus the three stages the pipeline reads past its end, stay under
+// 2 GiB (the kernel's buffer resources and offsets).
+static int64_t wrap_proj_bwd_max_tile(int64_t C) { return ((int64_t(1) << 31) - 1) / (C * 4) - 3 * 32; }
+
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
-    const int64_t gx = (C + 127) / 128;
+    const int64_t gx = (C + kWpbCols - 1) / kWpbCols;
     const void* fn = dt == kBF16 ? reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<bf16_t, 4, true>)
                                  : reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<float, 4, true>);
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 512, 0) != hipSuccess || per_cu < 1) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWpbThreads, 0) != hipSuccess || per_cu < 1) {
         (void)hipGetLastError();
         per_cu = 1;
     }
@@ -1228,30 +1408,54 @@ int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
     const int64_t blocks = (B + 31) / 32;
     if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;
+    const int64_t mt = wrap_proj_bwd_max_tile(C) / 32 * 32;
+    if (mt >= 32 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
     return (int)tiles;
 }
 
-hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
-                                const float* s_tok, const float* phi_pre, const float* phi_post, const float* phi_res,
-                                void* dres, void* dbr, float* dphi_part, int tiles, int64_t B, int64_t C,
-                                hipStream_t s, const float* d_step, int groups) {
+hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const void* res, const void* br,
+                                const float* w, const float* ep, const float* dP, const float* s_tok,
+                                const float* phi_pre, const float* phi_post, const float* phi_res, void* dres,
+                                void* dbr, float* dw_part, float* dphi_part, int tiles, int64_t B, int64_t C,
+                                hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (n != 4 || C % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
-    if (dt == kBF16 && (d_step == nullptr || groups < 1 || C % kFixedGroup != 0)) return hipErrorInvalidValue;
     int64_t tile = (B + tiles - 1) / tiles;
     tile = ((tile + 31) / 32) * 32;
-    const dim3 grid((unsigned)((C + 127) / 128), (unsigned)tiles);
+    if (tile > wrap_proj_bwd_max_tile(C)) return hipErrorInvalidValue;  // offsets past 2 GiB
+    const dim3 grid((unsigned)((C + kWpbCols - 1) / kWpbCols), (unsigned)tiles);
     const int tok = timing_begin("wrap_proj_bwd", s);
 #define MHC_WPB(TX_, D_)                                                                                          \
-    MHC_LAUNCH_GGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(512), 0, s, (const TX_*)res, (const TX_*)br, \
-                       dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, d_step, groups, dphi_part, B,  \
-                       (int)C, tile)
+    MHC_LAUNCH_GGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(kWpbThreads), 0, s, g, (const TX_*)res,        \
+                       (const TX_*)br, w, ep, dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, dw_part, \
+                       dphi_part, B, (int)C, tile)
     if (dt == kBF16) {
         if (decay) { MHC_WPB(bf16_t, true); } else { MHC_WPB(bf16_t, false); }
     } else {
         if (decay) { MHC_WPB(float, true); } else { MHC_WPB(float, false); }
     }
 #undef MHC_WPB
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_wrap_bwd_red(int dt, int n, bool decay, const float* g, const void* res, const void* br,
+                               const float* w, const float* coef, int64_t coef_stride, float* scal_out,
+                               float* ep_out, int64_t B, int64_t C, float eps, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (n != 4 || C % 4 != 0) return hipErrorInvalidValue;
+    const int64_t blocks = (B + 3) / 4;  // one token per wave, four waves per workgroup
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const int tok = timing_begin("wrap_bwd_reduce", s);
+#define MHC_WR(TX_, D_)                                                                                        \
+    MHC_LAUNCH_GGL((wrap_bwd_red_kernel<TX_, 4, D_>), dim3((unsigned)blocks), dim3(256), 0, s, g,             \
+                       (const TX_*)res, (const TX_*)br, w, coef, coef_stride, scal_out, ep_out, B, (int)C, eps)
+    if (dt == kBF16) {
+        if (decay) { MHC_WR(bf16_t, true); } else { MHC_WR(bf16_t, false); }
+    } else {
+        if (decay) { MHC_WR(float, true); } else { MHC_WR(float, false); }
+    }
+#undef MHC_WR
     timing_end(tok, s);
     return hipGetLastError();
 }
