@@ -555,7 +555,9 @@ __global__ __launch_bounds__(256) void wrap_bwd_red_kernel(const float* __restri
 // forms the stream operands of its rows in registers and runs them against
 // the Phi fragments at k = j*C + c (1 KB contiguous loads in the fragment
 // order of phi_split_kernel).  bf16 storage: every stream is exact in bf16,
-// so P = X.(hi + mid + lo) (three MFMAs per stream and N-tile).  fp32
+// so P = X.(hi + mid + lo) (three MFMAs per stream and N-tile; two, hi and
+// mid, for the decay streams, whose lo term is below 2^-17 of a term at
+// most 0.1 of the residual's), and sum X^2 runs on packed pairs.  fp32
 // storage: X is split into hi/mid/lo too and the six products down to 2^-16
 // relative weight are kept, as in proj_mfma_kernel.  p_part[ks][B][32],
 // ss_part[ks][B].
@@ -587,19 +589,30 @@ __device__ __forceinline__ wu32x4_t wop(const uint4& q) { return wu32x4_t{q.x, q
 
 template <typename TX> constexpr int wproj_mt() { return sizeof(TX) == 2 ? 4 : 2; }
 
+typedef __bf16 wbf16x2_t __attribute__((ext_vector_type(2)));
+
+// ss + a.x^2 + a.y^2 for a packed bf16 pair (v_dot2c_f32_bf16; the squares
+// of bf16 values are exact in fp32)
+__device__ __forceinline__ float wsq2(uint32_t a, float ss) {
+    const wbf16x2_t v = __builtin_bit_cast(wbf16x2_t, a);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
+}
+
+// Phi planes a stream's products use: bf16 storage keeps hi and mid only for
+// the decay streams (j >= 2: X_j <= 0.1 |r|), whose lo term is below 2^-17
+// of an already small term.
+template <typename TX, int J> constexpr int wproj_planes() { return (sizeof(TX) == 2 && J >= 2) ? 2 : 3; }
+
 // Stream J's MFMA products for one M-tile: r/b hold the tile row's 8
-// channels (raw 16-byte pieces and their values), g the stream's 6 Phi
-// fragments (plane p, N-tile nt at index 2p + nt).
+// channels (raw 16-byte pieces and their values), g the stream's Phi
+// fragments (plane p, N-tile nt at index 2p + nt).  bf16 storage: the stream
+// operand is the stored bf16 pair (r and b as loaded; the decay streams
+// packed from r * 0.1^(j-1) by the round-to-nearest-even conversion that
+// stores them), and sum X^2 runs on packed pairs.
 template <typename TX, int J, bool DECAY>
 __device__ __forceinline__ void wproj_stream(const uint4 (&rw)[sizeof(TX) / 2], const uint4 (&bw)[sizeof(TX) / 2],
                                              const float (&r)[8], const float (&b)[8], const uint4* g,
                                              wf32x4_t (&acc)[2], float& ss) {
-    float x[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        x[e] = wrap_stream<TX, J, DECAY>(r[e], b[e]);
-        ss += x[e] * x[e];
-    }
     if constexpr (sizeof(TX) == 2) {
         wu32x4_t a;
         if constexpr (J == 0) {
@@ -607,15 +620,25 @@ __device__ __forceinline__ void wproj_stream(const uint4 (&rw)[sizeof(TX) / 2], 
         } else if constexpr (J == 1) {
             a = wop(bw[0]);
         } else {
+            constexpr float m = decay_mult<J>();
 #pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = wpack(x[2 * e], x[2 * e + 1]);  // exact: x is a bf16 value
+            for (int e = 0; e < 4; ++e) a[e] = DECAY ? wpack(r[2 * e] * m, r[2 * e + 1] * m) : 0u;
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss = wsq2(a[e], ss);
+        constexpr int PL = wproj_planes<TX, J>();
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
-            for (int p = 0; p < 3; ++p) acc[nt] = wmfma16x16x32(a, wop(g[2 * p + nt]), acc[nt]);
+            for (int p = 0; p < PL; ++p) acc[nt] = wmfma16x16x32(a, wop(g[2 * p + nt]), acc[nt]);
         }
     } else {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            x[e] = wrap_stream<TX, J, DECAY>(r[e], b[e]);
+            ss += x[e] * x[e];
+        }
         wu32x4_t ah, am, al;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -655,6 +678,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
     constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
     constexpr int NHA = NSTR < 2 ? NSTR : 2;           // streams of the first Phi half
     constexpr int NHB = NSTR - NHA;
+    constexpr int PLB = wproj_planes<TX, 2>();  // planes of the decay streams
     static_assert(N == 4, "wrapper projection is instantiated for n = 4");
     static_assert(PASSES * RPP == TB, "stage rows");
     static_assert(3 * 9 * MT * 64 * 4 <= 2 * 2 * TB * PITCH, "epilogue reuses the stage buffers");
@@ -711,8 +735,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
         }
     };
     // Phi fragments of streams j0 .. j0+nj-1 at this wave's 32 channels of
-    // stage st (clamped to the last k step: past ce the operands are zero)
-    auto fetch_phi = [&](uint4* g, int j0, int nj, int64_t st) __attribute__((always_inline)) {
+    // stage st (clamped to the last k step: past ce the operands are zero);
+    // pl planes each
+    auto fetch_phi = [&](uint4* g, int j0, int nj, int pl, int64_t st) __attribute__((always_inline)) {
         const int64_t c0 = cb + srot(st) * KS + wave * 32;
 #pragma unroll
         for (int jj = 0; jj < nj; ++jj) {
@@ -720,7 +745,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
             kstep = kstep < ksteps ? kstep : ksteps - 1;
             const uint32_t so = (uint32_t)(kstep * 64 * 16);
 #pragma unroll
-            for (int q = 0; q < 6; ++q)
+            for (int q = 0; q < 2 * pl; ++q)
                 g[6 * jj + q] = buf_ld16<false, true>(prs, (uint32_t)((q * ksteps * 64 + lane) * 16), so);
         }
     };
@@ -776,8 +801,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
 
     if (nst > 0) {
         fetch_x(0);
-        fetch_phi(GA, 0, NHA, 0);
-        if constexpr (NHB > 0) fetch_phi(GB, 2, NHB, 0);
+        fetch_phi(GA, 0, NHA, 3, 0);
+        if constexpr (NHB > 0) fetch_phi(GB, 2, NHB, PLB, 0);
         commit(0, 0);
         __syncthreads();
         for (int64_t st = 0; st < nst; ++st) {
@@ -785,10 +810,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
             fetch_x(clampst(st + 1));
             __builtin_amdgcn_sched_barrier(0);
             compute_half(buf, GA, I0{}, IHA{});
-            fetch_phi(GA, 0, NHA, clampst(st + 1));
+            fetch_phi(GA, 0, NHA, 3, clampst(st + 1));
             if constexpr (NHB > 0) {
                 compute_half(buf, GB, I2{}, IHB{});
-                fetch_phi(GB, 2, NHB, clampst(st + 1));
+                fetch_phi(GB, 2, NHB, PLB, clampst(st + 1));
             }
             commit(clampst(st + 1), buf ^ 1);
             __syncthreads();
