@@ -165,6 +165,97 @@ __global__ MHC_ROW_BOUNDS(false) void wrap_fwd_kernel(const TX* __restrict__ res
     wrap_fwd_token<TX, N, VPT, DECAY>(b, coef, coef_stride, wv, rv, bv, out, C, eps, red);
 }
 
+// One token per wave, bf16 storage, C = 256 KQ: the row's 4-channel chunks
+// (lane l takes chunks l, l + 64, ..., KQ of them) stay in registers as
+// packed words, the row sum is a wave sum (no barrier), and the weight is
+// staged once per workgroup in LDS.  The second pass rebuilds the streams
+// from the packed words (kept from being hoisted by an empty asm that
+// "changes" them) rather than holding the row's fp32 values.  Rows that are
+// not whole rounds of 64 chunks run wrap_fwd_kernel: masking the last round
+// took the register count from 141 to about 200 at KQ = 28.
+template <int KQ, bool DECAY>
+__global__ __launch_bounds__(256) void wrap_fwd_wave_kernel(const bf16_t* __restrict__ res, const bf16_t* __restrict__ br,
+                                                            const float* __restrict__ w, const float* __restrict__ coef,
+                                                            int64_t coef_stride, float* __restrict__ out, int64_t B,
+                                                            int C, float eps) {
+    constexpr int N = 4;
+    extern __shared__ __align__(16) float wl[];  // C floats
+    for (int i = threadIdx.x; i < C; i += blockDim.x) wl[i] = w[i];
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t b = (int64_t)blockIdx.x * (blockDim.x / kWave) + (int64_t)wave_uniform(threadIdx.x / kWave);
+    if (b >= B) return;
+    uint32_t rw[KQ][2], bw[KQ][2];
+    const bf16_t* rb = res + b * (int64_t)C;
+    const bf16_t* bb = br + b * (int64_t)C;
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+        const int c0 = (k * kWave + lane) * 4;
+        const uint2 a = ld8_nt(rb + c0), c = ld8_nt(bb + c0);
+        rw[k][0] = a.x; rw[k][1] = a.y;
+        bw[k][0] = c.x; bw[k][1] = c.y;
+    }
+    const float* cf = coef + b * coef_stride;
+    float hp[N], cm[N], hs = 0.f;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        hp[j] = cf[j];
+        hs += cf[N + j];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < N; ++i) s += cf[2 * N + i * N + j];
+        cm[j] = s * (1.f / N);
+    }
+    hs *= 1.f / N;
+    auto unpack = [&](int k, int e, float& r, float& bv) __attribute__((always_inline)) {
+        const uint32_t wr = rw[k][e >> 1], wb = bw[k][e >> 1];
+        r = __uint_as_float((e & 1) ? (wr & 0xffff0000u) : (wr << 16));
+        bv = __uint_as_float((e & 1) ? (wb & 0xffff0000u) : (wb << 16));
+    };
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float r, bv, x[N];
+            unpack(k, e, r, bv);
+            wrap_streams<bf16_t, N, DECAY>(r, bv, x);
+            float xa = 0.f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) xa += hp[j] * x[j];
+            ss += xa * xa;
+        }
+    }
+    ss = group_sum<kWave>(ss);
+    const float inv = 1.f / sqrtf(ss / (float)C + eps);
+    const float hsi = hs * inv;
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) asm volatile("" : "+v"(rw[k][0]), "+v"(rw[k][1]), "+v"(bw[k][0]), "+v"(bw[k][1]));
+    float* ob = out + b * (int64_t)C;
+#pragma unroll
+    for (int k = 0; k < KQ; ++k) {
+        const int q = k * kWave + lane;
+        const float4 wq = *reinterpret_cast<const float4*>(&wl[q * 4]);
+        const float wv[4] = {wq.x, wq.y, wq.z, wq.w};
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float r, bv, x[N];
+            unpack(k, e, r, bv);
+            wrap_streams<bf16_t, N, DECAY>(r, bv, x);
+            float xa = 0.f, s = 0.f;
+#pragma unroll
+            for (int j = 0; j < N; ++j) {
+                xa += hp[j] * x[j];
+                s += cm[j] * x[j];
+            }
+            o[e] = s + hsi * (xa * wv[e]);
+        }
+        st16_nt(ob + q * 4, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                       __float_as_uint(o[3])));
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Backward row pass.  Per token the block forms, in one reduction,
 //   ss = sum xa^2, gwx = sum G w xa, u_j = sum G X_j, v_j = sum G w X_j,
@@ -1336,11 +1427,43 @@ static const void* pick_wrap_bwd(int dt, int vpt, bool pf, bool decay) {
 
 static bool wrap_prefetch(const RowTiling& t) { return t.threads <= 256; }
 
+// Chunks per lane of the one-token-per-wave forward (bf16 rows of
+// C = 256 KQ, KQ = 4, 8, ..., 32), 0 where the workgroup-per-token kernel runs.
+static int wrap_fwd_wave_kq(int dt, int64_t C) {
+    if (dt != kBF16 || C % 1024 != 0 || C > 8192) return 0;
+    return (int)(C / 256);
+}
+
 hipError_t launch_wrap_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
                            const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
                            hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (n != 4) return hipErrorInvalidValue;
+    if (const int kq = wrap_fwd_wave_kq(dt, C)) {
+        const int64_t blocks = (B + 3) / 4;  // one token per wave
+        if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+        const void* fn = nullptr;
+#define MHC_WFW(KQ_) fn = decay ? reinterpret_cast<const void*>(&wrap_fwd_wave_kernel<KQ_, true>) \
+                                : reinterpret_cast<const void*>(&wrap_fwd_wave_kernel<KQ_, false>)
+        switch (kq) {
+            case 4: MHC_WFW(4); break;
+            case 8: MHC_WFW(8); break;
+            case 12: MHC_WFW(12); break;
+            case 16: MHC_WFW(16); break;
+            case 20: MHC_WFW(20); break;
+            case 24: MHC_WFW(24); break;
+            case 28: MHC_WFW(28); break;
+            default: MHC_WFW(32); break;
+        }
+#undef MHC_WFW
+        int Ci = (int)C;
+        void* args[] = {(void*)&res, (void*)&br, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&out,
+                        (void*)&B, (void*)&Ci, (void*)&eps};
+        const int tok = timing_begin("wrap_fwd", s);
+        hipError_t e = mhc_launch_kernel(fn, dim3((unsigned)blocks), dim3(256), args, (size_t)C * 4, s);
+        timing_end(tok, s);
+        return e != hipSuccess ? e : hipGetLastError();
+    }
     const RowTiling t = choose_row_tiling(C, kLayerWC, kWrapFwdArrays * 2, 512);
     if (t.vpt <= 0) return hipErrorInvalidValue;
     const void* fn = pick_wrap_fwd(dt, t.vpt, decay);
