@@ -619,7 +619,7 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel-steps", type=int, default=10, help="steps of the per-kernel timing pass")
     ap.add_argument("--extra", action="append", default=None, choices=sorted(WORKLOADS),
                     help="with the default static workload: also measure these workloads as sub-records "
-                         "(default: dynamic, the reference layer's default path)")
+                         "(default: dynamic, the reference layer's default path, and wrapper)")
     ap.add_argument("--no-extra", action="store_true", help="no sub-records")
     ap.add_argument("--extra-steps", type=int, default=20, help="timed steps of each sub-record")
     a = ap.parse_args(argv)
@@ -631,7 +631,7 @@ def main(argv=None) -> int:
     if a.no_extra:
         a.extra = []
     elif a.extra is None:
-        a.extra = ["dynamic"]
+        a.extra = ["dynamic", "wrapper"]
 
     import torch
 
