@@ -1311,59 +1311,67 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
 
     const int64_t t_begin = (int64_t)blockIdx.y * tile;
     const int64_t t_end = (t_begin + tile < B) ? t_begin + tile : B;
+    const int64_t nrows = t_end > t_begin ? t_end - t_begin : 0;
+
+    // Every global access goes through a buffer resource over this block's
+    // rows [t_begin, t_end) (under 2 GiB each: proj_bwd_tiles): rows past
+    // t_end and lanes with nothing to load read zeros and such stores are
+    // dropped, so no access sits behind a branch and the compiler's wait
+    // counts stay exact across the two-stage prefetch.  Offsets are bytes.
+    const uint32_t xrow = (uint32_t)(K * (int64_t)sizeof(TX));
+    const buf_rsrc_t rs_x = make_buf_rsrc(x + t_begin * K, (uint32_t)(nrows * xrow));
+    const buf_rsrc_t rs_dx = make_buf_rsrc(dx + t_begin * K, (uint32_t)(nrows * xrow));
+    const buf_rsrc_t rs_p = make_buf_rsrc(dP + t_begin * dp_stride, (uint32_t)(nrows * dp_stride * 4));
+    const buf_rsrc_t rs_s = make_buf_rsrc(HAS_S ? s_tok + t_begin : s_tok, HAS_S ? (uint32_t)(nrows * 4) : 0u);
+    const int grp = QIN ? (int)((kb0 % C) / kFixedGroup) % groups : 0;
+    const buf_rsrc_t rs_q =
+        make_buf_rsrc(QIN ? dx_step + t_begin * groups : dx_step, QIN ? (uint32_t)(nrows * groups * 4) : 0u);
+    const uint32_t xo = lcol_ok ? (uint32_t)lrow * xrow + (uint32_t)(lcol * (int64_t)sizeof(TX)) : kBufOff;
+    const uint32_t po = (uint32_t)(dtk * dp_stride + dpo) * 4u;
+    const uint32_t so = tid < TB ? (uint32_t)tid * 4u : kBufOff;
+    const uint32_t qo = tid < TB ? (uint32_t)(tid * groups + grp) * 4u : kBufOff;
 
     // Two register sets of fetched stages: stage i+2 is fetched while stage i
     // computes and stage i+1 (fetched one stage earlier) moves into LDS.
     struct Fetched {
-        uint4 x[PASSES], d[PASSES];
-        float dp[4], s, q;
+        uint4 x[PASSES], d[PASSES], dp;
+        uint32_t s, q;
     };
     Fetched f0, f1;
-    auto fetch = [&](Fetched& f, int64_t t0) __attribute__((always_inline)) {
+    // the stage of rows rel .. rel + TB - 1 (relative to t_begin)
+    auto fetch = [&](Fetched& f, uint32_t rel) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
-            const int64_t t = t0 + lrow + p * RPP;
-            const int64_t off = (t < t_end ? t : t0) * K + (lcol_ok ? lcol : 0);
-            f.x[p] = ld16_nt(x + off);
-            if constexpr (ACC) f.d[p] = ld16_nt(dx + off);
+            const uint32_t off = xo + (rel + p * RPP) * xrow;
+            f.x[p] = buf_ld16<true>(rs_x, off, 0u);
+            if constexpr (ACC) f.d[p] = buf_ld16<true>(rs_dx, off, 0u);
         }
-        const int64_t td = t0 + dtk;
-        const int64_t tdc = td < t_end ? td : t0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) f.dp[q] = dP[tdc * dp_stride + (dpo + q < np ? dpo + q : 0)];
-        f.s = 0.f;
-        if constexpr (HAS_S) {
-            if (tid < TB) f.s = s_tok[(t0 + tid < t_end) ? t0 + tid : t0];
-        }
-        f.q = 0.f;
-        if constexpr (QIN) {
-            const int grp = (int)((kb0 % C) / kFixedGroup) % groups;
-            if (tid < TB) f.q = dx_step[((t0 + tid < t_end) ? t0 + tid : t0) * groups + grp];
-        }
+        f.dp = buf_ld16<false>(rs_p, po + rel * (uint32_t)dp_stride * 4u, 0u);
+        f.s = HAS_S ? buf_ld4(rs_s, so + rel * 4u, 0u) : 0u;
+        f.q = QIN ? buf_ld4(rs_q, qo + rel * (uint32_t)groups * 4u, 0u) : 0u;
     };
-    auto commit = [&](const Fetched& f, int64_t t0, int buf) __attribute__((always_inline)) {
+    auto commit = [&](const Fetched& f, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
-            const uint32_t m = (lcol_ok && t0 + row < t_end) ? 0xffffffffu : 0u;  // zero masked rows
             const uint4 vx = f.x[p];
             uint2* px = reinterpret_cast<uint2*>(&x_lds[row * PITCH + lvec * 16]);
-            px[0] = make_uint2(vx.x & m, vx.y & m);
-            px[1] = make_uint2(vx.z & m, vx.w & m);
+            px[0] = make_uint2(vx.x, vx.y);
+            px[1] = make_uint2(vx.z, vx.w);
             if constexpr (ACC) {
                 const uint4 vd = f.d[p];
                 uint2* pd = reinterpret_cast<uint2*>(&dx_lds[buf][row * PITCH + lvec * 16]);
-                pd[0] = make_uint2(vd.x & m, vd.y & m);
-                pd[1] = make_uint2(vd.z & m, vd.w & m);
+                pd[0] = make_uint2(vd.x, vd.y);
+                pd[1] = make_uint2(vd.z, vd.w);
             }
         }
         // dP of token dtk, o = dpo .. dpo + 3: split once into hi / lo bf16,
         // token-major (one 8-byte write each) and o-major copies
-        const bool tok_ok = t0 + dtk < t_end;
+        const uint32_t dw4[4] = {f.dp.x, f.dp.y, f.dp.z, f.dp.w};
         float hi[4], lo[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float v = (tok_ok && dpo + q < np) ? f.dp[q] : 0.f;
+            const float v = dpo + q < np ? __uint_as_float(dw4[q]) : 0.f;
             hi[q] = bf16_to_f32(f32_to_bf16(v));
             lo[q] = v - hi[q];
         }
@@ -1377,10 +1385,10 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
             dps_lds[3][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(lo[q]);
         }
         if constexpr (HAS_S) {
-            if (tid < TB) s_lds[tid] = (t0 + tid < t_end) ? f.s : 0.f;
+            if (tid < TB) s_lds[tid] = __uint_as_float(f.s);
         }
         if constexpr (QIN) {
-            if (tid < TB) q_lds[tid] = (t0 + tid < t_end) ? f.q : 0.f;
+            if (tid < TB) q_lds[tid] = __uint_as_float(f.q);
         }
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> u32x4_t {
@@ -1450,40 +1458,37 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
             }
         }
     };
-    auto store = [&](int64_t t0, int cur) __attribute__((always_inline)) {  // dx tile -> HBM, 16-byte pieces
+    auto store = [&](uint32_t rel, int cur) __attribute__((always_inline)) {  // dx tile -> HBM, 16-byte pieces
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
-            if (lcol_ok && t0 + row < t_end) {
-                const uint2* ps = reinterpret_cast<const uint2*>(&dx_lds[cur][row * PITCH + lvec * 16]);
-                const uint2 u0 = ps[0], u1 = ps[1];
-                st16_nt(dx + (t0 + row) * K + lcol, make_uint4(u0.x, u0.y, u1.x, u1.y));
-            }
+            const uint2* ps = reinterpret_cast<const uint2*>(&dx_lds[cur][row * PITCH + lvec * 16]);
+            const uint2 u0 = ps[0], u1 = ps[1];
+            buf_st16<true>(rs_dx, xo + (rel + p * RPP) * xrow, 0u, make_uint4(u0.x, u0.y, u1.x, u1.y));
         }
     };
 
-    if (t_begin < t_end) {
-        fetch(f0, t_begin);
-        commit(f0, t_begin, 0);
-        if (t_begin + TB < t_end) fetch(f1, t_begin + TB);
-    }
+    // fetches and commits past the last row read zeros
+    const uint32_t nr = (uint32_t)nrows;
+    fetch(f0, 0u);
+    commit(f0, 0);
+    fetch(f1, TB);
     __syncthreads();
-    for (int64_t t0 = t_begin; t0 < t_end; t0 += 2 * TB) {
-        // even stage t0 in LDS buffer 0; f1 holds stage t0 + TB
-        const int64_t t1 = t0 + TB, t2 = t0 + 2 * TB, t3 = t0 + 3 * TB;
-        if (t2 < t_end) fetch(f0, t2);
+    for (uint32_t r0 = 0; r0 < nr; r0 += 2 * TB) {
+        // even stage r0 in LDS buffer 0; f1 holds stage r0 + TB
+        fetch(f0, r0 + 2 * TB);
         compute(0);
         __syncthreads();  // the dx tile is complete
-        store(t0, 0);
-        if (t1 < t_end) commit(f1, t1, 1);
+        store(r0, 0);
+        commit(f1, 1);
         __syncthreads();
-        if (t1 >= t_end) break;
-        // odd stage t1 in LDS buffer 1; f0 holds stage t2
-        if (t3 < t_end) fetch(f1, t3);
+        if (r0 + TB >= nr) break;
+        // odd stage r0 + TB in LDS buffer 1; f0 holds stage r0 + 2 TB
+        fetch(f1, r0 + 3 * TB);
         compute(1);
         __syncthreads();
-        store(t1, 1);
-        if (t2 < t_end) commit(f0, t2, 0);
+        store(r0 + TB, 1);
+        commit(f0, 0);
         __syncthreads();
     }
     if (!wave_on) return;
@@ -2407,6 +2412,12 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
 // Token tiles of the projection backward: column blocks x tiles fill two
 // rounds of resident workgroups (rounded down, so a last partial round is
 // nearly full rather than leaving most CUs idle while it runs), at least one.
+// A token tile's rows of x / dx, plus the three stages the pipeline reads
+// past its end, under 2 GiB (the kernel's buffer resources and offsets).
+static int64_t proj_bwd_max_tile(int x_dtype, int64_t K) {
+    return ((int64_t(1) << 31) - 1) / (K * (x_dtype == kBF16 ? 2 : 4)) - 3 * 32;
+}
+
 int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
     const int64_t gx = (K + 127) / 128;
     const void* fn = x_dtype == kBF16 ? reinterpret_cast<const void*>(&proj_bwd_mfma_kernel<bf16_t, true, true>)
@@ -2420,6 +2431,8 @@ int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
     const int64_t blocks = (B + 31) / 32;
     if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;
+    const int64_t mt = proj_bwd_max_tile(x_dtype, K) / 32 * 32;
+    if (mt >= 32 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
     return (int)tiles;
 }
 
@@ -2436,6 +2449,7 @@ hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_s
     // token tile: a multiple of the 32-token block
     int64_t tile = (B + tiles - 1) / tiles;
     tile = ((tile + 31) / 32) * 32;
+    if (tile > proj_bwd_max_tile(x_dtype, K)) return hipErrorInvalidValue;  // offsets past 2 GiB
     const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
 #define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \
     MHC_LAUNCH_GGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP, dp_stride,  \

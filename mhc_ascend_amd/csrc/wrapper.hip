@@ -985,6 +985,10 @@ typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
 // about 3.75 ms for the same traffic without compute at C5).
 constexpr int kWpbThreads = 256;
 constexpr int kWpbCols = kWpbThreads / 64 * 16;
+// Waves per SIMD the register allocation targets: three for bf16 storage
+// (168 registers; the stages' chains of LDS reads and MFMAs are latency-
+// bound at two), two for fp32 storage, whose wider operands would spill.
+template <typename TX> constexpr int kWpbWaves() { return sizeof(TX) == 2 ? 3 : 2; }
 
 template <typename TX> constexpr int wpb_pitch() { return kWpbCols * (int)sizeof(TX) + 8; }
 constexpr int kWDpPitch = 40;
@@ -1024,7 +1028,7 @@ __device__ __forceinline__ void wlds_put4(char* p, const float (&v)[4]) {
 }
 
 template <typename TX, int N, bool DECAY>
-__global__ __launch_bounds__(kWpbThreads) void wrap_proj_bwd_kernel(
+__global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWpbWaves<TX>()))) void wrap_proj_bwd_kernel(
     const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
     const float* __restrict__ ep, const float* __restrict__ dP, const float* __restrict__ s_tok,
     const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
