@@ -313,9 +313,12 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
     const float inv = 1.f / r;
     const float k2 = tot[1] * inv * inv * inv / (float)C;
 
+    // Global stores of this routine go through resources with out-of-range
+    // offsets for lanes that store nothing: no store sits behind a branch
+    // (the caller's prefetch of the next token keeps exact wait counts).
+    float v = 0.f;
     if (threadIdx.x < NS + 2) {
         const int t = threadIdx.x;
-        float v;
         if (t < N * N) {
             v = tot[2 + t];
         } else if (t < N * N + N) {
@@ -326,11 +329,11 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
         } else {
             v = (t == NS) ? inv : k2;
         }
-        if (MODE == 0) {
-            sacc += v;
-        } else {
-            scal_out[b * (NS + 2) + t] = v;
-        }
+        if (MODE == 0) sacc += v;
+    }
+    if constexpr (MODE != 0) {
+        const buf_rsrc_t srs = make_buf_rsrc(scal_out + b * (NS + 2), (uint32_t)((NS + 2) * 4));
+        buf_st4(srs, threadIdx.x < NS + 2 ? (uint32_t)threadIdx.x * 4u : kBufOff, 0u, v);
     }
 
     if constexpr (MODE == 1 && sizeof(TX) == 2) {
@@ -363,17 +366,19 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
             }
         }
         const FixedScale fs = fixed_scale(half_wave_max_nonneg(m));
-        char* db = reinterpret_cast<char*>(dx + b * (int64_t)N * C);
+        const buf_rsrc_t drs = make_buf_rsrc(dx + b * (int64_t)N * C, (uint32_t)((int64_t)N * C * 2));
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
             const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-            if (c0 < C) {
+            const uint32_t o0 = c0 < C ? (uint32_t)c0 * 2u : kBufOff;
 #pragma unroll
-                for (int j = 0; j < N; ++j) st8_nt(db + ((int64_t)j * C + c0) * 2, fixed_pack4(a[j][k], fs.inv));
-            }
+            for (int j = 0; j < N; ++j) buf_st8<true>(drs, o0 + (uint32_t)(j * C * 2), 0u, fixed_pack4(a[j][k], fs.inv));
         }
-        if ((threadIdx.x & 31) == 0) dx_step[b * (blockDim.x / 32) + threadIdx.x / 32] = fs.step;
+        const int ng = blockDim.x / 32;
+        const buf_rsrc_t qrs = make_buf_rsrc(dx_step + b * ng, (uint32_t)(ng * 4));
+        buf_st4(qrs, (threadIdx.x & 31) == 0 ? (uint32_t)(threadIdx.x / 32) * 4u : kBufOff, 0u, fs.step);
     } else {
+        const buf_rsrc_t drs = make_buf_rsrc(dx + b * (int64_t)N * C, (uint32_t)((int64_t)N * C * (int64_t)sizeof(TX)));
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
             const int c0 = (k * blockDim.x + threadIdx.x) * WC;
@@ -389,19 +394,24 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
                 gxa[e] = wv[k][e] * gy * inv - xa * k2;
                 dwacc[k][e] += gy * xa * inv;
             }
-            if (c0 < C) {
-                TX* db = dx + b * (int64_t)N * C;
+            const uint32_t o0 = c0 < C ? (uint32_t)c0 * (uint32_t)sizeof(TX) : kBufOff;
 #pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    float d[WC];
+            for (int j = 0; j < N; ++j) {
+                float d[WC];
 #pragma unroll
-                    for (int e = 0; e < WC; ++e) {
-                        float s = cfv[j] * gxa[e];
+                for (int e = 0; e < WC; ++e) {
+                    float s = cfv[j] * gxa[e];
 #pragma unroll
-                        for (int i = 0; i < N; ++i) s += cfv[2 * N + i * N + j] * gv[i][k][e];
-                        d[e] = s;
-                    }
-                    store_run_nt<TX, WC>(db + (int64_t)j * C + c0, d);
+                    for (int i = 0; i < N; ++i) s += cfv[2 * N + i * N + j] * gv[i][k][e];
+                    d[e] = s;
+                }
+                const uint32_t o = o0 + (uint32_t)(j * C * (int)sizeof(TX));
+                static_assert(WC == 4, "4-channel chunks: one 16-byte (fp32) or 8-byte (bf16) store");
+                if constexpr (sizeof(TX) == 4) {
+                    buf_st16<true>(drs, o, 0u, make_uint4(__float_as_uint(d[0]), __float_as_uint(d[1]),
+                                                          __float_as_uint(d[2]), __float_as_uint(d[3])));
+                } else {
+                    buf_st8<true>(drs, o, 0u, make_uint2(pack_bf16x2(d[0], d[1]), pack_bf16x2(d[2], d[3])));
                 }
             }
         }
@@ -435,26 +445,22 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
         RawRows<TX, N, VPT, WC> xA, xB;
         RawRows<float, N, VPT, WC> gA, gB;
         float xv[N][VPT][WC], gv[N][VPT][WC];
-        if (b < B) {
-            load_rows_raw<TX, N, VPT, WC, true>(x + b * NCs, C, xA);
-            load_rows_raw<float, N, VPT, WC, true>(g + b * NCs, C, gA);
-        }
+        // every row load goes through a per-token resource (0 bytes past the
+        // last token), so the prefetch is unconditional
+        load_rows_raw_rs<TX, N, VPT, WC, true>(token_rows_rsrc(x, b, B, N, C), C, xA);
+        load_rows_raw_rs<float, N, VPT, WC, true>(token_rows_rsrc(g, b, B, N, C), C, gA);
         while (b < B) {
             const int64_t b1 = b + G;
-            if (b1 < B) {
-                load_rows_raw<TX, N, VPT, WC, true>(x + b1 * NCs, C, xB);
-                load_rows_raw<float, N, VPT, WC, true>(g + b1 * NCs, C, gB);
-            }
+            load_rows_raw_rs<TX, N, VPT, WC, true>(token_rows_rsrc(x, b1, B, N, C), C, xB);
+            load_rows_raw_rs<float, N, VPT, WC, true>(token_rows_rsrc(g, b1, B, N, C), C, gB);
             unpack_rows<TX, N, VPT, WC>(xA, C, xv);
             unpack_rows<float, N, VPT, WC>(gA, C, gv);
             bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,
                                        red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
-            if (b2 < B) {
-                load_rows_raw<TX, N, VPT, WC, true>(x + b2 * NCs, C, xA);
-                load_rows_raw<float, N, VPT, WC, true>(g + b2 * NCs, C, gA);
-            }
+            load_rows_raw_rs<TX, N, VPT, WC, true>(token_rows_rsrc(x, b2, B, N, C), C, xA);
+            load_rows_raw_rs<float, N, VPT, WC, true>(token_rows_rsrc(g, b2, B, N, C), C, gA);
             unpack_rows<TX, N, VPT, WC>(xB, C, xv);
             unpack_rows<float, N, VPT, WC>(gB, C, gv);
             bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,

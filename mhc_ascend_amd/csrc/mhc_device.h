@@ -111,6 +111,13 @@ __device__ __forceinline__ uint4 buf_ld16(buf_rsrc_t r, uint32_t voff, uint32_t 
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+template <bool NT>
+__device__ __forceinline__ uint2 buf_ld8(buf_rsrc_t r, uint32_t voff, uint32_t soff) {
+    constexpr int aux = NT ? 2 : 0;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, aux);
+    return make_uint2(v[0], v[1]);
+}
+
 template <bool PIN = false>
 __device__ __forceinline__ uint32_t buf_ld4(buf_rsrc_t r, uint32_t voff, uint32_t soff) {
     constexpr int aux = PIN ? (int)0x80000000u : 0;
@@ -125,6 +132,17 @@ __device__ __forceinline__ void buf_st16(buf_rsrc_t r, uint32_t voff, uint32_t s
     constexpr int aux = NT ? 2 : 0;
     typedef unsigned int u32x4v_t __attribute__((ext_vector_type(4)));
     __builtin_amdgcn_raw_buffer_store_b128(u32x4v_t{v.x, v.y, v.z, v.w}, r, (int)voff, (int)soff, aux);
+}
+
+template <bool NT>
+__device__ __forceinline__ void buf_st8(buf_rsrc_t r, uint32_t voff, uint32_t soff, uint2 v) {
+    constexpr int aux = NT ? 2 : 0;
+    typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2v_t{v.x, v.y}, r, (int)voff, (int)soff, aux);
+}
+
+__device__ __forceinline__ void buf_st4(buf_rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, (int)soff, 0);
 }
 
 // A per-lane buffer offset that fails the range check of any resource under

@@ -63,6 +63,48 @@ __device__ __forceinline__ void load_rows_raw(const T* __restrict__ base, int C,
     }
 }
 
+// The same loads through a buffer resource over one token's N rows (N * C
+// elements; a resource of 0 bytes for a token past the end reads zeros
+// without touching memory).  No load sits behind a branch, so a prefetch of
+// the next token can be issued unconditionally and the compiler's wait
+// counts stay exact (a conditional prefetch made it wait for every
+// outstanding load, the prefetch included, before using the current row).
+template <typename T, int N, int VPT, int WC, bool NTL>
+__device__ __forceinline__ void load_rows_raw_rs(buf_rsrc_t rs, int C, RawRows<T, N, VPT, WC>& r) {
+    constexpr int W = RawChunk<T, WC>::kWords;
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+        int c0 = (k * blockDim.x + threadIdx.x) * WC;
+        c0 = c0 < C ? c0 : 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const uint32_t off = (uint32_t)(((int64_t)i * C + c0) * (int64_t)sizeof(T));
+            if constexpr (W == 2) {
+                const uint2 q = buf_ld8<NTL>(rs, off, 0u);
+                r[i][k][0] = q.x;
+                r[i][k][1] = q.y;
+            } else {
+#pragma unroll
+                for (int s = 0; s < W / 4; ++s) {
+                    const uint4 q = buf_ld16<NTL>(rs, off + 16 * s, 0u);
+                    r[i][k][4 * s] = q.x;
+                    r[i][k][4 * s + 1] = q.y;
+                    r[i][k][4 * s + 2] = q.z;
+                    r[i][k][4 * s + 3] = q.w;
+                }
+            }
+        }
+    }
+}
+
+// Resource over token b's N rows of C elements of a [B, N, C] array (0 bytes
+// for b >= B); the rows are under 2 GiB (the register rows hold them).
+template <typename T>
+__device__ __forceinline__ buf_rsrc_t token_rows_rsrc(const T* base, int64_t b, int64_t B, int N, int C) {
+    const int64_t bb = b < B ? b : 0;
+    return make_buf_rsrc(base + bb * (int64_t)N * C, b < B ? (uint32_t)((int64_t)N * C * (int64_t)sizeof(T)) : 0u);
+}
+
 template <typename T, int N, int VPT, int WC>
 __device__ __forceinline__ void unpack_rows(const RawRows<T, N, VPT, WC>& r, int C, float (&v)[N][VPT][WC]) {
 #pragma unroll
