@@ -621,7 +621,9 @@ def main(argv=None) -> int:
                     help="with the default static workload: also measure these workloads as sub-records "
                          "(default: dynamic, the reference layer's default path, and wrapper)")
     ap.add_argument("--no-extra", action="store_true", help="no sub-records")
-    ap.add_argument("--extra-steps", type=int, default=20, help="timed steps of each sub-record")
+    ap.add_argument("--extra-steps", type=int, default=50,
+                    help="timed steps of each sub-record (enough that the first launch and the final drain, "
+                         "timed once per run, do not inflate the per-step figure)")
     a = ap.parse_args(argv)
 
     if a.gpus != 1:

@@ -911,13 +911,15 @@ hipError_t launch_layer_static_fwd(int x_dtype, int n, const void* x, const void
     return e != hipSuccess ? e : hipGetLastError();
 }
 
-// The backward hands one of its 2 + n^2 + 3n row sums to each thread.  With
-// bf16 x (8-byte x and dx accesses per lane) 512-lane workgroups with one
-// token in registers were measured faster than 256 lanes with the two-token
-// prefetch (C4 MODE 1: 216 -> 208 us); fp32 rows keep the prefetch.
+// The backward hands one of its 2 + n^2 + 3n row sums to each thread.  Both
+// storage dtypes run 256-lane workgroups with the two-token prefetch (C4
+// MODE 1: 213 -> 182 us against 512 lanes with one token in registers, once
+// the prefetch was unconditional; with the prefetch behind a branch the
+// 512-lane form had been the faster one).
 static RowTiling bwd_tiling(int64_t C, int n, int x_dtype = kF32) {
+    (void)x_dtype;
     if (n > 8) return RowTiling{0, 0};
-    return with_min_threads(choose_row_tiling(C, kLayerWC, 2 * n, x_dtype == kBF16 ? 512 : 256), 2 + n * n + 3 * n);
+    return with_min_threads(choose_row_tiling(C, kLayerWC, 2 * n, 256), 2 + n * n + 3 * n);
 }
 
 bool layer_bwd_is_wide(int n, int64_t C) { return bwd_tiling(C, n).vpt <= 0; }

@@ -349,8 +349,11 @@ __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restric
         sacc += v;
     }
 
-    TX* drb = dres + b * (int64_t)C;
-    TX* dbb = dbr + b * (int64_t)C;
+    // stores through row resources, out-of-range offsets past the row end:
+    // none behind a branch (the caller's prefetch keeps exact wait counts)
+    const buf_rsrc_t drs = make_buf_rsrc(dres + b * (int64_t)C, (uint32_t)((int64_t)C * (int64_t)sizeof(TX)));
+    const buf_rsrc_t dbs = make_buf_rsrc(dbr + b * (int64_t)C, (uint32_t)((int64_t)C * (int64_t)sizeof(TX)));
+    static_assert(kLayerWC == 4, "4-channel chunks: one 16-byte (fp32) or 8-byte (bf16) store");
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
@@ -373,9 +376,15 @@ __device__ __forceinline__ void wrap_bwd_token(int64_t b, const float* __restric
             dr[e] = a;
             db[e] = (N > 1) ? cm[N > 1 ? 1 : 0] * g + hp[N > 1 ? 1 : 0] * gxa : 0.f;
         }
-        if (c0 < C) {
-            store_run_nt<TX, WC>(drb + c0, dr);
-            store_run_nt<TX, WC>(dbb + c0, db);
+        const uint32_t o = c0 < C ? (uint32_t)c0 * (uint32_t)sizeof(TX) : kBufOff;
+        if constexpr (sizeof(TX) == 4) {
+            buf_st16<true>(drs, o, 0u, make_uint4(__float_as_uint(dr[0]), __float_as_uint(dr[1]), __float_as_uint(dr[2]),
+                                                  __float_as_uint(dr[3])));
+            buf_st16<true>(dbs, o, 0u, make_uint4(__float_as_uint(db[0]), __float_as_uint(db[1]), __float_as_uint(db[2]),
+                                                  __float_as_uint(db[3])));
+        } else {
+            buf_st8<true>(drs, o, 0u, make_uint2(pack_bf16x2(dr[0], dr[1]), pack_bf16x2(dr[2], dr[3])));
+            buf_st8<true>(dbs, o, 0u, make_uint2(pack_bf16x2(db[0], db[1]), pack_bf16x2(db[2], db[3])));
         }
     }
 }
@@ -406,18 +415,17 @@ __device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const
     RawRows<TX, 1, VPT, WC> rA, bA, rB, bB;
     float gv[1][VPT][WC], rv[1][VPT][WC], bv[1][VPT][WC];
     if constexpr (PF) {
-        if (b < B) {
-            load_rows_raw<float, 1, VPT, WC, true>(g + b * C, C, gA);
-            load_rows_raw<TX, 1, VPT, WC, true>(res + b * C, C, rA);
-            load_rows_raw<TX, 1, VPT, WC, true>(br + b * C, C, bA);
-        }
+        // row loads through per-token resources (0 bytes past the last
+        // token): the prefetch of the next token is unconditional, which
+        // keeps the compiler's wait before the current token partial
+        load_rows_raw_rs<float, 1, VPT, WC, true>(token_rows_rsrc(g, b, B, 1, C), C, gA);
+        load_rows_raw_rs<TX, 1, VPT, WC, true>(token_rows_rsrc(res, b, B, 1, C), C, rA);
+        load_rows_raw_rs<TX, 1, VPT, WC, true>(token_rows_rsrc(br, b, B, 1, C), C, bA);
         while (b < B) {
             const int64_t b1 = b + G;
-            if (b1 < B) {
-                load_rows_raw<float, 1, VPT, WC, true>(g + b1 * C, C, gB);
-                load_rows_raw<TX, 1, VPT, WC, true>(res + b1 * C, C, rB);
-                load_rows_raw<TX, 1, VPT, WC, true>(br + b1 * C, C, bB);
-            }
+            load_rows_raw_rs<float, 1, VPT, WC, true>(token_rows_rsrc(g, b1, B, 1, C), C, gB);
+            load_rows_raw_rs<TX, 1, VPT, WC, true>(token_rows_rsrc(res, b1, B, 1, C), C, rB);
+            load_rows_raw_rs<TX, 1, VPT, WC, true>(token_rows_rsrc(br, b1, B, 1, C), C, bB);
             unpack_rows<float, 1, VPT, WC>(gA, C, gv);
             unpack_rows<TX, 1, VPT, WC>(rA, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bA, C, bv);
@@ -425,11 +433,9 @@ __device__ __forceinline__ void wrap_bwd_rows(const float* __restrict__ g, const
                                               red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
-            if (b2 < B) {
-                load_rows_raw<float, 1, VPT, WC, true>(g + b2 * C, C, gA);
-                load_rows_raw<TX, 1, VPT, WC, true>(res + b2 * C, C, rA);
-                load_rows_raw<TX, 1, VPT, WC, true>(br + b2 * C, C, bA);
-            }
+            load_rows_raw_rs<float, 1, VPT, WC, true>(token_rows_rsrc(g, b2, B, 1, C), C, gA);
+            load_rows_raw_rs<TX, 1, VPT, WC, true>(token_rows_rsrc(res, b2, B, 1, C), C, rA);
+            load_rows_raw_rs<TX, 1, VPT, WC, true>(token_rows_rsrc(br, b2, B, 1, C), C, bA);
             unpack_rows<float, 1, VPT, WC>(gB, C, gv);
             unpack_rows<TX, 1, VPT, WC>(rB, C, rv);
             unpack_rows<TX, 1, VPT, WC>(bB, C, bv);
