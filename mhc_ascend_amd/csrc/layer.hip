@@ -123,29 +123,40 @@ __device__ __forceinline__ void fwd_token(int64_t b, const float* __restrict__ c
     block_sum<1>(v, red);
     const float r = sqrtf(v[0] / (float)C + eps);
     const float inv = 1.f / r;
-    TO* ob = out + b * (int64_t)N * C;
+    // stores through a resource over the token's output rows, out-of-range
+    // offsets past the row end (no store behind a branch)
+    const buf_rsrc_t ors = make_buf_rsrc(out + b * (int64_t)N * C, (uint32_t)((int64_t)N * C * (int64_t)sizeof(TO)));
+    static_assert(WC == 4, "4-channel chunks: one 16-byte (fp32) or 8-byte (bf16) store");
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
         const int c0 = (k * blockDim.x + threadIdx.x) * WC;
-        if (c0 < C) {
-            float y[WC];
+        const uint32_t o0 = c0 < C ? (uint32_t)c0 * (uint32_t)sizeof(TO) : kBufOff;
+        float y[WC];
 #pragma unroll
-            for (int e = 0; e < WC; ++e) y[e] = xa[k][e] * inv * wv[k][e];
+        for (int e = 0; e < WC; ++e) y[e] = xa[k][e] * inv * wv[k][e];
 #pragma unroll
-            for (int i = 0; i < N; ++i) {
-                float o[WC];
+        for (int i = 0; i < N; ++i) {
+            float o[WC];
 #pragma unroll
-                for (int e = 0; e < WC; ++e) {
-                    float s = cfv[N + i] * y[e];
+            for (int e = 0; e < WC; ++e) {
+                float s = cfv[N + i] * y[e];
 #pragma unroll
-                    for (int j = 0; j < N; ++j) s += cfv[2 * N + i * N + j] * xv[j][k][e];
-                    o[e] = s;
-                }
-                store_run_nt<TO, WC>(ob + (int64_t)i * C + c0, o);
+                for (int j = 0; j < N; ++j) s += cfv[2 * N + i * N + j] * xv[j][k][e];
+                o[e] = s;
+            }
+            const uint32_t off = o0 + (uint32_t)(i * C * (int)sizeof(TO));
+            if constexpr (sizeof(TO) == 4) {
+                buf_st16<true>(ors, off, 0u, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]),
+                                                        __float_as_uint(o[2]), __float_as_uint(o[3])));
+            } else {
+                buf_st8<true>(ors, off, 0u, make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])));
             }
         }
     }
-    if (threadIdx.x == 0 && rms_out) rms_out[b] = r;
+    if (rms_out) {
+        const buf_rsrc_t rrs = make_buf_rsrc(rms_out + b, 4u);
+        buf_st4(rrs, threadIdx.x == 0 ? 0u : kBufOff, 0u, r);
+    }
 }
 
 template <typename TX, typename TO, int N, int VPT>
