@@ -210,6 +210,56 @@ class DynamicWorkload:
         f = 2 * self.B * self.n * self.C * (2 * self.n + self.n * self.n)
         return {"proj": f, "proj_bwd": 2 * f}
 
+    def projection_ab(self, lib, reps):
+        """A/B of the projection's arithmetic at this workload's shape (inside
+        the timed build): the library's bf16-MFMA projection
+        (fused_rmsnorm_matmul_fwd, kernel "proj") against the benchmark
+        build's fp32-VALU one (kernel "proj_valu"), on x of the first input set
+        and Phi = [phi_pre; phi_post; phi_res]; both checked against float64
+        on 64 tokens."""
+        torch = self.torch
+        B, K, npr = self.B, self.n * self.C, 2 * self.n + self.n * self.n
+        x = self.xs[0].detach().reshape(B, K)
+        phi = torch.cat([self.layer.phi_pre, self.layer.phi_post, self.layer.phi_res]).detach().float().contiguous()
+        stream = lib.stream_of(x)
+        runs = {}
+        for kind, fn in (("mfma", "mhc_fused_rmsnorm_matmul_fwd"), ("valu", "mhc_timing_proj_valu")):
+            ws = torch.empty(getattr(lib.load(), fn + "_workspace_size")(B, K, npr), dtype=torch.uint8, device=x.device)
+            out = torch.empty(B, npr, device=x.device)
+            args = (x.data_ptr(), lib.BF16, phi.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), B, K, npr, stream)
+            runs[kind] = (fn, args, out, ws)
+        for fn, args, _, _ in runs.values():  # first launches load the code objects
+            lib.call(fn, *args)
+        torch.cuda.synchronize()
+        lib.timing_reset()
+        lib.timing_enable(True)
+        for _ in range(reps):
+            for fn, args, _, _ in runs.values():
+                lib.call(fn, *args)
+        torch.cuda.synchronize()
+        lib.timing_enable(False)
+        mfma_ms, mfma_n = lib.timing_query("proj")
+        valu_ms, valu_n = lib.timing_query("proj_valu")
+        ref = x[:64].double() @ phi.double().t()
+        scale = ref.abs().max().item()
+        err = {k: (runs[k][2][:64].double() - ref).abs().max().item() / scale for k in runs}
+        flops = 2 * B * K * npr
+        mfma_avg, valu_avg = mfma_ms / max(mfma_n, 1), valu_ms / max(valu_n, 1)
+        return {"shape": {"tokens": B, "k": K, "outputs": npr, "x_dtype": "bf16"},
+                "mfma": {"kernel": "proj_mfma_kernel (bf16 MFMA 16x16x32 on hi/mid/lo Phi planes)",
+                         "avg_ms": mfma_avg, "launches": mfma_n, "tflops": flops / (mfma_avg / 1e3) / 1e12,
+                         "gbps": 2 * B * K / (mfma_avg / 1e3) / 1e9, "max_rel_err_vs_fp64": err["mfma"]},
+                "valu": {"kernel": "proj_valu_kernel (fp32 FMA, one token per lane, Phi rows by scalar loads)",
+                         "avg_ms": valu_avg, "launches": valu_n, "tflops": flops / (valu_avg / 1e3) / 1e12,
+                         "gbps": 2 * B * K / (valu_avg / 1e3) / 1e9, "max_rel_err_vs_fp64": err["valu"]},
+                "valu_over_mfma": valu_avg / mfma_avg,
+                # np + 1 FMAs per element of x (the products and x^2) at the
+                # fp32 FMA issue rate without packed-FP32 forms: MI355X's
+                # published 157.3 TFLOP/s vector fp32 counts 2 FMAs per lane
+                # per cycle, so one FMA per lane per cycle is 39.3 T FMA/s
+                "valu_fma_issue_floor_ms": B * K * (npr + 1) / 39.3e12 * 1e3,
+                "timing": "HIP events around each kernel on its stream (timed build), after the workload's passes"}
+
     def config(self):
         return {"workload": "C4 MHCLayer dynamic-H fwd+bwd", "tokens": self.B, "n": self.n, "C": self.C,
                 "x_dtype": "bf16", "phi": [self.n * self.C, 2 * self.n + self.n * self.n], "sinkhorn_iters": 20}
@@ -746,6 +796,7 @@ def measure_workload(name, torch, mhc, _lib, device, steps, warmup, protocol_run
         _lib.timing_enable(False)
         for kname in KERNELS:
             timings[kname] = _lib.timing_query(kname)
+        proj_ab = wl.projection_ab(_lib, kernel_steps) if wl.name == "dynamic" else None
     kbytes = wl.kernel_bytes()
     kflops = wl.flops()
     kernels = {}
@@ -807,6 +858,8 @@ def measure_workload(name, torch, mhc, _lib, device, steps, warmup, protocol_run
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
+    if proj_ab is not None:
+        rec["projection_ab"] = proj_ab
     del wl
     torch.cuda.synchronize()
     torch.cuda.empty_cache()

@@ -23,6 +23,18 @@ int mhc_timing_enable(int enable);
 int mhc_timing_reset(void);
 int mhc_timing_query(const char* kernel, double* total_ms, int64_t* launches);
 
+/* A/B of the projection's arithmetic (the benchmark build only): the same
+ * out[b, o] = sum_k inp[b, k] weight[o, k] as mhc_fused_rmsnorm_matmul_fwd
+ * (inp [batch, k] F32 or BF16, weight [out_dim <= 32, k] fp32, k % 32 == 0,
+ * out [batch, out_dim] fp32), with the products on the VALU (fp32 FMAs, one
+ * token per lane, weight rows through scalar loads) instead of bf16 MFMA.
+ * Its main kernel times as "proj_valu" (the MFMA one as "proj").  No
+ * counterpart in the reference: it measures the choice of MFMA for the
+ * projection of fused_rmsnorm_matmul_fwd (bindings.cpp:480-528). */
+size_t mhc_timing_proj_valu_workspace_size(int64_t batch, int64_t k, int32_t out_dim);
+int mhc_timing_proj_valu(const void* inp, int32_t dtype, const float* weight, float* out, void* workspace,
+                         size_t workspace_bytes, int64_t batch, int64_t k, int32_t out_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,6 +113,8 @@ TIMING_SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
     "mhc_timing_enable": (ctypes.c_int, [ctypes.c_int]),
     "mhc_timing_reset": (ctypes.c_int, []),
     "mhc_timing_query": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
+    "mhc_timing_proj_valu_workspace_size": (_sz, [_i64, _i64, _i32]),
+    "mhc_timing_proj_valu": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, _sz, _i64, _i64, _i32, _vp]),
 }
 
 _lib = None

@@ -213,6 +213,7 @@ int mhc_timing_query(const char* kernel, double* total_ms, int64_t* launches) {
     *launches = it == g_totals.end() ? 0 : it->second.second;
     return MHC_SUCCESS;
 }
+
 #endif  // MHC_KERNEL_TIMING
 
 // ---- Sinkhorn ---------------------------------------------------------------
@@ -610,6 +611,38 @@ int mhc_fused_rmsnorm_matmul_fwd(const void* inp, int32_t dtype, const float* we
     if (e == hipSuccess) e = launch_proj_reduce(pp, w.ks, batch, out_dim, out, s);
     return hip_status(e);
 }
+
+#ifdef MHC_KERNEL_TIMING
+// The benchmark build's VALU projection, for the A/B against the MFMA one
+// (include/mhc_hip_timing.h).
+// [Phi^T [k][32] | P partials [ks][B][32] | sum x^2 partials [ks][B]]
+size_t mhc_timing_proj_valu_workspace_size(int64_t batch, int64_t k, int32_t out_dim) {
+    (void)out_dim;
+    if (batch <= 0 || k <= 0) return 256;
+    const int ks = proj_valu_ksplit(batch, k);
+    return align256((size_t)k * 32 * 4) + align256((size_t)ks * batch * 32 * 4) + align256((size_t)ks * batch * 4);
+}
+
+int mhc_timing_proj_valu(const void* inp, int32_t dtype, const float* weight, float* out, void* workspace,
+                         size_t workspace_bytes, int64_t batch, int64_t k, int32_t out_dim, void* stream) {
+    MHC_REQUIRE(batch >= 0 && k >= 1 && k % 32 == 0, "timing_proj_valu: batch >= 0 and k a positive multiple of 32");
+    MHC_REQUIRE(out_dim >= 1 && out_dim <= 32, "timing_proj_valu: out_dim must be 1..32");
+    MHC_REQUIRE(valid_dtype(dtype), "timing_proj_valu: dtype must be F32 or BF16");
+    MHC_REQUIRE(weight && (batch == 0 || (inp && out)), "timing_proj_valu: null pointer");
+    if (batch == 0) return MHC_SUCCESS;
+    if (!workspace || workspace_bytes < mhc_timing_proj_valu_workspace_size(batch, k, out_dim))
+        return fail(MHC_ERR_WORKSPACE, "timing_proj_valu: workspace too small");
+    const int ks = proj_valu_ksplit(batch, k);
+    char* ws = (char*)workspace;
+    float* phit = (float*)ws;
+    float* pp = (float*)(ws + align256((size_t)k * 32 * 4));
+    float* ss = (float*)(ws + align256((size_t)k * 32 * 4) + align256((size_t)ks * batch * 32 * 4));
+    hipStream_t s = (hipStream_t)stream;
+    hipError_t e = launch_proj_valu(dtype, inp, weight, out_dim, phit, pp, ss, batch, k, ks, s);
+    if (e == hipSuccess) e = launch_proj_reduce(pp, ks, batch, out_dim, out, s);
+    return hip_status(e);
+}
+#endif  // MHC_KERNEL_TIMING
 
 struct ProjBwdWs {
     int tiles;

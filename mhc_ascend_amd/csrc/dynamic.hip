@@ -1243,8 +1243,13 @@ __device__ __forceinline__ void lds_put4(char* p, const float (&v)[4]) {
 template <typename TX> constexpr int pb_pitch() { return 128 * (int)sizeof(TX) + 8; }
 constexpr int kDpPitch = 40;  // bf16 per row of the split dP copies (32 + 8 pad)
 
+// Waves per SIMD the register allocation targets: four for bf16 x (128
+// registers, no spills; four 35.6 KB workgroups share a CU's LDS), two for
+// fp32 x, whose split operands need more.
+template <typename TX> constexpr int kPbWaves() { return sizeof(TX) == 2 ? 4 : 2; }
+
 template <typename TX, bool ACC, bool HAS_S>
-__global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX>()))) void proj_bwd_mfma_kernel(
     const TX* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
     const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
     int n_pre, int o0, int np, TX* __restrict__ dx, const float* __restrict__ dx_step, int groups, int C,
@@ -1265,8 +1270,8 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     // Only the dx tile is double-buffered: a stage's store reads it while
     // the next stage is committed.  x, the dP copies and s of the next
     // stage are committed after the barrier that ends the compute reading
-    // them, so one copy each suffices (35.6 KB of LDS for bf16 x: three
-    // workgroups per CU instead of two).
+    // them, so one copy each suffices (35.6 KB of LDS for bf16 x: four
+    // workgroups fit a CU).
     __shared__ __align__(16) char x_lds[TB * PITCH];
     __shared__ __align__(16) char dx_lds[2][TB * PITCH];
     __shared__ __align__(16) bf16_t dps_lds[4][32 * kDpPitch];  // hi_row, lo_row, hi_col, lo_col
@@ -1331,13 +1336,20 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
     const uint32_t so = tid < TB ? (uint32_t)tid * 4u : kBufOff;
     const uint32_t qo = tid < TB ? (uint32_t)(tid * groups + grp) * 4u : kBufOff;
 
-    // Two register sets of fetched stages: stage i+2 is fetched while stage i
-    // computes and stage i+1 (fetched one stage earlier) moves into LDS.
+    // Two register sets of fetched row tiles: stage i+2 is fetched while
+    // stage i computes and stage i+1 (fetched one stage earlier) moves into
+    // LDS.  The stage's small records (dP, s, steps) are fetched one stage
+    // ahead, before the row tiles of the stage after, so that waiting for
+    // them leaves those in flight.
     struct Fetched {
-        uint4 x[PASSES], d[PASSES], dp;
+        uint4 x[PASSES], d[PASSES];
+    };
+    struct Small {
+        uint4 dp;
         uint32_t s, q;
     };
     Fetched f0, f1;
+    Small sm;
     // the stage of rows rel .. rel + TB - 1 (relative to t_begin)
     auto fetch = [&](Fetched& f, uint32_t rel) __attribute__((always_inline)) {
 #pragma unroll
@@ -1346,11 +1358,18 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
             f.x[p] = buf_ld16<true>(rs_x, off, 0u);
             if constexpr (ACC) f.d[p] = buf_ld16<true>(rs_dx, off, 0u);
         }
-        f.dp = buf_ld16<false>(rs_p, po + rel * (uint32_t)dp_stride * 4u, 0u);
-        f.s = HAS_S ? buf_ld4(rs_s, so + rel * 4u, 0u) : 0u;
-        f.q = QIN ? buf_ld4(rs_q, qo + rel * (uint32_t)groups * 4u, 0u) : 0u;
+    };
+    auto fetch_small = [&](uint32_t rel) __attribute__((always_inline)) {
+        sm.dp = buf_ld16<false>(rs_p, po + rel * (uint32_t)dp_stride * 4u, 0u);
+        sm.s = HAS_S ? buf_ld4(rs_s, so + rel * 4u, 0u) : 0u;
+        sm.q = QIN ? buf_ld4(rs_q, qo + rel * (uint32_t)groups * 4u, 0u) : 0u;
     };
     auto commit = [&](const Fetched& f, int buf) __attribute__((always_inline)) {
+        // s and the steps are consumed behind a branch below; an empty use of
+        // their registers makes every lane wait for them in straight-line
+        // code, so the compiler's wait counts do not carry them as possibly
+        // in flight past it.
+        asm volatile("" ::"v"(sm.s), "v"(sm.q));
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
@@ -1367,7 +1386,7 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
         }
         // dP of token dtk, o = dpo .. dpo + 3: split once into hi / lo bf16,
         // token-major (one 8-byte write each) and o-major copies
-        const uint32_t dw4[4] = {f.dp.x, f.dp.y, f.dp.z, f.dp.w};
+        const uint32_t dw4[4] = {sm.dp.x, sm.dp.y, sm.dp.z, sm.dp.w};
         float hi[4], lo[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1385,10 +1404,10 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
             dps_lds[3][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(lo[q]);
         }
         if constexpr (HAS_S) {
-            if (tid < TB) s_lds[tid] = __uint_as_float(f.s);
+            if (tid < TB) s_lds[tid] = __uint_as_float(sm.s);
         }
         if constexpr (QIN) {
-            if (tid < TB) q_lds[tid] = __uint_as_float(f.q);
+            if (tid < TB) q_lds[tid] = __uint_as_float(sm.q);
         }
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> u32x4_t {
@@ -1468,22 +1487,29 @@ __global__ __launch_bounds__(256) void proj_bwd_mfma_kernel(
         }
     };
 
-    // fetches and commits past the last row read zeros
+    // Fetches and commits past the last row read zeros.  Whole pairs of
+    // stages: with an odd count the last one reads only zeros, adds zeros and
+    // stores nothing.  An exit between the two would leave a path (seen by
+    // the compiler, never taken) from the first stage back to the loop head
+    // with its fetch outstanding, and the wait counts would then hold every
+    // loop head until that fetch had landed.
     const uint32_t nr = (uint32_t)nrows;
+    fetch_small(0u);
     fetch(f0, 0u);
     commit(f0, 0);
     fetch(f1, TB);
     __syncthreads();
     for (uint32_t r0 = 0; r0 < nr; r0 += 2 * TB) {
-        // even stage r0 in LDS buffer 0; f1 holds stage r0 + TB
+        // even stage r0 in LDS buffer 0; f1 holds the rows of stage r0 + TB
+        fetch_small(r0 + TB);
         fetch(f0, r0 + 2 * TB);
         compute(0);
         __syncthreads();  // the dx tile is complete
         store(r0, 0);
         commit(f1, 1);
         __syncthreads();
-        if (r0 + TB >= nr) break;
-        // odd stage r0 + TB in LDS buffer 1; f0 holds stage r0 + 2 TB
+        // odd stage r0 + TB in LDS buffer 1; f0 holds the rows of stage r0 + 2 TB
+        fetch_small(r0 + 2 * TB);
         fetch(f1, r0 + 3 * TB);
         compute(1);
         __syncthreads();
@@ -1651,6 +1677,122 @@ hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, fl
                        out);
     return hipGetLastError();
 }
+
+#ifdef MHC_KERNEL_TIMING
+// ---------------------------------------------------------------------------
+// VALU projection (the benchmark build only, for the A/B against
+// proj_mfma_kernel): the same P and sum-x^2 partials from fp32 FMAs.  One
+// token per lane; the rows Phi^T[k][0..31] are the same for every lane and
+// come through scalar loads; x is staged through LDS in 32-k slices with
+// coalesced 16-byte loads.  NP FMAs and one square per element of x.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void phi_t_kernel(const float* __restrict__ phi, int np, int64_t K,
+                                                    float* __restrict__ phit) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over K x 32
+    if (i >= K * 32) return;
+    const int64_t k = i >> 5;
+    const int o = (int)(i & 31);
+    phit[i] = o < np ? phi[(int64_t)o * K + k] : 0.f;
+}
+
+constexpr int kValuTB = 256;  // tokens per workgroup
+constexpr int kValuKC = 32;   // k per stage
+
+template <typename TX, int NP>
+__global__ __launch_bounds__(256) void proj_valu_kernel(const TX* __restrict__ x, const float* __restrict__ phit,
+                                                        float* __restrict__ p_part, float* __restrict__ ss_part,
+                                                        int64_t B, int64_t K, int64_t kchunk) {
+    constexpr int EPV = 16 / (int)sizeof(TX);
+    constexpr int VPR = kValuKC / EPV;
+    constexpr int PITCH = kValuKC * (int)sizeof(TX) + 16;
+    __shared__ __align__(16) char xs[kValuTB * PITCH];
+    const int tid = threadIdx.x;
+    const int64_t tok0 = (int64_t)blockIdx.x * kValuTB;
+    const int64_t ks = blockIdx.y;
+    const int64_t kb = ks * kchunk;
+    const int64_t ke = kb + kchunk < K ? kb + kchunk : K;
+    float acc[NP];
+#pragma unroll
+    for (int o = 0; o < NP; ++o) acc[o] = 0.f;
+    float ss = 0.f;
+    for (int64_t k0 = kb; k0 < ke; k0 += kValuKC) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < VPR; ++i) {
+            const int p = tid + 256 * i;
+            const int row = p / VPR;
+            const int vec = p % VPR;
+            const int64_t tok = tok0 + row;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (tok < B) v = *reinterpret_cast<const uint4*>(x + tok * K + k0 + vec * EPV);
+            *reinterpret_cast<uint4*>(&xs[row * PITCH + vec * 16]) = v;
+        }
+        __syncthreads();
+        const float* ph = phit + k0 * 32;
+#pragma unroll
+        for (int v = 0; v < VPR; ++v) {
+            const uint4 q = *reinterpret_cast<const uint4*>(&xs[tid * PITCH + v * 16]);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+            float xv[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                if constexpr (sizeof(TX) == 2) {
+                    xv[e] = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+                } else {
+                    xv[e] = __uint_as_float(w[e]);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const float* pr = ph + (v * EPV + e) * 32;
+                ss = fmaf(xv[e], xv[e], ss);
+#pragma unroll
+                for (int o = 0; o < NP; ++o) acc[o] = fmaf(xv[e], pr[o], acc[o]);
+            }
+        }
+    }
+    const int64_t tok = tok0 + tid;
+    if (tok < B) {
+        float4* out = reinterpret_cast<float4*>(p_part + (ks * B + tok) * kNPad);
+#pragma unroll
+        for (int o = 0; o < kNPad; o += 4) {
+            out[o / 4] = make_float4(o < NP ? acc[o < NP ? o : 0] : 0.f, o + 1 < NP ? acc[o + 1 < NP ? o + 1 : 0] : 0.f,
+                                     o + 2 < NP ? acc[o + 2 < NP ? o + 2 : 0] : 0.f,
+                                     o + 3 < NP ? acc[o + 3 < NP ? o + 3 : 0] : 0.f);
+        }
+        ss_part[ks * B + tok] = ss;
+    }
+}
+
+int proj_valu_ksplit(int64_t B, int64_t K) {
+    const int64_t tb = (B + kValuTB - 1) / kValuTB;
+    int64_t ks = (4 * (int64_t)device_cu_count() + tb - 1) / tb;
+    const int64_t kmax = K / kValuKC;
+    if (ks > kmax) ks = kmax;
+    return (int)(ks < 1 ? 1 : ks);
+}
+
+hipError_t launch_proj_valu(int x_dtype, const void* x, const float* phi, int np, float* phit, float* p_part,
+                            float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (K % kValuKC != 0 || np < 1 || np > kNPad || ks < 1) return hipErrorInvalidValue;
+    MHC_LAUNCH_GGL(phi_t_kernel, dim3((unsigned)((K * 32 + 255) / 256)), dim3(256), 0, s, phi, np, K, phit);
+    int64_t kchunk = (K + ks - 1) / ks;
+    kchunk = ((kchunk + kValuKC - 1) / kValuKC) * kValuKC;
+    const dim3 grid((unsigned)((B + kValuTB - 1) / kValuTB), (unsigned)ks);
+    const int tok = timing_begin("proj_valu", s);
+#define MHC_VALU(TX_, NP_) \
+    MHC_LAUNCH_GGL((proj_valu_kernel<TX_, NP_>), grid, dim3(256), 0, s, (const TX_*)x, phit, p_part, ss_part, B, K, kchunk)
+    if (x_dtype == kBF16) {
+        if (np <= 8) { MHC_VALU(bf16_t, 8); } else if (np <= 24) { MHC_VALU(bf16_t, 24); } else { MHC_VALU(bf16_t, 32); }
+    } else {
+        if (np <= 8) { MHC_VALU(float, 8); } else if (np <= 24) { MHC_VALU(float, 24); } else { MHC_VALU(float, 32); }
+    }
+#undef MHC_VALU
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+#endif  // MHC_KERNEL_TIMING
 
 #define MHC_DYN_N(n, ...)                                        \
     switch (n) {                                                 \
@@ -2414,8 +2556,10 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
 // nearly full rather than leaving most CUs idle while it runs), at least one.
 // A token tile's rows of x / dx, plus the three stages the pipeline reads
 // past its end, under 2 GiB (the kernel's buffer resources and offsets).
+// Tiles are whole pairs of 32-token stages; the pipeline reads up to four
+// stages past the end, and offsets stay under 2 GiB.
 static int64_t proj_bwd_max_tile(int x_dtype, int64_t K) {
-    return ((int64_t(1) << 31) - 1) / (K * (x_dtype == kBF16 ? 2 : 4)) - 3 * 32;
+    return ((int64_t(1) << 31) - 1) / (K * (x_dtype == kBF16 ? 2 : 4)) - 4 * 32;
 }
 
 int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
@@ -2431,8 +2575,8 @@ int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
     const int64_t blocks = (B + 31) / 32;
     if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;
-    const int64_t mt = proj_bwd_max_tile(x_dtype, K) / 32 * 32;
-    if (mt >= 32 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
+    const int64_t mt = proj_bwd_max_tile(x_dtype, K) / 64 * 64;
+    if (mt >= 64 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
     return (int)tiles;
 }
 
@@ -2446,9 +2590,9 @@ hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_s
     const int C = np > 0 ? (int)(K / (n_pre > 0 ? n_pre : 1)) : 0;
     if (x_dtype == kBF16 && (o0 != 0 || dx_step == nullptr || groups < 1 || C % kFixedGroup != 0))
         return hipErrorInvalidValue;
-    // token tile: a multiple of the 32-token block
+    // token tile: a multiple of two 32-token stages
     int64_t tile = (B + tiles - 1) / tiles;
-    tile = ((tile + 31) / 32) * 32;
+    tile = ((tile + 63) / 64) * 64;
     if (tile > proj_bwd_max_tile(x_dtype, K)) return hipErrorInvalidValue;  // offsets past 2 GiB
     const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
 #define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \

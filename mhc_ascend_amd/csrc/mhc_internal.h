@@ -233,6 +233,14 @@ hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, c
                               const float* phi_post, const float* phi_res, int n_pre, const bf16_raw_t* phib, int np,
                               float* p_part, float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s);
 hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s);
+#ifdef MHC_KERNEL_TIMING
+// The benchmark build's VALU projection (A/B against launch_proj_mfma): Phi
+// [np <= 32, K] fp32 is transposed into phit [K][32], then the same p_part
+// [ks][B][32] and ss_part[ks][B] from fp32 FMAs, ks from proj_valu_ksplit.
+int proj_valu_ksplit(int64_t B, int64_t K);
+hipError_t launch_proj_valu(int x_dtype, const void* x, const float* phi, int np, float* phit, float* p_part,
+                            float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s);
+#endif
 hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part, int ks, int64_t B, int64_t K,
                                const float* a_pre, const float* a_post, const float* a_res, const float* b_pre,
                                const float* b_post, const float* b_res, float* coef, float* p_out, float* rh,

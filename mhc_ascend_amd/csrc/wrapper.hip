@@ -495,9 +495,10 @@ __global__ MHC_ROW_BOUNDS(true) void wrap_bwd_pf_kernel(
 // factors of the stream parts to ep_out[b][kWrapEp]: with w_j the d r weight
 // of stream j, cm_j = (1/n) sum_i M_ij and hs = (1/n) sum_i h_post_i,
 //   (A_r, B_r, A_b, B_b) = (sum_j w_j cm_j, sum_j w_j h_pre_j, cm_1, h_pre_1),
-//   then h_pre_0..3, hs/r, k2, 0, 0,
-// so that d r = A_r G + B_r gxa + ... and d b = A_b G + B_b gxa + ... with
-// gxa = (hs/r) w G - k2 xa.  The stream parts of d r / d b and dw are formed
+// d r = A_r G + B_r gxa + ... and d b = A_b G + B_b gxa + ... with
+// gxa = (hs/r) w G - k2 xa; the record holds the factors of G, w G and xa:
+//   A_r, B_r hs/r, A_b, B_b hs/r, h_pre_0..3, hs/r, -B_r k2, -B_b k2, 0
+// (the last slot is free for s).  The stream parts of d r / d b and dw are formed
 // by the projection backward, which reads G once more: that read costs less
 // than writing the stream parts here and reading
 // them back there, and this pass then only reads.
@@ -618,24 +619,29 @@ __global__ __launch_bounds__(256) void wrap_bwd_red_kernel(const float* __restri
     float ep[kWrapEp];
 #pragma unroll
     for (int t = 0; t < kWrapEp; ++t) ep[t] = 0.f;
-    ep[0] = cm[0];
-    ep[1] = hp[0];
+    float a_r = cm[0], b_r = hp[0], a_b = 0.f, b_b = 0.f;
     if constexpr (N > 2) {
-        ep[0] += res_weight<2, DECAY>() * cm[2];
-        ep[1] += res_weight<2, DECAY>() * hp[2];
+        a_r += res_weight<2, DECAY>() * cm[2];
+        b_r += res_weight<2, DECAY>() * hp[2];
     }
     if constexpr (N > 3) {
-        ep[0] += res_weight<3, DECAY>() * cm[3];
-        ep[1] += res_weight<3, DECAY>() * hp[3];
+        a_r += res_weight<3, DECAY>() * cm[3];
+        b_r += res_weight<3, DECAY>() * hp[3];
     }
     if constexpr (N > 1) {
-        ep[2] = cm[1];
-        ep[3] = hp[1];
+        a_b = cm[1];
+        b_b = hp[1];
     }
+    const float hsi = hs * inv;
+    ep[0] = a_r;
+    ep[1] = b_r * hsi;
+    ep[2] = a_b;
+    ep[3] = b_b * hsi;
 #pragma unroll
     for (int j = 0; j < N; ++j) ep[4 + j] = hp[j];
-    ep[8] = hs * inv;
-    ep[9] = k2;
+    ep[8] = hsi;
+    ep[9] = -b_r * k2;
+    ep[10] = -b_b * k2;
     float* eo = ep_out + b * kWrapEp;
 #pragma unroll
     for (int t = 0; t < kWrapEp; ++t) {
@@ -1042,7 +1048,7 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
     int64_t B, int C, int64_t tile) {
     constexpr int NP = 2 * N + N * N;
     static_assert(NP <= 32, "projection rows must fit one 32-row tile");
-    static_assert(N <= 4 && kWrapEp == 12, "factor record: 4 + 4 h_pre + hs/r, k2, spare, s");
+    static_assert(N <= 4 && kWrapEp == 12, "factor record: 4 + 4 h_pre + hs/r, 2 xa factors, s");
     constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
     constexpr int TB = 32;
     constexpr int NT = kWpbThreads;
@@ -1151,13 +1157,19 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
     const uint32_t eo = ep_loader ? (uint32_t)(etk * kWrapEp + 4 * epc) * 4u : kBufOff;
     const uint32_t so = (ep_loader && epc == 2) ? (uint32_t)etk * 4u : kBufOff;
 
+    // Row tiles of a stage are fetched two stages ahead (two register sets);
+    // its small per-token records one stage ahead, before the row tiles of
+    // the stage after, so that waiting for them leaves those in flight.
     struct Fetched {
         uint4 v[2][PASSES];
         uint4 gq[GPASSES];
+    };
+    struct Small {
         uint4 e, dp;
         uint32_t s;
     };
     Fetched f0, f1;
+    Small sm;
     // the stage of rows rel .. rel + TB - 1 (relative to t_begin)
     auto fetch = [&](Fetched& f, uint32_t rel) __attribute__((always_inline)) {
 #pragma unroll
@@ -1169,11 +1181,19 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
 #pragma unroll
         for (int p = 0; p < GPASSES; ++p)
             f.gq[p] = buf_ld16<true>(rs_g, go + (rel + p * GRPP) * (uint32_t)C * 4u, 0u);
-        f.dp = buf_ld16<false>(rs_p, po + rel * 128u, 0u);
-        f.e = buf_ld16<false>(rs_e, eo + rel * (uint32_t)(kWrapEp * 4), 0u);
-        f.s = buf_ld4(rs_s, so + rel * 4u, 0u);
+    };
+    auto fetch_small = [&](uint32_t rel) __attribute__((always_inline)) {
+        sm.dp = buf_ld16<false>(rs_p, po + rel * 128u, 0u);
+        sm.e = buf_ld16<false>(rs_e, eo + rel * (uint32_t)(kWrapEp * 4), 0u);
+        sm.s = buf_ld4(rs_s, so + rel * 4u, 0u);
     };
     auto commit = [&](const Fetched& f) __attribute__((always_inline)) {
+        // The small records are consumed behind branches below; an empty use
+        // of their registers here makes every lane wait for them in straight-
+        // line code, so the compiler's wait counts do not carry them as
+        // possibly in flight past the branches.
+        asm volatile("" ::"v"(sm.dp.x), "v"(sm.dp.y), "v"(sm.dp.z), "v"(sm.dp.w), "v"(sm.e.x), "v"(sm.e.y),
+                     "v"(sm.e.z), "v"(sm.e.w), "v"(sm.s));
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
@@ -1189,7 +1209,7 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         for (int p = 0; p < GPASSES; ++p)
             *reinterpret_cast<uint4*>(&g_lds[(grow + p * GRPP) * GPITCH + gvec * 16]) = f.gq[p];
         if (dp_loader) {
-            const uint32_t dw4[4] = {f.dp.x, f.dp.y, f.dp.z, f.dp.w};
+            const uint32_t dw4[4] = {sm.dp.x, sm.dp.y, sm.dp.z, sm.dp.w};
             float hi[4], lo[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -1209,7 +1229,7 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         }
         if (ep_loader)
             *reinterpret_cast<uint4*>(&ep_lds[etk][4 * epc]) =
-                make_uint4(f.e.x, f.e.y, f.e.z, epc == 2 ? f.s : f.e.w);
+                make_uint4(sm.e.x, sm.e.y, sm.e.z, epc == 2 ? sm.s : sm.e.w);
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> wu32x4_t {
         const uint4 q = *reinterpret_cast<const uint4*>(p);
@@ -1273,9 +1293,10 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
             const float4 e0 = *reinterpret_cast<const float4*>(&ep_lds[t][0]);
             const float4 e1 = *reinterpret_cast<const float4*>(&ep_lds[t][4]);
             const float4 e2 = *reinterpret_cast<const float4*>(&ep_lds[t][8]);
-            const float a_r = e0.x, b_r = e0.y, a_b = e0.z, b_b = e0.w;
+            // d r = (A_r + B_r (hs/r) w) G - B_r k2 xa + s sx + dx_proj, d b alike
+            const float a_r = e0.x, brh = e0.y, a_b = e0.z, bbh = e0.w;
             const float hp[4] = {e1.x, e1.y, e1.z, e1.w};
-            const float hsi = e2.x, k2 = e2.y, st = e2.w;
+            const float hsi = e2.x, kr = e2.y, kb = e2.z, st = e2.w;
             const int col = wc0 + 4 * lg;
             const int boff = t * PITCH + col * (int)sizeof(TX);  // 8-byte aligned
             float rv[4], bv[4];
@@ -1295,10 +1316,9 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
                 if constexpr (N > 2) sx += res_weight<2, DECAY>() * x[2];
                 if constexpr (N > 3) sx += res_weight<3, DECAY>() * x[3];
                 const float gg = gv[i];
-                const float gxa = hsi * (wv[i] * gg) - k2 * xa;
-                dwacc[i] += hsi * (gg * xa);
-                drv[i] = a_r * gg + b_r * gxa + st * sx + pr[i];
-                dbv[i] = (N > 1) ? a_b * gg + b_b * gxa + st * x[N > 1 ? 1 : 0] + pb[i] : pb[i];
+                dwacc[i] = fmaf(hsi, gg * xa, dwacc[i]);
+                drv[i] = fmaf(st, sx, fmaf(kr, xa, fmaf(fmaf(brh, wv[i], a_r), gg, pr[i])));
+                dbv[i] = (N > 1) ? fmaf(st, x[N > 1 ? 1 : 0], fmaf(kb, xa, fmaf(fmaf(bbh, wv[i], a_b), gg, pb[i]))) : pb[i];
             }
             wlds_put4<TX>(out_lds[0] + boff, drv);
             wlds_put4<TX>(out_lds[1] + boff, dbv);
@@ -1320,7 +1340,8 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
     // Two register sets: stage i+2 is fetched while stage i computes
     // (fetches and commits past the last row read zeros).
     auto step = [&](uint32_t r, Fetched& fc, Fetched& fp) __attribute__((always_inline)) {
-        // stage r is in LDS, fc holds stage r + TB, fp is free
+        // stage r is in LDS, fc holds the rows of stage r + TB, fp is free
+        fetch_small(r + TB);
         fetch(fp, r + 2 * TB);
         compute();
         __syncthreads();
@@ -1329,13 +1350,18 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         __syncthreads();
     };
     const uint32_t nr = (uint32_t)nrows;
+    fetch_small(0u);
     fetch(f0, 0u);
     commit(f0);
     fetch(f1, TB);
     __syncthreads();
+    // Whole pairs of stages: with an odd count the last one reads only zeros,
+    // adds zeros and stores nothing.  An exit between the two would leave a
+    // path (seen by the compiler, never taken) from the first stage back to
+    // the loop head with its fetch outstanding, and the wait counts would
+    // then hold every loop head until that fetch had landed.
     for (uint32_t r0 = 0; r0 < nr; r0 += 2 * TB) {
         step(r0, f1, f0);
-        if (r0 + TB >= nr) break;
         step(r0 + TB, f0, f1);
     }
     if (!wave_on) return;
@@ -1550,8 +1576,9 @@ hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const vo
 // (rounded down, so a last partial round is nearly full rather than leaving
 // most CUs idle while it runs), at least one, and enough that a tile's rows
 // of G, plus the three stages the pipeline reads past its end, stay under
-// 2 GiB (the kernel's buffer resources and offsets).
-static int64_t wrap_proj_bwd_max_tile(int64_t C) { return ((int64_t(1) << 31) - 1) / (C * 4) - 3 * 32; }
+// 2 GiB (the kernel's buffer resources and offsets).  Tiles are whole pairs
+// of 32-token stages; the pipeline reads up to four stages past the end.
+static int64_t wrap_proj_bwd_max_tile(int64_t C) { return ((int64_t(1) << 31) - 1) / (C * 4) - 4 * 32; }
 
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
     const int64_t gx = (C + kWpbCols - 1) / kWpbCols;
@@ -1566,8 +1593,8 @@ int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
     const int64_t blocks = (B + 31) / 32;
     if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;
-    const int64_t mt = wrap_proj_bwd_max_tile(C) / 32 * 32;
-    if (mt >= 32 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
+    const int64_t mt = wrap_proj_bwd_max_tile(C) / 64 * 64;
+    if (mt >= 64 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
     return (int)tiles;
 }
 
@@ -1579,7 +1606,7 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
     if (B == 0) return hipSuccess;
     if (n != 4 || C % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
     int64_t tile = (B + tiles - 1) / tiles;
-    tile = ((tile + 31) / 32) * 32;
+    tile = ((tile + 63) / 64) * 64;
     if (tile > wrap_proj_bwd_max_tile(C)) return hipErrorInvalidValue;  // offsets past 2 GiB
     const dim3 grid((unsigned)((C + kWpbCols - 1) / kWpbCols), (unsigned)tiles);
     const int tok = timing_begin("wrap_proj_bwd", s);

@@ -43,7 +43,7 @@ def test_product_build_has_no_timing_state_and_the_bench_build_does():
     sources (include/mhc_hip_timing.h); the product library exports none of
     it.  The timed build exports every product entry as well."""
     text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "mhc_hip_timing.h")).read(), flags=re.S)
-    timing = set(re.findall(r"^\s*int\s+(mhc_timing_\w+)\s*\(", text, flags=re.M))
+    timing = set(re.findall(r"^\s*(?:int|size_t)\s+(mhc_timing_\w+)\s*\(", text, flags=re.M))
     assert timing == set(_lib.TIMING_SIGNATURES)
     product = ctypes.CDLL(_lib.LIB_PATH)
     assert not [n for n in timing if hasattr(product, n)]
