@@ -776,10 +776,12 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
     hipStream_t s = (hipStream_t)stream;
     const DynSaved d = dyn_saved(batch, n, hidden);
     float* w32 = saved + d.w_off;
-    hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
-    if (e != hipSuccess || batch == 0) return hip_status(e);
     const int64_t K = (int64_t)n * hidden;
     const ProjFwdWs w = proj_fwd_ws(batch, K, 2 * n + n * n);
+    hipError_t e = hipSuccess;
+    // the weight's fp32 copy: its own launch, or inside the Phi split's
+    if (batch == 0 || w.stream) e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
+    if (e != hipSuccess || batch == 0) return hip_status(e);
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "layer_dynamic_fwd: workspace smaller than mhc_layer_dynamic_fwd_workspace_size()");
     bf16_raw_t* phib = (bf16_raw_t*)((char*)workspace + w.phib_off);
@@ -790,7 +792,7 @@ int mhc_layer_dynamic_fwd(const void* x, int32_t x_dtype, const void* weight, in
         e = launch_proj_stream(x_dtype, x, (bf16_raw_t*)((char*)workspace + w.xpl_off), phi_pre, phi_post, phi_res,
                                n, nullptr, np, pp, ss, batch, K, w.ks, s);
     } else {
-        e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+        e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s, weight, weight_dtype, hidden, w32);
         if (e == hipSuccess) e = launch_proj_mfma(x_dtype, x, phib, np, pp, ss, batch, K, w.ks, s);
     }
     if (e == hipSuccess)
@@ -999,6 +1001,26 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
                                     n >= 16 ? (float*)(ws + w.hist_off) : nullptr, s);
+    }
+    // One projection tile (n <= 4) and few partial rows: the column sums of
+    // dPhi, dw and the db / dalpha partials in one launch after the
+    // projection backward.
+    const bool one_sum = batch > 0 && np <= kProjTile && !proj_bwd_wide_path(w.wdt, np, batch) &&
+                         column_sums_direct(rows_p) && column_sums_direct(rows_w) && column_sums_direct(rows_c);
+    if (one_sum) {
+        if (e == hipSuccess)
+            e = launch_proj_bwd(w.wdt, xk, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, 0, np, dxk, true,
+                                phip, rows_p, batch, K, s, step, w.groups);
+        if (e == hipSuccess && w.wdt != x_dtype) e = launch_cast_bf16(dxw, batch * K, grad_x, s);
+        if (e == hipSuccess) {
+            ColSumJobs jobs{};
+            jobs.j[0] = ColSumJob{phip, grad_phi, nullptr, (int64_t)np * K, rows_p, (int)(np * K), 0, 0, 0};
+            jobs.j[1] = ColSumJob{dw_part, grad_weight, nullptr, hidden, rows_w, hidden, weight_dtype == kBF16, 0, 0};
+            jobs.j[2] = ColSumJob{cpart, grad_b, grad_alpha, np + 3, rows_c, np, 0, 0, 0};
+            jobs.count = 3;
+            e = launch_multi_column_sum(jobs, s);
+        }
+        return hip_status(e);
     }
     if (e == hipSuccess)
         e = proj_bwd_all(w.wdt, xk, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, np, dxk, true, phip,

@@ -56,9 +56,16 @@ __device__ __forceinline__ void split3(float v, float& h, float& m, float& l) {
 // than 32 rows are split into output tiles of 32 rows, tile t at
 // phif + t * 6 * (K / 32) * 64 holding rows 32 t .. 32 t + 31; rows past np
 // are zero.  Grid-stride over tiles * 2 * (K / 32) * 64 fragments.
+// With w32 not null the same launch also converts the RMSNorm weight (wdt:
+// F32 or BF16, C elements) to fp32 (as weight_f32_kernel).
 __global__ __launch_bounds__(256) void phi_split_kernel(const float* __restrict__ pre, const float* __restrict__ post,
                                                         const float* __restrict__ res, int n, int np, int64_t K,
-                                                        uint4* __restrict__ phif) {
+                                                        uint4* __restrict__ phif, const void* __restrict__ wsrc,
+                                                        int wdt, int64_t C, float* __restrict__ w32) {
+    if (w32) {
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < C; i += (int64_t)gridDim.x * blockDim.x)
+            w32[i] = wdt == kBF16 ? bf16_to_f32(static_cast<const bf16_t*>(wsrc)[i]) : static_cast<const float*>(wsrc)[i];
+    }
     const int64_t ksteps = K / 32;
     const int64_t per_tile = 2 * ksteps * 64;
     const int64_t total = (int64_t)((np + 31) / 32) * per_tile;
@@ -1537,12 +1544,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX
 // Host launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
-                            bf16_t* phib, hipStream_t s) {
+                            bf16_t* phib, hipStream_t s, const void* weight, int w_dtype, int64_t C, float* w32) {
     const int64_t total = (int64_t)proj_tiles(np) * 2 * (K / 32) * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     MHC_LAUNCH_GGL(phi_split_kernel, dim3((unsigned)blocks), dim3(256), 0, s, pre, post, res, n, np, K,
-                       reinterpret_cast<uint4*>(phib));
+                       reinterpret_cast<uint4*>(phib), weight, w_dtype, C, w32);
     return hipGetLastError();
 }
 

@@ -501,6 +501,57 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
     if (MODE == 0 && threadIdx.x < NS) scal_out[(int64_t)blockIdx.x * NS + threadIdx.x] = sacc;
 }
 
+// Several deterministic column sums in one launch (ColSumJob in
+// mhc_internal.h): each job takes its own run of workgroups and sums as
+// layer_finalize_kernel's column blocks do (`phases` row phases of
+// 256 / phases columns, each phase over every phases-th row in order, the
+// phases added in order); columns below `split` go to `out` (fp32 or bf16),
+// the rest to `out2` (fp32).
+__global__ __launch_bounds__(256) void multi_column_sum_kernel(ColSumJobs jobs) {
+    __shared__ float cred[256];
+    int bid = (int)blockIdx.x;
+    int q = 0;
+    while (q + 1 < jobs.count && bid >= jobs.j[q].blocks) {
+        bid -= jobs.j[q].blocks;
+        ++q;
+    }
+    const ColSumJob jb = jobs.j[q];
+    const int phases = jb.phases;
+    const int cpb = 256 / phases;
+    const int cl = threadIdx.x % cpb;
+    const int ph = threadIdx.x / cpb;
+    const int64_t c = (int64_t)bid * cpb + cl;
+    const float* part = jb.part;
+    const int64_t cols = jb.cols;
+    float s = 0.f;
+    if (c < cols) {
+        int r = ph;
+        for (; r + 7 * phases < jb.rows; r += 8 * phases) {
+            float a[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = part[(int64_t)(r + u * phases) * cols + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += a[u];
+        }
+        for (; r < jb.rows; r += phases) s += part[(int64_t)r * cols + c];
+    }
+    float t = s;
+    if (phases > 1) {
+        cred[threadIdx.x] = s;
+        __syncthreads();
+        t = 0.f;
+        for (int k = 0; k < phases; ++k) t += cred[k * cpb + cl];
+    }
+    if (ph == 0 && c < cols) {
+        if (c < jb.split) {
+            if (jb.out_bf16) static_cast<bf16_t*>(jb.out)[c] = f32_to_bf16(t);
+            else static_cast<float*>(jb.out)[c] = t;
+        } else {
+            jb.out2[c - jb.split] = t;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Deterministic column sums of per-workgroup partials part[rows][cols]:
 // stage 1 (grid = col tiles of 256 x rsplit row groups) writes
@@ -984,6 +1035,27 @@ hipError_t launch_column_partial(const float* part, int rows, int64_t cols, floa
         MHC_LAUNCH_GGL(column_partial_kernel, dim3((unsigned)((cols + 255) / 256), rsplit), dim3(256), 0, s, part,
                            rows, cols, stage);
     }
+    return hipGetLastError();
+}
+
+bool column_sums_direct(int rows) { return rows >= 1 && rows <= kDirectRows; }
+
+hipError_t launch_multi_column_sum(ColSumJobs jobs, hipStream_t s) {
+    if (jobs.count < 1 || jobs.count > kMaxColSumJobs) return hipErrorInvalidValue;
+    int64_t blocks = 0;
+    for (int q = 0; q < jobs.count; ++q) {
+        ColSumJob& jb = jobs.j[q];
+        if (!column_sums_direct(jb.rows) || jb.cols < 1 || jb.split < 0 || jb.split > jb.cols ||
+            (jb.split < jb.cols && !jb.out2))
+            return hipErrorInvalidValue;
+        // as launch_layer_finalize; narrow jobs take more phases (shorter chains)
+        jb.phases = jb.cols <= 32 ? 16 : (jb.rows <= 16 ? 1 : (jb.rows <= 64 ? 2 : 4));
+        const int cpb = 256 / jb.phases;
+        jb.blocks = (int)((jb.cols + cpb - 1) / cpb);
+        blocks += jb.blocks;
+    }
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    MHC_LAUNCH_GGL(multi_column_sum_kernel, dim3((unsigned)blocks), dim3(256), 0, s, jobs);
     return hipGetLastError();
 }
 

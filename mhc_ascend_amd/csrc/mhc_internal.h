@@ -214,9 +214,11 @@ constexpr int dp_stride(int np) { return proj_tiles(np) * kProjTile; }
 // Largest number of projection rows (output tiles run one after another).
 constexpr int kMaxProjRows = 8192;
 // Phi [np rows, K] -> proj_tiles(np) output tiles of three bf16 planes
-// (3 * 32 * K bf16 each) in the projection kernel's operand order.
+// (3 * 32 * K bf16 each) in the projection kernel's operand order; with w32
+// the same launch converts the RMSNorm weight (C elements of w_dtype) too.
 hipError_t launch_phi_split(const float* pre, const float* post, const float* res, int n, int np, int64_t K,
-                            bf16_raw_t* phib, hipStream_t s);
+                            bf16_raw_t* phib, hipStream_t s, const void* weight = nullptr, int w_dtype = 0,
+                            int64_t C = 0, float* w32 = nullptr);
 int proj_ksplit(int64_t B, int64_t K, int np);
 // P partials of all proj_tiles(np) output tiles, tile-major:
 // p_part[tile][ks][B][32], plus ss_part[ks][B] = partial sums of x^2.
@@ -255,6 +257,28 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
                                float* hist, hipStream_t s);
+// Deterministic column sums of several partial matrices in one launch:
+// out[c] = sum_r part[r][c] over `rows` <= 512 rows (column_sums_direct),
+// columns c < split to `out` (bf16 when out_bf16, else fp32) and the rest to
+// out2 (fp32).  phases and blocks are set by the launcher.
+constexpr int kMaxColSumJobs = 3;
+struct ColSumJob {
+    const float* part;
+    void* out;
+    float* out2;
+    int64_t cols;
+    int rows;
+    int split;
+    int out_bf16;
+    int phases;
+    int blocks;
+};
+struct ColSumJobs {
+    ColSumJob j[kMaxColSumJobs];
+    int count;
+};
+bool column_sums_direct(int rows);
+hipError_t launch_multi_column_sum(ColSumJobs jobs, hipStream_t s);
 hipError_t launch_small_column_sum(const float* part, int rows, int cols, float* out_db, float* out_da, int np,
                                    hipStream_t s);
 // Projection backward (bf16 MFMA, split operands) over the flattened [B, K]
