@@ -240,9 +240,9 @@ class DynamicWorkload:
         lib.timing_enable(False)
         mfma_ms, mfma_n = lib.timing_query("proj")
         valu_ms, valu_n = lib.timing_query("proj_valu")
-        ref = x[:64].double() @ phi.double().t()
+        ref = x[:64].double().cpu() @ phi.double().cpu().t()
         scale = ref.abs().max().item()
-        err = {k: (runs[k][2][:64].double() - ref).abs().max().item() / scale for k in runs}
+        err = {k: (runs[k][2][:64].double().cpu() - ref).abs().max().item() / scale for k in runs}
         flops = 2 * B * K * npr
         mfma_avg, valu_avg = mfma_ms / max(mfma_n, 1), valu_ms / max(valu_n, 1)
         return {"shape": {"tokens": B, "k": K, "outputs": npr, "x_dtype": "bf16"},
