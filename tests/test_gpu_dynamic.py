@@ -305,13 +305,15 @@ def test_dynamic_layer_config_c4_full_size(device):
     _check_dyn(_run_dyn(sl, device), _oracle_dyn(sl), torch.bfloat16, "C4 slice")
 
 
-@pytest.mark.parametrize("B,C", [(1000, 1024), (257, 4096), (3001, 2048)])
+@pytest.mark.parametrize("B,C", [(1000, 1024), (257, 4096), (3001, 2048), (9001, 256)])
 def test_dynamic_layer_backward_many_tokens(device, B, C):
     """bf16 x at n = 4 with many tokens per persistent workgroup and a token
     count that fills no launch evenly: every token's dx (B <= 1000) or a
     strided third of them against the oracle, the parameter gradients against
     the oracle (B <= 1000) or by additivity over two parts split inside a
-    workgroup's token range."""
+    workgroup's token range.  At B = 9001 the whole batch has more than 512
+    rows of db / dalpha partials and takes the separate column-sum launches,
+    its two parts the single multi-job launch."""
     n = 4
     d = R.dynamic_layer_inputs(B, n, C, seed=B + C, alpha=0.3, phi_std=0.05, b_std=0.5)
     if B <= 1000:
