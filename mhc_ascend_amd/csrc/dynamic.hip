@@ -1247,33 +1247,39 @@ __device__ __forceinline__ void lds_put4(char* p, const float (&v)[4]) {
 
 // LDS row pitch of a 128-column stage tile (8-byte aligned rows; 8 extra
 // bytes spread the token rows read by the four lane groups over the banks).
-template <typename TX> constexpr int pb_pitch() { return 128 * (int)sizeof(TX) + 8; }
+template <typename TX, int CB> constexpr int pb_pitch() { return CB * (int)sizeof(TX) + 8; }
 constexpr int kDpPitch = 40;  // bf16 per row of the split dP copies (32 + 8 pad)
 
 // Waves per SIMD the register allocation targets: four for bf16 x (128
 // registers, no spills; four 35.6 KB workgroups share a CU's LDS), two for
 // fp32 x, whose split operands need more.
 template <typename TX> constexpr int kPbWaves() { return sizeof(TX) == 2 ? 4 : 2; }
+// Waves per workgroup (32 columns each): eight for bf16 x (256 columns), four
+// for fp32 x (128 columns).
+template <typename TX> constexpr int kPbNW() { return sizeof(TX) == 2 ? 8 : 4; }
 
 template <typename TX, bool ACC, bool HAS_S>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX>()))) void proj_bwd_mfma_kernel(
+__global__ __launch_bounds__(64 * kPbNW<TX>()) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX>()))) void proj_bwd_mfma_kernel(
     const TX* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
     const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
     int n_pre, int o0, int np, TX* __restrict__ dx, const float* __restrict__ dx_step, int groups, int C,
     float* __restrict__ dphi_part, int64_t B, int64_t K, int64_t tile) {
     // With bf16 x the incoming dx (ACC) is the row pass's int16 fixed-point
-    // stream part (fixed_scale) with steps dx_step[b][groups]: this block's
-    // 128 columns (channels c .. c + 127 of one stream) are group
+    // stream part (fixed_scale) with steps dx_step[b][groups]: each 128
+    // columns of this block (channels c .. c + 127 of one stream) are group
     // (c / 128) % groups of every token.  The sum is rounded once to bf16 on
     // the way out.
     constexpr bool QIN = ACC && sizeof(TX) == 2;
+    constexpr int NT = 64 * kPbNW<TX>();
     constexpr int TB = 32;                      // tokens per stage
-    constexpr int CB = 128;                     // columns per workgroup
+    constexpr int CB = 32 * kPbNW<TX>();        // columns per workgroup
+    constexpr int NG = CB / kFixedGroup;        // fixed-point groups per workgroup
     constexpr int EPV = 16 / sizeof(TX);        // elements per 16-byte vector
     constexpr int VPR = CB / EPV;               // vectors per tile row
-    constexpr int RPP = 256 / VPR;              // tile rows per load pass
+    constexpr int RPP = NT / VPR;               // tile rows per load pass
     constexpr int PASSES = TB / RPP;
-    constexpr int PITCH = pb_pitch<TX>();
+    constexpr int PITCH = pb_pitch<TX, CB>();
+    static_assert(PASSES * RPP == TB && CB % kFixedGroup == 0 && NG * TB <= NT, "stage shape");
     // Only the dx tile is double-buffered: a stage's store reads it while
     // the next stage is committed.  x, the dP copies and s of the next
     // stage are committed after the barrier that ends the compute reading
@@ -1283,7 +1289,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX
     __shared__ __align__(16) char dx_lds[2][TB * PITCH];
     __shared__ __align__(16) bf16_t dps_lds[4][32 * kDpPitch];  // hi_row, lo_row, hi_col, lo_col
     __shared__ float s_lds[TB];
-    __shared__ float q_lds[QIN ? TB : 1];
+    __shared__ float q_lds[QIN ? NG : 1][QIN ? TB : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1298,7 +1304,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX
     const int lvec = tid % VPR;
     const int64_t lcol = kb0 + (int64_t)lvec * EPV;
     const bool lcol_ok = lcol < K;
-    const int dtk = tid >> 3;
+    // dP loaders: lanes 0..255, token tid / 8, outputs 4 (tid % 8) .. + 3
+    const bool dp_on = tid < 256;
+    const int dtk = (tid & 255) >> 3;
     const int dpo = (tid & 7) * 4;
 
     // dx_proj A operands (Phi^T): Phi[8 lg + e][column 16 ct + lr]
@@ -1335,13 +1343,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX
     const buf_rsrc_t rs_dx = make_buf_rsrc(dx + t_begin * K, (uint32_t)(nrows * xrow));
     const buf_rsrc_t rs_p = make_buf_rsrc(dP + t_begin * dp_stride, (uint32_t)(nrows * dp_stride * 4));
     const buf_rsrc_t rs_s = make_buf_rsrc(HAS_S ? s_tok + t_begin : s_tok, HAS_S ? (uint32_t)(nrows * 4) : 0u);
-    const int grp = QIN ? (int)((kb0 % C) / kFixedGroup) % groups : 0;
+    // step loaders: lane tid < NG TB takes group tid / TB of token tid % TB
+    const int qg = tid / TB;
+    const int grp = QIN ? (int)(((kb0 + (int64_t)qg * kFixedGroup) % C) / kFixedGroup) % groups : 0;
     const buf_rsrc_t rs_q =
         make_buf_rsrc(QIN ? dx_step + t_begin * groups : dx_step, QIN ? (uint32_t)(nrows * groups * 4) : 0u);
     const uint32_t xo = lcol_ok ? (uint32_t)lrow * xrow + (uint32_t)(lcol * (int64_t)sizeof(TX)) : kBufOff;
-    const uint32_t po = (uint32_t)(dtk * dp_stride + dpo) * 4u;
+    const uint32_t po = dp_on ? (uint32_t)(dtk * dp_stride + dpo) * 4u : kBufOff;
     const uint32_t so = tid < TB ? (uint32_t)tid * 4u : kBufOff;
-    const uint32_t qo = tid < TB ? (uint32_t)(tid * groups + grp) * 4u : kBufOff;
+    const uint32_t qo = tid < NG * TB ? (uint32_t)((tid % TB) * groups + grp) * 4u : kBufOff;
 
     // Two register sets of fetched row tiles: stage i+2 is fetched while
     // stage i computes and stage i+1 (fetched one stage earlier) moves into
@@ -1376,7 +1386,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX
         // their registers makes every lane wait for them in straight-line
         // code, so the compiler's wait counts do not carry them as possibly
         // in flight past it.
-        asm volatile("" ::"v"(sm.s), "v"(sm.q));
+        asm volatile("" ::"v"(sm.s), "v"(sm.q), "v"(sm.dp.x), "v"(sm.dp.y), "v"(sm.dp.z), "v"(sm.dp.w));
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = lrow + p * RPP;
@@ -1393,28 +1403,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX
         }
         // dP of token dtk, o = dpo .. dpo + 3: split once into hi / lo bf16,
         // token-major (one 8-byte write each) and o-major copies
-        const uint32_t dw4[4] = {sm.dp.x, sm.dp.y, sm.dp.z, sm.dp.w};
-        float hi[4], lo[4];
+        if (dp_on) {
+            const uint32_t dw4[4] = {sm.dp.x, sm.dp.y, sm.dp.z, sm.dp.w};
+            float hi[4], lo[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float v = dpo + q < np ? __uint_as_float(dw4[q]) : 0.f;
-            hi[q] = bf16_to_f32(f32_to_bf16(v));
-            lo[q] = v - hi[q];
-        }
-        *reinterpret_cast<uint2*>(&dps_lds[0][dtk * kDpPitch + dpo]) =
-            make_uint2(pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
-        *reinterpret_cast<uint2*>(&dps_lds[1][dtk * kDpPitch + dpo]) =
-            make_uint2(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]));
+            for (int q = 0; q < 4; ++q) {
+                const float v = dpo + q < np ? __uint_as_float(dw4[q]) : 0.f;
+                hi[q] = bf16_to_f32(f32_to_bf16(v));
+                lo[q] = v - hi[q];
+            }
+            *reinterpret_cast<uint2*>(&dps_lds[0][dtk * kDpPitch + dpo]) =
+                make_uint2(pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
+            *reinterpret_cast<uint2*>(&dps_lds[1][dtk * kDpPitch + dpo]) =
+                make_uint2(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            dps_lds[2][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(hi[q]);
-            dps_lds[3][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(lo[q]);
+            for (int q = 0; q < 4; ++q) {
+                dps_lds[2][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(hi[q]);
+                dps_lds[3][(dpo + q) * kDpPitch + dtk] = f32_to_bf16(lo[q]);
+            }
         }
         if constexpr (HAS_S) {
             if (tid < TB) s_lds[tid] = __uint_as_float(sm.s);
         }
         if constexpr (QIN) {
-            if (tid < TB) q_lds[tid] = __uint_as_float(sm.q);
+            if (tid < NG * TB) q_lds[qg][tid % TB] = __uint_as_float(sm.q);
         }
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> u32x4_t {
@@ -1470,7 +1482,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX
                 float xv[4], dv[4];
                 lds_get4<TX>(xt + boff, xv);
                 if constexpr (QIN) {
-                    fixed_unpack4(*reinterpret_cast<const uint2*>(dt + boff), q_lds[t], dv);
+                    fixed_unpack4(*reinterpret_cast<const uint2*>(dt + boff), q_lds[c0 / kFixedGroup][t], dv);
                 } else if constexpr (ACC) {
                     lds_get4<TX>(dt + boff, dv);
                 } else {
@@ -2570,11 +2582,12 @@ static int64_t proj_bwd_max_tile(int x_dtype, int64_t K) {
 }
 
 int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
-    const int64_t gx = (K + 127) / 128;
+    const int cb = 32 * (x_dtype == kBF16 ? kPbNW<bf16_t>() : kPbNW<float>());
+    const int64_t gx = (K + cb - 1) / cb;
     const void* fn = x_dtype == kBF16 ? reinterpret_cast<const void*>(&proj_bwd_mfma_kernel<bf16_t, true, true>)
                                       : reinterpret_cast<const void*>(&proj_bwd_mfma_kernel<float, true, true>);
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu < 1) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 2 * cb, 0) != hipSuccess || per_cu < 1) {
         (void)hipGetLastError();
         per_cu = 1;
     }
@@ -2601,9 +2614,10 @@ hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_s
     int64_t tile = (B + tiles - 1) / tiles;
     tile = ((tile + 63) / 64) * 64;
     if (tile > proj_bwd_max_tile(x_dtype, K)) return hipErrorInvalidValue;  // offsets past 2 GiB
-    const dim3 grid((unsigned)((K + 127) / 128), (unsigned)tiles);
+    const int cb = 32 * (x_dtype == kBF16 ? kPbNW<bf16_t>() : kPbNW<float>());  // columns per workgroup
+    const dim3 grid((unsigned)((K + cb - 1) / cb), (unsigned)tiles);
 #define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \
-    MHC_LAUNCH_GGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(256), 0, s, (const TX_*)x, dP, dp_stride,  \
+    MHC_LAUNCH_GGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(2 * cb), 0, s, (const TX_*)x, dP, dp_stride,  \
                        s_tok, phi_pre, phi_post, phi_res, n_pre, o0, np, (TX_*)dx, dx_step, groups, C, dphi_part, B, K, \
                        tile)
     // The layer backward accumulates (with the r_h term on the first output
