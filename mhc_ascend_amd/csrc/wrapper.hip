@@ -989,13 +989,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
 // ---------------------------------------------------------------------------
 typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
 
-// Workgroup of the projection backward: 4 waves x 16 channels.  Two such
-// workgroups share a CU (register-bound at two waves per SIMD) and run their
-// stages out of step, so one's loads proceed while the other computes; one
-// 512-lane workgroup per CU moved its waves through the stages in lockstep
-// and left the memory pipe idle during the compute phase (5.05 against
-// about 3.75 ms for the same traffic without compute at C5).
-constexpr int kWpbThreads = 256;
+// Workgroup of the projection backward: 8 waves x 16 channels, one per CU at
+// three waves per SIMD of registers.  A stage's row pieces are 256 bytes of
+// r and b and 512 of G per token: the bare access pattern runs at 6.0 TB/s
+// in this shape against 5.5 with 4-wave workgroups over 64 channels (three
+// per CU), and the kernel went from 4.8-5.2 to 4.7 ms at C5.
+constexpr int kWpbThreads = 512;
 constexpr int kWpbCols = kWpbThreads / 64 * 16;
 // Waves per SIMD the register allocation targets: three for bf16 storage
 // (168 registers; the stages' chains of LDS reads and MFMAs are latency-
