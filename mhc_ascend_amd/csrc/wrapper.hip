@@ -996,10 +996,9 @@ typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
 // per CU), and the kernel went from 4.8-5.2 to 4.7 ms at C5.
 constexpr int kWpbThreads = 512;
 constexpr int kWpbCols = kWpbThreads / 64 * 16;
-// Waves per SIMD the register allocation targets: three for bf16 storage
-// (168 registers; the stages' chains of LDS reads and MFMAs are latency-
-// bound at two), two for fp32 storage, whose wider operands would spill.
-template <typename TX> constexpr int kWpbWaves() { return sizeof(TX) == 2 ? 3 : 2; }
+// Waves per SIMD the register allocation targets: two (one 8-wave workgroup
+// per CU either way), so three stages of rows and records fit in registers.
+template <typename TX> constexpr int kWpbWaves() { return 2; }
 
 template <typename TX> constexpr int wpb_pitch() { return kWpbCols * (int)sizeof(TX) + 8; }
 constexpr int kWDpPitch = 40;
@@ -1156,19 +1155,16 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
     const uint32_t eo = ep_loader ? (uint32_t)(etk * kWrapEp + 4 * epc) * 4u : kBufOff;
     const uint32_t so = (ep_loader && epc == 2) ? (uint32_t)etk * 4u : kBufOff;
 
-    // Row tiles of a stage are fetched two stages ahead (two register sets);
-    // its small per-token records one stage ahead, before the row tiles of
-    // the stage after, so that waiting for them leaves those in flight.
+    // A stage's row tiles and per-token records are fetched three stages
+    // ahead, into one of three register sets, so two stages stay in flight
+    // while one is committed.
     struct Fetched {
         uint4 v[2][PASSES];
         uint4 gq[GPASSES];
-    };
-    struct Small {
         uint4 e, dp;
         uint32_t s;
     };
-    Fetched f0, f1;
-    Small sm;
+    Fetched f0, f1, f2;
     // the stage of rows rel .. rel + TB - 1 (relative to t_begin)
     auto fetch = [&](Fetched& f, uint32_t rel) __attribute__((always_inline)) {
 #pragma unroll
@@ -1181,12 +1177,13 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         for (int p = 0; p < GPASSES; ++p)
             f.gq[p] = buf_ld16<true>(rs_g, go + (rel + p * GRPP) * (uint32_t)C * 4u, 0u);
     };
-    auto fetch_small = [&](uint32_t rel) __attribute__((always_inline)) {
+    auto fetch_small = [&](Fetched& sm, uint32_t rel) __attribute__((always_inline)) {
         sm.dp = buf_ld16<false>(rs_p, po + rel * 128u, 0u);
         sm.e = buf_ld16<false>(rs_e, eo + rel * (uint32_t)(kWrapEp * 4), 0u);
         sm.s = buf_ld4(rs_s, so + rel * 4u, 0u);
     };
     auto commit = [&](const Fetched& f) __attribute__((always_inline)) {
+        const Fetched& sm = f;
         // The small records are consumed behind branches below; an empty use
         // of their registers here makes every lane wait for them in straight-
         // line code, so the compiler's wait counts do not carry them as
@@ -1339,9 +1336,9 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
     // Two register sets: stage i+2 is fetched while stage i computes
     // (fetches and commits past the last row read zeros).
     auto step = [&](uint32_t r, Fetched& fc, Fetched& fp) __attribute__((always_inline)) {
-        // stage r is in LDS, fc holds the rows of stage r + TB, fp is free
-        fetch_small(r + TB);
-        fetch(fp, r + 2 * TB);
+        // stage r is in LDS, fc holds stage r + TB, fp is free
+        fetch_small(fp, r + 3 * TB);
+        fetch(fp, r + 3 * TB);
         compute();
         __syncthreads();
         store(r);
@@ -1349,19 +1346,23 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         __syncthreads();
     };
     const uint32_t nr = (uint32_t)nrows;
-    fetch_small(0u);
+    fetch_small(f0, 0u);
     fetch(f0, 0u);
     commit(f0);
+    fetch_small(f1, TB);
     fetch(f1, TB);
+    fetch_small(f2, 2 * TB);
+    fetch(f2, 2 * TB);
     __syncthreads();
-    // Whole pairs of stages: with an odd count the last one reads only zeros,
-    // adds zeros and stores nothing.  An exit between the two would leave a
-    // path (seen by the compiler, never taken) from the first stage back to
-    // the loop head with its fetch outstanding, and the wait counts would
-    // then hold every loop head until that fetch had landed.
-    for (uint32_t r0 = 0; r0 < nr; r0 += 2 * TB) {
+    // Whole triples of stages: stages past the last row read only zeros, add
+    // zeros and store nothing.  An exit between them would leave a path
+    // (seen by the compiler, never taken) from a stage back to the loop head
+    // with its fetch outstanding, and the wait counts would then hold every
+    // loop head until that fetch had landed.
+    for (uint32_t r0 = 0; r0 < nr; r0 += 3 * TB) {
         step(r0, f1, f0);
-        step(r0 + TB, f0, f1);
+        step(r0 + TB, f2, f1);
+        step(r0 + 2 * TB, f0, f2);
     }
     if (!wave_on) return;
     // dw partial: dwacc[i] sums this lane's tokens at channel wc0 + 4 lg + i;
@@ -1575,9 +1576,10 @@ hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const vo
 // (rounded down, so a last partial round is nearly full rather than leaving
 // most CUs idle while it runs), at least one, and enough that a tile's rows
 // of G, plus the three stages the pipeline reads past its end, stay under
-// 2 GiB (the kernel's buffer resources and offsets).  Tiles are whole pairs
-// of 32-token stages; the pipeline reads up to four stages past the end.
-static int64_t wrap_proj_bwd_max_tile(int64_t C) { return ((int64_t(1) << 31) - 1) / (C * 4) - 4 * 32; }
+// 2 GiB (the kernel's buffer resources and offsets).  Tiles are whole
+// triples of 32-token stages; the pipeline reads up to six stages past the
+// end.
+static int64_t wrap_proj_bwd_max_tile(int64_t C) { return ((int64_t(1) << 31) - 1) / (C * 4) - 6 * 32; }
 
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
     const int64_t gx = (C + kWpbCols - 1) / kWpbCols;
@@ -1592,8 +1594,8 @@ int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
     const int64_t blocks = (B + 31) / 32;
     if (tiles > blocks) tiles = blocks;
     if (tiles < 1) tiles = 1;
-    const int64_t mt = wrap_proj_bwd_max_tile(C) / 64 * 64;
-    if (mt >= 64 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
+    const int64_t mt = wrap_proj_bwd_max_tile(C) / 96 * 96;
+    if (mt >= 96 && (B + tiles - 1) / tiles > mt) tiles = (B + mt - 1) / mt;
     return (int)tiles;
 }
 
@@ -1605,7 +1607,7 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
     if (B == 0) return hipSuccess;
     if (n != 4 || C % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
     int64_t tile = (B + tiles - 1) / tiles;
-    tile = ((tile + 63) / 64) * 64;
+    tile = ((tile + 95) / 96) * 96;
     if (tile > wrap_proj_bwd_max_tile(C)) return hipErrorInvalidValue;  // offsets past 2 GiB
     const dim3 grid((unsigned)((C + kWpbCols - 1) / kWpbCols), (unsigned)tiles);
     const int tok = timing_begin("wrap_proj_bwd", s);
