@@ -983,8 +983,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
 // the per-token factors of wrap_bwd_red_kernel (sum_j w_j dX_j = A_r G +
 // B_r gxa, dX_1 = A_b G + B_b gxa).
 // Every term is summed in fp32 and d r / d b are rounded once to the storage
-// dtype.  Workgroup = 4 waves x 16 columns; stages of 32 tokens with r, b
-// and G staged in LDS (two stages in flight in registers); results go
+// dtype.  Workgroup = 8 waves x 16 columns; stages of 32 tokens with r, b
+// and G staged in LDS (three stages in flight in registers); results go
 // through one LDS tile per output and leave with coalesced 16-byte stores.
 // ---------------------------------------------------------------------------
 typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
