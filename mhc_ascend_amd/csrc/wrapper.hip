@@ -1238,7 +1238,32 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         const char* gt = g_lds;
         // dPhi: B operands x_j over tokens 8 lg .. + 7 at column wc0 + lr
         wu32x4_t xh[NSTR], xl[NSTR];
-        {
+        if constexpr (sizeof(TX) == 2) {
+            // bf16 pairs of tokens (e, e + 1) at column c straight from the
+            // raw halves; the decay streams rounded pairwise by one conversion
+            const int c = wc0 + lr;
+            uint32_t rr[8], bb[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = 8 * lg + e;
+                rr[e] = *reinterpret_cast<const uint16_t*>(rt + t * PITCH + c * 2);
+                bb[e] = *reinterpret_cast<const uint16_t*>(bt + t * PITCH + c * 2);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xh[0][e] = rr[2 * e] | (rr[2 * e + 1] << 16);
+                if constexpr (NSTR > 1) xh[1][e] = bb[2 * e] | (bb[2 * e + 1] << 16);
+                if constexpr (NSTR > 2) {
+                    const float r0 = __uint_as_float(rr[2 * e] << 16), r1 = __uint_as_float(rr[2 * e + 1] << 16);
+                    constexpr float m2 = decay_mult<2>();
+                    xh[2][e] = wpack(r0 * m2, r1 * m2);
+                    if constexpr (NSTR > 3) {
+                        constexpr float m3 = decay_mult<3>();
+                        xh[3][e] = wpack(r0 * m3, r1 * m3);
+                    }
+                }
+            }
+        } else {
             const int c = wc0 + lr;
             float xs[NSTR][8];
 #pragma unroll
@@ -1252,14 +1277,7 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
                 for (int j = 0; j < NSTR; ++j) xs[j][e] = x[j];
             }
 #pragma unroll
-            for (int j = 0; j < NSTR; ++j) {
-                if constexpr (sizeof(TX) == 2) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) xh[j][e] = wpack(xs[j][2 * e], xs[j][2 * e + 1]);  // exact
-                } else {
-                    wsplit_pack8(xs[j], xh[j], xl[j]);
-                }
-            }
+            for (int j = 0; j < NSTR; ++j) wsplit_pack8(xs[j], xh[j], xl[j]);
         }
 #pragma unroll
         for (int ot = 0; ot < 2; ++ot) {
