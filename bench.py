@@ -11,8 +11,9 @@ roofline of the dominant kernel (HIP events around each of its launches on
 the stream the library launches on, in a separate pass after the timed
 region), and a CPU baseline (the PyTorch oracle on the host cores, on a
 bounded token sample).  The default static workload (C3, the metric's
-configuration) also carries a sub-record of the dynamic-H workload (C4), the
-reference layer's default path, measured the same way.
+configuration) also carries sub-records of the dynamic-H workload (C4, the
+reference layer's default path), the wrapper (C5), the standalone operators
+(C2) and the forward-only entry at the C4 shape, each measured the same way.
 
 Workloads (the metric is quoted at n=4, C=4096):
   static  - C3: MHCLayer static-H, x fp32 [8192, 4, 4096]          (default)
@@ -669,7 +670,7 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel-steps", type=int, default=10, help="steps of the per-kernel timing pass")
     ap.add_argument("--extra", action="append", default=None, choices=sorted(WORKLOADS),
                     help="with the default static workload: also measure these workloads as sub-records "
-                         "(default: dynamic, the reference layer's default path, and wrapper)")
+                         "(default: dynamic, the reference layer's default path; wrapper; ops; infer)")
     ap.add_argument("--no-extra", action="store_true", help="no sub-records")
     ap.add_argument("--extra-steps", type=int, default=50,
                     help="timed steps of each sub-record (enough that the first launch and the final drain, "
@@ -683,7 +684,7 @@ def main(argv=None) -> int:
     if a.no_extra:
         a.extra = []
     elif a.extra is None:
-        a.extra = ["dynamic", "wrapper"]
+        a.extra = ["dynamic", "wrapper", "ops", "infer"]
 
     import torch
 
@@ -721,7 +722,8 @@ def main(argv=None) -> int:
                            a.cpu_seconds, a.copy_calib)
     if a.workload == "static" and a.extra:
         # the reference layer's default path (use_dynamic_h=True, layer.py:48)
-        # at the same n and C, measured the same way
+        # at the same n and C, and the other BASELINE configurations,
+        # measured the same way
         sub = {}
         for name in a.extra:
             sub[name] = measure_workload(name, torch, mhc, _lib, device, a.extra_steps, a.warmup, a.protocol_runs,

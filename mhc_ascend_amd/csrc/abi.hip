@@ -675,7 +675,7 @@ static ProjBwdWs proj_bwd_ws(int64_t batch, int64_t k, int32_t out_dim) {
 static hipError_t proj_bwd_all(int x_dtype, const void* x, const float* dp, int dp_stride_, const float* s_tok,
                                const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                                void* dx, bool accumulate, float* part, int tiles, float* stage, float* grad_phi,
-                               int64_t batch, int64_t K, hipStream_t s, const float* dx_step = nullptr,
+                               int64_t batch, int64_t K, hipStream_t s, const int32_t* dx_scale = nullptr,
                                int groups = 0) {
     if (batch > 0 && proj_bwd_wide_path(x_dtype, np, batch))
         return launch_proj_bwd_wide((const float*)x, dp, dp_stride_, s_tok, phi_pre, phi_post, phi_res, n_pre, np,
@@ -690,7 +690,7 @@ static hipError_t proj_bwd_all(int x_dtype, const void* x, const float* dp, int 
         } else {
             e = launch_proj_bwd(x_dtype, x, dp + o0, dp_stride_, o0 == 0 ? s_tok : nullptr, phi_pre, phi_post,
                                 phi_res, n_pre, o0, rows_t, dx, accumulate || o0 > 0, part, tiles, batch, K, s,
-                                dx_step, groups);
+                                dx_scale, groups);
         }
         if (e == hipSuccess)
             e = launch_column_finalize(0, kF32, part, rows, (int64_t)rows_t * K, stage, grad_phi + (int64_t)o0 * K,
@@ -889,9 +889,13 @@ int mhc_layer_dynamic_infer(const void* x, int32_t x_dtype, const void* packed, 
 // dx of bf16 x is rounded to bf16 once, from the fp32 sum of the row pass's
 // stream part and the projection's terms, as the reference's fp32 autograd
 // does.  With one 32-row projection tile (n <= 4) on the register-row
-// kernels and hidden % 128 == 0 the stream part travels as int16 fixed point
-// (one scale per half wave of the row kernel and token, in the workspace)
-// and the projection kernel rounds the sum.  Otherwise (n >= 8, rows the channel-loop kernels take,
+// kernels and hidden % 128 == 0 the stream part travels as fp16 against a
+// power-of-two scale (11 significant bits; one scale exponent per half wave
+// of the row kernel and token, in the workspace) and the projection kernel
+// rounds the sum: each element's stream part then enters the sum with a
+// relative error of at most 2^-11 (an eighth of the bf16 half-ulp) down to
+// 2^-28 of its group's largest element, and within 2^-39 of that largest
+// element below.  Otherwise (n >= 8, rows the channel-loop kernels take,
 // other hidden sizes) x is upcast once (exactly) and dx accumulates in fp32
 // across the kernels.
 static bool dyn_bwd_f32_acc(int32_t n, int32_t hidden, int32_t x_dtype) {
@@ -901,8 +905,8 @@ static bool dyn_bwd_f32_acc(int32_t n, int32_t hidden, int32_t x_dtype) {
 struct DynBwdWs {
     int grid, cblocks, tiles;
     int wdt;     // element type the row and projection kernels run on
-    int groups;  // fixed-point groups per token of the bf16 stream part
-    size_t dw_off, scal_off, dp_off, s_off, step_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, hist_off,
+    int groups;  // scale groups per token of the bf16 stream part
+    size_t dw_off, scal_off, dp_off, s_off, pscale_off, cpart_off, phip_off, stw_off, stp_off, xw_off, dxw_off, hist_off,
         rows_off, total;
 };
 
@@ -919,9 +923,9 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     w.scal_off = o; o += align256((size_t)batch * (n * n + 2 * n + 2) * 4);
     w.dp_off = o; o += align256((size_t)batch * dp_stride((int)np) * 4);
     w.s_off = o; o += align256((size_t)batch * 4);
-    // fixed-point steps of the bf16 stream part
-    w.groups = w.wdt == kBF16 ? layer_bwd_fixed_groups(w.wdt, n, hidden) : 0;
-    w.step_off = o; o += align256((size_t)batch * w.groups * 4);
+    // scale exponents of the bf16 stream part
+    w.groups = w.wdt == kBF16 ? layer_bwd_part_groups(w.wdt, n, hidden) : 0;
+    w.pscale_off = o; o += align256((size_t)batch * w.groups * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     // projection partials (per-tile path) or dP planes (all-tiles path)
     size_t phip = (size_t)w.tiles * tile_rows((int)np) * K * 4;
@@ -978,7 +982,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     float* stp = (float*)(ws + w.stp_off);
     float* xw = (float*)(ws + w.xw_off);
     float* dxw = (float*)(ws + w.dxw_off);
-    float* step = w.wdt == kBF16 ? (float*)(ws + w.step_off) : nullptr;
+    int32_t* pscale = w.wdt == kBF16 ? (int32_t*)(ws + w.pscale_off) : nullptr;
     // the tensors the row and projection kernels work on
     const void* xk = w.wdt != x_dtype ? (const void*)xw : x;
     void* dxk = w.wdt != x_dtype ? (void*)dxw : grad_x;
@@ -996,7 +1000,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         if (w.wdt != x_dtype) e = launch_weight_f32(x, x_dtype, batch * K, xw, s);
         if (e == hipSuccess)
             e = launch_layer_bwd(w.wdt, n, 1, grad_out, xk, w32, saved + d.coef_off, np, dxk, dw_part, scal, w.grid,
-                                 batch, hidden, rmsnorm_eps, (float*)(ws + w.rows_off), s, step);
+                                 batch, hidden, rmsnorm_eps, (float*)(ws + w.rows_off), s, pscale);
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
@@ -1010,7 +1014,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     if (one_sum) {
         if (e == hipSuccess)
             e = launch_proj_bwd(w.wdt, xk, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, 0, np, dxk, true,
-                                phip, rows_p, batch, K, s, step, w.groups);
+                                phip, rows_p, batch, K, s, pscale, w.groups);
         if (e == hipSuccess && w.wdt != x_dtype) e = launch_cast_bf16(dxw, batch * K, grad_x, s);
         if (e == hipSuccess) {
             ColSumJobs jobs{};
@@ -1024,7 +1028,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     }
     if (e == hipSuccess)
         e = proj_bwd_all(w.wdt, xk, dp, dp_stride(np), stok, phi_pre, phi_post, phi_res, n, np, dxk, true, phip,
-                         rows_p, stp, grad_phi, batch, K, s, step, w.groups);
+                         rows_p, stp, grad_phi, batch, K, s, pscale, w.groups);
     if (e == hipSuccess && w.wdt != x_dtype) e = launch_cast_bf16(dxw, batch * K, grad_x, s);
     if (e == hipSuccess)
         e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr, nullptr,

@@ -1262,24 +1262,24 @@ template <typename TX, bool ACC, bool HAS_S>
 __global__ __launch_bounds__(64 * kPbNW<TX>()) __attribute__((amdgpu_waves_per_eu(kPbWaves<TX>()))) void proj_bwd_mfma_kernel(
     const TX* __restrict__ x, const float* __restrict__ dP, int dp_stride, const float* __restrict__ s_tok,
     const float* __restrict__ phi_pre, const float* __restrict__ phi_post, const float* __restrict__ phi_res,
-    int n_pre, int o0, int np, TX* __restrict__ dx, const float* __restrict__ dx_step, int groups, int C,
+    int n_pre, int o0, int np, TX* __restrict__ dx, const int32_t* __restrict__ dx_scale, int groups, int C,
     float* __restrict__ dphi_part, int64_t B, int64_t K, int64_t tile) {
-    // With bf16 x the incoming dx (ACC) is the row pass's int16 fixed-point
-    // stream part (fixed_scale) with steps dx_step[b][groups]: each 128
-    // columns of this block (channels c .. c + 127 of one stream) are group
-    // (c / 128) % groups of every token.  The sum is rounded once to bf16 on
-    // the way out.
+    // With bf16 x the incoming dx (ACC) is the row pass's stream part as fp16
+    // against power-of-two scales (part_pack4) with exponents
+    // dx_scale[b][groups]: each 128 columns of this block (channels c .. c +
+    // 127 of one stream) are group (c / 128) % groups of every token.  The
+    // sum is rounded once to bf16 on the way out.
     constexpr bool QIN = ACC && sizeof(TX) == 2;
     constexpr int NT = 64 * kPbNW<TX>();
     constexpr int TB = 32;                      // tokens per stage
     constexpr int CB = 32 * kPbNW<TX>();        // columns per workgroup
-    constexpr int NG = CB / kFixedGroup;        // fixed-point groups per workgroup
+    constexpr int NG = CB / kPartGroup;         // stream-part scale groups per workgroup
     constexpr int EPV = 16 / sizeof(TX);        // elements per 16-byte vector
     constexpr int VPR = CB / EPV;               // vectors per tile row
     constexpr int RPP = NT / VPR;               // tile rows per load pass
     constexpr int PASSES = TB / RPP;
     constexpr int PITCH = pb_pitch<TX, CB>();
-    static_assert(PASSES * RPP == TB && CB % kFixedGroup == 0 && NG * TB <= NT, "stage shape");
+    static_assert(PASSES * RPP == TB && CB % kPartGroup == 0 && NG * TB <= NT, "stage shape");
     // Only the dx tile is double-buffered: a stage's store reads it while
     // the next stage is committed.  x, the dP copies and s of the next
     // stage are committed after the barrier that ends the compute reading
@@ -1289,7 +1289,7 @@ __global__ __launch_bounds__(64 * kPbNW<TX>()) __attribute__((amdgpu_waves_per_e
     __shared__ __align__(16) char dx_lds[2][TB * PITCH];
     __shared__ __align__(16) bf16_t dps_lds[4][32 * kDpPitch];  // hi_row, lo_row, hi_col, lo_col
     __shared__ float s_lds[TB];
-    __shared__ float q_lds[QIN ? NG : 1][QIN ? TB : 1];
+    __shared__ int q_lds[QIN ? NG : 1][QIN ? TB : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1345,9 +1345,9 @@ __global__ __launch_bounds__(64 * kPbNW<TX>()) __attribute__((amdgpu_waves_per_e
     const buf_rsrc_t rs_s = make_buf_rsrc(HAS_S ? s_tok + t_begin : s_tok, HAS_S ? (uint32_t)(nrows * 4) : 0u);
     // step loaders: lane tid < NG TB takes group tid / TB of token tid % TB
     const int qg = tid / TB;
-    const int grp = QIN ? (int)(((kb0 + (int64_t)qg * kFixedGroup) % C) / kFixedGroup) % groups : 0;
+    const int grp = QIN ? (int)(((kb0 + (int64_t)qg * kPartGroup) % C) / kPartGroup) % groups : 0;
     const buf_rsrc_t rs_q =
-        make_buf_rsrc(QIN ? dx_step + t_begin * groups : dx_step, QIN ? (uint32_t)(nrows * groups * 4) : 0u);
+        make_buf_rsrc(QIN ? dx_scale + t_begin * groups : dx_scale, QIN ? (uint32_t)(nrows * groups * 4) : 0u);
     const uint32_t xo = lcol_ok ? (uint32_t)lrow * xrow + (uint32_t)(lcol * (int64_t)sizeof(TX)) : kBufOff;
     const uint32_t po = dp_on ? (uint32_t)(dtk * dp_stride + dpo) * 4u : kBufOff;
     const uint32_t so = tid < TB ? (uint32_t)tid * 4u : kBufOff;
@@ -1426,7 +1426,7 @@ __global__ __launch_bounds__(64 * kPbNW<TX>()) __attribute__((amdgpu_waves_per_e
             if (tid < TB) s_lds[tid] = __uint_as_float(sm.s);
         }
         if constexpr (QIN) {
-            if (tid < NG * TB) q_lds[qg][tid % TB] = __uint_as_float(sm.q);
+            if (tid < NG * TB) q_lds[qg][tid % TB] = (int)sm.q;
         }
     };
     auto read16 = [&](const bf16_t* p) __attribute__((always_inline)) -> u32x4_t {
@@ -1482,7 +1482,7 @@ __global__ __launch_bounds__(64 * kPbNW<TX>()) __attribute__((amdgpu_waves_per_e
                 float xv[4], dv[4];
                 lds_get4<TX>(xt + boff, xv);
                 if constexpr (QIN) {
-                    fixed_unpack4(*reinterpret_cast<const uint2*>(dt + boff), q_lds[c0 / kFixedGroup][t], dv);
+                    part_unpack4(*reinterpret_cast<const uint2*>(dt + boff), q_lds[c0 / kPartGroup][t], dv);
                 } else if constexpr (ACC) {
                     lds_get4<TX>(dt + boff, dv);
                 } else {
@@ -2603,12 +2603,12 @@ int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K) {
 hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
                            const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int o0,
                            int np, void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
-                           hipStream_t s, const float* dx_step, int groups) {
+                           hipStream_t s, const int32_t* dx_scale, int groups) {
     if (B == 0) return hipSuccess;
     if (np < 1 || np > kProjTile || o0 < 0 || K % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
-    // bf16 x: one output tile, on the fixed-point stream part of the row pass
+    // bf16 x: one output tile, on the fp16 stream part of the row pass
     const int C = np > 0 ? (int)(K / (n_pre > 0 ? n_pre : 1)) : 0;
-    if (x_dtype == kBF16 && (o0 != 0 || dx_step == nullptr || groups < 1 || C % kFixedGroup != 0))
+    if (x_dtype == kBF16 && (o0 != 0 || dx_scale == nullptr || groups < 1 || C % kPartGroup != 0))
         return hipErrorInvalidValue;
     // token tile: a multiple of two 32-token stages
     int64_t tile = (B + tiles - 1) / tiles;
@@ -2618,7 +2618,7 @@ hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_s
     const dim3 grid((unsigned)((K + cb - 1) / cb), (unsigned)tiles);
 #define MHC_PROJ_BWD(TX_, ACC_, S_)                                                                              \
     MHC_LAUNCH_GGL((proj_bwd_mfma_kernel<TX_, ACC_, S_>), grid, dim3(2 * cb), 0, s, (const TX_*)x, dP, dp_stride,  \
-                       s_tok, phi_pre, phi_post, phi_res, n_pre, o0, np, (TX_*)dx, dx_step, groups, C, dphi_part, B, K, \
+                       s_tok, phi_pre, phi_post, phi_res, n_pre, o0, np, (TX_*)dx, dx_scale, groups, C, dphi_part, B, K, \
                        tile)
     // The layer backward accumulates (with the r_h term on the first output
     // tile only); the standalone operator starts from zero on its first tile.

@@ -265,7 +265,7 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
                                           const float (&xv)[N][VPT][kLayerWC],
                                           const float (&gv)[N][VPT][kLayerWC],
                                           float (&dwacc)[VPT][kLayerWC], float& sacc, TX* __restrict__ dx,
-                                          float* __restrict__ scal_out, float* __restrict__ dx_step, int C,
+                                          float* __restrict__ scal_out, int32_t* __restrict__ dx_scale, int C,
                                           float eps, float* red) {
     constexpr int WC = kLayerWC;
     constexpr int NC = coef_size<N>();
@@ -349,11 +349,11 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
 
     if constexpr (MODE == 1 && sizeof(TX) == 2) {
         // The dynamic backward's stream part with bf16 x: the projection
-        // kernel adds its terms and rounds once, so this part travels as int16
-        // fixed point (fixed_scale), one scale per half wave of this token:
-        // dx_step[b][threadIdx.x / 32].
+        // kernel adds its terms and rounds the sum once, so this part travels
+        // as fp16 against a power-of-two scale (part_pack4), one scale
+        // exponent per half wave of this token: dx_scale[b][threadIdx.x / 32].
         float a[N][VPT][WC];
-        float m = 0.f;
+        float m = 0.f;  // largest |value|: fmaxf drops NaN, keeps +Inf
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
 #pragma unroll
@@ -376,18 +376,34 @@ __device__ __forceinline__ void bwd_token(int64_t b, const float* __restrict__ c
                 }
             }
         }
-        const FixedScale fs = fixed_scale(half_wave_max_nonneg(m));
+        m = half_wave_max_nonneg(m);
+        if (__ballot(!(m < INFINITY))) {
+            // an infinite value in this wave: the scale comes from the finite
+            // values only (the whole wave takes this branch)
+            m = 0.f;
+#pragma unroll
+            for (int k = 0; k < VPT; ++k)
+#pragma unroll
+                for (int e = 0; e < WC; ++e)
+#pragma unroll
+                    for (int j = 0; j < N; ++j) {
+                        const float v = fabsf(a[j][k][e]);
+                        m = v < INFINITY ? fmaxf(m, v) : m;
+                    }
+            m = half_wave_max_nonneg(m);
+        }
+        const int ks = part_scale_exp(m);
         const buf_rsrc_t drs = make_buf_rsrc(dx + b * (int64_t)N * C, (uint32_t)((int64_t)N * C * 2));
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
             const int c0 = (k * blockDim.x + threadIdx.x) * WC;
             const uint32_t o0 = c0 < C ? (uint32_t)c0 * 2u : kBufOff;
 #pragma unroll
-            for (int j = 0; j < N; ++j) buf_st8<true>(drs, o0 + (uint32_t)(j * C * 2), 0u, fixed_pack4(a[j][k], fs.inv));
+            for (int j = 0; j < N; ++j) buf_st8<true>(drs, o0 + (uint32_t)(j * C * 2), 0u, part_pack4(a[j][k], ks));
         }
         const int ng = blockDim.x / 32;
-        const buf_rsrc_t qrs = make_buf_rsrc(dx_step + b * ng, (uint32_t)(ng * 4));
-        buf_st4(qrs, (threadIdx.x & 31) == 0 ? (uint32_t)(threadIdx.x / 32) * 4u : kBufOff, 0u, fs.step);
+        const buf_rsrc_t qrs = make_buf_rsrc(dx_scale + b * ng, (uint32_t)(ng * 4));
+        buf_st4(qrs, (threadIdx.x & 31) == 0 ? (uint32_t)(threadIdx.x / 32) * 4u : kBufOff, 0u, __int_as_float(ks));
     } else {
         const buf_rsrc_t drs = make_buf_rsrc(dx + b * (int64_t)N * C, (uint32_t)((int64_t)N * C * (int64_t)sizeof(TX)));
 #pragma unroll
@@ -434,7 +450,7 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
                                                     const float* __restrict__ w, const float* __restrict__ coef,
                                                     int64_t coef_stride, TX* __restrict__ dx,
                                                     float* __restrict__ dw_part, float* __restrict__ scal_out,
-                                                    float* __restrict__ dx_step, int64_t B, int C, float eps) {
+                                                    int32_t* __restrict__ dx_scale, int64_t B, int C, float eps) {
     constexpr int WC = kLayerWC;
     constexpr int NS = N * N + 2 * N;
     constexpr int NR = 2 + N * N + 3 * N;
@@ -466,7 +482,7 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
             load_rows_raw_rs<float, N, VPT, WC, true>(token_rows_rsrc(g, b1, B, N, C), C, gB);
             unpack_rows<TX, N, VPT, WC>(xA, C, xv);
             unpack_rows<float, N, VPT, WC>(gA, C, gv);
-            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,
+            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_scale, C, eps,
                                        red);
             if (b1 >= B) break;
             const int64_t b2 = b1 + G;
@@ -474,7 +490,7 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
             load_rows_raw_rs<float, N, VPT, WC, true>(token_rows_rsrc(g, b2, B, N, C), C, gA);
             unpack_rows<TX, N, VPT, WC>(xB, C, xv);
             unpack_rows<float, N, VPT, WC>(gB, C, gv);
-            bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,
+            bwd_token<TX, N, VPT, MODE>(b1, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_scale, C, eps,
                                        red);
             b = b2;
         }
@@ -487,7 +503,7 @@ __global__ MHC_ROW_BOUNDS(PF) void layer_bwd_kernel(const float* __restrict__ g,
             load_rows_raw<float, N, VPT, WC, true>(g + b * NCs, C, gr);
             unpack_rows<TX, N, VPT, WC>(xr, C, xv);
             unpack_rows<float, N, VPT, WC>(gr, C, gv);
-            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_step, C, eps,
+            bwd_token<TX, N, VPT, MODE>(b, coef, coef_stride, wv, xv, gv, dwacc, sacc, dx, scal_out, dx_scale, C, eps,
                                        red);
         }
     }
@@ -986,7 +1002,7 @@ static RowTiling bwd_tiling(int64_t C, int n, int x_dtype = kF32) {
 
 bool layer_bwd_is_wide(int n, int64_t C) { return bwd_tiling(C, n).vpt <= 0; }
 
-int layer_bwd_fixed_groups(int x_dtype, int n, int64_t C) {
+int layer_bwd_part_groups(int x_dtype, int n, int64_t C) {
     const RowTiling t = bwd_tiling(C, n, x_dtype);
     return t.vpt > 0 ? t.threads / 32 : 0;
 }
@@ -1004,7 +1020,7 @@ size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C) {
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s,
-                            float* dx_step) {
+                            int32_t* dx_scale) {
     const RowTiling t = bwd_tiling(C, n, x_dtype);
     if (t.vpt <= 0) {
         // the channel-loop kernels write a bf16 stream part; the dynamic
@@ -1013,12 +1029,12 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
         return launch_wide_bwd(x_dtype, n, mode, g, x, w, coef, coef_stride, dx, dw_part, scal_out, grid, B, C, eps,
                                scratch, s);
     }
-    if (mode == 1 && x_dtype == kBF16 && (dx_step == nullptr || C % kFixedGroup != 0)) return hipErrorInvalidValue;
+    if (mode == 1 && x_dtype == kBF16 && (dx_scale == nullptr || C % kPartGroup != 0)) return hipErrorInvalidValue;
     const void* fn = pick_bwd(x_dtype, n, t.vpt, mode, use_prefetch(t));
     if (!fn) return hipErrorInvalidValue;
     int Ci = (int)C;
     void* args[] = {(void*)&g, (void*)&x, (void*)&w, (void*)&coef, (void*)&coef_stride, (void*)&dx,
-                    (void*)&dw_part, (void*)&scal_out, (void*)&dx_step, (void*)&B, (void*)&Ci, (void*)&eps};
+                    (void*)&dw_part, (void*)&scal_out, (void*)&dx_scale, (void*)&B, (void*)&Ci, (void*)&eps};
     const int tok = timing_begin(mode == 0 ? "layer_bwd" : "layer_bwd_reduce", s);
     hipError_t e = mhc_launch_kernel(fn, dim3(grid), dim3(t.threads), args, 0, s);
     timing_end(tok, s);

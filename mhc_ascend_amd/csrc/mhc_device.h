@@ -370,48 +370,49 @@ __device__ __forceinline__ float half_wave_max_nonneg(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// Fixed-point transport of an fp32 row part between two kernels.
+// Half-precision transport of an fp32 row part between two kernels.
 //
 // Where a gradient is formed in two kernels (a row pass writes one part, a
 // later kernel adds the rest and rounds the sum once to bf16), the first part
-// travels through HBM in the 2 bytes per element the bf16 result occupies, as
-// int16 fractions of a per-group scale m (the group's largest |value|):
-// q = rne(32767 v / m) by v_cvt_pknorm_i16_f32 (clamped to [-1, 1], two
-// elements per instruction), v = q * (m / 32767) on the way back.  The error
-// is at most m / 65534 per element, far below the bf16 rounding of the final
-// sum (2^-8 relative), which stays the only rounding of the gradient.  A
-// group is one half wave's elements of a token row: every lane's 4-channel
-// chunks (all streams, all chunks k) of lanes 32h .. 32h + 31, whose
-// channels are the 128-channel ranges c / 128 = k * H + h (H = row-kernel
-// lanes / 32), so the row kernel finds m with one half-wave reduction and a
-// 128-column block of the row maps to one group.  A non-finite value makes
-// its group non-finite on the way back, as fp32 would.
+// travels through HBM in the 2 bytes per element the bf16 result occupies:
+// as fp16 values of v * 2^-k, with one power-of-two scale 2^k per group.  k
+// comes from the group's largest finite |value| m so that m * 2^-k lies in
+// [2^14, 2^15) (k = 0 for m = 0).  Scaling by a power of two is exact (the
+// ldexp on either side), and fp16 keeps 11 significant bits over its normal
+// range, so every element of magnitude at least 2^-28 m comes back with a
+// relative error of at most 2^-11 (one fp16 half-ulp, an eighth of the bf16
+// half-ulp of the final rounding); smaller elements come back within 2^-39 m.
+// NaN and +-Inf take no part in m and travel as fp16 NaN and +-Inf.  A group
+// is one half wave's elements of a token row: every lane's 4-channel chunks
+// (all streams, all chunks k) of lanes 32h .. 32h + 31, whose channels are
+// the 128-channel ranges c / 128 = k * H + h (H = row-kernel lanes / 32), so
+// the row kernel finds m with one half-wave reduction and a 128-column block
+// of the row maps to one group.
 // ---------------------------------------------------------------------------
-constexpr int kFixedGroup = 128;  // channels of one half wave's 4-channel chunks
+constexpr int kPartGroup = 128;  // channels of one half wave's 4-channel chunks
 
-typedef short fixed_s16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 part_h2_t __attribute__((ext_vector_type(2)));
 
-struct FixedScale {
-    float inv;   // 1 / m (0 for an all-zero group)
-    float step;  // m / 32767
-};
-
-__device__ __forceinline__ FixedScale fixed_scale(float m) {
-    return FixedScale{m > 0.f ? 1.f / m : 0.f, m * (1.f / 32767.f)};
+// Scale exponent k of a group whose largest finite |value| is m >= 0.
+__device__ __forceinline__ int part_scale_exp(float m) {
+    return m > 0.f ? __builtin_amdgcn_frexp_expf(m) - 15 : 0;
 }
 
-// Four values -> four int16 in 8 bytes (element 0 in the low half of .x).
-__device__ __forceinline__ uint2 fixed_pack4(const float (&v)[4], float inv) {
-    const fixed_s16x2_t a = __builtin_amdgcn_cvt_pknorm_i16(v[0] * inv, v[1] * inv);
-    const fixed_s16x2_t b = __builtin_amdgcn_cvt_pknorm_i16(v[2] * inv, v[3] * inv);
+// Four values -> four fp16 of v * 2^-k in 8 bytes (element 0 in the low half
+// of .x), rounded to nearest even.
+__device__ __forceinline__ uint2 part_pack4(const float (&v)[4], int k) {
+    const part_h2_t a = {(_Float16)__builtin_ldexpf(v[0], -k), (_Float16)__builtin_ldexpf(v[1], -k)};
+    const part_h2_t b = {(_Float16)__builtin_ldexpf(v[2], -k), (_Float16)__builtin_ldexpf(v[3], -k)};
     return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
 }
 
-__device__ __forceinline__ void fixed_unpack4(uint2 w, float step, float (&v)[4]) {
-    v[0] = (float)(int)(int16_t)(w.x & 0xffffu) * step;
-    v[1] = (float)((int)w.x >> 16) * step;
-    v[2] = (float)(int)(int16_t)(w.y & 0xffffu) * step;
-    v[3] = (float)((int)w.y >> 16) * step;
+__device__ __forceinline__ void part_unpack4(uint2 w, int k, float (&v)[4]) {
+    const part_h2_t a = __builtin_bit_cast(part_h2_t, w.x);
+    const part_h2_t b = __builtin_bit_cast(part_h2_t, w.y);
+    v[0] = __builtin_ldexpf((float)a[0], k);
+    v[1] = __builtin_ldexpf((float)a[1], k);
+    v[2] = __builtin_ldexpf((float)b[0], k);
+    v[3] = __builtin_ldexpf((float)b[1], k);
 }
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }

@@ -97,19 +97,20 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
 //         dh_pre_act] into scal_out[grid][n*n+2n]);
 // mode 1: dx = stream terms only, and per token scal_out[B][n*n+2n+2] =
 //         dM, dh_post_act, dh_pre_act, inv_rms, k2.  With bf16 x the stream
-//         terms are int16 fixed point (fixed_scale in mhc_device.h) with the
-//         steps dx_step[B][layer_bwd_fixed_groups] (register rows and
+//         terms are fp16 against power-of-two scales (part_pack4 in
+//         mhc_device.h) with the scale exponents
+//         dx_scale[B][layer_bwd_part_groups] (register rows and
 //         C % 128 == 0 only: other bf16 x rows are an error here).
 // scratch: layer_bwd_scratch_bytes (the channel-chunked wide backward's
 // partial row sums; 0 bytes and unused otherwise).
 hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s,
-                            float* dx_step = nullptr);
+                            int32_t* dx_scale = nullptr);
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C);
-// Fixed-point groups per token row of the mode-1 stream part (one per half
+// Scale groups per token row of the mode-1 stream part (one per half
 // wave of the register-row kernel; 0 when the channel-loop kernels run).
-int layer_bwd_fixed_groups(int x_dtype, int n, int64_t C);
+int layer_bwd_part_groups(int x_dtype, int n, int64_t C);
 size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C);
 // Whether the layer forward / backward of (n, C) runs the channel-loop
 // kernels of wide.hip rather than the register rows.
@@ -299,12 +300,12 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
                                 float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
                                 hipStream_t s);
 // With bf16 x (one output tile, accumulate) the incoming dx is the layer
-// backward's int16 fixed-point stream part with steps dx_step[B][groups]
-// (groups = layer_bwd_fixed_groups).
+// backward's fp16 stream part with scale exponents dx_scale[B][groups]
+// (groups = layer_bwd_part_groups).
 hipError_t launch_proj_bwd(int x_dtype, const void* x, const float* dP, int dp_stride, const float* s_tok,
                            const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int o0,
                            int np, void* dx, bool accumulate, float* dphi_part, int tiles, int64_t B, int64_t K,
-                           hipStream_t s, const float* dx_step = nullptr, int groups = 0);
+                           hipStream_t s, const int32_t* dx_scale = nullptr, int groups = 0);
 hipError_t launch_weight_f32(const void* w, int w_dtype, int64_t C, float* out, hipStream_t s);
 
 // ---- wrapper.hip -----------------------------------------------------------

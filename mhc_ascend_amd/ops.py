@@ -227,12 +227,11 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
     parameters of ``layer`` (an MHCLayer); returns fp32 [tokens, C]."""
     n = layer.expansion_rate
     C = residual.shape[-1]
-    # The fused wrapper kernels take n = 4 and 4-channel rows (with dynamic
-    # H 32-channel, 128-channel for bf16 storage) up to 16384 channels.  Other
+    # The fused wrapper kernels take n = 4 and 4-channel rows (32-channel
+    # with dynamic H, the projection's k step) up to 16384 channels.  Other
     # shapes build the n streams with device tensor ops, as layer.py:299-310
     # does, and run the layer on them (layer.py:313-316).
-    dyn_align = 128 if residual.dtype == torch.bfloat16 else 32
-    fused = n == 4 and C % 4 == 0 and C <= 16384 and (not layer.use_dynamic_h or C % dyn_align == 0)
+    fused = n == 4 and C % 4 == 0 and C <= 16384 and (not layer.use_dynamic_h or C % 32 == 0)
     if not fused:
         if n < 2:
             raise RuntimeError("mhc_residual_wrapper: expansion_rate must be >= 2 (stream 1 holds the branch)")

@@ -11,7 +11,7 @@ import torch
 import mhc_ascend_amd as mhc
 from mhc_ascend_amd import native
 from oracle import reference as R
-from tests.conftest import assert_close, assert_close_bf16, grad_atol
+from tests.conftest import assert_close, assert_close_bf16, assert_close_dyn_dx_bf16, grad_atol
 
 pytestmark = pytest.mark.gpu
 
@@ -75,7 +75,7 @@ def _check_dyn(got, want, x_dtype, tag):
     if gx is None:
         return
     if x_dtype == torch.bfloat16:
-        assert_close_bf16(gx, rgx, f"{tag} dx (bf16)")
+        assert_close_dyn_dx_bf16(gx, rgx, f"{tag} dx (bf16)")
     else:
         assert_close(gx, rgx, 1e-3, grad_atol(rgx, 1e-5), f"{tag} dx")
     for nm, a, e in zip(PARAMS, gp, rgp):
@@ -293,7 +293,7 @@ def test_dynamic_layer_config_c4_full_size(device):
     sub = {k: (v[idx] if k in ("x", "grad") else v) for k, v in d.items()}
     rout, rgx, _ = _oracle_dyn(sub)
     assert_close(out.cpu()[idx], rout, what="C4 out subsample", **FWD)
-    assert_close_bf16(g_full[0].cpu()[idx], rgx, "C4 dx subsample (bf16)")
+    assert_close_dyn_dx_bf16(g_full[0].cpu()[idx], rgx, "C4 dx subsample (bf16)")
     _, g1 = grads(slice(0, B // 2))
     _, g2 = grads(slice(B // 2, B))
     names = ["d_weight", "d_phi_pre", "d_phi_post", "d_phi_res", "d_alpha_pre", "d_alpha_post", "d_alpha_res",
@@ -331,7 +331,7 @@ def test_dynamic_layer_backward_many_tokens(device, B, C):
     idx = torch.arange(0, B, 3)
     sub = {k: (v[idx] if k in ("x", "grad") else v) for k, v in d.items()}
     _, rgx, _ = _oracle_dyn(sub)
-    assert_close_bf16(g_full[0].cpu()[idx], rgx, f"many tokens B={B} C={C} dx (every third token)")
+    assert_close_dyn_dx_bf16(g_full[0].cpu()[idx], rgx, f"many tokens B={B} C={C} dx (every third token)")
     h = 1200  # not a multiple of the block size
     g1, g2 = grads(slice(0, h)), grads(slice(h, B))
     for k in range(1, len(g_full)):

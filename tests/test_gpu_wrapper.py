@@ -108,7 +108,7 @@ def _check(got, want, dtype, names, tag):
 @pytest.mark.parametrize("dynamic", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
-@pytest.mark.parametrize("shape", [(3, 5, 256), (37, 1024)])
+@pytest.mark.parametrize("shape", [(3, 5, 256), (37, 1024), (19, 160), (2, 3, 224)])
 def test_wrapper_matches_oracle(device, dynamic, dtype, mode, shape):
     C = shape[-1]
     seed = len(shape) * 100 + C + (7 if dynamic else 0) + (3 if mode == "zero" else 0)
