@@ -1067,7 +1067,10 @@ int dyn_coef16_bwd_blocks(int64_t B) {
 // Workgroups stride over groups of 16 tokens; each lane sums its db / dalpha
 // terms over its tokens in order, then the block reduces them into
 // part[blk][27] = (db_pre[4], db_post[4], db_res[16], dalpha_pre, dalpha_post,
-// dalpha_res).
+// dalpha_res).  RES = false: the Sinkhorn adjoint's output is taken as zero
+// (a dM constant down each column, which the final column normalisation
+// removes), so dP_res, db_res and dalpha_res are zeros.
+template <bool RES>
 __global__ __launch_bounds__(256) void dyn_coef16_bwd_kernel(
     const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
     const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
@@ -1094,10 +1097,13 @@ __global__ __launch_bounds__(256) void dyn_coef16_bwd_kernel(
         const float* pv = p + tk * NP;
         const float inv = 1.f / rh[tk];
         const float pr = pv[2 * N + l];
-        const float e = expf(pr * ar * inv + b_res[l]);
-        float g = sc[l];  // dM element
-        sk16_backward(g, e, iters, sk_eps);
-        const float dt_res = g * e;
+        float dt_res = 0.f;
+        if constexpr (RES) {
+            const float e = expf(pr * ar * inv + b_res[l]);
+            float g = sc[l];  // dM element
+            sk16_backward(g, e, iters, sk_eps);
+            dt_res = g * e;
+        }
         const float hv = cf[l & 7];
         // dh_post_act[q] at sc[N*N + q], dh_pre_act[q] at sc[N*N + N + q]
         const float dh = (l < N) ? sc[N * N + N + (l & 3)] : sc[N * N + ((l - N) & 3)];
@@ -1872,14 +1878,20 @@ int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters) {
 hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
-                               float* hist, hipStream_t s) {
+                               float* hist, hipStream_t s, bool res_rows) {
     if (B == 0) return hipSuccess;
     const unsigned blocks = (unsigned)dyn_coef_bwd_blocks(n, B);
     if (n == 4) {
-        MHC_LAUNCH_GGL(dyn_coef16_bwd_kernel, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K, a_pre, a_post,
-                           a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        if (res_rows) {
+            MHC_LAUNCH_GGL(dyn_coef16_bwd_kernel<true>, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K, a_pre,
+                               a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        } else {
+            MHC_LAUNCH_GGL(dyn_coef16_bwd_kernel<false>, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        }
         return hipGetLastError();
     }
+    if (!res_rows) return hipErrorInvalidValue;
     if (n == skb::kN && iters <= skb::kTMax) {
         MHC_LAUNCH_GGL(dyn_coef32_bwd_kernel, dim3((unsigned)B), dim3(skb::kThreads), 0, s, scal, coef, p, rh, B, K,
                            a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);

@@ -254,10 +254,13 @@ int dyn_coef_bwd_blocks(int n, int64_t B);
 // iters * (n + 1) * n floats; 0 slots = iters too large for the region.
 constexpr size_t kSkHistBytes = size_t(64) << 20;
 int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters);
+// res_rows = false (n = 4 only): dM is taken as zero after the Sinkhorn
+// adjoint (the wrapper's column-constant dM, wrap_res_grad_vanishes): dP,
+// db and dalpha of the H_res rows are written as zeros and no adjoint runs.
 hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
-                               float* hist, hipStream_t s);
+                               float* hist, hipStream_t s, bool res_rows = true);
 // Deterministic column sums of several partial matrices in one launch:
 // out[c] = sum_r part[r][c] over `rows` <= 512 rows (column_sums_direct),
 // columns c < split to `out` (bf16 when out_bf16, else fp32) and the rest to
@@ -335,12 +338,13 @@ hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const vo
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C);
 // Dynamic-H backward, pass 2: d r / d b (written, rounded once), dw_part
 // [tiles][C] and dphi_part [tiles][np][n*C] from G, r, b, the factors of
-// launch_wrap_bwd_red, dP and s.
+// launch_wrap_bwd_red, dP and s.  res_rows = false: the H_res rows of dP are
+// zero and dphi_part holds only the 2n pre / post rows per tile.
 hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const void* res, const void* br,
                                 const float* w, const float* ep, const float* dP, const float* s_tok,
                                 const float* phi_pre, const float* phi_post, const float* phi_res, void* dres,
                                 void* dbr, float* dw_part, float* dphi_part, int tiles, int64_t B, int64_t C,
-                                hipStream_t s);
+                                bool res_rows, hipStream_t s);
 
 // ---- compat.hip ------------------------------------------------------------
 // The reference-shaped dynamic-H entries (mhc_layer_fwd_dynamic /

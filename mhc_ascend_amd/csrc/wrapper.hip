@@ -986,6 +986,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
 // dtype.  Workgroup = 8 waves x 16 columns; stages of 32 tokens with r, b
 // and G staged in LDS (three stages in flight in registers); results go
 // through one LDS tile per output and leave with coalesced 16-byte stores.
+//
+// RES = false: the H_res rows of dP are zero (every stream receives G / n
+// through the stream mean, so dM is constant down each column, and the
+// Sinkhorn pass, which ends with a column normalisation, maps it to zero:
+// wrap_res_grad_vanishes in abi.hip).  Only the 2N pre / post rows are
+// carried, and their hi / lo halves share one MFMA:
+//   dPhi: A rows 0..7 = dP_hi^T, rows 8..15 = dP_lo^T over the stage's
+//         tokens; dPhi[o] = D[o] + D[o + 8] (one 16x16x32 MFMA per stream
+//         instead of four);
+//   dx:   k = 0..7 Phi_hi x dP_hi, 8..15 Phi_lo x dP_hi, 16..23 Phi_hi x
+//         dP_lo, 24..31 zero (one MFMA per output and token half instead of
+//         three).
+// dphi_part then holds 2N rows per tile.
 // ---------------------------------------------------------------------------
 typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
 
@@ -1037,7 +1050,7 @@ __device__ __forceinline__ void wlds_put4(char* p, const float (&v)[4]) {
     }
 }
 
-template <typename TX, int N, bool DECAY>
+template <typename TX, int N, bool DECAY, bool RES>
 __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWpbWaves<TX>()))) void wrap_proj_bwd_kernel(
     const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
     const float* __restrict__ ep, const float* __restrict__ dP, const float* __restrict__ s_tok,
@@ -1045,7 +1058,9 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
     TX* __restrict__ dres, TX* __restrict__ dbr, float* __restrict__ dw_part, float* __restrict__ dphi_part,
     int64_t B, int C, int64_t tile) {
     constexpr int NP = 2 * N + N * N;
+    constexpr int NPO = RES ? NP : 2 * N;  // rows of dphi_part
     static_assert(NP <= 32, "projection rows must fit one 32-row tile");
+    static_assert(RES || 2 * N <= 8, "packed pre / post rows: at most 8");
     static_assert(N <= 4 && kWrapEp == 12, "factor record: 4 + 4 h_pre + hs/r, 2 xa factors, s");
     constexpr int NSTR = DECAY ? N : (N < 2 ? N : 2);  // streams with nonzero values
     constexpr int TB = 32;
@@ -1098,6 +1113,7 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
     const int epc = tid % 3;
 
     // dx_proj A operands: Phi_r^T and Phi_1^T at column wc0 + lr, o = 8 lg + e
+    // (RES = false: o = e, the hi, lo, hi and zero k-blocks by lg)
     wu32x4_t prh, prl, pbh, pbl;
     float wv[4];
     {
@@ -1105,7 +1121,7 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         float vr[8], vb[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int o = 8 * lg + e;
+            const int o = RES ? 8 * lg + e : e;
             float r = 0.f, b = 0.f;
             if (wave_on && o < NP) {
                 const float* rowp = phi_row(phi_pre, phi_post, phi_res, N, o, K);
@@ -1119,6 +1135,11 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         }
         wsplit_pack8(vr, prh, prl);
         wsplit_pack8(vb, pbh, pbl);
+        if constexpr (!RES) {
+            const wu32x4_t z = wu32x4_t{0u, 0u, 0u, 0u};
+            prh = lg == 1 ? prl : (lg == 3 ? z : prh);
+            pbh = lg == 1 ? pbl : (lg == 3 ? z : pbh);
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) wv[i] = wave_on ? w[cb0 + wc0 + 4 * lg + i] : 0.f;
     }
@@ -1204,7 +1225,30 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
 #pragma unroll
         for (int p = 0; p < GPASSES; ++p)
             *reinterpret_cast<uint4*>(&g_lds[(grow + p * GRPP) * GPITCH + gvec * 16]) = f.gq[p];
-        if (dp_loader) {
+        if constexpr (!RES) {
+            // token-major B rows [hi 0..7 | hi 0..7 | lo 0..7 | 0] in
+            // dps_lds[0], o-major A rows [hi 0..7 ; lo 0..7] in dps_lds[2]
+            if (dp_loader && dpo < 2 * N) {
+                const uint32_t dw4[4] = {sm.dp.x, sm.dp.y, sm.dp.z, sm.dp.w};
+                float hi[4], lo[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float v = __uint_as_float(dw4[q]);
+                    hi[q] = bf16_to_f32(f32_to_bf16(v));
+                    lo[q] = v - hi[q];
+                }
+                const uint2 h2 = make_uint2(wpack(hi[0], hi[1]), wpack(hi[2], hi[3]));
+                *reinterpret_cast<uint2*>(&dps_lds[0][dtk * kWDpPitch + dpo]) = h2;
+                *reinterpret_cast<uint2*>(&dps_lds[0][dtk * kWDpPitch + 8 + dpo]) = h2;
+                *reinterpret_cast<uint2*>(&dps_lds[0][dtk * kWDpPitch + 16 + dpo]) =
+                    make_uint2(wpack(lo[0], lo[1]), wpack(lo[2], lo[3]));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    dps_lds[2][(dpo + q) * kWDpPitch + dtk] = f32_to_bf16(hi[q]);
+                    dps_lds[2][(8 + dpo + q) * kWDpPitch + dtk] = f32_to_bf16(lo[q]);
+                }
+            }
+        } else if (dp_loader) {
             const uint32_t dw4[4] = {sm.dp.x, sm.dp.y, sm.dp.z, sm.dp.w};
             float hi[4], lo[4];
 #pragma unroll
@@ -1279,15 +1323,28 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
 #pragma unroll
             for (int j = 0; j < NSTR; ++j) wsplit_pack8(xs[j], xh[j], xl[j]);
         }
-#pragma unroll
-        for (int ot = 0; ot < 2; ++ot) {
-            const wu32x4_t ah = read16(&dps_lds[2][(16 * ot + lr) * kWDpPitch + 8 * lg]);
-            const wu32x4_t al = read16(&dps_lds[3][(16 * ot + lr) * kWDpPitch + 8 * lg]);
+        if constexpr (!RES) {
+            // rows lr < 8: dP_hi, else dP_lo (fp32 x: dP_hi x_lo into the hi rows)
+            const wu32x4_t a = read16(&dps_lds[2][lr * kWDpPitch + 8 * lg]);
 #pragma unroll
             for (int j = 0; j < NSTR; ++j) {
-                accP[j][ot] = wmfma16x16x32(ah, xh[j], accP[j][ot]);
-                accP[j][ot] = wmfma16x16x32(al, xh[j], accP[j][ot]);
-                if constexpr (sizeof(TX) == 4) accP[j][ot] = wmfma16x16x32(ah, xl[j], accP[j][ot]);
+                accP[j][0] = wmfma16x16x32(a, xh[j], accP[j][0]);
+                if constexpr (sizeof(TX) == 4) {
+                    const wu32x4_t z = wu32x4_t{0u, 0u, 0u, 0u};
+                    accP[j][0] = wmfma16x16x32(lr < 8 ? a : z, xl[j], accP[j][0]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int ot = 0; ot < 2; ++ot) {
+                const wu32x4_t ah = read16(&dps_lds[2][(16 * ot + lr) * kWDpPitch + 8 * lg]);
+                const wu32x4_t al = read16(&dps_lds[3][(16 * ot + lr) * kWDpPitch + 8 * lg]);
+#pragma unroll
+                for (int j = 0; j < NSTR; ++j) {
+                    accP[j][ot] = wmfma16x16x32(ah, xh[j], accP[j][ot]);
+                    accP[j][ot] = wmfma16x16x32(al, xh[j], accP[j][ot]);
+                    if constexpr (sizeof(TX) == 4) accP[j][ot] = wmfma16x16x32(ah, xl[j], accP[j][ot]);
+                }
             }
         }
         // dx_proj^T for d r and d b: D[column wc0 + 4 lg + i][token 16 tt + lr],
@@ -1296,14 +1353,16 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 16 * tt + lr;
             const wu32x4_t bh = read16(&dps_lds[0][t * kWDpPitch + 8 * lg]);
-            const wu32x4_t bl = read16(&dps_lds[1][t * kWDpPitch + 8 * lg]);
             wf32x4_t pr = wf32x4_t{0.f, 0.f, 0.f, 0.f}, pb = pr;
             pr = wmfma16x16x32(prh, bh, pr);
-            pr = wmfma16x16x32(prl, bh, pr);
-            pr = wmfma16x16x32(prh, bl, pr);
             pb = wmfma16x16x32(pbh, bh, pb);
-            pb = wmfma16x16x32(pbl, bh, pb);
-            pb = wmfma16x16x32(pbh, bl, pb);
+            if constexpr (RES) {
+                const wu32x4_t bl = read16(&dps_lds[1][t * kWDpPitch + 8 * lg]);
+                pr = wmfma16x16x32(prl, bh, pr);
+                pr = wmfma16x16x32(prh, bl, pr);
+                pb = wmfma16x16x32(pbl, bh, pb);
+                pb = wmfma16x16x32(pbh, bl, pb);
+            }
             const float4 e0 = *reinterpret_cast<const float4*>(&ep_lds[t][0]);
             const float4 e1 = *reinterpret_cast<const float4*>(&ep_lds[t][4]);
             const float4 e2 = *reinterpret_cast<const float4*>(&ep_lds[t][8]);
@@ -1364,6 +1423,10 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         __syncthreads();
     };
     const uint32_t nr = (uint32_t)nrows;
+    if constexpr (!RES) {
+        // k = 24..31 of the token-major dP rows stay zero
+        if (tid < TB * 8) dps_lds[0][(tid >> 3) * kWDpPitch + 24 + (tid & 7)] = 0;
+    }
     fetch_small(f0, 0u);
     fetch(f0, 0u);
     commit(f0);
@@ -1392,7 +1455,21 @@ __global__ __launch_bounds__(kWpbThreads) __attribute__((amdgpu_waves_per_eu(kWp
         for (int i = 0; i < 4; ++i) dw_part[(int64_t)blockIdx.y * C + cb0 + wc0 + 4 * lg + i] = dwacc[i];
     }
     // dPhi partial: accP[j][ot] register i holds o = 16 ot + 4 lg + i at channel wc0 + lr of stream j
-    float* out = dphi_part + (int64_t)blockIdx.y * NP * K;
+    // (RES = false: row 4 lg + i of the packed tile, o = 4 lg + i for lg < 2
+    // plus its lo half in lane + 32)
+    float* out = dphi_part + (int64_t)blockIdx.y * NPO * K;
+    if constexpr (!RES) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = (j < NSTR) ? xor32_add(accP[j < NSTR ? j : 0][0][i]) : 0.f;
+                const int o = 4 * lg + i;
+                if (lg < 2 && o < NPO) out[(int64_t)o * K + (int64_t)j * C + cb0 + wc0 + lr] = v;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < N; ++j) {
 #pragma unroll
@@ -1601,8 +1678,8 @@ static int64_t wrap_proj_bwd_max_tile(int64_t C) { return ((int64_t(1) << 31) - 
 
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C) {
     const int64_t gx = (C + kWpbCols - 1) / kWpbCols;
-    const void* fn = dt == kBF16 ? reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<bf16_t, 4, true>)
-                                 : reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<float, 4, true>);
+    const void* fn = dt == kBF16 ? reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<bf16_t, 4, true, true>)
+                                 : reinterpret_cast<const void*>(&wrap_proj_bwd_kernel<float, 4, true, true>);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kWpbThreads, 0) != hipSuccess || per_cu < 1) {
         (void)hipGetLastError();
@@ -1621,7 +1698,7 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
                                 const float* w, const float* ep, const float* dP, const float* s_tok,
                                 const float* phi_pre, const float* phi_post, const float* phi_res, void* dres,
                                 void* dbr, float* dw_part, float* dphi_part, int tiles, int64_t B, int64_t C,
-                                hipStream_t s) {
+                                bool res_rows, hipStream_t s) {
     if (B == 0) return hipSuccess;
     if (n != 4 || C % 32 != 0 || tiles < 1) return hipErrorInvalidValue;
     int64_t tile = (B + tiles - 1) / tiles;
@@ -1629,16 +1706,19 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
     if (tile > wrap_proj_bwd_max_tile(C)) return hipErrorInvalidValue;  // offsets past 2 GiB
     const dim3 grid((unsigned)((C + kWpbCols - 1) / kWpbCols), (unsigned)tiles);
     const int tok = timing_begin("wrap_proj_bwd", s);
-#define MHC_WPB(TX_, D_)                                                                                          \
-    MHC_LAUNCH_GGL((wrap_proj_bwd_kernel<TX_, 4, D_>), grid, dim3(kWpbThreads), 0, s, g, (const TX_*)res,        \
+#define MHC_WPB1(TX_, D_, R_)                                                                                     \
+    MHC_LAUNCH_GGL((wrap_proj_bwd_kernel<TX_, 4, D_, R_>), grid, dim3(kWpbThreads), 0, s, g, (const TX_*)res,    \
                        (const TX_*)br, w, ep, dP, s_tok, phi_pre, phi_post, phi_res, (TX_*)dres, (TX_*)dbr, dw_part, \
                        dphi_part, B, (int)C, tile)
+#define MHC_WPB(TX_, D_)                                   \
+    if (res_rows) { MHC_WPB1(TX_, D_, true); } else { MHC_WPB1(TX_, D_, false); }
     if (dt == kBF16) {
         if (decay) { MHC_WPB(bf16_t, true); } else { MHC_WPB(bf16_t, false); }
     } else {
         if (decay) { MHC_WPB(float, true); } else { MHC_WPB(float, false); }
     }
 #undef MHC_WPB
+#undef MHC_WPB1
     timing_end(tok, s);
     return hipGetLastError();
 }
