@@ -36,7 +36,7 @@ extern "C" {
 
 #define MHC_SUCCESS 0
 #define MHC_ERR_INVALID (-1)     /* bad pointer, shape or dtype (TORCH_CHECK in the reference) */
-#define MHC_ERR_UNSUPPORTED (-2) /* valid request this build has no kernel for (e.g. n not compiled) */
+#define MHC_ERR_UNSUPPORTED (-2) /* valid request this build has no kernel for (e.g. n > 64) */
 #define MHC_ERR_WORKSPACE (-3)   /* workspace smaller than the *_workspace_size query */
 
 /* ABI version: major * 10000 + minor * 100 + patch. */

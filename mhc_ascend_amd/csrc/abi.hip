@@ -40,12 +40,18 @@ static int hip_status(hipError_t e) {
 
 static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
 
-// The fused layer kernels are compiled for n in {2, 4, 8}; dynamic H needs
-// 2n + n^2 <= 32 projection outputs (n <= 4); the fused wrapper is n = 4.
-static bool supported_layer_n(int n) { return n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
-static bool supported_dynamic_n(int n) { return n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
+// The layer runs its fixed-n kernels for n in {2, 4, 8, 16, 32} and the
+// generic kernels (generic.hip) for every other n up to kGenMaxN, as the
+// reference takes any n up to MAX_EXPANSION_RATE = 64 (mhc_types.h:68); the
+// fused wrapper is n = 4.
+static bool supported_layer_n(int n) {
+    return n == 2 || n == 4 || n == 8 || n == 16 || n == 32 || generic_layer_n(n);
+}
+static bool supported_dynamic_n(int n) { return supported_layer_n(n); }
 // the standalone aggregate / distribute operators
-static bool supported_ops_n(int n) { return n == 1 || n == 2 || n == 4 || n == 8 || n == 16 || n == 32; }
+static bool supported_ops_n(int n) {
+    return n == 1 || n == 2 || n == 4 || n == 8 || n == 16 || n == 32 || generic_ops_n(n);
+}
 
 // ---------------------------------------------------------------------------
 // Device properties
@@ -249,9 +255,12 @@ static int check_layer_shape(const char* fn, int64_t batch, int32_t n, int32_t h
     if (num_iters < 0) return fail(MHC_ERR_INVALID, std::string(fn) + ": num_iters must be >= 0");
     if (!valid_dtype(x_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": x_dtype must be F32 or BF16");
     if (!supported_layer_n(n))
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) + " is not compiled in this build");
-    // register rows (n <= 8, 4-channel chunks that fit) or the channel-loop kernels
-    if ((layer_fwd_is_wide(n, hidden) || layer_bwd_is_wide(n, hidden)) && !wide_supported(n, hidden))
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) +
+                                             " is not supported (1 <= n <= " + std::to_string(kGenMaxN) + ")");
+    // register rows (n <= 8, 4-channel chunks that fit) or the channel-loop
+    // kernels; the generic-n kernels take any hidden size
+    if (!generic_layer_n(n) && (layer_fwd_is_wide(n, hidden) || layer_bwd_is_wide(n, hidden)) &&
+        !wide_supported(n, hidden))
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden=" + std::to_string(hidden) +
                                              " is too large for the row kernels at n=" + std::to_string(n));
     return MHC_SUCCESS;
@@ -297,7 +306,8 @@ static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32
     w.scal_off = align256((size_t)w.grid * hidden * sizeof(float));
     w.stage_off = w.scal_off + align256((size_t)w.grid * (n * n + 2 * n) * sizeof(float));
     w.hist_off = w.stage_off + align256(column_sums_stage_floats(hidden) * sizeof(float));
-    w.rows_off = w.hist_off + (n >= 16 ? kStaticSkHistBytes : 0);  // Sinkhorn adjoint history (wide n)
+    // Sinkhorn adjoint history (fixed n >= 16)
+    w.rows_off = w.hist_off + (n >= 16 && !generic_layer_n(n) ? kStaticSkHistBytes : 0);
     w.total = w.rows_off + align256(batch > 0 ? layer_bwd_scratch_bytes(x_dtype, n, batch, hidden) : 0);
     return w;
 }
@@ -341,7 +351,7 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
     if (e == hipSuccess)
         e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stage, grad_weight, scal_part, rows, h_pre,
                                   h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s,
-                                  n >= 16 ? (float*)((char*)workspace + w.hist_off) : nullptr);
+                                  n >= 16 && !generic_layer_n(n) ? (float*)((char*)workspace + w.hist_off) : nullptr);
     return hip_status(e);
 }
 
@@ -754,8 +764,8 @@ static int check_dyn(const char* fn, int64_t batch, int32_t n, int32_t hidden, i
     if (st) return st;
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (!supported_dynamic_n(n))
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": dynamic H is compiled for n in {2, 4, 8, 16, 32}, not n=" +
-                                             std::to_string(n));
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n=" + std::to_string(n) +
+                                             " is not supported (1 <= n <= " + std::to_string(kGenMaxN) + ")");
     if (((int64_t)n * hidden) % 32 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
     return MHC_SUCCESS;
@@ -938,7 +948,8 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     const size_t acc = w.wdt != x_dtype ? (size_t)batch * K * 4 : 0;
     w.xw_off = o; o += align256(acc);
     w.dxw_off = o; o += align256(acc);
-    w.hist_off = o; o += n >= 16 && batch > 0 ? kSkHistBytes : 0;  // Sinkhorn adjoint history
+    // Sinkhorn adjoint history (fixed n >= 16)
+    w.hist_off = o; o += n >= 16 && !generic_layer_n(n) && batch > 0 ? kSkHistBytes : 0;
     w.rows_off = o; o += align256(batch > 0 ? layer_bwd_scratch_bytes(w.wdt, n, batch, hidden) : 0);
     w.total = o;
     return w;
@@ -967,7 +978,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
     const DynBwdWs w = dyn_bwd_ws(batch, n, hidden, x_dtype);
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "layer_dynamic_bwd: workspace smaller than mhc_layer_dynamic_bwd_workspace_size()");
-    if (n >= 16 && batch > 0 && dyn_coef_bwd_hist_slots(n, batch, num_iters) < 1)
+    if (n >= 16 && !generic_layer_n(n) && batch > 0 && dyn_coef_bwd_hist_slots(n, batch, num_iters) < 1)
         return fail(MHC_ERR_UNSUPPORTED, "layer_dynamic_bwd: num_iters too large for the Sinkhorn history at n=" +
                                              std::to_string(n));
     hipStream_t s = (hipStream_t)stream;
@@ -1004,7 +1015,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
-                                    n >= 16 ? (float*)(ws + w.hist_off) : nullptr, s);
+                                    n >= 16 && !generic_layer_n(n) ? (float*)(ws + w.hist_off) : nullptr, s);
     }
     // One projection tile (n <= 4) and few partial rows: the column sums of
     // dPhi, dw and the db / dalpha partials in one launch after the

@@ -32,7 +32,8 @@ TIMED_LIB_PATH = os.path.join(PKG, "libmhc_hip_timed.so")
 AUTOGRAD_NAME = "_mhc_autograd"
 AUTOGRAD_PATH = os.path.join(PKG, AUTOGRAD_NAME + ".so")
 
-SOURCES = ["abi.hip", "compat.hip", "dynamic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wide.hip", "wrapper.hip"]
+SOURCES = ["abi.hip", "compat.hip", "dynamic.hip", "generic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wide.hip",
+           "wrapper.hip"]
 
 ARCH = os.environ.get("MHC_OFFLOAD_ARCH", "gfx950")
 

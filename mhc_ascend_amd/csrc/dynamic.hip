@@ -871,6 +871,141 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_wide_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Generic n (no compiled instantiation, n <= 64): the formulas of
+// dyn_coef_fwd_kernel / dyn_coef_bwd_wide_kernel with n taken at run time,
+// one token per group of NM = 16, 32 or 64 lanes (row r of t_res on lane r,
+// NM-float rows with the columns c >= n padding, skw_* Sinkhorn).  The
+// backward recomputes the Sinkhorn state per iteration (no history) and
+// writes its db / dalpha terms per token to part[b][np + 3].
+// ---------------------------------------------------------------------------
+template <int NM>
+__global__ __launch_bounds__(256) void dyn_coef_gen_fwd_kernel(
+    const float* __restrict__ p_part, const float* __restrict__ ss_part, int ks, int64_t B, int64_t K,
+    const float* __restrict__ a_pre, const float* __restrict__ a_post, const float* __restrict__ a_res,
+    const float* __restrict__ b_pre, const float* __restrict__ b_post, const float* __restrict__ b_res,
+    float* __restrict__ coef, float* __restrict__ p_out, float* __restrict__ rh, int n, int iters, float sk_eps,
+    float rms_eps) {
+    const int np = 2 * n + n * n;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t tok = gid / NM;
+    const int r = (int)(gid % NM);
+    const bool tv = tok < B;
+    const bool active = tv && r < n;
+    const int rr = r < n ? r : 0;
+    float pp = 0.f, pq = 0.f, pr[NM], ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NM; ++c) pr[c] = 0.f;
+    if (tv) {
+        for (int q = 0; q < ks; ++q) {
+            ss += ss_part[(int64_t)q * B + tok];
+            if (active) {
+                pp += p_part_at(p_part, ks, B, q, tok, rr);
+                pq += p_part_at(p_part, ks, B, q, tok, n + rr);
+#pragma unroll
+                for (int c = 0; c < NM; ++c) {
+                    if (c < n) pr[c] += p_part_at(p_part, ks, B, q, tok, 2 * n + rr * n + c);
+                }
+            }
+        }
+    }
+    const float r_h = sqrtf(ss / (float)K + rms_eps);
+    const float inv = 1.f / r_h;
+    const float hp = sigmoidf(pp * a_pre[0] * inv + b_pre[rr]);
+    const float hq = 2.f * sigmoidf(pq * a_post[0] * inv + b_post[rr]);
+    float e[NM];
+#pragma unroll
+    for (int c = 0; c < NM; ++c) e[c] = (active && c < n) ? expf(pr[c] * a_res[0] * inv + b_res[rr * n + c]) : 0.f;
+    skw_forward<NM>(e, n, iters, sk_eps, active);
+    if (active) {
+        float* cf = coef + tok * np;
+        cf[r] = hp;
+        cf[n + r] = hq;
+#pragma unroll
+        for (int c = 0; c < NM; ++c) {
+            if (c < n) cf[2 * n + r * n + c] = e[c];
+        }
+        if (p_out) {
+            float* po = p_out + tok * np;
+            po[r] = pp;
+            po[n + r] = pq;
+#pragma unroll
+            for (int c = 0; c < NM; ++c) {
+                if (c < n) po[2 * n + r * n + c] = pr[c];
+            }
+        }
+    }
+    if (tv && r == 0 && rh) rh[tok] = r_h;
+}
+
+template <int NM>
+__global__ __launch_bounds__(256) void dyn_coef_gen_bwd_kernel(
+    const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
+    const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
+    const float* __restrict__ a_post, const float* __restrict__ a_res, const float* __restrict__ b_res,
+    float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int n, int iters,
+    float sk_eps) {
+    const int np = 2 * n + n * n;
+    const int ns = n * n + 2 * n;
+    const int nv = np + 3;
+    const int npt = dp_stride(np);
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t tok = gid / NM;
+    const int r = (int)(gid % NM);
+    const bool tv = tok < B;
+    const bool active = tv && r < n;
+    const int rr = r < n ? r : 0;
+    const int64_t tk = tv ? tok : 0;
+    const float* sc = scal + tk * (ns + 2);
+    const float* cf = coef + tk * np;
+    const float* pv = p + tk * np;
+    const float ap = a_pre[0], aq = a_post[0], ar = a_res[0];
+    const float inv = 1.f / rh[tk];
+    float gm[NM], e[NM], pr[NM];
+#pragma unroll
+    for (int c = 0; c < NM; ++c) {
+        const bool on = active && c < n;
+        gm[c] = on ? sc[rr * n + c] : 0.f;
+        pr[c] = on ? pv[2 * n + rr * n + c] : 0.f;
+        e[c] = on ? expf(pr[c] * ar * inv + b_res[rr * n + c]) : 0.f;
+    }
+    skw_backward<NM>(gm, e, n, iters, sk_eps, active);
+    const float hp = cf[rr], hq = cf[n + rr];
+    const float dt_pre = active ? sc[n * n + n + rr] * hp * (1.f - hp) : 0.f;
+    const float dt_post = active ? sc[n * n + rr] * hq * (1.f - 0.5f * hq) : 0.f;
+    float lp = 0.f;
+#pragma unroll
+    for (int c = 0; c < NM; ++c) {
+        gm[c] = (active && c < n) ? gm[c] * e[c] : 0.f;  // dt_res row r
+        lp += gm[c] * pr[c];
+    }
+    const float l_pre = active ? dt_pre * pv[rr] : 0.f, l_post = active ? dt_post * pv[n + rr] : 0.f;
+    const float tot = group_sum<NM>(ap * l_pre + aq * l_post + ar * lp);
+    const float s_pre = group_sum<NM>(l_pre), s_post = group_sum<NM>(l_post), s_res = group_sum<NM>(lp);
+    if (active) {
+        float* dp = dp_out + tok * npt;
+        dp[r] = ap * dt_pre * inv;
+        dp[n + r] = aq * dt_post * inv;
+        float* pt = part + tok * nv;
+        pt[r] = dt_pre;
+        pt[n + r] = dt_post;
+#pragma unroll
+        for (int c = 0; c < NM; ++c) {
+            if (c < n) {
+                dp[2 * n + r * n + c] = ar * gm[c] * inv;
+                pt[2 * n + r * n + c] = gm[c];
+            }
+        }
+        if (r == 0) {
+            for (int o = np; o < npt; ++o) dp[o] = 0.f;
+            s_out[tok] = -tot * inv * inv * inv / (float)K;
+            pt[np] = s_pre * inv;
+            pt[np + 1] = s_post * inv;
+            pt[np + 2] = s_res * inv;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // n = 32: one token per 256-lane workgroup, the token's 32 x 32 matrix spread
 // over the workgroup (skb: lane t holds row i = t / 8, columns c0 .. c0 + 3
 // with c0 = 4 (t % 8)), so its Sinkhorn chain takes a barrier and a few
@@ -1834,6 +1969,15 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
                                const float* b_post, const float* b_res, float* coef, float* p_out, float* rh,
                                int iters, float sk_eps, float rms_eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
+    if (generic_layer_n(n)) {
+#define MHC_DCG_FWD(NM_)                                                                                          \
+    MHC_LAUNCH_GGL((dyn_coef_gen_fwd_kernel<NM_>), dim3((unsigned)((B * NM_ + 255) / 256)), dim3(256), 0, s,     \
+                       p_part, ss_part, ks, B, K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, n,   \
+                       iters, sk_eps, rms_eps)
+        if (n <= 16) { MHC_DCG_FWD(16); } else if (n <= 32) { MHC_DCG_FWD(32); } else { MHC_DCG_FWD(64); }
+#undef MHC_DCG_FWD
+        return hipGetLastError();
+    }
     if (n == 4) {
         MHC_LAUNCH_GGL(dyn_coef16_fwd_kernel, dim3((unsigned)((B * 16 + 255) / 256)), dim3(256), 0, s, p_part,
                            ss_part, ks, B, K, a_pre, a_post, a_res, b_pre, b_post, b_res, coef, p_out, rh, iters,
@@ -1854,10 +1998,10 @@ hipError_t launch_dyn_coef_fwd(int n, const float* p_part, const float* ss_part,
 }
 
 // Rows of the db / dalpha partials: one per workgroup, or one per token for
-// n >= 16.
+// n >= 16 and for the generic-n kernel.
 int dyn_coef_bwd_blocks(int n, int64_t B) {
     if (n == 4) return dyn_coef16_bwd_blocks(B);
-    if (n >= 16) return (int)(B < 1 ? 1 : B);
+    if (n >= 16 || generic_layer_n(n)) return (int)(B < 1 ? 1 : B);
     return (int)((B * pow2ceil(n) + 255) / 256);
 }
 
@@ -1865,7 +2009,7 @@ int dyn_coef_bwd_blocks(int n, int64_t B) {
 // number of 256-lane workgroups, at most one slot per token, as many as fit
 // kSkHistBytes of history; 0 if not even one workgroup's slots fit.
 int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters) {
-    if (n < 16) return 0;
+    if (n < 16 || generic_layer_n(n)) return 0;
     const int per_wg = 256 / n;
     const int64_t slot_bytes = (int64_t)(iters > 0 ? iters : 1) * (n + 1) * n * (int64_t)sizeof(float);
     const int64_t fit_wgs = (int64_t)kSkHistBytes / slot_bytes / per_wg;
@@ -1880,6 +2024,15 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
                                float* hist, hipStream_t s, bool res_rows) {
     if (B == 0) return hipSuccess;
+    if (generic_layer_n(n)) {
+        if (!res_rows) return hipErrorInvalidValue;
+#define MHC_DCG_BWD(NM_)                                                                                          \
+    MHC_LAUNCH_GGL((dyn_coef_gen_bwd_kernel<NM_>), dim3((unsigned)((B * NM_ + 255) / 256)), dim3(256), 0, s,     \
+                       scal, coef, p, rh, B, K, a_pre, a_post, a_res, b_res, dp_out, s_out, part, n, iters, sk_eps)
+        if (n <= 16) { MHC_DCG_BWD(16); } else if (n <= 32) { MHC_DCG_BWD(32); } else { MHC_DCG_BWD(64); }
+#undef MHC_DCG_BWD
+        return hipGetLastError();
+    }
     const unsigned blocks = (unsigned)dyn_coef_bwd_blocks(n, B);
     if (n == 4) {
         if (res_rows) {

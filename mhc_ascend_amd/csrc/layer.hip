@@ -809,6 +809,8 @@ int saved_w_offset(int n) { return ((2 * n + n * n + 63) / 64) * 64; }
 hipError_t launch_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res,
                               const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
                               hipStream_t s) {
+    if (generic_layer_n(n))
+        return launch_gen_static_coef(n, h_pre, h_post, h_res, weight, w_dtype, C, saved, iters, sk_eps, s);
     const int off = saved_w_offset(n);
     const unsigned blocks = 1 + (unsigned)((C + 2047) / 2048);
     if (w_dtype == kBF16) {
@@ -910,7 +912,7 @@ static bool use_prefetch(const RowTiling& t) { return t.threads <= 256; }
 // chunk that fits their row state; everything else runs the channel-loop
 // kernels of wide.hip.
 static RowTiling fwd_tiling(int64_t C, int n) {
-    if (n > 8) return RowTiling{0, 0};
+    if (n > 8 || generic_layer_n(n)) return RowTiling{0, 0};
     return choose_row_tiling(C, kLayerWC, n, 512);
 }
 
@@ -920,6 +922,8 @@ hipError_t launch_layer_fwd(int x_dtype, int n, const void* x, const float* w, c
                             int64_t coef_stride, void* out, int out_dtype, float* rms_out, int64_t B, int64_t C,
                             float eps, hipStream_t s, int64_t rms_scratch) {
     if (B == 0) return hipSuccess;
+    if (generic_layer_n(n))
+        return launch_gen_layer_fwd(x_dtype, out_dtype, n, x, w, coef, coef_stride, out, rms_out, B, C, eps, s);
     const RowTiling t = fwd_tiling(C, n);
     if (t.vpt <= 0)
         return launch_wide_fwd(x_dtype, out_dtype, n, x, w, coef, coef_stride, out, rms_out, B, C, eps, s, rms_scratch);
@@ -996,7 +1000,7 @@ hipError_t launch_layer_static_fwd(int x_dtype, int n, const void* x, const void
 // 512-lane form had been the faster one).
 static RowTiling bwd_tiling(int64_t C, int n, int x_dtype = kF32) {
     (void)x_dtype;
-    if (n > 8) return RowTiling{0, 0};
+    if (n > 8 || generic_layer_n(n)) return RowTiling{0, 0};
     return with_min_threads(choose_row_tiling(C, kLayerWC, 2 * n, 256), 2 + n * n + 3 * n);
 }
 
@@ -1008,12 +1012,14 @@ int layer_bwd_part_groups(int x_dtype, int n, int64_t C) {
 }
 
 int layer_bwd_grid(int x_dtype, int n, int64_t B, int64_t C) {
+    if (generic_layer_n(n)) return gen_layer_bwd_grid(B);
     const RowTiling t = bwd_tiling(C, n, x_dtype);
     if (t.vpt <= 0) return wide_bwd_grid(x_dtype, n, B, C);
     return persistent_grid(pick_bwd(x_dtype, n, t.vpt, 0, use_prefetch(t)), t.threads, B);
 }
 
 size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C) {
+    if (generic_layer_n(n)) return gen_layer_bwd_scratch_bytes(B, C);
     return bwd_tiling(C, n, x_dtype).vpt <= 0 ? wide_bwd_scratch_bytes(n, B, C) : 0;
 }
 
@@ -1021,6 +1027,13 @@ hipError_t launch_layer_bwd(int x_dtype, int n, int mode, const float* g, const 
                             const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                             int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s,
                             int32_t* dx_scale) {
+    if (generic_layer_n(n)) {
+        // the generic kernels write a full-precision stream part only for
+        // fp32 x; the dynamic entries send bf16 x through fp32 accumulation
+        if (mode == 1 && x_dtype == kBF16) return hipErrorInvalidValue;
+        return launch_gen_layer_bwd(x_dtype, n, mode, g, x, w, coef, coef_stride, dx, dw_part, scal_out, grid, B, C,
+                                    eps, scratch, s);
+    }
     const RowTiling t = bwd_tiling(C, n, x_dtype);
     if (t.vpt <= 0) {
         // the channel-loop kernels write a bf16 stream part; the dynamic
@@ -1111,6 +1124,13 @@ hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int row
                                   void* dw, const float* scal_part, int scal_rows, const float* h_pre,
                                   const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
                                   float* d_h_res, int iters, float sk_eps, hipStream_t s, float* sk_hist) {
+    if (n > 0 && generic_layer_n(n)) {
+        hipError_t e = launch_column_finalize(0, w_dtype, part, rows, cols, stage, dw, nullptr, 0, nullptr, nullptr,
+                                              nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+        if (e != hipSuccess) return e;
+        return launch_gen_static_finalize(n, scal_part, scal_rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res,
+                                          iters, sk_eps, s);
+    }
     if (n > 8) {
         // the static scalar gradients of wide n have their own kernel
         hipError_t e = launch_column_finalize(0, w_dtype, part, rows, cols, stage, dw, nullptr, 0, nullptr, nullptr,

@@ -74,6 +74,42 @@ inline hipError_t mhc_launch_kernel(const void* fn, dim3 grid, dim3 block, void*
 #define MHC_LAUNCH_GGL hipLaunchKernelGGL
 #endif
 
+// ---- generic.hip -----------------------------------------------------------
+// Expansion rates without a compiled instantiation (n <= kGenMaxN): the
+// layer's are n outside {2, 4, 8, 16, 32}, the stream operators' n outside
+// {1, 2, 4, 8, 16, 32}.  The layer launchers of layer.hip and dynamic.hip
+// and the operator launchers of ops.hip route these n here themselves.
+constexpr int kGenMaxN = 64;
+bool generic_layer_n(int n);
+bool generic_ops_n(int n);
+hipError_t launch_gen_static_coef(int n, const float* h_pre, const float* h_post, const float* h_res,
+                                  const void* weight, int w_dtype, int64_t C, float* saved, int iters, float sk_eps,
+                                  hipStream_t s);
+hipError_t launch_gen_layer_fwd(int x_dtype, int out_dtype, int n, const void* x, const float* w, const float* coef,
+                                int64_t coef_stride, void* out, float* rms_out, int64_t B, int64_t C, float eps,
+                                hipStream_t s);
+// Backward rows of the generic kernels: grid = gen_layer_bwd_grid(B)
+// persistent workgroups, scratch of gen_layer_bwd_scratch_bytes (each
+// workgroup's xa and gy rows); scal_out / dw_part as launch_layer_bwd.
+int gen_layer_bwd_grid(int64_t B);
+size_t gen_layer_bwd_scratch_bytes(int64_t B, int64_t C);
+hipError_t launch_gen_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
+                                const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
+                                int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s);
+hipError_t launch_gen_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
+                                      const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
+                                      float* d_h_res, int iters, float sk_eps, hipStream_t s);
+hipError_t launch_gen_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out,
+                                    float* h_act, int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_gen_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
+                                    void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
+hipError_t launch_gen_distribute_fwd(int dt, int n, const void* y, const float* H, int64_t hs, const float* M,
+                                     int64_t ms, const void* x, float* out, float* h_act, int64_t B, int64_t C,
+                                     hipStream_t s);
+hipError_t launch_gen_distribute_bwd(int dt, int n, const float* g, const void* x, const void* y, const float* M,
+                                     int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
+                                     float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s);
+
 // ---- layer.hip -------------------------------------------------------------
 // saved = [coef (2n + n^2) | pad | fp32 weight (C)], weight at saved_w_offset(n) floats
 int saved_w_offset(int n);

@@ -424,6 +424,12 @@ hipError_t launch_compute_rms(int dt, const void* x, float* rms, int64_t B, int6
 hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out, float* h_act,
                                 int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
+    if (generic_ops_n(n)) {
+        const int tok = timing_begin("aggregate_fwd", s);
+        const hipError_t e = launch_gen_aggregate_fwd(dt, n, x, H, hs, out, h_act, B, C, s);
+        timing_end(tok, s);
+        return e;
+    }
     const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1, 512);
     const int tok = timing_begin("aggregate_fwd", s);
     if (t.vpt <= 0) {
@@ -442,6 +448,12 @@ hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, in
 hipError_t launch_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
                                 void* gx, float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
+    if (generic_ops_n(n)) {
+        const int tok = timing_begin("aggregate_bwd", s);
+        const hipError_t e = launch_gen_aggregate_bwd(dt, n, g, x, h_act, hs, gx, gh_act, gh_raw, B, C, s);
+        timing_end(tok, s);
+        return e;
+    }
     const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1, 512);
     const int tok = timing_begin("aggregate_bwd", s);
     if (t.vpt <= 0) {
@@ -461,6 +473,7 @@ hipError_t launch_distribute_fwd(int dt, int n, const void* y, const float* H, i
                                  int64_t ms, const void* x, float* out, float* h_act, int64_t B, int64_t C,
                                  hipStream_t s) {
     if (B == 0) return hipSuccess;
+    if (generic_ops_n(n)) return launch_gen_distribute_fwd(dt, n, y, H, hs, M, ms, x, out, h_act, B, C, s);
     const RowTiling t = n > 8 ? RowTiling{0, 0} : choose_row_tiling(C, dt == kBF16 ? 8 : 4, n + 1, 512);
     const int tok = timing_begin("distribute_fwd", s);
     if (t.vpt <= 0) {
@@ -480,6 +493,8 @@ hipError_t launch_distribute_bwd(int dt, int n, const float* g, const void* x, c
                                  int64_t ms, const float* h_act, int64_t hs, void* gx, void* gy, float* gM,
                                  float* gh_act, float* gh_raw, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
+    if (generic_ops_n(n))
+        return launch_gen_distribute_bwd(dt, n, g, x, y, M, ms, h_act, hs, gx, gy, gM, gh_act, gh_raw, B, C, s);
     // the block hands one of the n*n + n row sums to each thread
     const RowTiling t =
         n > 8 ? RowTiling{0, 0} : with_min_threads(choose_row_tiling(C, dt == kBF16 ? 8 : 4, 2 * n + 1), n * n + n);

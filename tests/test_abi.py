@@ -70,9 +70,9 @@ def test_sinkhorn_rejects_n_above_a_wave_on_host():
 
 def test_layer_rejects_unsupported_and_invalid_on_host():
     lib = _lib.load()
-    # n not compiled -> UNSUPPORTED; bad dtype -> INVALID; hidden past the
+    # n above 64 -> UNSUPPORTED; bad dtype -> INVALID; hidden past the
     # channel-loop kernels' LDS row (12288 channels at n = 32) -> UNSUPPORTED
-    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 3, 64, 20, 1e-8, 1e-5, None) == -2
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 65, 64, 20, 1e-8, 1e-5, None) == -2
     assert lib.mhc_layer_static_fwd(1, 7, 1, 1, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
     assert lib.mhc_layer_static_fwd(1, 0, 1, 5, 1, 1, 1, 1, 1, 1, 8, 4, 64, 20, 1e-8, 1e-5, None) == -1
     assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 32, 12289, 20, 1e-8, 1e-5, None) == -2
@@ -86,19 +86,25 @@ def test_layer_rejects_unsupported_and_invalid_on_host():
 
 
 def test_expansion_rate_support_on_host():
-    """Layers compile n in {2, 4, 8, 16, 32}, dynamic H included (its
-    2n + n^2 projection rows run as 32-row output tiles); the fused wrapper
-    n = 4 (other n go through the layer).  All rejected before any device
-    work."""
+    """Layers take every n in 1..64 as the reference does (mhc_types.h:68):
+    fixed-n kernels for {2, 4, 8, 16, 32}, the generic kernels for the rest,
+    dynamic H included (its 2n + n^2 projection rows run as 32-row output
+    tiles or, above 128 rows, the streaming kernels); n > 64 is rejected.
+    The fused wrapper is n = 4 (other n go through the layer).  All checked
+    before any device work."""
     lib = _lib.load()
     # static layer: these n pass the host checks; with a null x they fail on that
-    for n in (2, 8, 16, 32):
+    for n in (1, 2, 3, 6, 8, 12, 16, 32, 64):
         assert lib.mhc_layer_static_fwd(None, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, n, 64, 20, 1e-8, 1e-5, None) == -1
         assert b"null x" in lib.mhc_last_error()
-    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 6, 64, 20, 1e-8, 1e-5, None) == -2
-    rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1 << 30, 8, 6, 64, 20, 1e-8,
+    assert lib.mhc_layer_static_fwd(1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 8, 65, 64, 20, 1e-8, 1e-5, None) == -2
+    rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1 << 30, 8, 65, 64, 20, 1e-8,
                                    1e-5, None)
-    assert rc == -2 and b"n=6 is not compiled" in lib.mhc_last_error()
+    assert rc == -2 and b"n=65 is not supported" in lib.mhc_last_error()
+    # dynamic n = 6 passes the shape checks; a null out then fails before any launch
+    rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, 1, 1, 1 << 30, 8, 6, 64, 20, 1e-8,
+                                   1e-5, None)
+    assert rc == -1 and b"null x/out" in lib.mhc_last_error()
     # dynamic n = 8 passes the shape checks; a null out then fails before any launch
     rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, 1, 1, 1 << 30, 8, 8, 64, 20, 1e-8,
                                    1e-5, None)

@@ -110,11 +110,12 @@ def test_stream_aggregate(device, dtype, shared, B, C):
 
 
 @pytest.mark.parametrize("n,C", [(1, 256), (2, 256), (8, 64), (16, 256), (32, 320), (1, 3), (4, 77), (8, 1001),
-                                 (32, 50)])
+                                 (32, 50), (3, 77), (6, 256), (12, 130), (20, 64), (64, 64)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_stream_ops_general_n(device, n, C, dtype):
-    """stream_aggregate and stream_distribute_mix_add at n = 1 .. 32 and
-    rows that are not a multiple of the vector (the distribute backward's
+    """stream_aggregate and stream_distribute_mix_add at n = 1 .. 64 (n = 3,
+    6, 12, 20, 64 on the generic kernels, n at run time) and rows that are
+    not a multiple of the vector (the distribute backward's
     n*n + n row sums need >= 72 lanes at n = 8; dM comes from the per-token
     Gram kernel at n >= 16)."""
     B = 9

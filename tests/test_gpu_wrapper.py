@@ -141,7 +141,8 @@ def test_wrapper_config_c5_width(device, dynamic):
 
 
 @pytest.mark.parametrize("n,dynamic,C", [(2, False, 256), (8, False, 256), (2, True, 256), (8, True, 128),
-                                         (32, False, 64), (32, True, 64), (4, False, 250)])
+                                         (32, False, 64), (32, True, 64), (4, False, 250), (6, False, 256),
+                                         (6, True, 128), (3, True, 96)])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
 def test_wrapper_general_n(device, n, dynamic, C, mode):
     """Shapes the fused wrapper kernels do not take (n != 4, or rows that
