@@ -1003,10 +1003,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
 typedef __bf16 wbf16x8b_t __attribute__((ext_vector_type(8)));
 
 // Workgroup of the projection backward: 8 waves x 16 channels, one per CU at
-// three waves per SIMD of registers.  A stage's row pieces are 256 bytes of
-// r and b and 512 of G per token: the bare access pattern runs at 6.0 TB/s
-// in this shape against 5.5 with 4-wave workgroups over 64 channels (three
-// per CU), and the kernel went from 4.8-5.2 to 4.7 ms at C5.
+// two waves per SIMD of registers.  A stage's row pieces are 256 bytes of
+// r and b and 512 of G per token; against 4-wave workgroups over 64 channels
+// (three per CU) the kernel went from 4.8-5.2 to 4.7 ms at C5.  The loads
+// and stores of this shape alone, with no compute, take 4.36-4.42 ms at C5
+// (5.1-5.2 TB/s for 8 bytes read and 4 written per element).
 constexpr int kWpbThreads = 512;
 constexpr int kWpbCols = kWpbThreads / 64 * 16;
 // Waves per SIMD the register allocation targets: two (one 8-wave workgroup
