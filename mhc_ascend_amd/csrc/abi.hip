@@ -1289,7 +1289,7 @@ int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dt
     bf16_raw_t* phib = (bf16_raw_t*)((char*)workspace + w.phib_off);
     float* pp = (float*)((char*)workspace + w.p_off);
     float* ss = (float*)((char*)workspace + w.ss_off);
-    e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+    e = launch_wrap_phi_planes(dtype, n, phi_pre, phi_post, phi_res, hidden, phib, s);
     if (e == hipSuccess) e = launch_wrap_proj(dtype, n, decay, residual, branch, phib, pp, ss, tokens, hidden, w.ks, s);
     if (e == hipSuccess)
         e = launch_dyn_coef_fwd(n, pp, ss, w.ks, tokens, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,

@@ -369,6 +369,11 @@ hipError_t launch_wrap_bwd_red(int dt, int n, bool decay, const float* g, const 
                                const float* w, const float* coef, int64_t coef_stride, float* scal_out,
                                float* ep_out, int64_t B, int64_t C, float eps, hipStream_t s);
 int wrap_proj_csplit(int64_t B, int64_t C);
+// Phi planes for launch_wrap_proj (n = 4): bf16 storage takes the five-slot
+// layout of wrap_phi_pack_kernel, fp32 storage phi_split_kernel's planes;
+// phib holds 6 * 32 * n * C bytes either way.
+hipError_t launch_wrap_phi_planes(int dt, int n, const float* phi_pre, const float* phi_post, const float* phi_res,
+                                  int64_t C, bf16_raw_t* phib, hipStream_t s);
 hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const void* br, const bf16_raw_t* phib,
                             float* p_part, float* ss_part, int64_t B, int64_t C, int ks, hipStream_t s);
 int wrap_proj_bwd_tiles(int dt, int64_t B, int64_t C);

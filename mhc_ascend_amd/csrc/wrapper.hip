@@ -729,11 +729,14 @@ __device__ __forceinline__ void wproj_stream(const uint4 (&rw)[sizeof(TX) / 2], 
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) ss = wsq2(a[e], ss);
+        // g[2 p + nt]: plane p of output tile nt, where tile 1 (rows
+        // 16..23) holds [hi | mid] at p = 0 and [lo | 0] at p = 1
+        // (wrap_phi_pack_kernel), so its last plane is not there
         constexpr int PL = wproj_planes<TX, J>();
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
-            for (int p = 0; p < PL; ++p) acc[nt] = wmfma16x16x32(a, wop(g[2 * p + nt]), acc[nt]);
+            for (int p = 0; p < PL - nt; ++p) acc[nt] = wmfma16x16x32(a, wop(g[2 * p + nt]), acc[nt]);
         }
     } else {
         float x[8];
@@ -782,6 +785,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
     constexpr int NHA = NSTR < 2 ? NSTR : 2;           // streams of the first Phi half
     constexpr int NHB = NSTR - NHA;
     constexpr int PLB = wproj_planes<TX, 2>();  // planes of the decay streams
+    constexpr bool PK = sizeof(TX) == 2;               // packed rows 16..23 (five Phi slots)
     static_assert(N == 4, "wrapper projection is instantiated for n = 4");
     static_assert(PASSES * RPP == TB, "stage rows");
     static_assert(3 * 9 * MT * 64 * 4 <= 2 * 2 * TB * PITCH, "epilogue reuses the stage buffers");
@@ -812,7 +816,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
     const uint32_t xbytes = (uint32_t)(rows * C * (int64_t)sizeof(TX));
     const buf_rsrc_t rrs = make_buf_rsrc(res + tok0 * C, xbytes);
     const buf_rsrc_t brs = make_buf_rsrc(br + tok0 * C, xbytes);
-    const buf_rsrc_t prs = make_buf_rsrc(phif, (uint32_t)(6 * ksteps * 64 * 16));
+    const buf_rsrc_t prs = make_buf_rsrc(phif, (uint32_t)((PK ? 5 : 6) * ksteps * 64 * 16));
     const int lrow = threadIdx.x / VPR;
     const int lvec = threadIdx.x % VPR;
     const uint32_t xoff = (uint32_t)(((int64_t)lrow * C + lvec * EPV) * (int64_t)sizeof(TX));
@@ -829,17 +833,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
     uint4 F[2][PASSES];
     uint4 GA[6 * (NHA > 0 ? NHA : 1)];
     uint4 GB[6 * (NHB > 0 ? NHB : 1)];
+    // Lanes whose 8 channels lie past the chunk end load from kBufOff (zeros),
+    // so the commit stores the loaded words as they are: a mask applied at
+    // the commit was moved by the compiler to just after the loads, and each
+    // stage then waited for its own prefetch in the middle of its MFMAs.
     auto fetch_x = [&](int64_t st) __attribute__((always_inline)) {
-        const uint32_t col = (uint32_t)((cb + srot(st) * KS) * (int64_t)sizeof(TX));
+        const int64_t c0 = cb + srot(st) * KS;
+        const uint32_t base =
+            c0 + lvec * EPV < ce ? xoff + (uint32_t)(c0 * (int64_t)sizeof(TX)) : kBufOff;
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
-            F[0][p] = buf_ld16<true, true>(rrs, xoff + p * xpass + col, 0u);
-            F[1][p] = buf_ld16<true, true>(brs, xoff + p * xpass + col, 0u);
+            F[0][p] = buf_ld16<true, true>(rrs, base + p * xpass, 0u);
+            F[1][p] = buf_ld16<true, true>(brs, base + p * xpass, 0u);
         }
     };
     // Phi fragments of streams j0 .. j0+nj-1 at this wave's 32 channels of
     // stage st (clamped to the last k step: past ce the operands are zero);
-    // pl planes each
+    // pl planes each, at slot 2p + nt (phi_split_kernel's planes; bf16
+    // storage: wrap_phi_pack_kernel's five slots, tile 1 one plane short).
     auto fetch_phi = [&](uint4* g, int j0, int nj, int pl, int64_t st) __attribute__((always_inline)) {
         const int64_t c0 = cb + srot(st) * KS + wave * 32;
 #pragma unroll
@@ -848,18 +859,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
             kstep = kstep < ksteps ? kstep : ksteps - 1;
             const uint32_t so = (uint32_t)(kstep * 64 * 16);
 #pragma unroll
-            for (int q = 0; q < 2 * pl; ++q)
-                g[6 * jj + q] = buf_ld16<false, true>(prs, (uint32_t)((q * ksteps * 64 + lane) * 16), so);
+            for (int q = 0; q < 2 * pl - (PK ? 1 : 0); ++q)
+                g[6 * jj + q] = buf_ld16<false>(prs, (uint32_t)((q * ksteps * 64 + lane) * 16), so);
         }
     };
-    auto commit = [&](int64_t st, int buf) __attribute__((always_inline)) {
-        const uint32_t m = (cb + srot(st) * KS + lvec * EPV < ce) ? 0xffffffffu : 0u;
+    auto commit = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
 #pragma unroll
             for (int p = 0; p < PASSES; ++p)
-                *reinterpret_cast<uint4*>(&xs[buf][a][(lrow + p * RPP) * PITCH + lvec * 16]) =
-                    make_uint4(F[a][p].x & m, F[a][p].y & m, F[a][p].z & m, F[a][p].w & m);
+                *reinterpret_cast<uint4*>(&xs[buf][a][(lrow + p * RPP) * PITCH + lvec * 16]) = F[a][p];
         }
     };
     // MFMAs of streams J0 (and J0 + 1 when two) against fragments g
@@ -906,7 +915,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
         fetch_x(0);
         fetch_phi(GA, 0, NHA, 3, 0);
         if constexpr (NHB > 0) fetch_phi(GB, 2, NHB, PLB, 0);
-        commit(0, 0);
+        commit(0);
         __syncthreads();
         for (int64_t st = 0; st < nst; ++st) {
             const int buf = (int)(st & 1);
@@ -918,7 +927,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
                 compute_half(buf, GB, I2{}, IHB{});
                 fetch_phi(GB, 2, NHB, PLB, clampst(st + 1));
             }
-            commit(clampst(st + 1), buf ^ 1);
+            commit(buf ^ 1);
             __syncthreads();
         }
     }
@@ -954,6 +963,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
     float* pp = p_part + (int64_t)blockIdx.y * B * KP;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+        if constexpr (PK) {
+            // packed tile: row 16 + c = column c (hi, lo) + column c + 8 (mid);
+            // rows 24..31 are zero
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float v = acc[mt][1][i] + __shfl_xor(acc[mt][1][i], 8);
+                acc[mt][1][i] = row < 8 ? v : 0.f;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int64_t tok = tok0 + mt * 16 + kg * 4 + i;
@@ -966,6 +984,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void w
         s2 = xor32_add(xor16_add(s2));
         const int64_t tok = tok0 + mt * 16 + row;
         if (kg == 0 && tok < B) ss_part[(int64_t)blockIdx.y * B + tok] = s2;
+    }
+}
+
+// Phi of the n = 4 wrapper (24 rows) as the bf16 MFMA B fragments of
+// wrap_proj_kernel's bf16-storage path: five slots per 32-wide k step ks,
+//   phif[(q * (K / 32) + ks) * 64 + lane]  (8 bf16, 16 bytes),
+// k = 32 ks + 8 (lane / 16) .. + 7, c = lane % 16, slot q = 2 p + nt as in
+// phi_split_kernel for tile 0 (rows 0..15), while tile 1 (rows 16..23,
+// half empty) takes two slots instead of three:
+//   q = 0, 2, 4: hi, mid, lo of row c
+//   q = 1:       hi of row 16 + c (c < 8), mid of row 16 + c - 8 (c >= 8)
+//   q = 3:       lo of row 16 + c (c < 8), zero (c >= 8)
+// One MFMA over slot 1 leaves the hi and mid products of rows 16..23 in
+// columns c and c + 8, which the kernel adds once at the end.
+__global__ __launch_bounds__(256) void wrap_phi_pack_kernel(const float* __restrict__ pre,
+                                                            const float* __restrict__ post,
+                                                            const float* __restrict__ res, int64_t K,
+                                                            uint4* __restrict__ phif) {
+    const int64_t ksteps = K / 32;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < ksteps * 64;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i & 63);
+        const int64_t ks = i >> 6;
+        const int c = lane & 15;
+        const int64_t k = ks * 32 + 8 * (lane >> 4);
+        float v0[8], v1[8];
+        load_run<float, 8>(phi_row(pre, post, res, 4, c, K) + k, v0);
+        load_run<float, 8>(phi_row(pre, post, res, 4, 16 + (c & 7), K) + k, v1);
+        uint32_t w[5][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float h0, m0, l0, h1, m1, l1;
+            wsplit3(v0[2 * e], h0, m0, l0);
+            wsplit3(v0[2 * e + 1], h1, m1, l1);
+            w[0][e] = wpack(h0, h1);
+            w[2][e] = wpack(m0, m1);
+            w[4][e] = wpack(l0, l1);
+            wsplit3(v1[2 * e], h0, m0, l0);
+            wsplit3(v1[2 * e + 1], h1, m1, l1);
+            w[1][e] = c < 8 ? wpack(h0, h1) : wpack(m0, m1);
+            w[3][e] = c < 8 ? wpack(l0, l1) : 0u;
+        }
+#pragma unroll
+        for (int q = 0; q < 5; ++q) phif[(q * ksteps + ks) * 64 + lane] = make_uint4(w[q][0], w[q][1], w[q][2], w[q][3]);
     }
 }
 
@@ -1643,6 +1705,18 @@ int wrap_proj_csplit(int64_t B, int64_t C) {
     if (ks > kmax) ks = kmax;
     if (ks < 1) ks = 1;
     return (int)ks;
+}
+
+hipError_t launch_wrap_phi_planes(int dt, int n, const float* phi_pre, const float* phi_post, const float* phi_res,
+                                  int64_t C, bf16_raw_t* phib, hipStream_t s) {
+    if (n != 4 || C % 32 != 0) return hipErrorInvalidValue;
+    const int64_t K = 4 * C;
+    if (dt != kBF16) return launch_phi_split(phi_pre, phi_post, phi_res, n, 2 * n + n * n, K, phib, s);
+    int64_t blocks = (K / 32 * 64 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    MHC_LAUNCH_GGL(wrap_phi_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, s, phi_pre, phi_post, phi_res, K,
+                   reinterpret_cast<uint4*>(phib));
+    return hipGetLastError();
 }
 
 hipError_t launch_wrap_proj(int dt, int n, bool decay, const void* res, const void* br, const bf16_raw_t* phib,
