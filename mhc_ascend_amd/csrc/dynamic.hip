@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
         kstep = kstep < ksteps ? kstep : ksteps - 1;
         const uint32_t so = (uint32_t)(kstep * 64 * 16);
 #pragma unroll
-        for (int q = 0; q < 6; ++q) g[q] = buf_ld16<false, true>(prs, (uint32_t)((q * ksteps * 64 + lane) * 16), so);
+        for (int q = 0; q < 6; ++q) g[q] = buf_ld16<false>(prs, (uint32_t)((q * ksteps * 64 + lane) * 16), so);
     };
     auto commit = [&](const uint4 (&f)[PASSES], int64_t st, int buf) __attribute__((always_inline)) {
         const uint32_t m = (kb + srot(st) * KS + lvec * EPV < ke) ? 0xffffffffu : 0u;
