@@ -122,83 +122,107 @@ __global__ MHC_ROW_BOUNDS(false) void compute_rms_kernel(const T* __restrict__ x
 // 700-816):  h = sigmoid(H), out = sum_i h_i x_i;
 //   bwd: dx_i = g h_i, dh_act_i = sum_c g x_i, dH_i = dh_act_i h_i (1 - h_i)
 // ---------------------------------------------------------------------------
-template <typename T, int N, int VPT>
+// TPW tokens per workgroup as in aggregate_bwd_kernel (C2: 216-217 against
+// 231-233 us with two).
+template <typename T, int N, int VPT, int TPW>
 __global__ MHC_ROW_BOUNDS(false) void aggregate_fwd_kernel(const T* __restrict__ x, const float* __restrict__ H,
                                                            int64_t h_stride, T* __restrict__ out,
-                                                           float* __restrict__ h_act, int C) {
+                                                           float* __restrict__ h_act, int64_t B, int C) {
     constexpr int WC = VecIO<T>::W;
-    const int64_t b = blockIdx.x;
-    float h[N];
+    const int64_t b0 = (int64_t)blockIdx.x * TPW;
+    RawRows<T, N, VPT, WC> xr[TPW];
 #pragma unroll
-    for (int i = 0; i < N; ++i) h[i] = sigmoidf(H[b * h_stride + i]);
-    float xv[N][VPT][WC];
-    load_rows<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xv);
-    float o[VPT][WC];
+    for (int t = 0; t < TPW; ++t)
+        load_rows_raw_rs<T, N, VPT, WC, true>(token_rows_rsrc(x, b0 + t, B, N, C), C, xr[t]);
 #pragma unroll
-    for (int k = 0; k < VPT; ++k) {
+    for (int t = 0; t < TPW; ++t) {
+        const int64_t b = b0 + t;
+        if (b >= B) break;  // the last workgroup's second token only
+        float h[N];
 #pragma unroll
-        for (int e = 0; e < WC; ++e) {
-            float s = 0.f;
-#pragma unroll
-            for (int i = 0; i < N; ++i) s += h[i] * xv[i][k][e];
-            o[k][e] = s;
-        }
-    }
-    store_row1<T, VPT, WC, true>(out + b * C, C, o);
-    if (threadIdx.x < N) h_act[b * N + threadIdx.x] = h[threadIdx.x];
-}
-
-template <typename T, int N, int VPT>
-__global__ MHC_ROW_BOUNDS(false) void aggregate_bwd_kernel(const T* __restrict__ g, const T* __restrict__ x,
-                                                           const float* __restrict__ h_act, int64_t h_stride,
-                                                           T* __restrict__ gx, float* __restrict__ gh_act,
-                                                           float* __restrict__ gh_raw, int C) {
-    constexpr int WC = VecIO<T>::W;
-    __shared__ float red[8 * N];
-    const int64_t b = blockIdx.x;
-    float h[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) h[i] = h_act[b * h_stride + i];
-    RawRows<T, 1, VPT, WC> gr;
-    RawRows<T, N, VPT, WC> xr;
-    float gv[1][VPT][WC], xv[N][VPT][WC];
-    load_rows_raw<T, 1, VPT, WC, true>(g + b * C, C, gr);
-    load_rows_raw<T, N, VPT, WC, true>(x + b * (int64_t)N * C, C, xr);
-    unpack_rows<T, 1, VPT, WC>(gr, C, gv);
-    unpack_rows<T, N, VPT, WC>(xr, C, xv);
-    float s[N];
-#pragma unroll
-    for (int i = 0; i < N; ++i) s[i] = 0.f;
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-#pragma unroll
-        for (int e = 0; e < WC; ++e) {
-#pragma unroll
-            for (int i = 0; i < N; ++i) s[i] += gv[0][k][e] * xv[i][k][e];
-        }
-    }
-    T* gb = gx + b * (int64_t)N * C;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        float d[VPT][WC];
+        for (int i = 0; i < N; ++i) h[i] = sigmoidf(H[b * h_stride + i]);
+        float xv[N][VPT][WC];
+        unpack_rows<T, N, VPT, WC>(xr[t], C, xv);
+        float o[VPT][WC];
 #pragma unroll
         for (int k = 0; k < VPT; ++k) {
 #pragma unroll
-            for (int e = 0; e < WC; ++e) d[k][e] = gv[0][k][e] * h[i];
-        }
-        store_row1<T, VPT, WC, true>(gb + (int64_t)i * C, C, d);
-    }
-    block_sum<N>(s, red);
-    if (threadIdx.x < N) {
-        const int i = threadIdx.x;
-        float si = 0.f, hi = 0.f;
+            for (int e = 0; e < WC; ++e) {
+                float s = 0.f;
 #pragma unroll
-        for (int q = 0; q < N; ++q) {
-            si = (q == i) ? s[q] : si;
-            hi = (q == i) ? h[q] : hi;
+                for (int i = 0; i < N; ++i) s += h[i] * xv[i][k][e];
+                o[k][e] = s;
+            }
         }
-        if (gh_act) gh_act[b * N + i] = si;
-        if (gh_raw) gh_raw[b * N + i] = si * hi * (1.f - hi);
+        store_row1<T, VPT, WC, true>(out + b * C, C, o);
+        if (threadIdx.x < N) h_act[b * N + threadIdx.x] = h[threadIdx.x];
+    }
+}
+
+// TPW tokens per workgroup (1 or 2): with two, both tokens' rows are loaded
+// up front, so the second token's loads run under the first one's sums,
+// stores and barrier (C2 [16384, 4, 4096] fp32: 405-406 against 425-429 us).
+// Rows go through buffer resources over one token each (token_rows_rsrc): a
+// token past B reads zeros and stores nothing.
+template <typename T, int N, int VPT, int TPW>
+__global__ MHC_ROW_BOUNDS(false) void aggregate_bwd_kernel(const T* __restrict__ g, const T* __restrict__ x,
+                                                           const float* __restrict__ h_act, int64_t h_stride,
+                                                           T* __restrict__ gx, float* __restrict__ gh_act,
+                                                           float* __restrict__ gh_raw, int64_t B, int C) {
+    constexpr int WC = VecIO<T>::W;
+    __shared__ float red[TPW][8 * N];
+    const int64_t b0 = (int64_t)blockIdx.x * TPW;
+    RawRows<T, 1, VPT, WC> gr[TPW];
+    RawRows<T, N, VPT, WC> xr[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        load_rows_raw_rs<T, 1, VPT, WC, true>(token_rows_rsrc(g, b0 + t, B, 1, C), C, gr[t]);
+        load_rows_raw_rs<T, N, VPT, WC, true>(token_rows_rsrc(x, b0 + t, B, N, C), C, xr[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        const int64_t b = b0 + t;
+        if (b >= B) break;  // the last workgroup's second token only
+        float h[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) h[i] = h_act[b * h_stride + i];
+        float gv[1][VPT][WC], xv[N][VPT][WC];
+        unpack_rows<T, 1, VPT, WC>(gr[t], C, gv);
+        unpack_rows<T, N, VPT, WC>(xr[t], C, xv);
+        float s[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) s[i] = 0.f;
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+#pragma unroll
+            for (int e = 0; e < WC; ++e) {
+#pragma unroll
+                for (int i = 0; i < N; ++i) s[i] += gv[0][k][e] * xv[i][k][e];
+            }
+        }
+        T* gb = gx + b * (int64_t)N * C;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            float d[VPT][WC];
+#pragma unroll
+            for (int k = 0; k < VPT; ++k) {
+#pragma unroll
+                for (int e = 0; e < WC; ++e) d[k][e] = gv[0][k][e] * h[i];
+            }
+            store_row1<T, VPT, WC, true>(gb + (int64_t)i * C, C, d);
+        }
+        block_sum<N>(s, red[t]);
+        if (threadIdx.x < N) {
+            const int i = threadIdx.x;
+            float si = 0.f, hi = 0.f;
+#pragma unroll
+            for (int q = 0; q < N; ++q) {
+                si = (q == i) ? s[q] : si;
+                hi = (q == i) ? h[q] : hi;
+            }
+            if (gh_act) gh_act[b * N + i] = si;
+            if (gh_raw) gh_raw[b * N + i] = si * hi * (1.f - hi);
+        }
     }
 }
 
@@ -437,10 +461,17 @@ hipError_t launch_aggregate_fwd(int dt, int n, const void* x, const float* H, in
         timing_end(tok, s);
         return e;
     }
-    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, MHC_LAUNCH_GGL((aggregate_fwd_kernel<T_, N_, V_>),
-                                                                                 dim3(B), dim3(t.threads), 0, s,
-                                                                                 (const T_*)x, H, hs, (T_*)out, h_act,
-                                                                                 (int)C))));
+#define MHC_AGG_FWD(TPW_)                                                                               \
+    MHC_LAUNCH_GGL((aggregate_fwd_kernel<T_, N_, V_, TPW_>), dim3((unsigned)((B + TPW_ - 1) / TPW_)),  \
+                   dim3(t.threads), 0, s, (const T_*)x, H, hs, (T_*)out, h_act, B, (int)C)
+    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, {
+        if constexpr (row_fits<T_>(2 * (N_ + 1), V_)) {
+            MHC_AGG_FWD(2);
+        } else {
+            MHC_AGG_FWD(1);
+        }
+    })));
+#undef MHC_AGG_FWD
     timing_end(tok, s);
     return hipGetLastError();
 }
@@ -461,10 +492,19 @@ hipError_t launch_aggregate_bwd(int dt, int n, const void* g, const void* x, con
         timing_end(tok, s);
         return e;
     }
-    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, MHC_LAUNCH_GGL((aggregate_bwd_kernel<T_, N_, V_>),
-                                                                                 dim3(B), dim3(t.threads), 0, s,
-                                                                                 (const T_*)g, (const T_*)x, h_act, hs,
-                                                                                 (T_*)gx, gh_act, gh_raw, (int)C))));
+    // two tokens per workgroup where both tokens' rows fit the row budget
+#define MHC_AGG_BWD(TPW_)                                                                                   \
+    MHC_LAUNCH_GGL((aggregate_bwd_kernel<T_, N_, V_, TPW_>), dim3((unsigned)((B + TPW_ - 1) / TPW_)),      \
+                   dim3(t.threads), 0, s, (const T_*)g, (const T_*)x, h_act, hs, (T_*)gx, gh_act, gh_raw, B, \
+                   (int)C)
+    MHC_OPS_T(dt, MHC_OPS_N(n, MHC_OPS_VPT(t.vpt, N_ + 1, T_, {
+        if constexpr (row_fits<T_>(2 * (N_ + 1), V_)) {
+            MHC_AGG_BWD(2);
+        } else {
+            MHC_AGG_BWD(1);
+        }
+    })));
+#undef MHC_AGG_BWD
     timing_end(tok, s);
     return hipGetLastError();
 }
