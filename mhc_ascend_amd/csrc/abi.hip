@@ -1425,8 +1425,12 @@ int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const v
     if (e == hipSuccess)
         e = launch_column_finalize(0, kF32, phip, rows_p, (int64_t)npo * K, stp, grad_phi, nullptr, 0, nullptr,
                                   nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
-    if (e == hipSuccess && npo < np) e = launch_fill_zero(grad_phi + (int64_t)npo * K, (int64_t)(np - npo) * K, s);
     if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
+    // the H_res rows: zeros, NaN where the alpha gradients (sums over the
+    // same tokens) are not finite, as the reference's would be then
+    if (e == hipSuccess && npo < np)
+        e = launch_fill_zero_carry(grad_phi + (int64_t)npo * K, (int64_t)(np - npo) * K, grad_b + npo, np - npo,
+                                   grad_alpha, 3, s);
     return hip_status(e);
 }
 
@@ -1487,9 +1491,10 @@ int mhc_wrapper_static_bwd(const float* grad_out, const void* residual, const vo
     if (e == hipSuccess)
         e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stage, grad_weight, scal_part, rows, h_pre,
                                   h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
-    // dH_res of the wrapper is zero up to eps (wrap_res_grad_vanishes)
+    // dH_res of the wrapper is zero up to eps (wrap_res_grad_vanishes); NaN
+    // where dH_pre (a sum over the same tokens) is not finite
     if (e == hipSuccess && wrap_res_grad_vanishes(num_iters, sinkhorn_eps))
-        e = launch_fill_zero(grad_h_res, (int64_t)n * n, s);
+        e = launch_fill_zero_carry(grad_h_res, (int64_t)n * n, nullptr, 0, grad_h_pre, n, s);
     return hip_status(e);
 }
 

@@ -751,6 +751,25 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, i
     if (i < n) p[i] = 0.f;
 }
 
+// p0[0, n0) and p1[0, n1) = s - s with s = c[0] + .. + c[nc - 1]: +0 while
+// the carrier sum is finite, NaN once it is not (no fast-math, so s - s is
+// not folded).  For gradients that vanish by construction but would be
+// non-finite on non-finite inputs, with a gradient sum over the same tokens
+// as the carrier.
+__global__ __launch_bounds__(256) void fill_zero_carry_kernel(float* __restrict__ p0, int64_t n0,
+                                                              float* __restrict__ p1, int64_t n1,
+                                                              const float* __restrict__ c, int nc) {
+    float s = 0.f;
+    for (int k = 0; k < nc; ++k) s += c[k];
+    const float z = s - s;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n0) {
+        p0[i] = z;
+    } else if (i - n0 < n1) {
+        p1[i - n0] = z;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
@@ -774,6 +793,16 @@ hipError_t launch_cast_bf16(const float* in, int64_t n, void* out, hipStream_t s
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     MHC_LAUNCH_GGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero_carry(float* p0, int64_t n0, float* p1, int64_t n1, const float* c, int nc,
+                                  hipStream_t s) {
+    if (n0 < 0 || n1 < 0) return hipErrorInvalidValue;
+    const int64_t n = n0 + n1;
+    if (n == 0) return hipSuccess;
+    MHC_LAUNCH_GGL(fill_zero_carry_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p0, n0, p1, n1, c,
+                   nc);
     return hipGetLastError();
 }
 

@@ -153,6 +153,10 @@ size_t layer_bwd_scratch_bytes(int x_dtype, int n, int64_t B, int64_t C);
 bool layer_fwd_is_wide(int n, int64_t C);
 bool layer_bwd_is_wide(int n, int64_t C);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s);
+// p0[0, n0) and p1[0, n1) = +0 while c[0] + .. + c[nc - 1] is finite, NaN
+// otherwise (fill_zero_carry_kernel)
+hipError_t launch_fill_zero_carry(float* p0, int64_t n0, float* p1, int64_t n1, const float* c, int nc,
+                                  hipStream_t s);
 // out[i] = bf16(in[i]) (round to nearest even) for n elements.
 hipError_t launch_cast_bf16(const float* in, int64_t n, void* out, hipStream_t s);
 // Two-stage deterministic column sum of part[rows][cols]: stage[rsplit][cols].

@@ -257,6 +257,22 @@ def build_wrapper_streams(residual: torch.Tensor, branch: torch.Tensor, n: int,
     return X
 
 
+class _StoredDecay(torch.autograd.Function):
+    """res * c stored in ``storage`` (value of the reference's tensor op,
+    layer.py:307-308), with the gradient of the product: g * c.  Infinite
+    values stay infinite (a straight-through sum s + (value - s) would turn
+    them into NaN)."""
+
+    @staticmethod
+    def forward(ctx, res, c, storage):
+        ctx.c = c
+        return (res.detach().float() * torch.tensor(c, dtype=torch.float32)).to(storage).to(res.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g * ctx.c, None, None
+
+
 def mhc_residual_wrapper(residual: torch.Tensor, branch: torch.Tensor, layer_fn, n: int,
                          mode: str = "decay", storage_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """MHCResidualWrapper.forward (layer.py:269-322): synthesise n streams,
@@ -287,10 +303,8 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch: torch.Tensor, layer_fn,
         elif storage_dtype is None:
             streams.append(res * (0.1 ** (i - 1)))
         else:
-            c = torch.tensor(0.1 ** (i - 1), dtype=torch.float32)
-            s = res * c.item()
-            value = (res.detach().float() * c).to(storage_dtype).to(res.dtype)
-            streams.append(s + (value - s).detach())
+            c = torch.tensor(0.1 ** (i - 1), dtype=torch.float32).item()
+            streams.append(_StoredDecay.apply(res, c, storage_dtype))
     X = torch.stack(streams[:n], dim=1)
     out = layer_fn(X).mean(dim=1)
     if T > 1:
