@@ -98,3 +98,100 @@ def test_wrapper_nonfinite_token(device, dynamic, dtype, value):
     keep = [0, 1, 2, 3, 5]
     assert torch.isfinite(out[keep]).all()
     assert torch.isfinite(rd.grad[keep]).all() and torch.isfinite(bd.grad[keep]).all()
+
+
+def _leaves(device, *ts):
+    return [t.to(device).requires_grad_(True) for t in ts], [t.double().requires_grad_(True) for t in ts]
+
+
+@pytest.mark.parametrize("value", [float("nan"), float("inf")])
+def test_operators_nonfinite(device, value):
+    g = torch.Generator().manual_seed(9)
+    # Sinkhorn: one entry of one matrix
+    a = _plant(torch.rand(6, 4, 4, generator=g) + 0.1, value, (3, 1, 2))
+    ga = torch.randn(6, 4, 4, generator=g)
+    (ad,), (ar,) = _leaves(device, a)
+    out = mhc.sinkhorn_knopp(ad, 20, 1e-8)
+    ref = R.sinkhorn_knopp(ar, 20, 1e-8)
+    out.backward(ga.to(device))
+    ref.backward(ga.double())
+    _masks_match(out, ref, "sinkhorn out")
+    _masks_match(ad.grad, ar.grad, "sinkhorn d inp")
+    # RMSNorm: one channel of one row
+    x = _plant(torch.randn(5, 96, generator=g), value, (2, 40))
+    w = 1 + 0.1 * torch.randn(96, generator=g)
+    gy = torch.randn(5, 96, generator=g)
+    (xd, wd), (xr, wr) = _leaves(device, x, w)
+    y = mhc.rmsnorm(xd, wd, 1e-5)
+    yr, _ = R.rmsnorm(xr, wr, 1e-5)
+    y.backward(gy.to(device))
+    yr.backward(gy.double())
+    _masks_match(y, yr, "rmsnorm out")
+    _masks_match(xd.grad, xr.grad, "rmsnorm dx")
+    _masks_match(wd.grad, wr.grad, "rmsnorm dw")
+    # stream aggregate: one element of x
+    xs = _plant(torch.randn(5, 4, 96, generator=g), value, (1, 2, 7))
+    H = torch.randn(5, 4, generator=g)
+    go = torch.randn(5, 96, generator=g)
+    (xsd, Hd), (xsr, Hr) = _leaves(device, xs, H)
+    o = mhc.stream_aggregate(xsd, Hd)
+    orf, _ = R.stream_aggregate(xsr, Hr)
+    o.backward(go.to(device))
+    orf.backward(go.double())
+    _masks_match(o, orf, "aggregate out")
+    _masks_match(xsd.grad, xsr.grad, "aggregate dx")
+    _masks_match(Hd.grad, Hr.grad, "aggregate dH")
+    # stream distribute: one element of y
+    yv = _plant(torch.randn(5, 96, generator=g), value, (3, 11))
+    Hp = torch.randn(5, 4, generator=g)
+    M = torch.rand(5, 4, 4, generator=g)
+    x2 = torch.randn(5, 4, 96, generator=g)
+    g2 = torch.randn(5, 4, 96, generator=g)
+    (yd, Hpd, Md, x2d), (yr2, Hpr, Mr, x2r) = _leaves(device, yv, Hp, M, x2)
+    d = mhc.stream_distribute_mix_add(yd, Hpd, Md, x2d)
+    dr, _ = R.stream_distribute_mix_add(yr2, Hpr, Mr, x2r)
+    d.backward(g2.to(device))
+    dr.backward(g2.double())
+    for got, want, what in ((d, dr, "distribute out"), (yd.grad, yr2.grad, "distribute dy"),
+                            (Hpd.grad, Hpr.grad, "distribute dH"), (Md.grad, Mr.grad, "distribute dM"),
+                            (x2d.grad, x2r.grad, "distribute dx")):
+        _masks_match(got, want, what)
+
+
+@pytest.mark.parametrize("dynamic", [False, True])
+def test_layer_nonfinite_cotangent(device, dynamic):
+    torch.manual_seed(5)
+    layer = mhc.MHCLayer(64, 4, use_dynamic_h=dynamic)
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(5, 4, 64, generator=g)
+    go = _plant(torch.randn(5, 4, 64, generator=g), float("nan"), (1, 3, 20))
+    names = DYN if dynamic else STA
+    w = layer.rmsnorm_weight.detach().double().requires_grad_(True)
+    ps = [getattr(layer, k).detach().double().requires_grad_(True) for k in names]
+    xr = x.double().requires_grad_(True)
+    fn = R.mhc_layer_dynamic if dynamic else R.mhc_layer_static
+    fn(xr, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64).backward(go.double())
+    layer = layer.to(device)
+    xd = x.to(device).requires_grad_(True)
+    layer(xd).backward(go.to(device))
+    _masks_match(xd.grad, xr.grad, "dx")
+    _masks_match(layer.rmsnorm_weight.grad, w.grad, "d weight")
+    for k, p in zip(names, ps):
+        _masks_match(getattr(layer, k).grad, p.grad, f"d {k}")
+
+
+@pytest.mark.parametrize("value", [float("nan"), float("inf")])
+def test_inference_nonfinite_token(device, value):
+    torch.manual_seed(6)
+    layer = mhc.MHCLayer(64, 4, use_dynamic_h=True)
+    g = torch.Generator().manual_seed(11)
+    x = _plant(torch.randn(5, 4, 64, generator=g), value, (0, 2, 33))
+    ps = [getattr(layer, k).detach().double() for k in DYN]
+    ref = R.mhc_layer_dynamic(x.double(), layer.rmsnorm_weight.detach().double(), *ps, 20, 1e-8, 1e-5,
+                              dtype=torch.float64)
+    layer = layer.to(device).eval()
+    layer.prepare_inference()
+    with torch.no_grad():
+        out = layer(x.to(device))
+    _masks_match(out, ref, "inference out")
+    assert torch.isfinite(out[1:]).all()
