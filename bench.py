@@ -1,7 +1,7 @@
 """Benchmark of the mHC layer forward+backward on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload static|dynamic|infer|infer_bf16|wrapper|ops] [--paper-configs]
+                    [--workload static|dynamic|infer|infer_bf16|wrapper|wrapper8|ops] [--paper-configs]
 
 Prints ONE JSON line: tokens/s of the whole fwd+bwd step (K steps timed on
 the host clock with nothing else in the timed region), the achieved HBM GB/s
@@ -21,6 +21,8 @@ Workloads (the metric is quoted at n=4, C=4096):
   infer   - C4 shape forward only (eval, no_grad, parameters packed once),
             fp32 output as the reference; infer_bf16 the same with bf16 output
   wrapper - C5: MHCResidualWrapper, residual/branch bf16 [65536, 4, 7168]
+  wrapper8 - the wrapper at n = 8 on [16384, 4, 7168] (run-time-n kernels),
+            with the unfused path timed beside it (not a BASELINE config)
   ops     - C2: standalone sinkhorn_knopp / rmsnorm / stream_aggregate fwd+bwd
             (value = the step's achieved HBM GB/s)
 --paper-configs runs the reference's 9-configuration sweep (benchmark.py:
@@ -440,6 +442,66 @@ class WrapperWorkload:
                            f"on {tok} of {self.tokens} tokens, n={self.n}, C={self.C}; median of {runs} runs")
 
 
+class Wrapper8Workload(WrapperWorkload):
+    """MHCResidualWrapper at expansion rate 8 (dynamic H, 'decay'), the C5
+    width on a quarter of its tokens: residual, branch bf16 [16384, 4, 7168]
+    (65,536 tokens).  Runs the run-time-n wrapper kernels; the record also
+    times the same step through the unfused path (the streams built with
+    device tensor ops, as layer.py:299-310, and the layer run on them)."""
+
+    name = "wrapper8"
+    Bo, T, n, C = 16384, 4, 8, 7168
+    metric = "mHC MHCResidualWrapper n=8 dynamic-H fwd+bwd tokens/sec (C5 width, 65,536 tokens)"
+
+    def step_bytes(self):
+        # as C5's count (r, b, g and d r, d b once each; Phi twice, dPhi once)
+        return 20 * self.F + 3 * self.phi_bytes()
+
+    def kernel_bytes(self):
+        F, n = self.F, self.n
+        # wrap_fwd reads r, b (bf16) and writes the fp32 mean; the backward's
+        # row sums read g and r, b; wrap_proj_bwd (d r, d b) reads g, r, b and
+        # the fp32 dX of the n streams and writes d r, d b
+        return {"wrap_fwd": 8 * F, "wrap_bwd_reduce": 8 * F, "wrap_proj_bwd": (12 + 4 * n) * F}
+
+    def flops(self):
+        return {}
+
+    def config(self):
+        c = super().config()
+        c["workload"] = "MHCResidualWrapper n=8 dynamic-H fwd+bwd (C5 width)"
+        return c
+
+    def unfused_ab(self, steps):
+        """ms per step of the unfused path on the same inputs and parameters."""
+        torch = self.torch
+        layer = self.wrapper.mhc
+
+        def step():
+            k = self.i % self.sets
+            self.i += 1
+            r, b, g = self.rs[k], self.bs[k], self.gs[k]
+            rr, bb = r.reshape(-1, self.C), b.reshape(-1, self.C)
+            X = torch.zeros(rr.shape[0], self.n, self.C, device=rr.device, dtype=rr.dtype)
+            X[:, 0] = rr
+            X[:, 1] = bb
+            for i in range(2, self.n):
+                X[:, i] = rr * (0.1 ** (i - 1))
+            out = layer(X).mean(dim=1).view(r.shape)
+            return torch.autograd.grad(out, [r, b] + self.params, g)
+
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return {"ms_per_step": (time.perf_counter() - t0) * 1e3 / steps, "steps": steps,
+                "path": "torch.zeros + slice copies + decay products (layer.py:299-310), MHCLayer on [tokens, 8, C], "
+                        "mean over streams; fwd+bwd through autograd"}
+
+
 class OpsWorkload:
     """C2: the standalone operators, fp32, forward + backward through autograd:
     sinkhorn_knopp [65536, 4, 4] ~U(0,1) (20 iterations, eps 1e-8), rmsnorm
@@ -535,10 +597,11 @@ class OpsWorkload:
 
 
 WORKLOADS = {"static": StaticWorkload, "dynamic": DynamicWorkload, "infer": InferWorkload,
-             "infer_bf16": InferBF16Workload, "wrapper": WrapperWorkload, "ops": OpsWorkload}
-KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "wrap_proj", "wrap_fwd", "wrap_bwd",
-           "wrap_bwd_reduce", "wrap_proj_bwd", "sinkhorn_fwd", "sinkhorn_bwd", "rmsnorm_fwd", "rmsnorm_bwd",
-           "aggregate_fwd", "aggregate_bwd")
+             "infer_bf16": InferBF16Workload, "wrapper": WrapperWorkload, "wrapper8": Wrapper8Workload,
+             "ops": OpsWorkload}
+KERNELS = ("layer_fwd", "layer_bwd", "layer_bwd_reduce", "proj", "proj_bwd", "proj_bwd_dphi", "wrap_proj",
+           "wrap_synth", "wrap_fwd", "wrap_bwd", "wrap_bwd_reduce", "wrap_proj_bwd", "sinkhorn_fwd", "sinkhorn_bwd",
+           "rmsnorm_fwd", "rmsnorm_bwd", "aggregate_fwd", "aggregate_bwd")
 
 
 # ---------------------------------------------------------------------------
@@ -799,6 +862,7 @@ def measure_workload(name, torch, mhc, _lib, device, steps, warmup, protocol_run
         for kname in KERNELS:
             timings[kname] = _lib.timing_query(kname)
         proj_ab = wl.projection_ab(_lib, kernel_steps) if wl.name == "dynamic" else None
+    unfused = wl.unfused_ab(steps) if hasattr(wl, "unfused_ab") else None
     kbytes = wl.kernel_bytes()
     kflops = wl.flops()
     kernels = {}
@@ -862,6 +926,8 @@ def measure_workload(name, torch, mhc, _lib, device, steps, warmup, protocol_run
     }
     if proj_ab is not None:
         rec["projection_ab"] = proj_ab
+    if unfused is not None:
+        rec["unfused_ab"] = unfused
     del wl
     torch.cuda.synchronize()
     torch.cuda.empty_cache()

@@ -300,10 +300,17 @@ int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dty
  * (dtype): streams X_0 = residual, X_1 = branch and, for i >= 2,
  * X_i = residual * 0.1^(i-1) rounded to dtype (MHC_WRAPPER_DECAY,
  * layer.py:306-308) or 0 (MHC_WRAPPER_ZERO); the mHC layer on X; the mean
- * over the n streams (layer.py:316) -> out [tokens, hidden] fp32.  X is never
- * materialised.  Parameters and `saved` are those of the layer entries
- * above.  Backward: grad_out [tokens, hidden] fp32 -> grad_residual,
- * grad_branch (dtype) and the layer's parameter gradients.
+ * over the n streams (layer.py:316) -> out [tokens, hidden] fp32.
+ * n = 2..8 and hidden % 4 == 0; with dynamic H also n * hidden % 32 == 0
+ * (others return MHC_ERR_UNSUPPORTED).  The row passes rebuild X from
+ * residual and branch in registers, so with static H, and with dynamic H at
+ * n = 4 and hidden % 32 == 0 (whose projection kernels rebuild it too), X
+ * never exists in memory.  For the other dynamic-H shapes the projection
+ * forward and backward read X from the workspace (a storage-dtype copy in
+ * the forward, fp32 in the backward, both sized by the queries below).
+ * Parameters and `saved` are those of the layer entries above.  Backward:
+ * grad_out [tokens, hidden] fp32 -> grad_residual, grad_branch (dtype) and
+ * the layer's parameter gradients.
  * Replaces MHCResidualWrapper.forward (layer.py:269-322) over
  * mhc_layer_fwd_dynamic / mhc_layer_bwd_dynamic (bindings.cpp:880-952,
  * 600-874) or the static layer chain. */

@@ -43,7 +43,7 @@ static bool valid_dtype(int dt) { return dt == kF32 || dt == kBF16; }
 // The layer runs its fixed-n kernels for n in {2, 4, 8, 16, 32} and the
 // generic kernels (generic.hip) for every other n up to kGenMaxN, as the
 // reference takes any n up to MAX_EXPANSION_RATE = 64 (mhc_types.h:68); the
-// fused wrapper is n = 4.
+// fused wrapper takes n = 2..8.
 static bool supported_layer_n(int n) {
     return n == 2 || n == 4 || n == 8 || n == 16 || n == 32 || generic_layer_n(n);
 }
@@ -1219,25 +1219,267 @@ int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dty
 }
 
 // ---- fused MHCResidualWrapper ------------------------------------------------
+// The n = 4 kernels of wrapper.hip: rows of whole 4-channel chunks that the
+// register-row kernels hold, 32-channel rows with dynamic H (the
+// projection's k step).  Every other accepted shape runs the run-time-n
+// kernels of wrapper_gen.hip.
+static bool wrap_fused4(int32_t n, int32_t hidden, bool dynamic) {
+    return n == 4 && hidden % 4 == 0 && (!dynamic || hidden % 32 == 0) && choose_row_tiling(hidden, 4, 6).vpt > 0;
+}
+
 static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidden, int32_t dtype, int32_t w_dtype,
                          int32_t mode, int32_t num_iters, bool dynamic) {
-    int st = check_layer_shape(fn, tokens, n, hidden, dtype, num_iters);
-    if (st) return st;
-    if (n != 4) return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper is compiled for n = 4");
+    if (tokens < 0) return fail(MHC_ERR_INVALID, std::string(fn) + ": tokens must be >= 0");
+    if (hidden < 1) return fail(MHC_ERR_INVALID, std::string(fn) + ": hidden must be >= 1");
+    if (num_iters < 0) return fail(MHC_ERR_INVALID, std::string(fn) + ": num_iters must be >= 0");
+    if (!valid_dtype(dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": dtype must be F32 or BF16");
+    // the reference writes stream 1 (layer.py:301), which needs n >= 2
+    if (n < 2) return fail(MHC_ERR_INVALID, std::string(fn) + ": n must be >= 2 (stream 1 holds the branch)");
+    if (n > kWgMaxN)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper takes n <= " + std::to_string(kWgMaxN));
     if (hidden % 4 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper needs hidden % 4 == 0");
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (mode != MHC_WRAPPER_DECAY && mode != MHC_WRAPPER_ZERO)
         return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");
-    if (dynamic && hidden % 32 != 0)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden must be a multiple of 32");
-    if (choose_row_tiling(hidden, 4, 6).vpt <= 0)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the row kernels");
+    if (!wrap_fused4(n, hidden, dynamic)) {
+        if (!wgen_supported(n, hidden))
+            return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the wrapper kernels");
+        if (dynamic && ((int64_t)n * hidden) % 32 != 0)
+            return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
+        if (dynamic && (int64_t)n * hidden > (int64_t(1) << 22))
+            return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden > 4194304 is not supported");
+    }
     return MHC_SUCCESS;
 }
 
 size_t mhc_wrapper_dynamic_saved_size(int64_t tokens, int32_t n, int32_t hidden) {
     return mhc_layer_dynamic_saved_size(tokens, n, hidden);
+}
+
+static bool wrap_res_grad_vanishes(int32_t num_iters, float sinkhorn_eps);
+
+// ---- run-time-n wrapper (wrapper_gen.hip) ---------------------------------------
+// The row passes rebuild the streams from r and b; with dynamic H the
+// layer's projection kernels (forward and backward) take the stream rows
+// X [tokens, n*C] from wgen_synth_kernel, and the backward folds their dX
+// over the streams.
+//
+// dynamic forward workspace: [X (4 bytes per element: the size query has no
+// dtype) | the layer projection's workspace (proj_fwd_ws)]
+struct WgenFwdWs {
+    ProjFwdWs p;
+    size_t p_base, total;
+};
+
+static WgenFwdWs wgen_fwd_ws(int64_t tokens, int32_t n, int32_t hidden) {
+    WgenFwdWs w{};
+    const int64_t K = (int64_t)n * hidden;
+    w.p = proj_fwd_ws(tokens, K, 2 * n + n * n);
+    w.p_base = align256((size_t)tokens * K * sizeof(float));
+    w.total = w.p_base + w.p.total;
+    return w;
+}
+
+// backward workspace: [per-token factors | dw partials | dw stage | ...]
+//   static:  [scalar rows per wave | their sum]
+//   dynamic: [per-token scalars | dP | s | coefficient partials | X (fp32) |
+//             dX (fp32) | dPhi partials | their stage]
+// With dynamic H the projection backward forms dX = dP . Phi (the s X term
+// joins in wgen_dx_kernel) over the rows of dP that do not vanish: the 2n
+// pre / post rows when wrap_res_grad_vanishes holds (as the n = 4 kernels),
+// else all 2n + n^2.
+struct WgenBwdWs {
+    int cblocks, ptiles, dtiles, srows;
+    size_t ep_off, dw_off, stw_off, scal_off, ssum_off, dp_off, s_off, cpart_off, x_off, dx_off, part_off, stp_off,
+        total;
+};
+
+static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dynamic) {
+    WgenBwdWs w{};
+    const int np = 2 * n + n * n;
+    const int ns = n * n + 2 * n;
+    const int64_t K = (int64_t)n * hidden;
+    size_t o = 0;
+    w.dtiles = tokens > 0 ? wgen_dx_tiles(tokens, hidden) : 1;
+    w.ep_off = o; o += align256((size_t)tokens * kWgEp * 4);
+    w.dw_off = o; o += align256((size_t)w.dtiles * hidden * 4);
+    w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
+    if (!dynamic) {
+        w.srows = tokens > 0 ? 4 * wgen_red_static_grid(tokens) : 1;
+        w.scal_off = o; o += align256((size_t)w.srows * ns * 4);
+        w.ssum_off = o; o += align256((size_t)ns * 4);
+        w.total = o;
+        return w;
+    }
+    w.cblocks = tokens > 0 ? dyn_coef_bwd_blocks(n, tokens) : 1;
+    w.ptiles = tokens > 0 ? proj_bwd_tiles(kF32, tokens, K) : 1;
+    w.scal_off = o; o += align256((size_t)tokens * (ns + 2) * 4);
+    w.dp_off = o; o += align256((size_t)tokens * dp_stride(np) * 4);
+    w.s_off = o; o += align256((size_t)tokens * 4);
+    w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
+    w.x_off = o; o += align256((size_t)tokens * K * 4);
+    w.dx_off = o; o += align256((size_t)tokens * K * 4);
+    // dPhi partials of the one-tile projection backward (up to 32 rows: all
+    // np rows, or the 2n pre / post rows); more rows go through
+    // launch_proj_bwd_small, which writes dPhi directly
+    const int rows1 = np <= kProjTile ? np : 2 * n;
+    w.part_off = o; o += align256((size_t)w.ptiles * rows1 * K * 4);
+    w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)rows1 * K) * 4);
+    w.total = o;
+    return w;
+}
+
+static int wgen_dynamic_fwd(const void* residual, const void* branch, int32_t dtype, bool decay, const void* weight,
+                            int32_t weight_dtype, const float* phi_pre, const float* phi_post, const float* phi_res,
+                            const float* alpha_pre, const float* alpha_post, const float* alpha_res,
+                            const float* b_pre, const float* b_post, const float* b_res, float* out, float* saved,
+                            void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
+                            int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, hipStream_t s) {
+    const DynSaved d = dyn_saved(tokens, n, hidden);
+    float* w32 = saved + d.w_off;
+    hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
+    if (e != hipSuccess || tokens == 0) return hip_status(e);
+    const WgenFwdWs w = wgen_fwd_ws(tokens, n, hidden);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "wrapper_dynamic_fwd: workspace smaller than mhc_wrapper_dynamic_fwd_workspace_size()");
+    const int64_t K = (int64_t)n * hidden;
+    const int np = 2 * n + n * n;
+    char* pw = (char*)workspace + w.p_base;
+    float* pp = (float*)(pw + w.p.p_off);
+    float* ss = (float*)(pw + w.p.ss_off);
+    e = launch_wgen_synth(dtype, dtype, n, decay, residual, branch, workspace, tokens, hidden, s);
+    if (e == hipSuccess) {
+        if (w.p.stream) {
+            e = launch_proj_stream(dtype, workspace, (bf16_raw_t*)(pw + w.p.xpl_off), phi_pre, phi_post, phi_res, n,
+                                   nullptr, np, pp, ss, tokens, K, w.p.ks, s);
+        } else {
+            bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
+            e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+            if (e == hipSuccess) e = launch_proj_mfma(dtype, workspace, phib, np, pp, ss, tokens, K, w.p.ks, s);
+        }
+    }
+    if (e == hipSuccess)
+        e = launch_dyn_coef_fwd(n, pp, ss, w.p.ks, tokens, K, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
+                                saved + d.coef_off, saved + d.p_off, saved + d.rh_off, num_iters, sinkhorn_eps,
+                                rmsnorm_eps, s);
+    if (e == hipSuccess)
+        e = launch_wgen_fwd(dtype, n, decay, residual, branch, w32, saved + d.coef_off, np, out, tokens, hidden,
+                            rmsnorm_eps, s);
+    return hip_status(e);
+}
+
+static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const void* branch, int32_t dtype,
+                            bool decay, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
+                            const float* phi_res, const float* alpha_pre, const float* alpha_post,
+                            const float* alpha_res, const float* b_res, const float* saved, void* grad_residual,
+                            void* grad_branch, void* grad_weight, float* grad_phi, float* grad_alpha, float* grad_b,
+                            void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
+                            int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, hipStream_t s) {
+    const WgenBwdWs w = wgen_bwd_ws(tokens, n, hidden, true);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "wrapper_dynamic_bwd: workspace smaller than mhc_wrapper_dynamic_bwd_workspace_size()");
+    char* ws = (char*)workspace;
+    float* ep = (float*)(ws + w.ep_off);
+    float* dw_part = (float*)(ws + w.dw_off);
+    float* stw = (float*)(ws + w.stw_off);
+    float* scal = (float*)(ws + w.scal_off);
+    float* dp = (float*)(ws + w.dp_off);
+    float* stok = (float*)(ws + w.s_off);
+    float* cpart = (float*)(ws + w.cpart_off);
+    float* X = (float*)(ws + w.x_off);
+    float* dX = (float*)(ws + w.dx_off);
+    float* part = (float*)(ws + w.part_off);
+    float* stp = (float*)(ws + w.stp_off);
+    const DynSaved d = dyn_saved(tokens, n, hidden);
+    const float* w32 = saved + d.w_off;
+    const int np = 2 * n + n * n;
+    const int64_t K = (int64_t)n * hidden;
+    // rows of dP the projection backward carries (the rest of dPhi: zeros)
+    const int rows = wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? 2 * n : np;
+    hipError_t e = hipSuccess;
+    int rows_w = w.dtiles, rows_c = w.cblocks;
+    if (tokens == 0) {
+        rows_w = rows_c = 1;
+        e = launch_fill_zero(dw_part, hidden, s);
+        if (e == hipSuccess) e = launch_fill_zero(cpart, np + 3, s);
+        if (e == hipSuccess) e = launch_fill_zero(grad_phi, (int64_t)rows * K, s);
+    } else {
+        e = launch_wgen_red(dtype, n, decay, false, grad_out, residual, branch, w32, saved + d.coef_off, np, scal, ep,
+                            tokens, hidden, rmsnorm_eps, s);
+        if (e == hipSuccess)
+            e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
+                                    alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
+                                    nullptr, s);
+        if (e == hipSuccess) e = launch_wgen_synth(dtype, kF32, n, decay, residual, branch, X, tokens, hidden, s);
+        if (e == hipSuccess) {
+            if (rows > kProjTile) {  // X and dX once for all output tiles
+                e = launch_proj_bwd_small(X, dp, dp_stride(np), nullptr, phi_pre, phi_post, phi_res, n, rows, dX,
+                                          false, grad_phi, tokens, K, s);
+            } else {
+                e = launch_proj_bwd(kF32, X, dp, dp_stride(np), nullptr, phi_pre, phi_post, phi_res, n, 0, rows, dX,
+                                    false, part, w.ptiles, tokens, K, s);
+                if (e == hipSuccess)
+                    e = launch_column_finalize(0, kF32, part, w.ptiles, (int64_t)rows * K, stp, grad_phi, nullptr, 0,
+                                               nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+            }
+        }
+        if (e == hipSuccess)
+            e = launch_wgen_dx(dtype, n, decay, grad_out, residual, branch, w32, ep, dX, stok, grad_residual,
+                               grad_branch, dw_part, w.dtiles, tokens, hidden, s);
+    }
+    if (e == hipSuccess)
+        e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr,
+                                   nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+    if (e == hipSuccess) e = launch_small_column_sum(cpart, rows_c, np + 3, grad_b, grad_alpha, np, s);
+    // the H_res rows of dPhi, db and dalpha: zeros, NaN where the alpha
+    // gradients (sums over the same tokens) are not finite, as the n = 4
+    // path writes them
+    if (e == hipSuccess && rows < np)
+        e = launch_fill_zero_carry(grad_phi + (int64_t)rows * K, (int64_t)(np - rows) * K, grad_b + rows, np - rows,
+                                   grad_alpha, 3, s);
+    if (e == hipSuccess && rows < np) e = launch_fill_zero_carry(grad_alpha + 2, 1, nullptr, 0, grad_alpha, 2, s);
+    return hip_status(e);
+}
+
+static int wgen_static_bwd(const float* grad_out, const void* residual, const void* branch, int32_t dtype, bool decay,
+                           int32_t weight_dtype, const float* h_pre, const float* h_post, const float* h_res,
+                           const float* saved, void* grad_residual, void* grad_branch, void* grad_weight,
+                           float* grad_h_pre, float* grad_h_post, float* grad_h_res, void* workspace,
+                           size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden, int32_t num_iters,
+                           float sinkhorn_eps, float rmsnorm_eps, hipStream_t s) {
+    const WgenBwdWs w = wgen_bwd_ws(tokens, n, hidden, false);
+    if (!workspace || workspace_bytes < w.total)
+        return fail(MHC_ERR_WORKSPACE, "wrapper_static_bwd: workspace smaller than mhc_wrapper_static_bwd_workspace_size()");
+    char* ws = (char*)workspace;
+    float* ep = (float*)(ws + w.ep_off);
+    float* dw_part = (float*)(ws + w.dw_off);
+    float* stw = (float*)(ws + w.stw_off);
+    float* scal = (float*)(ws + w.scal_off);
+    float* ssum = (float*)(ws + w.ssum_off);
+    const int ns = n * n + 2 * n;
+    const float* w32 = saved + saved_w_offset(n);
+    hipError_t e = hipSuccess;
+    int rows = w.dtiles;
+    if (tokens == 0) {
+        rows = 1;
+        e = launch_fill_zero(dw_part, hidden, s);
+        if (e == hipSuccess) e = launch_fill_zero(ssum, ns, s);
+    } else {
+        e = launch_wgen_red(dtype, n, decay, true, grad_out, residual, branch, w32, saved, 0, scal, ep, tokens, hidden,
+                            rmsnorm_eps, s);
+        if (e == hipSuccess) e = launch_small_column_sum(scal, w.srows, ns, ssum, ssum, ns, s);
+        if (e == hipSuccess)
+            e = launch_wgen_dx(dtype, n, decay, grad_out, residual, branch, w32, ep, nullptr, nullptr, grad_residual,
+                               grad_branch, dw_part, w.dtiles, tokens, hidden, s);
+    }
+    if (e == hipSuccess)
+        e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stw, grad_weight, ssum, 1, h_pre, h_post,
+                                   h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
+    // dH_res vanishes as in mhc_wrapper_static_bwd's n = 4 path
+    if (e == hipSuccess && wrap_res_grad_vanishes(num_iters, sinkhorn_eps))
+        e = launch_fill_zero_carry(grad_h_res, (int64_t)n * n, nullptr, 0, grad_h_pre, n, s);
+    return hip_status(e);
 }
 
 struct WrapFwdWs {
@@ -1258,6 +1500,7 @@ static WrapFwdWs wrap_fwd_ws(int64_t tokens, int32_t n, int32_t hidden) {
 
 size_t mhc_wrapper_dynamic_fwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden) {
     if (tokens < 0 || n < 1 || hidden < 1) return 0;
+    if (!wrap_fused4(n, hidden, true)) return wgen_fwd_ws(tokens, n, hidden).total;
     return wrap_fwd_ws(tokens, n, hidden).total;
 }
 
@@ -1276,6 +1519,11 @@ int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dt
                 "wrapper_dynamic_fwd: null parameter pointer");
     MHC_REQUIRE(tokens == 0 || (residual && branch && out), "wrapper_dynamic_fwd: null residual/branch/out");
     hipStream_t s = (hipStream_t)stream;
+    if (!wrap_fused4(n, hidden, true))
+        return wgen_dynamic_fwd(residual, branch, dtype, residual_mode == MHC_WRAPPER_DECAY, weight, weight_dtype,
+                                phi_pre, phi_post, phi_res, alpha_pre, alpha_post, alpha_res, b_pre, b_post, b_res,
+                                out, saved, workspace, workspace_bytes, tokens, n, hidden, num_iters, sinkhorn_eps,
+                                rmsnorm_eps, s);
     const DynSaved d = dyn_saved(tokens, n, hidden);
     float* w32 = saved + d.w_off;
     hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
@@ -1360,6 +1608,7 @@ static bool wrap_res_grad_vanishes(int32_t num_iters, float sinkhorn_eps) {
 size_t mhc_wrapper_dynamic_bwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
                                               int32_t residual_mode) {
     if (tokens < 0 || n < 1 || hidden < 1) return 0;
+    if (!wrap_fused4(n, hidden, true)) return wgen_bwd_ws(tokens, n, hidden, true).total;
     return wrap_bwd_ws(tokens, n, hidden, dtype, true, residual_mode == MHC_WRAPPER_DECAY).total;
 }
 
@@ -1379,10 +1628,15 @@ int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const v
     MHC_REQUIRE(tokens == 0 || (grad_out && residual && branch && grad_residual && grad_branch),
                 "wrapper_dynamic_bwd: null grad_out/residual/branch/grad pointer");
     const bool decay = residual_mode == MHC_WRAPPER_DECAY;
+    hipStream_t s = (hipStream_t)stream;
+    if (!wrap_fused4(n, hidden, true))
+        return wgen_dynamic_bwd(grad_out, residual, branch, dtype, decay, weight_dtype, phi_pre, phi_post, phi_res,
+                                alpha_pre, alpha_post, alpha_res, b_res, saved, grad_residual, grad_branch, grad_weight,
+                                grad_phi, grad_alpha, grad_b, workspace, workspace_bytes, tokens, n, hidden, num_iters,
+                                sinkhorn_eps, rmsnorm_eps, s);
     const WrapBwdWs w = wrap_bwd_ws(tokens, n, hidden, dtype, true, decay);
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "wrapper_dynamic_bwd: workspace smaller than mhc_wrapper_dynamic_bwd_workspace_size()");
-    hipStream_t s = (hipStream_t)stream;
     char* ws = (char*)workspace;
     float* dw_part = (float*)(ws + w.dw_off);
     float* scal = (float*)(ws + w.scal_off);
@@ -1447,6 +1701,9 @@ int mhc_wrapper_static_fwd(const void* residual, const void* branch, int32_t dty
     hipError_t e = launch_static_coef(n, h_pre, h_post, h_res, weight, weight_dtype, hidden, saved, num_iters,
                                       sinkhorn_eps, s);
     if (e != hipSuccess) return hip_status(e);
+    if (!wrap_fused4(n, hidden, false))
+        return hip_status(launch_wgen_fwd(dtype, n, residual_mode == MHC_WRAPPER_DECAY, residual, branch,
+                                          saved + saved_w_offset(n), saved, 0, out, tokens, hidden, rmsnorm_eps, s));
     return hip_status(launch_wrap_fwd(dtype, n, residual_mode == MHC_WRAPPER_DECAY, residual, branch,
                                       saved + saved_w_offset(n), saved, 0, out, tokens, hidden, rmsnorm_eps, s));
 }
@@ -1454,6 +1711,7 @@ int mhc_wrapper_static_fwd(const void* residual, const void* branch, int32_t dty
 size_t mhc_wrapper_static_bwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
                                              int32_t residual_mode) {
     if (tokens < 0 || n < 1 || hidden < 1) return 0;
+    if (!wrap_fused4(n, hidden, false)) return wgen_bwd_ws(tokens, n, hidden, false).total;
     return wrap_bwd_ws(tokens, n, hidden, dtype, false, residual_mode == MHC_WRAPPER_DECAY).total;
 }
 
@@ -1471,10 +1729,14 @@ int mhc_wrapper_static_bwd(const float* grad_out, const void* residual, const vo
     MHC_REQUIRE(tokens == 0 || (grad_out && residual && branch && grad_residual && grad_branch),
                 "wrapper_static_bwd: null grad_out/residual/branch/grad pointer");
     const bool decay = residual_mode == MHC_WRAPPER_DECAY;
+    hipStream_t s = (hipStream_t)stream;
+    if (!wrap_fused4(n, hidden, false))
+        return wgen_static_bwd(grad_out, residual, branch, dtype, decay, weight_dtype, h_pre, h_post, h_res, saved,
+                               grad_residual, grad_branch, grad_weight, grad_h_pre, grad_h_post, grad_h_res, workspace,
+                               workspace_bytes, tokens, n, hidden, num_iters, sinkhorn_eps, rmsnorm_eps, s);
     const WrapBwdWs w = wrap_bwd_ws(tokens, n, hidden, dtype, false, decay);
     if (!workspace || workspace_bytes < w.total)
         return fail(MHC_ERR_WORKSPACE, "wrapper_static_bwd: workspace smaller than mhc_wrapper_static_bwd_workspace_size()");
-    hipStream_t s = (hipStream_t)stream;
     float* dw_part = (float*)((char*)workspace + w.dw_off);
     float* scal_part = (float*)((char*)workspace + w.scal_off);
     float* stage = (float*)((char*)workspace + w.stw_off);

@@ -33,7 +33,7 @@ AUTOGRAD_NAME = "_mhc_autograd"
 AUTOGRAD_PATH = os.path.join(PKG, AUTOGRAD_NAME + ".so")
 
 SOURCES = ["abi.hip", "compat.hip", "dynamic.hip", "generic.hip", "layer.hip", "ops.hip", "sinkhorn.hip", "wide.hip",
-           "wrapper.hip"]
+           "wrapper.hip", "wrapper_gen.hip"]
 
 ARCH = os.environ.get("MHC_OFFLOAD_ARCH", "gfx950")
 

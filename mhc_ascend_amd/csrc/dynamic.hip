@@ -2656,15 +2656,14 @@ static WideScratch wide_scratch(int np, int64_t B, int64_t K) {
 
 size_t proj_bwd_wide_scratch_bytes(int np, int64_t B, int64_t K) { return wide_scratch(np, B, K).total; }
 
-hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, const float* s_tok,
-                                const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
-                                float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
-                                hipStream_t s) {
+hipError_t launch_proj_bwd_small(const float* x, const float* dP, int dp_stride, const float* s_tok,
+                                 const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
+                                 float* dx, bool accumulate, float* dphi, int64_t B, int64_t K, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (np <= kProjTile || B > kProjWideMaxB || K % 32 != 0) return hipErrorInvalidValue;
+    if (np <= kProjTile || np > kStreamOB || K % 32 != 0) return hipErrorInvalidValue;
     if (s_tok && !accumulate) return hipErrorInvalidValue;
     const unsigned cblocks = (unsigned)((K + 127) / 128);
-    if (np <= kStreamOB) {
+    {
         // 1-D grid: 8 XCD lanes x ceil(column blocks / 8) x 32-token blocks
         const unsigned tb32 = (unsigned)((B + 31) / 32);
         const dim3 gs(8u * ((cblocks + 7) / 8) * tb32);
@@ -2689,6 +2688,19 @@ hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, 
         timing_end(tg, s);
         return hipGetLastError();
     }
+}
+
+hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, const float* s_tok,
+                                const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
+                                float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
+                                hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (np <= kProjTile || B > kProjWideMaxB || K % 32 != 0) return hipErrorInvalidValue;
+    if (s_tok && !accumulate) return hipErrorInvalidValue;
+    if (np <= kStreamOB)
+        return launch_proj_bwd_small(x, dP, dp_stride, s_tok, phi_pre, phi_post, phi_res, n_pre, np, dx, accumulate,
+                                     dphi, B, K, s);
+    const unsigned cblocks = (unsigned)((K + 127) / 128);
     if (!scratch) return hipErrorInvalidValue;
     const int np32 = proj_tiles(np) * kProjTile;
     const int64_t Bp = (B + 31) / 32 * 32;

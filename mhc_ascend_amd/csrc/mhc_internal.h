@@ -338,6 +338,12 @@ int proj_bwd_tiles(int x_dtype, int64_t B, int64_t K);
 // and x^T as bf16 hi / lo planes (proj_bwd_wide_scratch_bytes).
 bool proj_bwd_wide_path(int x_dtype, int np, int64_t B);
 size_t proj_bwd_wide_scratch_bytes(int np, int64_t B, int64_t K);
+// 32 < np <= 128 at any batch: dx over all output tiles in one pass (one
+// workgroup per 128 columns x 32 tokens) and dPhi written directly (one
+// workgroup per 64 rows x 128 columns walking all tokens); fp32 x and dx.
+hipError_t launch_proj_bwd_small(const float* x, const float* dP, int dp_stride, const float* s_tok,
+                                 const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
+                                 float* dx, bool accumulate, float* dphi, int64_t B, int64_t K, hipStream_t s);
 hipError_t launch_proj_bwd_wide(const float* x, const float* dP, int dp_stride, const float* s_tok,
                                 const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                                 float* dx, bool accumulate, float* dphi, void* scratch, int64_t B, int64_t K,
@@ -390,6 +396,35 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
                                 const float* phi_pre, const float* phi_post, const float* phi_res, void* dres,
                                 void* dbr, float* dw_part, float* dphi_part, int tiles, int64_t B, int64_t C,
                                 bool res_rows, hipStream_t s);
+
+// ---- wrapper_gen.hip -------------------------------------------------------
+// MHCResidualWrapper for n = 2..8 with n at run time (the shapes the n = 4
+// kernels above do not take); hidden % 4 == 0.
+constexpr int kWgMaxN = 8;
+// Floats per token of the per-token factors of d r / d b.
+constexpr int kWgEp = 16;
+bool wgen_supported(int n, int64_t C);
+hipError_t launch_wgen_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
+                           const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
+                           hipStream_t s);
+// Waves of the static-H row sums (rows of its scal_out) are 4 x this grid.
+int wgen_red_static_grid(int64_t B);
+// Row sums of the backward: stat = false: scal_out[B][n*n+2n+2] per token;
+// stat = true: scal_out[4 * wgen_red_static_grid(B)][n*n+2n] per wave.
+// Both: ep_out[B][kWgEp].
+hipError_t launch_wgen_red(int dt, int n, bool decay, bool stat, const float* g, const void* res, const void* br,
+                           const float* w, const float* coef, int64_t coef_stride, float* scal_out, float* ep_out,
+                           int64_t B, int64_t C, float eps, hipStream_t s);
+int wgen_dx_tiles(int64_t B, int64_t C);
+// d r / d b and dw_part[tiles][C]; dX (fp32 [B][n*C] = dP . Phi per stream)
+// and s_tok (the r_h term's s per token) with dynamic H, both null with
+// static H.
+hipError_t launch_wgen_dx(int dt, int n, bool decay, const float* g, const void* res, const void* br,
+                          const float* w, const float* ep, const float* dX, const float* s_tok, void* dres, void* dbr,
+                          float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s);
+// X[B][n*C] in out_dt (kF32, or the storage dtype dt).
+hipError_t launch_wgen_synth(int dt, int out_dt, int n, bool decay, const void* res, const void* br, void* X,
+                             int64_t B, int64_t C, hipStream_t s);
 
 // ---- compat.hip ------------------------------------------------------------
 // The reference-shaped dynamic-H entries (mhc_layer_fwd_dynamic /

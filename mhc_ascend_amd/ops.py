@@ -227,11 +227,11 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
     parameters of ``layer`` (an MHCLayer); returns fp32 [tokens, C]."""
     n = layer.expansion_rate
     C = residual.shape[-1]
-    # The fused wrapper kernels take n = 4 and 4-channel rows (32-channel
-    # with dynamic H, the projection's k step) up to 16384 channels.  Other
-    # shapes build the n streams with device tensor ops, as layer.py:299-310
-    # does, and run the layer on them (layer.py:313-316).
-    fused = n == 4 and C % 4 == 0 and C <= 16384 and (not layer.use_dynamic_h or C % 32 == 0)
+    # The fused wrapper kernels take n = 2..8 and 4-channel rows (with
+    # dynamic H, n*C a multiple of the projection's k step of 32, up to 2^22).
+    # Other shapes build the n streams with device tensor ops, as
+    # layer.py:299-310 does, and run the layer on them (layer.py:313-316).
+    fused = 2 <= n <= 8 and C % 4 == 0 and (not layer.use_dynamic_h or ((n * C) % 32 == 0 and n * C <= 1 << 22))
     if not fused:
         if n < 2:
             raise RuntimeError("mhc_residual_wrapper: expansion_rate must be >= 2 (stream 1 holds the branch)")

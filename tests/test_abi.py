@@ -109,8 +109,13 @@ def test_expansion_rate_support_on_host():
     rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, 1, 1, 1 << 30, 8, 8, 64, 20, 1e-8,
                                    1e-5, None)
     assert rc == -1 and b"null x/out" in lib.mhc_last_error()
-    rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 2, 256, 20, 1e-8, 1e-5, None)
-    assert rc == -2 and b"fused wrapper is compiled for n = 4" in lib.mhc_last_error()
+    rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 16, 256, 20, 1e-8, 1e-5, None)
+    assert rc == -2 and b"the fused wrapper takes n <= 8" in lib.mhc_last_error()
+    rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 1, 256, 20, 1e-8, 1e-5, None)
+    assert rc == -1 and b"n must be >= 2" in lib.mhc_last_error()
+    # n = 2 passes the shape checks; a null out then fails before any launch
+    rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, None, 1, 8, 2, 256, 20, 1e-8, 1e-5, None)
+    assert rc == -1 and b"null residual/branch/out" in lib.mhc_last_error()
 
 
 def test_cpu_tensors_raise_no_fallback():

@@ -36,11 +36,12 @@ def test_layer_deterministic(device, dynamic, dtype):
     _twice(lambda: _module_run(layer, [x], go))
 
 
+@pytest.mark.parametrize("n", [4, 8])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_wrapper_deterministic(device, dynamic, dtype):
+def test_wrapper_deterministic(device, n, dynamic, dtype):
     torch.manual_seed(2)
-    wrap = mhc.MHCResidualWrapper(1024, 4, use_dynamic_h=dynamic).to(device)
+    wrap = mhc.MHCResidualWrapper(1024, n, use_dynamic_h=dynamic).to(device)
     r = torch.randn(2500, 1024, device=device).to(dtype)
     b = torch.randn(2500, 1024, device=device).to(dtype)
     go = torch.randn(2500, 1024, device=device)

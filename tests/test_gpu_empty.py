@@ -1,6 +1,6 @@
 """Zero-token inputs through the public API on the GPU: the standalone
 operators (forward and backward), MHCLayer with static and dynamic H and
-MHCResidualWrapper (fp32 and bf16, both residual modes) return empty outputs
+MHCResidualWrapper (n = 4 and 6, fp32 and bf16, both residual modes) return empty outputs
 of the right shape, and every parameter gradient is zero (a sum over no
 tokens), as torch's own ops give on the reference's PyTorch path
 (ops_pytorch_backward.py, layer.py:94-179, 269-322 applied to empty
@@ -65,12 +65,13 @@ def test_layer_on_empty_batch(device, dynamic, dtype):
     _zero_grads(layer)
 
 
+@pytest.mark.parametrize("n", [4, 6])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
 @pytest.mark.parametrize("shape", [(0, 64), (0, 3, 64)])
-def test_wrapper_on_empty_batch(device, dynamic, dtype, mode, shape):
-    wrap = mhc.MHCResidualWrapper(64, 4, residual_mode=mode, use_dynamic_h=dynamic).to(device)
+def test_wrapper_on_empty_batch(device, n, dynamic, dtype, mode, shape):
+    wrap = mhc.MHCResidualWrapper(64, n, residual_mode=mode, use_dynamic_h=dynamic).to(device)
     r = torch.randn(*shape, device=device).to(dtype).requires_grad_(True)
     b = torch.randn(*shape, device=device).to(dtype).requires_grad_(True)
     out = wrap(r, b)

@@ -35,11 +35,12 @@ def test_layer_transposed_input(device, dynamic, dtype):
     _same(_run(layer, [view], go), _run(layer, [view.contiguous()], go), "layer")
 
 
+@pytest.mark.parametrize("n", [4, 3])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_wrapper_strided_inputs(device, dynamic, dtype):
+def test_wrapper_strided_inputs(device, n, dynamic, dtype):
     torch.manual_seed(2)
-    wrap = mhc.MHCResidualWrapper(256, 4, use_dynamic_h=dynamic).to(device)
+    wrap = mhc.MHCResidualWrapper(256, n, use_dynamic_h=dynamic).to(device)
     big = torch.randn(40, 512, device=device).to(dtype)
     r = big[:, ::2]                      # every other channel
     b = torch.randn(256, 40, device=device).to(dtype).t()  # transposed

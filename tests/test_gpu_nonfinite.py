@@ -62,12 +62,13 @@ def test_layer_nonfinite_token(device, dynamic, value):
     assert torch.isfinite(out[keep]).all() and torch.isfinite(xd.grad[keep]).all()
 
 
+@pytest.mark.parametrize("n", [4, 5])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("value", [float("nan"), float("inf")])
-def test_wrapper_nonfinite_token(device, dynamic, dtype, value):
+def test_wrapper_nonfinite_token(device, n, dynamic, dtype, value):
     torch.manual_seed(4)
-    wrap = mhc.MHCResidualWrapper(64, 4, use_dynamic_h=dynamic)
+    wrap = mhc.MHCResidualWrapper(64, n, use_dynamic_h=dynamic)
     g = torch.Generator().manual_seed(8)
     res = _plant(torch.randn(6, 64, generator=g), value, (4, 17)).to(dtype)
     br = torch.randn(6, 64, generator=g).to(dtype)
@@ -82,7 +83,7 @@ def test_wrapper_nonfinite_token(device, dynamic, dtype, value):
         fn = lambda X: R.mhc_layer_dynamic(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
     else:
         fn = lambda X: R.mhc_layer_static(X, w, *ps, 20, 1e-8, 1e-5, dtype=torch.float64)
-    ref = R.mhc_residual_wrapper(r, b, fn, 4, "decay", storage_dtype=dtype)
+    ref = R.mhc_residual_wrapper(r, b, fn, n, "decay", storage_dtype=dtype)
     ref.backward(go.double())
     wrap = wrap.to(device)
     rd = res.to(device).requires_grad_(True)

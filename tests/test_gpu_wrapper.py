@@ -26,9 +26,9 @@ def _gen(seed):
     return torch.Generator().manual_seed(seed)
 
 
-def _make(C, dynamic, seed, alpha=0.3, phi_std=0.05):
+def _make(C, dynamic, seed, alpha=0.3, phi_std=0.05, n=4):
     torch.manual_seed(seed)
-    wrap = mhc.MHCResidualWrapper(C, 4, use_dynamic_h=dynamic)
+    wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=dynamic)
     layer = wrap.mhc
     g = _gen(seed + 1)
     with torch.no_grad():
@@ -61,7 +61,7 @@ def _oracle(wrap, res, br, grad, mode):
         fn = lambda X: R.mhc_layer_dynamic(X, w, *ps, it, eps, 1e-5, dtype=torch.float64)
     else:
         fn = lambda X: R.mhc_layer_static(X, w, *ps, it, eps, 1e-5, dtype=torch.float64)
-    out = R.mhc_residual_wrapper(r, b, fn, 4, mode, storage_dtype=res.dtype)
+    out = R.mhc_residual_wrapper(r, b, fn, layer.expansion_rate, mode, storage_dtype=res.dtype)
     out.backward(grad.double())
     return out.detach(), r.grad, b.grad, w.grad, [p.grad for p in ps]
 
@@ -145,9 +145,9 @@ def test_wrapper_config_c5_width(device, dynamic):
                                          (6, True, 128), (3, True, 96)])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
 def test_wrapper_general_n(device, n, dynamic, C, mode):
-    """Shapes the fused wrapper kernels do not take (n != 4, or rows that
-    are not a multiple of 4): the streams are built with device tensor ops
-    and run through the layer."""
+    """Other expansion rates on fp32 rows: n = 2..8 run the run-time-n
+    wrapper kernels; n = 32 and rows that are not a multiple of 4 build the
+    streams with device tensor ops and run them through the layer."""
     torch.manual_seed(n)
     wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=dynamic)
     wrap.residual_mode = mode
@@ -210,9 +210,10 @@ def test_wrapper_eval_no_grad_matches_training_forward(device):
     assert torch.equal(out_t, out_e)
 
 
+@pytest.mark.parametrize("n", [4, 3, 8])
 @pytest.mark.parametrize("dynamic", [True, False])
 @pytest.mark.parametrize("iters,eps", [(0, 1e-8), (1, 1e-8), (1, 0.1), (20, 0.1)])
-def test_wrapper_sinkhorn_settings(device, dynamic, iters, eps):
+def test_wrapper_sinkhorn_settings(device, n, dynamic, iters, eps):
     """Both sides of the rule that writes the H_res gradients as zeros.
     num_iters >= 1 with eps <= 1e-6: the last column normalisation removes
     the column-constant dM (zeros written, checked against the oracle's
@@ -221,10 +222,11 @@ def test_wrapper_sinkhorn_settings(device, dynamic, iters, eps):
     the H_res gradients are checked against the oracle's (with one
     iteration or none they are of the order of the other gradients; after
     20 iterations at eps = 0.1 about 1e-12 of them, measured on the
-    oracle)."""
+    oracle).  n = 3 and 8 run the run-time-n kernels (at n = 8 with all 80
+    projection rows: the small-np projection backward)."""
     C, B = 256, 37
-    seed = 900 + iters + int(eps * 100) + (7 if dynamic else 0)
-    wrap = _make(C, dynamic, seed)
+    seed = 900 + iters + int(eps * 100) + (7 if dynamic else 0) + 10 * n
+    wrap = _make(C, dynamic, seed, n=n)
     wrap.mhc.num_sinkhorn_iters = iters
     wrap.mhc.sinkhorn_eps = eps
     g = _gen(seed + 2)
@@ -235,9 +237,32 @@ def test_wrapper_sinkhorn_settings(device, dynamic, iters, eps):
     got = _run(wrap, res, br, grad, device)
     vanish = iters >= 1 and eps <= 1e-6
     names = DYN if dynamic else STA
-    _check(got, want, torch.bfloat16, names, f"dyn={dynamic} iters={iters} eps={eps}", res_vanish=vanish)
+    _check(got, want, torch.bfloat16, names, f"n={n} dyn={dynamic} iters={iters} eps={eps}", res_vanish=vanish)
     if not vanish and iters <= 1:
         # the oracle's H_res gradients are not negligible here
         fam = max(float(e.abs().max()) for nm, e in zip(names, want[4]) if nm.endswith("pre"))
         res_ref = max(float(e.abs().max()) for nm, e in zip(names, want[4]) if nm.endswith("res"))
         assert res_ref > 1e-4 * fam, (res_ref, fam)
+
+
+@pytest.mark.parametrize("n,dynamic,C", [(2, False, 256), (3, False, 96), (5, False, 160), (8, False, 256),
+                                         (2, True, 256), (3, True, 96), (5, True, 96), (6, True, 256),
+                                         (7, True, 96), (8, True, 256), (4, True, 264), (4, False, 17000)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["decay", "zero"])
+def test_wrapper_runtime_n_matches_oracle(device, n, dynamic, C, dtype, mode):
+    """The run-time-n wrapper kernels (n = 2..8; n = 4 rows the n = 4 kernels
+    refuse: 264 channels with dynamic H, 17000 with static H) against the
+    float64 oracle, every output and gradient, both storage dtypes and both
+    residual modes."""
+    seed = 1000 + 10 * n + (7 if dynamic else 0) + (3 if mode == "zero" else 0)
+    wrap = _make(C, dynamic, seed, n=n)
+    wrap.residual_mode = mode
+    g = _gen(seed + 2)
+    shape = (2, 3, C) if C > 1024 else (37, C)
+    res = torch.randn(*shape, generator=g).to(dtype)
+    br = torch.randn(*shape, generator=g).to(dtype)
+    grad = torch.randn(*shape, generator=g)
+    want = _oracle(wrap, res, br, grad, mode)
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, dtype, DYN if dynamic else STA, f"n={n} C={C} dyn={dynamic} {dtype} {mode}")
