@@ -458,11 +458,12 @@ class Wrapper8Workload(WrapperWorkload):
         return 20 * self.F + 3 * self.phi_bytes()
 
     def kernel_bytes(self):
-        F, n = self.F, self.n
+        F = self.F
         # wrap_fwd reads r, b (bf16) and writes the fp32 mean; the backward's
-        # row sums read g and r, b; wrap_proj_bwd (d r, d b) reads g, r, b and
-        # the fp32 dX of the n streams and writes d r, d b
-        return {"wrap_fwd": 8 * F, "wrap_bwd_reduce": 8 * F, "wrap_proj_bwd": (12 + 4 * n) * F}
+        # row sums read g and r, b; wrap_proj_bwd (d r, d b with dP . Phi
+        # folded in) reads g, r, b and writes d r, d b; proj_bwd_dphi (dPhi of
+        # the pre / post rows from the rebuilt streams) reads r, b
+        return {"wrap_fwd": 8 * F, "wrap_bwd_reduce": 8 * F, "wrap_proj_bwd": 12 * F, "proj_bwd_dphi": 4 * F}
 
     def flops(self):
         return {}

@@ -1283,14 +1283,17 @@ static WgenFwdWs wgen_fwd_ws(int64_t tokens, int32_t n, int32_t hidden) {
 
 // backward workspace: [per-token factors | dw partials | dw stage | ...]
 //   static:  [scalar rows per wave | their sum]
-//   dynamic: [per-token scalars | dP | s | coefficient partials | X (fp32) |
-//             dX (fp32) | dPhi partials | their stage]
-// With dynamic H the projection backward forms dX = dP . Phi (the s X term
-// joins in wgen_dx_kernel) over the rows of dP that do not vanish: the 2n
-// pre / post rows when wrap_res_grad_vanishes holds (as the n = 4 kernels),
-// else all 2n + n^2.
+//   dynamic: [per-token scalars | dP | s | coefficient partials | dPhi
+//             partials | their stage | X (fp32) | dX (fp32)]
+// With dynamic H and wrap_res_grad_vanishes (the default Sinkhorn settings)
+// only the 2n pre / post rows of dP are carried, as by the n = 4 kernels:
+// wgen_dphi_kernel forms their dPhi from r and b and wgen_dx_fold_kernel
+// folds dP . Phi into d r / d b, so the stream rows never exist in memory.
+// Otherwise (all 2n + n^2 rows) the layer's projection backward runs on the
+// stream rows X and writes dX = dP . Phi, which wgen_dx_kernel folds; the
+// size query has no Sinkhorn settings, so X and dX are always reserved.
 struct WgenBwdWs {
-    int cblocks, ptiles, dtiles, srows;
+    int cblocks, ptiles, dtiles, qtiles, ftiles, srows;
     size_t ep_off, dw_off, stw_off, scal_off, ssum_off, dp_off, s_off, cpart_off, x_off, dx_off, part_off, stp_off,
         total;
 };
@@ -1302,8 +1305,10 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
     const int64_t K = (int64_t)n * hidden;
     size_t o = 0;
     w.dtiles = tokens > 0 ? wgen_dx_tiles(tokens, hidden) : 1;
+    w.ftiles = tokens > 0 ? wgen_fold_tiles(tokens, hidden) : 1;
+    const int dw_rows = dynamic && w.ftiles > w.dtiles ? w.ftiles : w.dtiles;
     w.ep_off = o; o += align256((size_t)tokens * kWgEp * 4);
-    w.dw_off = o; o += align256((size_t)w.dtiles * hidden * 4);
+    w.dw_off = o; o += align256((size_t)dw_rows * hidden * 4);
     w.stw_off = o; o += align256(column_sums_stage_floats(hidden) * 4);
     if (!dynamic) {
         w.srows = tokens > 0 ? 4 * wgen_red_static_grid(tokens) : 1;
@@ -1318,14 +1323,17 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
     w.dp_off = o; o += align256((size_t)tokens * dp_stride(np) * 4);
     w.s_off = o; o += align256((size_t)tokens * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
+    // dPhi partials: the 2n pre / post rows per wgen_dphi_kernel tile, or
+    // the one-tile projection backward's (all np rows when np <= 32; more
+    // rows go through launch_proj_bwd_small, which writes dPhi directly)
+    w.qtiles = tokens > 0 ? wgen_dphi_tiles(tokens, hidden) : 1;
+    size_t part = (size_t)w.qtiles * 2 * n;
+    if (np <= kProjTile && (size_t)w.ptiles * np > part) part = (size_t)w.ptiles * np;
+    const int64_t srows = np <= kProjTile ? np : 2 * n;
+    w.part_off = o; o += align256(part * K * 4);
+    w.stp_off = o; o += align256(column_sums_stage_floats(srows * K) * 4);
     w.x_off = o; o += align256((size_t)tokens * K * 4);
     w.dx_off = o; o += align256((size_t)tokens * K * 4);
-    // dPhi partials of the one-tile projection backward (up to 32 rows: all
-    // np rows, or the 2n pre / post rows); more rows go through
-    // launch_proj_bwd_small, which writes dPhi directly
-    const int rows1 = np <= kProjTile ? np : 2 * n;
-    w.part_off = o; o += align256((size_t)w.ptiles * rows1 * K * 4);
-    w.stp_off = o; o += align256(column_sums_stage_floats((int64_t)rows1 * K) * 4);
     w.total = o;
     return w;
 }
@@ -1353,6 +1361,12 @@ static int wgen_dynamic_fwd(const void* residual, const void* branch, int32_t dt
         if (w.p.stream) {
             e = launch_proj_stream(dtype, workspace, (bf16_raw_t*)(pw + w.p.xpl_off), phi_pre, phi_post, phi_res, n,
                                    nullptr, np, pp, ss, tokens, K, w.p.ks, s);
+        } else if (dtype == kBF16 && np > kProjTile) {
+            bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
+            e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+            if (e == hipSuccess)
+                e = launch_proj_stream(dtype, workspace, nullptr, phi_pre, phi_post, phi_res, n, phib, np, pp, ss,
+                                       tokens, K, w.p.ks, s);
         } else {
             bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
             e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
@@ -1397,8 +1411,9 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
     const int64_t K = (int64_t)n * hidden;
     // rows of dP the projection backward carries (the rest of dPhi: zeros)
     const int rows = wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? 2 * n : np;
+    const bool fold = rows < np;
     hipError_t e = hipSuccess;
-    int rows_w = w.dtiles, rows_c = w.cblocks;
+    int rows_w = fold ? w.ftiles : w.dtiles, rows_c = w.cblocks;
     if (tokens == 0) {
         rows_w = rows_c = 1;
         e = launch_fill_zero(dw_part, hidden, s);
@@ -1411,8 +1426,20 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
                                     nullptr, s);
-        if (e == hipSuccess) e = launch_wgen_synth(dtype, kF32, n, decay, residual, branch, X, tokens, hidden, s);
-        if (e == hipSuccess) {
+        if (fold) {
+            if (e == hipSuccess)
+                e = launch_wgen_dphi(dtype, n, decay, residual, branch, dp, dp_stride(np), rows, part, w.qtiles, tokens,
+                                     hidden, s);
+            if (e == hipSuccess)
+                e = launch_column_finalize(0, kF32, part, w.qtiles, (int64_t)rows * K, stp, grad_phi, nullptr, 0,
+                                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
+            if (e == hipSuccess)
+                e = launch_wgen_dx_fold(dtype, n, decay, grad_out, residual, branch, w32, ep, dp, dp_stride(np), rows,
+                                        stok, phi_pre, phi_post, grad_residual, grad_branch, dw_part, w.ftiles,
+                                        tokens, hidden, s);
+        }
+        if (!fold && e == hipSuccess) e = launch_wgen_synth(dtype, kF32, n, decay, residual, branch, X, tokens, hidden, s);
+        if (!fold && e == hipSuccess) {
             if (rows > kProjTile) {  // X and dX once for all output tiles
                 e = launch_proj_bwd_small(X, dp, dp_stride(np), nullptr, phi_pre, phi_post, phi_res, n, rows, dX,
                                           false, grad_phi, tokens, K, s);
@@ -1424,7 +1451,7 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
                                                nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
             }
         }
-        if (e == hipSuccess)
+        if (!fold && e == hipSuccess)
             e = launch_wgen_dx(dtype, n, decay, grad_out, residual, branch, w32, ep, dX, stok, grad_residual,
                                grad_branch, dw_part, w.dtiles, tokens, hidden, s);
     }

@@ -422,6 +422,19 @@ int wgen_dx_tiles(int64_t B, int64_t C);
 hipError_t launch_wgen_dx(int dt, int n, bool decay, const float* g, const void* res, const void* br,
                           const float* w, const float* ep, const float* dX, const float* s_tok, void* dres, void* dbr,
                           float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s);
+// The projection backward over the pre / post rows (rows = 2n) without the
+// stream rows: dPhi partials dphi_part[tiles][rows][n*C] (tiles from
+// wgen_dphi_tiles), and d r / d b with dP . Phi folded over the streams
+// (dw_part[tiles][C], tiles from wgen_fold_tiles).
+int wgen_dphi_tiles(int64_t B, int64_t C);
+hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
+                            int dp_stride, int rows, float* dphi_part, int tiles, int64_t B, int64_t C,
+                            hipStream_t s);
+int wgen_fold_tiles(int64_t B, int64_t C);
+hipError_t launch_wgen_dx_fold(int dt, int n, bool decay, const float* g, const void* res, const void* br,
+                               const float* w, const float* ep, const float* dP, int dp_stride, int rows,
+                               const float* s_tok, const float* phi_pre, const float* phi_post, void* dres,
+                               void* dbr, float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s);
 // X[B][n*C] in out_dt (kF32, or the storage dtype dt).
 hipError_t launch_wgen_synth(int dt, int out_dt, int n, bool decay, const void* res, const void* br, void* X,
                              int64_t B, int64_t C, hipStream_t s);

@@ -24,11 +24,17 @@
 //                      factors of d r / d b
 //   wgen_dx_kernel     d r, d b (rounded once) and the dw partials:
 //                      workgroups of 1024 channels x one token tile; with
-//                      dynamic H it adds the projection backward's dX folded
-//                      over the streams
+//                      dynamic H it adds the layer projection backward's dX
+//                      folded over the streams (Sinkhorn settings where the
+//                      H_res rows of dP do not vanish)
+//   wgen_dphi_kernel   dynamic H, H_res rows of dP vanishing: dPhi of the
+//                      2n pre / post rows from the rebuilt streams
+//   wgen_dx_fold_kernel  the same case: d r, d b with dP . Phi folded over
+//                      the streams, and the dw partials
 //   wgen_synth_kernel  the stream rows [tokens, n*C] as the operand of the
-//                      layer's projection kernels (dynamic H only: the
-//                      forward's in the storage dtype, the backward's fp32)
+//                      layer's projection kernels (dynamic H: the forward's
+//                      in the storage dtype; the backward's in fp32 when the
+//                      H_res rows do not vanish)
 #include "mhc_device.h"
 #include "mhc_internal.h"
 
@@ -394,6 +400,210 @@ __global__ __launch_bounds__(256) void wgen_dx_kernel(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// The projection backward over the pre / post rows of dP (the H_res rows
+// vanish: every stream receives G / n through the stream mean), without
+// the stream rows in memory.
+//   dphi_part[tile][o][j*C + c] = sum over the tile's tokens of
+//                                 dP[t][o] X_j[t][c],  o < rows = 2n
+// Workgroup = 4 waves x 128 channels (two per lane) x one token tile; wave
+// q takes streams q and q + 4 (a wave-uniform choice) and keeps rows x 2 x 2
+// sums per lane; dP of a token is a wave-uniform record (scalar loads).
+// ---------------------------------------------------------------------------
+constexpr int kWgRows = 2 * kWgMaxN;  // pre / post rows of dP at most
+constexpr int kWgTokU = 4;            // tokens per step of the token loops
+
+namespace {
+// two consecutive elements (4- or 8-byte aligned) as one load
+template <typename TX>
+__device__ __forceinline__ void wg_load2(const TX* p, float (&v)[2]) {
+    if constexpr (sizeof(TX) == 2) {
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+        v[0] = __uint_as_float(w << 16);
+        v[1] = __uint_as_float(w & 0xffff0000u);
+    } else {
+        const float2 f = *reinterpret_cast<const float2*>(p);
+        v[0] = f.x;
+        v[1] = f.y;
+    }
+}
+
+// stream j with j known only at run time (wave-uniform)
+template <typename TX, bool DECAY>
+__device__ __forceinline__ float wg_stream_rt(int j, float r, float b) {
+    float m = 0.f;
+#pragma unroll
+    for (int q = 2; q < kWgMaxN; ++q) m = (j == q) ? kWgMult[q] : m;
+    return j == 0 ? r : (j == 1 ? b : (DECAY ? wg_round<TX>(r * m) : 0.f));
+}
+}  // namespace
+
+template <typename TX, bool DECAY>
+__global__ __launch_bounds__(256) void wgen_dphi_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
+                                                        const float* __restrict__ dP, int dp_stride, int rows,
+                                                        float* __restrict__ dphi_part, int64_t B, int C, int n,
+                                                        int64_t tile) {
+    constexpr int U = 8;  // tokens per step
+    const int lane = threadIdx.x & (kWave - 1);
+    const int q = (int)wave_uniform(threadIdx.x / kWave);
+    const int64_t c = ((int64_t)blockIdx.x * kWave + lane) * 2;  // two channels per lane
+    const bool active = c < C;                                    // C % 4 == 0: both
+    const int64_t t0 = (int64_t)blockIdx.y * tile;
+    const int64_t t1 = t0 + tile < B ? t0 + tile : B;
+    const int j0 = q, j1 = q + 4;
+    if (j0 >= n) return;  // wave-uniform; no barrier in this kernel
+    const bool has1 = j1 < n;
+    float a0[kWgRows][2], a1[kWgRows][2];
+#pragma unroll
+    for (int o = 0; o < kWgRows; ++o) a0[o][0] = a0[o][1] = a1[o][0] = a1[o][1] = 0.f;
+    const int64_t cc = active ? c : 0;
+    for (int64_t b0 = t0; b0 < t1; b0 += U) {
+        float rv[U][2], bv[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t t = b0 + u < t1 ? b0 + u : t0;
+            wg_load2<TX>(res + t * C + cc, rv[u]);
+            wg_load2<TX>(br + t * C + cc, bv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (b0 + u >= t1) break;
+            // dP rows are 128-byte aligned (dp_stride is a multiple of 32)
+            const float4* d4 = reinterpret_cast<const float4*>(dP + (b0 + u) * dp_stride);
+            float dv[kWgRows];
+#pragma unroll
+            for (int k = 0; k < kWgRows / 4; ++k) {
+                const float4 v = 4 * k < rows ? d4[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+                dv[4 * k] = v.x;
+                dv[4 * k + 1] = v.y;
+                dv[4 * k + 2] = v.z;
+                dv[4 * k + 3] = v.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float x0 = wg_stream_rt<TX, DECAY>(j0, rv[u][e], bv[u][e]);
+                const float x1 = has1 ? wg_stream_rt<TX, DECAY>(j1, rv[u][e], bv[u][e]) : 0.f;
+#pragma unroll
+                for (int o = 0; o < kWgRows; ++o) {
+                    if (o < rows) {
+                        a0[o][e] += dv[o] * x0;
+                        a1[o][e] += dv[o] * x1;
+                    }
+                }
+            }
+        }
+    }
+    if (!active) return;
+    const int64_t K = (int64_t)n * C;
+    float* part = dphi_part + (int64_t)blockIdx.y * rows * K;
+#pragma unroll
+    for (int o = 0; o < kWgRows; ++o) {
+        if (o < rows) {
+            *reinterpret_cast<float2*>(part + o * K + (int64_t)j0 * C + c) = make_float2(a0[o][0], a0[o][1]);
+            if (has1)
+                *reinterpret_cast<float2*>(part + o * K + (int64_t)j1 * C + c) = make_float2(a1[o][0], a1[o][1]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// d r, d b and dw partials with the projection's term formed here from dP
+// (rows o < rows = 2n, the H_res rows vanishing):
+//   d r += sum_o dP[t][o] Phi_r[o][c] + s sum_j w_j X_j,  Phi_r = sum_j w_j Phi_j
+//   d b += sum_o dP[t][o] Phi_1[o][c] + s b
+// on top of the stream parts of wgen_dx_kernel.  Two channels per lane, so
+// the folded Phi columns of the lane (2 x rows x 2 floats) stay in registers
+// across the token loop; workgroup = 512 channels x one token tile.
+// ---------------------------------------------------------------------------
+template <typename TX, int NM, bool DECAY>
+__global__ __launch_bounds__(256) void wgen_dx_fold_kernel(
+    const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
+    const float* __restrict__ ep, const float* __restrict__ dP, int dp_stride, int rows,
+    const float* __restrict__ s_tok, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
+    TX* __restrict__ dres, TX* __restrict__ dbr, float* __restrict__ dw_part, int64_t B, int C, int n,
+    int64_t tile) {
+    const int64_t c0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 2;
+    const bool active = c0 < C;  // C % 4 == 0: both channels
+    const int64_t t0 = (int64_t)blockIdx.y * tile;
+    const int64_t t1 = t0 + tile < B ? t0 + tile : B;
+    const int64_t K = (int64_t)n * C;
+    float pr[kWgRows][2], pb[kWgRows][2];
+#pragma unroll
+    for (int o = 0; o < kWgRows; ++o) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            float vr = 0.f, vb = 0.f;
+            if (active && o < rows) {
+                const float* row = o < n ? phi_pre + (int64_t)o * K : phi_post + (int64_t)(o - n) * K;
+                vr = row[c0 + e];
+#pragma unroll
+                for (int j = 2; j < NM; ++j) {
+                    if (j < n && DECAY) vr += kWgMult[j] * row[(int64_t)j * C + c0 + e];
+                }
+                vb = row[C + c0 + e];
+            }
+            pr[o][e] = vr;
+            pb[o][e] = vb;
+        }
+    }
+    float wv[2] = {0.f, 0.f}, dw[2] = {0.f, 0.f};
+    if (active) {
+        wv[0] = w[c0];
+        wv[1] = w[c0 + 1];
+    }
+    for (int64_t b = t0; b < t1; ++b) {
+        const float* e = ep + b * kWgEp;
+        const float e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3], e4 = e[4], e5 = e[5], e6 = e[6];
+        float hp[NM];
+#pragma unroll
+        for (int j = 0; j < NM; ++j) hp[j] = e[8 + j];
+        const float sv = s_tok[b];
+        const float* d = dP + b * dp_stride;
+        float dv[kWgRows];
+#pragma unroll
+        for (int o = 0; o < kWgRows; ++o) dv[o] = o < rows ? d[o] : 0.f;
+        if (!active) continue;
+        const int64_t off = b * (int64_t)C + c0;
+        const float2 gg2 = *reinterpret_cast<const float2*>(g + off);
+        const float gv[2] = {gg2.x, gg2.y};
+        float rv[2], bv[2];
+        wg_load2<TX>(res + off, rv);
+        wg_load2<TX>(br + off, bv);
+        float dr[2], db[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float xa = wg_xa<TX, NM, DECAY>(rv[q], bv[q], hp, n);
+            const float gq = gv[q];
+            const float wg = wv[q] * gq;
+            float pa = 0.f, pc = 0.f;
+#pragma unroll
+            for (int o = 0; o < kWgRows; ++o) {
+                pa += dv[o] * pr[o][q];
+                pc += dv[o] * pb[o][q];
+            }
+            float xs = rv[q];
+#pragma unroll
+            for (int j = 2; j < NM; ++j) {
+                if (j < n && DECAY) xs += kWgMult[j] * wg_stream<TX, DECAY>(j, rv[q], bv[q]);
+            }
+            dr[q] = e0 * gq + e1 * wg + e5 * xa + pa + sv * xs;
+            db[q] = e2 * gq + e3 * wg + e6 * xa + pc + sv * bv[q];
+            dw[q] += e4 * gq * xa;
+        }
+        if constexpr (sizeof(TX) == 2) {
+            *reinterpret_cast<uint32_t*>(dres + off) = pack_bf16x2(dr[0], dr[1]);
+            *reinterpret_cast<uint32_t*>(dbr + off) = pack_bf16x2(db[0], db[1]);
+        } else {
+            *reinterpret_cast<float2*>(dres + off) = make_float2(dr[0], dr[1]);
+            *reinterpret_cast<float2*>(dbr + off) = make_float2(db[0], db[1]);
+        }
+    }
+    if (active) {
+        dw_part[(int64_t)blockIdx.y * C + c0] = dw[0];
+        dw_part[(int64_t)blockIdx.y * C + c0 + 1] = dw[1];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // The stream rows X[b][j*C + c] (x_flat of the layer, layer.py:138) in TO.
 // ---------------------------------------------------------------------------
 template <typename TX, typename TO, int NM, bool DECAY>
@@ -527,6 +737,64 @@ hipError_t launch_wgen_dx(int dt, int n, bool decay, const float* g, const void*
                                        (const TX_*)res, (const TX_*)br, w, ep, dX, s_tok, (TX_*)dres, (TX_*)dbr,
                                        dw_part, B, Ci, n, tile));
     }
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+// Token tiles of wgen_dphi_kernel: 128-channel column blocks x tiles about
+// eight workgroups per CU, at most one tile per token.
+int wgen_dphi_tiles(int64_t B, int64_t C) {
+    const int64_t gx = (C + 127) / 128;
+    int64_t tiles = (8 * (int64_t)device_cu_count() + gx - 1) / gx;
+    if (tiles > B) tiles = B;
+    if (tiles < 1) tiles = 1;
+    return (int)tiles;
+}
+
+hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const void* br, const float* dP,
+                            int dp_stride, int rows, float* dphi_part, int tiles, int64_t B, int64_t C,
+                            hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!wgen_supported(n, C) || tiles < 1 || rows < 1 || rows > kWgRows) return hipErrorInvalidValue;
+    const int64_t tile = (B + tiles - 1) / tiles;
+    const dim3 grid((unsigned)((C + 127) / 128), (unsigned)tiles);
+    const int Ci = (int)C;
+    const int tok = timing_begin("proj_bwd_dphi", s);
+#define MHC_WGD(TX_, D_)                                                                                         \
+    MHC_LAUNCH_GGL((wgen_dphi_kernel<TX_, D_>), grid, dim3(256), 0, s, (const TX_*)res, (const TX_*)br, dP,       \
+                   dp_stride, rows, dphi_part, B, Ci, n, tile)
+    if (dt == kBF16) {
+        if (decay) { MHC_WGD(bf16_t, true); } else { MHC_WGD(bf16_t, false); }
+    } else {
+        if (decay) { MHC_WGD(float, true); } else { MHC_WGD(float, false); }
+    }
+#undef MHC_WGD
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+int wgen_fold_tiles(int64_t B, int64_t C) {
+    const int64_t gx = (C + 511) / 512;
+    int64_t tiles = (8 * (int64_t)device_cu_count() + gx - 1) / gx;
+    if (tiles > B) tiles = B;
+    if (tiles < 1) tiles = 1;
+    return (int)tiles;
+}
+
+hipError_t launch_wgen_dx_fold(int dt, int n, bool decay, const float* g, const void* res, const void* br,
+                               const float* w, const float* ep, const float* dP, int dp_stride, int rows,
+                               const float* s_tok, const float* phi_pre, const float* phi_post, void* dres,
+                               void* dbr, float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (!wgen_supported(n, C) || tiles < 1 || rows < 1 || rows > 2 * n) return hipErrorInvalidValue;
+    const int64_t tile = (B + tiles - 1) / tiles;
+    const dim3 grid((unsigned)((C + 511) / 512), (unsigned)tiles);
+    const int Ci = (int)C;
+    const int tok = timing_begin("wrap_proj_bwd", s);
+    MHC_WG_DISPATCH(dt, decay, n,
+                    MHC_LAUNCH_GGL((wgen_dx_fold_kernel<TX_, NM_, D_>), grid, dim3(256), 0, s, g, (const TX_*)res,
+                                   (const TX_*)br, w, ep, dP, dp_stride, rows, s_tok, phi_pre, phi_post, (TX_*)dres,
+                                   (TX_*)dbr, dw_part, B, Ci, n, tile));
     timing_end(tok, s);
     return hipGetLastError();
 }
