@@ -160,15 +160,15 @@ def test_dynamic_layer_unsupported_n_raises(device):
 
 
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n,B,C", [(1, 9, 96), (3, 7, 96), (3, 1100, 64), (5, 9, 160), (6, 5, 64), (7, 3, 32),
-                                   (12, 4, 128), (20, 3, 64), (64, 3, 64)])
+@pytest.mark.parametrize("n,B,C", [(1, 9, 96), (3, 7, 96), (3, 1100, 64), (5, 9, 160), (6, 5, 64), (6, 1100, 64),
+                                   (7, 3, 32), (12, 4, 128), (20, 3, 64), (64, 3, 64)])
 def test_dynamic_layer_runtime_n(device, x_dtype, n, B, C):
     """Expansion rates without a fixed-n kernel (the reference takes any n up
     to 64, mhc_types.h:68): the generic row kernels, the per-token Sinkhorn on
     16 / 32 / 64-lane groups with n at run time, dM on zero-padded fp32 MFMA
     blocks; the projection over 2n + n^2 rows (15 .. 4224) in 32-row tiles or
     the streaming kernels.  B = 1100 runs more tokens than the backward has
-    workgroups."""
+    workgroups (and, with bf16 x at n = 6, the one-pass projection)."""
     d = R.dynamic_layer_inputs(B, n, C, seed=n * 100 + B + C, x_dtype=x_dtype, alpha=0.1, phi_std=0.02, b_std=0.5)
     _check_dyn(_run_dyn(d, device), _oracle_dyn(d), x_dtype, f"n={n} B={B} C={C} {x_dtype}", family_floor=n == 1)
 
@@ -232,7 +232,7 @@ def test_dynamic_inference_equals_training_forward(device):
 
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("n,B,C", [(4, 1, 64), (4, 37, 1280), (2, 9, 256), (4, 300, 4096), (8, 5, 320),
-                                   (32, 4, 1280), (6, 7, 320), (12, 3, 64)])
+                                   (8, 1100, 64), (32, 4, 1280), (6, 7, 320), (12, 3, 64)])
 def test_dynamic_inference_packed_and_bf16_out(device, x_dtype, n, B, C):
     """The forward-only entry on packed parameters: its fp32 output is the
     training forward's bit for bit, its bf16 output is that result rounded to
