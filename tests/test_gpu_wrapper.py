@@ -247,14 +247,16 @@ def test_wrapper_sinkhorn_settings(device, n, dynamic, iters, eps):
 
 @pytest.mark.parametrize("n,dynamic,C", [(2, False, 256), (3, False, 96), (5, False, 160), (8, False, 256),
                                          (2, True, 256), (3, True, 96), (5, True, 96), (6, True, 256),
-                                         (7, True, 96), (8, True, 256), (4, True, 264), (4, False, 17000)])
+                                         (7, True, 96), (8, True, 256), (4, True, 264), (4, False, 17000),
+                                         (8, True, 4), (2, True, 16), (5, False, 4), (6, True, 1104)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
 def test_wrapper_runtime_n_matches_oracle(device, n, dynamic, C, dtype, mode):
     """The run-time-n wrapper kernels (n = 2..8; n = 4 rows the n = 4 kernels
-    refuse: 264 channels with dynamic H, 17000 with static H) against the
-    float64 oracle, every output and gradient, both storage dtypes and both
-    residual modes."""
+    refuse: 264 channels with dynamic H, 17000 with static H; rows of 4 and
+    16 channels, narrower than one wave's chunks; 1104 channels, a partial
+    column block of every backward kernel) against the float64 oracle, every
+    output and gradient, both storage dtypes and both residual modes."""
     seed = 1000 + 10 * n + (7 if dynamic else 0) + (3 if mode == "zero" else 0)
     wrap = _make(C, dynamic, seed, n=n)
     wrap.residual_mode = mode
