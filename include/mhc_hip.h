@@ -306,9 +306,11 @@ int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dty
  * residual and branch in registers, so with static H, and with dynamic H at
  * n = 4 and hidden % 32 == 0 (whose projection kernels rebuild it too), X
  * never exists in memory.  For the other dynamic-H shapes the projection
- * forward reads a storage-dtype copy of X from the workspace, and so does
- * the backward (fp32) when the Sinkhorn settings keep the H_res gradients
- * (num_iters == 0 or sinkhorn_eps > 1e-6); the queries below size both.
+ * forward reads a storage-dtype copy of X from the workspace (except with
+ * bf16 storage, n >= 5, tokens >= 1024 and hidden % 64 == 0, where it too
+ * rebuilds X), and so does the backward (fp32) when the Sinkhorn settings
+ * keep the H_res gradients (num_iters == 0 or sinkhorn_eps > 1e-6); the
+ * queries below size both.
  * Parameters and `saved` are those of the layer entries above.  Backward:
  * grad_out [tokens, hidden] fp32 -> grad_residual, grad_branch (dtype) and
  * the layer's parameter gradients.

@@ -1374,8 +1374,17 @@ static int wgen_dynamic_fwd(const void* residual, const void* branch, int32_t dt
     char* pw = (char*)workspace + w.p_base;
     float* pp = (float*)(pw + w.p.p_off);
     float* ss = (float*)(pw + w.p.ss_off);
-    e = launch_wgen_synth(dtype, dtype, n, decay, residual, branch, workspace, tokens, hidden, s);
-    if (e == hipSuccess) {
+    // bf16 rows of whole 64-channel stages: the streaming projection reads
+    // residual and branch and rebuilds the streams itself
+    if (proj_one_pass(dtype, np, tokens) && hidden % 64 == 0) {
+        bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
+        e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
+        if (e == hipSuccess)
+            e = launch_proj_stream_wrap(decay, residual, branch, hidden, phib, np, pp, ss, tokens, K, w.p.ks, s);
+    } else {
+        e = launch_wgen_synth(dtype, dtype, n, decay, residual, branch, workspace, tokens, hidden, s);
+    }
+    if (e == hipSuccess && !(proj_one_pass(dtype, np, tokens) && hidden % 64 == 0)) {
         if (w.p.stream) {
             e = launch_proj_stream(dtype, workspace, (bf16_raw_t*)(pw + w.p.xpl_off), phi_pre, phi_post, phi_res, n,
                                    nullptr, np, pp, ss, tokens, K, w.p.ks, s);

@@ -393,11 +393,19 @@ __global__ __launch_bounds__(256) void proj_xsplit_kernel(const float* __restric
     if (threadIdx.x == 0) ss_part[(int64_t)q * B + b] = ss[0];
 }
 
-template <int XPL, int MT, bool PHI_PLANES>
+// WRAP = 1 or 2 (the MHCResidualWrapper's streams, bf16 storage): x is not
+// in memory; xpl is the residual and xb the branch ([B][Cw] each) and the
+// stage's 16-byte pieces are read from the stream's source row (stream j =
+// k / Cw, each 64-k stage within one stream: Cw % 64 == 0) and, for
+// j >= 2, scaled by 0.1^(j-1) and rounded to bf16 at commit (WRAP = 1,
+// 'decay') or read as zeros (WRAP = 2, 'zero').
+template <int XPL, int MT, bool PHI_PLANES, int WRAP = 0>
 __global__ __launch_bounds__(256) void proj_stream_kernel(
     const bf16_t* __restrict__ xpl, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
     const float* __restrict__ phi_res, int n_pre, const uint4* __restrict__ phif, int np, float* __restrict__ p_part,
-    float* __restrict__ ss_part, int64_t B, int64_t K, int64_t kchunk, int ks, int oblocks, int64_t groups) {
+    float* __restrict__ ss_part, int64_t B, int64_t K, int64_t kchunk, int ks, int oblocks, int64_t groups,
+    const bf16_t* __restrict__ xb = nullptr, int Cw = 0) {
+    static_assert(WRAP == 0 || XPL == 1, "the wrapper's streams are bf16 rows");
     constexpr int TB = 16 * MT;
     constexpr int KS = kStreamKS;
     constexpr int PITCH = kStreamPitch;
@@ -444,21 +452,49 @@ __global__ __launch_bounds__(256) void proj_stream_kernel(
     static_assert((TB * 8) % 256 == 0, "whole planes per piece round");
     const int64_t rows = B - tok0 < TB ? B - tok0 : TB;
     buf_rsrc_t xr[XPL];
+    if constexpr (WRAP != 0) {
+        xr[0] = make_buf_rsrc(xpl + tok0 * Cw, (uint32_t)(rows * Cw * 2));
+    } else {
 #pragma unroll
-    for (int p2 = 0; p2 < XPL; ++p2)
-        xr[p2] = make_buf_rsrc(xpl + p2 * plane + tok0 * K, (uint32_t)(rows * K * 2));
+        for (int p2 = 0; p2 < XPL; ++p2)
+            xr[p2] = make_buf_rsrc(xpl + p2 * plane + tok0 * K, (uint32_t)(rows * K * 2));
+    }
+    const buf_rsrc_t xbr = WRAP != 0 ? make_buf_rsrc(xb + tok0 * Cw, (uint32_t)(rows * Cw * 2)) : xr[0];
     auto fetch_x = [&](uint4 (&f)[PPT], int st) __attribute__((always_inline)) {
         const int64_t k0 = kb + (int64_t)st * KS;
+        if constexpr (WRAP != 0) {
+            const int j = (int)k0 / Cw;  // wave-uniform
+            const int c0 = (int)k0 - j * Cw;
+            const bool none = WRAP == 2 && j >= 2;
 #pragma unroll
-        for (int u = 0; u < PPT; ++u) {
-            const int i = threadIdx.x + 256 * u;
-            const int r = (i / 8) % TB;
-            const int c = i % 8;
-            f[u] = buf_ld16<false, true>(xr[(256 * u) / (TB * 8)], (uint32_t)(((int64_t)r * K + k0 + 8 * c) * 2), 0u);
+            for (int u = 0; u < PPT; ++u) {
+                const int i = threadIdx.x + 256 * u;
+                const int r = (i / 8) % TB;
+                const int c = i % 8;
+                const uint32_t off = none ? kBufOff : (uint32_t)((r * Cw + c0 + 8 * c) * 2);
+                f[u] = buf_ld16<false, true>(j == 1 ? xbr : xr[0], off, 0u);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < PPT; ++u) {
+                const int i = threadIdx.x + 256 * u;
+                const int r = (i / 8) % TB;
+                const int c = i % 8;
+                f[u] = buf_ld16<false, true>(xr[(256 * u) / (TB * 8)], (uint32_t)(((int64_t)r * K + k0 + 8 * c) * 2),
+                                             0u);
+            }
         }
     };
     auto commit = [&](const uint4 (&f)[PPT], int st, int buf) __attribute__((always_inline)) {
         const int64_t k0 = kb + (int64_t)st * KS;
+        // decay streams: the stored stream value bf16(r * 0.1^(j-1))
+        float mult = 0.f;
+        if constexpr (WRAP == 1) {
+            const int j = (int)k0 / Cw;
+            double d = 1.0;
+            for (int e = 1; e < j; ++e) d *= 0.1;  // Python's 0.1 ** (j - 1), as the wrapper kernels take it
+            mult = j >= 2 ? (float)d : 0.f;
+        }
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int i = threadIdx.x + 256 * u;
@@ -466,8 +502,21 @@ __global__ __launch_bounds__(256) void proj_stream_kernel(
             const int r = (i / 8) % TB;
             const int c = i % 8;
             const uint32_t m = k0 + 8 * c < ke ? 0xffffffffu : 0u;
+            uint4 v = f[u];
+            if constexpr (WRAP == 1) {
+                if (mult != 0.f) {
+                    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float lo = __uint_as_float(w[e] << 16) * mult;
+                        const float hi = __uint_as_float(w[e] & 0xffff0000u) * mult;
+                        w[e] = pack_bf16(lo, hi);
+                    }
+                    v = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
             *reinterpret_cast<uint4*>(&xs[buf][(pl * TB + r) * PITCH + 16 * c]) =
-                make_uint4(f[u].x & m, f[u].y & m, f[u].z & m, f[u].w & m);
+                make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
         }
     };
     // Phi fragments of stage st (its two k steps) for the wave's two 16-row
@@ -1808,10 +1857,12 @@ hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, c
 #define MHC_STREAM(XPL_, MT_)                                                                                   \
     if (phib) {                                                                                                 \
         MHC_LAUNCH_GGL((proj_stream_kernel<XPL_, MT_, true>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,   \
-                           phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups);             \
+                           phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups,              \
+                           (const bf16_t*)nullptr, 0);                                                          \
     } else {                                                                                                    \
         MHC_LAUNCH_GGL((proj_stream_kernel<XPL_, MT_, false>), grid, dim3(256), 0, s, xp, phi_pre, phi_post,  \
-                           phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups);             \
+                           phi_res, n_pre, phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups,              \
+                           (const bf16_t*)nullptr, 0);                                                          \
     }
 #define MHC_STREAM_MT(XPL_)                               \
     if (mt == 2) {                                        \
@@ -1826,6 +1877,38 @@ hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, c
     }
 #undef MHC_STREAM_MT
 #undef MHC_STREAM
+    timing_end(tok, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_proj_stream_wrap(bool decay, const void* res, const void* br, int64_t Cw, const bf16_raw_t* phib,
+                                   int np, float* p_part, float* ss_part, int64_t B, int64_t K, int ks,
+                                   hipStream_t s) {
+    if (B == 0) return hipSuccess;
+    if (K % 32 != 0 || np <= kProjTile || ks < 1 || !phib || Cw < kStreamKS || Cw % kStreamKS != 0 ||
+        K % Cw != 0 || K > (int64_t(1) << 22))
+        return hipErrorInvalidValue;
+    int64_t kchunk = (K + ks - 1) / ks;
+    kchunk = ((kchunk + kStreamKS - 1) / kStreamKS) * kStreamKS;
+    const int mt = proj_stream_mt(B);
+    const int64_t tb = (B + 16 * mt - 1) / (16 * mt);
+    const int ob = (np + kStreamOB - 1) / kStreamOB;
+    const int64_t groups = tb * ks;
+    const dim3 grid((unsigned)(((groups + 7) / 8) * 8 * ob));
+    const int tok = timing_begin("proj", s);
+    const bf16_t* rp = reinterpret_cast<const bf16_t*>(res);
+    const bf16_t* bp = reinterpret_cast<const bf16_t*>(br);
+    const uint4* phif = reinterpret_cast<const uint4*>(phib);
+    const int Ci = (int)Cw;
+#define MHC_STREAM_W(MT_, W_)                                                                                     \
+    MHC_LAUNCH_GGL((proj_stream_kernel<1, MT_, true, W_>), grid, dim3(256), 0, s, rp, nullptr, nullptr, nullptr, 0, \
+                   phif, np, p_part, ss_part, B, K, kchunk, ks, ob, groups, bp, Ci)
+    if (mt == 2) {
+        if (decay) { MHC_STREAM_W(2, 1); } else { MHC_STREAM_W(2, 2); }
+    } else {
+        if (decay) { MHC_STREAM_W(4, 1); } else { MHC_STREAM_W(4, 2); }
+    }
+#undef MHC_STREAM_W
     timing_end(tok, s);
     return hipGetLastError();
 }

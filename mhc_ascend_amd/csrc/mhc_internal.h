@@ -275,6 +275,14 @@ constexpr size_t proj_xplanes_bytes(int64_t B, int64_t K) { return (size_t)(3 * 
 hipError_t launch_proj_stream(int x_dtype, const void* x, bf16_raw_t* xplanes, const float* phi_pre,
                               const float* phi_post, const float* phi_res, int n_pre, const bf16_raw_t* phib, int np,
                               float* p_part, float* ss_part, int64_t B, int64_t K, int ks, hipStream_t s);
+// The streaming projection of the MHCResidualWrapper's stream rows with
+// bf16 storage, read from residual / branch ([B][Cw] each, Cw % 64 == 0)
+// instead of a stream tensor (decay: streams j >= 2 are bf16(r 0.1^(j-1)),
+// else 0); Phi as the planes of launch_phi_split; p_part / ss_part as
+// launch_proj_mfma.
+hipError_t launch_proj_stream_wrap(bool decay, const void* res, const void* br, int64_t Cw, const bf16_raw_t* phib,
+                                   int np, float* p_part, float* ss_part, int64_t B, int64_t K, int ks,
+                                   hipStream_t s);
 hipError_t launch_proj_reduce(const float* p_part, int ks, int64_t B, int np, float* out, hipStream_t s);
 #ifdef MHC_KERNEL_TIMING
 // The benchmark build's VALU projection (A/B against launch_proj_mfma): Phi

@@ -268,3 +268,23 @@ def test_wrapper_runtime_n_matches_oracle(device, n, dynamic, C, dtype, mode):
     want = _oracle(wrap, res, br, grad, mode)
     got = _run(wrap, res, br, grad, device)
     _check(got, want, dtype, DYN if dynamic else STA, f"n={n} C={C} dyn={dynamic} {dtype} {mode}")
+
+
+@pytest.mark.parametrize("n", [5, 8])
+@pytest.mark.parametrize("mode", ["decay", "zero"])
+def test_wrapper_runtime_n_many_tokens(device, n, mode):
+    """bf16 storage from 1024 tokens up with whole 64-channel stages: the
+    forward projection rebuilds the streams from residual and branch inside
+    the streaming projection kernel (no stream rows in memory) - against the
+    float64 oracle, every output and gradient."""
+    C, B = 128, 1100
+    seed = 2000 + 10 * n + (3 if mode == "zero" else 0)
+    wrap = _make(C, True, seed, n=n)
+    wrap.residual_mode = mode
+    g = _gen(seed + 2)
+    res = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    br = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    grad = torch.randn(B, C, generator=g)
+    want = _oracle(wrap, res, br, grad, mode)
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, torch.bfloat16, DYN, f"n={n} B={B} {mode}")
