@@ -27,8 +27,9 @@
 //                      dynamic H it adds the layer projection backward's dX
 //                      folded over the streams (Sinkhorn settings where the
 //                      H_res rows of dP do not vanish)
-//   wgen_dphi_kernel   dynamic H, H_res rows of dP vanishing: dPhi of the
-//                      2n pre / post rows from the rebuilt streams
+//   wgen_dphi_mfma_kernel  dynamic H, H_res rows of dP vanishing: dPhi of
+//                      the 2n pre / post rows from the rebuilt streams
+//                      (bf16 MFMA)
 //   wgen_dx_fold_kernel  the same case: d r, d b with dP . Phi folded over
 //                      the streams, and the dw partials
 //   wgen_synth_kernel  the stream rows [tokens, n*C] as the operand of the
@@ -402,15 +403,11 @@ __global__ __launch_bounds__(256) void wgen_dx_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 // The projection backward over the pre / post rows of dP (the H_res rows
 // vanish: every stream receives G / n through the stream mean), without
-// the stream rows in memory.
+// the stream rows in memory:
 //   dphi_part[tile][o][j*C + c] = sum over the tile's tokens of
 //                                 dP[t][o] X_j[t][c],  o < rows = 2n
-// Workgroup = 4 waves x 128 channels (two per lane) x one token tile; wave
-// q takes streams q and q + 4 (a wave-uniform choice) and keeps rows x 2 x 2
-// sums per lane; dP of a token is a wave-uniform record (scalar loads).
 // ---------------------------------------------------------------------------
 constexpr int kWgRows = 2 * kWgMaxN;  // pre / post rows of dP at most
-constexpr int kWgTokU = 4;            // tokens per step of the token loops
 
 namespace {
 // two consecutive elements (4- or 8-byte aligned) as one load
@@ -426,81 +423,141 @@ __device__ __forceinline__ void wg_load2(const TX* p, float (&v)[2]) {
         v[1] = f.y;
     }
 }
+}  // namespace
 
-// stream j with j known only at run time (wave-uniform)
-template <typename TX, bool DECAY>
-__device__ __forceinline__ float wg_stream_rt(int j, float r, float b) {
-    float m = 0.f;
+// ---------------------------------------------------------------------------
+// The dPhi partials on bf16 MFMA 16x16x32: M = the rows o of dP (16,
+// zero past rows), N = 16 channels, K = 32 tokens.  A = dP^T split into hi
+// and lo bf16 parts (fp32 dP to 2^-16), B = X_j rebuilt from r and b (exact
+// in one bf16 plane with bf16 storage; split hi / lo with fp32 storage).
+// Workgroup = 4 waves x 16 channels (64 channels) x one token tile; each
+// 32-token step stages the r and b tile [32][64] and dP^T [16][32] in LDS,
+// and each wave runs 2 (bf16) or 3 (fp32) MFMAs per stream.
+// ---------------------------------------------------------------------------
+namespace {
+typedef __bf16 gbf16x8_t __attribute__((ext_vector_type(8)));
+typedef float gf32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int gu32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ gf32x4_t gmfma(gu32x4_t a, gu32x4_t b, gf32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gbf16x8_t, a), __builtin_bit_cast(gbf16x8_t, b),
+                                                   c, 0, 0, 0);
+}
+
+// 8 fp32 -> hi / lo bf16 parts, packed in MFMA operand order (element e in
+// half e % 2 of word e / 2)
+__device__ __forceinline__ void g_split8(const float (&v)[8], gu32x4_t& hi, gu32x4_t& lo) {
 #pragma unroll
-    for (int q = 2; q < kWgMaxN; ++q) m = (j == q) ? kWgMult[q] : m;
-    return j == 0 ? r : (j == 1 ? b : (DECAY ? wg_round<TX>(r * m) : 0.f));
+    for (int e = 0; e < 4; ++e) {
+        const float h0 = bf16_to_f32(f32_to_bf16(v[2 * e]));
+        const float h1 = bf16_to_f32(f32_to_bf16(v[2 * e + 1]));
+        hi[e] = pack_bf16x2(h0, h1);
+        lo[e] = pack_bf16x2(v[2 * e] - h0, v[2 * e + 1] - h1);
+    }
 }
 }  // namespace
 
-template <typename TX, bool DECAY>
-__global__ __launch_bounds__(256) void wgen_dphi_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
-                                                        const float* __restrict__ dP, int dp_stride, int rows,
-                                                        float* __restrict__ dphi_part, int64_t B, int C, int n,
-                                                        int64_t tile) {
-    constexpr int U = 8;  // tokens per step
-    const int lane = threadIdx.x & (kWave - 1);
-    const int q = (int)wave_uniform(threadIdx.x / kWave);
-    const int64_t c = ((int64_t)blockIdx.x * kWave + lane) * 2;  // two channels per lane
-    const bool active = c < C;                                    // C % 4 == 0: both
+constexpr int kWgDphiCB = 64;  // channels per workgroup of the MFMA dPhi kernel
+
+template <typename TX, int NM, bool DECAY>
+__global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restrict__ res, const TX* __restrict__ br,
+                                                             const float* __restrict__ dP, int dp_stride, int rows,
+                                                             float* __restrict__ dphi_part, int64_t B, int C, int n,
+                                                             int64_t tile) {
+    constexpr int CB = kWgDphiCB;
+    constexpr int TS = 32;
+    constexpr int RP = CB + 4;  // LDS row pitch (elements)
+    __shared__ __align__(16) float rl[TS][RP];
+    __shared__ __align__(16) float bl[TS][RP];
+    __shared__ __align__(16) float dpt[16][TS + 4];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int lr = lane & 15;
+    const int lg = lane >> 4;
+    const int64_t cb0 = (int64_t)blockIdx.x * CB;
     const int64_t t0 = (int64_t)blockIdx.y * tile;
     const int64_t t1 = t0 + tile < B ? t0 + tile : B;
-    const int j0 = q, j1 = q + 4;
-    if (j0 >= n) return;  // wave-uniform; no barrier in this kernel
-    const bool has1 = j1 < n;
-    float a0[kWgRows][2], a1[kWgRows][2];
+    gf32x4_t acc[NM];
 #pragma unroll
-    for (int o = 0; o < kWgRows; ++o) a0[o][0] = a0[o][1] = a1[o][0] = a1[o][1] = 0.f;
-    const int64_t cc = active ? c : 0;
-    for (int64_t b0 = t0; b0 < t1; b0 += U) {
-        float rv[U][2], bv[U][2];
+    for (int j = 0; j < NM; ++j) acc[j] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int64_t s0 = t0; s0 < t1; s0 += TS) {
+        // r and b tile: 32 tokens x 64 channels in 4-channel pieces, two per
+        // thread (a piece is all in or all out of the row: C % 4 == 0)
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t t = b0 + u < t1 ? b0 + u : t0;
-            wg_load2<TX>(res + t * C + cc, rv[u]);
-            wg_load2<TX>(br + t * C + cc, bv[u]);
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + 256 * u;
+            const int tt = i / (CB / 4);
+            const int c4 = (i % (CB / 4)) * 4;
+            const int64_t t = s0 + tt;
+            const int64_t c = cb0 + c4;
+            float rv[4] = {0.f, 0.f, 0.f, 0.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
+            if (t < t1 && c < C) {
+                load_run<TX, 4>(res + t * C + c, rv);
+                load_run<TX, 4>(br + t * C + c, bv);
+            }
+            *reinterpret_cast<float4*>(&rl[tt][c4]) = make_float4(rv[0], rv[1], rv[2], rv[3]);
+            *reinterpret_cast<float4*>(&bl[tt][c4]) = make_float4(bv[0], bv[1], bv[2], bv[3]);
+        }
+        // dP^T tile [16 rows][32 tokens]
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + 256 * u;
+            const int o = i / TS;
+            const int tt = i % TS;
+            const int64_t t = s0 + tt;
+            dpt[o][tt] = (o < rows && t < t1) ? dP[t * dp_stride + o] : 0.f;
+        }
+        __syncthreads();
+        // A = dP^T: row o = lr, tokens 8 lg .. + 7
+        float av[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) av[e] = dpt[lr][8 * lg + e];
+        gu32x4_t ah, al;
+        g_split8(av, ah, al);
+        // B = X_j: tokens 8 lg .. + 7 of channel 16 wave + lr
+        float rv[8], bv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            rv[e] = rl[8 * lg + e][16 * wave + lr];
+            bv[e] = bl[8 * lg + e][16 * wave + lr];
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (b0 + u >= t1) break;
-            // dP rows are 128-byte aligned (dp_stride is a multiple of 32)
-            const float4* d4 = reinterpret_cast<const float4*>(dP + (b0 + u) * dp_stride);
-            float dv[kWgRows];
+        for (int j = 0; j < NM; ++j) {
+            if (j < n) {
+                float xv[8];
 #pragma unroll
-            for (int k = 0; k < kWgRows / 4; ++k) {
-                const float4 v = 4 * k < rows ? d4[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-                dv[4 * k] = v.x;
-                dv[4 * k + 1] = v.y;
-                dv[4 * k + 2] = v.z;
-                dv[4 * k + 3] = v.w;
-            }
+                for (int e = 0; e < 8; ++e) xv[e] = wg_stream<TX, DECAY>(j, rv[e], bv[e]);
+                if constexpr (sizeof(TX) == 2) {
+                    gu32x4_t xb;
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const float x0 = wg_stream_rt<TX, DECAY>(j0, rv[u][e], bv[u][e]);
-                const float x1 = has1 ? wg_stream_rt<TX, DECAY>(j1, rv[u][e], bv[u][e]) : 0.f;
-#pragma unroll
-                for (int o = 0; o < kWgRows; ++o) {
-                    if (o < rows) {
-                        a0[o][e] += dv[o] * x0;
-                        a1[o][e] += dv[o] * x1;
-                    }
+                    for (int e = 0; e < 4; ++e) xb[e] = pack_bf16x2(xv[2 * e], xv[2 * e + 1]);  // exact
+                    acc[j] = gmfma(ah, xb, acc[j]);
+                    acc[j] = gmfma(al, xb, acc[j]);
+                } else {
+                    gu32x4_t xh, xl;
+                    g_split8(xv, xh, xl);
+                    acc[j] = gmfma(ah, xh, acc[j]);
+                    acc[j] = gmfma(al, xh, acc[j]);
+                    acc[j] = gmfma(ah, xl, acc[j]);
                 }
             }
         }
+        __syncthreads();
     }
-    if (!active) return;
+    // D[o = 4 lg + i][channel 16 wave + lr]
+    const int64_t c = cb0 + 16 * wave + lr;
+    if (c >= C) return;
     const int64_t K = (int64_t)n * C;
     float* part = dphi_part + (int64_t)blockIdx.y * rows * K;
 #pragma unroll
-    for (int o = 0; o < kWgRows; ++o) {
-        if (o < rows) {
-            *reinterpret_cast<float2*>(part + o * K + (int64_t)j0 * C + c) = make_float2(a0[o][0], a0[o][1]);
-            if (has1)
-                *reinterpret_cast<float2*>(part + o * K + (int64_t)j1 * C + c) = make_float2(a1[o][0], a1[o][1]);
+    for (int j = 0; j < NM; ++j) {
+        if (j < n) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int o = 4 * lg + i;
+                if (o < rows) part[o * K + (int64_t)j * C + c] = acc[j][i];
+            }
         }
     }
 }
@@ -741,10 +798,10 @@ hipError_t launch_wgen_dx(int dt, int n, bool decay, const float* g, const void*
     return hipGetLastError();
 }
 
-// Token tiles of wgen_dphi_kernel: 128-channel column blocks x tiles about
+// Token tiles of wgen_dphi_mfma_kernel: 64-channel column blocks x tiles about
 // eight workgroups per CU, at most one tile per token.
 int wgen_dphi_tiles(int64_t B, int64_t C) {
-    const int64_t gx = (C + 127) / 128;
+    const int64_t gx = (C + kWgDphiCB - 1) / kWgDphiCB;
     int64_t tiles = (8 * (int64_t)device_cu_count() + gx - 1) / gx;
     if (tiles > B) tiles = B;
     if (tiles < 1) tiles = 1;
@@ -757,18 +814,12 @@ hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const vo
     if (B == 0) return hipSuccess;
     if (!wgen_supported(n, C) || tiles < 1 || rows < 1 || rows > kWgRows) return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
-    const dim3 grid((unsigned)((C + 127) / 128), (unsigned)tiles);
+    const dim3 grid((unsigned)((C + kWgDphiCB - 1) / kWgDphiCB), (unsigned)tiles);
     const int Ci = (int)C;
     const int tok = timing_begin("proj_bwd_dphi", s);
-#define MHC_WGD(TX_, D_)                                                                                         \
-    MHC_LAUNCH_GGL((wgen_dphi_kernel<TX_, D_>), grid, dim3(256), 0, s, (const TX_*)res, (const TX_*)br, dP,       \
-                   dp_stride, rows, dphi_part, B, Ci, n, tile)
-    if (dt == kBF16) {
-        if (decay) { MHC_WGD(bf16_t, true); } else { MHC_WGD(bf16_t, false); }
-    } else {
-        if (decay) { MHC_WGD(float, true); } else { MHC_WGD(float, false); }
-    }
-#undef MHC_WGD
+    MHC_WG_DISPATCH(dt, decay, n,
+                    MHC_LAUNCH_GGL((wgen_dphi_mfma_kernel<TX_, NM_, D_>), grid, dim3(256), 0, s, (const TX_*)res,
+                                   (const TX_*)br, dP, dp_stride, rows, dphi_part, B, Ci, n, tile));
     timing_end(tok, s);
     return hipGetLastError();
 }
