@@ -13,7 +13,8 @@ region), and a CPU baseline (the PyTorch oracle on the host cores, on a
 bounded token sample).  The default static workload (C3, the metric's
 configuration) also carries sub-records of the dynamic-H workload (C4, the
 reference layer's default path), the wrapper (C5), the standalone operators
-(C2) and the forward-only entry at the C4 shape, each measured the same way.
+(C2), the forward-only entry at the C4 shape and the wrapper at n = 8 (with
+the unfused path timed beside it), each measured the same way.
 
 Workloads (the metric is quoted at n=4, C=4096):
   static  - C3: MHCLayer static-H, x fp32 [8192, 4, 4096]          (default)
@@ -734,7 +735,7 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel-steps", type=int, default=10, help="steps of the per-kernel timing pass")
     ap.add_argument("--extra", action="append", default=None, choices=sorted(WORKLOADS),
                     help="with the default static workload: also measure these workloads as sub-records "
-                         "(default: dynamic, the reference layer's default path; wrapper; ops; infer)")
+                         "(default: dynamic, the reference layer's default path; wrapper; ops; infer; wrapper8)")
     ap.add_argument("--no-extra", action="store_true", help="no sub-records")
     ap.add_argument("--extra-steps", type=int, default=50,
                     help="timed steps of each sub-record (enough that the first launch and the final drain, "
@@ -748,7 +749,7 @@ def main(argv=None) -> int:
     if a.no_extra:
         a.extra = []
     elif a.extra is None:
-        a.extra = ["dynamic", "wrapper", "ops", "infer"]
+        a.extra = ["dynamic", "wrapper", "ops", "infer", "wrapper8"]
 
     import torch
 
