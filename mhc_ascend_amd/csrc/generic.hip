@@ -259,7 +259,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(
             gen_wave_partial(a3, sred[2][s]);
         }
         __syncthreads();
-        if (threadIdx.x < 2 * n) {
+        if ((int)threadIdx.x < 2 * n) {
             const int t = threadIdx.x;
             const int s = t < n ? t : t - n;
             float v[3];
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_bwd_kernel(
     if constexpr (MODE == 0) {
         __syncthreads();
         float* so = scal_out + (int64_t)blockIdx.x * NS;
-        if (threadIdx.x < 2 * n) so[n * n + threadIdx.x] = acc_s[threadIdx.x];
+        if ((int)threadIdx.x < 2 * n) so[n * n + threadIdx.x] = acc_s[threadIdx.x];
     }
 }
 
@@ -450,7 +450,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_static_finalize_kernel(
             }
         }
     }
-    if (threadIdx.x < n) {
+    if ((int)threadIdx.x < n) {
         const int r = threadIdx.x;
         const float tp = sigmoidf(h_pre[r]);
         const float tq = 2.f * sigmoidf(h_post[r]);
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_aggregate_fwd_kernel(const T*
                                                                         float* __restrict__ h_act, int n, int C) {
     __shared__ float h[kGenMaxN];
     const int64_t b = blockIdx.x;
-    if (threadIdx.x < n) {
+    if ((int)threadIdx.x < n) {
         const float v = sigmoidf(H[b * h_stride + threadIdx.x]);
         h[threadIdx.x] = v;
         h_act[b * n + threadIdx.x] = v;
@@ -505,7 +505,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_aggregate_bwd_kernel(
         gen_wave_partial(a, sred[i]);
     }
     __syncthreads();
-    if (threadIdx.x < n) {
+    if ((int)threadIdx.x < n) {
         const int i = threadIdx.x;
         float t = 0.f;
 #pragma unroll
@@ -624,7 +624,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_distribute_bwd_kernel(
         }
     }
     __syncthreads();
-    if (threadIdx.x < n) {
+    if ((int)threadIdx.x < n) {
         const int i = threadIdx.x;
         float t = 0.f;
 #pragma unroll

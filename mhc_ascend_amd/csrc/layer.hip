@@ -225,6 +225,7 @@ __global__ MHC_ROW_BOUNDS(false) void layer_static_fwd_kernel(const TX* __restri
                                                               float sk_eps, float* __restrict__ out,
                                                               float* __restrict__ rms_out, int64_t B, int C,
                                                               float eps) {
+    (void)B;  // the grid is one workgroup per token
     constexpr int WC = kLayerWC;
     constexpr int NC = coef_size<N>();
     __shared__ float red[8];

@@ -109,7 +109,7 @@ template <typename T, int N, int VPT, int WC>
 __device__ __forceinline__ void unpack_rows(const RawRows<T, N, VPT, WC>& r, int C, float (&v)[N][VPT][WC]) {
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
-        const bool ok = (k * blockDim.x + threadIdx.x) * WC < C;
+        const bool ok = (int)((k * blockDim.x + threadIdx.x) * WC) < C;
 #pragma unroll
         for (int i = 0; i < N; ++i) {
 #pragma unroll
