@@ -331,6 +331,14 @@ int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dt
                             void* stream);
 size_t mhc_wrapper_dynamic_bwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
                                               int32_t residual_mode);
+/* The backward's workspace for given Sinkhorn settings: at n != 4 (and
+ * n = 4 rows the n = 4 kernels do not take) with num_iters >= 1 and
+ * sinkhorn_eps <= 1e-6 no stream rows are kept, and this is smaller than
+ * the query above (which covers every setting).  No counterpart in the
+ * reference (its op allocates its own buffers); for callers that size the
+ * workspace per call. */
+size_t mhc_wrapper_dynamic_bwd_workspace_size_for(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
+                                                  int32_t residual_mode, int32_t num_iters, float sinkhorn_eps);
 int mhc_wrapper_dynamic_bwd(const float* grad_out, const void* residual, const void* branch, int32_t dtype,
                             int32_t residual_mode, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
                             const float* phi_res, const float* alpha_pre, const float* alpha_post,

@@ -91,6 +91,7 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
                                                _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32, _f32,
                                                _vp]),
     "mhc_wrapper_dynamic_bwd_workspace_size": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "mhc_wrapper_dynamic_bwd_workspace_size_for": (_sz, [_i64, _i32, _i32, _i32, _i32, _i32, _f32]),
     "mhc_wrapper_dynamic_bwd": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                                _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32,
                                                _f32, _f32, _vp]),

@@ -1356,6 +1356,12 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
     return w;
 }
 
+// The run-time-n backward keeps the stream rows X and dX (the last regions
+// of its workspace) only when the H_res rows of dP do not vanish.
+static size_t wgen_bwd_need(const WgenBwdWs& w, int32_t num_iters, float sinkhorn_eps) {
+    return wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? w.x_off : w.total;
+}
+
 static int wgen_dynamic_fwd(const void* residual, const void* branch, int32_t dtype, bool decay, const void* weight,
                             int32_t weight_dtype, const float* phi_pre, const float* phi_post, const float* phi_res,
                             const float* alpha_pre, const float* alpha_post, const float* alpha_res,
@@ -1418,8 +1424,9 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
                             void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
                             int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, hipStream_t s) {
     const WgenBwdWs w = wgen_bwd_ws(tokens, n, hidden, true);
-    if (!workspace || workspace_bytes < w.total)
-        return fail(MHC_ERR_WORKSPACE, "wrapper_dynamic_bwd: workspace smaller than mhc_wrapper_dynamic_bwd_workspace_size()");
+    if (!workspace || workspace_bytes < wgen_bwd_need(w, num_iters, sinkhorn_eps))
+        return fail(MHC_ERR_WORKSPACE,
+                    "wrapper_dynamic_bwd: workspace smaller than mhc_wrapper_dynamic_bwd_workspace_size_for()");
     char* ws = (char*)workspace;
     float* ep = (float*)(ws + w.ep_off);
     float* dw_part = (float*)(ws + w.dw_off);
@@ -1663,6 +1670,13 @@ size_t mhc_wrapper_dynamic_bwd_workspace_size(int64_t tokens, int32_t n, int32_t
                                               int32_t residual_mode) {
     if (tokens < 0 || n < 1 || hidden < 1) return 0;
     if (!wrap_fused4(n, hidden, true)) return wgen_bwd_ws(tokens, n, hidden, true).total;
+    return wrap_bwd_ws(tokens, n, hidden, dtype, true, residual_mode == MHC_WRAPPER_DECAY).total;
+}
+
+size_t mhc_wrapper_dynamic_bwd_workspace_size_for(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
+                                                  int32_t residual_mode, int32_t num_iters, float sinkhorn_eps) {
+    if (tokens < 0 || n < 1 || hidden < 1) return 0;
+    if (!wrap_fused4(n, hidden, true)) return wgen_bwd_need(wgen_bwd_ws(tokens, n, hidden, true), num_iters, sinkhorn_eps);
     return wrap_bwd_ws(tokens, n, hidden, dtype, true, residual_mode == MHC_WRAPPER_DECAY).total;
 }
 

@@ -47,7 +47,7 @@ using torch::autograd::tensor_list;
     X(mhc_wrapper_dynamic_saved_size)         \
     X(mhc_wrapper_dynamic_fwd_workspace_size) \
     X(mhc_wrapper_dynamic_fwd)                \
-    X(mhc_wrapper_dynamic_bwd_workspace_size) \
+    X(mhc_wrapper_dynamic_bwd_workspace_size_for) \
     X(mhc_wrapper_dynamic_bwd)                \
     X(mhc_wrapper_static_fwd)                 \
     X(mhc_wrapper_static_bwd_workspace_size)  \
@@ -449,7 +449,8 @@ struct DynamicWrapper : public torch::autograd::Function<DynamicWrapper> {
         Tensor galpha = at::empty({3}, f32);
         Tensor gbias = at::empty({np}, f32);
         const int dt = dtype_code(r.scalar_type());
-        const size_t wsb = lib.mhc_wrapper_dynamic_bwd_workspace_size(T, (int32_t)n, (int32_t)C, dt, mode);
+        const size_t wsb = lib.mhc_wrapper_dynamic_bwd_workspace_size_for(T, (int32_t)n, (int32_t)C, dt, mode,
+                                                                          (int32_t)cfg[2], (float)cfg[3]);
         Tensor ws = workspace(wsb, r);
         check(lib.mhc_wrapper_dynamic_bwd(fp(g), r.data_ptr(), b.data_ptr(), dt, mode, dtype_code(w.scalar_type()),
                                           fp(sv[4]), fp(sv[5]), fp(sv[6]), fp(sv[7]), fp(sv[8]), fp(sv[9]),

@@ -712,7 +712,8 @@ def wrapper_dynamic_bwd(grad_out: torch.Tensor, residual: torch.Tensor, branch: 
     galpha = torch.empty((3,), dtype=torch.float32, device=dev)
     gbias = torch.empty((np_,), dtype=torch.float32, device=dev)
     with _lib.on_device(dev):
-        wsb = _lib.load().mhc_wrapper_dynamic_bwd_workspace_size(T, n, C, dtype_code(r.dtype), mode)
+        wsb = _lib.load().mhc_wrapper_dynamic_bwd_workspace_size_for(T, n, C, dtype_code(r.dtype), mode,
+                                                                     int(sinkhorn_iters), float(sinkhorn_eps))
         ws = _ws(dev, wsb)
         call("mhc_wrapper_dynamic_bwd", ptr(g), ptr(r), ptr(b), dtype_code(r.dtype), mode, dtype_code(wdt), ptr(pp),
              ptr(pq), ptr(pr), ptr(a[0]), ptr(a[1]), ptr(a[2]), ptr(br), ptr(saved), ptr(gr), ptr(gb), ptr(gw),

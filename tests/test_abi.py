@@ -118,6 +118,23 @@ def test_expansion_rate_support_on_host():
     assert rc == -1 and b"null residual/branch/out" in lib.mhc_last_error()
 
 
+def test_wrapper_backward_workspace_for_settings_on_host():
+    """The settings-aware size query of the wrapper backward: with the H_res
+    rows of dP vanishing (num_iters >= 1, eps <= 1e-6) the run-time-n path
+    keeps no stream rows, so its size drops below the all-settings query;
+    otherwise (and for the n = 4 kernels' shapes) the two agree."""
+    lib = _lib.load()
+    for n, C in ((8, 7168), (2, 256), (4, 264), (5, 96)):
+        full = lib.mhc_wrapper_dynamic_bwd_workspace_size(4096, n, C, 1, 0)
+        assert lib.mhc_wrapper_dynamic_bwd_workspace_size_for(4096, n, C, 1, 0, 0, 1e-8) == full
+        assert lib.mhc_wrapper_dynamic_bwd_workspace_size_for(4096, n, C, 1, 0, 1, 0.1) == full
+        small = lib.mhc_wrapper_dynamic_bwd_workspace_size_for(4096, n, C, 1, 0, 20, 1e-8)
+        # X and dX: 8 n C bytes per token
+        assert full - small >= 8 * n * C * 4096, (n, C, full, small)
+    full = lib.mhc_wrapper_dynamic_bwd_workspace_size(4096, 4, 4096, 1, 0)
+    assert lib.mhc_wrapper_dynamic_bwd_workspace_size_for(4096, 4, 4096, 1, 0, 20, 1e-8) == full
+
+
 def test_cpu_tensors_raise_no_fallback():
     import mhc_ascend_amd as mhc
     x = torch.rand(2, 4, 4)
