@@ -322,6 +322,11 @@ int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dty
 
 size_t mhc_wrapper_dynamic_saved_size(int64_t tokens, int32_t n, int32_t hidden);
 size_t mhc_wrapper_dynamic_fwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden);
+/* The forward's workspace for the given storage dtype (the query above
+ * covers both): with bf16 storage the run-time-n path mostly rebuilds the
+ * streams inside its projection and keeps no stream rows.  No counterpart
+ * in the reference; for callers that size the workspace per call. */
+size_t mhc_wrapper_dynamic_fwd_workspace_size_for(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype);
 int mhc_wrapper_dynamic_fwd(const void* residual, const void* branch, int32_t dtype, int32_t residual_mode,
                             const void* weight, int32_t weight_dtype, const float* phi_pre, const float* phi_post,
                             const float* phi_res, const float* alpha_pre, const float* alpha_post,

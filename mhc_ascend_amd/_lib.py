@@ -87,6 +87,7 @@ SIGNATURES: Dict[str, Tuple[object, List[object]]] = {
                                              _f32, _vp]),
     "mhc_wrapper_dynamic_saved_size": (_sz, [_i64, _i32, _i32]),
     "mhc_wrapper_dynamic_fwd_workspace_size": (_sz, [_i64, _i32, _i32]),
+    "mhc_wrapper_dynamic_fwd_workspace_size_for": (_sz, [_i64, _i32, _i32, _i32]),
     "mhc_wrapper_dynamic_fwd": (ctypes.c_int, [_vp, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                                _vp, _vp, _vp, _vp, _vp, _sz, _i64, _i32, _i32, _i32, _f32, _f32,
                                                _vp]),

@@ -1283,20 +1283,34 @@ static bool wrap_res_grad_vanishes(int32_t num_iters, float sinkhorn_eps);
 // X [tokens, n*C] from wgen_synth_kernel, and the backward folds their dX
 // over the streams.
 //
-// dynamic forward workspace: [X (4 bytes per element: the size query has no
-// dtype) | the layer projection's workspace (proj_fwd_ws)]
+// dynamic forward workspace: [the layer projection's workspace (proj_fwd_ws)
+// | X], X only where the projection does not rebuild the streams itself
+// (wgen_fwd_direct); the all-dtypes size query reserves X at 4 bytes per
+// element.
 struct WgenFwdWs {
     ProjFwdWs p;
-    size_t p_base, total;
+    size_t x_off, total;
 };
 
 static WgenFwdWs wgen_fwd_ws(int64_t tokens, int32_t n, int32_t hidden) {
     WgenFwdWs w{};
     const int64_t K = (int64_t)n * hidden;
     w.p = proj_fwd_ws(tokens, K, 2 * n + n * n);
-    w.p_base = align256((size_t)tokens * K * sizeof(float));
-    w.total = w.p_base + w.p.total;
+    w.x_off = align256(w.p.total);
+    w.total = w.x_off + align256((size_t)tokens * K * sizeof(float));
     return w;
+}
+
+// bf16 rows of whole 64-channel stages, more than 32 projection rows and
+// at least 1024 tokens: the streaming projection reads residual and branch
+// and rebuilds the streams itself
+static bool wgen_fwd_direct(int32_t dtype, int32_t n, int32_t hidden, int64_t tokens) {
+    return proj_one_pass(dtype, 2 * n + n * n, tokens) && hidden % 64 == 0;
+}
+
+static size_t wgen_fwd_need(const WgenFwdWs& w, int32_t dtype, int32_t n, int32_t hidden, int64_t tokens) {
+    if (wgen_fwd_direct(dtype, n, hidden, tokens)) return w.p.total;
+    return w.x_off + align256((size_t)tokens * n * hidden * dtype_size(dtype));
 }
 
 // backward workspace: [per-token factors | dw partials | dw stage | ...]
@@ -1373,37 +1387,32 @@ static int wgen_dynamic_fwd(const void* residual, const void* branch, int32_t dt
     hipError_t e = launch_weight_f32(weight, weight_dtype, hidden, w32, s);
     if (e != hipSuccess || tokens == 0) return hip_status(e);
     const WgenFwdWs w = wgen_fwd_ws(tokens, n, hidden);
-    if (!workspace || workspace_bytes < w.total)
-        return fail(MHC_ERR_WORKSPACE, "wrapper_dynamic_fwd: workspace smaller than mhc_wrapper_dynamic_fwd_workspace_size()");
+    if (!workspace || workspace_bytes < wgen_fwd_need(w, dtype, n, hidden, tokens))
+        return fail(MHC_ERR_WORKSPACE,
+                    "wrapper_dynamic_fwd: workspace smaller than mhc_wrapper_dynamic_fwd_workspace_size_for()");
     const int64_t K = (int64_t)n * hidden;
     const int np = 2 * n + n * n;
-    char* pw = (char*)workspace + w.p_base;
+    char* pw = (char*)workspace;
+    void* X = (char*)workspace + w.x_off;
     float* pp = (float*)(pw + w.p.p_off);
     float* ss = (float*)(pw + w.p.ss_off);
-    // bf16 rows of whole 64-channel stages: the streaming projection reads
-    // residual and branch and rebuilds the streams itself
-    if (proj_one_pass(dtype, np, tokens) && hidden % 64 == 0) {
-        bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
+    bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
+    if (wgen_fwd_direct(dtype, n, hidden, tokens)) {
         e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
         if (e == hipSuccess)
             e = launch_proj_stream_wrap(decay, residual, branch, hidden, phib, np, pp, ss, tokens, K, w.p.ks, s);
     } else {
-        e = launch_wgen_synth(dtype, dtype, n, decay, residual, branch, workspace, tokens, hidden, s);
-    }
-    if (e == hipSuccess && !(proj_one_pass(dtype, np, tokens) && hidden % 64 == 0)) {
-        if (w.p.stream) {
-            e = launch_proj_stream(dtype, workspace, (bf16_raw_t*)(pw + w.p.xpl_off), phi_pre, phi_post, phi_res, n,
-                                   nullptr, np, pp, ss, tokens, K, w.p.ks, s);
-        } else if (proj_one_pass(dtype, np, tokens)) {
-            bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
+        e = launch_wgen_synth(dtype, dtype, n, decay, residual, branch, X, tokens, hidden, s);
+        if (e == hipSuccess && w.p.stream) {
+            e = launch_proj_stream(dtype, X, (bf16_raw_t*)(pw + w.p.xpl_off), phi_pre, phi_post, phi_res, n, nullptr,
+                                   np, pp, ss, tokens, K, w.p.ks, s);
+        } else if (e == hipSuccess) {
             e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
-            if (e == hipSuccess)
-                e = launch_proj_stream(dtype, workspace, nullptr, phi_pre, phi_post, phi_res, n, phib, np, pp, ss,
-                                       tokens, K, w.p.ks, s);
-        } else {
-            bf16_raw_t* phib = (bf16_raw_t*)(pw + w.p.phib_off);
-            e = launch_phi_split(phi_pre, phi_post, phi_res, n, np, K, phib, s);
-            if (e == hipSuccess) e = launch_proj_mfma(dtype, workspace, phib, np, pp, ss, tokens, K, w.p.ks, s);
+            if (e == hipSuccess && proj_one_pass(dtype, np, tokens))
+                e = launch_proj_stream(dtype, X, nullptr, phi_pre, phi_post, phi_res, n, phib, np, pp, ss, tokens, K,
+                                       w.p.ks, s);
+            else if (e == hipSuccess)
+                e = launch_proj_mfma(dtype, X, phib, np, pp, ss, tokens, K, w.p.ks, s);
         }
     }
     if (e == hipSuccess)
@@ -1562,6 +1571,13 @@ static WrapFwdWs wrap_fwd_ws(int64_t tokens, int32_t n, int32_t hidden) {
 size_t mhc_wrapper_dynamic_fwd_workspace_size(int64_t tokens, int32_t n, int32_t hidden) {
     if (tokens < 0 || n < 1 || hidden < 1) return 0;
     if (!wrap_fused4(n, hidden, true)) return wgen_fwd_ws(tokens, n, hidden).total;
+    return wrap_fwd_ws(tokens, n, hidden).total;
+}
+
+size_t mhc_wrapper_dynamic_fwd_workspace_size_for(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype) {
+    if (tokens < 0 || n < 1 || hidden < 1 || !valid_dtype(dtype)) return 0;
+    if (!wrap_fused4(n, hidden, true))
+        return wgen_fwd_need(wgen_fwd_ws(tokens, n, hidden), dtype, n, hidden, tokens);
     return wrap_fwd_ws(tokens, n, hidden).total;
 }
 

@@ -45,7 +45,7 @@ using torch::autograd::tensor_list;
     X(mhc_layer_dynamic_bwd_workspace_size)   \
     X(mhc_layer_dynamic_bwd)                  \
     X(mhc_wrapper_dynamic_saved_size)         \
-    X(mhc_wrapper_dynamic_fwd_workspace_size) \
+    X(mhc_wrapper_dynamic_fwd_workspace_size_for) \
     X(mhc_wrapper_dynamic_fwd)                \
     X(mhc_wrapper_dynamic_bwd_workspace_size_for) \
     X(mhc_wrapper_dynamic_bwd)                \
@@ -415,7 +415,8 @@ struct DynamicWrapper : public torch::autograd::Function<DynamicWrapper> {
         Tensor out = at::empty({T, C}, f32);
         Tensor saved =
             at::empty({(int64_t)(lib.mhc_wrapper_dynamic_saved_size(T, (int32_t)n, (int32_t)C) / 4)}, f32);
-        const size_t wsb = lib.mhc_wrapper_dynamic_fwd_workspace_size(T, (int32_t)n, (int32_t)C);
+        const size_t wsb = lib.mhc_wrapper_dynamic_fwd_workspace_size_for(T, (int32_t)n, (int32_t)C,
+                                                                          dtype_code(r.scalar_type()));
         Tensor ws = workspace(wsb, r);
         check(lib.mhc_wrapper_dynamic_fwd(r.data_ptr(), b.data_ptr(), dtype_code(r.scalar_type()), (int32_t)mode,
                                           w.data_ptr(), dtype_code(w.scalar_type()), fp(ph[0]), fp(ph[1]), fp(ph[2]),

@@ -678,7 +678,7 @@ def wrapper_dynamic_fwd(residual: torch.Tensor, branch: torch.Tensor, residual_m
     lib = _lib.load()
     saved = torch.empty((lib.mhc_wrapper_dynamic_saved_size(T, n, C) // 4,), dtype=torch.float32, device=dev)
     with _lib.on_device(dev):
-        wsb = lib.mhc_wrapper_dynamic_fwd_workspace_size(T, n, C)
+        wsb = lib.mhc_wrapper_dynamic_fwd_workspace_size_for(T, n, C, dtype_code(r.dtype))
         ws = _ws(dev, wsb)
         call("mhc_wrapper_dynamic_fwd", ptr(r), ptr(b), dtype_code(r.dtype), mode, ptr(w), dtype_code(w.dtype),
              ptr(pp), ptr(pq), ptr(pr), ptr(a[0]), ptr(a[1]), ptr(a[2]), ptr(bp), ptr(bq), ptr(br), ptr(out),

@@ -135,6 +135,26 @@ def test_wrapper_backward_workspace_for_settings_on_host():
     assert lib.mhc_wrapper_dynamic_bwd_workspace_size_for(4096, 4, 4096, 1, 0, 20, 1e-8) == full
 
 
+def test_wrapper_forward_workspace_for_dtype_on_host():
+    """The dtype-aware size query of the wrapper forward: bf16 rows the
+    projection rebuilds itself (n >= 5, >= 1024 tokens, hidden % 64 == 0)
+    keep no stream rows; other run-time-n shapes keep them in their own
+    dtype; the all-dtypes query covers every case."""
+    lib = _lib.load()
+    for n, C, T in ((8, 7168, 4096), (5, 128, 1100), (3, 96, 4096), (8, 96, 4096), (8, 7168, 512)):
+        full = lib.mhc_wrapper_dynamic_fwd_workspace_size(T, n, C)
+        f32 = lib.mhc_wrapper_dynamic_fwd_workspace_size_for(T, n, C, 0)
+        b16 = lib.mhc_wrapper_dynamic_fwd_workspace_size_for(T, n, C, 1)
+        assert b16 <= f32 <= full, (n, C, T, b16, f32, full)
+        direct = n >= 5 and T >= 1024 and C % 64 == 0
+        if direct:
+            assert f32 - b16 >= 4 * n * C * T, (n, C, T)
+        else:
+            assert f32 - b16 >= 2 * n * C * T - 256, (n, C, T)
+    full = lib.mhc_wrapper_dynamic_fwd_workspace_size(4096, 4, 4096)
+    assert lib.mhc_wrapper_dynamic_fwd_workspace_size_for(4096, 4, 4096, 1) == full
+
+
 def test_cpu_tensors_raise_no_fallback():
     import mhc_ascend_amd as mhc
     x = torch.rand(2, 4, 4)
