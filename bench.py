@@ -364,6 +364,7 @@ class WrapperWorkload:
 
     def __init__(self, torch, mhc, device):
         self.torch = torch
+        self.mhc = mhc
         Bo, T, n, C = self.Bo, self.T, self.n, self.C
         nC = n * C
         g = torch.Generator(device=device).manual_seed(0)
@@ -499,9 +500,47 @@ class Wrapper8Workload(WrapperWorkload):
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
-        return {"ms_per_step": (time.perf_counter() - t0) * 1e3 / steps, "steps": steps,
-                "path": "torch.zeros + slice copies + decay products (layer.py:299-310), MHCLayer on [tokens, 8, C], "
-                        "mean over streams; fwd+bwd through autograd"}
+        rec = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / steps, "steps": steps,
+               "path": "torch.zeros + slice copies + decay products (layer.py:299-310), MHCLayer on [tokens, 8, C], "
+                       "mean over streams; fwd+bwd through autograd"}
+        rec["static_h"] = self.static_ab(steps)
+        return rec
+
+    def static_ab(self, steps):
+        """The same A/B with static H (use_dynamic_h=False): the fused
+        run-time-n wrapper against the tensor-op streams through the layer,
+        ms per fwd+bwd step on the same inputs."""
+        torch, mhc = self.torch, self.mhc
+        torch.manual_seed(0)
+        wrap = mhc.MHCResidualWrapper(self.C, self.n, use_dynamic_h=False).to(self.rs[0].device)
+        layer = wrap.mhc
+        params = list(wrap.parameters())
+
+        def fused(k):
+            out = wrap(self.rs[k], self.bs[k])
+            return torch.autograd.grad(out, [self.rs[k], self.bs[k]] + params, self.gs[k])
+
+        def unfused(k):
+            r, b = self.rs[k].reshape(-1, self.C), self.bs[k].reshape(-1, self.C)
+            X = torch.zeros(r.shape[0], self.n, self.C, device=r.device, dtype=r.dtype)
+            X[:, 0] = r
+            X[:, 1] = b
+            for i in range(2, self.n):
+                X[:, i] = r * (0.1 ** (i - 1))
+            out = layer(X).mean(dim=1).view(self.rs[k].shape)
+            return torch.autograd.grad(out, [self.rs[k], self.bs[k]] + params, self.gs[k])
+
+        res = {}
+        for name, fn in (("fused_ms_per_step", fused), ("unfused_ms_per_step", unfused)):
+            for i in range(2):
+                fn(i % self.sets)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(steps):
+                fn(i % self.sets)
+            torch.cuda.synchronize()
+            res[name] = (time.perf_counter() - t0) * 1e3 / steps
+        return res
 
 
 class OpsWorkload:
