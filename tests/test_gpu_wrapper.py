@@ -288,3 +288,21 @@ def test_wrapper_runtime_n_many_tokens(device, n, mode):
     want = _oracle(wrap, res, br, grad, mode)
     got = _run(wrap, res, br, grad, device)
     _check(got, want, torch.bfloat16, DYN, f"n={n} B={B} {mode}")
+
+
+@pytest.mark.parametrize("n,dynamic", [(3, True), (7, True), (5, False), (8, False)])
+@pytest.mark.parametrize("tokens", [1, 2, 17])
+def test_wrapper_runtime_n_few_tokens(device, n, dynamic, tokens):
+    """The run-time-n kernels on 1, 2 and 17 tokens (one wave per token in
+    the row passes; token tiles of one or two tokens in the backward) against
+    the float64 oracle, every gradient."""
+    C = 96
+    seed = 3000 + 10 * n + tokens + (7 if dynamic else 0)
+    wrap = _make(C, dynamic, seed, n=n)
+    g = _gen(seed + 2)
+    res = torch.randn(tokens, C, generator=g).to(torch.bfloat16)
+    br = torch.randn(tokens, C, generator=g).to(torch.bfloat16)
+    grad = torch.randn(tokens, C, generator=g)
+    want = _oracle(wrap, res, br, grad, "decay")
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, torch.bfloat16, DYN if dynamic else STA, f"n={n} tokens={tokens} dyn={dynamic}")
