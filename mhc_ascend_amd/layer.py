@@ -141,9 +141,12 @@ class MHCResidualWrapper(nn.Module):
     T > 1 and as [B*T, C] otherwise (layer.py:319-320).  ``use_post_norm``
     is accepted and ignored, as in the reference (layer.py:261).
 
-    All of it runs as one fused pass per direction (ops.mhc_residual_wrapper):
-    the [B*T, n, C] stream tensor of layer.py:299-310 and the layer's
-    [B*T, n, C] output are never materialised.
+    For n = 2..8 and hidden % 4 == 0 it runs fused (ops.mhc_residual_wrapper):
+    the layer's [B*T, n, C] output is never materialised, and the stream
+    tensor of layer.py:299-310 only where the dynamic projection needs it
+    (n != 4 with fp32 storage, fewer than 1024 tokens or hidden % 64 != 0,
+    and Sinkhorn settings that keep the H_res gradients).  Other shapes
+    build the streams with tensor ops and run the layer.
     """
 
     def __init__(self, hidden_dim: int, expansion_rate: int = 4, residual_mode: str = 'decay',

@@ -90,8 +90,8 @@ def test_expansion_rate_support_on_host():
     fixed-n kernels for {2, 4, 8, 16, 32}, the generic kernels for the rest,
     dynamic H included (its 2n + n^2 projection rows run as 32-row output
     tiles or, above 128 rows, the streaming kernels); n > 64 is rejected.
-    The fused wrapper is n = 4 (other n go through the layer).  All checked
-    before any device work."""
+    The fused wrapper takes n = 2..8 (other n go through the layer).  All
+    checked before any device work."""
     lib = _lib.load()
     # static layer: these n pass the host checks; with a null x they fail on that
     for n in (1, 2, 3, 6, 8, 12, 16, 32, 64):
