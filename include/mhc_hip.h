@@ -301,8 +301,9 @@ int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dty
  * X_i = residual * 0.1^(i-1) rounded to dtype (MHC_WRAPPER_DECAY,
  * layer.py:306-308) or 0 (MHC_WRAPPER_ZERO); the mHC layer on X; the mean
  * over the n streams (layer.py:316) -> out [tokens, hidden] fp32.
- * n = 2..8 and hidden % 4 == 0; with dynamic H also n * hidden % 32 == 0
- * (others return MHC_ERR_UNSUPPORTED).  The row passes rebuild X from
+ * hidden % 4 == 0 and n = 2..32 with static H, n = 2..8 with dynamic H,
+ * which also needs n * hidden % 32 == 0 (others return
+ * MHC_ERR_UNSUPPORTED).  The row passes rebuild X from
  * residual and branch in registers, so with static H, and with dynamic H at
  * n = 4 and hidden % 32 == 0 (whose projection kernels rebuild it too), X
  * never exists in memory.  For the other dynamic-H shapes the projection

@@ -1253,15 +1253,17 @@ static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidd
     if (!valid_dtype(dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": dtype must be F32 or BF16");
     // the reference writes stream 1 (layer.py:301), which needs n >= 2
     if (n < 2) return fail(MHC_ERR_INVALID, std::string(fn) + ": n must be >= 2 (stream 1 holds the branch)");
-    if (n > kWgMaxN)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper takes n <= " + std::to_string(kWgMaxN));
+    const int n_max = dynamic ? kWgMaxN : kWgMaxNStatic;
+    if (n > n_max)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper takes n <= " + std::to_string(n_max) +
+                                             (dynamic ? " with dynamic H" : " with static H"));
     if (hidden % 4 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper needs hidden % 4 == 0");
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (mode != MHC_WRAPPER_DECAY && mode != MHC_WRAPPER_ZERO)
         return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");
     if (!wrap_fused4(n, hidden, dynamic)) {
-        if (!wgen_supported(n, hidden))
+        if (!wgen_supported(n, hidden, dynamic))
             return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the wrapper kernels");
         if (dynamic && ((int64_t)n * hidden) % 32 != 0)
             return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
@@ -1477,9 +1479,9 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
                 e = launch_column_finalize(0, kF32, part, w.qtiles, (int64_t)rows * K, stp, grad_phi, nullptr, 0,
                                            nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
             if (e == hipSuccess)
-                e = launch_wgen_dx_fold(dtype, n, decay, grad_out, residual, branch, w32, ep, dp, dp_stride(np), rows,
-                                        stok, phi_pre, phi_post, grad_residual, grad_branch, dw_part, w.ftiles,
-                                        tokens, hidden, s);
+                e = launch_wgen_dx_fold(dtype, n, decay, grad_out, residual, branch, w32, saved + d.coef_off, np, ep,
+                                        dp, dp_stride(np), rows, stok, phi_pre, phi_post, grad_residual,
+                                        grad_branch, dw_part, w.ftiles, tokens, hidden, s);
         }
         if (!fold && e == hipSuccess) e = launch_wgen_synth(dtype, kF32, n, decay, residual, branch, X, tokens, hidden, s);
         if (!fold && e == hipSuccess) {
@@ -1495,8 +1497,8 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
             }
         }
         if (!fold && e == hipSuccess)
-            e = launch_wgen_dx(dtype, n, decay, grad_out, residual, branch, w32, ep, dX, stok, grad_residual,
-                               grad_branch, dw_part, w.dtiles, tokens, hidden, s);
+            e = launch_wgen_dx(dtype, n, decay, grad_out, residual, branch, w32, saved + d.coef_off, np, ep, dX, stok,
+                               grad_residual, grad_branch, dw_part, w.dtiles, tokens, hidden, s);
     }
     if (e == hipSuccess)
         e = launch_column_finalize(0, weight_dtype, dw_part, rows_w, hidden, stw, grad_weight, nullptr, 0, nullptr,
@@ -1540,8 +1542,8 @@ static int wgen_static_bwd(const float* grad_out, const void* residual, const vo
                             rmsnorm_eps, s);
         if (e == hipSuccess) e = launch_small_column_sum(scal, w.srows, ns, ssum, ssum, ns, s);
         if (e == hipSuccess)
-            e = launch_wgen_dx(dtype, n, decay, grad_out, residual, branch, w32, ep, nullptr, nullptr, grad_residual,
-                               grad_branch, dw_part, w.dtiles, tokens, hidden, s);
+            e = launch_wgen_dx(dtype, n, decay, grad_out, residual, branch, w32, saved, 0, ep, nullptr, nullptr,
+                               grad_residual, grad_branch, dw_part, w.dtiles, tokens, hidden, s);
     }
     if (e == hipSuccess)
         e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stw, grad_weight, ssum, 1, h_pre, h_post,

@@ -406,12 +406,13 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
                                 bool res_rows, hipStream_t s);
 
 // ---- wrapper_gen.hip -------------------------------------------------------
-// MHCResidualWrapper for n = 2..8 with n at run time (the shapes the n = 4
-// kernels above do not take); hidden % 4 == 0.
-constexpr int kWgMaxN = 8;
+// MHCResidualWrapper for n = 2..8 (dynamic H) or 2..32 (static H) with n at
+// run time (the shapes the n = 4 kernels above do not take); hidden % 4 == 0.
+constexpr int kWgMaxN = 8;          // dynamic H
+constexpr int kWgMaxNStatic = 32;   // static H
 // Floats per token of the per-token factors of d r / d b.
-constexpr int kWgEp = 16;
-bool wgen_supported(int n, int64_t C);
+constexpr int kWgEp = 8;
+bool wgen_supported(int n, int64_t C, bool dynamic);
 hipError_t launch_wgen_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
                            const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
                            hipStream_t s);
@@ -428,8 +429,9 @@ int wgen_dx_tiles(int64_t B, int64_t C);
 // and s_tok (the r_h term's s per token) with dynamic H, both null with
 // static H.
 hipError_t launch_wgen_dx(int dt, int n, bool decay, const float* g, const void* res, const void* br,
-                          const float* w, const float* ep, const float* dX, const float* s_tok, void* dres, void* dbr,
-                          float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s);
+                          const float* w, const float* coef, int64_t coef_stride, const float* ep, const float* dX,
+                          const float* s_tok, void* dres, void* dbr, float* dw_part, int tiles, int64_t B, int64_t C,
+                          hipStream_t s);
 // The projection backward over the pre / post rows (rows = 2n) without the
 // stream rows: dPhi partials dphi_part[tiles][rows][n*C] (tiles from
 // wgen_dphi_tiles), and d r / d b with dP . Phi folded over the streams
@@ -440,7 +442,8 @@ hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const vo
                             hipStream_t s);
 int wgen_fold_tiles(int64_t B, int64_t C);
 hipError_t launch_wgen_dx_fold(int dt, int n, bool decay, const float* g, const void* res, const void* br,
-                               const float* w, const float* ep, const float* dP, int dp_stride, int rows,
+                               const float* w, const float* coef, int64_t coef_stride, const float* ep,
+                               const float* dP, int dp_stride, int rows,
                                const float* s_tok, const float* phi_pre, const float* phi_post, void* dres,
                                void* dbr, float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s);
 // X[B][n*C] in out_dt (kF32, or the storage dtype dt).

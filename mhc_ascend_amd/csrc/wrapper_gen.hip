@@ -1,13 +1,14 @@
 // MHCResidualWrapper for the shapes the n = 4 kernels of wrapper.hip do not
-// take: expansion rates 2..8, and n = 4 rows those kernels refuse; any
-// hidden % 4 == 0 (layer.py:269-322).
+// take: expansion rates 2..8 with dynamic H, 2..32 with static H, and n = 4
+// rows those kernels refuse; any hidden % 4 == 0 (layer.py:269-322).
 //
 // The streams are rebuilt from r and b wherever a row pass needs them
 // (X_0 = r, X_1 = b, X_j = r * 0.1^(j-1) rounded to the storage dtype in
 // 'decay' mode, 0 in 'zero' mode: layer.py:299-310), with n taken at run
-// time: per-stream arrays have a compile-time capacity NM in {2, 4, 8} and
-// their loops run over it with a uniform j < n test, so nothing is indexed
-// at run time in registers.  The math is that of wrapper.hip:
+// time: per-stream arrays have a compile-time capacity NM in {2, 4, 8}
+// (also 16 and 32 for the static-H kernels) and their loops run over it
+// with a uniform j < n test, so nothing is indexed at run time in
+// registers.  The math is that of wrapper.hip:
 //   forward   out = hs (xa / r) w + sum_j cm_j X_j,  xa = sum_j h_pre_j X_j,
 //             r = sqrt(mean_c xa^2 + eps),  hs = (1/n) sum_i h_post_i,
 //             cm_j = (1/n) sum_i M_ij  (the stream mean of layer.py:316)
@@ -48,14 +49,13 @@ constexpr double wg_pow01(int e) { return e <= 0 ? 1.0 : 0.1 * wg_pow01(e - 1); 
 // Decay multiplier of stream j >= 2: Python's 0.1 ** (j - 1) as fp32 (the
 // product r * m is formed in fp32 by the reference's mul; the double
 // repeated product rounds to the same fp32 value as 0.1 ** e for e <= 63).
-constexpr float kWgMult[kWgMaxN] = {1.f,
-                                    0.f,
-                                    (float)wg_pow01(1),
-                                    (float)wg_pow01(2),
-                                    (float)wg_pow01(3),
-                                    (float)wg_pow01(4),
-                                    (float)wg_pow01(5),
-                                    (float)wg_pow01(6)};
+#define MHC_WG_M(e) (float)wg_pow01(e)
+constexpr float kWgMult[kWgMaxNStatic] = {
+    1.f,          0.f,          MHC_WG_M(1),  MHC_WG_M(2),  MHC_WG_M(3),  MHC_WG_M(4),  MHC_WG_M(5),  MHC_WG_M(6),
+    MHC_WG_M(7),  MHC_WG_M(8),  MHC_WG_M(9),  MHC_WG_M(10), MHC_WG_M(11), MHC_WG_M(12), MHC_WG_M(13), MHC_WG_M(14),
+    MHC_WG_M(15), MHC_WG_M(16), MHC_WG_M(17), MHC_WG_M(18), MHC_WG_M(19), MHC_WG_M(20), MHC_WG_M(21), MHC_WG_M(22),
+    MHC_WG_M(23), MHC_WG_M(24), MHC_WG_M(25), MHC_WG_M(26), MHC_WG_M(27), MHC_WG_M(28), MHC_WG_M(29), MHC_WG_M(30)};
+#undef MHC_WG_M
 
 template <typename TX>
 __device__ __forceinline__ float wg_round(float v) {
@@ -80,12 +80,33 @@ __device__ __forceinline__ float wg_rweight(int j) {
     return j == 0 ? 1.f : (j == 1 ? 0.f : (DECAY ? kWgMult[j] : 0.f));
 }
 
-// h_pre, cm = (1/n) column sums of M and hs = (1/n) sum h_post of one token.
+// h_pre, cm = (1/n) column sums of M and hs = (1/n) sum h_post of one token
+// (every lane of the wave calls it with the same cf).
 template <int NM>
 __device__ __forceinline__ void wg_coefs(const float* __restrict__ cf, int n, float (&hp)[NM], float (&cm)[NM],
                                          float& hs) {
     const float inv_n = 1.f / (float)n;
     hs = 0.f;
+    if constexpr (NM > 8) {
+        // lane j sums column j of M (n loads a lane instead of n^2
+        // unrolled ones), then the wave reads the n values back
+        const int lane = threadIdx.x & (kWave - 1);
+        float hl = 0.f, cl = 0.f;
+        if (lane < n) {
+            hl = cf[lane];
+            float sc = 0.f;
+            for (int i = 0; i < n; ++i) sc += cf[2 * n + i * n + lane];
+            cl = sc * inv_n;
+        }
+        for (int i = 0; i < n; ++i) hs += cf[n + i];
+        hs *= inv_n;
+#pragma unroll
+        for (int j = 0; j < NM; ++j) {
+            hp[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hl), j));
+            cm[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cl), j));
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NM; ++j) {
         hp[j] = 0.f;
@@ -197,9 +218,12 @@ __global__ __launch_bounds__(256) void wgen_fwd_kernel(const TX* __restrict__ re
 // coefficient backward's scalars (dM_ij = u_j / n, dh_post_act_i =
 // gwx / (n r), dh_pre_act_j = hs v_j / r - k2 z_j, then 1/r and k2): per
 // token in scal_out[b][n*n+2n+2] (dynamic H), or (STATIC) summed over the
-// tokens each wave takes (grid stride) into scal_out[wave][n*n+2n].  Both
-// write the per-token factors of d r / d b, ep_out[b][kWgEp]:
-//   [A_r, B_r hs/r, A_b, B_b hs/r, hs/r, -B_r k2, -B_b k2, 0, h_pre_0..7]
+// tokens each wave takes (grid stride) into scal_out[wave][n*n+2n]; the
+// static sums are kept per stream (lane j: sum u_j / n and sum dh_pre_act_j,
+// every lane: sum dh_post_act), since dM_ij does not depend on i, and
+// spread over the n*n+2n slots once per wave.  Both write the per-token
+// factors of d r / d b, ep_out[b][kWgEp]:
+//   [A_r, B_r hs/r, A_b, B_b hs/r, hs/r, -B_r k2, -B_b k2, 0]
 // with A_r = sum_j w_j cm_j, B_r = sum_j w_j h_pre_j, A_b = cm_1,
 // B_b = h_pre_1, so that d r = A_r G + B_r gxa and d b = A_b G + B_b gxa.
 // ---------------------------------------------------------------------------
@@ -210,26 +234,29 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
                                                        float* __restrict__ scal_out, float* __restrict__ ep_out,
                                                        int64_t B, int C, int n, float eps) {
     constexpr int NR = 2 + 3 * NM;
+    constexpr int U = NM > 8 ? 2 : kWgU;  // chunks in flight beside NR sums
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t wid = (int64_t)blockIdx.x * (blockDim.x / kWave) + (int64_t)wave_uniform(threadIdx.x / kWave);
     const int64_t nw = STATIC ? (int64_t)gridDim.x * (blockDim.x / kWave) : B;
     const int NS = n * n + 2 * n;
     const float inv_n = 1.f / (float)n;
     const int nq = C / 4;
-    float acc0 = 0.f, acc1 = 0.f;  // STATIC: slots lane and lane + 64
+    float acc_u = 0.f, acc_pre = 0.f, acc_post = 0.f;  // STATIC sums
+    // STATIC: one coefficient set for every token (coef_stride unused)
+    float hp[NM], cm[NM], hs;
+    if constexpr (STATIC) wg_coefs<NM>(coef, n, hp, cm, hs);
     for (int64_t b = wid; b < B; b += nw) {
-        float hp[NM], cm[NM], hs;
-        wg_coefs<NM>(coef + b * coef_stride, n, hp, cm, hs);
+        if constexpr (!STATIC) wg_coefs<NM>(coef + b * coef_stride, n, hp, cm, hs);
         float rs[NR];
 #pragma unroll
         for (int q = 0; q < NR; ++q) rs[q] = 0.f;
         const float* gb = g + b * (int64_t)C;
         const TX* rb = res + b * (int64_t)C;
         const TX* bb = br + b * (int64_t)C;
-        for (int q0 = 0; q0 < nq; q0 += kWgU * kWave) {
-            float gv[kWgU][4], wv[kWgU][4], rv[kWgU][4], bv[kWgU][4];
+        for (int q0 = 0; q0 < nq; q0 += U * kWave) {
+            float gv[U][4], wv[U][4], rv[U][4], bv[U][4];
 #pragma unroll
-            for (int u = 0; u < kWgU; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int q = q0 + u * kWave + lane;
                 const int c0 = (q < nq ? q : 0) * 4;
                 load_run_nt<float, 4>(gb + c0, gv[u]);
@@ -238,7 +265,7 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
                 load_run<TX, 4>(bb + c0, bv[u]);
             }
 #pragma unroll
-            for (int u = 0; u < kWgU; ++u) {
+            for (int u = 0; u < U; ++u) {
                 if (q0 + u * kWave + lane >= nq) continue;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -264,40 +291,46 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
         const float inv = 1.f / sqrtf(rs[0] / (float)C + eps);
         const float gwx = rs[1];
         const float k2 = hs * gwx * inv * inv * inv / (float)C;
-        auto slot = [&](int t) __attribute__((always_inline)) {
-            float v = 0.f;
-            if (t < n * n) {
-                const int j = t % n;
-                float u = 0.f;
-#pragma unroll
-                for (int jj = 0; jj < NM; ++jj) u = (jj == j) ? rs[2 + jj] : u;
-                v = u * inv_n;  // dM_ij = u_j / n
-            } else if (t < n * n + n) {
-                v = gwx * inv * inv_n;  // dh_post_act_i
-            } else if (t < NS) {
-                const int j = t - n * n - n;
-                float vv = 0.f, zz = 0.f;
-#pragma unroll
-                for (int jj = 0; jj < NM; ++jj) {
-                    vv = (jj == j) ? rs[2 + NM + jj] : vv;
-                    zz = (jj == j) ? rs[2 + 2 * NM + jj] : zz;
-                }
-                v = hs * inv * vv - k2 * zz;  // dh_pre_act_j
-            } else if (t == NS) {
-                v = inv;
-            } else if (t == NS + 1) {
-                v = k2;
-            }
-            return v;
-        };
-        const float v0 = slot(lane), v1 = slot(lane + kWave);
         if constexpr (STATIC) {
-            if (lane < NS) acc0 += v0;
-            if (lane + kWave < NS) acc1 += v1;
+            float uu = 0.f, vv = 0.f, zz = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < NM; ++jj) {
+                uu = (jj == lane) ? rs[2 + jj] : uu;
+                vv = (jj == lane) ? rs[2 + NM + jj] : vv;
+                zz = (jj == lane) ? rs[2 + 2 * NM + jj] : zz;
+            }
+            acc_u += uu * inv_n;                // dM_ij = u_j / n
+            acc_pre += hs * inv * vv - k2 * zz;  // dh_pre_act_j
+            acc_post += gwx * inv * inv_n;      // dh_post_act_i
         } else {
+            auto slot = [&](int t) __attribute__((always_inline)) {
+                float v = 0.f;
+                if (t < n * n) {
+                    const int j = t % n;
+                    float u = 0.f;
+#pragma unroll
+                    for (int jj = 0; jj < NM; ++jj) u = (jj == j) ? rs[2 + jj] : u;
+                    v = u * inv_n;  // dM_ij = u_j / n
+                } else if (t < n * n + n) {
+                    v = gwx * inv * inv_n;  // dh_post_act_i
+                } else if (t < NS) {
+                    const int j = t - n * n - n;
+                    float vv = 0.f, zz = 0.f;
+#pragma unroll
+                    for (int jj = 0; jj < NM; ++jj) {
+                        vv = (jj == j) ? rs[2 + NM + jj] : vv;
+                        zz = (jj == j) ? rs[2 + 2 * NM + jj] : zz;
+                    }
+                    v = hs * inv * vv - k2 * zz;  // dh_pre_act_j
+                } else if (t == NS) {
+                    v = inv;
+                } else if (t == NS + 1) {
+                    v = k2;
+                }
+                return v;
+            };
             float* so = scal_out + b * (int64_t)(NS + 2);
-            if (lane < NS + 2) so[lane] = v0;
-            if (lane + kWave < NS + 2) so[lane + kWave] = v1;
+            for (int t = lane; t < NS + 2; t += kWave) so[t] = slot(t);
         }
         float a_r = cm[0], b_r = hp[0];
 #pragma unroll
@@ -318,17 +351,22 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
         rec[5] = -b_r * k2;
         rec[6] = -b_b * k2;
         rec[7] = 0.f;
-#pragma unroll
-        for (int j = 0; j < kWgMaxN; ++j) rec[8 + j] = j < NM ? hp[j < NM ? j : 0] : 0.f;
         float ev = 0.f;
 #pragma unroll
         for (int k = 0; k < kWgEp; ++k) ev = (lane == k) ? rec[k] : ev;
         if (lane < kWgEp) ep_out[b * kWgEp + lane] = ev;
     }
     if constexpr (STATIC) {
+        // slots [dM (n x n) | dh_post_act (n) | dh_pre_act (n)]; the
+        // trip count is uniform, so every lane takes part in the shuffles
         float* so = scal_out + wid * (int64_t)NS;
-        if (lane < NS) so[lane] = acc0;
-        if (lane + kWave < NS) so[lane + kWave] = acc1;
+        for (int t0 = 0; t0 < NS; t0 += kWave) {
+            const int t = t0 + lane;
+            const int src = t < n * n ? t % n : (t < n * n + n ? 0 : t - n * n - n);
+            const float vu = __shfl(acc_u, src);
+            const float vp = __shfl(acc_pre, src);
+            if (t < NS) so[t] = t < n * n ? vu : (t < n * n + n ? acc_post : vp);
+        }
     }
 }
 
@@ -343,6 +381,7 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
 template <typename TX, int NM, bool DECAY, bool DYN>
 __global__ __launch_bounds__(256) void wgen_dx_kernel(const float* __restrict__ g, const TX* __restrict__ res,
                                                       const TX* __restrict__ br, const float* __restrict__ w,
+                                                      const float* __restrict__ coef, int64_t coef_stride,
                                                       const float* __restrict__ ep, const float* __restrict__ dX,
                                                       const float* __restrict__ s_tok, TX* __restrict__ dres,
                                                       TX* __restrict__ dbr, float* __restrict__ dw_part, int64_t B,
@@ -357,9 +396,10 @@ __global__ __launch_bounds__(256) void wgen_dx_kernel(const float* __restrict__ 
     for (int64_t b = t0; b < t1; ++b) {
         const float* e = ep + b * kWgEp;
         const float e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3], e4 = e[4], e5 = e[5], e6 = e[6];
+        const float* cf = coef + b * coef_stride;
         float hp[NM];
 #pragma unroll
-        for (int j = 0; j < NM; ++j) hp[j] = e[8 + j];
+        for (int j = 0; j < NM; ++j) hp[j] = j < n ? cf[j] : 0.f;
         const float sv = DYN ? s_tok[b] : 0.f;
         if (!active) continue;
         const int64_t o = b * (int64_t)C + c0;
@@ -574,7 +614,8 @@ __global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restric
 template <typename TX, int NM, bool DECAY>
 __global__ __launch_bounds__(256) void wgen_dx_fold_kernel(
     const float* __restrict__ g, const TX* __restrict__ res, const TX* __restrict__ br, const float* __restrict__ w,
-    const float* __restrict__ ep, const float* __restrict__ dP, int dp_stride, int rows,
+    const float* __restrict__ coef, int64_t coef_stride, const float* __restrict__ ep, const float* __restrict__ dP,
+    int dp_stride, int rows,
     const float* __restrict__ s_tok, const float* __restrict__ phi_pre, const float* __restrict__ phi_post,
     TX* __restrict__ dres, TX* __restrict__ dbr, float* __restrict__ dw_part, int64_t B, int C, int n,
     int64_t tile) {
@@ -610,9 +651,10 @@ __global__ __launch_bounds__(256) void wgen_dx_fold_kernel(
     for (int64_t b = t0; b < t1; ++b) {
         const float* e = ep + b * kWgEp;
         const float e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3], e4 = e[4], e5 = e[5], e6 = e[6];
+        const float* cf = coef + b * coef_stride;
         float hp[NM];
 #pragma unroll
-        for (int j = 0; j < NM; ++j) hp[j] = e[8 + j];
+        for (int j = 0; j < NM; ++j) hp[j] = j < n ? cf[j] : 0.f;
         const float sv = s_tok[b];
         const float* d = dP + b * dp_stride;
         float dv[kWgRows];
@@ -692,8 +734,11 @@ __global__ __launch_bounds__(256) void wgen_synth_kernel(const TX* __restrict__ 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-bool wgen_supported(int n, int64_t C) { return n >= 2 && n <= kWgMaxN && C >= 4 && C % 4 == 0 && C <= (1 << 28); }
+bool wgen_supported(int n, int64_t C, bool dynamic) {
+    return n >= 2 && n <= (dynamic ? kWgMaxN : kWgMaxNStatic) && C >= 4 && C % 4 == 0 && C <= (1 << 28);
+}
 
+// capacities of the kernels with dynamic H (n <= 8)
 #define MHC_WG_NM(n, ...)                   \
     if ((n) <= 2) {                         \
         constexpr int NM_ = 2; __VA_ARGS__; \
@@ -703,28 +748,40 @@ bool wgen_supported(int n, int64_t C) { return n >= 2 && n <= kWgMaxN && C >= 4 
         constexpr int NM_ = 8; __VA_ARGS__; \
     }
 
+// capacities of the kernels static H also runs (n <= 32)
+#define MHC_WG_NM_WIDE(n, ...)               \
+    if ((n) <= 8) {                          \
+        MHC_WG_NM(n, __VA_ARGS__)            \
+    } else if ((n) <= 16) {                  \
+        constexpr int NM_ = 16; __VA_ARGS__; \
+    } else {                                 \
+        constexpr int NM_ = 32; __VA_ARGS__; \
+    }
+
 // dt x decay x capacity dispatch of one kernel template K<TX, NM, DECAY, ...>
-#define MHC_WG_DISPATCH(dt, decay, n, LAUNCH)                                  \
+#define MHC_WG_DISPATCH_BY(NMX, dt, decay, n, ...)                            \
     if ((dt) == kBF16) {                                                       \
         using TX_ = bf16_t;                                                    \
-        if (decay) { constexpr bool D_ = true; MHC_WG_NM(n, LAUNCH); }         \
-        else { constexpr bool D_ = false; MHC_WG_NM(n, LAUNCH); }              \
+        if (decay) { constexpr bool D_ = true; NMX(n, __VA_ARGS__); }          \
+        else { constexpr bool D_ = false; NMX(n, __VA_ARGS__); }               \
     } else {                                                                   \
         using TX_ = float;                                                     \
-        if (decay) { constexpr bool D_ = true; MHC_WG_NM(n, LAUNCH); }         \
-        else { constexpr bool D_ = false; MHC_WG_NM(n, LAUNCH); }              \
+        if (decay) { constexpr bool D_ = true; NMX(n, __VA_ARGS__); }          \
+        else { constexpr bool D_ = false; NMX(n, __VA_ARGS__); }               \
     }
+#define MHC_WG_DISPATCH(dt, decay, n, ...) MHC_WG_DISPATCH_BY(MHC_WG_NM, dt, decay, n, __VA_ARGS__)
+#define MHC_WG_DISPATCH_WIDE(dt, decay, n, ...) MHC_WG_DISPATCH_BY(MHC_WG_NM_WIDE, dt, decay, n, __VA_ARGS__)
 
 hipError_t launch_wgen_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
                            const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
                            hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C)) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C, false)) return hipErrorInvalidValue;
     const int64_t blocks = (B + 3) / 4;  // one token per wave
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const int Ci = (int)C;
     const int tok = timing_begin("wrap_fwd", s);
-    MHC_WG_DISPATCH(dt, decay, n,
+    MHC_WG_DISPATCH_WIDE(dt, decay, n,
                     MHC_LAUNCH_GGL((wgen_fwd_kernel<TX_, NM_, D_>), dim3((unsigned)blocks), dim3(256), 0, s,
                                    (const TX_*)res, (const TX_*)br, w, coef, coef_stride, out, B, Ci, n, eps));
     timing_end(tok, s);
@@ -743,13 +800,13 @@ hipError_t launch_wgen_red(int dt, int n, bool decay, bool stat, const float* g,
                            const float* w, const float* coef, int64_t coef_stride, float* scal_out, float* ep_out,
                            int64_t B, int64_t C, float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C)) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C, !stat)) return hipErrorInvalidValue;
     const int64_t blocks = stat ? wgen_red_static_grid(B) : (B + 3) / 4;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const int Ci = (int)C;
     const int tok = timing_begin("wrap_bwd_reduce", s);
     if (stat) {
-        MHC_WG_DISPATCH(dt, decay, n,
+        MHC_WG_DISPATCH_WIDE(dt, decay, n,
                         MHC_LAUNCH_GGL((wgen_red_kernel<TX_, NM_, D_, true>), dim3((unsigned)blocks), dim3(256), 0, s,
                                        g, (const TX_*)res, (const TX_*)br, w, coef, coef_stride, scal_out, ep_out, B,
                                        Ci, n, eps));
@@ -774,25 +831,26 @@ int wgen_dx_tiles(int64_t B, int64_t C) {
 }
 
 hipError_t launch_wgen_dx(int dt, int n, bool decay, const float* g, const void* res, const void* br,
-                          const float* w, const float* ep, const float* dX, const float* s_tok, void* dres, void* dbr,
-                          float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s) {
+                          const float* w, const float* coef, int64_t coef_stride, const float* ep, const float* dX,
+                          const float* s_tok, void* dres, void* dbr, float* dw_part, int tiles, int64_t B, int64_t C,
+                          hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C) || tiles < 1) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C, dX != nullptr) || tiles < 1) return hipErrorInvalidValue;
+    if (dX && !s_tok) return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
     const dim3 grid((unsigned)((C + 1023) / 1024), (unsigned)tiles);
     const int Ci = (int)C;
     const int tok = timing_begin("wrap_proj_bwd", s);
-    if (dX && !s_tok) return hipErrorInvalidValue;
     if (dX) {
         MHC_WG_DISPATCH(dt, decay, n,
                         MHC_LAUNCH_GGL((wgen_dx_kernel<TX_, NM_, D_, true>), grid, dim3(256), 0, s, g,
-                                       (const TX_*)res, (const TX_*)br, w, ep, dX, s_tok, (TX_*)dres, (TX_*)dbr,
-                                       dw_part, B, Ci, n, tile));
+                                       (const TX_*)res, (const TX_*)br, w, coef, coef_stride, ep, dX, s_tok,
+                                       (TX_*)dres, (TX_*)dbr, dw_part, B, Ci, n, tile));
     } else {
-        MHC_WG_DISPATCH(dt, decay, n,
-                        MHC_LAUNCH_GGL((wgen_dx_kernel<TX_, NM_, D_, false>), grid, dim3(256), 0, s, g,
-                                       (const TX_*)res, (const TX_*)br, w, ep, dX, s_tok, (TX_*)dres, (TX_*)dbr,
-                                       dw_part, B, Ci, n, tile));
+        MHC_WG_DISPATCH_WIDE(dt, decay, n,
+                             MHC_LAUNCH_GGL((wgen_dx_kernel<TX_, NM_, D_, false>), grid, dim3(256), 0, s, g,
+                                            (const TX_*)res, (const TX_*)br, w, coef, coef_stride, ep, dX, s_tok,
+                                            (TX_*)dres, (TX_*)dbr, dw_part, B, Ci, n, tile));
     }
     timing_end(tok, s);
     return hipGetLastError();
@@ -812,7 +870,7 @@ hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const vo
                             int dp_stride, int rows, float* dphi_part, int tiles, int64_t B, int64_t C,
                             hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C) || tiles < 1 || rows < 1 || rows > kWgRows) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C, true) || tiles < 1 || rows < 1 || rows > kWgRows) return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
     const dim3 grid((unsigned)((C + kWgDphiCB - 1) / kWgDphiCB), (unsigned)tiles);
     const int Ci = (int)C;
@@ -833,19 +891,20 @@ int wgen_fold_tiles(int64_t B, int64_t C) {
 }
 
 hipError_t launch_wgen_dx_fold(int dt, int n, bool decay, const float* g, const void* res, const void* br,
-                               const float* w, const float* ep, const float* dP, int dp_stride, int rows,
+                               const float* w, const float* coef, int64_t coef_stride, const float* ep,
+                               const float* dP, int dp_stride, int rows,
                                const float* s_tok, const float* phi_pre, const float* phi_post, void* dres,
                                void* dbr, float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C) || tiles < 1 || rows < 1 || rows > 2 * n) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C, true) || tiles < 1 || rows < 1 || rows > 2 * n) return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
     const dim3 grid((unsigned)((C + 511) / 512), (unsigned)tiles);
     const int Ci = (int)C;
     const int tok = timing_begin("wrap_proj_bwd", s);
     MHC_WG_DISPATCH(dt, decay, n,
                     MHC_LAUNCH_GGL((wgen_dx_fold_kernel<TX_, NM_, D_>), grid, dim3(256), 0, s, g, (const TX_*)res,
-                                   (const TX_*)br, w, ep, dP, dp_stride, rows, s_tok, phi_pre, phi_post, (TX_*)dres,
-                                   (TX_*)dbr, dw_part, B, Ci, n, tile));
+                                   (const TX_*)br, w, coef, coef_stride, ep, dP, dp_stride, rows, s_tok, phi_pre,
+                                   phi_post, (TX_*)dres, (TX_*)dbr, dw_part, B, Ci, n, tile));
     timing_end(tok, s);
     return hipGetLastError();
 }
@@ -853,7 +912,7 @@ hipError_t launch_wgen_dx_fold(int dt, int n, bool decay, const float* g, const 
 hipError_t launch_wgen_synth(int dt, int out_dt, int n, bool decay, const void* res, const void* br, void* X,
                              int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C)) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C, true)) return hipErrorInvalidValue;
     int64_t blocks = (B * (C / 4) + 255) / 256;
     const int64_t cap = 16 * (int64_t)device_cu_count();
     if (blocks > cap) blocks = cap;
@@ -872,7 +931,10 @@ hipError_t launch_wgen_synth(int dt, int out_dt, int n, bool decay, const void* 
     return hipGetLastError();
 }
 
+#undef MHC_WG_DISPATCH_WIDE
 #undef MHC_WG_DISPATCH
+#undef MHC_WG_DISPATCH_BY
+#undef MHC_WG_NM_WIDE
 #undef MHC_WG_NM
 
 }  // namespace mhc

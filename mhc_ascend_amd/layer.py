@@ -141,7 +141,8 @@ class MHCResidualWrapper(nn.Module):
     T > 1 and as [B*T, C] otherwise (layer.py:319-320).  ``use_post_norm``
     is accepted and ignored, as in the reference (layer.py:261).
 
-    For n = 2..8 and hidden % 4 == 0 it runs fused (ops.mhc_residual_wrapper):
+    For hidden % 4 == 0 and n = 2..32 (static H) or n = 2..8 (dynamic H) it
+    runs fused (ops.mhc_residual_wrapper):
     the layer's [B*T, n, C] output is never materialised, and the stream
     tensor of layer.py:299-310 only where the dynamic projection needs it
     (n != 4 with fp32 storage, fewer than 1024 tokens or hidden % 64 != 0,

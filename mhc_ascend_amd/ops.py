@@ -227,11 +227,15 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
     parameters of ``layer`` (an MHCLayer); returns fp32 [tokens, C]."""
     n = layer.expansion_rate
     C = residual.shape[-1]
-    # The fused wrapper kernels take n = 2..8 and 4-channel rows (with
-    # dynamic H, n*C a multiple of the projection's k step of 32, up to 2^22).
-    # Other shapes build the n streams with device tensor ops, as
-    # layer.py:299-310 does, and run the layer on them (layer.py:313-316).
-    fused = 2 <= n <= 8 and C % 4 == 0 and (not layer.use_dynamic_h or ((n * C) % 32 == 0 and n * C <= 1 << 22))
+    # The fused wrapper kernels take 4-channel rows and n = 2..32 with static
+    # H, n = 2..8 with dynamic H (and n*C a multiple of the projection's k
+    # step of 32, up to 2^22).  Other shapes build the n streams with device
+    # tensor ops, as layer.py:299-310 does, and run the layer on them
+    # (layer.py:313-316).
+    if layer.use_dynamic_h:
+        fused = 2 <= n <= 8 and C % 4 == 0 and (n * C) % 32 == 0 and n * C <= 1 << 22
+    else:
+        fused = 2 <= n <= 32 and C % 4 == 0
     if not fused:
         if n < 2:
             raise RuntimeError("mhc_residual_wrapper: expansion_rate must be >= 2 (stream 1 holds the branch)")

@@ -90,8 +90,9 @@ def test_expansion_rate_support_on_host():
     fixed-n kernels for {2, 4, 8, 16, 32}, the generic kernels for the rest,
     dynamic H included (its 2n + n^2 projection rows run as 32-row output
     tiles or, above 128 rows, the streaming kernels); n > 64 is rejected.
-    The fused wrapper takes n = 2..8 (other n go through the layer).  All
-    checked before any device work."""
+    The fused wrapper takes n = 2..32 with static H and n = 2..8 with
+    dynamic H (other n go through the layer).  All checked before any device
+    work."""
     lib = _lib.load()
     # static layer: these n pass the host checks; with a null x they fail on that
     for n in (1, 2, 3, 6, 8, 12, 16, 32, 64):
@@ -109,8 +110,15 @@ def test_expansion_rate_support_on_host():
     rc = lib.mhc_layer_dynamic_fwd(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, 1, 1, 1 << 30, 8, 8, 64, 20, 1e-8,
                                    1e-5, None)
     assert rc == -1 and b"null x/out" in lib.mhc_last_error()
-    rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 16, 256, 20, 1e-8, 1e-5, None)
-    assert rc == -2 and b"the fused wrapper takes n <= 8" in lib.mhc_last_error()
+    rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 33, 256, 20, 1e-8, 1e-5, None)
+    assert rc == -2 and b"the fused wrapper takes n <= 32 with static H" in lib.mhc_last_error()
+    rc = lib.mhc_wrapper_dynamic_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1 << 30, 8, 16, 256, 20,
+                                     1e-8, 1e-5, None)
+    assert rc == -2 and b"the fused wrapper takes n <= 8 with dynamic H" in lib.mhc_last_error()
+    # static n = 16 and 32 pass the shape checks; a null out then fails before any launch
+    for n in (16, 32):
+        rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, None, 1, 8, n, 256, 20, 1e-8, 1e-5, None)
+        assert rc == -1 and b"null residual/branch/out" in lib.mhc_last_error()
     rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 1, 256, 20, 1e-8, 1e-5, None)
     assert rc == -1 and b"n must be >= 2" in lib.mhc_last_error()
     # n = 2 passes the shape checks; a null out then fails before any launch

@@ -145,9 +145,10 @@ def test_wrapper_config_c5_width(device, dynamic):
                                          (6, True, 128), (3, True, 96)])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
 def test_wrapper_general_n(device, n, dynamic, C, mode):
-    """Other expansion rates on fp32 rows: n = 2..8 run the run-time-n
-    wrapper kernels; n = 32 and rows that are not a multiple of 4 build the
-    streams with device tensor ops and run them through the layer."""
+    """Other expansion rates on fp32 rows: n = 2..8 (and n = 32 with static
+    H) run the run-time-n wrapper kernels; n = 32 with dynamic H and rows
+    that are not a multiple of 4 build the streams with device tensor ops and
+    run them through the layer."""
     torch.manual_seed(n)
     wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=dynamic)
     wrap.residual_mode = mode
@@ -210,8 +211,8 @@ def test_wrapper_eval_no_grad_matches_training_forward(device):
     assert torch.equal(out_t, out_e)
 
 
-@pytest.mark.parametrize("n", [4, 3, 8])
-@pytest.mark.parametrize("dynamic", [True, False])
+@pytest.mark.parametrize("n,dynamic", [(4, True), (4, False), (3, True), (3, False), (8, True), (8, False),
+                                       (16, False)])
 @pytest.mark.parametrize("iters,eps", [(0, 1e-8), (1, 1e-8), (1, 0.1), (20, 0.1)])
 def test_wrapper_sinkhorn_settings(device, n, dynamic, iters, eps):
     """Both sides of the rule that writes the H_res gradients as zeros.
@@ -223,7 +224,10 @@ def test_wrapper_sinkhorn_settings(device, n, dynamic, iters, eps):
     iteration or none they are of the order of the other gradients; after
     20 iterations at eps = 0.1 about 1e-12 of them, measured on the
     oracle).  n = 3 and 8 run the run-time-n kernels (at n = 8 with all 80
-    projection rows: the small-np projection backward)."""
+    projection rows: the small-np projection backward), and n = 16 with
+    static H (dynamic H at n = 16 is the tensor-op path, whose bf16 stream
+    gradients are rounded once per stream before autograd sums them, more
+    than this test's one-rounding tolerance)."""
     C, B = 256, 37
     seed = 900 + iters + int(eps * 100) + (7 if dynamic else 0) + 10 * n
     wrap = _make(C, dynamic, seed, n=n)
@@ -306,3 +310,42 @@ def test_wrapper_runtime_n_few_tokens(device, n, dynamic, tokens):
     want = _oracle(wrap, res, br, grad, "decay")
     got = _run(wrap, res, br, grad, device)
     _check(got, want, torch.bfloat16, DYN if dynamic else STA, f"n={n} tokens={tokens} dyn={dynamic}")
+
+
+@pytest.mark.parametrize("n,C", [(9, 96), (12, 256), (16, 160), (20, 64), (32, 256), (32, 4), (16, 1104)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["decay", "zero"])
+def test_wrapper_static_wide_n_matches_oracle(device, n, C, dtype, mode):
+    """Static H at n = 9..32: the run-time-n kernels with 16- and 32-stream
+    capacity (coefficients read back from the lanes, the per-stream sums
+    spread over the n*n + 2n scalar slots once per wave) against the float64
+    oracle, every output and gradient, both storage dtypes and residual
+    modes; in 'decay' mode stream 31 carries residual * 1e-30."""
+    seed = 4000 + 10 * n + (3 if mode == "zero" else 0) + (1 if dtype == torch.bfloat16 else 0)
+    wrap = _make(C, False, seed, n=n)
+    wrap.residual_mode = mode
+    g = _gen(seed + 2)
+    shape = (2, 3, C) if C > 1024 else (37, C)
+    res = torch.randn(*shape, generator=g).to(dtype)
+    br = torch.randn(*shape, generator=g).to(dtype)
+    grad = torch.randn(*shape, generator=g)
+    want = _oracle(wrap, res, br, grad, mode)
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, dtype, STA, f"n={n} C={C} {dtype} {mode}")
+
+
+@pytest.mark.parametrize("n", [16, 32])
+def test_wrapper_static_wide_n_many_tokens(device, n):
+    """Static H at n = 16 and 32 on 9000 tokens: more tokens than the static
+    row-sum grid's waves, so each wave sums several tokens before it spreads
+    its per-stream sums - against the float64 oracle, every gradient."""
+    C, B = 64, 9000
+    seed = 5000 + n
+    wrap = _make(C, False, seed, n=n)
+    g = _gen(seed + 2)
+    res = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    br = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    grad = torch.randn(B, C, generator=g)
+    want = _oracle(wrap, res, br, grad, "decay")
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, torch.bfloat16, STA, f"n={n} B={B}")
