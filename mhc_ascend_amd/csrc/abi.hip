@@ -299,6 +299,11 @@ struct StaticBwdWs {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// The static Sinkhorn adjoint keeps its per-iteration state in a workspace
+// region (kStaticSkHistBytes) for n >= 16 and the generic n; without it
+// those finalize kernels recompute the forward iterations.
+static bool static_sk_hist(int32_t n) { return n >= 16 || generic_layer_n(n); }
+
 static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_dtype) {
     StaticBwdWs w{};
     w.grid = batch > 0 ? layer_bwd_grid(x_dtype, n, batch, hidden) : 1;
@@ -306,8 +311,8 @@ static StaticBwdWs static_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32
     w.scal_off = align256((size_t)w.grid * hidden * sizeof(float));
     w.stage_off = w.scal_off + align256((size_t)w.grid * (n * n + 2 * n) * sizeof(float));
     w.hist_off = w.stage_off + align256(column_sums_stage_floats(hidden) * sizeof(float));
-    // Sinkhorn adjoint history (fixed n >= 16)
-    w.rows_off = w.hist_off + (n >= 16 && !generic_layer_n(n) ? kStaticSkHistBytes : 0);
+    // Sinkhorn adjoint history
+    w.rows_off = w.hist_off + (static_sk_hist(n) ? kStaticSkHistBytes : 0);
     w.total = w.rows_off + align256(batch > 0 ? layer_bwd_scratch_bytes(x_dtype, n, batch, hidden) : 0);
     return w;
 }
@@ -351,7 +356,7 @@ int mhc_layer_static_bwd(const float* grad_out, const void* x, int32_t x_dtype, 
     if (e == hipSuccess)
         e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stage, grad_weight, scal_part, rows, h_pre,
                                   h_post, h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s,
-                                  n >= 16 && !generic_layer_n(n) ? (float*)((char*)workspace + w.hist_off) : nullptr);
+                                  static_sk_hist(n) ? (float*)((char*)workspace + w.hist_off) : nullptr);
     return hip_status(e);
 }
 
@@ -966,8 +971,10 @@ static DynBwdWs dyn_bwd_ws(int64_t batch, int32_t n, int32_t hidden, int32_t x_d
     const size_t acc = w.wdt != x_dtype ? (size_t)batch * K * 4 : 0;
     w.xw_off = o; o += align256(acc);
     w.dxw_off = o; o += align256(acc);
-    // Sinkhorn adjoint history (fixed n >= 16)
-    w.hist_off = o; o += n >= 16 && !generic_layer_n(n) && batch > 0 ? kSkHistBytes : 0;
+    // Sinkhorn adjoint history (fixed n >= 16: kSkHistBytes; generic n: the
+    // region dyn_coef_gen_hist_bytes sizes for the batch)
+    w.hist_off = o;
+    o += n >= 16 && !generic_layer_n(n) && batch > 0 ? kSkHistBytes : align256(dyn_coef_gen_hist_bytes(n, batch));
     w.rows_off = o; o += align256(batch > 0 ? layer_bwd_scratch_bytes(w.wdt, n, batch, hidden) : 0);
     w.total = o;
     return w;
@@ -1033,7 +1040,7 @@ int mhc_layer_dynamic_bwd(const float* grad_out, const void* x, int32_t x_dtype,
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, batch, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
-                                    n >= 16 && !generic_layer_n(n) ? (float*)(ws + w.hist_off) : nullptr, s);
+                                    (n >= 16 || generic_layer_n(n)) ? (float*)(ws + w.hist_off) : nullptr, s);
     }
     // One projection tile (n <= 4) and few partial rows: the column sums of
     // dPhi, dw and the db / dalpha partials in one launch after the
@@ -1316,7 +1323,8 @@ static size_t wgen_fwd_need(const WgenFwdWs& w, int32_t dtype, int32_t n, int32_
 }
 
 // backward workspace: [per-token factors | dw partials | dw stage | ...]
-//   static:  [scalar rows per wave | their sum]
+//   static:  [scalar rows per wave | their sum | Sinkhorn history
+//            (static_sk_hist)]
 //   dynamic: [per-token scalars | dP | s | coefficient partials | dPhi
 //             partials | their stage | X (fp32) | dX (fp32)]
 // With dynamic H and wrap_res_grad_vanishes (the default Sinkhorn settings)
@@ -1328,9 +1336,10 @@ static size_t wgen_fwd_need(const WgenFwdWs& w, int32_t dtype, int32_t n, int32_
 // size query has no Sinkhorn settings, so X and dX are always reserved.
 struct WgenBwdWs {
     int cblocks, ptiles, dtiles, qtiles, ftiles, srows;
-    size_t ep_off, dw_off, stw_off, scal_off, ssum_off, dp_off, s_off, cpart_off, x_off, dx_off, part_off, stp_off,
-        total;
+    size_t ep_off, dw_off, stw_off, scal_off, ssum_off, hist_off, dp_off, s_off, cpart_off, x_off, dx_off, part_off,
+        stp_off, total;
 };
+
 
 static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dynamic) {
     WgenBwdWs w{};
@@ -1348,6 +1357,7 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
         w.srows = tokens > 0 ? 4 * wgen_red_static_grid(tokens) : 1;
         w.scal_off = o; o += align256((size_t)w.srows * ns * 4);
         w.ssum_off = o; o += align256((size_t)ns * 4);
+        w.hist_off = o; o += static_sk_hist(n) ? kStaticSkHistBytes : 0;
         w.total = o;
         return w;
     }
@@ -1467,10 +1477,12 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
     } else {
         e = launch_wgen_red(dtype, n, decay, false, grad_out, residual, branch, w32, saved + d.coef_off, np, scal, ep,
                             tokens, hidden, rmsnorm_eps, s);
+        // with the H_res rows vanishing no Sinkhorn adjoint runs (their dP,
+        // db and dalpha are zeros, overwritten with the NaN carry below)
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
-                                    nullptr, s);
+                                    nullptr, s, !fold);
         if (fold) {
             if (e == hipSuccess)
                 e = launch_wgen_dphi(dtype, n, decay, residual, branch, dp, dp_stride(np), rows, part, w.qtiles, tokens,
@@ -1547,7 +1559,8 @@ static int wgen_static_bwd(const float* grad_out, const void* residual, const vo
     }
     if (e == hipSuccess)
         e = launch_column_finalize(n, weight_dtype, dw_part, rows, hidden, stw, grad_weight, ssum, 1, h_pre, h_post,
-                                   h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s);
+                                   h_res, grad_h_pre, grad_h_post, grad_h_res, num_iters, sinkhorn_eps, s,
+                                   static_sk_hist(n) ? (float*)(ws + w.hist_off) : nullptr);
     // dH_res vanishes as in mhc_wrapper_static_bwd's n = 4 path
     if (e == hipSuccess && wrap_res_grad_vanishes(num_iters, sinkhorn_eps))
         e = launch_fill_zero_carry(grad_h_res, (int64_t)n * n, nullptr, 0, grad_h_pre, n, s);

@@ -763,9 +763,11 @@ __global__ __launch_bounds__(256) void dyn_coef_fwd_kernel(
 //   s = d r_h / (K r_h)  (coefficient of x_flat in dx)
 // dp_out[b][dp_stride(np)] (np rounded up to 32, zero padded), s_out[b];
 // per-workgroup partial sums of db (np values) and dalpha (3) in
-// part[blk][np + 3].
+// part[blk][np + 3].  RES = false: the Sinkhorn adjoint's output is taken as
+// zero (as in dyn_coef16_bwd_kernel<false>), so no adjoint runs and dP_res,
+// db_res and dalpha_res are zeros.
 // ---------------------------------------------------------------------------
-template <int N>
+template <int N, bool RES = true>
 __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
     const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
     const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
@@ -793,11 +795,11 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_kernel(
     float gm[N], e[N], pr[N];
 #pragma unroll
     for (int c = 0; c < N; ++c) {
-        gm[c] = active ? sc[rr * N + c] : 0.f;
-        pr[c] = pv[2 * N + rr * N + c];
-        e[c] = active ? expf(pr[c] * ar * inv + b_res[rr * N + c]) : 0.f;
+        gm[c] = RES && active ? sc[rr * N + c] : 0.f;
+        pr[c] = RES ? pv[2 * N + rr * N + c] : 0.f;
+        e[c] = RES && active ? expf(pr[c] * ar * inv + b_res[rr * N + c]) : 0.f;
     }
-    sk_backward<N>(gm, e, iters, sk_eps, active);
+    if constexpr (RES) sk_backward<N>(gm, e, iters, sk_eps, active);
     const float hp = cf[rr], hq = cf[N + rr];
     const float dt_pre = active ? sc[N * N + N + rr] * hp * (1.f - hp) : 0.f;
     const float dt_post = active ? sc[N * N + rr] * hq * (1.f - 0.5f * hq) : 0.f;
@@ -924,8 +926,7 @@ __global__ __launch_bounds__(256) void dyn_coef_bwd_wide_kernel(
 // dyn_coef_fwd_kernel / dyn_coef_bwd_wide_kernel with n taken at run time,
 // one token per group of NM = 16, 32 or 64 lanes (row r of t_res on lane r,
 // NM-float rows with the columns c >= n padding, skw_* Sinkhorn).  The
-// backward recomputes the Sinkhorn state per iteration (no history) and
-// writes its db / dalpha terms per token to part[b][np + 3].
+// backward writes its db / dalpha terms per token to part[b][np + 3].
 // ---------------------------------------------------------------------------
 template <int NM>
 __global__ __launch_bounds__(256) void dyn_coef_gen_fwd_kernel(
@@ -986,70 +987,87 @@ __global__ __launch_bounds__(256) void dyn_coef_gen_fwd_kernel(
     if (tv && r == 0 && rh) rh[tok] = r_h;
 }
 
-template <int NM>
+// Backward: groups of NM lanes take tokens slot, slot + slots, ... (a trip
+// count the same for every lane of the grid).  With hist, each group keeps
+// its Sinkhorn adjoint's per-iteration state in its own
+// skw_hist_floats(NM, n, iters) floats of hist (O(iters) steps); without,
+// the state is recomputed per iteration.  RES = false: the adjoint's output
+// is taken as zero (as in dyn_coef_bwd_kernel<N, false>).
+template <int NM, bool RES>
 __global__ __launch_bounds__(256) void dyn_coef_gen_bwd_kernel(
     const float* __restrict__ scal, const float* __restrict__ coef, const float* __restrict__ p,
     const float* __restrict__ rh, int64_t B, int64_t K, const float* __restrict__ a_pre,
     const float* __restrict__ a_post, const float* __restrict__ a_res, const float* __restrict__ b_res,
     float* __restrict__ dp_out, float* __restrict__ s_out, float* __restrict__ part, int n, int iters,
-    float sk_eps) {
+    float sk_eps, float* __restrict__ hist) {
     const int np = 2 * n + n * n;
     const int ns = n * n + 2 * n;
     const int nv = np + 3;
     const int npt = dp_stride(np);
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t tok = gid / NM;
+    const int64_t slot = gid / NM;
+    const int64_t slots = (int64_t)gridDim.x * blockDim.x / NM;
     const int r = (int)(gid % NM);
-    const bool tv = tok < B;
-    const bool active = tv && r < n;
-    const int rr = r < n ? r : 0;
-    const int64_t tk = tv ? tok : 0;
-    const float* sc = scal + tk * (ns + 2);
-    const float* cf = coef + tk * np;
-    const float* pv = p + tk * np;
+    float* hs = hist ? hist + slot * skw_hist_floats(NM, n, iters) : nullptr;
     const float ap = a_pre[0], aq = a_post[0], ar = a_res[0];
-    const float inv = 1.f / rh[tk];
-    float gm[NM], e[NM], pr[NM];
-#pragma unroll
-    for (int c = 0; c < NM; ++c) {
-        const bool on = active && c < n;
-        gm[c] = on ? sc[rr * n + c] : 0.f;
-        pr[c] = on ? pv[2 * n + rr * n + c] : 0.f;
-        e[c] = on ? expf(pr[c] * ar * inv + b_res[rr * n + c]) : 0.f;
-    }
-    skw_backward<NM>(gm, e, n, iters, sk_eps, active);
-    const float hp = cf[rr], hq = cf[n + rr];
-    const float dt_pre = active ? sc[n * n + n + rr] * hp * (1.f - hp) : 0.f;
-    const float dt_post = active ? sc[n * n + rr] * hq * (1.f - 0.5f * hq) : 0.f;
-    float lp = 0.f;
-#pragma unroll
-    for (int c = 0; c < NM; ++c) {
-        gm[c] = (active && c < n) ? gm[c] * e[c] : 0.f;  // dt_res row r
-        lp += gm[c] * pr[c];
-    }
-    const float l_pre = active ? dt_pre * pv[rr] : 0.f, l_post = active ? dt_post * pv[n + rr] : 0.f;
-    const float tot = group_sum<NM>(ap * l_pre + aq * l_post + ar * lp);
-    const float s_pre = group_sum<NM>(l_pre), s_post = group_sum<NM>(l_post), s_res = group_sum<NM>(lp);
-    if (active) {
-        float* dp = dp_out + tok * npt;
-        dp[r] = ap * dt_pre * inv;
-        dp[n + r] = aq * dt_post * inv;
-        float* pt = part + tok * nv;
-        pt[r] = dt_pre;
-        pt[n + r] = dt_post;
+    for (int64_t base = 0; base < B; base += slots) {
+        const int64_t tok = base + slot;
+        const bool tv = tok < B;
+        const bool active = tv && r < n;
+        const int rr = r < n ? r : 0;
+        const int64_t tk = tv ? tok : 0;
+        const float* sc = scal + tk * (ns + 2);
+        const float* cf = coef + tk * np;
+        const float* pv = p + tk * np;
+        const float inv = 1.f / rh[tk];
+        float gm[NM], e[NM], pr[NM];
 #pragma unroll
         for (int c = 0; c < NM; ++c) {
-            if (c < n) {
-                dp[2 * n + r * n + c] = ar * gm[c] * inv;
-                pt[2 * n + r * n + c] = gm[c];
+            const bool on = RES && active && c < n;
+            gm[c] = on ? sc[rr * n + c] : 0.f;
+            pr[c] = on ? pv[2 * n + rr * n + c] : 0.f;
+            e[c] = on ? expf(pr[c] * ar * inv + b_res[rr * n + c]) : 0.f;
+        }
+        if constexpr (RES) {
+            if (hs) {
+                skw_backward_mem<NM>(gm, e, n, iters, sk_eps, active, hs, r, NM);
+            } else {
+                skw_backward<NM>(gm, e, n, iters, sk_eps, active);
             }
         }
-        if (r == 0) {
-            for (int o = np; o < npt; ++o) dp[o] = 0.f;
-            s_out[tok] = -tot * inv * inv * inv / (float)K;
-            pt[np] = s_pre * inv;
-            pt[np + 1] = s_post * inv;
-            pt[np + 2] = s_res * inv;
+        const float hp = cf[rr], hq = cf[n + rr];
+        const float dt_pre = active ? sc[n * n + n + rr] * hp * (1.f - hp) : 0.f;
+        const float dt_post = active ? sc[n * n + rr] * hq * (1.f - 0.5f * hq) : 0.f;
+        float lp = 0.f;
+#pragma unroll
+        for (int c = 0; c < NM; ++c) {
+            gm[c] = (active && c < n) ? gm[c] * e[c] : 0.f;  // dt_res row r
+            lp += gm[c] * pr[c];
+        }
+        const float l_pre = active ? dt_pre * pv[rr] : 0.f, l_post = active ? dt_post * pv[n + rr] : 0.f;
+        const float tot = group_sum<NM>(ap * l_pre + aq * l_post + ar * lp);
+        const float s_pre = group_sum<NM>(l_pre), s_post = group_sum<NM>(l_post), s_res = group_sum<NM>(lp);
+        if (active) {
+            float* dp = dp_out + tok * npt;
+            dp[r] = ap * dt_pre * inv;
+            dp[n + r] = aq * dt_post * inv;
+            float* pt = part + tok * nv;
+            pt[r] = dt_pre;
+            pt[n + r] = dt_post;
+#pragma unroll
+            for (int c = 0; c < NM; ++c) {
+                if (c < n) {
+                    dp[2 * n + r * n + c] = ar * gm[c] * inv;
+                    pt[2 * n + r * n + c] = gm[c];
+                }
+            }
+            if (r == 0) {
+                for (int o = np; o < npt; ++o) dp[o] = 0.f;
+                s_out[tok] = -tot * inv * inv * inv / (float)K;
+                pt[np] = s_pre * inv;
+                pt[np + 1] = s_post * inv;
+                pt[np + 2] = s_res * inv;
+            }
         }
     }
 }
@@ -2103,17 +2121,56 @@ int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters) {
     return (int)(wgs * per_wg);
 }
 
+// Generic n: the coefficient backward's lane-group width, and the workgroups
+// of token slots whose Sinkhorn history fits the region the dynamic
+// backward's workspace reserves (dyn_coef_gen_hist_bytes; 0: none fit).
+static int dyn_coef_gen_nm(int n) { return n <= 16 ? 16 : (n <= 32 ? 32 : 64); }
+constexpr int kGenHistIters = 20;  // iterations the reserved region is sized for
+
+size_t dyn_coef_gen_hist_bytes(int n, int64_t B) {
+    if (!generic_layer_n(n) || B <= 0) return 0;
+    const int nm = dyn_coef_gen_nm(n), per_wg = 256 / nm;
+    const int64_t wgs = (B + per_wg - 1) / per_wg;
+    const size_t need = (size_t)wgs * per_wg * (size_t)skw_hist_floats(nm, n, kGenHistIters) * sizeof(float);
+    return need < kSkHistBytes ? need : kSkHistBytes;
+}
+
+static int64_t dyn_coef_gen_hist_wgs(int n, int64_t B, int iters) {
+    const int nm = dyn_coef_gen_nm(n), per_wg = 256 / nm;
+    const int64_t slot_bytes = skw_hist_floats(nm, n, iters) * (int64_t)sizeof(float);
+    if (slot_bytes <= 0) return 0;
+    const int64_t fit = (int64_t)dyn_coef_gen_hist_bytes(n, B) / slot_bytes / per_wg;
+    const int64_t wgs = (B + per_wg - 1) / per_wg;
+    return wgs < fit ? wgs : fit;
+}
+
 hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
                                float* hist, hipStream_t s, bool res_rows) {
     if (B == 0) return hipSuccess;
     if (generic_layer_n(n)) {
-        if (!res_rows) return hipErrorInvalidValue;
-#define MHC_DCG_BWD(NM_)                                                                                          \
-    MHC_LAUNCH_GGL((dyn_coef_gen_bwd_kernel<NM_>), dim3((unsigned)((B * NM_ + 255) / 256)), dim3(256), 0, s,     \
-                       scal, coef, p, rh, B, K, a_pre, a_post, a_res, b_res, dp_out, s_out, part, n, iters, sk_eps)
-        if (n <= 16) { MHC_DCG_BWD(16); } else if (n <= 32) { MHC_DCG_BWD(32); } else { MHC_DCG_BWD(64); }
+        // one token per lane group, or (history in hist) as many token slots
+        // as the history region holds, each taking several tokens
+        const int nm = dyn_coef_gen_nm(n);
+        int64_t blocks = (B * nm + 255) / 256;
+        float* h = nullptr;
+        if (res_rows && hist && iters > 0) {
+            const int64_t wgs = dyn_coef_gen_hist_wgs(n, B, iters);
+            if (wgs >= 1) {
+                blocks = wgs;
+                h = hist;
+            }
+        }
+        if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+#define MHC_DCG_BWD(NM_, RES_)                                                                                     \
+    MHC_LAUNCH_GGL((dyn_coef_gen_bwd_kernel<NM_, RES_>), dim3((unsigned)blocks), dim3(256), 0, s, scal, coef, p, rh, \
+                       B, K, a_pre, a_post, a_res, b_res, dp_out, s_out, part, n, iters, sk_eps, h)
+        if (res_rows) {
+            if (nm == 16) { MHC_DCG_BWD(16, true); } else if (nm == 32) { MHC_DCG_BWD(32, true); } else { MHC_DCG_BWD(64, true); }
+        } else {
+            if (nm == 16) { MHC_DCG_BWD(16, false); } else if (nm == 32) { MHC_DCG_BWD(32, false); } else { MHC_DCG_BWD(64, false); }
+        }
 #undef MHC_DCG_BWD
         return hipGetLastError();
     }
@@ -2124,6 +2181,16 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
                                a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
         } else {
             MHC_LAUNCH_GGL(dyn_coef16_bwd_kernel<false>, dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        }
+        return hipGetLastError();
+    }
+    if (!res_rows && (n == 2 || n == 8)) {
+        if (n == 2) {
+            MHC_LAUNCH_GGL((dyn_coef_bwd_kernel<2, false>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
+                               a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
+        } else {
+            MHC_LAUNCH_GGL((dyn_coef_bwd_kernel<8, false>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
                                a_pre, a_post, a_res, b_res, dp_out, s_out, part, iters, sk_eps);
         }
         return hipGetLastError();

@@ -418,18 +418,31 @@ __global__ __launch_bounds__(kGenThreads) void gen_gram_kernel(const float* __re
 // + 2n] = [dM, dh_post_act, dh_pre_act] (layer.hip's finalize, generic n):
 // column totals in LDS (fixed order), then dH_pre = dh_pre_act h_pre (1 -
 // h_pre), dH_post = dh_post_act h_post (1 - h_post / 2) and dH_res =
-// SK^T(dM) * exp(H_res), the adjoint one row per lane of wave 0.
+// SK^T(dM) * exp(H_res), the adjoint one row per lane of wave 0 (with hist,
+// skw_hist_floats(kWave, n, iters) floats, the iterations' state in memory;
+// without, recomputed per iteration).
 // ---------------------------------------------------------------------------
 template <int NM>
 __global__ __launch_bounds__(kGenThreads) void gen_static_finalize_kernel(
     const float* __restrict__ scal_part, int rows, const float* __restrict__ h_pre, const float* __restrict__ h_post,
     const float* __restrict__ h_res, float* __restrict__ d_h_pre, float* __restrict__ d_h_post,
-    float* __restrict__ d_h_res, int n, int iters, float eps) {
+    float* __restrict__ d_h_res, int n, int iters, float eps, float* __restrict__ hist) {
     __shared__ float tot[NM * NM + 2 * NM];
     const int NS = n * n + 2 * n;
+    // column totals in row order; each lane's next RB rows are loaded
+    // together so that their latencies overlap
+    constexpr int RB = 8;
     for (int k = threadIdx.x; k < NS; k += kGenThreads) {
         float s = 0.f;
-        for (int r = 0; r < rows; ++r) s += scal_part[(int64_t)r * NS + k];
+        int r = 0;
+        for (; r + RB <= rows; r += RB) {
+            float v[RB];
+#pragma unroll
+            for (int j = 0; j < RB; ++j) v[j] = scal_part[(int64_t)(r + j) * NS + k];
+#pragma unroll
+            for (int j = 0; j < RB; ++j) s += v[j];
+        }
+        for (; r < rows; ++r) s += scal_part[(int64_t)r * NS + k];
         tot[k] = s;
     }
     __syncthreads();
@@ -442,7 +455,11 @@ __global__ __launch_bounds__(kGenThreads) void gen_static_finalize_kernel(
             e[c] = (active && c < n) ? expf(h_res[r * n + c]) : 0.f;
             gm[c] = (active && c < n) ? tot[r * n + c] : 0.f;
         }
-        skw_backward<NM>(gm, e, n, iters, eps, active);
+        if (hist) {
+            skw_backward_mem<NM>(gm, e, n, iters, eps, active, hist, r, kWave);
+        } else {
+            skw_backward<NM>(gm, e, n, iters, eps, active);
+        }
         if (active) {
 #pragma unroll
             for (int c = 0; c < NM; ++c) {
@@ -736,10 +753,13 @@ hipError_t launch_gen_layer_bwd(int x_dtype, int n, int mode, const float* g, co
 
 hipError_t launch_gen_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
                                       const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                      float* d_h_res, int iters, float sk_eps, hipStream_t s) {
+                                      float* d_h_res, int iters, float sk_eps, hipStream_t s, float* hist,
+                                      size_t hist_bytes) {
     if (!generic_layer_n(n) || rows < 1) return hipErrorInvalidValue;
+    // the history when it fits, else the recomputing adjoint
+    if ((size_t)skw_hist_floats(kWave, n, iters) * sizeof(float) > hist_bytes) hist = nullptr;
     MHC_GEN_NM(n, MHC_LAUNCH_GGL((gen_static_finalize_kernel<NM_>), dim3(1), dim3(kGenThreads), 0, s, scal_part, rows,
-                                 h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, n, iters, sk_eps));
+                                 h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res, n, iters, sk_eps, hist));
     return hipGetLastError();
 }
 

@@ -1159,7 +1159,7 @@ hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int row
                                               nullptr, nullptr, nullptr, nullptr, 0, 0.f, s);
         if (e != hipSuccess) return e;
         return launch_gen_static_finalize(n, scal_part, scal_rows, h_pre, h_post, h_res, d_h_pre, d_h_post, d_h_res,
-                                          iters, sk_eps, s);
+                                          iters, sk_eps, s, sk_hist, sk_hist ? kStaticSkHistBytes : 0);
     }
     if (n > 8) {
         // the static scalar gradients of wide n have their own kernel

@@ -645,6 +645,67 @@ __device__ __forceinline__ void skw_backward(float (&g)[NM], const float (&x0)[N
     }
 }
 
+// The same adjoint with each iteration's state kept in memory (O(iters)
+// steps instead of O(iters^2)), as sk_backward_mem does: lane r of a group
+// of ld lanes (ld >= NM; the lanes of one wave share a history when several
+// groups run in it) stores column c < n of iteration t at
+// hist[(t * (n + 1) + c) * ld + r] and the row scale at c = n
+// (skw_hist_floats(ld, n, iters) floats); each lane reads back only what it
+// wrote.  Same arithmetic as skw_backward, so the same results.
+template <int NM>
+__device__ __forceinline__ void skw_backward_mem(float (&g)[NM], const float (&x0)[NM], int n, int iters,
+                                                 float eps, bool active, float* __restrict__ hist, int r, int ld) {
+    float a[NM];
+#pragma unroll
+    for (int c = 0; c < NM; ++c) a[c] = x0[c];
+    for (int t = 0; t < iters; ++t) {
+        float rinv;
+        sk_row_step<NM>(a, eps, active, rinv);
+        float* h = hist + (int64_t)t * (n + 1) * ld + r;
+#pragma unroll
+        for (int c = 0; c < NM; ++c) {
+            if (c < n) h[(int64_t)c * ld] = a[c];
+        }
+        h[(int64_t)n * ld] = rinv;
+        skw_col_step<NM>(a, n, eps);
+    }
+    // iteration t - 1's state is loaded while iteration t's adjoint runs;
+    // the padding columns c >= n stay zero, as in the forward
+    float A[NM], ri = 0.f;
+#pragma unroll
+    for (int c = 0; c < NM; ++c) A[c] = 0.f;
+    if (iters > 0) {
+        const float* h = hist + (int64_t)(iters - 1) * (n + 1) * ld + r;
+#pragma unroll
+        for (int c = 0; c < NM; ++c) {
+            if (c < n) A[c] = h[(int64_t)c * ld];
+        }
+        ri = h[(int64_t)n * ld];
+    }
+    for (int t = iters - 1; t >= 0; --t) {
+        float An[NM], rn = 0.f;
+#pragma unroll
+        for (int c = 0; c < NM; ++c) An[c] = 0.f;
+        if (t > 0) {
+            const float* h = hist + (int64_t)(t - 1) * (n + 1) * ld + r;
+#pragma unroll
+            for (int c = 0; c < NM; ++c) {
+                if (c < n) An[c] = h[(int64_t)c * ld];
+            }
+            rn = h[(int64_t)n * ld];
+        }
+        skw_adjoint_step<NM>(g, A, n, ri, eps);
+#pragma unroll
+        for (int c = 0; c < NM; ++c) A[c] = An[c];
+        ri = rn;
+    }
+}
+
+// floats of skw_backward_mem's history for one group of ld lanes
+__host__ __device__ constexpr int64_t skw_hist_floats(int ld, int n, int iters) {
+    return (int64_t)(iters > 0 ? iters : 0) * (n + 1) * ld;
+}
+
 // ---------------------------------------------------------------------------
 // Sinkhorn-Knopp on a 4 x 4 matrix held one element per lane in a 16-lane DPP
 // row (lane 4 r + c of the row holds element (r, c)): a row sum is a quad

@@ -96,9 +96,12 @@ size_t gen_layer_bwd_scratch_bytes(int64_t B, int64_t C);
 hipError_t launch_gen_layer_bwd(int x_dtype, int n, int mode, const float* g, const void* x, const float* w,
                                 const float* coef, int64_t coef_stride, void* dx, float* dw_part, float* scal_out,
                                 int grid, int64_t B, int64_t C, float eps, float* scratch, hipStream_t s);
+// hist (hist_bytes, may be null): the Sinkhorn adjoint's per-iteration state,
+// used when skw_hist_floats(kWave, n, iters) floats fit.
 hipError_t launch_gen_static_finalize(int n, const float* scal_part, int rows, const float* h_pre,
                                       const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
-                                      float* d_h_res, int iters, float sk_eps, hipStream_t s);
+                                      float* d_h_res, int iters, float sk_eps, hipStream_t s, float* hist,
+                                      size_t hist_bytes);
 hipError_t launch_gen_aggregate_fwd(int dt, int n, const void* x, const float* H, int64_t hs, void* out,
                                     float* h_act, int64_t B, int64_t C, hipStream_t s);
 hipError_t launch_gen_aggregate_bwd(int dt, int n, const void* g, const void* x, const float* h_act, int64_t hs,
@@ -172,7 +175,8 @@ hipError_t launch_layer_finalize(int n, int w_dtype, const float* stage, int rsp
 // gradients when n > 0: one launch when rows is small (the finalize reads the
 // partials directly), else a first pass into stage[column_sums_stage_floats].
 size_t column_sums_stage_floats(int64_t cols);
-// sk_hist (kStaticSkHistBytes, n >= 16 only): the static Sinkhorn adjoint's history.
+// sk_hist (kStaticSkHistBytes, n >= 16 and the generic n; null elsewhere):
+// the static Sinkhorn adjoint's history.
 hipError_t launch_column_finalize(int n, int w_dtype, const float* part, int rows, int64_t cols, float* stage,
                                   void* dw, const float* scal_part, int scal_rows, const float* h_pre,
                                   const float* h_post, const float* h_res, float* d_h_pre, float* d_h_post,
@@ -300,11 +304,16 @@ int dyn_coef_bwd_blocks(int n, int64_t B);
 // n >= 16: the Sinkhorn adjoint's per-iteration history lives in a region
 // of kSkHistBytes (hist; null for n < 16), split into token slots of
 // iters * (n + 1) * n floats; 0 slots = iters too large for the region.
+// Generic n: a region of dyn_coef_gen_hist_bytes(n, B) (at most
+// kSkHistBytes; hist may be null), used when one workgroup's token slots fit
+// it at the call's iters, else each iteration's state is recomputed.
 constexpr size_t kSkHistBytes = size_t(64) << 20;
 int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters);
-// res_rows = false (n = 4 only): dM is taken as zero after the Sinkhorn
-// adjoint (the wrapper's column-constant dM, wrap_res_grad_vanishes): dP,
-// db and dalpha of the H_res rows are written as zeros and no adjoint runs.
+size_t dyn_coef_gen_hist_bytes(int n, int64_t B);
+// res_rows = false (n = 2, 4, 8 and the generic n): dM is taken as zero after
+// the Sinkhorn adjoint (the wrapper's column-constant dM,
+// wrap_res_grad_vanishes): dP, db and dalpha of the H_res rows are written as
+// zeros and no adjoint runs.
 hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, const float* p, const float* rh,
                                int64_t B, int64_t K, const float* a_pre, const float* a_post, const float* a_res,
                                const float* b_res, float* dp_out, float* s_out, float* part, int iters, float sk_eps,
