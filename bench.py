@@ -450,8 +450,8 @@ class Wrapper8Workload(WrapperWorkload):
     (65,536 tokens).  Runs the run-time-n wrapper kernels; the record also
     times the same step through the unfused path (the streams built with
     device tensor ops, as layer.py:299-310, and the layer run on them), the
-    static-H step both ways, and static H at n = 16 and 32 both ways on
-    [8192, 4096]."""
+    static-H step both ways, and n = 16 and 32 both ways (static H on
+    [8192, 4096], dynamic H on [8192, 1024])."""
 
     name = "wrapper8"
     Bo, T, n, C = 16384, 4, 8, 7168
@@ -506,14 +506,15 @@ class Wrapper8Workload(WrapperWorkload):
                "path": "torch.zeros + slice copies + decay products (layer.py:299-310), MHCLayer on [tokens, 8, C], "
                        "mean over streams; fwd+bwd through autograd"}
         rec["static_h"] = self.static_ab(steps)
-        rec["static_wide_n"] = [self.static_wide_ab(n, steps) for n in (16, 32)]
+        rec["static_wide_n"] = [self.wide_ab(n, steps, False, C=4096) for n in (16, 32)]
+        rec["dynamic_wide_n"] = [self.wide_ab(n, steps, True, C=1024) for n in (16, 32)]
         return rec
 
-    def static_wide_ab(self, n, steps, tokens=8192, C=4096):
-        """Static H at n = 16 / 32 (the run-time-n kernels' 16- and 32-stream
-        capacities) on bf16 [8192, 4096] residual / branch, 'decay': the
-        fused wrapper against the tensor-op streams through the layer, ms per
-        fwd+bwd step, inputs and parameters shared by both paths."""
+    def wide_ab(self, n, steps, dynamic, tokens=8192, C=4096):
+        """n = 16 / 32 (the run-time-n kernels' 16- and 32-stream capacities)
+        on bf16 [tokens, C] residual / branch, 'decay', static or dynamic H:
+        the fused wrapper against the tensor-op streams through the layer, ms
+        per fwd+bwd step, inputs and parameters shared by both paths."""
         torch, mhc = self.torch, self.mhc
         dev = self.rs[0].device
         g = torch.Generator(device=dev).manual_seed(n)
@@ -521,7 +522,7 @@ class Wrapper8Workload(WrapperWorkload):
         bs = [torch.randn(tokens, C, device=dev, generator=g).bfloat16().requires_grad_(True) for _ in range(2)]
         gs = [torch.randn(tokens, C, device=dev, generator=g) for _ in range(2)]
         torch.manual_seed(n)
-        wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=False).to(dev)
+        wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=dynamic).to(dev)
         layer = wrap.mhc
         params = list(wrap.parameters())
 
@@ -537,7 +538,7 @@ class Wrapper8Workload(WrapperWorkload):
                 X[:, i] = r * (0.1 ** (i - 1))
             return torch.autograd.grad(layer(X).mean(dim=1), [r, b] + params, gs[k])
 
-        res = {"n": n, "tokens": tokens, "hidden": C}
+        res = {"n": n, "tokens": tokens, "hidden": C, "dynamic_h": dynamic}
         for name, fn in (("fused_ms_per_step", fused), ("unfused_ms_per_step", unfused)):
             for i in range(2):
                 fn(i % 2)

@@ -301,17 +301,18 @@ int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dty
  * X_i = residual * 0.1^(i-1) rounded to dtype (MHC_WRAPPER_DECAY,
  * layer.py:306-308) or 0 (MHC_WRAPPER_ZERO); the mHC layer on X; the mean
  * over the n streams (layer.py:316) -> out [tokens, hidden] fp32.
- * hidden % 4 == 0 and n = 2..32 with static H, n = 2..8 with dynamic H,
- * which also needs n * hidden % 32 == 0 (others return
- * MHC_ERR_UNSUPPORTED).  The row passes rebuild X from
- * residual and branch in registers, so with static H, and with dynamic H at
- * n = 4 and hidden % 32 == 0 (whose projection kernels rebuild it too), X
- * never exists in memory.  For the other dynamic-H shapes the projection
- * forward reads a storage-dtype copy of X from the workspace (except with
- * bf16 storage, n >= 5, tokens >= 1024 and hidden % 64 == 0, where it too
- * rebuilds X), and so does the backward (fp32) when the Sinkhorn settings
- * keep the H_res gradients (num_iters == 0 or sinkhorn_eps > 1e-6); the
- * queries below size both.
+ * n = 2..32 and hidden % 4 == 0; dynamic H also needs n * hidden % 32 == 0
+ * and, past n = 10 (more than 128 projection rows), a backward at Sinkhorn
+ * settings under which the H_res gradients vanish (num_iters >= 1 and
+ * sinkhorn_eps <= 1e-6, the defaults); others return MHC_ERR_UNSUPPORTED.
+ * The row passes rebuild X from residual and branch in registers, so with
+ * static H, and with dynamic H at n = 4 and hidden % 32 == 0 (whose
+ * projection kernels rebuild it too), X never exists in memory.  For the
+ * other dynamic-H shapes the projection forward reads a storage-dtype copy
+ * of X from the workspace (except with bf16 storage, n >= 5, tokens >= 1024
+ * and hidden % 64 == 0, where it too rebuilds X), and so does the backward
+ * (fp32) when the Sinkhorn settings keep the H_res gradients (num_iters == 0
+ * or sinkhorn_eps > 1e-6) or n > 8; the queries below size both.
  * Parameters and `saved` are those of the layer entries above.  Backward:
  * grad_out [tokens, hidden] fp32 -> grad_residual, grad_branch (dtype) and
  * the layer's parameter gradients.

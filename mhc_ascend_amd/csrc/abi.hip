@@ -1260,17 +1260,15 @@ static int check_wrapper(const char* fn, int64_t tokens, int32_t n, int32_t hidd
     if (!valid_dtype(dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": dtype must be F32 or BF16");
     // the reference writes stream 1 (layer.py:301), which needs n >= 2
     if (n < 2) return fail(MHC_ERR_INVALID, std::string(fn) + ": n must be >= 2 (stream 1 holds the branch)");
-    const int n_max = dynamic ? kWgMaxN : kWgMaxNStatic;
-    if (n > n_max)
-        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper takes n <= " + std::to_string(n_max) +
-                                             (dynamic ? " with dynamic H" : " with static H"));
+    if (n > kWgMaxN)
+        return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper takes n <= " + std::to_string(kWgMaxN));
     if (hidden % 4 != 0)
         return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": the fused wrapper needs hidden % 4 == 0");
     if (!valid_dtype(w_dtype)) return fail(MHC_ERR_INVALID, std::string(fn) + ": weight_dtype must be F32 or BF16");
     if (mode != MHC_WRAPPER_DECAY && mode != MHC_WRAPPER_ZERO)
         return fail(MHC_ERR_INVALID, std::string(fn) + ": residual_mode must be MHC_WRAPPER_DECAY or MHC_WRAPPER_ZERO");
     if (!wrap_fused4(n, hidden, dynamic)) {
-        if (!wgen_supported(n, hidden, dynamic))
+        if (!wgen_supported(n, hidden))
             return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": hidden too large for the wrapper kernels");
         if (dynamic && ((int64_t)n * hidden) % 32 != 0)
             return fail(MHC_ERR_UNSUPPORTED, std::string(fn) + ": n*hidden must be a multiple of 32");
@@ -1367,12 +1365,15 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
     w.dp_off = o; o += align256((size_t)tokens * dp_stride(np) * 4);
     w.s_off = o; o += align256((size_t)tokens * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
-    // dPhi partials: the 2n pre / post rows per wgen_dphi_kernel tile, or
-    // the one-tile projection backward's (all np rows when np <= 32; more
-    // rows go through launch_proj_bwd_small, which writes dPhi directly)
+    // dPhi partials: the 2n pre / post rows per wgen_dphi_kernel tile
+    // (n <= kWgFoldMaxN), or the one-tile projection backward's (np rows
+    // when np <= 32, the 2n pre / post rows when 2n <= 32 and n is past the
+    // fold kernels; more rows go through launch_proj_bwd_small, which
+    // writes dPhi directly)
     w.qtiles = tokens > 0 ? wgen_dphi_tiles(tokens, hidden) : 1;
-    size_t part = (size_t)w.qtiles * 2 * n;
+    size_t part = n <= kWgFoldMaxN ? (size_t)w.qtiles * 2 * n : 0;
     if (np <= kProjTile && (size_t)w.ptiles * np > part) part = (size_t)w.ptiles * np;
+    if (n > kWgFoldMaxN && 2 * n <= kProjTile && (size_t)w.ptiles * 2 * n > part) part = (size_t)w.ptiles * 2 * n;
     const int64_t srows = np <= kProjTile ? np : 2 * n;
     w.part_off = o; o += align256(part * K * 4);
     w.stp_off = o; o += align256(column_sums_stage_floats(srows * K) * 4);
@@ -1383,9 +1384,10 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
 }
 
 // The run-time-n backward keeps the stream rows X and dX (the last regions
-// of its workspace) only when the H_res rows of dP do not vanish.
-static size_t wgen_bwd_need(const WgenBwdWs& w, int32_t num_iters, float sinkhorn_eps) {
-    return wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? w.x_off : w.total;
+// of its workspace) only when the H_res rows of dP do not vanish or n is
+// past the fold kernels.
+static size_t wgen_bwd_need(const WgenBwdWs& w, int32_t n, int32_t num_iters, float sinkhorn_eps) {
+    return n <= kWgFoldMaxN && wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? w.x_off : w.total;
 }
 
 static int wgen_dynamic_fwd(const void* residual, const void* branch, int32_t dtype, bool decay, const void* weight,
@@ -1444,8 +1446,15 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
                             void* grad_branch, void* grad_weight, float* grad_phi, float* grad_alpha, float* grad_b,
                             void* workspace, size_t workspace_bytes, int64_t tokens, int32_t n, int32_t hidden,
                             int32_t num_iters, float sinkhorn_eps, float rmsnorm_eps, hipStream_t s) {
+    const int np = 2 * n + n * n;
+    // rows of dP the projection backward carries (the rest of dPhi: zeros)
+    const int rows = wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? 2 * n : np;
+    if (rows > kProjTile && rows > proj_bwd_small_max_rows())
+        return fail(MHC_ERR_UNSUPPORTED, "wrapper_dynamic_bwd: at n = " + std::to_string(n) +
+                                             " the fused wrapper needs num_iters >= 1 and sinkhorn_eps <= 1e-6 "
+                                             "(the H_res gradients then vanish)");
     const WgenBwdWs w = wgen_bwd_ws(tokens, n, hidden, true);
-    if (!workspace || workspace_bytes < wgen_bwd_need(w, num_iters, sinkhorn_eps))
+    if (!workspace || workspace_bytes < wgen_bwd_need(w, n, num_iters, sinkhorn_eps))
         return fail(MHC_ERR_WORKSPACE,
                     "wrapper_dynamic_bwd: workspace smaller than mhc_wrapper_dynamic_bwd_workspace_size_for()");
     char* ws = (char*)workspace;
@@ -1462,11 +1471,9 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
     float* stp = (float*)(ws + w.stp_off);
     const DynSaved d = dyn_saved(tokens, n, hidden);
     const float* w32 = saved + d.w_off;
-    const int np = 2 * n + n * n;
     const int64_t K = (int64_t)n * hidden;
-    // rows of dP the projection backward carries (the rest of dPhi: zeros)
-    const int rows = wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? 2 * n : np;
-    const bool fold = rows < np;
+    // up to n = kWgFoldMaxN the pre / post rows need no stream rows
+    const bool fold = rows < np && n <= kWgFoldMaxN;
     hipError_t e = hipSuccess;
     int rows_w = fold ? w.ftiles : w.dtiles, rows_c = w.cblocks;
     if (tokens == 0) {
@@ -1482,7 +1489,7 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
         if (e == hipSuccess)
             e = launch_dyn_coef_bwd(n, scal, saved + d.coef_off, saved + d.p_off, saved + d.rh_off, tokens, K,
                                     alpha_pre, alpha_post, alpha_res, b_res, dp, stok, cpart, num_iters, sinkhorn_eps,
-                                    nullptr, s, !fold);
+                                    nullptr, s, rows == np);
         if (fold) {
             if (e == hipSuccess)
                 e = launch_wgen_dphi(dtype, n, decay, residual, branch, dp, dp_stride(np), rows, part, w.qtiles, tokens,
@@ -1707,7 +1714,8 @@ size_t mhc_wrapper_dynamic_bwd_workspace_size(int64_t tokens, int32_t n, int32_t
 size_t mhc_wrapper_dynamic_bwd_workspace_size_for(int64_t tokens, int32_t n, int32_t hidden, int32_t dtype,
                                                   int32_t residual_mode, int32_t num_iters, float sinkhorn_eps) {
     if (tokens < 0 || n < 1 || hidden < 1) return 0;
-    if (!wrap_fused4(n, hidden, true)) return wgen_bwd_need(wgen_bwd_ws(tokens, n, hidden, true), num_iters, sinkhorn_eps);
+    if (!wrap_fused4(n, hidden, true))
+        return wgen_bwd_need(wgen_bwd_ws(tokens, n, hidden, true), n, num_iters, sinkhorn_eps);
     return wrap_bwd_ws(tokens, n, hidden, dtype, true, residual_mode == MHC_WRAPPER_DECAY).total;
 }
 

@@ -2185,6 +2185,23 @@ hipError_t launch_dyn_coef_bwd(int n, const float* scal, const float* coef, cons
         }
         return hipGetLastError();
     }
+    if (!res_rows && n >= 16) {
+        // no adjoint runs: the run-time-n kernel on n-lane groups
+        const int64_t gblocks = (B * n + 255) / 256;
+        if (gblocks > 0x7fffffff) return hipErrorInvalidValue;
+        if (n == 16) {
+            MHC_LAUNCH_GGL((dyn_coef_gen_bwd_kernel<16, false>), dim3((unsigned)gblocks), dim3(256), 0, s, scal, coef,
+                               p, rh, B, K, a_pre, a_post, a_res, b_res, dp_out, s_out, part, n, iters, sk_eps,
+                               (float*)nullptr);
+        } else if (n == 32) {
+            MHC_LAUNCH_GGL((dyn_coef_gen_bwd_kernel<32, false>), dim3((unsigned)gblocks), dim3(256), 0, s, scal, coef,
+                               p, rh, B, K, a_pre, a_post, a_res, b_res, dp_out, s_out, part, n, iters, sk_eps,
+                               (float*)nullptr);
+        } else {
+            return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     if (!res_rows && (n == 2 || n == 8)) {
         if (n == 2) {
             MHC_LAUNCH_GGL((dyn_coef_bwd_kernel<2, false>), dim3(blocks), dim3(256), 0, s, scal, coef, p, rh, B, K,
@@ -2806,6 +2823,8 @@ static WideScratch wide_scratch(int np, int64_t B, int64_t K) {
 }
 
 size_t proj_bwd_wide_scratch_bytes(int np, int64_t B, int64_t K) { return wide_scratch(np, B, K).total; }
+
+int proj_bwd_small_max_rows() { return kStreamOB; }
 
 hipError_t launch_proj_bwd_small(const float* x, const float* dP, int dp_stride, const float* s_tok,
                                  const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,

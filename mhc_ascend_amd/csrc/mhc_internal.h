@@ -310,7 +310,7 @@ int dyn_coef_bwd_blocks(int n, int64_t B);
 constexpr size_t kSkHistBytes = size_t(64) << 20;
 int dyn_coef_bwd_hist_slots(int n, int64_t B, int iters);
 size_t dyn_coef_gen_hist_bytes(int n, int64_t B);
-// res_rows = false (n = 2, 4, 8 and the generic n): dM is taken as zero after
+// res_rows = false (any n): dM is taken as zero after
 // the Sinkhorn adjoint (the wrapper's column-constant dM,
 // wrap_res_grad_vanishes): dP, db and dalpha of the H_res rows are written as
 // zeros and no adjoint runs.
@@ -358,6 +358,8 @@ size_t proj_bwd_wide_scratch_bytes(int np, int64_t B, int64_t K);
 // 32 < np <= 128 at any batch: dx over all output tiles in one pass (one
 // workgroup per 128 columns x 32 tokens) and dPhi written directly (one
 // workgroup per 64 rows x 128 columns walking all tokens); fp32 x and dx.
+// rows (np) launch_proj_bwd_small takes at most
+int proj_bwd_small_max_rows();
 hipError_t launch_proj_bwd_small(const float* x, const float* dP, int dp_stride, const float* s_tok,
                                  const float* phi_pre, const float* phi_post, const float* phi_res, int n_pre, int np,
                                  float* dx, bool accumulate, float* dphi, int64_t B, int64_t K, hipStream_t s);
@@ -415,13 +417,14 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
                                 bool res_rows, hipStream_t s);
 
 // ---- wrapper_gen.hip -------------------------------------------------------
-// MHCResidualWrapper for n = 2..8 (dynamic H) or 2..32 (static H) with n at
-// run time (the shapes the n = 4 kernels above do not take); hidden % 4 == 0.
-constexpr int kWgMaxN = 8;          // dynamic H
-constexpr int kWgMaxNStatic = 32;   // static H
+// MHCResidualWrapper for n = 2..32 with n at run time (the shapes the n = 4
+// kernels above do not take); hidden % 4 == 0.  The dPhi / fold kernels
+// (the dynamic-H backward without stream rows) take n <= kWgFoldMaxN.
+constexpr int kWgMaxN = 32;
+constexpr int kWgFoldMaxN = 8;
 // Floats per token of the per-token factors of d r / d b.
 constexpr int kWgEp = 8;
-bool wgen_supported(int n, int64_t C, bool dynamic);
+bool wgen_supported(int n, int64_t C);
 hipError_t launch_wgen_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
                            const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
                            hipStream_t s);

@@ -1,14 +1,13 @@
 // MHCResidualWrapper for the shapes the n = 4 kernels of wrapper.hip do not
-// take: expansion rates 2..8 with dynamic H, 2..32 with static H, and n = 4
-// rows those kernels refuse; any hidden % 4 == 0 (layer.py:269-322).
+// take: expansion rates 2..32 and n = 4 rows those kernels refuse; any
+// hidden % 4 == 0 (layer.py:269-322).
 //
 // The streams are rebuilt from r and b wherever a row pass needs them
 // (X_0 = r, X_1 = b, X_j = r * 0.1^(j-1) rounded to the storage dtype in
 // 'decay' mode, 0 in 'zero' mode: layer.py:299-310), with n taken at run
-// time: per-stream arrays have a compile-time capacity NM in {2, 4, 8}
-// (also 16 and 32 for the static-H kernels) and their loops run over it
-// with a uniform j < n test, so nothing is indexed at run time in
-// registers.  The math is that of wrapper.hip:
+// time: per-stream arrays have a compile-time capacity NM in {2, 4, 8, 16,
+// 32} (the dPhi / fold kernels: up to 8) and their loops run over it with a
+// uniform j < n test, so nothing is indexed at run time in registers.  The math is that of wrapper.hip:
 //   forward   out = hs (xa / r) w + sum_j cm_j X_j,  xa = sum_j h_pre_j X_j,
 //             r = sqrt(mean_c xa^2 + eps),  hs = (1/n) sum_i h_post_i,
 //             cm_j = (1/n) sum_i M_ij  (the stream mean of layer.py:316)
@@ -27,16 +26,16 @@
 //                      workgroups of 1024 channels x one token tile; with
 //                      dynamic H it adds the layer projection backward's dX
 //                      folded over the streams (Sinkhorn settings where the
-//                      H_res rows of dP do not vanish)
-//   wgen_dphi_mfma_kernel  dynamic H, H_res rows of dP vanishing: dPhi of
-//                      the 2n pre / post rows from the rebuilt streams
-//                      (bf16 MFMA)
+//                      H_res rows of dP do not vanish, and n > 8)
+//   wgen_dphi_mfma_kernel  dynamic H, H_res rows of dP vanishing, n <= 8:
+//                      dPhi of the 2n pre / post rows from the rebuilt
+//                      streams (bf16 MFMA)
 //   wgen_dx_fold_kernel  the same case: d r, d b with dP . Phi folded over
 //                      the streams, and the dw partials
 //   wgen_synth_kernel  the stream rows [tokens, n*C] as the operand of the
 //                      layer's projection kernels (dynamic H: the forward's
 //                      in the storage dtype; the backward's in fp32 when the
-//                      H_res rows do not vanish)
+//                      H_res rows do not vanish or n > 8)
 #include "mhc_device.h"
 #include "mhc_internal.h"
 
@@ -50,7 +49,7 @@ constexpr double wg_pow01(int e) { return e <= 0 ? 1.0 : 0.1 * wg_pow01(e - 1); 
 // product r * m is formed in fp32 by the reference's mul; the double
 // repeated product rounds to the same fp32 value as 0.1 ** e for e <= 63).
 #define MHC_WG_M(e) (float)wg_pow01(e)
-constexpr float kWgMult[kWgMaxNStatic] = {
+constexpr float kWgMult[kWgMaxN] = {
     1.f,          0.f,          MHC_WG_M(1),  MHC_WG_M(2),  MHC_WG_M(3),  MHC_WG_M(4),  MHC_WG_M(5),  MHC_WG_M(6),
     MHC_WG_M(7),  MHC_WG_M(8),  MHC_WG_M(9),  MHC_WG_M(10), MHC_WG_M(11), MHC_WG_M(12), MHC_WG_M(13), MHC_WG_M(14),
     MHC_WG_M(15), MHC_WG_M(16), MHC_WG_M(17), MHC_WG_M(18), MHC_WG_M(19), MHC_WG_M(20), MHC_WG_M(21), MHC_WG_M(22),
@@ -447,7 +446,7 @@ __global__ __launch_bounds__(256) void wgen_dx_kernel(const float* __restrict__ 
 //   dphi_part[tile][o][j*C + c] = sum over the tile's tokens of
 //                                 dP[t][o] X_j[t][c],  o < rows = 2n
 // ---------------------------------------------------------------------------
-constexpr int kWgRows = 2 * kWgMaxN;  // pre / post rows of dP at most
+constexpr int kWgRows = 2 * kWgFoldMaxN;  // pre / post rows of dP at most
 
 namespace {
 // two consecutive elements (4- or 8-byte aligned) as one load
@@ -734,11 +733,9 @@ __global__ __launch_bounds__(256) void wgen_synth_kernel(const TX* __restrict__ 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-bool wgen_supported(int n, int64_t C, bool dynamic) {
-    return n >= 2 && n <= (dynamic ? kWgMaxN : kWgMaxNStatic) && C >= 4 && C % 4 == 0 && C <= (1 << 28);
-}
+bool wgen_supported(int n, int64_t C) { return n >= 2 && n <= kWgMaxN && C >= 4 && C % 4 == 0 && C <= (1 << 28); }
 
-// capacities of the kernels with dynamic H (n <= 8)
+// capacities of the dPhi / fold kernels (n <= kWgFoldMaxN)
 #define MHC_WG_NM(n, ...)                   \
     if ((n) <= 2) {                         \
         constexpr int NM_ = 2; __VA_ARGS__; \
@@ -748,7 +745,7 @@ bool wgen_supported(int n, int64_t C, bool dynamic) {
         constexpr int NM_ = 8; __VA_ARGS__; \
     }
 
-// capacities of the kernels static H also runs (n <= 32)
+// capacities of the row kernels (n <= kWgMaxN)
 #define MHC_WG_NM_WIDE(n, ...)               \
     if ((n) <= 8) {                          \
         MHC_WG_NM(n, __VA_ARGS__)            \
@@ -776,7 +773,7 @@ hipError_t launch_wgen_fwd(int dt, int n, bool decay, const void* res, const voi
                            const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,
                            hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C, false)) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C)) return hipErrorInvalidValue;
     const int64_t blocks = (B + 3) / 4;  // one token per wave
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const int Ci = (int)C;
@@ -800,7 +797,7 @@ hipError_t launch_wgen_red(int dt, int n, bool decay, bool stat, const float* g,
                            const float* w, const float* coef, int64_t coef_stride, float* scal_out, float* ep_out,
                            int64_t B, int64_t C, float eps, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C, !stat)) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C)) return hipErrorInvalidValue;
     const int64_t blocks = stat ? wgen_red_static_grid(B) : (B + 3) / 4;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
     const int Ci = (int)C;
@@ -811,10 +808,10 @@ hipError_t launch_wgen_red(int dt, int n, bool decay, bool stat, const float* g,
                                        g, (const TX_*)res, (const TX_*)br, w, coef, coef_stride, scal_out, ep_out, B,
                                        Ci, n, eps));
     } else {
-        MHC_WG_DISPATCH(dt, decay, n,
-                        MHC_LAUNCH_GGL((wgen_red_kernel<TX_, NM_, D_, false>), dim3((unsigned)blocks), dim3(256), 0,
-                                       s, g, (const TX_*)res, (const TX_*)br, w, coef, coef_stride, scal_out, ep_out,
-                                       B, Ci, n, eps));
+        MHC_WG_DISPATCH_WIDE(dt, decay, n,
+                             MHC_LAUNCH_GGL((wgen_red_kernel<TX_, NM_, D_, false>), dim3((unsigned)blocks), dim3(256),
+                                            0, s, g, (const TX_*)res, (const TX_*)br, w, coef, coef_stride, scal_out,
+                                            ep_out, B, Ci, n, eps));
     }
     timing_end(tok, s);
     return hipGetLastError();
@@ -835,17 +832,17 @@ hipError_t launch_wgen_dx(int dt, int n, bool decay, const float* g, const void*
                           const float* s_tok, void* dres, void* dbr, float* dw_part, int tiles, int64_t B, int64_t C,
                           hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C, dX != nullptr) || tiles < 1) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C) || tiles < 1) return hipErrorInvalidValue;
     if (dX && !s_tok) return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
     const dim3 grid((unsigned)((C + 1023) / 1024), (unsigned)tiles);
     const int Ci = (int)C;
     const int tok = timing_begin("wrap_proj_bwd", s);
     if (dX) {
-        MHC_WG_DISPATCH(dt, decay, n,
-                        MHC_LAUNCH_GGL((wgen_dx_kernel<TX_, NM_, D_, true>), grid, dim3(256), 0, s, g,
-                                       (const TX_*)res, (const TX_*)br, w, coef, coef_stride, ep, dX, s_tok,
-                                       (TX_*)dres, (TX_*)dbr, dw_part, B, Ci, n, tile));
+        MHC_WG_DISPATCH_WIDE(dt, decay, n,
+                             MHC_LAUNCH_GGL((wgen_dx_kernel<TX_, NM_, D_, true>), grid, dim3(256), 0, s, g,
+                                            (const TX_*)res, (const TX_*)br, w, coef, coef_stride, ep, dX, s_tok,
+                                            (TX_*)dres, (TX_*)dbr, dw_part, B, Ci, n, tile));
     } else {
         MHC_WG_DISPATCH_WIDE(dt, decay, n,
                              MHC_LAUNCH_GGL((wgen_dx_kernel<TX_, NM_, D_, false>), grid, dim3(256), 0, s, g,
@@ -870,7 +867,8 @@ hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const vo
                             int dp_stride, int rows, float* dphi_part, int tiles, int64_t B, int64_t C,
                             hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C, true) || tiles < 1 || rows < 1 || rows > kWgRows) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C) || n > kWgFoldMaxN || tiles < 1 || rows < 1 || rows > kWgRows)
+        return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
     const dim3 grid((unsigned)((C + kWgDphiCB - 1) / kWgDphiCB), (unsigned)tiles);
     const int Ci = (int)C;
@@ -896,7 +894,8 @@ hipError_t launch_wgen_dx_fold(int dt, int n, bool decay, const float* g, const 
                                const float* s_tok, const float* phi_pre, const float* phi_post, void* dres,
                                void* dbr, float* dw_part, int tiles, int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C, true) || tiles < 1 || rows < 1 || rows > 2 * n) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C) || n > kWgFoldMaxN || tiles < 1 || rows < 1 || rows > 2 * n)
+        return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
     const dim3 grid((unsigned)((C + 511) / 512), (unsigned)tiles);
     const int Ci = (int)C;
@@ -912,20 +911,20 @@ hipError_t launch_wgen_dx_fold(int dt, int n, bool decay, const float* g, const 
 hipError_t launch_wgen_synth(int dt, int out_dt, int n, bool decay, const void* res, const void* br, void* X,
                              int64_t B, int64_t C, hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C, true)) return hipErrorInvalidValue;
+    if (!wgen_supported(n, C)) return hipErrorInvalidValue;
     int64_t blocks = (B * (C / 4) + 255) / 256;
     const int64_t cap = 16 * (int64_t)device_cu_count();
     if (blocks > cap) blocks = cap;
     const int Ci = (int)C;
     const int tok = timing_begin("wrap_synth", s);
     if (out_dt == kF32) {
-        MHC_WG_DISPATCH(dt, decay, n,
-                        MHC_LAUNCH_GGL((wgen_synth_kernel<TX_, float, NM_, D_>), dim3((unsigned)blocks), dim3(256), 0,
-                                       s, (const TX_*)res, (const TX_*)br, (float*)X, B, Ci, n));
+        MHC_WG_DISPATCH_WIDE(dt, decay, n,
+                             MHC_LAUNCH_GGL((wgen_synth_kernel<TX_, float, NM_, D_>), dim3((unsigned)blocks), dim3(256),
+                                            0, s, (const TX_*)res, (const TX_*)br, (float*)X, B, Ci, n));
     } else {
-        MHC_WG_DISPATCH(dt, decay, n,
-                        MHC_LAUNCH_GGL((wgen_synth_kernel<TX_, TX_, NM_, D_>), dim3((unsigned)blocks), dim3(256), 0,
-                                       s, (const TX_*)res, (const TX_*)br, (TX_*)X, B, Ci, n));
+        MHC_WG_DISPATCH_WIDE(dt, decay, n,
+                             MHC_LAUNCH_GGL((wgen_synth_kernel<TX_, TX_, NM_, D_>), dim3((unsigned)blocks), dim3(256),
+                                            0, s, (const TX_*)res, (const TX_*)br, (TX_*)X, B, Ci, n));
     }
     timing_end(tok, s);
     return hipGetLastError();

@@ -141,13 +141,14 @@ class MHCResidualWrapper(nn.Module):
     T > 1 and as [B*T, C] otherwise (layer.py:319-320).  ``use_post_norm``
     is accepted and ignored, as in the reference (layer.py:261).
 
-    For hidden % 4 == 0 and n = 2..32 (static H) or n = 2..8 (dynamic H) it
-    runs fused (ops.mhc_residual_wrapper):
-    the layer's [B*T, n, C] output is never materialised, and the stream
-    tensor of layer.py:299-310 only where the dynamic projection needs it
-    (n != 4 with fp32 storage, fewer than 1024 tokens or hidden % 64 != 0,
-    and Sinkhorn settings that keep the H_res gradients).  Other shapes
-    build the streams with tensor ops and run the layer.
+    For hidden % 4 == 0 and n = 2..32 it runs fused
+    (ops.mhc_residual_wrapper; with dynamic H past n = 10 at Sinkhorn
+    settings under which the H_res gradients vanish, the defaults): the
+    layer's [B*T, n, C] output is never materialised, and the stream tensor
+    of layer.py:299-310 only where the dynamic projection needs it (n != 4
+    with fp32 storage, fewer than 1024 tokens or hidden % 64 != 0, Sinkhorn
+    settings that keep the H_res gradients, and the backward past n = 8).
+    Other shapes build the streams with tensor ops and run the layer.
     """
 
     def __init__(self, hidden_dim: int, expansion_rate: int = 4, residual_mode: str = 'decay',

@@ -227,15 +227,19 @@ def mhc_residual_wrapper(residual: torch.Tensor, branch_output: torch.Tensor, la
     parameters of ``layer`` (an MHCLayer); returns fp32 [tokens, C]."""
     n = layer.expansion_rate
     C = residual.shape[-1]
-    # The fused wrapper kernels take 4-channel rows and n = 2..32 with static
-    # H, n = 2..8 with dynamic H (and n*C a multiple of the projection's k
-    # step of 32, up to 2^22).  Other shapes build the n streams with device
-    # tensor ops, as layer.py:299-310 does, and run the layer on them
-    # (layer.py:313-316).
+    # The fused wrapper kernels take 4-channel rows and n = 2..32; with
+    # dynamic H also n*C a multiple of the projection's k step of 32, up to
+    # 2^22, and past n = 10 (2n + n^2 > 128 projection rows) Sinkhorn
+    # settings under which the H_res gradients vanish (at least one
+    # iteration, eps <= 1e-6: the defaults).  Other shapes build the n
+    # streams with device tensor ops, as layer.py:299-310 does, and run the
+    # layer on them (layer.py:313-316).
+    fused = 2 <= n <= 32 and C % 4 == 0
     if layer.use_dynamic_h:
-        fused = 2 <= n <= 8 and C % 4 == 0 and (n * C) % 32 == 0 and n * C <= 1 << 22
-    else:
-        fused = 2 <= n <= 32 and C % 4 == 0
+        # the library's test, in float32: iters >= 1 and 0 <= eps <= 1e-6f
+        eps32 = float(torch.tensor(float(layer.sinkhorn_eps), dtype=torch.float32))
+        vanish = int(layer.num_sinkhorn_iters) >= 1 and 0.0 <= eps32 <= float(torch.tensor(1e-6, dtype=torch.float32))
+        fused = fused and (n * C) % 32 == 0 and n * C <= 1 << 22 and (n <= 10 or vanish)
     if not fused:
         if n < 2:
             raise RuntimeError("mhc_residual_wrapper: expansion_rate must be >= 2 (stream 1 holds the branch)")

@@ -90,9 +90,9 @@ def test_expansion_rate_support_on_host():
     fixed-n kernels for {2, 4, 8, 16, 32}, the generic kernels for the rest,
     dynamic H included (its 2n + n^2 projection rows run as 32-row output
     tiles or, above 128 rows, the streaming kernels); n > 64 is rejected.
-    The fused wrapper takes n = 2..32 with static H and n = 2..8 with
-    dynamic H (other n go through the layer).  All checked before any device
-    work."""
+    The fused wrapper takes n = 2..32 (other n go through the layer); with
+    dynamic H past n = 10 its backward needs Sinkhorn settings under which
+    the H_res gradients vanish.  All checked before any device work."""
     lib = _lib.load()
     # static layer: these n pass the host checks; with a null x they fail on that
     for n in (1, 2, 3, 6, 8, 12, 16, 32, 64):
@@ -111,14 +111,22 @@ def test_expansion_rate_support_on_host():
                                    1e-5, None)
     assert rc == -1 and b"null x/out" in lib.mhc_last_error()
     rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 33, 256, 20, 1e-8, 1e-5, None)
-    assert rc == -2 and b"the fused wrapper takes n <= 32 with static H" in lib.mhc_last_error()
-    rc = lib.mhc_wrapper_dynamic_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1 << 30, 8, 16, 256, 20,
+    assert rc == -2 and b"the fused wrapper takes n <= 32" in lib.mhc_last_error()
+    rc = lib.mhc_wrapper_dynamic_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1 << 30, 8, 33, 256, 20,
                                      1e-8, 1e-5, None)
-    assert rc == -2 and b"the fused wrapper takes n <= 8 with dynamic H" in lib.mhc_last_error()
-    # static n = 16 and 32 pass the shape checks; a null out then fails before any launch
+    assert rc == -2 and b"the fused wrapper takes n <= 32" in lib.mhc_last_error()
+    # n = 16 and 32 pass the shape checks; a null out then fails before any launch
     for n in (16, 32):
         rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, None, 1, 8, n, 256, 20, 1e-8, 1e-5, None)
         assert rc == -1 and b"null residual/branch/out" in lib.mhc_last_error()
+        rc = lib.mhc_wrapper_dynamic_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, 1, 1, 1 << 30, 8, n, 256,
+                                         20, 1e-8, 1e-5, None)
+        assert rc == -1 and b"null residual/branch/out" in lib.mhc_last_error()
+    # dynamic n = 16 backward with no Sinkhorn iteration (H_res gradients kept:
+    # 288 projection rows) is refused before the workspace is looked at
+    rc = lib.mhc_wrapper_dynamic_bwd(1, 1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, None, 0, 8, 16, 256, 0,
+                                     1e-8, 1e-5, None)
+    assert rc == -2 and b"needs num_iters >= 1 and sinkhorn_eps <= 1e-6" in lib.mhc_last_error()
     rc = lib.mhc_wrapper_static_fwd(1, 1, 1, 0, 1, 1, 1, 1, 1, 1, 1, 8, 1, 256, 20, 1e-8, 1e-5, None)
     assert rc == -1 and b"n must be >= 2" in lib.mhc_last_error()
     # n = 2 passes the shape checks; a null out then fails before any launch

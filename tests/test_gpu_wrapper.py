@@ -145,10 +145,9 @@ def test_wrapper_config_c5_width(device, dynamic):
                                          (6, True, 128), (3, True, 96)])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
 def test_wrapper_general_n(device, n, dynamic, C, mode):
-    """Other expansion rates on fp32 rows: n = 2..8 (and n = 32 with static
-    H) run the run-time-n wrapper kernels; n = 32 with dynamic H and rows
-    that are not a multiple of 4 build the streams with device tensor ops and
-    run them through the layer."""
+    """Other expansion rates on fp32 rows: n = 2..8 and 32 run the run-time-n
+    wrapper kernels; rows that are not a multiple of 4 build the streams
+    with device tensor ops and run them through the layer."""
     torch.manual_seed(n)
     wrap = mhc.MHCResidualWrapper(C, n, use_dynamic_h=dynamic)
     wrap.residual_mode = mode
@@ -212,7 +211,7 @@ def test_wrapper_eval_no_grad_matches_training_forward(device):
 
 
 @pytest.mark.parametrize("n,dynamic", [(4, True), (4, False), (3, True), (3, False), (8, True), (8, False),
-                                       (16, False)])
+                                       (10, True), (16, False)])
 @pytest.mark.parametrize("iters,eps", [(0, 1e-8), (1, 1e-8), (1, 0.1), (20, 0.1)])
 def test_wrapper_sinkhorn_settings(device, n, dynamic, iters, eps):
     """Both sides of the rule that writes the H_res gradients as zeros.
@@ -224,10 +223,12 @@ def test_wrapper_sinkhorn_settings(device, n, dynamic, iters, eps):
     iteration or none they are of the order of the other gradients; after
     20 iterations at eps = 0.1 about 1e-12 of them, measured on the
     oracle).  n = 3 and 8 run the run-time-n kernels (at n = 8 with all 80
-    projection rows: the small-np projection backward), and n = 16 with
-    static H (dynamic H at n = 16 is the tensor-op path, whose bf16 stream
-    gradients are rounded once per stream before autograd sums them, more
-    than this test's one-rounding tolerance)."""
+    projection rows: the small-np projection backward), n = 10 with dynamic
+    H (120 rows: the most the fused wrapper carries when the H_res
+    gradients do not vanish) and n = 16 with static H (dynamic H at n = 16
+    takes the tensor-op path at the settings that keep the H_res gradients,
+    and its bf16 stream gradients are rounded once per stream before
+    autograd sums them, more than this test's one-rounding tolerance)."""
     C, B = 256, 37
     seed = 900 + iters + int(eps * 100) + (7 if dynamic else 0) + 10 * n
     wrap = _make(C, dynamic, seed, n=n)
@@ -349,3 +350,44 @@ def test_wrapper_static_wide_n_many_tokens(device, n):
     want = _oracle(wrap, res, br, grad, "decay")
     got = _run(wrap, res, br, grad, device)
     _check(got, want, torch.bfloat16, STA, f"n={n} B={B}")
+
+
+@pytest.mark.parametrize("n,C", [(9, 96), (12, 256), (16, 160), (20, 64), (32, 128), (16, 1104)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", ["decay", "zero"])
+def test_wrapper_dynamic_wide_n_matches_oracle(device, n, C, dtype, mode):
+    """Dynamic H at n = 9..32 (past the dPhi / fold kernels): the row
+    kernels with 16- and 32-stream capacity, the stream rows in fp32 for the
+    projection backward over the 2n pre / post rows of dP (one 32-row tile
+    up to n = 16, the small-np kernels above), the coefficient backward with
+    no Sinkhorn adjoint - against the float64 oracle, every output and
+    gradient, both storage dtypes and residual modes."""
+    seed = 6000 + 10 * n + (3 if mode == "zero" else 0) + (1 if dtype == torch.bfloat16 else 0)
+    wrap = _make(C, True, seed, n=n)
+    wrap.residual_mode = mode
+    g = _gen(seed + 2)
+    shape = (2, 3, C) if C > 1024 else (37, C)
+    res = torch.randn(*shape, generator=g).to(dtype)
+    br = torch.randn(*shape, generator=g).to(dtype)
+    grad = torch.randn(*shape, generator=g)
+    want = _oracle(wrap, res, br, grad, mode)
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, dtype, DYN, f"n={n} C={C} {dtype} {mode}")
+
+
+@pytest.mark.parametrize("n,C", [(16, 128), (32, 64)])
+def test_wrapper_dynamic_wide_n_many_tokens(device, n, C):
+    """Dynamic H at n = 16 and 32 on 1100 bf16 tokens with whole 64-channel
+    stages: the forward projection rebuilds the streams inside the streaming
+    projection kernel (288 / 1088 rows) - against the float64 oracle, every
+    gradient."""
+    B = 1100
+    seed = 7000 + n
+    wrap = _make(C, True, seed, n=n)
+    g = _gen(seed + 2)
+    res = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    br = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    grad = torch.randn(B, C, generator=g)
+    want = _oracle(wrap, res, br, grad, "decay")
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, torch.bfloat16, DYN, f"n={n} B={B}")
