@@ -422,8 +422,9 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
 // (the dynamic-H backward without stream rows) take n <= kWgFoldMaxN.
 constexpr int kWgMaxN = 32;
 constexpr int kWgFoldMaxN = 8;
-// Floats per token of the per-token factors of d r / d b.
-constexpr int kWgEp = 8;
+// Floats per token of the per-token factors of d r / d b (and h_pre up to
+// capacity 8).
+constexpr int kWgEp = 16;
 bool wgen_supported(int n, int64_t C);
 hipError_t launch_wgen_fwd(int dt, int n, bool decay, const void* res, const void* br, const float* w,
                            const float* coef, int64_t coef_stride, float* out, int64_t B, int64_t C, float eps,

@@ -222,7 +222,8 @@ __global__ __launch_bounds__(256) void wgen_fwd_kernel(const TX* __restrict__ re
 // every lane: sum dh_post_act), since dM_ij does not depend on i, and
 // spread over the n*n+2n slots once per wave.  Both write the per-token
 // factors of d r / d b, ep_out[b][kWgEp]:
-//   [A_r, B_r hs/r, A_b, B_b hs/r, hs/r, -B_r k2, -B_b k2, 0]
+//   [A_r, B_r hs/r, A_b, B_b hs/r, hs/r, -B_r k2, -B_b k2, 0, h_pre_0..7]
+// (h_pre only up to capacity 8: the wider kernels read it from coef)
 // with A_r = sum_j w_j cm_j, B_r = sum_j w_j h_pre_j, A_b = cm_1,
 // B_b = h_pre_1, so that d r = A_r G + B_r gxa and d b = A_b G + B_b gxa.
 // ---------------------------------------------------------------------------
@@ -350,6 +351,8 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
         rec[5] = -b_r * k2;
         rec[6] = -b_b * k2;
         rec[7] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rec[8 + j] = NM <= 8 && j < NM ? hp[j < NM ? j : 0] : 0.f;
         float ev = 0.f;
 #pragma unroll
         for (int k = 0; k < kWgEp; ++k) ev = (lane == k) ? rec[k] : ev;
@@ -395,10 +398,12 @@ __global__ __launch_bounds__(256) void wgen_dx_kernel(const float* __restrict__ 
     for (int64_t b = t0; b < t1; ++b) {
         const float* e = ep + b * kWgEp;
         const float e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3], e4 = e[4], e5 = e[5], e6 = e[6];
+        // h_pre from the record (one scalar load with the factors) up to
+        // capacity 8, else from the coefficients
         const float* cf = coef + b * coef_stride;
         float hp[NM];
 #pragma unroll
-        for (int j = 0; j < NM; ++j) hp[j] = j < n ? cf[j] : 0.f;
+        for (int j = 0; j < NM; ++j) hp[j] = NM <= 8 ? e[8 + (j < 8 ? j : 0)] : (j < n ? cf[j] : 0.f);
         const float sv = DYN ? s_tok[b] : 0.f;
         if (!active) continue;
         const int64_t o = b * (int64_t)C + c0;
@@ -650,10 +655,12 @@ __global__ __launch_bounds__(256) void wgen_dx_fold_kernel(
     for (int64_t b = t0; b < t1; ++b) {
         const float* e = ep + b * kWgEp;
         const float e0 = e[0], e1 = e[1], e2 = e[2], e3 = e[3], e4 = e[4], e5 = e[5], e6 = e[6];
+        // h_pre from the record (one scalar load with the factors) up to
+        // capacity 8, else from the coefficients
         const float* cf = coef + b * coef_stride;
         float hp[NM];
 #pragma unroll
-        for (int j = 0; j < NM; ++j) hp[j] = j < n ? cf[j] : 0.f;
+        for (int j = 0; j < NM; ++j) hp[j] = NM <= 8 ? e[8 + (j < 8 ? j : 0)] : (j < n ? cf[j] : 0.f);
         const float sv = s_tok[b];
         const float* d = dP + b * dp_stride;
         float dv[kWgRows];
