@@ -36,7 +36,7 @@ def test_layer_deterministic(device, dynamic, dtype):
     _twice(lambda: _module_run(layer, [x], go))
 
 
-@pytest.mark.parametrize("n", [4, 8])
+@pytest.mark.parametrize("n", [4, 8, 32])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_wrapper_deterministic(device, n, dynamic, dtype):

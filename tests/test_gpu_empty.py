@@ -65,7 +65,7 @@ def test_layer_on_empty_batch(device, dynamic, dtype):
     _zero_grads(layer)
 
 
-@pytest.mark.parametrize("n", [4, 6])
+@pytest.mark.parametrize("n", [4, 6, 16])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["decay", "zero"])

@@ -35,7 +35,7 @@ def test_layer_transposed_input(device, dynamic, dtype):
     _same(_run(layer, [view], go), _run(layer, [view.contiguous()], go), "layer")
 
 
-@pytest.mark.parametrize("n", [4, 3])
+@pytest.mark.parametrize("n", [4, 3, 16])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_wrapper_strided_inputs(device, n, dynamic, dtype):

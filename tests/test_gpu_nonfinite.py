@@ -62,7 +62,7 @@ def test_layer_nonfinite_token(device, dynamic, value):
     assert torch.isfinite(out[keep]).all() and torch.isfinite(xd.grad[keep]).all()
 
 
-@pytest.mark.parametrize("n", [4, 5])
+@pytest.mark.parametrize("n", [4, 5, 16])
 @pytest.mark.parametrize("dynamic", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("value", [float("nan"), float("inf")])
