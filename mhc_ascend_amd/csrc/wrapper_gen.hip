@@ -292,6 +292,7 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
         const float gwx = rs[1];
         const float k2 = hs * gwx * inv * inv * inv / (float)C;
         if constexpr (STATIC) {
+            // lane j's stream sums (u_j, v_j, z_j) into its running sums
             float uu = 0.f, vv = 0.f, zz = 0.f;
 #pragma unroll
             for (int jj = 0; jj < NM; ++jj) {
@@ -299,9 +300,9 @@ __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__
                 vv = (jj == lane) ? rs[2 + NM + jj] : vv;
                 zz = (jj == lane) ? rs[2 + 2 * NM + jj] : zz;
             }
-            acc_u += uu * inv_n;                // dM_ij = u_j / n
+            acc_u += uu * inv_n;                 // dM_ij = u_j / n
             acc_pre += hs * inv * vv - k2 * zz;  // dh_pre_act_j
-            acc_post += gwx * inv * inv_n;      // dh_post_act_i
+            acc_post += gwx * inv * inv_n;       // dh_post_act_i
         } else {
             auto slot = [&](int t) __attribute__((always_inline)) {
                 float v = 0.f;
