@@ -7,7 +7,8 @@
 // 'decay' mode, 0 in 'zero' mode: layer.py:299-310), with n taken at run
 // time: per-stream arrays have a compile-time capacity NM in {2, 4, 8, 16,
 // 32} (the dPhi / fold kernels: up to 8) and their loops run over it with a
-// uniform j < n test, so nothing is indexed at run time in registers.  The math is that of wrapper.hip:
+// uniform j < n test, so nothing is indexed at run time in registers.  The
+// math is that of wrapper.hip:
 //   forward   out = hs (xa / r) w + sum_j cm_j X_j,  xa = sum_j h_pre_j X_j,
 //             r = sqrt(mean_c xa^2 + eps),  hs = (1/n) sum_i h_post_i,
 //             cm_j = (1/n) sum_i M_ij  (the stream mean of layer.py:316)
@@ -223,9 +224,9 @@ __global__ __launch_bounds__(256) void wgen_fwd_kernel(const TX* __restrict__ re
 // spread over the n*n+2n slots once per wave.  Both write the per-token
 // factors of d r / d b, ep_out[b][kWgEp]:
 //   [A_r, B_r hs/r, A_b, B_b hs/r, hs/r, -B_r k2, -B_b k2, 0, h_pre_0..7]
-// (h_pre only up to capacity 8: the wider kernels read it from coef)
 // with A_r = sum_j w_j cm_j, B_r = sum_j w_j h_pre_j, A_b = cm_1,
-// B_b = h_pre_1, so that d r = A_r G + B_r gxa and d b = A_b G + B_b gxa.
+// B_b = h_pre_1, so that d r = A_r G + B_r gxa and d b = A_b G + B_b gxa
+// (h_pre only up to capacity 8: the wider kernels read it from coef).
 // ---------------------------------------------------------------------------
 template <typename TX, int NM, bool DECAY, bool STATIC>
 __global__ __launch_bounds__(256) void wgen_red_kernel(const float* __restrict__ g, const TX* __restrict__ res,
