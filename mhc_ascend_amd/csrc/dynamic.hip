@@ -1367,16 +1367,14 @@ __global__ __launch_bounds__(1024) void small_column_sum_kernel(const float* __r
         const int col = c0 + cl;
         float s = 0.f;
         if (col < cols) {
+            // the phase's rows in order, 8 loads in flight
             int q = ph;
-            for (; q + 96 < rows; q += 128) {
-                const float a0 = part[(int64_t)q * cols + col];
-                const float a1 = part[(int64_t)(q + 32) * cols + col];
-                const float a2 = part[(int64_t)(q + 64) * cols + col];
-                const float a3 = part[(int64_t)(q + 96) * cols + col];
-                s += a0;
-                s += a1;
-                s += a2;
-                s += a3;
+            for (; q + 224 < rows; q += 256) {
+                float a[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) a[k] = part[(int64_t)(q + 32 * k) * cols + col];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) s += a[k];
             }
             for (; q < rows; q += 32) s += part[(int64_t)q * cols + col];
         }
