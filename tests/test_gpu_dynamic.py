@@ -174,14 +174,15 @@ def test_dynamic_layer_unsupported_n_raises(device):
 
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("n,B,C", [(1, 9, 96), (3, 7, 96), (3, 1100, 64), (5, 9, 160), (6, 5, 64), (6, 1100, 64),
-                                   (7, 3, 32), (12, 4, 128), (20, 3, 64), (64, 3, 64), (64, 300, 64)])
+                                   (6, 4200, 32), (7, 3, 32), (12, 4, 128), (20, 3, 64), (64, 3, 64), (64, 300, 64)])
 def test_dynamic_layer_runtime_n(device, x_dtype, n, B, C):
     """Expansion rates without a fixed-n kernel (the reference takes any n up
     to 64, mhc_types.h:68): the generic row kernels, the per-token Sinkhorn on
     16 / 32 / 64-lane groups with n at run time, dM on zero-padded fp32 MFMA
     blocks; the projection over 2n + n^2 rows (15 .. 4224) in 32-row tiles or
     the streaming kernels.  B = 1100 runs more tokens than the backward has
-    workgroups (and, with bf16 x at n = 6, the one-pass projection); at
+    workgroups (and, with bf16 x at n = 6, the one-pass projection, also
+    over 4200 tokens); at
     n = 64, 300 tokens are more than the Sinkhorn history region's 200 token
     slots, so each slot takes several tokens."""
     d = R.dynamic_layer_inputs(B, n, C, seed=n * 100 + B + C, x_dtype=x_dtype, alpha=0.1, phi_std=0.02, b_std=0.5)

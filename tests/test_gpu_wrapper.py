@@ -391,3 +391,20 @@ def test_wrapper_dynamic_wide_n_many_tokens(device, n, C):
     want = _oracle(wrap, res, br, grad, "decay")
     got = _run(wrap, res, br, grad, device)
     _check(got, want, torch.bfloat16, DYN, f"n={n} B={B}")
+
+
+@pytest.mark.parametrize("n,C", [(5, 128), (16, 64)])
+def test_wrapper_projection_many_token_blocks(device, n, C):
+    """4200 bf16 tokens (65 full 64-token blocks of the streaming projection
+    and a partial one) with the projection rebuilding the streams from
+    residual and branch - against the float64 oracle, every gradient."""
+    B = 4200
+    seed = 8000 + n
+    wrap = _make(C, True, seed, n=n)
+    g = _gen(seed + 2)
+    res = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    br = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    grad = torch.randn(B, C, generator=g)
+    want = _oracle(wrap, res, br, grad, "decay")
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, torch.bfloat16, DYN, f"n={n} B={B}")
