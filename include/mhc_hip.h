@@ -312,7 +312,8 @@ int mhc_layer_bwd_dynamic(const float* grad_output, const void* x, int32_t x_dty
  * of X from the workspace (except with bf16 storage, n >= 5, tokens >= 1024
  * and hidden % 64 == 0, where it too rebuilds X), and so does the backward
  * (fp32) when the Sinkhorn settings keep the H_res gradients (num_iters == 0
- * or sinkhorn_eps > 1e-6) or n > 8; the queries below size both.
+ * or sinkhorn_eps > 1e-6), and for n > 16, or n > 8 with hidden < 2048; the
+ * queries below size both.
  * Parameters and `saved` are those of the layer entries above.  Backward:
  * grad_out [tokens, hidden] fp32 -> grad_residual, grad_branch (dtype) and
  * the layer's parameter gradients.

@@ -1332,6 +1332,16 @@ static size_t wgen_fwd_need(const WgenFwdWs& w, int32_t dtype, int32_t n, int32_
 // Otherwise (all 2n + n^2 rows) the layer's projection backward runs on the
 // stream rows X and writes dX = dP . Phi, which wgen_dx_kernel folds; the
 // size query has no Sinkhorn settings, so X and dX are always reserved.
+// The dPhi / fold kernels (no stream rows in the backward) where the H_res
+// rows vanish: n <= 8, and n <= kWgFoldMaxN on rows of at least 2048
+// channels (narrower rows leave the fold's 512-channel workgroups too few
+// for the per-workgroup fold of Phi over 2n rows and n streams; measured at
+// n = 16, 8192 tokens: 1.29 against 1.13 ms per step at 1024 channels,
+// 3.58 against 4.09 at 4096).
+static bool wgen_fold_ok(int32_t n, int32_t hidden) {
+    return n <= 8 || (n <= kWgFoldMaxN && hidden >= 2048);
+}
+
 struct WgenBwdWs {
     int cblocks, ptiles, dtiles, qtiles, ftiles, srows;
     size_t ep_off, dw_off, stw_off, scal_off, ssum_off, hist_off, dp_off, s_off, cpart_off, x_off, dx_off, part_off,
@@ -1366,14 +1376,14 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
     w.s_off = o; o += align256((size_t)tokens * 4);
     w.cpart_off = o; o += align256((size_t)w.cblocks * (np + 3) * 4);
     // dPhi partials: the 2n pre / post rows per wgen_dphi_kernel tile
-    // (n <= kWgFoldMaxN), or the one-tile projection backward's (np rows
-    // when np <= 32, the 2n pre / post rows when 2n <= 32 and n is past the
-    // fold kernels; more rows go through launch_proj_bwd_small, which
-    // writes dPhi directly)
+    // (wgen_fold_ok), or the one-tile projection backward's (np rows when
+    // np <= 32, the 2n pre / post rows when 2n <= 32 without the fold; more
+    // rows go through launch_proj_bwd_small, which writes dPhi directly)
     w.qtiles = tokens > 0 ? wgen_dphi_tiles(tokens, hidden) : 1;
-    size_t part = n <= kWgFoldMaxN ? (size_t)w.qtiles * 2 * n : 0;
+    size_t part = wgen_fold_ok(n, hidden) ? (size_t)w.qtiles * 2 * n : 0;
     if (np <= kProjTile && (size_t)w.ptiles * np > part) part = (size_t)w.ptiles * np;
-    if (n > kWgFoldMaxN && 2 * n <= kProjTile && (size_t)w.ptiles * 2 * n > part) part = (size_t)w.ptiles * 2 * n;
+    if (!wgen_fold_ok(n, hidden) && 2 * n <= kProjTile && (size_t)w.ptiles * 2 * n > part)
+        part = (size_t)w.ptiles * 2 * n;
     const int64_t srows = np <= kProjTile ? np : 2 * n;
     w.part_off = o; o += align256(part * K * 4);
     w.stp_off = o; o += align256(column_sums_stage_floats(srows * K) * 4);
@@ -1384,10 +1394,10 @@ static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dyn
 }
 
 // The run-time-n backward keeps the stream rows X and dX (the last regions
-// of its workspace) only when the H_res rows of dP do not vanish or n is
-// past the fold kernels.
-static size_t wgen_bwd_need(const WgenBwdWs& w, int32_t n, int32_t num_iters, float sinkhorn_eps) {
-    return n <= kWgFoldMaxN && wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? w.x_off : w.total;
+// of its workspace) only when the H_res rows of dP do not vanish or the
+// shape is not one for the fold kernels.
+static size_t wgen_bwd_need(const WgenBwdWs& w, int32_t n, int32_t hidden, int32_t num_iters, float sinkhorn_eps) {
+    return wgen_fold_ok(n, hidden) && wrap_res_grad_vanishes(num_iters, sinkhorn_eps) ? w.x_off : w.total;
 }
 
 static int wgen_dynamic_fwd(const void* residual, const void* branch, int32_t dtype, bool decay, const void* weight,
@@ -1454,7 +1464,7 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
                                              " the fused wrapper needs num_iters >= 1 and sinkhorn_eps <= 1e-6 "
                                              "(the H_res gradients then vanish)");
     const WgenBwdWs w = wgen_bwd_ws(tokens, n, hidden, true);
-    if (!workspace || workspace_bytes < wgen_bwd_need(w, n, num_iters, sinkhorn_eps))
+    if (!workspace || workspace_bytes < wgen_bwd_need(w, n, hidden, num_iters, sinkhorn_eps))
         return fail(MHC_ERR_WORKSPACE,
                     "wrapper_dynamic_bwd: workspace smaller than mhc_wrapper_dynamic_bwd_workspace_size_for()");
     char* ws = (char*)workspace;
@@ -1472,8 +1482,8 @@ static int wgen_dynamic_bwd(const float* grad_out, const void* residual, const v
     const DynSaved d = dyn_saved(tokens, n, hidden);
     const float* w32 = saved + d.w_off;
     const int64_t K = (int64_t)n * hidden;
-    // up to n = kWgFoldMaxN the pre / post rows need no stream rows
-    const bool fold = rows < np && n <= kWgFoldMaxN;
+    // the fold kernels' shapes carry the pre / post rows without stream rows
+    const bool fold = rows < np && wgen_fold_ok(n, hidden);
     hipError_t e = hipSuccess;
     int rows_w = fold ? w.ftiles : w.dtiles, rows_c = w.cblocks;
     if (tokens == 0) {
@@ -1715,7 +1725,7 @@ size_t mhc_wrapper_dynamic_bwd_workspace_size_for(int64_t tokens, int32_t n, int
                                                   int32_t residual_mode, int32_t num_iters, float sinkhorn_eps) {
     if (tokens < 0 || n < 1 || hidden < 1) return 0;
     if (!wrap_fused4(n, hidden, true))
-        return wgen_bwd_need(wgen_bwd_ws(tokens, n, hidden, true), n, num_iters, sinkhorn_eps);
+        return wgen_bwd_need(wgen_bwd_ws(tokens, n, hidden, true), n, hidden, num_iters, sinkhorn_eps);
     return wrap_bwd_ws(tokens, n, hidden, dtype, true, residual_mode == MHC_WRAPPER_DECAY).total;
 }
 

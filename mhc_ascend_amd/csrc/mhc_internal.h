@@ -421,7 +421,7 @@ hipError_t launch_wrap_proj_bwd(int dt, int n, bool decay, const float* g, const
 // kernels above do not take); hidden % 4 == 0.  The dPhi / fold kernels
 // (the dynamic-H backward without stream rows) take n <= kWgFoldMaxN.
 constexpr int kWgMaxN = 32;
-constexpr int kWgFoldMaxN = 8;
+constexpr int kWgFoldMaxN = 16;
 // Floats per token of the per-token factors of d r / d b (and h_pre up to
 // capacity 8).
 constexpr int kWgEp = 16;

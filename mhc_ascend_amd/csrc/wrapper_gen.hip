@@ -6,7 +6,7 @@
 // (X_0 = r, X_1 = b, X_j = r * 0.1^(j-1) rounded to the storage dtype in
 // 'decay' mode, 0 in 'zero' mode: layer.py:299-310), with n taken at run
 // time: per-stream arrays have a compile-time capacity NM in {2, 4, 8, 16,
-// 32} (the dPhi / fold kernels: up to 8) and their loops run over it with a
+// 32} (the dPhi / fold kernels: up to 16) and their loops run over it with a
 // uniform j < n test, so nothing is indexed at run time in registers.  The
 // math is that of wrapper.hip:
 //   forward   out = hs (xa / r) w + sum_j cm_j X_j,  xa = sum_j h_pre_j X_j,
@@ -27,8 +27,10 @@
 //                      workgroups of 1024 channels x one token tile; with
 //                      dynamic H it adds the layer projection backward's dX
 //                      folded over the streams (Sinkhorn settings where the
-//                      H_res rows of dP do not vanish, and n > 8)
-//   wgen_dphi_mfma_kernel  dynamic H, H_res rows of dP vanishing, n <= 8:
+//                      H_res rows of dP do not vanish, and shapes the fold
+//                      kernels do not take)
+//   wgen_dphi_mfma_kernel  dynamic H, H_res rows of dP vanishing, n <= 8, or
+//                      n <= 16 on rows of 2048 channels or more:
 //                      dPhi of the 2n pre / post rows from the rebuilt
 //                      streams (bf16 MFMA)
 //   wgen_dx_fold_kernel  the same case: d r, d b with dP . Phi folded over
@@ -36,7 +38,7 @@
 //   wgen_synth_kernel  the stream rows [tokens, n*C] as the operand of the
 //                      layer's projection kernels (dynamic H: the forward's
 //                      in the storage dtype; the backward's in fp32 when the
-//                      H_res rows do not vanish or n > 8)
+//                      fold kernels do not run)
 #include "mhc_device.h"
 #include "mhc_internal.h"
 
@@ -453,7 +455,6 @@ __global__ __launch_bounds__(256) void wgen_dx_kernel(const float* __restrict__ 
 //   dphi_part[tile][o][j*C + c] = sum over the tile's tokens of
 //                                 dP[t][o] X_j[t][c],  o < rows = 2n
 // ---------------------------------------------------------------------------
-constexpr int kWgRows = 2 * kWgFoldMaxN;  // pre / post rows of dP at most
 
 namespace {
 // two consecutive elements (4- or 8-byte aligned) as one load
@@ -512,10 +513,11 @@ __global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restric
                                                              int64_t tile) {
     constexpr int CB = kWgDphiCB;
     constexpr int TS = 32;
-    constexpr int RP = CB + 4;  // LDS row pitch (elements)
+    constexpr int RP = CB + 4;          // LDS row pitch (elements)
+    constexpr int MI = (2 * NM + 15) / 16;  // 16-row MFMA tiles of the 2n rows
     __shared__ __align__(16) float rl[TS][RP];
     __shared__ __align__(16) float bl[TS][RP];
-    __shared__ __align__(16) float dpt[16][TS + 4];
+    __shared__ __align__(16) float dpt[16 * MI][TS + 4];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
@@ -524,9 +526,12 @@ __global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restric
     const int64_t cb0 = (int64_t)blockIdx.x * CB;
     const int64_t t0 = (int64_t)blockIdx.y * tile;
     const int64_t t1 = t0 + tile < B ? t0 + tile : B;
-    gf32x4_t acc[NM];
+    gf32x4_t acc[NM][MI];
 #pragma unroll
-    for (int j = 0; j < NM; ++j) acc[j] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NM; ++j) {
+#pragma unroll
+        for (int m = 0; m < MI; ++m) acc[j][m] = gf32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
     for (int64_t s0 = t0; s0 < t1; s0 += TS) {
         // r and b tile: 32 tokens x 64 channels in 4-channel pieces, two per
         // thread (a piece is all in or all out of the row: C % 4 == 0)
@@ -545,9 +550,9 @@ __global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restric
             *reinterpret_cast<float4*>(&rl[tt][c4]) = make_float4(rv[0], rv[1], rv[2], rv[3]);
             *reinterpret_cast<float4*>(&bl[tt][c4]) = make_float4(bv[0], bv[1], bv[2], bv[3]);
         }
-        // dP^T tile [16 rows][32 tokens]
+        // dP^T tile [16 MI rows][32 tokens]
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < 2 * MI; ++u) {
             const int i = tid + 256 * u;
             const int o = i / TS;
             const int tt = i % TS;
@@ -555,12 +560,15 @@ __global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restric
             dpt[o][tt] = (o < rows && t < t1) ? dP[t * dp_stride + o] : 0.f;
         }
         __syncthreads();
-        // A = dP^T: row o = lr, tokens 8 lg .. + 7
-        float av[8];
+        // A = dP^T: row o = 16 m + lr, tokens 8 lg .. + 7
+        gu32x4_t ah[MI], al[MI];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) av[e] = dpt[lr][8 * lg + e];
-        gu32x4_t ah, al;
-        g_split8(av, ah, al);
+        for (int m = 0; m < MI; ++m) {
+            float av[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) av[e] = dpt[16 * m + lr][8 * lg + e];
+            g_split8(av, ah[m], al[m]);
+        }
         // B = X_j: tokens 8 lg .. + 7 of channel 16 wave + lr
         float rv[8], bv[8];
 #pragma unroll
@@ -578,20 +586,26 @@ __global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restric
                     gu32x4_t xb;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) xb[e] = pack_bf16x2(xv[2 * e], xv[2 * e + 1]);  // exact
-                    acc[j] = gmfma(ah, xb, acc[j]);
-                    acc[j] = gmfma(al, xb, acc[j]);
+#pragma unroll
+                    for (int m = 0; m < MI; ++m) {
+                        acc[j][m] = gmfma(ah[m], xb, acc[j][m]);
+                        acc[j][m] = gmfma(al[m], xb, acc[j][m]);
+                    }
                 } else {
                     gu32x4_t xh, xl;
                     g_split8(xv, xh, xl);
-                    acc[j] = gmfma(ah, xh, acc[j]);
-                    acc[j] = gmfma(al, xh, acc[j]);
-                    acc[j] = gmfma(ah, xl, acc[j]);
+#pragma unroll
+                    for (int m = 0; m < MI; ++m) {
+                        acc[j][m] = gmfma(ah[m], xh, acc[j][m]);
+                        acc[j][m] = gmfma(al[m], xh, acc[j][m]);
+                        acc[j][m] = gmfma(ah[m], xl, acc[j][m]);
+                    }
                 }
             }
         }
         __syncthreads();
     }
-    // D[o = 4 lg + i][channel 16 wave + lr]
+    // D[o = 16 m + 4 lg + i][channel 16 wave + lr]
     const int64_t c = cb0 + 16 * wave + lr;
     if (c >= C) return;
     const int64_t K = (int64_t)n * C;
@@ -600,9 +614,12 @@ __global__ __launch_bounds__(256) void wgen_dphi_mfma_kernel(const TX* __restric
     for (int j = 0; j < NM; ++j) {
         if (j < n) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int o = 4 * lg + i;
-                if (o < rows) part[o * K + (int64_t)j * C + c] = acc[j][i];
+            for (int m = 0; m < MI; ++m) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int o = 16 * m + 4 * lg + i;
+                    if (o < rows) part[o * K + (int64_t)j * C + c] = acc[j][m][i];
+                }
             }
         }
     }
@@ -630,9 +647,10 @@ __global__ __launch_bounds__(256) void wgen_dx_fold_kernel(
     const int64_t t0 = (int64_t)blockIdx.y * tile;
     const int64_t t1 = t0 + tile < B ? t0 + tile : B;
     const int64_t K = (int64_t)n * C;
-    float pr[kWgRows][2], pb[kWgRows][2];
+    constexpr int RW = 2 * NM;  // pre / post rows of dP at most
+    float pr[RW][2], pb[RW][2];
 #pragma unroll
-    for (int o = 0; o < kWgRows; ++o) {
+    for (int o = 0; o < RW; ++o) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             float vr = 0.f, vb = 0.f;
@@ -665,9 +683,9 @@ __global__ __launch_bounds__(256) void wgen_dx_fold_kernel(
         for (int j = 0; j < NM; ++j) hp[j] = NM <= 8 ? e[8 + (j < 8 ? j : 0)] : (j < n ? cf[j] : 0.f);
         const float sv = s_tok[b];
         const float* d = dP + b * dp_stride;
-        float dv[kWgRows];
+        float dv[RW];
 #pragma unroll
-        for (int o = 0; o < kWgRows; ++o) dv[o] = o < rows ? d[o] : 0.f;
+        for (int o = 0; o < RW; ++o) dv[o] = o < rows ? d[o] : 0.f;
         if (!active) continue;
         const int64_t off = b * (int64_t)C + c0;
         const float2 gg2 = *reinterpret_cast<const float2*>(g + off);
@@ -683,7 +701,7 @@ __global__ __launch_bounds__(256) void wgen_dx_fold_kernel(
             const float wg = wv[q] * gq;
             float pa = 0.f, pc = 0.f;
 #pragma unroll
-            for (int o = 0; o < kWgRows; ++o) {
+            for (int o = 0; o < RW; ++o) {
                 pa += dv[o] * pr[o][q];
                 pc += dv[o] * pb[o][q];
             }
@@ -745,21 +763,21 @@ __global__ __launch_bounds__(256) void wgen_synth_kernel(const TX* __restrict__ 
 bool wgen_supported(int n, int64_t C) { return n >= 2 && n <= kWgMaxN && C >= 4 && C % 4 == 0 && C <= (1 << 28); }
 
 // capacities of the dPhi / fold kernels (n <= kWgFoldMaxN)
-#define MHC_WG_NM(n, ...)                   \
-    if ((n) <= 2) {                         \
-        constexpr int NM_ = 2; __VA_ARGS__; \
-    } else if ((n) <= 4) {                  \
-        constexpr int NM_ = 4; __VA_ARGS__; \
-    } else {                                \
-        constexpr int NM_ = 8; __VA_ARGS__; \
+#define MHC_WG_NM(n, ...)                    \
+    if ((n) <= 2) {                          \
+        constexpr int NM_ = 2; __VA_ARGS__;  \
+    } else if ((n) <= 4) {                   \
+        constexpr int NM_ = 4; __VA_ARGS__;  \
+    } else if ((n) <= 8) {                   \
+        constexpr int NM_ = 8; __VA_ARGS__;  \
+    } else {                                 \
+        constexpr int NM_ = 16; __VA_ARGS__; \
     }
 
 // capacities of the row kernels (n <= kWgMaxN)
 #define MHC_WG_NM_WIDE(n, ...)               \
-    if ((n) <= 8) {                          \
+    if ((n) <= 16) {                         \
         MHC_WG_NM(n, __VA_ARGS__)            \
-    } else if ((n) <= 16) {                  \
-        constexpr int NM_ = 16; __VA_ARGS__; \
     } else {                                 \
         constexpr int NM_ = 32; __VA_ARGS__; \
     }
@@ -876,7 +894,7 @@ hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const vo
                             int dp_stride, int rows, float* dphi_part, int tiles, int64_t B, int64_t C,
                             hipStream_t s) {
     if (B == 0) return hipSuccess;
-    if (!wgen_supported(n, C) || n > kWgFoldMaxN || tiles < 1 || rows < 1 || rows > kWgRows)
+    if (!wgen_supported(n, C) || n > kWgFoldMaxN || tiles < 1 || rows < 1 || rows > 2 * n)
         return hipErrorInvalidValue;
     const int64_t tile = (B + tiles - 1) / tiles;
     const dim3 grid((unsigned)((C + kWgDphiCB - 1) / kWgDphiCB), (unsigned)tiles);
@@ -889,10 +907,15 @@ hipError_t launch_wgen_dphi(int dt, int n, bool decay, const void* res, const vo
     return hipGetLastError();
 }
 
+// Token tiles of wgen_dx_fold_kernel: 512-channel column blocks x tiles
+// about eight workgroups per CU, each tile at least 64 tokens (every
+// workgroup first folds its channels' Phi columns over the n streams: 4n^2
+// loads a lane, which a tile of a few tokens would not amortise).
 int wgen_fold_tiles(int64_t B, int64_t C) {
     const int64_t gx = (C + 511) / 512;
     int64_t tiles = (8 * (int64_t)device_cu_count() + gx - 1) / gx;
-    if (tiles > B) tiles = B;
+    const int64_t by_tokens = (B + 63) / 64;
+    if (tiles > by_tokens) tiles = by_tokens;
     if (tiles < 1) tiles = 1;
     return (int)tiles;
 }

@@ -147,7 +147,8 @@ class MHCResidualWrapper(nn.Module):
     layer's [B*T, n, C] output is never materialised, and the stream tensor
     of layer.py:299-310 only where the dynamic projection needs it (n != 4
     with fp32 storage, fewer than 1024 tokens or hidden % 64 != 0, Sinkhorn
-    settings that keep the H_res gradients, and the backward past n = 8).
+    settings that keep the H_res gradients, and the backward past n = 16 or
+    past n = 8 on rows narrower than 2048 channels).
     Other shapes build the streams with tensor ops and run the layer.
     """
 

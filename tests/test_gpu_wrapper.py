@@ -352,16 +352,18 @@ def test_wrapper_static_wide_n_many_tokens(device, n):
     _check(got, want, torch.bfloat16, STA, f"n={n} B={B}")
 
 
-@pytest.mark.parametrize("n,C", [(9, 96), (12, 256), (16, 160), (20, 64), (32, 128), (16, 1104)])
+@pytest.mark.parametrize("n,C", [(9, 96), (12, 256), (16, 160), (20, 64), (32, 128), (16, 1104), (12, 2048),
+                                 (16, 2048)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["decay", "zero"])
 def test_wrapper_dynamic_wide_n_matches_oracle(device, n, C, dtype, mode):
-    """Dynamic H at n = 9..32 (past the dPhi / fold kernels): the row
-    kernels with 16- and 32-stream capacity, the stream rows in fp32 for the
-    projection backward over the 2n pre / post rows of dP (one 32-row tile
-    up to n = 16, the small-np kernels above), the coefficient backward with
-    no Sinkhorn adjoint - against the float64 oracle, every output and
-    gradient, both storage dtypes and residual modes."""
+    """Dynamic H at n = 9..32: the row kernels with 16- and 32-stream
+    capacity, the coefficient backward with no Sinkhorn adjoint, and for the
+    2n pre / post rows of dP either the dPhi / fold kernels (n <= 16 on rows
+    of 2048 channels or more: 32 dP rows in two MFMA tiles) or fp32 stream
+    rows for the layer's projection backward (one 32-row tile up to n = 16,
+    the small-np kernels above) - against the float64 oracle, every output
+    and gradient, both storage dtypes and residual modes."""
     seed = 6000 + 10 * n + (3 if mode == "zero" else 0) + (1 if dtype == torch.bfloat16 else 0)
     wrap = _make(C, True, seed, n=n)
     wrap.residual_mode = mode
@@ -408,3 +410,18 @@ def test_wrapper_projection_many_token_blocks(device, n, C):
     want = _oracle(wrap, res, br, grad, "decay")
     got = _run(wrap, res, br, grad, device)
     _check(got, want, torch.bfloat16, DYN, f"n={n} B={B}")
+
+
+def test_wrapper_dynamic_fold_16_streams_many_tokens(device):
+    """Dynamic H at n = 16 on 2048-channel rows and 300 tokens: the dPhi /
+    fold kernels at their 16-stream capacity over several token tiles -
+    against the float64 oracle, every gradient."""
+    n, C, B = 16, 2048, 300
+    wrap = _make(C, True, 9100, n=n)
+    g = _gen(9102)
+    res = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    br = torch.randn(B, C, generator=g).to(torch.bfloat16)
+    grad = torch.randn(B, C, generator=g)
+    want = _oracle(wrap, res, br, grad, "decay")
+    got = _run(wrap, res, br, grad, device)
+    _check(got, want, torch.bfloat16, DYN, f"n={n} C={C} B={B}")
