@@ -1326,18 +1326,19 @@ static size_t wgen_fwd_need(const WgenFwdWs& w, int32_t dtype, int32_t n, int32_
 //   dynamic: [per-token scalars | dP | s | coefficient partials | dPhi
 //             partials | their stage | X (fp32) | dX (fp32)]
 // With dynamic H and wrap_res_grad_vanishes (the default Sinkhorn settings)
-// only the 2n pre / post rows of dP are carried, as by the n = 4 kernels:
-// wgen_dphi_kernel forms their dPhi from r and b and wgen_dx_fold_kernel
-// folds dP . Phi into d r / d b, so the stream rows never exist in memory.
-// Otherwise (all 2n + n^2 rows) the layer's projection backward runs on the
+// only the 2n pre / post rows of dP are carried, as by the n = 4 kernels;
+// on the shapes wgen_fold_ok takes, wgen_dphi_kernel forms their dPhi from
+// r and b and wgen_dx_fold_kernel folds dP . Phi into d r / d b, so the
+// stream rows never exist in memory.  Otherwise (all 2n + n^2 rows, or the
+// 2n rows on other shapes) the layer's projection backward runs on the
 // stream rows X and writes dX = dP . Phi, which wgen_dx_kernel folds; the
 // size query has no Sinkhorn settings, so X and dX are always reserved.
-// The dPhi / fold kernels (no stream rows in the backward) where the H_res
-// rows vanish: n <= 8, and n <= kWgFoldMaxN on rows of at least 2048
-// channels (narrower rows leave the fold's 512-channel workgroups too few
-// for the per-workgroup fold of Phi over 2n rows and n streams; measured at
-// n = 16, 8192 tokens: 1.29 against 1.13 ms per step at 1024 channels,
-// 3.58 against 4.09 at 4096).
+//
+// The dPhi / fold kernels: n <= 8, and n <= kWgFoldMaxN on rows of at least
+// 2048 channels (narrower rows leave the fold's 512-channel workgroups too
+// few for the per-workgroup fold of Phi over 2n rows and n streams;
+// measured at n = 16, 8192 tokens: 1.29 against 1.13 ms per step at 1024
+// channels, 3.58 against 4.09 at 4096).
 static bool wgen_fold_ok(int32_t n, int32_t hidden) {
     return n <= 8 || (n <= kWgFoldMaxN && hidden >= 2048);
 }
@@ -1347,7 +1348,6 @@ struct WgenBwdWs {
     size_t ep_off, dw_off, stw_off, scal_off, ssum_off, hist_off, dp_off, s_off, cpart_off, x_off, dx_off, part_off,
         stp_off, total;
 };
-
 
 static WgenBwdWs wgen_bwd_ws(int64_t tokens, int32_t n, int32_t hidden, bool dynamic) {
     WgenBwdWs w{};
