@@ -1047,6 +1047,18 @@ __global__ __launch_bounds__(256) void dyn_coef_gen_bwd_kernel(
         const float l_pre = active ? dt_pre * pv[rr] : 0.f, l_post = active ? dt_post * pv[n + rr] : 0.f;
         const float tot = group_sum<NM>(ap * l_pre + aq * l_post + ar * lp);
         const float s_pre = group_sum<NM>(l_pre), s_post = group_sum<NM>(l_post), s_res = group_sum<NM>(lp);
+        if constexpr (!RES) {
+            // the H_res rows' zeros, written by the whole lane group in
+            // consecutive runs
+            if (tv) {
+                float* dp = dp_out + tok * npt + 2 * n;
+                float* pt = part + tok * nv + 2 * n;
+                for (int q = r; q < n * n; q += NM) {
+                    dp[q] = 0.f;
+                    pt[q] = 0.f;
+                }
+            }
+        }
         if (active) {
             float* dp = dp_out + tok * npt;
             dp[r] = ap * dt_pre * inv;
@@ -1054,11 +1066,13 @@ __global__ __launch_bounds__(256) void dyn_coef_gen_bwd_kernel(
             float* pt = part + tok * nv;
             pt[r] = dt_pre;
             pt[n + r] = dt_post;
+            if constexpr (RES) {
 #pragma unroll
-            for (int c = 0; c < NM; ++c) {
-                if (c < n) {
-                    dp[2 * n + r * n + c] = ar * gm[c] * inv;
-                    pt[2 * n + r * n + c] = gm[c];
+                for (int c = 0; c < NM; ++c) {
+                    if (c < n) {
+                        dp[2 * n + r * n + c] = ar * gm[c] * inv;
+                        pt[2 * n + r * n + c] = gm[c];
+                    }
                 }
             }
             if (r == 0) {
