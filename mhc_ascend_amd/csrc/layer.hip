@@ -77,6 +77,16 @@ __global__ __launch_bounds__(256) void static_coef_kernel(const float* __restric
         float a = r < 16 ? expf(h_res[r]) : 0.f;
         sk16_forward(a, iters, eps);
         if (r < 16) saved[2 * N + r] = a;
+    } else if constexpr (N == skw16::kN) {
+        // the 16 x 16 matrix on wave 0, four elements per lane (the
+        // finalize's adjoint recomputes it with the same code)
+        const int i = skw16::row(), c0 = skw16::col0();
+        float a[skw16::kV];
+#pragma unroll
+        for (int k = 0; k < skw16::kV; ++k) a[k] = expf(h_res[i * N + c0 + k]);
+        skw16::forward(a, iters, eps);
+#pragma unroll
+        for (int k = 0; k < skw16::kV; ++k) saved[2 * N + i * N + c0 + k] = a[k];
     } else {
         float a[N];
 #pragma unroll

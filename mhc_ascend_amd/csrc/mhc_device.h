@@ -900,4 +900,87 @@ __device__ __forceinline__ void backward(float (&g)[kV], const float (&x0)[kV], 
 }
 }  // namespace skb
 
+// ---------------------------------------------------------------------------
+// Sinkhorn-Knopp on one 16 x 16 matrix held by one wave (the static H_res at
+// n = 16): lane t holds row t / 4, columns 4 (t % 4) .. 4 (t % 4) + 3.  A row
+// is a quad (DPP); a column is lanes t, t +- 4, t +- 8 of each 16-lane row
+// (row_ror 4 and 8, as sk16_col_sum) and the four rows (the lane-swap ops),
+// so an iteration is a few dozen full-rate instructions with no barrier.
+// Same formulas as sk_forward / sk_adjoint_step (ops_pytorch_backward.py:
+// 9-33, 36-72); the adjoint keeps each iteration's state in registers
+// (iters <= kTMax).  The whole wave must be active.
+// ---------------------------------------------------------------------------
+namespace skw16 {
+constexpr int kN = 16;
+constexpr int kV = 4;     // columns per lane
+constexpr int kTMax = 32; // iterations the adjoint keeps in registers
+
+__device__ __forceinline__ int row() { return (threadIdx.x & (kWave - 1)) >> 2; }
+__device__ __forceinline__ int col0() { return (threadIdx.x & 3) * kV; }
+
+__device__ __forceinline__ float col_sum(float v) {
+    v += dpp::mov<dpp::kRowRor4>(v);
+    v += dpp::mov<dpp::kRowRor8>(v);
+    v = xor16_add(v);
+    return xor32_add(v);
+}
+
+__device__ __forceinline__ void row_scale(float (&a)[kV], float eps, float& rinv) {
+    float s = ((a[0] + a[1]) + a[2]) + a[3];
+    s = group_sum<4>(s);
+    rinv = rcp_nr(s + eps);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] *= rinv;
+}
+
+__device__ __forceinline__ void col_scale(float (&a)[kV], float eps) {
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] *= rcp_nr(col_sum(a[k]) + eps);
+}
+
+// a: the lane's four elements of X in, of SK(X) out.
+__device__ __forceinline__ void forward(float (&a)[kV], int iters, float eps) {
+    for (int t = 0; t < iters; ++t) {
+        float ri;
+        row_scale(a, eps, ri);
+        col_scale(a, eps);
+    }
+}
+
+// g: the lane's elements of dL/dM in, dL/dX out; x0: elements of X.
+// Requires iters <= kTMax.
+__device__ __forceinline__ void backward(float (&g)[kV], const float (&x0)[kV], int iters, float eps) {
+    float hA[kTMax][kV], hr[kTMax];
+    float a[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] = x0[k];
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+        if (t < iters) {
+            row_scale(a, eps, hr[t]);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) hA[t][k] = a[k];
+            col_scale(a, eps);
+        }
+    }
+#pragma unroll
+    for (int t = kTMax - 1; t >= 0; --t) {
+        if (t < iters) {
+            // column step, then the row step of iteration t
+            float dA[kV];
+#pragma unroll
+            for (int k = 0; k < kV; ++k) {
+                const float cinv = rcp_nr(col_sum(hA[t][k]) + eps);
+                const float dot = col_sum(g[k] * (hA[t][k] * cinv));
+                dA[k] = (g[k] - dot) * cinv;
+            }
+            float rdot = ((dA[0] * hA[t][0] + dA[1] * hA[t][1]) + dA[2] * hA[t][2]) + dA[3] * hA[t][3];
+            rdot = group_sum<4>(rdot);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) g[k] = (dA[k] - rdot) * hr[t];
+        }
+    }
+}
+}  // namespace skw16
+
 }  // namespace mhc

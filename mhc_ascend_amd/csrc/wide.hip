@@ -624,6 +624,7 @@ __global__ __launch_bounds__(kWideThreads) void stream_gram_kernel(const float* 
 // finalize) dH_pre = dh_pre_act h_pre (1 - h_pre), dH_post = dh_post_act
 // h_post (1 - h_post / 2) and dH_res = SK^T(dM) * exp(H_res), the Sinkhorn
 // adjoint on the whole workgroup for n = 32 (iters <= skb::kTMax, state in
+// registers), on wave 0 for n = 16 (iters <= skw16::kTMax, state in
 // registers), otherwise one row per lane of the first n lanes with its
 // per-iteration state in hist (iters * (n + 1) * n floats) or, without hist,
 // recomputed.
@@ -686,7 +687,24 @@ __global__ __launch_bounds__(kStaticFinalizeThreads) void wide_static_finalize_k
             for (int k = 0; k < skb::kV; ++k) d_h_res[i * N + c0 + k] = gm[k] * e[k];
         }
     }
-    if (threadIdx.x < N && (N != skb::kN || iters > skb::kTMax)) {
+    if constexpr (N == skw16::kN) {
+        if (iters <= skw16::kTMax && threadIdx.x < kWave) {
+            // wave 0 on the 16 x 16 matrix, four elements per lane
+            const int i = skw16::row(), c0 = skw16::col0();
+            float e[skw16::kV], gm[skw16::kV];
+#pragma unroll
+            for (int k = 0; k < skw16::kV; ++k) {
+                e[k] = expf(h_res[i * N + c0 + k]);
+                gm[k] = tot[i * N + c0 + k];
+            }
+            skw16::backward(gm, e, iters, eps);
+#pragma unroll
+            for (int k = 0; k < skw16::kV; ++k) d_h_res[i * N + c0 + k] = gm[k] * e[k];
+        }
+    }
+    const bool lane_rows = (N == skb::kN && iters > skb::kTMax) || (N == skw16::kN && iters > skw16::kTMax) ||
+                           (N != skb::kN && N != skw16::kN);
+    if (threadIdx.x < N && lane_rows) {
         const int r = threadIdx.x;
         float e[N], gm[N];
 #pragma unroll
