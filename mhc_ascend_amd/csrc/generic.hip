@@ -18,7 +18,8 @@
 //   * the n x n Gram matrix sum_c g_i x_j (dM): fp32 MFMA over zero-padded
 //     stream blocks of 16 or 32 (gen_gram_kernel);
 //   * Sinkhorn-Knopp and its exact adjoint: one row per lane in a group of
-//     NM lanes (skw_* in mhc_device.h).
+//     NM lanes (skw_* in mhc_device.h); the static H_res at n <= 16 on one
+//     wave, four elements per lane (skw16::forward_n / backward_n).
 // Every reduction has a fixed order, so the results are deterministic.
 //
 // Math (layer.py:142-170, ops_pytorch_backward.py:9-150), per token with
@@ -75,7 +76,8 @@ __device__ __forceinline__ void gen_wave_partial(float v, float* slots) {
 // Static coefficients (layer.py:146-160): h_pre = sigmoid(H_pre), h_post =
 // 2 sigmoid(H_post), M = SK(exp(H_res)) once, into saved[0 .. 2n + n^2), and
 // the fp32 copy of the RMSNorm weight at saved[w_off ..].  Workgroup 0 forms
-// the coefficients (rows of M on the lanes of wave 0); the others copy
+// the coefficients on wave 0 (n <= 16: four elements of M per lane; else a
+// row per lane); the others copy
 // 2048-channel pieces of the weight.
 // ---------------------------------------------------------------------------
 template <int NM, typename TW>
@@ -91,13 +93,29 @@ __global__ __launch_bounds__(kGenThreads) void gen_static_coef_kernel(
     if (threadIdx.x >= kWave) return;
     const int r = threadIdx.x;
     const bool active = r < n;
+    if (active) {
+        saved[r] = sigmoidf(h_pre[r]);
+        saved[n + r] = 2.f * sigmoidf(h_post[r]);
+    }
+    if constexpr (NM == skw16::kN) {
+        // the zero-padded 16 x 16 matrix on the wave, four elements per lane
+        // (the finalize's adjoint recomputes it with the same code)
+        const int i = skw16::row(), c0 = skw16::col0();
+        float a[skw16::kV];
+#pragma unroll
+        for (int k = 0; k < skw16::kV; ++k) a[k] = (i < n && c0 + k < n) ? expf(h_res[i * n + c0 + k]) : 0.f;
+        skw16::forward_n(a, n, iters, eps);
+#pragma unroll
+        for (int k = 0; k < skw16::kV; ++k) {
+            if (i < n && c0 + k < n) saved[2 * n + i * n + c0 + k] = a[k];
+        }
+        return;
+    }
     float e[NM];
 #pragma unroll
     for (int c = 0; c < NM; ++c) e[c] = (active && c < n) ? expf(h_res[r * n + c]) : 0.f;
     skw_forward<NM>(e, n, iters, eps, active);
     if (active) {
-        saved[r] = sigmoidf(h_pre[r]);
-        saved[n + r] = 2.f * sigmoidf(h_post[r]);
 #pragma unroll
         for (int c = 0; c < NM; ++c) {
             if (c < n) saved[2 * n + r * n + c] = e[c];
@@ -418,9 +436,10 @@ __global__ __launch_bounds__(kGenThreads) void gen_gram_kernel(const float* __re
 // + 2n] = [dM, dh_post_act, dh_pre_act] (layer.hip's finalize, generic n):
 // column totals in LDS (fixed order), then dH_pre = dh_pre_act h_pre (1 -
 // h_pre), dH_post = dh_post_act h_post (1 - h_post / 2) and dH_res =
-// SK^T(dM) * exp(H_res), the adjoint one row per lane of wave 0 (with hist,
-// skw_hist_floats(kWave, n, iters) floats, the iterations' state in memory;
-// without, recomputed per iteration).
+// SK^T(dM) * exp(H_res): for n <= 16 (iters <= skw16::kTMax) on wave 0,
+// four elements per lane; otherwise the adjoint one row per lane of wave 0
+// (with hist, skw_hist_floats(kWave, n, iters) floats, the iterations' state
+// in memory; without, recomputed per iteration).
 // ---------------------------------------------------------------------------
 template <int NM>
 __global__ __launch_bounds__(kGenThreads) void gen_static_finalize_kernel(
@@ -446,7 +465,25 @@ __global__ __launch_bounds__(kGenThreads) void gen_static_finalize_kernel(
         tot[k] = s;
     }
     __syncthreads();
-    if (threadIdx.x < kWave) {
+    const bool one_wave = NM == skw16::kN && iters <= skw16::kTMax;
+    if (one_wave && threadIdx.x < kWave) {
+        // n <= 16: the zero-padded 16 x 16 matrix on wave 0, four elements
+        // per lane, each iteration's state in registers
+        const int i = skw16::row(), c0 = skw16::col0();
+        float e[skw16::kV], gm[skw16::kV];
+#pragma unroll
+        for (int k = 0; k < skw16::kV; ++k) {
+            const bool on = i < n && c0 + k < n;
+            e[k] = on ? expf(h_res[i * n + c0 + k]) : 0.f;
+            gm[k] = on ? tot[i * n + c0 + k] : 0.f;
+        }
+        skw16::backward_n(gm, e, n, iters, eps);
+#pragma unroll
+        for (int k = 0; k < skw16::kV; ++k) {
+            if (i < n && c0 + k < n) d_h_res[i * n + c0 + k] = gm[k] * e[k];
+        }
+    }
+    if (!one_wave && threadIdx.x < kWave) {
         const int r = threadIdx.x;
         const bool active = r < n;
         float e[NM], gm[NM];

@@ -981,6 +981,70 @@ __device__ __forceinline__ void backward(float (&g)[kV], const float (&x0)[kV], 
         }
     }
 }
+
+// The same for an n x n matrix with n <= 16 zero-padded to 16 x 16 (rows
+// r >= n and columns c >= n hold zeros): padded rows take a zero row scale
+// and padded columns no column step (with eps = 0 their scale would be
+// 1/0), as the skw_* functions treat their padding.
+__device__ __forceinline__ void row_scale_n(float (&a)[kV], float eps, bool active, float& rinv) {
+    float s = ((a[0] + a[1]) + a[2]) + a[3];
+    s = group_sum<4>(s);
+    rinv = active ? rcp_nr(s + eps) : 0.f;
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] *= rinv;
+}
+
+__device__ __forceinline__ void col_scale_n(float (&a)[kV], int n, float eps) {
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        const float s = col_sum(a[k]);
+        if (col0() + k < n) a[k] *= rcp_nr(s + eps);
+    }
+}
+
+__device__ __forceinline__ void forward_n(float (&a)[kV], int n, int iters, float eps) {
+    const bool active = row() < n;
+    for (int t = 0; t < iters; ++t) {
+        float ri;
+        row_scale_n(a, eps, active, ri);
+        col_scale_n(a, n, eps);
+    }
+}
+
+__device__ __forceinline__ void backward_n(float (&g)[kV], const float (&x0)[kV], int n, int iters, float eps) {
+    const bool active = row() < n;
+    float hA[kTMax][kV], hr[kTMax];
+    float a[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] = x0[k];
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+        if (t < iters) {
+            row_scale_n(a, eps, active, hr[t]);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) hA[t][k] = a[k];
+            col_scale_n(a, n, eps);
+        }
+    }
+#pragma unroll
+    for (int t = kTMax - 1; t >= 0; --t) {
+        if (t < iters) {
+            float dA[kV];
+#pragma unroll
+            for (int k = 0; k < kV; ++k) {
+                const bool on = col0() + k < n;
+                const float cs = col_sum(hA[t][k]);
+                const float cinv = on ? rcp_nr(cs + eps) : 0.f;
+                const float dot = col_sum(g[k] * (hA[t][k] * cinv));
+                dA[k] = on ? (g[k] - dot) * cinv : 0.f;
+            }
+            float rdot = ((dA[0] * hA[t][0] + dA[1] * hA[t][1]) + dA[2] * hA[t][2]) + dA[3] * hA[t][3];
+            rdot = group_sum<4>(rdot);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) g[k] = col0() + k < n ? (dA[k] - rdot) * hr[t] : 0.f;
+        }
+    }
+}
 }  // namespace skw16
 
 }  // namespace mhc
