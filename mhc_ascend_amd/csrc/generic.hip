@@ -19,7 +19,8 @@
 //     stream blocks of 16 or 32 (gen_gram_kernel);
 //   * Sinkhorn-Knopp and its exact adjoint: one row per lane in a group of
 //     NM lanes (skw_* in mhc_device.h); the static H_res at n <= 16 on one
-//     wave, four elements per lane (skw16::forward_n / backward_n).
+//     wave, four elements per lane (skw16::forward_n / backward_n), and at
+//     n in 17..31 on the whole workgroup (skb::forward_n / backward_n).
 // Every reduction has a fixed order, so the results are deterministic.
 //
 // Math (layer.py:142-170, ops_pytorch_backward.py:9-150), per token with
@@ -38,6 +39,7 @@ namespace mhc {
 constexpr int kGenThreads = 256;
 constexpr int kGenWaves = kGenThreads / kWave;
 constexpr int kGenChunk = 64;  // channels per LDS chunk of the mixing loops
+static_assert(kGenThreads == skb::kThreads, "the static Sinkhorn at n in 17..31 takes the whole workgroup");
 
 bool generic_layer_n(int n) {
     return n >= 1 && n <= kGenMaxN && !(n == 2 || n == 4 || n == 8 || n == 16 || n == 32);
@@ -76,8 +78,8 @@ __device__ __forceinline__ void gen_wave_partial(float v, float* slots) {
 // Static coefficients (layer.py:146-160): h_pre = sigmoid(H_pre), h_post =
 // 2 sigmoid(H_post), M = SK(exp(H_res)) once, into saved[0 .. 2n + n^2), and
 // the fp32 copy of the RMSNorm weight at saved[w_off ..].  Workgroup 0 forms
-// the coefficients on wave 0 (n <= 16: four elements of M per lane; else a
-// row per lane); the others copy
+// the coefficients (n <= 16: four elements of M per lane of wave 0; n in
+// 17..31: the whole workgroup; else a row per lane of wave 0); the others copy
 // 2048-channel pieces of the weight.
 // ---------------------------------------------------------------------------
 template <int NM, typename TW>
@@ -88,6 +90,25 @@ __global__ __launch_bounds__(kGenThreads) void gen_static_coef_kernel(
         const int c0 = (int)(blockIdx.x - 1) * 2048;
         for (int c = c0 + (int)threadIdx.x; c < C && c < c0 + 2048; c += kGenThreads)
             saved[w_off + c] = VecIO<TW>::scalar(w + c);
+        return;
+    }
+    if constexpr (NM == skb::kN) {
+        // n in 17..31: the zero-padded 32 x 32 matrix on the whole workgroup
+        // (the finalize's adjoint recomputes it with the same code)
+        if ((int)threadIdx.x < n) {
+            saved[threadIdx.x] = sigmoidf(h_pre[threadIdx.x]);
+            saved[n + threadIdx.x] = 2.f * sigmoidf(h_post[threadIdx.x]);
+        }
+        __shared__ float part[skb::kPartFloats];
+        const int i = skb::row(), c0 = skb::col0();
+        float a[skb::kV];
+#pragma unroll
+        for (int k = 0; k < skb::kV; ++k) a[k] = (i < n && c0 + k < n) ? expf(h_res[i * n + c0 + k]) : 0.f;
+        skb::forward_n(a, n, iters, eps, part);
+#pragma unroll
+        for (int k = 0; k < skb::kV; ++k) {
+            if (i < n && c0 + k < n) saved[2 * n + i * n + c0 + k] = a[k];
+        }
         return;
     }
     if (threadIdx.x >= kWave) return;
@@ -437,7 +458,9 @@ __global__ __launch_bounds__(kGenThreads) void gen_gram_kernel(const float* __re
 // column totals in LDS (fixed order), then dH_pre = dh_pre_act h_pre (1 -
 // h_pre), dH_post = dh_post_act h_post (1 - h_post / 2) and dH_res =
 // SK^T(dM) * exp(H_res): for n <= 16 (iters <= skw16::kTMax) on wave 0,
-// four elements per lane; otherwise the adjoint one row per lane of wave 0
+// four elements per lane, for n in 17..31 (iters <= skb::kTMax) on the
+// whole workgroup, zero-padded to 32 x 32; otherwise the adjoint one row per
+// lane of wave 0
 // (with hist, skw_hist_floats(kWave, n, iters) floats, the iterations' state
 // in memory; without, recomputed per iteration).
 // ---------------------------------------------------------------------------
@@ -466,6 +489,28 @@ __global__ __launch_bounds__(kGenThreads) void gen_static_finalize_kernel(
     }
     __syncthreads();
     const bool one_wave = NM == skw16::kN && iters <= skw16::kTMax;
+    const bool whole_wg = NM == skb::kN && iters <= skb::kTMax;
+    if constexpr (NM == skb::kN) {
+        if (whole_wg) {
+            // n in 17..31: the zero-padded 32 x 32 matrix on the whole
+            // workgroup (every thread takes part in its barriers)
+            __shared__ float part[skb::kPartFloats];
+            __shared__ float hc[skb::kHistFloats];
+            const int i = skb::row(), c0 = skb::col0();
+            float e[skb::kV], gm[skb::kV];
+#pragma unroll
+            for (int k = 0; k < skb::kV; ++k) {
+                const bool on = i < n && c0 + k < n;
+                e[k] = on ? expf(h_res[i * n + c0 + k]) : 0.f;
+                gm[k] = on ? tot[i * n + c0 + k] : 0.f;
+            }
+            skb::backward_n(gm, e, n, iters, eps, part, hc);
+#pragma unroll
+            for (int k = 0; k < skb::kV; ++k) {
+                if (i < n && c0 + k < n) d_h_res[i * n + c0 + k] = gm[k] * e[k];
+            }
+        }
+    }
     if (one_wave && threadIdx.x < kWave) {
         // n <= 16: the zero-padded 16 x 16 matrix on wave 0, four elements
         // per lane, each iteration's state in registers
@@ -483,7 +528,7 @@ __global__ __launch_bounds__(kGenThreads) void gen_static_finalize_kernel(
             if (i < n && c0 + k < n) d_h_res[i * n + c0 + k] = gm[k] * e[k];
         }
     }
-    if (!one_wave && threadIdx.x < kWave) {
+    if (!one_wave && !whole_wg && threadIdx.x < kWave) {
         const int r = threadIdx.x;
         const bool active = r < n;
         float e[NM], gm[NM];

@@ -898,6 +898,80 @@ __device__ __forceinline__ void backward(float (&g)[kV], const float (&x0)[kV], 
         }
     }
 }
+
+// The same for an n x n matrix with n <= 32 zero-padded to 32 x 32: padded
+// rows (r >= n) take a zero row scale and padded columns (c >= n) a zero
+// column scale (no 1/0 with eps = 0), so they stay zero and the adjoint
+// leaves the real entries as the unpadded one does; g comes back with
+// don't-care values in the padded columns.
+__device__ __forceinline__ void row_scale_n(float (&a)[kV], float eps, bool active, float& rinv) {
+    float s = ((a[0] + a[1]) + a[2]) + a[3];
+    s = group_sum<kLPR>(s);
+    rinv = active ? rcp_nr(s + eps) : 0.f;
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] *= rinv;
+}
+
+__device__ __forceinline__ void col_scale_n(float (&a)[kV], int n, float eps, float* buf, float (&cinv)[kV]) {
+    float s[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) s[k] = a[k];
+    col_total(s, buf);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        cinv[k] = col0() + k < n ? rcp_nr(s[k] + eps) : 0.f;
+        a[k] *= cinv[k];
+    }
+}
+
+__device__ __forceinline__ void forward_n(float (&a)[kV], int n, int iters, float eps, float* part) {
+    const bool active = row() < n;
+    for (int t = 0; t < iters; ++t) {
+        float ri, ci[kV];
+        row_scale_n(a, eps, active, ri);
+        col_scale_n(a, n, eps, part + (t & 1) * kNW * kN, ci);
+    }
+}
+
+__device__ __forceinline__ void backward_n(float (&g)[kV], const float (&x0)[kV], int n, int iters, float eps,
+                                           float* part, float* hc) {
+    const bool active = row() < n;
+    float hA[kTMax][kV], hr[kTMax];
+    float a[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) a[k] = x0[k];
+    const bool writer = threadIdx.x < kLPR;  // row 0 stores the column scales
+#pragma unroll
+    for (int t = 0; t < kTMax; ++t) {
+        if (t < iters) {
+            row_scale_n(a, eps, active, hr[t]);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) hA[t][k] = a[k];
+            float ci[kV];
+            col_scale_n(a, n, eps, part + (t & 1) * kNW * kN, ci);
+            if (writer) *reinterpret_cast<float4*>(hc + t * kN + col0()) = make_float4(ci[0], ci[1], ci[2], ci[3]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = kTMax - 1; t >= 0; --t) {
+        if (t < iters) {
+            const float4 cv = *reinterpret_cast<const float4*>(hc + t * kN + col0());
+            const float ci[kV] = {cv.x, cv.y, cv.z, cv.w};
+            float d[kV];
+#pragma unroll
+            for (int k = 0; k < kV; ++k) d[k] = g[k] * (hA[t][k] * ci[k]);
+            col_total(d, part + ((t + 1) & 1) * kNW * kN);
+            float dA[kV];
+#pragma unroll
+            for (int k = 0; k < kV; ++k) dA[k] = (g[k] - d[k]) * ci[k];
+            float rd = ((dA[0] * hA[t][0] + dA[1] * hA[t][1]) + dA[2] * hA[t][2]) + dA[3] * hA[t][3];
+            rd = group_sum<kLPR>(rd);
+#pragma unroll
+            for (int k = 0; k < kV; ++k) g[k] = (dA[k] - rd) * hr[t];
+        }
+    }
+}
 }  // namespace skb
 
 // ---------------------------------------------------------------------------
